@@ -1,0 +1,31 @@
+// capi_util.hip.h -- error plumbing for the extern "C" entry points.
+// Entry points return D2P_OK (0) or a non-zero code; the message of the last
+// failure on the calling thread is available from d2p_last_error().
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+
+namespace d2p_amd {
+void set_last_error(const char* fmt, ...);
+}
+
+#define D2P_OK 0
+#define D2P_ERR_ARG 1
+#define D2P_ERR_HIP 2
+
+#define D2P_REQUIRE(cond, msg)                                                   \
+    do {                                                                         \
+        if (!(cond)) {                                                           \
+            d2p_amd::set_last_error("%s", msg);                                  \
+            return D2P_ERR_ARG;                                                  \
+        }                                                                        \
+    } while (0)
+
+#define D2P_HIP(expr)                                                            \
+    do {                                                                         \
+        hipError_t e_ = (expr);                                                  \
+        if (e_ != hipSuccess) {                                                  \
+            d2p_amd::set_last_error("%s failed: %s", #expr, hipGetErrorString(e_)); \
+            return D2P_ERR_HIP;                                                  \
+        }                                                                        \
+    } while (0)

@@ -1,0 +1,61 @@
+// common.hip -- error state and batch-scaling kernel of the C ABI.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "capi_util.hip.h"
+#include "dp_common.hip.h"
+#include "../../include/d2p_amd.h"
+
+namespace d2p_amd {
+
+static thread_local char g_last_error[512] = "";
+
+void set_last_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+}
+
+// dst = g[b] * src over [B, n]; float4 body when the row length allows it.
+__global__ void __launch_bounds__(256)
+scale_by_batch_kernel(const float* __restrict__ src, const float* __restrict__ g,
+                      float* __restrict__ dst, long long n, long long total4, int vec) {
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (vec) {
+        typedef float v4f __attribute__((ext_vector_type(4)));
+        const v4f* s4 = reinterpret_cast<const v4f*>(src);
+        v4f* d4 = reinterpret_cast<v4f*>(dst);
+        const long long n4 = n >> 2;
+        for (; idx < total4; idx += stride) {
+            const float gb = g[idx / n4];
+            v4f v = __builtin_nontemporal_load(s4 + idx);
+            __builtin_nontemporal_store(v * gb, d4 + idx);
+        }
+    } else {
+        for (; idx < total4; idx += stride) dst[idx] = g[idx / n] * src[idx];
+    }
+}
+
+}  // namespace d2p_amd
+
+extern "C" const char* d2p_last_error(void) { return d2p_amd::g_last_error; }
+
+extern "C" int d2p_abi_version(void) { return 1; }
+
+extern "C" int d2p_scale_by_batch(const float* src, const float* g, float* dst, int B,
+                                  long long per_batch, void* stream) {
+    D2P_REQUIRE(B >= 0 && per_batch >= 0, "negative size");
+    if (B == 0 || per_batch == 0) return D2P_OK;
+    D2P_REQUIRE(src && g && dst, "null pointer argument");
+    const bool vec = (per_batch % 4 == 0) && (((uintptr_t)src | (uintptr_t)dst) % 16 == 0);
+    const long long total = (long long)B * per_batch;
+    const long long work = vec ? total / 4 : total;
+    long long blocks = (work + 255) / 256;
+    if (blocks > 256 * 64) blocks = 256 * 64;
+    hipLaunchKernelGGL(d2p_amd::scale_by_batch_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, src, g, dst, per_batch, work, vec ? 1 : 0);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}

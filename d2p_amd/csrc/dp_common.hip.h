@@ -1,0 +1,95 @@
+// dp_common.hip.h -- device helpers shared by the soft-DP wavefront kernels
+// (gfx950 / CDNA4, wave64).
+//
+// Numeric contract (restating /root/reference/src/common/numerics.h:23-105):
+//   * sentinels NINF = -1e30 and PINF = +1e30 stand for -inf/+inf;
+//   * a soft-max of terms v_k is  m + T*log(sum_k exp((v_k - m)/T))  with m the
+//     largest term, so the DP value stays on the same fp32 rounding grid as the
+//     reference (alpha = m + small correction).  The correction is computed with
+//     the native base-2 transcendentals: exp((x-m)/T) = exp2((x-m)*log2(e)/T)
+//     and T*log(s) = (T*ln2)*log2(s).
+// Only the rounding of the small correction differs from the reference, which
+// moves alpha by at most one ulp in rare cells.
+
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace d2p_amd {
+
+constexpr float kNINF = -1e30f;
+constexpr float kPINF = 1e30f;
+constexpr float kLog2e = 1.44269504088896341f;
+constexpr float kLn2 = 0.69314718055994531f;
+
+// Native v_exp_f32 / v_log_f32 (base 2).  exp2 of a very negative argument is 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// Whole-wave lane shifts through DPP (no LDS round trip).
+// wave_shr1: lane r receives lane r-1's value, lane 0 receives `fill`.
+__device__ __forceinline__ float wave_shr1(float v, float fill) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(
+        __float_as_int(fill), __float_as_int(v), 0x138, 0xf, 0xf, false));
+}
+// wave_shl1: lane r receives lane r+1's value, lane 63 receives `fill`.
+__device__ __forceinline__ float wave_shl1(float v, float fill) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(
+        __float_as_int(fill), __float_as_int(v), 0x130, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float lane_bcast(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Orders this wave's LDS writes before its later LDS reads of other lanes' data.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Online log-sum-exp accumulator in natural units with the exp2 scale c = log2(e)/T:
+// keeps (m, z) with  LSE = m + T*ln(z).
+struct OnlineLSE {
+    float m, z;
+    __device__ __forceinline__ void init() { m = kNINF; z = 0.0f; }
+    __device__ __forceinline__ void add(float x, float c) {
+        float d = (x - m) * c;
+        float e = fast_exp2(-fabsf(d));
+        bool up = d > 0.0f;
+        z = up ? fmaf(z, e, 1.0f) : z + e;
+        m = up ? x : m;
+    }
+    __device__ __forceinline__ void merge(float m2, float z2, float c) {
+        float M = fmaxf(m, m2);
+        float za = (m <= kNINF) ? 0.0f : z * fast_exp2((m - M) * c);
+        float zb = (m2 <= kNINF) ? 0.0f : z2 * fast_exp2((m2 - M) * c);
+        m = M;
+        z = za + zb;
+    }
+};
+
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    return wave_reduce(v, [](float a, float b) { return a + b; });
+}
+
+// Combines per-lane OnlineLSE states across the wave; result valid in every lane.
+__device__ __forceinline__ void wave_merge_lse(OnlineLSE& s, float c) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        float m2 = __shfl_xor(s.m, off, 64);
+        float z2 = __shfl_xor(s.z, off, 64);
+        s.merge(m2, z2, c);
+    }
+}
+
+}  // namespace d2p_amd

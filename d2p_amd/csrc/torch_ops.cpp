@@ -1,0 +1,415 @@
+// torch_ops.cpp -- PyTorch dispatcher registration of the d2p operators on ROCm.
+//
+// Schemas are byte-identical to the reference's TORCH_LIBRARY_FRAGMENT(d2p, m):
+//   /root/reference/src/sw/registry.cpp:30-44
+//   /root/reference/src/sw_affine/registry.cpp:74-89
+//   /root/reference/src/dtw/registry.cpp:127-132
+// On PyTorch-ROCm a HIP tensor carries the CUDA dispatch key, so the HIP
+// implementations register under CUDA / AutogradCUDA.  Every implementation
+// validates on the host (same messages as the reference), allocates outputs and
+// workspaces through the torch caching allocator, and calls the C ABI of
+// libd2p_amd.so on the current HIP stream.  There is no CPU implementation: CPU
+// tensors raise.
+
+#include <torch/torch.h>
+#include <torch/library.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include <limits>
+#include <tuple>
+#include <vector>
+
+#include "../../include/d2p_amd.h"
+
+namespace {
+
+using torch::Tensor;
+using torch::autograd::AutogradContext;
+using torch::autograd::tensor_list;
+
+#define D2P_CALL(expr)                                                          \
+    do {                                                                        \
+        int rc_ = (expr);                                                       \
+        TORCH_CHECK(rc_ == 0, "d2p_amd kernel call failed: ", d2p_last_error()); \
+    } while (0)
+
+// same wording as /root/reference/src/common/torch_utils.h:31-66
+#define CHECK_INPUT_DEV(x)                                                      \
+    TORCH_CHECK((x).is_cuda(), #x " must be a CUDA tensor");                   \
+    TORCH_CHECK((x).is_contiguous(), #x " must be contiguous");                \
+    TORCH_CHECK((x).scalar_type() == torch::kFloat32, #x " must be float32, got ", \
+                (x).scalar_type())
+
+inline void* current_stream() {
+    return (void*)c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream();
+}
+
+struct Dims {
+    int B, L1, L2;
+};
+
+int checked_dim(int64_t v, const char* name) {
+    TORCH_CHECK(v >= 0 && v <= std::numeric_limits<int>::max(), name,
+                " must fit int32 CUDA kernel indexing, got ", v);
+    return static_cast<int>(v);
+}
+
+// /root/reference/src/sw/torch_cuda.cpp:41-65 (message prefix per family)
+Dims checked_dims(const Tensor& x, const char* family) {
+    TORCH_CHECK(x.dim() == 3, "scores must be 3D (B, L1, L2)");
+    Dims d{checked_dim(x.size(0), "scores batch dimension"),
+           checked_dim(x.size(1), "scores L1 dimension"),
+           checked_dim(x.size(2), "scores L2 dimension")};
+    const int64_t cells = (int64_t(d.L1) + 1) * (int64_t(d.L2) + 1);
+    TORCH_CHECK(cells <= std::numeric_limits<int>::max(), family,
+                " CUDA DP table is too large for 32-bit kernel indexing: ",
+                "(L1 + 1) * (L2 + 1) = ", cells, " exceeds ", std::numeric_limits<int>::max());
+    return d;
+}
+
+// /root/reference/src/sw/torch_cuda.cpp:67-111
+Tensor resolve_lengths(const c10::optional<Tensor>& lengths_opt, const Dims& d,
+                       const torch::Device& device) {
+    if (!lengths_opt.has_value() || !lengths_opt->defined()) {
+        // built on the device: no host round trip, nothing to validate
+        Tensor l = torch::empty({d.B, 2}, torch::TensorOptions().dtype(torch::kInt32).device(device));
+        l.select(1, 0).fill_(d.L1);
+        l.select(1, 1).fill_(d.L2);
+        return l;
+    }
+    const Tensor& lengths = *lengths_opt;
+    TORCH_CHECK(lengths.is_cuda(), "lengths must be a CUDA tensor");
+    TORCH_CHECK(lengths.is_contiguous(), "lengths must be contiguous");
+    TORCH_CHECK(lengths.dim() == 2 && lengths.size(0) == d.B && lengths.size(1) == 2,
+                "lengths must be [B, 2] with B = ", d.B, ", got ", lengths.sizes());
+    TORCH_CHECK(lengths.scalar_type() == torch::kInt32, "lengths must be int32");
+    TORCH_CHECK(lengths.device() == device, "lengths must be on same device as scores, got ",
+                lengths.device(), " vs ", device);
+    auto host = lengths.to(torch::kCPU);
+    auto acc = host.accessor<int32_t, 2>();
+    for (int b = 0; b < d.B; ++b) {
+        TORCH_CHECK(acc[b][0] >= 0 && acc[b][0] <= d.L1, "lengths[", b,
+                    ",0] must be between 0 and ", d.L1, ", got ", acc[b][0]);
+        TORCH_CHECK(acc[b][1] >= 0 && acc[b][1] <= d.L2, "lengths[", b,
+                    ",1] must be between 0 and ", d.L2, ", got ", acc[b][1]);
+    }
+    return lengths;
+}
+
+Tensor workspace(size_t bytes, const Tensor& like) {
+    return torch::empty({(int64_t)std::max<size_t>(bytes, 1)},
+                        like.options().dtype(torch::kUInt8));
+}
+
+float scalar_value(const Tensor& t, const char* name) {
+    TORCH_CHECK(t.numel() == 1, name, " must be a scalar tensor");
+    return t.to(torch::kCPU, torch::kFloat32).item<float>();
+}
+
+Tensor grad_param_sum(const Tensor& grad_value, const Tensor& per_batch) {
+    return (grad_value.to(torch::kFloat32) * per_batch).sum().reshape({1});
+}
+
+// g[b] * src, through the C ABI (autograd backward of value -> scores)
+Tensor scale_by_batch(const Tensor& src, const Tensor& g) {
+    Tensor gg = g.to(src.device(), torch::kFloat32).contiguous();
+    TORCH_CHECK(gg.numel() == src.size(0), "grad_value must have one entry per batch element");
+    Tensor out = torch::empty_like(src);
+    D2P_CALL(d2p_scale_by_batch(src.data_ptr<float>(), gg.data_ptr<float>(),
+                                out.data_ptr<float>(), (int)src.size(0),
+                                (long long)(src.numel() / std::max<int64_t>(src.size(0), 1)),
+                                current_stream()));
+    return out;
+}
+
+[[noreturn]] void not_yet(const char* op) {
+    TORCH_CHECK_NOT_IMPLEMENTED(false, "d2p_amd: ", op,
+                                " has no MI355X kernel in this build yet");
+}
+
+// ---------------------------------------------------------------------------
+// linear-gap soft Smith-Waterman
+// ---------------------------------------------------------------------------
+
+struct SwOut {
+    Tensor partition, marginals, grad_gap, grad_T;
+};
+
+SwOut sw_run(const Tensor& scores, const Tensor& lengths, const Dims& d, float gap, float T) {
+    auto opt = scores.options();
+    SwOut o{torch::empty({d.B}, opt), torch::empty({d.B, d.L1, d.L2}, opt),
+            torch::empty({d.B}, opt), torch::empty({d.B}, opt)};
+    const size_t ws_bytes = d2p_sw_workspace_bytes(d.B, d.L1, d.L2);
+    Tensor ws = workspace(ws_bytes, scores);
+    D2P_CALL(d2p_sw_forward_marginals(
+        scores.data_ptr<float>(), lengths.data_ptr<int>(), d.B, d.L1, d.L2, gap, T,
+        o.partition.data_ptr<float>(), o.marginals.data_ptr<float>(),
+        o.grad_gap.data_ptr<float>(), o.grad_T.data_ptr<float>(), ws.data_ptr(), ws_bytes,
+        current_stream()));
+    return o;
+}
+
+// Autograd semantics of SoftSWRegularCUDAFunction
+// (/root/reference/src/sw/torch_cuda.cpp:178-411): outputs {value, marginals};
+// d value / d scores = marginals, so backward scales the saved marginals.
+class SoftSWFunction : public torch::autograd::Function<SoftSWFunction> {
+   public:
+    static tensor_list forward(AutogradContext* ctx, Tensor scores, Tensor gap_t, Tensor temp_t,
+                               Tensor lengths, double gap, double temperature) {
+        ctx->set_materialize_grads(false);
+        CHECK_INPUT_DEV(scores);
+        Dims d = checked_dims(scores, "SW");
+        c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+        SwOut o = sw_run(scores, lengths, d, (float)gap, (float)temperature);
+        ctx->save_for_backward({o.marginals, o.grad_gap, o.grad_T});
+        return {o.partition, o.marginals};
+    }
+
+    static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
+        auto saved = ctx->get_saved_variables();
+        Tensor marg = saved[0], ggap = saved[1], gT = saved[2];
+        c10::hip::HIPGuardMasqueradingAsCUDA guard(marg.device());
+        Tensor grad_value = grads[0], grad_marg = grads[1];
+        Tensor grad_scores, grad_gap, grad_T;
+        if (grad_value.defined() && grad_value.numel() > 0) {
+            grad_scores = scale_by_batch(marg, grad_value);
+            if (ctx->needs_input_grad(1)) grad_gap = grad_param_sum(grad_value, ggap);
+            if (ctx->needs_input_grad(2)) grad_T = grad_param_sum(grad_value, gT);
+        }
+        if (grad_marg.defined() && grad_marg.numel() > 0) not_yet("soft_sw marginal-path backward");
+        return {grad_scores, grad_gap, grad_T, Tensor(), Tensor(), Tensor()};
+    }
+};
+
+std::vector<Tensor> soft_sw_t(Tensor scores, Tensor gap, Tensor temperature, Tensor lengths) {
+    CHECK_INPUT_DEV(scores);
+    Dims d = checked_dims(scores, "SW");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    const float g = scalar_value(gap, "gap");
+    const float T = scalar_value(temperature, "temperature");
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    return SoftSWFunction::apply(scores, gap, temperature, l, g, T);
+}
+
+std::vector<Tensor> soft_sw_float(Tensor scores, double gap, double temperature,
+                                  c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    Dims d = checked_dims(scores, "SW");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    return SoftSWFunction::apply(scores, Tensor(), Tensor(), l, gap, temperature);
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> soft_sw_with_grads(Tensor scores, double gap,
+                                                              double temperature,
+                                                              c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    Dims d = checked_dims(scores, "SW");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    SwOut o = sw_run(scores, l, d, (float)gap, (float)temperature);
+    return {o.partition, o.marginals, o.grad_gap, o.grad_T};
+}
+
+Tensor soft_sw_hvp(Tensor, Tensor, double, double, c10::optional<Tensor>) { not_yet("soft_sw_hvp"); }
+Tensor soft_sw_param_jacobian(Tensor, int64_t, double, double, c10::optional<Tensor>) {
+    not_yet("soft_sw_param_jacobian");
+}
+std::tuple<Tensor, Tensor, Tensor> soft_sw_backward_full(Tensor, Tensor, double, double,
+                                                         c10::optional<Tensor>) {
+    not_yet("soft_sw_backward_full");
+}
+
+std::vector<Tensor> sw_forward(Tensor s, double g, double t, c10::optional<Tensor> l) {
+    return soft_sw_float(s, g, t, l);
+}
+std::vector<Tensor> sw_forward_t(Tensor s, Tensor g, Tensor t, Tensor l) { return soft_sw_t(s, g, t, l); }
+std::tuple<Tensor, Tensor> sw_value_grad_params(Tensor s, double g, double t,
+                                                c10::optional<Tensor> l) {
+    auto r = soft_sw_with_grads(s, g, t, l);
+    return {std::get<2>(r), std::get<3>(r)};
+}
+std::tuple<Tensor, Tensor, Tensor> sw_marginals_backward(Tensor s, Tensor gm, double g, double t,
+                                                         c10::optional<Tensor> l) {
+    return soft_sw_backward_full(s, gm, g, t, l);
+}
+Tensor sw_marginals_hvp(Tensor s, Tensor v, double g, double t, c10::optional<Tensor> l) {
+    return soft_sw_hvp(s, v, g, t, l);
+}
+Tensor sw_marginals_grad_gap(Tensor s, double g, double t, c10::optional<Tensor> l) {
+    return soft_sw_param_jacobian(s, 0, g, t, l);
+}
+Tensor sw_marginals_grad_temp(Tensor s, double g, double t, c10::optional<Tensor> l) {
+    return soft_sw_param_jacobian(s, 1, g, t, l);
+}
+
+// ---------------------------------------------------------------------------
+// placeholders for the affine and DTW families (kernels land separately)
+// ---------------------------------------------------------------------------
+std::vector<Tensor> swa_t(Tensor, Tensor, Tensor, Tensor, Tensor) { not_yet("soft_sw_affine"); }
+std::vector<Tensor> swa_float(Tensor, double, double, double, c10::optional<Tensor>) {
+    not_yet("soft_sw_affine_float");
+}
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> swa_with_grads(Tensor, double, double, double,
+                                                                  c10::optional<Tensor>) {
+    not_yet("soft_sw_affine_with_grads");
+}
+Tensor swa_hvp(Tensor, Tensor, double, double, double, c10::optional<Tensor>) {
+    not_yet("soft_sw_affine_hvp");
+}
+Tensor swa_param_jacobian(Tensor, int64_t, double, double, double, c10::optional<Tensor>) {
+    not_yet("soft_sw_affine_param_jacobian");
+}
+std::tuple<Tensor, Tensor, Tensor, Tensor> swa_backward_full(Tensor, Tensor, double, double,
+                                                             double, c10::optional<Tensor>) {
+    not_yet("soft_sw_affine_backward_full");
+}
+std::tuple<Tensor, Tensor, Tensor> swa_value_grad_params(Tensor, double, double, double,
+                                                         c10::optional<Tensor>) {
+    not_yet("sw_affine_value_grad_params");
+}
+Tensor swa_marg_grad(Tensor, double, double, double, c10::optional<Tensor>) {
+    not_yet("sw_affine_marginals_grad_*");
+}
+
+std::vector<Tensor> dtw_t(Tensor, Tensor, Tensor, int64_t) { not_yet("soft_dtw"); }
+std::vector<Tensor> dtw_float(Tensor, double, c10::optional<Tensor>, c10::optional<int64_t>) {
+    not_yet("soft_dtw_float");
+}
+std::tuple<Tensor, Tensor, Tensor> dtw_with_grads(Tensor, double, c10::optional<Tensor>,
+                                                  c10::optional<int64_t>) {
+    not_yet("soft_dtw_with_grads");
+}
+Tensor dtw_hvp(Tensor, Tensor, double, c10::optional<Tensor>, c10::optional<int64_t>) {
+    not_yet("soft_dtw_hvp");
+}
+Tensor dtw_param_jacobian(Tensor, double, c10::optional<Tensor>, c10::optional<int64_t>) {
+    not_yet("soft_dtw_param_jacobian");
+}
+std::tuple<Tensor, Tensor> dtw_backward_full(Tensor, Tensor, double, c10::optional<Tensor>,
+                                             c10::optional<int64_t>) {
+    not_yet("soft_dtw_backward_full");
+}
+
+[[noreturn]] void cpu_unsupported() {
+    TORCH_CHECK(false,
+                "d2p_amd implements the MI355X (HIP) path only: move the inputs to a "
+                "HIP device (device='cuda' on PyTorch-ROCm)");
+}
+
+}  // namespace
+
+TORCH_LIBRARY(d2p, m) {
+    // /root/reference/src/sw/registry.cpp:30-44
+    m.def("soft_sw(Tensor scores, Tensor gap, Tensor temperature, Tensor lengths) -> Tensor[]");
+    m.def("soft_sw_float(Tensor scores, float gap, float temperature, Tensor? lengths) -> Tensor[]");
+    m.def("soft_sw_with_grads(Tensor scores, float gap, float temperature, Tensor? lengths) -> (Tensor, Tensor, Tensor, Tensor)");
+    m.def("soft_sw_hvp(Tensor scores, Tensor tangent, float gap, float temperature, Tensor? lengths) -> Tensor");
+    m.def("soft_sw_param_jacobian(Tensor scores, int param_type, float gap, float temperature, Tensor? lengths) -> Tensor");
+    m.def("soft_sw_backward_full(Tensor scores, Tensor grad_alignment, float gap, float temperature, Tensor? lengths) -> (Tensor, Tensor, Tensor)");
+    m.def("sw_forward(Tensor scores, float gap, float temp, Tensor? lengths) -> Tensor[]");
+    m.def("sw_forward_t(Tensor scores, Tensor gap, Tensor temp, Tensor lengths) -> Tensor[]");
+    m.def("sw_value_grad_params(Tensor scores, float gap, float temp, Tensor? lengths) -> (Tensor, Tensor)");
+    m.def("sw_marginals_backward(Tensor scores, Tensor grad_marginals, float gap, float temp, Tensor? lengths) -> (Tensor, Tensor, Tensor)");
+    m.def("sw_marginals_hvp(Tensor scores, Tensor v, float gap, float temp, Tensor? lengths) -> Tensor");
+    m.def("sw_marginals_grad_gap(Tensor scores, float gap, float temp, Tensor? lengths) -> Tensor");
+    m.def("sw_marginals_grad_temp(Tensor scores, float gap, float temp, Tensor? lengths) -> Tensor");
+
+    // /root/reference/src/sw_affine/registry.cpp:74-89
+    m.def("soft_sw_affine(Tensor scores, Tensor gap_open, Tensor gap_ext, Tensor temperature, Tensor lengths) -> Tensor[]");
+    m.def("soft_sw_affine_float(Tensor scores, float gap_open, float gap_ext, float temperature, Tensor? lengths) -> Tensor[]");
+    m.def("soft_sw_affine_with_grads(Tensor scores, float gap_open, float gap_ext, float temperature, Tensor? lengths) -> (Tensor, Tensor, Tensor, Tensor, Tensor)");
+    m.def("soft_sw_affine_hvp(Tensor scores, Tensor tangent, float gap_open, float gap_ext, float temperature, Tensor? lengths) -> Tensor");
+    m.def("soft_sw_affine_param_jacobian(Tensor scores, int param_type, float gap_open, float gap_ext, float temperature, Tensor? lengths) -> Tensor");
+    m.def("soft_sw_affine_backward_full(Tensor scores, Tensor grad_alignment, float gap_open, float gap_ext, float temperature, Tensor? lengths) -> (Tensor, Tensor, Tensor, Tensor)");
+    m.def("sw_affine_forward(Tensor scores, float gap_open, float gap_ext, float temp, Tensor? lengths) -> Tensor[]");
+    m.def("sw_affine_forward_t(Tensor scores, Tensor gap_open, Tensor gap_ext, Tensor temp, Tensor lengths) -> Tensor[]");
+    m.def("sw_affine_value_grad_params(Tensor scores, float gap_open, float gap_ext, float temp, Tensor? lengths) -> (Tensor, Tensor, Tensor)");
+    m.def("sw_affine_marginals_backward(Tensor scores, Tensor grad_marginals, float gap_open, float gap_ext, float temp, Tensor? lengths) -> (Tensor, Tensor, Tensor, Tensor)");
+    m.def("sw_affine_marginals_hvp(Tensor scores, Tensor v, float gap_open, float gap_ext, float temp, Tensor? lengths) -> Tensor");
+    m.def("sw_affine_marginals_grad_gap_open(Tensor scores, float gap_open, float gap_ext, float temp, Tensor? lengths) -> Tensor");
+    m.def("sw_affine_marginals_grad_gap_ext(Tensor scores, float gap_open, float gap_ext, float temp, Tensor? lengths) -> Tensor");
+    m.def("sw_affine_marginals_grad_temp(Tensor scores, float gap_open, float gap_ext, float temp, Tensor? lengths) -> Tensor");
+
+    // /root/reference/src/dtw/registry.cpp:127-132
+    m.def("soft_dtw(Tensor costs, Tensor temperature, Tensor lengths, int bandwidth) -> Tensor[]");
+    m.def("soft_dtw_float(Tensor costs, float temperature, Tensor? lengths, int? bandwidth) -> Tensor[]");
+    m.def("soft_dtw_with_grads(Tensor costs, float temperature, Tensor? lengths, int? bandwidth) -> (Tensor, Tensor, Tensor)");
+    m.def("soft_dtw_hvp(Tensor costs, Tensor tangent, float temperature, Tensor? lengths, int? bandwidth) -> Tensor");
+    m.def("soft_dtw_param_jacobian(Tensor costs, float temperature, Tensor? lengths, int? bandwidth) -> Tensor");
+    m.def("soft_dtw_backward_full(Tensor costs, Tensor grad_alignment, float temperature, Tensor? lengths, int? bandwidth) -> (Tensor, Tensor)");
+}
+
+TORCH_LIBRARY_IMPL(d2p, CUDA, m) {
+    m.impl("soft_sw", soft_sw_t);
+    m.impl("soft_sw_float", soft_sw_float);
+    m.impl("soft_sw_with_grads", soft_sw_with_grads);
+    m.impl("soft_sw_hvp", soft_sw_hvp);
+    m.impl("soft_sw_param_jacobian", soft_sw_param_jacobian);
+    m.impl("soft_sw_backward_full", soft_sw_backward_full);
+    m.impl("sw_forward", sw_forward);
+    m.impl("sw_forward_t", sw_forward_t);
+    m.impl("sw_value_grad_params", sw_value_grad_params);
+    m.impl("sw_marginals_backward", sw_marginals_backward);
+    m.impl("sw_marginals_hvp", sw_marginals_hvp);
+    m.impl("sw_marginals_grad_gap", sw_marginals_grad_gap);
+    m.impl("sw_marginals_grad_temp", sw_marginals_grad_temp);
+
+    m.impl("soft_sw_affine", swa_t);
+    m.impl("soft_sw_affine_float", swa_float);
+    m.impl("soft_sw_affine_with_grads", swa_with_grads);
+    m.impl("soft_sw_affine_hvp", swa_hvp);
+    m.impl("soft_sw_affine_param_jacobian", swa_param_jacobian);
+    m.impl("soft_sw_affine_backward_full", swa_backward_full);
+    m.impl("sw_affine_forward", swa_float);
+    m.impl("sw_affine_forward_t", swa_t);
+    m.impl("sw_affine_value_grad_params", swa_value_grad_params);
+    m.impl("sw_affine_marginals_backward", swa_backward_full);
+    m.impl("sw_affine_marginals_hvp", swa_hvp);
+    m.impl("sw_affine_marginals_grad_gap_open", swa_marg_grad);
+    m.impl("sw_affine_marginals_grad_gap_ext", swa_marg_grad);
+    m.impl("sw_affine_marginals_grad_temp", swa_marg_grad);
+
+    m.impl("soft_dtw", dtw_t);
+    m.impl("soft_dtw_float", dtw_float);
+    m.impl("soft_dtw_with_grads", dtw_with_grads);
+    m.impl("soft_dtw_hvp", dtw_hvp);
+    m.impl("soft_dtw_param_jacobian", dtw_param_jacobian);
+    m.impl("soft_dtw_backward_full", dtw_backward_full);
+}
+
+// Autograd-registered ops, as in the reference
+// (/root/reference/src/sw/torch_cuda.cpp:876-883 and the affine/DTW equivalents).
+TORCH_LIBRARY_IMPL(d2p, AutogradCUDA, m) {
+    m.impl("soft_sw", soft_sw_t);
+    m.impl("soft_sw_float", soft_sw_float);
+    m.impl("sw_forward", sw_forward);
+    m.impl("sw_forward_t", sw_forward_t);
+    m.impl("soft_sw_affine", swa_t);
+    m.impl("soft_sw_affine_float", swa_float);
+    m.impl("sw_affine_forward", swa_float);
+    m.impl("sw_affine_forward_t", swa_t);
+    m.impl("soft_dtw", dtw_t);
+    m.impl("soft_dtw_float", dtw_float);
+}
+
+namespace {
+void cpu_boxed(const c10::OperatorHandle&, torch::jit::Stack*) { cpu_unsupported(); }
+const char* const kAllOps[] = {
+    "soft_sw", "soft_sw_float", "soft_sw_with_grads", "soft_sw_hvp", "soft_sw_param_jacobian",
+    "soft_sw_backward_full", "sw_forward", "sw_forward_t", "sw_value_grad_params",
+    "sw_marginals_backward", "sw_marginals_hvp", "sw_marginals_grad_gap",
+    "sw_marginals_grad_temp", "soft_sw_affine", "soft_sw_affine_float",
+    "soft_sw_affine_with_grads", "soft_sw_affine_hvp", "soft_sw_affine_param_jacobian",
+    "soft_sw_affine_backward_full", "sw_affine_forward", "sw_affine_forward_t",
+    "sw_affine_value_grad_params", "sw_affine_marginals_backward", "sw_affine_marginals_hvp",
+    "sw_affine_marginals_grad_gap_open", "sw_affine_marginals_grad_gap_ext",
+    "sw_affine_marginals_grad_temp", "soft_dtw", "soft_dtw_float", "soft_dtw_with_grads",
+    "soft_dtw_hvp", "soft_dtw_param_jacobian", "soft_dtw_backward_full"};
+}  // namespace
+
+TORCH_LIBRARY_IMPL(d2p, CPU, m) {
+    for (const char* name : kAllOps)
+        m.impl(name, torch::CppFunction::makeFromBoxedFunction<&cpu_boxed>());
+}

@@ -1,0 +1,69 @@
+/*
+ * d2p_amd.h -- C ABI of the MI355X (gfx950) soft-alignment DP kernels.
+ *
+ * This is the drop-in boundary for the reference's device layer (L1 in the
+ * reference: extern "C" host wrappers in src/{sw,sw_affine,dtw}/kernels.cuh that
+ * take plain device pointers and sizes).  Every entry point:
+ *   - takes device pointers to caller-owned, contiguous buffers (float32 data,
+ *     int32 lengths [B,2] with 0 <= lengths[b,0] <= max_L1, 0 <= lengths[b,1] <= max_L2),
+ *   - never allocates: scratch memory is a caller-provided workspace whose size the
+ *     matching *_workspace_bytes() function returns,
+ *   - enqueues its kernels on `stream` (a hipStream_t passed as void*; NULL = the
+ *     default stream) and returns without synchronising,
+ *   - returns 0 on success, non-zero on failure; d2p_last_error() then describes it.
+ * Outputs are fully written (padded cells of the marginal matrices are zero).
+ * No torch types cross this boundary; the PyTorch operator layer
+ * (d2p_amd/csrc/torch_ops.cpp) is one client of it.
+ */
+#ifndef D2P_AMD_H
+#define D2P_AMD_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* d2p_last_error(void);
+
+/* ABI version of this library (incremented on incompatible changes). */
+int d2p_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Linear-gap soft Smith-Waterman
+ * ------------------------------------------------------------------------- */
+
+/* Workspace bytes needed by d2p_sw_forward_marginals for the given padded shape. */
+size_t d2p_sw_workspace_bytes(int B, int max_L1, int max_L2);
+
+/* Forward value and marginals in one call.
+ * Replaces the pair sw_regular_forward[_warp] + sw_regular_backward[_warp]
+ * (/root/reference/src/sw/kernels.cuh:139-207) as sequenced by
+ * SoftSWRegularCUDAFunction::forward (/root/reference/src/sw/torch_cuda.cpp:215-241).
+ *   scores    [B, max_L1, max_L2]   input
+ *   partition [B]                   out: soft alignment value S
+ *   marginals [B, max_L1, max_L2]   out: dS/dscores (zero in padding)
+ *   grad_gap  [B]                   out: dS/dgap
+ *   grad_T    [B]                   out: dS/dtemperature                        */
+int d2p_sw_forward_marginals(const float* scores, const int* lengths, int B, int max_L1,
+                             int max_L2, float gap, float temperature, float* partition,
+                             float* marginals, float* grad_gap, float* grad_T,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Shared helpers
+ * ------------------------------------------------------------------------- */
+
+/* dst[b, k] = g[b] * src[b, k] for k < per_batch (src and dst may alias).
+ * Replaces the ATen expression `grad_score.view({B,1,1}) * posteriors` of the
+ * reference autograd backward (/root/reference/src/sw/torch_cuda.cpp:314,
+ * src/sw_affine/torch_cuda.cpp, src/dtw/torch_cuda.cpp). */
+int d2p_scale_by_batch(const float* src, const float* g, float* dst, int B,
+                       long long per_batch, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* D2P_AMD_H */

@@ -1,0 +1,338 @@
+"""CPU parity checker for the d2p_amd HIP path (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg
+may import this module.  It wraps two interchangeable CPU libraries behind one
+numpy interface:
+
+* ``liboracle.so`` -- this repo's C restatement of the reference CPU kernels
+  (``oracle/d2p_oracle.c``; each function cites the reference file:line it
+  follows);
+* ``_ref/libd2p_ref.so`` -- the reference's own CPU kernels
+  (``/root/reference/src/{sw,sw_affine,dtw}/kernels_cpu.cpp``), compiled by
+  ``oracle/Makefile`` where those sources exist.
+
+Both expose the reference's CPU signatures (``src/sw/kernels_cpu.h:95-183``,
+``src/sw_affine/kernels_cpu.h:80-167``, ``src/dtw/kernels_cpu.h:83-161``), so
+the same Python code drives either and their outputs can be compared bit for
+bit.  The composite helpers at the bottom restate the reference's binding-level
+call sequences (``src/sw/torch_cpu.cpp:114-259``,
+``src/sw_affine/torch_cpu.cpp:122-290``, ``src/dtw/torch_cpu.cpp:122-256``).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_LIB = os.path.join(HERE, "liboracle.so")
+REF_LIB = os.path.join(HERE, "_ref", "libd2p_ref.so")
+
+_F = ctypes.POINTER(ctypes.c_float)
+_I = ctypes.POINTER(ctypes.c_int)
+_i = ctypes.c_int
+_f = ctypes.c_float
+_l = ctypes.c_int64
+
+# (oracle symbol, reference symbol, argtypes)
+_SIGS = {
+    "sw_forward": ("oracle_sw_forward", "sw_regular_forward_cpu",
+                   [_F, _F, _F, _I, _i, _i, _i, _f, _f]),
+    "sw_backward": ("oracle_sw_backward", "sw_regular_backward_cpu",
+                    [_F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f]),
+    "sw_hvp": ("oracle_sw_hvp", "sw_regular_hvp_cpu",
+               [_F, _F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f]),
+    "sw_param_grad": ("oracle_sw_param_grad", "sw_regular_param_grad_cpu",
+                      [_F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f, _i]),
+    "swa_forward": ("oracle_swa_forward", "sw_affine_forward_cpu",
+                    [_F, _F, _F, _I, _i, _i, _i, _f, _f, _f]),
+    "swa_backward": ("oracle_swa_backward", "sw_affine_backward_cpu",
+                     [_F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f, _f]),
+    "swa_hvp": ("oracle_swa_hvp", "sw_affine_hvp_cpu",
+                [_F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f, _f]),
+    "swa_param_grad": ("oracle_swa_param_grad", "sw_affine_param_grad_cpu",
+                       [_F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f, _f, _i]),
+    "dtw_forward": ("oracle_dtw_forward", "dtw_forward_cpu",
+                    [_F, _F, _F, _I, _i, _i, _i, _f, _l]),
+    "dtw_backward": ("oracle_dtw_backward", "dtw_backward_cpu",
+                     [_F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _l]),
+    "dtw_hvp": ("oracle_dtw_hvp", "dtw_hvp_cpu",
+                [_F, _F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _l]),
+    "dtw_param_grad": ("oracle_dtw_param_grad", "dtw_param_grad_cpu",
+                       [_F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _l]),
+}
+
+
+def _p(a: np.ndarray):
+    if a.dtype == np.int32:
+        return a.ctypes.data_as(_I)
+    return a.ctypes.data_as(_F)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def _lengths(lengths, B, L1, L2) -> np.ndarray:
+    if lengths is None:
+        out = np.empty((B, 2), dtype=np.int32)
+        out[:, 0] = L1
+        out[:, 1] = L2
+        return out
+    return np.ascontiguousarray(np.asarray(lengths, dtype=np.int32)).reshape(B, 2)
+
+
+class CpuKernels:
+    """numpy front end over one CPU library (``kind`` = "oracle" or "reference")."""
+
+    def __init__(self, kind: str = "oracle"):
+        if kind not in ("oracle", "reference"):
+            raise ValueError(kind)
+        path = ORACLE_LIB if kind == "oracle" else REF_LIB
+        if not os.path.exists(path):
+            raise FileNotFoundError(
+                f"{path} is not built; run `make -C oracle` (reference build needs "
+                "/root/reference)")
+        if kind == "reference":
+            import torch  # noqa: F401  -- loads libtorch_cpu/libc10 the library links
+        self.kind = kind
+        self.path = path
+        self.lib = ctypes.CDLL(path)
+        self.fn = {}
+        for name, (osym, rsym, argt) in _SIGS.items():
+            f = getattr(self.lib, osym if kind == "oracle" else rsym)
+            f.argtypes = argt
+            f.restype = None
+            self.fn[name] = f
+
+    # ---------------- linear-gap SW ----------------
+    def sw_forward(self, scores, lengths, gap, T):
+        s = _f32(scores)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        alpha = np.zeros((B, (L1 + 1) * (L2 + 1)), np.float32)
+        part = np.zeros((B,), np.float32)
+        self.fn["sw_forward"](_p(s), _p(alpha), _p(part), _p(ln), B, L1, L2, gap, T)
+        return alpha, part
+
+    def sw_backward(self, alpha, scores, part, lengths, gap, T):
+        s = _f32(scores)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        beta = np.zeros_like(alpha)
+        post = np.zeros_like(s)
+        gg = np.zeros((B,), np.float32)
+        gt = np.zeros((B,), np.float32)
+        self.fn["sw_backward"](_p(alpha), _p(s), _p(part), _p(beta), _p(post), _p(gg),
+                               _p(gt), _p(ln), B, L1, L2, gap, T)
+        return post, gg, gt
+
+    def sw_hvp(self, alpha, scores, part, V, lengths, gap, T):
+        s = _f32(scores)
+        v = _f32(V)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        da = np.zeros_like(alpha)
+        dp = np.zeros((B,), np.float32)
+        be = np.zeros_like(alpha)
+        dbe = np.zeros_like(alpha)
+        H = np.zeros_like(s)
+        self.fn["sw_hvp"](_p(alpha), _p(s), _p(part), _p(v), _p(da), _p(dp), _p(be),
+                          _p(dbe), _p(H), _p(ln), B, L1, L2, gap, T)
+        return H, dp
+
+    def sw_param_grad(self, alpha, scores, part, dS, lengths, gap, T, ptype):
+        s = _f32(scores)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        dS = _f32(dS)
+        U = np.zeros_like(alpha)
+        be = np.zeros_like(alpha)
+        W = np.zeros_like(alpha)
+        dP = np.zeros_like(s)
+        self.fn["sw_param_grad"](_p(alpha), _p(s), _p(part), _p(dS), _p(U), _p(be), _p(W),
+                                 _p(dP), _p(ln), B, L1, L2, gap, T, ptype)
+        return dP
+
+    # ---------------- affine SW ----------------
+    def swa_forward(self, scores, lengths, go, ge, T):
+        s = _f32(scores)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        alpha = np.zeros((B, 3 * (L1 + 1) * (L2 + 1)), np.float32)
+        part = np.zeros((B,), np.float32)
+        self.fn["swa_forward"](_p(s), _p(alpha), _p(part), _p(ln), B, L1, L2, go, ge, T)
+        return alpha, part
+
+    def swa_backward(self, alpha, scores, part, lengths, go, ge, T):
+        s = _f32(scores)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        beta = np.zeros_like(alpha)
+        post = np.zeros_like(s)
+        g_o = np.zeros((B,), np.float32)
+        g_e = np.zeros((B,), np.float32)
+        gt = np.zeros((B,), np.float32)
+        self.fn["swa_backward"](_p(alpha), _p(s), _p(part), _p(beta), _p(post), _p(g_o),
+                                _p(g_e), _p(gt), _p(ln), B, L1, L2, go, ge, T)
+        return post, g_o, g_e, gt
+
+    def swa_hvp(self, alpha, scores, part, V, lengths, go, ge, T):
+        s = _f32(scores)
+        v = _f32(V)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        da = np.zeros_like(alpha)
+        dp = np.zeros((B,), np.float32)
+        dbe = np.zeros_like(alpha)
+        H = np.zeros_like(s)
+        self.fn["swa_hvp"](_p(alpha), _p(s), _p(part), _p(v), _p(da), _p(dp), _p(dbe),
+                           _p(H), _p(ln), B, L1, L2, go, ge, T)
+        return H, dp
+
+    def swa_param_grad(self, alpha, scores, part, dS, lengths, go, ge, T, ptype):
+        s = _f32(scores)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        dS = _f32(dS)
+        U = np.zeros_like(alpha)
+        be = np.zeros_like(alpha)
+        W = np.zeros_like(alpha)
+        dP = np.zeros_like(s)
+        self.fn["swa_param_grad"](_p(alpha), _p(s), _p(part), _p(dS), _p(U), _p(be),
+                                  _p(W), _p(dP), _p(ln), B, L1, L2, go, ge, T, ptype)
+        return dP
+
+    # ---------------- DTW ----------------
+    def dtw_forward(self, costs, lengths, T, bandwidth=-1):
+        c = _f32(costs)
+        B, L1, L2 = c.shape
+        ln = _lengths(lengths, B, L1, L2)
+        alpha = np.zeros((B, (L1 + 1) * (L2 + 1)), np.float32)
+        score = np.zeros((B,), np.float32)
+        self.fn["dtw_forward"](_p(c), _p(alpha), _p(score), _p(ln), B, L1, L2, T, bandwidth)
+        return alpha, score
+
+    def dtw_backward(self, alpha, costs, score, lengths, T, bandwidth=-1):
+        c = _f32(costs)
+        B, L1, L2 = c.shape
+        ln = _lengths(lengths, B, L1, L2)
+        beta = np.zeros_like(alpha)
+        post = np.zeros_like(c)
+        gt = np.zeros((B,), np.float32)
+        self.fn["dtw_backward"](_p(alpha), _p(c), _p(score), _p(beta), _p(post), _p(gt),
+                                _p(ln), B, L1, L2, T, bandwidth)
+        return post, gt
+
+    def dtw_hvp(self, alpha, costs, score, V, lengths, T, bandwidth=-1):
+        c = _f32(costs)
+        v = _f32(V)
+        B, L1, L2 = c.shape
+        ln = _lengths(lengths, B, L1, L2)
+        da = np.zeros_like(alpha)
+        ds = np.zeros((B,), np.float32)
+        be = np.zeros_like(alpha)
+        dbe = np.zeros_like(alpha)
+        H = np.zeros_like(c)
+        self.fn["dtw_hvp"](_p(alpha), _p(c), _p(score), _p(v), _p(da), _p(ds), _p(be),
+                           _p(dbe), _p(H), _p(ln), B, L1, L2, T, bandwidth)
+        return H, ds
+
+    def dtw_param_grad(self, alpha, costs, score, lengths, T, bandwidth=-1):
+        c = _f32(costs)
+        B, L1, L2 = c.shape
+        ln = _lengths(lengths, B, L1, L2)
+        U = np.zeros_like(alpha)
+        be = np.zeros_like(alpha)
+        W = np.zeros_like(alpha)
+        dP = np.zeros_like(c)
+        self.fn["dtw_param_grad"](_p(alpha), _p(c), _p(score), _p(U), _p(be), _p(W),
+                                  _p(dP), _p(ln), B, L1, L2, T, bandwidth)
+        return dP
+
+    # ---------------- binding-level composites ----------------
+    def soft_sw(self, scores, gap=-1.0, T=1.0, lengths=None):
+        """value, marginals, grad_gap, grad_T (src/sw/torch_cpu.cpp:114-165)."""
+        alpha, part = self.sw_forward(scores, lengths, gap, T)
+        post, gg, gt = self.sw_backward(alpha, scores, part, lengths, gap, T)
+        return part, post, gg, gt
+
+    def soft_sw_hvp(self, scores, V, gap=-1.0, T=1.0, lengths=None):
+        alpha, part = self.sw_forward(scores, lengths, gap, T)
+        return self.sw_hvp(alpha, scores, part, V, lengths, gap, T)[0]
+
+    def soft_sw_param_jacobian(self, scores, ptype, gap=-1.0, T=1.0, lengths=None):
+        alpha, part = self.sw_forward(scores, lengths, gap, T)
+        _, gg, gt = self.sw_backward(alpha, scores, part, lengths, gap, T)
+        return self.sw_param_grad(alpha, scores, part, gg if ptype == 0 else gt,
+                                  lengths, gap, T, ptype)
+
+    def soft_sw_affine(self, scores, go=-2.0, ge=-0.5, T=1.0, lengths=None):
+        alpha, part = self.swa_forward(scores, lengths, go, ge, T)
+        post, g_o, g_e, gt = self.swa_backward(alpha, scores, part, lengths, go, ge, T)
+        return part, post, g_o, g_e, gt
+
+    def soft_sw_affine_hvp(self, scores, V, go=-2.0, ge=-0.5, T=1.0, lengths=None):
+        alpha, part = self.swa_forward(scores, lengths, go, ge, T)
+        return self.swa_hvp(alpha, scores, part, V, lengths, go, ge, T)[0]
+
+    def soft_sw_affine_param_jacobian(self, scores, ptype, go=-2.0, ge=-0.5, T=1.0,
+                                      lengths=None):
+        alpha, part = self.swa_forward(scores, lengths, go, ge, T)
+        _, g_o, g_e, gt = self.swa_backward(alpha, scores, part, lengths, go, ge, T)
+        dS = (g_o, g_e, gt)[ptype]
+        return self.swa_param_grad(alpha, scores, part, dS, lengths, go, ge, T, ptype)
+
+    def soft_dtw(self, costs, T=1.0, lengths=None, bandwidth=-1):
+        alpha, score = self.dtw_forward(costs, lengths, T, bandwidth)
+        post, gt = self.dtw_backward(alpha, costs, score, lengths, T, bandwidth)
+        return score, post, gt
+
+    def soft_dtw_hvp(self, costs, V, T=1.0, lengths=None, bandwidth=-1):
+        alpha, score = self.dtw_forward(costs, lengths, T, bandwidth)
+        return self.dtw_hvp(alpha, costs, score, V, lengths, T, bandwidth)[0]
+
+    def soft_dtw_param_jacobian(self, costs, T=1.0, lengths=None, bandwidth=-1):
+        alpha, score = self.dtw_forward(costs, lengths, T, bandwidth)
+        return self.dtw_param_grad(alpha, costs, score, lengths, T, bandwidth)
+
+
+_cache = {}
+
+
+def get(kind: str = "oracle") -> CpuKernels:
+    if kind not in _cache:
+        _cache[kind] = CpuKernels(kind)
+    return _cache[kind]
+
+
+def reference_available() -> bool:
+    return os.path.exists(REF_LIB)
+
+
+def set_threads(n: int) -> None:
+    """Thread count for both libraries (OpenMP for the oracle, ATen for _ref)."""
+    lib = ctypes.CDLL(ORACLE_LIB)
+    try:
+        gomp = ctypes.CDLL("libgomp.so.1")
+        gomp.omp_set_num_threads(int(n))
+    except OSError:
+        pass
+    del lib
+    try:
+        import torch
+        torch.set_num_threads(int(n))
+    except Exception:
+        pass
+
+
+def build(quiet: bool = True) -> None:
+    """Compile liboracle.so (and _ref when /root/reference exists)."""
+    import subprocess
+    r = subprocess.run(["make", "-C", HERE, "all"], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("oracle build failed:\n" + r.stdout + r.stderr)
+    if not quiet:
+        print(r.stdout)

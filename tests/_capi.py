@@ -1,0 +1,80 @@
+"""ctypes binding of the C ABI in include/d2p_amd.h (libd2p_amd.so).
+
+GPU parity tests call the kernels through this boundary with device buffers
+owned by torch; no torch types cross it.
+"""
+import ctypes
+import os
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(ROOT, "d2p_amd", "libd2p_amd.so")
+HEADER = os.path.join(ROOT, "include", "d2p_amd.h")
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_z = ctypes.c_size_t
+_ll = ctypes.c_longlong
+
+SIGNATURES = {
+    "d2p_last_error": (ctypes.c_char_p, []),
+    "d2p_abi_version": (_i, []),
+    "d2p_sw_workspace_bytes": (_z, [_i, _i, _i]),
+    "d2p_sw_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _f, _p, _p, _p, _p, _p, _z, _p]),
+    "d2p_scale_by_batch": (_i, [_p, _p, _p, _i, _ll, _p]),
+}
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        _lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(_lib, name)
+            fn.restype = res
+            fn.argtypes = args
+    return _lib
+
+
+def check(rc):
+    if rc != 0:
+        raise RuntimeError(f"d2p C ABI call failed ({rc}): {lib().d2p_last_error().decode()}")
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def sw_forward_marginals(scores, lengths, gap, T):
+    """Returns (partition, marginals, grad_gap, grad_T) computed through the C ABI."""
+    import torch
+    B, L1, L2 = scores.shape
+    dev = scores.device
+    if lengths is None:
+        lengths = torch.tensor([[L1, L2]] * B, dtype=torch.int32, device=dev)
+    lengths = lengths.to(dev, torch.int32).contiguous()
+    part = torch.empty(B, device=dev)
+    marg = torch.empty(B, L1, L2, device=dev)
+    gg = torch.empty(B, device=dev)
+    gt = torch.empty(B, device=dev)
+    nbytes = lib().d2p_sw_workspace_bytes(B, L1, L2)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    check(lib().d2p_sw_forward_marginals(ptr(scores), ptr(lengths), B, L1, L2, gap, T,
+                                         ptr(part), ptr(marg), ptr(gg), ptr(gt), ptr(ws),
+                                         nbytes, stream()))
+    return part, marg, gg, gt
+
+
+def scale_by_batch(src, g):
+    import torch
+    out = torch.empty_like(src)
+    B = src.shape[0]
+    check(lib().d2p_scale_by_batch(ptr(src), ptr(g), ptr(out), B, src.numel() // B, stream()))
+    return out
