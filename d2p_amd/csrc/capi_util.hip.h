@@ -7,7 +7,23 @@
 
 namespace d2p_amd {
 void set_last_error(const char* fmt, ...);
+
+// Kernel timing hooks (see d2p_profile_enable): when enabled, every launch of
+// this library is bracketed by HIP events recorded on the launch stream.
+bool profiling_enabled();
+void profile_begin(hipStream_t stream, hipEvent_t* start);
+void profile_end(const char* name, hipStream_t stream, hipEvent_t start);
 }
+
+// Launches `kernel` and, when profiling is on, times it with events on `stream`.
+#define D2P_LAUNCH(name, kernel, grid, block, lds, stream, ...)                  \
+    do {                                                                         \
+        hipEvent_t ev0_ = nullptr;                                               \
+        const bool prof_ = d2p_amd::profiling_enabled();                         \
+        if (prof_) d2p_amd::profile_begin((stream), &ev0_);                     \
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);       \
+        if (prof_) d2p_amd::profile_end(name, (stream), ev0_);                   \
+    } while (0)
 
 #define D2P_OK 0
 #define D2P_ERR_ARG 1

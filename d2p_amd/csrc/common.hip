@@ -1,6 +1,12 @@
 // common.hip -- error state and batch-scaling kernel of the C ABI.
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
 
 #include "capi_util.hip.h"
 #include "dp_common.hip.h"
@@ -15,6 +21,57 @@ void set_last_error(const char* fmt, ...) {
     va_start(ap, fmt);
     vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
     va_end(ap);
+}
+
+// ---------------------------------------------------------------------------
+// kernel timing registry
+// ---------------------------------------------------------------------------
+namespace {
+struct PendingLaunch {
+    std::string name;
+    hipEvent_t start, end;
+};
+struct KernelStats {
+    long long count = 0;
+    double total_ms = 0.0, min_ms = 1e30, max_ms = 0.0;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<PendingLaunch> g_pending;
+std::map<std::string, KernelStats> g_stats;
+
+void resolve_pending_locked() {
+    for (auto& p : g_pending) {
+        hipEventSynchronize(p.end);
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, p.start, p.end) == hipSuccess) {
+            KernelStats& k = g_stats[p.name];
+            k.count += 1;
+            k.total_ms += ms;
+            k.min_ms = ms < k.min_ms ? ms : k.min_ms;
+            k.max_ms = ms > k.max_ms ? ms : k.max_ms;
+        }
+        hipEventDestroy(p.start);
+        hipEventDestroy(p.end);
+    }
+    g_pending.clear();
+}
+}  // namespace
+
+bool profiling_enabled() { return g_prof_on; }
+
+void profile_begin(hipStream_t stream, hipEvent_t* start) {
+    if (hipEventCreate(start) != hipSuccess) { *start = nullptr; return; }
+    hipEventRecord(*start, stream);
+}
+
+void profile_end(const char* name, hipStream_t stream, hipEvent_t start) {
+    if (!start) return;
+    hipEvent_t end;
+    if (hipEventCreate(&end) != hipSuccess) { hipEventDestroy(start); return; }
+    hipEventRecord(end, stream);
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    g_pending.push_back({name, start, end});
 }
 
 // dst = g[b] * src over [B, n]; float4 body when the row length allows it.
@@ -44,6 +101,34 @@ extern "C" const char* d2p_last_error(void) { return d2p_amd::g_last_error; }
 
 extern "C" int d2p_abi_version(void) { return 1; }
 
+extern "C" int d2p_profile_enable(int on) {
+    std::lock_guard<std::mutex> lk(d2p_amd::g_prof_mu);
+    d2p_amd::g_prof_on = on != 0;
+    return D2P_OK;
+}
+
+extern "C" void d2p_profile_reset(void) {
+    std::lock_guard<std::mutex> lk(d2p_amd::g_prof_mu);
+    d2p_amd::resolve_pending_locked();
+    d2p_amd::g_stats.clear();
+}
+
+extern "C" int d2p_profile_report(char* buf, size_t len) {
+    std::lock_guard<std::mutex> lk(d2p_amd::g_prof_mu);
+    d2p_amd::resolve_pending_locked();
+    std::string out;
+    char line[256];
+    for (auto& kv : d2p_amd::g_stats) {
+        const auto& k = kv.second;
+        snprintf(line, sizeof(line), "%s %lld %.6f %.6f %.6f\n", kv.first.c_str(), k.count,
+                 k.total_ms, k.min_ms, k.max_ms);
+        out += line;
+    }
+    D2P_REQUIRE(buf != nullptr && len > out.size(), "report buffer too small");
+    memcpy(buf, out.c_str(), out.size() + 1);
+    return D2P_OK;
+}
+
 extern "C" int d2p_scale_by_batch(const float* src, const float* g, float* dst, int B,
                                   long long per_batch, void* stream) {
     D2P_REQUIRE(B >= 0 && per_batch >= 0, "negative size");
@@ -54,8 +139,8 @@ extern "C" int d2p_scale_by_batch(const float* src, const float* g, float* dst, 
     const long long work = vec ? total / 4 : total;
     long long blocks = (work + 255) / 256;
     if (blocks > 256 * 64) blocks = 256 * 64;
-    hipLaunchKernelGGL(d2p_amd::scale_by_batch_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                       (hipStream_t)stream, src, g, dst, per_batch, work, vec ? 1 : 0);
+    D2P_LAUNCH("scale_by_batch", d2p_amd::scale_by_batch_kernel, dim3((unsigned)blocks),
+               dim3(256), 0, (hipStream_t)stream, src, g, dst, per_batch, work, vec ? 1 : 0);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }

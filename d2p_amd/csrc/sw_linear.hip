@@ -415,13 +415,13 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
     D2P_HIP(hipFuncSetAttribute((const void*)sw::sw_backward_kernel<sw::PB>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
     float* alpha_sk = (float*)workspace;
-    hipLaunchKernelGGL(sw::sw_forward_kernel<sw::PF>, dim3(B), dim3(sw::NW * 64), lds_f, st,
-                       scores, lengths, alpha_sk, partition, max_L1, max_L2, ns, gap,
-                       temperature, ring_f);
+    D2P_LAUNCH("sw_forward", sw::sw_forward_kernel<sw::PF>, dim3(B), dim3(sw::NW * 64), lds_f,
+               st, scores, lengths, alpha_sk, partition, max_L1, max_L2, ns, gap, temperature,
+               ring_f);
     D2P_HIP(hipGetLastError());
-    hipLaunchKernelGGL(sw::sw_backward_kernel<sw::PB>, dim3(B), dim3(sw::NW * 64), lds_b, st,
-                       scores, lengths, alpha_sk, partition, marginals, grad_gap, grad_T,
-                       max_L1, max_L2, ns, gap, temperature, ring_b);
+    D2P_LAUNCH("sw_backward", sw::sw_backward_kernel<sw::PB>, dim3(B), dim3(sw::NW * 64),
+               lds_b, st, scores, lengths, alpha_sk, partition, marginals, grad_gap, grad_T,
+               max_L1, max_L2, ns, gap, temperature, ring_b);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }

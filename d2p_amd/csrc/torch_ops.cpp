@@ -152,33 +152,60 @@ SwOut sw_run(const Tensor& scores, const Tensor& lengths, const Dims& d, float g
 
 // Autograd semantics of SoftSWRegularCUDAFunction
 // (/root/reference/src/sw/torch_cuda.cpp:178-411): outputs {value, marginals};
-// d value / d scores = marginals, so backward scales the saved marginals.
-class SoftSWFunction : public torch::autograd::Function<SoftSWFunction> {
+// d value / d scores = marginals, so backward scales the saved marginals, and
+// the parameter gradients are sum_b grad_value[b] * dS_b/dtheta, shape [1].
+// Two Function classes share this logic: float parameters (no parameter
+// inputs) and tensor parameters (gap / temperature receive gradients).
+tensor_list sw_autograd_forward(AutogradContext* ctx, const Tensor& scores,
+                                const Tensor& lengths, double gap, double temperature) {
+    ctx->set_materialize_grads(false);
+    CHECK_INPUT_DEV(scores);
+    Dims d = checked_dims(scores, "SW");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    SwOut o = sw_run(scores, lengths, d, (float)gap, (float)temperature);
+    ctx->save_for_backward({o.marginals, o.grad_gap, o.grad_T});
+    return {o.partition, o.marginals};
+}
+
+// returns {grad_scores, grad_gap, grad_T}
+tensor_list sw_autograd_backward(AutogradContext* ctx, const tensor_list& grads,
+                                 bool want_gap, bool want_T) {
+    auto saved = ctx->get_saved_variables();
+    Tensor marg = saved[0], ggap = saved[1], gT = saved[2];
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(marg.device());
+    Tensor grad_value = grads[0], grad_marg = grads[1];
+    Tensor grad_scores, grad_gap, grad_T;
+    if (grad_value.defined() && grad_value.numel() > 0) {
+        grad_scores = scale_by_batch(marg, grad_value);
+        if (want_gap) grad_gap = grad_param_sum(grad_value, ggap);
+        if (want_T) grad_T = grad_param_sum(grad_value, gT);
+    }
+    if (grad_marg.defined() && grad_marg.numel() > 0) not_yet("soft_sw marginal-path backward");
+    return {grad_scores, grad_gap, grad_T};
+}
+
+class SoftSWFloatFunction : public torch::autograd::Function<SoftSWFloatFunction> {
+   public:
+    static tensor_list forward(AutogradContext* ctx, Tensor scores, Tensor lengths, double gap,
+                               double temperature) {
+        return sw_autograd_forward(ctx, scores, lengths, gap, temperature);
+    }
+    static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
+        auto g = sw_autograd_backward(ctx, grads, false, false);
+        return {g[0], Tensor(), Tensor(), Tensor()};
+    }
+};
+
+class SoftSWTensorFunction : public torch::autograd::Function<SoftSWTensorFunction> {
    public:
     static tensor_list forward(AutogradContext* ctx, Tensor scores, Tensor gap_t, Tensor temp_t,
                                Tensor lengths, double gap, double temperature) {
-        ctx->set_materialize_grads(false);
-        CHECK_INPUT_DEV(scores);
-        Dims d = checked_dims(scores, "SW");
-        c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
-        SwOut o = sw_run(scores, lengths, d, (float)gap, (float)temperature);
-        ctx->save_for_backward({o.marginals, o.grad_gap, o.grad_T});
-        return {o.partition, o.marginals};
+        return sw_autograd_forward(ctx, scores, lengths, gap, temperature);
     }
-
     static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
-        auto saved = ctx->get_saved_variables();
-        Tensor marg = saved[0], ggap = saved[1], gT = saved[2];
-        c10::hip::HIPGuardMasqueradingAsCUDA guard(marg.device());
-        Tensor grad_value = grads[0], grad_marg = grads[1];
-        Tensor grad_scores, grad_gap, grad_T;
-        if (grad_value.defined() && grad_value.numel() > 0) {
-            grad_scores = scale_by_batch(marg, grad_value);
-            if (ctx->needs_input_grad(1)) grad_gap = grad_param_sum(grad_value, ggap);
-            if (ctx->needs_input_grad(2)) grad_T = grad_param_sum(grad_value, gT);
-        }
-        if (grad_marg.defined() && grad_marg.numel() > 0) not_yet("soft_sw marginal-path backward");
-        return {grad_scores, grad_gap, grad_T, Tensor(), Tensor(), Tensor()};
+        auto g = sw_autograd_backward(ctx, grads, ctx->needs_input_grad(1),
+                                      ctx->needs_input_grad(2));
+        return {g[0], g[1], g[2], Tensor(), Tensor(), Tensor()};
     }
 };
 
@@ -189,7 +216,7 @@ std::vector<Tensor> soft_sw_t(Tensor scores, Tensor gap, Tensor temperature, Ten
     const float g = scalar_value(gap, "gap");
     const float T = scalar_value(temperature, "temperature");
     Tensor l = resolve_lengths(lengths, d, scores.device());
-    return SoftSWFunction::apply(scores, gap, temperature, l, g, T);
+    return SoftSWTensorFunction::apply(scores, gap, temperature, l, g, T);
 }
 
 std::vector<Tensor> soft_sw_float(Tensor scores, double gap, double temperature,
@@ -198,7 +225,7 @@ std::vector<Tensor> soft_sw_float(Tensor scores, double gap, double temperature,
     Dims d = checked_dims(scores, "SW");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
     Tensor l = resolve_lengths(lengths, d, scores.device());
-    return SoftSWFunction::apply(scores, Tensor(), Tensor(), l, gap, temperature);
+    return SoftSWFloatFunction::apply(scores, l, gap, temperature);
 }
 
 std::tuple<Tensor, Tensor, Tensor, Tensor> soft_sw_with_grads(Tensor scores, double gap,

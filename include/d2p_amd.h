@@ -30,6 +30,16 @@ const char* d2p_last_error(void);
 /* ABI version of this library (incremented on incompatible changes). */
 int d2p_abi_version(void);
 
+/* Kernel timing (instrumentation; no counterpart in the reference, which has no
+ * tracing).  While enabled, every kernel this library launches is bracketed by
+ * HIP events recorded on the launch stream.  d2p_profile_report() waits for the
+ * recorded events and writes one line per kernel name:
+ *   "<name> <launches> <total_ms> <min_ms> <max_ms>\n"
+ * d2p_profile_reset() drops the accumulated statistics. */
+int d2p_profile_enable(int on);
+int d2p_profile_report(char* buf, size_t len);
+void d2p_profile_reset(void);
+
 /* ---------------------------------------------------------------------------
  * Linear-gap soft Smith-Waterman
  * ------------------------------------------------------------------------- */
