@@ -55,6 +55,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 struct OnlineLSE {
     float m, z;
     __device__ __forceinline__ void init() { m = kNINF; z = 0.0f; }
+    // Starting state that lets add() take NINF (invalid) cells without a branch:
+    // they can only accumulate at the NINF scale, which the first finite cell
+    // wipes out (its d is huge, so z restarts at 1), and merge() drops a state
+    // whose m is still <= NINF.
+    __device__ __forceinline__ void init_open() { m = -3.0e38f; z = 0.0f; }
     __device__ __forceinline__ void add(float x, float c) {
         float d = (x - m) * c;
         float e = fast_exp2(-fabsf(d));

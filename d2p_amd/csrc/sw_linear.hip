@@ -72,6 +72,26 @@ __device__ __forceinline__ int stripe_at(int gc, int wave, int lag, int nch, int
     return q;
 }
 
+// Steps stored per stripe in the skewed alpha table: whole forward chunks plus the
+// two leading steps t = -2, -1 (always NINF), so every chunk stores unconditionally.
+__host__ __device__ inline int stored_steps(int L2max) {
+    return ((L2max + 63 + PF - 1) / PF) * PF + 2;
+}
+
+// Shift registers that gather one lane's per-step value across a chunk of P steps:
+// push_from_top: lane 63 inserts, everything moves down one lane per step, so after
+//   the chunk lane 64-P+u holds step u's value;
+// push_from_bottom: lane 0 inserts, everything moves up one lane per step, so lane
+//   P-1-u holds step u's value.
+__device__ __forceinline__ float push_from_top(float reg, float v, int lane) {
+    const float moved = wave_shl1(reg, 0.0f);
+    return lane == 63 ? v : moved;
+}
+__device__ __forceinline__ float push_from_bottom(float reg, float v, int lane) {
+    const float moved = wave_shr1(reg, 0.0f);
+    return lane == 0 ? v : moved;
+}
+
 template <int P>
 __global__ void __launch_bounds__(NW * 64)
 sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
@@ -95,10 +115,11 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     const int nch = (nsteps + P - 1) / P;
     const int lag = stripe_lag<P>(nch);
     const int total = (NS > 0 && L2 > 0) ? (NS - 1) * lag + nch : 0;
-    const size_t NT = (size_t)L2max + 65;
+    const size_t NT = (size_t)stored_steps(L2max);
+    const float* sbase = scores + (size_t)b * L1max * L2max;
 
     OnlineLSE acc;
-    acc.init();
+    acc.init_open();
     float cur = kNINF, up_prev = kNINF;
     float nxt[P];
 
@@ -107,13 +128,10 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
         const int s = stripe_at(gc, wave, lag, nch, NS, &k);
         if (s >= 0) {
             const int i0 = s * 64;
-            const int row = i0 + lane;
-            const bool row_ok = row < L1;
+            const bool row_ok = i0 + lane < L1;
             const int t0 = k * P;
-            const float* srow = scores + (size_t)b * L1max * L2max;
-            // stage this chunk's score parallelogram (first chunk of a stripe only;
-            // later chunks were prefetched during the previous chunk)
             if (k == 0) {
+                // first chunk of a stripe: stage its scores now, reset the row state
                 cur = kNINF;
                 up_prev = kNINF;
 #pragma unroll
@@ -121,51 +139,61 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                     const int rl = q * (64 / P) + lane / P, u = lane % P;
                     const int col = t0 + u - rl, grow = i0 + rl;
                     float v = 0.0f;
-                    if (grow < L1 && col >= 0 && col < L2) v = srow[(size_t)grow * L2max + col];
+                    if (grow < L1 && col >= 0 && col < L2) v = sbase[(size_t)grow * L2max + col];
                     tile[rl * (P + 1) + u] = v;
                 }
             }
-            // prefetch the next chunk
             const bool has_next = (k + 1) < nch;
-            if (has_next) {
+            if (has_next) {  // prefetch the next chunk's scores into registers
 #pragma unroll
                 for (int q = 0; q < P; ++q) {
                     const int rl = q * (64 / P) + lane / P, u = lane % P;
                     const int col = t0 + P + u - rl, grow = i0 + rl;
                     float v = 0.0f;
-                    if (grow < L1 && col >= 0 && col < L2) v = srow[(size_t)grow * L2max + col];
+                    if (grow < L1 && col >= 0 && col < L2) v = sbase[(size_t)grow * L2max + col];
                     nxt[q] = v;
                 }
             }
-            wave_lds_sync();
             float* out = alpha_sk + ((size_t)b * NSmax + s) * NT * 64 + lane;
             if (k == 0) { out[0] = kNINF; out[64] = kNINF; }  // steps t = -2, -1
-            const float* ring_up = rings + ((wave + NW - 1) % NW) * ring_len;
-            float* ring_me = rings + wave * ring_len;
-            const int i = row + 1;
+            // lane 0's up values for this chunk (bottom row of the stripe above):
+            // lane u of `ring_vals` holds column t0 + u
+            float ring_vals = kNINF;
+            if (s > 0 && lane < P)
+                ring_vals = rings[((wave + NW - 1) % NW) * ring_len + ((t0 + lane) & rmask)];
+            wave_lds_sync();
+            float sv[P];
+#pragma unroll
+            for (int u = 0; u < P; ++u) sv[u] = tile[lane * (P + 1) + u];
+            float bottom = kNINF;  // gathers lane 63's alpha of every step (push_from_top)
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t0 + u;
                 const int col = t - lane;
-                const bool ok = row_ok && col >= 0 && col < L2;
-                const float sv = tile[lane * (P + 1) + u];
+                const bool ok = row_ok && (unsigned)col < (unsigned)L2;
                 float up = wave_shr1(cur, kNINF);
-                const float rv = (s > 0) ? ring_up[t & rmask] : kNINF;
-                if (lane == 0) up = rv;
+                const float r0 = lane_bcast(ring_vals, u);
+                up = (lane == 0) ? r0 : up;
                 const float diag = up_prev;
                 up_prev = up;
-                const int j = col + 1;
-                const float vd = (i > 1 && j > 1) ? diag + sv : kNINF;
-                const float vu = (i > 1) ? up + gap : kNINF;
-                const float vl = (j > 1) ? cur + gap : kNINF;
-                const float m = fmaxf(fmaxf(vd, vu), fmaxf(vl, sv));
+                // out-of-table neighbours are NINF, so no i>1 / j>1 guards are needed
+                const float vd = diag + sv[u];
+                const float vu = up + gap;
+                const float vl = cur + gap;
+                const float m = fmaxf(fmaxf(vd, vu), fmaxf(vl, sv[u]));
                 const float sum = fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c) +
-                                  fast_exp2((vl - m) * c) + fast_exp2((sv - m) * c);
+                                  fast_exp2((vl - m) * c) + fast_exp2((sv[u] - m) * c);
                 const float a = m + tl * fast_log2(sum);
                 cur = ok ? a : kNINF;
-                if (t < nsteps) out[(size_t)(t + 2) * 64] = cur;
-                if (lane == 63 && ok) ring_me[col & rmask] = cur;
-                if (ok) acc.add(cur, c);
+                out[(size_t)(t + 2) * 64] = cur;
+                bottom = push_from_top(bottom, cur, lane);
+                acc.add(cur, c);
+            }
+            // publish lane 63's row for the stripe below: lane 64-P+u holds step u,
+            // whose lane-63 column is t0+u-63
+            if (lane >= 64 - P) {
+                const int col = t0 + (lane - (64 - P)) - 63;
+                if (col >= 0 && col < L2) rings[wave * ring_len + (col & rmask)] = bottom;
             }
             if (has_next) {
 #pragma unroll
@@ -217,15 +245,15 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     const int nch = (nsteps + P - 1) / P;
     const int lag = stripe_lag<P>(nch);
     const int total = (NS > 0 && L2 > 0) ? (NS - 1) * lag + nch : 0;
-    const size_t NT = (size_t)L2max + 65;
-    const float* srow = scores + (size_t)b * L1max * L2max;
-    float* prow = post + (size_t)b * L1max * L2max;
+    const size_t NT = (size_t)stored_steps(L2max);
+    const float* sbase = scores + (size_t)b * L1max * L2max;
+    float* pbase = post + (size_t)b * L1max * L2max;
 
     // zero the padded part of the marginal matrix
     if (L1 < L1max || L2 < L2max) {
         for (size_t idx = threadIdx.x; idx < (size_t)L1max * L2max; idx += NW * 64) {
             const int r = (int)(idx / L2max), cc = (int)(idx % L2max);
-            if (r >= L1 || cc >= L2) prow[idx] = 0.0f;
+            if (r >= L1 || cc >= L2) pbase[idx] = 0.0f;
         }
     }
 
@@ -239,11 +267,10 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         if (q >= 0) {
             const int s = NS - 1 - q;
             const int i0 = s * 64;
-            const int row = i0 + lane;
-            const bool row_ok = row < L1;
+            const bool row_ok = i0 + lane < L1;
             const int t_hi = nsteps - 1 - k * P;
             const float* abase = alpha_sk + ((size_t)b * NSmax + s) * NT * 64 + lane;
-            const float* aup = alpha_sk + ((size_t)b * NSmax + (s - 1)) * NT * 64 + 63;
+            const float* aup = alpha_sk + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT * 64 + 63;
             if (k == 0) {
                 in_left = in_up = in_diag = in_diag_next = 0.0f;
 #pragma unroll
@@ -251,7 +278,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     const int rl = qq * (64 / P) + lane / P, u = lane % P;
                     const int col = t_hi - u - rl, grow = i0 + rl;
                     float v = 0.0f;
-                    if (grow < L1 && col >= 0 && col < L2) v = srow[(size_t)grow * L2max + col];
+                    if (grow < L1 && col >= 0 && col < L2) v = sbase[(size_t)grow * L2max + col];
                     tile[rl * (P + 1) + u] = v;
                 }
 #pragma unroll
@@ -266,14 +293,14 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 }
             }
             const bool has_next = (k + 1) < nch;
-            if (has_next) {
+            if (has_next) {  // prefetch scores, own alpha and the row above for the next chunk
                 const int th2 = t_hi - P;
 #pragma unroll
                 for (int qq = 0; qq < P; ++qq) {
                     const int rl = qq * (64 / P) + lane / P, u = lane % P;
                     const int col = th2 - u - rl, grow = i0 + rl;
                     float v = 0.0f;
-                    if (grow < L1 && col >= 0 && col < L2) v = srow[(size_t)grow * L2max + col];
+                    if (grow < L1 && col >= 0 && col < L2) v = sbase[(size_t)grow * L2max + col];
                     nxt[qq] = v;
                 }
 #pragma unroll
@@ -287,59 +314,75 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     if (t <= nsteps - 1) nBv = aup[(size_t)(t + 2) * 64];
                 }
             }
-            wave_lds_sync();
-            const float* rU_in = ringU + wave * ring_len;            // from stripe s+1
-            const float* rD_in = ringD + wave * ring_len;
-            float* rU_out = ringU + ((wave + 1) % NW) * ring_len;   // to stripe s-1
-            float* rD_out = ringD + ((wave + 1) % NW) * ring_len;
+            // contributions from the stripe below for lane 63, columns t_hi-u-63 (up)
+            // and t_hi-u-62 (diagonal): lane u of preU / preD holds step u's value
             const bool below = (s + 1) < NS;
-            const int i = row + 1;
+            float preU = 0.0f, preD = 0.0f;
+            if (below && lane < P) {
+                const int tt = t_hi - lane;
+                preU = ringU[wave * ring_len + ((tt - 63) & rmask)];
+                preD = ringD[wave * ring_len + ((tt - 62) & rmask)];
+            }
+            wave_lds_sync();
+            float sv[P];
+#pragma unroll
+            for (int u = 0; u < P; ++u) sv[u] = tile[lane * (P + 1) + u];
+            float topU = 0.0f, topD = 0.0f;  // gather lane 0's outputs (push_from_bottom)
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t_hi - u;
                 const int col = t - lane;
-                const int j = col + 1;
-                const bool ok = row_ok && col >= 0 && col < L2;
-                const float sv = tile[lane * (P + 1) + u];
+                const bool ok = row_ok && (unsigned)col < (unsigned)L2;
                 const float a0 = A[u], a1 = A[u + 1];
                 float upa = wave_shr1(a1, kNINF);
                 float dga = wave_shr1(A[u + 2], kNINF);
                 const float bu0 = lane_bcast(Bv, u);
                 const float bd0 = lane_bcast(Bv, u + 1);
-                if (lane == 0) { upa = bu0; dga = bd0; }
-                // contributions from the stripe below reach lane 63 through the ring
-                const float ru = below ? rU_in[(t - 63) & rmask] : 0.0f;
-                const float rd = below ? rD_in[(t - 62) & rmask] : 0.0f;
-                if (lane == 63) { in_up = ru; in_diag = rd; }
+                upa = (lane == 0) ? bu0 : upa;
+                dga = (lane == 0) ? bd0 : dga;
+                const float ru = lane_bcast(preU, u);
+                const float rd = lane_bcast(preD, u);
+                in_up = (lane == 63) ? ru : in_up;
+                in_diag = (lane == 63) ? rd : in_diag;
 
-                const float vd = (i > 1 && j > 1) ? dga + sv : kNINF;
-                const float vu = (i > 1) ? upa + gap : kNINF;
-                const float vl = (j > 1) ? a1 + gap : kNINF;
-                const float m = fmaxf(fmaxf(vd, vu), fmaxf(vl, sv));
+                // out-of-table predecessors are NINF: no i>1 / j>1 guards needed
+                const float vd = dga + sv[u];
+                const float vu = upa + gap;
+                const float vl = a1 + gap;
+                const float m = fmaxf(fmaxf(vd, vu), fmaxf(vl, sv[u]));
                 const float e0 = fast_exp2((vd - m) * c), e1 = fast_exp2((vu - m) * c);
-                const float e2 = fast_exp2((vl - m) * c), e3 = fast_exp2((sv - m) * c);
+                const float e2 = fast_exp2((vl - m) * c), e3 = fast_exp2((sv[u] - m) * c);
                 const float rin = fast_rcp(((e0 + e1) + e2) + e3);
                 const float w0 = e0 * rin, w1 = e1 * rin, w2 = e2 * rin, w3 = e3 * rin;
                 float lp = (a0 - S) * c;
                 lp = lp < 0.0f ? lp : 0.0f;
                 const float binit = fast_exp2(lp);
+                // reference accumulation order: init, diagonal, left, up successor
                 float beta = ((binit + in_diag) + in_left) + in_up;
                 const bool live = ok && (beta != 0.0f) && (fabsf(beta) <= 3.0e38f);
                 beta = live ? beta : 0.0f;
                 const float pv = live ? beta * (w0 + w3) : 0.0f;
-                if (ok) tile[lane * (P + 1) + u] = pv;
                 const float od = live ? beta * w0 : 0.0f;
                 const float ou = live ? beta * w1 : 0.0f;
                 const float ol = live ? beta * w2 : 0.0f;
+                tile[lane * (P + 1) + u] = pv;
                 g_acc += ou;
                 g_acc += ol;
-                p_acc += pv * sv;
-                // lane 0 hands its up/diag contributions to the stripe above
-                if (lane == 0) { rU_out[t & rmask] = ou; rD_out[t & rmask] = od; }
+                p_acc += pv * sv[u];
+                topU = push_from_bottom(topU, ou, lane);
+                topD = push_from_bottom(topD, od, lane);
                 in_left = ol;
                 in_up = wave_shl1(ou, 0.0f);
                 in_diag = in_diag_next;
                 in_diag_next = wave_shl1(od, 0.0f);
+            }
+            // hand lane 0's up / diagonal contributions to the stripe above: lane P-1-u
+            // holds step u, whose lane-0 column is t_hi-u
+            if (lane < P) {
+                const int tt = t_hi - (P - 1 - lane);
+                const int slot = ((wave + 1) % NW) * ring_len + (tt & rmask);
+                ringU[slot] = topU;
+                ringD[slot] = topD;
             }
             wave_lds_sync();
             // write this chunk's marginals (contiguous row segments)
@@ -348,7 +391,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const int rl = qq * (64 / P) + lane / P, u = lane % P;
                 const int col = t_hi - u - rl, grow = i0 + rl;
                 if (grow < L1 && col >= 0 && col < L2)
-                    prow[(size_t)grow * L2max + col] = tile[rl * (P + 1) + u];
+                    pbase[(size_t)grow * L2max + col] = tile[rl * (P + 1) + u];
             }
             wave_lds_sync();
             if (has_next) {
@@ -387,7 +430,7 @@ using namespace d2p_amd;
 extern "C" size_t d2p_sw_workspace_bytes(int B, int max_L1, int max_L2) {
     if (B <= 0 || max_L1 <= 0 || max_L2 <= 0) return 0;
     const size_t ns = ((size_t)max_L1 + 63) / 64;
-    return (size_t)B * ns * ((size_t)max_L2 + 65) * 64 * sizeof(float);
+    return (size_t)B * ns * (size_t)sw::stored_steps(max_L2) * 64 * sizeof(float);
 }
 
 extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths, int B,
