@@ -39,6 +39,18 @@ __device__ __forceinline__ float wave_shl1(float v, float fill) {
         __float_as_int(fill), __float_as_int(v), 0x130, 0xf, 0xf, false));
 }
 
+// DPP shifts whose boundary lane takes its value from `old` (per lane) instead of a
+// constant: with these, lane 0 / lane 63 read a neighbour value staged in a register
+// with no extra select.
+__device__ __forceinline__ float wave_shr1_or(float v, float old) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(
+        __float_as_int(old), __float_as_int(v), 0x138, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_shl1_or(float v, float old) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(
+        __float_as_int(old), __float_as_int(v), 0x130, 0xf, 0xf, false));
+}
+
 __device__ __forceinline__ float lane_bcast(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }

@@ -8,24 +8,31 @@
 //      alpha[0,0] = 0, rest of row/col 0 = NINF,  S = LSE_T over cells 0..L1 x 0..L2.
 //
 // Mapping (one workgroup per batch element, NW wave64s):
-//   * rows are cut into 64-row stripes; lane r of the wave that owns stripe s
+//   * rows are cut into 64-row stripes; stripe s belongs to wave s % NW.  Lane r
 //     holds DP row 64*s+r+1 and sweeps the columns with a one-column skew per lane
-//     (lane r works on column t-r at step t), so the 64 cells a wave computes at a
-//     step lie on one anti-diagonal;
-//   * the up / diagonal neighbours come from lane r-1 through a DPP wave shift;
-//     lane 0 gets them from the stripe above through an LDS ring written by that
-//     stripe's lane 63;
-//   * stripes form a software pipeline: stripe s runs `lag` chunks of P steps
-//     behind stripe s-1; all waves meet at a workgroup barrier after every chunk;
-//   * scores (and, in the backward, marginals) are staged per chunk through a
-//     padded LDS tile so every HBM access is a contiguous row segment;
-//   * the forward stores alpha in a skewed layout alpha_sk[b][stripe][t][lane],
-//     one contiguous 256-byte vector per wave step, which the backward streams back
-//     in reverse.
-// The backward is the reverse sweep of the reference (scatter form, no atomics):
-// every cell receives its successors' contributions from the DPP neighbour or its
-// own previous step, in the reference's accumulation order
+//     (lane r works on column t-r at step t), so a wave's 64 cells at one step lie on
+//     one anti-diagonal;
+//   * the up / diagonal neighbours come from lane r-1 through a DPP wave shift; the
+//     boundary lane reads the stripe above through an LDS ring, staged in the DPP
+//     "old" operand;
+//   * waves do not meet at barriers: each wave publishes its progress (stripe, chunks
+//     done) in LDS with release semantics, and a stripe waits, chunk by chunk, only
+//     for the part of the stripe above it reads (and, so that the ring is not
+//     overwritten, for the stripe below to have caught up);
+//   * scores (and, in the backward, marginals) are staged per chunk of P steps through
+//     a padded LDS tile so every HBM access is a contiguous row segment;
+//   * the forward stores alpha in a skewed layout alpha_sk[b][stripe][t][lane], one
+//     contiguous 256-byte vector per wave step, which the backward streams back in
+//     reverse.
+// The backward is the reverse sweep of the reference (scatter form, no atomics): each
+// cell receives its successors' contributions from the DPP neighbour or from its own
+// previous step, in the reference's accumulation order
 //   beta = ((beta_init + from(i+1,j+1)) + from(i,j+1)) + from(i+1,j).
+//
+// Every wait is bounded: a wave that spins SPIN_LIMIT times sets bit 0 of the
+// element's status word and goes on, so a logic error can never hang the GPU.
+
+#include <vector>
 
 #include "dp_common.hip.h"
 #include "../../include/d2p_amd.h"
@@ -34,146 +41,161 @@
 namespace d2p_amd {
 namespace sw {
 
-constexpr int NW = 8;      // waves per workgroup
-constexpr int PF = 32;     // steps per chunk, forward sweep
-constexpr int PB = 16;     // steps per chunk, backward sweep (holds more state per step)
+constexpr int NW = 8;                // waves per workgroup
+constexpr int PF = 16;               // steps per chunk, forward sweep
+constexpr int PB = 8;                // steps per chunk, backward sweep (more state per step)
+constexpr int SPIN_LIMIT = 1 << 22;  // ~0.2 s of polling before giving up
+constexpr int PROG_STRIDE = 1 << 16; // progress word = stripe * PROG_STRIDE + chunks done
+constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do not publish
 
-// Chunks of lag between consecutive stripes: lane 63 of stripe s-1 produces
-// column c at step c+63 and lane 0 of stripe s consumes it at step c, so the
-// producer's chunk must precede the consumer's (63/P + 2 chunks); and a wave's
-// next stripe must start only after its previous one ended, (NW-1)*lag >= nch,
-// which also keeps the LDS rings free of overlap between pipeline generations.
-template <int P>
-__host__ __device__ inline int stripe_lag(int nch) {
-    const int lagmin = 63 / P + 2;
-    int l = (nch + NW - 2) / (NW - 1);
-    return l > lagmin ? l : lagmin;
+// A stripe's chunk k reads boundary values the neighbouring stripe produces up to
+// 62 + P steps later in its own sweep, i.e. in its chunk k + 1 + 62/P; so it waits
+// until that stripe has completed k + lead(P) chunks.
+constexpr int lead(int P) { return 2 + 62 / P; }
+
+// Ring length (columns) of one stripe boundary.  It must exceed the pipeline window
+// (LEAD chunks plus back-pressure slack); when a wave owns several stripes (more
+// than NW stripes) it must also satisfy NW * R > L2 + 64 + 4P, which rules out a
+// cycle of back-pressure waits across a whole round of waves.
+__host__ inline int ring_len(int max_L1, int max_L2) {
+    const int ns = (max_L1 + 63) / 64;
+    int r = 256;
+    if (ns > NW) {
+        const int need = (max_L2 + 64 + 4 * PF + NW - 1) / NW + 1;
+        r = r > need ? r : need;
+    }
+    return (r + PF - 1) / PF * PF;   // a multiple of both chunk lengths
 }
 
-template <int P>
-__host__ inline int ring_len_for(int L2max) {
-    int nch = (L2max + 63 + P - 1) / P;
-    int need = (stripe_lag<P>(nch) + 2) * P;
-    int r = 64;
-    while (r < need) r <<= 1;
-    return r;
-}
-
-// Stripe scheduled at global chunk gc for this wave, or -1.  Stripe order q runs
-// 0..NS-1 and starts at chunk q*lag; stripes of one wave never overlap in time.
-__device__ __forceinline__ int stripe_at(int gc, int wave, int lag, int nch, int NS, int* k) {
-    int qmax = gc / lag;
-    if (qmax > NS - 1) qmax = NS - 1;
-    if (qmax < wave) return -1;
-    int q = qmax - ((qmax - wave) % NW);
-    int kk = gc - q * lag;
-    if (kk >= nch) return -1;
-    *k = kk;
-    return q;
-}
-
-// Steps stored per stripe in the skewed alpha table: whole forward chunks plus the
-// two leading steps t = -2, -1 (always NINF), so every chunk stores unconditionally.
+// Steps stored per stripe in the skewed alpha table: whole chunks plus the two
+// leading steps t = -2, -1 (always NINF).
 __host__ __device__ inline int stored_steps(int L2max) {
     return ((L2max + 63 + PF - 1) / PF) * PF + 2;
 }
 
-// Shift registers that gather one lane's per-step value across a chunk of P steps:
-// push_from_top: lane 63 inserts, everything moves down one lane per step, so after
-//   the chunk lane 64-P+u holds step u's value;
-// push_from_bottom: lane 0 inserts, everything moves up one lane per step, so lane
-//   P-1-u holds step u's value.
-__device__ __forceinline__ float push_from_top(float reg, float v, int lane) {
-    const float moved = wave_shl1(reg, 0.0f);
-    return lane == 63 ? v : moved;
+__host__ inline size_t status_bytes(int B) { return ((size_t)B * sizeof(int) + 255) / 256 * 256; }
+
+__device__ __forceinline__ void publish(int* prog, int wave, int value) {
+    __hip_atomic_store(prog + wave, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-__device__ __forceinline__ float push_from_bottom(float reg, float v, int lane) {
-    const float moved = wave_shr1(reg, 0.0f);
-    return lane == 0 ? v : moved;
+
+// Waits until prog[w] >= need; bounded.  The loaded value is made wave-uniform.
+__device__ __forceinline__ void wait_for(int* prog, int w, int need, int* status_b) {
+    int spins = 0;
+    while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(
+               prog + w, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) < need) {
+        __builtin_amdgcn_s_sleep(2);
+        if (++spins >= SPIN_LIMIT) {
+            atomicOr(status_b, 1);
+            return;
+        }
+    }
+}
+
+__device__ __forceinline__ int ring_index(int slot, int R) {
+    slot %= R;
+    return slot < 0 ? slot + R : slot;
+}
+
+// Loads the score parallelogram of one chunk into this lane's registers: value q
+// belongs to row rl(q) = q*(64/P) + lane/P and step u(q) = lane%P, i.e. the cell at
+// column t_first + dir*u - rl (dir = +1 forward, -1 for the reverse sweep).
+template <int P>
+__device__ __forceinline__ void load_chunk(float (&v)[P], const float* sbase, int i0, int L1,
+                                           int L2, int L2max, int lane, int t_first, int dir) {
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+        const int rl = q * (64 / P) + lane / P, u = lane % P;
+        const int col = t_first + dir * u - rl, grow = i0 + rl;
+        float x = 0.0f;
+        if (grow < L1 && col >= 0 && col < L2) x = sbase[(size_t)grow * L2max + col];
+        v[q] = x;
+    }
 }
 
 template <int P>
+__device__ __forceinline__ void store_tile(float* tile, const float (&v)[P], int lane) {
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+        const int rl = q * (64 / P) + lane / P, u = lane % P;
+        tile[rl * (P + 1) + u] = v[q];
+    }
+}
+
 __global__ void __launch_bounds__(NW * 64)
 sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                   float* __restrict__ alpha_sk, float* __restrict__ partition,
-                  int L1max, int L2max, int NSmax, float gap, float T, int ring_len) {
+                  int* __restrict__ status, int L1max, int L2max, int NSmax, float gap, float T,
+                  int R) {
+    constexpr int P = PF;
+    constexpr int LEAD = lead(P);
     extern __shared__ float smem[];
+    __shared__ int prog[NW];
     __shared__ float red_m[NW], red_z[NW];
     const int b = blockIdx.x;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float* tile = smem + wave * 64 * (P + 1);
-    float* rings = smem + NW * 64 * (P + 1);
-    const int rmask = ring_len - 1;
+    float* rings = smem + NW * 64 * (P + 1);            // [2 parities][NW][R]
+    float* sink = rings + 2 * NW * R + wave * DUMMY;     // per-wave write sink
+    int* st = status + b;
+
+    if (lane == 0) prog[wave] = -1;
+    if (threadIdx.x == 0) *st = 0;
+    __syncthreads();
 
     const int L1 = min(max(lengths[2 * b], 0), L1max);
     const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
     const float c = kLog2e / T;
     const float tl = T * kLn2;
-    const int NS = (L1 + 63) >> 6;
+    const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
     const int nsteps = L2 + 63;
     const int nch = (nsteps + P - 1) / P;
-    const int lag = stripe_lag<P>(nch);
-    const int total = (NS > 0 && L2 > 0) ? (NS - 1) * lag + nch : 0;
     const size_t NT = (size_t)stored_steps(L2max);
     const float* sbase = scores + (size_t)b * L1max * L2max;
 
     OnlineLSE acc;
     acc.init_open();
-    float cur = kNINF, up_prev = kNINF;
     float nxt[P];
 
-    for (int gc = 0; gc < total; ++gc) {
-        int k = 0;
-        const int s = stripe_at(gc, wave, lag, nch, NS, &k);
-        if (s >= 0) {
-            const int i0 = s * 64;
-            const bool row_ok = i0 + lane < L1;
+    for (int s = wave; s < NS; s += NW) {
+        const int i0 = s * 64;
+        const int L2eff = (i0 + lane < L1) ? L2 : 0;   // rows past L1 are never valid
+        const float* ring_in =
+            rings + ((((s - 1) / NW) & 1) * NW + (s + NW - 1) % NW) * R;
+        float* ring_out = rings + (((s / NW) & 1) * NW + wave) * R;
+        float* out = alpha_sk + ((size_t)b * NSmax + s) * NT * 64 + lane;
+        out[0] = kNINF;   // steps t = -2, -1
+        out[64] = kNINF;
+        load_chunk(nxt, sbase, i0, L1, L2, L2max, lane, 0, 1);
+        store_tile(tile, nxt, lane);
+        float cur = kNINF, up_prev = kNINF;
+
+        for (int k = 0; k < nch; ++k) {
             const int t0 = k * P;
-            if (k == 0) {
-                // first chunk of a stripe: stage its scores now, reset the row state
-                cur = kNINF;
-                up_prev = kNINF;
-#pragma unroll
-                for (int q = 0; q < P; ++q) {
-                    const int rl = q * (64 / P) + lane / P, u = lane % P;
-                    const int col = t0 + u - rl, grow = i0 + rl;
-                    float v = 0.0f;
-                    if (grow < L1 && col >= 0 && col < L2) v = sbase[(size_t)grow * L2max + col];
-                    tile[rl * (P + 1) + u] = v;
-                }
+            if (s > 0) wait_for(prog, (s - 1) % NW, (s - 1) * PROG_STRIDE + min(k + LEAD, nch), st);
+            if (s + 1 < NS) {
+                const int need = k - 2 - R / P;   // slots of steps < kP+P-R must be consumed
+                if (need > 0) wait_for(prog, (s + 1) % NW, (s + 1) * PROG_STRIDE + need, st);
             }
-            const bool has_next = (k + 1) < nch;
-            if (has_next) {  // prefetch the next chunk's scores into registers
-#pragma unroll
-                for (int q = 0; q < P; ++q) {
-                    const int rl = q * (64 / P) + lane / P, u = lane % P;
-                    const int col = t0 + P + u - rl, grow = i0 + rl;
-                    float v = 0.0f;
-                    if (grow < L1 && col >= 0 && col < L2) v = sbase[(size_t)grow * L2max + col];
-                    nxt[q] = v;
-                }
-            }
-            float* out = alpha_sk + ((size_t)b * NSmax + s) * NT * 64 + lane;
-            if (k == 0) { out[0] = kNINF; out[64] = kNINF; }  // steps t = -2, -1
-            // lane 0's up values for this chunk (bottom row of the stripe above):
-            // lane u of `ring_vals` holds column t0 + u
-            float ring_vals = kNINF;
-            if (s > 0 && lane < P)
-                ring_vals = rings[((wave + NW - 1) % NW) * ring_len + ((t0 + lane) & rmask)];
+            const bool has_next = k + 1 < nch;
+            if (has_next) load_chunk(nxt, sbase, i0, L1, L2, L2max, lane, t0 + P, 1);
+            // lane 0's up values: column t0+j sits in lane j (ring slot = producer step)
+            float rreg = kNINF;
+            if (s > 0 && lane < P) rreg = ring_in[ring_index(t0 + lane + 63, R)];
+            // lane 63 publishes its alpha of step u into ring slot (t0+u) % R; the
+            // other lanes write into the sink (R is a multiple of P: no wrap in a chunk)
+            float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             wave_lds_sync();
             float sv[P];
 #pragma unroll
             for (int u = 0; u < P; ++u) sv[u] = tile[lane * (P + 1) + u];
-            float bottom = kNINF;  // gathers lane 63's alpha of every step (push_from_top)
+            float* outc = out + (size_t)(t0 + 2) * 64;
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t0 + u;
-                const int col = t - lane;
-                const bool ok = row_ok && (unsigned)col < (unsigned)L2;
-                float up = wave_shr1(cur, kNINF);
-                const float r0 = lane_bcast(ring_vals, u);
-                up = (lane == 0) ? r0 : up;
+                const float up = wave_shr1_or(cur, rreg);   // lane 0: stripe above
+                rreg = wave_shl1(rreg, kNINF);
                 const float diag = up_prev;
                 up_prev = up;
                 // out-of-table neighbours are NINF, so no i>1 / j>1 guards are needed
@@ -184,26 +206,15 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                 const float sum = fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c) +
                                   fast_exp2((vl - m) * c) + fast_exp2((sv[u] - m) * c);
                 const float a = m + tl * fast_log2(sum);
+                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
                 cur = ok ? a : kNINF;
-                out[(size_t)(t + 2) * 64] = cur;
-                bottom = push_from_top(bottom, cur, lane);
+                outc[u * 64] = cur;
+                pub[u] = cur;
                 acc.add(cur, c);
             }
-            // publish lane 63's row for the stripe below: lane 64-P+u holds step u,
-            // whose lane-63 column is t0+u-63
-            if (lane >= 64 - P) {
-                const int col = t0 + (lane - (64 - P)) - 63;
-                if (col >= 0 && col < L2) rings[wave * ring_len + (col & rmask)] = bottom;
-            }
-            if (has_next) {
-#pragma unroll
-                for (int q = 0; q < P; ++q) {
-                    const int rl = q * (64 / P) + lane / P, u = lane % P;
-                    tile[rl * (P + 1) + u] = nxt[q];
-                }
-            }
+            if (has_next) store_tile(tile, nxt, lane);
+            publish(prog, wave, s * PROG_STRIDE + k + 1);
         }
-        __syncthreads();
     }
 
     // partition: merge lanes, waves, and the cell (0,0) whose alpha is 0
@@ -219,32 +230,36 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     }
 }
 
-template <int P>
 __global__ void __launch_bounds__(NW * 64)
 sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                    const float* __restrict__ alpha_sk, const float* __restrict__ partition,
                    float* __restrict__ post, float* __restrict__ grad_gap,
-                   float* __restrict__ grad_T, int L1max, int L2max, int NSmax, float gap,
-                   float T, int ring_len) {
+                   float* __restrict__ grad_T, int* __restrict__ status, int L1max, int L2max,
+                   int NSmax, float gap, float T, int R) {
+    constexpr int P = PB;
+    constexpr int LEAD = lead(P);
     extern __shared__ float smem[];
+    __shared__ int prog[NW];
     __shared__ float red_g[NW], red_p[NW];
     const int b = blockIdx.x;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float* tile = smem + wave * 64 * (P + 1);
-    float* ringU = smem + NW * 64 * (P + 1);
-    float* ringD = ringU + NW * ring_len;
-    const int rmask = ring_len - 1;
+    float2* rings = reinterpret_cast<float2*>(smem + NW * 64 * (P + 1));  // [2][NW][R] (up, diag)
+    float2* sink = rings + 2 * NW * R + wave * DUMMY;
+    int* st = status + b;
+
+    if (lane == 0) prog[wave] = -1;
+    __syncthreads();
 
     const int L1 = min(max(lengths[2 * b], 0), L1max);
     const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
     const float c = kLog2e / T;
     const float S = partition[b];
-    const int NS = (L1 + 63) >> 6;
+    const float Sc = S * c;
+    const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
     const int nsteps = L2 + 63;
     const int nch = (nsteps + P - 1) / P;
-    const int lag = stripe_lag<P>(nch);
-    const int total = (NS > 0 && L2 > 0) ? (NS - 1) * lag + nch : 0;
     const size_t NT = (size_t)stored_steps(L2max);
     const float* sbase = scores + (size_t)b * L1max * L2max;
     float* pbase = post + (size_t)b * L1max * L2max;
@@ -258,94 +273,92 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     }
 
     float g_acc = 0.0f, p_acc = 0.0f;
-    float A[P + 2], nA[P], Bv = kNINF, nBv = kNINF, nxt[P];
-    float in_left = 0.0f, in_up = 0.0f, in_diag = 0.0f, in_diag_next = 0.0f;
+    float A[P + 2], nA[P], nxt[P];
 
-    for (int gc = 0; gc < total; ++gc) {
-        int k = 0;
-        const int q = stripe_at(gc, wave, lag, nch, NS, &k);
-        if (q >= 0) {
-            const int s = NS - 1 - q;
-            const int i0 = s * 64;
-            const bool row_ok = i0 + lane < L1;
-            const int t_hi = nsteps - 1 - k * P;
-            const float* abase = alpha_sk + ((size_t)b * NSmax + s) * NT * 64 + lane;
-            const float* aup = alpha_sk + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT * 64 + 63;
-            if (k == 0) {
-                in_left = in_up = in_diag = in_diag_next = 0.0f;
+    // Stripes run bottom-up: order q = 0..NS-1 handles stripe NS-1-q, on wave q % NW.
+    for (int q = wave; q < NS; q += NW) {
+        const int s = NS - 1 - q;
+        const int i0 = s * 64;
+        const int L2eff = (i0 + lane < L1) ? L2 : 0;
+        const float* abase = alpha_sk + ((size_t)b * NSmax + s) * NT * 64 + lane;
+        const float* aup = alpha_sk + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT * 64 + 63;
+        const float2* ring_in =
+            rings + ((((q - 1) / NW) & 1) * NW + (q + NW - 1) % NW) * R;   // from stripe s+1
+        float2* ring_out = rings + (((q / NW) & 1) * NW + wave) * R;       // to stripe s-1
+        const bool below = q > 0;
+        const bool above = q + 1 < NS;
+
+        int t_hi = nsteps - 1;
+        load_chunk(nxt, sbase, i0, L1, L2, L2max, lane, t_hi, -1);
+        store_tile(tile, nxt, lane);
 #pragma unroll
-                for (int qq = 0; qq < P; ++qq) {
-                    const int rl = qq * (64 / P) + lane / P, u = lane % P;
-                    const int col = t_hi - u - rl, grow = i0 + rl;
-                    float v = 0.0f;
-                    if (grow < L1 && col >= 0 && col < L2) v = sbase[(size_t)grow * L2max + col];
-                    tile[rl * (P + 1) + u] = v;
-                }
-#pragma unroll
-                for (int qq = 0; qq < P + 2; ++qq) {
-                    const int t = t_hi - qq;
-                    A[qq] = (t >= -2) ? abase[(size_t)(t + 2) * 64] : kNINF;
-                }
-                Bv = kNINF;
-                if (s > 0 && lane <= P) {
-                    const int t = t_hi - lane + 63;
-                    if (t <= nsteps - 1) Bv = aup[(size_t)(t + 2) * 64];
-                }
+        for (int j = 0; j < P + 2; ++j) {
+            const int t = t_hi - j;
+            A[j] = t >= -2 ? abase[(size_t)(t + 2) * 64] : kNINF;
+        }
+        float bv = kNINF;    // lane j: alpha of the row above at lane-63 step t_hi - j + 63
+        if (s > 0 && lane <= P) {
+            const int t = t_hi - lane + 63;
+            if (t <= nsteps - 1) bv = aup[(size_t)(t + 2) * 64];
+        }
+        float in_left = 0.0f, in_up = 0.0f, in_diag = 0.0f, in_diag_next = 0.0f;
+
+        for (int k = 0; k < nch; ++k) {
+            t_hi = nsteps - 1 - k * P;
+            if (below) wait_for(prog, (q - 1) % NW, (q - 1) * PROG_STRIDE + min(k + LEAD, nch), st);
+            if (above) {
+                const int need = k - 2 - R / P;   // slots of steps < kP+P-R must be consumed
+                if (need > 0) wait_for(prog, (q + 1) % NW, (q + 1) * PROG_STRIDE + need, st);
             }
-            const bool has_next = (k + 1) < nch;
-            if (has_next) {  // prefetch scores, own alpha and the row above for the next chunk
+            const bool has_next = k + 1 < nch;
+            float nbv = kNINF;
+            if (has_next) {
                 const int th2 = t_hi - P;
+                load_chunk(nxt, sbase, i0, L1, L2, L2max, lane, th2, -1);
 #pragma unroll
-                for (int qq = 0; qq < P; ++qq) {
-                    const int rl = qq * (64 / P) + lane / P, u = lane % P;
-                    const int col = th2 - u - rl, grow = i0 + rl;
-                    float v = 0.0f;
-                    if (grow < L1 && col >= 0 && col < L2) v = sbase[(size_t)grow * L2max + col];
-                    nxt[qq] = v;
+                for (int j = 0; j < P; ++j) {
+                    const int t = th2 - 2 - j;
+                    nA[j] = t >= -2 ? abase[(size_t)(t + 2) * 64] : kNINF;
                 }
-#pragma unroll
-                for (int qq = 0; qq < P; ++qq) {
-                    const int t = th2 - 2 - qq;
-                    nA[qq] = (t >= -2) ? abase[(size_t)(t + 2) * 64] : kNINF;
-                }
-                nBv = kNINF;
                 if (s > 0 && lane <= P) {
                     const int t = th2 - lane + 63;
-                    if (t <= nsteps - 1) nBv = aup[(size_t)(t + 2) * 64];
+                    if (t <= nsteps - 1) nbv = aup[(size_t)(t + 2) * 64];
                 }
             }
-            // contributions from the stripe below for lane 63, columns t_hi-u-63 (up)
-            // and t_hi-u-62 (diagonal): lane u of preU / preD holds step u's value
-            const bool below = (s + 1) < NS;
-            float preU = 0.0f, preD = 0.0f;
-            if (below && lane < P) {
-                const int tt = t_hi - lane;
-                preU = ringU[wave * ring_len + ((tt - 63) & rmask)];
-                preD = ringD[wave * ring_len + ((tt - 62) & rmask)];
+            // Contributions from the stripe below for lane 63.  The producer (lane 0 of
+            // stripe s+1) wrote the pair for its column c into slot (nsteps-1-c) % R;
+            // lane 63 at step u needs column t_hi-u-63 (up) and t_hi-u-62 (diagonal),
+            // i.e. slots kP+u+63 and kP+u+62.  Lane 63-j holds step j; the register is
+            // shifted up one lane per step so lane 63 sees the step it needs next.
+            float pre_u = 0.0f, pre_d = 0.0f;
+            if (below && lane >= 64 - P) {
+                const int j = 63 - lane;
+                pre_u = ring_in[ring_index(k * P + j + 63, R)].x;
+                pre_d = ring_in[ring_index(k * P + j + 62, R)].y;
             }
+            // lane 0 publishes (up, diag) of step u into slot (kP+u) % R
+            float2* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
             wave_lds_sync();
             float sv[P];
 #pragma unroll
             for (int u = 0; u < P; ++u) sv[u] = tile[lane * (P + 1) + u];
-            float topU = 0.0f, topD = 0.0f;  // gather lane 0's outputs (push_from_bottom)
+            // lane 63 starts the chunk with the ring's values for steps 0 and 1
+            {
+                const float u0 = lane_bcast(pre_u, 63), d0 = lane_bcast(pre_d, 63);
+                const float d1 = lane_bcast(pre_d, 62);
+                if (lane == 63) { in_up = u0; in_diag = d0; in_diag_next = d1; }
+            }
+            float pre_d2 = wave_shr1(pre_d, 0.0f);   // lane 63 = step 1 (then shifted on)
+            pre_d2 = wave_shr1(pre_d2, 0.0f);        // lane 63 = step 2
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t_hi - u;
-                const int col = t - lane;
-                const bool ok = row_ok && (unsigned)col < (unsigned)L2;
                 const float a0 = A[u], a1 = A[u + 1];
-                float upa = wave_shr1(a1, kNINF);
-                float dga = wave_shr1(A[u + 2], kNINF);
-                const float bu0 = lane_bcast(Bv, u);
-                const float bd0 = lane_bcast(Bv, u + 1);
-                upa = (lane == 0) ? bu0 : upa;
-                dga = (lane == 0) ? bd0 : dga;
-                const float ru = lane_bcast(preU, u);
-                const float rd = lane_bcast(preD, u);
-                in_up = (lane == 63) ? ru : in_up;
-                in_diag = (lane == 63) ? rd : in_diag;
-
-                // out-of-table predecessors are NINF: no i>1 / j>1 guards needed
+                // up / diagonal alphas from lane r-1; lane 0 takes the row above
+                const float bv_next = wave_shl1(bv, kNINF);
+                const float upa = wave_shr1_or(a1, bv);
+                const float dga = wave_shr1_or(A[u + 2], bv_next);
+                bv = bv_next;
                 const float vd = dga + sv[u];
                 const float vu = upa + gap;
                 const float vl = a1 + gap;
@@ -353,61 +366,49 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const float e0 = fast_exp2((vd - m) * c), e1 = fast_exp2((vu - m) * c);
                 const float e2 = fast_exp2((vl - m) * c), e3 = fast_exp2((sv[u] - m) * c);
                 const float rin = fast_rcp(((e0 + e1) + e2) + e3);
-                const float w0 = e0 * rin, w1 = e1 * rin, w2 = e2 * rin, w3 = e3 * rin;
-                float lp = (a0 - S) * c;
+                float lp = a0 * c - Sc;
                 lp = lp < 0.0f ? lp : 0.0f;
                 const float binit = fast_exp2(lp);
                 // reference accumulation order: init, diagonal, left, up successor
-                float beta = ((binit + in_diag) + in_left) + in_up;
-                const bool live = ok && (beta != 0.0f) && (fabsf(beta) <= 3.0e38f);
-                beta = live ? beta : 0.0f;
-                const float pv = live ? beta * (w0 + w3) : 0.0f;
-                const float od = live ? beta * w0 : 0.0f;
-                const float ou = live ? beta * w1 : 0.0f;
-                const float ol = live ? beta * w2 : 0.0f;
+                const float beta = ((binit + in_diag) + in_left) + in_up;
+                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
+                const bool live = ok && (beta <= 3.0e38f);    // skips inf / NaN like the reference
+                const float br = live ? beta * rin : 0.0f;
+                const float od = br * e0, ou = br * e1, ol = br * e2;
+                const float pv = br * (e0 + e3);
                 tile[lane * (P + 1) + u] = pv;
                 g_acc += ou;
                 g_acc += ol;
                 p_acc += pv * sv[u];
-                topU = push_from_bottom(topU, ou, lane);
-                topD = push_from_bottom(topD, od, lane);
+                pub[u] = make_float2(ou, od);
+                // successor contributions for the next steps; lane 63 takes the ring
+                pre_u = wave_shr1(pre_u, 0.0f);
                 in_left = ol;
-                in_up = wave_shl1(ou, 0.0f);
+                in_up = wave_shl1_or(ou, pre_u);
                 in_diag = in_diag_next;
-                in_diag_next = wave_shl1(od, 0.0f);
-            }
-            // hand lane 0's up / diagonal contributions to the stripe above: lane P-1-u
-            // holds step u, whose lane-0 column is t_hi-u
-            if (lane < P) {
-                const int tt = t_hi - (P - 1 - lane);
-                const int slot = ((wave + 1) % NW) * ring_len + (tt & rmask);
-                ringU[slot] = topU;
-                ringD[slot] = topD;
+                in_diag_next = wave_shl1_or(od, pre_d2);
+                pre_d2 = wave_shr1(pre_d2, 0.0f);
             }
             wave_lds_sync();
             // write this chunk's marginals (contiguous row segments)
 #pragma unroll
-            for (int qq = 0; qq < P; ++qq) {
-                const int rl = qq * (64 / P) + lane / P, u = lane % P;
+            for (int j = 0; j < P; ++j) {
+                const int rl = j * (64 / P) + lane / P, u = lane % P;
                 const int col = t_hi - u - rl, grow = i0 + rl;
                 if (grow < L1 && col >= 0 && col < L2)
                     pbase[(size_t)grow * L2max + col] = tile[rl * (P + 1) + u];
             }
             wave_lds_sync();
             if (has_next) {
-#pragma unroll
-                for (int qq = 0; qq < P; ++qq) {
-                    const int rl = qq * (64 / P) + lane / P, u = lane % P;
-                    tile[rl * (P + 1) + u] = nxt[qq];
-                }
+                store_tile(tile, nxt, lane);
                 A[0] = A[P];
                 A[1] = A[P + 1];
 #pragma unroll
-                for (int qq = 0; qq < P; ++qq) A[qq + 2] = nA[qq];
-                Bv = nBv;
+                for (int j = 0; j < P; ++j) A[j + 2] = nA[j];
+                bv = nbv;
             }
+            publish(prog, wave, q * PROG_STRIDE + k + 1);
         }
-        __syncthreads();
     }
 
     g_acc = wave_sum(g_acc);
@@ -430,7 +431,20 @@ using namespace d2p_amd;
 extern "C" size_t d2p_sw_workspace_bytes(int B, int max_L1, int max_L2) {
     if (B <= 0 || max_L1 <= 0 || max_L2 <= 0) return 0;
     const size_t ns = ((size_t)max_L1 + 63) / 64;
-    return (size_t)B * ns * (size_t)sw::stored_steps(max_L2) * 64 * sizeof(float);
+    return sw::status_bytes(B) +
+           (size_t)B * ns * (size_t)sw::stored_steps(max_L2) * 64 * sizeof(float);
+}
+
+extern "C" int d2p_sw_status(const void* workspace, int B, int* status, void* stream) {
+    D2P_REQUIRE(status != nullptr, "null status pointer");
+    *status = 0;
+    if (B <= 0 || workspace == nullptr) return D2P_OK;
+    std::vector<int> host(B);
+    D2P_HIP(hipMemcpyAsync(host.data(), workspace, sizeof(int) * B, hipMemcpyDeviceToHost,
+                           (hipStream_t)stream));
+    D2P_HIP(hipStreamSynchronize((hipStream_t)stream));
+    for (int v : host) *status |= v;
+    return D2P_OK;
 }
 
 extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths, int B,
@@ -445,26 +459,29 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
                 "null pointer argument");
     const size_t need = d2p_sw_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), "workspace too small");
+    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * sw::PB, "max_L2 too large");
     hipStream_t st = (hipStream_t)stream;
     const int ns = (max_L1 + 63) / 64;
-    const int ring_f = sw::ring_len_for<sw::PF>(max_L2);
-    const int ring_b = sw::ring_len_for<sw::PB>(max_L2);
-    const size_t lds_f = (size_t)sw::NW * 64 * (sw::PF + 1) * 4 + (size_t)sw::NW * ring_f * 4;
-    const size_t lds_b = (size_t)sw::NW * 64 * (sw::PB + 1) * 4 + 2 * (size_t)sw::NW * ring_b * 4;
-    D2P_REQUIRE(lds_f <= 150 * 1024 && lds_b <= 150 * 1024,
-                "max_L2 too large for the LDS stripe rings");
-    D2P_HIP(hipFuncSetAttribute((const void*)sw::sw_forward_kernel<sw::PF>,
+    const int R = sw::ring_len(max_L1, max_L2);
+    const size_t lds_f = (size_t)sw::NW * 64 * (sw::PF + 1) * sizeof(float) +
+                         (2 * (size_t)sw::NW * R + sw::NW * sw::DUMMY) * sizeof(float);
+    const size_t lds_b = (size_t)sw::NW * 64 * (sw::PB + 1) * sizeof(float) +
+                         (2 * (size_t)sw::NW * R + sw::NW * sw::DUMMY) * sizeof(float2);
+    D2P_REQUIRE(lds_b <= 150 * 1024,
+                "sequence too long for the LDS stripe rings (max_L2 with more than 512 rows)");
+    D2P_HIP(hipFuncSetAttribute((const void*)sw::sw_forward_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_f));
-    D2P_HIP(hipFuncSetAttribute((const void*)sw::sw_backward_kernel<sw::PB>,
+    D2P_HIP(hipFuncSetAttribute((const void*)sw::sw_backward_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
-    float* alpha_sk = (float*)workspace;
-    D2P_LAUNCH("sw_forward", sw::sw_forward_kernel<sw::PF>, dim3(B), dim3(sw::NW * 64), lds_f,
-               st, scores, lengths, alpha_sk, partition, max_L1, max_L2, ns, gap, temperature,
-               ring_f);
+    int* status = (int*)workspace;
+    float* alpha_sk = (float*)((char*)workspace + sw::status_bytes(B));
+    D2P_LAUNCH("sw_forward", sw::sw_forward_kernel, dim3(B), dim3(sw::NW * 64), lds_f, st,
+               scores, lengths, alpha_sk, partition, status, max_L1, max_L2, ns, gap,
+               temperature, R);
     D2P_HIP(hipGetLastError());
-    D2P_LAUNCH("sw_backward", sw::sw_backward_kernel<sw::PB>, dim3(B), dim3(sw::NW * 64),
-               lds_b, st, scores, lengths, alpha_sk, partition, marginals, grad_gap, grad_T,
-               max_L1, max_L2, ns, gap, temperature, ring_b);
+    D2P_LAUNCH("sw_backward", sw::sw_backward_kernel, dim3(B), dim3(sw::NW * 64), lds_b, st,
+               scores, lengths, alpha_sk, partition, marginals, grad_gap, grad_T, status,
+               max_L1, max_L2, ns, gap, temperature, R);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }

@@ -47,6 +47,12 @@ void d2p_profile_reset(void);
 /* Workspace bytes needed by d2p_sw_forward_marginals for the given padded shape. */
 size_t d2p_sw_workspace_bytes(int B, int max_L1, int max_L2);
 
+/* Status of the last d2p_sw_forward_marginals call that used `workspace`: ORs the
+ * per-element status words into *status (0 = clean; bit 0 = a pipeline wait hit its
+ * spin bound, i.e. the results are not to be trusted).  Synchronises `stream`.  No
+ * counterpart in the reference (its kernels do not wait on each other). */
+int d2p_sw_status(const void* workspace, int B, int* status, void* stream);
+
 /* Forward value and marginals in one call.
  * Replaces the pair sw_regular_forward[_warp] + sw_regular_backward[_warp]
  * (/root/reference/src/sw/kernels.cuh:139-207) as sequenced by

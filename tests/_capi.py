@@ -21,6 +21,10 @@ SIGNATURES = {
     "d2p_abi_version": (_i, []),
     "d2p_sw_workspace_bytes": (_z, [_i, _i, _i]),
     "d2p_sw_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _f, _p, _p, _p, _p, _p, _z, _p]),
+    "d2p_sw_status": (_i, [_p, _i, ctypes.POINTER(_i), _p]),
+    "d2p_profile_enable": (_i, [_i]),
+    "d2p_profile_report": (_i, [ctypes.c_char_p, _z]),
+    "d2p_profile_reset": (None, []),
     "d2p_scale_by_batch": (_i, [_p, _p, _p, _i, _ll, _p]),
 }
 
@@ -69,6 +73,9 @@ def sw_forward_marginals(scores, lengths, gap, T):
     check(lib().d2p_sw_forward_marginals(ptr(scores), ptr(lengths), B, L1, L2, gap, T,
                                          ptr(part), ptr(marg), ptr(gg), ptr(gt), ptr(ws),
                                          nbytes, stream()))
+    st = ctypes.c_int(0)
+    check(lib().d2p_sw_status(ptr(ws), B, ctypes.byref(st), stream()))
+    assert st.value == 0, f"pipeline status {st.value}: a stripe wait hit its spin bound"
     return part, marg, gg, gt
 
 
