@@ -55,11 +55,13 @@ __device__ __forceinline__ float lane_bcast(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// Orders this wave's LDS writes before its later LDS reads of other lanes' data.
+// Completes this wave's outstanding LDS operations and stops the compiler from
+// moving memory accesses across this point.  LDS is one in-order memory per CU, so
+// this orders the wave's LDS writes before its later LDS reads (of any lane) and
+// before a flag write that other waves poll.  Unlike a C++ fence it does not wait
+// for outstanding global loads/stores (vmcnt), so HBM prefetches stay in flight.
 __device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
 // Online log-sum-exp accumulator in natural units with the exp2 scale c = log2(e)/T:

@@ -43,7 +43,7 @@ namespace sw {
 
 constexpr int NW = 8;                // waves per workgroup
 constexpr int PF = 16;               // steps per chunk, forward sweep
-constexpr int PB = 8;                // steps per chunk, backward sweep (more state per step)
+constexpr int PB = 16;               // steps per chunk, backward sweep
 constexpr int SPIN_LIMIT = 1 << 22;  // ~0.2 s of polling before giving up
 constexpr int PROG_STRIDE = 1 << 16; // progress word = stripe * PROG_STRIDE + chunks done
 constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do not publish
@@ -67,29 +67,39 @@ __host__ inline int ring_len(int max_L1, int max_L2) {
     return (r + PF - 1) / PF * PF;   // a multiple of both chunk lengths
 }
 
-// Steps stored per stripe in the skewed alpha table: whole chunks plus the two
-// leading steps t = -2, -1 (always NINF).
+// Steps stored per stripe in the skewed alpha table: APAD leading steps t < 0 (all
+// NINF, so the reverse sweep reads the steps before the first one without guards)
+// and then whole forward chunks.
+constexpr int APAD = PB + 2;
 __host__ __device__ inline int stored_steps(int L2max) {
-    return ((L2max + 63 + PF - 1) / PF) * PF + 2;
+    return APAD + ((L2max + 63 + PF - 1) / PF) * PF;
 }
 
 __host__ inline size_t status_bytes(int B) { return ((size_t)B * sizeof(int) + 255) / 256 * 256; }
+constexpr size_t TRASH_BYTES = 256;  // one line the backward's masked lanes store into
 
+// Progress flags live in LDS.  The writer completes its LDS writes (ring data)
+// before the flag write; a reader that sees the flag issues its data reads after the
+// flag read.  LDS executes each wave's operations in order, so relaxed atomics plus
+// an LDS-only wait suffice.  (A C++ release/acquire, or a volatile access, would also
+// drain every HBM load and store in flight, i.e. s_waitcnt vmcnt(0), every chunk.)
 __device__ __forceinline__ void publish(int* prog, int wave, int value) {
-    __hip_atomic_store(prog + wave, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    wave_lds_sync();
+    __hip_atomic_store(prog + wave, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Waits until prog[w] >= need; bounded.  The loaded value is made wave-uniform.
 __device__ __forceinline__ void wait_for(int* prog, int w, int need, int* status_b) {
     int spins = 0;
     while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(
-               prog + w, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) < need) {
+               prog + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < need) {
         __builtin_amdgcn_s_sleep(2);
         if (++spins >= SPIN_LIMIT) {
             atomicOr(status_b, 1);
-            return;
+            break;
         }
     }
+    wave_lds_sync();
 }
 
 __device__ __forceinline__ int ring_index(int slot, int R) {
@@ -97,29 +107,120 @@ __device__ __forceinline__ int ring_index(int slot, int R) {
     return slot < 0 ? slot + R : slot;
 }
 
-// Loads the score parallelogram of one chunk into this lane's registers: value q
-// belongs to row rl(q) = q*(64/P) + lane/P and step u(q) = lane%P, i.e. the cell at
-// column t_first + dir*u - rl (dir = +1 forward, -1 for the reverse sweep).
+// Direct HBM -> LDS load of one dword per lane (global_load_lds_dword): lane l's value
+// lands at LDS byte address lds + 4*l; the LDS address travels in M0.  Each call then
+// advances `lds` by `lds_step` and `voff` by `vstep` bytes.  Written as inline
+// assembly so that (a) the compiler does not make every later LDS access wait for
+// the load (completion is waited for explicitly with wait_vmcnt), and (b) the running
+// addresses stay in two registers instead of being hoisted out of the loop as one
+// precomputed address per instruction.
+// M0 is a reserved register the compiler may use itself (LDS-DMA builtins, indexed
+// register moves); this file uses neither, so clobbering it here is safe, and the
+// compiler's reminder about reserved clobbers is silenced.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+template <int LDS_STEP>
+__device__ __forceinline__ void lds_dma_dword(const float* sbase, uint32_t& voff, uint32_t& lds,
+                                              uint32_t vstep) {
+    __asm__ volatile(
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dword %0, %2\n\t"
+        "s_add_u32 %1, %1, %4\n\t"
+        "v_add_u32 %0, %3, %0"
+        : "+v"(voff), "+s"(lds)
+        : "s"(sbase), "s"(vstep), "n"(LDS_STEP)
+        : "memory", "m0", "scc");
+}
+#pragma clang diagnostic pop
+
+// Waits until at most N vector-memory operations of this wave are outstanding
+// (gfx9 counts loads, stores and LDS DMA on one in-order counter).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Accesses base + byte offset with a wave-uniform base and a 32-bit per-lane offset,
+// the form the scalar-base global instructions take (no 64-bit address per lane).
+__device__ __forceinline__ float lane_load(const float* base, unsigned off_bytes) {
+    return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + off_bytes);
+}
+__device__ __forceinline__ void lane_store(float* base, unsigned off_bytes, float v) {
+    *reinterpret_cast<float*>(reinterpret_cast<char*>(base) + off_bytes) = v;
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    return (uint32_t)(uintptr_t)p;   // low half of a flat LDS address = LDS offset
+}
+
+// A chunk covers P steps of a stripe's 64 rows; cell (row r, step u) is column
+// t_first + DIR*u - r of DP row i0 + r (DIR = +1 forward, -1 reverse sweep).
+//
+// Score tiles are staged with P direct-to-LDS loads: instruction i, lane P*j+u
+// carries row r = i+P*j, step u, and lands at float 65*i + P*j + u of the tile.  Row r,
+// step u is therefore at 65*(r%P) + P*(r/P) + u, whose bank (mod 64) is r+u: the
+// per-step column read of the 64 lanes is conflict-free.  The backward reuses the
+// tile for the marginals it produces, and instruction i of the write-out stores
+// tile floats 65*i .. 65*i+63 back to the same cells.
 template <int P>
-__device__ __forceinline__ void load_chunk(float (&v)[P], const float* sbase, int i0, int L1,
-                                           int L2, int L2max, int lane, int t_first, int dir) {
+struct ChunkTile {
+    static constexpr int FLOATS = 65 * P;
+    __device__ static int read_base(int lane) { return 65 * (lane % P) + P * (lane / P); }
+};
+
+// True when every cell of the chunk lies inside the (max_L1 x max_L2) matrix.  Then
+// cell addresses of instruction i are the lane's address of instruction 0 plus
+// i*(L2max-1): one wave-uniform increment, no per-lane clamping.
+template <int P, int DIR>
+__device__ __forceinline__ bool chunk_inside(int i0, int L1max, int L2max, int t_first) {
+    const int lo = DIR > 0 ? t_first - 63 : t_first - (P - 1) - 63;
+    const int hi = DIR > 0 ? t_first + P - 1 : t_first;
+    return lo >= 0 && hi < L2max && i0 + 63 < L1max;
+}
+
+template <int P, int DIR>
+__device__ __forceinline__ int chunk_offset0(int i0, int L2max, int lane, int t_first) {
+    const int u = lane % P, pj = lane - u;
+    return (i0 + pj) * L2max + t_first + DIR * u - pj;
+}
+
+// Issues the P loads of one score chunk.  Cells outside the matrix read a clamped
+// in-matrix address; the sweeps mask every cell outside the element's lengths.
+template <int P, int DIR>
+__device__ __forceinline__ void dma_scores(uint32_t tile_lds, const float* sbase, int i0,
+                                           int L1max, int L2max, int lane, int t_first) {
+    if (chunk_inside<P, DIR>(i0, L1max, L2max, t_first)) {
+        uint32_t voff = (uint32_t)chunk_offset0<P, DIR>(i0, L2max, lane, t_first) * 4u;
+        const uint32_t vstep = (uint32_t)(L2max - 1) * 4u;
 #pragma unroll
-    for (int q = 0; q < P; ++q) {
-        const int rl = q * (64 / P) + lane / P, u = lane % P;
-        const int col = t_first + dir * u - rl, grow = i0 + rl;
-        float x = 0.0f;
-        if (grow < L1 && col >= 0 && col < L2) x = sbase[(size_t)grow * L2max + col];
-        v[q] = x;
+        for (int i = 0; i < P; ++i) lds_dma_dword<260>(sbase, voff, tile_lds, vstep);
+    } else {
+        const int u = lane % P, pj = lane - u;
+        // row/column of instruction 0; instruction i moves one row down, one column left
+        int row = i0 + pj, col = t_first + DIR * u - pj;
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            uint32_t voff = (uint32_t)(min(row, L1max - 1) * L2max +
+                                       min(max(col, 0), L2max - 1)) * 4u;
+            lds_dma_dword<260>(sbase, voff, tile_lds, 0u);
+            ++row;
+            --col;
+        }
     }
 }
 
-template <int P>
-__device__ __forceinline__ void store_tile(float* tile, const float (&v)[P], int lane) {
-#pragma unroll
-    for (int q = 0; q < P; ++q) {
-        const int rl = q * (64 / P) + lane / P, u = lane % P;
-        tile[rl * (P + 1) + u] = v[q];
-    }
+// Lane j (j <= P) of the reverse sweep needs the alpha that lane 63 of the stripe
+// above computed at step t_hi - j + 63, i.e. the cell above this stripe's first row
+// (NINF for the first stripe and past the last step).  One load for all lanes.
+template <int P = PB>
+__device__ __forceinline__ float row_above(const float* aup, int s, int lane,
+                                           int t_hi, int nsteps) {
+    if (s == 0) return kNINF;
+    const int t = t_hi - lane + 63;
+    const float v = lane_load(aup, ((unsigned)min(t, nsteps - 1) * 64u + 63u) * 4u);
+    return (lane <= P && t <= nsteps - 1) ? v : kNINF;
 }
 
 __global__ void __launch_bounds__(NW * 64)
@@ -134,11 +235,14 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     __shared__ float red_m[NW], red_z[NW];
     const int b = blockIdx.x;
     const int lane = threadIdx.x & 63;
+    const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    float* tile = smem + wave * 64 * (P + 1);
-    float* rings = smem + NW * 64 * (P + 1);            // [2 parities][NW][R]
-    float* sink = rings + 2 * NW * R + wave * DUMMY;     // per-wave write sink
+    using Tile = ChunkTile<P>;
+    float* tiles = smem + wave * 2 * Tile::FLOATS;         // double-buffered score chunk
+    float* rings = smem + NW * 2 * Tile::FLOATS;           // [2 parities][NW][R]
+    float* sink = rings + 2 * NW * R + wave * DUMMY;       // per-wave write sink
     int* st = status + b;
+    const int tbase = Tile::read_base(lane);
 
     if (lane == 0) prog[wave] = -1;
     if (threadIdx.x == 0) *st = 0;
@@ -156,7 +260,6 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
 
     OnlineLSE acc;
     acc.init_open();
-    float nxt[P];
 
     for (int s = wave; s < NS; s += NW) {
         const int i0 = s * 64;
@@ -164,11 +267,13 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
         const float* ring_in =
             rings + ((((s - 1) / NW) & 1) * NW + (s + NW - 1) % NW) * R;
         float* ring_out = rings + (((s / NW) & 1) * NW + wave) * R;
-        float* out = alpha_sk + ((size_t)b * NSmax + s) * NT * 64 + lane;
-        out[0] = kNINF;   // steps t = -2, -1
-        out[64] = kNINF;
-        load_chunk(nxt, sbase, i0, L1, L2, L2max, lane, 0, 1);
-        store_tile(tile, nxt, lane);
+        // wave-uniform base (step 0) + 32-bit lane offset: scalar-base stores
+        float* out = alpha_sk + (((size_t)b * NSmax + s) * NT + APAD) * 64;
+#pragma unroll
+        for (int t = -APAD; t < 0; ++t) lane_store(out + t * 64, ul4, kNINF);
+        wave_lds_sync();   // the previous stripe's tile reads are complete
+        const uint32_t tile_lds = lds_address(tiles);
+        dma_scores<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
         float cur = kNINF, up_prev = kNINF;
 
         for (int k = 0; k < nch; ++k) {
@@ -178,19 +283,23 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                 const int need = k - 2 - R / P;   // slots of steps < kP+P-R must be consumed
                 if (need > 0) wait_for(prog, (s + 1) % NW, (s + 1) * PROG_STRIDE + need, st);
             }
-            const bool has_next = k + 1 < nch;
-            if (has_next) load_chunk(nxt, sbase, i0, L1, L2, L2max, lane, t0 + P, 1);
+            // this chunk's scores: loaded one chunk ago, followed by exactly the P
+            // alpha stores of that chunk (the first chunk's load is the last issued)
+            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            const float* tile = tiles + (k & 1) * Tile::FLOATS;
+            float sv[P];
+#pragma unroll
+            for (int u = 0; u < P; ++u) sv[u] = tile[tbase + u];
             // lane 0's up values: column t0+j sits in lane j (ring slot = producer step)
             float rreg = kNINF;
             if (s > 0 && lane < P) rreg = ring_in[ring_index(t0 + lane + 63, R)];
+            if (k + 1 < nch)
+                dma_scores<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0, L1max,
+                                 L2max, lane, t0 + P);
             // lane 63 publishes its alpha of step u into ring slot (t0+u) % R; the
             // other lanes write into the sink (R is a multiple of P: no wrap in a chunk)
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
-            wave_lds_sync();
-            float sv[P];
-#pragma unroll
-            for (int u = 0; u < P; ++u) sv[u] = tile[lane * (P + 1) + u];
-            float* outc = out + (size_t)(t0 + 2) * 64;
+            float* outc = out + (size_t)t0 * 64;
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t0 + u;
@@ -208,11 +317,10 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                 const float a = m + tl * fast_log2(sum);
                 const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
                 cur = ok ? a : kNINF;
-                outc[u * 64] = cur;
+                lane_store(outc + u * 64, ul4, cur);
                 pub[u] = cur;
                 acc.add(cur, c);
             }
-            if (has_next) store_tile(tile, nxt, lane);
             publish(prog, wave, s * PROG_STRIDE + k + 1);
         }
     }
@@ -234,8 +342,8 @@ __global__ void __launch_bounds__(NW * 64)
 sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                    const float* __restrict__ alpha_sk, const float* __restrict__ partition,
                    float* __restrict__ post, float* __restrict__ grad_gap,
-                   float* __restrict__ grad_T, int* __restrict__ status, int L1max, int L2max,
-                   int NSmax, float gap, float T, int R) {
+                   float* __restrict__ grad_T, int* __restrict__ status, float* __restrict__ trash,
+                   int L1max, int L2max, int NSmax, float gap, float T, int R) {
     constexpr int P = PB;
     constexpr int LEAD = lead(P);
     extern __shared__ float smem[];
@@ -243,11 +351,14 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     __shared__ float red_g[NW], red_p[NW];
     const int b = blockIdx.x;
     const int lane = threadIdx.x & 63;
+    const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    float* tile = smem + wave * 64 * (P + 1);
-    float2* rings = reinterpret_cast<float2*>(smem + NW * 64 * (P + 1));  // [2][NW][R] (up, diag)
+    using Tile = ChunkTile<P>;
+    float* tiles = smem + wave * 2 * Tile::FLOATS;   // double-buffered scores -> marginals
+    float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * Tile::FLOATS);  // [2][NW][R] (up, diag)
     float2* sink = rings + 2 * NW * R + wave * DUMMY;
     int* st = status + b;
+    const int tbase = Tile::read_base(lane);
 
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
@@ -273,15 +384,16 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     }
 
     float g_acc = 0.0f, p_acc = 0.0f;
-    float A[P + 2], nA[P], nxt[P];
+    float A[P + 2], nA[P];
 
     // Stripes run bottom-up: order q = 0..NS-1 handles stripe NS-1-q, on wave q % NW.
     for (int q = wave; q < NS; q += NW) {
         const int s = NS - 1 - q;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
-        const float* abase = alpha_sk + ((size_t)b * NSmax + s) * NT * 64 + lane;
-        const float* aup = alpha_sk + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT * 64 + 63;
+        // wave-uniform bases at step 0; lanes add 32-bit offsets (scalar-base loads)
+        const float* abase = alpha_sk + (((size_t)b * NSmax + s) * NT + APAD) * 64;
+        const float* aup = alpha_sk + (((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT + APAD) * 64;
         const float2* ring_in =
             rings + ((((q - 1) / NW) & 1) * NW + (q + NW - 1) % NW) * R;   // from stripe s+1
         float2* ring_out = rings + (((q / NW) & 1) * NW + wave) * R;       // to stripe s-1
@@ -289,18 +401,15 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         const bool above = q + 1 < NS;
 
         int t_hi = nsteps - 1;
-        load_chunk(nxt, sbase, i0, L1, L2, L2max, lane, t_hi, -1);
-        store_tile(tile, nxt, lane);
+        {
+            const float* ap = abase + (ptrdiff_t)t_hi * 64;
 #pragma unroll
-        for (int j = 0; j < P + 2; ++j) {
-            const int t = t_hi - j;
-            A[j] = t >= -2 ? abase[(size_t)(t + 2) * 64] : kNINF;
+            for (int j = 0; j < P + 2; ++j) A[j] = lane_load(ap - j * 64, ul4);
         }
-        float bv = kNINF;    // lane j: alpha of the row above at lane-63 step t_hi - j + 63
-        if (s > 0 && lane <= P) {
-            const int t = t_hi - lane + 63;
-            if (t <= nsteps - 1) bv = aup[(size_t)(t + 2) * 64];
-        }
+        float bv = row_above(aup, s, lane, t_hi, nsteps);
+        wave_lds_sync();   // the previous stripe's tile reads are complete
+        const uint32_t tile_lds = lds_address(tiles);
+        dma_scores<P, -1>(tile_lds, sbase, i0, L1max, L2max, lane, t_hi);
         float in_left = 0.0f, in_up = 0.0f, in_diag = 0.0f, in_diag_next = 0.0f;
 
         for (int k = 0; k < nch; ++k) {
@@ -310,20 +419,15 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const int need = k - 2 - R / P;   // slots of steps < kP+P-R must be consumed
                 if (need > 0) wait_for(prog, (q + 1) % NW, (q + 1) * PROG_STRIDE + need, st);
             }
-            const bool has_next = k + 1 < nch;
-            float nbv = kNINF;
-            if (has_next) {
-                const int th2 = t_hi - P;
-                load_chunk(nxt, sbase, i0, L1, L2, L2max, lane, th2, -1);
+            // this chunk's scores: loaded one chunk ago, followed by exactly the P
+            // marginal stores of that chunk (the first chunk's load is the last issued)
+            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            float* tile = tiles + (k & 1) * Tile::FLOATS;
+            float sv[P];
 #pragma unroll
-                for (int j = 0; j < P; ++j) {
-                    const int t = th2 - 2 - j;
-                    nA[j] = t >= -2 ? abase[(size_t)(t + 2) * 64] : kNINF;
-                }
-                if (s > 0 && lane <= P) {
-                    const int t = th2 - lane + 63;
-                    if (t <= nsteps - 1) nbv = aup[(size_t)(t + 2) * 64];
-                }
+            for (int u = 0; u < P; ++u) {
+                sv[u] = tile[tbase + u];
+                __asm__("" : "+v"(sv[u]));   // read every score now (not under a mask)
             }
             // Contributions from the stripe below for lane 63.  The producer (lane 0 of
             // stripe s+1) wrote the pair for its column c into slot (nsteps-1-c) % R;
@@ -336,12 +440,22 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 pre_u = ring_in[ring_index(k * P + j + 63, R)].x;
                 pre_d = ring_in[ring_index(k * P + j + 62, R)].y;
             }
+            // prefetch the next chunk: alphas and the row above into registers (these
+            // loads precede the score load, so they do not disturb its count), scores
+            // straight into the other tile buffer
+            const bool has_next = k + 1 < nch;
+            float nbv = kNINF;
+            if (has_next) {
+                const int th2 = t_hi - P;
+                const float* ap = abase + (ptrdiff_t)(th2 - 2) * 64;
+#pragma unroll
+                for (int j = 0; j < P; ++j) nA[j] = lane_load(ap - j * 64, ul4);
+                nbv = row_above(aup, s, lane, th2, nsteps);
+                dma_scores<P, -1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0, L1max,
+                                  L2max, lane, th2);
+            }
             // lane 0 publishes (up, diag) of step u into slot (kP+u) % R
             float2* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
-            wave_lds_sync();
-            float sv[P];
-#pragma unroll
-            for (int u = 0; u < P; ++u) sv[u] = tile[lane * (P + 1) + u];
             // lane 63 starts the chunk with the ring's values for steps 0 and 1
             {
                 const float u0 = lane_bcast(pre_u, 63), d0 = lane_bcast(pre_d, 63);
@@ -353,33 +467,35 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t_hi - u;
+                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
+                // cells outside the element hold arbitrary tensor data: neutralise them
+                const float sc = ok ? sv[u] : kNINF;
                 const float a0 = A[u], a1 = A[u + 1];
                 // up / diagonal alphas from lane r-1; lane 0 takes the row above
                 const float bv_next = wave_shl1(bv, kNINF);
                 const float upa = wave_shr1_or(a1, bv);
                 const float dga = wave_shr1_or(A[u + 2], bv_next);
                 bv = bv_next;
-                const float vd = dga + sv[u];
+                const float vd = dga + sc;
                 const float vu = upa + gap;
                 const float vl = a1 + gap;
-                const float m = fmaxf(fmaxf(vd, vu), fmaxf(vl, sv[u]));
+                const float m = fmaxf(fmaxf(vd, vu), fmaxf(vl, sc));
                 const float e0 = fast_exp2((vd - m) * c), e1 = fast_exp2((vu - m) * c);
-                const float e2 = fast_exp2((vl - m) * c), e3 = fast_exp2((sv[u] - m) * c);
+                const float e2 = fast_exp2((vl - m) * c), e3 = fast_exp2((sc - m) * c);
                 const float rin = fast_rcp(((e0 + e1) + e2) + e3);
                 float lp = a0 * c - Sc;
                 lp = lp < 0.0f ? lp : 0.0f;
                 const float binit = fast_exp2(lp);
                 // reference accumulation order: init, diagonal, left, up successor
                 const float beta = ((binit + in_diag) + in_left) + in_up;
-                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
                 const bool live = ok && (beta <= 3.0e38f);    // skips inf / NaN like the reference
                 const float br = live ? beta * rin : 0.0f;
                 const float od = br * e0, ou = br * e1, ol = br * e2;
                 const float pv = br * (e0 + e3);
-                tile[lane * (P + 1) + u] = pv;
+                tile[tbase + u] = pv;
                 g_acc += ou;
                 g_acc += ol;
-                p_acc += pv * sv[u];
+                p_acc += pv * sc;
                 pub[u] = make_float2(ou, od);
                 // successor contributions for the next steps; lane 63 takes the ring
                 pre_u = wave_shr1(pre_u, 0.0f);
@@ -390,17 +506,31 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 pre_d2 = wave_shr1(pre_d2, 0.0f);
             }
             wave_lds_sync();
-            // write this chunk's marginals (contiguous row segments)
+            // write this chunk's marginals back over the cells the scores came from:
+            // exactly P stores (cells outside the element's lengths go to the trash
+            // line in boundary chunks, and carry 0 in inside chunks)
+            if (chunk_inside<P, -1>(i0, L1max, L2max, t_hi)) {
+                uint32_t off4 = (uint32_t)chunk_offset0<P, -1>(i0, L2max, lane, t_hi) * 4u;
+                const uint32_t step4 = (uint32_t)(L2max - 1) * 4u;
 #pragma unroll
-            for (int j = 0; j < P; ++j) {
-                const int rl = j * (64 / P) + lane / P, u = lane % P;
-                const int col = t_hi - u - rl, grow = i0 + rl;
-                if (grow < L1 && col >= 0 && col < L2)
-                    pbase[(size_t)grow * L2max + col] = tile[rl * (P + 1) + u];
+                for (int i = 0; i < P; ++i) {
+                    lane_store(pbase, off4, tile[65 * i + lane]);
+                    off4 += step4;
+                    __asm__ volatile("" : "+v"(off4));   // keep one running offset
+                }
+            } else {
+                const int u = lane % P, pj = lane - u;
+                int row = i0 + pj, col = t_hi - u - pj;
+#pragma unroll
+                for (int i = 0; i < P; ++i) {
+                    const bool in = row < L1 && col >= 0 && col < L2;
+                    float* dst = in ? pbase + (size_t)row * L2max + col : trash + lane;
+                    *dst = tile[65 * i + lane];
+                    ++row;
+                    --col;
+                }
             }
-            wave_lds_sync();
             if (has_next) {
-                store_tile(tile, nxt, lane);
                 A[0] = A[P];
                 A[1] = A[P + 1];
 #pragma unroll
@@ -431,7 +561,7 @@ using namespace d2p_amd;
 extern "C" size_t d2p_sw_workspace_bytes(int B, int max_L1, int max_L2) {
     if (B <= 0 || max_L1 <= 0 || max_L2 <= 0) return 0;
     const size_t ns = ((size_t)max_L1 + 63) / 64;
-    return sw::status_bytes(B) +
+    return sw::status_bytes(B) + sw::TRASH_BYTES +
            (size_t)B * ns * (size_t)sw::stored_steps(max_L2) * 64 * sizeof(float);
 }
 
@@ -460,13 +590,13 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
     const size_t need = d2p_sw_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), "workspace too small");
     D2P_REQUIRE(max_L2 + 63 < (1 << 16) * sw::PB, "max_L2 too large");
+    // per-lane byte offsets within one batch element are 32-bit
+    D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
     hipStream_t st = (hipStream_t)stream;
     const int ns = (max_L1 + 63) / 64;
     const int R = sw::ring_len(max_L1, max_L2);
-    const size_t lds_f = (size_t)sw::NW * 64 * (sw::PF + 1) * sizeof(float) +
-                         (2 * (size_t)sw::NW * R + sw::NW * sw::DUMMY) * sizeof(float);
-    const size_t lds_b = (size_t)sw::NW * 64 * (sw::PB + 1) * sizeof(float) +
-                         (2 * (size_t)sw::NW * R + sw::NW * sw::DUMMY) * sizeof(float2);
+    const size_t lds_f = (size_t)sw::NW * 2 * 65 * sw::PF * sizeof(float) + (2 * (size_t)sw::NW * R + sw::NW * sw::DUMMY) * sizeof(float);
+    const size_t lds_b = (size_t)sw::NW * 2 * 65 * sw::PB * sizeof(float) + (2 * (size_t)sw::NW * R + sw::NW * sw::DUMMY) * sizeof(float2);
     D2P_REQUIRE(lds_b <= 150 * 1024,
                 "sequence too long for the LDS stripe rings (max_L2 with more than 512 rows)");
     D2P_HIP(hipFuncSetAttribute((const void*)sw::sw_forward_kernel,
@@ -474,13 +604,14 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
     D2P_HIP(hipFuncSetAttribute((const void*)sw::sw_backward_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
     int* status = (int*)workspace;
-    float* alpha_sk = (float*)((char*)workspace + sw::status_bytes(B));
+    float* trash = (float*)((char*)workspace + sw::status_bytes(B));
+    float* alpha_sk = (float*)((char*)trash + sw::TRASH_BYTES);
     D2P_LAUNCH("sw_forward", sw::sw_forward_kernel, dim3(B), dim3(sw::NW * 64), lds_f, st,
                scores, lengths, alpha_sk, partition, status, max_L1, max_L2, ns, gap,
                temperature, R);
     D2P_HIP(hipGetLastError());
     D2P_LAUNCH("sw_backward", sw::sw_backward_kernel, dim3(B), dim3(sw::NW * 64), lds_b, st,
-               scores, lengths, alpha_sk, partition, marginals, grad_gap, grad_T, status,
+               scores, lengths, alpha_sk, partition, marginals, grad_gap, grad_T, status, trash,
                max_L1, max_L2, ns, gap, temperature, R);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
