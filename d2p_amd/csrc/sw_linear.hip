@@ -57,9 +57,9 @@ constexpr int lead(int P) { return 2 + 62 / P; }
 // (LEAD chunks plus back-pressure slack); when a wave owns several stripes (more
 // than NW stripes) it must also satisfy NW * R > L2 + 64 + 4P, which rules out a
 // cycle of back-pressure waits across a whole round of waves.
-__host__ inline int ring_len(int max_L1, int max_L2) {
+__host__ inline int ring_len(int max_L1, int max_L2, int min_len) {
     const int ns = (max_L1 + 63) / 64;
-    int r = 256;
+    int r = min_len;
     if (ns > NW) {
         const int need = (max_L2 + 64 + 4 * PF + NW - 1) / NW + 1;
         r = r > need ? r : need;
@@ -211,21 +211,10 @@ __device__ __forceinline__ void dma_scores(uint32_t tile_lds, const float* sbase
     }
 }
 
-// Lane j (j <= P) of the reverse sweep needs the alpha that lane 63 of the stripe
-// above computed at step t_hi - j + 63, i.e. the cell above this stripe's first row
-// (NINF for the first stripe and past the last step).  One load for all lanes.
-template <int P = PB>
-__device__ __forceinline__ float row_above(const float* aup, int s, int lane,
-                                           int t_hi, int nsteps) {
-    if (s == 0) return kNINF;
-    const int t = t_hi - lane + 63;
-    const float v = lane_load(aup, ((unsigned)min(t, nsteps - 1) * 64u + 63u) * 4u);
-    return (lane <= P && t <= nsteps - 1) ? v : kNINF;
-}
-
 __global__ void __launch_bounds__(NW * 64)
 sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
-                  float* __restrict__ alpha_sk, float* __restrict__ partition,
+                  float* __restrict__ alpha_sk, float* __restrict__ brow,
+                  float* __restrict__ partition,
                   int* __restrict__ status, int L1max, int L2max, int NSmax, float gap, float T,
                   int R) {
     constexpr int P = PF;
@@ -269,6 +258,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
         float* ring_out = rings + (((s / NW) & 1) * NW + wave) * R;
         // wave-uniform base (step 0) + 32-bit lane offset: scalar-base stores
         float* out = alpha_sk + (((size_t)b * NSmax + s) * NT + APAD) * 64;
+        float* brow_s = brow + ((size_t)b * NSmax + s) * NT;   // last row, by step
 #pragma unroll
         for (int t = -APAD; t < 0; ++t) lane_store(out + t * 64, ul4, kNINF);
         wave_lds_sync();   // the previous stripe's tile reads are complete
@@ -283,8 +273,8 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                 const int need = k - 2 - R / P;   // slots of steps < kP+P-R must be consumed
                 if (need > 0) wait_for(prog, (s + 1) % NW, (s + 1) * PROG_STRIDE + need, st);
             }
-            // this chunk's scores: loaded one chunk ago, followed by exactly the P
-            // alpha stores of that chunk (the first chunk's load is the last issued)
+            // this chunk's scores: loaded one chunk ago, followed by the P + 1 stores of
+            // that chunk (the first chunk's load is the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
             const float* tile = tiles + (k & 1) * Tile::FLOATS;
             float sv[P];
@@ -321,6 +311,10 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                 pub[u] = cur;
                 acc.add(cur, c);
             }
+            // the stripe's last row (lane 63) by step, contiguous, for the reverse sweep
+            // of the stripe below; one store instruction
+            wave_lds_sync();
+            if (lane < P) lane_store(brow_s, (unsigned)(t0 + lane) * 4u, ring_out[t0 % R + lane]);
             publish(prog, wave, s * PROG_STRIDE + k + 1);
         }
     }
@@ -340,7 +334,8 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
 
 __global__ void __launch_bounds__(NW * 64)
 sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
-                   const float* __restrict__ alpha_sk, const float* __restrict__ partition,
+                   const float* __restrict__ alpha_sk, const float* __restrict__ brow,
+                   const float* __restrict__ partition,
                    float* __restrict__ post, float* __restrict__ grad_gap,
                    float* __restrict__ grad_T, int* __restrict__ status, float* __restrict__ trash,
                    int L1max, int L2max, int NSmax, float gap, float T, int R) {
@@ -353,9 +348,15 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // Per wave, two chunk buffers, each: the score tile (then the chunk's marginals),
+    // P alpha rows (steps t_hi-2 .. t_hi-P-1, 64 lanes each) and one row of values from
+    // the stripe above.  All three arrive by direct-to-LDS loads one chunk ahead.
     using Tile = ChunkTile<P>;
-    float* tiles = smem + wave * 2 * Tile::FLOATS;   // double-buffered scores -> marginals
-    float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * Tile::FLOATS);  // [2][NW][R] (up, diag)
+    constexpr int ABUF = Tile::FLOATS;            // alpha rows
+    constexpr int RBUF = ABUF + P * 64;           // row above
+    constexpr int BUF = RBUF + 64;
+    float* bufs = smem + wave * 2 * BUF;
+    float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * BUF);  // [2][NW][R] (up, diag)
     float2* sink = rings + 2 * NW * R + wave * DUMMY;
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
@@ -384,51 +385,70 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     }
 
     float g_acc = 0.0f, p_acc = 0.0f;
-    float A[P + 2], nA[P];
+    float A[P + 2];
 
     // Stripes run bottom-up: order q = 0..NS-1 handles stripe NS-1-q, on wave q % NW.
     for (int q = wave; q < NS; q += NW) {
         const int s = NS - 1 - q;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
-        // wave-uniform bases at step 0; lanes add 32-bit offsets (scalar-base loads)
-        const float* abase = alpha_sk + (((size_t)b * NSmax + s) * NT + APAD) * 64;
-        const float* aup = alpha_sk + (((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT + APAD) * 64;
+        // alpha tables of this stripe and of the one above, from step -APAD
+        const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * NT * 64;
+        const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
         const float2* ring_in =
             rings + ((((q - 1) / NW) & 1) * NW + (q + NW - 1) % NW) * R;   // from stripe s+1
         float2* ring_out = rings + (((q / NW) & 1) * NW + wave) * R;       // to stripe s-1
         const bool below = q > 0;
         const bool above = q + 1 < NS;
 
-        int t_hi = nsteps - 1;
-        {
-            const float* ap = abase + (ptrdiff_t)t_hi * 64;
+        // Loads of chunk k (t_hi = nsteps-1-kP) into buffer k&1: P score loads, P alpha
+        // rows, and the row-above values (lane j <= P: the alpha of the last row of the
+        // stripe above at step t_hi - j + 63, clamped to the last step; lanes past P
+        // repeat lane P's address).  2P+1 loads.
+        auto issue_chunk = [&](int k) {
+            const int th = nsteps - 1 - k * P;
+            const uint32_t buf = lds_address(bufs + (k & 1) * BUF);
+            dma_scores<P, -1>(buf, sbase, i0, L1max, L2max, lane, th);
+            uint32_t voff = (uint32_t)((th - 2 + APAD) * 64) * 4u + ul4;
+            uint32_t lds = buf + ABUF * 4;
 #pragma unroll
-            for (int j = 0; j < P + 2; ++j) A[j] = lane_load(ap - j * 64, ul4);
-        }
-        float bv = row_above(aup, s, lane, t_hi, nsteps);
-        wave_lds_sync();   // the previous stripe's tile reads are complete
-        const uint32_t tile_lds = lds_address(tiles);
-        dma_scores<P, -1>(tile_lds, sbase, i0, L1max, L2max, lane, t_hi);
+            for (int j = 0; j < P; ++j) lds_dma_dword<256>(astripe, voff, lds, (uint32_t)-256);
+            uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
+            uint32_t rl = buf + RBUF * 4;
+            lds_dma_dword<0>(bup, roff, rl, 0u);
+        };
+
+        // the first two alphas of chunk 0 (steps nsteps-1, nsteps-2); later chunks
+        // carry them over from the previous chunk
+        A[P] = lane_load(astripe + (size_t)(nsteps - 1 + APAD) * 64, ul4);
+        A[P + 1] = lane_load(astripe + (size_t)(nsteps - 2 + APAD) * 64, ul4);
+        __asm__ volatile("" ::"v"(A[P]), "v"(A[P + 1]));   // completes the two loads here
+        wave_lds_sync();   // the previous stripe's buffer reads are complete
+        issue_chunk(0);
         float in_left = 0.0f, in_up = 0.0f, in_diag = 0.0f, in_diag_next = 0.0f;
 
         for (int k = 0; k < nch; ++k) {
-            t_hi = nsteps - 1 - k * P;
+            const int t_hi = nsteps - 1 - k * P;
             if (below) wait_for(prog, (q - 1) % NW, (q - 1) * PROG_STRIDE + min(k + LEAD, nch), st);
             if (above) {
                 const int need = k - 2 - R / P;   // slots of steps < kP+P-R must be consumed
                 if (need > 0) wait_for(prog, (q + 1) % NW, (q + 1) * PROG_STRIDE + need, st);
             }
-            // this chunk's scores: loaded one chunk ago, followed by exactly the P
-            // marginal stores of that chunk (the first chunk's load is the last issued)
+            // this chunk's loads were issued one chunk ago and followed by exactly the P
+            // marginal stores of that chunk (the first chunk's are the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
-            float* tile = tiles + (k & 1) * Tile::FLOATS;
+            float* buf = bufs + (k & 1) * BUF;
+            float* tile = buf;
             float sv[P];
 #pragma unroll
-            for (int u = 0; u < P; ++u) {
-                sv[u] = tile[tbase + u];
-                __asm__("" : "+v"(sv[u]));   // read every score now (not under a mask)
-            }
+            for (int u = 0; u < P; ++u) sv[u] = tile[tbase + u];
+            A[0] = A[P];
+            A[1] = A[P + 1];
+#pragma unroll
+            for (int j = 0; j < P; ++j) A[j + 2] = buf[ABUF + j * 64 + lane];
+            // lane j: alpha of the row above at lane-63 step t_hi - j + 63
+            float bv = buf[RBUF + lane];
+            bv = (s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1) ? bv : kNINF;
             // Contributions from the stripe below for lane 63.  The producer (lane 0 of
             // stripe s+1) wrote the pair for its column c into slot (nsteps-1-c) % R;
             // lane 63 at step u needs column t_hi-u-63 (up) and t_hi-u-62 (diagonal),
@@ -440,20 +460,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 pre_u = ring_in[ring_index(k * P + j + 63, R)].x;
                 pre_d = ring_in[ring_index(k * P + j + 62, R)].y;
             }
-            // prefetch the next chunk: alphas and the row above into registers (these
-            // loads precede the score load, so they do not disturb its count), scores
-            // straight into the other tile buffer
-            const bool has_next = k + 1 < nch;
-            float nbv = kNINF;
-            if (has_next) {
-                const int th2 = t_hi - P;
-                const float* ap = abase + (ptrdiff_t)(th2 - 2) * 64;
-#pragma unroll
-                for (int j = 0; j < P; ++j) nA[j] = lane_load(ap - j * 64, ul4);
-                nbv = row_above(aup, s, lane, th2, nsteps);
-                dma_scores<P, -1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0, L1max,
-                                  L2max, lane, th2);
-            }
+            if (k + 1 < nch) issue_chunk(k + 1);
             // lane 0 publishes (up, diag) of step u into slot (kP+u) % R
             float2* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
             // lane 63 starts the chunk with the ring's values for steps 0 and 1
@@ -530,13 +537,6 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     --col;
                 }
             }
-            if (has_next) {
-                A[0] = A[P];
-                A[1] = A[P + 1];
-#pragma unroll
-                for (int j = 0; j < P; ++j) A[j + 2] = nA[j];
-                bv = nbv;
-            }
             publish(prog, wave, q * PROG_STRIDE + k + 1);
         }
     }
@@ -561,8 +561,9 @@ using namespace d2p_amd;
 extern "C" size_t d2p_sw_workspace_bytes(int B, int max_L1, int max_L2) {
     if (B <= 0 || max_L1 <= 0 || max_L2 <= 0) return 0;
     const size_t ns = ((size_t)max_L1 + 63) / 64;
+    // status words | trash line | skewed alpha table | last row of every stripe
     return sw::status_bytes(B) + sw::TRASH_BYTES +
-           (size_t)B * ns * (size_t)sw::stored_steps(max_L2) * 64 * sizeof(float);
+           (size_t)B * ns * (size_t)sw::stored_steps(max_L2) * 65 * sizeof(float);
 }
 
 extern "C" int d2p_sw_status(const void* workspace, int B, int* status, void* stream) {
@@ -594,10 +595,13 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
     D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
     hipStream_t st = (hipStream_t)stream;
     const int ns = (max_L1 + 63) / 64;
-    const int R = sw::ring_len(max_L1, max_L2);
-    const size_t lds_f = (size_t)sw::NW * 2 * 65 * sw::PF * sizeof(float) + (2 * (size_t)sw::NW * R + sw::NW * sw::DUMMY) * sizeof(float);
-    const size_t lds_b = (size_t)sw::NW * 2 * 65 * sw::PB * sizeof(float) + (2 * (size_t)sw::NW * R + sw::NW * sw::DUMMY) * sizeof(float2);
-    D2P_REQUIRE(lds_b <= 150 * 1024,
+    const int Rf = sw::ring_len(max_L1, max_L2, 256);
+    const int Rb = sw::ring_len(max_L1, max_L2, 128);
+    const size_t lds_f = (size_t)sw::NW * 2 * 65 * sw::PF * sizeof(float) +
+                         (2 * (size_t)sw::NW * Rf + sw::NW * sw::DUMMY) * sizeof(float);
+    const size_t lds_b = (size_t)sw::NW * 2 * (65 * sw::PB + 64 * sw::PB + 64) * sizeof(float) +
+                         (2 * (size_t)sw::NW * Rb + sw::NW * sw::DUMMY) * sizeof(float2);
+    D2P_REQUIRE(lds_f <= 160 * 1024 - 256 && lds_b <= 160 * 1024 - 256,
                 "sequence too long for the LDS stripe rings (max_L2 with more than 512 rows)");
     D2P_HIP(hipFuncSetAttribute((const void*)sw::sw_forward_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_f));
@@ -606,13 +610,15 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
     int* status = (int*)workspace;
     float* trash = (float*)((char*)workspace + sw::status_bytes(B));
     float* alpha_sk = (float*)((char*)trash + sw::TRASH_BYTES);
+    float* brow = alpha_sk + (size_t)B * ns * sw::stored_steps(max_L2) * 64;
     D2P_LAUNCH("sw_forward", sw::sw_forward_kernel, dim3(B), dim3(sw::NW * 64), lds_f, st,
-               scores, lengths, alpha_sk, partition, status, max_L1, max_L2, ns, gap,
-               temperature, R);
+               scores, lengths, alpha_sk, brow, partition, status, max_L1, max_L2, ns, gap,
+               temperature, Rf);
     D2P_HIP(hipGetLastError());
     D2P_LAUNCH("sw_backward", sw::sw_backward_kernel, dim3(B), dim3(sw::NW * 64), lds_b, st,
-               scores, lengths, alpha_sk, partition, marginals, grad_gap, grad_T, status, trash,
-               max_L1, max_L2, ns, gap, temperature, R);
+               scores, lengths, alpha_sk, brow, partition, marginals, grad_gap, grad_T, status,
+               trash,
+               max_L1, max_L2, ns, gap, temperature, Rb);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
