@@ -1,0 +1,505 @@
+// sw_affine.hip -- affine-gap soft Smith-Waterman on gfx950.
+//
+// Reference behaviour restated (not translated):
+//   forward   /root/reference/src/sw_affine/kernels_cpu.cpp:94-195
+//   backward  /root/reference/src/sw_affine/kernels_cpu.cpp:201-356
+// Three states per cell (i, j >= 1):
+//   M = LSE_T(M[i-1,j-1]+s, I[i-1,j-1]+s, D[i-1,j-1]+s (only i>1 && j>1), s)
+//   I = LSE_T(M[i-1,j]+open, I[i-1,j]+ext)            (only i > 1)
+//   D = LSE_T(M[i,j-1]+open, D[i,j-1]+ext)            (only j > 1)
+// so a gap of length k costs open + (k-1)*ext; M[0,0] = 0, every other row/column 0
+// value is NINF, and S = LSE_T over the three states of all cells 0..L1 x 0..L2.
+// The marginal of cell (i,j) is beta_M * (sum of M's four weights).
+//
+// Mapping: the stripe pipeline of wavefront.hip.h.  The forward carries (M, I, D) per
+// lane; lane 0 of a stripe reads (M, I, D) of the stripe above from a float4 ring.
+// The three planes are stored as skewed tables table[b][stripe][plane][step][lane]
+// plus each stripe's last row by step.  The backward runs three beta channels; a
+// cell's successors hand it, in the reference's accumulation order,
+//   beta_M = ((init + from M[i+1,j+1]) + from D[i,j+1]) + from I[i+1,j]
+//   beta_I =  (init + from M[i+1,j+1]) + from I[i+1,j]
+//   beta_D =  (init + from M[i+1,j+1]) + from D[i,j+1].
+
+#include <vector>
+
+#include "wavefront.hip.h"
+#include "../../include/d2p_amd.h"
+#include "capi_util.hip.h"
+
+namespace d2p_amd {
+namespace swa {
+
+using namespace wf;
+
+constexpr int PF = 16;           // steps per chunk, forward
+constexpr int PB = 8;            // steps per chunk, backward (three alpha planes staged)
+constexpr int DUMMY = 64 + PF;   // per-wave sink entries for the lanes that do not publish
+
+__device__ __forceinline__ float lse2(float a, float b, float c, float tl) {
+    const float m = fmaxf(a, b);
+    return m + tl * fast_log2(fast_exp2((a - m) * c) + fast_exp2((b - m) * c));
+}
+
+__device__ __forceinline__ float lse4(float a, float b, float x, float y, float c, float tl) {
+    const float m = fmaxf(fmaxf(a, b), fmaxf(x, y));
+    const float z = ((fast_exp2((a - m) * c) + fast_exp2((b - m) * c)) + fast_exp2((x - m) * c)) +
+                    fast_exp2((y - m) * c);
+    return m + tl * fast_log2(z);
+}
+
+__global__ void __launch_bounds__(NW * 64)
+swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
+                   float* __restrict__ alpha_sk, float* __restrict__ brow,
+                   float* __restrict__ partition, int* __restrict__ status, int L1max, int L2max,
+                   int NSmax, float go, float ge, float T, int R) {
+    constexpr int P = PF;
+    extern __shared__ float smem[];
+    __shared__ int prog[NW];
+    __shared__ float red_m[NW], red_z[NW];
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const unsigned ul4 = (unsigned)lane * 4u;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    using Tile = ChunkTile<P>;
+    float* tiles = smem + wave * 2 * Tile::FLOATS;   // double-buffered score chunk
+    float4* rings = reinterpret_cast<float4*>(smem + NW * 2 * Tile::FLOATS);   // [2][NW][R]
+    float4* sink = rings + 2 * NW * R + wave * DUMMY;
+    int* st = status + b;
+    const int tbase = Tile::read_base(lane);
+
+    if (lane == 0) prog[wave] = -1;
+    if (threadIdx.x == 0) *st = 0;
+    __syncthreads();
+
+    const int L1 = min(max(lengths[2 * b], 0), L1max);
+    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const float c = kLog2e / T;
+    const float tl = T * kLn2;
+    const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
+    const int nsteps = L2 + 63;
+    const int nch = (nsteps + P - 1) / P;
+    const size_t NT = (size_t)stored_steps(L2max);
+    const size_t PLANE = NT * 64;
+    const float* sbase = scores + (size_t)b * L1max * L2max;
+
+    OnlineLSE acc;
+    acc.init_open();
+
+    for (int s = wave; s < NS; s += NW) {
+        const int i0 = s * 64;
+        const int L2eff = (i0 + lane < L1) ? L2 : 0;
+        const float4* ring_in = ring_from(rings, s, R);
+        float4* ring_out = ring_of(rings, s, R);
+        float* out = alpha_sk + ((size_t)b * NSmax + s) * 3 * PLANE + APAD * 64;   // M, step 0
+        float* brow_s = brow + ((size_t)b * NSmax + s) * 3 * NT;                    // [3][NT]
+        wave_lds_sync();   // the previous stripe's tile reads are complete
+        const uint32_t tile_lds = lds_address(tiles);
+        dma_tile<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
+        float cM = kNINF, cI = kNINF, cD = kNINF;      // this lane's previous step
+        float pM = kNINF, pI = kNINF, pD = kNINF;      // up values of the previous step
+
+        for (int k = 0; k < nch; ++k) {
+            const int t0 = k * P;
+            chunk_waits<P>(prog, s, NS, k, nch, R, st);
+            // this chunk's scores: loaded one chunk ago and followed by the 3P + 3
+            // stores of that chunk (the first chunk's load is the last issued)
+            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<3 * P>();
+            const float* tile = tiles + (k & 1) * Tile::FLOATS;
+            float sv[P];
+#pragma unroll
+            for (int u = 0; u < P; ++u) sv[u] = tile[tbase + u];
+            // lane 0's up values: column t0+j sits in lane j
+            float rM = kNINF, rI = kNINF, rD = kNINF;
+            if (s > 0 && lane < P) {
+                const float4 r = ring_in[ring_index(t0 + lane + 63, R)];
+                rM = r.x;
+                rI = r.y;
+                rD = r.z;
+            }
+            if (k + 1 < nch)
+                dma_tile<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0, L1max,
+                               L2max, lane, t0 + P);
+            float4* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
+            float* outc = out + (size_t)t0 * 64;
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                const int t = t0 + u;
+                const float uM = wave_shr1_or(cM, rM), uI = wave_shr1_or(cI, rI),
+                            uD = wave_shr1_or(cD, rD);
+                rM = wave_shl1(rM, kNINF);
+                rI = wave_shl1(rI, kNINF);
+                rD = wave_shl1(rD, kNINF);
+                const float dM = pM, dI = pI, dD = pD;   // diagonal = previous step's up
+                pM = uM;
+                pI = uI;
+                pD = uD;
+                const float sc = sv[u];
+                // out-of-table neighbours are NINF: no i>1 / j>1 guards are needed
+                const float M = lse4(dM + sc, dI + sc, dD + sc, sc, c, tl);
+                const float I = lse2(uM + go, uI + ge, c, tl);
+                const float D = lse2(cM + go, cD + ge, c, tl);
+                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
+                cM = ok ? M : kNINF;
+                cI = ok ? I : kNINF;
+                cD = ok ? D : kNINF;
+                lane_store(outc + u * 64, ul4, cM);
+                lane_store(outc + PLANE + u * 64, ul4, cI);
+                lane_store(outc + 2 * PLANE + u * 64, ul4, cD);
+                pub[u] = make_float4(cM, cI, cD, 0.0f);
+                acc.add(cM, c);
+                acc.add(cI, c);
+                acc.add(cD, c);
+            }
+            // the stripe's last row by step, per plane: three store instructions
+            wave_lds_sync();
+            if (lane < P) {
+                const float4 r = ring_out[t0 % R + lane];
+                const unsigned o = (unsigned)(t0 + lane) * 4u;
+                lane_store(brow_s, o, r.x);
+                lane_store(brow_s + NT, o, r.y);
+                lane_store(brow_s + 2 * NT, o, r.z);
+            }
+            publish(prog, wave, s * PROG_STRIDE + k + 1);
+        }
+    }
+
+    // partition: merge lanes, waves, and the cell M[0,0] = 0
+    wave_merge_lse(acc, c);
+    if (lane == 0) { red_m[wave] = acc.m; red_z[wave] = acc.z; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        OnlineLSE tot;
+        tot.m = 0.0f;
+        tot.z = 1.0f;
+        for (int w = 0; w < NW; ++w) tot.merge(red_m[w], red_z[w], c);
+        partition[b] = tot.m + tl * fast_log2(tot.z);
+    }
+}
+
+__global__ void __launch_bounds__(NW * 64)
+swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
+                    const float* __restrict__ alpha_sk, const float* __restrict__ brow,
+                    const float* __restrict__ partition, float* __restrict__ post,
+                    float* __restrict__ grad_open, float* __restrict__ grad_ext,
+                    float* __restrict__ grad_T, int* __restrict__ status,
+                    float* __restrict__ trash, int L1max, int L2max, int NSmax, float go,
+                    float ge, float T, int R) {
+    constexpr int P = PB;
+    extern __shared__ float smem[];
+    __shared__ int prog[NW];
+    __shared__ float red_o[NW], red_e[NW], red_p[NW];
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const unsigned ul4 = (unsigned)lane * 4u;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // Per wave: one in-flight input buffer (scores tile, P rows of each alpha plane,
+    // the row above for each plane), read into registers at the start of each chunk
+    // before the next chunk's loads are issued into it, and one output tile.
+    using Tile = ChunkTile<P>;
+    constexpr int AROWS = Tile::FLOATS;             // 3 planes x P rows x 64
+    constexpr int RROW = AROWS + 3 * P * 64;        // 3 planes x 64
+    constexpr int OTILE = RROW + 3 * 64;
+    constexpr int WFLOATS = OTILE + Tile::FLOATS;
+    float* wbuf = smem + wave * WFLOATS;
+    float* otile = wbuf + OTILE;
+    // rings [2][NW][R]: (up M, up I, diag M, diag I) and diag D, from lane 0 upward
+    float4* ring4 = reinterpret_cast<float4*>(smem + NW * WFLOATS);
+    float* ring1 = reinterpret_cast<float*>(ring4 + 2 * NW * R);
+    float4* sink4 = reinterpret_cast<float4*>(ring1 + 2 * NW * R) + wave * (64 + P);
+    float* sink1 = reinterpret_cast<float*>(reinterpret_cast<float4*>(ring1 + 2 * NW * R) +
+                                            NW * (64 + P)) + wave * (64 + P);
+    int* st = status + b;
+    const int tbase = Tile::read_base(lane);
+
+    if (lane == 0) prog[wave] = -1;
+    __syncthreads();
+
+    const int L1 = min(max(lengths[2 * b], 0), L1max);
+    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const float c = kLog2e / T;
+    const float S = partition[b];
+    const float Sc = S * c;
+    const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
+    const int nsteps = L2 + 63;
+    const int nch = (nsteps + P - 1) / P;
+    const size_t NT = (size_t)stored_steps(L2max);
+    const size_t PLANE = NT * 64;
+    const float* sbase = scores + (size_t)b * L1max * L2max;
+    float* pbase = post + (size_t)b * L1max * L2max;
+
+    zero_padding(pbase, L1, L2, L1max, L2max, NW * 64);
+
+    float g_open = 0.0f, g_ext = 0.0f, p_acc = 0.0f;
+    float AM[P + 2], AI[P + 2], AD[P + 2];
+
+    for (int q = wave; q < NS; q += NW) {
+        const int s = NS - 1 - q;
+        const int i0 = s * 64;
+        const int L2eff = (i0 + lane < L1) ? L2 : 0;
+        const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * 3 * PLANE;   // M at step -APAD
+        const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * 3 * NT;
+        const float4* r4_in = ring_from(ring4, q, R);
+        const float* r1_in = ring_from(ring1, q, R);
+        float4* r4_out = ring_of(ring4, q, R);
+        float* r1_out = ring_of(ring1, q, R);
+        const bool below = q > 0;
+        const uint32_t in_lds = lds_address(wbuf);
+
+        // Loads of chunk k (t_hi = nsteps-1-kP): the score tile, P alpha rows per plane
+        // (steps t_hi-2 .. t_hi-P-1) and the stripe above's last row per plane at steps
+        // t_hi - j + 63 for lane j <= P (clamped; lanes past P repeat lane P).
+        // 4P + 3 loads.
+        auto issue_chunk = [&](int k) {
+            const int th = nsteps - 1 - k * P;
+            dma_tile<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl)
+                dma_rows<P, -1>(in_lds + (AROWS + pl * P * 64) * 4, astripe + pl * PLANE, th - 2,
+                                ul4);
+            const uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) {
+                uint32_t o = roff, l = in_lds + (RROW + pl * 64) * 4;
+                lds_dma_dword<0>(bup + pl * NT, o, l, 0u);
+            }
+        };
+
+        // the first two steps of chunk 0 (later chunks carry them over)
+        {
+            const float* a0 = astripe + (size_t)(nsteps - 1 + APAD) * 64;
+            const float* a1 = astripe + (size_t)(nsteps - 2 + APAD) * 64;
+            AM[P] = lane_load(a0, ul4);
+            AM[P + 1] = lane_load(a1, ul4);
+            AI[P] = lane_load(a0 + PLANE, ul4);
+            AI[P + 1] = lane_load(a1 + PLANE, ul4);
+            AD[P] = lane_load(a0 + 2 * PLANE, ul4);
+            AD[P + 1] = lane_load(a1 + 2 * PLANE, ul4);
+            __asm__ volatile("" ::"v"(AM[P]), "v"(AM[P + 1]), "v"(AI[P]), "v"(AI[P + 1]),
+                             "v"(AD[P]), "v"(AD[P + 1]));   // completes these loads here
+        }
+        wave_lds_sync();   // the previous stripe's buffer reads are complete
+        issue_chunk(0);
+        // successor contributions waiting for this lane's next steps
+        float lM = 0.0f, lD = 0.0f;                              // from (i, j+1)
+        float uM = 0.0f, uI = 0.0f;                              // from (i+1, j)
+        float dM = 0.0f, dI = 0.0f, dD = 0.0f;                   // from (i+1, j+1)
+        float dM2 = 0.0f, dI2 = 0.0f, dD2 = 0.0f;                // ... one step later
+
+        for (int k = 0; k < nch; ++k) {
+            const int t_hi = nsteps - 1 - k * P;
+            chunk_waits<P>(prog, q, NS, k, nch, R, st);
+            // this chunk's loads, followed by exactly the P marginal stores of the
+            // previous chunk (the first chunk's loads are the last issued)
+            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            float sv[P];
+#pragma unroll
+            for (int u = 0; u < P; ++u) sv[u] = wbuf[tbase + u];
+            AM[0] = AM[P];
+            AM[1] = AM[P + 1];
+            AI[0] = AI[P];
+            AI[1] = AI[P + 1];
+            AD[0] = AD[P];
+            AD[1] = AD[P + 1];
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                AM[j + 2] = wbuf[AROWS + j * 64 + lane];
+                AI[j + 2] = wbuf[AROWS + P * 64 + j * 64 + lane];
+                AD[j + 2] = wbuf[AROWS + 2 * P * 64 + j * 64 + lane];
+            }
+            const bool row_ok = s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1;
+            float bM = row_ok ? wbuf[RROW + lane] : kNINF;
+            float bI = row_ok ? wbuf[RROW + 64 + lane] : kNINF;
+            float bD = row_ok ? wbuf[RROW + 128 + lane] : kNINF;
+            // Contributions from the stripe below for lane 63 (see the linear kernel):
+            // lane 63-j holds step j; up flows from slot kP+j+63, diagonal from kP+j+62.
+            float qUM = 0.0f, qUI = 0.0f, qDM = 0.0f, qDI = 0.0f, qDD = 0.0f;
+            if (below && lane >= 64 - P) {
+                const int j = 63 - lane;
+                const float4 ru = r4_in[ring_index(k * P + j + 63, R)];
+                const int id = ring_index(k * P + j + 62, R);
+                const float4 rd = r4_in[id];
+                qUM = ru.x;
+                qUI = ru.y;
+                qDM = rd.z;
+                qDI = rd.w;
+                qDD = r1_in[id];
+            }
+            wave_lds_sync();   // every read of the input buffer is complete
+            if (k + 1 < nch) issue_chunk(k + 1);
+            float4* pub4 = (lane == 0) ? r4_out + ring_index(k * P, R) : sink4 + lane;
+            float* pub1 = (lane == 0) ? r1_out + ring_index(k * P, R) : sink1 + lane;
+            // lane 63 starts the chunk with the ring's values for steps 0 and 1
+            {
+                const float u0M = lane_bcast(qUM, 63), u0I = lane_bcast(qUI, 63);
+                const float d0M = lane_bcast(qDM, 63), d0I = lane_bcast(qDI, 63),
+                            d0D = lane_bcast(qDD, 63);
+                const float d1M = lane_bcast(qDM, 62), d1I = lane_bcast(qDI, 62),
+                            d1D = lane_bcast(qDD, 62);
+                if (lane == 63) {
+                    uM = u0M; uI = u0I;
+                    dM = d0M; dI = d0I; dD = d0D;
+                    dM2 = d1M; dI2 = d1I; dD2 = d1D;
+                }
+            }
+            // lane 63 = step 2 of the diagonal flows (then shifted on)
+            qDM = wave_shr1(wave_shr1(qDM, 0.0f), 0.0f);
+            qDI = wave_shr1(wave_shr1(qDI, 0.0f), 0.0f);
+            qDD = wave_shr1(wave_shr1(qDD, 0.0f), 0.0f);
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                const int t = t_hi - u;
+                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
+                // cells outside the element hold arbitrary tensor data: neutralise them
+                const float sc = ok ? sv[u] : kNINF;
+                // predecessors: left = own previous step, up / diagonal = lane r-1 (lane 0:
+                // the stripe above's last row)
+                const float nbM = wave_shl1(bM, kNINF), nbI = wave_shl1(bI, kNINF),
+                            nbD = wave_shl1(bD, kNINF);
+                const float upM = wave_shr1_or(AM[u + 1], bM), upI = wave_shr1_or(AI[u + 1], bI);
+                const float dgM = wave_shr1_or(AM[u + 2], nbM), dgI = wave_shr1_or(AI[u + 2], nbI),
+                            dgD = wave_shr1_or(AD[u + 2], nbD);
+                bM = nbM;
+                bI = nbI;
+                bD = nbD;
+                const float lfM = AM[u + 1], lfD = AD[u + 1];
+                // M: diagonal + start weights
+                const float v0 = dgM + sc, v1 = dgI + sc, v2 = dgD + sc;
+                const float m4 = fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
+                const float e0 = fast_exp2((v0 - m4) * c), e1 = fast_exp2((v1 - m4) * c);
+                const float e2 = fast_exp2((v2 - m4) * c), e3 = fast_exp2((sc - m4) * c);
+                const float esum = ((e0 + e1) + e2) + e3;
+                // I: open from M above, extend from I above
+                const float i0v = upM + go, i1v = upI + ge;
+                const float mi = fmaxf(i0v, i1v);
+                const float f0 = fast_exp2((i0v - mi) * c), f1 = fast_exp2((i1v - mi) * c);
+                // D: open from M left, extend from D left
+                const float d0v = lfM + go, d1v = lfD + ge;
+                const float md = fmaxf(d0v, d1v);
+                const float g0 = fast_exp2((d0v - md) * c), g1 = fast_exp2((d1v - md) * c);
+                // betas in the reference's accumulation order
+                float lp;
+                lp = AM[u] * c - Sc;
+                const float initM = fast_exp2(lp < 0.0f ? lp : 0.0f);
+                lp = AI[u] * c - Sc;
+                const float initI = fast_exp2(lp < 0.0f ? lp : 0.0f);
+                lp = AD[u] * c - Sc;
+                const float initD = fast_exp2(lp < 0.0f ? lp : 0.0f);
+                const float betaM = ((initM + dM) + lM) + uM;
+                const float betaI = (initI + dI) + uI;
+                const float betaD = (initD + dD) + lD;
+                // skip inf / NaN betas like the reference; cells outside the element
+                const float brM = (ok && betaM <= 3.0e38f) ? betaM * fast_rcp(esum) : 0.0f;
+                const float brI = (ok && betaI <= 3.0e38f) ? betaI * fast_rcp(f0 + f1) : 0.0f;
+                const float brD = (ok && betaD <= 3.0e38f) ? betaD * fast_rcp(g0 + g1) : 0.0f;
+                const float pv = brM * esum;
+                otile[tbase + u] = pv;
+                p_acc += pv * sc;
+                const float oUM = brI * f0, oUI = brI * f1;            // to (i-1, j)
+                const float oLM = brD * g0, oLD = brD * g1;            // to (i, j-1)
+                const float oDM = brM * e0, oDI = brM * e1, oDD = brM * e2;   // to (i-1, j-1)
+                g_open += oUM;
+                g_open += oLM;
+                g_ext += oUI;
+                g_ext += oLD;
+                pub4[u] = make_float4(oUM, oUI, oDM, oDI);
+                pub1[u] = oDD;
+                // successor contributions for the next steps; lane 63 takes the ring
+                qUM = wave_shr1(qUM, 0.0f);
+                qUI = wave_shr1(qUI, 0.0f);
+                lM = oLM;
+                lD = oLD;
+                uM = wave_shl1_or(oUM, qUM);
+                uI = wave_shl1_or(oUI, qUI);
+                dM = dM2;
+                dI = dI2;
+                dD = dD2;
+                dM2 = wave_shl1_or(oDM, qDM);
+                dI2 = wave_shl1_or(oDI, qDI);
+                dD2 = wave_shl1_or(oDD, qDD);
+                qDM = wave_shr1(qDM, 0.0f);
+                qDI = wave_shr1(qDI, 0.0f);
+                qDD = wave_shr1(qDD, 0.0f);
+            }
+            wave_lds_sync();
+            write_tile<P, -1>(otile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
+            publish(prog, wave, q * PROG_STRIDE + k + 1);
+        }
+    }
+
+    g_open = wave_sum(g_open);
+    g_ext = wave_sum(g_ext);
+    p_acc = wave_sum(p_acc);
+    if (lane == 0) { red_o[wave] = g_open; red_e[wave] = g_ext; red_p[wave] = p_acc; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float go_s = 0.0f, ge_s = 0.0f, p = 0.0f;
+        for (int w = 0; w < NW; ++w) { go_s += red_o[w]; ge_s += red_e[w]; p += red_p[w]; }
+        grad_open[b] = go_s;
+        grad_ext[b] = ge_s;
+        grad_T[b] = (S - (p + (go_s * go + ge_s * ge))) / T;
+    }
+}
+
+}  // namespace swa
+}  // namespace d2p_amd
+
+using namespace d2p_amd;
+
+namespace {
+size_t swa_table_floats(int B, int max_L1, int max_L2) {
+    const size_t ns = ((size_t)max_L1 + 63) / 64;
+    return (size_t)B * ns * 3 * (size_t)wf::stored_steps(max_L2);   // per lane-row of 64
+}
+}  // namespace
+
+extern "C" size_t d2p_swa_workspace_bytes(int B, int max_L1, int max_L2) {
+    if (B <= 0 || max_L1 <= 0 || max_L2 <= 0) return 0;
+    // status words | trash line | skewed (M, I, D) tables | last row of every stripe
+    return wf::status_bytes(B) + wf::TRASH_BYTES +
+           swa_table_floats(B, max_L1, max_L2) * 65 * sizeof(float);
+}
+
+extern "C" int d2p_swa_forward_marginals(const float* scores, const int* lengths, int B,
+                                         int max_L1, int max_L2, float gap_open, float gap_ext,
+                                         float temperature, float* partition, float* marginals,
+                                         float* grad_open, float* grad_ext, float* grad_T,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+    D2P_REQUIRE(B >= 0 && max_L1 >= 0 && max_L2 >= 0, "negative dimension");
+    D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(scores && lengths && partition && marginals && grad_open && grad_ext && grad_T,
+                "null pointer argument");
+    const size_t need = d2p_swa_workspace_bytes(B, max_L1, max_L2);
+    D2P_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), "workspace too small");
+    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * swa::PB, "max_L2 too large");
+    D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
+    hipStream_t st = (hipStream_t)stream;
+    const int ns = (max_L1 + 63) / 64;
+    const int Rf = wf::ring_len(max_L1, max_L2, 256);
+    const int Rb = wf::ring_len(max_L1, max_L2, 128);
+    const size_t lds_f = (size_t)wf::NW * 2 * 65 * swa::PF * sizeof(float) +
+                         (2 * (size_t)wf::NW * Rf + wf::NW * swa::DUMMY) * sizeof(float4);
+    const size_t wfloats = 65 * swa::PB + 3 * swa::PB * 64 + 3 * 64 + 65 * swa::PB;
+    const size_t lds_b = (size_t)wf::NW * wfloats * sizeof(float) +
+                         2 * (size_t)wf::NW * Rb * (sizeof(float4) + sizeof(float)) +
+                         (size_t)wf::NW * (64 + swa::PB) * (sizeof(float4) + sizeof(float));
+    D2P_REQUIRE(lds_f <= 160 * 1024 - 256 && lds_b <= 160 * 1024 - 256,
+                "sequence too long for the LDS stripe rings (max_L2 with more than 512 rows)");
+    D2P_HIP(hipFuncSetAttribute((const void*)swa::swa_forward_kernel,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_f));
+    D2P_HIP(hipFuncSetAttribute((const void*)swa::swa_backward_kernel,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
+    int* status = (int*)workspace;
+    float* trash = (float*)((char*)workspace + wf::status_bytes(B));
+    float* alpha_sk = (float*)((char*)trash + wf::TRASH_BYTES);
+    float* brow = alpha_sk + swa_table_floats(B, max_L1, max_L2) * 64;
+    D2P_LAUNCH("swa_forward", swa::swa_forward_kernel, dim3(B), dim3(wf::NW * 64), lds_f, st,
+               scores, lengths, alpha_sk, brow, partition, status, max_L1, max_L2, ns, gap_open,
+               gap_ext, temperature, Rf);
+    D2P_HIP(hipGetLastError());
+    D2P_LAUNCH("swa_backward", swa::swa_backward_kernel, dim3(B), dim3(wf::NW * 64), lds_b, st,
+               scores, lengths, alpha_sk, brow, partition, marginals, grad_open, grad_ext, grad_T,
+               status, trash, max_L1, max_L2, ns, gap_open, gap_ext, temperature, Rb);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}

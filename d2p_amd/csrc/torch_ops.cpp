@@ -272,16 +272,137 @@ Tensor sw_marginals_grad_temp(Tensor s, double g, double t, c10::optional<Tensor
 }
 
 // ---------------------------------------------------------------------------
-// placeholders for the affine and DTW families (kernels land separately)
+// affine-gap soft Smith-Waterman
 // ---------------------------------------------------------------------------
-std::vector<Tensor> swa_t(Tensor, Tensor, Tensor, Tensor, Tensor) { not_yet("soft_sw_affine"); }
-std::vector<Tensor> swa_float(Tensor, double, double, double, c10::optional<Tensor>) {
-    not_yet("soft_sw_affine_float");
+
+// /root/reference/src/sw_affine/torch_cuda.cpp:34-66
+Dims checked_dims_affine(const Tensor& x) {
+    TORCH_CHECK(x.dim() == 3, "scores must be 3D (B, L1, L2)");
+    Dims d{checked_dim(x.size(0), "scores batch dimension"),
+           checked_dim(x.size(1), "scores L1 dimension"),
+           checked_dim(x.size(2), "scores L2 dimension")};
+    const int64_t cells = 3 * (int64_t(d.L1) + 1) * (int64_t(d.L2) + 1);
+    TORCH_CHECK(cells <= std::numeric_limits<int>::max(),
+                "sw_affine DP table too large: 3 * (L1 + 1) * (L2 + 1) exceeds CUDA int index range");
+    return d;
 }
-std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> swa_with_grads(Tensor, double, double, double,
-                                                                  c10::optional<Tensor>) {
-    not_yet("soft_sw_affine_with_grads");
+
+struct SwaOut {
+    Tensor partition, marginals, grad_open, grad_ext, grad_T;
+};
+
+SwaOut swa_run(const Tensor& scores, const Tensor& lengths, const Dims& d, float go, float ge,
+               float T) {
+    auto opt = scores.options();
+    SwaOut o{torch::empty({d.B}, opt), torch::empty({d.B, d.L1, d.L2}, opt),
+             torch::empty({d.B}, opt), torch::empty({d.B}, opt), torch::empty({d.B}, opt)};
+    const size_t ws_bytes = d2p_swa_workspace_bytes(d.B, d.L1, d.L2);
+    Tensor ws = workspace(ws_bytes, scores);
+    D2P_CALL(d2p_swa_forward_marginals(
+        scores.data_ptr<float>(), lengths.data_ptr<int>(), d.B, d.L1, d.L2, go, ge, T,
+        o.partition.data_ptr<float>(), o.marginals.data_ptr<float>(),
+        o.grad_open.data_ptr<float>(), o.grad_ext.data_ptr<float>(), o.grad_T.data_ptr<float>(),
+        ws.data_ptr(), ws_bytes, current_stream()));
+    return o;
 }
+
+// Autograd semantics of SoftSWAffineCUDAFunction
+// (/root/reference/src/sw_affine/torch_cuda.cpp:126-400): outputs {value, marginals};
+// d value / d scores = marginals; parameter gradients sum_b grad_value[b] * dS_b/dtheta.
+tensor_list swa_autograd_forward(AutogradContext* ctx, const Tensor& scores, const Tensor& lengths,
+                                 double go, double ge, double T) {
+    ctx->set_materialize_grads(false);
+    CHECK_INPUT_DEV(scores);
+    Dims d = checked_dims_affine(scores);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    SwaOut o = swa_run(scores, lengths, d, (float)go, (float)ge, (float)T);
+    ctx->save_for_backward({o.marginals, o.grad_open, o.grad_ext, o.grad_T});
+    return {o.partition, o.marginals};
+}
+
+// returns {grad_scores, grad_open, grad_ext, grad_T}
+tensor_list swa_autograd_backward(AutogradContext* ctx, const tensor_list& grads, bool want_o,
+                                  bool want_e, bool want_T) {
+    auto saved = ctx->get_saved_variables();
+    Tensor marg = saved[0];
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(marg.device());
+    Tensor grad_value = grads[0], grad_marg = grads[1];
+    Tensor gs, go, ge, gT;
+    if (grad_value.defined() && grad_value.numel() > 0) {
+        gs = scale_by_batch(marg, grad_value);
+        if (want_o) go = grad_param_sum(grad_value, saved[1]);
+        if (want_e) ge = grad_param_sum(grad_value, saved[2]);
+        if (want_T) gT = grad_param_sum(grad_value, saved[3]);
+    }
+    if (grad_marg.defined() && grad_marg.numel() > 0)
+        not_yet("soft_sw_affine marginal-path backward");
+    return {gs, go, ge, gT};
+}
+
+class SoftSWAffineFloatFunction : public torch::autograd::Function<SoftSWAffineFloatFunction> {
+   public:
+    static tensor_list forward(AutogradContext* ctx, Tensor scores, Tensor lengths, double go,
+                               double ge, double T) {
+        return swa_autograd_forward(ctx, scores, lengths, go, ge, T);
+    }
+    static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
+        auto g = swa_autograd_backward(ctx, grads, false, false, false);
+        return {g[0], Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
+class SoftSWAffineTensorFunction : public torch::autograd::Function<SoftSWAffineTensorFunction> {
+   public:
+    static tensor_list forward(AutogradContext* ctx, Tensor scores, Tensor go_t, Tensor ge_t,
+                               Tensor temp_t, Tensor lengths, double go, double ge, double T) {
+        return swa_autograd_forward(ctx, scores, lengths, go, ge, T);
+    }
+    static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
+        auto g = swa_autograd_backward(ctx, grads, ctx->needs_input_grad(1),
+                                       ctx->needs_input_grad(2), ctx->needs_input_grad(3));
+        return {g[0], g[1], g[2], g[3], Tensor(), Tensor(), Tensor(), Tensor()};
+    }
+};
+
+std::vector<Tensor> swa_t(Tensor scores, Tensor gap_open, Tensor gap_ext, Tensor temperature,
+                          Tensor lengths) {
+    CHECK_INPUT_DEV(scores);
+    Dims d = checked_dims_affine(scores);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    const float go = scalar_value(gap_open, "gap_open");
+    const float ge = scalar_value(gap_ext, "gap_ext");
+    const float T = scalar_value(temperature, "temperature");
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    return SoftSWAffineTensorFunction::apply(scores, gap_open, gap_ext, temperature, l, go, ge, T);
+}
+
+std::vector<Tensor> swa_float(Tensor scores, double gap_open, double gap_ext, double temperature,
+                              c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    Dims d = checked_dims_affine(scores);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    return SoftSWAffineFloatFunction::apply(scores, l, gap_open, gap_ext, temperature);
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> swa_with_grads(Tensor scores, double gap_open,
+                                                                  double gap_ext,
+                                                                  double temperature,
+                                                                  c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    Dims d = checked_dims_affine(scores);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    SwaOut o = swa_run(scores, l, d, (float)gap_open, (float)gap_ext, (float)temperature);
+    return {o.partition, o.marginals, o.grad_open, o.grad_ext, o.grad_T};
+}
+
+std::tuple<Tensor, Tensor, Tensor> swa_value_grad_params(Tensor s, double go, double ge, double t,
+                                                         c10::optional<Tensor> l) {
+    auto r = swa_with_grads(s, go, ge, t, l);
+    return {std::get<2>(r), std::get<3>(r), std::get<4>(r)};
+}
+
 Tensor swa_hvp(Tensor, Tensor, double, double, double, c10::optional<Tensor>) {
     not_yet("soft_sw_affine_hvp");
 }
@@ -292,14 +413,13 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> swa_backward_full(Tensor, Tensor, dou
                                                              double, c10::optional<Tensor>) {
     not_yet("soft_sw_affine_backward_full");
 }
-std::tuple<Tensor, Tensor, Tensor> swa_value_grad_params(Tensor, double, double, double,
-                                                         c10::optional<Tensor>) {
-    not_yet("sw_affine_value_grad_params");
-}
 Tensor swa_marg_grad(Tensor, double, double, double, c10::optional<Tensor>) {
     not_yet("sw_affine_marginals_grad_*");
 }
 
+// ---------------------------------------------------------------------------
+// placeholders for the DTW family (kernels land separately)
+// ---------------------------------------------------------------------------
 std::vector<Tensor> dtw_t(Tensor, Tensor, Tensor, int64_t) { not_yet("soft_dtw"); }
 std::vector<Tensor> dtw_float(Tensor, double, c10::optional<Tensor>, c10::optional<int64_t>) {
     not_yet("soft_dtw_float");

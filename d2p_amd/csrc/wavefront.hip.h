@@ -1,0 +1,287 @@
+// wavefront.hip.h -- the stripe-pipeline machinery shared by every soft-DP sweep
+// (linear / affine Smith-Waterman, DTW; value, marginal, tangent and dual sweeps).
+//
+// Geometry (one workgroup per batch element, NW wave64s):
+//   * DP rows are cut into 64-row stripes; stripe s runs on wave s % NW.  Lane r
+//     holds DP row 64*s + r + 1 and sweeps the columns with a one-column skew per
+//     lane: at step t lane r works on column t - r (0-based), so the wave's 64 cells
+//     of one step lie on one anti-diagonal and a stripe takes L2 + 63 steps;
+//   * neighbours inside a stripe move between lanes with DPP; the stripe boundary
+//     goes through an LDS ring (one slot per column) from the producing stripe's
+//     edge lane to the consuming stripe's edge lane;
+//   * waves never meet at a barrier.  Each wave publishes its progress word
+//     (stripe * PROG_STRIDE + chunks done) in LDS; a stripe waits, chunk by chunk,
+//     for the part of the neighbouring stripe it reads and, so that a ring is not
+//     overwritten, for its consumer to have caught up.  Every wait is bounded: a
+//     wave that polls SPIN_LIMIT times sets bit 0 of the element's status word and
+//     goes on, so a logic error can never hang the GPU;
+//   * per-cell inputs (scores, costs, tangents) arrive one chunk (P steps) ahead by
+//     direct-to-LDS loads, laid out so the per-step column read is conflict-free;
+//     stored DP tables use a skewed layout table[stripe][step][lane] (one 256-byte
+//     row per wave step) that both sweep directions stream contiguously.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dp_common.hip.h"
+
+namespace d2p_amd {
+namespace wf {
+
+constexpr int NW = 8;                 // waves per workgroup
+constexpr int SPIN_LIMIT = 1 << 22;   // ~0.2 s of polling before giving up
+constexpr int PROG_STRIDE = 1 << 16;  // progress word = stripe * PROG_STRIDE + chunks done
+constexpr int APAD = 18;              // table steps stored before step 0 (>= P + 2)
+constexpr int STEP_QUANTUM = 16;      // stored steps are a multiple of this (>= every P)
+constexpr size_t TRASH_BYTES = 256;   // one line that masked lanes store into
+
+// A stripe's chunk k reads boundary values the neighbouring stripe produces up to
+// 62 + P steps later in its own sweep, i.e. in its chunk k + 1 + 62/P; so it waits
+// until that stripe has completed k + lead(P) chunks.
+__host__ __device__ constexpr int lead(int P) { return 2 + 62 / P; }
+
+// Ring length (columns) of one stripe boundary.  It must exceed the pipeline window
+// (LEAD chunks plus back-pressure slack); when a wave owns several stripes (more
+// than NW stripes) it must also satisfy NW * R > L2 + 64 + 4*STEP_QUANTUM, which
+// rules out a cycle of back-pressure waits across a whole round of waves.  A
+// multiple of STEP_QUANTUM, hence of every chunk length.
+__host__ inline int ring_len(int max_L1, int max_L2, int min_len) {
+    const int ns = (max_L1 + 63) / 64;
+    int r = min_len;
+    if (ns > NW) {
+        const int need = (max_L2 + 64 + 4 * STEP_QUANTUM + NW - 1) / NW + 1;
+        r = r > need ? r : need;
+    }
+    return (r + STEP_QUANTUM - 1) / STEP_QUANTUM * STEP_QUANTUM;
+}
+
+// Steps stored per stripe and plane in a skewed table: APAD leading steps t < 0
+// (never written by a sweep; readers mask them) and then whole chunks.
+__host__ __device__ inline int stored_steps(int L2max) {
+    return APAD + ((L2max + 63 + STEP_QUANTUM - 1) / STEP_QUANTUM) * STEP_QUANTUM;
+}
+
+__host__ inline size_t status_bytes(int B) { return ((size_t)B * sizeof(int) + 255) / 256 * 256; }
+__host__ inline size_t round256(size_t n) { return (n + 255) / 256 * 256; }
+
+// ---------------------------------------------------------------- progress flags
+
+// Progress flags live in LDS.  The writer completes its LDS writes (ring data)
+// before the flag write; a reader that sees the flag issues its data reads after the
+// flag read.  LDS executes each wave's operations in order, so relaxed atomics plus
+// an LDS-only wait suffice (a C++ release/acquire would also drain every HBM load
+// and store in flight).
+__device__ __forceinline__ void publish(int* prog, int wave, int value) {
+    wave_lds_sync();
+    __hip_atomic_store(prog + wave, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Waits until prog[w] >= need; bounded.  The loaded value is made wave-uniform.
+__device__ __forceinline__ void wait_for(int* prog, int w, int need, int* status_b) {
+    int spins = 0;
+    while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(
+               prog + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < need) {
+        __builtin_amdgcn_s_sleep(2);
+        if (++spins >= SPIN_LIMIT) {
+            atomicOr(status_b, 1);
+            break;
+        }
+    }
+    wave_lds_sync();
+}
+
+// The chunk-level waits of sweep order q (q = stripe for forward sweeps, the
+// reversed stripe index for reverse sweeps) before its chunk k: the producer q-1
+// must be LEAD chunks ahead, and the consumer q+1 must have consumed the ring slots
+// this chunk overwrites.
+template <int P>
+__device__ __forceinline__ void chunk_waits(int* prog, int q, int NS, int k, int nch, int R,
+                                            int* status_b) {
+    if (q > 0) wait_for(prog, (q - 1) % NW, (q - 1) * PROG_STRIDE + min(k + lead(P), nch), status_b);
+    if (q + 1 < NS) {
+        const int need = k - 2 - R / P;   // slots of steps < kP+P-R must be consumed
+        if (need > 0) wait_for(prog, (q + 1) % NW, (q + 1) * PROG_STRIDE + need, status_b);
+    }
+}
+
+__device__ __forceinline__ int ring_index(int slot, int R) {
+    slot %= R;
+    return slot < 0 ? slot + R : slot;
+}
+
+// Parity-double-buffered rings [2][NW][R] of element type E: the ring sweep order q
+// writes, and the ring it reads (written by q - 1).
+template <class E>
+__device__ __forceinline__ E* ring_of(E* rings, int q, int R) {
+    return rings + (((q / NW) & 1) * NW + q % NW) * R;
+}
+template <class E>
+__device__ __forceinline__ E* ring_from(E* rings, int q, int R) {
+    return rings + ((((q - 1) / NW) & 1) * NW + (q + NW - 1) % NW) * R;
+}
+
+// ------------------------------------------------------------ direct-to-LDS loads
+
+// One dword per lane straight from HBM into LDS (global_load_lds_dword): lane l's
+// value lands at LDS byte address lds + 4*l; the LDS address travels in M0.  Each
+// call then advances `lds` by LDS_STEP and `voff` by `vstep` bytes.  Inline assembly,
+// so that (a) the compiler does not make every later LDS access wait for the load
+// (completion is waited for explicitly with wait_vmcnt), and (b) the running
+// addresses stay in two registers instead of being hoisted out of the loop as one
+// precomputed address per instruction.
+// M0 is a reserved register the compiler may use itself (LDS-DMA builtins, indexed
+// register moves); these kernels use neither, so clobbering it here is safe, and the
+// compiler's reminder about reserved clobbers is silenced.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+template <int LDS_STEP>
+__device__ __forceinline__ void lds_dma_dword(const float* sbase, uint32_t& voff, uint32_t& lds,
+                                              uint32_t vstep) {
+    __asm__ volatile(
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dword %0, %2\n\t"
+        "s_add_u32 %1, %1, %4\n\t"
+        "v_add_u32 %0, %3, %0"
+        : "+v"(voff), "+s"(lds)
+        : "s"(sbase), "s"(vstep), "n"(LDS_STEP)
+        : "memory", "m0", "scc");
+}
+#pragma clang diagnostic pop
+
+// Waits until at most N vector-memory operations of this wave are outstanding
+// (gfx9 counts loads, stores and LDS DMA on one in-order counter).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    return (uint32_t)(uintptr_t)p;   // low half of a flat LDS address = LDS offset
+}
+
+// Accesses base + byte offset with a wave-uniform base and a 32-bit per-lane offset,
+// the form the scalar-base global instructions take (no 64-bit address per lane).
+__device__ __forceinline__ float lane_load(const float* base, unsigned off_bytes) {
+    return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + off_bytes);
+}
+__device__ __forceinline__ void lane_store(float* base, unsigned off_bytes, float v) {
+    *reinterpret_cast<float*>(reinterpret_cast<char*>(base) + off_bytes) = v;
+}
+
+// ------------------------------------------------------------ chunk tiles
+
+// A chunk covers P steps of a stripe's 64 rows; cell (row r, step u) is column
+// t_first + DIR*u - r of DP row i0 + r (DIR = +1 forward, -1 reverse sweep).
+//
+// Tiles of per-cell matrices are staged with P direct-to-LDS loads: instruction i,
+// lane P*j+u carries row r = i+P*j, step u, and lands at float 65*i + P*j + u of the
+// tile.  Row r, step u is therefore at 65*(r%P) + P*(r/P) + u, whose bank (mod 64)
+// is r+u: the per-step column read of the 64 lanes is conflict-free.  Output tiles
+// use the same layout, and instruction i of the write-out stores tile floats
+// 65*i .. 65*i+63.
+template <int P>
+struct ChunkTile {
+    static_assert(64 % P == 0, "chunk length must divide 64");
+    static constexpr int FLOATS = 65 * P;
+    __device__ static int read_base(int lane) { return 65 * (lane % P) + P * (lane / P); }
+};
+
+// True when every cell of the chunk lies inside the (max_L1 x max_L2) matrix.  Then
+// cell addresses of instruction i are the lane's address of instruction 0 plus
+// i*(L2max-1): one wave-uniform increment, no per-lane clamping.
+template <int P, int DIR>
+__device__ __forceinline__ bool chunk_inside(int i0, int L1max, int L2max, int t_first) {
+    const int lo = DIR > 0 ? t_first - 63 : t_first - (P - 1) - 63;
+    const int hi = DIR > 0 ? t_first + P - 1 : t_first;
+    return lo >= 0 && hi < L2max && i0 + 63 < L1max;
+}
+
+template <int P, int DIR>
+__device__ __forceinline__ int chunk_offset0(int i0, int L2max, int lane, int t_first) {
+    const int u = lane % P, pj = lane - u;
+    return (i0 + pj) * L2max + t_first + DIR * u - pj;
+}
+
+// Issues the P loads of one chunk of a row-major [L1max][L2max] matrix into a tile.
+// Cells outside the matrix read a clamped in-matrix address; the sweeps mask every
+// cell outside the element's lengths.
+template <int P, int DIR>
+__device__ __forceinline__ void dma_tile(uint32_t tile_lds, const float* mbase, int i0, int L1max,
+                                         int L2max, int lane, int t_first) {
+    if (chunk_inside<P, DIR>(i0, L1max, L2max, t_first)) {
+        uint32_t voff = (uint32_t)chunk_offset0<P, DIR>(i0, L2max, lane, t_first) * 4u;
+        const uint32_t vstep = (uint32_t)(L2max - 1) * 4u;
+#pragma unroll
+        for (int i = 0; i < P; ++i) lds_dma_dword<260>(mbase, voff, tile_lds, vstep);
+    } else {
+        const int u = lane % P, pj = lane - u;
+        // row/column of instruction 0; instruction i moves one row down, one column left
+        int row = i0 + pj, col = t_first + DIR * u - pj;
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            uint32_t voff = (uint32_t)(min(row, L1max - 1) * L2max +
+                                       min(max(col, 0), L2max - 1)) * 4u;
+            lds_dma_dword<260>(mbase, voff, tile_lds, 0u);
+            ++row;
+            --col;
+        }
+    }
+}
+
+// Issues the P loads of P consecutive steps t_first, t_first + DIR, ... of one plane
+// of a skewed table (plane_base = the plane's step -APAD) into P LDS rows of 64.
+template <int P, int DIR>
+__device__ __forceinline__ void dma_rows(uint32_t rows_lds, const float* plane_base, int t_first,
+                                         unsigned ul4) {
+    uint32_t voff = (uint32_t)(t_first + APAD) * 256u + ul4;
+#pragma unroll
+    for (int j = 0; j < P; ++j) lds_dma_dword<256>(plane_base, voff, rows_lds, (uint32_t)(DIR * 256));
+}
+
+// Writes a chunk's output tile back to a row-major [L1max][L2max] matrix: exactly P
+// stores.  Inside chunks write every cell (cells outside the element's lengths must
+// hold 0 in the tile); boundary chunks send the cells outside the element's lengths
+// to the trash line.
+template <int P, int DIR>
+__device__ __forceinline__ void write_tile(const float* tile, float* obase, float* trash, int i0,
+                                           int L1, int L2, int L1max, int L2max, int lane,
+                                           int t_first) {
+    if (chunk_inside<P, DIR>(i0, L1max, L2max, t_first)) {
+        uint32_t off4 = (uint32_t)chunk_offset0<P, DIR>(i0, L2max, lane, t_first) * 4u;
+        const uint32_t step4 = (uint32_t)(L2max - 1) * 4u;
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            lane_store(obase, off4, tile[65 * i + lane]);
+            off4 += step4;
+            __asm__ volatile("" : "+v"(off4));   // keep one running offset
+        }
+    } else {
+        const int u = lane % P, pj = lane - u;
+        int row = i0 + pj, col = t_first + DIR * u - pj;
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const bool in = row < L1 && col >= 0 && col < L2;
+            float* dst = in ? obase + (size_t)row * L2max + col : trash + lane;
+            *dst = tile[65 * i + lane];
+            ++row;
+            --col;
+        }
+    }
+}
+
+// Zeroes the cells of a row-major [L1max][L2max] output outside [0,L1) x [0,L2),
+// with all threads of the workgroup.
+__device__ __forceinline__ void zero_padding(float* obase, int L1, int L2, int L1max, int L2max,
+                                             int nthreads) {
+    if (L1 >= L1max && L2 >= L2max) return;
+    for (int r = 0; r < L1max; ++r) {
+        const int c0 = r < L1 ? L2 : 0;
+        for (int c = c0 + (int)threadIdx.x; c < L2max; c += nthreads)
+            obase[(size_t)r * L2max + c] = 0.0f;
+    }
+}
+
+}  // namespace wf
+}  // namespace d2p_amd

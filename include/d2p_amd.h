@@ -68,6 +68,29 @@ int d2p_sw_forward_marginals(const float* scores, const int* lengths, int B, int
                              void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Affine-gap soft Smith-Waterman (gap of length k costs open + (k-1)*ext)
+ * ------------------------------------------------------------------------- */
+
+/* Workspace bytes needed by d2p_swa_forward_marginals for the given padded shape.
+ * Like every *_forward_marginals workspace it starts with the per-element status
+ * words that d2p_sw_status reads. */
+size_t d2p_swa_workspace_bytes(int B, int max_L1, int max_L2);
+
+/* Forward value and marginals in one call.
+ * Replaces the pair sw_affine_forward + sw_affine_backward
+ * (/root/reference/src/sw_affine/kernels.cuh:165-223) as sequenced by
+ * SoftSWAffineCUDAFunction::forward (/root/reference/src/sw_affine/torch_cuda.cpp:166-190).
+ *   scores     [B, max_L1, max_L2]  input
+ *   partition  [B]                  out: soft alignment value S
+ *   marginals  [B, max_L1, max_L2]  out: dS/dscores (zero in padding)
+ *   grad_open, grad_ext, grad_T [B] out: dS/dgap_open, dS/dgap_ext, dS/dtemperature */
+int d2p_swa_forward_marginals(const float* scores, const int* lengths, int B, int max_L1,
+                              int max_L2, float gap_open, float gap_ext, float temperature,
+                              float* partition, float* marginals, float* grad_open,
+                              float* grad_ext, float* grad_T, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Shared helpers
  * ------------------------------------------------------------------------- */
 

@@ -22,6 +22,9 @@ SIGNATURES = {
     "d2p_sw_workspace_bytes": (_z, [_i, _i, _i]),
     "d2p_sw_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _f, _p, _p, _p, _p, _p, _z, _p]),
     "d2p_sw_status": (_i, [_p, _i, ctypes.POINTER(_i), _p]),
+    "d2p_swa_workspace_bytes": (_z, [_i, _i, _i]),
+    "d2p_swa_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _f, _f, _p, _p, _p, _p, _p, _p,
+                                       _z, _p]),
     "d2p_profile_enable": (_i, [_i]),
     "d2p_profile_report": (_i, [ctypes.c_char_p, _z]),
     "d2p_profile_reset": (None, []),
@@ -77,6 +80,40 @@ def sw_forward_marginals(scores, lengths, gap, T):
     check(lib().d2p_sw_status(ptr(ws), B, ctypes.byref(st), stream()))
     assert st.value == 0, f"pipeline status {st.value}: a stripe wait hit its spin bound"
     return part, marg, gg, gt
+
+
+def _lengths(lengths, B, L1, L2, dev):
+    import torch
+    if lengths is None:
+        lengths = torch.tensor([[L1, L2]] * B, dtype=torch.int32, device=dev)
+    return lengths.to(dev, torch.int32).contiguous()
+
+
+def _workspace(nbytes, dev):
+    import torch
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+
+
+def _check_status(ws, B):
+    st = ctypes.c_int(0)
+    check(lib().d2p_sw_status(ptr(ws), B, ctypes.byref(st), stream()))
+    assert st.value == 0, f"pipeline status {st.value}: a stripe wait hit its spin bound"
+
+
+def swa_forward_marginals(scores, lengths, go, ge, T):
+    """Affine gap: (partition, marginals, grad_open, grad_ext, grad_T) through the C ABI."""
+    import torch
+    B, L1, L2 = scores.shape
+    dev = scores.device
+    lengths = _lengths(lengths, B, L1, L2, dev)
+    outs = [torch.empty(B, device=dev), torch.empty(B, L1, L2, device=dev)] + \
+        [torch.empty(B, device=dev) for _ in range(3)]
+    nbytes = lib().d2p_swa_workspace_bytes(B, L1, L2)
+    ws = _workspace(nbytes, dev)
+    check(lib().d2p_swa_forward_marginals(ptr(scores), ptr(lengths), B, L1, L2, go, ge, T,
+                                          *[ptr(o) for o in outs], ptr(ws), nbytes, stream()))
+    _check_status(ws, B)
+    return tuple(outs)
 
 
 def scale_by_batch(src, g):

@@ -54,7 +54,9 @@ CASES = [
     (6, 2, 1, 128, -1.0, 1.0),
     (7, 1, 1, 1, -1.0, 1.0),
     (8, 2, 200, 300, -1.0, 0.5),
-    (9, 9, 300, 70, -2.0, 1.5),        # more stripes than waves in a workgroup
+    (9, 9, 300, 70, -2.0, 1.5),
+    (10, 2, 600, 90, -1.0, 1.0),       # more stripes than waves in a workgroup
+    (11, 1, 1100, 300, -1.0, 1.0),     # ... more than two rounds of waves
 ]
 
 
