@@ -1,0 +1,363 @@
+// dtw.hip -- soft dynamic time warping on gfx950.
+//
+// Reference behaviour restated (not translated):
+//   forward   /root/reference/src/dtw/kernels_cpu.cpp:58-121
+//   backward  /root/reference/src/dtw/kernels_cpu.cpp:127-223
+//   band      /root/reference/src/dtw/kernels_cpu.cpp:24-29 (float arithmetic)
+// DP over the costs c[i,j] (i, j >= 1):
+//   alpha[i,j] = c[i,j] + softmin_T(alpha[i-1,j-1], alpha[i-1,j], alpha[i,j-1])
+//   softmin_T(x) = m - T*log(sum exp((m - x)/T)),  m = min(x)
+// alpha[0,0] = 0, every other row/column 0 value is PINF, cells outside the
+// Sakoe-Chiba band (|j - i*L2/L1| > bandwidth, bandwidth >= 0) are PINF, and the
+// value is alpha[L1, L2].  The backward starts from beta[L1,L2] = 1, spreads beta
+// to the predecessors through the softmin weights, and the marginal is beta; the
+// temperature gradient is sum beta * (softmin - E_w[alpha_pred]) / T.
+//
+// Mapping: the stripe pipeline of wavefront.hip.h with the linear Smith-Waterman
+// layout (one alpha plane).  The band test needs i*L2/L1 per row: each lane computes
+// it once per stripe, so the per-cell test is a subtraction and a compare.
+
+#include <vector>
+
+#include "wavefront.hip.h"
+#include "../../include/d2p_amd.h"
+#include "capi_util.hip.h"
+
+namespace d2p_amd {
+namespace dtw {
+
+using namespace wf;
+
+constexpr int PF = 16;               // steps per chunk, forward sweep
+constexpr int PB = 16;               // steps per chunk, backward sweep
+constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do not publish
+
+// i*L2/L1 of (1-based) row i in float, as the reference's band test computes it.
+__device__ __forceinline__ float band_centre(int i, int L1, int L2) {
+    return L1 > 0 ? (float)((long long)i * L2) / (float)L1 : 0.0f;
+}
+
+// Cell (row centre ej, 1-based column j) lies in the band (bandwidth < 0: no band).
+__device__ __forceinline__ bool in_band(float ej, int j, float bw) {
+    return bw < 0.0f || fabsf((float)j - ej) <= bw;
+}
+
+__global__ void __launch_bounds__(NW * 64)
+dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ lengths,
+                   float* __restrict__ alpha_sk, float* __restrict__ brow,
+                   float* __restrict__ value, int* __restrict__ status, int L1max, int L2max,
+                   int NSmax, float T, int bandwidth, int R) {
+    constexpr int P = PF;
+    extern __shared__ float smem[];
+    __shared__ int prog[NW];
+    __shared__ float terminal;
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const unsigned ul4 = (unsigned)lane * 4u;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    using Tile = ChunkTile<P>;
+    float* tiles = smem + wave * 2 * Tile::FLOATS;         // double-buffered cost chunk
+    float* rings = smem + NW * 2 * Tile::FLOATS;           // [2 parities][NW][R]
+    float* sink = rings + 2 * NW * R + wave * DUMMY;       // per-wave write sink
+    int* st = status + b;
+    const int tbase = Tile::read_base(lane);
+
+    if (lane == 0) prog[wave] = -1;
+    if (threadIdx.x == 0) {
+        *st = 0;
+        terminal = kPINF;
+    }
+    __syncthreads();
+
+    const int L1 = min(max(lengths[2 * b], 0), L1max);
+    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const float c = kLog2e / T;
+    const float tl = T * kLn2;
+    // a band test with an empty side is always true (reference: L1 == 0 || L2 == 0)
+    const float bw = (bandwidth < 0 || L1 == 0 || L2 == 0) ? -1.0f : (float)bandwidth;
+    const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
+    const int nsteps = L2 + 63;
+    const int nch = (nsteps + P - 1) / P;
+    const size_t NT = (size_t)stored_steps(L2max);
+    const float* cbase = costs + (size_t)b * L1max * L2max;
+
+    for (int s = wave; s < NS; s += NW) {
+        const int i0 = s * 64;
+        const int L2eff = (i0 + lane < L1) ? L2 : 0;   // rows past L1 are never valid
+        const float ej = band_centre(i0 + lane + 1, L1, L2);
+        const bool last_row = i0 + lane == L1 - 1;
+        const float* ring_in = ring_from(rings, s, R);
+        float* ring_out = ring_of(rings, s, R);
+        float* out = alpha_sk + (((size_t)b * NSmax + s) * NT + APAD) * 64;
+        float* brow_s = brow + ((size_t)b * NSmax + s) * NT;   // last row, by step
+        // steps t < 0 hold the column-0 boundary (PINF), read by the reverse sweep
+#pragma unroll
+        for (int t = -APAD; t < 0; ++t) lane_store(out + t * 64, ul4, kPINF);
+        wave_lds_sync();   // the previous stripe's tile reads are complete
+        const uint32_t tile_lds = lds_address(tiles);
+        dma_tile<P, 1>(tile_lds, cbase, i0, L1max, L2max, lane, 0);
+        // lane 0 of the first stripe sees alpha[0,0] = 0 as its first diagonal
+        float cur = kPINF, up_prev = (s == 0 && lane == 0) ? 0.0f : kPINF;
+
+        for (int k = 0; k < nch; ++k) {
+            const int t0 = k * P;
+            chunk_waits<P>(prog, s, NS, k, nch, R, st);
+            // this chunk's costs: loaded one chunk ago, followed by the P + 1 stores of
+            // that chunk (the first chunk's load is the last issued)
+            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            const float* tile = tiles + (k & 1) * Tile::FLOATS;
+            float cv[P];
+#pragma unroll
+            for (int u = 0; u < P; ++u) cv[u] = tile[tbase + u];
+            // lane 0's up values: column t0+j sits in lane j (row 0 is PINF)
+            float rreg = kPINF;
+            if (s > 0 && lane < P) rreg = ring_in[ring_index(t0 + lane + 63, R)];
+            if (k + 1 < nch)
+                dma_tile<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, cbase, i0, L1max,
+                               L2max, lane, t0 + P);
+            float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
+            float* outc = out + (size_t)t0 * 64;
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                const int t = t0 + u;
+                const float up = wave_shr1_or(cur, rreg);   // lane 0: stripe above
+                rreg = wave_shl1(rreg, kPINF);
+                const float diag = up_prev;
+                up_prev = up;
+                // out-of-table and out-of-band neighbours are PINF
+                const float m = fminf(fminf(diag, up), cur);
+                const float z = (fast_exp2((m - diag) * c) + fast_exp2((m - up) * c)) +
+                                fast_exp2((m - cur) * c);
+                const float a = cv[u] + (m - tl * fast_log2(z));
+                const int col = t - lane;
+                const bool ok = (unsigned)col < (unsigned)L2eff && in_band(ej, col + 1, bw);
+                cur = ok ? a : kPINF;
+                lane_store(outc + u * 64, ul4, cur);
+                pub[u] = cur;
+                if (ok && last_row && col == L2 - 1) terminal = cur;
+            }
+            // the stripe's last row (lane 63) by step, contiguous, for the reverse sweep
+            // of the stripe below; one store instruction
+            wave_lds_sync();
+            if (lane < P) lane_store(brow_s, (unsigned)(t0 + lane) * 4u, ring_out[t0 % R + lane]);
+            publish(prog, wave, s * PROG_STRIDE + k + 1);
+        }
+    }
+
+    __syncthreads();
+    if (threadIdx.x == 0) value[b] = NS > 0 ? terminal : ((L1 == 0 && L2 == 0) ? 0.0f : kPINF);
+}
+
+__global__ void __launch_bounds__(NW * 64)
+dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ lengths,
+                    const float* __restrict__ alpha_sk, const float* __restrict__ brow,
+                    float* __restrict__ post, float* __restrict__ grad_T,
+                    int* __restrict__ status, float* __restrict__ trash, int L1max, int L2max,
+                    int NSmax, float T, int bandwidth, int R) {
+    constexpr int P = PB;
+    extern __shared__ float smem[];
+    __shared__ int prog[NW];
+    __shared__ float red_g[NW];
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const unsigned ul4 = (unsigned)lane * 4u;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // Per wave, two chunk buffers, each: the cost tile (then the chunk's marginals),
+    // P alpha rows (steps t_hi-2 .. t_hi-P-1) and one row of values from the stripe
+    // above.  All three arrive by direct-to-LDS loads one chunk ahead.
+    using Tile = ChunkTile<P>;
+    constexpr int ABUF = Tile::FLOATS;
+    constexpr int RBUF = ABUF + P * 64;
+    constexpr int BUF = RBUF + 64;
+    float* bufs = smem + wave * 2 * BUF;
+    float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * BUF);  // [2][NW][R] (up, diag)
+    float2* sink = rings + 2 * NW * R + wave * DUMMY;
+    int* st = status + b;
+    const int tbase = Tile::read_base(lane);
+
+    if (lane == 0) prog[wave] = -1;
+    __syncthreads();
+
+    const int L1 = min(max(lengths[2 * b], 0), L1max);
+    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const float c = kLog2e / T;
+    const float bw = (bandwidth < 0 || L1 == 0 || L2 == 0) ? -1.0f : (float)bandwidth;
+    const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
+    const int nsteps = L2 + 63;
+    const int nch = (nsteps + P - 1) / P;
+    const size_t NT = (size_t)stored_steps(L2max);
+    const float* cbase = costs + (size_t)b * L1max * L2max;
+    float* pbase = post + (size_t)b * L1max * L2max;
+
+    zero_padding(pbase, L1, L2, L1max, L2max, NW * 64);
+
+    float g_acc = 0.0f;
+    float A[P + 2];
+
+    // Stripes run bottom-up: order q = 0..NS-1 handles stripe NS-1-q, on wave q % NW.
+    for (int q = wave; q < NS; q += NW) {
+        const int s = NS - 1 - q;
+        const int i0 = s * 64;
+        const int L2eff = (i0 + lane < L1) ? L2 : 0;
+        const float ej = band_centre(i0 + lane + 1, L1, L2);
+        // the terminal cell (L1, L2) starts with beta = 1
+        const int term_step = (i0 + lane == L1 - 1) ? L2 - 1 + lane : -1000000;
+        const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * NT * 64;
+        const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
+        const float2* ring_in = ring_from(rings, q, R);   // from stripe s+1
+        float2* ring_out = ring_of(rings, q, R);          // to stripe s-1
+        const bool below = q > 0;
+
+        auto issue_chunk = [&](int k) {
+            const int th = nsteps - 1 - k * P;
+            const uint32_t buf = lds_address(bufs + (k & 1) * BUF);
+            dma_tile<P, -1>(buf, cbase, i0, L1max, L2max, lane, th);
+            dma_rows<P, -1>(buf + ABUF * 4, astripe, th - 2, ul4);
+            uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
+            uint32_t rl = buf + RBUF * 4;
+            lds_dma_dword<0>(bup, roff, rl, 0u);
+        };
+
+        A[P] = lane_load(astripe + (size_t)(nsteps - 1 + APAD) * 64, ul4);
+        A[P + 1] = lane_load(astripe + (size_t)(nsteps - 2 + APAD) * 64, ul4);
+        __asm__ volatile("" ::"v"(A[P]), "v"(A[P + 1]));   // completes the two loads here
+        wave_lds_sync();   // the previous stripe's buffer reads are complete
+        issue_chunk(0);
+        float in_left = 0.0f, in_up = 0.0f, in_diag = 0.0f, in_diag_next = 0.0f;
+
+        for (int k = 0; k < nch; ++k) {
+            const int t_hi = nsteps - 1 - k * P;
+            chunk_waits<P>(prog, q, NS, k, nch, R, st);
+            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            float* buf = bufs + (k & 1) * BUF;
+            float* tile = buf;
+            float cv[P];
+#pragma unroll
+            for (int u = 0; u < P; ++u) cv[u] = tile[tbase + u];
+            A[0] = A[P];
+            A[1] = A[P + 1];
+#pragma unroll
+            for (int j = 0; j < P; ++j) A[j + 2] = buf[ABUF + j * 64 + lane];
+            // lane j: alpha of the row above at lane-63 step t_hi - j + 63 (row 0: PINF)
+            float bv = buf[RBUF + lane];
+            bv = (s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1) ? bv : kPINF;
+            float pre_u = 0.0f, pre_d = 0.0f;
+            if (below && lane >= 64 - P) {
+                const int j = 63 - lane;
+                pre_u = ring_in[ring_index(k * P + j + 63, R)].x;
+                pre_d = ring_in[ring_index(k * P + j + 62, R)].y;
+            }
+            if (k + 1 < nch) issue_chunk(k + 1);
+            float2* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
+            {
+                const float u0 = lane_bcast(pre_u, 63), d0 = lane_bcast(pre_d, 63);
+                const float d1 = lane_bcast(pre_d, 62);
+                if (lane == 63) { in_up = u0; in_diag = d0; in_diag_next = d1; }
+            }
+            float pre_d2 = wave_shr1(pre_d, 0.0f);
+            pre_d2 = wave_shr1(pre_d2, 0.0f);
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                const int t = t_hi - u;
+                const int col = t - lane;
+                const bool ok = (unsigned)col < (unsigned)L2eff && in_band(ej, col + 1, bw);
+                const float a0 = A[u], a1 = A[u + 1];
+                const float bv_next = wave_shl1(bv, kPINF);
+                const float upa = wave_shr1_or(a1, bv);
+                const float dga = wave_shr1_or(A[u + 2], bv_next);
+                bv = bv_next;
+                // softmin weights over (diagonal, up, left); none if all are PINF
+                const float m = fminf(fminf(dga, upa), a1);
+                const float ed = fast_exp2((m - dga) * c), eu = fast_exp2((m - upa) * c);
+                const float el = fast_exp2((m - a1) * c);
+                const float rin = m < kPINF ? fast_rcp((ed + eu) + el) : 0.0f;
+                // reference accumulation order: init, diagonal, left, up successor
+                const float binit = t == term_step ? 1.0f : 0.0f;
+                const float beta = ((binit + in_diag) + in_left) + in_up;
+                const float bl = ok ? beta : 0.0f;
+                const float br = bl * rin;
+                const float od = br * ed, ou = br * eu, ol = br * el;
+                tile[tbase + u] = bl;
+                // temperature gradient: beta * (softmin value - E_w[predecessor alpha])
+                const float cost = ok ? cv[u] : 0.0f;
+                const float smv = a0 - cost;
+                const float ea = (od * dga + ou * upa) + ol * a1;   // beta * E_w[alpha_pred]
+                g_acc += (ok && smv < kPINF) ? bl * smv - ea : 0.0f;
+                pub[u] = make_float2(ou, od);
+                pre_u = wave_shr1(pre_u, 0.0f);
+                in_left = ol;
+                in_up = wave_shl1_or(ou, pre_u);
+                in_diag = in_diag_next;
+                in_diag_next = wave_shl1_or(od, pre_d2);
+                pre_d2 = wave_shr1(pre_d2, 0.0f);
+            }
+            wave_lds_sync();
+            write_tile<P, -1>(tile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
+            publish(prog, wave, q * PROG_STRIDE + k + 1);
+        }
+    }
+
+    g_acc = wave_sum(g_acc);
+    if (lane == 0) red_g[wave] = g_acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float g = 0.0f;
+        for (int w = 0; w < NW; ++w) g += red_g[w];
+        grad_T[b] = g / T;
+    }
+}
+
+}  // namespace dtw
+}  // namespace d2p_amd
+
+using namespace d2p_amd;
+
+extern "C" size_t d2p_dtw_workspace_bytes(int B, int max_L1, int max_L2) {
+    if (B <= 0 || max_L1 <= 0 || max_L2 <= 0) return 0;
+    const size_t ns = ((size_t)max_L1 + 63) / 64;
+    // status words | trash line | skewed alpha table | last row of every stripe
+    return wf::status_bytes(B) + wf::TRASH_BYTES +
+           (size_t)B * ns * (size_t)wf::stored_steps(max_L2) * 65 * sizeof(float);
+}
+
+extern "C" int d2p_dtw_forward_marginals(const float* costs, const int* lengths, int B,
+                                         int max_L1, int max_L2, float temperature,
+                                         int bandwidth, float* value, float* marginals,
+                                         float* grad_T, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
+    D2P_REQUIRE(B >= 0 && max_L1 >= 0 && max_L2 >= 0, "negative dimension");
+    D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(costs && lengths && value && marginals && grad_T, "null pointer argument");
+    const size_t need = d2p_dtw_workspace_bytes(B, max_L1, max_L2);
+    D2P_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), "workspace too small");
+    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * dtw::PB, "max_L2 too large");
+    D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
+    hipStream_t st = (hipStream_t)stream;
+    const int ns = (max_L1 + 63) / 64;
+    const int Rf = wf::ring_len(max_L1, max_L2, 256);
+    const int Rb = wf::ring_len(max_L1, max_L2, 128);
+    const size_t lds_f = (size_t)wf::NW * 2 * 65 * dtw::PF * sizeof(float) +
+                         (2 * (size_t)wf::NW * Rf + wf::NW * dtw::DUMMY) * sizeof(float);
+    const size_t lds_b = (size_t)wf::NW * 2 * (65 * dtw::PB + 64 * dtw::PB + 64) * sizeof(float) +
+                         (2 * (size_t)wf::NW * Rb + wf::NW * dtw::DUMMY) * sizeof(float2);
+    D2P_REQUIRE(lds_f <= 160 * 1024 - 256 && lds_b <= 160 * 1024 - 256,
+                "sequence too long for the LDS stripe rings (max_L2 with more than 512 rows)");
+    D2P_HIP(hipFuncSetAttribute((const void*)dtw::dtw_forward_kernel,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_f));
+    D2P_HIP(hipFuncSetAttribute((const void*)dtw::dtw_backward_kernel,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
+    int* status = (int*)workspace;
+    float* trash = (float*)((char*)workspace + wf::status_bytes(B));
+    float* alpha_sk = (float*)((char*)trash + wf::TRASH_BYTES);
+    float* brow = alpha_sk + (size_t)B * ns * wf::stored_steps(max_L2) * 64;
+    D2P_LAUNCH("dtw_forward", dtw::dtw_forward_kernel, dim3(B), dim3(wf::NW * 64), lds_f, st,
+               costs, lengths, alpha_sk, brow, value, status, max_L1, max_L2, ns, temperature,
+               bandwidth, Rf);
+    D2P_HIP(hipGetLastError());
+    D2P_LAUNCH("dtw_backward", dtw::dtw_backward_kernel, dim3(B), dim3(wf::NW * 64), lds_b, st,
+               costs, lengths, alpha_sk, brow, marginals, grad_T, status, trash, max_L1, max_L2,
+               ns, temperature, bandwidth, Rb);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}

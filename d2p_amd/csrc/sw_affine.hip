@@ -92,6 +92,13 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         float4* ring_out = ring_of(rings, s, R);
         float* out = alpha_sk + ((size_t)b * NSmax + s) * 3 * PLANE + APAD * 64;   // M, step 0
         float* brow_s = brow + ((size_t)b * NSmax + s) * 3 * NT;                    // [3][NT]
+        // steps t < 0 hold the column-0 boundary (NINF), read by the reverse sweep
+#pragma unroll
+        for (int t = -APAD; t < 0; ++t) {
+            lane_store(out + t * 64, ul4, kNINF);
+            lane_store(out + PLANE + t * 64, ul4, kNINF);
+            lane_store(out + 2 * PLANE + t * 64, ul4, kNINF);
+        }
         wave_lds_sync();   // the previous stripe's tile reads are complete
         const uint32_t tile_lds = lds_address(tiles);
         dma_tile<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);

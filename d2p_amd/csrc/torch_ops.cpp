@@ -70,7 +70,7 @@ Dims checked_dims(const Tensor& x, const char* family) {
 
 // /root/reference/src/sw/torch_cuda.cpp:67-111
 Tensor resolve_lengths(const c10::optional<Tensor>& lengths_opt, const Dims& d,
-                       const torch::Device& device) {
+                       const torch::Device& device, const char* input = "scores") {
     if (!lengths_opt.has_value() || !lengths_opt->defined()) {
         // built on the device: no host round trip, nothing to validate
         Tensor l = torch::empty({d.B, 2}, torch::TensorOptions().dtype(torch::kInt32).device(device));
@@ -84,8 +84,8 @@ Tensor resolve_lengths(const c10::optional<Tensor>& lengths_opt, const Dims& d,
     TORCH_CHECK(lengths.dim() == 2 && lengths.size(0) == d.B && lengths.size(1) == 2,
                 "lengths must be [B, 2] with B = ", d.B, ", got ", lengths.sizes());
     TORCH_CHECK(lengths.scalar_type() == torch::kInt32, "lengths must be int32");
-    TORCH_CHECK(lengths.device() == device, "lengths must be on same device as scores, got ",
-                lengths.device(), " vs ", device);
+    TORCH_CHECK(lengths.device() == device, "lengths must be on same device as ", input,
+                ", got ", lengths.device(), " vs ", device);
     auto host = lengths.to(torch::kCPU);
     auto acc = host.accessor<int32_t, 2>();
     for (int b = 0; b < d.B; ++b) {
@@ -418,16 +418,108 @@ Tensor swa_marg_grad(Tensor, double, double, double, c10::optional<Tensor>) {
 }
 
 // ---------------------------------------------------------------------------
-// placeholders for the DTW family (kernels land separately)
+// soft DTW
 // ---------------------------------------------------------------------------
-std::vector<Tensor> dtw_t(Tensor, Tensor, Tensor, int64_t) { not_yet("soft_dtw"); }
-std::vector<Tensor> dtw_float(Tensor, double, c10::optional<Tensor>, c10::optional<int64_t>) {
-    not_yet("soft_dtw_float");
+
+// /root/reference/src/dtw/torch_cuda.cpp:33-83
+Dims checked_dims_dtw(const Tensor& costs) {
+    TORCH_CHECK(costs.dim() == 3, "costs must be 3D (B, L1, L2)");
+    const int64_t B = costs.size(0), L1 = costs.size(1), L2 = costs.size(2);
+    TORCH_CHECK(B >= 0 && B <= std::numeric_limits<int>::max(),
+                "DTW batch size is too large for CUDA kernels: ", B);
+    TORCH_CHECK(L1 >= 0 && L1 <= std::numeric_limits<int>::max() - 1,
+                "DTW L1 dimension is too large for CUDA kernels: ", L1);
+    TORCH_CHECK(L2 >= 0 && L2 <= std::numeric_limits<int>::max() - 1,
+                "DTW L2 dimension is too large for CUDA kernels: ", L2);
+    const int64_t cells = (L1 + 1) * (L2 + 1);
+    TORCH_CHECK(cells <= std::numeric_limits<int>::max(),
+                "DTW alpha table is too large for CUDA kernels: ", cells);
+    return Dims{(int)B, (int)L1, (int)L2};
 }
-std::tuple<Tensor, Tensor, Tensor> dtw_with_grads(Tensor, double, c10::optional<Tensor>,
-                                                  c10::optional<int64_t>) {
-    not_yet("soft_dtw_with_grads");
+
+int checked_bandwidth(int64_t bw) {
+    TORCH_CHECK(bw >= std::numeric_limits<int>::min() && bw <= std::numeric_limits<int>::max(),
+                "DTW bandwidth is out of CUDA int range: ", bw);
+    return (int)bw;
 }
+
+struct DtwOut {
+    Tensor value, marginals, grad_T;
+};
+
+DtwOut dtw_run(const Tensor& costs, const Tensor& lengths, const Dims& d, float T, int bw) {
+    auto opt = costs.options();
+    DtwOut o{torch::empty({d.B}, opt), torch::empty({d.B, d.L1, d.L2}, opt),
+             torch::empty({d.B}, opt)};
+    const size_t ws_bytes = d2p_dtw_workspace_bytes(d.B, d.L1, d.L2);
+    Tensor ws = workspace(ws_bytes, costs);
+    D2P_CALL(d2p_dtw_forward_marginals(
+        costs.data_ptr<float>(), lengths.data_ptr<int>(), d.B, d.L1, d.L2, T, bw,
+        o.value.data_ptr<float>(), o.marginals.data_ptr<float>(), o.grad_T.data_ptr<float>(),
+        ws.data_ptr(), ws_bytes, current_stream()));
+    return o;
+}
+
+// Autograd semantics of SoftDTWCUDAFunction (/root/reference/src/dtw/torch_cuda.cpp:139-325):
+// inputs (costs, temperature, lengths, bandwidth), outputs {value, marginals}.
+class SoftDTWFunction : public torch::autograd::Function<SoftDTWFunction> {
+   public:
+    static tensor_list forward(AutogradContext* ctx, Tensor costs, Tensor temperature,
+                               Tensor lengths, int64_t bandwidth) {
+        ctx->set_materialize_grads(false);
+        CHECK_INPUT_DEV(costs);
+        Dims d = checked_dims_dtw(costs);
+        TORCH_CHECK(temperature.numel() == 1, "temperature must be a scalar tensor");
+        c10::hip::HIPGuardMasqueradingAsCUDA guard(costs.device());
+        const int bw = checked_bandwidth(bandwidth);
+        Tensor l = resolve_lengths(lengths, d, costs.device(), "costs");
+        const float T = scalar_value(temperature, "temperature");
+        DtwOut o = dtw_run(costs, l, d, T, bw);
+        ctx->save_for_backward({o.marginals, o.grad_T});
+        return {o.value, o.marginals};
+    }
+    static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
+        auto saved = ctx->get_saved_variables();
+        Tensor marg = saved[0], gT = saved[1];
+        c10::hip::HIPGuardMasqueradingAsCUDA guard(marg.device());
+        Tensor grad_value = grads[0], grad_marg = grads[1];
+        Tensor gc, gt;
+        if (grad_value.defined() && grad_value.numel() > 0) {
+            gc = scale_by_batch(marg, grad_value);
+            if (ctx->needs_input_grad(1)) gt = grad_param_sum(grad_value, gT);
+        }
+        if (grad_marg.defined() && grad_marg.numel() > 0)
+            not_yet("soft_dtw marginal-path backward");
+        return {gc, gt, Tensor(), Tensor()};
+    }
+};
+
+std::vector<Tensor> dtw_t(Tensor costs, Tensor temperature, Tensor lengths, int64_t bandwidth) {
+    return SoftDTWFunction::apply(costs, temperature, lengths, bandwidth);
+}
+
+std::vector<Tensor> dtw_float(Tensor costs, double temperature, c10::optional<Tensor> lengths,
+                              c10::optional<int64_t> bandwidth) {
+    CHECK_INPUT_DEV(costs);
+    Dims d = checked_dims_dtw(costs);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(costs.device());
+    Tensor temp_t = torch::tensor({(float)temperature}, costs.options());
+    Tensor l = resolve_lengths(lengths, d, costs.device(), "costs");
+    return SoftDTWFunction::apply(costs, temp_t, l, bandwidth.has_value() ? *bandwidth : -1);
+}
+
+std::tuple<Tensor, Tensor, Tensor> dtw_with_grads(Tensor costs, double temperature,
+                                                  c10::optional<Tensor> lengths,
+                                                  c10::optional<int64_t> bandwidth) {
+    CHECK_INPUT_DEV(costs);
+    Dims d = checked_dims_dtw(costs);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(costs.device());
+    Tensor l = resolve_lengths(lengths, d, costs.device(), "costs");
+    const int bw = checked_bandwidth(bandwidth.has_value() ? *bandwidth : -1);
+    DtwOut o = dtw_run(costs, l, d, (float)temperature, bw);
+    return {o.value, o.marginals, o.grad_T};
+}
+
 Tensor dtw_hvp(Tensor, Tensor, double, c10::optional<Tensor>, c10::optional<int64_t>) {
     not_yet("soft_dtw_hvp");
 }

@@ -55,8 +55,9 @@ __host__ inline int ring_len(int max_L1, int max_L2, int min_len) {
     return (r + STEP_QUANTUM - 1) / STEP_QUANTUM * STEP_QUANTUM;
 }
 
-// Steps stored per stripe and plane in a skewed table: APAD leading steps t < 0
-// (never written by a sweep; readers mask them) and then whole chunks.
+// Steps stored per stripe and plane in a skewed table: APAD leading steps t < 0,
+// which the forward sweep fills with the column-0 boundary value (reverse sweeps
+// read the cells left of column 0 from them without guards), then whole chunks.
 __host__ __device__ inline int stored_steps(int L2max) {
     return APAD + ((L2max + 63 + STEP_QUANTUM - 1) / STEP_QUANTUM) * STEP_QUANTUM;
 }

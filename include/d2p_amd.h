@@ -91,6 +91,26 @@ int d2p_swa_forward_marginals(const float* scores, const int* lengths, int B, in
                               size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Soft dynamic time warping (optional Sakoe-Chiba band)
+ * ------------------------------------------------------------------------- */
+
+/* Workspace bytes needed by d2p_dtw_forward_marginals (status words first). */
+size_t d2p_dtw_workspace_bytes(int B, int max_L1, int max_L2);
+
+/* Forward value and alignment marginals in one call.
+ * Replaces the pair dtw_forward + dtw_backward (/root/reference/src/dtw/kernels.cuh:95-129)
+ * as sequenced by SoftDTWCUDAFunction::forward (/root/reference/src/dtw/torch_cuda.cpp:141-205).
+ *   costs     [B, max_L1, max_L2]  input
+ *   bandwidth                      Sakoe-Chiba half-width in cells, < 0 = no band
+ *   value     [B]                  out: soft-DTW value alpha[L1, L2]
+ *   marginals [B, max_L1, max_L2]  out: dvalue/dcosts (zero in padding and off-band)
+ *   grad_T    [B]                  out: dvalue/dtemperature */
+int d2p_dtw_forward_marginals(const float* costs, const int* lengths, int B, int max_L1,
+                              int max_L2, float temperature, int bandwidth, float* value,
+                              float* marginals, float* grad_T, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Shared helpers
  * ------------------------------------------------------------------------- */
 

@@ -25,6 +25,8 @@ SIGNATURES = {
     "d2p_swa_workspace_bytes": (_z, [_i, _i, _i]),
     "d2p_swa_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _f, _f, _p, _p, _p, _p, _p, _p,
                                        _z, _p]),
+    "d2p_dtw_workspace_bytes": (_z, [_i, _i, _i]),
+    "d2p_dtw_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _i, _p, _p, _p, _p, _z, _p]),
     "d2p_profile_enable": (_i, [_i]),
     "d2p_profile_report": (_i, [ctypes.c_char_p, _z]),
     "d2p_profile_reset": (None, []),
@@ -111,6 +113,22 @@ def swa_forward_marginals(scores, lengths, go, ge, T):
     nbytes = lib().d2p_swa_workspace_bytes(B, L1, L2)
     ws = _workspace(nbytes, dev)
     check(lib().d2p_swa_forward_marginals(ptr(scores), ptr(lengths), B, L1, L2, go, ge, T,
+                                          *[ptr(o) for o in outs], ptr(ws), nbytes, stream()))
+    _check_status(ws, B)
+    return tuple(outs)
+
+
+def dtw_forward_marginals(costs, lengths, T, bandwidth=-1):
+    """Soft DTW: (value, marginals, grad_T) through the C ABI."""
+    import torch
+    B, L1, L2 = costs.shape
+    dev = costs.device
+    lengths = _lengths(lengths, B, L1, L2, dev)
+    outs = [torch.empty(B, device=dev), torch.empty(B, L1, L2, device=dev),
+            torch.empty(B, device=dev)]
+    nbytes = lib().d2p_dtw_workspace_bytes(B, L1, L2)
+    ws = _workspace(nbytes, dev)
+    check(lib().d2p_dtw_forward_marginals(ptr(costs), ptr(lengths), B, L1, L2, T, bandwidth,
                                           *[ptr(o) for o in outs], ptr(ws), nbytes, stream()))
     _check_status(ws, B)
     return tuple(outs)
