@@ -29,7 +29,6 @@ namespace dtw {
 using namespace wf;
 
 constexpr int PF = 16;               // steps per chunk, forward sweep
-constexpr int PB = 16;               // steps per chunk, backward sweep
 constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do not publish
 
 // i*L2/L1 of (1-based) row i in float, as the reference's band test computes it.
@@ -57,8 +56,8 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = ChunkTile<P>;
     float* tiles = smem + wave * 2 * Tile::FLOATS;         // double-buffered cost chunk
-    float* rings = smem + NW * 2 * Tile::FLOATS;           // [2 parities][NW][R]
-    float* sink = rings + 2 * NW * R + wave * DUMMY;       // per-wave write sink
+    float* rings = smem + NW * 2 * Tile::FLOATS;           // [NW][R]
+    float* sink = rings + NW * R + wave * DUMMY;       // per-wave write sink
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
 
@@ -148,14 +147,14 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
     if (threadIdx.x == 0) value[b] = NS > 0 ? terminal : ((L1 == 0 && L2 == 0) ? 0.0f : kPINF);
 }
 
+template <int P>
 __global__ void __launch_bounds__(NW * 64)
 dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ lengths,
                     const float* __restrict__ alpha_sk, const float* __restrict__ brow,
                     float* __restrict__ post, float* __restrict__ grad_T,
                     int* __restrict__ status, float* __restrict__ trash, int L1max, int L2max,
                     int NSmax, float T, int bandwidth, int R) {
-    constexpr int P = PB;
-    extern __shared__ float smem[];
+        extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red_g[NW];
     const int b = blockIdx.x;
@@ -170,8 +169,8 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
     constexpr int RBUF = ABUF + P * 64;
     constexpr int BUF = RBUF + 64;
     float* bufs = smem + wave * 2 * BUF;
-    float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * BUF);  // [2][NW][R] (up, diag)
-    float2* sink = rings + 2 * NW * R + wave * DUMMY;
+    float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * BUF);  // [NW][R] (up, diag)
+    float2* sink = rings + NW * R + wave * DUMMY;
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
 
@@ -331,22 +330,30 @@ extern "C" int d2p_dtw_forward_marginals(const float* costs, const int* lengths,
     D2P_REQUIRE(costs && lengths && value && marginals && grad_T, "null pointer argument");
     const size_t need = d2p_dtw_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), "workspace too small");
-    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * dtw::PB, "max_L2 too large");
+    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 8, "max_L2 too large");
     D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
     hipStream_t st = (hipStream_t)stream;
     const int ns = (max_L1 + 63) / 64;
     const int Rf = wf::ring_len(max_L1, max_L2, 256);
     const int Rb = wf::ring_len(max_L1, max_L2, 128);
     const size_t lds_f = (size_t)wf::NW * 2 * 65 * dtw::PF * sizeof(float) +
-                         (2 * (size_t)wf::NW * Rf + wf::NW * dtw::DUMMY) * sizeof(float);
-    const size_t lds_b = (size_t)wf::NW * 2 * (65 * dtw::PB + 64 * dtw::PB + 64) * sizeof(float) +
-                         (2 * (size_t)wf::NW * Rb + wf::NW * dtw::DUMMY) * sizeof(float2);
-    D2P_REQUIRE(lds_f <= 160 * 1024 - 256 && lds_b <= 160 * 1024 - 256,
-                "sequence too long for the LDS stripe rings (max_L2 with more than 512 rows)");
+                         ((size_t)wf::NW * Rf + wf::NW * dtw::DUMMY) * sizeof(float);
+    // backward: 16-step chunks when they fit in LDS, else 8-step chunks (long rows
+    // need long rings)
+    auto lds_bwd = [&](int P) {
+        return (size_t)wf::NW * 2 * (65 * P + 64 * P + 64) * sizeof(float) +
+               ((size_t)wf::NW * Rb + wf::NW * dtw::DUMMY) * sizeof(float2);
+    };
+    const size_t lds_limit = 160 * 1024 - 256;
+    const int Pb = lds_bwd(16) <= lds_limit ? 16 : 8;
+    const size_t lds_b = lds_bwd(Pb);
+    D2P_REQUIRE(lds_f <= lds_limit && lds_b <= lds_limit,
+                "sequence too long for the LDS stripe rings");
+    const void* bwd_kernel = Pb == 16 ? (const void*)dtw::dtw_backward_kernel<16>
+                                      : (const void*)dtw::dtw_backward_kernel<8>;
     D2P_HIP(hipFuncSetAttribute((const void*)dtw::dtw_forward_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_f));
-    D2P_HIP(hipFuncSetAttribute((const void*)dtw::dtw_backward_kernel,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
+    D2P_HIP(hipFuncSetAttribute(bwd_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
     int* status = (int*)workspace;
     float* trash = (float*)((char*)workspace + wf::status_bytes(B));
     float* alpha_sk = (float*)((char*)trash + wf::TRASH_BYTES);
@@ -355,7 +362,12 @@ extern "C" int d2p_dtw_forward_marginals(const float* costs, const int* lengths,
                costs, lengths, alpha_sk, brow, value, status, max_L1, max_L2, ns, temperature,
                bandwidth, Rf);
     D2P_HIP(hipGetLastError());
-    D2P_LAUNCH("dtw_backward", dtw::dtw_backward_kernel, dim3(B), dim3(wf::NW * 64), lds_b, st,
+    if (Pb == 16)
+        D2P_LAUNCH("dtw_backward", dtw::dtw_backward_kernel<16>, dim3(B), dim3(wf::NW * 64), lds_b, st,
+               costs, lengths, alpha_sk, brow, marginals, grad_T, status, trash, max_L1, max_L2,
+               ns, temperature, bandwidth, Rb);
+    else
+        D2P_LAUNCH("dtw_backward", dtw::dtw_backward_kernel<8>, dim3(B), dim3(wf::NW * 64), lds_b, st,
                costs, lengths, alpha_sk, brow, marginals, grad_T, status, trash, max_L1, max_L2,
                ns, temperature, bandwidth, Rb);
     D2P_HIP(hipGetLastError());

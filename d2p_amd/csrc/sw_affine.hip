@@ -62,8 +62,8 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = ChunkTile<P>;
     float* tiles = smem + wave * 2 * Tile::FLOATS;   // double-buffered score chunk
-    float4* rings = reinterpret_cast<float4*>(smem + NW * 2 * Tile::FLOATS);   // [2][NW][R]
-    float4* sink = rings + 2 * NW * R + wave * DUMMY;
+    float4* rings = reinterpret_cast<float4*>(smem + NW * 2 * Tile::FLOATS);   // [NW][R]
+    float4* sink = rings + NW * R + wave * DUMMY;
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
 
@@ -209,11 +209,11 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
     constexpr int WFLOATS = OTILE + Tile::FLOATS;
     float* wbuf = smem + wave * WFLOATS;
     float* otile = wbuf + OTILE;
-    // rings [2][NW][R]: (up M, up I, diag M, diag I) and diag D, from lane 0 upward
+    // rings [NW][R]: (up M, up I, diag M, diag I) and diag D, from lane 0 upward
     float4* ring4 = reinterpret_cast<float4*>(smem + NW * WFLOATS);
-    float* ring1 = reinterpret_cast<float*>(ring4 + 2 * NW * R);
-    float4* sink4 = reinterpret_cast<float4*>(ring1 + 2 * NW * R) + wave * (64 + P);
-    float* sink1 = reinterpret_cast<float*>(reinterpret_cast<float4*>(ring1 + 2 * NW * R) +
+    float* ring1 = reinterpret_cast<float*>(ring4 + NW * R);
+    float4* sink4 = reinterpret_cast<float4*>(ring1 + NW * R) + wave * (64 + P);
+    float* sink1 = reinterpret_cast<float*>(reinterpret_cast<float4*>(ring1 + NW * R) +
                                             NW * (64 + P)) + wave * (64 + P);
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
@@ -225,7 +225,6 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
     const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
     const float c = kLog2e / T;
     const float S = partition[b];
-    const float Sc = S * c;
     const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
     const int nsteps = L2 + 63;
     const int nch = (nsteps + P - 1) / P;
@@ -385,11 +384,11 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 const float g0 = fast_exp2((d0v - md) * c), g1 = fast_exp2((d1v - md) * c);
                 // betas in the reference's accumulation order
                 float lp;
-                lp = AM[u] * c - Sc;
+                lp = (AM[u] - S) * c;   // subtract first: exact for nearby values
                 const float initM = fast_exp2(lp < 0.0f ? lp : 0.0f);
-                lp = AI[u] * c - Sc;
+                lp = (AI[u] - S) * c;
                 const float initI = fast_exp2(lp < 0.0f ? lp : 0.0f);
-                lp = AD[u] * c - Sc;
+                lp = (AD[u] - S) * c;
                 const float initD = fast_exp2(lp < 0.0f ? lp : 0.0f);
                 const float betaM = ((initM + dM) + lM) + uM;
                 const float betaI = (initI + dI) + uI;
@@ -485,10 +484,10 @@ extern "C" int d2p_swa_forward_marginals(const float* scores, const int* lengths
     const int Rf = wf::ring_len(max_L1, max_L2, 256);
     const int Rb = wf::ring_len(max_L1, max_L2, 128);
     const size_t lds_f = (size_t)wf::NW * 2 * 65 * swa::PF * sizeof(float) +
-                         (2 * (size_t)wf::NW * Rf + wf::NW * swa::DUMMY) * sizeof(float4);
+                         ((size_t)wf::NW * Rf + wf::NW * swa::DUMMY) * sizeof(float4);
     const size_t wfloats = 65 * swa::PB + 3 * swa::PB * 64 + 3 * 64 + 65 * swa::PB;
     const size_t lds_b = (size_t)wf::NW * wfloats * sizeof(float) +
-                         2 * (size_t)wf::NW * Rb * (sizeof(float4) + sizeof(float)) +
+                         (size_t)wf::NW * Rb * (sizeof(float4) + sizeof(float)) +
                          (size_t)wf::NW * (64 + swa::PB) * (sizeof(float4) + sizeof(float));
     D2P_REQUIRE(lds_f <= 160 * 1024 - 256 && lds_b <= 160 * 1024 - 256,
                 "sequence too long for the LDS stripe rings (max_L2 with more than 512 rows)");

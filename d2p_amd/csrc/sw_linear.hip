@@ -29,7 +29,6 @@ namespace sw {
 using namespace wf;
 
 constexpr int PF = 16;               // steps per chunk, forward sweep
-constexpr int PB = 16;               // steps per chunk, backward sweep
 constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do not publish
 
 __global__ void __launch_bounds__(NW * 64)
@@ -48,8 +47,8 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = ChunkTile<P>;
     float* tiles = smem + wave * 2 * Tile::FLOATS;         // double-buffered score chunk
-    float* rings = smem + NW * 2 * Tile::FLOATS;           // [2 parities][NW][R]
-    float* sink = rings + 2 * NW * R + wave * DUMMY;       // per-wave write sink
+    float* rings = smem + NW * 2 * Tile::FLOATS;           // [NW][R]
+    float* sink = rings + NW * R + wave * DUMMY;       // per-wave write sink
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
 
@@ -147,6 +146,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     }
 }
 
+template <int P>
 __global__ void __launch_bounds__(NW * 64)
 sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                    const float* __restrict__ alpha_sk, const float* __restrict__ brow,
@@ -154,8 +154,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                    float* __restrict__ post, float* __restrict__ grad_gap,
                    float* __restrict__ grad_T, int* __restrict__ status, float* __restrict__ trash,
                    int L1max, int L2max, int NSmax, float gap, float T, int R) {
-    constexpr int P = PB;
-    extern __shared__ float smem[];
+        extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red_g[NW], red_p[NW];
     const int b = blockIdx.x;
@@ -170,8 +169,8 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     constexpr int RBUF = ABUF + P * 64;           // row above
     constexpr int BUF = RBUF + 64;
     float* bufs = smem + wave * 2 * BUF;
-    float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * BUF);  // [2][NW][R] (up, diag)
-    float2* sink = rings + 2 * NW * R + wave * DUMMY;
+    float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * BUF);  // [NW][R] (up, diag)
+    float2* sink = rings + NW * R + wave * DUMMY;
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
 
@@ -182,7 +181,6 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
     const float c = kLog2e / T;
     const float S = partition[b];
-    const float Sc = S * c;
     const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
     const int nsteps = L2 + 63;
     const int nch = (nsteps + P - 1) / P;
@@ -289,7 +287,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const float e0 = fast_exp2((vd - m) * c), e1 = fast_exp2((vu - m) * c);
                 const float e2 = fast_exp2((vl - m) * c), e3 = fast_exp2((sc - m) * c);
                 const float rin = fast_rcp(((e0 + e1) + e2) + e3);
-                float lp = a0 * c - Sc;
+                float lp = (a0 - S) * c;   // subtract first: exact for nearby values
                 lp = lp < 0.0f ? lp : 0.0f;
                 const float binit = fast_exp2(lp);
                 // reference accumulation order: init, diagonal, left, up successor
@@ -369,7 +367,7 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
                 "null pointer argument");
     const size_t need = d2p_sw_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), "workspace too small");
-    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * sw::PB, "max_L2 too large");
+    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 8, "max_L2 too large");
     // per-lane byte offsets within one batch element are 32-bit
     D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
     hipStream_t st = (hipStream_t)stream;
@@ -377,15 +375,23 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
     const int Rf = wf::ring_len(max_L1, max_L2, 256);
     const int Rb = wf::ring_len(max_L1, max_L2, 128);
     const size_t lds_f = (size_t)wf::NW * 2 * 65 * sw::PF * sizeof(float) +
-                         (2 * (size_t)wf::NW * Rf + wf::NW * sw::DUMMY) * sizeof(float);
-    const size_t lds_b = (size_t)wf::NW * 2 * (65 * sw::PB + 64 * sw::PB + 64) * sizeof(float) +
-                         (2 * (size_t)wf::NW * Rb + wf::NW * sw::DUMMY) * sizeof(float2);
-    D2P_REQUIRE(lds_f <= 160 * 1024 - 256 && lds_b <= 160 * 1024 - 256,
-                "sequence too long for the LDS stripe rings (max_L2 with more than 512 rows)");
+                         ((size_t)wf::NW * Rf + wf::NW * sw::DUMMY) * sizeof(float);
+    // backward: 16-step chunks when they fit in LDS, else 8-step chunks (long rows
+    // need long rings)
+    auto lds_bwd = [&](int P) {
+        return (size_t)wf::NW * 2 * (65 * P + 64 * P + 64) * sizeof(float) +
+               ((size_t)wf::NW * Rb + wf::NW * sw::DUMMY) * sizeof(float2);
+    };
+    const size_t lds_limit = 160 * 1024 - 256;
+    const int Pb = lds_bwd(16) <= lds_limit ? 16 : 8;
+    const size_t lds_b = lds_bwd(Pb);
+    D2P_REQUIRE(lds_f <= lds_limit && lds_b <= lds_limit,
+                "sequence too long for the LDS stripe rings");
+    const void* bwd_kernel = Pb == 16 ? (const void*)sw::sw_backward_kernel<16>
+                                      : (const void*)sw::sw_backward_kernel<8>;
     D2P_HIP(hipFuncSetAttribute((const void*)sw::sw_forward_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_f));
-    D2P_HIP(hipFuncSetAttribute((const void*)sw::sw_backward_kernel,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
+    D2P_HIP(hipFuncSetAttribute(bwd_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
     int* status = (int*)workspace;
     float* trash = (float*)((char*)workspace + wf::status_bytes(B));
     float* alpha_sk = (float*)((char*)trash + wf::TRASH_BYTES);
@@ -394,10 +400,14 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
                scores, lengths, alpha_sk, brow, partition, status, max_L1, max_L2, ns, gap,
                temperature, Rf);
     D2P_HIP(hipGetLastError());
-    D2P_LAUNCH("sw_backward", sw::sw_backward_kernel, dim3(B), dim3(wf::NW * 64), lds_b, st,
+    if (Pb == 16)
+        D2P_LAUNCH("sw_backward", sw::sw_backward_kernel<16>, dim3(B), dim3(wf::NW * 64), lds_b, st,
                scores, lengths, alpha_sk, brow, partition, marginals, grad_gap, grad_T, status,
-               trash,
-               max_L1, max_L2, ns, gap, temperature, Rb);
+               trash, max_L1, max_L2, ns, gap, temperature, Rb);
+    else
+        D2P_LAUNCH("sw_backward", sw::sw_backward_kernel<8>, dim3(B), dim3(wf::NW * 64), lds_b, st,
+               scores, lengths, alpha_sk, brow, partition, marginals, grad_gap, grad_T, status,
+               trash, max_L1, max_L2, ns, gap, temperature, Rb);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }

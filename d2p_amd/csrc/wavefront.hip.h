@@ -41,15 +41,17 @@ constexpr size_t TRASH_BYTES = 256;   // one line that masked lanes store into
 __host__ __device__ constexpr int lead(int P) { return 2 + 62 / P; }
 
 // Ring length (columns) of one stripe boundary.  It must exceed the pipeline window
-// (LEAD chunks plus back-pressure slack); when a wave owns several stripes (more
-// than NW stripes) it must also satisfy NW * R > L2 + 64 + 4*STEP_QUANTUM, which
-// rules out a cycle of back-pressure waits across a whole round of waves.  A
-// multiple of STEP_QUANTUM, hence of every chunk length.
+// (LEAD chunks plus back-pressure slack).  When a wave owns several stripes (more
+// than NW stripes) its ring is reused by its next stripe only after the consumer of
+// the previous one has finished; that wait closes a chain of back-pressure waits
+// through the other NW - 1 rings, which cannot stall as long as
+// (NW - 1) * R > L2 + 64 + 4*STEP_QUANTUM.  A multiple of STEP_QUANTUM, hence of
+// every chunk length.
 __host__ inline int ring_len(int max_L1, int max_L2, int min_len) {
     const int ns = (max_L1 + 63) / 64;
     int r = min_len;
     if (ns > NW) {
-        const int need = (max_L2 + 64 + 4 * STEP_QUANTUM + NW - 1) / NW + 1;
+        const int need = (max_L2 + 64 + 4 * STEP_QUANTUM + NW - 2) / (NW - 1) + 1;
         r = r > need ? r : need;
     }
     return (r + STEP_QUANTUM - 1) / STEP_QUANTUM * STEP_QUANTUM;
@@ -94,10 +96,14 @@ __device__ __forceinline__ void wait_for(int* prog, int w, int need, int* status
 // The chunk-level waits of sweep order q (q = stripe for forward sweeps, the
 // reversed stripe index for reverse sweeps) before its chunk k: the producer q-1
 // must be LEAD chunks ahead, and the consumer q+1 must have consumed the ring slots
-// this chunk overwrites.
+// this chunk overwrites.  Before its first chunk, a stripe that reuses its wave's
+// ring (q >= NW) also waits until the consumer of the ring's previous stripe
+// (q - NW + 1) has finished.
 template <int P>
 __device__ __forceinline__ void chunk_waits(int* prog, int q, int NS, int k, int nch, int R,
                                             int* status_b) {
+    if (k == 0 && q >= NW)
+        wait_for(prog, (q + 1) % NW, (q - NW + 1) * PROG_STRIDE + nch, status_b);
     if (q > 0) wait_for(prog, (q - 1) % NW, (q - 1) * PROG_STRIDE + min(k + lead(P), nch), status_b);
     if (q + 1 < NS) {
         const int need = k - 2 - R / P;   // slots of steps < kP+P-R must be consumed
@@ -110,15 +116,15 @@ __device__ __forceinline__ int ring_index(int slot, int R) {
     return slot < 0 ? slot + R : slot;
 }
 
-// Parity-double-buffered rings [2][NW][R] of element type E: the ring sweep order q
+// One ring of R elements of type E per wave ([NW][R]): the ring sweep order q
 // writes, and the ring it reads (written by q - 1).
 template <class E>
 __device__ __forceinline__ E* ring_of(E* rings, int q, int R) {
-    return rings + (((q / NW) & 1) * NW + q % NW) * R;
+    return rings + (q % NW) * R;
 }
 template <class E>
 __device__ __forceinline__ E* ring_from(E* rings, int q, int R) {
-    return rings + ((((q - 1) / NW) & 1) * NW + (q + NW - 1) % NW) * R;
+    return rings + ((q + NW - 1) % NW) * R;
 }
 
 // ------------------------------------------------------------ direct-to-LDS loads

@@ -181,9 +181,10 @@ void oracle_sw_forward(const float* scores, float* alpha, float* partition,
 }
 
 /* sw/kernels_cpu.cpp:154-271 */
-void oracle_sw_backward(const float* alpha, const float* scores, const float* partition,
-                        float* beta, float* posteriors, float* grad_gap, float* grad_T,
-                        const int* lengths, int B, int maxL1, int maxL2, float gap, float T) {
+static void sw_backward_impl(const float* alpha, const float* scores, const float* partition,
+                             float* beta, float* posteriors, float* grad_gap, float* grad_T,
+                             double* sums64, const int* lengths, int B, int maxL1, int maxL2,
+                             float gap, float T) {
     const size_t astride = (size_t)(maxL1 + 1) * (maxL2 + 1);
     const size_t sstride = (size_t)maxL1 * maxL2;
     const size_t acols = (size_t)maxL2 + 1, scols = (size_t)maxL2;
@@ -201,6 +202,7 @@ void oracle_sw_backward(const float* alpha, const float* scores, const float* pa
             for (int j = 0; j <= L2; ++j)
                 be[AIDX(i, j)] = xexp(clamp_lp((a[AIDX(i, j)] - S) / T));
         float gsum = 0.0f;
+        double gsum_d = 0.0;
         FOR_DIAG_REV(L1, L2, i, j) {
             float sc = s[SIDX(i, j)];
             float bij = be[AIDX(i, j)];
@@ -213,15 +215,52 @@ void oracle_sw_backward(const float* alpha, const float* scores, const float* pa
             softmax_w(v, w, 4, T);
             post[SIDX(i, j)] += bij * (w[0] + w[3]);
             if (i > 1 && j > 1 && w[0] > 0.0f) be[AIDX(i - 1, j - 1)] += bij * w[0];
-            if (i > 1 && w[1] > 0.0f) { be[AIDX(i - 1, j)] += bij * w[1]; gsum += bij * w[1]; }
-            if (j > 1 && w[2] > 0.0f) { be[AIDX(i, j - 1)] += bij * w[2]; gsum += bij * w[2]; }
+            if (i > 1 && w[1] > 0.0f) {
+                be[AIDX(i - 1, j)] += bij * w[1];
+                gsum += bij * w[1];
+                gsum_d += (double)(bij * w[1]);
+            }
+            if (j > 1 && w[2] > 0.0f) {
+                be[AIDX(i, j - 1)] += bij * w[2];
+                gsum += bij * w[2];
+                gsum_d += (double)(bij * w[2]);
+            }
         }
         kahan k = {0.0f, 0.0f};
         for (size_t q = 0; q < sstride; ++q) kadd(&k, post[q] * s[q]);
         float expected = k.s + gsum * gap;
         grad_gap[b] = gsum;
         grad_T[b] = (S - expected) / T;
+        if (sums64) {
+            double e = 0.0;
+            for (size_t q = 0; q < sstride; ++q) e += (double)post[q] * s[q];
+            sums64[2 * b] = gsum_d;
+            sums64[2 * b + 1] = ((double)S - (e + gsum_d * gap)) / T;
+        }
     }
+}
+
+void oracle_sw_backward(const float* alpha, const float* scores, const float* partition,
+                        float* beta, float* posteriors, float* grad_gap, float* grad_T,
+                        const int* lengths, int B, int maxL1, int maxL2, float gap, float T) {
+    sw_backward_impl(alpha, scores, partition, beta, posteriors, grad_gap, grad_T, NULL, lengths,
+                     B, maxL1, maxL2, gap, T);
+}
+
+/* The same reverse sweep; additionally sums every per-cell term of grad_gap and
+ * grad_T in double: sums64[2b] = dS/dgap, sums64[2b+1] = dS/dT.  The fp32 outputs
+ * are the reference's (sequential fp32 sums, which drift from the exact sum on
+ * large tables); the double sums isolate that drift for the parity tests. */
+void oracle_sw_backward_sums64(const float* alpha, const float* scores, const float* partition,
+                               float* beta, float* posteriors, double* sums64,
+                               const int* lengths, int B, int maxL1, int maxL2, float gap,
+                               float T) {
+    float* gg = (float*)malloc(sizeof(float) * (B > 0 ? B : 1));
+    float* gt = (float*)malloc(sizeof(float) * (B > 0 ? B : 1));
+    sw_backward_impl(alpha, scores, partition, beta, posteriors, gg, gt, sums64, lengths, B,
+                     maxL1, maxL2, gap, T);
+    free(gg);
+    free(gt);
 }
 
 /* sw/kernels_cpu.cpp:279-477 */
@@ -449,10 +488,10 @@ void oracle_swa_forward(const float* scores, float* alpha, float* partition,
 }
 
 /* sw_affine/kernels_cpu.cpp:201-356 */
-void oracle_swa_backward(const float* alpha, const float* scores, const float* partition,
-                         float* beta, float* posteriors, float* grad_open, float* grad_ext,
-                         float* grad_T, const int* lengths, int B, int maxL1, int maxL2,
-                         float go, float ge, float T) {
+static void swa_backward_impl(const float* alpha, const float* scores, const float* partition,
+                              float* beta, float* posteriors, float* grad_open, float* grad_ext,
+                              float* grad_T, double* sums64, const int* lengths, int B,
+                              int maxL1, int maxL2, float go, float ge, float T) {
     const size_t cstride = (size_t)(maxL1 + 1) * (maxL2 + 1);
     const size_t astride = 3 * cstride;
     const size_t sstride = (size_t)maxL1 * maxL2;
@@ -474,6 +513,7 @@ void oracle_swa_backward(const float* alpha, const float* scores, const float* p
                     be[id] = xexp(clamp_lp((a[id] - S) / T));
                 }
         float gopen = 0.0f, gext = 0.0f;
+        double gopen_d = 0.0, gext_d = 0.0;
         FOR_DIAG_REV(L1, L2, i, j) {
             size_t c = AIDX(i, j), cd = AIDX(i - 1, j - 1), cu = AIDX(i - 1, j), cl = AIDX(i, j - 1);
             float sc = s[SIDX(i, j)];
@@ -500,8 +540,16 @@ void oracle_swa_backward(const float* alpha, const float* scores, const float* p
                 v[1] = (i > 1) ? a[PI(cu)] + ge : NINF;
                 softmax_w(v, w, 2, T);
                 if (i > 1) {
-                    if (w[0] > 0.0f) { be[PM(cu)] += bI * w[0]; gopen += bI * w[0]; }
-                    if (w[1] > 0.0f) { be[PI(cu)] += bI * w[1]; gext += bI * w[1]; }
+                    if (w[0] > 0.0f) {
+                        be[PM(cu)] += bI * w[0];
+                        gopen += bI * w[0];
+                        gopen_d += (double)(bI * w[0]);
+                    }
+                    if (w[1] > 0.0f) {
+                        be[PI(cu)] += bI * w[1];
+                        gext += bI * w[1];
+                        gext_d += (double)(bI * w[1]);
+                    }
                 }
             }
             float bD = be[PD(c)];
@@ -511,8 +559,16 @@ void oracle_swa_backward(const float* alpha, const float* scores, const float* p
                 v[1] = (j > 1) ? a[PD(cl)] + ge : NINF;
                 softmax_w(v, w, 2, T);
                 if (j > 1) {
-                    if (w[0] > 0.0f) { be[PM(cl)] += bD * w[0]; gopen += bD * w[0]; }
-                    if (w[1] > 0.0f) { be[PD(cl)] += bD * w[1]; gext += bD * w[1]; }
+                    if (w[0] > 0.0f) {
+                        be[PM(cl)] += bD * w[0];
+                        gopen += bD * w[0];
+                        gopen_d += (double)(bD * w[0]);
+                    }
+                    if (w[1] > 0.0f) {
+                        be[PD(cl)] += bD * w[1];
+                        gext += bD * w[1];
+                        gext_d += (double)(bD * w[1]);
+                    }
                 }
             }
         }
@@ -523,8 +579,40 @@ void oracle_swa_backward(const float* alpha, const float* scores, const float* p
         grad_open[b] = gopen;
         grad_ext[b] = gext;
         grad_T[b] = (S - expected) / T;
+        if (sums64) {
+            double e = 0.0;
+            for (size_t q = 0; q < sstride; ++q) e += (double)post[q] * s[q];
+            sums64[3 * b] = gopen_d;
+            sums64[3 * b + 1] = gext_d;
+            sums64[3 * b + 2] = ((double)S - (e + gopen_d * go + gext_d * ge)) / T;
+        }
     }
 }
+
+void oracle_swa_backward(const float* alpha, const float* scores, const float* partition,
+                         float* beta, float* posteriors, float* grad_open, float* grad_ext,
+                         float* grad_T, const int* lengths, int B, int maxL1, int maxL2,
+                         float go, float ge, float T) {
+    swa_backward_impl(alpha, scores, partition, beta, posteriors, grad_open, grad_ext, grad_T,
+                      NULL, lengths, B, maxL1, maxL2, go, ge, T);
+}
+
+/* The same reverse sweep with the parameter sums also taken in double:
+ * sums64[3b..3b+2] = dS/dopen, dS/dext, dS/dT (see oracle_sw_backward_sums64). */
+void oracle_swa_backward_sums64(const float* alpha, const float* scores, const float* partition,
+                                float* beta, float* posteriors, double* sums64,
+                                const int* lengths, int B, int maxL1, int maxL2, float go,
+                                float ge, float T) {
+    const size_t n = sizeof(float) * (B > 0 ? B : 1);
+    float *g0 = (float*)malloc(n), *g1 = (float*)malloc(n), *g2 = (float*)malloc(n);
+    swa_backward_impl(alpha, scores, partition, beta, posteriors, g0, g1, g2, sums64, lengths,
+                      B, maxL1, maxL2, go, ge, T);
+    free(g0);
+    free(g1);
+    free(g2);
+}
+
+
 
 /* sw_affine/kernels_cpu.cpp:362-631 */
 void oracle_swa_hvp(const float* alpha, const float* scores, const float* partition,
@@ -869,9 +957,10 @@ void oracle_dtw_forward(const float* costs, float* alpha, float* score,
 }
 
 /* dtw/kernels_cpu.cpp:127-223 */
-void oracle_dtw_backward(const float* alpha, const float* costs, const float* score,
-                         float* beta, float* posteriors, float* grad_T,
-                         const int* lengths, int B, int maxL1, int maxL2, float T, int64_t bw) {
+static void dtw_backward_impl(const float* alpha, const float* costs, const float* score,
+                              float* beta, float* posteriors, float* grad_T, double* sums64,
+                              const int* lengths, int B, int maxL1, int maxL2, float T,
+                              int64_t bw) {
     (void)score;
     const size_t astride = (size_t)(maxL1 + 1) * (maxL2 + 1);
     const size_t sstride = (size_t)maxL1 * maxL2;
@@ -887,6 +976,7 @@ void oracle_dtw_backward(const float* alpha, const float* costs, const float* sc
         for (size_t q = 0; q < astride; ++q) be[q] = 0.0f;
         be[AIDX(L1, L2)] = 1.0f;
         float gT = 0.0f;
+        double gT_d = 0.0;
         FOR_DIAG_REV(L1, L2, i, j) {
             if (!in_band(i, j, L1, L2, bw)) continue;
             float bij = be[AIDX(i, j)];
@@ -907,11 +997,33 @@ void oracle_dtw_backward(const float* alpha, const float* costs, const float* sc
             if (smv < PINF) {
                 float Ea = wd * ad + wu * au + wl * al;
                 gT += bij * (smv - Ea) / T;
+                gT_d += (double)(bij * (smv - Ea) / T);
             }
         }
         grad_T[b] = gT;
+        if (sums64) sums64[b] = gT_d;
     }
 }
+
+void oracle_dtw_backward(const float* alpha, const float* costs, const float* score,
+                         float* beta, float* posteriors, float* grad_T,
+                         const int* lengths, int B, int maxL1, int maxL2, float T, int64_t bw) {
+    dtw_backward_impl(alpha, costs, score, beta, posteriors, grad_T, NULL, lengths, B, maxL1,
+                      maxL2, T, bw);
+}
+
+/* The same reverse sweep with dS/dT also summed in double into sums64[b]. */
+void oracle_dtw_backward_sums64(const float* alpha, const float* costs, const float* score,
+                                float* beta, float* posteriors, double* sums64,
+                                const int* lengths, int B, int maxL1, int maxL2, float T,
+                                int64_t bw) {
+    float* gt = (float*)malloc(sizeof(float) * (B > 0 ? B : 1));
+    dtw_backward_impl(alpha, costs, score, beta, posteriors, gt, sums64, lengths, B, maxL1,
+                      maxL2, T, bw);
+    free(gt);
+}
+
+
 
 /* dtw/kernels_cpu.cpp:229-377 */
 void oracle_dtw_hvp(const float* alpha, const float* costs, const float* score,

@@ -71,6 +71,22 @@ void oracle_dtw_param_grad(const float* alpha, const float* costs, const float* 
                            const int* lengths, int B, int L1, int L2, float T,
                            int64_t bandwidth);
 
+/* Test-only extensions (no reference counterpart): the backward sweeps again, with
+ * the per-element parameter gradients also accumulated in double from the same
+ * fp32 per-cell terms.  sums64: SW [B][2] (gap, T), affine [B][3] (open, ext, T),
+ * DTW [B] (T). */
+void oracle_sw_backward_sums64(const float* alpha, const float* scores, const float* partition,
+                               float* beta, float* posteriors, double* sums64,
+                               const int* lengths, int B, int L1, int L2, float gap, float T);
+void oracle_swa_backward_sums64(const float* alpha, const float* scores, const float* partition,
+                                float* beta, float* posteriors, double* sums64,
+                                const int* lengths, int B, int L1, int L2, float gap_open,
+                                float gap_ext, float T);
+void oracle_dtw_backward_sums64(const float* alpha, const float* costs, const float* score,
+                                float* beta, float* posteriors, double* sums64,
+                                const int* lengths, int B, int L1, int L2, float T,
+                                int64_t bandwidth);
+
 int oracle_max_threads(void);
 
 #ifdef __cplusplus

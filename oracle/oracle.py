@@ -65,9 +65,25 @@ _SIGS = {
 }
 
 
+_D = ctypes.POINTER(ctypes.c_double)
+
+# test-only extensions of the oracle (no reference counterpart): backward sweeps
+# whose parameter gradients are also summed in double
+_SIGS64 = {
+    "sw_backward_sums64": ("oracle_sw_backward_sums64",
+                           [_F, _F, _F, _F, _F, _D, _I, _i, _i, _i, _f, _f]),
+    "swa_backward_sums64": ("oracle_swa_backward_sums64",
+                            [_F, _F, _F, _F, _F, _D, _I, _i, _i, _i, _f, _f, _f]),
+    "dtw_backward_sums64": ("oracle_dtw_backward_sums64",
+                            [_F, _F, _F, _F, _F, _D, _I, _i, _i, _i, _f, _l]),
+}
+
+
 def _p(a: np.ndarray):
     if a.dtype == np.int32:
         return a.ctypes.data_as(_I)
+    if a.dtype == np.float64:
+        return a.ctypes.data_as(_D)
     return a.ctypes.data_as(_F)
 
 
@@ -106,6 +122,43 @@ class CpuKernels:
             f.argtypes = argt
             f.restype = None
             self.fn[name] = f
+        if kind == "oracle":
+            for name, (osym, argt) in _SIGS64.items():
+                f = getattr(self.lib, osym)
+                f.argtypes = argt
+                f.restype = None
+                self.fn[name] = f
+
+    def param_grads64(self, family, inputs, lengths, *params, bandwidth=-1):
+        """Per-element parameter gradients with the reference's per-cell terms summed
+        in double (oracle only): SW [B,2] (gap, T), affine [B,3] (open, ext, T),
+        DTW [B] (T)."""
+        if self.kind != "oracle":
+            raise RuntimeError("double-accumulated sums exist in the oracle only")
+        x = _f32(inputs)
+        B, L1, L2 = x.shape
+        ln = _lengths(lengths, B, L1, L2)
+        post = np.zeros_like(x)
+        if family == "sw":
+            alpha, part = self.sw_forward(x, lengths, *params)
+            out = np.zeros((B, 2), np.float64)
+            self.fn["sw_backward_sums64"](_p(alpha), _p(x), _p(part), _p(np.zeros_like(alpha)),
+                                          _p(post), _p(out), _p(ln), B, L1, L2, *params)
+        elif family == "swa":
+            alpha, part = self.swa_forward(x, lengths, *params)
+            out = np.zeros((B, 3), np.float64)
+            self.fn["swa_backward_sums64"](_p(alpha), _p(x), _p(part),
+                                           _p(np.zeros_like(alpha)), _p(post), _p(out), _p(ln),
+                                           B, L1, L2, *params)
+        elif family == "dtw":
+            alpha, score = self.dtw_forward(x, lengths, params[0], bandwidth)
+            out = np.zeros((B,), np.float64)
+            self.fn["dtw_backward_sums64"](_p(alpha), _p(x), _p(score), _p(np.zeros_like(alpha)),
+                                           _p(post), _p(out), _p(ln), B, L1, L2, params[0],
+                                           bandwidth)
+        else:
+            raise ValueError(family)
+        return out
 
     # ---------------- linear-gap SW ----------------
     def sw_forward(self, scores, lengths, gap, T):

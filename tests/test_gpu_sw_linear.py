@@ -5,17 +5,18 @@ PyTorch API; the oracle (oracle/liboracle.so, bit-identical to the reference's
 own CPU kernels) supplies the expected values on the same seeded inputs.
 
 Tolerances: value within 1e-5 relative, marginals within
-1e-4 absolute.  grad_gap is a sum of 2*L1*L2 positive terms that the reference
-accumulates sequentially in fp32; at 512x512 that sum alone is off by up to
-7e-5 relative from a float64 finite difference (the HIP tree reduction is
-closer), so grad_gap is held to 3e-4 relative.  grad_T is a difference of two
-O(S) numbers divided by T: 1e-3 relative plus 2e-5 * S / T.
+1e-4 absolute.  grad_gap within 3e-4 relative and grad_T within 1e-3 relative
+plus 2e-5 * S / T (a difference of two O(S) numbers divided by T) -- of the
+reference, or, where the reference's sequential fp32 sum over millions of cells
+has drifted further than that, of the reference's per-cell terms summed in
+double (tests/_paramgrad.py).
 """
 import numpy as np
 import pytest
 import torch
 
 import _capi
+from _paramgrad import check_param_grad
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -29,14 +30,16 @@ def _seeded(seed, shape, scale=1.0):
     return torch.randn(shape, generator=g, dtype=torch.float32) * scale
 
 
-def _check(gpu, ref, lengths=None, gap=-1.0, T=1.0):
+def _check(gpu, ref, lengths=None, gap=-1.0, T=1.0, scores=None):
     part, marg, gg, gt = [x.detach().cpu().numpy() for x in gpu]
     rp, rm, rg, rt = ref
     np.testing.assert_allclose(part, rp, rtol=VALUE_RTOL, atol=1e-6)
     assert np.abs(marg - rm).max() <= MARG_ATOL, np.abs(marg - rm).max()
-    np.testing.assert_allclose(gg, rg, rtol=3e-4, atol=1e-4)
-    tol = 1e-3 * np.abs(rt) + 2e-5 * (np.abs(rp) + 1.0) / T
-    assert np.all(np.abs(gt - rt) <= tol), (gt, rt)
+    k = O.get("oracle")
+    exact = lambda: k.param_grads64("sw", scores, lengths, gap, T)
+    check_param_grad(gg, rg, lambda: exact()[:, 0])
+    check_param_grad(gt, rt, lambda: exact()[:, 1], rtol=1e-3,
+                     atol=2e-5 * (np.abs(rp).max() + 1.0) / T)
     if lengths is not None:
         for b, (l1, l2) in enumerate(lengths):
             assert np.all(marg[b, l1:, :] == 0.0) and np.all(marg[b, :, l2:] == 0.0)
@@ -57,6 +60,8 @@ CASES = [
     (9, 9, 300, 70, -2.0, 1.5),
     (10, 2, 600, 90, -1.0, 1.0),       # more stripes than waves in a workgroup
     (11, 1, 1100, 300, -1.0, 1.0),     # ... more than two rounds of waves
+    (12, 1, 600, 2500, -1.0, 1.0),     # long rows: rings too long for 16-step backward chunks
+    (13, 1, 4096, 4096, -1.0, 1.0),    # config C5 element (64 stripes, 8 rounds of waves)
 ]
 
 
@@ -66,7 +71,7 @@ def test_sw_capi_matches_oracle(cuda, seed, B, L1, L2, gap, T):
     ref = O.get("oracle").soft_sw(s.numpy(), gap, T)
     out = _capi.sw_forward_marginals(s.to(cuda), None, gap, T)
     torch.cuda.synchronize()
-    _check(out, ref, gap=gap, T=T)
+    _check(out, ref, gap=gap, T=T, scores=s.numpy())
 
 
 def test_sw_capi_ragged_lengths(cuda):
@@ -81,7 +86,7 @@ def test_sw_capi_ragged_lengths(cuda):
     ref = O.get("oracle").soft_sw(s.numpy(), -1.0, 0.5, lengths)
     out = _capi.sw_forward_marginals(s.to(cuda), torch.from_numpy(lengths).to(cuda), -1.0, 0.5)
     torch.cuda.synchronize()
-    _check(out, ref, lengths=lengths, gap=-1.0, T=0.5)
+    _check(out, ref, lengths=lengths, gap=-1.0, T=0.5, scores=s.numpy())
 
 
 def test_sw_capi_config_c2_full_size(cuda):
@@ -90,7 +95,7 @@ def test_sw_capi_config_c2_full_size(cuda):
     ref = O.get("oracle").soft_sw(s.numpy(), -1.0, 1.0)
     out = _capi.sw_forward_marginals(s.to(cuda), None, -1.0, 1.0)
     torch.cuda.synchronize()
-    _check(out, ref)
+    _check(out, ref, scores=s.numpy())
     marg = out[1]
     assert float(marg.min()) >= 0.0 and float(marg.max()) <= 1.0 + 1e-5
 
