@@ -101,6 +101,10 @@ __device__ __forceinline__ float wave_sum(float v) {
     return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 
+__device__ __forceinline__ double wave_sum(double v) {
+    return wave_reduce(v, [](double a, double b) { return a + b; });
+}
+
 // Combines per-lane OnlineLSE states across the wave; result valid in every lane.
 __device__ __forceinline__ void wave_merge_lse(OnlineLSE& s, float c) {
 #pragma unroll

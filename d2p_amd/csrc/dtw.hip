@@ -312,7 +312,7 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
 using namespace d2p_amd;
 
 extern "C" size_t d2p_dtw_workspace_bytes(int B, int max_L1, int max_L2) {
-    if (B <= 0 || max_L1 <= 0 || max_L2 <= 0) return 0;
+    if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
     const size_t ns = ((size_t)max_L1 + 63) / 64;
     // status words | trash line | skewed alpha table | last row of every stripe
     return wf::status_bytes(B) + wf::TRASH_BYTES +
@@ -329,7 +329,7 @@ extern "C" int d2p_dtw_forward_marginals(const float* costs, const int* lengths,
     if (B == 0) return D2P_OK;
     D2P_REQUIRE(costs && lengths && value && marginals && grad_T, "null pointer argument");
     const size_t need = d2p_dtw_workspace_bytes(B, max_L1, max_L2);
-    D2P_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), "workspace too small");
+    D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 8, "max_L2 too large");
     D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
     hipStream_t st = (hipStream_t)stream;

@@ -459,7 +459,7 @@ size_t swa_table_floats(int B, int max_L1, int max_L2) {
 }  // namespace
 
 extern "C" size_t d2p_swa_workspace_bytes(int B, int max_L1, int max_L2) {
-    if (B <= 0 || max_L1 <= 0 || max_L2 <= 0) return 0;
+    if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
     // status words | trash line | skewed (M, I, D) tables | last row of every stripe
     return wf::status_bytes(B) + wf::TRASH_BYTES +
            swa_table_floats(B, max_L1, max_L2) * 65 * sizeof(float);
@@ -476,7 +476,7 @@ extern "C" int d2p_swa_forward_marginals(const float* scores, const int* lengths
     D2P_REQUIRE(scores && lengths && partition && marginals && grad_open && grad_ext && grad_T,
                 "null pointer argument");
     const size_t need = d2p_swa_workspace_bytes(B, max_L1, max_L2);
-    D2P_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), "workspace too small");
+    D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     D2P_REQUIRE(max_L2 + 63 < (1 << 16) * swa::PB, "max_L2 too large");
     D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
     hipStream_t st = (hipStream_t)stream;

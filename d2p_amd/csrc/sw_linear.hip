@@ -17,11 +17,13 @@
 // previous step, in the reference's accumulation order
 //   beta = ((beta_init + from(i+1,j+1)) + from(i,j+1)) + from(i+1,j).
 
+#include <type_traits>
 #include <vector>
 
 #include "wavefront.hip.h"
 #include "../../include/d2p_amd.h"
 #include "capi_util.hip.h"
+#include "sw_internal.hip.h"
 
 namespace d2p_amd {
 namespace sw {
@@ -146,7 +148,9 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     }
 }
 
-template <int P>
+// PRECISE: accumulate dS/dgap and dS/dT per lane in double (second-order callers,
+// whose Jacobians amplify errors in these sums).
+template <int P, bool PRECISE = false>
 __global__ void __launch_bounds__(NW * 64)
 sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                    const float* __restrict__ alpha_sk, const float* __restrict__ brow,
@@ -156,7 +160,8 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                    int L1max, int L2max, int NSmax, float gap, float T, int R) {
         extern __shared__ float smem[];
     __shared__ int prog[NW];
-    __shared__ float red_g[NW], red_p[NW];
+    using Acc = typename std::conditional<PRECISE, double, float>::type;
+    __shared__ Acc red_g[NW], red_p[NW];
     const int b = blockIdx.x;
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
@@ -190,7 +195,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
 
     zero_padding(pbase, L1, L2, L1max, L2max, NW * 64);
 
-    float g_acc = 0.0f, p_acc = 0.0f;
+    Acc g_acc = 0, p_acc = 0;
     float A[P + 2];
 
     // Stripes run bottom-up: order q = 0..NS-1 handles stripe NS-1-q, on wave q % NW.
@@ -297,9 +302,9 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const float od = br * e0, ou = br * e1, ol = br * e2;
                 const float pv = br * (e0 + e3);
                 tile[tbase + u] = pv;
-                g_acc += ou;
-                g_acc += ol;
-                p_acc += pv * sc;
+                g_acc += (Acc)ou;
+                g_acc += (Acc)ol;
+                p_acc += (Acc)(pv * sc);
                 pub[u] = make_float2(ou, od);
                 // successor contributions for the next steps; lane 63 takes the ring
                 pre_u = wave_shr1(pre_u, 0.0f);
@@ -323,11 +328,112 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     if (lane == 0) { red_g[wave] = g_acc; red_p[wave] = p_acc; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        float g = 0.0f, p = 0.0f;
+        Acc g = 0, p = 0;
         for (int w = 0; w < NW; ++w) { g += red_g[w]; p += red_p[w]; }
-        grad_gap[b] = g;
-        grad_T[b] = (S - (p + g * gap)) / T;
+        grad_gap[b] = (float)g;
+        grad_T[b] = (float)(((Acc)S - (p + g * (Acc)gap)) / (Acc)T);
     }
+}
+
+}  // namespace sw
+}  // namespace d2p_amd
+
+namespace d2p_amd {
+namespace sw {
+
+size_t table_floats(int B, int max_L1, int max_L2) {
+    const size_t ns = ((size_t)max_L1 + 63) / 64;
+    return (size_t)B * ns * (size_t)wf::stored_steps(max_L2) * 65;
+}
+
+Layout layout(void* workspace, int B, int max_L1, int max_L2) {
+    Layout l;
+    l.status = (int*)workspace;
+    l.trash = (float*)((char*)workspace + wf::status_bytes(B));
+    l.alpha_sk = (float*)((char*)l.trash + wf::TRASH_BYTES);
+    const size_t ns = ((size_t)max_L1 + 63) / 64;
+    l.brow = l.alpha_sk + (size_t)B * ns * wf::stored_steps(max_L2) * 64;
+    l.bytes = wf::status_bytes(B) + wf::TRASH_BYTES + table_floats(B, max_L1, max_L2) * sizeof(float);
+    return l;
+}
+
+namespace {
+constexpr size_t kLdsLimit = 160 * 1024 - 256;
+
+size_t lds_forward(int max_L1, int max_L2) {
+    const int R = wf::ring_len(max_L1, max_L2, 256);
+    return (size_t)wf::NW * 2 * 65 * PF * sizeof(float) +
+           ((size_t)wf::NW * R + wf::NW * DUMMY) * sizeof(float);
+}
+
+size_t lds_backward(int max_L1, int max_L2, int P) {
+    const int R = wf::ring_len(max_L1, max_L2, 128);
+    return (size_t)wf::NW * 2 * (65 * P + 64 * P + 64) * sizeof(float) +
+           ((size_t)wf::NW * R + wf::NW * DUMMY) * sizeof(float2);
+}
+
+// backward: 16-step chunks when they fit in LDS, else 8-step chunks (long rows need
+// long rings)
+int backward_chunk(int max_L1, int max_L2) {
+    return lds_backward(max_L1, max_L2, 16) <= kLdsLimit ? 16 : 8;
+}
+}  // namespace
+
+int check_shape(int B, int max_L1, int max_L2, float temperature) {
+    D2P_REQUIRE(B >= 0 && max_L1 >= 0 && max_L2 >= 0, "negative dimension");
+    D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
+    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 4, "max_L2 too large");
+    // per-lane byte offsets within one batch element are 32-bit
+    D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
+    D2P_REQUIRE(lds_forward(max_L1, max_L2) <= kLdsLimit &&
+                    lds_backward(max_L1, max_L2, backward_chunk(max_L1, max_L2)) <= kLdsLimit,
+                "sequence too long for the LDS stripe rings");
+    return D2P_OK;
+}
+
+int launch_forward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
+                   float gap, float T, const Layout& ws, float* partition, hipStream_t st) {
+    const int ns = (max_L1 + 63) / 64;
+    const int R = wf::ring_len(max_L1, max_L2, 256);
+    const size_t lds = lds_forward(max_L1, max_L2);
+    D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    D2P_LAUNCH("sw_forward", sw_forward_kernel, dim3(B), dim3(wf::NW * 64), lds, st, scores,
+               lengths, ws.alpha_sk, ws.brow, partition, ws.status, max_L1, max_L2, ns, gap, T, R);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
+template <int P, bool PRECISE>
+int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
+                      float gap, float T, const Layout& ws, const float* partition,
+                      float* marginals, float* grad_gap, float* grad_T, hipStream_t st) {
+    const int ns = (max_L1 + 63) / 64;
+    const int R = wf::ring_len(max_L1, max_L2, 128);
+    const size_t lds = lds_backward(max_L1, max_L2, P);
+    D2P_HIP(hipFuncSetAttribute((const void*)sw_backward_kernel<P, PRECISE>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    D2P_LAUNCH("sw_backward", (sw_backward_kernel<P, PRECISE>), dim3(B), dim3(wf::NW * 64), lds,
+               st, scores, lengths, ws.alpha_sk, ws.brow, partition, marginals, grad_gap, grad_T,
+               ws.status, ws.trash, max_L1, max_L2, ns, gap, T, R);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
+int launch_backward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
+                    float gap, float T, const Layout& ws, const float* partition,
+                    float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
+                    bool precise) {
+    const int P = backward_chunk(max_L1, max_L2);
+    if (P == 16)
+        return precise ? launch_backward_p<16, true>(scores, lengths, B, max_L1, max_L2, gap, T, ws,
+                                                     partition, marginals, grad_gap, grad_T, st)
+                       : launch_backward_p<16, false>(scores, lengths, B, max_L1, max_L2, gap, T,
+                                                      ws, partition, marginals, grad_gap, grad_T, st);
+    return precise ? launch_backward_p<8, true>(scores, lengths, B, max_L1, max_L2, gap, T, ws,
+                                                partition, marginals, grad_gap, grad_T, st)
+                   : launch_backward_p<8, false>(scores, lengths, B, max_L1, max_L2, gap, T, ws,
+                                                 partition, marginals, grad_gap, grad_T, st);
 }
 
 }  // namespace sw
@@ -336,11 +442,9 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
 using namespace d2p_amd;
 
 extern "C" size_t d2p_sw_workspace_bytes(int B, int max_L1, int max_L2) {
-    if (B <= 0 || max_L1 <= 0 || max_L2 <= 0) return 0;
-    const size_t ns = ((size_t)max_L1 + 63) / 64;
+    if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
     // status words | trash line | skewed alpha table | last row of every stripe
-    return wf::status_bytes(B) + wf::TRASH_BYTES +
-           (size_t)B * ns * (size_t)wf::stored_steps(max_L2) * 65 * sizeof(float);
+    return sw::layout(nullptr, B, max_L1, max_L2).bytes;
 }
 
 extern "C" int d2p_sw_status(const void* workspace, int B, int* status, void* stream) {
@@ -360,54 +464,18 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
                                         float* partition, float* marginals, float* grad_gap,
                                         float* grad_T, void* workspace,
                                         size_t workspace_bytes, void* stream) {
-    D2P_REQUIRE(B >= 0 && max_L1 >= 0 && max_L2 >= 0, "negative dimension");
-    D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
+    const int rc = sw::check_shape(B, max_L1, max_L2, temperature);
+    if (rc != D2P_OK) return rc;
     if (B == 0) return D2P_OK;
     D2P_REQUIRE(scores && lengths && partition && marginals && grad_gap && grad_T,
                 "null pointer argument");
     const size_t need = d2p_sw_workspace_bytes(B, max_L1, max_L2);
-    D2P_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), "workspace too small");
-    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 8, "max_L2 too large");
-    // per-lane byte offsets within one batch element are 32-bit
-    D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
+    D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
-    const int ns = (max_L1 + 63) / 64;
-    const int Rf = wf::ring_len(max_L1, max_L2, 256);
-    const int Rb = wf::ring_len(max_L1, max_L2, 128);
-    const size_t lds_f = (size_t)wf::NW * 2 * 65 * sw::PF * sizeof(float) +
-                         ((size_t)wf::NW * Rf + wf::NW * sw::DUMMY) * sizeof(float);
-    // backward: 16-step chunks when they fit in LDS, else 8-step chunks (long rows
-    // need long rings)
-    auto lds_bwd = [&](int P) {
-        return (size_t)wf::NW * 2 * (65 * P + 64 * P + 64) * sizeof(float) +
-               ((size_t)wf::NW * Rb + wf::NW * sw::DUMMY) * sizeof(float2);
-    };
-    const size_t lds_limit = 160 * 1024 - 256;
-    const int Pb = lds_bwd(16) <= lds_limit ? 16 : 8;
-    const size_t lds_b = lds_bwd(Pb);
-    D2P_REQUIRE(lds_f <= lds_limit && lds_b <= lds_limit,
-                "sequence too long for the LDS stripe rings");
-    const void* bwd_kernel = Pb == 16 ? (const void*)sw::sw_backward_kernel<16>
-                                      : (const void*)sw::sw_backward_kernel<8>;
-    D2P_HIP(hipFuncSetAttribute((const void*)sw::sw_forward_kernel,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_f));
-    D2P_HIP(hipFuncSetAttribute(bwd_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
-    int* status = (int*)workspace;
-    float* trash = (float*)((char*)workspace + wf::status_bytes(B));
-    float* alpha_sk = (float*)((char*)trash + wf::TRASH_BYTES);
-    float* brow = alpha_sk + (size_t)B * ns * wf::stored_steps(max_L2) * 64;
-    D2P_LAUNCH("sw_forward", sw::sw_forward_kernel, dim3(B), dim3(wf::NW * 64), lds_f, st,
-               scores, lengths, alpha_sk, brow, partition, status, max_L1, max_L2, ns, gap,
-               temperature, Rf);
-    D2P_HIP(hipGetLastError());
-    if (Pb == 16)
-        D2P_LAUNCH("sw_backward", sw::sw_backward_kernel<16>, dim3(B), dim3(wf::NW * 64), lds_b, st,
-               scores, lengths, alpha_sk, brow, partition, marginals, grad_gap, grad_T, status,
-               trash, max_L1, max_L2, ns, gap, temperature, Rb);
-    else
-        D2P_LAUNCH("sw_backward", sw::sw_backward_kernel<8>, dim3(B), dim3(wf::NW * 64), lds_b, st,
-               scores, lengths, alpha_sk, brow, partition, marginals, grad_gap, grad_T, status,
-               trash, max_L1, max_L2, ns, gap, temperature, Rb);
-    D2P_HIP(hipGetLastError());
-    return D2P_OK;
+    const sw::Layout ws = sw::layout(workspace, B, max_L1, max_L2);
+    int r = sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
+                               partition, st);
+    if (r != D2P_OK) return r;
+    return sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
+                               partition, marginals, grad_gap, grad_T, st);
 }

@@ -1,0 +1,662 @@
+// sw_second.hip -- second-order quantities of linear-gap soft Smith-Waterman on
+// gfx950: Hessian-vector products and Jacobians of the marginals with respect to
+// gap and temperature.
+//
+// Reference behaviour restated (not translated):
+//   HVP          /root/reference/src/sw/kernels_cpu.cpp:279-477
+//   param grad   /root/reference/src/sw/kernels_cpu.cpp:491-710 (0 = gap, 1 = T)
+// Both are a forward tangent sweep followed by a two-channel reverse sweep.  With
+// w the softmax weights of a cell over its candidates v = (diag + s, up + gap,
+// left + gap, s) and d the candidates' tangents:
+//   tangent      x[i,j] = sum_k w_k d_k (+ (alpha - E_w[v]) / T for the temperature)
+//                d = (x_diag + V, x_up, x_left, V)             HVP (V = direction)
+//                d = (x_diag, x_up + 1, x_left + 1, 0)         d/dgap
+//                d = (x_diag, x_up, x_left, 0)                 d/dT
+//   reverse      beta as in the marginal backward; a second channel g with
+//                g_pred += g w_k + beta dw_k,  dw_k = w_k (d_k - E_w[d]) / T
+//                (+ w_k (E_w[v] - v_k) / T^2 for the temperature), started from
+//                beta_init (x - dS) / T  (HVP: first; param: last, with
+//                - beta_init (alpha - S) / T^2 for the temperature), and the output
+//                of a cell is g (w_diag + w_sky) + beta (dw_diag + dw_sky).
+// For the HVP dS = sum_cells beta_init x (computed by the tangent sweep); for a
+// parameter it is dS/dtheta from the marginal backward.
+//
+// Mapping: the stripe pipeline of wavefront.hip.h.  The tangent sweep runs like the
+// forward (its tangent crosses stripes through a float ring) and reads the primal
+// alpha table like the backward; the reverse sweep is the backward with a second
+// flow channel (float4 ring: beta and g towards the up and diagonal neighbours).
+// Inputs arrive by direct-to-LDS loads one chunk ahead into one buffer per wave,
+// copied to registers at the start of each chunk before the next chunk's loads.
+
+#include <vector>
+
+#include "wavefront.hip.h"
+#include "../../include/d2p_amd.h"
+#include "capi_util.hip.h"
+#include "sw_internal.hip.h"
+
+namespace d2p_amd {
+namespace sw2 {
+
+using namespace wf;
+
+enum Mode { HVP = 0, GAP = 1, TEMP = 2 };
+
+// ------------------------------------------------------------------ tangent sweep
+
+template <int MODE, int P>
+__global__ void __launch_bounds__(NW * 64)
+sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
+                  const int* __restrict__ lengths, const float* __restrict__ alpha_sk,
+                  const float* __restrict__ brow, const float* __restrict__ partition,
+                  float* __restrict__ tan_sk, float* __restrict__ tan_brow,
+                  float* __restrict__ sdot, int* __restrict__ status, int L1max, int L2max,
+                  int NSmax, float gap, float T, int R) {
+    constexpr bool HAS_V = MODE == HVP;
+    using Tile = ChunkTile<P>;
+    constexpr int VT = Tile::FLOATS;                         // direction tile
+    constexpr int AR = VT + (HAS_V ? Tile::FLOATS : 0);      // P alpha rows
+    constexpr int RR = AR + P * 64;                          // row above
+    constexpr int BUF = RR + 64;
+    constexpr int SINK = 64 + P;
+    extern __shared__ float smem[];
+    __shared__ int prog[NW];
+    __shared__ float red[NW];
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const unsigned ul4 = (unsigned)lane * 4u;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float* buf = smem + wave * BUF;
+    float* rings = smem + NW * BUF;                          // [NW][R] tangent of lane 63
+    float* sink = rings + NW * R + wave * SINK;
+    int* st = status + b;
+    const int tbase = Tile::read_base(lane);
+
+    if (lane == 0) prog[wave] = -1;
+    __syncthreads();
+
+    const int L1 = min(max(lengths[2 * b], 0), L1max);
+    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const float c = kLog2e / T;
+    const float rT = 1.0f / T;
+    const float S = partition[b];
+    const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
+    const int nsteps = L2 + 63;
+    const int nch = (nsteps + P - 1) / P;
+    const size_t NT = (size_t)stored_steps(L2max);
+    const float* sbase = scores + (size_t)b * L1max * L2max;
+    const float* vbase = HAS_V ? V + (size_t)b * L1max * L2max : nullptr;
+    const uint32_t in_lds = lds_address(buf);
+    float sacc = 0.0f;   // sum of beta_init * tangent (HVP)
+
+    for (int s = wave; s < NS; s += NW) {
+        const int i0 = s * 64;
+        const int L2eff = (i0 + lane < L1) ? L2 : 0;
+        const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * NT * 64;   // step -APAD
+        const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
+        float* tout = tan_sk + (((size_t)b * NSmax + s) * NT + APAD) * 64;
+        float* tb_s = tan_brow + ((size_t)b * NSmax + s) * NT;
+        const float* ring_in = ring_from(rings, s, R);
+        float* ring_out = ring_of(rings, s, R);
+
+        // Loads of chunk k (steps t0 .. t0+P-1): the score (and direction) tiles, the
+        // P alpha rows, and for lane j <= P the last row of the stripe above at step
+        // t0 + 62 + j (clamped; lanes past P repeat lane P).
+        auto issue_chunk = [&](int k) {
+            const int t0 = k * P;
+            dma_tile<P, 1>(in_lds, sbase, i0, L1max, L2max, lane, t0);
+            if (HAS_V) dma_tile<P, 1>(in_lds + VT * 4, vbase, i0, L1max, L2max, lane, t0);
+            dma_rows<P, 1>(in_lds + AR * 4, astripe, t0, ul4);
+            uint32_t roff = (uint32_t)min(t0 + 62 + min(lane, P), nsteps - 1) * 4u;
+            uint32_t rl = in_lds + RR * 4;
+            lds_dma_dword<0>(bup, roff, rl, 0u);
+        };
+
+        // tangents of the column-0 boundary are 0
+#pragma unroll
+        for (int t = -APAD; t < 0; ++t) lane_store(tout + t * 64, ul4, 0.0f);
+        wave_lds_sync();
+        issue_chunk(0);
+        float Aw[P + 2];
+        Aw[P] = kNINF;        // alpha at steps -2, -1: column-0 boundary
+        Aw[P + 1] = kNINF;
+        float cur = 0.0f, up_prev = 0.0f;   // tangents: previous step, its up value
+
+        for (int k = 0; k < nch; ++k) {
+            const int t0 = k * P;
+            chunk_waits<P>(prog, s, NS, k, nch, R, st);
+            // this chunk's loads, followed by exactly the P + 1 stores of the previous
+            // chunk (the first chunk's loads are the last issued)
+            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            float sv[P], vv[P];
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                sv[u] = buf[tbase + u];
+                vv[u] = HAS_V ? buf[VT + tbase + u] : 0.0f;
+            }
+            Aw[0] = Aw[P];
+            Aw[1] = Aw[P + 1];
+#pragma unroll
+            for (int j = 0; j < P; ++j) Aw[j + 2] = buf[AR + j * 64 + lane];
+            // lane j: alpha of the last row above at step t0 + 62 + j (row 0: NINF)
+            float bv = buf[RR + lane];
+            bv = (s > 0 && lane <= P && t0 + 62 + lane <= nsteps - 1) ? bv : kNINF;
+            // lane 0's up tangents: column t0+j sits in lane j (row 0: 0)
+            float rreg = 0.0f;
+            if (s > 0 && lane < P) rreg = ring_in[ring_index(t0 + lane + 63, R)];
+            wave_lds_sync();   // every read of the input buffer is complete
+            if (k + 1 < nch) issue_chunk(k + 1);
+            float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
+            float* toutc = tout + (size_t)t0 * 64;
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                const int t = t0 + u;
+                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
+                const float sc = ok ? sv[u] : kNINF;
+                const float vd = ok ? vv[u] : 0.0f;
+                // primal predecessors: left = own previous step, up / diagonal = lane
+                // r-1 one / two steps back (lane 0: the last row above)
+                const float a0 = Aw[u + 2], a1 = Aw[u + 1];
+                const float dga = wave_shr1_or(Aw[u], bv);
+                const float bvn = wave_shl1(bv, kNINF);
+                const float upa = wave_shr1_or(a1, bvn);
+                bv = bvn;
+                // tangent predecessors
+                const float tu = wave_shr1_or(cur, rreg);
+                rreg = wave_shl1(rreg, 0.0f);
+                const float td = up_prev;
+                up_prev = tu;
+                const float tl = cur;
+                const float v0 = dga + sc, v1 = upa + gap, v2 = a1 + gap;
+                const float m = fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
+                const float e0 = fast_exp2((v0 - m) * c), e1 = fast_exp2((v1 - m) * c);
+                const float e2 = fast_exp2((v2 - m) * c), e3 = fast_exp2((sc - m) * c);
+                const float rin = fast_rcp(((e0 + e1) + e2) + e3);
+                float x;
+                if (MODE == HVP) {
+                    x = (((e0 * (td + vd) + e1 * tu) + e2 * tl) + e3 * vd) * rin;
+                } else if (MODE == GAP) {
+                    x = ((e0 * td + e1 * (tu + 1.0f)) + e2 * (tl + 1.0f)) * rin;
+                } else {
+                    const float ev = (((e0 * v0 + e1 * v1) + e2 * v2) + e3 * sc) * rin;
+                    x = ((e0 * td + e1 * tu) + e2 * tl) * rin + (a0 - ev) * rT;
+                }
+                cur = ok ? x : 0.0f;
+                lane_store(toutc + u * 64, ul4, cur);
+                pub[u] = cur;
+                if (MODE == HVP) {
+                    float lp = (a0 - S) * c;
+                    lp = lp < 0.0f ? lp : 0.0f;
+                    sacc += fast_exp2(lp) * cur;
+                }
+            }
+            // the stripe's last row of tangents by step: one store instruction
+            wave_lds_sync();
+            if (lane < P) lane_store(tb_s, (unsigned)(t0 + lane) * 4u, ring_out[t0 % R + lane]);
+            publish(prog, wave, s * PROG_STRIDE + k + 1);
+        }
+    }
+
+    if (MODE == HVP) {
+        sacc = wave_sum(sacc);
+        if (lane == 0) red[wave] = sacc;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float t = 0.0f;
+            for (int w = 0; w < NW; ++w) t += red[w];
+            sdot[b] = t;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ reverse sweep
+
+// DOT: instead of writing the per-cell output, accumulate its dot product with the
+// matrix passed as V (the marginal cotangent) into dot[b].
+template <int MODE, int P, bool DOT>
+__global__ void __launch_bounds__(NW * 64)
+sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
+               const int* __restrict__ lengths, const float* __restrict__ alpha_sk,
+               const float* __restrict__ brow, const float* __restrict__ tan_sk,
+               const float* __restrict__ tan_brow, const float* __restrict__ partition,
+               const float* __restrict__ dS, float* __restrict__ out, float* __restrict__ dot,
+               int* __restrict__ status, float* __restrict__ trash, int L1max, int L2max,
+               int NSmax, float gap, float T, int R) {
+    constexpr bool HAS_V = MODE == HVP || DOT;
+    using Tile = ChunkTile<P>;
+    constexpr int VT = Tile::FLOATS;
+    constexpr int AR = VT + (HAS_V ? Tile::FLOATS : 0);     // P alpha rows
+    constexpr int XR = AR + P * 64;                         // P tangent rows
+    constexpr int RA = XR + P * 64;                         // alpha row above
+    constexpr int RX = RA + 64;                             // tangent row above
+    constexpr int OT = RX + 64;                             // output tile
+    constexpr int BUF = OT + (DOT ? 0 : Tile::FLOATS);
+    constexpr int SINK = 64 + P;
+    extern __shared__ float smem[];
+    __shared__ int prog[NW];
+    __shared__ float red[NW];
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const unsigned ul4 = (unsigned)lane * 4u;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float* buf = smem + wave * BUF;
+    float* otile = buf + OT;
+    float4* rings = reinterpret_cast<float4*>(smem + NW * BUF);   // [NW][R]
+    float4* sink = rings + NW * R + wave * SINK;
+    int* st = status + b;
+    const int tbase = Tile::read_base(lane);
+
+    if (lane == 0) prog[wave] = -1;
+    __syncthreads();
+
+    const int L1 = min(max(lengths[2 * b], 0), L1max);
+    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const float c = kLog2e / T;
+    const float rT = 1.0f / T;
+    const float S = partition[b];
+    const float dSb = dS[b];
+    const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
+    const int nsteps = L2 + 63;
+    const int nch = (nsteps + P - 1) / P;
+    const size_t NT = (size_t)stored_steps(L2max);
+    const float* sbase = scores + (size_t)b * L1max * L2max;
+    const float* vbase = HAS_V ? V + (size_t)b * L1max * L2max : nullptr;
+    float* obase = DOT ? nullptr : out + (size_t)b * L1max * L2max;
+    const uint32_t in_lds = lds_address(buf);
+
+    if (!DOT) zero_padding(obase, L1, L2, L1max, L2max, NW * 64);
+
+    float dacc = 0.0f;
+    float A[P + 2], X[P + 2];
+
+    for (int q = wave; q < NS; q += NW) {
+        const int s = NS - 1 - q;
+        const int i0 = s * 64;
+        const int L2eff = (i0 + lane < L1) ? L2 : 0;
+        const size_t sb = ((size_t)b * NSmax + s) * NT;
+        const size_t ub = ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
+        const float* astripe = alpha_sk + sb * 64;
+        const float* xstripe = tan_sk + sb * 64;
+        const float* bup = brow + ub;
+        const float* xup = tan_brow + ub;
+        const float4* ring_in = ring_from(rings, q, R);
+        float4* ring_out = ring_of(rings, q, R);
+        const bool below = q > 0;
+
+        auto issue_chunk = [&](int k) {
+            const int th = nsteps - 1 - k * P;
+            dma_tile<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
+            if (HAS_V) dma_tile<P, -1>(in_lds + VT * 4, vbase, i0, L1max, L2max, lane, th);
+            dma_rows<P, -1>(in_lds + AR * 4, astripe, th - 2, ul4);
+            dma_rows<P, -1>(in_lds + XR * 4, xstripe, th - 2, ul4);
+            const uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
+            uint32_t o = roff, l = in_lds + RA * 4;
+            lds_dma_dword<0>(bup, o, l, 0u);
+            o = roff;
+            l = in_lds + RX * 4;
+            lds_dma_dword<0>(xup, o, l, 0u);
+        };
+
+        {
+            const float* a0p = astripe + (size_t)(nsteps - 1 + APAD) * 64;
+            const float* x0p = xstripe + (size_t)(nsteps - 1 + APAD) * 64;
+            A[P] = lane_load(a0p, ul4);
+            A[P + 1] = lane_load(a0p - 64, ul4);
+            X[P] = lane_load(x0p, ul4);
+            X[P + 1] = lane_load(x0p - 64, ul4);
+            __asm__ volatile("" ::"v"(A[P]), "v"(A[P + 1]), "v"(X[P]), "v"(X[P + 1]));
+        }
+        wave_lds_sync();
+        issue_chunk(0);
+        // successor flows: (beta, g) from the left successor, up successor, diagonal
+        float lb = 0.0f, lg = 0.0f, ubt = 0.0f, ug = 0.0f;
+        float db = 0.0f, dg = 0.0f, db2 = 0.0f, dg2 = 0.0f;
+
+        for (int k = 0; k < nch; ++k) {
+            const int t_hi = nsteps - 1 - k * P;
+            chunk_waits<P>(prog, q, NS, k, nch, R, st);
+            // this chunk's loads, followed by the P output stores of the previous
+            // chunk (none when accumulating a dot product; the first chunk's loads
+            // are the last issued)
+            if (k == 0 || DOT) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            float sv[P], vv[P];
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                sv[u] = buf[tbase + u];
+                vv[u] = HAS_V ? buf[VT + tbase + u] : 0.0f;
+            }
+            A[0] = A[P];
+            A[1] = A[P + 1];
+            X[0] = X[P];
+            X[1] = X[P + 1];
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                A[j + 2] = buf[AR + j * 64 + lane];
+                X[j + 2] = buf[XR + j * 64 + lane];
+            }
+            const bool row_ok = s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1;
+            float bA = row_ok ? buf[RA + lane] : kNINF;
+            float bX = row_ok ? buf[RX + lane] : 0.0f;
+            // flows from the stripe below for lane 63 (see the marginal backward):
+            // lane 63-j holds step j; up flows from slot kP+j+63, diagonal kP+j+62
+            float qub = 0.0f, qug = 0.0f, qdb = 0.0f, qdg = 0.0f;
+            if (below && lane >= 64 - P) {
+                const int j = 63 - lane;
+                const float4 ru = ring_in[ring_index(k * P + j + 63, R)];
+                const float4 rd = ring_in[ring_index(k * P + j + 62, R)];
+                qub = ru.x;
+                qug = ru.y;
+                qdb = rd.z;
+                qdg = rd.w;
+            }
+            wave_lds_sync();   // every read of the input buffer is complete
+            if (k + 1 < nch) issue_chunk(k + 1);
+            float4* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
+            {
+                const float u0b = lane_bcast(qub, 63), u0g = lane_bcast(qug, 63);
+                const float d0b = lane_bcast(qdb, 63), d0g = lane_bcast(qdg, 63);
+                const float d1b = lane_bcast(qdb, 62), d1g = lane_bcast(qdg, 62);
+                if (lane == 63) {
+                    ubt = u0b; ug = u0g;
+                    db = d0b; dg = d0g;
+                    db2 = d1b; dg2 = d1g;
+                }
+            }
+            qdb = wave_shr1(wave_shr1(qdb, 0.0f), 0.0f);
+            qdg = wave_shr1(wave_shr1(qdg, 0.0f), 0.0f);
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                const int t = t_hi - u;
+                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
+                const float sc = ok ? sv[u] : kNINF;
+                const float vd = ok ? vv[u] : 0.0f;
+                // primal and tangent predecessors
+                const float a0 = A[u], a1 = A[u + 1], x0 = X[u], x1 = X[u + 1];
+                const float nA = wave_shl1(bA, kNINF), nX = wave_shl1(bX, 0.0f);
+                const float upa = wave_shr1_or(a1, bA), upx = wave_shr1_or(x1, bX);
+                const float dga = wave_shr1_or(A[u + 2], nA), dgx = wave_shr1_or(X[u + 2], nX);
+                bA = nA;
+                bX = nX;
+                const float v0 = dga + sc, v1 = upa + gap, v2 = a1 + gap;
+                const float m = fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
+                const float e0 = fast_exp2((v0 - m) * c), e1 = fast_exp2((v1 - m) * c);
+                const float e2 = fast_exp2((v2 - m) * c), e3 = fast_exp2((sc - m) * c);
+                const float rin = fast_rcp(((e0 + e1) + e2) + e3);
+                const float w0 = e0 * rin, w1 = e1 * rin, w2 = e2 * rin, w3 = e3 * rin;
+                // candidate tangents and the weight tangents
+                float d0, d1, d2, d3;
+                if (MODE == HVP) {
+                    d0 = dgx + vd; d1 = upx; d2 = x1; d3 = vd;
+                } else if (MODE == GAP) {
+                    d0 = dgx; d1 = upx + 1.0f; d2 = x1 + 1.0f; d3 = 0.0f;
+                } else {
+                    d0 = dgx; d1 = upx; d2 = x1; d3 = 0.0f;
+                }
+                const float mean = ((w0 * d0 + w1 * d1) + w2 * d2) + w3 * d3;
+                float dw0 = w0 * (d0 - mean) * rT, dw1 = w1 * (d1 - mean) * rT;
+                float dw2 = w2 * (d2 - mean) * rT, dw3 = w3 * (d3 - mean) * rT;
+                if (MODE == TEMP) {
+                    const float ev = ((w0 * v0 + w1 * v1) + w2 * v2) + w3 * sc;
+                    const float rT2 = rT * rT;
+                    dw0 += w0 * (ev - v0) * rT2;
+                    dw1 += w1 * (ev - v1) * rT2;
+                    dw2 += w2 * (ev - v2) * rT2;
+                    dw3 += w3 * (ev - sc) * rT2;
+                }
+                // channels in the reference's accumulation order
+                float lp = (a0 - S) * c;
+                lp = lp < 0.0f ? lp : 0.0f;
+                const float binit = fast_exp2(lp);
+                const float beta = ((binit + db) + lb) + ubt;
+                float g;
+                bool live;
+                if (MODE == HVP) {
+                    g = ((binit * (x0 - dSb) * rT + dg) + lg) + ug;
+                    live = ok && beta <= 3.0e38f && beta != 0.0f;
+                } else {
+                    float init = binit * (x0 - dSb) * rT;
+                    if (MODE == TEMP) init -= binit * (a0 - S) * rT * rT;
+                    g = ((dg + lg) + ug) + init;
+                    live = ok && !(beta <= 1e-20f && fabsf(g) <= 1e-20f);
+                }
+                const float bl = live ? beta : 0.0f;
+                const float gl = live ? g : 0.0f;
+                const float o = gl * (w0 + w3) + bl * (dw0 + dw3);
+                if (DOT) dacc += o * vd;
+                else otile[tbase + u] = o;
+                const float ob0 = bl * w0, ob1 = bl * w1, ob2 = bl * w2;
+                const float og0 = gl * w0 + bl * dw0, og1 = gl * w1 + bl * dw1;
+                const float og2 = gl * w2 + bl * dw2;
+                pub[u] = make_float4(ob1, og1, ob0, og0);
+                // successor flows for the next steps; lane 63 takes the ring
+                qub = wave_shr1(qub, 0.0f);
+                qug = wave_shr1(qug, 0.0f);
+                lb = ob2;
+                lg = og2;
+                ubt = wave_shl1_or(ob1, qub);
+                ug = wave_shl1_or(og1, qug);
+                db = db2;
+                dg = dg2;
+                db2 = wave_shl1_or(ob0, qdb);
+                dg2 = wave_shl1_or(og0, qdg);
+                qdb = wave_shr1(qdb, 0.0f);
+                qdg = wave_shr1(qdg, 0.0f);
+            }
+            wave_lds_sync();
+            if (!DOT) write_tile<P, -1>(otile, obase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
+            publish(prog, wave, q * PROG_STRIDE + k + 1);
+        }
+    }
+
+    if (DOT) {
+        dacc = wave_sum(dacc);
+        if (lane == 0) red[wave] = dacc;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float t = 0.0f;
+            for (int w = 0; w < NW; ++w) t += red[w];
+            dot[b] = t;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ host side
+
+constexpr size_t kLdsLimit = 160 * 1024 - 256;
+constexpr int PT = 16;   // tangent sweep chunk
+
+size_t lds_tangent(int mode, int max_L1, int max_L2) {
+    const int R = ring_len(max_L1, max_L2, 256);
+    const int buf = 65 * PT * (mode == HVP ? 2 : 1) + PT * 64 + 64;
+    return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + PT)) * sizeof(float);
+}
+
+size_t lds_dual(bool has_v, bool dot, int P, int max_L1, int max_L2) {
+    const int R = ring_len(max_L1, max_L2, 128);
+    const int buf = 65 * P * (has_v ? 2 : 1) + 2 * P * 64 + 128 + (dot ? 0 : 65 * P);
+    return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + P)) * sizeof(float4);
+}
+
+// Largest reverse-sweep chunk (8 or 4 steps) whose buffers and rings fit in LDS.
+int dual_chunk(bool has_v, bool dot, int max_L1, int max_L2) {
+    if (lds_dual(has_v, dot, 8, max_L1, max_L2) <= kLdsLimit) return 8;
+    if (lds_dual(has_v, dot, 4, max_L1, max_L2) <= kLdsLimit) return 4;
+    return 0;
+}
+
+// Workspace after the primal layout: tangent table + last rows, then [B] each of
+// the tangent sweep's dS, the partition, dS/dgap and dS/dT.
+struct Second {
+    sw::Layout prim;
+    float* tan_sk;
+    float* tan_brow;
+    float* sdot;
+    float* part;
+    float* dgap;
+    float* dT;
+    size_t bytes;
+};
+
+Second second_layout(void* ws, int B, int L1, int L2) {
+    Second w;
+    w.prim = sw::layout(ws, B, L1, L2);
+    char* p = (char*)ws + round256(w.prim.bytes);
+    const size_t ns = ((size_t)L1 + 63) / 64;
+    w.tan_sk = (float*)p;
+    w.tan_brow = w.tan_sk + (size_t)B * ns * stored_steps(L2) * 64;
+    p += round256(sw::table_floats(B, L1, L2) * sizeof(float));
+    w.sdot = (float*)p;
+    w.part = w.sdot + B;
+    w.dgap = w.part + B;
+    w.dT = w.dgap + B;
+    p += round256((size_t)4 * B * sizeof(float));
+    w.bytes = (size_t)(p - (char*)ws);
+    return w;
+}
+
+template <int MODE>
+int launch_tangent(const float* scores, const float* V, const int* lengths, int B, int L1, int L2,
+                   float gap, float T, const Second& w, float* sdot, hipStream_t st) {
+    const int ns = (L1 + 63) / 64;
+    const int R = ring_len(L1, L2, 256);
+    const size_t lds = lds_tangent(MODE, L1, L2);
+    D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
+    auto kern = sw_tangent_kernel<MODE, PT>;
+    D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+    D2P_LAUNCH("sw_tangent", kern, dim3(B), dim3(NW * 64), lds, st, scores, V, lengths,
+               w.prim.alpha_sk, w.prim.brow, w.part, w.tan_sk, w.tan_brow, sdot, w.prim.status,
+               L1, L2, ns, gap, T, R);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
+template <int MODE, bool DOT>
+int launch_dual(const float* scores, const float* V, const int* lengths, int B, int L1, int L2,
+                float gap, float T, const Second& w, const float* dS, float* out, float* dot,
+                hipStream_t st) {
+    const int ns = (L1 + 63) / 64;
+    const int R = ring_len(L1, L2, 128);
+    constexpr bool has_v = MODE == HVP || DOT;
+    const int P = dual_chunk(has_v, DOT, L1, L2);
+    D2P_REQUIRE(P > 0, "sequence too long for the LDS stripe rings");
+    const size_t lds = lds_dual(has_v, DOT, P, L1, L2);
+    auto k8 = sw_dual_kernel<MODE, 8, DOT>;
+    auto k4 = sw_dual_kernel<MODE, 4, DOT>;
+    auto kern = P == 8 ? k8 : k4;
+    D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+    D2P_LAUNCH("sw_dual", kern, dim3(B), dim3(NW * 64), lds, st, scores, V, lengths,
+               w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, w.part, dS, out, dot,
+               w.prim.status, w.prim.trash, L1, L2, ns, gap, T, R);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
+int check(int B, int L1, int L2, float T) {
+    const int rc = sw::check_shape(B, L1, L2, T);
+    if (rc != D2P_OK) return rc;
+    D2P_REQUIRE(lds_tangent(HVP, L1, L2) <= kLdsLimit && dual_chunk(true, false, L1, L2) > 0,
+                "sequence too long for the LDS stripe rings");
+    return D2P_OK;
+}
+
+}  // namespace sw2
+}  // namespace d2p_amd
+
+using namespace d2p_amd;
+
+#define D2P_TRY(...)                    \
+    do {                                \
+        const int rc_ = (__VA_ARGS__);  \
+        if (rc_ != D2P_OK) return rc_;  \
+    } while (0)
+
+extern "C" size_t d2p_sw_second_workspace_bytes(int B, int max_L1, int max_L2) {
+    if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
+    return sw2::second_layout(nullptr, B, max_L1, max_L2).bytes;
+}
+
+extern "C" int d2p_sw_hvp(const float* scores, const float* tangent, const int* lengths, int B,
+                          int max_L1, int max_L2, float gap, float temperature, float* hvp,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+    D2P_TRY(sw2::check(B, max_L1, max_L2, temperature));
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(scores && tangent && lengths && hvp, "null pointer argument");
+    const size_t need = d2p_sw_second_workspace_bytes(B, max_L1, max_L2);
+    D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    const sw2::Second w = sw2::second_layout(workspace, B, max_L1, max_L2);
+    D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, w.prim,
+                               w.part, st));
+    D2P_TRY(sw2::launch_tangent<sw2::HVP>(scores, tangent, lengths, B, max_L1, max_L2, gap,
+                                          temperature, w, w.sdot, st));
+    return sw2::launch_dual<sw2::HVP, false>(scores, tangent, lengths, B, max_L1, max_L2, gap,
+                                             temperature, w, w.sdot, hvp, nullptr, st);
+}
+
+extern "C" int d2p_sw_param_jacobian(const float* scores, int param_type, const int* lengths,
+                                     int B, int max_L1, int max_L2, float gap, float temperature,
+                                     float* jacobian, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+    D2P_TRY(sw2::check(B, max_L1, max_L2, temperature));
+    D2P_REQUIRE(param_type == 0 || param_type == 1, "param_type must be 0 or 1");
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(scores && lengths && jacobian, "null pointer argument");
+    const size_t need = d2p_sw_second_workspace_bytes(B, max_L1, max_L2);
+    D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    const sw2::Second w = sw2::second_layout(workspace, B, max_L1, max_L2);
+    D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, w.prim,
+                               w.part, st));
+    // dS/dtheta from the marginal backward; its marginals go to the output, which the
+    // reverse sweep below overwrites completely
+    D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, w.prim,
+                                w.part, jacobian, w.dgap, w.dT, st, true));
+    if (param_type == 0) {
+        D2P_TRY(sw2::launch_tangent<sw2::GAP>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
+                                              temperature, w, nullptr, st));
+        return sw2::launch_dual<sw2::GAP, false>(scores, nullptr, lengths, B, max_L1, max_L2,
+                                                 gap, temperature, w, w.dgap, jacobian, nullptr,
+                                                 st);
+    }
+    D2P_TRY(sw2::launch_tangent<sw2::TEMP>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
+                                           temperature, w, nullptr, st));
+    return sw2::launch_dual<sw2::TEMP, false>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
+                                              temperature, w, w.dT, jacobian, nullptr, st);
+}
+
+extern "C" int d2p_sw_backward_full(const float* scores, const float* grad_alignment,
+                                    const int* lengths, int B, int max_L1, int max_L2, float gap,
+                                    float temperature, float* grad_scores, float* grad_gap,
+                                    float* grad_T, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+    D2P_TRY(sw2::check(B, max_L1, max_L2, temperature));
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(scores && grad_alignment && lengths && grad_scores && grad_gap && grad_T,
+                "null pointer argument");
+    const size_t need = d2p_sw_second_workspace_bytes(B, max_L1, max_L2);
+    D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    const sw2::Second w = sw2::second_layout(workspace, B, max_L1, max_L2);
+    const float* ga = grad_alignment;
+    D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, w.prim,
+                               w.part, st));
+    // dS/dgap and dS/dT; the marginals land in grad_scores, overwritten by the HVP
+    D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, w.prim,
+                                w.part, grad_scores, w.dgap, w.dT, st, true));
+    // grad_scores = H grad_alignment
+    D2P_TRY(sw2::launch_tangent<sw2::HVP>(scores, ga, lengths, B, max_L1, max_L2, gap,
+                                          temperature, w, w.sdot, st));
+    D2P_TRY(sw2::launch_dual<sw2::HVP, false>(scores, ga, lengths, B, max_L1, max_L2, gap,
+                                              temperature, w, w.sdot, grad_scores, nullptr, st));
+    // grad_gap[b] = <grad_alignment, dP/dgap>, grad_T[b] = <grad_alignment, dP/dT>
+    D2P_TRY(sw2::launch_tangent<sw2::GAP>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
+                                          temperature, w, nullptr, st));
+    D2P_TRY(sw2::launch_dual<sw2::GAP, true>(scores, ga, lengths, B, max_L1, max_L2, gap,
+                                             temperature, w, w.dgap, nullptr, grad_gap, st));
+    D2P_TRY(sw2::launch_tangent<sw2::TEMP>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
+                                           temperature, w, nullptr, st));
+    return sw2::launch_dual<sw2::TEMP, true>(scores, ga, lengths, B, max_L1, max_L2, gap,
+                                             temperature, w, w.dT, nullptr, grad_T, st);
+}

@@ -67,6 +67,41 @@ int d2p_sw_forward_marginals(const float* scores, const int* lengths, int B, int
                              float* marginals, float* grad_gap, float* grad_T,
                              void* workspace, size_t workspace_bytes, void* stream);
 
+/* Workspace bytes of the second-order linear-gap entry points below (d2p_sw_hvp,
+ * d2p_sw_param_jacobian, d2p_sw_backward_full). */
+size_t d2p_sw_second_workspace_bytes(int B, int max_L1, int max_L2);
+
+/* Hessian-vector product of the partition: hvp = (d^2 S / dscores^2) . tangent.
+ * Replaces sw_regular_hvp (/root/reference/src/sw/kernels.cuh:209-236) as sequenced by
+ * soft_sw_regular_hvp_cuda (/root/reference/src/sw/torch_cuda.cpp:507-567), which
+ * runs the forward first.
+ *   tangent, hvp [B, max_L1, max_L2]                                              */
+int d2p_sw_hvp(const float* scores, const float* tangent, const int* lengths, int B,
+               int max_L1, int max_L2, float gap, float temperature, float* hvp,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* Jacobian of the marginals with respect to gap (param_type 0) or temperature (1).
+ * Replaces sw_regular_param_grad (/root/reference/src/sw/kernels.cuh:238-281) as
+ * sequenced by soft_sw_regular_param_jacobian_cuda
+ * (/root/reference/src/sw/torch_cuda.cpp:573-668): forward, backward for dS/dtheta,
+ * then the tangent and reverse sweeps.
+ *   jacobian [B, max_L1, max_L2]                                                  */
+int d2p_sw_param_jacobian(const float* scores, int param_type, const int* lengths, int B,
+                          int max_L1, int max_L2, float gap, float temperature,
+                          float* jacobian, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* Backward of the marginals output for a cotangent grad_alignment:
+ *   grad_scores = H . grad_alignment,
+ *   grad_gap[b] = <grad_alignment[b], dP_b/dgap>, grad_T[b] = <grad_alignment[b], dP_b/dT>
+ * (per element; soft_sw_backward_full_cuda, /root/reference/src/sw/torch_cuda.cpp:670-790,
+ * returns their sums over the batch).  The two dot products are accumulated inside
+ * the reverse sweeps; the Jacobians are never written. */
+int d2p_sw_backward_full(const float* scores, const float* grad_alignment, const int* lengths,
+                         int B, int max_L1, int max_L2, float gap, float temperature,
+                         float* grad_scores, float* grad_gap, float* grad_T, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Affine-gap soft Smith-Waterman (gap of length k costs open + (k-1)*ext)
  * ------------------------------------------------------------------------- */

@@ -27,6 +27,10 @@ SIGNATURES = {
                                        _z, _p]),
     "d2p_dtw_workspace_bytes": (_z, [_i, _i, _i]),
     "d2p_dtw_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _i, _p, _p, _p, _p, _z, _p]),
+    "d2p_sw_second_workspace_bytes": (_z, [_i, _i, _i]),
+    "d2p_sw_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _p, _p, _z, _p]),
+    "d2p_sw_param_jacobian": (_i, [_p, _i, _p, _i, _i, _i, _f, _f, _p, _p, _z, _p]),
+    "d2p_sw_backward_full": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _p, _p, _p, _p, _z, _p]),
     "d2p_profile_enable": (_i, [_i]),
     "d2p_profile_report": (_i, [ctypes.c_char_p, _z]),
     "d2p_profile_reset": (None, []),
@@ -132,6 +136,53 @@ def dtw_forward_marginals(costs, lengths, T, bandwidth=-1):
                                           *[ptr(o) for o in outs], ptr(ws), nbytes, stream()))
     _check_status(ws, B)
     return tuple(outs)
+
+
+def _second_ws(B, L1, L2, dev):
+    nbytes = lib().d2p_sw_second_workspace_bytes(B, L1, L2)
+    return _workspace(nbytes, dev), nbytes
+
+
+def sw_hvp(scores, V, lengths, gap, T):
+    import torch
+    B, L1, L2 = scores.shape
+    dev = scores.device
+    lengths = _lengths(lengths, B, L1, L2, dev)
+    out = torch.empty(B, L1, L2, device=dev)
+    ws, nbytes = _second_ws(B, L1, L2, dev)
+    check(lib().d2p_sw_hvp(ptr(scores), ptr(V), ptr(lengths), B, L1, L2, gap, T, ptr(out),
+                           ptr(ws), nbytes, stream()))
+    _check_status(ws, B)
+    return out
+
+
+def sw_param_jacobian(scores, ptype, lengths, gap, T):
+    import torch
+    B, L1, L2 = scores.shape
+    dev = scores.device
+    lengths = _lengths(lengths, B, L1, L2, dev)
+    out = torch.empty(B, L1, L2, device=dev)
+    ws, nbytes = _second_ws(B, L1, L2, dev)
+    check(lib().d2p_sw_param_jacobian(ptr(scores), ptype, ptr(lengths), B, L1, L2, gap, T,
+                                      ptr(out), ptr(ws), nbytes, stream()))
+    _check_status(ws, B)
+    return out
+
+
+def sw_backward_full(scores, grad_alignment, lengths, gap, T):
+    import torch
+    B, L1, L2 = scores.shape
+    dev = scores.device
+    lengths = _lengths(lengths, B, L1, L2, dev)
+    gs = torch.empty(B, L1, L2, device=dev)
+    gg = torch.empty(B, device=dev)
+    gt = torch.empty(B, device=dev)
+    ws, nbytes = _second_ws(B, L1, L2, dev)
+    check(lib().d2p_sw_backward_full(ptr(scores), ptr(grad_alignment), ptr(lengths), B, L1, L2,
+                                     gap, T, ptr(gs), ptr(gg), ptr(gt), ptr(ws), nbytes,
+                                     stream()))
+    _check_status(ws, B)
+    return gs, gg, gt
 
 
 def scale_by_batch(src, g):
