@@ -150,12 +150,54 @@ SwOut sw_run(const Tensor& scores, const Tensor& lengths, const Dims& d, float g
     return o;
 }
 
+// Second-order entry points (HVP, Jacobians, marginal-path backward) through the C ABI.
+Tensor second_workspace(const Dims& d, const Tensor& like) {
+    return workspace(d2p_sw_second_workspace_bytes(d.B, d.L1, d.L2), like);
+}
+
+Tensor sw_hvp_run(const Tensor& scores, const Tensor& tangent, const Tensor& lengths,
+                  const Dims& d, float gap, float T) {
+    Tensor out = torch::empty({d.B, d.L1, d.L2}, scores.options());
+    Tensor ws = second_workspace(d, scores);
+    D2P_CALL(d2p_sw_hvp(scores.data_ptr<float>(), tangent.data_ptr<float>(),
+                        lengths.data_ptr<int>(), d.B, d.L1, d.L2, gap, T, out.data_ptr<float>(),
+                        ws.data_ptr(), ws.numel(), current_stream()));
+    return out;
+}
+
+// returns (grad_scores [B,L1,L2], per-element <ga, dP/dgap> [B], <ga, dP/dT> [B])
+std::tuple<Tensor, Tensor, Tensor> sw_backward_full_run(const Tensor& scores, const Tensor& ga,
+                                                        const Tensor& lengths, const Dims& d,
+                                                        float gap, float T) {
+    auto opt = scores.options();
+    Tensor gs = torch::empty({d.B, d.L1, d.L2}, opt);
+    Tensor gg = torch::empty({d.B}, opt), gt = torch::empty({d.B}, opt);
+    Tensor ws = second_workspace(d, scores);
+    D2P_CALL(d2p_sw_backward_full(scores.data_ptr<float>(), ga.data_ptr<float>(),
+                                  lengths.data_ptr<int>(), d.B, d.L1, d.L2, gap, T,
+                                  gs.data_ptr<float>(), gg.data_ptr<float>(), gt.data_ptr<float>(),
+                                  ws.data_ptr(), ws.numel(), current_stream()));
+    return {gs, gg, gt};
+}
+
+// The marginal cotangent as the reference prepares it
+// (/root/reference/src/sw/torch_cuda.cpp:325-338): same shape, float32, contiguous.
+Tensor prepare_cotangent(Tensor g, const Tensor& like, const char* name) {
+    TORCH_CHECK(g.sizes() == like.sizes(), name, " shape mismatch: expected ", like.sizes(),
+                " but got ", g.sizes());
+    TORCH_CHECK(g.is_cuda(), name, " must be on CUDA, got ", g.device());
+    if (g.scalar_type() != torch::kFloat32) g = g.to(torch::kFloat32);
+    if (g.device() != like.device()) g = g.to(like.device());
+    return g.contiguous();
+}
+
 // Autograd semantics of SoftSWRegularCUDAFunction
 // (/root/reference/src/sw/torch_cuda.cpp:178-411): outputs {value, marginals};
-// d value / d scores = marginals, so backward scales the saved marginals, and
-// the parameter gradients are sum_b grad_value[b] * dS_b/dtheta, shape [1].
-// Two Function classes share this logic: float parameters (no parameter
-// inputs) and tensor parameters (gap / temperature receive gradients).
+// d value / d scores = marginals, so the value path scales the saved marginals; the
+// marginal path adds the HVP against the marginal cotangent and its dot products
+// with dP/dgap and dP/dT; parameter gradients are summed over the batch, shape [1].
+// Two Function classes share this logic: float parameters (no parameter inputs)
+// and tensor parameters (gap / temperature receive gradients).
 tensor_list sw_autograd_forward(AutogradContext* ctx, const Tensor& scores,
                                 const Tensor& lengths, double gap, double temperature) {
     ctx->set_materialize_grads(false);
@@ -163,7 +205,9 @@ tensor_list sw_autograd_forward(AutogradContext* ctx, const Tensor& scores,
     Dims d = checked_dims(scores, "SW");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
     SwOut o = sw_run(scores, lengths, d, (float)gap, (float)temperature);
-    ctx->save_for_backward({o.marginals, o.grad_gap, o.grad_T});
+    ctx->save_for_backward({scores, lengths, o.marginals, o.grad_gap, o.grad_T});
+    ctx->saved_data["gap"] = gap;
+    ctx->saved_data["temperature"] = temperature;
     return {o.partition, o.marginals};
 }
 
@@ -171,7 +215,7 @@ tensor_list sw_autograd_forward(AutogradContext* ctx, const Tensor& scores,
 tensor_list sw_autograd_backward(AutogradContext* ctx, const tensor_list& grads,
                                  bool want_gap, bool want_T) {
     auto saved = ctx->get_saved_variables();
-    Tensor marg = saved[0], ggap = saved[1], gT = saved[2];
+    Tensor scores = saved[0], lengths = saved[1], marg = saved[2], ggap = saved[3], gT = saved[4];
     c10::hip::HIPGuardMasqueradingAsCUDA guard(marg.device());
     Tensor grad_value = grads[0], grad_marg = grads[1];
     Tensor grad_scores, grad_gap, grad_T;
@@ -180,7 +224,17 @@ tensor_list sw_autograd_backward(AutogradContext* ctx, const tensor_list& grads,
         if (want_gap) grad_gap = grad_param_sum(grad_value, ggap);
         if (want_T) grad_T = grad_param_sum(grad_value, gT);
     }
-    if (grad_marg.defined() && grad_marg.numel() > 0) not_yet("soft_sw marginal-path backward");
+    if (grad_marg.defined() && grad_marg.numel() > 0) {
+        Tensor gm = prepare_cotangent(grad_marg, scores, "grad_posteriors");
+        const float gap = (float)ctx->saved_data["gap"].toDouble();
+        const float T = (float)ctx->saved_data["temperature"].toDouble();
+        Dims d = checked_dims(scores, "SW");
+        auto r = sw_backward_full_run(scores, gm, lengths, d, gap, T);
+        grad_scores = grad_scores.defined() ? grad_scores + std::get<0>(r) : std::get<0>(r);
+        Tensor tg = std::get<1>(r).sum().reshape({1}), tt = std::get<2>(r).sum().reshape({1});
+        if (want_gap) grad_gap = grad_gap.defined() ? grad_gap + tg : tg;
+        if (want_T) grad_T = grad_T.defined() ? grad_T + tt : tt;
+    }
     return {grad_scores, grad_gap, grad_T};
 }
 
@@ -239,13 +293,52 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> soft_sw_with_grads(Tensor scores, dou
     return {o.partition, o.marginals, o.grad_gap, o.grad_T};
 }
 
-Tensor soft_sw_hvp(Tensor, Tensor, double, double, c10::optional<Tensor>) { not_yet("soft_sw_hvp"); }
-Tensor soft_sw_param_jacobian(Tensor, int64_t, double, double, c10::optional<Tensor>) {
-    not_yet("soft_sw_param_jacobian");
+Tensor soft_sw_hvp(Tensor scores, Tensor tangent, double gap, double temperature,
+                   c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    CHECK_INPUT_DEV(tangent);
+    TORCH_CHECK(tangent.sizes() == scores.sizes(), "tangent must have same shape as scores");
+    TORCH_CHECK(tangent.device() == scores.device(), "tangent must be on same device as scores, got ",
+                tangent.device(), " vs ", scores.device());
+    Dims d = checked_dims(scores, "SW");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    return sw_hvp_run(scores, tangent, l, d, (float)gap, (float)temperature);
 }
-std::tuple<Tensor, Tensor, Tensor> soft_sw_backward_full(Tensor, Tensor, double, double,
-                                                         c10::optional<Tensor>) {
-    not_yet("soft_sw_backward_full");
+
+Tensor soft_sw_param_jacobian(Tensor scores, int64_t param_type, double gap, double temperature,
+                              c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    TORCH_CHECK(param_type >= 0 && param_type <= 1, "param_type must be 0 or 1");
+    Dims d = checked_dims(scores, "SW");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    Tensor out = torch::empty({d.B, d.L1, d.L2}, scores.options());
+    Tensor ws = second_workspace(d, scores);
+    D2P_CALL(d2p_sw_param_jacobian(scores.data_ptr<float>(), (int)param_type, l.data_ptr<int>(),
+                                   d.B, d.L1, d.L2, (float)gap, (float)temperature,
+                                   out.data_ptr<float>(), ws.data_ptr(), ws.numel(),
+                                   current_stream()));
+    return out;
+}
+
+std::tuple<Tensor, Tensor, Tensor> soft_sw_backward_full(Tensor scores, Tensor grad_alignment,
+                                                         double gap, double temperature,
+                                                         c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    TORCH_CHECK(grad_alignment.sizes() == scores.sizes(),
+                "grad_alignment must have same shape as scores");
+    TORCH_CHECK(grad_alignment.is_cuda(), "grad_alignment must be a CUDA tensor");
+    TORCH_CHECK(grad_alignment.device() == scores.device(),
+                "grad_alignment must be on same device as scores, got ", grad_alignment.device(),
+                " vs ", scores.device());
+    Dims d = checked_dims(scores, "SW");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    Tensor ga = grad_alignment.contiguous();
+    if (ga.scalar_type() != torch::kFloat32) ga = ga.to(torch::kFloat32);
+    auto r = sw_backward_full_run(scores, ga, l, d, (float)gap, (float)temperature);
+    return {std::get<0>(r), std::get<1>(r).sum().reshape({1}), std::get<2>(r).sum().reshape({1})};
 }
 
 std::vector<Tensor> sw_forward(Tensor s, double g, double t, c10::optional<Tensor> l) {

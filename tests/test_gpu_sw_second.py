@@ -115,3 +115,46 @@ def test_sw_backward_full(cuda):
         per = 1e-4 * max(1.0, np.abs(J).max()) + allow
         tol = per * np.abs(ga.numpy()).sum(axis=(1, 2))
         assert np.all(np.abs(got - ref) <= tol), (p, got, ref, tol)
+
+
+def test_sw_ops_match_capi(cuda):
+    """torch.ops.d2p second-order ops route to the same kernels."""
+    import d2p_amd
+    from d2p_amd import ops
+    s = _seeded(21, (2, 50, 60))
+    v = _seeded(22, (2, 50, 60))
+    k = O.get("oracle")
+    _close(d2p_amd.soft_sw_hvp(s.to(cuda), v.to(cuda), -1.0, 1.0, None),
+           k.soft_sw_hvp(s.numpy(), v.numpy(), -1.0, 1.0), "soft_sw_hvp op")
+    _close(ops.sw.marginals_hvp(s.to(cuda), v.to(cuda), -1.0, 1.0),
+           k.soft_sw_hvp(s.numpy(), v.numpy(), -1.0, 1.0), "sw_marginals_hvp op")
+    for p, fn in ((0, ops.sw.marginals_grad_gap), (1, ops.sw.marginals_grad_temp)):
+        ref, allow = _jacobian_ref(k, s.numpy(), p, -1.0, 1.0)
+        _close(d2p_amd.soft_sw_param_jacobian(s.to(cuda), p, -1.0, 1.0, None), ref,
+               "soft_sw_param_jacobian op", allow)
+        _close(fn(s.to(cuda), -1.0, 1.0), ref, "sw_marginals_grad op", allow)
+    gs, gg, gt = d2p_amd.soft_sw_backward_full(s.to(cuda), v.to(cuda), -1.0, 1.0, None)
+    assert gg.shape == (1,) and gt.shape == (1,)
+    _close(gs, k.soft_sw_hvp(s.numpy(), v.numpy(), -1.0, 1.0), "backward_full op")
+
+
+def test_sw_marginal_path_autograd(cuda):
+    """loss = <W, marginals>: d loss / d scores = H W, d loss / d gap = <W, dP/dgap>."""
+    import d2p_amd
+    s = _seeded(31, (2, 40, 45))
+    W = _seeded(32, (2, 40, 45))
+    k = O.get("oracle")
+    x = s.to(cuda).requires_grad_(True)
+    gap = torch.tensor(-1.0, device=cuda, requires_grad=True)
+    T = torch.tensor(0.8, device=cuda, requires_grad=True)
+    res = d2p_amd.soft_sw(x, gap=gap, temperature=T)
+    loss = (res.marginals * W.to(cuda)).sum() + 0.5 * res.value.sum()
+    loss.backward()
+    rp, rm, rgg, rgt = k.soft_sw(s.numpy(), -1.0, 0.8)
+    expect = k.soft_sw_hvp(s.numpy(), W.numpy(), -1.0, 0.8) + 0.5 * rm
+    _close(x.grad, expect, "marginal-path grad_scores")
+    for p, g, rv in ((0, gap, rgg), (1, T, rgt)):
+        J, allow = _jacobian_ref(k, s.numpy(), p, -1.0, 0.8)
+        ref = float((J.astype(np.float64) * W.numpy()).sum() + 0.5 * rv.sum())
+        tol = (1e-4 * max(1.0, np.abs(J).max()) + allow) * float(np.abs(W.numpy()).sum()) + 1e-3 * abs(ref)
+        assert abs(float(g.grad) - ref) <= tol, (p, float(g.grad), ref, tol)
