@@ -22,6 +22,7 @@
 #include "wavefront.hip.h"
 #include "../../include/d2p_amd.h"
 #include "capi_util.hip.h"
+#include "dtw_internal.hip.h"
 
 namespace d2p_amd {
 namespace dtw {
@@ -309,14 +310,88 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
 }  // namespace dtw
 }  // namespace d2p_amd
 
+namespace d2p_amd {
+namespace dtw {
+
+namespace {
+constexpr size_t kLdsLimit = 160 * 1024 - 256;
+
+size_t lds_forward(int max_L1, int max_L2) {
+    const int R = ring_len(max_L1, max_L2, 256);
+    return (size_t)NW * 2 * 65 * PF * sizeof(float) + ((size_t)NW * R + NW * DUMMY) * sizeof(float);
+}
+
+size_t lds_backward(int max_L1, int max_L2, int P) {
+    const int R = ring_len(max_L1, max_L2, 128);
+    return (size_t)NW * 2 * (65 * P + 64 * P + 64) * sizeof(float) +
+           ((size_t)NW * R + NW * DUMMY) * sizeof(float2);
+}
+
+// 16-step backward chunks when they fit in LDS, else 8-step chunks
+int backward_chunk(int max_L1, int max_L2) {
+    return lds_backward(max_L1, max_L2, 16) <= kLdsLimit ? 16 : 8;
+}
+
+template <int P>
+int launch_backward_p(const float* costs, const int* lengths, int B, int max_L1, int max_L2,
+                      float T, int bandwidth, const Layout& ws, float* marginals, float* grad_T,
+                      hipStream_t st) {
+    const int ns = (max_L1 + 63) / 64;
+    const int R = ring_len(max_L1, max_L2, 128);
+    const size_t lds = lds_backward(max_L1, max_L2, P);
+    D2P_HIP(hipFuncSetAttribute((const void*)dtw_backward_kernel<P>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    D2P_LAUNCH("dtw_backward", dtw_backward_kernel<P>, dim3(B), dim3(NW * 64), lds, st, costs,
+               lengths, ws.alpha_sk, ws.brow, marginals, grad_T, ws.status, ws.trash, max_L1,
+               max_L2, ns, T, bandwidth, R);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+}  // namespace
+
+int check_shape(int B, int max_L1, int max_L2, float temperature) {
+    D2P_REQUIRE(B >= 0 && max_L1 >= 0 && max_L2 >= 0, "negative dimension");
+    D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
+    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 4, "max_L2 too large");
+    D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
+    D2P_REQUIRE(lds_forward(max_L1, max_L2) <= kLdsLimit &&
+                    lds_backward(max_L1, max_L2, backward_chunk(max_L1, max_L2)) <= kLdsLimit,
+                "sequence too long for the LDS stripe rings");
+    return D2P_OK;
+}
+
+int launch_forward(const float* costs, const int* lengths, int B, int max_L1, int max_L2,
+                   float T, int bandwidth, const Layout& ws, float* value, hipStream_t st) {
+    const int ns = (max_L1 + 63) / 64;
+    const int R = ring_len(max_L1, max_L2, 256);
+    const size_t lds = lds_forward(max_L1, max_L2);
+    D2P_HIP(hipFuncSetAttribute((const void*)dtw_forward_kernel,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    D2P_LAUNCH("dtw_forward", dtw_forward_kernel, dim3(B), dim3(NW * 64), lds, st, costs, lengths,
+               ws.alpha_sk, ws.brow, value, ws.status, max_L1, max_L2, ns, T, bandwidth, R);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
+int launch_backward(const float* costs, const int* lengths, int B, int max_L1, int max_L2,
+                    float T, int bandwidth, const Layout& ws, float* marginals, float* grad_T,
+                    hipStream_t st) {
+    if (backward_chunk(max_L1, max_L2) == 16)
+        return launch_backward_p<16>(costs, lengths, B, max_L1, max_L2, T, bandwidth, ws,
+                                     marginals, grad_T, st);
+    return launch_backward_p<8>(costs, lengths, B, max_L1, max_L2, T, bandwidth, ws, marginals,
+                                grad_T, st);
+}
+
+}  // namespace dtw
+}  // namespace d2p_amd
+
 using namespace d2p_amd;
 
 extern "C" size_t d2p_dtw_workspace_bytes(int B, int max_L1, int max_L2) {
     if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
-    const size_t ns = ((size_t)max_L1 + 63) / 64;
     // status words | trash line | skewed alpha table | last row of every stripe
-    return wf::status_bytes(B) + wf::TRASH_BYTES +
-           (size_t)B * ns * (size_t)wf::stored_steps(max_L2) * 65 * sizeof(float);
+    return wf::layout(nullptr, B, max_L1, max_L2).bytes;
 }
 
 extern "C" int d2p_dtw_forward_marginals(const float* costs, const int* lengths, int B,
@@ -324,52 +399,17 @@ extern "C" int d2p_dtw_forward_marginals(const float* costs, const int* lengths,
                                          int bandwidth, float* value, float* marginals,
                                          float* grad_T, void* workspace, size_t workspace_bytes,
                                          void* stream) {
-    D2P_REQUIRE(B >= 0 && max_L1 >= 0 && max_L2 >= 0, "negative dimension");
-    D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
+    const int rc = dtw::check_shape(B, max_L1, max_L2, temperature);
+    if (rc != D2P_OK) return rc;
     if (B == 0) return D2P_OK;
     D2P_REQUIRE(costs && lengths && value && marginals && grad_T, "null pointer argument");
     const size_t need = d2p_dtw_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
-    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 8, "max_L2 too large");
-    D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
     hipStream_t st = (hipStream_t)stream;
-    const int ns = (max_L1 + 63) / 64;
-    const int Rf = wf::ring_len(max_L1, max_L2, 256);
-    const int Rb = wf::ring_len(max_L1, max_L2, 128);
-    const size_t lds_f = (size_t)wf::NW * 2 * 65 * dtw::PF * sizeof(float) +
-                         ((size_t)wf::NW * Rf + wf::NW * dtw::DUMMY) * sizeof(float);
-    // backward: 16-step chunks when they fit in LDS, else 8-step chunks (long rows
-    // need long rings)
-    auto lds_bwd = [&](int P) {
-        return (size_t)wf::NW * 2 * (65 * P + 64 * P + 64) * sizeof(float) +
-               ((size_t)wf::NW * Rb + wf::NW * dtw::DUMMY) * sizeof(float2);
-    };
-    const size_t lds_limit = 160 * 1024 - 256;
-    const int Pb = lds_bwd(16) <= lds_limit ? 16 : 8;
-    const size_t lds_b = lds_bwd(Pb);
-    D2P_REQUIRE(lds_f <= lds_limit && lds_b <= lds_limit,
-                "sequence too long for the LDS stripe rings");
-    const void* bwd_kernel = Pb == 16 ? (const void*)dtw::dtw_backward_kernel<16>
-                                      : (const void*)dtw::dtw_backward_kernel<8>;
-    D2P_HIP(hipFuncSetAttribute((const void*)dtw::dtw_forward_kernel,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_f));
-    D2P_HIP(hipFuncSetAttribute(bwd_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
-    int* status = (int*)workspace;
-    float* trash = (float*)((char*)workspace + wf::status_bytes(B));
-    float* alpha_sk = (float*)((char*)trash + wf::TRASH_BYTES);
-    float* brow = alpha_sk + (size_t)B * ns * wf::stored_steps(max_L2) * 64;
-    D2P_LAUNCH("dtw_forward", dtw::dtw_forward_kernel, dim3(B), dim3(wf::NW * 64), lds_f, st,
-               costs, lengths, alpha_sk, brow, value, status, max_L1, max_L2, ns, temperature,
-               bandwidth, Rf);
-    D2P_HIP(hipGetLastError());
-    if (Pb == 16)
-        D2P_LAUNCH("dtw_backward", dtw::dtw_backward_kernel<16>, dim3(B), dim3(wf::NW * 64), lds_b, st,
-               costs, lengths, alpha_sk, brow, marginals, grad_T, status, trash, max_L1, max_L2,
-               ns, temperature, bandwidth, Rb);
-    else
-        D2P_LAUNCH("dtw_backward", dtw::dtw_backward_kernel<8>, dim3(B), dim3(wf::NW * 64), lds_b, st,
-               costs, lengths, alpha_sk, brow, marginals, grad_T, status, trash, max_L1, max_L2,
-               ns, temperature, bandwidth, Rb);
-    D2P_HIP(hipGetLastError());
-    return D2P_OK;
+    const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2);
+    const int r = dtw::launch_forward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth,
+                                      ws, value, st);
+    if (r != D2P_OK) return r;
+    return dtw::launch_backward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth, ws,
+                                marginals, grad_T, st);
 }

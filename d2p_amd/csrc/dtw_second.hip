@@ -1,0 +1,547 @@
+// dtw_second.hip -- second-order quantities of soft DTW on gfx950: Hessian-vector
+// products and the Jacobian of the alignment marginals with respect to temperature.
+//
+// Reference behaviour restated (not translated):
+//   HVP          /root/reference/src/dtw/kernels_cpu.cpp:229-377
+//   param grad   /root/reference/src/dtw/kernels_cpu.cpp:383-534 (temperature only)
+// With w the softmin weights of a cell over its predecessors (diag, up, left) and
+// x their tangents (0 outside the table and the band):
+//   tangent   HVP   x[i,j] = V[i,j] + sum_k w_k x_k
+//             T     x[i,j] = (softmin - E_w[alpha_pred]) / T + sum_k w_k x_k
+//   reverse   beta and a second channel g both start at the terminal cell (beta 1,
+//             g 0) and flow to the predecessors: beta_k += beta w_k,
+//             g_k += g w_k + beta dw_k with
+//             HVP   dw_k = w_k (E_w[x] - x_k) / T
+//             T     dw_k = w_k ((E_w[x] - x_k) / T + (alpha_k - E_w[alpha]) / T^2);
+//             the output of a cell is g.
+// Mapping: the stripe pipeline of wavefront.hip.h, as in sw_second.hip: the tangent
+// sweep reads the primal table like the reverse sweep and passes its tangent like
+// the forward; the reverse sweep carries (beta, g) pairs.
+
+#include <vector>
+
+#include "wavefront.hip.h"
+#include "../../include/d2p_amd.h"
+#include "capi_util.hip.h"
+#include "dtw_internal.hip.h"
+
+namespace d2p_amd {
+namespace dtw2 {
+
+using namespace wf;
+
+enum Mode { HVP = 0, TEMP = 1 };
+
+__device__ __forceinline__ float band_centre(int i, int L1, int L2) {
+    return L1 > 0 ? (float)((long long)i * L2) / (float)L1 : 0.0f;
+}
+__device__ __forceinline__ bool in_band(float ej, int j, float bw) {
+    return bw < 0.0f || fabsf((float)j - ej) <= bw;
+}
+
+template <int MODE, int P>
+__global__ void __launch_bounds__(NW * 64)
+dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ lengths,
+                   const float* __restrict__ alpha_sk, const float* __restrict__ brow,
+                   float* __restrict__ tan_sk, float* __restrict__ tan_brow,
+                   int* __restrict__ status, int L1max, int L2max, int NSmax, float T,
+                   int bandwidth, int R) {
+    using Tile = ChunkTile<P>;
+    constexpr int AR = Tile::FLOATS;      // P alpha rows after the input tile
+    constexpr int RR = AR + P * 64;       // row above
+    constexpr int BUF = RR + 64;
+    constexpr int SINK = 64 + P;
+    extern __shared__ float smem[];
+    __shared__ int prog[NW];
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const unsigned ul4 = (unsigned)lane * 4u;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float* buf = smem + wave * BUF;
+    float* rings = smem + NW * BUF;
+    float* sink = rings + NW * R + wave * SINK;
+    int* st = status + b;
+    const int tbase = Tile::read_base(lane);
+
+    if (lane == 0) prog[wave] = -1;
+    __syncthreads();
+
+    const int L1 = min(max(lengths[2 * b], 0), L1max);
+    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const float c = kLog2e / T;
+    const float rT = 1.0f / T;
+    const float bw = (bandwidth < 0 || L1 == 0 || L2 == 0) ? -1.0f : (float)bandwidth;
+    const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
+    const int nsteps = L2 + 63;
+    const int nch = (nsteps + P - 1) / P;
+    const size_t NT = (size_t)stored_steps(L2max);
+    const float* ibase = input + (size_t)b * L1max * L2max;   // V (HVP) or costs (T)
+    const uint32_t in_lds = lds_address(buf);
+
+    for (int s = wave; s < NS; s += NW) {
+        const int i0 = s * 64;
+        const int L2eff = (i0 + lane < L1) ? L2 : 0;
+        const float ej = band_centre(i0 + lane + 1, L1, L2);
+        const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * NT * 64;
+        const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
+        float* tout = tan_sk + (((size_t)b * NSmax + s) * NT + APAD) * 64;
+        float* tb_s = tan_brow + ((size_t)b * NSmax + s) * NT;
+        const float* ring_in = ring_from(rings, s, R);
+        float* ring_out = ring_of(rings, s, R);
+
+        auto issue_chunk = [&](int k) {
+            const int t0 = k * P;
+            dma_tile<P, 1>(in_lds, ibase, i0, L1max, L2max, lane, t0);
+            dma_rows<P, 1>(in_lds + AR * 4, astripe, t0, ul4);
+            uint32_t roff = (uint32_t)min(t0 + 62 + min(lane, P), nsteps - 1) * 4u;
+            uint32_t rl = in_lds + RR * 4;
+            lds_dma_dword<0>(bup, roff, rl, 0u);
+        };
+
+#pragma unroll
+        for (int t = -APAD; t < 0; ++t) lane_store(tout + t * 64, ul4, 0.0f);
+        wave_lds_sync();
+        issue_chunk(0);
+        float Aw[P + 2];
+        Aw[P] = kPINF;   // alpha at steps -2, -1: column-0 boundary
+        Aw[P + 1] = kPINF;
+        float cur = 0.0f, up_prev = 0.0f;
+
+        for (int k = 0; k < nch; ++k) {
+            const int t0 = k * P;
+            chunk_waits<P>(prog, s, NS, k, nch, R, st);
+            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            float iv[P];
+#pragma unroll
+            for (int u = 0; u < P; ++u) iv[u] = buf[tbase + u];
+            Aw[0] = Aw[P];
+            Aw[1] = Aw[P + 1];
+#pragma unroll
+            for (int j = 0; j < P; ++j) Aw[j + 2] = buf[AR + j * 64 + lane];
+            float bv = buf[RR + lane];
+            bv = (s > 0 && lane <= P && t0 + 62 + lane <= nsteps - 1) ? bv : kPINF;
+            float rreg = 0.0f;
+            if (s > 0 && lane < P) rreg = ring_in[ring_index(t0 + lane + 63, R)];
+            wave_lds_sync();
+            if (k + 1 < nch) issue_chunk(k + 1);
+            float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
+            float* toutc = tout + (size_t)t0 * 64;
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                const int t = t0 + u;
+                const int col = t - lane;
+                const bool ok = (unsigned)col < (unsigned)L2eff && in_band(ej, col + 1, bw);
+                const float a0 = Aw[u + 2], a1 = Aw[u + 1];
+                const float dga = wave_shr1_or(Aw[u], bv);
+                const float bvn = wave_shl1(bv, kPINF);
+                const float upa = wave_shr1_or(a1, bvn);
+                bv = bvn;
+                const float tu = wave_shr1_or(cur, rreg);
+                rreg = wave_shl1(rreg, 0.0f);
+                const float td = up_prev;
+                up_prev = tu;
+                const float tl = cur;
+                const float m = fminf(fminf(dga, upa), a1);
+                const float ed = fast_exp2((m - dga) * c), eu = fast_exp2((m - upa) * c);
+                const float el = fast_exp2((m - a1) * c);
+                const float rin = m < kPINF ? fast_rcp((ed + eu) + el) : 0.0f;
+                const float wsum = ((ed * td + eu * tu) + el * tl) * rin;
+                float x;
+                if (MODE == HVP) {
+                    x = iv[u] + wsum;
+                } else {
+                    const float ea = ((ed * dga + eu * upa) + el * a1) * rin;
+                    x = ((a0 - iv[u]) - ea) * rT + wsum;
+                }
+                cur = ok ? x : 0.0f;
+                lane_store(toutc + u * 64, ul4, cur);
+                pub[u] = cur;
+            }
+            wave_lds_sync();
+            if (lane < P) lane_store(tb_s, (unsigned)(t0 + lane) * 4u, ring_out[t0 % R + lane]);
+            publish(prog, wave, s * PROG_STRIDE + k + 1);
+        }
+    }
+}
+
+// DOT: accumulate <V, output> into dot[b] instead of writing the output.
+template <int MODE, int P, bool DOT>
+__global__ void __launch_bounds__(NW * 64)
+dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
+                const float* __restrict__ alpha_sk, const float* __restrict__ brow,
+                const float* __restrict__ tan_sk, const float* __restrict__ tan_brow,
+                float* __restrict__ out, float* __restrict__ dot, int* __restrict__ status,
+                float* __restrict__ trash, int L1max, int L2max, int NSmax, float T,
+                int bandwidth, int R) {
+    using Tile = ChunkTile<P>;
+    constexpr int AR = DOT ? Tile::FLOATS : 0;   // P alpha rows (after the V tile)
+    constexpr int XR = AR + P * 64;
+    constexpr int RA = XR + P * 64;
+    constexpr int RX = RA + 64;
+    constexpr int OT = RX + 64;
+    constexpr int BUF = OT + (DOT ? 0 : Tile::FLOATS);
+    constexpr int SINK = 64 + P;
+    extern __shared__ float smem[];
+    __shared__ int prog[NW];
+    __shared__ float red[NW];
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const unsigned ul4 = (unsigned)lane * 4u;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float* buf = smem + wave * BUF;
+    float* otile = buf + OT;
+    float4* rings = reinterpret_cast<float4*>(smem + NW * BUF);
+    float4* sink = rings + NW * R + wave * SINK;
+    int* st = status + b;
+    const int tbase = Tile::read_base(lane);
+
+    if (lane == 0) prog[wave] = -1;
+    __syncthreads();
+
+    const int L1 = min(max(lengths[2 * b], 0), L1max);
+    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const float c = kLog2e / T;
+    const float rT = 1.0f / T;
+    const float bw = (bandwidth < 0 || L1 == 0 || L2 == 0) ? -1.0f : (float)bandwidth;
+    const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
+    const int nsteps = L2 + 63;
+    const int nch = (nsteps + P - 1) / P;
+    const size_t NT = (size_t)stored_steps(L2max);
+    const float* vbase = DOT ? V + (size_t)b * L1max * L2max : nullptr;
+    float* obase = DOT ? nullptr : out + (size_t)b * L1max * L2max;
+    const uint32_t in_lds = lds_address(buf);
+
+    if (!DOT) zero_padding(obase, L1, L2, L1max, L2max, NW * 64);
+
+    float dacc = 0.0f;
+    float A[P + 2], X[P + 2];
+
+    for (int q = wave; q < NS; q += NW) {
+        const int s = NS - 1 - q;
+        const int i0 = s * 64;
+        const int L2eff = (i0 + lane < L1) ? L2 : 0;
+        const float ej = band_centre(i0 + lane + 1, L1, L2);
+        const int term_step = (i0 + lane == L1 - 1) ? L2 - 1 + lane : -1000000;
+        const size_t sb = ((size_t)b * NSmax + s) * NT;
+        const size_t ub = ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
+        const float* astripe = alpha_sk + sb * 64;
+        const float* xstripe = tan_sk + sb * 64;
+        const float* bup = brow + ub;
+        const float* xup = tan_brow + ub;
+        const float4* ring_in = ring_from(rings, q, R);
+        float4* ring_out = ring_of(rings, q, R);
+        const bool below = q > 0;
+
+        auto issue_chunk = [&](int k) {
+            const int th = nsteps - 1 - k * P;
+            if (DOT) dma_tile<P, -1>(in_lds, vbase, i0, L1max, L2max, lane, th);
+            dma_rows<P, -1>(in_lds + AR * 4, astripe, th - 2, ul4);
+            dma_rows<P, -1>(in_lds + XR * 4, xstripe, th - 2, ul4);
+            const uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
+            uint32_t o = roff, l = in_lds + RA * 4;
+            lds_dma_dword<0>(bup, o, l, 0u);
+            o = roff;
+            l = in_lds + RX * 4;
+            lds_dma_dword<0>(xup, o, l, 0u);
+        };
+
+        {
+            const float* a0p = astripe + (size_t)(nsteps - 1 + APAD) * 64;
+            const float* x0p = xstripe + (size_t)(nsteps - 1 + APAD) * 64;
+            A[P] = lane_load(a0p, ul4);
+            A[P + 1] = lane_load(a0p - 64, ul4);
+            X[P] = lane_load(x0p, ul4);
+            X[P + 1] = lane_load(x0p - 64, ul4);
+            __asm__ volatile("" ::"v"(A[P]), "v"(A[P + 1]), "v"(X[P]), "v"(X[P + 1]));
+        }
+        wave_lds_sync();
+        issue_chunk(0);
+        float lb = 0.0f, lg = 0.0f, ubt = 0.0f, ug = 0.0f;
+        float db = 0.0f, dg = 0.0f, db2 = 0.0f, dg2 = 0.0f;
+
+        for (int k = 0; k < nch; ++k) {
+            const int t_hi = nsteps - 1 - k * P;
+            chunk_waits<P>(prog, q, NS, k, nch, R, st);
+            if (k == 0 || DOT) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            float vv[P];
+#pragma unroll
+            for (int u = 0; u < P; ++u) vv[u] = DOT ? buf[tbase + u] : 0.0f;
+            A[0] = A[P];
+            A[1] = A[P + 1];
+            X[0] = X[P];
+            X[1] = X[P + 1];
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                A[j + 2] = buf[AR + j * 64 + lane];
+                X[j + 2] = buf[XR + j * 64 + lane];
+            }
+            const bool row_ok = s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1;
+            float bA = row_ok ? buf[RA + lane] : kPINF;
+            float bX = row_ok ? buf[RX + lane] : 0.0f;
+            float qub = 0.0f, qug = 0.0f, qdb = 0.0f, qdg = 0.0f;
+            if (below && lane >= 64 - P) {
+                const int j = 63 - lane;
+                const float4 ru = ring_in[ring_index(k * P + j + 63, R)];
+                const float4 rd = ring_in[ring_index(k * P + j + 62, R)];
+                qub = ru.x;
+                qug = ru.y;
+                qdb = rd.z;
+                qdg = rd.w;
+            }
+            wave_lds_sync();
+            if (k + 1 < nch) issue_chunk(k + 1);
+            float4* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
+            {
+                const float u0b = lane_bcast(qub, 63), u0g = lane_bcast(qug, 63);
+                const float d0b = lane_bcast(qdb, 63), d0g = lane_bcast(qdg, 63);
+                const float d1b = lane_bcast(qdb, 62), d1g = lane_bcast(qdg, 62);
+                if (lane == 63) {
+                    ubt = u0b; ug = u0g;
+                    db = d0b; dg = d0g;
+                    db2 = d1b; dg2 = d1g;
+                }
+            }
+            qdb = wave_shr1(wave_shr1(qdb, 0.0f), 0.0f);
+            qdg = wave_shr1(wave_shr1(qdg, 0.0f), 0.0f);
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                const int t = t_hi - u;
+                const int col = t - lane;
+                const bool ok = (unsigned)col < (unsigned)L2eff && in_band(ej, col + 1, bw);
+                const float a1 = A[u + 1], x1 = X[u + 1];
+                const float nA = wave_shl1(bA, kPINF), nX = wave_shl1(bX, 0.0f);
+                const float upa = wave_shr1_or(a1, bA), upx = wave_shr1_or(x1, bX);
+                const float dga = wave_shr1_or(A[u + 2], nA), dgx = wave_shr1_or(X[u + 2], nX);
+                bA = nA;
+                bX = nX;
+                const float m = fminf(fminf(dga, upa), a1);
+                const float ed = fast_exp2((m - dga) * c), eu = fast_exp2((m - upa) * c);
+                const float el = fast_exp2((m - a1) * c);
+                const float rin = m < kPINF ? fast_rcp((ed + eu) + el) : 0.0f;
+                const float wd = ed * rin, wu = eu * rin, wl = el * rin;
+                const float ex = (wd * dgx + wu * upx) + wl * x1;
+                float dwd = wd * (ex - dgx) * rT, dwu = wu * (ex - upx) * rT,
+                      dwl = wl * (ex - x1) * rT;
+                if (MODE == TEMP) {
+                    const float ea = (wd * dga + wu * upa) + wl * a1;
+                    const float rT2 = rT * rT;
+                    dwd += wd * (dga - ea) * rT2;
+                    dwu += wu * (upa - ea) * rT2;
+                    dwl += wl * (a1 - ea) * rT2;
+                }
+                // reference accumulation order: init, diagonal, left, up successor
+                const float binit = t == term_step ? 1.0f : 0.0f;
+                const float beta = ((binit + db) + lb) + ubt;
+                const float g = ((dg + lg) + ug);
+                const bool live = MODE == HVP ? (ok && beta != 0.0f)
+                                              : (ok && !(beta == 0.0f && fabsf(g) < 1e-20f));
+                const float bl = live ? beta : 0.0f;
+                const float gl = live ? g : 0.0f;
+                if (DOT) dacc += gl * (ok ? vv[u] : 0.0f);
+                else otile[tbase + u] = gl;
+                const float obd = bl * wd, obu = bl * wu, obl = bl * wl;
+                const float ogd = gl * wd + bl * dwd, ogu = gl * wu + bl * dwu;
+                const float ogl = gl * wl + bl * dwl;
+                pub[u] = make_float4(obu, ogu, obd, ogd);
+                qub = wave_shr1(qub, 0.0f);
+                qug = wave_shr1(qug, 0.0f);
+                lb = obl;
+                lg = ogl;
+                ubt = wave_shl1_or(obu, qub);
+                ug = wave_shl1_or(ogu, qug);
+                db = db2;
+                dg = dg2;
+                db2 = wave_shl1_or(obd, qdb);
+                dg2 = wave_shl1_or(ogd, qdg);
+                qdb = wave_shr1(qdb, 0.0f);
+                qdg = wave_shr1(qdg, 0.0f);
+            }
+            wave_lds_sync();
+            if (!DOT) write_tile<P, -1>(otile, obase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
+            publish(prog, wave, q * PROG_STRIDE + k + 1);
+        }
+    }
+
+    if (DOT) {
+        dacc = wave_sum(dacc);
+        if (lane == 0) red[wave] = dacc;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float t = 0.0f;
+            for (int w = 0; w < NW; ++w) t += red[w];
+            dot[b] = t;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ host side
+
+constexpr size_t kLdsLimit = 160 * 1024 - 256;
+constexpr int PT = 16;
+
+size_t lds_tangent(int L1, int L2) {
+    const int R = ring_len(L1, L2, 256);
+    return (size_t)NW * (65 * PT + PT * 64 + 64) * sizeof(float) +
+           ((size_t)NW * R + NW * (64 + PT)) * sizeof(float);
+}
+
+size_t lds_dual(bool dot, int P, int L1, int L2) {
+    const int R = ring_len(L1, L2, 128);
+    const int buf = (dot ? 65 * P : 0) + 2 * P * 64 + 128 + (dot ? 0 : 65 * P);
+    return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + P)) * sizeof(float4);
+}
+
+int dual_chunk(bool dot, int L1, int L2) {
+    if (lds_dual(dot, 16, L1, L2) <= kLdsLimit) return 16;
+    if (lds_dual(dot, 8, L1, L2) <= kLdsLimit) return 8;
+    if (lds_dual(dot, 4, L1, L2) <= kLdsLimit) return 4;
+    return 0;
+}
+
+struct Second {
+    Layout prim;
+    float* tan_sk;
+    float* tan_brow;
+    float* value;
+    float* scratch;
+    size_t bytes;
+};
+
+Second second_layout(void* ws, int B, int L1, int L2) {
+    Second w;
+    w.prim = layout(ws, B, L1, L2);
+    char* p = (char*)ws + round256(w.prim.bytes);
+    const size_t ns = ((size_t)L1 + 63) / 64;
+    w.tan_sk = (float*)p;
+    w.tan_brow = w.tan_sk + (size_t)B * ns * stored_steps(L2) * 64;
+    p += round256(table_floats(B, L1, L2) * sizeof(float));
+    w.value = (float*)p;
+    w.scratch = w.value + B;
+    p += round256((size_t)2 * B * sizeof(float));
+    w.bytes = (size_t)(p - (char*)ws);
+    return w;
+}
+
+template <int MODE>
+int launch_tangent(const float* input, const int* lengths, int B, int L1, int L2, float T,
+                   int bw, const Second& w, hipStream_t st) {
+    const int ns = (L1 + 63) / 64;
+    const int R = ring_len(L1, L2, 256);
+    const size_t lds = lds_tangent(L1, L2);
+    D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
+    auto kern = dtw_tangent_kernel<MODE, PT>;
+    D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+    D2P_LAUNCH("dtw_tangent", kern, dim3(B), dim3(NW * 64), lds, st, input, lengths,
+               w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, w.prim.status, L1, L2, ns, T,
+               bw, R);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
+template <int MODE, bool DOT>
+int launch_dual(const float* V, const int* lengths, int B, int L1, int L2, float T, int bw,
+                const Second& w, float* out, float* dot, hipStream_t st) {
+    const int ns = (L1 + 63) / 64;
+    const int R = ring_len(L1, L2, 128);
+    const int P = dual_chunk(DOT, L1, L2);
+    D2P_REQUIRE(P > 0, "sequence too long for the LDS stripe rings");
+    const size_t lds = lds_dual(DOT, P, L1, L2);
+    auto k16 = dtw_dual_kernel<MODE, 16, DOT>;
+    auto k8 = dtw_dual_kernel<MODE, 8, DOT>;
+    auto k4 = dtw_dual_kernel<MODE, 4, DOT>;
+    auto kern = P == 16 ? k16 : (P == 8 ? k8 : k4);
+    D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+    D2P_LAUNCH("dtw_dual", kern, dim3(B), dim3(NW * 64), lds, st, V, lengths, w.prim.alpha_sk,
+               w.prim.brow, w.tan_sk, w.tan_brow, out, dot, w.prim.status, w.prim.trash, L1, L2,
+               ns, T, bw, R);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
+int check(int B, int L1, int L2, float T) {
+    const int rc = dtw::check_shape(B, L1, L2, T);
+    if (rc != D2P_OK) return rc;
+    D2P_REQUIRE(lds_tangent(L1, L2) <= kLdsLimit && dual_chunk(false, L1, L2) > 0,
+                "sequence too long for the LDS stripe rings");
+    return D2P_OK;
+}
+
+}  // namespace dtw2
+}  // namespace d2p_amd
+
+using namespace d2p_amd;
+
+#define D2P_TRY(...)                    \
+    do {                                \
+        const int rc_ = (__VA_ARGS__);  \
+        if (rc_ != D2P_OK) return rc_;  \
+    } while (0)
+
+extern "C" size_t d2p_dtw_second_workspace_bytes(int B, int max_L1, int max_L2) {
+    if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
+    return dtw2::second_layout(nullptr, B, max_L1, max_L2).bytes;
+}
+
+extern "C" int d2p_dtw_hvp(const float* costs, const float* tangent, const int* lengths, int B,
+                           int max_L1, int max_L2, float temperature, int bandwidth, float* hvp,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+    D2P_TRY(dtw2::check(B, max_L1, max_L2, temperature));
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(costs && tangent && lengths && hvp, "null pointer argument");
+    D2P_REQUIRE(workspace && workspace_bytes >= d2p_dtw_second_workspace_bytes(B, max_L1, max_L2),
+                "workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    const dtw2::Second w = dtw2::second_layout(workspace, B, max_L1, max_L2);
+    D2P_TRY(dtw::launch_forward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth, w.prim,
+                                w.value, st));
+    D2P_TRY(dtw2::launch_tangent<dtw2::HVP>(tangent, lengths, B, max_L1, max_L2, temperature,
+                                            bandwidth, w, st));
+    return dtw2::launch_dual<dtw2::HVP, false>(nullptr, lengths, B, max_L1, max_L2, temperature,
+                                               bandwidth, w, hvp, nullptr, st);
+}
+
+extern "C" int d2p_dtw_param_jacobian(const float* costs, const int* lengths, int B, int max_L1,
+                                      int max_L2, float temperature, int bandwidth,
+                                      float* jacobian, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+    D2P_TRY(dtw2::check(B, max_L1, max_L2, temperature));
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(costs && lengths && jacobian, "null pointer argument");
+    D2P_REQUIRE(workspace && workspace_bytes >= d2p_dtw_second_workspace_bytes(B, max_L1, max_L2),
+                "workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    const dtw2::Second w = dtw2::second_layout(workspace, B, max_L1, max_L2);
+    D2P_TRY(dtw::launch_forward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth, w.prim,
+                                w.value, st));
+    D2P_TRY(dtw2::launch_tangent<dtw2::TEMP>(costs, lengths, B, max_L1, max_L2, temperature,
+                                             bandwidth, w, st));
+    return dtw2::launch_dual<dtw2::TEMP, false>(nullptr, lengths, B, max_L1, max_L2, temperature,
+                                                bandwidth, w, jacobian, nullptr, st);
+}
+
+extern "C" int d2p_dtw_backward_full(const float* costs, const float* grad_alignment,
+                                     const int* lengths, int B, int max_L1, int max_L2,
+                                     float temperature, int bandwidth, float* grad_costs,
+                                     float* grad_T, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+    D2P_TRY(dtw2::check(B, max_L1, max_L2, temperature));
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(costs && grad_alignment && lengths && grad_costs && grad_T,
+                "null pointer argument");
+    D2P_REQUIRE(workspace && workspace_bytes >= d2p_dtw_second_workspace_bytes(B, max_L1, max_L2),
+                "workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    const dtw2::Second w = dtw2::second_layout(workspace, B, max_L1, max_L2);
+    D2P_TRY(dtw::launch_forward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth, w.prim,
+                                w.value, st));
+    D2P_TRY(dtw2::launch_tangent<dtw2::HVP>(grad_alignment, lengths, B, max_L1, max_L2,
+                                            temperature, bandwidth, w, st));
+    D2P_TRY(dtw2::launch_dual<dtw2::HVP, false>(nullptr, lengths, B, max_L1, max_L2, temperature,
+                                                bandwidth, w, grad_costs, nullptr, st));
+    D2P_TRY(dtw2::launch_tangent<dtw2::TEMP>(costs, lengths, B, max_L1, max_L2, temperature,
+                                             bandwidth, w, st));
+    return dtw2::launch_dual<dtw2::TEMP, true>(grad_alignment, lengths, B, max_L1, max_L2,
+                                               temperature, bandwidth, w, nullptr, grad_T, st);
+}

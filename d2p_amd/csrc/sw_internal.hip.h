@@ -4,23 +4,12 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
+#include "wavefront.hip.h"
+
 namespace d2p_amd {
 namespace sw {
 
-// Floats of one skewed alpha-like table plus the last rows of every stripe
-// (B * stripes * stored_steps * (64 + 1)).
-size_t table_floats(int B, int max_L1, int max_L2);
-
-// Workspace prefix of every linear-gap entry point: per-element status words, the
-// trash line, then one alpha table with its last rows.
-struct Layout {
-    int* status;
-    float* trash;
-    float* alpha_sk;
-    float* brow;
-    size_t bytes;   // bytes of this prefix
-};
-Layout layout(void* workspace, int B, int max_L1, int max_L2);
+using Layout = wf::Layout;
 
 // Checks shared by the entry points (sizes, LDS budget); D2P_OK or an error code.
 int check_shape(int B, int max_L1, int max_L2, float temperature);

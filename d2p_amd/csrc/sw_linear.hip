@@ -341,22 +341,6 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
 namespace d2p_amd {
 namespace sw {
 
-size_t table_floats(int B, int max_L1, int max_L2) {
-    const size_t ns = ((size_t)max_L1 + 63) / 64;
-    return (size_t)B * ns * (size_t)wf::stored_steps(max_L2) * 65;
-}
-
-Layout layout(void* workspace, int B, int max_L1, int max_L2) {
-    Layout l;
-    l.status = (int*)workspace;
-    l.trash = (float*)((char*)workspace + wf::status_bytes(B));
-    l.alpha_sk = (float*)((char*)l.trash + wf::TRASH_BYTES);
-    const size_t ns = ((size_t)max_L1 + 63) / 64;
-    l.brow = l.alpha_sk + (size_t)B * ns * wf::stored_steps(max_L2) * 64;
-    l.bytes = wf::status_bytes(B) + wf::TRASH_BYTES + table_floats(B, max_L1, max_L2) * sizeof(float);
-    return l;
-}
-
 namespace {
 constexpr size_t kLdsLimit = 160 * 1024 - 256;
 
@@ -444,7 +428,7 @@ using namespace d2p_amd;
 extern "C" size_t d2p_sw_workspace_bytes(int B, int max_L1, int max_L2) {
     if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
     // status words | trash line | skewed alpha table | last row of every stripe
-    return sw::layout(nullptr, B, max_L1, max_L2).bytes;
+    return wf::layout(nullptr, B, max_L1, max_L2).bytes;
 }
 
 extern "C" int d2p_sw_status(const void* workspace, int B, int* status, void* stream) {
@@ -472,7 +456,7 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
     const size_t need = d2p_sw_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
-    const sw::Layout ws = sw::layout(workspace, B, max_L1, max_L2);
+    const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2);
     int r = sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
                                partition, st);
     if (r != D2P_OK) return r;

@@ -487,7 +487,7 @@ int dual_chunk(bool has_v, bool dot, int max_L1, int max_L2) {
 // Workspace after the primal layout: tangent table + last rows, then [B] each of
 // the tangent sweep's dS, the partition, dS/dgap and dS/dT.
 struct Second {
-    sw::Layout prim;
+    Layout prim;
     float* tan_sk;
     float* tan_brow;
     float* sdot;
@@ -499,12 +499,12 @@ struct Second {
 
 Second second_layout(void* ws, int B, int L1, int L2) {
     Second w;
-    w.prim = sw::layout(ws, B, L1, L2);
+    w.prim = layout(ws, B, L1, L2);
     char* p = (char*)ws + round256(w.prim.bytes);
     const size_t ns = ((size_t)L1 + 63) / 64;
     w.tan_sk = (float*)p;
     w.tan_brow = w.tan_sk + (size_t)B * ns * stored_steps(L2) * 64;
-    p += round256(sw::table_floats(B, L1, L2) * sizeof(float));
+    p += round256(table_floats(B, L1, L2) * sizeof(float));
     w.sdot = (float*)p;
     w.part = w.sdot + B;
     w.dgap = w.part + B;

@@ -553,8 +553,27 @@ DtwOut dtw_run(const Tensor& costs, const Tensor& lengths, const Dims& d, float 
     return o;
 }
 
+Tensor dtw_second_workspace(const Dims& d, const Tensor& like) {
+    return workspace(d2p_dtw_second_workspace_bytes(d.B, d.L1, d.L2), like);
+}
+
+// (grad_costs = H . ga, per-element <ga, dP/dT>)
+std::tuple<Tensor, Tensor> dtw_backward_full_run(const Tensor& costs, const Tensor& ga,
+                                                 const Tensor& lengths, const Dims& d, float T,
+                                                 int bw) {
+    Tensor gc = torch::empty({d.B, d.L1, d.L2}, costs.options());
+    Tensor gt = torch::empty({d.B}, costs.options());
+    Tensor ws = dtw_second_workspace(d, costs);
+    D2P_CALL(d2p_dtw_backward_full(costs.data_ptr<float>(), ga.data_ptr<float>(),
+                                   lengths.data_ptr<int>(), d.B, d.L1, d.L2, T, bw,
+                                   gc.data_ptr<float>(), gt.data_ptr<float>(), ws.data_ptr(),
+                                   ws.numel(), current_stream()));
+    return {gc, gt};
+}
+
 // Autograd semantics of SoftDTWCUDAFunction (/root/reference/src/dtw/torch_cuda.cpp:139-325):
-// inputs (costs, temperature, lengths, bandwidth), outputs {value, marginals}.
+// inputs (costs, temperature, lengths, bandwidth), outputs {value, marginals}; the
+// marginal path adds the HVP against the marginal cotangent and <cotangent, dP/dT>.
 class SoftDTWFunction : public torch::autograd::Function<SoftDTWFunction> {
    public:
     static tensor_list forward(AutogradContext* ctx, Tensor costs, Tensor temperature,
@@ -568,12 +587,14 @@ class SoftDTWFunction : public torch::autograd::Function<SoftDTWFunction> {
         Tensor l = resolve_lengths(lengths, d, costs.device(), "costs");
         const float T = scalar_value(temperature, "temperature");
         DtwOut o = dtw_run(costs, l, d, T, bw);
-        ctx->save_for_backward({o.marginals, o.grad_T});
+        ctx->save_for_backward({costs, l, o.marginals, o.grad_T});
+        ctx->saved_data["temperature"] = (double)T;
+        ctx->saved_data["bandwidth"] = (int64_t)bw;
         return {o.value, o.marginals};
     }
     static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
         auto saved = ctx->get_saved_variables();
-        Tensor marg = saved[0], gT = saved[1];
+        Tensor costs = saved[0], lengths = saved[1], marg = saved[2], gT = saved[3];
         c10::hip::HIPGuardMasqueradingAsCUDA guard(marg.device());
         Tensor grad_value = grads[0], grad_marg = grads[1];
         Tensor gc, gt;
@@ -581,8 +602,18 @@ class SoftDTWFunction : public torch::autograd::Function<SoftDTWFunction> {
             gc = scale_by_batch(marg, grad_value);
             if (ctx->needs_input_grad(1)) gt = grad_param_sum(grad_value, gT);
         }
-        if (grad_marg.defined() && grad_marg.numel() > 0)
-            not_yet("soft_dtw marginal-path backward");
+        if (grad_marg.defined() && grad_marg.numel() > 0) {
+            Tensor gm = prepare_cotangent(grad_marg, costs, "grad_posteriors");
+            Dims d = checked_dims_dtw(costs);
+            auto r = dtw_backward_full_run(costs, gm, lengths, d,
+                                           (float)ctx->saved_data["temperature"].toDouble(),
+                                           (int)ctx->saved_data["bandwidth"].toInt());
+            gc = gc.defined() ? gc + std::get<0>(r) : std::get<0>(r);
+            if (ctx->needs_input_grad(1)) {
+                Tensor t = std::get<1>(r).sum().reshape({1});
+                gt = gt.defined() ? gt + t : t;
+            }
+        }
         return {gc, gt, Tensor(), Tensor()};
     }
 };
@@ -613,15 +644,58 @@ std::tuple<Tensor, Tensor, Tensor> dtw_with_grads(Tensor costs, double temperatu
     return {o.value, o.marginals, o.grad_T};
 }
 
-Tensor dtw_hvp(Tensor, Tensor, double, c10::optional<Tensor>, c10::optional<int64_t>) {
-    not_yet("soft_dtw_hvp");
+Tensor dtw_hvp(Tensor costs, Tensor tangent, double temperature, c10::optional<Tensor> lengths,
+               c10::optional<int64_t> bandwidth) {
+    CHECK_INPUT_DEV(costs);
+    CHECK_INPUT_DEV(tangent);
+    TORCH_CHECK(tangent.sizes() == costs.sizes(), "tangent must have same shape as costs");
+    TORCH_CHECK(tangent.device() == costs.device(), "tangent must be on same device as costs, got ",
+                tangent.device(), " vs ", costs.device());
+    Dims d = checked_dims_dtw(costs);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(costs.device());
+    Tensor l = resolve_lengths(lengths, d, costs.device(), "costs");
+    const int bw = checked_bandwidth(bandwidth.has_value() ? *bandwidth : -1);
+    Tensor out = torch::empty({d.B, d.L1, d.L2}, costs.options());
+    Tensor ws = dtw_second_workspace(d, costs);
+    D2P_CALL(d2p_dtw_hvp(costs.data_ptr<float>(), tangent.data_ptr<float>(), l.data_ptr<int>(),
+                         d.B, d.L1, d.L2, (float)temperature, bw, out.data_ptr<float>(),
+                         ws.data_ptr(), ws.numel(), current_stream()));
+    return out;
 }
-Tensor dtw_param_jacobian(Tensor, double, c10::optional<Tensor>, c10::optional<int64_t>) {
-    not_yet("soft_dtw_param_jacobian");
+
+Tensor dtw_param_jacobian(Tensor costs, double temperature, c10::optional<Tensor> lengths,
+                          c10::optional<int64_t> bandwidth) {
+    CHECK_INPUT_DEV(costs);
+    Dims d = checked_dims_dtw(costs);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(costs.device());
+    Tensor l = resolve_lengths(lengths, d, costs.device(), "costs");
+    const int bw = checked_bandwidth(bandwidth.has_value() ? *bandwidth : -1);
+    Tensor out = torch::empty({d.B, d.L1, d.L2}, costs.options());
+    Tensor ws = dtw_second_workspace(d, costs);
+    D2P_CALL(d2p_dtw_param_jacobian(costs.data_ptr<float>(), l.data_ptr<int>(), d.B, d.L1, d.L2,
+                                    (float)temperature, bw, out.data_ptr<float>(), ws.data_ptr(),
+                                    ws.numel(), current_stream()));
+    return out;
 }
-std::tuple<Tensor, Tensor> dtw_backward_full(Tensor, Tensor, double, c10::optional<Tensor>,
-                                             c10::optional<int64_t>) {
-    not_yet("soft_dtw_backward_full");
+
+std::tuple<Tensor, Tensor> dtw_backward_full(Tensor costs, Tensor grad_alignment,
+                                             double temperature, c10::optional<Tensor> lengths,
+                                             c10::optional<int64_t> bandwidth) {
+    CHECK_INPUT_DEV(costs);
+    TORCH_CHECK(grad_alignment.sizes() == costs.sizes(),
+                "grad_alignment must have same shape as costs");
+    TORCH_CHECK(grad_alignment.is_cuda(), "grad_alignment must be a CUDA tensor");
+    TORCH_CHECK(grad_alignment.device() == costs.device(),
+                "grad_alignment must be on same device as costs, got ", grad_alignment.device(),
+                " vs ", costs.device());
+    Dims d = checked_dims_dtw(costs);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(costs.device());
+    Tensor l = resolve_lengths(lengths, d, costs.device(), "costs");
+    const int bw = checked_bandwidth(bandwidth.has_value() ? *bandwidth : -1);
+    Tensor ga = grad_alignment.contiguous();
+    if (ga.scalar_type() != torch::kFloat32) ga = ga.to(torch::kFloat32);
+    auto r = dtw_backward_full_run(costs, ga, l, d, (float)temperature, bw);
+    return {std::get<0>(r), std::get<1>(r).sum().reshape({1})};
 }
 
 [[noreturn]] void cpu_unsupported() {

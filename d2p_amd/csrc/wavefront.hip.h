@@ -67,6 +67,34 @@ __host__ __device__ inline int stored_steps(int L2max) {
 __host__ inline size_t status_bytes(int B) { return ((size_t)B * sizeof(int) + 255) / 256 * 256; }
 __host__ inline size_t round256(size_t n) { return (n + 255) / 256 * 256; }
 
+// Floats of `planes` skewed tables plus the last rows of every stripe per plane
+// (B * stripes * planes * stored_steps * (64 + 1)).
+__host__ inline size_t table_floats(int B, int max_L1, int max_L2, int planes = 1) {
+    const size_t ns = ((size_t)max_L1 + 63) / 64;
+    return (size_t)B * ns * planes * (size_t)stored_steps(max_L2) * 65;
+}
+
+// Workspace prefix of every entry point: per-element status words, the trash line,
+// then the primal table(s) with their last rows.
+struct Layout {
+    int* status;
+    float* trash;
+    float* alpha_sk;   // [B][stripe][plane][step][64]
+    float* brow;       // [B][stripe][plane][step]
+    size_t bytes;      // bytes of this prefix
+};
+
+__host__ inline Layout layout(void* workspace, int B, int max_L1, int max_L2, int planes = 1) {
+    Layout l;
+    l.status = (int*)workspace;
+    l.trash = (float*)((char*)workspace + status_bytes(B));
+    l.alpha_sk = (float*)((char*)l.trash + TRASH_BYTES);
+    const size_t ns = ((size_t)max_L1 + 63) / 64;
+    l.brow = l.alpha_sk + (size_t)B * ns * planes * stored_steps(max_L2) * 64;
+    l.bytes = status_bytes(B) + TRASH_BYTES + table_floats(B, max_L1, max_L2, planes) * sizeof(float);
+    return l;
+}
+
 // ---------------------------------------------------------------- progress flags
 
 // Progress flags live in LDS.  The writer completes its LDS writes (ring data)

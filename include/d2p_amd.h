@@ -145,6 +145,32 @@ int d2p_dtw_forward_marginals(const float* costs, const int* lengths, int B, int
                               float* marginals, float* grad_T, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* Workspace bytes of the second-order DTW entry points below. */
+size_t d2p_dtw_second_workspace_bytes(int B, int max_L1, int max_L2);
+
+/* Hessian-vector product of the soft-DTW value: hvp = (d^2 value / dcosts^2) . tangent.
+ * Replaces dtw_hvp (/root/reference/src/dtw/kernels.cuh:131-151) as sequenced by
+ * soft_dtw_hvp_cuda (/root/reference/src/dtw/torch_cuda.cpp:420-482). */
+int d2p_dtw_hvp(const float* costs, const float* tangent, const int* lengths, int B, int max_L1,
+                int max_L2, float temperature, int bandwidth, float* hvp, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/* Jacobian of the alignment marginals with respect to temperature.
+ * Replaces dtw_param_grad (/root/reference/src/dtw/kernels.cuh:153-174) as sequenced by
+ * soft_dtw_param_jacobian_cuda (/root/reference/src/dtw/torch_cuda.cpp:484-540). */
+int d2p_dtw_param_jacobian(const float* costs, const int* lengths, int B, int max_L1,
+                           int max_L2, float temperature, int bandwidth, float* jacobian,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* Backward of the marginals output for a cotangent grad_alignment:
+ * grad_costs = H . grad_alignment and grad_T[b] = <grad_alignment[b], dP_b/dT> (per element;
+ * soft_dtw_backward_full_cuda, /root/reference/src/dtw/torch_cuda.cpp:542-640, returns the
+ * batch sum). */
+int d2p_dtw_backward_full(const float* costs, const float* grad_alignment, const int* lengths,
+                          int B, int max_L1, int max_L2, float temperature, int bandwidth,
+                          float* grad_costs, float* grad_T, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Shared helpers
  * ------------------------------------------------------------------------- */

@@ -31,6 +31,10 @@ SIGNATURES = {
     "d2p_sw_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _p, _p, _z, _p]),
     "d2p_sw_param_jacobian": (_i, [_p, _i, _p, _i, _i, _i, _f, _f, _p, _p, _z, _p]),
     "d2p_sw_backward_full": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _p, _p, _p, _p, _z, _p]),
+    "d2p_dtw_second_workspace_bytes": (_z, [_i, _i, _i]),
+    "d2p_dtw_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _i, _p, _p, _z, _p]),
+    "d2p_dtw_param_jacobian": (_i, [_p, _p, _i, _i, _i, _f, _i, _p, _p, _z, _p]),
+    "d2p_dtw_backward_full": (_i, [_p, _p, _p, _i, _i, _i, _f, _i, _p, _p, _p, _z, _p]),
     "d2p_profile_enable": (_i, [_i]),
     "d2p_profile_report": (_i, [ctypes.c_char_p, _z]),
     "d2p_profile_reset": (None, []),
@@ -183,6 +187,49 @@ def sw_backward_full(scores, grad_alignment, lengths, gap, T):
                                      stream()))
     _check_status(ws, B)
     return gs, gg, gt
+
+
+def dtw_hvp(costs, V, lengths, T, bw=-1):
+    import torch
+    B, L1, L2 = costs.shape
+    dev = costs.device
+    lengths = _lengths(lengths, B, L1, L2, dev)
+    out = torch.empty(B, L1, L2, device=dev)
+    nbytes = lib().d2p_dtw_second_workspace_bytes(B, L1, L2)
+    ws = _workspace(nbytes, dev)
+    check(lib().d2p_dtw_hvp(ptr(costs), ptr(V), ptr(lengths), B, L1, L2, T, bw, ptr(out),
+                            ptr(ws), nbytes, stream()))
+    _check_status(ws, B)
+    return out
+
+
+def dtw_param_jacobian(costs, lengths, T, bw=-1):
+    import torch
+    B, L1, L2 = costs.shape
+    dev = costs.device
+    lengths = _lengths(lengths, B, L1, L2, dev)
+    out = torch.empty(B, L1, L2, device=dev)
+    nbytes = lib().d2p_dtw_second_workspace_bytes(B, L1, L2)
+    ws = _workspace(nbytes, dev)
+    check(lib().d2p_dtw_param_jacobian(ptr(costs), ptr(lengths), B, L1, L2, T, bw, ptr(out),
+                                       ptr(ws), nbytes, stream()))
+    _check_status(ws, B)
+    return out
+
+
+def dtw_backward_full(costs, ga, lengths, T, bw=-1):
+    import torch
+    B, L1, L2 = costs.shape
+    dev = costs.device
+    lengths = _lengths(lengths, B, L1, L2, dev)
+    gc = torch.empty(B, L1, L2, device=dev)
+    gt = torch.empty(B, device=dev)
+    nbytes = lib().d2p_dtw_second_workspace_bytes(B, L1, L2)
+    ws = _workspace(nbytes, dev)
+    check(lib().d2p_dtw_backward_full(ptr(costs), ptr(ga), ptr(lengths), B, L1, L2, T, bw,
+                                      ptr(gc), ptr(gt), ptr(ws), nbytes, stream()))
+    _check_status(ws, B)
+    return gc, gt
 
 
 def scale_by_batch(src, g):
