@@ -25,6 +25,7 @@
 #include "wavefront.hip.h"
 #include "../../include/d2p_amd.h"
 #include "capi_util.hip.h"
+#include "swa_internal.hip.h"
 
 namespace d2p_amd {
 namespace swa {
@@ -449,20 +450,77 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
 }  // namespace swa
 }  // namespace d2p_amd
 
-using namespace d2p_amd;
+namespace d2p_amd {
+namespace swa {
 
 namespace {
-size_t swa_table_floats(int B, int max_L1, int max_L2) {
-    const size_t ns = ((size_t)max_L1 + 63) / 64;
-    return (size_t)B * ns * 3 * (size_t)wf::stored_steps(max_L2);   // per lane-row of 64
+constexpr size_t kLdsLimit = 160 * 1024 - 256;
+
+size_t lds_forward(int max_L1, int max_L2) {
+    const int R = ring_len(max_L1, max_L2, 256);
+    return (size_t)NW * 2 * 65 * PF * sizeof(float) + ((size_t)NW * R + NW * DUMMY) * sizeof(float4);
+}
+
+size_t lds_backward(int max_L1, int max_L2) {
+    const int R = ring_len(max_L1, max_L2, 128);
+    const size_t wfloats = 65 * PB + 3 * PB * 64 + 3 * 64 + 65 * PB;
+    return (size_t)NW * wfloats * sizeof(float) +
+           (size_t)NW * R * (sizeof(float4) + sizeof(float)) +
+           (size_t)NW * (64 + PB) * (sizeof(float4) + sizeof(float));
 }
 }  // namespace
 
+int check_shape(int B, int max_L1, int max_L2, float temperature) {
+    D2P_REQUIRE(B >= 0 && max_L1 >= 0 && max_L2 >= 0, "negative dimension");
+    D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
+    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 4, "max_L2 too large");
+    D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
+    D2P_REQUIRE(lds_forward(max_L1, max_L2) <= kLdsLimit &&
+                    lds_backward(max_L1, max_L2) <= kLdsLimit,
+                "sequence too long for the LDS stripe rings");
+    return D2P_OK;
+}
+
+int launch_forward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
+                   float go, float ge, float T, const Layout& ws, float* partition,
+                   hipStream_t st) {
+    const int ns = (max_L1 + 63) / 64;
+    const int R = ring_len(max_L1, max_L2, 256);
+    const size_t lds = lds_forward(max_L1, max_L2);
+    D2P_HIP(hipFuncSetAttribute((const void*)swa_forward_kernel,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    D2P_LAUNCH("swa_forward", swa_forward_kernel, dim3(B), dim3(NW * 64), lds, st, scores,
+               lengths, ws.alpha_sk, ws.brow, partition, ws.status, max_L1, max_L2, ns, go, ge, T,
+               R);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
+int launch_backward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
+                    float go, float ge, float T, const Layout& ws, const float* partition,
+                    float* marginals, float* grad_open, float* grad_ext, float* grad_T,
+                    hipStream_t st) {
+    const int ns = (max_L1 + 63) / 64;
+    const int R = ring_len(max_L1, max_L2, 128);
+    const size_t lds = lds_backward(max_L1, max_L2);
+    D2P_HIP(hipFuncSetAttribute((const void*)swa_backward_kernel,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    D2P_LAUNCH("swa_backward", swa_backward_kernel, dim3(B), dim3(NW * 64), lds, st, scores,
+               lengths, ws.alpha_sk, ws.brow, partition, marginals, grad_open, grad_ext, grad_T,
+               ws.status, ws.trash, max_L1, max_L2, ns, go, ge, T, R);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
+}  // namespace swa
+}  // namespace d2p_amd
+
+using namespace d2p_amd;
+
 extern "C" size_t d2p_swa_workspace_bytes(int B, int max_L1, int max_L2) {
     if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
-    // status words | trash line | skewed (M, I, D) tables | last row of every stripe
-    return wf::status_bytes(B) + wf::TRASH_BYTES +
-           swa_table_floats(B, max_L1, max_L2) * 65 * sizeof(float);
+    // status words | trash line | skewed (M, I, D) tables | last rows of every stripe
+    return wf::layout(nullptr, B, max_L1, max_L2, 3).bytes;
 }
 
 extern "C" int d2p_swa_forward_marginals(const float* scores, const int* lengths, int B,
@@ -470,42 +528,19 @@ extern "C" int d2p_swa_forward_marginals(const float* scores, const int* lengths
                                          float temperature, float* partition, float* marginals,
                                          float* grad_open, float* grad_ext, float* grad_T,
                                          void* workspace, size_t workspace_bytes, void* stream) {
-    D2P_REQUIRE(B >= 0 && max_L1 >= 0 && max_L2 >= 0, "negative dimension");
-    D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
+    const int rc = swa::check_shape(B, max_L1, max_L2, temperature);
+    if (rc != D2P_OK) return rc;
     if (B == 0) return D2P_OK;
     D2P_REQUIRE(scores && lengths && partition && marginals && grad_open && grad_ext && grad_T,
                 "null pointer argument");
     const size_t need = d2p_swa_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
-    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * swa::PB, "max_L2 too large");
-    D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
     hipStream_t st = (hipStream_t)stream;
-    const int ns = (max_L1 + 63) / 64;
-    const int Rf = wf::ring_len(max_L1, max_L2, 256);
-    const int Rb = wf::ring_len(max_L1, max_L2, 128);
-    const size_t lds_f = (size_t)wf::NW * 2 * 65 * swa::PF * sizeof(float) +
-                         ((size_t)wf::NW * Rf + wf::NW * swa::DUMMY) * sizeof(float4);
-    const size_t wfloats = 65 * swa::PB + 3 * swa::PB * 64 + 3 * 64 + 65 * swa::PB;
-    const size_t lds_b = (size_t)wf::NW * wfloats * sizeof(float) +
-                         (size_t)wf::NW * Rb * (sizeof(float4) + sizeof(float)) +
-                         (size_t)wf::NW * (64 + swa::PB) * (sizeof(float4) + sizeof(float));
-    D2P_REQUIRE(lds_f <= 160 * 1024 - 256 && lds_b <= 160 * 1024 - 256,
-                "sequence too long for the LDS stripe rings (max_L2 with more than 512 rows)");
-    D2P_HIP(hipFuncSetAttribute((const void*)swa::swa_forward_kernel,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_f));
-    D2P_HIP(hipFuncSetAttribute((const void*)swa::swa_backward_kernel,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_b));
-    int* status = (int*)workspace;
-    float* trash = (float*)((char*)workspace + wf::status_bytes(B));
-    float* alpha_sk = (float*)((char*)trash + wf::TRASH_BYTES);
-    float* brow = alpha_sk + swa_table_floats(B, max_L1, max_L2) * 64;
-    D2P_LAUNCH("swa_forward", swa::swa_forward_kernel, dim3(B), dim3(wf::NW * 64), lds_f, st,
-               scores, lengths, alpha_sk, brow, partition, status, max_L1, max_L2, ns, gap_open,
-               gap_ext, temperature, Rf);
-    D2P_HIP(hipGetLastError());
-    D2P_LAUNCH("swa_backward", swa::swa_backward_kernel, dim3(B), dim3(wf::NW * 64), lds_b, st,
-               scores, lengths, alpha_sk, brow, partition, marginals, grad_open, grad_ext, grad_T,
-               status, trash, max_L1, max_L2, ns, gap_open, gap_ext, temperature, Rb);
-    D2P_HIP(hipGetLastError());
-    return D2P_OK;
+    const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 3);
+    const int r = swa::launch_forward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
+                                      temperature, ws, partition, st);
+    if (r != D2P_OK) return r;
+    return swa::launch_backward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
+                                temperature, ws, partition, marginals, grad_open, grad_ext,
+                                grad_T, st);
 }
