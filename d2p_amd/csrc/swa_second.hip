@@ -1,0 +1,819 @@
+// swa_second.hip -- second-order quantities of affine-gap soft Smith-Waterman on
+// gfx950: Hessian-vector products and Jacobians of the marginals with respect to
+// gap_open, gap_ext and temperature.
+//
+// Reference behaviour restated (not translated):
+//   HVP          /root/reference/src/sw_affine/kernels_cpu.cpp:362-631
+//   param grad   /root/reference/src/sw_affine/kernels_cpu.cpp:643-921 (0 open, 1 ext, 2 T)
+// Each of the three states X in {M, I, D} has softmax weights over its candidates:
+//   M: (M, I, D)[i-1,j-1] + s and s;  I: M[i-1,j] + open, I[i-1,j] + ext;
+//   D: M[i,j-1] + open, D[i,j-1] + ext  (no weights when every candidate is NINF).
+// The tangent sweep gives x_X = sum_k w_k d_k (+ (X - E_w[v]) / T for the
+// temperature) with d the candidates' tangents:
+//   HVP  d_M = (x_M + V, x_I + V, x_D + V, V) at the diagonal, d_I, d_D plain;
+//   open / ext: +1 on the open / extend candidates of I and D.
+// The reverse sweep carries beta and a second channel g per state, with
+//   g_pred += g w_k + beta dw_k,  dw_k = w_k (d_k - E_w[d]) / T
+//   (+ w_k (E_w[v] - v_k) / T^2 for the temperature),
+// started from beta_init (x - dS) / T (HVP: first in the accumulation; param: last,
+// with - beta_init (X - S) / T^2 for the temperature).  Output per cell: HVP
+// g_M (sum w_M) + beta_M (sum dw_M); param g_M.
+//
+// Mapping: the stripe pipeline of wavefront.hip.h.  The tangent sweep carries the
+// (x_M, x_I, x_D) triple across stripes in a float4 ring; the reverse sweep sends
+// (beta, g) flows upward in three rings: up flows to (M, I), diagonal flows to
+// (M, I) and to D.  Only the edge lane writes these rings (exec-masked stores), so
+// they need no per-lane sinks.
+
+#include <vector>
+
+#include "wavefront.hip.h"
+#include "../../include/d2p_amd.h"
+#include "capi_util.hip.h"
+#include "swa_internal.hip.h"
+
+namespace d2p_amd {
+namespace swa2 {
+
+using namespace wf;
+
+enum Mode { HVP = 0, OPEN = 1, EXT = 2, TEMP = 3 };
+
+// ------------------------------------------------------------------ tangent sweep
+
+template <int MODE, int P>
+__global__ void __launch_bounds__(NW * 64)
+swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
+                   const int* __restrict__ lengths, const float* __restrict__ alpha_sk,
+                   const float* __restrict__ brow, const float* __restrict__ partition,
+                   float* __restrict__ tan_sk, float* __restrict__ tan_brow,
+                   float* __restrict__ sdot, int* __restrict__ status, int L1max, int L2max,
+                   int NSmax, float go, float ge, float T, int R) {
+    constexpr bool HAS_V = MODE == HVP;
+    using Tile = ChunkTile<P>;
+    constexpr int VT = Tile::FLOATS;
+    constexpr int AR = VT + (HAS_V ? Tile::FLOATS : 0);   // 3 planes x P alpha rows
+    constexpr int RR = AR + 3 * P * 64;                   // 3 planes x row above
+    constexpr int BUF = RR + 3 * 64;
+    constexpr int SINK = 64 + P;
+    extern __shared__ float smem[];
+    __shared__ int prog[NW];
+    __shared__ float red[NW];
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const unsigned ul4 = (unsigned)lane * 4u;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float* buf = smem + wave * BUF;
+    float4* rings = reinterpret_cast<float4*>(smem + NW * BUF);
+    float4* sink = rings + NW * R + wave * SINK;
+    int* st = status + b;
+    const int tbase = Tile::read_base(lane);
+
+    if (lane == 0) prog[wave] = -1;
+    __syncthreads();
+
+    const int L1 = min(max(lengths[2 * b], 0), L1max);
+    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const float c = kLog2e / T;
+    const float rT = 1.0f / T;
+    const float S = partition[b];
+    const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
+    const int nsteps = L2 + 63;
+    const int nch = (nsteps + P - 1) / P;
+    const size_t NT = (size_t)stored_steps(L2max);
+    const size_t PL = NT * 64;
+    const float* sbase = scores + (size_t)b * L1max * L2max;
+    const float* vbase = HAS_V ? V + (size_t)b * L1max * L2max : nullptr;
+    const uint32_t in_lds = lds_address(buf);
+    float sacc = 0.0f;
+
+    for (int s = wave; s < NS; s += NW) {
+        const int i0 = s * 64;
+        const int L2eff = (i0 + lane < L1) ? L2 : 0;
+        const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * 3 * PL;
+        const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * 3 * NT;
+        float* tout = tan_sk + ((size_t)b * NSmax + s) * 3 * PL + APAD * 64;
+        float* tb_s = tan_brow + ((size_t)b * NSmax + s) * 3 * NT;
+        const float4* ring_in = ring_from(rings, s, R);
+        float4* ring_out = ring_of(rings, s, R);
+
+        auto issue_chunk = [&](int k) {
+            const int t0 = k * P;
+            dma_tile<P, 1>(in_lds, sbase, i0, L1max, L2max, lane, t0);
+            if (HAS_V) dma_tile<P, 1>(in_lds + VT * 4, vbase, i0, L1max, L2max, lane, t0);
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl)
+                dma_rows<P, 1>(in_lds + (AR + pl * P * 64) * 4, astripe + pl * PL, t0, ul4);
+            const uint32_t roff = (uint32_t)min(t0 + 62 + min(lane, P), nsteps - 1) * 4u;
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) {
+                uint32_t o = roff, l = in_lds + (RR + pl * 64) * 4;
+                lds_dma_dword<0>(bup + pl * NT, o, l, 0u);
+            }
+        };
+
+#pragma unroll
+        for (int t = -APAD; t < 0; ++t)
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) lane_store(tout + pl * PL + t * 64, ul4, 0.0f);
+        wave_lds_sync();
+        issue_chunk(0);
+        float AM[P + 2], AI[P + 2], AD[P + 2];
+        AM[P] = AM[P + 1] = AI[P] = AI[P + 1] = AD[P] = AD[P + 1] = kNINF;
+        float cM = 0.0f, cI = 0.0f, cD = 0.0f;      // tangents at the previous step
+        float pM = 0.0f, pI = 0.0f, pD = 0.0f;      // their up values
+
+        for (int k = 0; k < nch; ++k) {
+            const int t0 = k * P;
+            chunk_waits<P>(prog, s, NS, k, nch, R, st);
+            // this chunk's loads, followed by the 3P + 3 stores of the previous chunk
+            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<3 * P>();
+            float sv[P], vv[P];
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                sv[u] = buf[tbase + u];
+                vv[u] = HAS_V ? buf[VT + tbase + u] : 0.0f;
+            }
+            AM[0] = AM[P]; AM[1] = AM[P + 1];
+            AI[0] = AI[P]; AI[1] = AI[P + 1];
+            AD[0] = AD[P]; AD[1] = AD[P + 1];
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                AM[j + 2] = buf[AR + j * 64 + lane];
+                AI[j + 2] = buf[AR + P * 64 + j * 64 + lane];
+                AD[j + 2] = buf[AR + 2 * P * 64 + j * 64 + lane];
+            }
+            const bool row_ok = s > 0 && lane <= P && t0 + 62 + lane <= nsteps - 1;
+            float bM = row_ok ? buf[RR + lane] : kNINF;
+            float bI = row_ok ? buf[RR + 64 + lane] : kNINF;
+            float bD = row_ok ? buf[RR + 128 + lane] : kNINF;
+            float rM = 0.0f, rI = 0.0f, rD = 0.0f;
+            if (s > 0 && lane < P) {
+                const float4 r = ring_in[ring_index(t0 + lane + 63, R)];
+                rM = r.x;
+                rI = r.y;
+                rD = r.z;
+            }
+            wave_lds_sync();
+            if (k + 1 < nch) issue_chunk(k + 1);
+            float4* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
+            float* toutc = tout + (size_t)t0 * 64;
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                const int t = t0 + u;
+                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
+                const float sc = ok ? sv[u] : kNINF;
+                const float vd = ok ? vv[u] : 0.0f;
+                // primal predecessors
+                const float dM = wave_shr1_or(AM[u], bM), dI = wave_shr1_or(AI[u], bI),
+                            dD = wave_shr1_or(AD[u], bD);
+                const float nbM = wave_shl1(bM, kNINF), nbI = wave_shl1(bI, kNINF),
+                            nbD = wave_shl1(bD, kNINF);
+                const float uM = wave_shr1_or(AM[u + 1], nbM), uI = wave_shr1_or(AI[u + 1], nbI);
+                bM = nbM;
+                bI = nbI;
+                bD = nbD;
+                const float lM = AM[u + 1], lD = AD[u + 1];
+                // tangent predecessors
+                const float tuM = wave_shr1_or(cM, rM), tuI = wave_shr1_or(cI, rI),
+                            tuD = wave_shr1_or(cD, rD);
+                rM = wave_shl1(rM, 0.0f);
+                rI = wave_shl1(rI, 0.0f);
+                rD = wave_shl1(rD, 0.0f);
+                const float tdM = pM, tdI = pI, tdD = pD;
+                pM = tuM;
+                pI = tuI;
+                pD = tuD;
+                // M
+                const float v0 = dM + sc, v1 = dI + sc, v2 = dD + sc;
+                const float m4 = fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
+                const float e0 = fast_exp2((v0 - m4) * c), e1 = fast_exp2((v1 - m4) * c);
+                const float e2 = fast_exp2((v2 - m4) * c), e3 = fast_exp2((sc - m4) * c);
+                const float r4 = fast_rcp(((e0 + e1) + e2) + e3);
+                // I
+                const float i0v = uM + go, i1v = uI + ge;
+                const float mi = fmaxf(i0v, i1v);
+                const float f0 = fast_exp2((i0v - mi) * c), f1 = fast_exp2((i1v - mi) * c);
+                const float ri = mi > kNINF ? fast_rcp(f0 + f1) : 0.0f;
+                // D
+                const float d0v = lM + go, d1v = lD + ge;
+                const float md = fmaxf(d0v, d1v);
+                const float g0 = fast_exp2((d0v - md) * c), g1 = fast_exp2((d1v - md) * c);
+                const float rd = md > kNINF ? fast_rcp(g0 + g1) : 0.0f;
+                float xM, xI, xD;
+                if (MODE == HVP) {
+                    xM = (((e0 * (tdM + vd) + e1 * (tdI + vd)) + e2 * (tdD + vd)) + e3 * vd) * r4;
+                    xI = (f0 * tuM + f1 * tuI) * ri;
+                    xD = (g0 * cM + g1 * cD) * rd;
+                } else {
+                    const float ao = MODE == OPEN ? 1.0f : 0.0f, ae = MODE == EXT ? 1.0f : 0.0f;
+                    xM = ((e0 * tdM + e1 * tdI) + e2 * tdD) * r4;
+                    xI = (f0 * (tuM + ao) + f1 * (tuI + ae)) * ri;
+                    xD = (g0 * (cM + ao) + g1 * (cD + ae)) * rd;
+                    if (MODE == TEMP) {
+                        const float E4 = (((e0 * v0 + e1 * v1) + e2 * v2) + e3 * sc) * r4;
+                        const float E2i = (f0 * i0v + f1 * i1v) * ri;
+                        const float E2d = (g0 * d0v + g1 * d1v) * rd;
+                        xM += (AM[u + 2] - E4) * rT;
+                        xI += ri > 0.0f ? (AI[u + 2] - E2i) * rT : 0.0f;
+                        xD += rd > 0.0f ? (AD[u + 2] - E2d) * rT : 0.0f;
+                    }
+                }
+                cM = ok ? xM : 0.0f;
+                cI = ok ? xI : 0.0f;
+                cD = ok ? xD : 0.0f;
+                lane_store(toutc + u * 64, ul4, cM);
+                lane_store(toutc + PL + u * 64, ul4, cI);
+                lane_store(toutc + 2 * PL + u * 64, ul4, cD);
+                pub[u] = make_float4(cM, cI, cD, 0.0f);
+                if (MODE == HVP) {
+                    float lp;
+                    lp = (AM[u + 2] - S) * c;
+                    sacc += fast_exp2(lp < 0.0f ? lp : 0.0f) * cM;
+                    lp = (AI[u + 2] - S) * c;
+                    sacc += fast_exp2(lp < 0.0f ? lp : 0.0f) * cI;
+                    lp = (AD[u + 2] - S) * c;
+                    sacc += fast_exp2(lp < 0.0f ? lp : 0.0f) * cD;
+                }
+            }
+            wave_lds_sync();
+            if (lane < P) {
+                const float4 r = ring_out[t0 % R + lane];
+                const unsigned o = (unsigned)(t0 + lane) * 4u;
+                lane_store(tb_s, o, r.x);
+                lane_store(tb_s + NT, o, r.y);
+                lane_store(tb_s + 2 * NT, o, r.z);
+            }
+            publish(prog, wave, s * PROG_STRIDE + k + 1);
+        }
+    }
+
+    if (MODE == HVP) {
+        sacc = wave_sum(sacc);
+        if (lane == 0) red[wave] = sacc;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float t = 0.0f;
+            for (int w = 0; w < NW; ++w) t += red[w];
+            sdot[b] = t;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ reverse sweep
+
+template <int MODE, int P, bool DOT>
+__global__ void __launch_bounds__(NW * 64)
+swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
+                const int* __restrict__ lengths, const float* __restrict__ alpha_sk,
+                const float* __restrict__ brow, const float* __restrict__ tan_sk,
+                const float* __restrict__ tan_brow, const float* __restrict__ partition,
+                const float* __restrict__ dS, float* __restrict__ out, float* __restrict__ dot,
+                int* __restrict__ status, float* __restrict__ trash, int L1max, int L2max,
+                int NSmax, float go, float ge, float T, int R) {
+    constexpr bool HAS_V = MODE == HVP || DOT;
+    using Tile = ChunkTile<P>;
+    constexpr int VT = Tile::FLOATS;
+    constexpr int AR = VT + (HAS_V ? Tile::FLOATS : 0);   // 3 x P alpha rows
+    constexpr int XR = AR + 3 * P * 64;                   // 3 x P tangent rows
+    constexpr int RA = XR + 3 * P * 64;                   // 3 alpha rows above
+    constexpr int RX = RA + 3 * 64;                       // 3 tangent rows above
+    constexpr int OT = RX + 3 * 64;
+    constexpr int BUF = OT + (DOT ? 0 : Tile::FLOATS);
+    extern __shared__ float smem[];
+    __shared__ int prog[NW];
+    __shared__ float red[NW];
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const unsigned ul4 = (unsigned)lane * 4u;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float* buf = smem + wave * BUF;
+    float* otile = buf + OT;
+    // rings [NW][R]: (beta, g) up flows to (M, I); diagonal flows to (M, I); to D
+    float4* ringU = reinterpret_cast<float4*>(smem + NW * BUF);
+    float4* ringD = ringU + NW * R;
+    float2* ringE = reinterpret_cast<float2*>(ringD + NW * R);
+    int* st = status + b;
+    const int tbase = Tile::read_base(lane);
+
+    if (lane == 0) prog[wave] = -1;
+    __syncthreads();
+
+    const int L1 = min(max(lengths[2 * b], 0), L1max);
+    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const float c = kLog2e / T;
+    const float rT = 1.0f / T;
+    const float S = partition[b];
+    const float dSb = dS[b];
+    const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
+    const int nsteps = L2 + 63;
+    const int nch = (nsteps + P - 1) / P;
+    const size_t NT = (size_t)stored_steps(L2max);
+    const size_t PL = NT * 64;
+    const float* sbase = scores + (size_t)b * L1max * L2max;
+    const float* vbase = HAS_V ? V + (size_t)b * L1max * L2max : nullptr;
+    float* obase = DOT ? nullptr : out + (size_t)b * L1max * L2max;
+    const uint32_t in_lds = lds_address(buf);
+
+    if (!DOT) zero_padding(obase, L1, L2, L1max, L2max, NW * 64);
+
+    float dacc = 0.0f;
+    float AM[P + 2], AI[P + 2], AD[P + 2], XM[P + 2], XI[P + 2], XD[P + 2];
+
+    for (int q = wave; q < NS; q += NW) {
+        const int s = NS - 1 - q;
+        const int i0 = s * 64;
+        const int L2eff = (i0 + lane < L1) ? L2 : 0;
+        const size_t sb = ((size_t)b * NSmax + s) * 3;
+        const size_t ub = ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * 3;
+        const float* astripe = alpha_sk + sb * PL;
+        const float* xstripe = tan_sk + sb * PL;
+        const float* bupA = brow + ub * NT;
+        const float* bupX = tan_brow + ub * NT;
+        const float4* inU = ring_from(ringU, q, R);
+        const float4* inD = ring_from(ringD, q, R);
+        const float2* inE = ring_from(ringE, q, R);
+        float4* outU = ring_of(ringU, q, R);
+        float4* outD = ring_of(ringD, q, R);
+        float2* outE = ring_of(ringE, q, R);
+        const bool below = q > 0;
+
+        auto issue_chunk = [&](int k) {
+            const int th = nsteps - 1 - k * P;
+            dma_tile<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
+            if (HAS_V) dma_tile<P, -1>(in_lds + VT * 4, vbase, i0, L1max, L2max, lane, th);
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) {
+                dma_rows<P, -1>(in_lds + (AR + pl * P * 64) * 4, astripe + pl * PL, th - 2, ul4);
+                dma_rows<P, -1>(in_lds + (XR + pl * P * 64) * 4, xstripe + pl * PL, th - 2, ul4);
+            }
+            const uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) {
+                uint32_t o = roff, l = in_lds + (RA + pl * 64) * 4;
+                lds_dma_dword<0>(bupA + pl * NT, o, l, 0u);
+                o = roff;
+                l = in_lds + (RX + pl * 64) * 4;
+                lds_dma_dword<0>(bupX + pl * NT, o, l, 0u);
+            }
+        };
+
+        {
+            const size_t o0 = (size_t)(nsteps - 1 + APAD) * 64, o1 = o0 - 64;
+            AM[P] = lane_load(astripe + o0, ul4);
+            AM[P + 1] = lane_load(astripe + o1, ul4);
+            AI[P] = lane_load(astripe + PL + o0, ul4);
+            AI[P + 1] = lane_load(astripe + PL + o1, ul4);
+            AD[P] = lane_load(astripe + 2 * PL + o0, ul4);
+            AD[P + 1] = lane_load(astripe + 2 * PL + o1, ul4);
+            XM[P] = lane_load(xstripe + o0, ul4);
+            XM[P + 1] = lane_load(xstripe + o1, ul4);
+            XI[P] = lane_load(xstripe + PL + o0, ul4);
+            XI[P + 1] = lane_load(xstripe + PL + o1, ul4);
+            XD[P] = lane_load(xstripe + 2 * PL + o0, ul4);
+            XD[P + 1] = lane_load(xstripe + 2 * PL + o1, ul4);
+            __asm__ volatile("" ::"v"(AM[P]), "v"(AM[P + 1]), "v"(AI[P]), "v"(AI[P + 1]),
+                             "v"(AD[P]), "v"(AD[P + 1]), "v"(XM[P]), "v"(XM[P + 1]),
+                             "v"(XI[P]), "v"(XI[P + 1]), "v"(XD[P]), "v"(XD[P + 1]));
+        }
+        wave_lds_sync();
+        issue_chunk(0);
+        // pending successor flows (beta b*, channel g*): from (i, j+1) to M and D; from
+        // (i+1, j) to M and I; from (i+1, j+1) to M, I, D (this step and the next)
+        float lbM = 0, lgM = 0, lbD = 0, lgD = 0;
+        float ubM = 0, ugM = 0, ubI = 0, ugI = 0;
+        float dbM = 0, dgM = 0, dbI = 0, dgI = 0, dbD = 0, dgD = 0;
+        float ebM = 0, egM = 0, ebI = 0, egI = 0, ebD = 0, egD = 0;
+
+        for (int k = 0; k < nch; ++k) {
+            const int t_hi = nsteps - 1 - k * P;
+            chunk_waits<P>(prog, q, NS, k, nch, R, st);
+            if (k == 0 || DOT) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            float sv[P], vv[P];
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                sv[u] = buf[tbase + u];
+                vv[u] = HAS_V ? buf[VT + tbase + u] : 0.0f;
+            }
+            AM[0] = AM[P]; AM[1] = AM[P + 1];
+            AI[0] = AI[P]; AI[1] = AI[P + 1];
+            AD[0] = AD[P]; AD[1] = AD[P + 1];
+            XM[0] = XM[P]; XM[1] = XM[P + 1];
+            XI[0] = XI[P]; XI[1] = XI[P + 1];
+            XD[0] = XD[P]; XD[1] = XD[P + 1];
+#pragma unroll
+            for (int j = 0; j < P; ++j) {
+                AM[j + 2] = buf[AR + j * 64 + lane];
+                AI[j + 2] = buf[AR + P * 64 + j * 64 + lane];
+                AD[j + 2] = buf[AR + 2 * P * 64 + j * 64 + lane];
+                XM[j + 2] = buf[XR + j * 64 + lane];
+                XI[j + 2] = buf[XR + P * 64 + j * 64 + lane];
+                XD[j + 2] = buf[XR + 2 * P * 64 + j * 64 + lane];
+            }
+            const bool row_ok = s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1;
+            float bAM = row_ok ? buf[RA + lane] : kNINF;
+            float bAI = row_ok ? buf[RA + 64 + lane] : kNINF;
+            float bAD = row_ok ? buf[RA + 128 + lane] : kNINF;
+            float bXM = row_ok ? buf[RX + lane] : 0.0f;
+            float bXI = row_ok ? buf[RX + 64 + lane] : 0.0f;
+            float bXD = row_ok ? buf[RX + 128 + lane] : 0.0f;
+            // flows from the stripe below for lane 63: lane 63-j holds step j
+            float4 qU = make_float4(0, 0, 0, 0), qD = make_float4(0, 0, 0, 0);
+            float2 qE = make_float2(0, 0);
+            if (below && lane >= 64 - P) {
+                const int j = 63 - lane;
+                qU = inU[ring_index(k * P + j + 63, R)];
+                const int id = ring_index(k * P + j + 62, R);
+                qD = inD[id];
+                qE = inE[id];
+            }
+            wave_lds_sync();
+            if (k + 1 < nch) issue_chunk(k + 1);
+            const int slot0 = ring_index(k * P, R);
+            {
+                const float a0 = lane_bcast(qU.x, 63), a1 = lane_bcast(qU.y, 63);
+                const float a2 = lane_bcast(qU.z, 63), a3 = lane_bcast(qU.w, 63);
+                const float d0 = lane_bcast(qD.x, 63), d1 = lane_bcast(qD.y, 63);
+                const float d2 = lane_bcast(qD.z, 63), d3 = lane_bcast(qD.w, 63);
+                const float d4 = lane_bcast(qE.x, 63), d5 = lane_bcast(qE.y, 63);
+                const float n0 = lane_bcast(qD.x, 62), n1 = lane_bcast(qD.y, 62);
+                const float n2 = lane_bcast(qD.z, 62), n3 = lane_bcast(qD.w, 62);
+                const float n4 = lane_bcast(qE.x, 62), n5 = lane_bcast(qE.y, 62);
+                if (lane == 63) {
+                    ubM = a0; ugM = a1; ubI = a2; ugI = a3;
+                    dbM = d0; dgM = d1; dbI = d2; dgI = d3; dbD = d4; dgD = d5;
+                    ebM = n0; egM = n1; ebI = n2; egI = n3; ebD = n4; egD = n5;
+                }
+            }
+            float qdb0 = wave_shr1(wave_shr1(qD.x, 0.0f), 0.0f);
+            float qdg0 = wave_shr1(wave_shr1(qD.y, 0.0f), 0.0f);
+            float qdb1 = wave_shr1(wave_shr1(qD.z, 0.0f), 0.0f);
+            float qdg1 = wave_shr1(wave_shr1(qD.w, 0.0f), 0.0f);
+            float qdb2 = wave_shr1(wave_shr1(qE.x, 0.0f), 0.0f);
+            float qdg2 = wave_shr1(wave_shr1(qE.y, 0.0f), 0.0f);
+            float qub0 = qU.x, qug0 = qU.y, qub1 = qU.z, qug1 = qU.w;
+#pragma unroll
+            for (int u = 0; u < P; ++u) {
+                const int t = t_hi - u;
+                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
+                const float sc = ok ? sv[u] : kNINF;
+                const float vd = ok ? vv[u] : 0.0f;
+                // primal and tangent predecessors
+                const float nAM = wave_shl1(bAM, kNINF), nAI = wave_shl1(bAI, kNINF),
+                            nAD = wave_shl1(bAD, kNINF);
+                const float nXM = wave_shl1(bXM, 0.0f), nXI = wave_shl1(bXI, 0.0f),
+                            nXD = wave_shl1(bXD, 0.0f);
+                const float upM = wave_shr1_or(AM[u + 1], bAM), upI = wave_shr1_or(AI[u + 1], bAI);
+                const float uxM = wave_shr1_or(XM[u + 1], bXM), uxI = wave_shr1_or(XI[u + 1], bXI);
+                const float dgAM = wave_shr1_or(AM[u + 2], nAM), dgAI = wave_shr1_or(AI[u + 2], nAI),
+                            dgAD = wave_shr1_or(AD[u + 2], nAD);
+                const float dxM = wave_shr1_or(XM[u + 2], nXM), dxI = wave_shr1_or(XI[u + 2], nXI),
+                            dxD = wave_shr1_or(XD[u + 2], nXD);
+                bAM = nAM; bAI = nAI; bAD = nAD;
+                bXM = nXM; bXI = nXI; bXD = nXD;
+                const float lfM = AM[u + 1], lfD = AD[u + 1], lxM = XM[u + 1], lxD = XD[u + 1];
+                // M: weights over (M, I, D) diagonal + s, and s
+                const float v0 = dgAM + sc, v1 = dgAI + sc, v2 = dgAD + sc;
+                const float m4 = fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
+                const float e0 = fast_exp2((v0 - m4) * c), e1 = fast_exp2((v1 - m4) * c);
+                const float e2 = fast_exp2((v2 - m4) * c), e3 = fast_exp2((sc - m4) * c);
+                const float r4 = fast_rcp(((e0 + e1) + e2) + e3);
+                const float w0 = e0 * r4, w1 = e1 * r4, w2 = e2 * r4, w3 = e3 * r4;
+                // I: open from M above, extend from I above
+                const float i0v = upM + go, i1v = upI + ge;
+                const float mi = fmaxf(i0v, i1v);
+                const float f0 = fast_exp2((i0v - mi) * c), f1 = fast_exp2((i1v - mi) * c);
+                const float ri = mi > kNINF ? fast_rcp(f0 + f1) : 0.0f;
+                const float wi0 = f0 * ri, wi1 = f1 * ri;
+                // D: open from M left, extend from D left
+                const float d0v = lfM + go, d1v = lfD + ge;
+                const float md = fmaxf(d0v, d1v);
+                const float g0 = fast_exp2((d0v - md) * c), g1 = fast_exp2((d1v - md) * c);
+                const float rd = md > kNINF ? fast_rcp(g0 + g1) : 0.0f;
+                const float wd0 = g0 * rd, wd1 = g1 * rd;
+                // candidate tangents
+                const float ao = MODE == OPEN ? 1.0f : 0.0f, ae = MODE == EXT ? 1.0f : 0.0f;
+                const float vt = MODE == HVP ? vd : 0.0f;
+                const float dm0 = dxM + vt, dm1 = dxI + vt, dm2 = dxD + vt, dm3 = vt;
+                const float di0 = uxM + ao, di1 = uxI + ae;
+                const float dd0 = lxM + ao, dd1 = lxD + ae;
+                const float mM = ((w0 * dm0 + w1 * dm1) + w2 * dm2) + w3 * dm3;
+                const float mI = wi0 * di0 + wi1 * di1;
+                const float mD = wd0 * dd0 + wd1 * dd1;
+                float dw0 = w0 * (dm0 - mM) * rT, dw1 = w1 * (dm1 - mM) * rT;
+                float dw2 = w2 * (dm2 - mM) * rT, dw3 = w3 * (dm3 - mM) * rT;
+                float dwi0 = wi0 * (di0 - mI) * rT, dwi1 = wi1 * (di1 - mI) * rT;
+                float dwd0 = wd0 * (dd0 - mD) * rT, dwd1 = wd1 * (dd1 - mD) * rT;
+                if (MODE == TEMP) {
+                    const float rT2 = rT * rT;
+                    const float E4 = ((w0 * v0 + w1 * v1) + w2 * v2) + w3 * sc;
+                    dw0 += w0 * (E4 - v0) * rT2;
+                    dw1 += w1 * (E4 - v1) * rT2;
+                    dw2 += w2 * (E4 - v2) * rT2;
+                    dw3 += w3 * (E4 - sc) * rT2;
+                    const float Ei = wi0 * i0v + wi1 * i1v;
+                    dwi0 += wi0 * (Ei - i0v) * rT2;
+                    dwi1 += wi1 * (Ei - i1v) * rT2;
+                    const float Ed = wd0 * d0v + wd1 * d1v;
+                    dwd0 += wd0 * (Ed - d0v) * rT2;
+                    dwd1 += wd1 * (Ed - d1v) * rT2;
+                }
+                // initial values of the two channels
+                float lp;
+                lp = (AM[u] - S) * c;
+                const float biM = fast_exp2(lp < 0.0f ? lp : 0.0f);
+                lp = (AI[u] - S) * c;
+                const float biI = fast_exp2(lp < 0.0f ? lp : 0.0f);
+                lp = (AD[u] - S) * c;
+                const float biD = fast_exp2(lp < 0.0f ? lp : 0.0f);
+                const float giM = biM * (XM[u] - dSb) * rT;
+                const float giI = biI * (XI[u] - dSb) * rT;
+                const float giD = biD * (XD[u] - dSb) * rT;
+                // channels in the reference's accumulation order (init first for the
+                // HVP; last for the parameter Jacobians, then the temperature term of
+                // reachable states)
+                const float bM = ((biM + dbM) + lbM) + ubM;
+                const float bI = (biI + dbI) + ubI;
+                const float bD = (biD + dbD) + lbD;
+                float gM, gI, gD;
+                if (MODE == HVP) {
+                    gM = ((giM + dgM) + lgM) + ugM;
+                    gI = (giI + dgI) + ugI;
+                    gD = (giD + dgD) + lgD;
+                } else {
+                    gM = ((dgM + lgM) + ugM) + giM;
+                    gI = (dgI + ugI) + giI;
+                    gD = (dgD + lgD) + giD;
+                    if (MODE == TEMP) {
+                        const float rT2 = rT * rT;
+                        if (AM[u] > kNINF) gM -= biM * (AM[u] - S) * rT2;
+                        if (AI[u] > kNINF) gI -= biI * (AI[u] - S) * rT2;
+                        if (AD[u] > kNINF) gD -= biD * (AD[u] - S) * rT2;
+                    }
+                }
+                const float BM = ok ? bM : 0.0f, BI = ok ? bI : 0.0f, BD = ok ? bD : 0.0f;
+                const float GM = ok ? gM : 0.0f, GI = ok ? gI : 0.0f, GD = ok ? gD : 0.0f;
+                const float o = MODE == HVP
+                                    ? GM * (((w0 + w1) + w2) + w3) + BM * (((dw0 + dw1) + dw2) + dw3)
+                                    : GM;
+                if (DOT) dacc += o * vd;
+                else otile[tbase + u] = o;
+                // flows to the predecessors
+                const float obM0 = BM * w0, obI0 = BM * w1, obD0 = BM * w2;
+                const float ogM0 = GM * w0 + BM * dw0, ogI0 = GM * w1 + BM * dw1;
+                const float ogD0 = GM * w2 + BM * dw2;
+                const float obMu = BI * wi0, obIu = BI * wi1;
+                const float ogMu = GI * wi0 + BI * dwi0, ogIu = GI * wi1 + BI * dwi1;
+                const float obMl = BD * wd0, obDl = BD * wd1;
+                const float ogMl = GD * wd0 + BD * dwd0, ogDl = GD * wd1 + BD * dwd1;
+                if (lane == 0) {
+                    outU[slot0 + u] = make_float4(obMu, ogMu, obIu, ogIu);
+                    outD[slot0 + u] = make_float4(obM0, ogM0, obI0, ogI0);
+                    outE[slot0 + u] = make_float2(obD0, ogD0);
+                }
+                // successor flows for the next steps; lane 63 takes the rings
+                qub0 = wave_shr1(qub0, 0.0f);
+                qug0 = wave_shr1(qug0, 0.0f);
+                qub1 = wave_shr1(qub1, 0.0f);
+                qug1 = wave_shr1(qug1, 0.0f);
+                lbM = obMl; lgM = ogMl; lbD = obDl; lgD = ogDl;
+                ubM = wave_shl1_or(obMu, qub0);
+                ugM = wave_shl1_or(ogMu, qug0);
+                ubI = wave_shl1_or(obIu, qub1);
+                ugI = wave_shl1_or(ogIu, qug1);
+                dbM = ebM; dgM = egM; dbI = ebI; dgI = egI; dbD = ebD; dgD = egD;
+                ebM = wave_shl1_or(obM0, qdb0);
+                egM = wave_shl1_or(ogM0, qdg0);
+                ebI = wave_shl1_or(obI0, qdb1);
+                egI = wave_shl1_or(ogI0, qdg1);
+                ebD = wave_shl1_or(obD0, qdb2);
+                egD = wave_shl1_or(ogD0, qdg2);
+                qdb0 = wave_shr1(qdb0, 0.0f);
+                qdg0 = wave_shr1(qdg0, 0.0f);
+                qdb1 = wave_shr1(qdb1, 0.0f);
+                qdg1 = wave_shr1(qdg1, 0.0f);
+                qdb2 = wave_shr1(qdb2, 0.0f);
+                qdg2 = wave_shr1(qdg2, 0.0f);
+            }
+            wave_lds_sync();
+            if (!DOT) write_tile<P, -1>(otile, obase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
+            publish(prog, wave, q * PROG_STRIDE + k + 1);
+        }
+    }
+
+    if (DOT) {
+        dacc = wave_sum(dacc);
+        if (lane == 0) red[wave] = dacc;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float t = 0.0f;
+            for (int w = 0; w < NW; ++w) t += red[w];
+            dot[b] = t;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ host side
+
+constexpr size_t kLdsLimit = 160 * 1024 - 256;
+constexpr int PT = 8;   // tangent sweep chunk
+constexpr int PD = 4;   // reverse sweep chunk
+
+size_t lds_tangent(bool has_v, int L1, int L2) {
+    const int R = ring_len(L1, L2, 256);
+    const int buf = 65 * PT * (has_v ? 2 : 1) + 3 * PT * 64 + 3 * 64;
+    return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + PT)) * sizeof(float4);
+}
+
+size_t lds_dual(bool has_v, bool dot, int L1, int L2) {
+    const int R = ring_len(L1, L2, 128);
+    const int buf = 65 * PD * (has_v ? 2 : 1) + 6 * PD * 64 + 6 * 64 + (dot ? 0 : 65 * PD);
+    return (size_t)NW * buf * sizeof(float) +
+           (size_t)NW * R * (2 * sizeof(float4) + sizeof(float2));
+}
+
+struct Second {
+    Layout prim;
+    float* tan_sk;
+    float* tan_brow;
+    float* sdot;
+    float* part;
+    float* dS[3];   // dS/dopen, dS/dext, dS/dT
+    size_t bytes;
+};
+
+Second second_layout(void* ws, int B, int L1, int L2) {
+    Second w;
+    w.prim = layout(ws, B, L1, L2, 3);
+    char* p = (char*)ws + round256(w.prim.bytes);
+    const size_t ns = ((size_t)L1 + 63) / 64;
+    w.tan_sk = (float*)p;
+    w.tan_brow = w.tan_sk + (size_t)B * ns * 3 * stored_steps(L2) * 64;
+    p += round256(table_floats(B, L1, L2, 3) * sizeof(float));
+    w.sdot = (float*)p;
+    w.part = w.sdot + B;
+    w.dS[0] = w.part + B;
+    w.dS[1] = w.dS[0] + B;
+    w.dS[2] = w.dS[1] + B;
+    p += round256((size_t)5 * B * sizeof(float));
+    w.bytes = (size_t)(p - (char*)ws);
+    return w;
+}
+
+template <int MODE>
+int launch_tangent(const float* scores, const float* V, const int* lengths, int B, int L1, int L2,
+                   float go, float ge, float T, const Second& w, float* sdot, hipStream_t st) {
+    const int ns = (L1 + 63) / 64;
+    const int R = ring_len(L1, L2, 256);
+    const size_t lds = lds_tangent(MODE == HVP, L1, L2);
+    D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
+    auto kern = swa_tangent_kernel<MODE, PT>;
+    D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+    D2P_LAUNCH("swa_tangent", kern, dim3(B), dim3(NW * 64), lds, st, scores, V, lengths,
+               w.prim.alpha_sk, w.prim.brow, w.part, w.tan_sk, w.tan_brow, sdot, w.prim.status,
+               L1, L2, ns, go, ge, T, R);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
+template <int MODE, bool DOT>
+int launch_dual(const float* scores, const float* V, const int* lengths, int B, int L1, int L2,
+                float go, float ge, float T, const Second& w, const float* dS, float* out,
+                float* dot, hipStream_t st) {
+    const int ns = (L1 + 63) / 64;
+    const int R = ring_len(L1, L2, 128);
+    const size_t lds = lds_dual(MODE == HVP || DOT, DOT, L1, L2);
+    D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
+    auto kern = swa_dual_kernel<MODE, PD, DOT>;
+    D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+    D2P_LAUNCH("swa_dual", kern, dim3(B), dim3(NW * 64), lds, st, scores, V, lengths,
+               w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, w.part, dS, out, dot,
+               w.prim.status, w.prim.trash, L1, L2, ns, go, ge, T, R);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
+template <int MODE, bool DOT>
+int param_pass(const float* scores, const float* ga, const int* lengths, int B, int L1, int L2,
+               float go, float ge, float T, const Second& w, float* out, float* dot,
+               hipStream_t st) {
+    const int rc = launch_tangent<MODE>(scores, nullptr, lengths, B, L1, L2, go, ge, T, w,
+                                        nullptr, st);
+    if (rc != D2P_OK) return rc;
+    return launch_dual<MODE, DOT>(scores, ga, lengths, B, L1, L2, go, ge, T, w, w.dS[MODE - 1],
+                                  out, dot, st);
+}
+
+int check(int B, int L1, int L2, float T) {
+    const int rc = swa::check_shape(B, L1, L2, T);
+    if (rc != D2P_OK) return rc;
+    D2P_REQUIRE(lds_tangent(true, L1, L2) <= kLdsLimit && lds_dual(true, false, L1, L2) <= kLdsLimit,
+                "sequence too long for the LDS stripe rings");
+    return D2P_OK;
+}
+
+}  // namespace swa2
+}  // namespace d2p_amd
+
+using namespace d2p_amd;
+
+#define D2P_TRY(...)                    \
+    do {                                \
+        const int rc_ = (__VA_ARGS__);  \
+        if (rc_ != D2P_OK) return rc_;  \
+    } while (0)
+
+extern "C" size_t d2p_swa_second_workspace_bytes(int B, int max_L1, int max_L2) {
+    if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
+    return swa2::second_layout(nullptr, B, max_L1, max_L2).bytes;
+}
+
+extern "C" int d2p_swa_hvp(const float* scores, const float* tangent, const int* lengths, int B,
+                           int max_L1, int max_L2, float gap_open, float gap_ext,
+                           float temperature, float* hvp, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    D2P_TRY(swa2::check(B, max_L1, max_L2, temperature));
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(scores && tangent && lengths && hvp, "null pointer argument");
+    D2P_REQUIRE(workspace && workspace_bytes >= d2p_swa_second_workspace_bytes(B, max_L1, max_L2),
+                "workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    const swa2::Second w = swa2::second_layout(workspace, B, max_L1, max_L2);
+    D2P_TRY(swa::launch_forward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
+                                temperature, w.prim, w.part, st));
+    D2P_TRY(swa2::launch_tangent<swa2::HVP>(scores, tangent, lengths, B, max_L1, max_L2, gap_open,
+                                            gap_ext, temperature, w, w.sdot, st));
+    return swa2::launch_dual<swa2::HVP, false>(scores, tangent, lengths, B, max_L1, max_L2,
+                                               gap_open, gap_ext, temperature, w, w.sdot, hvp,
+                                               nullptr, st);
+}
+
+extern "C" int d2p_swa_param_jacobian(const float* scores, int param_type, const int* lengths,
+                                      int B, int max_L1, int max_L2, float gap_open,
+                                      float gap_ext, float temperature, float* jacobian,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+    D2P_TRY(swa2::check(B, max_L1, max_L2, temperature));
+    D2P_REQUIRE(param_type >= 0 && param_type <= 2, "param_type must be 0, 1 or 2");
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(scores && lengths && jacobian, "null pointer argument");
+    D2P_REQUIRE(workspace && workspace_bytes >= d2p_swa_second_workspace_bytes(B, max_L1, max_L2),
+                "workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    const swa2::Second w = swa2::second_layout(workspace, B, max_L1, max_L2);
+    D2P_TRY(swa::launch_forward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
+                                temperature, w.prim, w.part, st));
+    // dS/dtheta from the marginal backward (marginals into the output, overwritten below)
+    D2P_TRY(swa::launch_backward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
+                                 temperature, w.prim, w.part, jacobian, w.dS[0], w.dS[1], w.dS[2],
+                                 st));
+    switch (param_type) {
+        case 0:
+            return swa2::param_pass<swa2::OPEN, false>(scores, nullptr, lengths, B, max_L1, max_L2,
+                                                       gap_open, gap_ext, temperature, w,
+                                                       jacobian, nullptr, st);
+        case 1:
+            return swa2::param_pass<swa2::EXT, false>(scores, nullptr, lengths, B, max_L1, max_L2,
+                                                      gap_open, gap_ext, temperature, w, jacobian,
+                                                      nullptr, st);
+        default:
+            return swa2::param_pass<swa2::TEMP, false>(scores, nullptr, lengths, B, max_L1, max_L2,
+                                                       gap_open, gap_ext, temperature, w,
+                                                       jacobian, nullptr, st);
+    }
+}
+
+extern "C" int d2p_swa_backward_full(const float* scores, const float* grad_alignment,
+                                     const int* lengths, int B, int max_L1, int max_L2,
+                                     float gap_open, float gap_ext, float temperature,
+                                     float* grad_scores, float* grad_open, float* grad_ext,
+                                     float* grad_T, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+    D2P_TRY(swa2::check(B, max_L1, max_L2, temperature));
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(scores && grad_alignment && lengths && grad_scores && grad_open && grad_ext &&
+                    grad_T,
+                "null pointer argument");
+    D2P_REQUIRE(workspace && workspace_bytes >= d2p_swa_second_workspace_bytes(B, max_L1, max_L2),
+                "workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    const swa2::Second w = swa2::second_layout(workspace, B, max_L1, max_L2);
+    const float* ga = grad_alignment;
+    D2P_TRY(swa::launch_forward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
+                                temperature, w.prim, w.part, st));
+    D2P_TRY(swa::launch_backward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
+                                 temperature, w.prim, w.part, grad_scores, w.dS[0], w.dS[1],
+                                 w.dS[2], st));
+    D2P_TRY(swa2::launch_tangent<swa2::HVP>(scores, ga, lengths, B, max_L1, max_L2, gap_open,
+                                            gap_ext, temperature, w, w.sdot, st));
+    D2P_TRY(swa2::launch_dual<swa2::HVP, false>(scores, ga, lengths, B, max_L1, max_L2, gap_open,
+                                                gap_ext, temperature, w, w.sdot, grad_scores,
+                                                nullptr, st));
+    D2P_TRY(swa2::param_pass<swa2::OPEN, true>(scores, ga, lengths, B, max_L1, max_L2, gap_open,
+                                               gap_ext, temperature, w, nullptr, grad_open, st));
+    D2P_TRY(swa2::param_pass<swa2::EXT, true>(scores, ga, lengths, B, max_L1, max_L2, gap_open,
+                                              gap_ext, temperature, w, nullptr, grad_ext, st));
+    return swa2::param_pass<swa2::TEMP, true>(scores, ga, lengths, B, max_L1, max_L2, gap_open,
+                                              gap_ext, temperature, w, nullptr, grad_T, st);
+}

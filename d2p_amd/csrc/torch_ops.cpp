@@ -123,11 +123,6 @@ Tensor scale_by_batch(const Tensor& src, const Tensor& g) {
     return out;
 }
 
-[[noreturn]] void not_yet(const char* op) {
-    TORCH_CHECK_NOT_IMPLEMENTED(false, "d2p_amd: ", op,
-                                " has no MI355X kernel in this build yet");
-}
-
 // ---------------------------------------------------------------------------
 // linear-gap soft Smith-Waterman
 // ---------------------------------------------------------------------------
@@ -399,6 +394,29 @@ SwaOut swa_run(const Tensor& scores, const Tensor& lengths, const Dims& d, float
     return o;
 }
 
+Tensor swa_second_workspace(const Dims& d, const Tensor& like) {
+    return workspace(d2p_swa_second_workspace_bytes(d.B, d.L1, d.L2), like);
+}
+
+// returns (grad_scores [B,L1,L2], per-element <ga, dP/dopen>, <ga, dP/dext>, <ga, dP/dT> [B])
+std::tuple<Tensor, Tensor, Tensor, Tensor> swa_backward_full_run(const Tensor& scores,
+                                                                 const Tensor& ga,
+                                                                 const Tensor& lengths,
+                                                                 const Dims& d, float go, float ge,
+                                                                 float T) {
+    auto opt = scores.options();
+    Tensor gs = torch::empty({d.B, d.L1, d.L2}, opt);
+    Tensor g_o = torch::empty({d.B}, opt), g_e = torch::empty({d.B}, opt);
+    Tensor g_t = torch::empty({d.B}, opt);
+    Tensor ws = swa_second_workspace(d, scores);
+    D2P_CALL(d2p_swa_backward_full(scores.data_ptr<float>(), ga.data_ptr<float>(),
+                                   lengths.data_ptr<int>(), d.B, d.L1, d.L2, go, ge, T,
+                                   gs.data_ptr<float>(), g_o.data_ptr<float>(),
+                                   g_e.data_ptr<float>(), g_t.data_ptr<float>(), ws.data_ptr(),
+                                   ws.numel(), current_stream()));
+    return {gs, g_o, g_e, g_t};
+}
+
 // Autograd semantics of SoftSWAffineCUDAFunction
 // (/root/reference/src/sw_affine/torch_cuda.cpp:126-400): outputs {value, marginals};
 // d value / d scores = marginals; parameter gradients sum_b grad_value[b] * dS_b/dtheta.
@@ -409,7 +427,10 @@ tensor_list swa_autograd_forward(AutogradContext* ctx, const Tensor& scores, con
     Dims d = checked_dims_affine(scores);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
     SwaOut o = swa_run(scores, lengths, d, (float)go, (float)ge, (float)T);
-    ctx->save_for_backward({o.marginals, o.grad_open, o.grad_ext, o.grad_T});
+    ctx->save_for_backward({scores, lengths, o.marginals, o.grad_open, o.grad_ext, o.grad_T});
+    ctx->saved_data["gap_open"] = go;
+    ctx->saved_data["gap_ext"] = ge;
+    ctx->saved_data["temperature"] = T;
     return {o.partition, o.marginals};
 }
 
@@ -417,18 +438,32 @@ tensor_list swa_autograd_forward(AutogradContext* ctx, const Tensor& scores, con
 tensor_list swa_autograd_backward(AutogradContext* ctx, const tensor_list& grads, bool want_o,
                                   bool want_e, bool want_T) {
     auto saved = ctx->get_saved_variables();
-    Tensor marg = saved[0];
+    Tensor scores = saved[0], lengths = saved[1], marg = saved[2];
     c10::hip::HIPGuardMasqueradingAsCUDA guard(marg.device());
     Tensor grad_value = grads[0], grad_marg = grads[1];
     Tensor gs, go, ge, gT;
     if (grad_value.defined() && grad_value.numel() > 0) {
         gs = scale_by_batch(marg, grad_value);
-        if (want_o) go = grad_param_sum(grad_value, saved[1]);
-        if (want_e) ge = grad_param_sum(grad_value, saved[2]);
-        if (want_T) gT = grad_param_sum(grad_value, saved[3]);
+        if (want_o) go = grad_param_sum(grad_value, saved[3]);
+        if (want_e) ge = grad_param_sum(grad_value, saved[4]);
+        if (want_T) gT = grad_param_sum(grad_value, saved[5]);
     }
-    if (grad_marg.defined() && grad_marg.numel() > 0)
-        not_yet("soft_sw_affine marginal-path backward");
+    if (grad_marg.defined() && grad_marg.numel() > 0) {
+        // marginal path: HVP against the cotangent plus its dot products with
+        // dP/dopen, dP/dext and dP/dT (/root/reference/src/sw_affine/torch_cuda.cpp:284-393)
+        Tensor gm = prepare_cotangent(grad_marg, scores, "grad_posteriors");
+        Dims d = checked_dims_affine(scores);
+        auto r = swa_backward_full_run(scores, gm, lengths, d,
+                                       (float)ctx->saved_data["gap_open"].toDouble(),
+                                       (float)ctx->saved_data["gap_ext"].toDouble(),
+                                       (float)ctx->saved_data["temperature"].toDouble());
+        gs = gs.defined() ? gs + std::get<0>(r) : std::get<0>(r);
+        Tensor to = std::get<1>(r).sum().reshape({1}), te = std::get<2>(r).sum().reshape({1});
+        Tensor tt = std::get<3>(r).sum().reshape({1});
+        if (want_o) go = go.defined() ? go + to : to;
+        if (want_e) ge = ge.defined() ? ge + te : te;
+        if (want_T) gT = gT.defined() ? gT + tt : tt;
+    }
     return {gs, go, ge, gT};
 }
 
@@ -496,18 +531,78 @@ std::tuple<Tensor, Tensor, Tensor> swa_value_grad_params(Tensor s, double go, do
     return {std::get<2>(r), std::get<3>(r), std::get<4>(r)};
 }
 
-Tensor swa_hvp(Tensor, Tensor, double, double, double, c10::optional<Tensor>) {
-    not_yet("soft_sw_affine_hvp");
+// /root/reference/src/sw_affine/torch_cuda.cpp:508-578
+Tensor swa_hvp(Tensor scores, Tensor tangent, double gap_open, double gap_ext, double temperature,
+               c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    CHECK_INPUT_DEV(tangent);
+    TORCH_CHECK(scores.dim() == 3, "scores must be 3D");
+    TORCH_CHECK(scores.sizes() == tangent.sizes(), "scores and tangent must have same shape");
+    TORCH_CHECK(tangent.device() == scores.device(), "tangent must be on same device as scores, got ",
+                tangent.device(), " vs ", scores.device());
+    Dims d = checked_dims_affine(scores);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    Tensor out = torch::empty({d.B, d.L1, d.L2}, scores.options());
+    Tensor ws = swa_second_workspace(d, scores);
+    D2P_CALL(d2p_swa_hvp(scores.data_ptr<float>(), tangent.data_ptr<float>(), l.data_ptr<int>(),
+                         d.B, d.L1, d.L2, (float)gap_open, (float)gap_ext, (float)temperature,
+                         out.data_ptr<float>(), ws.data_ptr(), ws.numel(), current_stream()));
+    return out;
 }
-Tensor swa_param_jacobian(Tensor, int64_t, double, double, double, c10::optional<Tensor>) {
-    not_yet("soft_sw_affine_param_jacobian");
+
+// /root/reference/src/sw_affine/torch_cuda.cpp:580-679
+Tensor swa_param_jacobian(Tensor scores, int64_t param_type, double gap_open, double gap_ext,
+                          double temperature, c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    TORCH_CHECK(scores.dim() == 3, "scores must be 3D");
+    TORCH_CHECK(param_type >= 0 && param_type <= 2, "param_type must be 0, 1, or 2");
+    Dims d = checked_dims_affine(scores);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    Tensor out = torch::empty({d.B, d.L1, d.L2}, scores.options());
+    Tensor ws = swa_second_workspace(d, scores);
+    D2P_CALL(d2p_swa_param_jacobian(scores.data_ptr<float>(), (int)param_type, l.data_ptr<int>(),
+                                    d.B, d.L1, d.L2, (float)gap_open, (float)gap_ext,
+                                    (float)temperature, out.data_ptr<float>(), ws.data_ptr(),
+                                    ws.numel(), current_stream()));
+    return out;
 }
-std::tuple<Tensor, Tensor, Tensor, Tensor> swa_backward_full(Tensor, Tensor, double, double,
-                                                             double, c10::optional<Tensor>) {
-    not_yet("soft_sw_affine_backward_full");
+
+// /root/reference/src/sw_affine/torch_cuda.cpp:681-817
+std::tuple<Tensor, Tensor, Tensor, Tensor> swa_backward_full(Tensor scores, Tensor grad_alignment,
+                                                             double gap_open, double gap_ext,
+                                                             double temperature,
+                                                             c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    TORCH_CHECK(scores.dim() == 3, "scores must be 3D (B, L1, L2)");
+    TORCH_CHECK(grad_alignment.sizes() == scores.sizes(),
+                "grad_alignment must have same shape as scores");
+    TORCH_CHECK(grad_alignment.is_cuda(), "grad_alignment must be a CUDA tensor");
+    TORCH_CHECK(grad_alignment.device() == scores.device(),
+                "grad_alignment must be on same device as scores, got ", grad_alignment.device(),
+                " vs ", scores.device());
+    Dims d = checked_dims_affine(scores);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    Tensor ga = grad_alignment.contiguous();
+    if (ga.scalar_type() != torch::kFloat32) ga = ga.to(torch::kFloat32);
+    auto r = swa_backward_full_run(scores, ga, l, d, (float)gap_open, (float)gap_ext,
+                                   (float)temperature);
+    return {std::get<0>(r), std::get<1>(r).sum().reshape({1}), std::get<2>(r).sum().reshape({1}),
+            std::get<3>(r).sum().reshape({1})};
 }
-Tensor swa_marg_grad(Tensor, double, double, double, c10::optional<Tensor>) {
-    not_yet("sw_affine_marginals_grad_*");
+
+// sw_affine_marginals_grad_{gap_open,gap_ext,temp}
+// (/root/reference/src/sw_affine/torch_cuda.cpp:878-910)
+Tensor swa_marg_grad_open(Tensor s, double go, double ge, double t, c10::optional<Tensor> l) {
+    return swa_param_jacobian(s, 0, go, ge, t, l);
+}
+Tensor swa_marg_grad_ext(Tensor s, double go, double ge, double t, c10::optional<Tensor> l) {
+    return swa_param_jacobian(s, 1, go, ge, t, l);
+}
+Tensor swa_marg_grad_temp(Tensor s, double go, double ge, double t, c10::optional<Tensor> l) {
+    return swa_param_jacobian(s, 2, go, ge, t, l);
 }
 
 // ---------------------------------------------------------------------------
@@ -773,9 +868,9 @@ TORCH_LIBRARY_IMPL(d2p, CUDA, m) {
     m.impl("sw_affine_value_grad_params", swa_value_grad_params);
     m.impl("sw_affine_marginals_backward", swa_backward_full);
     m.impl("sw_affine_marginals_hvp", swa_hvp);
-    m.impl("sw_affine_marginals_grad_gap_open", swa_marg_grad);
-    m.impl("sw_affine_marginals_grad_gap_ext", swa_marg_grad);
-    m.impl("sw_affine_marginals_grad_temp", swa_marg_grad);
+    m.impl("sw_affine_marginals_grad_gap_open", swa_marg_grad_open);
+    m.impl("sw_affine_marginals_grad_gap_ext", swa_marg_grad_ext);
+    m.impl("sw_affine_marginals_grad_temp", swa_marg_grad_temp);
 
     m.impl("soft_dtw", dtw_t);
     m.impl("soft_dtw_float", dtw_float);

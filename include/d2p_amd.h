@@ -125,6 +125,42 @@ int d2p_swa_forward_marginals(const float* scores, const int* lengths, int B, in
                               float* grad_ext, float* grad_T, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* Workspace bytes of the second-order affine-gap entry points below (d2p_swa_hvp,
+ * d2p_swa_param_jacobian, d2p_swa_backward_full). */
+size_t d2p_swa_second_workspace_bytes(int B, int max_L1, int max_L2);
+
+/* Hessian-vector product of the partition: hvp = (d^2 S / dscores^2) . tangent.
+ * Replaces sw_affine_hvp (/root/reference/src/sw_affine/kernels.cuh:225-231) as
+ * sequenced by soft_sw_affine_hvp_cuda (/root/reference/src/sw_affine/torch_cuda.cpp:508-578),
+ * which runs the forward first.
+ *   tangent, hvp [B, max_L1, max_L2]                                              */
+int d2p_swa_hvp(const float* scores, const float* tangent, const int* lengths, int B,
+                int max_L1, int max_L2, float gap_open, float gap_ext, float temperature,
+                float* hvp, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Jacobian of the marginals with respect to gap_open (param_type 0), gap_ext (1) or
+ * temperature (2).  Replaces sw_affine_param_grad
+ * (/root/reference/src/sw_affine/kernels.cuh:256-265) as sequenced by
+ * soft_sw_affine_param_jacobian_cuda (/root/reference/src/sw_affine/torch_cuda.cpp:580-679):
+ * forward, backward for dS/dtheta, then the tangent and reverse sweeps.
+ *   jacobian [B, max_L1, max_L2]                                                  */
+int d2p_swa_param_jacobian(const float* scores, int param_type, const int* lengths, int B,
+                           int max_L1, int max_L2, float gap_open, float gap_ext,
+                           float temperature, float* jacobian, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* Backward of the marginals output for a cotangent grad_alignment:
+ *   grad_scores = H . grad_alignment, and per element the dot products of
+ *   grad_alignment[b] with dP_b/dgap_open, dP_b/dgap_ext and dP_b/dT
+ * (soft_sw_affine_backward_full_cuda, /root/reference/src/sw_affine/torch_cuda.cpp:681-817,
+ * returns their sums over the batch).  The dot products are accumulated inside the
+ * reverse sweeps; the Jacobians are never written. */
+int d2p_swa_backward_full(const float* scores, const float* grad_alignment, const int* lengths,
+                          int B, int max_L1, int max_L2, float gap_open, float gap_ext,
+                          float temperature, float* grad_scores, float* grad_open,
+                          float* grad_ext, float* grad_T, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Soft dynamic time warping (optional Sakoe-Chiba band)
  * ------------------------------------------------------------------------- */

@@ -31,6 +31,11 @@ SIGNATURES = {
     "d2p_sw_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _p, _p, _z, _p]),
     "d2p_sw_param_jacobian": (_i, [_p, _i, _p, _i, _i, _i, _f, _f, _p, _p, _z, _p]),
     "d2p_sw_backward_full": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _p, _p, _p, _p, _z, _p]),
+    "d2p_swa_second_workspace_bytes": (_z, [_i, _i, _i]),
+    "d2p_swa_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _f, _p, _p, _z, _p]),
+    "d2p_swa_param_jacobian": (_i, [_p, _i, _p, _i, _i, _i, _f, _f, _f, _p, _p, _z, _p]),
+    "d2p_swa_backward_full": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _f, _p, _p, _p, _p, _p, _z,
+                                   _p]),
     "d2p_dtw_second_workspace_bytes": (_z, [_i, _i, _i]),
     "d2p_dtw_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _i, _p, _p, _z, _p]),
     "d2p_dtw_param_jacobian": (_i, [_p, _p, _i, _i, _i, _f, _i, _p, _p, _z, _p]),
@@ -187,6 +192,52 @@ def sw_backward_full(scores, grad_alignment, lengths, gap, T):
                                      stream()))
     _check_status(ws, B)
     return gs, gg, gt
+
+
+def _swa_second_ws(B, L1, L2, dev):
+    nbytes = lib().d2p_swa_second_workspace_bytes(B, L1, L2)
+    return _workspace(nbytes, dev), nbytes
+
+
+def swa_hvp(scores, V, lengths, go, ge, T):
+    import torch
+    B, L1, L2 = scores.shape
+    dev = scores.device
+    lengths = _lengths(lengths, B, L1, L2, dev)
+    out = torch.empty(B, L1, L2, device=dev)
+    ws, nbytes = _swa_second_ws(B, L1, L2, dev)
+    check(lib().d2p_swa_hvp(ptr(scores), ptr(V), ptr(lengths), B, L1, L2, go, ge, T, ptr(out),
+                            ptr(ws), nbytes, stream()))
+    _check_status(ws, B)
+    return out
+
+
+def swa_param_jacobian(scores, ptype, lengths, go, ge, T):
+    import torch
+    B, L1, L2 = scores.shape
+    dev = scores.device
+    lengths = _lengths(lengths, B, L1, L2, dev)
+    out = torch.empty(B, L1, L2, device=dev)
+    ws, nbytes = _swa_second_ws(B, L1, L2, dev)
+    check(lib().d2p_swa_param_jacobian(ptr(scores), ptype, ptr(lengths), B, L1, L2, go, ge, T,
+                                       ptr(out), ptr(ws), nbytes, stream()))
+    _check_status(ws, B)
+    return out
+
+
+def swa_backward_full(scores, grad_alignment, lengths, go, ge, T):
+    import torch
+    B, L1, L2 = scores.shape
+    dev = scores.device
+    lengths = _lengths(lengths, B, L1, L2, dev)
+    gs = torch.empty(B, L1, L2, device=dev)
+    gp = [torch.empty(B, device=dev) for _ in range(3)]
+    ws, nbytes = _swa_second_ws(B, L1, L2, dev)
+    check(lib().d2p_swa_backward_full(ptr(scores), ptr(grad_alignment), ptr(lengths), B, L1, L2,
+                                      go, ge, T, ptr(gs), *[ptr(g) for g in gp], ptr(ws), nbytes,
+                                      stream()))
+    _check_status(ws, B)
+    return (gs, *gp)
 
 
 def dtw_hvp(costs, V, lengths, T, bw=-1):
