@@ -7,6 +7,8 @@ HVP and Jacobian entries 1e-4 * max(1, max|ref|).  Parameter gradients are sums
 of cancelling per-cell terms: 1e-3 relative plus 1e-5 * (|value| + 1) / T.  The
 Jacobians also move with the fp32 evaluation of dS/dtheta (each entry by that
 error times P / T): 1e-5 * |dS/dtheta| / T * max(P) is added at these sizes.
+The temperature Jacobians of SW carry per-cell terms P (alpha - S) / T^2 whose
+inputs hold fp32 rounding of |alpha| <= |value|: 4e-7 * (|value| + 1) / T^2 more.
 """
 import os
 
@@ -71,4 +73,6 @@ def test_hip_matches_golden(cuda, path):
         _check(name, f"grad_{pn}", _np(g), dS, 1e-5 * (vmax + 1.0) / T, 1e-3)
         want = f[f"jac_{pn}"]
         allow = 1e-5 * np.abs(dS).max() / T * pmax
+        if pn == "T" and not name.startswith("dtw"):
+            allow += 4e-7 * (vmax + 1.0) / T ** 2
         _check(name, f"jac_{pn}", _np(J), want, 1e-4 * max(1.0, np.abs(want).max()) + allow)
