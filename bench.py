@@ -1,20 +1,29 @@
 #!/usr/bin/env python3
-"""Benchmark of the north-star path on one MI355X.
+"""Benchmark of the soft-alignment DP path on one MI355X.
 
-Workload (config C2): ``d2p_amd.soft_sw(scores, gap=-1.0, temperature=1.0)``
-followed by ``value.sum().backward()`` on a fresh ``requires_grad`` leaf, with
-scores [256, 512, 512] ~ N(0,1) fp32 (seed 1, drawn on the CPU, copied to the
-device before timing).  One step = that forward + backward; the metric is DP
-cells per second (B*L1*L2 per step).
+Default workload (config C2, the metric's configuration):
+``d2p_amd.soft_sw(scores, gap=-1.0, temperature=1.0)`` followed by
+``value.sum().backward()`` on a fresh ``requires_grad`` leaf, scores
+[256, 512, 512] ~ N(0,1) fp32 (seed 1, drawn on the CPU, copied to the device
+before timing).  One step = that forward + backward; the metric is DP cells per
+second (B*L1*L2 per step).
 
-Prints one JSON line (see the keys below) with:
+``--config`` selects the other configurations of the same path (not the
+metric's line; same output format): ``c3`` affine gap, ragged lengths;
+``c4`` soft DTW on squared-distance costs at T=0.1; ``c5`` linear gap
+[16, 4096, 4096]; ``c5hvp`` the Hessian-vector product on the C5 shapes.
+
+Prints one JSON line with:
   * ``roofline``: the dominant kernel (largest share of the timed region),
     its algorithmic HBM bytes per launch divided by its average launch time,
-    timed with HIP events recorded by the kernel library on its own stream;
-  * ``step_roofline``: the whole step at 16 algorithmic bytes per cell;
-  * ``cpu_baseline``: the reference's own CPU kernels (oracle/_ref, built from
-    the reference sources) run in the reference's autograd call sequence on the
-    host cores, on the full C2 batch.
+    timed with HIP events the kernel library records on the launch stream;
+    ``traffic`` is the HBM bytes per launch of that kernel measured with
+    rocprofv3 --pmc (FETCH_SIZE x2 calibration + WRITE_SIZE), read from
+    profiles/<kernel>_<config>_pmc.md when that summary exists;
+  * ``step_roofline``: the whole step at its algorithmic bytes;
+  * ``cpu_baseline`` (C2 only, rank 0): the reference's own CPU kernels
+    (oracle/_ref, built from the reference sources; else the C restatement)
+    run in the reference's autograd call sequence on the host cores.
 Only one GPU is supported: ``--gpus`` above 1 exits with a message.
 """
 from __future__ import annotations
@@ -23,6 +32,7 @@ import argparse
 import ctypes
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -32,14 +42,117 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "DP cells/sec fwd+bwd, soft_sw B=256 512x512 fp32; achieved HBM GB/s %"
-B, L1, L2 = 256, 512, 512
-GAP, TEMP, SEED = -1.0, 1.0, 1
 
-# algorithmic HBM bytes per DP cell attributed to each kernel of one step:
-# the forward op must read scores (4) and write marginals (4); the autograd
-# backward must read the saved marginals (4) and write grad_scores (4).  The
-# scores read is attributed to sw_forward, the marginal write to sw_backward.
-ALGO_BYTES_PER_CELL = {"sw_forward": 4, "sw_backward": 4, "scale_by_batch": 8}
+
+def _randn(g, shape, scale=1.0):
+    import torch
+    return torch.randn(shape, generator=g, dtype=torch.float32) * scale
+
+
+# Per configuration: inputs (seeded, on the CPU), the step, the cells per step,
+# algorithmic bytes per step and per kernel launch (bytes per cell of the public
+# contract, attributed to the kernel that moves them).
+def make_c2():
+    import torch
+    g = torch.Generator().manual_seed(1)
+    B, L1, L2 = 256, 512, 512
+    scores = _randn(g, (B, L1, L2))
+    cells = B * L1 * L2
+    return dict(
+        name="c2", inputs={"scores": scores}, cells=cells, algo_step=16 * cells,
+        # forward op: read scores (sw_forward), write marginals (sw_backward);
+        # autograd backward: read marginals + write grad_scores (scale_by_batch)
+        algo_kernel={"sw_forward": 4 * cells, "sw_backward": 4 * cells,
+                     "scale_by_batch": 8 * cells},
+        workload="C2: soft_sw linear gap, scores [256,512,512] fp32, gap=-1, T=1, "
+                 "fwd (value+marginals) + value.sum().backward()",
+        extra={"B": B, "L1": L1, "L2": L2, "gap": -1.0, "temperature": 1.0})
+
+
+def make_c3():
+    import torch
+    g = torch.Generator().manual_seed(2)
+    B, L = 64, 1024
+    scores = _randn(g, (B, L, L), 2.0)
+    lens = torch.randint(256, 1025, (B, 2), generator=g, dtype=torch.int32)
+    valid = int((lens[:, 0].long() * lens[:, 1].long()).sum())
+    padded = B * L * L
+    return dict(
+        name="c3", inputs={"scores": scores, "lengths": lens}, cells=valid,
+        algo_step=8 * valid + 8 * padded,
+        algo_kernel={"swa_forward": 4 * valid, "swa_backward": 4 * padded,
+                     "scale_by_batch": 4 * valid + 4 * padded},
+        workload="C3: soft_sw_affine, scores 2*N(0,1) [64,1024,1024], lengths U[256,1024], "
+                 "gap_open=-11, gap_ext=-1, T=0.5, fwd + value.sum().backward(); cells = valid",
+        extra={"B": B, "L1": L, "L2": L, "valid_cells": valid, "padded_cells": padded})
+
+
+def make_c4():
+    import torch
+    g = torch.Generator().manual_seed(3)
+    B, L, D = 512, 256, 64
+    x = _randn(g, (B, L, D))
+    y = _randn(g, (B, L, D))
+    costs = torch.cdist(x, y, compute_mode="donot_use_mm_for_euclid_dist") ** 2
+    cells = B * L * L
+    return dict(
+        name="c4", inputs={"costs": costs.contiguous()}, cells=cells, algo_step=16 * cells,
+        algo_kernel={"dtw_forward": 4 * cells, "dtw_backward": 4 * cells,
+                     "scale_by_batch": 8 * cells},
+        workload="C4: soft_dtw, squared-distance costs of 64-d features [512,256,256], T=0.1, "
+                 "fwd + cost.sum().backward()",
+        extra={"B": B, "L1": L, "L2": L, "temperature": 0.1})
+
+
+def make_c5(hvp=False):
+    import torch
+    g = torch.Generator().manual_seed(4)
+    B, L = 16, 4096
+    scores = _randn(g, (B, L, L))
+    V = _randn(g, (B, L, L))
+    cells = B * L * L
+    if hvp:
+        return dict(
+            name="c5hvp", inputs={"scores": scores, "V": V}, cells=cells, algo_step=12 * cells,
+            # read scores + V, write H
+            algo_kernel={"sw_forward": 4 * cells, "sw_tangent": 4 * cells,
+                         "sw_dual": 4 * cells},
+            workload="C5 HVP: soft_sw_hvp(scores, V, -1, 1) on [16,4096,4096]",
+            extra={"B": B, "L1": L, "L2": L})
+    return dict(
+        name="c5", inputs={"scores": scores}, cells=cells, algo_step=16 * cells,
+        algo_kernel={"sw_forward": 4 * cells, "sw_backward": 4 * cells,
+                     "scale_by_batch": 8 * cells},
+        workload="C5: soft_sw linear gap [16,4096,4096], gap=-1, T=1, fwd + "
+                 "value.sum().backward()",
+        extra={"B": B, "L1": L, "L2": L})
+
+
+CONFIGS = {"c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5,
+           "c5hvp": lambda: make_c5(hvp=True)}
+
+
+def make_step(cfg, dev):
+    import d2p_amd
+    x = {k: v.to(dev) for k, v in cfg["inputs"].items()}
+    name = cfg["name"]
+    if name in ("c2", "c5"):
+        def step():
+            s = x["scores"].detach().requires_grad_(True)
+            d2p_amd.soft_sw(s, gap=-1.0, temperature=1.0).value.sum().backward()
+    elif name == "c3":
+        def step():
+            s = x["scores"].detach().requires_grad_(True)
+            d2p_amd.soft_sw_affine(s, gap_open=-11.0, gap_ext=-1.0, temperature=0.5,
+                                   lengths=x["lengths"]).value.sum().backward()
+    elif name == "c4":
+        def step():
+            c = x["costs"].detach().requires_grad_(True)
+            d2p_amd.soft_dtw(c, temperature=0.1).cost.sum().backward()
+    else:
+        def step():
+            d2p_amd.soft_sw_hvp(x["scores"], x["V"], -1.0, 1.0, None)
+    return step
 
 
 def kernel_stats(lib):
@@ -52,6 +165,16 @@ def kernel_stats(lib):
         out[name] = {"launches": int(cnt), "total_ms": float(tot), "avg_ms": float(tot) / int(cnt),
                      "min_ms": float(mn), "max_ms": float(mx)}
     return out
+
+
+def measured_traffic(kernel, config):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if present:
+    the summary carries a line ``traffic_bytes_per_launch: <N>``."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{config}_pmc.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
 
 
 def cpu_baseline(scores_np, runs=3):
@@ -67,9 +190,9 @@ def cpu_baseline(scores_np, runs=3):
     ones = np.ones((scores_np.shape[0], 1, 1), np.float32)
 
     def step():
-        alpha, part = k.sw_forward(scores_np, None, GAP, TEMP)
-        k.sw_backward(alpha, scores_np, part, None, GAP, TEMP)
-        post, _, _ = k.sw_backward(alpha, scores_np, part, None, GAP, TEMP)
+        alpha, part = k.sw_forward(scores_np, None, -1.0, 1.0)
+        k.sw_backward(alpha, scores_np, part, None, -1.0, 1.0)
+        post, _, _ = k.sw_backward(alpha, scores_np, part, None, -1.0, 1.0)
         return ones * post
 
     step()  # warm-up
@@ -90,32 +213,24 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported "
-              "(the soft-DP batch would shard over B with no exchange; see DESIGN.md)",
-              file=sys.stderr)
+              "(the soft-DP batch would shard over B with no exchange)", file=sys.stderr)
         sys.exit(2)
 
     import torch
-    import d2p_amd
     from d2p_amd import _ops
 
     dev = torch.device("cuda:0")
-    g = torch.Generator().manual_seed(SEED)
-    scores_cpu = torch.randn((B, L1, L2), generator=g, dtype=torch.float32)
-    scores = scores_cpu.to(dev)
+    cfg = CONFIGS[args.config]()
+    step = make_step(cfg, dev)
 
     lib = ctypes.CDLL(_ops.KERNEL_LIBRARY)
     lib.d2p_profile_report.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
     lib.d2p_last_error.restype = ctypes.c_char_p
-
-    def step():
-        x = scores.detach().requires_grad_(True)
-        res = d2p_amd.soft_sw(x, gap=GAP, temperature=TEMP)
-        res.value.sum().backward()
-        return x
 
     for _ in range(args.warmup):
         step()
@@ -132,17 +247,19 @@ def main():
     lib.d2p_profile_enable(0)
     kstats = kernel_stats(lib)
 
-    cells = B * L1 * L2
+    cells = cfg["cells"]
     ms_per_step = elapsed * 1e3 / args.steps
     value = cells * args.steps / elapsed
-    dominant = max(kstats, key=lambda k: kstats[k]["total_ms"])
-    d = kstats[dominant]
-    algo_bytes = ALGO_BYTES_PER_CELL[dominant] * cells
+    timed = {k: v for k, v in kstats.items() if k in cfg["algo_kernel"]}
+    dominant = max(timed, key=lambda k: timed[k]["total_ms"])
+    d = timed[dominant]
+    algo_bytes = cfg["algo_kernel"][dominant]
     achieved = algo_bytes / (d["avg_ms"] * 1e-3) / 1e9
-    step_gbs = 16 * cells / (ms_per_step * 1e-3) / 1e9
+    step_gbs = cfg["algo_step"] / (ms_per_step * 1e-3) / 1e9
+    traffic = measured_traffic(dominant, cfg["name"])
 
     out = {
-        "metric": METRIC,
+        "metric": METRIC if cfg["name"] == "c2" else f"DP cells/sec, config {cfg['name']}",
         "value": value,
         "unit": "cells/s",
         "n_gpus": 1,
@@ -153,22 +270,20 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded N(0,1) scores, generated on the CPU)",
-        "config": {"workload": "C2: soft_sw linear gap, scores [256,512,512] fp32, gap=-1, "
-                               "T=1, fwd (value+marginals) + value.sum().backward()",
-                   "B": B, "L1": L1, "L2": L2, "gap": GAP, "temperature": TEMP,
-                   "parallelism": "single GPU, one workgroup per batch element"},
+        "data": "synthetic (seeded draws generated on the CPU)",
+        "config": dict({"workload": cfg["workload"],
+                        "parallelism": "single GPU, one workgroup per batch element"},
+                       **cfg["extra"]),
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": None,
-                     "algo_bytes_per_launch": algo_bytes,
+                     "traffic": traffic, "algo_bytes_per_launch": algo_bytes,
                      "avg_launch_ms": d["avg_ms"]},
-        "step_roofline": {"algo_bytes_per_step": 16 * cells, "achieved": step_gbs,
+        "step_roofline": {"algo_bytes_per_step": cfg["algo_step"], "achieved": step_gbs,
                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": step_gbs / HBM_PEAK_GBS},
         "kernels_ms": {k: round(v["avg_ms"], 5) for k, v in kstats.items()},
     }
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(scores_cpu.numpy())
+    if cfg["name"] == "c2" and not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(cfg["inputs"]["scores"].numpy())
     print(json.dumps(out), flush=True)
 
 
