@@ -12,6 +12,21 @@
  * float rounding of beta depends on the order in which successors are
  * visited.  Build with -ffp-contract=off (see oracle/Makefile) so no FMA
  * contraction changes the rounding.
+ *
+ * Pinning (no function here is unpinned): every entry point is checked
+ *   - bit for bit against the reference's own CPU kernels compiled from
+ *     /root/reference/src/{sw,sw_affine,dtw}/kernels_cpu.cpp by oracle/Makefile
+ *     (tests/test_oracle_reference.py), including low temperature, the exp clamp,
+ *     large near-tied costs, ragged/empty lengths and DTW bands;
+ *   - bit for bit against golden fixtures written from that build
+ *     (tests/golden/, tests/test_golden.py), which travel where the reference
+ *     does not;
+ *   - against mathematics (tests/test_oracle_math.py): 1x1 / 1xN closed forms,
+ *     path enumeration, a float64 autograd restatement of the recurrences for
+ *     values, marginals, parameter gradients, HVPs and parameter Jacobians,
+ *     hard-max limits, HVP symmetry and linearity, thread-count invariance.
+ * The *_sums64 extensions (double sums of the reference's per-cell parameter
+ * gradient terms) are pinned by the float64 restatement.
  */
 #include "d2p_oracle.h"
 

@@ -321,3 +321,21 @@ def test_worked_example_motif():
     for i, j, mass in want:
         assert int(m[i].argmax()) == j
         assert round(float(m[i, j]), 2) == mass
+
+
+def test_double_summed_parameter_gradients_against_math():
+    """oracle param_grads64 (the reference's per-cell terms summed in double, used by
+    the GPU parity tests) against the float64 restatement."""
+    s = _rand(110, (2, 9, 11))
+    c = np.abs(s) + 0.05
+    ln = np.array([[9, 11], [5, 7]], np.int32)
+    g = _k().param_grads64("sw", s, ln, -0.8, 0.7)
+    _, _, mg, mt = M.sw(s, -0.8, 0.7, ln)
+    _close(g[:, 0], mg, 2e-5, 2e-5, "sums64 gap")
+    _close(g[:, 1], mt, 2e-5, 2e-5, "sums64 T")
+    g = _k().param_grads64("swa", s, ln, -1.5, -0.4, 0.7)
+    _, _, mo, me, mt = M.swa(s, -1.5, -0.4, 0.7, ln)
+    for k, want in enumerate((mo, me, mt)):
+        _close(g[:, k], want, 2e-5, 2e-5, f"sums64 affine {k}")
+    g = _k().param_grads64("dtw", c, ln, 0.7)
+    _close(g, M.dtw(c, 0.7, -1, ln)[2], 2e-5, 2e-5, "sums64 dtw")
