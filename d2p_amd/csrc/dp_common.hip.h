@@ -97,6 +97,16 @@ __device__ __forceinline__ float wave_reduce(float v, Op op) {
     return v;
 }
 
+// Sum of a[0..N) in a balanced tree (short dependency chain; N a power of two).
+template <int N, typename T>
+__device__ __forceinline__ T tree_sum(const T* a) {
+    if constexpr (N == 1) {
+        return a[0];
+    } else {
+        return tree_sum<N / 2>(a) + tree_sum<N / 2>(a + N / 2);
+    }
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
     return wave_reduce(v, [](float a, float b) { return a + b; });
 }

@@ -47,12 +47,11 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    using Tile = ChunkTile<P>;
+    using Tile = QuadTile<P>;
     float* tiles = smem + wave * 2 * Tile::FLOATS;         // double-buffered score chunk
     float* rings = smem + NW * 2 * Tile::FLOATS;           // [NW][R]
     float* sink = rings + NW * R + wave * DUMMY;       // per-wave write sink
     int* st = status + b;
-    const int tbase = Tile::read_base(lane);
 
     if (lane == 0) prog[wave] = -1;
     if (threadIdx.x == 0) *st = 0;
@@ -72,6 +71,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     acc.init_open();
 
     for (int s = wave; s < NS; s += NW) {
+        set_pipeline_priority(s % NW);
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;   // rows past L1 are never valid
         const float* ring_in = ring_from(rings, s, R);
@@ -83,7 +83,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
         for (int t = -APAD; t < 0; ++t) lane_store(out + t * 64, ul4, kNINF);
         wave_lds_sync();   // the previous stripe's tile reads are complete
         const uint32_t tile_lds = lds_address(tiles);
-        dma_tile<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
+        dma_quads<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
         float cur = kNINF, up_prev = kNINF;
 
         for (int k = 0; k < nch; ++k) {
@@ -94,14 +94,13 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
             const float* tile = tiles + (k & 1) * Tile::FLOATS;
             float sv[P];
-#pragma unroll
-            for (int u = 0; u < P; ++u) sv[u] = tile[tbase + u];
+            read_quads<P, 1>(tile, lane, sv);
             // lane 0's up values: column t0+j sits in lane j (ring slot = producer step)
             float rreg = kNINF;
             if (s > 0 && lane < P) rreg = ring_in[ring_index(t0 + lane + 63, R)];
             if (k + 1 < nch)
-                dma_tile<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0, L1max,
-                                 L2max, lane, t0 + P);
+                dma_quads<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0, L1max,
+                                  L2max, lane, t0 + P);
             // lane 63 publishes its alpha of step u into ring slot (t0+u) % R; the
             // other lanes write into the sink (R is a multiple of P: no wrap in a chunk)
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
@@ -169,7 +168,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     // Per wave, two chunk buffers, each: the score tile (then the chunk's marginals),
     // P alpha rows (steps t_hi-2 .. t_hi-P-1, 64 lanes each) and one row of values from
     // the stripe above.  All three arrive by direct-to-LDS loads one chunk ahead.
-    using Tile = ChunkTile<P>;
+    using Tile = QuadTile<P>;
     constexpr int ABUF = Tile::FLOATS;            // alpha rows
     constexpr int RBUF = ABUF + P * 64;           // row above
     constexpr int BUF = RBUF + 64;
@@ -177,7 +176,11 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * BUF);  // [NW][R] (up, diag)
     float2* sink = rings + NW * R + wave * DUMMY;
     int* st = status + b;
-    const int tbase = Tile::read_base(lane);
+    // the chunk's marginals go to an output tile laid over its own buffer, whose
+    // inputs are all in registers by then (the next chunk loads into the other one)
+    using OutTile = ChunkTile<P>;
+    static_assert(OutTile::FLOATS <= BUF, "output tile fits the chunk buffer");
+    const int obase_lane = OutTile::read_base(lane);
 
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
@@ -200,6 +203,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
 
     // Stripes run bottom-up: order q = 0..NS-1 handles stripe NS-1-q, on wave q % NW.
     for (int q = wave; q < NS; q += NW) {
+        set_pipeline_priority(q % NW);
         const int s = NS - 1 - q;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
@@ -210,15 +214,15 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         float2* ring_out = ring_of(rings, q, R);          // to stripe s-1
         const bool below = q > 0;
 
-        // Loads of chunk k (t_hi = nsteps-1-kP) into buffer k&1: P score loads, P alpha
-        // rows, and the row-above values (lane j <= P: the alpha of the last row of the
-        // stripe above at step t_hi - j + 63, clamped to the last step; lanes past P
-        // repeat lane P's address).  2P+1 loads.
+        // Loads of chunk k (t_hi = nsteps-1-kP) into buffer k&1: the score quad tile, P
+        // alpha rows (steps t_hi-2 .. t_hi-P-1, four per load), and the row-above values
+        // (lane j <= P: the alpha of the last row of the stripe above at step
+        // t_hi - j + 63, clamped to the last step; lanes past P repeat lane P's address).
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
             const uint32_t buf = lds_address(bufs + (k & 1) * BUF);
-            dma_tile<P, -1>(buf, sbase, i0, L1max, L2max, lane, th);
-            dma_rows<P, -1>(buf + ABUF * 4, astripe, th - 2, ul4);
+            dma_quads<P, -1>(buf, sbase, i0, L1max, L2max, lane, th);
+            dma_rows4<P, -1>(buf + ABUF * 4, astripe, th - 2, ul4);
             uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
             uint32_t rl = buf + RBUF * 4;
             lds_dma_dword<0>(bup, roff, rl, 0u);
@@ -240,14 +244,12 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             // marginal stores of that chunk (the first chunk's are the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
             float* buf = bufs + (k & 1) * BUF;
-            float* tile = buf;
             float sv[P];
-#pragma unroll
-            for (int u = 0; u < P; ++u) sv[u] = tile[tbase + u];
+            read_quads<P, -1>(buf, lane, sv);
             A[0] = A[P];
             A[1] = A[P + 1];
 #pragma unroll
-            for (int j = 0; j < P; ++j) A[j + 2] = buf[ABUF + j * 64 + lane];
+            for (int j = 0; j < P; ++j) A[j + 2] = buf[ABUF + rows_row<P, -1>(j) * 64 + lane];
             // lane j: alpha of the row above at lane-63 step t_hi - j + 63
             float bv = buf[RBUF + lane];
             bv = (s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1) ? bv : kNINF;
@@ -271,6 +273,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const float d1 = lane_bcast(pre_d, 62);
                 if (lane == 63) { in_up = u0; in_diag = d0; in_diag_next = d1; }
             }
+            Acc gs[P], ps[P];
             float pre_d2 = wave_shr1(pre_d, 0.0f);   // lane 63 = step 1 (then shifted on)
             pre_d2 = wave_shr1(pre_d2, 0.0f);        // lane 63 = step 2
 #pragma unroll
@@ -301,10 +304,9 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const float br = live ? beta * rin : 0.0f;
                 const float od = br * e0, ou = br * e1, ol = br * e2;
                 const float pv = br * (e0 + e3);
-                tile[tbase + u] = pv;
-                g_acc += (Acc)ou;
-                g_acc += (Acc)ol;
-                p_acc += (Acc)(pv * sc);
+                buf[obase_lane + u] = pv;
+                gs[u] = (Acc)ou + (Acc)ol;
+                ps[u] = (Acc)(pv * sc);
                 pub[u] = make_float2(ou, od);
                 // successor contributions for the next steps; lane 63 takes the ring
                 pre_u = wave_shr1(pre_u, 0.0f);
@@ -314,11 +316,14 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 in_diag_next = wave_shl1_or(od, pre_d2);
                 pre_d2 = wave_shr1(pre_d2, 0.0f);
             }
+            // the chunk's parameter-gradient terms: balanced sums, then one add each
+            g_acc += tree_sum<P>(gs);
+            p_acc += tree_sum<P>(ps);
             wave_lds_sync();
             // write this chunk's marginals back over the cells the scores came from:
             // exactly P stores (cells outside the element's lengths go to the trash
             // line in boundary chunks, and carry 0 in inside chunks)
-            write_tile<P, -1>(tile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
+            write_tile<P, -1>(buf, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             publish(prog, wave, q * PROG_STRIDE + k + 1);
         }
     }
@@ -346,13 +351,13 @@ constexpr size_t kLdsLimit = 160 * 1024 - 256;
 
 size_t lds_forward(int max_L1, int max_L2) {
     const int R = wf::ring_len(max_L1, max_L2, 256);
-    return (size_t)wf::NW * 2 * 65 * PF * sizeof(float) +
+    return (size_t)wf::NW * 2 * 64 * PF * sizeof(float) +
            ((size_t)wf::NW * R + wf::NW * DUMMY) * sizeof(float);
 }
 
 size_t lds_backward(int max_L1, int max_L2, int P) {
     const int R = wf::ring_len(max_L1, max_L2, 128);
-    return (size_t)wf::NW * 2 * (65 * P + 64 * P + 64) * sizeof(float) +
+    return (size_t)wf::NW * 2 * (64 * P + 64 * P + 64) * sizeof(float) +
            ((size_t)wf::NW * R + wf::NW * DUMMY) * sizeof(float2);
 }
 

@@ -95,6 +95,17 @@ __host__ inline Layout layout(void* workspace, int B, int max_L1, int max_L2, in
     return l;
 }
 
+// Issue priority of a wave by its stripe's place in the pipeline: every stripe
+// waits on the one before it, so the upstream stripes set the pace and are served
+// first; downstream stripes fill the issue slots they leave.  `pos` = pipeline
+// position of the stripe among those in flight (0 = most upstream).
+__device__ __forceinline__ void set_pipeline_priority(int pos) {
+    if (pos < 2) __builtin_amdgcn_s_setprio(3);
+    else if (pos < 4) __builtin_amdgcn_s_setprio(2);
+    else if (pos < 6) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
+}
+
 // ---------------------------------------------------------------- progress flags
 
 // Progress flags live in LDS.  The writer completes its LDS writes (ring data)
@@ -176,6 +187,20 @@ __device__ __forceinline__ void lds_dma_dword(const float* sbase, uint32_t& voff
         "s_mov_b32 m0, %1\n\t"
         "s_nop 0\n\t"
         "global_load_lds_dword %0, %2\n\t"
+        "s_add_u32 %1, %1, %4\n\t"
+        "v_add_u32 %0, %3, %0"
+        : "+v"(voff), "+s"(lds)
+        : "s"(sbase), "s"(vstep), "n"(LDS_STEP)
+        : "memory", "m0", "scc");
+}
+// The same with 16 bytes per lane: lane l's four dwords land at LDS M0 + 16*l.
+template <int LDS_STEP>
+__device__ __forceinline__ void lds_dma_dwordx4(const float* sbase, uint32_t& voff, uint32_t& lds,
+                                                uint32_t vstep) {
+    __asm__ volatile(
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %2\n\t"
         "s_add_u32 %1, %1, %4\n\t"
         "v_add_u32 %0, %3, %0"
         : "+v"(voff), "+s"(lds)
@@ -286,9 +311,14 @@ __device__ __forceinline__ void write_tile(const float* tile, float* obase, floa
     if (chunk_inside<P, DIR>(i0, L1max, L2max, t_first)) {
         uint32_t off4 = (uint32_t)chunk_offset0<P, DIR>(i0, L2max, lane, t_first) * 4u;
         const uint32_t step4 = (uint32_t)(L2max - 1) * 4u;
+        // all LDS reads first (one wait), then the stores: the empty asm that keeps
+        // one running offset would otherwise order each read behind the last store
+        float v[P];
+#pragma unroll
+        for (int i = 0; i < P; ++i) v[i] = tile[65 * i + lane];
 #pragma unroll
         for (int i = 0; i < P; ++i) {
-            lane_store(obase, off4, tile[65 * i + lane]);
+            lane_store(obase, off4, v[i]);
             off4 += step4;
             __asm__ volatile("" : "+v"(off4));   // keep one running offset
         }
@@ -305,6 +335,152 @@ __device__ __forceinline__ void write_tile(const float* tile, float* obase, floa
         }
     }
 }
+
+// ------------------------------------------------------------ quad tiles
+
+// A chunk of P steps (P = 8 or 16) of a stripe's 64 rows staged with 16-byte
+// direct-to-LDS loads: row r occupies P consecutive floats; its quad q (steps
+// 4q .. 4q+3) sits at slot q ^ swz(r), the four values in memory-column order
+// (ascending steps for DIR = +1, descending for DIR = -1).  swz spreads the 16
+// lanes of one LDS pass over all 64 banks, so the per-lane 16-byte row reads are
+// conflict-free.  An inside chunk takes P/4 loads (instruction i: lane l carries
+// the 16 bytes at tile float 256*i + 4*l); a boundary chunk takes P clamped dword
+// loads into the same layout.  Output tiles use the same layout.
+template <int P>
+struct QuadTile {
+    static_assert(P == 8 || P == 16, "quad tiles hold 8 or 16 steps");
+    static constexpr int FLOATS = 64 * P;
+    static constexpr int NQ = P / 4;                // quads per row
+    static constexpr int ROWS_X4 = 64 / NQ;         // rows per 16-byte instruction
+    __device__ static int swz(int r) { return (r / (16 / NQ)) & (NQ - 1); }
+    __device__ static int slot(int r, int q) { return P * r + 4 * (q ^ swz(r)); }
+    // step of element e of the quad q
+    template <int DIR>
+    __device__ static constexpr int step(int q, int e) { return DIR > 0 ? 4 * q + e : 4 * q + 3 - e; }
+};
+
+// (row, column) of tile float f = 64*j + lane of the dword form, relative to i0.
+template <int P, int DIR>
+__device__ __forceinline__ void quad_cell(int f, int t_first, int& r, int& col) {
+    using Q = QuadTile<P>;
+    r = f / P;
+    const int s = f % P;
+    const int q = (s >> 2) ^ Q::swz(r);
+    col = t_first + DIR * Q::template step<DIR>(q, s & 3) - r;
+}
+
+// Byte offset in the matrix of the 16 bytes an inside chunk's instruction 0 moves
+// for this lane (the lowest column of the lane's quad); instruction i adds
+// i * ROWS_X4 * (L2max - 1) floats.
+template <int P, int DIR>
+__device__ __forceinline__ uint32_t quad_offset0(int i0, int L2max, int lane, int t_first) {
+    using Q = QuadTile<P>;
+    const int r = lane / Q::NQ;
+    const int q = (lane % Q::NQ) ^ Q::swz(r);
+    const int c_lo = DIR > 0 ? t_first + 4 * q - r : t_first - 4 * q - 3 - r;
+    return (uint32_t)((i0 + r) * L2max + c_lo) * 4u;
+}
+
+// Issues the loads of one chunk of a row-major [L1max][L2max] matrix into a quad tile.
+template <int P, int DIR>
+__device__ __forceinline__ void dma_quads(uint32_t tile_lds, const float* mbase, int i0,
+                                          int L1max, int L2max, int lane, int t_first) {
+    using Q = QuadTile<P>;
+    if (chunk_inside<P, DIR>(i0, L1max, L2max, t_first)) {
+        uint32_t voff = quad_offset0<P, DIR>(i0, L2max, lane, t_first);
+        const uint32_t vstep = (uint32_t)(Q::ROWS_X4 * (L2max - 1)) * 4u;
+#pragma unroll
+        for (int i = 0; i < Q::NQ; ++i) lds_dma_dwordx4<1024>(mbase, voff, tile_lds, vstep);
+    } else {
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            int r, col;
+            quad_cell<P, DIR>(64 * j + lane, t_first, r, col);
+            uint32_t voff = (uint32_t)(min(i0 + r, L1max - 1) * L2max +
+                                       min(max(col, 0), L2max - 1)) * 4u;
+            lds_dma_dword<256>(mbase, voff, tile_lds, 0u);
+        }
+    }
+}
+
+// The lane's P values (row = lane), in step order.
+template <int P, int DIR>
+__device__ __forceinline__ void read_quads(const float* tile, int lane, float (&v)[P]) {
+    using Q = QuadTile<P>;
+#pragma unroll
+    for (int q = 0; q < Q::NQ; ++q) {
+        const float4 x = *reinterpret_cast<const float4*>(tile + Q::slot(lane, q));
+        v[Q::template step<DIR>(q, 0)] = x.x;
+        v[Q::template step<DIR>(q, 1)] = x.y;
+        v[Q::template step<DIR>(q, 2)] = x.z;
+        v[Q::template step<DIR>(q, 3)] = x.w;
+    }
+}
+
+// Stores the lane's values of quad q (steps 4q .. 4q+3) into its row of the tile.
+template <int P, int DIR>
+__device__ __forceinline__ void put_quad(float* tile, int lane, int q, const float* v) {
+    using Q = QuadTile<P>;
+    float4 x;
+    x.x = v[Q::template step<DIR>(q, 0)];
+    x.y = v[Q::template step<DIR>(q, 1)];
+    x.z = v[Q::template step<DIR>(q, 2)];
+    x.w = v[Q::template step<DIR>(q, 3)];
+    *reinterpret_cast<float4*>(tile + Q::slot(lane, q)) = x;
+}
+
+// Writes a quad tile back to a row-major [L1max][L2max] matrix: P/4 16-byte stores
+// for an inside chunk (cells outside the element's lengths must hold 0), P dword
+// stores for a boundary chunk (cells outside the lengths go to the trash line).
+template <int P, int DIR>
+__device__ __forceinline__ void write_quads(const float* tile, float* obase, float* trash, int i0,
+                                            int L1, int L2, int L1max, int L2max, int lane,
+                                            int t_first) {
+    using Q = QuadTile<P>;
+    if (chunk_inside<P, DIR>(i0, L1max, L2max, t_first)) {
+        uint32_t off = quad_offset0<P, DIR>(i0, L2max, lane, t_first);
+        const uint32_t step = (uint32_t)(Q::ROWS_X4 * (L2max - 1)) * 4u;
+        float4 v[Q::NQ];
+#pragma unroll
+        for (int i = 0; i < Q::NQ; ++i)
+            v[i] = *reinterpret_cast<const float4*>(tile + 256 * i + 4 * lane);
+#pragma unroll
+        for (int i = 0; i < Q::NQ; ++i) {
+            *reinterpret_cast<float4*>(reinterpret_cast<char*>(obase) + off) = v[i];
+            off += step;
+            __asm__ volatile("" : "+v"(off));   // keep one running offset
+        }
+    } else {
+        float v[P];
+#pragma unroll
+        for (int j = 0; j < P; ++j) v[j] = tile[64 * j + lane];
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            int r, col;
+            quad_cell<P, DIR>(64 * j + lane, t_first, r, col);
+            const int row = i0 + r;
+            const bool in = row < L1 && col >= 0 && col < L2;
+            float* dst = in ? obase + (size_t)row * L2max + col : trash + lane;
+            *dst = v[j];
+        }
+    }
+}
+
+// Issues the loads of P consecutive steps of one plane of a skewed table with
+// 16-byte loads (four 256-byte step rows per instruction).  LDS row j then holds
+// step t_first + j for DIR = +1 and step t_first - (P - 1) + j for DIR = -1; read
+// step t_first + DIR*j at row rows_row<P, DIR>(j).
+template <int P, int DIR>
+__device__ __forceinline__ void dma_rows4(uint32_t rows_lds, const float* plane_base, int t_first,
+                                          unsigned ul4) {
+    static_assert(P % 4 == 0, "rows come in fours");
+    const int t_lo = DIR > 0 ? t_first : t_first - (P - 1);
+    uint32_t voff = (uint32_t)(t_lo + APAD) * 256u + 4u * ul4;
+#pragma unroll
+    for (int j = 0; j < P / 4; ++j) lds_dma_dwordx4<1024>(plane_base, voff, rows_lds, 1024u);
+}
+template <int P, int DIR>
+__device__ __host__ constexpr int rows_row(int j) { return DIR > 0 ? j : P - 1 - j; }
 
 // Zeroes the cells of a row-major [L1max][L2max] output outside [0,L1) x [0,L2),
 // with all threads of the workgroup.
