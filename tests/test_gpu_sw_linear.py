@@ -100,12 +100,15 @@ def test_sw_capi_config_c2_full_size(cuda):
     assert float(marg.min()) >= 0.0 and float(marg.max()) <= 1.0 + 1e-5
 
 
-def test_scale_by_batch(cuda):
-    src = _seeded(3, (5, 33, 17)).to(cuda)
-    g = _seeded(4, (5,)).to(cuda)
+@pytest.mark.parametrize("shape", [(5, 33, 17), (3, 64, 80), (2, 512, 512)])
+def test_scale_by_batch(cuda, shape):
+    """Scalar rows (33*17 floats), 16-byte rows with a partial last chunk (1280
+    float4s), and the C2 row length."""
+    src = _seeded(3, shape).to(cuda)
+    g = _seeded(4, (shape[0],)).to(cuda)
     out = _capi.scale_by_batch(src, g)
     torch.cuda.synchronize()
-    torch.testing.assert_close(out, g.view(5, 1, 1) * src, rtol=0, atol=0)
+    torch.testing.assert_close(out, g.view(-1, 1, 1) * src, rtol=0, atol=0)
 
 
 def test_soft_sw_api_value_backward(cuda):
