@@ -66,6 +66,16 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 // Online log-sum-exp accumulator in natural units with the exp2 scale c = log2(e)/T:
 // keeps (m, z) with  LSE = m + T*ln(z).
+// Sum of a[0..N) in a balanced tree (short dependency chain; N a power of two).
+template <int N, typename T>
+__device__ __forceinline__ T tree_sum(const T* a) {
+    if constexpr (N == 1) {
+        return a[0];
+    } else {
+        return tree_sum<N / 2>(a) + tree_sum<N / 2>(a + N / 2);
+    }
+}
+
 struct OnlineLSE {
     float m, z;
     __device__ __forceinline__ void init() { m = kNINF; z = 0.0f; }
@@ -81,6 +91,24 @@ struct OnlineLSE {
         z = up ? fmaf(z, e, 1.0f) : z + e;
         m = up ? x : m;
     }
+    // Adds N values at once: one rescale to the block's max, then N independent
+    // exp2 terms summed in a balanced tree (no serial chain through m and z).
+    template <int N>
+    __device__ __forceinline__ void add_block(const float* x, float c) {
+        float mx[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) mx[i] = x[i];
+#pragma unroll
+        for (int w = N / 2; w >= 1; w /= 2)
+#pragma unroll
+            for (int i = 0; i < w; ++i) mx[i] = fmaxf(mx[i], mx[i + w]);
+        const float M = fmaxf(m, mx[0]);
+        float e[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) e[i] = fast_exp2((x[i] - M) * c);
+        z = z * fast_exp2((m - M) * c) + tree_sum<N>(e);
+        m = M;
+    }
     __device__ __forceinline__ void merge(float m2, float z2, float c) {
         float M = fmaxf(m, m2);
         float za = (m <= kNINF) ? 0.0f : z * fast_exp2((m - M) * c);
@@ -95,16 +123,6 @@ __device__ __forceinline__ float wave_reduce(float v, Op op) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
     return v;
-}
-
-// Sum of a[0..N) in a balanced tree (short dependency chain; N a power of two).
-template <int N, typename T>
-__device__ __forceinline__ T tree_sum(const T* a) {
-    if constexpr (N == 1) {
-        return a[0];
-    } else {
-        return tree_sum<N / 2>(a) + tree_sum<N / 2>(a + N / 2);
-    }
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

@@ -113,7 +113,7 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             // stores of that chunk (the first chunk's load is the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<3 * P>();
             const float* tile = tiles + (k & 1) * Tile::FLOATS;
-            float sv[P];
+            float sv[P], aM[P], aI[P], aD[P];
 #pragma unroll
             for (int u = 0; u < P; ++u) sv[u] = tile[tbase + u];
             // lane 0's up values: column t0+j sits in lane j
@@ -154,10 +154,13 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 lane_store(outc + PLANE + u * 64, ul4, cI);
                 lane_store(outc + 2 * PLANE + u * 64, ul4, cD);
                 pub[u] = make_float4(cM, cI, cD, 0.0f);
-                acc.add(cM, c);
-                acc.add(cI, c);
-                acc.add(cD, c);
+                aM[u] = cM;
+                aI[u] = cI;
+                aD[u] = cD;
             }
+            acc.add_block<P>(aM, c);
+            acc.add_block<P>(aI, c);
+            acc.add_block<P>(aD, c);
             // the stripe's last row by step, per plane: three store instructions
             wave_lds_sync();
             if (lane < P) {

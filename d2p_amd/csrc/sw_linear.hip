@@ -93,7 +93,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             // that chunk (the first chunk's load is the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
             const float* tile = tiles + (k & 1) * Tile::FLOATS;
-            float sv[P];
+            float sv[P], av[P];
             read_quads<P, 1>(tile, lane, sv);
             // lane 0's up values: column t0+j sits in lane j (ring slot = producer step)
             float rreg = kNINF;
@@ -124,8 +124,9 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                 cur = ok ? a : kNINF;
                 lane_store(outc + u * 64, ul4, cur);
                 pub[u] = cur;
-                acc.add(cur, c);
+                av[u] = cur;
             }
+            acc.add_block<P>(av, c);
             // the stripe's last row (lane 63) by step, contiguous, for the reverse sweep
             // of the stripe below; one store instruction
             wave_lds_sync();

@@ -13,7 +13,9 @@ the reference sums sequentially in fp32.  The expected Jacobian is therefore the
 reference's sweep driven by dS/dtheta summed in double from the reference's own
 per-cell terms (oracle.param_grads64), and the tolerance adds the conditioning
 allowance 2e-6 * |dS/dtheta| / T * max(P): any two fp32 evaluations of dS/dtheta
-differ by ~1e-6 relative and every Jacobian entry moves by that error times P / T.
+differ by ~1e-6 relative and every Jacobian entry moves by that error times P / T;
+plus 3x the reference's own movement under half-ulp noise on the scores (the GPU's
+alphas and partition round differently).
 """
 import numpy as np
 import pytest
@@ -41,7 +43,19 @@ def _jacobian_ref(k, s, ptype, go, ge, T, lengths=None):
     dS = k.param_grads64("swa", s, lengths, go, ge, T)[:, ptype]
     J = k.swa_param_grad(alpha, s, part, dS.astype(np.float32), lengths, go, ge, T, ptype)
     allow = 2e-6 * np.abs(dS) / T * post.reshape(len(dS), -1).max(axis=1, initial=0.0)
-    return J, float(allow.max(initial=0.0))
+    return J, float(allow.max(initial=0.0)) + _noise_move(k, s, ptype, go, ge, T, lengths, J)
+
+
+def _noise_move(k, s, ptype, go, ge, T, lengths, J):
+    """3x the reference's own Jacobian movement under half-ulp noise on the scores:
+    any fp32 evaluation (the GPU's alphas and partition round differently) perturbs
+    the sweep by about that much."""
+    rng = np.random.default_rng(0)
+    sp = (s * (1 + 6e-8 * rng.standard_normal(s.shape))).astype(np.float32)
+    alpha, part = k.swa_forward(sp, lengths, go, ge, T)
+    dS = k.param_grads64("swa", sp, lengths, go, ge, T)[:, ptype]
+    Jp = k.swa_param_grad(alpha, sp, part, dS.astype(np.float32), lengths, go, ge, T, ptype)
+    return 3.0 * float(np.abs(Jp - J).max(initial=0.0))
 
 
 def _close(gpu, ref, what, extra=0.0):

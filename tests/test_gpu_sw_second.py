@@ -17,7 +17,8 @@ isolates the summation drift.  What remains is conditioning: any two fp32
 evaluations of dS/dtheta differ by ~1e-6 relative (the HIP terms against the
 reference's: 1.1e-6 at 100x120), and each Jacobian entry moves by that error
 times P / T.  The Jacobian tolerance therefore adds 2e-6 * |dS/dtheta| / T *
-max(P) to the 1e-4 contract.
+max(P) to the 1e-4 contract, plus 3x the reference's own movement under half-ulp
+noise on the scores (the GPU's alphas and partition round differently).
 """
 import numpy as np
 import pytest
@@ -44,7 +45,19 @@ def _jacobian_ref(k, s, ptype, gap, T, lengths=None):
     dS = k.param_grads64("sw", s, lengths, gap, T)[:, ptype]
     J = k.sw_param_grad(alpha, s, part, dS.astype(np.float32), lengths, gap, T, ptype)
     allow = 2e-6 * np.abs(dS) / T * post.reshape(len(dS), -1).max(axis=1, initial=0.0)
-    return J, float(allow.max(initial=0.0))
+    return J, float(allow.max(initial=0.0)) + _noise_move(k, s, ptype, gap, T, lengths, J)
+
+
+def _noise_move(k, s, ptype, gap, T, lengths, J):
+    """3x the reference's own Jacobian movement under half-ulp noise on the scores:
+    any fp32 evaluation (the GPU's alphas and partition round differently) perturbs
+    the sweep by about that much."""
+    rng = np.random.default_rng(0)
+    sp = (s * (1 + 6e-8 * rng.standard_normal(s.shape))).astype(np.float32)
+    alpha, part = k.sw_forward(sp, lengths, gap, T)
+    dS = k.param_grads64("sw", sp, lengths, gap, T)[:, ptype]
+    Jp = k.sw_param_grad(alpha, sp, part, dS.astype(np.float32), lengths, gap, T, ptype)
+    return 3.0 * float(np.abs(Jp - J).max(initial=0.0))
 
 
 def _close(gpu, ref, what, extra=0.0):
