@@ -21,9 +21,10 @@ Prints one JSON line with:
     rocprofv3 --pmc (FETCH_SIZE x2 calibration + WRITE_SIZE), read from
     profiles/<kernel>_<config>_pmc.md when that summary exists;
   * ``step_roofline``: the whole step at its algorithmic bytes;
-  * ``cpu_baseline`` (C2 only, rank 0): the reference's own CPU kernels
-    (oracle/_ref, built from the reference sources; else the C restatement)
-    run in the reference's autograd call sequence on the host cores.
+  * ``cpu_baseline``: the reference's own CPU kernels (oracle/_ref, built from
+    the reference sources; else the C restatement) run in the reference's autograd
+    call sequence on the host cores: the full batch for C2, a bounded sample of
+    the batch for the other configurations.
 Only one GPU is supported: ``--gpus`` above 1 exits with a message.
 """
 from __future__ import annotations
@@ -177,6 +178,58 @@ def measured_traffic(kernel, config):
     return float(m.group(1)) if m else None
 
 
+def cpu_baseline_config(cfg, max_elems):
+    """The reference CPU call sequence of a configuration on a bounded sample of its
+    batch (the first max_elems elements; parallel over the batch as the reference)."""
+    import numpy as np
+    from oracle import oracle as O
+    kind = "reference" if O.reference_available() else "port"
+    k = O.get("oracle" if kind == "port" else "reference")
+    n = max_elems
+    cores = max(1, min(16, os.cpu_count() or 1, n))
+    O.set_threads(cores)
+    name = cfg["name"]
+    x = {kk: v[:n].contiguous().numpy() for kk, v in cfg["inputs"].items()}
+    if name == "c3":
+        ln = x["lengths"]
+        cells = int((ln[:, 0].astype(np.int64) * ln[:, 1]).sum())
+
+        def step():
+            a, p = k.swa_forward(x["scores"], ln, -11.0, -1.0, 0.5)
+            k.swa_backward(a, x["scores"], p, ln, -11.0, -1.0, 0.5)
+            post = k.swa_backward(a, x["scores"], p, ln, -11.0, -1.0, 0.5)[0]
+            return post
+        what = "fwd + 2x bwd DP + scale"
+    elif name == "c4":
+        cells = x["costs"].size
+
+        def step():
+            a, sc = k.dtw_forward(x["costs"], None, 0.1)
+            k.dtw_backward(a, x["costs"], sc, None, 0.1)
+            return k.dtw_backward(a, x["costs"], sc, None, 0.1)[0]
+        what = "fwd + 2x bwd DP + scale"
+    elif name == "c5":
+        cells = x["scores"].size
+
+        def step():
+            a, p = k.sw_forward(x["scores"], None, -1.0, 1.0)
+            k.sw_backward(a, x["scores"], p, None, -1.0, 1.0)
+            return k.sw_backward(a, x["scores"], p, None, -1.0, 1.0)[0]
+        what = "fwd + 2x bwd DP + scale"
+    else:
+        cells = x["scores"].size
+
+        def step():
+            a, p = k.sw_forward(x["scores"], None, -1.0, 1.0)
+            return k.sw_hvp(a, x["scores"], p, x["V"], None, -1.0, 1.0)[0]
+        what = "fwd + HVP sweeps"
+    t0 = time.perf_counter()
+    step()
+    t = time.perf_counter() - t0
+    return {"value": cells / t, "unit": "cells/s", "cores": cores, "kind": kind,
+            "sample": f"first {n} batch elements, {what}, one timed run ({t:.2f} s)"}
+
+
 def cpu_baseline(scores_np, runs=3):
     """The reference CPU path timed on the host: per step, SoftSWRegularCPUFunction
     runs forward + backward DP in its forward and the backward DP again in its
@@ -282,8 +335,12 @@ def main():
                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": step_gbs / HBM_PEAK_GBS},
         "kernels_ms": {k: round(v["avg_ms"], 5) for k, v in kstats.items()},
     }
-    if cfg["name"] == "c2" and not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(cfg["inputs"]["scores"].numpy())
+    if not args.no_cpu_baseline:
+        if cfg["name"] == "c2":
+            out["cpu_baseline"] = cpu_baseline(cfg["inputs"]["scores"].numpy())
+        else:
+            sample = {"c3": 16, "c4": 64, "c5": 1, "c5hvp": 1}[cfg["name"]]
+            out["cpu_baseline"] = cpu_baseline_config(cfg, sample)
     print(json.dumps(out), flush=True)
 
 
