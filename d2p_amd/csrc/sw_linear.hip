@@ -105,27 +105,37 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             // other lanes write into the sink (R is a multiple of P: no wrap in a chunk)
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             float* outc = out + (size_t)t0 * 64;
+            // FULL: every cell of the chunk lies inside the element, no validity masks
+            auto steps = [&](auto full) {
+                constexpr bool FULL = decltype(full)::value;
 #pragma unroll
-            for (int u = 0; u < P; ++u) {
-                const int t = t0 + u;
-                const float up = wave_shr1_or(cur, rreg);   // lane 0: stripe above
-                rreg = wave_shl1(rreg, kNINF);
-                const float diag = up_prev;
-                up_prev = up;
-                // out-of-table neighbours are NINF, so no i>1 / j>1 guards are needed
-                const float vd = diag + sv[u];
-                const float vu = up + gap;
-                const float vl = cur + gap;
-                const float m = fmaxf(fmaxf(vd, vu), fmaxf(vl, sv[u]));
-                const float sum = fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c) +
-                                  fast_exp2((vl - m) * c) + fast_exp2((sv[u] - m) * c);
-                const float a = m + tl * fast_log2(sum);
-                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
-                cur = ok ? a : kNINF;
-                lane_store(outc + u * 64, ul4, cur);
-                pub[u] = cur;
-                av[u] = cur;
-            }
+                for (int u = 0; u < P; ++u) {
+                    const int t = t0 + u;
+                    const float up = wave_shr1_or(cur, rreg);   // lane 0: stripe above
+                    rreg = wave_shl1(rreg, kNINF);
+                    const float diag = up_prev;
+                    up_prev = up;
+                    // out-of-table neighbours are NINF, so no i>1 / j>1 guards are needed
+                    const float vd = diag + sv[u];
+                    const float vu = up + gap;
+                    const float vl = cur + gap;
+                    const float m = fmaxf(fmaxf(vd, vu), fmaxf(vl, sv[u]));
+                    const float sum = (fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c)) +
+                                      (fast_exp2((vl - m) * c) + fast_exp2((sv[u] - m) * c));
+                    const float a = m + tl * fast_log2(sum);
+                    if (FULL) {
+                        cur = a;
+                    } else {
+                        const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
+                        cur = ok ? a : kNINF;
+                    }
+                    lane_store(outc + u * 64, ul4, cur);
+                    pub[u] = cur;
+                    av[u] = cur;
+                }
+            };
+            if (i0 + 63 < L1 && t0 >= 63 && t0 + P <= L2) steps(std::true_type{});
+            else steps(std::false_type{});
             acc.add_block<P>(av, c);
             // the stripe's last row (lane 63) by step, contiguous, for the reverse sweep
             // of the stripe below; one store instruction
@@ -277,10 +287,13 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             Acc gs[P], ps[P];
             float pre_d2 = wave_shr1(pre_d, 0.0f);   // lane 63 = step 1 (then shifted on)
             pre_d2 = wave_shr1(pre_d2, 0.0f);        // lane 63 = step 2
+            // FULL: every cell of the chunk lies inside the element, no validity masks
+            auto steps = [&](auto full) {
+            constexpr bool FULL = decltype(full)::value;
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t_hi - u;
-                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
+                const bool ok = FULL || (unsigned)(t - lane) < (unsigned)L2eff;
                 // cells outside the element hold arbitrary tensor data: neutralise them
                 const float sc = ok ? sv[u] : kNINF;
                 const float a0 = A[u], a1 = A[u + 1];
@@ -317,6 +330,10 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 in_diag_next = wave_shl1_or(od, pre_d2);
                 pre_d2 = wave_shr1(pre_d2, 0.0f);
             }
+            };
+            if (i0 + 63 < L1 && t_hi - P - 62 >= 0 && t_hi < L2) steps(std::true_type{});
+            else steps(std::false_type{});
+
             // the chunk's parameter-gradient terms: balanced sums, then one add each
             g_acc += tree_sum<P>(gs);
             p_acc += tree_sum<P>(ps);
