@@ -348,6 +348,9 @@ __device__ __forceinline__ void write_tile(const float* tile, float* obase, floa
 // loads into the same layout.  Output tiles use the same layout.
 template <int P>
 struct QuadTile {
+    // swz has a period of 16 rows, which divides the 64/NQ rows one 16-byte
+    // instruction covers: successive instructions see the same swizzle per lane (the
+    // running-offset loads rely on it)
     static_assert(P == 8 || P == 16, "quad tiles hold 8 or 16 steps");
     static constexpr int FLOATS = 64 * P;
     static constexpr int NQ = P / 4;                // quads per row
