@@ -19,6 +19,8 @@
 
 #include <vector>
 
+#include <type_traits>
+
 #include "wavefront.hip.h"
 #include "../../include/d2p_amd.h"
 #include "capi_util.hip.h"
@@ -117,6 +119,9 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                                L2max, lane, t0 + P);
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             float* outc = out + (size_t)t0 * 64;
+            // FULL: every cell of the chunk lies inside the element, no validity masks
+            auto steps = [&](auto full) {
+            constexpr bool FULL = decltype(full)::value;
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t0 + u;
@@ -130,12 +135,15 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                                 fast_exp2((m - cur) * c);
                 const float a = cv[u] + (m - tl * fast_log2(z));
                 const int col = t - lane;
-                const bool ok = (unsigned)col < (unsigned)L2eff && in_band(ej, col + 1, bw);
+                const bool ok = FULL || ((unsigned)col < (unsigned)L2eff && in_band(ej, col + 1, bw));
                 cur = ok ? a : kPINF;
                 lane_store(outc + u * 64, ul4, cur);
                 pub[u] = cur;
                 if (ok && last_row && col == L2 - 1) terminal = cur;
             }
+            };
+            if (bw < 0 && i0 + 63 < L1 && t0 >= 63 && t0 + P <= L2) steps(std::true_type{});
+            else steps(std::false_type{});
             // the stripe's last row (lane 63) by step, contiguous, for the reverse sweep
             // of the stripe below; one store instruction
             wave_lds_sync();
@@ -256,11 +264,14 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
             }
             float pre_d2 = wave_shr1(pre_d, 0.0f);
             pre_d2 = wave_shr1(pre_d2, 0.0f);
+            // FULL: every cell of the chunk lies inside the element, no validity masks
+            auto steps = [&](auto full) {
+            constexpr bool FULL = decltype(full)::value;
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t_hi - u;
                 const int col = t - lane;
-                const bool ok = (unsigned)col < (unsigned)L2eff && in_band(ej, col + 1, bw);
+                const bool ok = FULL || ((unsigned)col < (unsigned)L2eff && in_band(ej, col + 1, bw));
                 const float a0 = A[u], a1 = A[u + 1];
                 const float bv_next = wave_shl1(bv, kPINF);
                 const float upa = wave_shr1_or(a1, bv);
@@ -291,6 +302,9 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
                 in_diag_next = wave_shl1_or(od, pre_d2);
                 pre_d2 = wave_shr1(pre_d2, 0.0f);
             }
+            };
+            if (bw < 0 && i0 + 63 < L1 && t_hi - P - 62 >= 0 && t_hi < L2) steps(std::true_type{});
+            else steps(std::false_type{});
             wave_lds_sync();
             write_tile<P, -1>(tile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             publish(prog, wave, q * PROG_STRIDE + k + 1);

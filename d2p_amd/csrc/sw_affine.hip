@@ -22,6 +22,8 @@
 
 #include <vector>
 
+#include <type_traits>
+
 #include "wavefront.hip.h"
 #include "../../include/d2p_amd.h"
 #include "capi_util.hip.h"
@@ -129,6 +131,9 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                                L2max, lane, t0 + P);
             float4* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             float* outc = out + (size_t)t0 * 64;
+            // FULL: every cell of the chunk lies inside the element, no validity masks
+            auto steps = [&](auto full) {
+            constexpr bool FULL = decltype(full)::value;
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t0 + u;
@@ -146,7 +151,7 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const float M = lse4(dM + sc, dI + sc, dD + sc, sc, c, tl);
                 const float I = lse2(uM + go, uI + ge, c, tl);
                 const float D = lse2(cM + go, cD + ge, c, tl);
-                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
+                const bool ok = FULL || (unsigned)(t - lane) < (unsigned)L2eff;
                 cM = ok ? M : kNINF;
                 cI = ok ? I : kNINF;
                 cD = ok ? D : kNINF;
@@ -158,6 +163,9 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 aI[u] = cI;
                 aD[u] = cD;
             }
+            };
+            if (i0 + 63 < L1 && t0 >= 63 && t0 + P <= L2) steps(std::true_type{});
+            else steps(std::false_type{});
             acc.add_block<P>(aM, c);
             acc.add_block<P>(aI, c);
             acc.add_block<P>(aD, c);
@@ -355,10 +363,13 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
             qDM = wave_shr1(wave_shr1(qDM, 0.0f), 0.0f);
             qDI = wave_shr1(wave_shr1(qDI, 0.0f), 0.0f);
             qDD = wave_shr1(wave_shr1(qDD, 0.0f), 0.0f);
+            // FULL: every cell of the chunk lies inside the element, no validity masks
+            auto steps = [&](auto full) {
+            constexpr bool FULL = decltype(full)::value;
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t_hi - u;
-                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
+                const bool ok = FULL || (unsigned)(t - lane) < (unsigned)L2eff;
                 // cells outside the element hold arbitrary tensor data: neutralise them
                 const float sc = ok ? sv[u] : kNINF;
                 // predecessors: left = own previous step, up / diagonal = lane r-1 (lane 0:
@@ -430,6 +441,9 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 qDI = wave_shr1(qDI, 0.0f);
                 qDD = wave_shr1(qDD, 0.0f);
             }
+            };
+            if (i0 + 63 < L1 && t_hi - P - 62 >= 0 && t_hi < L2) steps(std::true_type{});
+            else steps(std::false_type{});
             wave_lds_sync();
             write_tile<P, -1>(otile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             publish(prog, wave, q * PROG_STRIDE + k + 1);
