@@ -13,6 +13,9 @@ void set_last_error(const char* fmt, ...);
 bool profiling_enabled();
 void profile_begin(hipStream_t stream, hipEvent_t* start);
 void profile_end(const char* name, hipStream_t stream, hipEvent_t start);
+
+// Compute units of the current device (cached per device; 0 if unknown).
+int device_cus();
 }
 
 // Launches `kernel` and, when profiling is on, times it with events on `stream`.

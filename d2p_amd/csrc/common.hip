@@ -3,6 +3,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <string>
@@ -59,6 +60,19 @@ void resolve_pending_locked() {
 }  // namespace
 
 bool profiling_enabled() { return g_prof_on; }
+
+int device_cus() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        cached[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
 
 void profile_begin(hipStream_t stream, hipEvent_t* start) {
     if (hipEventCreate(start) != hipSuccess) { *start = nullptr; return; }

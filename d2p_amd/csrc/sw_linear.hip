@@ -17,6 +17,8 @@
 // previous step, in the reference's accumulation order
 //   beta = ((beta_init + from(i+1,j+1)) + from(i,j+1)) + from(i+1,j).
 
+#include <atomic>
+#include <cstdlib>
 #include <type_traits>
 #include <vector>
 
@@ -33,28 +35,45 @@ using namespace wf;
 constexpr int PF = 16;               // steps per chunk, forward sweep
 constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do not publish
 
+// Tag of the progress words: the launch's epoch in the high half, a marker and the
+// chunks done in the low half.
+__device__ __forceinline__ uint64_t progress_word(uint32_t epoch, int chunks) {
+    return ((uint64_t)epoch << 32) | (uint32_t)chunks;
+}
+
+// One part (G > 1: a workgroup owns stripes [part*SPW, part*SPW + SPW) of its element;
+// G == 1: all of them).  The first stripe of a part > 0 reads the last row of the
+// previous part's last stripe from `brow` (device-coherent loads, one chunk ahead)
+// after that part's progress word allows it; the last stripe of a part publishes its
+// own word two chunks behind its stores.  G == 1 writes the partition; G > 1 writes
+// the part's (max, scaled sum) for sw_partition_merge.
 __global__ void __launch_bounds__(NW * 64)
 sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                   float* __restrict__ alpha_sk, float* __restrict__ brow,
-                  float* __restrict__ partition,
-                  int* __restrict__ status, int L1max, int L2max, int NSmax, float gap, float T,
-                  int R) {
+                  float* __restrict__ partition, int* __restrict__ status,
+                  uint64_t* __restrict__ fflag, float2* __restrict__ fpart, int B, int L1max,
+                  int L2max, int NSmax, float gap, float T, int R, int G, int SPW,
+                  uint32_t epoch) {
     constexpr int P = PF;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red_m[NW], red_z[NW];
-    const int b = blockIdx.x;
+    int b, part;
+    split_decode(blockIdx.x, G, b, part);
+    if (b >= B) return;
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = QuadTile<P>;
-    float* tiles = smem + wave * 2 * Tile::FLOATS;         // double-buffered score chunk
-    float* rings = smem + NW * 2 * Tile::FLOATS;           // [NW][R]
-    float* sink = rings + NW * R + wave * DUMMY;       // per-wave write sink
+    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 64;        // two score chunks, two rows
+    float* tiles = smem + wave * WBUF;                     // double-buffered score chunk
+    float* rbufs = tiles + 2 * Tile::FLOATS;               // boundary row of a chunk
+    float* rings = smem + NW * WBUF;                       // [NW][R]
+    float* sink = rings + NW * R + wave * DUMMY;           // per-wave write sink
     int* st = status + b;
 
     if (lane == 0) prog[wave] = -1;
-    if (threadIdx.x == 0) *st = 0;
+    if (G == 1 && threadIdx.x == 0) *st = 0;               // G > 1: reset before the launch
     __syncthreads();
 
     const int L1 = min(max(lengths[2 * b], 0), L1max);
@@ -66,41 +85,76 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     const int nch = (nsteps + P - 1) / P;
     const size_t NT = (size_t)stored_steps(L2max);
     const float* sbase = scores + (size_t)b * L1max * L2max;
+    const int s_begin = part * SPW;
+    const int NL = max(min(NS, s_begin + SPW) - s_begin, 0);   // stripes of this part
+    const bool has_next = s_begin + NL < NS;
+    const uint64_t* flag_in = fflag + (size_t)b * G + (part > 0 ? part - 1 : 0);
+    uint64_t* flag_out = fflag + (size_t)b * G + part;
 
     OnlineLSE acc;
     acc.init_open();
 
-    for (int s = wave; s < NS; s += NW) {
-        set_pipeline_priority(s % NW);
+    for (int l = wave; l < NL; l += NW) {
+        const int s = s_begin + l;
+        set_pipeline_priority(l % NW);
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;   // rows past L1 are never valid
-        const float* ring_in = ring_from(rings, s, R);
-        float* ring_out = ring_of(rings, s, R);
+        const float* ring_in = ring_from(rings, l, R);
+        float* ring_out = ring_of(rings, l, R);
         // wave-uniform base (step 0) + 32-bit lane offset: scalar-base stores
         float* out = alpha_sk + (((size_t)b * NSmax + s) * NT + APAD) * 64;
         float* brow_s = brow + ((size_t)b * NSmax + s) * NT;   // last row, by step
+        const float* brow_up = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
+        const bool x_in = l == 0 && part > 0;      // row above from the previous part
+        const bool x_out = l == NL - 1 && has_next;  // last row feeds the next part
 #pragma unroll
         for (int t = -APAD; t < 0; ++t) lane_store(out + t * 64, ul4, kNINF);
         wave_lds_sync();   // the previous stripe's tile reads are complete
         const uint32_t tile_lds = lds_address(tiles);
+        const uint32_t row_lds = lds_address(rbufs);
+        // the boundary row of chunk k: lane j < P carries the step kP + 63 + j
+        auto issue_row = [&](int k) {
+            uint32_t off = (uint32_t)min(k * P + 63 + min(lane, P - 1), nsteps - 1) * 4u;
+            uint32_t dst = row_lds + (uint32_t)((k & 1) * 64 * 4);
+            lds_dma_dword_sys<0>(brow_up, off, dst, 0u);
+        };
+        int seen = -1;       // chunks of the previous part known to be complete
+        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
+        if (x_in) {
+            seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
+            issue_row(0);
+        }
         dma_quads<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
         float cur = kNINF, up_prev = kNINF;
 
         for (int k = 0; k < nch; ++k) {
             const int t0 = k * P;
-            chunk_waits<P>(prog, s, NS, k, nch, R, st);
-            // this chunk's scores: loaded one chunk ago, followed by the P + 1 stores of
-            // that chunk (the first chunk's load is the last issued)
+            chunk_waits<P>(prog, l, NL, k, nch, R, st);
+            // this chunk's loads were issued one chunk ago and followed by at least the
+            // P + 1 stores of that chunk (the first chunk's loads are the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (x_in && k > 0) {
+                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
+                const int got = flag_chunks(fl, epoch);
+                seen = got > seen ? got : seen;
+            }
             const float* tile = tiles + (k & 1) * Tile::FLOATS;
             float sv[P], av[P];
             read_quads<P, 1>(tile, lane, sv);
             // lane 0's up values: column t0+j sits in lane j (ring slot = producer step)
             float rreg = kNINF;
-            if (s > 0 && lane < P) rreg = ring_in[ring_index(t0 + lane + 63, R)];
-            if (k + 1 < nch)
+            if (s > 0 && lane < P)
+                rreg = x_in ? rbufs[(k & 1) * 64 + lane] : ring_in[ring_index(t0 + lane + 63, R)];
+            if (k + 1 < nch) {
+                if (x_in) {
+                    const int need = min(k + 1 + lead(P), nch);
+                    if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                    issue_row(k + 1);
+                }
                 dma_quads<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0, L1max,
                                   L2max, lane, t0 + P);
+                if (x_in) fl = load_flag_async(flag_in);
+            }
             // lane 63 publishes its alpha of step u into ring slot (t0+u) % R; the
             // other lanes write into the sink (R is a multiple of P: no wrap in a chunk)
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
@@ -138,23 +192,69 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             else steps(std::false_type{});
             acc.add_block<P>(av, c);
             // the stripe's last row (lane 63) by step, contiguous, for the reverse sweep
-            // of the stripe below; one store instruction
+            // of the stripe below and the next part; one store instruction
             wave_lds_sync();
-            if (lane < P) lane_store(brow_s, (unsigned)(t0 + lane) * 4u, ring_out[t0 % R + lane]);
-            publish(prog, wave, s * PROG_STRIDE + k + 1);
+            if (lane < P) {
+                const float v = ring_out[t0 % R + lane];
+                if (x_out) store_sys(brow_s + t0 + lane, v);
+                else lane_store(brow_s, (unsigned)(t0 + lane) * 4u, v);
+            }
+            publish(prog, wave, l * PROG_STRIDE + k + 1);
+            if (x_out && k >= 2) {
+                // at least 2 * (P/4 + P + 1) vector-memory operations follow the row
+                // stores of chunk k - 2: those (and everything before) are complete
+                wait_vmcnt<2 * (Tile::NQ + P + 1) - Tile::NQ>();
+                if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
+            }
+        }
+        if (x_out) {
+            wait_vmcnt<0>();
+            if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
         }
     }
 
-    // partition: merge lanes, waves, and the cell (0,0) whose alpha is 0
+    // partition: merge lanes, waves, and (once per element) the cell (0,0) whose alpha is 0
     wave_merge_lse(acc, c);
     if (lane == 0) { red_m[wave] = acc.m; red_z[wave] = acc.z; }
     __syncthreads();
     if (threadIdx.x == 0) {
         OnlineLSE tot;
-        tot.m = 0.0f;
-        tot.z = 1.0f;
+        if (G == 1) {
+            tot.m = 0.0f;
+            tot.z = 1.0f;
+        } else {
+            tot.init();
+        }
         for (int w = 0; w < NW; ++w) tot.merge(red_m[w], red_z[w], c);
-        partition[b] = tot.m + tl * fast_log2(tot.z);
+        if (G == 1) partition[b] = tot.m + tl * fast_log2(tot.z);
+        else fpart[(size_t)b * G + part] = make_float2(tot.m, tot.z);
+    }
+}
+
+// partition[b] of a split element: the parts' (max, scaled sum) and the cell (0,0).
+__global__ void sw_partition_merge(const float2* __restrict__ fpart, float* __restrict__ partition,
+                                   int B, int G, float T) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    const float c = kLog2e / T;
+    OnlineLSE tot;
+    tot.m = 0.0f;
+    tot.z = 1.0f;
+    for (int g = 0; g < G; ++g) {
+        const float2 v = fpart[(size_t)b * G + g];
+        tot.merge(v.x, v.y, c);
+    }
+    partition[b] = tot.m + T * kLn2 * fast_log2(tot.z);
+}
+
+// Status words and progress words of split elements start at zero.
+__global__ void split_reset(int* __restrict__ status, uint64_t* __restrict__ fflag,
+                            uint64_t* __restrict__ bflag, int B, int G) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < B) status[i] = 0;
+    if (i < B * G) {
+        store_flag(fflag + i, 0);
+        store_flag(bflag + i, 0);
     }
 }
 
@@ -167,12 +267,19 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                    const float* __restrict__ partition,
                    float* __restrict__ post, float* __restrict__ grad_gap,
                    float* __restrict__ grad_T, int* __restrict__ status, float* __restrict__ trash,
-                   int L1max, int L2max, int NSmax, float gap, float T, int R) {
-        extern __shared__ float smem[];
+                   uint64_t* __restrict__ bflag, float2* __restrict__ flows,
+                   double* __restrict__ bpart, int B, int L1max, int L2max, int NSmax, float gap,
+                   float T, int R, int G, int SPW, uint32_t epoch) {
+    extern __shared__ float smem[];
     __shared__ int prog[NW];
     using Acc = typename std::conditional<PRECISE, double, float>::type;
     __shared__ Acc red_g[NW], red_p[NW];
-    const int b = blockIdx.x;
+    // parts run bottom-up: the part below (the producer of this one's flows) is
+    // dispatched first
+    int b, dpart;
+    split_decode(blockIdx.x, G, b, dpart);
+    if (b >= B) return;
+    const int part = G - 1 - dpart;
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -182,7 +289,9 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     using Tile = QuadTile<P>;
     constexpr int ABUF = Tile::FLOATS;            // alpha rows
     constexpr int RBUF = ABUF + P * 64;           // row above
-    constexpr int BUF = RBUF + 64;
+    constexpr int FBUF = RBUF + 64;               // flows from the part below (2P+2 floats)
+    constexpr int BUF = FBUF + 64;
+    static_assert(2 * P + 2 <= 64, "boundary flows fit their buffer");
     float* bufs = smem + wave * 2 * BUF;
     float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * BUF);  // [NW][R] (up, diag)
     float2* sink = rings + NW * R + wave * DUMMY;
@@ -207,15 +316,25 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     const float* sbase = scores + (size_t)b * L1max * L2max;
     float* pbase = post + (size_t)b * L1max * L2max;
 
-    zero_padding(pbase, L1, L2, L1max, L2max, NW * 64);
+    {   // each part zeroes its share of the rows' padding
+        const int rows = (L1max + G - 1) / G;
+        zero_padding(pbase, L1, L2, L1max, L2max, NW * 64, part * rows,
+                     min(L1max, part * rows + rows));
+    }
 
     Acc g_acc = 0, p_acc = 0;
     float A[P + 2];
+    const int s_begin = part * SPW;
+    const int NL = max(min(NS, s_begin + SPW) - s_begin, 0);   // stripes of this part
+    const bool has_next = s_begin + NL < NS;
+    const uint64_t* flag_in = bflag + (size_t)b * G + (part + 1 < G ? part + 1 : part);
+    uint64_t* flag_out = bflag + (size_t)b * G + part;
 
-    // Stripes run bottom-up: order q = 0..NS-1 handles stripe NS-1-q, on wave q % NW.
-    for (int q = wave; q < NS; q += NW) {
+    // Stripes run bottom-up: order q = 0..NL-1 handles stripe s_begin+NL-1-q, on wave
+    // q % NW.
+    for (int q = wave; q < NL; q += NW) {
         set_pipeline_priority(q % NW);
-        const int s = NS - 1 - q;
+        const int s = s_begin + NL - 1 - q;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
         // alpha tables of this stripe and of the one above, from step -APAD
@@ -223,7 +342,15 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
         const float2* ring_in = ring_from(rings, q, R);   // from stripe s+1
         float2* ring_out = ring_of(rings, q, R);          // to stripe s-1
-        const bool below = q > 0;
+        const bool x_in = q == 0 && has_next;             // flows from the part below
+        const bool x_out = q == NL - 1 && part > 0;       // flows to the part above
+        const bool below = q > 0 || x_in;
+        // boundary flows by producer step: written by stripe s (x_out), read from s + 1
+        float2* flows_out = flows + ((size_t)b * NSmax + s) * NT;
+        const float* flows_in =
+            reinterpret_cast<const float*>(flows + ((size_t)b * NSmax + (x_in ? s + 1 : s)) * NT);
+        int seen = -1;       // chunks of the part below known to be complete
+        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
 
         // Loads of chunk k (t_hi = nsteps-1-kP) into buffer k&1: the score quad tile, P
         // alpha rows (steps t_hi-2 .. t_hi-P-1, four per load), and the row-above values
@@ -237,6 +364,14 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
             uint32_t rl = buf + RBUF * 4;
             lds_dma_dword<0>(bup, roff, rl, 0u);
+            if (x_in) {
+                // flows of producer slots kP+62 .. kP+62+P (float2 each): float f of the
+                // range in lane f, clamped to the last slot
+                uint32_t foff = (uint32_t)min((k * P + 62) * 2 + min(lane, 2 * P + 1),
+                                              (nsteps - 1) * 2 + 1) * 4u;
+                uint32_t fdst = buf + FBUF * 4;
+                lds_dma_dword_sys<0>(flows_in, foff, fdst, 0u);
+            }
         };
 
         // the first two alphas of chunk 0 (steps nsteps-1, nsteps-2); later chunks
@@ -245,15 +380,21 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         A[P + 1] = lane_load(astripe + (size_t)(nsteps - 2 + APAD) * 64, ul4);
         __asm__ volatile("" ::"v"(A[P]), "v"(A[P + 1]));   // completes the two loads here
         wave_lds_sync();   // the previous stripe's buffer reads are complete
+        if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
         issue_chunk(0);
         float in_left = 0.0f, in_up = 0.0f, in_diag = 0.0f, in_diag_next = 0.0f;
 
         for (int k = 0; k < nch; ++k) {
             const int t_hi = nsteps - 1 - k * P;
-            chunk_waits<P>(prog, q, NS, k, nch, R, st);
+            chunk_waits<P>(prog, q, NL, k, nch, R, st);
             // this chunk's loads were issued one chunk ago and followed by exactly the P
             // marginal stores of that chunk (the first chunk's are the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (x_in && k > 0) {
+                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
+                const int got = flag_chunks(fl, epoch);
+                seen = got > seen ? got : seen;
+            }
             float* buf = bufs + (k & 1) * BUF;
             float sv[P];
             read_quads<P, -1>(buf, lane, sv);
@@ -272,10 +413,22 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             float pre_u = 0.0f, pre_d = 0.0f;
             if (below && lane >= 64 - P) {
                 const int j = 63 - lane;
-                pre_u = ring_in[ring_index(k * P + j + 63, R)].x;
-                pre_d = ring_in[ring_index(k * P + j + 62, R)].y;
+                if (x_in) {
+                    pre_u = buf[FBUF + 2 * (j + 1)];
+                    pre_d = buf[FBUF + 2 * j + 1];
+                } else {
+                    pre_u = ring_in[ring_index(k * P + j + 63, R)].x;
+                    pre_d = ring_in[ring_index(k * P + j + 62, R)].y;
+                }
             }
-            if (k + 1 < nch) issue_chunk(k + 1);
+            if (k + 1 < nch) {
+                if (x_in) {
+                    const int need = min(k + 1 + lead(P), nch);
+                    if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                }
+                issue_chunk(k + 1);
+                if (x_in) fl = load_flag_async(flag_in);
+            }
             // lane 0 publishes (up, diag) of step u into slot (kP+u) % R
             float2* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
             // lane 63 starts the chunk with the ring's values for steps 0 and 1
@@ -343,6 +496,20 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             // line in boundary chunks, and carry 0 in inside chunks)
             write_tile<P, -1>(buf, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             publish(prog, wave, q * PROG_STRIDE + k + 1);
+            if (x_out) {
+                // this chunk's flows to the part above, by producer step
+                if (lane < P) store_sys2(flows_out + k * P + lane, ring_out[ring_index(k * P, R) + lane]);
+                if (k >= 2) {
+                    // at least 2 * (P/4 + P + 1) + P + 3 vector-memory operations follow
+                    // the flow stores of chunk k - 2: those are complete
+                    wait_vmcnt<2 * Tile::NQ + 2 * P + 3>();
+                    if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
+                }
+            }
+        }
+        if (x_out) {
+            wait_vmcnt<0>();
+            if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
         }
     }
 
@@ -353,9 +520,31 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     if (threadIdx.x == 0) {
         Acc g = 0, p = 0;
         for (int w = 0; w < NW; ++w) { g += red_g[w]; p += red_p[w]; }
-        grad_gap[b] = (float)g;
-        grad_T[b] = (float)(((Acc)S - (p + g * (Acc)gap)) / (Acc)T);
+        if (G == 1) {
+            grad_gap[b] = (float)g;
+            grad_T[b] = (float)(((Acc)S - (p + g * (Acc)gap)) / (Acc)T);
+        } else {
+            bpart[((size_t)b * G + part) * 2] = (double)g;
+            bpart[((size_t)b * G + part) * 2 + 1] = (double)p;
+        }
     }
+}
+
+// grad_gap[b], grad_T[b] of a split element from the parts' sums.
+template <bool PRECISE>
+__global__ void sw_grad_merge(const double* __restrict__ bpart, const float* __restrict__ partition,
+                              float* __restrict__ grad_gap, float* __restrict__ grad_T, int B,
+                              int G, float gap, float T) {
+    using Acc = typename std::conditional<PRECISE, double, float>::type;
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    Acc g = 0, p = 0;
+    for (int i = 0; i < G; ++i) {
+        g += (Acc)bpart[((size_t)b * G + i) * 2];
+        p += (Acc)bpart[((size_t)b * G + i) * 2 + 1];
+    }
+    grad_gap[b] = (float)g;
+    grad_T[b] = (float)(((Acc)partition[b] - (p + g * (Acc)gap)) / (Acc)T);
 }
 
 }  // namespace sw
@@ -367,22 +556,23 @@ namespace sw {
 namespace {
 constexpr size_t kLdsLimit = 160 * 1024 - 256;
 
-size_t lds_forward(int max_L1, int max_L2) {
-    const int R = wf::ring_len(max_L1, max_L2, 256);
-    return (size_t)wf::NW * 2 * 64 * PF * sizeof(float) +
+// LDS of one workgroup whose stripes' boundaries use rings of R columns
+size_t lds_forward_r(int R) {
+    return (size_t)wf::NW * (2 * 64 * PF + 2 * 64) * sizeof(float) +
            ((size_t)wf::NW * R + wf::NW * DUMMY) * sizeof(float);
 }
-
-size_t lds_backward(int max_L1, int max_L2, int P) {
-    const int R = wf::ring_len(max_L1, max_L2, 128);
-    return (size_t)wf::NW * 2 * (64 * P + 64 * P + 64) * sizeof(float) +
+size_t lds_backward_r(int R, int P) {
+    return (size_t)wf::NW * 2 * (64 * P + 64 * P + 64 + 64) * sizeof(float) +
            ((size_t)wf::NW * R + wf::NW * DUMMY) * sizeof(float2);
 }
+// rings of a workgroup that runs `rows` rows of stripes
+int ring_forward(int rows, int max_L2) { return wf::ring_len(rows, max_L2, 256); }
+int ring_backward(int rows, int max_L2) { return wf::ring_len(rows, max_L2, 128); }
 
 // backward: 16-step chunks when they fit in LDS, else 8-step chunks (long rows need
 // long rings)
-int backward_chunk(int max_L1, int max_L2) {
-    return lds_backward(max_L1, max_L2, 16) <= kLdsLimit ? 16 : 8;
+int backward_chunk(int rows, int max_L2) {
+    return lds_backward_r(ring_backward(rows, max_L2), 16) <= kLdsLimit ? 16 : 8;
 }
 }  // namespace
 
@@ -392,21 +582,62 @@ int check_shape(int B, int max_L1, int max_L2, float temperature) {
     D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 4, "max_L2 too large");
     // per-lane byte offsets within one batch element are 32-bit
     D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
-    D2P_REQUIRE(lds_forward(max_L1, max_L2) <= kLdsLimit &&
-                    lds_backward(max_L1, max_L2, backward_chunk(max_L1, max_L2)) <= kLdsLimit,
+    // an unsplit element is the longest pipeline a launch may run
+    const int Rb = ring_backward(max_L1, max_L2);
+    D2P_REQUIRE(lds_forward_r(ring_forward(max_L1, max_L2)) <= kLdsLimit &&
+                    lds_backward_r(Rb, backward_chunk(max_L1, max_L2)) <= kLdsLimit,
                 "sequence too long for the LDS stripe rings");
     return D2P_OK;
+}
+
+namespace {
+// One launch counter per process: the epoch that tags the launch's progress words.
+std::atomic<uint32_t> g_epoch{0};
+uint32_t next_epoch() {
+    uint32_t e = ++g_epoch;
+    return e != 0 ? e : ++g_epoch;
+}
+}  // namespace
+
+Split choose_split(int B, int max_L1, const Layout& ws) {
+    const int ns = (max_L1 + 63) / 64;
+    Split sp{1, ns > 0 ? ns : 1};
+    if (ws.fflag == nullptr || ns <= 1) return sp;
+    int G = 0;
+    if (const char* e = getenv("D2P_AMD_SPLIT")) G = atoi(e);
+    if (G <= 0) {
+        // one stripe per wave, while every part of the grid is resident at once
+        if (ns <= wf::NW) return sp;
+        G = (ns + wf::NW - 1) / wf::NW;
+        const int cus = device_cus();
+        while (G > 1 && wf::split_grid(B, G) > cus) --G;
+    }
+    G = G < ns ? G : ns;
+    if (G <= 1) return sp;
+    sp.SPW = (ns + G - 1) / G;
+    sp.G = (ns + sp.SPW - 1) / sp.SPW;   // no part without stripes
+    return sp;
 }
 
 int launch_forward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                    float gap, float T, const Layout& ws, float* partition, hipStream_t st) {
     const int ns = (max_L1 + 63) / 64;
-    const int R = wf::ring_len(max_L1, max_L2, 256);
-    const size_t lds = lds_forward(max_L1, max_L2);
+    const Split sp = choose_split(B, max_L1, ws);
+    const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
+    const size_t lds = lds_forward_r(R);
+    const uint32_t epoch = next_epoch();
+    if (sp.G > 1)
+        D2P_LAUNCH("split_reset", split_reset, dim3((B * sp.G + 255) / 256), dim3(256), 0, st,
+                   ws.status, ws.fflag, ws.bflag, B, sp.G);
     D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH("sw_forward", sw_forward_kernel, dim3(B), dim3(wf::NW * 64), lds, st, scores,
-               lengths, ws.alpha_sk, ws.brow, partition, ws.status, max_L1, max_L2, ns, gap, T, R);
+    D2P_LAUNCH("sw_forward", sw_forward_kernel, dim3(wf::split_grid(B, sp.G)),
+               dim3(wf::NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
+               ws.status, ws.fflag, ws.fpart, B, max_L1, max_L2, ns, gap, T, R, sp.G, sp.SPW,
+               epoch);
+    if (sp.G > 1)
+        D2P_LAUNCH("sw_partition_merge", sw_partition_merge, dim3((B + 255) / 256), dim3(256), 0,
+                   st, ws.fpart, partition, B, sp.G, T);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -414,15 +645,20 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
 template <int P, bool PRECISE>
 int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                       float gap, float T, const Layout& ws, const float* partition,
-                      float* marginals, float* grad_gap, float* grad_T, hipStream_t st) {
+                      float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
+                      const Split& sp, int R) {
     const int ns = (max_L1 + 63) / 64;
-    const int R = wf::ring_len(max_L1, max_L2, 128);
-    const size_t lds = lds_backward(max_L1, max_L2, P);
+    const size_t lds = lds_backward_r(R, P);
+    const uint32_t epoch = next_epoch();
     D2P_HIP(hipFuncSetAttribute((const void*)sw_backward_kernel<P, PRECISE>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH("sw_backward", (sw_backward_kernel<P, PRECISE>), dim3(B), dim3(wf::NW * 64), lds,
-               st, scores, lengths, ws.alpha_sk, ws.brow, partition, marginals, grad_gap, grad_T,
-               ws.status, ws.trash, max_L1, max_L2, ns, gap, T, R);
+    D2P_LAUNCH("sw_backward", (sw_backward_kernel<P, PRECISE>), dim3(wf::split_grid(B, sp.G)),
+               dim3(wf::NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
+               marginals, grad_gap, grad_T, ws.status, ws.trash, ws.bflag, ws.flows, ws.bpart, B,
+               max_L1, max_L2, ns, gap, T, R, sp.G, sp.SPW, epoch);
+    if (sp.G > 1)
+        D2P_LAUNCH("sw_grad_merge", sw_grad_merge<PRECISE>, dim3((B + 255) / 256), dim3(256), 0,
+                   st, ws.bpart, partition, grad_gap, grad_T, B, sp.G, gap, T);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -431,16 +667,16 @@ int launch_backward(const float* scores, const int* lengths, int B, int max_L1, 
                     float gap, float T, const Layout& ws, const float* partition,
                     float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
                     bool precise) {
-    const int P = backward_chunk(max_L1, max_L2);
-    if (P == 16)
-        return precise ? launch_backward_p<16, true>(scores, lengths, B, max_L1, max_L2, gap, T, ws,
-                                                     partition, marginals, grad_gap, grad_T, st)
-                       : launch_backward_p<16, false>(scores, lengths, B, max_L1, max_L2, gap, T,
-                                                      ws, partition, marginals, grad_gap, grad_T, st);
-    return precise ? launch_backward_p<8, true>(scores, lengths, B, max_L1, max_L2, gap, T, ws,
-                                                partition, marginals, grad_gap, grad_T, st)
-                   : launch_backward_p<8, false>(scores, lengths, B, max_L1, max_L2, gap, T, ws,
-                                                 partition, marginals, grad_gap, grad_T, st);
+    const Split sp = choose_split(B, max_L1, ws);
+    const int rows = sp.G > 1 ? sp.SPW * 64 : max_L1;
+    const int R = ring_backward(rows, max_L2);
+    const int P = backward_chunk(rows, max_L2);
+#define D2P_SW_BWD(P_, PR_)                                                                   \
+    launch_backward_p<P_, PR_>(scores, lengths, B, max_L1, max_L2, gap, T, ws, partition,    \
+                               marginals, grad_gap, grad_T, st, sp, R)
+    if (P == 16) return precise ? D2P_SW_BWD(16, true) : D2P_SW_BWD(16, false);
+    return precise ? D2P_SW_BWD(8, true) : D2P_SW_BWD(8, false);
+#undef D2P_SW_BWD
 }
 
 }  // namespace sw
@@ -450,8 +686,9 @@ using namespace d2p_amd;
 
 extern "C" size_t d2p_sw_workspace_bytes(int B, int max_L1, int max_L2) {
     if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
-    // status words | trash line | skewed alpha table | last row of every stripe
-    return wf::layout(nullptr, B, max_L1, max_L2).bytes;
+    // status words | trash line | skewed alpha table | last row of every stripe |
+    // split-element progress words, boundary flows and partial sums
+    return wf::layout(nullptr, B, max_L1, max_L2, 1, true).bytes;
 }
 
 extern "C" int d2p_sw_status(const void* workspace, int B, int* status, void* stream) {
@@ -479,7 +716,7 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
     const size_t need = d2p_sw_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
-    const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2);
+    const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 1, true);
     int r = sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
                                partition, st);
     if (r != D2P_OK) return r;

@@ -81,10 +81,19 @@ struct Layout {
     float* trash;
     float* alpha_sk;   // [B][stripe][plane][step][64]
     float* brow;       // [B][stripe][plane][step]
+    // split elements (present when layout() is asked for them; up to one part per
+    // stripe): progress words of the forward and reverse boundaries [B][stripe],
+    // reverse-sweep boundary flows [B][stripe][step], per-part partial results
+    uint64_t* fflag;
+    uint64_t* bflag;
+    float2* flows;
+    float2* fpart;     // [B][stripe] (max, scaled sum) of the partition
+    double* bpart;     // [B][stripe][2] parameter-gradient sums
     size_t bytes;      // bytes of this prefix
 };
 
-__host__ inline Layout layout(void* workspace, int B, int max_L1, int max_L2, int planes = 1) {
+__host__ inline Layout layout(void* workspace, int B, int max_L1, int max_L2, int planes = 1,
+                              bool split = false) {
     Layout l;
     l.status = (int*)workspace;
     l.trash = (float*)((char*)workspace + status_bytes(B));
@@ -92,6 +101,24 @@ __host__ inline Layout layout(void* workspace, int B, int max_L1, int max_L2, in
     const size_t ns = ((size_t)max_L1 + 63) / 64;
     l.brow = l.alpha_sk + (size_t)B * ns * planes * stored_steps(max_L2) * 64;
     l.bytes = status_bytes(B) + TRASH_BYTES + table_floats(B, max_L1, max_L2, planes) * sizeof(float);
+    l.fflag = l.bflag = nullptr;
+    l.flows = l.fpart = nullptr;
+    l.bpart = nullptr;
+    if (split) {
+        char* p = (char*)workspace + round256(l.bytes);
+        const size_t parts = (size_t)B * (ns > 0 ? ns : 1);
+        l.fflag = (uint64_t*)p;
+        p += round256(parts * sizeof(uint64_t));
+        l.bflag = (uint64_t*)p;
+        p += round256(parts * sizeof(uint64_t));
+        l.flows = (float2*)p;
+        p += round256(parts * (size_t)stored_steps(max_L2) * sizeof(float2));
+        l.fpart = (float2*)p;
+        p += round256(parts * sizeof(float2));
+        l.bpart = (double*)p;
+        p += round256(parts * 2 * sizeof(double));
+        l.bytes = (size_t)(p - (char*)workspace);
+    }
     return l;
 }
 
@@ -104,6 +131,86 @@ __device__ __forceinline__ void set_pipeline_priority(int pos) {
     else if (pos < 4) __builtin_amdgcn_s_setprio(2);
     else if (pos < 6) __builtin_amdgcn_s_setprio(1);
     else __builtin_amdgcn_s_setprio(0);
+}
+
+// ---------------------------------------------------------------- split elements
+
+// An element's stripes may be divided among G workgroups ("parts"); part p owns the
+// stripes [p*SPW, (p+1)*SPW).  Inside a part the stripes form the LDS pipeline below;
+// between parts the boundary row (forward) or the boundary flows (reverse sweeps) go
+// through global memory with device-coherent (sc0 sc1) accesses, and a per-part
+// progress word ((epoch << 32) | chunks done) orders producer and consumer.  The
+// epoch is new for every launch, so stale words of earlier launches never match.
+// Workgroups are numbered so that the parts of one element share blockIdx % 8 (the
+// XCD on MI355X: their boundary traffic stays in one L2 in practice; correctness
+// does not depend on it) and every producer part has a lower index than its
+// consumer, so it is dispatched first.
+constexpr int XCDS = 8;
+
+__host__ __device__ inline int split_grid(int B, int G) {
+    return XCDS * ((B + XCDS - 1) / XCDS) * G;
+}
+
+// (element, part in dispatch order) of a workgroup; element >= B: idle workgroup.
+__device__ __forceinline__ void split_decode(int bid, int G, int& b, int& part) {
+    const int x = bid % XCDS, j = bid / XCDS;
+    b = x + XCDS * (j / G);
+    part = j % G;
+}
+
+// device-coherent global accesses (bypass the non-coherent caches)
+__device__ __forceinline__ void store_sys(float* p, float v) {
+    __asm__ volatile("global_store_dword %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_sys2(float2* p, float2 v) {
+    __asm__ volatile("global_store_dwordx2 %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_flag(uint64_t* p, uint64_t v) {
+    __asm__ volatile("global_store_dwordx2 %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
+}
+// issues the load; the value is valid after a vmcnt wait that covers it
+__device__ __forceinline__ uint64_t load_flag_async(const uint64_t* p) {
+    uint64_t v;
+    __asm__ volatile("global_load_dwordx2 %0, %1, off sc0 sc1" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+__device__ __forceinline__ uint64_t load_flag(const uint64_t* p) {
+    uint64_t v;
+    __asm__ volatile("global_load_dwordx2 %0, %1, off sc0 sc1\n\ts_waitcnt vmcnt(0)"
+                     : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+__device__ __forceinline__ int load_status(const int* p) {
+    int v;
+    __asm__ volatile("global_load_dword %0, %1, off sc0 sc1\n\ts_waitcnt vmcnt(0)"
+                     : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+
+// Chunks a progress word reports for this epoch (-1: an earlier launch's word).
+__device__ __forceinline__ int flag_chunks(uint64_t v, uint32_t epoch) {
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    return hi == epoch ? (int)lo : -1;
+}
+
+// Waits until the part's progress word reports `need` chunks of this epoch; returns
+// the chunks seen.  Bounded by wall time (0.2 s of the 100 MHz counter); on timeout,
+// or when another wave of the element has already timed out, the element's status
+// gets bit 0 and the wait gives up.
+__device__ __forceinline__ int wait_part(const uint64_t* flag, uint32_t epoch, int need,
+                                         int* status_b) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (true) {
+        const int got = flag_chunks(load_flag(flag), epoch);
+        if (got >= need) return got;
+        if (__builtin_amdgcn_readfirstlane(load_status(status_b)) != 0) return need;
+        if (__builtin_amdgcn_s_memrealtime() - t0 > 20000000ull) {
+            atomicOr(status_b, 1);
+            return need;
+        }
+        __builtin_amdgcn_s_sleep(8);
+    }
 }
 
 // ---------------------------------------------------------------- progress flags
@@ -193,6 +300,22 @@ __device__ __forceinline__ void lds_dma_dword(const float* sbase, uint32_t& voff
         : "s"(sbase), "s"(vstep), "n"(LDS_STEP)
         : "memory", "m0", "scc");
 }
+// The same with device-coherent (sc0 sc1) reads, for data another workgroup wrote
+// during this launch.
+template <int LDS_STEP>
+__device__ __forceinline__ void lds_dma_dword_sys(const float* sbase, uint32_t& voff,
+                                                  uint32_t& lds, uint32_t vstep) {
+    __asm__ volatile(
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dword %0, %2 sc0 sc1\n\t"
+        "s_add_u32 %1, %1, %4\n\t"
+        "v_add_u32 %0, %3, %0"
+        : "+v"(voff), "+s"(lds)
+        : "s"(sbase), "s"(vstep), "n"(LDS_STEP)
+        : "memory", "m0", "scc");
+}
+
 // The same with 16 bytes per lane: lane l's four dwords land at LDS M0 + 16*l.
 template <int LDS_STEP>
 __device__ __forceinline__ void lds_dma_dwordx4(const float* sbase, uint32_t& voff, uint32_t& lds,
@@ -485,12 +608,13 @@ __device__ __forceinline__ void dma_rows4(uint32_t rows_lds, const float* plane_
 template <int P, int DIR>
 __device__ __host__ constexpr int rows_row(int j) { return DIR > 0 ? j : P - 1 - j; }
 
-// Zeroes the cells of a row-major [L1max][L2max] output outside [0,L1) x [0,L2),
-// with all threads of the workgroup.
+// Zeroes the cells of a row-major [L1max][L2max] output outside [0,L1) x [0,L2) in
+// rows [r_begin, r_end) (default: all), with all threads of the workgroup.
 __device__ __forceinline__ void zero_padding(float* obase, int L1, int L2, int L1max, int L2max,
-                                             int nthreads) {
+                                             int nthreads, int r_begin = 0, int r_end = -1) {
     if (L1 >= L1max && L2 >= L2max) return;
-    for (int r = 0; r < L1max; ++r) {
+    if (r_end < 0) r_end = L1max;
+    for (int r = r_begin; r < r_end; ++r) {
         const int c0 = r < L1 ? L2 : 0;
         for (int c = c0 + (int)threadIdx.x; c < L2max; c += nthreads)
             obase[(size_t)r * L2max + c] = 0.0f;

@@ -1,0 +1,93 @@
+"""Split elements of the linear-gap sweeps: an element's stripes divided among
+several workgroups ("parts") that hand the boundary row (forward) and the boundary
+flows (reverse sweep) to each other through global memory.
+
+D2P_AMD_SPLIT=<n> forces n parts per element (1: never split); unset, the library
+splits only long elements of small batches.  Every case is checked against the CPU
+oracle to the north-star tolerances (value 1e-5 relative, marginals 1e-4
+absolute, parameter gradients as in test_gpu_sw_linear), with the pipeline status
+words required to stay 0 (no wait ran into its bound).  The HVP case checks that
+the second-order entry points, whose primal sweeps are the same kernels, stay
+within 1e-4 * max(1, max|H|).
+"""
+import numpy as np
+import pytest
+import torch
+
+import _capi
+from oracle import oracle as O
+from test_gpu_sw_linear import _check, _seeded
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture
+def parts(monkeypatch):
+    def force(n):
+        monkeypatch.setenv("D2P_AMD_SPLIT", str(n))
+    return force
+
+
+CASES = [
+    # (seed, B, L1, L2, parts)
+    (20, 2, 600, 90, 1),       # unsplit, more stripes than waves
+    (21, 1, 1100, 300, 1),     # unsplit, more than two rounds of waves
+    (22, 1, 300, 200, 2),      # 5 stripes in parts of 3 and 2
+    (23, 3, 500, 257, 8),      # one stripe per part
+    (24, 2, 1300, 150, 2),     # parts of 11 and 10 stripes: several stripes per wave
+    (25, 1, 1100, 2500, 2),    # long rows: 8-step backward chunks, parts of 9 stripes
+    (26, 9, 200, 70, 4),       # B not a multiple of 8: idle workgroups in the grid
+    (27, 2, 1024, 1024, 0),    # automatic choice (2 parts of 8 stripes)
+    (28, 1, 129, 64, 3),       # last part of a single short stripe
+]
+
+
+@pytest.mark.parametrize("seed,B,L1,L2,n", CASES)
+def test_sw_split_matches_oracle(cuda, parts, seed, B, L1, L2, n):
+    parts(n)
+    s = _seeded(seed, (B, L1, L2))
+    ref = O.get("oracle").soft_sw(s.numpy(), -1.0, 1.0)
+    out = _capi.sw_forward_marginals(s.to(cuda), None, -1.0, 1.0)
+    torch.cuda.synchronize()
+    _check(out, ref, scores=s.numpy())
+
+
+def test_sw_split_ragged(cuda, parts):
+    """Ragged lengths under 4 parts of 3 stripes: elements whose later parts hold no
+    stripe, empty elements, and one-row elements."""
+    parts(4)
+    B, L1, L2 = 7, 700, 170
+    s = _seeded(29, (B, L1, L2), 2.0)
+    g = np.random.default_rng(29)
+    lengths = np.stack([g.integers(0, L1 + 1, B), g.integers(0, L2 + 1, B)], 1).astype(np.int32)
+    lengths[0] = [L1, L2]
+    lengths[1] = [0, 5]
+    lengths[2] = [640, 0]
+    lengths[3] = [1, 1]
+    lengths[4] = [193, 170]      # the first part only (stripes 0..3 of 11)
+    ref = O.get("oracle").soft_sw(s.numpy(), -1.0, 0.5, lengths)
+    out = _capi.sw_forward_marginals(s.to(cuda), torch.from_numpy(lengths).to(cuda), -1.0, 0.5)
+    torch.cuda.synchronize()
+    _check(out, ref, lengths=lengths, gap=-1.0, T=0.5, scores=s.numpy())
+
+
+def test_sw_split_repeated_launches(cuda, parts):
+    """Consecutive launches on one workspace: the progress words of one launch never
+    satisfy the waits of the next (epochs), and the results repeat exactly."""
+    parts(3)
+    s = _seeded(30, (2, 700, 120)).to(cuda)
+    first = _capi.sw_forward_marginals(s, None, -1.0, 1.0)
+    for _ in range(3):
+        again = _capi.sw_forward_marginals(s, None, -1.0, 1.0)
+        for a, b in zip(first, again):
+            torch.testing.assert_close(a, b, rtol=0, atol=0)
+
+
+def test_sw_split_hvp(cuda, parts):
+    parts(3)
+    s = _seeded(31, (2, 700, 90))
+    v = _seeded(32, (2, 700, 90))
+    ref = O.get("oracle").soft_sw_hvp(s.numpy(), v.numpy(), -1.0, 1.0)
+    got = _capi.sw_hvp(s.to(cuda), v.to(cuda), None, -1.0, 1.0).cpu().numpy()
+    tol = 1e-4 * max(1.0, float(np.abs(ref).max()))
+    assert float(np.abs(got - ref).max()) <= tol
