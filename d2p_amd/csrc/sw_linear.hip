@@ -606,11 +606,16 @@ Split choose_split(int B, int max_L1, const Layout& ws) {
     int G = 0;
     if (const char* e = getenv("D2P_AMD_SPLIT")) G = atoi(e);
     if (G <= 0) {
-        // one stripe per wave, while every part of the grid is resident at once
-        if (ns <= wf::NW) return sp;
-        G = (ns + wf::NW - 1) / wf::NW;
+        // Parts of 4 stripes (one wave per SIMD: the pipeline's per-step latency is
+        // lowest when a wave has its SIMD to itself) if the whole grid is resident at
+        // once; else parts of 8 (one stripe per wave), or as few parts as fit.
+        if (ns <= 4) return sp;
         const int cus = device_cus();
-        while (G > 1 && wf::split_grid(B, G) > cus) --G;
+        G = (ns + 3) / 4;
+        if (wf::split_grid(B, G) > cus) {
+            G = (ns + wf::NW - 1) / wf::NW;
+            while (G > 1 && wf::split_grid(B, G) > cus) --G;
+        }
     }
     G = G < ns ? G : ns;
     if (G <= 1) return sp;

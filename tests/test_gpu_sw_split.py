@@ -37,7 +37,7 @@ CASES = [
     (24, 2, 1300, 150, 2),     # parts of 11 and 10 stripes: several stripes per wave
     (25, 1, 1100, 2500, 2),    # long rows: 8-step backward chunks, parts of 9 stripes
     (26, 9, 200, 70, 4),       # B not a multiple of 8: idle workgroups in the grid
-    (27, 2, 1024, 1024, 0),    # automatic choice (2 parts of 8 stripes)
+    (27, 2, 1024, 1024, 0),    # automatic choice (4 parts of 4 stripes)
     (28, 1, 129, 64, 3),       # last part of a single short stripe
 ]
 
