@@ -16,6 +16,9 @@ void profile_end(const char* name, hipStream_t stream, hipEvent_t start);
 
 // Compute units of the current device (cached per device; 0 if unknown).
 int device_cus();
+
+// A new nonzero launch epoch (tags the progress words of split elements).
+uint32_t next_epoch();
 }
 
 // Launches `kernel` and, when profiling is on, times it with events on `stream`.

@@ -61,6 +61,12 @@ void resolve_pending_locked() {
 
 bool profiling_enabled() { return g_prof_on; }
 
+uint32_t next_epoch() {
+    static std::atomic<uint32_t> epoch{0};
+    const uint32_t e = ++epoch;
+    return e != 0 ? e : ++epoch;
+}
+
 int device_cus() {
     static std::atomic<int> cached[64];
     int dev = 0;

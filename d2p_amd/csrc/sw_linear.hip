@@ -35,12 +35,6 @@ using namespace wf;
 constexpr int PF = 16;               // steps per chunk, forward sweep
 constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do not publish
 
-// Tag of the progress words: the launch's epoch in the high half, a marker and the
-// chunks done in the low half.
-__device__ __forceinline__ uint64_t progress_word(uint32_t epoch, int chunks) {
-    return ((uint64_t)epoch << 32) | (uint32_t)chunks;
-}
-
 // One part (G > 1: a workgroup owns stripes [part*SPW, part*SPW + SPW) of its element;
 // G == 1: all of them).  The first stripe of a part > 0 reads the last row of the
 // previous part's last stripe from `brow` (device-coherent loads, one chunk ahead)
@@ -589,15 +583,6 @@ int check_shape(int B, int max_L1, int max_L2, float temperature) {
                 "sequence too long for the LDS stripe rings");
     return D2P_OK;
 }
-
-namespace {
-// One launch counter per process: the epoch that tags the launch's progress words.
-std::atomic<uint32_t> g_epoch{0};
-uint32_t next_epoch() {
-    uint32_t e = ++g_epoch;
-    return e != 0 ? e : ++g_epoch;
-}
-}  // namespace
 
 Split choose_split(int B, int max_L1, const Layout& ws) {
     const int ns = (max_L1 + 63) / 64;

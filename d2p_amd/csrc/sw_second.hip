@@ -50,19 +50,26 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                   const int* __restrict__ lengths, const float* __restrict__ alpha_sk,
                   const float* __restrict__ brow, const float* __restrict__ partition,
                   float* __restrict__ tan_sk, float* __restrict__ tan_brow,
-                  float* __restrict__ sdot, int* __restrict__ status, int L1max, int L2max,
-                  int NSmax, float gap, float T, int R) {
+                  float* __restrict__ sdot, int* __restrict__ status,
+                  uint64_t* __restrict__ tflag, float* __restrict__ spart, int B, int L1max,
+                  int L2max, int NSmax, float gap, float T, int R, int G, int SPW,
+                  uint32_t epoch) {
     constexpr bool HAS_V = MODE == HVP;
     using Tile = ChunkTile<P>;
     constexpr int VT = Tile::FLOATS;                         // direction tile
     constexpr int AR = VT + (HAS_V ? Tile::FLOATS : 0);      // P alpha rows
     constexpr int RR = AR + P * 64;                          // row above
-    constexpr int BUF = RR + 64;
+    constexpr int TR = RR + 64;                              // tangent row of the part above
+    constexpr int BUF = TR + 64;
     constexpr int SINK = 64 + P;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red[NW];
-    const int b = blockIdx.x;
+    // parts as in the primal forward: part p > 0 takes its first stripe's tangent row
+    // above from part p - 1 through tan_brow
+    int b, part;
+    split_decode(blockIdx.x, G, b, part);
+    if (b >= B) return;
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -88,16 +95,27 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     const float* vbase = HAS_V ? V + (size_t)b * L1max * L2max : nullptr;
     const uint32_t in_lds = lds_address(buf);
     float sacc = 0.0f;   // sum of beta_init * tangent (HVP)
+    const int s_begin = part * SPW;
+    const int NL = max(min(NS, s_begin + SPW) - s_begin, 0);   // stripes of this part
+    const bool has_next = s_begin + NL < NS;
+    const uint64_t* flag_in = tflag + (size_t)b * G + (part > 0 ? part - 1 : 0);
+    uint64_t* flag_out = tflag + (size_t)b * G + part;
 
-    for (int s = wave; s < NS; s += NW) {
+    for (int l = wave; l < NL; l += NW) {
+        const int s = s_begin + l;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
         const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * NT * 64;   // step -APAD
         const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
         float* tout = tan_sk + (((size_t)b * NSmax + s) * NT + APAD) * 64;
         float* tb_s = tan_brow + ((size_t)b * NSmax + s) * NT;
-        const float* ring_in = ring_from(rings, s, R);
-        float* ring_out = ring_of(rings, s, R);
+        const float* tb_up = tan_brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
+        const float* ring_in = ring_from(rings, l, R);
+        float* ring_out = ring_of(rings, l, R);
+        const bool x_in = l == 0 && part > 0;        // tangent row above from part - 1
+        const bool x_out = l == NL - 1 && has_next;  // tangent row feeds part + 1
+        int seen = -1;       // chunks of the previous part known to be complete
+        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
 
         // Loads of chunk k (steps t0 .. t0+P-1): the score (and direction) tiles, the
         // P alpha rows, and for lane j <= P the last row of the stripe above at step
@@ -110,12 +128,19 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             uint32_t roff = (uint32_t)min(t0 + 62 + min(lane, P), nsteps - 1) * 4u;
             uint32_t rl = in_lds + RR * 4;
             lds_dma_dword<0>(bup, roff, rl, 0u);
+            if (x_in) {
+                // lane j < P: the tangent of the last row above at step t0 + 63 + j
+                uint32_t toff = (uint32_t)min(t0 + 63 + min(lane, P - 1), nsteps - 1) * 4u;
+                uint32_t tl = in_lds + TR * 4;
+                lds_dma_dword_sys<0>(tb_up, toff, tl, 0u);
+            }
         };
 
         // tangents of the column-0 boundary are 0
 #pragma unroll
         for (int t = -APAD; t < 0; ++t) lane_store(tout + t * 64, ul4, 0.0f);
         wave_lds_sync();
+        if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
         issue_chunk(0);
         float Aw[P + 2];
         Aw[P] = kNINF;        // alpha at steps -2, -1: column-0 boundary
@@ -124,10 +149,15 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
 
         for (int k = 0; k < nch; ++k) {
             const int t0 = k * P;
-            chunk_waits<P>(prog, s, NS, k, nch, R, st);
-            // this chunk's loads, followed by exactly the P + 1 stores of the previous
+            chunk_waits<P>(prog, l, NL, k, nch, R, st);
+            // this chunk's loads, followed by at least the P + 1 stores of the previous
             // chunk (the first chunk's loads are the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (x_in && k > 0) {
+                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
+                const int got = flag_chunks(fl, epoch);
+                seen = got > seen ? got : seen;
+            }
             float sv[P], vv[P];
 #pragma unroll
             for (int u = 0; u < P; ++u) {
@@ -143,9 +173,17 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             bv = (s > 0 && lane <= P && t0 + 62 + lane <= nsteps - 1) ? bv : kNINF;
             // lane 0's up tangents: column t0+j sits in lane j (row 0: 0)
             float rreg = 0.0f;
-            if (s > 0 && lane < P) rreg = ring_in[ring_index(t0 + lane + 63, R)];
+            if (s > 0 && lane < P)
+                rreg = x_in ? buf[TR + lane] : ring_in[ring_index(t0 + lane + 63, R)];
             wave_lds_sync();   // every read of the input buffer is complete
-            if (k + 1 < nch) issue_chunk(k + 1);
+            if (k + 1 < nch) {
+                if (x_in) {
+                    const int need = min(k + 1 + lead(P), nch);
+                    if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                }
+                issue_chunk(k + 1);
+                if (x_in) fl = load_flag_async(flag_in);
+            }
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             float* toutc = tout + (size_t)t0 * 64;
 #pragma unroll
@@ -192,8 +230,22 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             }
             // the stripe's last row of tangents by step: one store instruction
             wave_lds_sync();
-            if (lane < P) lane_store(tb_s, (unsigned)(t0 + lane) * 4u, ring_out[t0 % R + lane]);
-            publish(prog, wave, s * PROG_STRIDE + k + 1);
+            if (lane < P) {
+                const float v = ring_out[t0 % R + lane];
+                if (x_out) store_sys(tb_s + t0 + lane, v);
+                else lane_store(tb_s, (unsigned)(t0 + lane) * 4u, v);
+            }
+            publish(prog, wave, l * PROG_STRIDE + k + 1);
+            if (x_out && k >= 2) {
+                // at least 2P + 1 loads and 2P + 2 stores follow the row store of chunk
+                // k - 2: it (and everything before) is complete
+                wait_vmcnt<(4 * P + 3 < 63 ? 4 * P + 3 : 63)>();
+                if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
+            }
+        }
+        if (x_out) {
+            wait_vmcnt<0>();
+            if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
         }
     }
 
@@ -204,7 +256,8 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
         if (threadIdx.x == 0) {
             float t = 0.0f;
             for (int w = 0; w < NW; ++w) t += red[w];
-            sdot[b] = t;
+            if (G == 1) sdot[b] = t;
+            else spart[(size_t)b * G + part] = t;
         }
     }
 }
@@ -220,8 +273,10 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                const float* __restrict__ brow, const float* __restrict__ tan_sk,
                const float* __restrict__ tan_brow, const float* __restrict__ partition,
                const float* __restrict__ dS, float* __restrict__ out, float* __restrict__ dot,
-               int* __restrict__ status, float* __restrict__ trash, int L1max, int L2max,
-               int NSmax, float gap, float T, int R) {
+               int* __restrict__ status, float* __restrict__ trash,
+               uint64_t* __restrict__ dflag, float4* __restrict__ flows4,
+               float* __restrict__ spart, int B, int L1max, int L2max, int NSmax, float gap,
+               float T, int R, int G, int SPW, uint32_t epoch) {
     constexpr bool HAS_V = MODE == HVP || DOT;
     using Tile = ChunkTile<P>;
     constexpr int VT = Tile::FLOATS;
@@ -230,12 +285,19 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     constexpr int RA = XR + P * 64;                         // alpha row above
     constexpr int RX = RA + 64;                             // tangent row above
     constexpr int OT = RX + 64;                             // output tile
-    constexpr int BUF = OT + (DOT ? 0 : Tile::FLOATS);
+    constexpr int FB = OT + (DOT ? 0 : Tile::FLOATS);       // flows from the part below
+    constexpr int BUF = FB + 64;
+    static_assert(4 * P + 2 <= 64, "boundary flows fit their buffer");
     constexpr int SINK = 64 + P;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red[NW];
-    const int b = blockIdx.x;
+    // parts as in the primal backward: bottom-up, part p < G - 1 takes its last
+    // stripe's flows from below from part p + 1 through flows4
+    int b, dpart;
+    split_decode(blockIdx.x, G, b, dpart);
+    if (b >= B) return;
+    const int part = G - 1 - dpart;
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -264,13 +326,22 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     float* obase = DOT ? nullptr : out + (size_t)b * L1max * L2max;
     const uint32_t in_lds = lds_address(buf);
 
-    if (!DOT) zero_padding(obase, L1, L2, L1max, L2max, NW * 64);
+    if (!DOT) {   // each part zeroes its share of the rows' padding
+        const int rows = (L1max + G - 1) / G;
+        zero_padding(obase, L1, L2, L1max, L2max, NW * 64, part * rows,
+                     min(L1max, part * rows + rows));
+    }
 
     float dacc = 0.0f;
     float A[P + 2], X[P + 2];
+    const int s_begin = part * SPW;
+    const int NL = max(min(NS, s_begin + SPW) - s_begin, 0);   // stripes of this part
+    const bool has_next = s_begin + NL < NS;
+    const uint64_t* flag_in = dflag + (size_t)b * G + (part + 1 < G ? part + 1 : part);
+    uint64_t* flag_out = dflag + (size_t)b * G + part;
 
-    for (int q = wave; q < NS; q += NW) {
-        const int s = NS - 1 - q;
+    for (int q = wave; q < NL; q += NW) {
+        const int s = s_begin + NL - 1 - q;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
         const size_t sb = ((size_t)b * NSmax + s) * NT;
@@ -281,7 +352,15 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
         const float* xup = tan_brow + ub;
         const float4* ring_in = ring_from(rings, q, R);
         float4* ring_out = ring_of(rings, q, R);
-        const bool below = q > 0;
+        const bool x_in = q == 0 && has_next;             // flows from the part below
+        const bool x_out = q == NL - 1 && part > 0;       // flows to the part above
+        const bool below = q > 0 || x_in;
+        // boundary flows by producer step: written by stripe s (x_out), read from s + 1
+        float4* flows_out = flows4 + ((size_t)b * NSmax + s) * NT;
+        const float* flows_in = reinterpret_cast<const float*>(
+            flows4 + ((size_t)b * NSmax + (x_in ? s + 1 : s)) * NT);
+        int seen = -1;       // chunks of the part below known to be complete
+        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
 
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
@@ -295,6 +374,14 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             o = roff;
             l = in_lds + RX * 4;
             lds_dma_dword<0>(xup, o, l, 0u);
+            if (x_in) {
+                // flows of producer slots kP+62 .. kP+62+P (float4 each): float f of the
+                // range in lane f, clamped to the last slot
+                uint32_t foff = (uint32_t)min((k * P + 62) * 4 + min(lane, 4 * P + 1),
+                                              (nsteps - 1) * 4 + 3) * 4u;
+                uint32_t fdst = in_lds + FB * 4;
+                lds_dma_dword_sys<0>(flows_in, foff, fdst, 0u);
+            }
         };
 
         {
@@ -307,6 +394,7 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             __asm__ volatile("" ::"v"(A[P]), "v"(A[P + 1]), "v"(X[P]), "v"(X[P + 1]));
         }
         wave_lds_sync();
+        if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
         issue_chunk(0);
         // successor flows: (beta, g) from the left successor, up successor, diagonal
         float lb = 0.0f, lg = 0.0f, ubt = 0.0f, ug = 0.0f;
@@ -314,11 +402,16 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
 
         for (int k = 0; k < nch; ++k) {
             const int t_hi = nsteps - 1 - k * P;
-            chunk_waits<P>(prog, q, NS, k, nch, R, st);
-            // this chunk's loads, followed by the P output stores of the previous
-            // chunk (none when accumulating a dot product; the first chunk's loads
-            // are the last issued)
+            chunk_waits<P>(prog, q, NL, k, nch, R, st);
+            // this chunk's loads, followed by at least the P output stores of the
+            // previous chunk (none when accumulating a dot product; the first chunk's
+            // loads are the last issued)
             if (k == 0 || DOT) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (x_in && k > 0) {
+                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
+                const int got = flag_chunks(fl, epoch);
+                seen = got > seen ? got : seen;
+            }
             float sv[P], vv[P];
 #pragma unroll
             for (int u = 0; u < P; ++u) {
@@ -342,15 +435,29 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             float qub = 0.0f, qug = 0.0f, qdb = 0.0f, qdg = 0.0f;
             if (below && lane >= 64 - P) {
                 const int j = 63 - lane;
-                const float4 ru = ring_in[ring_index(k * P + j + 63, R)];
-                const float4 rd = ring_in[ring_index(k * P + j + 62, R)];
-                qub = ru.x;
-                qug = ru.y;
-                qdb = rd.z;
-                qdg = rd.w;
+                if (x_in) {
+                    qub = buf[FB + 4 * (j + 1)];
+                    qug = buf[FB + 4 * (j + 1) + 1];
+                    qdb = buf[FB + 4 * j + 2];
+                    qdg = buf[FB + 4 * j + 3];
+                } else {
+                    const float4 ru = ring_in[ring_index(k * P + j + 63, R)];
+                    const float4 rd = ring_in[ring_index(k * P + j + 62, R)];
+                    qub = ru.x;
+                    qug = ru.y;
+                    qdb = rd.z;
+                    qdg = rd.w;
+                }
             }
             wave_lds_sync();   // every read of the input buffer is complete
-            if (k + 1 < nch) issue_chunk(k + 1);
+            if (k + 1 < nch) {
+                if (x_in) {
+                    const int need = min(k + 1 + lead(P), nch);
+                    if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                }
+                issue_chunk(k + 1);
+                if (x_in) fl = load_flag_async(flag_in);
+            }
             float4* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
             {
                 const float u0b = lane_bcast(qub, 63), u0g = lane_bcast(qug, 63);
@@ -445,6 +552,20 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             wave_lds_sync();
             if (!DOT) write_tile<P, -1>(otile, obase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             publish(prog, wave, q * PROG_STRIDE + k + 1);
+            if (x_out) {
+                // this chunk's flows to the part above, by producer step
+                if (lane < P) store_sys4(flows_out + k * P + lane, ring_out[ring_index(k * P, R) + lane]);
+                if (k >= 2) {
+                    // at least 3P + 2 loads, 2 flow stores and (DOT: none, else 2P) output
+                    // stores follow the flow store of chunk k - 2: it is complete
+                    wait_vmcnt<(DOT ? 3 * P + 4 : 5 * P + 4)>();
+                    if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
+                }
+            }
+        }
+        if (x_out) {
+            wait_vmcnt<0>();
+            if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
         }
     }
 
@@ -455,9 +576,19 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
         if (threadIdx.x == 0) {
             float t = 0.0f;
             for (int w = 0; w < NW; ++w) t += red[w];
-            dot[b] = t;
+            if (G == 1) dot[b] = t;
+            else spart[(size_t)b * G + part] = t;
         }
     }
+}
+
+// Sum of the parts' partial results of a split element.
+__global__ void sum_parts(const float* __restrict__ spart, float* __restrict__ out, int B, int G) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    float t = 0.0f;
+    for (int g = 0; g < G; ++g) t += spart[(size_t)b * G + g];
+    out[b] = t;
 }
 
 // ------------------------------------------------------------------ host side
@@ -465,27 +596,32 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
 constexpr size_t kLdsLimit = 160 * 1024 - 256;
 constexpr int PT = 16;   // tangent sweep chunk
 
-size_t lds_tangent(int mode, int max_L1, int max_L2) {
-    const int R = ring_len(max_L1, max_L2, 256);
-    const int buf = 65 * PT * (mode == HVP ? 2 : 1) + PT * 64 + 64;
+// LDS of one workgroup whose stripe boundaries use rings of R columns
+size_t lds_tangent_r(int mode, int R) {
+    const int buf = 65 * PT * (mode == HVP ? 2 : 1) + PT * 64 + 64 + 64;
     return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + PT)) * sizeof(float);
 }
+size_t lds_tangent(int mode, int max_L1, int max_L2) {
+    return lds_tangent_r(mode, ring_len(max_L1, max_L2, 256));
+}
 
-size_t lds_dual(bool has_v, bool dot, int P, int max_L1, int max_L2) {
-    const int R = ring_len(max_L1, max_L2, 128);
-    const int buf = 65 * P * (has_v ? 2 : 1) + 2 * P * 64 + 128 + (dot ? 0 : 65 * P);
+size_t lds_dual_r(bool has_v, bool dot, int P, int R) {
+    const int buf = 65 * P * (has_v ? 2 : 1) + 2 * P * 64 + 128 + (dot ? 0 : 65 * P) + 64;
     return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + P)) * sizeof(float4);
 }
 
-// Largest reverse-sweep chunk (8 or 4 steps) whose buffers and rings fit in LDS.
-int dual_chunk(bool has_v, bool dot, int max_L1, int max_L2) {
-    if (lds_dual(has_v, dot, 8, max_L1, max_L2) <= kLdsLimit) return 8;
-    if (lds_dual(has_v, dot, 4, max_L1, max_L2) <= kLdsLimit) return 4;
+// Largest reverse-sweep chunk (8 or 4 steps) whose buffers and rings fit in LDS, for a
+// workgroup that runs `rows` rows of stripes.
+int dual_chunk(bool has_v, bool dot, int rows, int max_L2) {
+    const int R = ring_len(rows, max_L2, 128);
+    if (lds_dual_r(has_v, dot, 8, R) <= kLdsLimit) return 8;
+    if (lds_dual_r(has_v, dot, 4, R) <= kLdsLimit) return 4;
     return 0;
 }
 
 // Workspace after the primal layout: tangent table + last rows, then [B] each of
-// the tangent sweep's dS, the partition, dS/dgap and dS/dT.
+// the tangent sweep's dS, the partition, dS/dgap and dS/dT, then for split elements
+// the parts' partial sums and the reverse sweep's boundary flows (float4 by step).
 struct Second {
     Layout prim;
     float* tan_sk;
@@ -494,6 +630,8 @@ struct Second {
     float* part;
     float* dgap;
     float* dT;
+    float* spart;     // [B][stripe]
+    float4* flows4;   // [B][stripe][step]
     size_t bytes;
 };
 
@@ -510,6 +648,11 @@ Second second_layout(void* ws, int B, int L1, int L2) {
     w.dgap = w.part + B;
     w.dT = w.dgap + B;
     p += round256((size_t)4 * B * sizeof(float));
+    const size_t parts = (size_t)B * (ns > 0 ? ns : 1);
+    w.spart = (float*)p;
+    p += round256(parts * sizeof(float));
+    w.flows4 = (float4*)p;
+    p += round256(parts * (size_t)stored_steps(L2) * sizeof(float4));
     w.bytes = (size_t)(p - (char*)ws);
     return w;
 }
@@ -518,15 +661,20 @@ template <int MODE>
 int launch_tangent(const float* scores, const float* V, const int* lengths, int B, int L1, int L2,
                    float gap, float T, const Second& w, float* sdot, hipStream_t st) {
     const int ns = (L1 + 63) / 64;
-    const int R = ring_len(L1, L2, 256);
-    const size_t lds = lds_tangent(MODE, L1, L2);
+    const sw::Split sp = sw::choose_split(B, L1, w.prim);
+    const int R = ring_len(sp.G > 1 ? sp.SPW * 64 : L1, L2, 256);
+    const size_t lds = lds_tangent_r(MODE, R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     auto kern = sw_tangent_kernel<MODE, PT>;
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
-    D2P_LAUNCH("sw_tangent", kern, dim3(B), dim3(NW * 64), lds, st, scores, V, lengths,
-               w.prim.alpha_sk, w.prim.brow, w.part, w.tan_sk, w.tan_brow, sdot, w.prim.status,
-               L1, L2, ns, gap, T, R);
+    D2P_LAUNCH("sw_tangent", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
+               lengths, w.prim.alpha_sk, w.prim.brow, w.part, w.tan_sk, w.tan_brow, sdot,
+               w.prim.status, w.prim.fflag, w.spart, B, L1, L2, ns, gap, T, R, sp.G, sp.SPW,
+               next_epoch());
+    if (MODE == HVP && sp.G > 1)
+        D2P_LAUNCH("sum_parts", sum_parts, dim3((B + 255) / 256), dim3(256), 0, st, w.spart, sdot,
+                   B, sp.G);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -536,19 +684,25 @@ int launch_dual(const float* scores, const float* V, const int* lengths, int B, 
                 float gap, float T, const Second& w, const float* dS, float* out, float* dot,
                 hipStream_t st) {
     const int ns = (L1 + 63) / 64;
-    const int R = ring_len(L1, L2, 128);
+    const sw::Split sp = sw::choose_split(B, L1, w.prim);
+    const int rows = sp.G > 1 ? sp.SPW * 64 : L1;
+    const int R = ring_len(rows, L2, 128);
     constexpr bool has_v = MODE == HVP || DOT;
-    const int P = dual_chunk(has_v, DOT, L1, L2);
+    const int P = dual_chunk(has_v, DOT, rows, L2);
     D2P_REQUIRE(P > 0, "sequence too long for the LDS stripe rings");
-    const size_t lds = lds_dual(has_v, DOT, P, L1, L2);
+    const size_t lds = lds_dual_r(has_v, DOT, P, R);
     auto k8 = sw_dual_kernel<MODE, 8, DOT>;
     auto k4 = sw_dual_kernel<MODE, 4, DOT>;
     auto kern = P == 8 ? k8 : k4;
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
-    D2P_LAUNCH("sw_dual", kern, dim3(B), dim3(NW * 64), lds, st, scores, V, lengths,
-               w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, w.part, dS, out, dot,
-               w.prim.status, w.prim.trash, L1, L2, ns, gap, T, R);
+    D2P_LAUNCH("sw_dual", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
+               lengths, w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, w.part, dS, out, dot,
+               w.prim.status, w.prim.trash, w.prim.bflag, w.flows4, w.spart, B, L1, L2, ns, gap,
+               T, R, sp.G, sp.SPW, next_epoch());
+    if (DOT && sp.G > 1)
+        D2P_LAUNCH("sum_parts", sum_parts, dim3((B + 255) / 256), dim3(256), 0, st, w.spart, dot,
+                   B, sp.G);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }

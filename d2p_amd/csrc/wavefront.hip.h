@@ -187,6 +187,18 @@ __device__ __forceinline__ int load_status(const int* p) {
     return v;
 }
 
+// 16 bytes per lane, device-coherent
+__device__ __forceinline__ void store_sys4(float4* p, float4 v) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 w = {v.x, v.y, v.z, v.w};
+    __asm__ volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(p), "v"(w) : "memory");
+}
+
+// A progress word: the launch's epoch in the high half, the chunks done in the low.
+__device__ __forceinline__ uint64_t progress_word(uint32_t epoch, int chunks) {
+    return ((uint64_t)epoch << 32) | (uint32_t)chunks;
+}
+
 // Chunks a progress word reports for this epoch (-1: an earlier launch's word).
 __device__ __forceinline__ int flag_chunks(uint64_t v, uint32_t epoch) {
     const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));

@@ -7,8 +7,9 @@ splits only long elements of small batches.  Every case is checked against the C
 oracle to the north-star tolerances (value 1e-5 relative, marginals 1e-4
 absolute, parameter gradients as in test_gpu_sw_linear), with the pipeline status
 words required to stay 0 (no wait ran into its bound).  The HVP case checks that
-the second-order entry points, whose primal sweeps are the same kernels, stay
-within 1e-4 * max(1, max|H|).
+the second-order entry points (primal sweeps, tangent sweep and two-channel reverse
+sweep all split) stay within 1e-4 * max(1, max|H|), and the Jacobians and the
+marginal-path backward within the allowances of test_gpu_sw_second.
 """
 import numpy as np
 import pytest
@@ -17,6 +18,7 @@ import torch
 import _capi
 from oracle import oracle as O
 from test_gpu_sw_linear import _check, _seeded
+from test_gpu_sw_second import _close, _jacobian_ref
 
 pytestmark = pytest.mark.gpu
 
@@ -83,11 +85,49 @@ def test_sw_split_repeated_launches(cuda, parts):
             torch.testing.assert_close(a, b, rtol=0, atol=0)
 
 
-def test_sw_split_hvp(cuda, parts):
-    parts(3)
+@pytest.mark.parametrize("n", [2, 3, 11])
+def test_sw_split_hvp(cuda, parts, n):
+    parts(n)
     s = _seeded(31, (2, 700, 90))
     v = _seeded(32, (2, 700, 90))
     ref = O.get("oracle").soft_sw_hvp(s.numpy(), v.numpy(), -1.0, 1.0)
-    got = _capi.sw_hvp(s.to(cuda), v.to(cuda), None, -1.0, 1.0).cpu().numpy()
-    tol = 1e-4 * max(1.0, float(np.abs(ref).max()))
-    assert float(np.abs(got - ref).max()) <= tol
+    _close(_capi.sw_hvp(s.to(cuda), v.to(cuda), None, -1.0, 1.0), ref, f"hvp, {n} parts")
+
+
+def test_sw_split_hvp_ragged(cuda, parts):
+    parts(4)
+    B, L1, L2 = 5, 700, 110
+    s = _seeded(34, (B, L1, L2))
+    v = _seeded(35, (B, L1, L2))
+    lens = np.array([[700, 110], [0, 40], [193, 0], [1, 1], [257, 81]], np.int32)
+    ref = O.get("oracle").soft_sw_hvp(s.numpy(), v.numpy(), -1.0, 0.7, lens)
+    got = _capi.sw_hvp(s.to(cuda), v.to(cuda), torch.from_numpy(lens).to(cuda), -1.0, 0.7)
+    _close(got, ref, "hvp ragged, 4 parts")
+
+
+@pytest.mark.parametrize("n", [2, 4])
+def test_sw_split_param_jacobian(cuda, parts, n):
+    parts(n)
+    s = _seeded(33, (2, 500, 80))
+    k = O.get("oracle")
+    for p in (0, 1):
+        ref, allow = _jacobian_ref(k, s.numpy(), p, -1.0, 1.0)
+        _close(_capi.sw_param_jacobian(s.to(cuda), p, None, -1.0, 1.0), ref,
+               f"dP/d{('gap', 'T')[p]}, {n} parts", allow)
+
+
+def test_sw_split_backward_full(cuda, parts):
+    """The dot-product reverse sweeps (<ga, dP/dtheta>) sum their parts."""
+    parts(3)
+    B, L1, L2 = 2, 450, 96
+    s = _seeded(36, (B, L1, L2))
+    ga = _seeded(37, (B, L1, L2))
+    k = O.get("oracle")
+    gs, gg, gt = _capi.sw_backward_full(s.to(cuda), ga.to(cuda), None, -1.0, 1.0)
+    _close(gs, k.soft_sw_hvp(s.numpy(), ga.numpy(), -1.0, 1.0), "backward_full scores")
+    for p, g in ((0, gg), (1, gt)):
+        J, allow = _jacobian_ref(k, s.numpy(), p, -1.0, 1.0)
+        ref = (J.astype(np.float64) * ga.numpy()).sum(axis=(1, 2))
+        per = 1e-4 * max(1.0, np.abs(J).max()) + allow
+        tol = per * np.abs(ga.numpy()).sum(axis=(1, 2))
+        assert np.all(np.abs(g.cpu().numpy() - ref) <= tol), (p, g.cpu().numpy(), ref, tol)
