@@ -53,25 +53,33 @@ __device__ __forceinline__ float lse4(float a, float b, float x, float y, float 
 __global__ void __launch_bounds__(NW * 64)
 swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                    float* __restrict__ alpha_sk, float* __restrict__ brow,
-                   float* __restrict__ partition, int* __restrict__ status, int L1max, int L2max,
-                   int NSmax, float go, float ge, float T, int R) {
+                   float* __restrict__ partition, int* __restrict__ status,
+                   uint64_t* __restrict__ fflag, float2* __restrict__ fpart, int B, int L1max,
+                   int L2max, int NSmax, float go, float ge, float T, int R, int G, int SPW,
+                   uint32_t epoch) {
     constexpr int P = PF;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red_m[NW], red_z[NW];
-    const int b = blockIdx.x;
+    // part of the element as in the linear forward: the first stripe of a part > 0
+    // reads the previous part's last rows (M, I, D) from brow
+    int b, part;
+    split_decode(blockIdx.x, G, b, part);
+    if (b >= B) return;
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = ChunkTile<P>;
-    float* tiles = smem + wave * 2 * Tile::FLOATS;   // double-buffered score chunk
-    float4* rings = reinterpret_cast<float4*>(smem + NW * 2 * Tile::FLOATS);   // [NW][R]
+    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 3 * 64;   // two score chunks, two row sets
+    float* tiles = smem + wave * WBUF;                    // double-buffered score chunk
+    float* rbufs = tiles + 2 * Tile::FLOATS;              // [2][plane][64] rows above
+    float4* rings = reinterpret_cast<float4*>(smem + NW * WBUF);   // [NW][R]
     float4* sink = rings + NW * R + wave * DUMMY;
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
 
     if (lane == 0) prog[wave] = -1;
-    if (threadIdx.x == 0) *st = 0;
+    if (G == 1 && threadIdx.x == 0) *st = 0;              // G > 1: reset before the launch
     __syncthreads();
 
     const int L1 = min(max(lengths[2 * b], 0), L1max);
@@ -85,16 +93,28 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     const size_t PLANE = NT * 64;
     const float* sbase = scores + (size_t)b * L1max * L2max;
 
+    const int s_begin = part * SPW;
+    const int NL = max(min(NS, s_begin + SPW) - s_begin, 0);   // stripes of this part
+    const bool has_next = s_begin + NL < NS;
+    const uint64_t* flag_in = fflag + (size_t)b * G + (part > 0 ? part - 1 : 0);
+    uint64_t* flag_out = fflag + (size_t)b * G + part;
+
     OnlineLSE acc;
     acc.init_open();
 
-    for (int s = wave; s < NS; s += NW) {
+    for (int l = wave; l < NL; l += NW) {
+        const int s = s_begin + l;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
-        const float4* ring_in = ring_from(rings, s, R);
-        float4* ring_out = ring_of(rings, s, R);
+        const float4* ring_in = ring_from(rings, l, R);
+        float4* ring_out = ring_of(rings, l, R);
         float* out = alpha_sk + ((size_t)b * NSmax + s) * 3 * PLANE + APAD * 64;   // M, step 0
         float* brow_s = brow + ((size_t)b * NSmax + s) * 3 * NT;                    // [3][NT]
+        const float* brow_up = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * 3 * NT;
+        const bool x_in = l == 0 && part > 0;        // rows above from the previous part
+        const bool x_out = l == NL - 1 && has_next;  // last rows feed the next part
+        int seen = -1;       // chunks of the previous part known to be complete
+        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
         // steps t < 0 hold the column-0 boundary (NINF), read by the reverse sweep
 #pragma unroll
         for (int t = -APAD; t < 0; ++t) {
@@ -104,16 +124,36 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         }
         wave_lds_sync();   // the previous stripe's tile reads are complete
         const uint32_t tile_lds = lds_address(tiles);
+        const uint32_t row_lds = lds_address(rbufs);
+        // the rows above of chunk k: lane j < P carries the step kP + 63 + j, per plane
+        auto issue_rows = [&](int k) {
+            const uint32_t off = (uint32_t)min(k * P + 63 + min(lane, P - 1), nsteps - 1) * 4u;
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) {
+                uint32_t o = off;
+                uint32_t dst = row_lds + (uint32_t)(((k & 1) * 3 + pl) * 64 * 4);
+                lds_dma_dword_sys<0>(brow_up + pl * NT, o, dst, 0u);
+            }
+        };
+        if (x_in) {
+            seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
+            issue_rows(0);
+        }
         dma_tile<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
         float cM = kNINF, cI = kNINF, cD = kNINF;      // this lane's previous step
         float pM = kNINF, pI = kNINF, pD = kNINF;      // up values of the previous step
 
         for (int k = 0; k < nch; ++k) {
             const int t0 = k * P;
-            chunk_waits<P>(prog, s, NS, k, nch, R, st);
-            // this chunk's scores: loaded one chunk ago and followed by the 3P + 3
-            // stores of that chunk (the first chunk's load is the last issued)
+            chunk_waits<P>(prog, l, NL, k, nch, R, st);
+            // this chunk's scores: loaded one chunk ago and followed by at least the
+            // 3P + 3 stores of that chunk (the first chunk's load is the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<3 * P>();
+            if (x_in && k > 0) {
+                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
+                const int got = flag_chunks(fl, epoch);
+                seen = got > seen ? got : seen;
+            }
             const float* tile = tiles + (k & 1) * Tile::FLOATS;
             float sv[P], aM[P], aI[P], aD[P];
 #pragma unroll
@@ -121,14 +161,28 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             // lane 0's up values: column t0+j sits in lane j
             float rM = kNINF, rI = kNINF, rD = kNINF;
             if (s > 0 && lane < P) {
-                const float4 r = ring_in[ring_index(t0 + lane + 63, R)];
-                rM = r.x;
-                rI = r.y;
-                rD = r.z;
+                if (x_in) {
+                    const float* rb = rbufs + (k & 1) * 3 * 64;
+                    rM = rb[lane];
+                    rI = rb[64 + lane];
+                    rD = rb[128 + lane];
+                } else {
+                    const float4 r = ring_in[ring_index(t0 + lane + 63, R)];
+                    rM = r.x;
+                    rI = r.y;
+                    rD = r.z;
+                }
             }
-            if (k + 1 < nch)
+            if (k + 1 < nch) {
+                if (x_in) {
+                    const int need = min(k + 1 + lead(P), nch);
+                    if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                    issue_rows(k + 1);
+                }
                 dma_tile<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0, L1max,
                                L2max, lane, t0 + P);
+                if (x_in) fl = load_flag_async(flag_in);
+            }
             float4* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             float* outc = out + (size_t)t0 * 64;
             // FULL: every cell of the chunk lies inside the element, no validity masks
@@ -173,12 +227,28 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             wave_lds_sync();
             if (lane < P) {
                 const float4 r = ring_out[t0 % R + lane];
-                const unsigned o = (unsigned)(t0 + lane) * 4u;
-                lane_store(brow_s, o, r.x);
-                lane_store(brow_s + NT, o, r.y);
-                lane_store(brow_s + 2 * NT, o, r.z);
+                if (x_out) {
+                    store_sys(brow_s + t0 + lane, r.x);
+                    store_sys(brow_s + NT + t0 + lane, r.y);
+                    store_sys(brow_s + 2 * NT + t0 + lane, r.z);
+                } else {
+                    const unsigned o = (unsigned)(t0 + lane) * 4u;
+                    lane_store(brow_s, o, r.x);
+                    lane_store(brow_s + NT, o, r.y);
+                    lane_store(brow_s + 2 * NT, o, r.z);
+                }
             }
-            publish(prog, wave, s * PROG_STRIDE + k + 1);
+            publish(prog, wave, l * PROG_STRIDE + k + 1);
+            if (x_out && k >= 2) {
+                // at least P loads and 6P + 6 stores follow the row stores of chunk
+                // k - 2 (more than the counter holds): those are complete
+                wait_vmcnt<63>();
+                if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
+            }
+        }
+        if (x_out) {
+            wait_vmcnt<0>();
+            if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
         }
     }
 
@@ -188,10 +258,15 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     __syncthreads();
     if (threadIdx.x == 0) {
         OnlineLSE tot;
-        tot.m = 0.0f;
-        tot.z = 1.0f;
+        if (G == 1) {
+            tot.m = 0.0f;
+            tot.z = 1.0f;
+        } else {
+            tot.init();
+        }
         for (int w = 0; w < NW; ++w) tot.merge(red_m[w], red_z[w], c);
-        partition[b] = tot.m + tl * fast_log2(tot.z);
+        if (G == 1) partition[b] = tot.m + tl * fast_log2(tot.z);
+        else fpart[(size_t)b * G + part] = make_float2(tot.m, tot.z);
     }
 }
 
@@ -201,13 +276,20 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                     const float* __restrict__ partition, float* __restrict__ post,
                     float* __restrict__ grad_open, float* __restrict__ grad_ext,
                     float* __restrict__ grad_T, int* __restrict__ status,
-                    float* __restrict__ trash, int L1max, int L2max, int NSmax, float go,
-                    float ge, float T, int R) {
+                    float* __restrict__ trash, uint64_t* __restrict__ bflag,
+                    float4* __restrict__ flows4, float* __restrict__ flows1,
+                    double* __restrict__ bpart, int B, int L1max, int L2max, int NSmax, float go,
+                    float ge, float T, int R, int G, int SPW, uint32_t epoch) {
     constexpr int P = PB;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red_o[NW], red_e[NW], red_p[NW];
-    const int b = blockIdx.x;
+    // parts run bottom-up as in the linear backward; the last stripe of a part below
+    // the first hands its flows to the part above through flows4 / flows1
+    int b, dpart;
+    split_decode(blockIdx.x, G, b, dpart);
+    if (b >= B) return;
+    const int part = G - 1 - dpart;
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -218,7 +300,10 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
     constexpr int AROWS = Tile::FLOATS;             // 3 planes x P rows x 64
     constexpr int RROW = AROWS + 3 * P * 64;        // 3 planes x 64
     constexpr int OTILE = RROW + 3 * 64;
-    constexpr int WFLOATS = OTILE + Tile::FLOATS;
+    constexpr int FB4 = OTILE + Tile::FLOATS;       // flows from the part below: float4s
+    constexpr int FB1 = FB4 + 64;                   // ... and the diagonal D flows
+    constexpr int WFLOATS = FB1 + 64;
+    static_assert(4 * P + 4 <= 64, "boundary flows fit their buffer");
     float* wbuf = smem + wave * WFLOATS;
     float* otile = wbuf + OTILE;
     // rings [NW][R]: (up M, up I, diag M, diag I) and diag D, from lane 0 upward
@@ -245,13 +330,22 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
     const float* sbase = scores + (size_t)b * L1max * L2max;
     float* pbase = post + (size_t)b * L1max * L2max;
 
-    zero_padding(pbase, L1, L2, L1max, L2max, NW * 64);
+    {   // each part zeroes its share of the rows' padding
+        const int rows = (L1max + G - 1) / G;
+        zero_padding(pbase, L1, L2, L1max, L2max, NW * 64, part * rows,
+                     min(L1max, part * rows + rows));
+    }
 
     float g_open = 0.0f, g_ext = 0.0f, p_acc = 0.0f;
     float AM[P + 2], AI[P + 2], AD[P + 2];
+    const int s_begin = part * SPW;
+    const int NL = max(min(NS, s_begin + SPW) - s_begin, 0);   // stripes of this part
+    const bool has_next = s_begin + NL < NS;
+    const uint64_t* flag_in = bflag + (size_t)b * G + (part + 1 < G ? part + 1 : part);
+    uint64_t* flag_out = bflag + (size_t)b * G + part;
 
-    for (int q = wave; q < NS; q += NW) {
-        const int s = NS - 1 - q;
+    for (int q = wave; q < NL; q += NW) {
+        const int s = s_begin + NL - 1 - q;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
         const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * 3 * PLANE;   // M at step -APAD
@@ -260,8 +354,17 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
         const float* r1_in = ring_from(ring1, q, R);
         float4* r4_out = ring_of(ring4, q, R);
         float* r1_out = ring_of(ring1, q, R);
-        const bool below = q > 0;
+        const bool x_in = q == 0 && has_next;             // flows from the part below
+        const bool x_out = q == NL - 1 && part > 0;       // flows to the part above
+        const bool below = q > 0 || x_in;
         const uint32_t in_lds = lds_address(wbuf);
+        // boundary flows by producer step: written by stripe s (x_out), read from s + 1
+        const size_t fo = ((size_t)b * NSmax + s) * NT;
+        const size_t fi = ((size_t)b * NSmax + (x_in ? s + 1 : s)) * NT;
+        const float* f4_in = reinterpret_cast<const float*>(flows4 + fi);
+        const float* f1_in = flows1 + fi;
+        int seen = -1;       // chunks of the part below known to be complete
+        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
 
         // Loads of chunk k (t_hi = nsteps-1-kP): the score tile, P alpha rows per plane
         // (steps t_hi-2 .. t_hi-P-1) and the stripe above's last row per plane at steps
@@ -280,6 +383,17 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 uint32_t o = roff, l = in_lds + (RROW + pl * 64) * 4;
                 lds_dma_dword<0>(bup + pl * NT, o, l, 0u);
             }
+            if (x_in) {
+                // flows of producer slots kP+62 .. kP+62+P: float f of the float4 range
+                // and the D flow of slot kP+62+f in lane f, clamped to the last slot
+                uint32_t o = (uint32_t)min((k * P + 62) * 4 + min(lane, 4 * P + 3),
+                                           (nsteps - 1) * 4 + 3) * 4u;
+                uint32_t l = in_lds + FB4 * 4;
+                lds_dma_dword_sys<0>(f4_in, o, l, 0u);
+                o = (uint32_t)min(k * P + 62 + min(lane, P), nsteps - 1) * 4u;
+                l = in_lds + FB1 * 4;
+                lds_dma_dword_sys<0>(f1_in, o, l, 0u);
+            }
         };
 
         // the first two steps of chunk 0 (later chunks carry them over)
@@ -296,6 +410,7 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                              "v"(AD[P]), "v"(AD[P + 1]));   // completes these loads here
         }
         wave_lds_sync();   // the previous stripe's buffer reads are complete
+        if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
         issue_chunk(0);
         // successor contributions waiting for this lane's next steps
         float lM = 0.0f, lD = 0.0f;                              // from (i, j+1)
@@ -305,10 +420,15 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
 
         for (int k = 0; k < nch; ++k) {
             const int t_hi = nsteps - 1 - k * P;
-            chunk_waits<P>(prog, q, NS, k, nch, R, st);
-            // this chunk's loads, followed by exactly the P marginal stores of the
+            chunk_waits<P>(prog, q, NL, k, nch, R, st);
+            // this chunk's loads, followed by at least the P marginal stores of the
             // previous chunk (the first chunk's loads are the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (x_in && k > 0) {
+                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
+                const int got = flag_chunks(fl, epoch);
+                seen = got > seen ? got : seen;
+            }
             float sv[P];
 #pragma unroll
             for (int u = 0; u < P; ++u) sv[u] = wbuf[tbase + u];
@@ -333,17 +453,32 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
             float qUM = 0.0f, qUI = 0.0f, qDM = 0.0f, qDI = 0.0f, qDD = 0.0f;
             if (below && lane >= 64 - P) {
                 const int j = 63 - lane;
-                const float4 ru = r4_in[ring_index(k * P + j + 63, R)];
-                const int id = ring_index(k * P + j + 62, R);
-                const float4 rd = r4_in[id];
-                qUM = ru.x;
-                qUI = ru.y;
-                qDM = rd.z;
-                qDI = rd.w;
-                qDD = r1_in[id];
+                if (x_in) {
+                    qUM = wbuf[FB4 + 4 * (j + 1)];
+                    qUI = wbuf[FB4 + 4 * (j + 1) + 1];
+                    qDM = wbuf[FB4 + 4 * j + 2];
+                    qDI = wbuf[FB4 + 4 * j + 3];
+                    qDD = wbuf[FB1 + j];
+                } else {
+                    const float4 ru = r4_in[ring_index(k * P + j + 63, R)];
+                    const int id = ring_index(k * P + j + 62, R);
+                    const float4 rd = r4_in[id];
+                    qUM = ru.x;
+                    qUI = ru.y;
+                    qDM = rd.z;
+                    qDI = rd.w;
+                    qDD = r1_in[id];
+                }
             }
             wave_lds_sync();   // every read of the input buffer is complete
-            if (k + 1 < nch) issue_chunk(k + 1);
+            if (k + 1 < nch) {
+                if (x_in) {
+                    const int need = min(k + 1 + lead(P), nch);
+                    if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                }
+                issue_chunk(k + 1);
+                if (x_in) fl = load_flag_async(flag_in);
+            }
             float4* pub4 = (lane == 0) ? r4_out + ring_index(k * P, R) : sink4 + lane;
             float* pub1 = (lane == 0) ? r1_out + ring_index(k * P, R) : sink1 + lane;
             // lane 63 starts the chunk with the ring's values for steps 0 and 1
@@ -447,6 +582,24 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
             wave_lds_sync();
             write_tile<P, -1>(otile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             publish(prog, wave, q * PROG_STRIDE + k + 1);
+            if (x_out) {
+                // this chunk's flows to the part above, by producer step
+                if (lane < P) {
+                    const int slot = ring_index(k * P, R) + lane;
+                    store_sys4(flows4 + fo + k * P + lane, r4_out[slot]);
+                    store_sys(flows1 + fo + k * P + lane, r1_out[slot]);
+                }
+                if (k >= 2) {
+                    // at least 4P + 3 loads, 2P marginal stores and 4 flow stores follow
+                    // the flow stores of chunk k - 2: those are complete
+                    wait_vmcnt<6 * P + 7>();
+                    if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
+                }
+            }
+        }
+        if (x_out) {
+            wait_vmcnt<0>();
+            if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
         }
     }
 
@@ -458,10 +611,36 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
     if (threadIdx.x == 0) {
         float go_s = 0.0f, ge_s = 0.0f, p = 0.0f;
         for (int w = 0; w < NW; ++w) { go_s += red_o[w]; ge_s += red_e[w]; p += red_p[w]; }
-        grad_open[b] = go_s;
-        grad_ext[b] = ge_s;
-        grad_T[b] = (S - (p + (go_s * go + ge_s * ge))) / T;
+        if (G == 1) {
+            grad_open[b] = go_s;
+            grad_ext[b] = ge_s;
+            grad_T[b] = (S - (p + (go_s * go + ge_s * ge))) / T;
+        } else {
+            double* bp = bpart + ((size_t)b * G + part) * 4;
+            bp[0] = go_s;
+            bp[1] = ge_s;
+            bp[2] = p;
+        }
     }
+}
+
+// grad_open[b], grad_ext[b], grad_T[b] of a split element from the parts' sums.
+__global__ void swa_grad_merge(const double* __restrict__ bpart, const float* __restrict__ partition,
+                               float* __restrict__ grad_open, float* __restrict__ grad_ext,
+                               float* __restrict__ grad_T, int B, int G, float go, float ge,
+                               float T) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    float go_s = 0.0f, ge_s = 0.0f, p = 0.0f;
+    for (int i = 0; i < G; ++i) {
+        const double* bp = bpart + ((size_t)b * G + i) * 4;
+        go_s += (float)bp[0];
+        ge_s += (float)bp[1];
+        p += (float)bp[2];
+    }
+    grad_open[b] = go_s;
+    grad_ext[b] = ge_s;
+    grad_T[b] = (partition[b] - (p + (go_s * go + ge_s * ge))) / T;
 }
 
 }  // namespace swa
@@ -473,18 +652,19 @@ namespace swa {
 namespace {
 constexpr size_t kLdsLimit = 160 * 1024 - 256;
 
-size_t lds_forward(int max_L1, int max_L2) {
-    const int R = ring_len(max_L1, max_L2, 256);
-    return (size_t)NW * 2 * 65 * PF * sizeof(float) + ((size_t)NW * R + NW * DUMMY) * sizeof(float4);
+// LDS of one workgroup whose stripe boundaries use rings of R columns
+size_t lds_forward_r(int R) {
+    return (size_t)NW * (2 * 65 * PF + 2 * 3 * 64) * sizeof(float) +
+           ((size_t)NW * R + NW * DUMMY) * sizeof(float4);
 }
-
-size_t lds_backward(int max_L1, int max_L2) {
-    const int R = ring_len(max_L1, max_L2, 128);
-    const size_t wfloats = 65 * PB + 3 * PB * 64 + 3 * 64 + 65 * PB;
+size_t lds_backward_r(int R) {
+    const size_t wfloats = 65 * PB + 3 * PB * 64 + 3 * 64 + 65 * PB + 2 * 64;
     return (size_t)NW * wfloats * sizeof(float) +
            (size_t)NW * R * (sizeof(float4) + sizeof(float)) +
            (size_t)NW * (64 + PB) * (sizeof(float4) + sizeof(float));
 }
+int ring_forward(int rows, int max_L2) { return ring_len(rows, max_L2, 256); }
+int ring_backward(int rows, int max_L2) { return ring_len(rows, max_L2, 128); }
 }  // namespace
 
 int check_shape(int B, int max_L1, int max_L2, float temperature) {
@@ -492,23 +672,36 @@ int check_shape(int B, int max_L1, int max_L2, float temperature) {
     D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
     D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 4, "max_L2 too large");
     D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
-    D2P_REQUIRE(lds_forward(max_L1, max_L2) <= kLdsLimit &&
-                    lds_backward(max_L1, max_L2) <= kLdsLimit,
+    // an unsplit element is the longest pipeline a launch may run
+    D2P_REQUIRE(lds_forward_r(ring_forward(max_L1, max_L2)) <= kLdsLimit &&
+                    lds_backward_r(ring_backward(max_L1, max_L2)) <= kLdsLimit,
                 "sequence too long for the LDS stripe rings");
     return D2P_OK;
+}
+
+// The affine layout's flows area: a float4 plane, then a float plane, of
+// ws.flow_slots entries each.
+constexpr int kFlowBytes = sizeof(float4) + sizeof(float);
+
+Layout affine_layout(void* workspace, int B, int max_L1, int max_L2, bool split) {
+    return layout(workspace, B, max_L1, max_L2, 3, split, kFlowBytes);
 }
 
 int launch_forward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                    float go, float ge, float T, const Layout& ws, float* partition,
                    hipStream_t st) {
     const int ns = (max_L1 + 63) / 64;
-    const int R = ring_len(max_L1, max_L2, 256);
-    const size_t lds = lds_forward(max_L1, max_L2);
+    const Split sp = choose_split(B, max_L1, ws);
+    const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
+    const size_t lds = lds_forward_r(R);
+    if (sp.G > 1 && launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
     D2P_HIP(hipFuncSetAttribute((const void*)swa_forward_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH("swa_forward", swa_forward_kernel, dim3(B), dim3(NW * 64), lds, st, scores,
-               lengths, ws.alpha_sk, ws.brow, partition, ws.status, max_L1, max_L2, ns, go, ge, T,
-               R);
+    D2P_LAUNCH("swa_forward", swa_forward_kernel, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds,
+               st, scores, lengths, ws.alpha_sk, ws.brow, partition, ws.status, ws.fflag,
+               ws.fpart, B, max_L1, max_L2, ns, go, ge, T, R, sp.G, sp.SPW, next_epoch());
+    if (sp.G > 1 && launch_partition_merge(ws, partition, B, sp.G, T, st) != D2P_OK)
+        return D2P_ERR_HIP;
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -518,13 +711,20 @@ int launch_backward(const float* scores, const int* lengths, int B, int max_L1, 
                     float* marginals, float* grad_open, float* grad_ext, float* grad_T,
                     hipStream_t st) {
     const int ns = (max_L1 + 63) / 64;
-    const int R = ring_len(max_L1, max_L2, 128);
-    const size_t lds = lds_backward(max_L1, max_L2);
+    const Split sp = choose_split(B, max_L1, ws);
+    const int R = ring_backward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
+    const size_t lds = lds_backward_r(R);
+    float4* flows4 = reinterpret_cast<float4*>(ws.flows);
+    float* flows1 = sp.G > 1 ? reinterpret_cast<float*>(flows4 + ws.flow_slots) : nullptr;
     D2P_HIP(hipFuncSetAttribute((const void*)swa_backward_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH("swa_backward", swa_backward_kernel, dim3(B), dim3(NW * 64), lds, st, scores,
-               lengths, ws.alpha_sk, ws.brow, partition, marginals, grad_open, grad_ext, grad_T,
-               ws.status, ws.trash, max_L1, max_L2, ns, go, ge, T, R);
+    D2P_LAUNCH("swa_backward", swa_backward_kernel, dim3(split_grid(B, sp.G)), dim3(NW * 64),
+               lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition, marginals, grad_open,
+               grad_ext, grad_T, ws.status, ws.trash, ws.bflag, flows4, flows1, ws.bpart, B,
+               max_L1, max_L2, ns, go, ge, T, R, sp.G, sp.SPW, next_epoch());
+    if (sp.G > 1)
+        D2P_LAUNCH("swa_grad_merge", swa_grad_merge, dim3((B + 255) / 256), dim3(256), 0, st,
+                   ws.bpart, partition, grad_open, grad_ext, grad_T, B, sp.G, go, ge, T);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -536,8 +736,9 @@ using namespace d2p_amd;
 
 extern "C" size_t d2p_swa_workspace_bytes(int B, int max_L1, int max_L2) {
     if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
-    // status words | trash line | skewed (M, I, D) tables | last rows of every stripe
-    return wf::layout(nullptr, B, max_L1, max_L2, 3).bytes;
+    // status words | trash line | skewed (M, I, D) tables | last rows of every stripe |
+    // split-element progress words, boundary flows and partial sums
+    return swa::affine_layout(nullptr, B, max_L1, max_L2, true).bytes;
 }
 
 extern "C" int d2p_swa_forward_marginals(const float* scores, const int* lengths, int B,
@@ -553,7 +754,7 @@ extern "C" int d2p_swa_forward_marginals(const float* scores, const int* lengths
     const size_t need = d2p_swa_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
-    const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 3);
+    const wf::Layout ws = swa::affine_layout(workspace, B, max_L1, max_L2, true);
     const int r = swa::launch_forward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
                                       temperature, ws, partition, st);
     if (r != D2P_OK) return r;

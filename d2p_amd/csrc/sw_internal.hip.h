@@ -11,13 +11,8 @@ namespace sw {
 
 using Layout = wf::Layout;
 
-// Parts per element (G) and stripes per part (SPW) of a launch: G > 1 only when the
-// layout has the split areas.  D2P_AMD_SPLIT=<n> in the environment forces n parts
-// (at most one per stripe); unset or 0 chooses automatically.
-struct Split {
-    int G, SPW;
-};
-Split choose_split(int B, int max_L1, const Layout& ws);
+using Split = wf::Split;
+using wf::choose_split;
 
 // Checks shared by the entry points (sizes, LDS budget); D2P_OK or an error code.
 int check_shape(int B, int max_L1, int max_L2, float temperature);

@@ -40,7 +40,7 @@ constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do 
 // previous part's last stripe from `brow` (device-coherent loads, one chunk ahead)
 // after that part's progress word allows it; the last stripe of a part publishes its
 // own word two chunks behind its stores.  G == 1 writes the partition; G > 1 writes
-// the part's (max, scaled sum) for sw_partition_merge.
+// the part's (max, scaled sum) for the partition merge.
 __global__ void __launch_bounds__(NW * 64)
 sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                   float* __restrict__ alpha_sk, float* __restrict__ brow,
@@ -222,33 +222,6 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
         for (int w = 0; w < NW; ++w) tot.merge(red_m[w], red_z[w], c);
         if (G == 1) partition[b] = tot.m + tl * fast_log2(tot.z);
         else fpart[(size_t)b * G + part] = make_float2(tot.m, tot.z);
-    }
-}
-
-// partition[b] of a split element: the parts' (max, scaled sum) and the cell (0,0).
-__global__ void sw_partition_merge(const float2* __restrict__ fpart, float* __restrict__ partition,
-                                   int B, int G, float T) {
-    const int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= B) return;
-    const float c = kLog2e / T;
-    OnlineLSE tot;
-    tot.m = 0.0f;
-    tot.z = 1.0f;
-    for (int g = 0; g < G; ++g) {
-        const float2 v = fpart[(size_t)b * G + g];
-        tot.merge(v.x, v.y, c);
-    }
-    partition[b] = tot.m + T * kLn2 * fast_log2(tot.z);
-}
-
-// Status words and progress words of split elements start at zero.
-__global__ void split_reset(int* __restrict__ status, uint64_t* __restrict__ fflag,
-                            uint64_t* __restrict__ bflag, int B, int G) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < B) status[i] = 0;
-    if (i < B * G) {
-        store_flag(fflag + i, 0);
-        store_flag(bflag + i, 0);
     }
 }
 
@@ -584,31 +557,6 @@ int check_shape(int B, int max_L1, int max_L2, float temperature) {
     return D2P_OK;
 }
 
-Split choose_split(int B, int max_L1, const Layout& ws) {
-    const int ns = (max_L1 + 63) / 64;
-    Split sp{1, ns > 0 ? ns : 1};
-    if (ws.fflag == nullptr || ns <= 1) return sp;
-    int G = 0;
-    if (const char* e = getenv("D2P_AMD_SPLIT")) G = atoi(e);
-    if (G <= 0) {
-        // Parts of 4 stripes (one wave per SIMD: the pipeline's per-step latency is
-        // lowest when a wave has its SIMD to itself) if the whole grid is resident at
-        // once; else parts of 8 (one stripe per wave), or as few parts as fit.
-        if (ns <= 4) return sp;
-        const int cus = device_cus();
-        G = (ns + 3) / 4;
-        if (wf::split_grid(B, G) > cus) {
-            G = (ns + wf::NW - 1) / wf::NW;
-            while (G > 1 && wf::split_grid(B, G) > cus) --G;
-        }
-    }
-    G = G < ns ? G : ns;
-    if (G <= 1) return sp;
-    sp.SPW = (ns + G - 1) / G;
-    sp.G = (ns + sp.SPW - 1) / sp.SPW;   // no part without stripes
-    return sp;
-}
-
 int launch_forward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                    float gap, float T, const Layout& ws, float* partition, hipStream_t st) {
     const int ns = (max_L1 + 63) / 64;
@@ -616,18 +564,15 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
     const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
     const size_t lds = lds_forward_r(R);
     const uint32_t epoch = next_epoch();
-    if (sp.G > 1)
-        D2P_LAUNCH("split_reset", split_reset, dim3((B * sp.G + 255) / 256), dim3(256), 0, st,
-                   ws.status, ws.fflag, ws.bflag, B, sp.G);
+    if (sp.G > 1 && wf::launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
     D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     D2P_LAUNCH("sw_forward", sw_forward_kernel, dim3(wf::split_grid(B, sp.G)),
                dim3(wf::NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
                ws.status, ws.fflag, ws.fpart, B, max_L1, max_L2, ns, gap, T, R, sp.G, sp.SPW,
                epoch);
-    if (sp.G > 1)
-        D2P_LAUNCH("sw_partition_merge", sw_partition_merge, dim3((B + 255) / 256), dim3(256), 0,
-                   st, ws.fpart, partition, B, sp.G, T);
+    if (sp.G > 1 && wf::launch_partition_merge(ws, partition, B, sp.G, T, st) != D2P_OK)
+        return D2P_ERR_HIP;
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }

@@ -12,6 +12,10 @@ using Layout = wf::Layout;   // three planes (M, I, D)
 
 int check_shape(int B, int max_L1, int max_L2, float temperature);
 
+// The first-order workspace prefix; split: with the split-element areas (the flows
+// area holds a float4 and a float per stripe and step).
+Layout affine_layout(void* workspace, int B, int max_L1, int max_L2, bool split);
+
 // Forward sweep: (M, I, D) tables, last rows and partition[B] (status words reset).
 int launch_forward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                    float go, float ge, float T, const Layout& ws, float* partition,

@@ -644,7 +644,7 @@ struct Second {
 
 Second second_layout(void* ws, int B, int L1, int L2) {
     Second w;
-    w.prim = layout(ws, B, L1, L2, 3);
+    w.prim = swa::affine_layout(ws, B, L1, L2, true);
     char* p = (char*)ws + round256(w.prim.bytes);
     const size_t ns = ((size_t)L1 + 63) / 64;
     w.tan_sk = (float*)p;

@@ -86,14 +86,16 @@ struct Layout {
     // reverse-sweep boundary flows [B][stripe][step], per-part partial results
     uint64_t* fflag;
     uint64_t* bflag;
-    float2* flows;
+    float2* flows;     // (linear SW: float2 per step; affine: a float4 and a float
+                       // plane of flow_slots each)
+    size_t flow_slots; // B * stripes * stored steps
     float2* fpart;     // [B][stripe] (max, scaled sum) of the partition
-    double* bpart;     // [B][stripe][2] parameter-gradient sums
+    double* bpart;     // [B][stripe][4] parameter-gradient sums
     size_t bytes;      // bytes of this prefix
 };
 
 __host__ inline Layout layout(void* workspace, int B, int max_L1, int max_L2, int planes = 1,
-                              bool split = false) {
+                              bool split = false, int flow_bytes = 8) {
     Layout l;
     l.status = (int*)workspace;
     l.trash = (float*)((char*)workspace + status_bytes(B));
@@ -103,6 +105,7 @@ __host__ inline Layout layout(void* workspace, int B, int max_L1, int max_L2, in
     l.bytes = status_bytes(B) + TRASH_BYTES + table_floats(B, max_L1, max_L2, planes) * sizeof(float);
     l.fflag = l.bflag = nullptr;
     l.flows = l.fpart = nullptr;
+    l.flow_slots = 0;
     l.bpart = nullptr;
     if (split) {
         char* p = (char*)workspace + round256(l.bytes);
@@ -112,15 +115,31 @@ __host__ inline Layout layout(void* workspace, int B, int max_L1, int max_L2, in
         l.bflag = (uint64_t*)p;
         p += round256(parts * sizeof(uint64_t));
         l.flows = (float2*)p;
-        p += round256(parts * (size_t)stored_steps(max_L2) * sizeof(float2));
+        l.flow_slots = parts * (size_t)stored_steps(max_L2);
+        p += round256(l.flow_slots * (size_t)flow_bytes);
         l.fpart = (float2*)p;
         p += round256(parts * sizeof(float2));
         l.bpart = (double*)p;
-        p += round256(parts * 2 * sizeof(double));
+        p += round256(parts * 4 * sizeof(double));
         l.bytes = (size_t)(p - (char*)workspace);
     }
     return l;
 }
+
+// Parts per element (G) and stripes per part (SPW) of a launch: G > 1 only when the
+// layout has the split areas.  D2P_AMD_SPLIT=<n> in the environment forces n parts
+// (at most one per stripe); unset or 0 chooses automatically.
+struct Split {
+    int G, SPW;
+};
+Split choose_split(int B, int max_L1, const Layout& ws);
+
+// Before a split forward sweep: status words and progress words to zero.
+int launch_split_reset(const Layout& ws, int B, int G, hipStream_t st);
+// After it: partition[b] from the parts' (max, scaled sum) in ws.fpart and the cell
+// (0, 0), whose value is 0.
+int launch_partition_merge(const Layout& ws, float* partition, int B, int G, float T,
+                           hipStream_t st);
 
 // Issue priority of a wave by its stripe's place in the pipeline: every stripe
 // waits on the one before it, so the upstream stripes set the pace and are served

@@ -76,6 +76,9 @@ def test_workspace_sizes(lib, fn, planes):
     if fn == "d2p_sw_workspace_bytes":
         # split elements: boundary flows, one (up, diagonal) pair per stripe and step
         table += 2 * 2 * steps * 2 * 4
+    elif fn == "d2p_swa_workspace_bytes":
+        # split elements: boundary flows, a float4 and a float per stripe and step
+        table += 2 * 2 * steps * 5 * 4
     assert table <= small <= table + 4096
     # every workspace starts with status words: never zero for B > 0
     assert f(1, 0, 0) > 0

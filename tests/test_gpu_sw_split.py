@@ -131,3 +131,57 @@ def test_sw_split_backward_full(cuda, parts):
         per = 1e-4 * max(1.0, np.abs(J).max()) + allow
         tol = per * np.abs(ga.numpy()).sum(axis=(1, 2))
         assert np.all(np.abs(g.cpu().numpy() - ref) <= tol), (p, g.cpu().numpy(), ref, tol)
+
+
+# ---------------------------------------------------------------- affine gap
+
+AFFINE_CASES = [
+    # (seed, B, L1, L2, gap_open, gap_ext, T, parts)
+    (40, 2, 600, 90, -2.0, -0.5, 1.0, 1),     # unsplit, more stripes than waves
+    (41, 1, 300, 200, -11.0, -1.0, 0.5, 2),   # parts of 3 and 2 stripes
+    (42, 3, 500, 130, -2.0, -0.5, 1.0, 8),    # one stripe per part
+    (43, 2, 1300, 150, -3.0, -1.0, 1.0, 2),   # several stripes per wave in each part
+    (44, 9, 200, 70, -2.0, -0.5, 1.0, 4),     # idle workgroups in the grid
+    (45, 2, 1024, 1024, -11.0, -1.0, 0.5, 0), # automatic choice (4 parts of 4 stripes)
+]
+
+
+@pytest.mark.parametrize("seed,B,L1,L2,go,ge,T,n", AFFINE_CASES)
+def test_affine_split_matches_oracle(cuda, parts, seed, B, L1, L2, go, ge, T, n):
+    from test_gpu_sw_affine import _check as _check_affine
+    parts(n)
+    s = _seeded(seed, (B, L1, L2), 2.0)
+    ref = O.get("oracle").soft_sw_affine(s.numpy(), go, ge, T)
+    gpu = _capi.swa_forward_marginals(s.to(cuda), None, go, ge, T)
+    torch.cuda.synchronize()
+    _check_affine(gpu, ref, s.numpy(), go, ge, T)
+
+
+def test_affine_split_ragged(cuda, parts):
+    """Config C3 style lengths under 4 parts: elements whose later parts are empty."""
+    from test_gpu_sw_affine import _check as _check_affine
+    parts(4)
+    B, L1, L2 = 6, 700, 260
+    s = _seeded(46, (B, L1, L2), 2.0)
+    g = torch.Generator().manual_seed(47)
+    lens = torch.randint(64, L1 + 1, (B, 2), generator=g, dtype=torch.int32)
+    lens[:, 1] = torch.clamp(lens[:, 1], max=L2)
+    lens[1] = torch.tensor([0, 100])
+    lens[2] = torch.tensor([640, 0])
+    lens[3] = torch.tensor([L1, L2])
+    lens[4] = torch.tensor([150, 260])
+    ref = O.get("oracle").soft_sw_affine(s.numpy(), -11.0, -1.0, 0.5, lens.numpy())
+    gpu = _capi.swa_forward_marginals(s.to(cuda), lens.to(cuda), -11.0, -1.0, 0.5)
+    torch.cuda.synchronize()
+    _check_affine(gpu, ref, s.numpy(), -11.0, -1.0, 0.5, lens.tolist())
+
+
+def test_affine_split_hvp(cuda, parts):
+    """The affine second-order entry points run split primal sweeps."""
+    from test_gpu_sw_affine_second import _close as _close_affine
+    parts(3)
+    s = _seeded(48, (2, 600, 70))
+    v = _seeded(49, (2, 600, 70))
+    ref = O.get("oracle").soft_sw_affine_hvp(s.numpy(), v.numpy(), -2.0, -0.5, 1.0)
+    _close_affine(_capi.swa_hvp(s.to(cuda), v.to(cuda), None, -2.0, -0.5, 1.0), ref,
+                  "affine hvp, split primal sweeps")
