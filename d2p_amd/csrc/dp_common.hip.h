@@ -27,16 +27,18 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
-// Whole-wave lane shifts through DPP (no LDS round trip).
-// wave_shr1: lane r receives lane r-1's value, lane 0 receives `fill`.
-__device__ __forceinline__ float wave_shr1(float v, float fill) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(
-        __float_as_int(fill), __float_as_int(v), 0x138, 0xf, 0xf, false));
+// Whole-wave lane shifts through DPP (no LDS round trip).  The boundary lane
+// receives 0 (bound_ctrl: one instruction, no fill register); the sweeps use these
+// where the boundary lane's value is 0 or is never read.
+// wave_shr1: lane r receives lane r-1's value, lane 0 receives 0.
+__device__ __forceinline__ float wave_shr1(float v) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x138, 0xf, 0xf, true));
 }
-// wave_shl1: lane r receives lane r+1's value, lane 63 receives `fill`.
-__device__ __forceinline__ float wave_shl1(float v, float fill) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(
-        __float_as_int(fill), __float_as_int(v), 0x130, 0xf, 0xf, false));
+// wave_shl1: lane r receives lane r+1's value, lane 63 receives 0.
+__device__ __forceinline__ float wave_shl1(float v) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x130, 0xf, 0xf, true));
 }
 
 // DPP shifts whose boundary lane takes its value from `old` (per lane) instead of a

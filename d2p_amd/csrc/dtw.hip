@@ -126,7 +126,7 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
             for (int u = 0; u < P; ++u) {
                 const int t = t0 + u;
                 const float up = wave_shr1_or(cur, rreg);   // lane 0: stripe above
-                rreg = wave_shl1(rreg, kPINF);
+                rreg = wave_shl1(rreg);
                 const float diag = up_prev;
                 up_prev = up;
                 // out-of-table and out-of-band neighbours are PINF
@@ -262,8 +262,8 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
                 const float d1 = lane_bcast(pre_d, 62);
                 if (lane == 63) { in_up = u0; in_diag = d0; in_diag_next = d1; }
             }
-            float pre_d2 = wave_shr1(pre_d, 0.0f);
-            pre_d2 = wave_shr1(pre_d2, 0.0f);
+            float pre_d2 = wave_shr1(pre_d);
+            pre_d2 = wave_shr1(pre_d2);
             // FULL: every cell of the chunk lies inside the element, no validity masks
             auto steps = [&](auto full) {
             constexpr bool FULL = decltype(full)::value;
@@ -273,7 +273,7 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
                 const int col = t - lane;
                 const bool ok = FULL || ((unsigned)col < (unsigned)L2eff && in_band(ej, col + 1, bw));
                 const float a0 = A[u], a1 = A[u + 1];
-                const float bv_next = wave_shl1(bv, kPINF);
+                const float bv_next = wave_shl1(bv);
                 const float upa = wave_shr1_or(a1, bv);
                 const float dga = wave_shr1_or(A[u + 2], bv_next);
                 bv = bv_next;
@@ -295,12 +295,12 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
                 const float ea = (od * dga + ou * upa) + ol * a1;   // beta * E_w[alpha_pred]
                 g_acc += (ok && smv < kPINF) ? bl * smv - ea : 0.0f;
                 pub[u] = make_float2(ou, od);
-                pre_u = wave_shr1(pre_u, 0.0f);
+                pre_u = wave_shr1(pre_u);
                 in_left = ol;
                 in_up = wave_shl1_or(ou, pre_u);
                 in_diag = in_diag_next;
                 in_diag_next = wave_shl1_or(od, pre_d2);
-                pre_d2 = wave_shr1(pre_d2, 0.0f);
+                pre_d2 = wave_shr1(pre_d2);
             }
             };
             if (bw < 0 && i0 + 63 < L1 && t_hi - P - 62 >= 0 && t_hi < L2) steps(std::true_type{});

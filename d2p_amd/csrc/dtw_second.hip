@@ -133,11 +133,11 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
                 const bool ok = (unsigned)col < (unsigned)L2eff && in_band(ej, col + 1, bw);
                 const float a0 = Aw[u + 2], a1 = Aw[u + 1];
                 const float dga = wave_shr1_or(Aw[u], bv);
-                const float bvn = wave_shl1(bv, kPINF);
+                const float bvn = wave_shl1(bv);
                 const float upa = wave_shr1_or(a1, bvn);
                 bv = bvn;
                 const float tu = wave_shr1_or(cur, rreg);
-                rreg = wave_shl1(rreg, 0.0f);
+                rreg = wave_shl1(rreg);
                 const float td = up_prev;
                 up_prev = tu;
                 const float tl = cur;
@@ -301,15 +301,15 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
                     db2 = d1b; dg2 = d1g;
                 }
             }
-            qdb = wave_shr1(wave_shr1(qdb, 0.0f), 0.0f);
-            qdg = wave_shr1(wave_shr1(qdg, 0.0f), 0.0f);
+            qdb = wave_shr1(wave_shr1(qdb));
+            qdg = wave_shr1(wave_shr1(qdg));
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t_hi - u;
                 const int col = t - lane;
                 const bool ok = (unsigned)col < (unsigned)L2eff && in_band(ej, col + 1, bw);
                 const float a1 = A[u + 1], x1 = X[u + 1];
-                const float nA = wave_shl1(bA, kPINF), nX = wave_shl1(bX, 0.0f);
+                const float nA = wave_shl1(bA), nX = wave_shl1(bX);
                 const float upa = wave_shr1_or(a1, bA), upx = wave_shr1_or(x1, bX);
                 const float dga = wave_shr1_or(A[u + 2], nA), dgx = wave_shr1_or(X[u + 2], nX);
                 bA = nA;
@@ -343,8 +343,8 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
                 const float ogd = gl * wd + bl * dwd, ogu = gl * wu + bl * dwu;
                 const float ogl = gl * wl + bl * dwl;
                 pub[u] = make_float4(obu, ogu, obd, ogd);
-                qub = wave_shr1(qub, 0.0f);
-                qug = wave_shr1(qug, 0.0f);
+                qub = wave_shr1(qub);
+                qug = wave_shr1(qug);
                 lb = obl;
                 lg = ogl;
                 ubt = wave_shl1_or(obu, qub);
@@ -353,8 +353,8 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
                 dg = dg2;
                 db2 = wave_shl1_or(obd, qdb);
                 dg2 = wave_shl1_or(ogd, qdg);
-                qdb = wave_shr1(qdb, 0.0f);
-                qdg = wave_shr1(qdg, 0.0f);
+                qdb = wave_shr1(qdb);
+                qdg = wave_shr1(qdg);
             }
             wave_lds_sync();
             if (!DOT) write_tile<P, -1>(otile, obase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);

@@ -193,9 +193,9 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const int t = t0 + u;
                 const float uM = wave_shr1_or(cM, rM), uI = wave_shr1_or(cI, rI),
                             uD = wave_shr1_or(cD, rD);
-                rM = wave_shl1(rM, kNINF);
-                rI = wave_shl1(rI, kNINF);
-                rD = wave_shl1(rD, kNINF);
+                rM = wave_shl1(rM);
+                rI = wave_shl1(rI);
+                rD = wave_shl1(rD);
                 const float dM = pM, dI = pI, dD = pD;   // diagonal = previous step's up
                 pM = uM;
                 pI = uI;
@@ -495,9 +495,9 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 }
             }
             // lane 63 = step 2 of the diagonal flows (then shifted on)
-            qDM = wave_shr1(wave_shr1(qDM, 0.0f), 0.0f);
-            qDI = wave_shr1(wave_shr1(qDI, 0.0f), 0.0f);
-            qDD = wave_shr1(wave_shr1(qDD, 0.0f), 0.0f);
+            qDM = wave_shr1(wave_shr1(qDM));
+            qDI = wave_shr1(wave_shr1(qDI));
+            qDD = wave_shr1(wave_shr1(qDD));
             // FULL: every cell of the chunk lies inside the element, no validity masks
             auto steps = [&](auto full) {
             constexpr bool FULL = decltype(full)::value;
@@ -509,8 +509,8 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 const float sc = ok ? sv[u] : kNINF;
                 // predecessors: left = own previous step, up / diagonal = lane r-1 (lane 0:
                 // the stripe above's last row)
-                const float nbM = wave_shl1(bM, kNINF), nbI = wave_shl1(bI, kNINF),
-                            nbD = wave_shl1(bD, kNINF);
+                const float nbM = wave_shl1(bM), nbI = wave_shl1(bI),
+                            nbD = wave_shl1(bD);
                 const float upM = wave_shr1_or(AM[u + 1], bM), upI = wave_shr1_or(AI[u + 1], bI);
                 const float dgM = wave_shr1_or(AM[u + 2], nbM), dgI = wave_shr1_or(AI[u + 2], nbI),
                             dgD = wave_shr1_or(AD[u + 2], nbD);
@@ -560,8 +560,8 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 pub4[u] = make_float4(oUM, oUI, oDM, oDI);
                 pub1[u] = oDD;
                 // successor contributions for the next steps; lane 63 takes the ring
-                qUM = wave_shr1(qUM, 0.0f);
-                qUI = wave_shr1(qUI, 0.0f);
+                qUM = wave_shr1(qUM);
+                qUI = wave_shr1(qUI);
                 lM = oLM;
                 lD = oLD;
                 uM = wave_shl1_or(oUM, qUM);
@@ -572,9 +572,9 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 dM2 = wave_shl1_or(oDM, qDM);
                 dI2 = wave_shl1_or(oDI, qDI);
                 dD2 = wave_shl1_or(oDD, qDD);
-                qDM = wave_shr1(qDM, 0.0f);
-                qDI = wave_shr1(qDI, 0.0f);
-                qDD = wave_shr1(qDD, 0.0f);
+                qDM = wave_shr1(qDM);
+                qDI = wave_shr1(qDI);
+                qDD = wave_shr1(qDD);
             }
             };
             if (i0 + 63 < L1 && t_hi - P - 62 >= 0 && t_hi < L2) steps(std::true_type{});

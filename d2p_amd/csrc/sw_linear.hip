@@ -160,7 +160,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                 for (int u = 0; u < P; ++u) {
                     const int t = t0 + u;
                     const float up = wave_shr1_or(cur, rreg);   // lane 0: stripe above
-                    rreg = wave_shl1(rreg, kNINF);
+                    rreg = wave_shl1(rreg);
                     const float diag = up_prev;
                     up_prev = up;
                     // out-of-table neighbours are NINF, so no i>1 / j>1 guards are needed
@@ -405,8 +405,8 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 if (lane == 63) { in_up = u0; in_diag = d0; in_diag_next = d1; }
             }
             Acc gs[P], ps[P];
-            float pre_d2 = wave_shr1(pre_d, 0.0f);   // lane 63 = step 1 (then shifted on)
-            pre_d2 = wave_shr1(pre_d2, 0.0f);        // lane 63 = step 2
+            float pre_d2 = wave_shr1(pre_d);   // lane 63 = step 1 (then shifted on)
+            pre_d2 = wave_shr1(pre_d2);        // lane 63 = step 2
             // FULL: every cell of the chunk lies inside the element, no validity masks
             auto steps = [&](auto full) {
             constexpr bool FULL = decltype(full)::value;
@@ -418,7 +418,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const float sc = ok ? sv[u] : kNINF;
                 const float a0 = A[u], a1 = A[u + 1];
                 // up / diagonal alphas from lane r-1; lane 0 takes the row above
-                const float bv_next = wave_shl1(bv, kNINF);
+                const float bv_next = wave_shl1(bv);
                 const float upa = wave_shr1_or(a1, bv);
                 const float dga = wave_shr1_or(A[u + 2], bv_next);
                 bv = bv_next;
@@ -443,12 +443,12 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 ps[u] = (Acc)(pv * sc);
                 pub[u] = make_float2(ou, od);
                 // successor contributions for the next steps; lane 63 takes the ring
-                pre_u = wave_shr1(pre_u, 0.0f);
+                pre_u = wave_shr1(pre_u);
                 in_left = ol;
                 in_up = wave_shl1_or(ou, pre_u);
                 in_diag = in_diag_next;
                 in_diag_next = wave_shl1_or(od, pre_d2);
-                pre_d2 = wave_shr1(pre_d2, 0.0f);
+                pre_d2 = wave_shr1(pre_d2);
             }
             };
             if (i0 + 63 < L1 && t_hi - P - 62 >= 0 && t_hi < L2) steps(std::true_type{});

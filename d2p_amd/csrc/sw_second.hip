@@ -196,12 +196,12 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 // r-1 one / two steps back (lane 0: the last row above)
                 const float a0 = Aw[u + 2], a1 = Aw[u + 1];
                 const float dga = wave_shr1_or(Aw[u], bv);
-                const float bvn = wave_shl1(bv, kNINF);
+                const float bvn = wave_shl1(bv);
                 const float upa = wave_shr1_or(a1, bvn);
                 bv = bvn;
                 // tangent predecessors
                 const float tu = wave_shr1_or(cur, rreg);
-                rreg = wave_shl1(rreg, 0.0f);
+                rreg = wave_shl1(rreg);
                 const float td = up_prev;
                 up_prev = tu;
                 const float tl = cur;
@@ -469,8 +469,8 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                     db2 = d1b; dg2 = d1g;
                 }
             }
-            qdb = wave_shr1(wave_shr1(qdb, 0.0f), 0.0f);
-            qdg = wave_shr1(wave_shr1(qdg, 0.0f), 0.0f);
+            qdb = wave_shr1(wave_shr1(qdb));
+            qdg = wave_shr1(wave_shr1(qdg));
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t_hi - u;
@@ -479,7 +479,7 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 const float vd = ok ? vv[u] : 0.0f;
                 // primal and tangent predecessors
                 const float a0 = A[u], a1 = A[u + 1], x0 = X[u], x1 = X[u + 1];
-                const float nA = wave_shl1(bA, kNINF), nX = wave_shl1(bX, 0.0f);
+                const float nA = wave_shl1(bA), nX = wave_shl1(bX);
                 const float upa = wave_shr1_or(a1, bA), upx = wave_shr1_or(x1, bX);
                 const float dga = wave_shr1_or(A[u + 2], nA), dgx = wave_shr1_or(X[u + 2], nX);
                 bA = nA;
@@ -536,8 +536,8 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 const float og2 = gl * w2 + bl * dw2;
                 pub[u] = make_float4(ob1, og1, ob0, og0);
                 // successor flows for the next steps; lane 63 takes the ring
-                qub = wave_shr1(qub, 0.0f);
-                qug = wave_shr1(qug, 0.0f);
+                qub = wave_shr1(qub);
+                qug = wave_shr1(qug);
                 lb = ob2;
                 lg = og2;
                 ubt = wave_shl1_or(ob1, qub);
@@ -546,8 +546,8 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 dg = dg2;
                 db2 = wave_shl1_or(ob0, qdb);
                 dg2 = wave_shl1_or(og0, qdg);
-                qdb = wave_shr1(qdb, 0.0f);
-                qdg = wave_shr1(qdg, 0.0f);
+                qdb = wave_shr1(qdb);
+                qdg = wave_shr1(qdg);
             }
             wave_lds_sync();
             if (!DOT) write_tile<P, -1>(otile, obase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);

@@ -167,8 +167,8 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
                 // primal predecessors
                 const float dM = wave_shr1_or(AM[u], bM), dI = wave_shr1_or(AI[u], bI),
                             dD = wave_shr1_or(AD[u], bD);
-                const float nbM = wave_shl1(bM, kNINF), nbI = wave_shl1(bI, kNINF),
-                            nbD = wave_shl1(bD, kNINF);
+                const float nbM = wave_shl1(bM), nbI = wave_shl1(bI),
+                            nbD = wave_shl1(bD);
                 const float uM = wave_shr1_or(AM[u + 1], nbM), uI = wave_shr1_or(AI[u + 1], nbI);
                 bM = nbM;
                 bI = nbI;
@@ -177,9 +177,9 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
                 // tangent predecessors
                 const float tuM = wave_shr1_or(cM, rM), tuI = wave_shr1_or(cI, rI),
                             tuD = wave_shr1_or(cD, rD);
-                rM = wave_shl1(rM, 0.0f);
-                rI = wave_shl1(rI, 0.0f);
-                rD = wave_shl1(rD, 0.0f);
+                rM = wave_shl1(rM);
+                rI = wave_shl1(rI);
+                rD = wave_shl1(rD);
                 const float tdM = pM, tdI = pI, tdD = pD;
                 pM = tuM;
                 pI = tuI;
@@ -445,12 +445,12 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                     ebM = n0; egM = n1; ebI = n2; egI = n3; ebD = n4; egD = n5;
                 }
             }
-            float qdb0 = wave_shr1(wave_shr1(qD.x, 0.0f), 0.0f);
-            float qdg0 = wave_shr1(wave_shr1(qD.y, 0.0f), 0.0f);
-            float qdb1 = wave_shr1(wave_shr1(qD.z, 0.0f), 0.0f);
-            float qdg1 = wave_shr1(wave_shr1(qD.w, 0.0f), 0.0f);
-            float qdb2 = wave_shr1(wave_shr1(qE.x, 0.0f), 0.0f);
-            float qdg2 = wave_shr1(wave_shr1(qE.y, 0.0f), 0.0f);
+            float qdb0 = wave_shr1(wave_shr1(qD.x));
+            float qdg0 = wave_shr1(wave_shr1(qD.y));
+            float qdb1 = wave_shr1(wave_shr1(qD.z));
+            float qdg1 = wave_shr1(wave_shr1(qD.w));
+            float qdb2 = wave_shr1(wave_shr1(qE.x));
+            float qdg2 = wave_shr1(wave_shr1(qE.y));
             float qub0 = qU.x, qug0 = qU.y, qub1 = qU.z, qug1 = qU.w;
 #pragma unroll
             for (int u = 0; u < P; ++u) {
@@ -459,10 +459,10 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 const float sc = ok ? sv[u] : kNINF;
                 const float vd = ok ? vv[u] : 0.0f;
                 // primal and tangent predecessors
-                const float nAM = wave_shl1(bAM, kNINF), nAI = wave_shl1(bAI, kNINF),
-                            nAD = wave_shl1(bAD, kNINF);
-                const float nXM = wave_shl1(bXM, 0.0f), nXI = wave_shl1(bXI, 0.0f),
-                            nXD = wave_shl1(bXD, 0.0f);
+                const float nAM = wave_shl1(bAM), nAI = wave_shl1(bAI),
+                            nAD = wave_shl1(bAD);
+                const float nXM = wave_shl1(bXM), nXI = wave_shl1(bXI),
+                            nXD = wave_shl1(bXD);
                 const float upM = wave_shr1_or(AM[u + 1], bAM), upI = wave_shr1_or(AI[u + 1], bAI);
                 const float uxM = wave_shr1_or(XM[u + 1], bXM), uxI = wave_shr1_or(XI[u + 1], bXI);
                 const float dgAM = wave_shr1_or(AM[u + 2], nAM), dgAI = wave_shr1_or(AI[u + 2], nAI),
@@ -572,10 +572,10 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                     outE[slot0 + u] = make_float2(obD0, ogD0);
                 }
                 // successor flows for the next steps; lane 63 takes the rings
-                qub0 = wave_shr1(qub0, 0.0f);
-                qug0 = wave_shr1(qug0, 0.0f);
-                qub1 = wave_shr1(qub1, 0.0f);
-                qug1 = wave_shr1(qug1, 0.0f);
+                qub0 = wave_shr1(qub0);
+                qug0 = wave_shr1(qug0);
+                qub1 = wave_shr1(qub1);
+                qug1 = wave_shr1(qug1);
                 lbM = obMl; lgM = ogMl; lbD = obDl; lgD = ogDl;
                 ubM = wave_shl1_or(obMu, qub0);
                 ugM = wave_shl1_or(ogMu, qug0);
@@ -588,12 +588,12 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 egI = wave_shl1_or(ogI0, qdg1);
                 ebD = wave_shl1_or(obD0, qdb2);
                 egD = wave_shl1_or(ogD0, qdg2);
-                qdb0 = wave_shr1(qdb0, 0.0f);
-                qdg0 = wave_shr1(qdg0, 0.0f);
-                qdb1 = wave_shr1(qdb1, 0.0f);
-                qdg1 = wave_shr1(qdg1, 0.0f);
-                qdb2 = wave_shr1(qdb2, 0.0f);
-                qdg2 = wave_shr1(qdg2, 0.0f);
+                qdb0 = wave_shr1(qdb0);
+                qdg0 = wave_shr1(qdg0);
+                qdb1 = wave_shr1(qdb1);
+                qdg1 = wave_shr1(qdg1);
+                qdb2 = wave_shr1(qdb2);
+                qdg2 = wave_shr1(qdg2);
             }
             wave_lds_sync();
             if (!DOT) write_tile<P, -1>(otile, obase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
