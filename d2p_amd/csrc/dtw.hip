@@ -245,7 +245,7 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
             A[0] = A[P];
             A[1] = A[P + 1];
 #pragma unroll
-            for (int j = 0; j < P; ++j) A[j + 2] = buf[ABUF + j * 64 + lane];
+            for (int j = 0; j < P; ++j) A[j + 2] = buf[ABUF + rows_row<P, -1>(j) * 64 + lane];
             // lane j: alpha of the row above at lane-63 step t_hi - j + 63 (row 0: PINF)
             float bv = buf[RBUF + lane];
             bv = (s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1) ? bv : kPINF;

@@ -272,8 +272,8 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
             X[1] = X[P + 1];
 #pragma unroll
             for (int j = 0; j < P; ++j) {
-                A[j + 2] = buf[AR + j * 64 + lane];
-                X[j + 2] = buf[XR + j * 64 + lane];
+                A[j + 2] = buf[AR + rows_row<P, -1>(j) * 64 + lane];
+                X[j + 2] = buf[XR + rows_row<P, -1>(j) * 64 + lane];
             }
             const bool row_ok = s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1;
             float bA = row_ok ? buf[RA + lane] : kPINF;

@@ -369,7 +369,7 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
         // Loads of chunk k (t_hi = nsteps-1-kP): the score tile, P alpha rows per plane
         // (steps t_hi-2 .. t_hi-P-1) and the stripe above's last row per plane at steps
         // t_hi - j + 63 for lane j <= P (clamped; lanes past P repeat lane P).
-        // 4P + 3 loads.
+        // P + 3P/4 + 3 loads.
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
             dma_tile<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
@@ -440,9 +440,10 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
             AD[1] = AD[P + 1];
 #pragma unroll
             for (int j = 0; j < P; ++j) {
-                AM[j + 2] = wbuf[AROWS + j * 64 + lane];
-                AI[j + 2] = wbuf[AROWS + P * 64 + j * 64 + lane];
-                AD[j + 2] = wbuf[AROWS + 2 * P * 64 + j * 64 + lane];
+                const int r = rows_row<P, -1>(j) * 64 + lane;
+                AM[j + 2] = wbuf[AROWS + r];
+                AI[j + 2] = wbuf[AROWS + P * 64 + r];
+                AD[j + 2] = wbuf[AROWS + 2 * P * 64 + r];
             }
             const bool row_ok = s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1;
             float bM = row_ok ? wbuf[RROW + lane] : kNINF;
@@ -590,9 +591,9 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                     store_sys(flows1 + fo + k * P + lane, r1_out[slot]);
                 }
                 if (k >= 2) {
-                    // at least 4P + 3 loads, 2P marginal stores and 4 flow stores follow
-                    // the flow stores of chunk k - 2: those are complete
-                    wait_vmcnt<6 * P + 7>();
+                    // at least P + 3P/4 + 3 loads, 2P marginal stores and 4 flow stores
+                    // follow the flow stores of chunk k - 2: those are complete
+                    wait_vmcnt<3 * P + 3 * P / 4 + 7>();
                     if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
                 }
             }

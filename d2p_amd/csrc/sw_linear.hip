@@ -327,7 +327,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             const int th = nsteps - 1 - k * P;
             const uint32_t buf = lds_address(bufs + (k & 1) * BUF);
             dma_quads<P, -1>(buf, sbase, i0, L1max, L2max, lane, th);
-            dma_rows4<P, -1>(buf + ABUF * 4, astripe, th - 2, ul4);
+            dma_rows<P, -1>(buf + ABUF * 4, astripe, th - 2, ul4);
             uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
             uint32_t rl = buf + RBUF * 4;
             lds_dma_dword<0>(bup, roff, rl, 0u);

@@ -237,9 +237,9 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             }
             publish(prog, wave, l * PROG_STRIDE + k + 1);
             if (x_out && k >= 2) {
-                // at least 2P + 1 loads and 2P + 2 stores follow the row store of chunk
-                // k - 2: it (and everything before) is complete
-                wait_vmcnt<(4 * P + 3 < 63 ? 4 * P + 3 : 63)>();
+                // at least P + P/4 + 1 loads and 2P + 2 stores follow the row store of
+                // chunk k - 2: it (and everything before) is complete
+                wait_vmcnt<3 * P + P / 4 + 3>();
                 if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
             }
         }
@@ -424,8 +424,8 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             X[1] = X[P + 1];
 #pragma unroll
             for (int j = 0; j < P; ++j) {
-                A[j + 2] = buf[AR + j * 64 + lane];
-                X[j + 2] = buf[XR + j * 64 + lane];
+                A[j + 2] = buf[AR + rows_row<P, -1>(j) * 64 + lane];
+                X[j + 2] = buf[XR + rows_row<P, -1>(j) * 64 + lane];
             }
             const bool row_ok = s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1;
             float bA = row_ok ? buf[RA + lane] : kNINF;
@@ -556,9 +556,9 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 // this chunk's flows to the part above, by producer step
                 if (lane < P) store_sys4(flows_out + k * P + lane, ring_out[ring_index(k * P, R) + lane]);
                 if (k >= 2) {
-                    // at least 3P + 2 loads, 2 flow stores and (DOT: none, else 2P) output
-                    // stores follow the flow store of chunk k - 2: it is complete
-                    wait_vmcnt<(DOT ? 3 * P + 4 : 5 * P + 4)>();
+                    // at least P + P/2 + 2 loads, 2 flow stores and (DOT: none, else 2P)
+                    // output stores follow the flow store of chunk k - 2: it is complete
+                    wait_vmcnt<(DOT ? P + P / 2 + 4 : 3 * P + P / 2 + 4)>();
                     if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
                 }
             }

@@ -403,12 +403,13 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             XD[0] = XD[P]; XD[1] = XD[P + 1];
 #pragma unroll
             for (int j = 0; j < P; ++j) {
-                AM[j + 2] = buf[AR + j * 64 + lane];
-                AI[j + 2] = buf[AR + P * 64 + j * 64 + lane];
-                AD[j + 2] = buf[AR + 2 * P * 64 + j * 64 + lane];
-                XM[j + 2] = buf[XR + j * 64 + lane];
-                XI[j + 2] = buf[XR + P * 64 + j * 64 + lane];
-                XD[j + 2] = buf[XR + 2 * P * 64 + j * 64 + lane];
+                const int r = rows_row<P, -1>(j) * 64 + lane;
+                AM[j + 2] = buf[AR + r];
+                AI[j + 2] = buf[AR + P * 64 + r];
+                AD[j + 2] = buf[AR + 2 * P * 64 + r];
+                XM[j + 2] = buf[XR + r];
+                XI[j + 2] = buf[XR + P * 64 + r];
+                XD[j + 2] = buf[XR + 2 * P * 64 + r];
             }
             const bool row_ok = s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1;
             float bAM = row_ok ? buf[RA + lane] : kNINF;

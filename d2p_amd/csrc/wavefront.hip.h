@@ -361,6 +361,21 @@ __device__ __forceinline__ void lds_dma_dwordx4(const float* sbase, uint32_t& vo
         : "s"(sbase), "s"(vstep), "n"(LDS_STEP)
         : "memory", "m0", "scc");
 }
+// The same, marked non-temporal: for data read exactly once (the skewed tables), so
+// that it does not push reused lines (the score rows of the next chunk) out of L2.
+template <int LDS_STEP>
+__device__ __forceinline__ void lds_dma_dwordx4_nt(const float* sbase, uint32_t& voff,
+                                                   uint32_t& lds, uint32_t vstep) {
+    __asm__ volatile(
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %2 nt\n\t"
+        "s_add_u32 %1, %1, %4\n\t"
+        "v_add_u32 %0, %3, %0"
+        : "+v"(voff), "+s"(lds)
+        : "s"(sbase), "s"(vstep), "n"(LDS_STEP)
+        : "memory", "m0", "scc");
+}
 #pragma clang diagnostic pop
 
 // Waits until at most N vector-memory operations of this wave are outstanding
@@ -444,15 +459,6 @@ __device__ __forceinline__ void dma_tile(uint32_t tile_lds, const float* mbase, 
     }
 }
 
-// Issues the P loads of P consecutive steps t_first, t_first + DIR, ... of one plane
-// of a skewed table (plane_base = the plane's step -APAD) into P LDS rows of 64.
-template <int P, int DIR>
-__device__ __forceinline__ void dma_rows(uint32_t rows_lds, const float* plane_base, int t_first,
-                                         unsigned ul4) {
-    uint32_t voff = (uint32_t)(t_first + APAD) * 256u + ul4;
-#pragma unroll
-    for (int j = 0; j < P; ++j) lds_dma_dword<256>(plane_base, voff, rows_lds, (uint32_t)(DIR * 256));
-}
 
 // Writes a chunk's output tile back to a row-major [L1max][L2max] matrix: exactly P
 // stores.  Inside chunks write every cell (cells outside the element's lengths must
@@ -623,18 +629,19 @@ __device__ __forceinline__ void write_quads(const float* tile, float* obase, flo
     }
 }
 
-// Issues the loads of P consecutive steps of one plane of a skewed table with
-// 16-byte loads (four 256-byte step rows per instruction).  LDS row j then holds
+// Issues the loads of P consecutive steps of one plane of a skewed table (plane_base =
+// the plane's step -APAD) into P LDS rows of 64, with 16-byte non-temporal loads
+// (four 256-byte step rows per instruction, P/4 instructions).  LDS row j then holds
 // step t_first + j for DIR = +1 and step t_first - (P - 1) + j for DIR = -1; read
 // step t_first + DIR*j at row rows_row<P, DIR>(j).
 template <int P, int DIR>
-__device__ __forceinline__ void dma_rows4(uint32_t rows_lds, const float* plane_base, int t_first,
-                                          unsigned ul4) {
+__device__ __forceinline__ void dma_rows(uint32_t rows_lds, const float* plane_base, int t_first,
+                                         unsigned ul4) {
     static_assert(P % 4 == 0, "rows come in fours");
     const int t_lo = DIR > 0 ? t_first : t_first - (P - 1);
     uint32_t voff = (uint32_t)(t_lo + APAD) * 256u + 4u * ul4;
 #pragma unroll
-    for (int j = 0; j < P / 4; ++j) lds_dma_dwordx4<1024>(plane_base, voff, rows_lds, 1024u);
+    for (int j = 0; j < P / 4; ++j) lds_dma_dwordx4_nt<1024>(plane_base, voff, rows_lds, 1024u);
 }
 template <int P, int DIR>
 __device__ __host__ constexpr int rows_row(int j) { return DIR > 0 ? j : P - 1 - j; }
