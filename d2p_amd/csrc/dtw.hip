@@ -47,26 +47,33 @@ __device__ __forceinline__ bool in_band(float ej, int j, float bw) {
 __global__ void __launch_bounds__(NW * 64)
 dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ lengths,
                    float* __restrict__ alpha_sk, float* __restrict__ brow,
-                   float* __restrict__ value, int* __restrict__ status, int L1max, int L2max,
-                   int NSmax, float T, int bandwidth, int R) {
+                   float* __restrict__ value, int* __restrict__ status,
+                   uint64_t* __restrict__ fflag, int B, int L1max, int L2max, int NSmax,
+                   float T, int bandwidth, int R, int G, int SPW, uint32_t epoch) {
     constexpr int P = PF;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float terminal;
-    const int b = blockIdx.x;
+    // part of the element as in the linear-SW forward: the first stripe of a part > 0
+    // reads the previous part's last row from brow
+    int b, part;
+    split_decode(blockIdx.x, G, b, part);
+    if (b >= B) return;
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = ChunkTile<P>;
-    float* tiles = smem + wave * 2 * Tile::FLOATS;         // double-buffered cost chunk
-    float* rings = smem + NW * 2 * Tile::FLOATS;           // [NW][R]
-    float* sink = rings + NW * R + wave * DUMMY;       // per-wave write sink
+    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 64;        // two cost chunks, two rows
+    float* tiles = smem + wave * WBUF;                     // double-buffered cost chunk
+    float* rbufs = tiles + 2 * Tile::FLOATS;               // boundary row of a chunk
+    float* rings = smem + NW * WBUF;                       // [NW][R]
+    float* sink = rings + NW * R + wave * DUMMY;           // per-wave write sink
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
 
     if (lane == 0) prog[wave] = -1;
     if (threadIdx.x == 0) {
-        *st = 0;
+        if (G == 1) *st = 0;                               // G > 1: reset before the launch
         terminal = kPINF;
     }
     __syncthreads();
@@ -82,41 +89,76 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
     const int nch = (nsteps + P - 1) / P;
     const size_t NT = (size_t)stored_steps(L2max);
     const float* cbase = costs + (size_t)b * L1max * L2max;
+    const int s_begin = part * SPW;
+    const int NL = max(min(NS, s_begin + SPW) - s_begin, 0);   // stripes of this part
+    const bool has_next = s_begin + NL < NS;
+    const uint64_t* flag_in = fflag + (size_t)b * G + (part > 0 ? part - 1 : 0);
+    uint64_t* flag_out = fflag + (size_t)b * G + part;
 
-    for (int s = wave; s < NS; s += NW) {
+    for (int l = wave; l < NL; l += NW) {
+        const int s = s_begin + l;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;   // rows past L1 are never valid
         const float ej = band_centre(i0 + lane + 1, L1, L2);
         const bool last_row = i0 + lane == L1 - 1;
-        const float* ring_in = ring_from(rings, s, R);
-        float* ring_out = ring_of(rings, s, R);
+        const float* ring_in = ring_from(rings, l, R);
+        float* ring_out = ring_of(rings, l, R);
         float* out = alpha_sk + (((size_t)b * NSmax + s) * NT + APAD) * 64;
         float* brow_s = brow + ((size_t)b * NSmax + s) * NT;   // last row, by step
+        const float* brow_up = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
+        const bool x_in = l == 0 && part > 0;        // row above from the previous part
+        const bool x_out = l == NL - 1 && has_next;  // last row feeds the next part
+        int seen = -1;       // chunks of the previous part known to be complete
+        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
         // steps t < 0 hold the column-0 boundary (PINF), read by the reverse sweep
 #pragma unroll
         for (int t = -APAD; t < 0; ++t) lane_store(out + t * 64, ul4, kPINF);
         wave_lds_sync();   // the previous stripe's tile reads are complete
         const uint32_t tile_lds = lds_address(tiles);
+        const uint32_t row_lds = lds_address(rbufs);
+        // the boundary row of chunk k: lane j < P carries the step kP + 63 + j
+        auto issue_row = [&](int k) {
+            uint32_t off = (uint32_t)min(k * P + 63 + min(lane, P - 1), nsteps - 1) * 4u;
+            uint32_t dst = row_lds + (uint32_t)((k & 1) * 64 * 4);
+            lds_dma_dword_sys<0>(brow_up, off, dst, 0u);
+        };
+        if (x_in) {
+            seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
+            issue_row(0);
+        }
         dma_tile<P, 1>(tile_lds, cbase, i0, L1max, L2max, lane, 0);
         // lane 0 of the first stripe sees alpha[0,0] = 0 as its first diagonal
         float cur = kPINF, up_prev = (s == 0 && lane == 0) ? 0.0f : kPINF;
 
         for (int k = 0; k < nch; ++k) {
             const int t0 = k * P;
-            chunk_waits<P>(prog, s, NS, k, nch, R, st);
-            // this chunk's costs: loaded one chunk ago, followed by the P + 1 stores of
-            // that chunk (the first chunk's load is the last issued)
+            chunk_waits<P>(prog, l, NL, k, nch, R, st);
+            // this chunk's costs: loaded one chunk ago, followed by at least the P + 1
+            // stores of that chunk (the first chunk's load is the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (x_in && k > 0) {
+                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
+                const int got = flag_chunks(fl, epoch);
+                seen = got > seen ? got : seen;
+            }
             const float* tile = tiles + (k & 1) * Tile::FLOATS;
             float cv[P];
 #pragma unroll
             for (int u = 0; u < P; ++u) cv[u] = tile[tbase + u];
             // lane 0's up values: column t0+j sits in lane j (row 0 is PINF)
             float rreg = kPINF;
-            if (s > 0 && lane < P) rreg = ring_in[ring_index(t0 + lane + 63, R)];
-            if (k + 1 < nch)
+            if (s > 0 && lane < P)
+                rreg = x_in ? rbufs[(k & 1) * 64 + lane] : ring_in[ring_index(t0 + lane + 63, R)];
+            if (k + 1 < nch) {
+                if (x_in) {
+                    const int need = min(k + 1 + lead(P), nch);
+                    if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                    issue_row(k + 1);
+                }
                 dma_tile<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, cbase, i0, L1max,
                                L2max, lane, t0 + P);
+                if (x_in) fl = load_flag_async(flag_in);
+            }
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             float* outc = out + (size_t)t0 * 64;
             // FULL: every cell of the chunk lies inside the element, no validity masks
@@ -147,13 +189,31 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
             // the stripe's last row (lane 63) by step, contiguous, for the reverse sweep
             // of the stripe below; one store instruction
             wave_lds_sync();
-            if (lane < P) lane_store(brow_s, (unsigned)(t0 + lane) * 4u, ring_out[t0 % R + lane]);
-            publish(prog, wave, s * PROG_STRIDE + k + 1);
+            if (lane < P) {
+                const float v = ring_out[t0 % R + lane];
+                if (x_out) store_sys(brow_s + t0 + lane, v);
+                else lane_store(brow_s, (unsigned)(t0 + lane) * 4u, v);
+            }
+            publish(prog, wave, l * PROG_STRIDE + k + 1);
+            if (x_out && k >= 2) {
+                // at least P loads and 2P + 2 stores follow the row store of chunk k - 2:
+                // it (and everything before) is complete
+                wait_vmcnt<3 * P + 2>();
+                if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
+            }
+        }
+        if (x_out) {
+            wait_vmcnt<0>();
+            if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
         }
     }
 
+    // the value: the terminal cell, in the part that owns the last stripe (part 0 for
+    // an element without stripes)
     __syncthreads();
-    if (threadIdx.x == 0) value[b] = NS > 0 ? terminal : ((L1 == 0 && L2 == 0) ? 0.0f : kPINF);
+    const bool owner = NS > 0 ? (NL > 0 && s_begin + NL == NS) : part == 0;
+    if (threadIdx.x == 0 && owner)
+        value[b] = NS > 0 ? terminal : ((L1 == 0 && L2 == 0) ? 0.0f : kPINF);
 }
 
 template <int P>
@@ -161,12 +221,18 @@ __global__ void __launch_bounds__(NW * 64)
 dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ lengths,
                     const float* __restrict__ alpha_sk, const float* __restrict__ brow,
                     float* __restrict__ post, float* __restrict__ grad_T,
-                    int* __restrict__ status, float* __restrict__ trash, int L1max, int L2max,
-                    int NSmax, float T, int bandwidth, int R) {
-        extern __shared__ float smem[];
+                    int* __restrict__ status, float* __restrict__ trash,
+                    uint64_t* __restrict__ bflag, float2* __restrict__ flows,
+                    double* __restrict__ bpart, int B, int L1max, int L2max, int NSmax, float T,
+                    int bandwidth, int R, int G, int SPW, uint32_t epoch) {
+    extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red_g[NW];
-    const int b = blockIdx.x;
+    // parts run bottom-up as in the linear-SW backward
+    int b, dpart;
+    split_decode(blockIdx.x, G, b, dpart);
+    if (b >= B) return;
+    const int part = G - 1 - dpart;
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -176,7 +242,9 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
     using Tile = ChunkTile<P>;
     constexpr int ABUF = Tile::FLOATS;
     constexpr int RBUF = ABUF + P * 64;
-    constexpr int BUF = RBUF + 64;
+    constexpr int FBUF = RBUF + 64;               // flows from the part below (2P+2 floats)
+    constexpr int BUF = FBUF + 64;
+    static_assert(2 * P + 2 <= 64, "boundary flows fit their buffer");
     float* bufs = smem + wave * 2 * BUF;
     float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * BUF);  // [NW][R] (up, diag)
     float2* sink = rings + NW * R + wave * DUMMY;
@@ -197,14 +265,24 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
     const float* cbase = costs + (size_t)b * L1max * L2max;
     float* pbase = post + (size_t)b * L1max * L2max;
 
-    zero_padding(pbase, L1, L2, L1max, L2max, NW * 64);
+    {   // each part zeroes its share of the rows' padding
+        const int rows = (L1max + G - 1) / G;
+        zero_padding(pbase, L1, L2, L1max, L2max, NW * 64, part * rows,
+                     min(L1max, part * rows + rows));
+    }
 
     float g_acc = 0.0f;
     float A[P + 2];
+    const int s_begin = part * SPW;
+    const int NL = max(min(NS, s_begin + SPW) - s_begin, 0);   // stripes of this part
+    const bool has_next = s_begin + NL < NS;
+    const uint64_t* flag_in = bflag + (size_t)b * G + (part + 1 < G ? part + 1 : part);
+    uint64_t* flag_out = bflag + (size_t)b * G + part;
 
-    // Stripes run bottom-up: order q = 0..NS-1 handles stripe NS-1-q, on wave q % NW.
-    for (int q = wave; q < NS; q += NW) {
-        const int s = NS - 1 - q;
+    // Stripes run bottom-up: order q = 0..NL-1 handles stripe s_begin+NL-1-q, on wave
+    // q % NW.
+    for (int q = wave; q < NL; q += NW) {
+        const int s = s_begin + NL - 1 - q;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
         const float ej = band_centre(i0 + lane + 1, L1, L2);
@@ -214,7 +292,15 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
         const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
         const float2* ring_in = ring_from(rings, q, R);   // from stripe s+1
         float2* ring_out = ring_of(rings, q, R);          // to stripe s-1
-        const bool below = q > 0;
+        const bool x_in = q == 0 && has_next;             // flows from the part below
+        const bool x_out = q == NL - 1 && part > 0;       // flows to the part above
+        const bool below = q > 0 || x_in;
+        // boundary flows by producer step: written by stripe s (x_out), read from s + 1
+        float2* flows_out = flows + ((size_t)b * NSmax + s) * NT;
+        const float* flows_in =
+            reinterpret_cast<const float*>(flows + ((size_t)b * NSmax + (x_in ? s + 1 : s)) * NT);
+        int seen = -1;       // chunks of the part below known to be complete
+        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
 
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
@@ -224,19 +310,35 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
             uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
             uint32_t rl = buf + RBUF * 4;
             lds_dma_dword<0>(bup, roff, rl, 0u);
+            if (x_in) {
+                // flows of producer slots kP+62 .. kP+62+P (float2 each): float f of the
+                // range in lane f, clamped to the last slot
+                uint32_t foff = (uint32_t)min((k * P + 62) * 2 + min(lane, 2 * P + 1),
+                                              (nsteps - 1) * 2 + 1) * 4u;
+                uint32_t fdst = buf + FBUF * 4;
+                lds_dma_dword_sys<0>(flows_in, foff, fdst, 0u);
+            }
         };
 
         A[P] = lane_load(astripe + (size_t)(nsteps - 1 + APAD) * 64, ul4);
         A[P + 1] = lane_load(astripe + (size_t)(nsteps - 2 + APAD) * 64, ul4);
         __asm__ volatile("" ::"v"(A[P]), "v"(A[P + 1]));   // completes the two loads here
         wave_lds_sync();   // the previous stripe's buffer reads are complete
+        if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
         issue_chunk(0);
         float in_left = 0.0f, in_up = 0.0f, in_diag = 0.0f, in_diag_next = 0.0f;
 
         for (int k = 0; k < nch; ++k) {
             const int t_hi = nsteps - 1 - k * P;
-            chunk_waits<P>(prog, q, NS, k, nch, R, st);
+            chunk_waits<P>(prog, q, NL, k, nch, R, st);
+            // this chunk's loads were issued one chunk ago and followed by at least the
+            // P marginal stores of that chunk (the first chunk's are the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (x_in && k > 0) {
+                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
+                const int got = flag_chunks(fl, epoch);
+                seen = got > seen ? got : seen;
+            }
             float* buf = bufs + (k & 1) * BUF;
             float* tile = buf;
             float cv[P];
@@ -252,10 +354,22 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
             float pre_u = 0.0f, pre_d = 0.0f;
             if (below && lane >= 64 - P) {
                 const int j = 63 - lane;
-                pre_u = ring_in[ring_index(k * P + j + 63, R)].x;
-                pre_d = ring_in[ring_index(k * P + j + 62, R)].y;
+                if (x_in) {
+                    pre_u = buf[FBUF + 2 * (j + 1)];
+                    pre_d = buf[FBUF + 2 * j + 1];
+                } else {
+                    pre_u = ring_in[ring_index(k * P + j + 63, R)].x;
+                    pre_d = ring_in[ring_index(k * P + j + 62, R)].y;
+                }
             }
-            if (k + 1 < nch) issue_chunk(k + 1);
+            if (k + 1 < nch) {
+                if (x_in) {
+                    const int need = min(k + 1 + lead(P), nch);
+                    if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                }
+                issue_chunk(k + 1);
+                if (x_in) fl = load_flag_async(flag_in);
+            }
             float2* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
             {
                 const float u0 = lane_bcast(pre_u, 63), d0 = lane_bcast(pre_d, 63);
@@ -308,6 +422,20 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
             wave_lds_sync();
             write_tile<P, -1>(tile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             publish(prog, wave, q * PROG_STRIDE + k + 1);
+            if (x_out) {
+                // this chunk's flows to the part above, by producer step
+                if (lane < P) store_sys2(flows_out + k * P + lane, ring_out[ring_index(k * P, R) + lane]);
+                if (k >= 2) {
+                    // at least P + P/4 + 1 loads, 2P marginal stores and 2 flow stores
+                    // follow the flow store of chunk k - 2: it is complete
+                    wait_vmcnt<3 * P + P / 4 + 3>();
+                    if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
+                }
+            }
+        }
+        if (x_out) {
+            wait_vmcnt<0>();
+            if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
         }
     }
 
@@ -317,8 +445,19 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
     if (threadIdx.x == 0) {
         float g = 0.0f;
         for (int w = 0; w < NW; ++w) g += red_g[w];
-        grad_T[b] = g / T;
+        if (G == 1) grad_T[b] = g / T;
+        else bpart[((size_t)b * G + part) * 4] = g;
     }
+}
+
+// grad_T[b] of a split element from the parts' sums.
+__global__ void dtw_grad_merge(const double* __restrict__ bpart, float* __restrict__ grad_T,
+                               int B, int G, float T) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    float g = 0.0f;
+    for (int i = 0; i < G; ++i) g += (float)bpart[((size_t)b * G + i) * 4];
+    grad_T[b] = g / T;
 }
 
 }  // namespace dtw
@@ -330,34 +469,38 @@ namespace dtw {
 namespace {
 constexpr size_t kLdsLimit = 160 * 1024 - 256;
 
-size_t lds_forward(int max_L1, int max_L2) {
-    const int R = ring_len(max_L1, max_L2, 256);
-    return (size_t)NW * 2 * 65 * PF * sizeof(float) + ((size_t)NW * R + NW * DUMMY) * sizeof(float);
+// LDS of one workgroup whose stripe boundaries use rings of R columns
+size_t lds_forward_r(int R) {
+    return (size_t)NW * (2 * 65 * PF + 2 * 64) * sizeof(float) +
+           ((size_t)NW * R + NW * DUMMY) * sizeof(float);
 }
-
-size_t lds_backward(int max_L1, int max_L2, int P) {
-    const int R = ring_len(max_L1, max_L2, 128);
-    return (size_t)NW * 2 * (65 * P + 64 * P + 64) * sizeof(float) +
+size_t lds_backward_r(int R, int P) {
+    return (size_t)NW * 2 * (65 * P + 64 * P + 64 + 64) * sizeof(float) +
            ((size_t)NW * R + NW * DUMMY) * sizeof(float2);
 }
+int ring_forward(int rows, int max_L2) { return ring_len(rows, max_L2, 256); }
+int ring_backward(int rows, int max_L2) { return ring_len(rows, max_L2, 128); }
 
 // 16-step backward chunks when they fit in LDS, else 8-step chunks
-int backward_chunk(int max_L1, int max_L2) {
-    return lds_backward(max_L1, max_L2, 16) <= kLdsLimit ? 16 : 8;
+int backward_chunk(int rows, int max_L2) {
+    return lds_backward_r(ring_backward(rows, max_L2), 16) <= kLdsLimit ? 16 : 8;
 }
 
 template <int P>
 int launch_backward_p(const float* costs, const int* lengths, int B, int max_L1, int max_L2,
                       float T, int bandwidth, const Layout& ws, float* marginals, float* grad_T,
-                      hipStream_t st) {
+                      hipStream_t st, const Split& sp, int R) {
     const int ns = (max_L1 + 63) / 64;
-    const int R = ring_len(max_L1, max_L2, 128);
-    const size_t lds = lds_backward(max_L1, max_L2, P);
+    const size_t lds = lds_backward_r(R, P);
     D2P_HIP(hipFuncSetAttribute((const void*)dtw_backward_kernel<P>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH("dtw_backward", dtw_backward_kernel<P>, dim3(B), dim3(NW * 64), lds, st, costs,
-               lengths, ws.alpha_sk, ws.brow, marginals, grad_T, ws.status, ws.trash, max_L1,
-               max_L2, ns, T, bandwidth, R);
+    D2P_LAUNCH("dtw_backward", dtw_backward_kernel<P>, dim3(split_grid(B, sp.G)), dim3(NW * 64),
+               lds, st, costs, lengths, ws.alpha_sk, ws.brow, marginals, grad_T, ws.status,
+               ws.trash, ws.bflag, ws.flows, ws.bpart, B, max_L1, max_L2, ns, T, bandwidth, R,
+               sp.G, sp.SPW, next_epoch());
+    if (sp.G > 1)
+        D2P_LAUNCH("dtw_grad_merge", dtw_grad_merge, dim3((B + 255) / 256), dim3(256), 0, st,
+                   ws.bpart, grad_T, B, sp.G, T);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -368,8 +511,10 @@ int check_shape(int B, int max_L1, int max_L2, float temperature) {
     D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
     D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 4, "max_L2 too large");
     D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
-    D2P_REQUIRE(lds_forward(max_L1, max_L2) <= kLdsLimit &&
-                    lds_backward(max_L1, max_L2, backward_chunk(max_L1, max_L2)) <= kLdsLimit,
+    // an unsplit element is the longest pipeline a launch may run
+    D2P_REQUIRE(lds_forward_r(ring_forward(max_L1, max_L2)) <= kLdsLimit &&
+                    lds_backward_r(ring_backward(max_L1, max_L2),
+                                   backward_chunk(max_L1, max_L2)) <= kLdsLimit,
                 "sequence too long for the LDS stripe rings");
     return D2P_OK;
 }
@@ -377,12 +522,15 @@ int check_shape(int B, int max_L1, int max_L2, float temperature) {
 int launch_forward(const float* costs, const int* lengths, int B, int max_L1, int max_L2,
                    float T, int bandwidth, const Layout& ws, float* value, hipStream_t st) {
     const int ns = (max_L1 + 63) / 64;
-    const int R = ring_len(max_L1, max_L2, 256);
-    const size_t lds = lds_forward(max_L1, max_L2);
+    const Split sp = choose_split(B, max_L1, ws);
+    const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
+    const size_t lds = lds_forward_r(R);
+    if (sp.G > 1 && launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
     D2P_HIP(hipFuncSetAttribute((const void*)dtw_forward_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH("dtw_forward", dtw_forward_kernel, dim3(B), dim3(NW * 64), lds, st, costs, lengths,
-               ws.alpha_sk, ws.brow, value, ws.status, max_L1, max_L2, ns, T, bandwidth, R);
+    D2P_LAUNCH("dtw_forward", dtw_forward_kernel, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds,
+               st, costs, lengths, ws.alpha_sk, ws.brow, value, ws.status, ws.fflag, B, max_L1,
+               max_L2, ns, T, bandwidth, R, sp.G, sp.SPW, next_epoch());
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -390,11 +538,14 @@ int launch_forward(const float* costs, const int* lengths, int B, int max_L1, in
 int launch_backward(const float* costs, const int* lengths, int B, int max_L1, int max_L2,
                     float T, int bandwidth, const Layout& ws, float* marginals, float* grad_T,
                     hipStream_t st) {
-    if (backward_chunk(max_L1, max_L2) == 16)
+    const Split sp = choose_split(B, max_L1, ws);
+    const int rows = sp.G > 1 ? sp.SPW * 64 : max_L1;
+    const int R = ring_backward(rows, max_L2);
+    if (backward_chunk(rows, max_L2) == 16)
         return launch_backward_p<16>(costs, lengths, B, max_L1, max_L2, T, bandwidth, ws,
-                                     marginals, grad_T, st);
+                                     marginals, grad_T, st, sp, R);
     return launch_backward_p<8>(costs, lengths, B, max_L1, max_L2, T, bandwidth, ws, marginals,
-                                grad_T, st);
+                                grad_T, st, sp, R);
 }
 
 }  // namespace dtw
@@ -404,8 +555,9 @@ using namespace d2p_amd;
 
 extern "C" size_t d2p_dtw_workspace_bytes(int B, int max_L1, int max_L2) {
     if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
-    // status words | trash line | skewed alpha table | last row of every stripe
-    return wf::layout(nullptr, B, max_L1, max_L2).bytes;
+    // status words | trash line | skewed alpha table | last row of every stripe |
+    // split-element progress words, boundary flows and partial sums
+    return wf::layout(nullptr, B, max_L1, max_L2, 1, true).bytes;
 }
 
 extern "C" int d2p_dtw_forward_marginals(const float* costs, const int* lengths, int B,
@@ -420,7 +572,7 @@ extern "C" int d2p_dtw_forward_marginals(const float* costs, const int* lengths,
     const size_t need = d2p_dtw_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
-    const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2);
+    const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 1, true);
     const int r = dtw::launch_forward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth,
                                       ws, value, st);
     if (r != D2P_OK) return r;

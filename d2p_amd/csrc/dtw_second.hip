@@ -409,7 +409,7 @@ struct Second {
 
 Second second_layout(void* ws, int B, int L1, int L2) {
     Second w;
-    w.prim = layout(ws, B, L1, L2);
+    w.prim = layout(ws, B, L1, L2, 1, true);
     char* p = (char*)ws + round256(w.prim.bytes);
     const size_t ns = ((size_t)L1 + 63) / 64;
     w.tan_sk = (float*)p;

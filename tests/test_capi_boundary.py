@@ -73,7 +73,7 @@ def test_workspace_sizes(lib, fn, planes):
     # floats per plane, plus one last row per stripe and plane
     steps = 18 + (120 + 63 + 15) // 16 * 16
     table = 2 * 2 * planes * steps * (64 + 1) * 4
-    if fn == "d2p_sw_workspace_bytes":
+    if fn in ("d2p_sw_workspace_bytes", "d2p_dtw_workspace_bytes"):
         # split elements: boundary flows, one (up, diagonal) pair per stripe and step
         table += 2 * 2 * steps * 2 * 4
     elif fn == "d2p_swa_workspace_bytes":

@@ -1,6 +1,7 @@
-"""Split elements of the linear-gap sweeps: an element's stripes divided among
-several workgroups ("parts") that hand the boundary row (forward) and the boundary
-flows (reverse sweep) to each other through global memory.
+"""Split elements: an element's stripes divided among several workgroups ("parts")
+that hand the boundary row (forward) and the boundary flows (reverse sweep) to each
+other through global memory -- linear-gap and affine-gap Smith-Waterman and
+soft-DTW.
 
 D2P_AMD_SPLIT=<n> forces n parts per element (1: never split); unset, the library
 splits only long elements of small batches.  Every case is checked against the CPU
@@ -185,3 +186,43 @@ def test_affine_split_hvp(cuda, parts):
     ref = O.get("oracle").soft_sw_affine_hvp(s.numpy(), v.numpy(), -2.0, -0.5, 1.0)
     _close_affine(_capi.swa_hvp(s.to(cuda), v.to(cuda), None, -2.0, -0.5, 1.0), ref,
                   "affine hvp, split primal sweeps")
+
+
+# ---------------------------------------------------------------- soft-DTW
+
+DTW_CASES = [
+    # (seed, B, L1, L2, T, bandwidth, parts)
+    (50, 2, 600, 90, 1.0, -1, 1),      # unsplit, more stripes than waves
+    (51, 1, 300, 200, 0.5, -1, 2),     # parts of 3 and 2 stripes
+    (52, 3, 500, 130, 1.0, -1, 8),     # one stripe per part
+    (53, 2, 1300, 150, 1.0, -1, 2),    # several stripes per wave in each part
+    (54, 2, 700, 650, 1.0, 40, 3),     # Sakoe-Chiba band across parts
+    (55, 1, 1100, 2500, 1.0, -1, 2),   # long rows: 8-step backward chunks
+    (56, 2, 1024, 1024, 0.5, -1, 0),   # automatic choice (4 parts of 4 stripes)
+]
+
+
+@pytest.mark.parametrize("seed,B,L1,L2,T,bw,n", DTW_CASES)
+def test_dtw_split_matches_oracle(cuda, parts, seed, B, L1, L2, T, bw, n):
+    from test_gpu_dtw import _check as _check_dtw
+    parts(n)
+    c = _seeded(seed, (B, L1, L2)).abs()
+    ref = O.get("oracle").soft_dtw(c.numpy(), T, None, bw)
+    gpu = _capi.dtw_forward_marginals(c.to(cuda), None, T, bw)
+    torch.cuda.synchronize()
+    _check_dtw(gpu, ref, c.numpy(), T, bw)
+
+
+def test_dtw_split_ragged(cuda, parts):
+    """Ragged lengths under 4 parts: the terminal cell in any part, empty elements."""
+    from test_gpu_dtw import _check as _check_dtw
+    parts(4)
+    B, L1, L2 = 6, 700, 170
+    c = _seeded(57, (B, L1, L2)).abs()
+    lens = torch.tensor([[700, 170], [0, 50], [640, 0], [0, 0], [193, 123], [1, 170]],
+                        dtype=torch.int32)
+    for bw in (-1, 30):
+        ref = O.get("oracle").soft_dtw(c.numpy(), 0.7, lens.numpy(), bw)
+        gpu = _capi.dtw_forward_marginals(c.to(cuda), lens.to(cuda), 0.7, bw)
+        torch.cuda.synchronize()
+        _check_dtw(gpu, ref, c.numpy(), 0.7, bw, lens.tolist())
