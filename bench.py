@@ -21,10 +21,13 @@ Prints one JSON line with:
     rocprofv3 --pmc (FETCH_SIZE x2 calibration + WRITE_SIZE), read from
     profiles/<kernel>_<config>_pmc.md when that summary exists;
   * ``step_roofline``: the whole step at its algorithmic bytes;
+  * ``valu``: VALUBusy of the dominant kernel measured with rocprofv3 SQ counters,
+    read from profiles/sw_<config>_valu.md when that summary exists (the sweeps
+    are bound by their per-step dependency chain, not by HBM);
   * ``cpu_baseline``: the reference's own CPU kernels (oracle/_ref, built from
     the reference sources; else the C restatement) run in the reference's autograd
-    call sequence on the host cores: the full batch for C2, a bounded sample of
-    the batch for the other configurations.
+    call sequence on up to 16 host cores, on the configuration's full batch: the
+    median of as many runs as fill about 10 s.
 Only one GPU is supported: ``--gpus`` above 1 exits with a message.
 """
 from __future__ import annotations
@@ -42,6 +45,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+CPU_TARGET_S = 10.0   # CPU baseline: repeat the step for about this long
 METRIC = "DP cells/sec fwd+bwd, soft_sw B=256 512x512 fp32; achieved HBM GB/s %"
 
 
@@ -178,6 +182,31 @@ def measured_traffic(kernel, config):
     return float(m.group(1)) if m else None
 
 
+def measured_valu(kernel, config):
+    """VALUBusy (%) of a kernel from a committed rocprofv3 SQ-counter summary, if
+    present: the table row ``| VALUBusy (%) | ... |`` under a header naming each
+    kernel in backticks."""
+    path = os.path.join(ROOT, "profiles", f"sw_{config}_valu.md")
+    if not os.path.exists(path):
+        return None
+    head, busy = None, None
+    for line in open(path):
+        if not line.startswith("|"):
+            continue
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if head is None and any(c.startswith("`") for c in cells):
+            head = cells
+        elif cells and cells[0] == "VALUBusy (%)":
+            busy = cells
+    if head is None or busy is None:
+        return None
+    for name, val in zip(head, busy):
+        if name.strip("`").startswith(kernel):
+            return {"kernel": kernel, "valu_busy_pct": float(val),
+                    "source": os.path.relpath(path, ROOT)}
+    return None
+
+
 def cpu_baseline_config(cfg, max_elems):
     """The reference CPU call sequence of a configuration on a bounded sample of its
     batch (the first max_elems elements; parallel over the batch as the reference)."""
@@ -185,7 +214,7 @@ def cpu_baseline_config(cfg, max_elems):
     from oracle import oracle as O
     kind = "reference" if O.reference_available() else "port"
     k = O.get("oracle" if kind == "port" else "reference")
-    n = max_elems
+    n = min(max_elems, len(next(iter(cfg["inputs"].values()))))
     cores = max(1, min(16, os.cpu_count() or 1, n))
     O.set_threads(cores)
     name = cfg["name"]
@@ -223,14 +252,25 @@ def cpu_baseline_config(cfg, max_elems):
             a, p = k.sw_forward(x["scores"], None, -1.0, 1.0)
             return k.sw_hvp(a, x["scores"], p, x["V"], None, -1.0, 1.0)[0]
         what = "fwd + HVP sweeps"
-    t0 = time.perf_counter()
-    step()
-    t = time.perf_counter() - t0
+    t, runs = _timed_runs(step)
     return {"value": cells / t, "unit": "cells/s", "cores": cores, "kind": kind,
-            "sample": f"first {n} batch elements, {what}, one timed run ({t:.2f} s)"}
+            "sample": f"first {n} of {len(next(iter(cfg['inputs'].values())))} batch elements, "
+                      f"{what}, median of {runs} runs after 1 warm-up ({t:.3f} s each)"}
 
 
-def cpu_baseline(scores_np, runs=3):
+def _timed_runs(step, target_s=CPU_TARGET_S, max_runs=200):
+    """Median time of a CPU step: one warm-up run, then timed runs until they add
+    up to target_s seconds (at least 3, at most max_runs)."""
+    step()
+    times = []
+    while len(times) < 3 or (sum(times) < target_s and len(times) < max_runs):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(scores_np):
     """The reference CPU path timed on the host: per step, SoftSWRegularCPUFunction
     runs forward + backward DP in its forward and the backward DP again in its
     backward, then scales the posteriors (src/sw/torch_cpu.cpp:114-259)."""
@@ -248,13 +288,7 @@ def cpu_baseline(scores_np, runs=3):
         post, _, _ = k.sw_backward(alpha, scores_np, part, None, -1.0, 1.0)
         return ones * post
 
-    step()  # warm-up
-    times = []
-    for _ in range(runs):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
+    t, runs = _timed_runs(step)
     cells = scores_np.shape[0] * scores_np.shape[1] * scores_np.shape[2]
     return {"value": cells / t, "unit": "cells/s", "cores": cores, "kind": kind,
             "sample": f"full C2 batch {list(scores_np.shape)} fwd + 2x bwd DP + scale, "
@@ -325,7 +359,8 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded draws generated on the CPU)",
         "config": dict({"workload": cfg["workload"],
-                        "parallelism": "single GPU, one workgroup per batch element"},
+                        "parallelism": "single GPU; one workgroup per batch element, long "
+                                       "elements of small batches split over several"},
                        **cfg["extra"]),
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
@@ -333,13 +368,14 @@ def main():
                      "avg_launch_ms": d["avg_ms"]},
         "step_roofline": {"algo_bytes_per_step": cfg["algo_step"], "achieved": step_gbs,
                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": step_gbs / HBM_PEAK_GBS},
+        "valu": measured_valu(dominant, cfg["name"]),
         "kernels_ms": {k: round(v["avg_ms"], 5) for k, v in kstats.items()},
     }
     if not args.no_cpu_baseline:
         if cfg["name"] == "c2":
             out["cpu_baseline"] = cpu_baseline(cfg["inputs"]["scores"].numpy())
         else:
-            sample = {"c3": 16, "c4": 64, "c5": 1, "c5hvp": 1}[cfg["name"]]
+            sample = {"c3": 64, "c4": 512, "c5": 16, "c5hvp": 16}[cfg["name"]]
             out["cpu_baseline"] = cpu_baseline_config(cfg, sample)
     print(json.dumps(out), flush=True)
 
