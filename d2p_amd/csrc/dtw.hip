@@ -486,12 +486,22 @@ int backward_chunk(int rows, int max_L2) {
     return lds_backward_r(ring_backward(rows, max_L2), 16) <= kLdsLimit ? 16 : 8;
 }
 
+// Stripes per part that a launch may not exceed: 0 when the rings of an unsplit
+// element fit in LDS, else NW (the minimum rings of such parts always fit).
+int max_stripes_forward(int max_L1, int max_L2) {
+    return lds_forward_r(ring_forward(max_L1, max_L2)) <= kLdsLimit ? 0 : NW;
+}
+int max_stripes_backward(int max_L1, int max_L2) {
+    return lds_backward_r(ring_backward(max_L1, max_L2), 8) <= kLdsLimit ? 0 : NW;
+}
+
 template <int P>
 int launch_backward_p(const float* costs, const int* lengths, int B, int max_L1, int max_L2,
                       float T, int bandwidth, const Layout& ws, float* marginals, float* grad_T,
                       hipStream_t st, const Split& sp, int R) {
     const int ns = (max_L1 + 63) / 64;
     const size_t lds = lds_backward_r(R, P);
+    D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     D2P_HIP(hipFuncSetAttribute((const void*)dtw_backward_kernel<P>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     D2P_LAUNCH("dtw_backward", dtw_backward_kernel<P>, dim3(split_grid(B, sp.G)), dim3(NW * 64),
@@ -511,20 +521,18 @@ int check_shape(int B, int max_L1, int max_L2, float temperature) {
     D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
     D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 4, "max_L2 too large");
     D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
-    // an unsplit element is the longest pipeline a launch may run
-    D2P_REQUIRE(lds_forward_r(ring_forward(max_L1, max_L2)) <= kLdsLimit &&
-                    lds_backward_r(ring_backward(max_L1, max_L2),
-                                   backward_chunk(max_L1, max_L2)) <= kLdsLimit,
-                "sequence too long for the LDS stripe rings");
+    // rings that do not fit for an unsplit element force parts of at most NW
+    // stripes, whose minimum rings fit whatever the row length
     return D2P_OK;
 }
 
 int launch_forward(const float* costs, const int* lengths, int B, int max_L1, int max_L2,
                    float T, int bandwidth, const Layout& ws, float* value, hipStream_t st) {
     const int ns = (max_L1 + 63) / 64;
-    const Split sp = choose_split(B, max_L1, ws);
+    const Split sp = choose_split(B, max_L1, ws, max_stripes_forward(max_L1, max_L2));
     const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
     const size_t lds = lds_forward_r(R);
+    D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     if (sp.G > 1 && launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
     D2P_HIP(hipFuncSetAttribute((const void*)dtw_forward_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
@@ -538,7 +546,7 @@ int launch_forward(const float* costs, const int* lengths, int B, int max_L1, in
 int launch_backward(const float* costs, const int* lengths, int B, int max_L1, int max_L2,
                     float T, int bandwidth, const Layout& ws, float* marginals, float* grad_T,
                     hipStream_t st) {
-    const Split sp = choose_split(B, max_L1, ws);
+    const Split sp = choose_split(B, max_L1, ws, max_stripes_backward(max_L1, max_L2));
     const int rows = sp.G > 1 ? sp.SPW * 64 : max_L1;
     const int R = ring_backward(rows, max_L2);
     if (backward_chunk(rows, max_L2) == 16)

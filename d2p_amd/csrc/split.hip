@@ -40,23 +40,28 @@ __global__ void partition_merge_kernel(const float2* __restrict__ fpart,
 
 }  // namespace
 
-Split choose_split(int B, int max_L1, const Layout& ws) {
+Split choose_split(int B, int max_L1, const Layout& ws, int max_spw) {
     const int ns = (max_L1 + 63) / 64;
     Split sp{1, ns > 0 ? ns : 1};
     if (ws.fflag == nullptr || ns <= 1) return sp;
     int G = 0;
     if (const char* e = getenv("D2P_AMD_SPLIT")) G = atoi(e);
-    if (G <= 0) {
+    if (G <= 0 && ns > 4) {
         // Parts of 4 stripes (one wave per SIMD: the pipeline's per-step latency is
         // lowest when a wave has its SIMD to itself) if the whole grid is resident at
         // once; else parts of 8 (one stripe per wave), or as few parts as fit.
-        if (ns <= 4) return sp;
         const int cus = device_cus();
         G = (ns + 3) / 4;
         if (split_grid(B, G) > cus) {
             G = (ns + NW - 1) / NW;
             while (G > 1 && split_grid(B, G) > cus) --G;
         }
+    }
+    // an unsplit element whose rings do not fit in LDS: parts of at most max_spw
+    // stripes, whatever the device or the environment asks for
+    if (max_spw > 0 && ns > max_spw) {
+        const int g_min = (ns + max_spw - 1) / max_spw;
+        G = G > g_min ? G : g_min;
     }
     G = G < ns ? G : ns;
     if (G <= 1) return sp;

@@ -666,6 +666,15 @@ size_t lds_backward_r(int R) {
 }
 int ring_forward(int rows, int max_L2) { return ring_len(rows, max_L2, 256); }
 int ring_backward(int rows, int max_L2) { return ring_len(rows, max_L2, 128); }
+
+// Stripes per part that a launch may not exceed: 0 when the rings of an unsplit
+// element fit in LDS, else NW (the minimum rings of such parts always fit).
+int max_stripes_forward(int max_L1, int max_L2) {
+    return lds_forward_r(ring_forward(max_L1, max_L2)) <= kLdsLimit ? 0 : NW;
+}
+int max_stripes_backward(int max_L1, int max_L2) {
+    return lds_backward_r(ring_backward(max_L1, max_L2)) <= kLdsLimit ? 0 : NW;
+}
 }  // namespace
 
 int check_shape(int B, int max_L1, int max_L2, float temperature) {
@@ -673,10 +682,8 @@ int check_shape(int B, int max_L1, int max_L2, float temperature) {
     D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
     D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 4, "max_L2 too large");
     D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
-    // an unsplit element is the longest pipeline a launch may run
-    D2P_REQUIRE(lds_forward_r(ring_forward(max_L1, max_L2)) <= kLdsLimit &&
-                    lds_backward_r(ring_backward(max_L1, max_L2)) <= kLdsLimit,
-                "sequence too long for the LDS stripe rings");
+    // rings that do not fit for an unsplit element force parts of at most NW
+    // stripes, whose minimum rings fit whatever the row length
     return D2P_OK;
 }
 
@@ -692,9 +699,10 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
                    float go, float ge, float T, const Layout& ws, float* partition,
                    hipStream_t st) {
     const int ns = (max_L1 + 63) / 64;
-    const Split sp = choose_split(B, max_L1, ws);
+    const Split sp = choose_split(B, max_L1, ws, max_stripes_forward(max_L1, max_L2));
     const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
     const size_t lds = lds_forward_r(R);
+    D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     if (sp.G > 1 && launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
     D2P_HIP(hipFuncSetAttribute((const void*)swa_forward_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
@@ -712,9 +720,10 @@ int launch_backward(const float* scores, const int* lengths, int B, int max_L1, 
                     float* marginals, float* grad_open, float* grad_ext, float* grad_T,
                     hipStream_t st) {
     const int ns = (max_L1 + 63) / 64;
-    const Split sp = choose_split(B, max_L1, ws);
+    const Split sp = choose_split(B, max_L1, ws, max_stripes_backward(max_L1, max_L2));
     const int R = ring_backward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
     const size_t lds = lds_backward_r(R);
+    D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     float4* flows4 = reinterpret_cast<float4*>(ws.flows);
     float* flows1 = sp.G > 1 ? reinterpret_cast<float*>(flows4 + ws.flow_slots) : nullptr;
     D2P_HIP(hipFuncSetAttribute((const void*)swa_backward_kernel,

@@ -541,6 +541,16 @@ int ring_backward(int rows, int max_L2) { return wf::ring_len(rows, max_L2, 128)
 int backward_chunk(int rows, int max_L2) {
     return lds_backward_r(ring_backward(rows, max_L2), 16) <= kLdsLimit ? 16 : 8;
 }
+
+// Stripes per part that a launch may not exceed: 0 when the rings of an unsplit
+// element fit in LDS, else NW (a part of at most NW stripes needs only the minimum
+// ring, which always fits).
+int max_stripes_forward(int max_L1, int max_L2) {
+    return lds_forward_r(ring_forward(max_L1, max_L2)) <= kLdsLimit ? 0 : wf::NW;
+}
+int max_stripes_backward(int max_L1, int max_L2) {
+    return lds_backward_r(ring_backward(max_L1, max_L2), 8) <= kLdsLimit ? 0 : wf::NW;
+}
 }  // namespace
 
 int check_shape(int B, int max_L1, int max_L2, float temperature) {
@@ -549,20 +559,18 @@ int check_shape(int B, int max_L1, int max_L2, float temperature) {
     D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 4, "max_L2 too large");
     // per-lane byte offsets within one batch element are 32-bit
     D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
-    // an unsplit element is the longest pipeline a launch may run
-    const int Rb = ring_backward(max_L1, max_L2);
-    D2P_REQUIRE(lds_forward_r(ring_forward(max_L1, max_L2)) <= kLdsLimit &&
-                    lds_backward_r(Rb, backward_chunk(max_L1, max_L2)) <= kLdsLimit,
-                "sequence too long for the LDS stripe rings");
+    // rings that do not fit for an unsplit element force parts of at most NW
+    // stripes, whose minimum rings fit whatever the row length
     return D2P_OK;
 }
 
 int launch_forward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                    float gap, float T, const Layout& ws, float* partition, hipStream_t st) {
     const int ns = (max_L1 + 63) / 64;
-    const Split sp = choose_split(B, max_L1, ws);
+    const Split sp = choose_split(B, max_L1, ws, max_stripes_forward(max_L1, max_L2));
     const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
     const size_t lds = lds_forward_r(R);
+    D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     const uint32_t epoch = next_epoch();
     if (sp.G > 1 && wf::launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
     D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel,
@@ -584,6 +592,7 @@ int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1
                       const Split& sp, int R) {
     const int ns = (max_L1 + 63) / 64;
     const size_t lds = lds_backward_r(R, P);
+    D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     const uint32_t epoch = next_epoch();
     D2P_HIP(hipFuncSetAttribute((const void*)sw_backward_kernel<P, PRECISE>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
@@ -602,7 +611,7 @@ int launch_backward(const float* scores, const int* lengths, int B, int max_L1, 
                     float gap, float T, const Layout& ws, const float* partition,
                     float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
                     bool precise) {
-    const Split sp = choose_split(B, max_L1, ws);
+    const Split sp = choose_split(B, max_L1, ws, max_stripes_backward(max_L1, max_L2));
     const int rows = sp.G > 1 ? sp.SPW * 64 : max_L1;
     const int R = ring_backward(rows, max_L2);
     const int P = backward_chunk(rows, max_L2);

@@ -661,7 +661,9 @@ template <int MODE>
 int launch_tangent(const float* scores, const float* V, const int* lengths, int B, int L1, int L2,
                    float gap, float T, const Second& w, float* sdot, hipStream_t st) {
     const int ns = (L1 + 63) / 64;
-    const sw::Split sp = sw::choose_split(B, L1, w.prim);
+    // rings of an unsplit element that do not fit: parts of at most NW stripes
+    const sw::Split sp =
+        sw::choose_split(B, L1, w.prim, lds_tangent(MODE, L1, L2) <= kLdsLimit ? 0 : NW);
     const int R = ring_len(sp.G > 1 ? sp.SPW * 64 : L1, L2, 256);
     const size_t lds = lds_tangent_r(MODE, R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
@@ -684,10 +686,11 @@ int launch_dual(const float* scores, const float* V, const int* lengths, int B, 
                 float gap, float T, const Second& w, const float* dS, float* out, float* dot,
                 hipStream_t st) {
     const int ns = (L1 + 63) / 64;
-    const sw::Split sp = sw::choose_split(B, L1, w.prim);
+    constexpr bool has_v = MODE == HVP || DOT;
+    const sw::Split sp =
+        sw::choose_split(B, L1, w.prim, dual_chunk(has_v, DOT, L1, L2) > 0 ? 0 : NW);
     const int rows = sp.G > 1 ? sp.SPW * 64 : L1;
     const int R = ring_len(rows, L2, 128);
-    constexpr bool has_v = MODE == HVP || DOT;
     const int P = dual_chunk(has_v, DOT, rows, L2);
     D2P_REQUIRE(P > 0, "sequence too long for the LDS stripe rings");
     const size_t lds = lds_dual_r(has_v, DOT, P, R);
@@ -708,11 +711,8 @@ int launch_dual(const float* scores, const float* V, const int* lengths, int B, 
 }
 
 int check(int B, int L1, int L2, float T) {
-    const int rc = sw::check_shape(B, L1, L2, T);
-    if (rc != D2P_OK) return rc;
-    D2P_REQUIRE(lds_tangent(HVP, L1, L2) <= kLdsLimit && dual_chunk(true, false, L1, L2) > 0,
-                "sequence too long for the LDS stripe rings");
-    return D2P_OK;
+    // rings that do not fit for an unsplit element force parts of at most NW stripes
+    return sw::check_shape(B, L1, L2, T);
 }
 
 }  // namespace sw2

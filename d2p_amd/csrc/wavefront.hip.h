@@ -128,11 +128,13 @@ __host__ inline Layout layout(void* workspace, int B, int max_L1, int max_L2, in
 
 // Parts per element (G) and stripes per part (SPW) of a launch: G > 1 only when the
 // layout has the split areas.  D2P_AMD_SPLIT=<n> in the environment forces n parts
-// (at most one per stripe); unset or 0 chooses automatically.
+// (at most one per stripe); unset or 0 chooses automatically.  max_spw > 0: the
+// rings of an unsplit element do not fit in LDS, so no part may hold more than
+// max_spw stripes (a part of at most NW stripes needs only the minimum ring).
 struct Split {
     int G, SPW;
 };
-Split choose_split(int B, int max_L1, const Layout& ws);
+Split choose_split(int B, int max_L1, const Layout& ws, int max_spw = 0);
 
 // Before a split forward sweep: status words and progress words to zero.
 int launch_split_reset(const Layout& ws, int B, int G, hipStream_t st);

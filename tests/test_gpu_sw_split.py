@@ -226,3 +226,46 @@ def test_dtw_split_ragged(cuda, parts):
         gpu = _capi.dtw_forward_marginals(c.to(cuda), lens.to(cuda), 0.7, bw)
         torch.cuda.synchronize()
         _check_dtw(gpu, ref, c.numpy(), 0.7, bw, lens.tolist())
+
+
+# ------------------------------------------------- rows too long for unsplit rings
+
+# An unsplit element with more stripes than waves needs stripe rings about a row
+# long; when they do not fit in LDS the launch splits the element into parts of at
+# most 8 stripes, whose minimum rings always fit -- also when D2P_AMD_SPLIT=1.
+@pytest.mark.parametrize("n", [0, 1])
+def test_sw_long_rows_force_parts(cuda, parts, n):
+    parts(n)
+    s = _seeded(60, (1, 600, 12000))
+    ref = O.get("oracle").soft_sw(s.numpy(), -1.0, 1.0)
+    out = _capi.sw_forward_marginals(s.to(cuda), None, -1.0, 1.0)
+    torch.cuda.synchronize()
+    _check(out, ref, scores=s.numpy())
+
+
+def test_sw_hvp_long_rows_force_parts(cuda, parts):
+    parts(1)
+    s = _seeded(61, (1, 600, 6000))
+    v = _seeded(62, (1, 600, 6000))
+    ref = O.get("oracle").soft_sw_hvp(s.numpy(), v.numpy(), -1.0, 1.0)
+    _close(_capi.sw_hvp(s.to(cuda), v.to(cuda), None, -1.0, 1.0), ref, "hvp, 600 x 6000")
+
+
+def test_affine_long_rows_force_parts(cuda, parts):
+    from test_gpu_sw_affine import _check as _check_affine
+    parts(1)
+    s = _seeded(63, (1, 600, 4000), 2.0)
+    ref = O.get("oracle").soft_sw_affine(s.numpy(), -11.0, -1.0, 0.5)
+    gpu = _capi.swa_forward_marginals(s.to(cuda), None, -11.0, -1.0, 0.5)
+    torch.cuda.synchronize()
+    _check_affine(gpu, ref, s.numpy(), -11.0, -1.0, 0.5)
+
+
+def test_dtw_long_rows_force_parts(cuda, parts):
+    from test_gpu_dtw import _check as _check_dtw
+    parts(1)
+    c = _seeded(64, (1, 600, 12000)).abs()
+    ref = O.get("oracle").soft_dtw(c.numpy(), 1.0, None, -1)
+    gpu = _capi.dtw_forward_marginals(c.to(cuda), None, 1.0, -1)
+    torch.cuda.synchronize()
+    _check_dtw(gpu, ref, c.numpy(), 1.0, -1)
