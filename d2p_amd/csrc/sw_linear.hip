@@ -425,10 +425,17 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const float vd = dga + sc;
                 const float vu = upa + gap;
                 const float vl = a1 + gap;
-                const float m = fmaxf(fmaxf(vd, vu), fmaxf(vl, sc));
-                const float e0 = fast_exp2((vd - m) * c), e1 = fast_exp2((vu - m) * c);
-                const float e2 = fast_exp2((vl - m) * c), e3 = fast_exp2((sc - m) * c);
-                const float rin = fast_rcp(((e0 + e1) + e2) + e3);
+                // The weights e_k / sum e: an error in the common shift m*c cancels, so
+                // each exponent is one fma, exact up to the rounding of m*c.  That
+                // rounding is ~2^75 at the 1e30 sentinels of cells outside the element,
+                // so m is floored far below any real alpha (those cells' e_k become 0
+                // and their flows are selected away, not multiplied).
+                const float m = fmaxf(fmaxf(vd, vu), fmaxf(fmaxf(vl, sc), -1e20f));
+                const float mc = m * c;
+                const float e0 = fast_exp2(fmaf(vd, c, -mc)), e1 = fast_exp2(fmaf(vu, c, -mc));
+                const float e2 = fast_exp2(fmaf(vl, c, -mc)), e3 = fast_exp2(fmaf(sc, c, -mc));
+                const float e03 = e0 + e3, e12 = e1 + e2;
+                const float rin = fast_rcp(e12 + e03);
                 float lp = (a0 - S) * c;   // subtract first: exact for nearby values
                 lp = lp < 0.0f ? lp : 0.0f;
                 const float binit = fast_exp2(lp);
@@ -437,9 +444,10 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const bool live = ok && (beta <= 3.0e38f);    // skips inf / NaN like the reference
                 const float br = live ? beta * rin : 0.0f;
                 const float od = br * e0, ou = br * e1, ol = br * e2;
-                const float pv = br * (e0 + e3);
+                const float pv = br * e03;
                 buf[obase_lane + u] = pv;
-                gs[u] = (Acc)ou + (Acc)ol;
+                if (PRECISE) gs[u] = (Acc)ou + (Acc)ol;
+                else gs[u] = br * e12;
                 ps[u] = (Acc)(pv * sc);
                 pub[u] = make_float2(ou, od);
                 // successor contributions for the next steps; lane 63 takes the ring
