@@ -63,9 +63,11 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = ChunkTile<P>;
-    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 64;        // two cost chunks, two rows
+    constexpr int WBUF = 2 * Tile::FLOATS + 3 * 64;        // two cost chunks, two rows, slot
     float* tiles = smem + wave * WBUF;                     // double-buffered cost chunk
     float* rbufs = tiles + 2 * Tile::FLOATS;               // boundary row of a chunk
+    float* fslot = rbufs + 2 * 64;                         // prefetched progress word
+    const uint32_t fslot_lds = lds_address(fslot);
     float* rings = smem + NW * WBUF;                       // [NW][R]
     float* sink = rings + NW * R + wave * DUMMY;           // per-wave write sink
     int* st = status + b;
@@ -109,7 +111,6 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
         const bool x_in = l == 0 && part > 0;        // row above from the previous part
         const bool x_out = l == NL - 1 && has_next;  // last row feeds the next part
         int seen = -1;       // chunks of the previous part known to be complete
-        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
         // steps t < 0 hold the column-0 boundary (PINF), read by the reverse sweep
 #pragma unroll
         for (int t = -APAD; t < 0; ++t) lane_store(out + t * 64, ul4, kPINF);
@@ -137,8 +138,8 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
             // stores of that chunk (the first chunk's load is the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
             if (x_in && k > 0) {
-                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
-                const int got = flag_chunks(fl, epoch);
+                // its progress word, loaded one chunk ago before those stores
+                const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
             const float* tile = tiles + (k & 1) * Tile::FLOATS;
@@ -157,7 +158,7 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                 }
                 dma_tile<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, cbase, i0, L1max,
                                L2max, lane, t0 + P);
-                if (x_in) fl = load_flag_async(flag_in);
+                if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             float* outc = out + (size_t)t0 * 64;
@@ -245,8 +246,10 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
     constexpr int FBUF = RBUF + 64;               // flows from the part below (2P+2 floats)
     constexpr int BUF = FBUF + 64;
     static_assert(2 * P + 2 <= 64, "boundary flows fit their buffer");
-    float* bufs = smem + wave * 2 * BUF;
-    float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * BUF);  // [NW][R] (up, diag)
+    float* bufs = smem + wave * (2 * BUF + 64);
+    float* fslot = bufs + 2 * BUF;                 // prefetched progress word
+    const uint32_t fslot_lds = lds_address(fslot);
+    float2* rings = reinterpret_cast<float2*>(smem + NW * (2 * BUF + 64));  // [NW][R] (up, diag)
     float2* sink = rings + NW * R + wave * DUMMY;
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
@@ -300,7 +303,6 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
         const float* flows_in =
             reinterpret_cast<const float*>(flows + ((size_t)b * NSmax + (x_in ? s + 1 : s)) * NT);
         int seen = -1;       // chunks of the part below known to be complete
-        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
 
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
@@ -335,8 +337,8 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
             // P marginal stores of that chunk (the first chunk's are the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
             if (x_in && k > 0) {
-                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
-                const int got = flag_chunks(fl, epoch);
+                // its progress word, loaded one chunk ago before those stores
+                const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
             float* buf = bufs + (k & 1) * BUF;
@@ -368,7 +370,7 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
                 }
                 issue_chunk(k + 1);
-                if (x_in) fl = load_flag_async(flag_in);
+                if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             float2* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
             {
@@ -471,11 +473,11 @@ constexpr size_t kLdsLimit = 160 * 1024 - 256;
 
 // LDS of one workgroup whose stripe boundaries use rings of R columns
 size_t lds_forward_r(int R) {
-    return (size_t)NW * (2 * 65 * PF + 2 * 64) * sizeof(float) +
+    return (size_t)NW * (2 * 65 * PF + 3 * 64) * sizeof(float) +
            ((size_t)NW * R + NW * DUMMY) * sizeof(float);
 }
 size_t lds_backward_r(int R, int P) {
-    return (size_t)NW * 2 * (65 * P + 64 * P + 64 + 64) * sizeof(float) +
+    return (size_t)NW * (2 * (65 * P + 64 * P + 64 + 64) + 64) * sizeof(float) +
            ((size_t)NW * R + NW * DUMMY) * sizeof(float2);
 }
 int ring_forward(int rows, int max_L2) { return ring_len(rows, max_L2, 256); }

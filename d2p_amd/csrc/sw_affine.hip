@@ -70,9 +70,11 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = ChunkTile<P>;
-    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 3 * 64;   // two score chunks, two row sets
+    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 3 * 64 + 64;   // + progress-word slot
     float* tiles = smem + wave * WBUF;                    // double-buffered score chunk
     float* rbufs = tiles + 2 * Tile::FLOATS;              // [2][plane][64] rows above
+    float* fslot = rbufs + 2 * 3 * 64;                    // prefetched progress word
+    const uint32_t fslot_lds = lds_address(fslot);
     float4* rings = reinterpret_cast<float4*>(smem + NW * WBUF);   // [NW][R]
     float4* sink = rings + NW * R + wave * DUMMY;
     int* st = status + b;
@@ -114,7 +116,6 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         const bool x_in = l == 0 && part > 0;        // rows above from the previous part
         const bool x_out = l == NL - 1 && has_next;  // last rows feed the next part
         int seen = -1;       // chunks of the previous part known to be complete
-        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
         // steps t < 0 hold the column-0 boundary (NINF), read by the reverse sweep
 #pragma unroll
         for (int t = -APAD; t < 0; ++t) {
@@ -150,8 +151,8 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             // 3P + 3 stores of that chunk (the first chunk's load is the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<3 * P>();
             if (x_in && k > 0) {
-                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
-                const int got = flag_chunks(fl, epoch);
+                // its progress word, loaded one chunk ago before those stores
+                const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
             const float* tile = tiles + (k & 1) * Tile::FLOATS;
@@ -181,7 +182,7 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 }
                 dma_tile<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0, L1max,
                                L2max, lane, t0 + P);
-                if (x_in) fl = load_flag_async(flag_in);
+                if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             float4* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             float* outc = out + (size_t)t0 * 64;
@@ -302,10 +303,13 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
     constexpr int OTILE = RROW + 3 * 64;
     constexpr int FB4 = OTILE + Tile::FLOATS;       // flows from the part below: float4s
     constexpr int FB1 = FB4 + 64;                   // ... and the diagonal D flows
-    constexpr int WFLOATS = FB1 + 64;
+    constexpr int FSLOT = FB1 + 64;                 // prefetched progress word
+    constexpr int WFLOATS = FSLOT + 64;
     static_assert(4 * P + 4 <= 64, "boundary flows fit their buffer");
     float* wbuf = smem + wave * WFLOATS;
     float* otile = wbuf + OTILE;
+    float* fslot = wbuf + FSLOT;
+    const uint32_t fslot_lds = lds_address(fslot);
     // rings [NW][R]: (up M, up I, diag M, diag I) and diag D, from lane 0 upward
     float4* ring4 = reinterpret_cast<float4*>(smem + NW * WFLOATS);
     float* ring1 = reinterpret_cast<float*>(ring4 + NW * R);
@@ -364,7 +368,6 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
         const float* f4_in = reinterpret_cast<const float*>(flows4 + fi);
         const float* f1_in = flows1 + fi;
         int seen = -1;       // chunks of the part below known to be complete
-        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
 
         // Loads of chunk k (t_hi = nsteps-1-kP): the score tile, P alpha rows per plane
         // (steps t_hi-2 .. t_hi-P-1) and the stripe above's last row per plane at steps
@@ -425,8 +428,8 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
             // previous chunk (the first chunk's loads are the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
             if (x_in && k > 0) {
-                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
-                const int got = flag_chunks(fl, epoch);
+                // its progress word, loaded one chunk ago before those stores
+                const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
             float sv[P];
@@ -478,7 +481,7 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
                 }
                 issue_chunk(k + 1);
-                if (x_in) fl = load_flag_async(flag_in);
+                if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             float4* pub4 = (lane == 0) ? r4_out + ring_index(k * P, R) : sink4 + lane;
             float* pub1 = (lane == 0) ? r1_out + ring_index(k * P, R) : sink1 + lane;
@@ -655,11 +658,11 @@ constexpr size_t kLdsLimit = 160 * 1024 - 256;
 
 // LDS of one workgroup whose stripe boundaries use rings of R columns
 size_t lds_forward_r(int R) {
-    return (size_t)NW * (2 * 65 * PF + 2 * 3 * 64) * sizeof(float) +
+    return (size_t)NW * (2 * 65 * PF + 2 * 3 * 64 + 64) * sizeof(float) +
            ((size_t)NW * R + NW * DUMMY) * sizeof(float4);
 }
 size_t lds_backward_r(int R) {
-    const size_t wfloats = 65 * PB + 3 * PB * 64 + 3 * 64 + 65 * PB + 2 * 64;
+    const size_t wfloats = 65 * PB + 3 * PB * 64 + 3 * 64 + 65 * PB + 3 * 64;
     return (size_t)NW * wfloats * sizeof(float) +
            (size_t)NW * R * (sizeof(float4) + sizeof(float)) +
            (size_t)NW * (64 + PB) * (sizeof(float4) + sizeof(float));

@@ -59,9 +59,11 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = QuadTile<P>;
-    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 64;        // two score chunks, two rows
+    constexpr int WBUF = 2 * Tile::FLOATS + 3 * 64;        // two score chunks, two rows, slot
     float* tiles = smem + wave * WBUF;                     // double-buffered score chunk
     float* rbufs = tiles + 2 * Tile::FLOATS;               // boundary row of a chunk
+    float* fslot = rbufs + 2 * 64;                         // prefetched progress word
+    const uint32_t fslot_lds = lds_address(fslot);
     float* rings = smem + NW * WBUF;                       // [NW][R]
     float* sink = rings + NW * R + wave * DUMMY;           // per-wave write sink
     int* st = status + b;
@@ -113,7 +115,6 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             lds_dma_dword_sys<0>(brow_up, off, dst, 0u);
         };
         int seen = -1;       // chunks of the previous part known to be complete
-        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
         if (x_in) {
             seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
             issue_row(0);
@@ -128,8 +129,8 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             // P + 1 stores of that chunk (the first chunk's loads are the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
             if (x_in && k > 0) {
-                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
-                const int got = flag_chunks(fl, epoch);
+                // its progress word, loaded one chunk ago before those stores
+                const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
             const float* tile = tiles + (k & 1) * Tile::FLOATS;
@@ -147,7 +148,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                 }
                 dma_quads<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0, L1max,
                                   L2max, lane, t0 + P);
-                if (x_in) fl = load_flag_async(flag_in);
+                if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             // lane 63 publishes its alpha of step u into ring slot (t0+u) % R; the
             // other lanes write into the sink (R is a multiple of P: no wrap in a chunk)
@@ -259,8 +260,10 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     constexpr int FBUF = RBUF + 64;               // flows from the part below (2P+2 floats)
     constexpr int BUF = FBUF + 64;
     static_assert(2 * P + 2 <= 64, "boundary flows fit their buffer");
-    float* bufs = smem + wave * 2 * BUF;
-    float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * BUF);  // [NW][R] (up, diag)
+    float* bufs = smem + wave * (2 * BUF + 64);
+    float* fslot = bufs + 2 * BUF;                 // prefetched progress word
+    const uint32_t fslot_lds = lds_address(fslot);
+    float2* rings = reinterpret_cast<float2*>(smem + NW * (2 * BUF + 64));  // [NW][R] (up, diag)
     float2* sink = rings + NW * R + wave * DUMMY;
     int* st = status + b;
     // the chunk's marginals go to an output tile laid over its own buffer, whose
@@ -317,7 +320,6 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         const float* flows_in =
             reinterpret_cast<const float*>(flows + ((size_t)b * NSmax + (x_in ? s + 1 : s)) * NT);
         int seen = -1;       // chunks of the part below known to be complete
-        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
 
         // Loads of chunk k (t_hi = nsteps-1-kP) into buffer k&1: the score quad tile, P
         // alpha rows (steps t_hi-2 .. t_hi-P-1, four per load), and the row-above values
@@ -358,8 +360,8 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             // marginal stores of that chunk (the first chunk's are the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
             if (x_in && k > 0) {
-                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
-                const int got = flag_chunks(fl, epoch);
+                // its progress word, loaded one chunk ago before those stores
+                const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
             float* buf = bufs + (k & 1) * BUF;
@@ -394,7 +396,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
                 }
                 issue_chunk(k + 1);
-                if (x_in) fl = load_flag_async(flag_in);
+                if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             // lane 0 publishes (up, diag) of step u into slot (kP+u) % R
             float2* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
@@ -533,11 +535,11 @@ constexpr size_t kLdsLimit = 160 * 1024 - 256;
 
 // LDS of one workgroup whose stripes' boundaries use rings of R columns
 size_t lds_forward_r(int R) {
-    return (size_t)wf::NW * (2 * 64 * PF + 2 * 64) * sizeof(float) +
+    return (size_t)wf::NW * (2 * 64 * PF + 3 * 64) * sizeof(float) +
            ((size_t)wf::NW * R + wf::NW * DUMMY) * sizeof(float);
 }
 size_t lds_backward_r(int R, int P) {
-    return (size_t)wf::NW * 2 * (64 * P + 64 * P + 64 + 64) * sizeof(float) +
+    return (size_t)wf::NW * (2 * (64 * P + 64 * P + 64 + 64) + 64) * sizeof(float) +
            ((size_t)wf::NW * R + wf::NW * DUMMY) * sizeof(float2);
 }
 // rings of a workgroup that runs `rows` rows of stripes

@@ -60,7 +60,8 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     constexpr int AR = VT + (HAS_V ? Tile::FLOATS : 0);      // P alpha rows
     constexpr int RR = AR + P * 64;                          // row above
     constexpr int TR = RR + 64;                              // tangent row of the part above
-    constexpr int BUF = TR + 64;
+    constexpr int FS = TR + 64;                              // prefetched progress word
+    constexpr int BUF = FS + 64;
     constexpr int SINK = 64 + P;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
@@ -74,6 +75,8 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float* buf = smem + wave * BUF;
+    float* fslot = buf + FS;
+    const uint32_t fslot_lds = lds_address(fslot);
     float* rings = smem + NW * BUF;                          // [NW][R] tangent of lane 63
     float* sink = rings + NW * R + wave * SINK;
     int* st = status + b;
@@ -115,7 +118,6 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
         const bool x_in = l == 0 && part > 0;        // tangent row above from part - 1
         const bool x_out = l == NL - 1 && has_next;  // tangent row feeds part + 1
         int seen = -1;       // chunks of the previous part known to be complete
-        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
 
         // Loads of chunk k (steps t0 .. t0+P-1): the score (and direction) tiles, the
         // P alpha rows, and for lane j <= P the last row of the stripe above at step
@@ -154,8 +156,8 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             // chunk (the first chunk's loads are the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
             if (x_in && k > 0) {
-                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
-                const int got = flag_chunks(fl, epoch);
+                // its progress word, loaded one chunk ago before those stores
+                const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
             float sv[P], vv[P];
@@ -182,7 +184,7 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
                 }
                 issue_chunk(k + 1);
-                if (x_in) fl = load_flag_async(flag_in);
+                if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             float* toutc = tout + (size_t)t0 * 64;
@@ -286,7 +288,8 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     constexpr int RX = RA + 64;                             // tangent row above
     constexpr int OT = RX + 64;                             // output tile
     constexpr int FB = OT + (DOT ? 0 : Tile::FLOATS);       // flows from the part below
-    constexpr int BUF = FB + 64;
+    constexpr int FS = FB + 64;                             // prefetched progress word
+    constexpr int BUF = FS + 64;
     static_assert(4 * P + 2 <= 64, "boundary flows fit their buffer");
     constexpr int SINK = 64 + P;
     extern __shared__ float smem[];
@@ -303,6 +306,8 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float* buf = smem + wave * BUF;
     float* otile = buf + OT;
+    float* fslot = buf + FS;
+    const uint32_t fslot_lds = lds_address(fslot);
     float4* rings = reinterpret_cast<float4*>(smem + NW * BUF);   // [NW][R]
     float4* sink = rings + NW * R + wave * SINK;
     int* st = status + b;
@@ -360,7 +365,6 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
         const float* flows_in = reinterpret_cast<const float*>(
             flows4 + ((size_t)b * NSmax + (x_in ? s + 1 : s)) * NT);
         int seen = -1;       // chunks of the part below known to be complete
-        uint64_t fl = 0;     // its progress word, loaded one chunk ahead
 
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
@@ -408,8 +412,8 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             // loads are the last issued)
             if (k == 0 || DOT) wait_vmcnt<0>(); else wait_vmcnt<P>();
             if (x_in && k > 0) {
-                __asm__ volatile("" : "+v"(fl));   // complete: issued before those stores
-                const int got = flag_chunks(fl, epoch);
+                // its progress word, loaded one chunk ago before those stores
+                const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
             float sv[P], vv[P];
@@ -456,7 +460,7 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
                 }
                 issue_chunk(k + 1);
-                if (x_in) fl = load_flag_async(flag_in);
+                if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             float4* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
             {
@@ -598,7 +602,7 @@ constexpr int PT = 16;   // tangent sweep chunk
 
 // LDS of one workgroup whose stripe boundaries use rings of R columns
 size_t lds_tangent_r(int mode, int R) {
-    const int buf = 65 * PT * (mode == HVP ? 2 : 1) + PT * 64 + 64 + 64;
+    const int buf = 65 * PT * (mode == HVP ? 2 : 1) + PT * 64 + 64 + 64 + 64;
     return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + PT)) * sizeof(float);
 }
 size_t lds_tangent(int mode, int max_L1, int max_L2) {
@@ -606,7 +610,7 @@ size_t lds_tangent(int mode, int max_L1, int max_L2) {
 }
 
 size_t lds_dual_r(bool has_v, bool dot, int P, int R) {
-    const int buf = 65 * P * (has_v ? 2 : 1) + 2 * P * 64 + 128 + (dot ? 0 : 65 * P) + 64;
+    const int buf = 65 * P * (has_v ? 2 : 1) + 2 * P * 64 + 128 + (dot ? 0 : 65 * P) + 128;
     return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + P)) * sizeof(float4);
 }
 

@@ -189,12 +189,6 @@ __device__ __forceinline__ void store_sys2(float2* p, float2 v) {
 __device__ __forceinline__ void store_flag(uint64_t* p, uint64_t v) {
     __asm__ volatile("global_store_dwordx2 %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
 }
-// issues the load; the value is valid after a vmcnt wait that covers it
-__device__ __forceinline__ uint64_t load_flag_async(const uint64_t* p) {
-    uint64_t v;
-    __asm__ volatile("global_load_dwordx2 %0, %1, off sc0 sc1" : "=v"(v) : "v"(p) : "memory");
-    return v;
-}
 __device__ __forceinline__ uint64_t load_flag(const uint64_t* p) {
     uint64_t v;
     __asm__ volatile("global_load_dwordx2 %0, %1, off sc0 sc1\n\ts_waitcnt vmcnt(0)"
@@ -225,6 +219,17 @@ __device__ __forceinline__ int flag_chunks(uint64_t v, uint32_t epoch) {
     const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
     const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
     return hi == epoch ? (int)lo : -1;
+}
+
+// A progress word prefetched one chunk ahead lands in the wave's 64-dword LDS slot
+// (lane l loads dword min(l, 1) of the word), never in a VGPR: the compiler takes a
+// VGPR written by an asynchronous load as defined when the load issues, and could
+// copy it before the data arrives.  Read the slot with flag_chunks_lds after a
+// vmcnt wait that covers the load, and before the next load into it.
+__device__ __forceinline__ void flag_load_lds(const uint64_t* flag, uint32_t slot_lds, int lane);
+__device__ __forceinline__ int flag_chunks_lds(const float* slot, uint32_t epoch) {
+    const uint32_t lo = __float_as_uint(slot[0]), hi = __float_as_uint(slot[1]);
+    return flag_chunks(((uint64_t)hi << 32) | lo, epoch);
 }
 
 // Waits until the part's progress word reports `need` chunks of this epoch; returns
@@ -379,6 +384,11 @@ __device__ __forceinline__ void lds_dma_dwordx4_nt(const float* sbase, uint32_t&
         : "memory", "m0", "scc");
 }
 #pragma clang diagnostic pop
+
+__device__ __forceinline__ void flag_load_lds(const uint64_t* flag, uint32_t slot_lds, int lane) {
+    uint32_t voff = lane > 0 ? 4u : 0u;
+    lds_dma_dword_sys<0>(reinterpret_cast<const float*>(flag), voff, slot_lds, 0u);
+}
 
 // Waits until at most N vector-memory operations of this wave are outstanding
 // (gfx9 counts loads, stores and LDS DMA on one in-order counter).
