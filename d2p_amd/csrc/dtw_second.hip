@@ -44,20 +44,29 @@ __global__ void __launch_bounds__(NW * 64)
 dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ lengths,
                    const float* __restrict__ alpha_sk, const float* __restrict__ brow,
                    float* __restrict__ tan_sk, float* __restrict__ tan_brow,
-                   int* __restrict__ status, int L1max, int L2max, int NSmax, float T,
-                   int bandwidth, int R) {
+                   int* __restrict__ status, uint64_t* __restrict__ tflag, int B, int L1max,
+                   int L2max, int NSmax, float T, int bandwidth, int R, int G, int SPW,
+                   uint32_t epoch) {
     using Tile = ChunkTile<P>;
     constexpr int AR = Tile::FLOATS;      // P alpha rows after the input tile
     constexpr int RR = AR + P * 64;       // row above
-    constexpr int BUF = RR + 64;
+    constexpr int TR = RR + 64;           // tangent row of the part above
+    constexpr int FS = TR + 64;           // prefetched progress word
+    constexpr int BUF = FS + 64;
     constexpr int SINK = 64 + P;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
-    const int b = blockIdx.x;
+    // parts as in the primal forward: part p > 0 takes its first stripe's tangent row
+    // above from part p - 1 through tan_brow
+    int b, part;
+    split_decode(blockIdx.x, G, b, part);
+    if (b >= B) return;
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float* buf = smem + wave * BUF;
+    float* fslot = buf + FS;
+    const uint32_t fslot_lds = lds_address(fslot);
     float* rings = smem + NW * BUF;
     float* sink = rings + NW * R + wave * SINK;
     int* st = status + b;
@@ -77,8 +86,14 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
     const size_t NT = (size_t)stored_steps(L2max);
     const float* ibase = input + (size_t)b * L1max * L2max;   // V (HVP) or costs (T)
     const uint32_t in_lds = lds_address(buf);
+    const int s_begin = part * SPW;
+    const int NL = max(min(NS, s_begin + SPW) - s_begin, 0);   // stripes of this part
+    const bool has_next = s_begin + NL < NS;
+    const uint64_t* flag_in = tflag + (size_t)b * G + (part > 0 ? part - 1 : 0);
+    uint64_t* flag_out = tflag + (size_t)b * G + part;
 
-    for (int s = wave; s < NS; s += NW) {
+    for (int l = wave; l < NL; l += NW) {
+        const int s = s_begin + l;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
         const float ej = band_centre(i0 + lane + 1, L1, L2);
@@ -86,8 +101,12 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
         const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
         float* tout = tan_sk + (((size_t)b * NSmax + s) * NT + APAD) * 64;
         float* tb_s = tan_brow + ((size_t)b * NSmax + s) * NT;
-        const float* ring_in = ring_from(rings, s, R);
-        float* ring_out = ring_of(rings, s, R);
+        const float* tb_up = tan_brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
+        const float* ring_in = ring_from(rings, l, R);
+        float* ring_out = ring_of(rings, l, R);
+        const bool x_in = l == 0 && part > 0;        // tangent row above from part - 1
+        const bool x_out = l == NL - 1 && has_next;  // tangent row feeds part + 1
+        int seen = -1;       // chunks of the previous part known to be complete
 
         auto issue_chunk = [&](int k) {
             const int t0 = k * P;
@@ -96,11 +115,18 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
             uint32_t roff = (uint32_t)min(t0 + 62 + min(lane, P), nsteps - 1) * 4u;
             uint32_t rl = in_lds + RR * 4;
             lds_dma_dword<0>(bup, roff, rl, 0u);
+            if (x_in) {
+                // lane j < P: the tangent of the last row above at step t0 + 63 + j
+                uint32_t toff = (uint32_t)min(t0 + 63 + min(lane, P - 1), nsteps - 1) * 4u;
+                uint32_t tl = in_lds + TR * 4;
+                lds_dma_dword_sys<0>(tb_up, toff, tl, 0u);
+            }
         };
 
 #pragma unroll
         for (int t = -APAD; t < 0; ++t) lane_store(tout + t * 64, ul4, 0.0f);
         wave_lds_sync();
+        if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
         issue_chunk(0);
         float Aw[P + 2];
         Aw[P] = kPINF;   // alpha at steps -2, -1: column-0 boundary
@@ -109,8 +135,15 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
 
         for (int k = 0; k < nch; ++k) {
             const int t0 = k * P;
-            chunk_waits<P>(prog, s, NS, k, nch, R, st);
+            chunk_waits<P>(prog, l, NL, k, nch, R, st);
+            // this chunk's loads, followed by at least the P + 1 stores of the previous
+            // chunk
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (x_in && k > 0) {
+                // its progress word, loaded one chunk ago before those stores
+                const int got = flag_chunks_lds(fslot, epoch);
+                seen = got > seen ? got : seen;
+            }
             float iv[P];
 #pragma unroll
             for (int u = 0; u < P; ++u) iv[u] = buf[tbase + u];
@@ -121,9 +154,17 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
             float bv = buf[RR + lane];
             bv = (s > 0 && lane <= P && t0 + 62 + lane <= nsteps - 1) ? bv : kPINF;
             float rreg = 0.0f;
-            if (s > 0 && lane < P) rreg = ring_in[ring_index(t0 + lane + 63, R)];
+            if (s > 0 && lane < P)
+                rreg = x_in ? buf[TR + lane] : ring_in[ring_index(t0 + lane + 63, R)];
             wave_lds_sync();
-            if (k + 1 < nch) issue_chunk(k + 1);
+            if (k + 1 < nch) {
+                if (x_in) {
+                    const int need = min(k + 1 + lead(P), nch);
+                    if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                }
+                issue_chunk(k + 1);
+                if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
+            }
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             float* toutc = tout + (size_t)t0 * 64;
 #pragma unroll
@@ -158,8 +199,22 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
                 pub[u] = cur;
             }
             wave_lds_sync();
-            if (lane < P) lane_store(tb_s, (unsigned)(t0 + lane) * 4u, ring_out[t0 % R + lane]);
-            publish(prog, wave, s * PROG_STRIDE + k + 1);
+            if (lane < P) {
+                const float v = ring_out[t0 % R + lane];
+                if (x_out) store_sys(tb_s + t0 + lane, v);
+                else lane_store(tb_s, (unsigned)(t0 + lane) * 4u, v);
+            }
+            publish(prog, wave, l * PROG_STRIDE + k + 1);
+            if (x_out && k >= 2) {
+                // at least P + P/4 + 1 loads and 2P + 2 stores follow the row store of
+                // chunk k - 2: it (and everything before) is complete
+                wait_vmcnt<3 * P + P / 4 + 3>();
+                if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
+            }
+        }
+        if (x_out) {
+            wait_vmcnt<0>();
+            if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
         }
     }
 }
@@ -171,25 +226,37 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
                 const float* __restrict__ alpha_sk, const float* __restrict__ brow,
                 const float* __restrict__ tan_sk, const float* __restrict__ tan_brow,
                 float* __restrict__ out, float* __restrict__ dot, int* __restrict__ status,
-                float* __restrict__ trash, int L1max, int L2max, int NSmax, float T,
-                int bandwidth, int R) {
+                float* __restrict__ trash, uint64_t* __restrict__ dflag,
+                float4* __restrict__ flows4, float* __restrict__ spart, int B, int L1max,
+                int L2max, int NSmax, float T, int bandwidth, int R, int G, int SPW,
+                uint32_t epoch) {
     using Tile = ChunkTile<P>;
     constexpr int AR = DOT ? Tile::FLOATS : 0;   // P alpha rows (after the V tile)
     constexpr int XR = AR + P * 64;
     constexpr int RA = XR + P * 64;
     constexpr int RX = RA + 64;
     constexpr int OT = RX + 64;
-    constexpr int BUF = OT + (DOT ? 0 : Tile::FLOATS);
+    constexpr int FB = OT + (DOT ? 0 : Tile::FLOATS);   // flows from the part below
+    constexpr int FS = FB + 64;                         // prefetched progress word
+    constexpr int BUF = FS + 64;
+    static_assert(4 * P <= 64, "boundary flows fit their buffer");
     constexpr int SINK = 64 + P;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red[NW];
-    const int b = blockIdx.x;
+    // parts run bottom-up as in the primal backward; the last stripe of a part below
+    // the first hands its flows to the part above through flows4
+    int b, dpart;
+    split_decode(blockIdx.x, G, b, dpart);
+    if (b >= B) return;
+    const int part = G - 1 - dpart;
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float* buf = smem + wave * BUF;
     float* otile = buf + OT;
+    float* fslot = buf + FS;
+    const uint32_t fslot_lds = lds_address(fslot);
     float4* rings = reinterpret_cast<float4*>(smem + NW * BUF);
     float4* sink = rings + NW * R + wave * SINK;
     int* st = status + b;
@@ -211,13 +278,22 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
     float* obase = DOT ? nullptr : out + (size_t)b * L1max * L2max;
     const uint32_t in_lds = lds_address(buf);
 
-    if (!DOT) zero_padding(obase, L1, L2, L1max, L2max, NW * 64);
+    if (!DOT) {   // each part zeroes its share of the rows' padding
+        const int rows = (L1max + G - 1) / G;
+        zero_padding(obase, L1, L2, L1max, L2max, NW * 64, part * rows,
+                     min(L1max, part * rows + rows));
+    }
 
     float dacc = 0.0f;
     float A[P + 2], X[P + 2];
+    const int s_begin = part * SPW;
+    const int NL = max(min(NS, s_begin + SPW) - s_begin, 0);   // stripes of this part
+    const bool has_next = s_begin + NL < NS;
+    const uint64_t* flag_in = dflag + (size_t)b * G + (part + 1 < G ? part + 1 : part);
+    uint64_t* flag_out = dflag + (size_t)b * G + part;
 
-    for (int q = wave; q < NS; q += NW) {
-        const int s = NS - 1 - q;
+    for (int q = wave; q < NL; q += NW) {
+        const int s = s_begin + NL - 1 - q;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
         const float ej = band_centre(i0 + lane + 1, L1, L2);
@@ -230,7 +306,14 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
         const float* xup = tan_brow + ub;
         const float4* ring_in = ring_from(rings, q, R);
         float4* ring_out = ring_of(rings, q, R);
-        const bool below = q > 0;
+        const bool x_in = q == 0 && has_next;             // flows from the part below
+        const bool x_out = q == NL - 1 && part > 0;       // flows to the part above
+        const bool below = q > 0 || x_in;
+        // boundary flows by producer step: written by stripe s (x_out), read from s + 1
+        float4* flows_out = flows4 + ((size_t)b * NSmax + s) * NT;
+        const float* flows_in = reinterpret_cast<const float*>(
+            flows4 + ((size_t)b * NSmax + (x_in ? s + 1 : s)) * NT);
+        int seen = -1;       // chunks of the part below known to be complete
 
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
@@ -243,6 +326,14 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
             o = roff;
             l = in_lds + RX * 4;
             lds_dma_dword<0>(xup, o, l, 0u);
+            if (x_in) {
+                // flows of producer slots kP+62 .. kP+62+P (float4 each), from .z of the
+                // first to .y of the last: float f of that range in lane f, clamped to
+                // the last slot
+                o = (uint32_t)min((k * P + 62) * 4 + 2 + min(lane, 4 * P - 1), (nsteps - 1) * 4 + 3) * 4u;
+                l = in_lds + FB * 4;
+                lds_dma_dword_sys<0>(flows_in, o, l, 0u);
+            }
         };
 
         {
@@ -255,14 +346,22 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
             __asm__ volatile("" ::"v"(A[P]), "v"(A[P + 1]), "v"(X[P]), "v"(X[P + 1]));
         }
         wave_lds_sync();
+        if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
         issue_chunk(0);
         float lb = 0.0f, lg = 0.0f, ubt = 0.0f, ug = 0.0f;
         float db = 0.0f, dg = 0.0f, db2 = 0.0f, dg2 = 0.0f;
 
         for (int k = 0; k < nch; ++k) {
             const int t_hi = nsteps - 1 - k * P;
-            chunk_waits<P>(prog, q, NS, k, nch, R, st);
+            chunk_waits<P>(prog, q, NL, k, nch, R, st);
+            // this chunk's loads, followed by at least the P output stores of the
+            // previous chunk (none when accumulating a dot product)
             if (k == 0 || DOT) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (x_in && k > 0) {
+                // its progress word, loaded one chunk ago before those stores
+                const int got = flag_chunks_lds(fslot, epoch);
+                seen = got > seen ? got : seen;
+            }
             float vv[P];
 #pragma unroll
             for (int u = 0; u < P; ++u) vv[u] = DOT ? buf[tbase + u] : 0.0f;
@@ -281,15 +380,30 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
             float qub = 0.0f, qug = 0.0f, qdb = 0.0f, qdg = 0.0f;
             if (below && lane >= 64 - P) {
                 const int j = 63 - lane;
-                const float4 ru = ring_in[ring_index(k * P + j + 63, R)];
-                const float4 rd = ring_in[ring_index(k * P + j + 62, R)];
-                qub = ru.x;
-                qug = ru.y;
-                qdb = rd.z;
-                qdg = rd.w;
+                if (x_in) {
+                    // .z, .w of slot kP+62+j and .x, .y of slot kP+63+j
+                    qdb = buf[FB + 4 * j];
+                    qdg = buf[FB + 4 * j + 1];
+                    qub = buf[FB + 4 * j + 2];
+                    qug = buf[FB + 4 * j + 3];
+                } else {
+                    const float4 ru = ring_in[ring_index(k * P + j + 63, R)];
+                    const float4 rd = ring_in[ring_index(k * P + j + 62, R)];
+                    qub = ru.x;
+                    qug = ru.y;
+                    qdb = rd.z;
+                    qdg = rd.w;
+                }
             }
             wave_lds_sync();
-            if (k + 1 < nch) issue_chunk(k + 1);
+            if (k + 1 < nch) {
+                if (x_in) {
+                    const int need = min(k + 1 + lead(P), nch);
+                    if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                }
+                issue_chunk(k + 1);
+                if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
+            }
             float4* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
             {
                 const float u0b = lane_bcast(qub, 63), u0g = lane_bcast(qug, 63);
@@ -359,6 +473,20 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
             wave_lds_sync();
             if (!DOT) write_tile<P, -1>(otile, obase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             publish(prog, wave, q * PROG_STRIDE + k + 1);
+            if (x_out) {
+                // this chunk's flows to the part above, by producer step
+                if (lane < P) store_sys4(flows_out + k * P + lane, ring_out[ring_index(k * P, R) + lane]);
+                if (k >= 2) {
+                    // at least P/2 + 2 (DOT: + P) loads, 2 flow stores and (DOT: none,
+                    // else 2P) output stores follow the flow store of chunk k - 2
+                    wait_vmcnt<(DOT ? P + P / 2 + 4 : 2 * P + P / 2 + 4)>();
+                    if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
+                }
+            }
+        }
+        if (x_out) {
+            wait_vmcnt<0>();
+            if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
         }
     }
 
@@ -369,7 +497,8 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
         if (threadIdx.x == 0) {
             float t = 0.0f;
             for (int w = 0; w < NW; ++w) t += red[w];
-            dot[b] = t;
+            if (G == 1) dot[b] = t;
+            else spart[(size_t)b * G + part] = t;
         }
     }
 }
@@ -379,31 +508,39 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
 constexpr size_t kLdsLimit = 160 * 1024 - 256;
 constexpr int PT = 16;
 
-size_t lds_tangent(int L1, int L2) {
-    const int R = ring_len(L1, L2, 256);
-    return (size_t)NW * (65 * PT + PT * 64 + 64) * sizeof(float) +
+// LDS of one workgroup whose stripe boundaries use rings of R columns
+size_t lds_tangent_r(int R) {
+    return (size_t)NW * (65 * PT + PT * 64 + 64 + 64 + 64) * sizeof(float) +
            ((size_t)NW * R + NW * (64 + PT)) * sizeof(float);
 }
+size_t lds_tangent(int L1, int L2) { return lds_tangent_r(ring_len(L1, L2, 256)); }
 
-size_t lds_dual(bool dot, int P, int L1, int L2) {
-    const int R = ring_len(L1, L2, 128);
-    const int buf = (dot ? 65 * P : 0) + 2 * P * 64 + 128 + (dot ? 0 : 65 * P);
+size_t lds_dual_r(bool dot, int P, int R) {
+    const int buf = (dot ? 65 * P : 0) + 2 * P * 64 + 128 + (dot ? 0 : 65 * P) + 128;
     return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + P)) * sizeof(float4);
 }
 
-int dual_chunk(bool dot, int L1, int L2) {
-    if (lds_dual(dot, 16, L1, L2) <= kLdsLimit) return 16;
-    if (lds_dual(dot, 8, L1, L2) <= kLdsLimit) return 8;
-    if (lds_dual(dot, 4, L1, L2) <= kLdsLimit) return 4;
+// Largest reverse-sweep chunk (16, 8 or 4 steps) whose buffers and rings fit in LDS,
+// for a workgroup that runs `rows` rows of stripes.
+int dual_chunk(bool dot, int rows, int L2) {
+    const int R = ring_len(rows, L2, 128);
+    if (lds_dual_r(dot, 16, R) <= kLdsLimit) return 16;
+    if (lds_dual_r(dot, 8, R) <= kLdsLimit) return 8;
+    if (lds_dual_r(dot, 4, R) <= kLdsLimit) return 4;
     return 0;
 }
 
+// Workspace after the primal layout: tangent table + last rows, [B] scalars, then for
+// split elements the parts' partial sums and the reverse sweep's boundary flows
+// (float4 by step).
 struct Second {
     Layout prim;
     float* tan_sk;
     float* tan_brow;
     float* value;
     float* scratch;
+    float* spart;     // [B][stripe]
+    float4* flows4;   // [B][stripe][step]
     size_t bytes;
 };
 
@@ -418,6 +555,11 @@ Second second_layout(void* ws, int B, int L1, int L2) {
     w.value = (float*)p;
     w.scratch = w.value + B;
     p += round256((size_t)2 * B * sizeof(float));
+    const size_t parts = (size_t)B * (ns > 0 ? ns : 1);
+    w.spart = (float*)p;
+    p += round256(parts * sizeof(float));
+    w.flows4 = (float4*)p;
+    p += round256(parts * (size_t)stored_steps(L2) * sizeof(float4));
     w.bytes = (size_t)(p - (char*)ws);
     return w;
 }
@@ -426,15 +568,17 @@ template <int MODE>
 int launch_tangent(const float* input, const int* lengths, int B, int L1, int L2, float T,
                    int bw, const Second& w, hipStream_t st) {
     const int ns = (L1 + 63) / 64;
-    const int R = ring_len(L1, L2, 256);
-    const size_t lds = lds_tangent(L1, L2);
+    // rings of an unsplit element that do not fit: parts of at most NW stripes
+    const Split sp = choose_split(B, L1, w.prim, lds_tangent(L1, L2) <= kLdsLimit ? 0 : NW);
+    const int R = ring_len(sp.G > 1 ? sp.SPW * 64 : L1, L2, 256);
+    const size_t lds = lds_tangent_r(R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     auto kern = dtw_tangent_kernel<MODE, PT>;
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
-    D2P_LAUNCH("dtw_tangent", kern, dim3(B), dim3(NW * 64), lds, st, input, lengths,
-               w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, w.prim.status, L1, L2, ns, T,
-               bw, R);
+    D2P_LAUNCH("dtw_tangent", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, input,
+               lengths, w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, w.prim.status,
+               w.prim.fflag, B, L1, L2, ns, T, bw, R, sp.G, sp.SPW, next_epoch());
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -443,30 +587,30 @@ template <int MODE, bool DOT>
 int launch_dual(const float* V, const int* lengths, int B, int L1, int L2, float T, int bw,
                 const Second& w, float* out, float* dot, hipStream_t st) {
     const int ns = (L1 + 63) / 64;
-    const int R = ring_len(L1, L2, 128);
-    const int P = dual_chunk(DOT, L1, L2);
+    const Split sp = choose_split(B, L1, w.prim, dual_chunk(DOT, L1, L2) > 0 ? 0 : NW);
+    const int rows = sp.G > 1 ? sp.SPW * 64 : L1;
+    const int R = ring_len(rows, L2, 128);
+    const int P = dual_chunk(DOT, rows, L2);
     D2P_REQUIRE(P > 0, "sequence too long for the LDS stripe rings");
-    const size_t lds = lds_dual(DOT, P, L1, L2);
+    const size_t lds = lds_dual_r(DOT, P, R);
     auto k16 = dtw_dual_kernel<MODE, 16, DOT>;
     auto k8 = dtw_dual_kernel<MODE, 8, DOT>;
     auto k4 = dtw_dual_kernel<MODE, 4, DOT>;
     auto kern = P == 16 ? k16 : (P == 8 ? k8 : k4);
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
-    D2P_LAUNCH("dtw_dual", kern, dim3(B), dim3(NW * 64), lds, st, V, lengths, w.prim.alpha_sk,
-               w.prim.brow, w.tan_sk, w.tan_brow, out, dot, w.prim.status, w.prim.trash, L1, L2,
-               ns, T, bw, R);
+    D2P_LAUNCH("dtw_dual", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, V, lengths,
+               w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, out, dot, w.prim.status,
+               w.prim.trash, w.prim.bflag, w.flows4, w.spart, B, L1, L2, ns, T, bw, R, sp.G,
+               sp.SPW, next_epoch());
+    if (DOT && sp.G > 1 && launch_sum_parts(w.spart, dot, B, sp.G, st) != D2P_OK)
+        return D2P_ERR_HIP;
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
 
-int check(int B, int L1, int L2, float T) {
-    const int rc = dtw::check_shape(B, L1, L2, T);
-    if (rc != D2P_OK) return rc;
-    D2P_REQUIRE(lds_tangent(L1, L2) <= kLdsLimit && dual_chunk(false, L1, L2) > 0,
-                "sequence too long for the LDS stripe rings");
-    return D2P_OK;
-}
+// rings that do not fit for an unsplit element force parts of at most NW stripes
+int check(int B, int L1, int L2, float T) { return dtw::check_shape(B, L1, L2, T); }
 
 }  // namespace dtw2
 }  // namespace d2p_amd

@@ -38,7 +38,24 @@ __global__ void partition_merge_kernel(const float2* __restrict__ fpart,
     partition[b] = tot.m + T * kLn2 * fast_log2(tot.z);
 }
 
+// Sum of the parts' partial results of a split element.
+__global__ void sum_parts_kernel(const float* __restrict__ spart, float* __restrict__ out, int B,
+                                 int G) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    float t = 0.0f;
+    for (int g = 0; g < G; ++g) t += spart[(size_t)b * G + g];
+    out[b] = t;
+}
+
 }  // namespace
+
+int launch_sum_parts(const float* spart, float* out, int B, int G, hipStream_t st) {
+    D2P_LAUNCH("sum_parts", sum_parts_kernel, dim3((B + 255) / 256), dim3(256), 0, st, spart, out,
+               B, G);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
 
 Split choose_split(int B, int max_L1, const Layout& ws, int max_spw) {
     const int ns = (max_L1 + 63) / 64;

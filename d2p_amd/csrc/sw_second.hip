@@ -586,15 +586,6 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     }
 }
 
-// Sum of the parts' partial results of a split element.
-__global__ void sum_parts(const float* __restrict__ spart, float* __restrict__ out, int B, int G) {
-    const int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= B) return;
-    float t = 0.0f;
-    for (int g = 0; g < G; ++g) t += spart[(size_t)b * G + g];
-    out[b] = t;
-}
-
 // ------------------------------------------------------------------ host side
 
 constexpr size_t kLdsLimit = 160 * 1024 - 256;
@@ -678,9 +669,8 @@ int launch_tangent(const float* scores, const float* V, const int* lengths, int 
                lengths, w.prim.alpha_sk, w.prim.brow, w.part, w.tan_sk, w.tan_brow, sdot,
                w.prim.status, w.prim.fflag, w.spart, B, L1, L2, ns, gap, T, R, sp.G, sp.SPW,
                next_epoch());
-    if (MODE == HVP && sp.G > 1)
-        D2P_LAUNCH("sum_parts", sum_parts, dim3((B + 255) / 256), dim3(256), 0, st, w.spart, sdot,
-                   B, sp.G);
+    if (MODE == HVP && sp.G > 1 && launch_sum_parts(w.spart, sdot, B, sp.G, st) != D2P_OK)
+        return D2P_ERR_HIP;
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -707,9 +697,8 @@ int launch_dual(const float* scores, const float* V, const int* lengths, int B, 
                lengths, w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, w.part, dS, out, dot,
                w.prim.status, w.prim.trash, w.prim.bflag, w.flows4, w.spart, B, L1, L2, ns, gap,
                T, R, sp.G, sp.SPW, next_epoch());
-    if (DOT && sp.G > 1)
-        D2P_LAUNCH("sum_parts", sum_parts, dim3((B + 255) / 256), dim3(256), 0, st, w.spart, dot,
-                   B, sp.G);
+    if (DOT && sp.G > 1 && launch_sum_parts(w.spart, dot, B, sp.G, st) != D2P_OK)
+        return D2P_ERR_HIP;
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }

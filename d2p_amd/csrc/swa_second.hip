@@ -47,23 +47,33 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
                    const int* __restrict__ lengths, const float* __restrict__ alpha_sk,
                    const float* __restrict__ brow, const float* __restrict__ partition,
                    float* __restrict__ tan_sk, float* __restrict__ tan_brow,
-                   float* __restrict__ sdot, int* __restrict__ status, int L1max, int L2max,
-                   int NSmax, float go, float ge, float T, int R) {
+                   float* __restrict__ sdot, int* __restrict__ status,
+                   uint64_t* __restrict__ tflag, float* __restrict__ spart, int B, int L1max,
+                   int L2max, int NSmax, float go, float ge, float T, int R, int G, int SPW,
+                   uint32_t epoch) {
     constexpr bool HAS_V = MODE == HVP;
     using Tile = ChunkTile<P>;
     constexpr int VT = Tile::FLOATS;
     constexpr int AR = VT + (HAS_V ? Tile::FLOATS : 0);   // 3 planes x P alpha rows
     constexpr int RR = AR + 3 * P * 64;                   // 3 planes x row above
-    constexpr int BUF = RR + 3 * 64;
+    constexpr int TR = RR + 3 * 64;                       // 3 tangent rows of the part above
+    constexpr int FS = TR + 3 * 64;                       // prefetched progress word
+    constexpr int BUF = FS + 64;
     constexpr int SINK = 64 + P;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red[NW];
-    const int b = blockIdx.x;
+    // parts as in the primal forward: part p > 0 takes its first stripe's tangent rows
+    // above from part p - 1 through tan_brow
+    int b, part;
+    split_decode(blockIdx.x, G, b, part);
+    if (b >= B) return;
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float* buf = smem + wave * BUF;
+    float* fslot = buf + FS;
+    const uint32_t fslot_lds = lds_address(fslot);
     float4* rings = reinterpret_cast<float4*>(smem + NW * BUF);
     float4* sink = rings + NW * R + wave * SINK;
     int* st = status + b;
@@ -86,16 +96,26 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
     const float* vbase = HAS_V ? V + (size_t)b * L1max * L2max : nullptr;
     const uint32_t in_lds = lds_address(buf);
     float sacc = 0.0f;
+    const int s_begin = part * SPW;
+    const int NL = max(min(NS, s_begin + SPW) - s_begin, 0);   // stripes of this part
+    const bool has_next = s_begin + NL < NS;
+    const uint64_t* flag_in = tflag + (size_t)b * G + (part > 0 ? part - 1 : 0);
+    uint64_t* flag_out = tflag + (size_t)b * G + part;
 
-    for (int s = wave; s < NS; s += NW) {
+    for (int l = wave; l < NL; l += NW) {
+        const int s = s_begin + l;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
         const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * 3 * PL;
         const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * 3 * NT;
         float* tout = tan_sk + ((size_t)b * NSmax + s) * 3 * PL + APAD * 64;
         float* tb_s = tan_brow + ((size_t)b * NSmax + s) * 3 * NT;
-        const float4* ring_in = ring_from(rings, s, R);
-        float4* ring_out = ring_of(rings, s, R);
+        const float* tb_up = tan_brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * 3 * NT;
+        const float4* ring_in = ring_from(rings, l, R);
+        float4* ring_out = ring_of(rings, l, R);
+        const bool x_in = l == 0 && part > 0;        // tangent rows above from part - 1
+        const bool x_out = l == NL - 1 && has_next;  // tangent rows feed part + 1
+        int seen = -1;       // chunks of the previous part known to be complete
 
         auto issue_chunk = [&](int k) {
             const int t0 = k * P;
@@ -107,8 +127,17 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
             const uint32_t roff = (uint32_t)min(t0 + 62 + min(lane, P), nsteps - 1) * 4u;
 #pragma unroll
             for (int pl = 0; pl < 3; ++pl) {
-                uint32_t o = roff, l = in_lds + (RR + pl * 64) * 4;
-                lds_dma_dword<0>(bup + pl * NT, o, l, 0u);
+                uint32_t o = roff, la = in_lds + (RR + pl * 64) * 4;
+                lds_dma_dword<0>(bup + pl * NT, o, la, 0u);
+            }
+            if (x_in) {
+                // lane j < P: the tangents of the last row above at step t0 + 63 + j
+                const uint32_t toff = (uint32_t)min(t0 + 63 + min(lane, P - 1), nsteps - 1) * 4u;
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl) {
+                    uint32_t o = toff, la = in_lds + (TR + pl * 64) * 4;
+                    lds_dma_dword_sys<0>(tb_up + pl * NT, o, la, 0u);
+                }
             }
         };
 
@@ -117,6 +146,7 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
 #pragma unroll
             for (int pl = 0; pl < 3; ++pl) lane_store(tout + pl * PL + t * 64, ul4, 0.0f);
         wave_lds_sync();
+        if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
         issue_chunk(0);
         float AM[P + 2], AI[P + 2], AD[P + 2];
         AM[P] = AM[P + 1] = AI[P] = AI[P + 1] = AD[P] = AD[P + 1] = kNINF;
@@ -125,9 +155,15 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
 
         for (int k = 0; k < nch; ++k) {
             const int t0 = k * P;
-            chunk_waits<P>(prog, s, NS, k, nch, R, st);
-            // this chunk's loads, followed by the 3P + 3 stores of the previous chunk
+            chunk_waits<P>(prog, l, NL, k, nch, R, st);
+            // this chunk's loads, followed by at least the 3P + 3 stores of the previous
+            // chunk
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<3 * P>();
+            if (x_in && k > 0) {
+                // its progress word, loaded one chunk ago before those stores
+                const int got = flag_chunks_lds(fslot, epoch);
+                seen = got > seen ? got : seen;
+            }
             float sv[P], vv[P];
 #pragma unroll
             for (int u = 0; u < P; ++u) {
@@ -149,13 +185,26 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
             float bD = row_ok ? buf[RR + 128 + lane] : kNINF;
             float rM = 0.0f, rI = 0.0f, rD = 0.0f;
             if (s > 0 && lane < P) {
-                const float4 r = ring_in[ring_index(t0 + lane + 63, R)];
-                rM = r.x;
-                rI = r.y;
-                rD = r.z;
+                if (x_in) {
+                    rM = buf[TR + lane];
+                    rI = buf[TR + 64 + lane];
+                    rD = buf[TR + 128 + lane];
+                } else {
+                    const float4 r = ring_in[ring_index(t0 + lane + 63, R)];
+                    rM = r.x;
+                    rI = r.y;
+                    rD = r.z;
+                }
             }
             wave_lds_sync();
-            if (k + 1 < nch) issue_chunk(k + 1);
+            if (k + 1 < nch) {
+                if (x_in) {
+                    const int need = min(k + 1 + lead(P), nch);
+                    if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                }
+                issue_chunk(k + 1);
+                if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
+            }
             float4* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             float* toutc = tout + (size_t)t0 * 64;
 #pragma unroll
@@ -239,12 +288,28 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
             wave_lds_sync();
             if (lane < P) {
                 const float4 r = ring_out[t0 % R + lane];
-                const unsigned o = (unsigned)(t0 + lane) * 4u;
-                lane_store(tb_s, o, r.x);
-                lane_store(tb_s + NT, o, r.y);
-                lane_store(tb_s + 2 * NT, o, r.z);
+                if (x_out) {
+                    store_sys(tb_s + t0 + lane, r.x);
+                    store_sys(tb_s + NT + t0 + lane, r.y);
+                    store_sys(tb_s + 2 * NT + t0 + lane, r.z);
+                } else {
+                    const unsigned o = (unsigned)(t0 + lane) * 4u;
+                    lane_store(tb_s, o, r.x);
+                    lane_store(tb_s + NT, o, r.y);
+                    lane_store(tb_s + 2 * NT, o, r.z);
+                }
             }
-            publish(prog, wave, s * PROG_STRIDE + k + 1);
+            publish(prog, wave, l * PROG_STRIDE + k + 1);
+            if (x_out && k >= 2) {
+                // at least P + 3P/4 + 3 loads and 6P + 6 stores follow the row stores of
+                // chunk k - 2 (more than the counter holds): those are complete
+                wait_vmcnt<63>();
+                if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
+            }
+        }
+        if (x_out) {
+            wait_vmcnt<0>();
+            if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
         }
     }
 
@@ -255,7 +320,8 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
         if (threadIdx.x == 0) {
             float t = 0.0f;
             for (int w = 0; w < NW; ++w) t += red[w];
-            sdot[b] = t;
+            if (G == 1) sdot[b] = t;
+            else spart[(size_t)b * G + part] = t;
         }
     }
 }
@@ -269,8 +335,11 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 const float* __restrict__ brow, const float* __restrict__ tan_sk,
                 const float* __restrict__ tan_brow, const float* __restrict__ partition,
                 const float* __restrict__ dS, float* __restrict__ out, float* __restrict__ dot,
-                int* __restrict__ status, float* __restrict__ trash, int L1max, int L2max,
-                int NSmax, float go, float ge, float T, int R) {
+                int* __restrict__ status, float* __restrict__ trash,
+                uint64_t* __restrict__ dflag, float4* __restrict__ fU, float4* __restrict__ fD,
+                float2* __restrict__ fE, float* __restrict__ spart, int B, int L1max,
+                int L2max, int NSmax, float go, float ge, float T, int R, int G, int SPW,
+                uint32_t epoch) {
     constexpr bool HAS_V = MODE == HVP || DOT;
     using Tile = ChunkTile<P>;
     constexpr int VT = Tile::FLOATS;
@@ -279,16 +348,29 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     constexpr int RA = XR + 3 * P * 64;                   // 3 alpha rows above
     constexpr int RX = RA + 3 * 64;                       // 3 tangent rows above
     constexpr int OT = RX + 3 * 64;
-    constexpr int BUF = OT + (DOT ? 0 : Tile::FLOATS);
+    // flows from the part below: up (float4), diagonal (float4), diagonal to D (float2)
+    constexpr int FBU = OT + (DOT ? 0 : Tile::FLOATS);
+    constexpr int FBD = FBU + 64;
+    constexpr int FBE = FBD + 64;
+    constexpr int FS = FBE + 64;                          // prefetched progress word
+    constexpr int BUF = FS + 64;
+    static_assert(4 * P <= 64, "boundary flows fit their buffers");
     extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red[NW];
-    const int b = blockIdx.x;
+    // parts run bottom-up as in the primal backward; the last stripe of a part below
+    // the first hands its flows to the part above through fU / fD / fE
+    int b, dpart;
+    split_decode(blockIdx.x, G, b, dpart);
+    if (b >= B) return;
+    const int part = G - 1 - dpart;
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float* buf = smem + wave * BUF;
     float* otile = buf + OT;
+    float* fslot = buf + FS;
+    const uint32_t fslot_lds = lds_address(fslot);
     // rings [NW][R]: (beta, g) up flows to (M, I); diagonal flows to (M, I); to D
     float4* ringU = reinterpret_cast<float4*>(smem + NW * BUF);
     float4* ringD = ringU + NW * R;
@@ -315,13 +397,22 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     float* obase = DOT ? nullptr : out + (size_t)b * L1max * L2max;
     const uint32_t in_lds = lds_address(buf);
 
-    if (!DOT) zero_padding(obase, L1, L2, L1max, L2max, NW * 64);
+    if (!DOT) {   // each part zeroes its share of the rows' padding
+        const int rows = (L1max + G - 1) / G;
+        zero_padding(obase, L1, L2, L1max, L2max, NW * 64, part * rows,
+                     min(L1max, part * rows + rows));
+    }
 
     float dacc = 0.0f;
     float AM[P + 2], AI[P + 2], AD[P + 2], XM[P + 2], XI[P + 2], XD[P + 2];
+    const int s_begin = part * SPW;
+    const int NL = max(min(NS, s_begin + SPW) - s_begin, 0);   // stripes of this part
+    const bool has_next = s_begin + NL < NS;
+    const uint64_t* flag_in = dflag + (size_t)b * G + (part + 1 < G ? part + 1 : part);
+    uint64_t* flag_out = dflag + (size_t)b * G + part;
 
-    for (int q = wave; q < NS; q += NW) {
-        const int s = NS - 1 - q;
+    for (int q = wave; q < NL; q += NW) {
+        const int s = s_begin + NL - 1 - q;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
         const size_t sb = ((size_t)b * NSmax + s) * 3;
@@ -336,7 +427,13 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
         float4* outU = ring_of(ringU, q, R);
         float4* outD = ring_of(ringD, q, R);
         float2* outE = ring_of(ringE, q, R);
-        const bool below = q > 0;
+        const bool x_in = q == 0 && has_next;             // flows from the part below
+        const bool x_out = q == NL - 1 && part > 0;       // flows to the part above
+        const bool below = q > 0 || x_in;
+        // boundary flows by producer step: written by stripe s (x_out), read from s + 1
+        const size_t fo = ((size_t)b * NSmax + s) * NT;
+        const size_t fi = ((size_t)b * NSmax + (x_in ? s + 1 : s)) * NT;
+        int seen = -1;       // chunks of the part below known to be complete
 
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
@@ -355,6 +452,21 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 o = roff;
                 l = in_lds + (RX + pl * 64) * 4;
                 lds_dma_dword<0>(bupX + pl * NT, o, l, 0u);
+            }
+            if (x_in) {
+                // up flows of producer slots kP+63 .. kP+62+P, diagonal flows of slots
+                // kP+62 .. kP+61+P: float f of each range in lane f, clamped to the last
+                // slot
+                const int last = nsteps - 1;
+                uint32_t o = (uint32_t)min((k * P + 63) * 4 + min(lane, 4 * P - 1), last * 4 + 3) * 4u;
+                uint32_t l = in_lds + FBU * 4;
+                lds_dma_dword_sys<0>(reinterpret_cast<const float*>(fU + fi), o, l, 0u);
+                o = (uint32_t)min((k * P + 62) * 4 + min(lane, 4 * P - 1), last * 4 + 3) * 4u;
+                l = in_lds + FBD * 4;
+                lds_dma_dword_sys<0>(reinterpret_cast<const float*>(fD + fi), o, l, 0u);
+                o = (uint32_t)min((k * P + 62) * 2 + min(lane, 2 * P - 1), last * 2 + 1) * 4u;
+                l = in_lds + FBE * 4;
+                lds_dma_dword_sys<0>(reinterpret_cast<const float*>(fE + fi), o, l, 0u);
             }
         };
 
@@ -377,6 +489,7 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                              "v"(XI[P]), "v"(XI[P + 1]), "v"(XD[P]), "v"(XD[P + 1]));
         }
         wave_lds_sync();
+        if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
         issue_chunk(0);
         // pending successor flows (beta b*, channel g*): from (i, j+1) to M and D; from
         // (i+1, j) to M and I; from (i+1, j+1) to M, I, D (this step and the next)
@@ -387,8 +500,15 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
 
         for (int k = 0; k < nch; ++k) {
             const int t_hi = nsteps - 1 - k * P;
-            chunk_waits<P>(prog, q, NS, k, nch, R, st);
+            chunk_waits<P>(prog, q, NL, k, nch, R, st);
+            // this chunk's loads, followed by at least the P output stores of the
+            // previous chunk (none when accumulating a dot product)
             if (k == 0 || DOT) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (x_in && k > 0) {
+                // its progress word, loaded one chunk ago before those stores
+                const int got = flag_chunks_lds(fslot, epoch);
+                seen = got > seen ? got : seen;
+            }
             float sv[P], vv[P];
 #pragma unroll
             for (int u = 0; u < P; ++u) {
@@ -423,13 +543,28 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             float2 qE = make_float2(0, 0);
             if (below && lane >= 64 - P) {
                 const int j = 63 - lane;
-                qU = inU[ring_index(k * P + j + 63, R)];
-                const int id = ring_index(k * P + j + 62, R);
-                qD = inD[id];
-                qE = inE[id];
+                if (x_in) {
+                    qU = make_float4(buf[FBU + 4 * j], buf[FBU + 4 * j + 1], buf[FBU + 4 * j + 2],
+                                     buf[FBU + 4 * j + 3]);
+                    qD = make_float4(buf[FBD + 4 * j], buf[FBD + 4 * j + 1], buf[FBD + 4 * j + 2],
+                                     buf[FBD + 4 * j + 3]);
+                    qE = make_float2(buf[FBE + 2 * j], buf[FBE + 2 * j + 1]);
+                } else {
+                    qU = inU[ring_index(k * P + j + 63, R)];
+                    const int id = ring_index(k * P + j + 62, R);
+                    qD = inD[id];
+                    qE = inE[id];
+                }
             }
             wave_lds_sync();
-            if (k + 1 < nch) issue_chunk(k + 1);
+            if (k + 1 < nch) {
+                if (x_in) {
+                    const int need = min(k + 1 + lead(P), nch);
+                    if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                }
+                issue_chunk(k + 1);
+                if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
+            }
             const int slot0 = ring_index(k * P, R);
             {
                 const float a0 = lane_bcast(qU.x, 63), a1 = lane_bcast(qU.y, 63);
@@ -599,6 +734,25 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             wave_lds_sync();
             if (!DOT) write_tile<P, -1>(otile, obase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             publish(prog, wave, q * PROG_STRIDE + k + 1);
+            if (x_out) {
+                // this chunk's flows to the part above, by producer step
+                if (lane < P) {
+                    const int sl = slot0 + lane;
+                    store_sys4(fU + fo + k * P + lane, outU[sl]);
+                    store_sys4(fD + fo + k * P + lane, outD[sl]);
+                    store_sys2(fE + fo + k * P + lane, outE[sl]);
+                }
+                if (k >= 2) {
+                    // at least P + 3P/2 + 6 loads, 6 flow stores and (DOT: none, else 2P)
+                    // output stores follow the flow stores of chunk k - 2: complete
+                    wait_vmcnt<(DOT ? P + 3 * P / 2 + 12 : 3 * P + 3 * P / 2 + 12)>();
+                    if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
+                }
+            }
+        }
+        if (x_out) {
+            wait_vmcnt<0>();
+            if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
         }
     }
 
@@ -609,7 +763,8 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
         if (threadIdx.x == 0) {
             float t = 0.0f;
             for (int w = 0; w < NW; ++w) t += red[w];
-            dot[b] = t;
+            if (G == 1) dot[b] = t;
+            else spart[(size_t)b * G + part] = t;
         }
     }
 }
@@ -620,19 +775,25 @@ constexpr size_t kLdsLimit = 160 * 1024 - 256;
 constexpr int PT = 8;   // tangent sweep chunk
 constexpr int PD = 4;   // reverse sweep chunk
 
-size_t lds_tangent(bool has_v, int L1, int L2) {
-    const int R = ring_len(L1, L2, 256);
-    const int buf = 65 * PT * (has_v ? 2 : 1) + 3 * PT * 64 + 3 * 64;
+// LDS of one workgroup whose stripe boundaries use rings of R columns
+size_t lds_tangent_r(bool has_v, int R) {
+    const int buf = 65 * PT * (has_v ? 2 : 1) + 3 * PT * 64 + 3 * 64 + 3 * 64 + 64;
     return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + PT)) * sizeof(float4);
 }
+size_t lds_tangent(bool has_v, int L1, int L2) { return lds_tangent_r(has_v, ring_len(L1, L2, 256)); }
 
-size_t lds_dual(bool has_v, bool dot, int L1, int L2) {
-    const int R = ring_len(L1, L2, 128);
-    const int buf = 65 * PD * (has_v ? 2 : 1) + 6 * PD * 64 + 6 * 64 + (dot ? 0 : 65 * PD);
+size_t lds_dual_r(bool has_v, bool dot, int R) {
+    const int buf = 65 * PD * (has_v ? 2 : 1) + 6 * PD * 64 + 6 * 64 + (dot ? 0 : 65 * PD) + 4 * 64;
     return (size_t)NW * buf * sizeof(float) +
            (size_t)NW * R * (2 * sizeof(float4) + sizeof(float2));
 }
+size_t lds_dual(bool has_v, bool dot, int L1, int L2) {
+    return lds_dual_r(has_v, dot, ring_len(L1, L2, 128));
+}
 
+// Workspace after the primal layout: tangent tables + last rows, [B] scalars, then for
+// split elements the parts' partial sums and the reverse sweep's boundary flows by
+// step (up and diagonal (beta, g) pairs to M and I, float4 each; diagonal pair to D).
 struct Second {
     Layout prim;
     float* tan_sk;
@@ -640,6 +801,10 @@ struct Second {
     float* sdot;
     float* part;
     float* dS[3];   // dS/dopen, dS/dext, dS/dT
+    float* spart;   // [B][stripe]
+    float4* fU;     // [B][stripe][step]
+    float4* fD;
+    float2* fE;
     size_t bytes;
 };
 
@@ -657,6 +822,16 @@ Second second_layout(void* ws, int B, int L1, int L2) {
     w.dS[1] = w.dS[0] + B;
     w.dS[2] = w.dS[1] + B;
     p += round256((size_t)5 * B * sizeof(float));
+    const size_t parts = (size_t)B * (ns > 0 ? ns : 1);
+    const size_t slots = parts * (size_t)stored_steps(L2);
+    w.spart = (float*)p;
+    p += round256(parts * sizeof(float));
+    w.fU = (float4*)p;
+    p += round256(slots * sizeof(float4));
+    w.fD = (float4*)p;
+    p += round256(slots * sizeof(float4));
+    w.fE = (float2*)p;
+    p += round256(slots * sizeof(float2));
     w.bytes = (size_t)(p - (char*)ws);
     return w;
 }
@@ -665,15 +840,21 @@ template <int MODE>
 int launch_tangent(const float* scores, const float* V, const int* lengths, int B, int L1, int L2,
                    float go, float ge, float T, const Second& w, float* sdot, hipStream_t st) {
     const int ns = (L1 + 63) / 64;
-    const int R = ring_len(L1, L2, 256);
-    const size_t lds = lds_tangent(MODE == HVP, L1, L2);
+    constexpr bool has_v = MODE == HVP;
+    // rings of an unsplit element that do not fit: parts of at most NW stripes
+    const Split sp = choose_split(B, L1, w.prim, lds_tangent(has_v, L1, L2) <= kLdsLimit ? 0 : NW);
+    const int R = ring_len(sp.G > 1 ? sp.SPW * 64 : L1, L2, 256);
+    const size_t lds = lds_tangent_r(has_v, R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     auto kern = swa_tangent_kernel<MODE, PT>;
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
-    D2P_LAUNCH("swa_tangent", kern, dim3(B), dim3(NW * 64), lds, st, scores, V, lengths,
-               w.prim.alpha_sk, w.prim.brow, w.part, w.tan_sk, w.tan_brow, sdot, w.prim.status,
-               L1, L2, ns, go, ge, T, R);
+    D2P_LAUNCH("swa_tangent", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
+               lengths, w.prim.alpha_sk, w.prim.brow, w.part, w.tan_sk, w.tan_brow, sdot,
+               w.prim.status, w.prim.fflag, w.spart, B, L1, L2, ns, go, ge, T, R, sp.G, sp.SPW,
+               next_epoch());
+    if (MODE == HVP && sp.G > 1 && launch_sum_parts(w.spart, sdot, B, sp.G, st) != D2P_OK)
+        return D2P_ERR_HIP;
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -683,15 +864,21 @@ int launch_dual(const float* scores, const float* V, const int* lengths, int B, 
                 float go, float ge, float T, const Second& w, const float* dS, float* out,
                 float* dot, hipStream_t st) {
     const int ns = (L1 + 63) / 64;
-    const int R = ring_len(L1, L2, 128);
-    const size_t lds = lds_dual(MODE == HVP || DOT, DOT, L1, L2);
+    constexpr bool has_v = MODE == HVP || DOT;
+    const Split sp =
+        choose_split(B, L1, w.prim, lds_dual(has_v, DOT, L1, L2) <= kLdsLimit ? 0 : NW);
+    const int R = ring_len(sp.G > 1 ? sp.SPW * 64 : L1, L2, 128);
+    const size_t lds = lds_dual_r(has_v, DOT, R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     auto kern = swa_dual_kernel<MODE, PD, DOT>;
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
-    D2P_LAUNCH("swa_dual", kern, dim3(B), dim3(NW * 64), lds, st, scores, V, lengths,
-               w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, w.part, dS, out, dot,
-               w.prim.status, w.prim.trash, L1, L2, ns, go, ge, T, R);
+    D2P_LAUNCH("swa_dual", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
+               lengths, w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, w.part, dS, out, dot,
+               w.prim.status, w.prim.trash, w.prim.bflag, w.fU, w.fD, w.fE, w.spart, B, L1, L2,
+               ns, go, ge, T, R, sp.G, sp.SPW, next_epoch());
+    if (DOT && sp.G > 1 && launch_sum_parts(w.spart, dot, B, sp.G, st) != D2P_OK)
+        return D2P_ERR_HIP;
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -707,13 +894,8 @@ int param_pass(const float* scores, const float* ga, const int* lengths, int B, 
                                   out, dot, st);
 }
 
-int check(int B, int L1, int L2, float T) {
-    const int rc = swa::check_shape(B, L1, L2, T);
-    if (rc != D2P_OK) return rc;
-    D2P_REQUIRE(lds_tangent(true, L1, L2) <= kLdsLimit && lds_dual(true, false, L1, L2) <= kLdsLimit,
-                "sequence too long for the LDS stripe rings");
-    return D2P_OK;
-}
+// rings that do not fit for an unsplit element force parts of at most NW stripes
+int check(int B, int L1, int L2, float T) { return swa::check_shape(B, L1, L2, T); }
 
 }  // namespace swa2
 }  // namespace d2p_amd

@@ -142,6 +142,8 @@ int launch_split_reset(const Layout& ws, int B, int G, hipStream_t st);
 // (0, 0), whose value is 0.
 int launch_partition_merge(const Layout& ws, float* partition, int B, int G, float T,
                            hipStream_t st);
+// out[b] = sum of the G parts' partial results spart[b][part].
+int launch_sum_parts(const float* spart, float* out, int B, int G, hipStream_t st);
 
 // Issue priority of a wave by its stripe's place in the pipeline: every stripe
 // waits on the one before it, so the upstream stripes set the pace and are served

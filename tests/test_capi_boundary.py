@@ -143,13 +143,14 @@ def test_second_order_validation(lib):
     rc = lib.d2p_swa_backward_full(FAKE, FAKE, FAKE, 2, 10, 10, -2.0, -0.5, 1.0, FAKE, FAKE,
                                    FAKE, FAKE, FAKE, ctypes.c_size_t(8), None)
     assert rc == D2P_ERR_ARG and "workspace" in _err(lib)
-    # more stripes than waves: without split parts (the affine second-order sweeps)
-    # the stripe rings must hold a row's worth of steps
-    rc = lib.d2p_swa_hvp(FAKE, FAKE, FAKE, 1, 1024, 200000, -2.0, -0.5, 1.0, FAKE, FAKE, z, None)
-    assert rc == D2P_ERR_ARG and "LDS" in _err(lib)
-    # the linear-gap sweeps split such elements instead; the workspace check still
-    # runs before any device work
+    # more stripes than waves and rows too long for unsplit stripe rings: every sweep
+    # splits such elements into parts instead of refusing them; the workspace check
+    # still runs before any device work
     rc = lib.d2p_sw_hvp(FAKE, FAKE, FAKE, 1, 1024, 200000, -1.0, 1.0, FAKE, FAKE, z, None)
+    assert rc == D2P_ERR_ARG and "workspace" in _err(lib)
+    rc = lib.d2p_swa_hvp(FAKE, FAKE, FAKE, 1, 1024, 200000, -2.0, -0.5, 1.0, FAKE, FAKE, z, None)
+    assert rc == D2P_ERR_ARG and "workspace" in _err(lib)
+    rc = lib.d2p_dtw_hvp(FAKE, FAKE, FAKE, 1, 1024, 200000, 1.0, -1, FAKE, FAKE, z, None)
     assert rc == D2P_ERR_ARG and "workspace" in _err(lib)
 
 

@@ -177,15 +177,63 @@ def test_affine_split_ragged(cuda, parts):
     _check_affine(gpu, ref, s.numpy(), -11.0, -1.0, 0.5, lens.tolist())
 
 
-def test_affine_split_hvp(cuda, parts):
-    """The affine second-order entry points run split primal sweeps."""
+@pytest.mark.parametrize("n", [2, 3, 11])
+def test_affine_split_hvp(cuda, parts, n):
+    """Primal, tangent and two-channel reverse sweeps of the affine HVP all split."""
     from test_gpu_sw_affine_second import _close as _close_affine
-    parts(3)
-    s = _seeded(48, (2, 600, 70))
-    v = _seeded(49, (2, 600, 70))
+    parts(n)
+    s = _seeded(48, (2, 700, 90))
+    v = _seeded(49, (2, 700, 90))
     ref = O.get("oracle").soft_sw_affine_hvp(s.numpy(), v.numpy(), -2.0, -0.5, 1.0)
     _close_affine(_capi.swa_hvp(s.to(cuda), v.to(cuda), None, -2.0, -0.5, 1.0), ref,
-                  "affine hvp, split primal sweeps")
+                  f"affine hvp, {n} parts")
+
+
+def test_affine_split_hvp_ragged(cuda, parts):
+    from test_gpu_sw_affine_second import _close as _close_affine
+    parts(4)
+    B, L1, L2 = 5, 700, 110
+    s = _seeded(70, (B, L1, L2))
+    v = _seeded(71, (B, L1, L2))
+    lens = np.array([[700, 110], [0, 40], [193, 0], [1, 1], [257, 81]], np.int32)
+    ref = O.get("oracle").soft_sw_affine_hvp(s.numpy(), v.numpy(), -2.0, -0.5, 0.7, lens)
+    got = _capi.swa_hvp(s.to(cuda), v.to(cuda), torch.from_numpy(lens).to(cuda), -2.0, -0.5,
+                        0.7)
+    _close_affine(got, ref, "affine hvp ragged, 4 parts")
+
+
+@pytest.mark.parametrize("n", [2, 4])
+def test_affine_split_param_jacobian(cuda, parts, n):
+    from test_gpu_sw_affine_second import _close as _close_affine
+    from test_gpu_sw_affine_second import _jacobian_ref as _jacobian_affine
+    parts(n)
+    s = _seeded(72, (2, 500, 80))
+    k = O.get("oracle")
+    for p in (0, 1, 2):
+        ref, allow = _jacobian_affine(k, s.numpy(), p, -2.0, -0.5, 1.0)
+        _close_affine(_capi.swa_param_jacobian(s.to(cuda), p, None, -2.0, -0.5, 1.0), ref,
+                      f"affine dP/d{('open', 'ext', 'T')[p]}, {n} parts", allow)
+
+
+def test_affine_split_backward_full(cuda, parts):
+    """The affine dot-product reverse sweeps sum their parts."""
+    from test_gpu_sw_affine_second import _close as _close_affine
+    from test_gpu_sw_affine_second import _jacobian_ref as _jacobian_affine
+    parts(3)
+    B, L1, L2 = 2, 450, 96
+    go, ge, T = -2.0, -0.5, 1.0
+    s = _seeded(73, (B, L1, L2))
+    ga = _seeded(74, (B, L1, L2))
+    k = O.get("oracle")
+    gs, *gp = _capi.swa_backward_full(s.to(cuda), ga.to(cuda), None, go, ge, T)
+    _close_affine(gs, k.soft_sw_affine_hvp(s.numpy(), ga.numpy(), go, ge, T),
+                  "affine backward_full scores")
+    for p, g in enumerate(gp):
+        J, allow = _jacobian_affine(k, s.numpy(), p, go, ge, T)
+        ref = (J.astype(np.float64) * ga.numpy()).sum(axis=(1, 2))
+        per = 1e-4 * max(1.0, np.abs(J).max()) + allow
+        tol = per * np.abs(ga.numpy()).sum(axis=(1, 2))
+        assert np.all(np.abs(g.cpu().numpy() - ref) <= tol), (p, g.cpu().numpy(), ref, tol)
 
 
 # ---------------------------------------------------------------- soft-DTW
@@ -226,6 +274,66 @@ def test_dtw_split_ragged(cuda, parts):
         gpu = _capi.dtw_forward_marginals(c.to(cuda), lens.to(cuda), 0.7, bw)
         torch.cuda.synchronize()
         _check_dtw(gpu, ref, c.numpy(), 0.7, bw, lens.tolist())
+
+
+@pytest.mark.parametrize("n,bw", [(2, -1), (3, 40), (11, -1)])
+def test_dtw_split_hvp(cuda, parts, n, bw):
+    """Primal, tangent and two-channel reverse sweeps of the soft-DTW HVP all split."""
+    from test_gpu_dtw_second import _close as _close_dtw
+    parts(n)
+    c = _seeded(75, (2, 700, 90)).abs()
+    v = _seeded(76, (2, 700, 90))
+    ref = O.get("oracle").soft_dtw_hvp(c.numpy(), v.numpy(), 0.8, None, bw)
+    _close_dtw(_capi.dtw_hvp(c.to(cuda), v.to(cuda), None, 0.8, bw), ref,
+               f"dtw hvp, {n} parts, band {bw}")
+
+
+def test_dtw_split_second_ragged(cuda, parts):
+    from test_gpu_dtw_second import _close as _close_dtw, _jac_allow
+    parts(4)
+    B, L1, L2 = 5, 700, 110
+    c = _seeded(77, (B, L1, L2)).abs()
+    v = _seeded(78, (B, L1, L2))
+    lens = np.array([[700, 110], [0, 40], [193, 0], [1, 1], [257, 81]], np.int32)
+    lt = torch.from_numpy(lens).to(cuda)
+    k = O.get("oracle")
+    for bw in (-1, 30):
+        _close_dtw(_capi.dtw_hvp(c.to(cuda), v.to(cuda), lt, 0.7, bw),
+                   k.soft_dtw_hvp(c.numpy(), v.numpy(), 0.7, lens, bw),
+                   f"dtw hvp ragged, 4 parts, band {bw}")
+        _close_dtw(_capi.dtw_param_jacobian(c.to(cuda), lt, 0.7, bw),
+                   k.soft_dtw_param_jacobian(c.numpy(), 0.7, lens, bw),
+                   f"dtw jacobian ragged, 4 parts, band {bw}",
+                   _jac_allow(k, c.numpy(), 0.7, lens, bw))
+
+
+@pytest.mark.parametrize("n", [2, 4])
+def test_dtw_split_param_jacobian(cuda, parts, n):
+    from test_gpu_dtw_second import _close as _close_dtw, _jac_allow
+    parts(n)
+    c = _seeded(79, (2, 500, 80)).abs()
+    k = O.get("oracle")
+    _close_dtw(_capi.dtw_param_jacobian(c.to(cuda), None, 1.0, -1),
+               k.soft_dtw_param_jacobian(c.numpy(), 1.0, None, -1), f"dtw dP/dT, {n} parts",
+               _jac_allow(k, c.numpy(), 1.0))
+
+
+def test_dtw_split_backward_full(cuda, parts):
+    """The soft-DTW dot-product reverse sweep (<W, dP/dT>) sums its parts."""
+    from test_gpu_dtw_second import _close as _close_dtw, _jac_allow
+    parts(3)
+    B, L1, L2 = 2, 450, 96
+    c = _seeded(80, (B, L1, L2)).abs()
+    W = _seeded(81, (B, L1, L2))
+    k = O.get("oracle")
+    gc, gt = _capi.dtw_backward_full(c.to(cuda), W.to(cuda), None, 0.8)
+    _close_dtw(gc, k.soft_dtw_hvp(c.numpy(), W.numpy(), 0.8), "dtw backward_full costs")
+    J = k.soft_dtw_param_jacobian(c.numpy(), 0.8)
+    ref = (J.astype(np.float64) * W.numpy()).sum(axis=(1, 2))
+    per = 1e-4 * max(1.0, np.abs(J).max()) + _jac_allow(k, c.numpy(), 0.8)
+    tol = per * np.abs(W.numpy()).sum(axis=(1, 2))
+    got = gt.cpu().numpy()
+    assert np.all(np.abs(got - ref) <= tol), (got, ref, tol)
 
 
 # ------------------------------------------------- rows too long for unsplit rings
@@ -269,3 +377,22 @@ def test_dtw_long_rows_force_parts(cuda, parts):
     gpu = _capi.dtw_forward_marginals(c.to(cuda), None, 1.0, -1)
     torch.cuda.synchronize()
     _check_dtw(gpu, ref, c.numpy(), 1.0, -1)
+
+
+def test_affine_hvp_long_rows_force_parts(cuda, parts):
+    from test_gpu_sw_affine_second import _close as _close_affine
+    parts(1)
+    s = _seeded(65, (1, 600, 3000))
+    v = _seeded(66, (1, 600, 3000))
+    ref = O.get("oracle").soft_sw_affine_hvp(s.numpy(), v.numpy(), -2.0, -0.5, 1.0)
+    _close_affine(_capi.swa_hvp(s.to(cuda), v.to(cuda), None, -2.0, -0.5, 1.0), ref,
+                  "affine hvp, 600 x 3000")
+
+
+def test_dtw_hvp_long_rows_force_parts(cuda, parts):
+    from test_gpu_dtw_second import _close as _close_dtw
+    parts(1)
+    c = _seeded(67, (1, 600, 6000)).abs()
+    v = _seeded(68, (1, 600, 6000))
+    ref = O.get("oracle").soft_dtw_hvp(c.numpy(), v.numpy(), 1.0, None, -1)
+    _close_dtw(_capi.dtw_hvp(c.to(cuda), v.to(cuda), None, 1.0, -1), ref, "dtw hvp, 600 x 6000")
