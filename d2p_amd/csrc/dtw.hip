@@ -31,25 +31,15 @@ namespace dtw {
 
 using namespace wf;
 
-constexpr int PF = 16;               // steps per chunk, forward sweep
 constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do not publish
-
-// i*L2/L1 of (1-based) row i in float, as the reference's band test computes it.
-__device__ __forceinline__ float band_centre(int i, int L1, int L2) {
-    return L1 > 0 ? (float)((long long)i * L2) / (float)L1 : 0.0f;
-}
-
-// Cell (row centre ej, 1-based column j) lies in the band (bandwidth < 0: no band).
-__device__ __forceinline__ bool in_band(float ej, int j, float bw) {
-    return bw < 0.0f || fabsf((float)j - ej) <= bw;
-}
 
 __global__ void __launch_bounds__(NW * 64)
 dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ lengths,
                    float* __restrict__ alpha_sk, float* __restrict__ brow,
                    float* __restrict__ value, int* __restrict__ status,
                    uint64_t* __restrict__ fflag, int B, int L1max, int L2max, int NSmax,
-                   float T, int bandwidth, int R, int G, int SPW, uint32_t epoch) {
+                   size_t elem_steps, float T, int bandwidth, int R, int G, int SPW,
+                   uint32_t epoch) {
     constexpr int P = PF;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
@@ -96,6 +86,11 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
     const bool has_next = s_begin + NL < NS;
     const uint64_t* flag_in = fflag + (size_t)b * G + (part > 0 ? part - 1 : 0);
     uint64_t* flag_out = fflag + (size_t)b * G + part;
+    const int stride = band_stride(L1, L2, bw, (int)NT);   // table steps per stripe
+    if ((size_t)NS * stride > elem_steps) {   // never: the host reserves enough
+        if (threadIdx.x == 0) atomicOr(st, 2);
+        return;
+    }
 
     for (int l = wave; l < NL; l += NW) {
         const int s = s_begin + l;
@@ -105,15 +100,42 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
         const bool last_row = i0 + lane == L1 - 1;
         const float* ring_in = ring_from(rings, l, R);
         float* ring_out = ring_of(rings, l, R);
-        float* out = alpha_sk + (((size_t)b * NSmax + s) * NT + APAD) * 64;
+        // the chunks [k_lo, k_end) of the stripe's band window (all without a band),
+        // and the steps [up_lo, up_end) the stripe above computed
+        int t_lo, t_hi;
+        band_window(s, L1, L2, bw, t_lo, t_hi);
+        const int k_lo = __builtin_amdgcn_readfirstlane(t_lo <= t_hi ? min(t_lo / P, nch) : nch);
+        const int k_end = __builtin_amdgcn_readfirstlane(t_lo <= t_hi ? t_hi / P + 1 : nch);
+        int up_lo = 0, up_end = 0;
+        if (s > 0) {
+            band_window(s - 1, L1, L2, bw, t_lo, t_hi);
+            up_lo = t_lo <= t_hi ? (t_lo / P) * P : nch * P;
+            up_end = t_lo <= t_hi ? (t_hi / P + 1) * P : nch * P;
+        }
+        float* out = band_stripe(alpha_sk, b, elem_steps, s, stride, k_lo) + APAD * 64;
         float* brow_s = brow + ((size_t)b * NSmax + s) * NT;   // last row, by step
         const float* brow_up = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
         const bool x_in = l == 0 && part > 0;        // row above from the previous part
         const bool x_out = l == NL - 1 && has_next;  // last row feeds the next part
         int seen = -1;       // chunks of the previous part known to be complete
-        // steps t < 0 hold the column-0 boundary (PINF), read by the reverse sweep
+        // the APAD steps before the window hold the column-0 / off-band boundary
+        // (PINF), read by the reverse sweep; so does the chunk after it
 #pragma unroll
-        for (int t = -APAD; t < 0; ++t) lane_store(out + t * 64, ul4, kPINF);
+        for (int t = -APAD; t < 0; ++t) lane_store(out + (k_lo * P + t) * 64, ul4, kPINF);
+        if (k_end < nch) {
+#pragma unroll
+            for (int t = 0; t < P; ++t) lane_store(out + (k_end * P + t) * 64, ul4, kPINF);
+        }
+        // the last row outside the window is PINF
+        for (int t = lane; t < k_lo * P; t += 64) {
+            if (x_out) store_sys(brow_s + t, kPINF);
+            else brow_s[t] = kPINF;
+        }
+        for (int t = k_end * P + lane; t < nch * P; t += 64) {
+            if (x_out) store_sys(brow_s + t, kPINF);
+            else brow_s[t] = kPINF;
+        }
+        publish(prog, wave, l * PROG_STRIDE + k_lo);   // nothing to do before the window
         wave_lds_sync();   // the previous stripe's tile reads are complete
         const uint32_t tile_lds = lds_address(tiles);
         const uint32_t row_lds = lds_address(rbufs);
@@ -123,21 +145,25 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
             uint32_t dst = row_lds + (uint32_t)((k & 1) * 64 * 4);
             lds_dma_dword_sys<0>(brow_up, off, dst, 0u);
         };
-        if (x_in) {
-            seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
-            issue_row(0);
+        if (k_lo < k_end) {
+            if (x_in) {
+                seen = wait_part(flag_in, epoch, min(k_lo + lead(P), nch), st);
+                issue_row(k_lo);
+            }
+            dma_tile<P, 1>(tile_lds + (k_lo & 1) * Tile::FLOATS * 4, cbase, i0, L1max, L2max,
+                           lane, k_lo * P);
         }
-        dma_tile<P, 1>(tile_lds, cbase, i0, L1max, L2max, lane, 0);
-        // lane 0 of the first stripe sees alpha[0,0] = 0 as its first diagonal
-        float cur = kPINF, up_prev = (s == 0 && lane == 0) ? 0.0f : kPINF;
+        // lane 0 of the first stripe sees alpha[0,0] = 0 as its first diagonal (when
+        // its window starts at step 0)
+        float cur = kPINF, up_prev = (s == 0 && lane == 0 && k_lo == 0) ? 0.0f : kPINF;
 
-        for (int k = 0; k < nch; ++k) {
+        for (int k = k_lo; k < k_end; ++k) {
             const int t0 = k * P;
-            chunk_waits<P>(prog, l, NL, k, nch, R, st);
+            chunk_waits<P>(prog, l, NL, k, nch, R, st, k_lo);
             // this chunk's costs: loaded one chunk ago, followed by at least the P + 1
             // stores of that chunk (the first chunk's load is the last issued)
-            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
-            if (x_in && k > 0) {
+            if (k == k_lo) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (x_in && k > k_lo) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
@@ -146,11 +172,15 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
             float cv[P];
 #pragma unroll
             for (int u = 0; u < P; ++u) cv[u] = tile[tbase + u];
-            // lane 0's up values: column t0+j sits in lane j (row 0 is PINF)
+            // lane 0's up values: column t0+j sits in lane j (row 0 is PINF; so are the
+            // steps the stripe above did not compute, which lie off the band)
             float rreg = kPINF;
-            if (s > 0 && lane < P)
-                rreg = x_in ? rbufs[(k & 1) * 64 + lane] : ring_in[ring_index(t0 + lane + 63, R)];
-            if (k + 1 < nch) {
+            if (s > 0 && lane < P) {
+                const int tu = t0 + lane + 63;
+                if (x_in) rreg = rbufs[(k & 1) * 64 + lane];
+                else if (tu >= up_lo && tu < up_end) rreg = ring_in[ring_index(tu, R)];
+            }
+            if (k + 1 < k_end) {
                 if (x_in) {
                     const int need = min(k + 1 + lead(P), nch);
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
@@ -203,6 +233,7 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                 if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
             }
         }
+        publish(prog, wave, l * PROG_STRIDE + nch);   // nothing to do after the window
         if (x_out) {
             wait_vmcnt<0>();
             if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
@@ -224,8 +255,9 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
                     float* __restrict__ post, float* __restrict__ grad_T,
                     int* __restrict__ status, float* __restrict__ trash,
                     uint64_t* __restrict__ bflag, float2* __restrict__ flows,
-                    double* __restrict__ bpart, int B, int L1max, int L2max, int NSmax, float T,
-                    int bandwidth, int R, int G, int SPW, uint32_t epoch) {
+                    double* __restrict__ bpart, int B, int L1max, int L2max, int NSmax,
+                    size_t elem_steps, float T, int bandwidth, int R, int G, int SPW,
+                    uint32_t epoch) {
     extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red_g[NW];
@@ -281,6 +313,11 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
     const bool has_next = s_begin + NL < NS;
     const uint64_t* flag_in = bflag + (size_t)b * G + (part + 1 < G ? part + 1 : part);
     uint64_t* flag_out = bflag + (size_t)b * G + part;
+    const int stride = band_stride(L1, L2, bw, (int)NT);   // table steps per stripe
+    if ((size_t)NS * stride > elem_steps) {   // never: the host reserves enough
+        if (threadIdx.x == 0) atomicOr(st, 2);
+        return;
+    }
 
     // Stripes run bottom-up: order q = 0..NL-1 handles stripe s_begin+NL-1-q, on wave
     // q % NW.
@@ -291,7 +328,22 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
         const float ej = band_centre(i0 + lane + 1, L1, L2);
         // the terminal cell (L1, L2) starts with beta = 1
         const int term_step = (i0 + lane == L1 - 1) ? L2 - 1 + lane : -1000000;
-        const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * NT * 64;
+        // the stripe's band window as reverse chunks [k_lo, k_end) (chunk k covers steps
+        // nsteps-1-kP down to nsteps-kP-P), its table from forward chunk kf_lo, and the
+        // reverse slots [dn_lo, dn_end) the stripe below computed
+        int t_lo, t_hi;
+        band_window(s, L1, L2, bw, t_lo, t_hi);
+        const bool none = t_lo > t_hi;
+        const int k_lo = __builtin_amdgcn_readfirstlane(none ? nch : (nsteps - 1 - t_hi) / P);
+        const int k_end = __builtin_amdgcn_readfirstlane(none ? nch : (nsteps - 1 - t_lo) / P + 1);
+        const int kf_lo = __builtin_amdgcn_readfirstlane(none ? 0 : t_lo / PF);
+        int dn_lo = 0, dn_end = 0;
+        if (s + 1 < NS) {
+            band_window(s + 1, L1, L2, bw, t_lo, t_hi);
+            dn_lo = t_lo <= t_hi ? ((nsteps - 1 - t_hi) / P) * P : nch * P;
+            dn_end = t_lo <= t_hi ? ((nsteps - 1 - t_lo) / P + 1) * P : nch * P;
+        }
+        const float* astripe = band_stripe(alpha_sk, b, elem_steps, s, stride, kf_lo);
         const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
         const float2* ring_in = ring_from(rings, q, R);   // from stripe s+1
         float2* ring_out = ring_of(rings, q, R);          // to stripe s-1
@@ -322,21 +374,44 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
             }
         };
 
-        A[P] = lane_load(astripe + (size_t)(nsteps - 1 + APAD) * 64, ul4);
-        A[P + 1] = lane_load(astripe + (size_t)(nsteps - 2 + APAD) * 64, ul4);
+        if (bw >= 0.0f) {
+            // cells of the stripe's rows at steps outside the window: off the band, zero
+            const int a_end = nsteps - k_end * P;   // steps below are not swept
+            const int b_beg = nsteps - k_lo * P;    // nor are steps from here on
+            const int rows = min(64, L1 - i0);
+            for (int r = 0; r < rows; ++r) {
+                float* row = pbase + (size_t)(i0 + r) * L2max;
+                const int c1 = min(L2, a_end - r);
+                for (int cc = lane; cc < c1; cc += 64) row[cc] = 0.0f;
+                for (int cc = max(0, b_beg - r) + lane; cc < L2; cc += 64) row[cc] = 0.0f;
+            }
+        }
+        publish(prog, wave, q * PROG_STRIDE + k_lo);   // nothing to do before the window
+        if (k_lo == k_end) {
+            publish(prog, wave, q * PROG_STRIDE + nch);
+            if (x_out) {
+                if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
+            }
+            continue;
+        }
+        {
+            const int th0 = nsteps - 1 - k_lo * P;   // the window's first step
+            A[P] = lane_load(astripe + (size_t)(th0 + APAD) * 64, ul4);
+            A[P + 1] = lane_load(astripe + (size_t)(th0 - 1 + APAD) * 64, ul4);
+        }
         __asm__ volatile("" ::"v"(A[P]), "v"(A[P + 1]));   // completes the two loads here
         wave_lds_sync();   // the previous stripe's buffer reads are complete
-        if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
-        issue_chunk(0);
+        if (x_in) seen = wait_part(flag_in, epoch, min(k_lo + lead(P), nch), st);
+        issue_chunk(k_lo);
         float in_left = 0.0f, in_up = 0.0f, in_diag = 0.0f, in_diag_next = 0.0f;
 
-        for (int k = 0; k < nch; ++k) {
+        for (int k = k_lo; k < k_end; ++k) {
             const int t_hi = nsteps - 1 - k * P;
-            chunk_waits<P>(prog, q, NL, k, nch, R, st);
+            chunk_waits<P>(prog, q, NL, k, nch, R, st, k_lo);
             // this chunk's loads were issued one chunk ago and followed by at least the
             // P marginal stores of that chunk (the first chunk's are the last issued)
-            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
-            if (x_in && k > 0) {
+            if (k == k_lo) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (x_in && k > k_lo) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
@@ -355,16 +430,19 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
             bv = (s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1) ? bv : kPINF;
             float pre_u = 0.0f, pre_d = 0.0f;
             if (below && lane >= 64 - P) {
+                // slots the stripe below did not compute carry no flow (off the band)
                 const int j = 63 - lane;
+                const int su = k * P + j + 63, sd = su - 1;
+                const bool ou = su >= dn_lo && su < dn_end, od = sd >= dn_lo && sd < dn_end;
                 if (x_in) {
-                    pre_u = buf[FBUF + 2 * (j + 1)];
-                    pre_d = buf[FBUF + 2 * j + 1];
+                    pre_u = ou ? buf[FBUF + 2 * (j + 1)] : 0.0f;
+                    pre_d = od ? buf[FBUF + 2 * j + 1] : 0.0f;
                 } else {
-                    pre_u = ring_in[ring_index(k * P + j + 63, R)].x;
-                    pre_d = ring_in[ring_index(k * P + j + 62, R)].y;
+                    pre_u = ou ? ring_in[ring_index(su, R)].x : 0.0f;
+                    pre_d = od ? ring_in[ring_index(sd, R)].y : 0.0f;
                 }
             }
-            if (k + 1 < nch) {
+            if (k + 1 < k_end) {
                 if (x_in) {
                     const int need = min(k + 1 + lead(P), nch);
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
@@ -435,6 +513,7 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
                 }
             }
         }
+        publish(prog, wave, q * PROG_STRIDE + nch);   // nothing to do after the window
         if (x_out) {
             wait_vmcnt<0>();
             if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
@@ -508,8 +587,8 @@ int launch_backward_p(const float* costs, const int* lengths, int B, int max_L1,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     D2P_LAUNCH("dtw_backward", dtw_backward_kernel<P>, dim3(split_grid(B, sp.G)), dim3(NW * 64),
                lds, st, costs, lengths, ws.alpha_sk, ws.brow, marginals, grad_T, ws.status,
-               ws.trash, ws.bflag, ws.flows, ws.bpart, B, max_L1, max_L2, ns, T, bandwidth, R,
-               sp.G, sp.SPW, next_epoch());
+               ws.trash, ws.bflag, ws.flows, ws.bpart, B, max_L1, max_L2, ns, ws.elem_steps, T,
+               bandwidth, R, sp.G, sp.SPW, next_epoch());
     if (sp.G > 1)
         D2P_LAUNCH("dtw_grad_merge", dtw_grad_merge, dim3((B + 255) / 256), dim3(256), 0, st,
                    ws.bpart, grad_T, B, sp.G, T);
@@ -540,7 +619,7 @@ int launch_forward(const float* costs, const int* lengths, int B, int max_L1, in
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     D2P_LAUNCH("dtw_forward", dtw_forward_kernel, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds,
                st, costs, lengths, ws.alpha_sk, ws.brow, value, ws.status, ws.fflag, B, max_L1,
-               max_L2, ns, T, bandwidth, R, sp.G, sp.SPW, next_epoch());
+               max_L2, ns, ws.elem_steps, T, bandwidth, R, sp.G, sp.SPW, next_epoch());
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -563,11 +642,18 @@ int launch_backward(const float* costs, const int* lengths, int B, int max_L1, i
 
 using namespace d2p_amd;
 
-extern "C" size_t d2p_dtw_workspace_bytes(int B, int max_L1, int max_L2) {
+extern "C" size_t d2p_dtw_workspace_bytes_banded(int B, int max_L1, int max_L2, int bandwidth) {
     if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
-    // status words | trash line | skewed alpha table | last row of every stripe |
-    // split-element progress words, boundary flows and partial sums
-    return wf::layout(nullptr, B, max_L1, max_L2, 1, true).bytes;
+    // status words | trash line | skewed alpha table (banded: each stripe's window) |
+    // last row of every stripe | split-element progress words, boundary flows and
+    // partial sums
+    return wf::layout(nullptr, B, max_L1, max_L2, 1, true, 8,
+                      dtw::band_elem_steps(max_L1, max_L2, bandwidth))
+        .bytes;
+}
+
+extern "C" size_t d2p_dtw_workspace_bytes(int B, int max_L1, int max_L2) {
+    return d2p_dtw_workspace_bytes_banded(B, max_L1, max_L2, -1);
 }
 
 extern "C" int d2p_dtw_forward_marginals(const float* costs, const int* lengths, int B,
@@ -579,10 +665,11 @@ extern "C" int d2p_dtw_forward_marginals(const float* costs, const int* lengths,
     if (rc != D2P_OK) return rc;
     if (B == 0) return D2P_OK;
     D2P_REQUIRE(costs && lengths && value && marginals && grad_T, "null pointer argument");
-    const size_t need = d2p_dtw_workspace_bytes(B, max_L1, max_L2);
+    const size_t need = d2p_dtw_workspace_bytes_banded(B, max_L1, max_L2, bandwidth);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
-    const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 1, true);
+    const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 1, true, 8,
+                                     dtw::band_elem_steps(max_L1, max_L2, bandwidth));
     const int r = dtw::launch_forward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth,
                                       ws, value, st);
     if (r != D2P_OK) return r;

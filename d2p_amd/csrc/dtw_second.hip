@@ -32,12 +32,12 @@ using namespace wf;
 
 enum Mode { HVP = 0, TEMP = 1 };
 
-__device__ __forceinline__ float band_centre(int i, int L1, int L2) {
-    return L1 > 0 ? (float)((long long)i * L2) / (float)L1 : 0.0f;
-}
-__device__ __forceinline__ bool in_band(float ej, int j, float bw) {
-    return bw < 0.0f || fabsf((float)j - ej) <= bw;
-}
+using dtw::band_centre;
+using dtw::band_stride;
+using dtw::band_stripe;
+using dtw::band_window;
+using dtw::in_band;
+using dtw::PF;
 
 template <int MODE, int P>
 __global__ void __launch_bounds__(NW * 64)
@@ -45,8 +45,9 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
                    const float* __restrict__ alpha_sk, const float* __restrict__ brow,
                    float* __restrict__ tan_sk, float* __restrict__ tan_brow,
                    int* __restrict__ status, uint64_t* __restrict__ tflag, int B, int L1max,
-                   int L2max, int NSmax, float T, int bandwidth, int R, int G, int SPW,
-                   uint32_t epoch) {
+                   int L2max, int NSmax, size_t elem_steps, float T, int bandwidth, int R, int G,
+                   int SPW, uint32_t epoch) {
+    static_assert(P == PF, "the tangent table shares the primal table's chunks");
     using Tile = ChunkTile<P>;
     constexpr int AR = Tile::FLOATS;      // P alpha rows after the input tile
     constexpr int RR = AR + P * 64;       // row above
@@ -91,15 +92,32 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
     const bool has_next = s_begin + NL < NS;
     const uint64_t* flag_in = tflag + (size_t)b * G + (part > 0 ? part - 1 : 0);
     uint64_t* flag_out = tflag + (size_t)b * G + part;
+    const int stride = band_stride(L1, L2, bw, (int)NT);   // table steps per stripe
+    if ((size_t)NS * stride > elem_steps) {   // never: the host reserves enough
+        if (threadIdx.x == 0) atomicOr(st, 2);
+        return;
+    }
 
     for (int l = wave; l < NL; l += NW) {
         const int s = s_begin + l;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
         const float ej = band_centre(i0 + lane + 1, L1, L2);
-        const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * NT * 64;
+        // the chunks [k_lo, k_end) of the stripe's band window, and the steps
+        // [up_lo, up_end) the stripe above computed
+        int t_lo, t_hi;
+        band_window(s, L1, L2, bw, t_lo, t_hi);
+        const int k_lo = __builtin_amdgcn_readfirstlane(t_lo <= t_hi ? min(t_lo / P, nch) : nch);
+        const int k_end = __builtin_amdgcn_readfirstlane(t_lo <= t_hi ? t_hi / P + 1 : nch);
+        int up_lo = 0, up_end = 0;
+        if (s > 0) {
+            band_window(s - 1, L1, L2, bw, t_lo, t_hi);
+            up_lo = t_lo <= t_hi ? (t_lo / P) * P : nch * P;
+            up_end = t_lo <= t_hi ? (t_hi / P + 1) * P : nch * P;
+        }
+        const float* astripe = band_stripe(alpha_sk, b, elem_steps, s, stride, k_lo);
         const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
-        float* tout = tan_sk + (((size_t)b * NSmax + s) * NT + APAD) * 64;
+        float* tout = band_stripe(tan_sk, b, elem_steps, s, stride, k_lo) + APAD * 64;
         float* tb_s = tan_brow + ((size_t)b * NSmax + s) * NT;
         const float* tb_up = tan_brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
         const float* ring_in = ring_from(rings, l, R);
@@ -123,23 +141,41 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
             }
         };
 
+        // tangents of the APAD steps before the window and of the chunk after it: 0
+        // (column 0 and off the band)
 #pragma unroll
-        for (int t = -APAD; t < 0; ++t) lane_store(tout + t * 64, ul4, 0.0f);
+        for (int t = -APAD; t < 0; ++t) lane_store(tout + (k_lo * P + t) * 64, ul4, 0.0f);
+        if (k_end < nch) {
+#pragma unroll
+            for (int t = 0; t < P; ++t) lane_store(tout + (k_end * P + t) * 64, ul4, 0.0f);
+        }
+        // so are the last row's tangents outside the window
+        for (int t = lane; t < k_lo * P; t += 64) {
+            if (x_out) store_sys(tb_s + t, 0.0f);
+            else tb_s[t] = 0.0f;
+        }
+        for (int t = k_end * P + lane; t < nch * P; t += 64) {
+            if (x_out) store_sys(tb_s + t, 0.0f);
+            else tb_s[t] = 0.0f;
+        }
+        publish(prog, wave, l * PROG_STRIDE + k_lo);   // nothing to do before the window
         wave_lds_sync();
-        if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
-        issue_chunk(0);
+        if (k_lo < k_end) {
+            if (x_in) seen = wait_part(flag_in, epoch, min(k_lo + lead(P), nch), st);
+            issue_chunk(k_lo);
+        }
         float Aw[P + 2];
-        Aw[P] = kPINF;   // alpha at steps -2, -1: column-0 boundary
+        Aw[P] = kPINF;   // alpha at the two steps before the window: column 0 or off band
         Aw[P + 1] = kPINF;
         float cur = 0.0f, up_prev = 0.0f;
 
-        for (int k = 0; k < nch; ++k) {
+        for (int k = k_lo; k < k_end; ++k) {
             const int t0 = k * P;
-            chunk_waits<P>(prog, l, NL, k, nch, R, st);
+            chunk_waits<P>(prog, l, NL, k, nch, R, st, k_lo);
             // this chunk's loads, followed by at least the P + 1 stores of the previous
             // chunk
-            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
-            if (x_in && k > 0) {
+            if (k == k_lo) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (x_in && k > k_lo) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
@@ -153,11 +189,15 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
             for (int j = 0; j < P; ++j) Aw[j + 2] = buf[AR + j * 64 + lane];
             float bv = buf[RR + lane];
             bv = (s > 0 && lane <= P && t0 + 62 + lane <= nsteps - 1) ? bv : kPINF;
+            // tangents of the row above (0 at the steps the stripe above did not compute)
             float rreg = 0.0f;
-            if (s > 0 && lane < P)
-                rreg = x_in ? buf[TR + lane] : ring_in[ring_index(t0 + lane + 63, R)];
+            if (s > 0 && lane < P) {
+                const int tu = t0 + lane + 63;
+                if (x_in) rreg = buf[TR + lane];
+                else if (tu >= up_lo && tu < up_end) rreg = ring_in[ring_index(tu, R)];
+            }
             wave_lds_sync();
-            if (k + 1 < nch) {
+            if (k + 1 < k_end) {
                 if (x_in) {
                     const int need = min(k + 1 + lead(P), nch);
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
@@ -191,8 +231,16 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
                 if (MODE == HVP) {
                     x = iv[u] + wsum;
                 } else {
-                    const float ea = ((ed * dga + eu * upa) + el * a1) * rin;
-                    x = ((a0 - iv[u]) - ea) * rT + wsum;
+                    // softmin - E_w[alpha], both relative to the smallest predecessor m:
+                    // the alphas grow with the path length, and the weights' sum
+                    // differs from 1 by an ulp or two, so E_w[alpha] taken whole would
+                    // carry that ulp times |alpha| into every cell.  Without a finite
+                    // predecessor (cell (1,1), whose alpha[0,0] = 0 this sweep does not
+                    // read, and unreachable cells) the weights are 0 and the term is
+                    // alpha - cost, as in the reference.
+                    const float mp = m < kPINF ? m : 0.0f;
+                    const float ea = ((ed * (dga - mp) + eu * (upa - mp)) + el * (a1 - mp)) * rin;
+                    x = (((a0 - iv[u]) - mp) - ea) * rT + wsum;
                 }
                 cur = ok ? x : 0.0f;
                 lane_store(toutc + u * 64, ul4, cur);
@@ -212,6 +260,7 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
                 if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
             }
         }
+        publish(prog, wave, l * PROG_STRIDE + nch);   // nothing to do after the window
         if (x_out) {
             wait_vmcnt<0>();
             if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
@@ -228,8 +277,8 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
                 float* __restrict__ out, float* __restrict__ dot, int* __restrict__ status,
                 float* __restrict__ trash, uint64_t* __restrict__ dflag,
                 float4* __restrict__ flows4, float* __restrict__ spart, int B, int L1max,
-                int L2max, int NSmax, float T, int bandwidth, int R, int G, int SPW,
-                uint32_t epoch) {
+                int L2max, int NSmax, size_t elem_steps, float T, int bandwidth, int R, int G,
+                int SPW, uint32_t epoch) {
     using Tile = ChunkTile<P>;
     constexpr int AR = DOT ? Tile::FLOATS : 0;   // P alpha rows (after the V tile)
     constexpr int XR = AR + P * 64;
@@ -291,6 +340,11 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
     const bool has_next = s_begin + NL < NS;
     const uint64_t* flag_in = dflag + (size_t)b * G + (part + 1 < G ? part + 1 : part);
     uint64_t* flag_out = dflag + (size_t)b * G + part;
+    const int stride = band_stride(L1, L2, bw, (int)NT);   // table steps per stripe
+    if ((size_t)NS * stride > elem_steps) {   // never: the host reserves enough
+        if (threadIdx.x == 0) atomicOr(st, 2);
+        return;
+    }
 
     for (int q = wave; q < NL; q += NW) {
         const int s = s_begin + NL - 1 - q;
@@ -298,10 +352,24 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
         const float ej = band_centre(i0 + lane + 1, L1, L2);
         const int term_step = (i0 + lane == L1 - 1) ? L2 - 1 + lane : -1000000;
-        const size_t sb = ((size_t)b * NSmax + s) * NT;
+        // the stripe's band window as reverse chunks [k_lo, k_end), its tables from
+        // forward chunk kf_lo, and the reverse slots [dn_lo, dn_end) the stripe below
+        // computed
+        int t_lo, t_hi;
+        band_window(s, L1, L2, bw, t_lo, t_hi);
+        const bool none = t_lo > t_hi;
+        const int k_lo = __builtin_amdgcn_readfirstlane(none ? nch : (nsteps - 1 - t_hi) / P);
+        const int k_end = __builtin_amdgcn_readfirstlane(none ? nch : (nsteps - 1 - t_lo) / P + 1);
+        const int kf_lo = __builtin_amdgcn_readfirstlane(none ? 0 : t_lo / PF);
+        int dn_lo = 0, dn_end = 0;
+        if (s + 1 < NS) {
+            band_window(s + 1, L1, L2, bw, t_lo, t_hi);
+            dn_lo = t_lo <= t_hi ? ((nsteps - 1 - t_hi) / P) * P : nch * P;
+            dn_end = t_lo <= t_hi ? ((nsteps - 1 - t_lo) / P + 1) * P : nch * P;
+        }
         const size_t ub = ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
-        const float* astripe = alpha_sk + sb * 64;
-        const float* xstripe = tan_sk + sb * 64;
+        const float* astripe = band_stripe(alpha_sk, b, elem_steps, s, stride, kf_lo);
+        const float* xstripe = band_stripe(tan_sk, b, elem_steps, s, stride, kf_lo);
         const float* bup = brow + ub;
         const float* xup = tan_brow + ub;
         const float4* ring_in = ring_from(rings, q, R);
@@ -336,9 +404,30 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
             }
         };
 
+        if (!DOT && bw >= 0.0f) {
+            // cells of the stripe's rows at steps outside the window: off the band, zero
+            const int a_end = nsteps - k_end * P;   // steps below are not swept
+            const int b_beg = nsteps - k_lo * P;    // nor are steps from here on
+            const int rows = min(64, L1 - i0);
+            for (int r = 0; r < rows; ++r) {
+                float* row = obase + (size_t)(i0 + r) * L2max;
+                const int c1 = min(L2, a_end - r);
+                for (int cc = lane; cc < c1; cc += 64) row[cc] = 0.0f;
+                for (int cc = max(0, b_beg - r) + lane; cc < L2; cc += 64) row[cc] = 0.0f;
+            }
+        }
+        publish(prog, wave, q * PROG_STRIDE + k_lo);   // nothing to do before the window
+        if (k_lo == k_end) {
+            publish(prog, wave, q * PROG_STRIDE + nch);
+            if (x_out) {
+                if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
+            }
+            continue;
+        }
         {
-            const float* a0p = astripe + (size_t)(nsteps - 1 + APAD) * 64;
-            const float* x0p = xstripe + (size_t)(nsteps - 1 + APAD) * 64;
+            const int th0 = nsteps - 1 - k_lo * P;   // the window's first step
+            const float* a0p = astripe + (size_t)(th0 + APAD) * 64;
+            const float* x0p = xstripe + (size_t)(th0 + APAD) * 64;
             A[P] = lane_load(a0p, ul4);
             A[P + 1] = lane_load(a0p - 64, ul4);
             X[P] = lane_load(x0p, ul4);
@@ -346,18 +435,18 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
             __asm__ volatile("" ::"v"(A[P]), "v"(A[P + 1]), "v"(X[P]), "v"(X[P + 1]));
         }
         wave_lds_sync();
-        if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
-        issue_chunk(0);
+        if (x_in) seen = wait_part(flag_in, epoch, min(k_lo + lead(P), nch), st);
+        issue_chunk(k_lo);
         float lb = 0.0f, lg = 0.0f, ubt = 0.0f, ug = 0.0f;
         float db = 0.0f, dg = 0.0f, db2 = 0.0f, dg2 = 0.0f;
 
-        for (int k = 0; k < nch; ++k) {
+        for (int k = k_lo; k < k_end; ++k) {
             const int t_hi = nsteps - 1 - k * P;
-            chunk_waits<P>(prog, q, NL, k, nch, R, st);
+            chunk_waits<P>(prog, q, NL, k, nch, R, st, k_lo);
             // this chunk's loads, followed by at least the P output stores of the
             // previous chunk (none when accumulating a dot product)
-            if (k == 0 || DOT) wait_vmcnt<0>(); else wait_vmcnt<P>();
-            if (x_in && k > 0) {
+            if (k == k_lo || DOT) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (x_in && k > k_lo) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
@@ -379,24 +468,31 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
             float bX = row_ok ? buf[RX + lane] : 0.0f;
             float qub = 0.0f, qug = 0.0f, qdb = 0.0f, qdg = 0.0f;
             if (below && lane >= 64 - P) {
+                // slots the stripe below did not compute carry no flow (off the band)
                 const int j = 63 - lane;
+                const int su = k * P + j + 63, sd = su - 1;
+                const bool ou = su >= dn_lo && su < dn_end, od = sd >= dn_lo && sd < dn_end;
                 if (x_in) {
                     // .z, .w of slot kP+62+j and .x, .y of slot kP+63+j
-                    qdb = buf[FB + 4 * j];
-                    qdg = buf[FB + 4 * j + 1];
-                    qub = buf[FB + 4 * j + 2];
-                    qug = buf[FB + 4 * j + 3];
+                    qdb = od ? buf[FB + 4 * j] : 0.0f;
+                    qdg = od ? buf[FB + 4 * j + 1] : 0.0f;
+                    qub = ou ? buf[FB + 4 * j + 2] : 0.0f;
+                    qug = ou ? buf[FB + 4 * j + 3] : 0.0f;
                 } else {
-                    const float4 ru = ring_in[ring_index(k * P + j + 63, R)];
-                    const float4 rd = ring_in[ring_index(k * P + j + 62, R)];
-                    qub = ru.x;
-                    qug = ru.y;
-                    qdb = rd.z;
-                    qdg = rd.w;
+                    if (ou) {
+                        const float4 ru = ring_in[ring_index(su, R)];
+                        qub = ru.x;
+                        qug = ru.y;
+                    }
+                    if (od) {
+                        const float4 rd = ring_in[ring_index(sd, R)];
+                        qdb = rd.z;
+                        qdg = rd.w;
+                    }
                 }
             }
             wave_lds_sync();
-            if (k + 1 < nch) {
+            if (k + 1 < k_end) {
                 if (x_in) {
                     const int need = min(k + 1 + lead(P), nch);
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
@@ -433,15 +529,24 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
                 const float el = fast_exp2((m - a1) * c);
                 const float rin = m < kPINF ? fast_rcp((ed + eu) + el) : 0.0f;
                 const float wd = ed * rin, wu = eu * rin, wl = el * rin;
-                const float ex = (wd * dgx + wu * upx) + wl * x1;
-                float dwd = wd * (ex - dgx) * rT, dwu = wu * (ex - upx) * rT,
-                      dwl = wl * (ex - x1) * rT;
+                // E_w[x] - x_k and (for the temperature) alpha_k - E_w[alpha], with the
+                // means taken relative to the predecessor of the smallest alpha m (the
+                // largest weight; finite whenever any weight is not 0): the weights' sum
+                // differs from 1 by an ulp or two, which must not multiply tangents and
+                // alphas that grow with the path length.  Predecessors of weight 0 may
+                // carry any finite tangent; their products with the weight are 0.
+                const float xp = a1 <= m ? x1 : (upa <= m ? upx : dgx);
+                const float pdx = dgx - xp, pux = upx - xp, plx = x1 - xp;
+                const float ex = (wd * pdx + wu * pux) + wl * plx;   // E_w[x] - xp
+                float dwd = wd * (ex - pdx) * rT, dwu = wu * (ex - pux) * rT;
+                float dwl = wl * (ex - plx) * rT;
                 if (MODE == TEMP) {
-                    const float ea = (wd * dga + wu * upa) + wl * a1;
+                    const float pda = dga - m, pua = upa - m, pla = a1 - m;
+                    const float ea = (wd * pda + wu * pua) + wl * pla;   // E_w[alpha] - m
                     const float rT2 = rT * rT;
-                    dwd += wd * (dga - ea) * rT2;
-                    dwu += wu * (upa - ea) * rT2;
-                    dwl += wl * (a1 - ea) * rT2;
+                    dwd += wd * (pda - ea) * rT2;
+                    dwu += wu * (pua - ea) * rT2;
+                    dwl += wl * (pla - ea) * rT2;
                 }
                 // reference accumulation order: init, diagonal, left, up successor
                 const float binit = t == term_step ? 1.0f : 0.0f;
@@ -484,6 +589,7 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
                 }
             }
         }
+        publish(prog, wave, q * PROG_STRIDE + nch);   // nothing to do after the window
         if (x_out) {
             wait_vmcnt<0>();
             if (lane == 0) store_flag(flag_out, progress_word(epoch, nch));
@@ -544,14 +650,16 @@ struct Second {
     size_t bytes;
 };
 
-Second second_layout(void* ws, int B, int L1, int L2) {
+// bandwidth >= 0: banded primal and tangent tables (the windows of the band)
+Second second_layout(void* ws, int B, int L1, int L2, int bandwidth) {
     Second w;
-    w.prim = layout(ws, B, L1, L2, 1, true);
+    const size_t es = dtw::band_elem_steps(L1, L2, bandwidth);
+    w.prim = layout(ws, B, L1, L2, 1, true, 8, es);
     char* p = (char*)ws + round256(w.prim.bytes);
     const size_t ns = ((size_t)L1 + 63) / 64;
     w.tan_sk = (float*)p;
-    w.tan_brow = w.tan_sk + (size_t)B * ns * stored_steps(L2) * 64;
-    p += round256(table_floats(B, L1, L2) * sizeof(float));
+    w.tan_brow = w.tan_sk + (size_t)B * es * 64;
+    p += round256(table_floats(B, L1, L2, 1, es) * sizeof(float));
     w.value = (float*)p;
     w.scratch = w.value + B;
     p += round256((size_t)2 * B * sizeof(float));
@@ -578,7 +686,8 @@ int launch_tangent(const float* input, const int* lengths, int B, int L1, int L2
                                 (int)lds));
     D2P_LAUNCH("dtw_tangent", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, input,
                lengths, w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, w.prim.status,
-               w.prim.fflag, B, L1, L2, ns, T, bw, R, sp.G, sp.SPW, next_epoch());
+               w.prim.fflag, B, L1, L2, ns, w.prim.elem_steps, T, bw, R, sp.G, sp.SPW,
+               next_epoch());
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -601,8 +710,8 @@ int launch_dual(const float* V, const int* lengths, int B, int L1, int L2, float
                                 (int)lds));
     D2P_LAUNCH("dtw_dual", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, V, lengths,
                w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, out, dot, w.prim.status,
-               w.prim.trash, w.prim.bflag, w.flows4, w.spart, B, L1, L2, ns, T, bw, R, sp.G,
-               sp.SPW, next_epoch());
+               w.prim.trash, w.prim.bflag, w.flows4, w.spart, B, L1, L2, ns, w.prim.elem_steps,
+               T, bw, R, sp.G, sp.SPW, next_epoch());
     if (DOT && sp.G > 1 && launch_sum_parts(w.spart, dot, B, sp.G, st) != D2P_OK)
         return D2P_ERR_HIP;
     D2P_HIP(hipGetLastError());
@@ -623,9 +732,14 @@ using namespace d2p_amd;
         if (rc_ != D2P_OK) return rc_;  \
     } while (0)
 
-extern "C" size_t d2p_dtw_second_workspace_bytes(int B, int max_L1, int max_L2) {
+extern "C" size_t d2p_dtw_second_workspace_bytes_banded(int B, int max_L1, int max_L2,
+                                                         int bandwidth) {
     if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
-    return dtw2::second_layout(nullptr, B, max_L1, max_L2).bytes;
+    return dtw2::second_layout(nullptr, B, max_L1, max_L2, bandwidth).bytes;
+}
+
+extern "C" size_t d2p_dtw_second_workspace_bytes(int B, int max_L1, int max_L2) {
+    return d2p_dtw_second_workspace_bytes_banded(B, max_L1, max_L2, -1);
 }
 
 extern "C" int d2p_dtw_hvp(const float* costs, const float* tangent, const int* lengths, int B,
@@ -634,10 +748,12 @@ extern "C" int d2p_dtw_hvp(const float* costs, const float* tangent, const int* 
     D2P_TRY(dtw2::check(B, max_L1, max_L2, temperature));
     if (B == 0) return D2P_OK;
     D2P_REQUIRE(costs && tangent && lengths && hvp, "null pointer argument");
-    D2P_REQUIRE(workspace && workspace_bytes >= d2p_dtw_second_workspace_bytes(B, max_L1, max_L2),
+    D2P_REQUIRE(workspace && workspace_bytes >=
+                                 d2p_dtw_second_workspace_bytes_banded(B, max_L1, max_L2,
+                                                                       bandwidth),
                 "workspace too small");
     hipStream_t st = (hipStream_t)stream;
-    const dtw2::Second w = dtw2::second_layout(workspace, B, max_L1, max_L2);
+    const dtw2::Second w = dtw2::second_layout(workspace, B, max_L1, max_L2, bandwidth);
     D2P_TRY(dtw::launch_forward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth, w.prim,
                                 w.value, st));
     D2P_TRY(dtw2::launch_tangent<dtw2::HVP>(tangent, lengths, B, max_L1, max_L2, temperature,
@@ -653,10 +769,12 @@ extern "C" int d2p_dtw_param_jacobian(const float* costs, const int* lengths, in
     D2P_TRY(dtw2::check(B, max_L1, max_L2, temperature));
     if (B == 0) return D2P_OK;
     D2P_REQUIRE(costs && lengths && jacobian, "null pointer argument");
-    D2P_REQUIRE(workspace && workspace_bytes >= d2p_dtw_second_workspace_bytes(B, max_L1, max_L2),
+    D2P_REQUIRE(workspace && workspace_bytes >=
+                                 d2p_dtw_second_workspace_bytes_banded(B, max_L1, max_L2,
+                                                                       bandwidth),
                 "workspace too small");
     hipStream_t st = (hipStream_t)stream;
-    const dtw2::Second w = dtw2::second_layout(workspace, B, max_L1, max_L2);
+    const dtw2::Second w = dtw2::second_layout(workspace, B, max_L1, max_L2, bandwidth);
     D2P_TRY(dtw::launch_forward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth, w.prim,
                                 w.value, st));
     D2P_TRY(dtw2::launch_tangent<dtw2::TEMP>(costs, lengths, B, max_L1, max_L2, temperature,
@@ -674,10 +792,12 @@ extern "C" int d2p_dtw_backward_full(const float* costs, const float* grad_align
     if (B == 0) return D2P_OK;
     D2P_REQUIRE(costs && grad_alignment && lengths && grad_costs && grad_T,
                 "null pointer argument");
-    D2P_REQUIRE(workspace && workspace_bytes >= d2p_dtw_second_workspace_bytes(B, max_L1, max_L2),
+    D2P_REQUIRE(workspace && workspace_bytes >=
+                                 d2p_dtw_second_workspace_bytes_banded(B, max_L1, max_L2,
+                                                                       bandwidth),
                 "workspace too small");
     hipStream_t st = (hipStream_t)stream;
-    const dtw2::Second w = dtw2::second_layout(workspace, B, max_L1, max_L2);
+    const dtw2::Second w = dtw2::second_layout(workspace, B, max_L1, max_L2, bandwidth);
     D2P_TRY(dtw::launch_forward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth, w.prim,
                                 w.value, st));
     D2P_TRY(dtw2::launch_tangent<dtw2::HVP>(grad_alignment, lengths, B, max_L1, max_L2,

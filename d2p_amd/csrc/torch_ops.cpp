@@ -639,7 +639,7 @@ DtwOut dtw_run(const Tensor& costs, const Tensor& lengths, const Dims& d, float 
     auto opt = costs.options();
     DtwOut o{torch::empty({d.B}, opt), torch::empty({d.B, d.L1, d.L2}, opt),
              torch::empty({d.B}, opt)};
-    const size_t ws_bytes = d2p_dtw_workspace_bytes(d.B, d.L1, d.L2);
+    const size_t ws_bytes = d2p_dtw_workspace_bytes_banded(d.B, d.L1, d.L2, bw);
     Tensor ws = workspace(ws_bytes, costs);
     D2P_CALL(d2p_dtw_forward_marginals(
         costs.data_ptr<float>(), lengths.data_ptr<int>(), d.B, d.L1, d.L2, T, bw,
@@ -648,8 +648,8 @@ DtwOut dtw_run(const Tensor& costs, const Tensor& lengths, const Dims& d, float 
     return o;
 }
 
-Tensor dtw_second_workspace(const Dims& d, const Tensor& like) {
-    return workspace(d2p_dtw_second_workspace_bytes(d.B, d.L1, d.L2), like);
+Tensor dtw_second_workspace(const Dims& d, int bw, const Tensor& like) {
+    return workspace(d2p_dtw_second_workspace_bytes_banded(d.B, d.L1, d.L2, bw), like);
 }
 
 // (grad_costs = H . ga, per-element <ga, dP/dT>)
@@ -658,7 +658,7 @@ std::tuple<Tensor, Tensor> dtw_backward_full_run(const Tensor& costs, const Tens
                                                  int bw) {
     Tensor gc = torch::empty({d.B, d.L1, d.L2}, costs.options());
     Tensor gt = torch::empty({d.B}, costs.options());
-    Tensor ws = dtw_second_workspace(d, costs);
+    Tensor ws = dtw_second_workspace(d, bw, costs);
     D2P_CALL(d2p_dtw_backward_full(costs.data_ptr<float>(), ga.data_ptr<float>(),
                                    lengths.data_ptr<int>(), d.B, d.L1, d.L2, T, bw,
                                    gc.data_ptr<float>(), gt.data_ptr<float>(), ws.data_ptr(),
@@ -751,7 +751,7 @@ Tensor dtw_hvp(Tensor costs, Tensor tangent, double temperature, c10::optional<T
     Tensor l = resolve_lengths(lengths, d, costs.device(), "costs");
     const int bw = checked_bandwidth(bandwidth.has_value() ? *bandwidth : -1);
     Tensor out = torch::empty({d.B, d.L1, d.L2}, costs.options());
-    Tensor ws = dtw_second_workspace(d, costs);
+    Tensor ws = dtw_second_workspace(d, bw, costs);
     D2P_CALL(d2p_dtw_hvp(costs.data_ptr<float>(), tangent.data_ptr<float>(), l.data_ptr<int>(),
                          d.B, d.L1, d.L2, (float)temperature, bw, out.data_ptr<float>(),
                          ws.data_ptr(), ws.numel(), current_stream()));
@@ -766,7 +766,7 @@ Tensor dtw_param_jacobian(Tensor costs, double temperature, c10::optional<Tensor
     Tensor l = resolve_lengths(lengths, d, costs.device(), "costs");
     const int bw = checked_bandwidth(bandwidth.has_value() ? *bandwidth : -1);
     Tensor out = torch::empty({d.B, d.L1, d.L2}, costs.options());
-    Tensor ws = dtw_second_workspace(d, costs);
+    Tensor ws = dtw_second_workspace(d, bw, costs);
     D2P_CALL(d2p_dtw_param_jacobian(costs.data_ptr<float>(), l.data_ptr<int>(), d.B, d.L1, d.L2,
                                     (float)temperature, bw, out.data_ptr<float>(), ws.data_ptr(),
                                     ws.numel(), current_stream()));

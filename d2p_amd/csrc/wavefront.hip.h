@@ -68,10 +68,13 @@ __host__ inline size_t status_bytes(int B) { return ((size_t)B * sizeof(int) + 2
 __host__ inline size_t round256(size_t n) { return (n + 255) / 256 * 256; }
 
 // Floats of `planes` skewed tables plus the last rows of every stripe per plane
-// (B * stripes * planes * stored_steps * (64 + 1)).
-__host__ inline size_t table_floats(int B, int max_L1, int max_L2, int planes = 1) {
+// (B * stripes * planes * stored_steps * (64 + 1)).  elem_steps > 0: each element's
+// table holds only elem_steps steps of 64 (a banded table); the last rows stay whole.
+__host__ inline size_t table_floats(int B, int max_L1, int max_L2, int planes = 1,
+                                    size_t elem_steps = 0) {
     const size_t ns = ((size_t)max_L1 + 63) / 64;
-    return (size_t)B * ns * planes * (size_t)stored_steps(max_L2) * 65;
+    const size_t rows = ns * (size_t)stored_steps(max_L2);
+    return (size_t)B * planes * ((elem_steps ? elem_steps : rows) * 64 + rows);
 }
 
 // Workspace prefix of every entry point: per-element status words, the trash line,
@@ -79,8 +82,9 @@ __host__ inline size_t table_floats(int B, int max_L1, int max_L2, int planes = 
 struct Layout {
     int* status;
     float* trash;
-    float* alpha_sk;   // [B][stripe][plane][step][64]
+    float* alpha_sk;   // [B][stripe][plane][step][64] (banded: [B][elem_steps][64])
     float* brow;       // [B][stripe][plane][step]
+    size_t elem_steps; // table steps of 64 per element and plane
     // split elements (present when layout() is asked for them; up to one part per
     // stripe): progress words of the forward and reverse boundaries [B][stripe],
     // reverse-sweep boundary flows [B][stripe][step], per-part partial results
@@ -95,14 +99,16 @@ struct Layout {
 };
 
 __host__ inline Layout layout(void* workspace, int B, int max_L1, int max_L2, int planes = 1,
-                              bool split = false, int flow_bytes = 8) {
+                              bool split = false, int flow_bytes = 8, size_t elem_steps = 0) {
     Layout l;
     l.status = (int*)workspace;
     l.trash = (float*)((char*)workspace + status_bytes(B));
     l.alpha_sk = (float*)((char*)l.trash + TRASH_BYTES);
     const size_t ns = ((size_t)max_L1 + 63) / 64;
-    l.brow = l.alpha_sk + (size_t)B * ns * planes * stored_steps(max_L2) * 64;
-    l.bytes = status_bytes(B) + TRASH_BYTES + table_floats(B, max_L1, max_L2, planes) * sizeof(float);
+    l.elem_steps = elem_steps ? elem_steps : ns * (size_t)stored_steps(max_L2);
+    l.brow = l.alpha_sk + (size_t)B * planes * l.elem_steps * 64;
+    l.bytes = status_bytes(B) + TRASH_BYTES +
+              table_floats(B, max_L1, max_L2, planes, elem_steps) * sizeof(float);
     l.fflag = l.bflag = nullptr;
     l.flows = l.fpart = nullptr;
     l.flow_slots = 0;
@@ -282,13 +288,14 @@ __device__ __forceinline__ void wait_for(int* prog, int w, int need, int* status
 // The chunk-level waits of sweep order q (q = stripe for forward sweeps, the
 // reversed stripe index for reverse sweeps) before its chunk k: the producer q-1
 // must be LEAD chunks ahead, and the consumer q+1 must have consumed the ring slots
-// this chunk overwrites.  Before its first chunk, a stripe that reuses its wave's
-// ring (q >= NW) also waits until the consumer of the ring's previous stripe
-// (q - NW + 1) has finished.
+// this chunk overwrites.  Before its first chunk (k_first: a stripe that sweeps only
+// a window of its steps starts there), a stripe that reuses its wave's ring (q >= NW)
+// also waits until the consumer of the ring's previous stripe (q - NW + 1) has
+// finished.
 template <int P>
 __device__ __forceinline__ void chunk_waits(int* prog, int q, int NS, int k, int nch, int R,
-                                            int* status_b) {
-    if (k == 0 && q >= NW)
+                                            int* status_b, int k_first = 0) {
+    if (k == k_first && q >= NW)
         wait_for(prog, (q + 1) % NW, (q - NW + 1) * PROG_STRIDE + nch, status_b);
     if (q > 0) wait_for(prog, (q - 1) % NW, (q - 1) * PROG_STRIDE + min(k + lead(P), nch), status_b);
     if (q + 1 < NS) {

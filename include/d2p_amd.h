@@ -165,8 +165,17 @@ int d2p_swa_backward_full(const float* scores, const float* grad_alignment, cons
  * Soft dynamic time warping (optional Sakoe-Chiba band)
  * ------------------------------------------------------------------------- */
 
-/* Workspace bytes needed by d2p_dtw_forward_marginals (status words first). */
+/* Workspace bytes needed by d2p_dtw_forward_marginals (status words first), enough
+ * for any bandwidth. */
 size_t d2p_dtw_workspace_bytes(int B, int max_L1, int max_L2);
+
+/* Workspace bytes needed by d2p_dtw_forward_marginals for one bandwidth: with a
+ * Sakoe-Chiba band (bandwidth >= 0) the skewed alpha table keeps only each stripe's
+ * band window, about (max_L2 + stripes * (2 * bandwidth + 160)) * 256 bytes per
+ * element instead of stripes * (max_L2 + 63) * 256.  bandwidth < 0 gives
+ * d2p_dtw_workspace_bytes.  No counterpart in the reference (its bindings allocate
+ * full (L1+1) x (L2+1) tables, /root/reference/src/dtw/torch_cuda.cpp:166-169). */
+size_t d2p_dtw_workspace_bytes_banded(int B, int max_L1, int max_L2, int bandwidth);
 
 /* Forward value and alignment marginals in one call.
  * Replaces the pair dtw_forward + dtw_backward (/root/reference/src/dtw/kernels.cuh:95-129)
@@ -181,8 +190,13 @@ int d2p_dtw_forward_marginals(const float* costs, const int* lengths, int B, int
                               float* marginals, float* grad_T, void* workspace,
                               size_t workspace_bytes, void* stream);
 
-/* Workspace bytes of the second-order DTW entry points below. */
+/* Workspace bytes of the second-order DTW entry points below, enough for any
+ * bandwidth. */
 size_t d2p_dtw_second_workspace_bytes(int B, int max_L1, int max_L2);
+
+/* The same for one bandwidth: banded primal and tangent tables as in
+ * d2p_dtw_workspace_bytes_banded.  No counterpart in the reference. */
+size_t d2p_dtw_second_workspace_bytes_banded(int B, int max_L1, int max_L2, int bandwidth);
 
 /* Hessian-vector product of the soft-DTW value: hvp = (d^2 value / dcosts^2) . tangent.
  * Replaces dtw_hvp (/root/reference/src/dtw/kernels.cuh:131-151) as sequenced by

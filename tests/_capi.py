@@ -26,6 +26,7 @@ SIGNATURES = {
     "d2p_swa_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _f, _f, _p, _p, _p, _p, _p, _p,
                                        _z, _p]),
     "d2p_dtw_workspace_bytes": (_z, [_i, _i, _i]),
+    "d2p_dtw_workspace_bytes_banded": (_z, [_i, _i, _i, _i]),
     "d2p_dtw_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _i, _p, _p, _p, _p, _z, _p]),
     "d2p_sw_second_workspace_bytes": (_z, [_i, _i, _i]),
     "d2p_sw_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _p, _p, _z, _p]),
@@ -37,6 +38,7 @@ SIGNATURES = {
     "d2p_swa_backward_full": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _f, _p, _p, _p, _p, _p, _z,
                                    _p]),
     "d2p_dtw_second_workspace_bytes": (_z, [_i, _i, _i]),
+    "d2p_dtw_second_workspace_bytes_banded": (_z, [_i, _i, _i, _i]),
     "d2p_dtw_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _i, _p, _p, _z, _p]),
     "d2p_dtw_param_jacobian": (_i, [_p, _p, _i, _i, _i, _f, _i, _p, _p, _z, _p]),
     "d2p_dtw_backward_full": (_i, [_p, _p, _p, _i, _i, _i, _f, _i, _p, _p, _p, _z, _p]),

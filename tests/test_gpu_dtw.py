@@ -6,7 +6,11 @@ own CPU kernels, src/dtw/kernels_cpu.cpp) supplies the expected values on the
 same seeded inputs.
 
 Tolerances: value within 1e-5 relative, marginals within 1e-4 absolute (the
-north-star contract).  grad_T = sum beta * (softmin - E[alpha_pred]) / T is a
+north-star contract).  A soft-DTW value is the expected path cost minus an entropy
+term of the same size (T log of the number of paths), so it can cancel to near
+zero while both terms are hundreds; the value check therefore also allows 1e-7 of
+the expected path cost sum(P * c), about one fp32 rounding of the cancelling
+terms.  grad_T = sum beta * (softmin - E[alpha_pred]) / T is a
 sum of cancelling terms of size |alpha| / T: 1e-3 relative plus 1e-5 * |value| / T
 of the reference, or of its per-cell terms summed in double where the
 reference's sequential fp32 sum has drifted further (tests/_paramgrad.py).
@@ -41,7 +45,9 @@ def _sq_dist_costs(seed, B, L1, L2, D):
 def _check(gpu, ref, costs, T, bw=-1, lengths=None):
     v, marg, gt = [x.detach().cpu().numpy() for x in gpu]
     rv, rm, rt = ref
-    np.testing.assert_allclose(v, rv, rtol=VALUE_RTOL, atol=1e-6)
+    cancel = (rm.astype(np.float64) * costs).sum(axis=(1, 2))   # expected path cost
+    tol = VALUE_RTOL * np.abs(rv) + 1e-7 * np.abs(cancel) + 1e-6
+    assert np.all(np.abs(v.astype(np.float64) - rv) <= tol), (v, rv, tol)
     assert np.abs(marg - rm).max() <= MARG_ATOL, np.abs(marg - rm).max()
     k = O.get("oracle")
     ln = None if lengths is None else np.asarray(lengths, np.int32)

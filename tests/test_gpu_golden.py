@@ -9,6 +9,9 @@ Jacobians also move with the fp32 evaluation of dS/dtheta (each entry by that
 error times P / T): 1e-5 * |dS/dtheta| / T * max(P) is added at these sizes.
 The temperature Jacobians of SW carry per-cell terms P (alpha - S) / T^2 whose
 inputs hold fp32 rounding of |alpha| <= |value|: 4e-7 * (|value| + 1) / T^2 more.
+The soft-DTW temperature Jacobian is exactly 0 at (1,1) and (L1,L2) (every path
+passes both cells, so P = 1 there at every T); what the reference's fp32 sweeps
+leave in those cells measures the rounding they accumulate, and 3x that is added.
 """
 import os
 
@@ -75,4 +78,8 @@ def test_hip_matches_golden(cuda, path):
         allow = 1e-5 * np.abs(dS).max() / T * pmax
         if pn == "T" and not name.startswith("dtw"):
             allow += 4e-7 * (vmax + 1.0) / T ** 2
+        if pn == "T" and name.startswith("dtw"):
+            zeros = [abs(float(want[b, 0, 0])) + abs(float(want[b, l1 - 1, l2 - 1]))
+                     for b, (l1, l2) in enumerate(f["lengths"]) if l1 > 0 and l2 > 0]
+            allow += 3.0 * max(zeros, default=0.0)
         _check(name, f"jac_{pn}", _np(J), want, 1e-4 * max(1.0, np.abs(want).max()) + allow)
