@@ -11,7 +11,10 @@ second (B*L1*L2 per step).
 ``--config`` selects the other configurations of the same path (not the
 metric's line; same output format): ``c3`` affine gap, ragged lengths;
 ``c4`` soft DTW on squared-distance costs at T=0.1; ``c5`` linear gap
-[16, 4096, 4096]; ``c5hvp`` the Hessian-vector product on the C5 shapes.
+[16, 4096, 4096]; ``c5hvp`` the Hessian-vector product on the C5 shapes;
+``c4band`` C4 under a Sakoe-Chiba band of 16; ``dtwlong`` soft DTW [16, 4096,
+4096] under a band of 64 (the banded sweeps; cells are the full tables' cells,
+as the reference sweeps them).
 
 Prints one JSON line with:
   * ``roofline``: the dominant kernel (largest share of the timed region),
@@ -133,8 +136,56 @@ def make_c5(hvp=False):
         extra={"B": B, "L1": L, "L2": L})
 
 
+def _band_cells(B, L1, L2, bw):
+    """Cells of the Sakoe-Chiba band |j - i*L2/L1| <= bw, per the reference's float
+    test (/root/reference/src/dtw/kernels_cpu.cpp:24-29)."""
+    import numpy as np
+    i = np.arange(1, L1 + 1)
+    e = (i * L2).astype(np.float32) / np.float32(L1)
+    lo = np.maximum(np.ceil(e - bw), 1)
+    hi = np.minimum(np.floor(e + bw), L2)
+    return B * int(np.maximum(hi - lo + 1, 0).sum())
+
+
+def make_c4band():
+    cfg = make_c4()
+    B, L = 512, 256
+    band = _band_cells(B, L, L, 16)
+    cfg.update(
+        name="c4band", bandwidth=16, temperature=0.1,
+        # forward: read the in-band costs; the marginals and the gradient are dense
+        algo_step=4 * band + 12 * cfg["cells"],
+        algo_kernel={"dtw_forward": 4 * band, "dtw_backward": 4 * cfg["cells"],
+                     "scale_by_batch": 8 * cfg["cells"]},
+        workload="C4 banded: soft_dtw(costs, T=0.1, bandwidth=16), squared-distance costs "
+                 "of 64-d features [512,256,256], fwd + cost.sum().backward(); cells = full "
+                 "tables",
+        extra={"B": B, "L1": L, "L2": L, "temperature": 0.1, "bandwidth": 16,
+               "band_cells": band})
+    return cfg
+
+
+def make_dtwlong():
+    import torch
+    g = torch.Generator().manual_seed(5)
+    B, L, bw = 16, 4096, 64
+    costs = _randn(g, (B, L, L)).abs_()
+    cells = B * L * L
+    band = _band_cells(B, L, L, bw)
+    return dict(
+        name="dtwlong", inputs={"costs": costs}, cells=cells, bandwidth=bw, temperature=1.0,
+        algo_step=4 * band + 12 * cells,
+        algo_kernel={"dtw_forward": 4 * band, "dtw_backward": 4 * cells,
+                     "scale_by_batch": 8 * cells},
+        workload="long banded DTW: soft_dtw(|N(0,1)| costs [16,4096,4096], T=1, "
+                 "bandwidth=64), fwd + cost.sum().backward(); cells = full tables",
+        extra={"B": B, "L1": L, "L2": L, "temperature": 1.0, "bandwidth": bw,
+               "band_cells": band})
+
+
 CONFIGS = {"c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5,
-           "c5hvp": lambda: make_c5(hvp=True)}
+           "c5hvp": lambda: make_c5(hvp=True), "c4band": make_c4band,
+           "dtwlong": make_dtwlong}
 
 
 def make_step(cfg, dev):
@@ -154,6 +205,12 @@ def make_step(cfg, dev):
         def step():
             c = x["costs"].detach().requires_grad_(True)
             d2p_amd.soft_dtw(c, temperature=0.1).cost.sum().backward()
+    elif name in ("c4band", "dtwlong"):
+        T, bw = cfg["temperature"], cfg["bandwidth"]
+
+        def step():
+            c = x["costs"].detach().requires_grad_(True)
+            d2p_amd.soft_dtw(c, temperature=T, bandwidth=bw).cost.sum().backward()
     else:
         def step():
             d2p_amd.soft_sw_hvp(x["scores"], x["V"], -1.0, 1.0, None)
@@ -229,13 +286,14 @@ def cpu_baseline_config(cfg, max_elems):
             post = k.swa_backward(a, x["scores"], p, ln, -11.0, -1.0, 0.5)[0]
             return post
         what = "fwd + 2x bwd DP + scale"
-    elif name == "c4":
+    elif name in ("c4", "c4band", "dtwlong"):
         cells = x["costs"].size
+        T, bw = cfg.get("temperature", 0.1), cfg.get("bandwidth", -1)
 
         def step():
-            a, sc = k.dtw_forward(x["costs"], None, 0.1)
-            k.dtw_backward(a, x["costs"], sc, None, 0.1)
-            return k.dtw_backward(a, x["costs"], sc, None, 0.1)[0]
+            a, sc = k.dtw_forward(x["costs"], None, T, bw)
+            k.dtw_backward(a, x["costs"], sc, None, T, bw)
+            return k.dtw_backward(a, x["costs"], sc, None, T, bw)[0]
         what = "fwd + 2x bwd DP + scale"
     elif name == "c5":
         cells = x["scores"].size
@@ -375,7 +433,8 @@ def main():
         if cfg["name"] == "c2":
             out["cpu_baseline"] = cpu_baseline(cfg["inputs"]["scores"].numpy())
         else:
-            sample = {"c3": 64, "c4": 512, "c5": 16, "c5hvp": 16}[cfg["name"]]
+            sample = {"c3": 64, "c4": 512, "c5": 16, "c5hvp": 16, "c4band": 512,
+                      "dtwlong": 16}[cfg["name"]]
             out["cpu_baseline"] = cpu_baseline_config(cfg, sample)
     print(json.dumps(out), flush=True)
 

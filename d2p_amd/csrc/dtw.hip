@@ -53,10 +53,11 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = ChunkTile<P>;
-    constexpr int WBUF = 2 * Tile::FLOATS + 3 * 64;        // two cost chunks, two rows, slot
+    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 64;        // two cost chunks, two rows
     float* tiles = smem + wave * WBUF;                     // double-buffered cost chunk
     float* rbufs = tiles + 2 * Tile::FLOATS;               // boundary row of a chunk
-    float* fslot = rbufs + 2 * 64;                         // prefetched progress word
+    __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
+                                  // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
     float* rings = smem + NW * WBUF;                       // [NW][R]
     float* sink = rings + NW * R + wave * DUMMY;           // per-wave write sink
@@ -112,7 +113,9 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
             up_lo = t_lo <= t_hi ? (t_lo / P) * P : nch * P;
             up_end = t_lo <= t_hi ? (t_hi / P + 1) * P : nch * P;
         }
-        float* out = band_stripe(alpha_sk, b, elem_steps, s, stride, k_lo) + APAD * 64;
+        // table step t of this stripe at out + (t - sh) * 64
+        const int sh = k_lo * P;
+        float* out = band_stripe(alpha_sk, b, elem_steps, s, stride) + APAD * 64;
         float* brow_s = brow + ((size_t)b * NSmax + s) * NT;   // last row, by step
         const float* brow_up = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
         const bool x_in = l == 0 && part > 0;        // row above from the previous part
@@ -121,10 +124,10 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
         // the APAD steps before the window hold the column-0 / off-band boundary
         // (PINF), read by the reverse sweep; so does the chunk after it
 #pragma unroll
-        for (int t = -APAD; t < 0; ++t) lane_store(out + (k_lo * P + t) * 64, ul4, kPINF);
+        for (int t = -APAD; t < 0; ++t) lane_store(out + t * 64, ul4, kPINF);
         if (k_end < nch) {
 #pragma unroll
-            for (int t = 0; t < P; ++t) lane_store(out + (k_end * P + t) * 64, ul4, kPINF);
+            for (int t = 0; t < P; ++t) lane_store(out + (k_end * P - sh + t) * 64, ul4, kPINF);
         }
         // the last row outside the window is PINF
         for (int t = lane; t < k_lo * P; t += 64) {
@@ -191,7 +194,7 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                 if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
-            float* outc = out + (size_t)t0 * 64;
+            float* outc = out + (size_t)(t0 - sh) * 64;
             // FULL: every cell of the chunk lies inside the element, no validity masks
             auto steps = [&](auto full) {
             constexpr bool FULL = decltype(full)::value;
@@ -278,10 +281,11 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
     constexpr int FBUF = RBUF + 64;               // flows from the part below (2P+2 floats)
     constexpr int BUF = FBUF + 64;
     static_assert(2 * P + 2 <= 64, "boundary flows fit their buffer");
-    float* bufs = smem + wave * (2 * BUF + 64);
-    float* fslot = bufs + 2 * BUF;                 // prefetched progress word
+    float* bufs = smem + wave * 2 * BUF;
+    __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
+                                  // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
-    float2* rings = reinterpret_cast<float2*>(smem + NW * (2 * BUF + 64));  // [NW][R] (up, diag)
+    float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * BUF);  // [NW][R] (up, diag)
     float2* sink = rings + NW * R + wave * DUMMY;
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
@@ -343,7 +347,9 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
             dn_lo = t_lo <= t_hi ? ((nsteps - 1 - t_hi) / P) * P : nch * P;
             dn_end = t_lo <= t_hi ? ((nsteps - 1 - t_lo) / P + 1) * P : nch * P;
         }
-        const float* astripe = band_stripe(alpha_sk, b, elem_steps, s, stride, kf_lo);
+        // table step t of this stripe at astripe + (t - sh + APAD) * 64
+        const int sh = kf_lo * PF;
+        const float* astripe = band_stripe(alpha_sk, b, elem_steps, s, stride);
         const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
         const float2* ring_in = ring_from(rings, q, R);   // from stripe s+1
         float2* ring_out = ring_of(rings, q, R);          // to stripe s-1
@@ -360,7 +366,7 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
             const int th = nsteps - 1 - k * P;
             const uint32_t buf = lds_address(bufs + (k & 1) * BUF);
             dma_tile<P, -1>(buf, cbase, i0, L1max, L2max, lane, th);
-            dma_rows<P, -1>(buf + ABUF * 4, astripe, th - 2, ul4);
+            dma_rows<P, -1>(buf + ABUF * 4, astripe, th - 2 - sh, ul4);
             uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
             uint32_t rl = buf + RBUF * 4;
             lds_dma_dword<0>(bup, roff, rl, 0u);
@@ -396,8 +402,8 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
         }
         {
             const int th0 = nsteps - 1 - k_lo * P;   // the window's first step
-            A[P] = lane_load(astripe + (size_t)(th0 + APAD) * 64, ul4);
-            A[P + 1] = lane_load(astripe + (size_t)(th0 - 1 + APAD) * 64, ul4);
+            A[P] = lane_load(astripe + (size_t)(th0 - sh + APAD) * 64, ul4);
+            A[P + 1] = lane_load(astripe + (size_t)(th0 - sh - 1 + APAD) * 64, ul4);
         }
         __asm__ volatile("" ::"v"(A[P]), "v"(A[P + 1]));   // completes the two loads here
         wave_lds_sync();   // the previous stripe's buffer reads are complete
@@ -548,15 +554,17 @@ namespace d2p_amd {
 namespace dtw {
 
 namespace {
-constexpr size_t kLdsLimit = 160 * 1024 - 256;
+// dynamic LDS bound: 160 KiB less the kernels' static arrays (progress words,
+// reductions, the prefetched progress-word slot)
+constexpr size_t kLdsLimit = 160 * 1024 - 512;
 
 // LDS of one workgroup whose stripe boundaries use rings of R columns
 size_t lds_forward_r(int R) {
-    return (size_t)NW * (2 * 65 * PF + 3 * 64) * sizeof(float) +
+    return (size_t)NW * (2 * 65 * PF + 2 * 64) * sizeof(float) +
            ((size_t)NW * R + NW * DUMMY) * sizeof(float);
 }
 size_t lds_backward_r(int R, int P) {
-    return (size_t)NW * (2 * (65 * P + 64 * P + 64 + 64) + 64) * sizeof(float) +
+    return (size_t)NW * 2 * (65 * P + 64 * P + 64 + 64) * sizeof(float) +
            ((size_t)NW * R + NW * DUMMY) * sizeof(float2);
 }
 int ring_forward(int rows, int max_L2) { return ring_len(rows, max_L2, 256); }

@@ -85,21 +85,18 @@ __host__ inline size_t band_elem_steps(int max_L1, int max_L2, int bandwidth) {
     return banded < full ? banded : full;
 }
 
-// Address of table step -APAD of stripe s, whose window starts at forward chunk k_lo
-// (the stripe's stored steps begin at k_lo*PF - APAD): table step t of the stripe is
-// at the result + (t + APAD) * 64.  Integer arithmetic: the result may lie before the
-// table for k_lo > 0, but every step the sweeps touch lies inside it.
-__device__ __forceinline__ const float* band_stripe(const float* table, int b, size_t elem_steps,
-                                                    int s, int stride, int k_lo) {
-    const long long off = (long long)b * (long long)elem_steps + (long long)s * stride -
-                          (long long)k_lo * PF;
-    return reinterpret_cast<const float*>(reinterpret_cast<uintptr_t>(table) +
-                                          (uintptr_t)(off * 256));
-}
+// Address of the first stored step of stripe s (a table step -APAD without a band).
+// A stripe whose window starts at forward chunk k_lo stores steps from
+// k_lo*PF - APAD on: table step t sits at the result + (t - k_lo*PF + APAD) * 64.
+// Plain pointer arithmetic from the table pointer, so the compiler keeps the
+// accesses in the global address space.
 __device__ __forceinline__ float* band_stripe(float* table, int b, size_t elem_steps, int s,
-                                              int stride, int k_lo) {
-    return const_cast<float*>(
-        band_stripe(static_cast<const float*>(table), b, elem_steps, s, stride, k_lo));
+                                              int stride) {
+    return table + ((size_t)b * elem_steps + (size_t)s * stride) * 64;
+}
+__device__ __forceinline__ const float* band_stripe(const float* table, int b, size_t elem_steps,
+                                                    int s, int stride) {
+    return table + ((size_t)b * elem_steps + (size_t)s * stride) * 64;
 }
 
 // Checks shared by the entry points (sizes, LDS budget); D2P_OK or an error code.

@@ -52,8 +52,7 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
     constexpr int AR = Tile::FLOATS;      // P alpha rows after the input tile
     constexpr int RR = AR + P * 64;       // row above
     constexpr int TR = RR + 64;           // tangent row of the part above
-    constexpr int FS = TR + 64;           // prefetched progress word
-    constexpr int BUF = FS + 64;
+    constexpr int BUF = TR + 64;
     constexpr int SINK = 64 + P;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
@@ -66,7 +65,8 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float* buf = smem + wave * BUF;
-    float* fslot = buf + FS;
+    __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
+                                  // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
     float* rings = smem + NW * BUF;
     float* sink = rings + NW * R + wave * SINK;
@@ -115,9 +115,11 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
             up_lo = t_lo <= t_hi ? (t_lo / P) * P : nch * P;
             up_end = t_lo <= t_hi ? (t_hi / P + 1) * P : nch * P;
         }
-        const float* astripe = band_stripe(alpha_sk, b, elem_steps, s, stride, k_lo);
+        // table step t of this stripe at astripe + (t - sh + APAD) * 64, tout + (t - sh) * 64
+        const int sh = k_lo * P;
+        const float* astripe = band_stripe(alpha_sk, b, elem_steps, s, stride);
         const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
-        float* tout = band_stripe(tan_sk, b, elem_steps, s, stride, k_lo) + APAD * 64;
+        float* tout = band_stripe(tan_sk, b, elem_steps, s, stride) + APAD * 64;
         float* tb_s = tan_brow + ((size_t)b * NSmax + s) * NT;
         const float* tb_up = tan_brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
         const float* ring_in = ring_from(rings, l, R);
@@ -129,7 +131,7 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
         auto issue_chunk = [&](int k) {
             const int t0 = k * P;
             dma_tile<P, 1>(in_lds, ibase, i0, L1max, L2max, lane, t0);
-            dma_rows<P, 1>(in_lds + AR * 4, astripe, t0, ul4);
+            dma_rows<P, 1>(in_lds + AR * 4, astripe, t0 - sh, ul4);
             uint32_t roff = (uint32_t)min(t0 + 62 + min(lane, P), nsteps - 1) * 4u;
             uint32_t rl = in_lds + RR * 4;
             lds_dma_dword<0>(bup, roff, rl, 0u);
@@ -144,10 +146,10 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
         // tangents of the APAD steps before the window and of the chunk after it: 0
         // (column 0 and off the band)
 #pragma unroll
-        for (int t = -APAD; t < 0; ++t) lane_store(tout + (k_lo * P + t) * 64, ul4, 0.0f);
+        for (int t = -APAD; t < 0; ++t) lane_store(tout + t * 64, ul4, 0.0f);
         if (k_end < nch) {
 #pragma unroll
-            for (int t = 0; t < P; ++t) lane_store(tout + (k_end * P + t) * 64, ul4, 0.0f);
+            for (int t = 0; t < P; ++t) lane_store(tout + (k_end * P - sh + t) * 64, ul4, 0.0f);
         }
         // so are the last row's tangents outside the window
         for (int t = lane; t < k_lo * P; t += 64) {
@@ -206,7 +208,7 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
                 if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
-            float* toutc = tout + (size_t)t0 * 64;
+            float* toutc = tout + (size_t)(t0 - sh) * 64;
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t0 + u;
@@ -286,8 +288,7 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
     constexpr int RX = RA + 64;
     constexpr int OT = RX + 64;
     constexpr int FB = OT + (DOT ? 0 : Tile::FLOATS);   // flows from the part below
-    constexpr int FS = FB + 64;                         // prefetched progress word
-    constexpr int BUF = FS + 64;
+    constexpr int BUF = FB + 64;
     static_assert(4 * P <= 64, "boundary flows fit their buffer");
     constexpr int SINK = 64 + P;
     extern __shared__ float smem[];
@@ -304,7 +305,8 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float* buf = smem + wave * BUF;
     float* otile = buf + OT;
-    float* fslot = buf + FS;
+    __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
+                                  // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
     float4* rings = reinterpret_cast<float4*>(smem + NW * BUF);
     float4* sink = rings + NW * R + wave * SINK;
@@ -368,8 +370,10 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
             dn_end = t_lo <= t_hi ? ((nsteps - 1 - t_lo) / P + 1) * P : nch * P;
         }
         const size_t ub = ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
-        const float* astripe = band_stripe(alpha_sk, b, elem_steps, s, stride, kf_lo);
-        const float* xstripe = band_stripe(tan_sk, b, elem_steps, s, stride, kf_lo);
+        // table step t of this stripe at astripe / xstripe + (t - sh + APAD) * 64
+        const int sh = kf_lo * PF;
+        const float* astripe = band_stripe(alpha_sk, b, elem_steps, s, stride);
+        const float* xstripe = band_stripe(tan_sk, b, elem_steps, s, stride);
         const float* bup = brow + ub;
         const float* xup = tan_brow + ub;
         const float4* ring_in = ring_from(rings, q, R);
@@ -386,8 +390,8 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
             if (DOT) dma_tile<P, -1>(in_lds, vbase, i0, L1max, L2max, lane, th);
-            dma_rows<P, -1>(in_lds + AR * 4, astripe, th - 2, ul4);
-            dma_rows<P, -1>(in_lds + XR * 4, xstripe, th - 2, ul4);
+            dma_rows<P, -1>(in_lds + AR * 4, astripe, th - 2 - sh, ul4);
+            dma_rows<P, -1>(in_lds + XR * 4, xstripe, th - 2 - sh, ul4);
             const uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
             uint32_t o = roff, l = in_lds + RA * 4;
             lds_dma_dword<0>(bup, o, l, 0u);
@@ -426,8 +430,8 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
         }
         {
             const int th0 = nsteps - 1 - k_lo * P;   // the window's first step
-            const float* a0p = astripe + (size_t)(th0 + APAD) * 64;
-            const float* x0p = xstripe + (size_t)(th0 + APAD) * 64;
+            const float* a0p = astripe + (size_t)(th0 - sh + APAD) * 64;
+            const float* x0p = xstripe + (size_t)(th0 - sh + APAD) * 64;
             A[P] = lane_load(a0p, ul4);
             A[P + 1] = lane_load(a0p - 64, ul4);
             X[P] = lane_load(x0p, ul4);
@@ -611,18 +615,20 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
 
 // ------------------------------------------------------------------ host side
 
-constexpr size_t kLdsLimit = 160 * 1024 - 256;
+// dynamic LDS bound: 160 KiB less the kernels' static arrays (progress words,
+// reductions, the prefetched progress-word slot)
+constexpr size_t kLdsLimit = 160 * 1024 - 512;
 constexpr int PT = 16;
 
 // LDS of one workgroup whose stripe boundaries use rings of R columns
 size_t lds_tangent_r(int R) {
-    return (size_t)NW * (65 * PT + PT * 64 + 64 + 64 + 64) * sizeof(float) +
+    return (size_t)NW * (65 * PT + PT * 64 + 64 + 64) * sizeof(float) +
            ((size_t)NW * R + NW * (64 + PT)) * sizeof(float);
 }
 size_t lds_tangent(int L1, int L2) { return lds_tangent_r(ring_len(L1, L2, 256)); }
 
 size_t lds_dual_r(bool dot, int P, int R) {
-    const int buf = (dot ? 65 * P : 0) + 2 * P * 64 + 128 + (dot ? 0 : 65 * P) + 128;
+    const int buf = (dot ? 65 * P : 0) + 2 * P * 64 + 128 + (dot ? 0 : 65 * P) + 64;
     return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + P)) * sizeof(float4);
 }
 

@@ -70,10 +70,11 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = ChunkTile<P>;
-    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 3 * 64 + 64;   // + progress-word slot
+    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 3 * 64;
     float* tiles = smem + wave * WBUF;                    // double-buffered score chunk
     float* rbufs = tiles + 2 * Tile::FLOATS;              // [2][plane][64] rows above
-    float* fslot = rbufs + 2 * 3 * 64;                    // prefetched progress word
+    __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
+                                  // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
     float4* rings = reinterpret_cast<float4*>(smem + NW * WBUF);   // [NW][R]
     float4* sink = rings + NW * R + wave * DUMMY;
@@ -303,12 +304,12 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
     constexpr int OTILE = RROW + 3 * 64;
     constexpr int FB4 = OTILE + Tile::FLOATS;       // flows from the part below: float4s
     constexpr int FB1 = FB4 + 64;                   // ... and the diagonal D flows
-    constexpr int FSLOT = FB1 + 64;                 // prefetched progress word
-    constexpr int WFLOATS = FSLOT + 64;
+    constexpr int WFLOATS = FB1 + 64;
     static_assert(4 * P + 4 <= 64, "boundary flows fit their buffer");
     float* wbuf = smem + wave * WFLOATS;
     float* otile = wbuf + OTILE;
-    float* fslot = wbuf + FSLOT;
+    __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
+                                  // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
     // rings [NW][R]: (up M, up I, diag M, diag I) and diag D, from lane 0 upward
     float4* ring4 = reinterpret_cast<float4*>(smem + NW * WFLOATS);
@@ -654,15 +655,17 @@ namespace d2p_amd {
 namespace swa {
 
 namespace {
-constexpr size_t kLdsLimit = 160 * 1024 - 256;
+// dynamic LDS bound: 160 KiB less the kernels' static arrays (progress words,
+// reductions, the prefetched progress-word slot)
+constexpr size_t kLdsLimit = 160 * 1024 - 512;
 
 // LDS of one workgroup whose stripe boundaries use rings of R columns
 size_t lds_forward_r(int R) {
-    return (size_t)NW * (2 * 65 * PF + 2 * 3 * 64 + 64) * sizeof(float) +
+    return (size_t)NW * (2 * 65 * PF + 2 * 3 * 64) * sizeof(float) +
            ((size_t)NW * R + NW * DUMMY) * sizeof(float4);
 }
 size_t lds_backward_r(int R) {
-    const size_t wfloats = 65 * PB + 3 * PB * 64 + 3 * 64 + 65 * PB + 3 * 64;
+    const size_t wfloats = 65 * PB + 3 * PB * 64 + 3 * 64 + 65 * PB + 2 * 64;
     return (size_t)NW * wfloats * sizeof(float) +
            (size_t)NW * R * (sizeof(float4) + sizeof(float)) +
            (size_t)NW * (64 + PB) * (sizeof(float4) + sizeof(float));

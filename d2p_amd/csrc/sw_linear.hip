@@ -59,10 +59,11 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = QuadTile<P>;
-    constexpr int WBUF = 2 * Tile::FLOATS + 3 * 64;        // two score chunks, two rows, slot
+    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 64;        // two score chunks, two rows
     float* tiles = smem + wave * WBUF;                     // double-buffered score chunk
     float* rbufs = tiles + 2 * Tile::FLOATS;               // boundary row of a chunk
-    float* fslot = rbufs + 2 * 64;                         // prefetched progress word
+    __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
+                                  // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
     float* rings = smem + NW * WBUF;                       // [NW][R]
     float* sink = rings + NW * R + wave * DUMMY;           // per-wave write sink
@@ -260,10 +261,11 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     constexpr int FBUF = RBUF + 64;               // flows from the part below (2P+2 floats)
     constexpr int BUF = FBUF + 64;
     static_assert(2 * P + 2 <= 64, "boundary flows fit their buffer");
-    float* bufs = smem + wave * (2 * BUF + 64);
-    float* fslot = bufs + 2 * BUF;                 // prefetched progress word
+    float* bufs = smem + wave * 2 * BUF;
+    __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
+                                  // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
-    float2* rings = reinterpret_cast<float2*>(smem + NW * (2 * BUF + 64));  // [NW][R] (up, diag)
+    float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * BUF);  // [NW][R] (up, diag)
     float2* sink = rings + NW * R + wave * DUMMY;
     int* st = status + b;
     // the chunk's marginals go to an output tile laid over its own buffer, whose
@@ -531,15 +533,17 @@ namespace d2p_amd {
 namespace sw {
 
 namespace {
-constexpr size_t kLdsLimit = 160 * 1024 - 256;
+// dynamic LDS bound: 160 KiB less the kernels' static arrays (progress words,
+// reductions, the prefetched progress-word slot)
+constexpr size_t kLdsLimit = 160 * 1024 - 512;
 
 // LDS of one workgroup whose stripes' boundaries use rings of R columns
 size_t lds_forward_r(int R) {
-    return (size_t)wf::NW * (2 * 64 * PF + 3 * 64) * sizeof(float) +
+    return (size_t)wf::NW * (2 * 64 * PF + 2 * 64) * sizeof(float) +
            ((size_t)wf::NW * R + wf::NW * DUMMY) * sizeof(float);
 }
 size_t lds_backward_r(int R, int P) {
-    return (size_t)wf::NW * (2 * (64 * P + 64 * P + 64 + 64) + 64) * sizeof(float) +
+    return (size_t)wf::NW * 2 * (64 * P + 64 * P + 64 + 64) * sizeof(float) +
            ((size_t)wf::NW * R + wf::NW * DUMMY) * sizeof(float2);
 }
 // rings of a workgroup that runs `rows` rows of stripes

@@ -60,8 +60,7 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     constexpr int AR = VT + (HAS_V ? Tile::FLOATS : 0);      // P alpha rows
     constexpr int RR = AR + P * 64;                          // row above
     constexpr int TR = RR + 64;                              // tangent row of the part above
-    constexpr int FS = TR + 64;                              // prefetched progress word
-    constexpr int BUF = FS + 64;
+    constexpr int BUF = TR + 64;
     constexpr int SINK = 64 + P;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
@@ -75,7 +74,8 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float* buf = smem + wave * BUF;
-    float* fslot = buf + FS;
+    __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
+                                  // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
     float* rings = smem + NW * BUF;                          // [NW][R] tangent of lane 63
     float* sink = rings + NW * R + wave * SINK;
@@ -288,8 +288,7 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     constexpr int RX = RA + 64;                             // tangent row above
     constexpr int OT = RX + 64;                             // output tile
     constexpr int FB = OT + (DOT ? 0 : Tile::FLOATS);       // flows from the part below
-    constexpr int FS = FB + 64;                             // prefetched progress word
-    constexpr int BUF = FS + 64;
+    constexpr int BUF = FB + 64;
     static_assert(4 * P + 2 <= 64, "boundary flows fit their buffer");
     constexpr int SINK = 64 + P;
     extern __shared__ float smem[];
@@ -306,7 +305,8 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float* buf = smem + wave * BUF;
     float* otile = buf + OT;
-    float* fslot = buf + FS;
+    __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
+                                  // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
     float4* rings = reinterpret_cast<float4*>(smem + NW * BUF);   // [NW][R]
     float4* sink = rings + NW * R + wave * SINK;
@@ -588,12 +588,14 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
 
 // ------------------------------------------------------------------ host side
 
-constexpr size_t kLdsLimit = 160 * 1024 - 256;
+// dynamic LDS bound: 160 KiB less the kernels' static arrays (progress words,
+// reductions, the prefetched progress-word slot)
+constexpr size_t kLdsLimit = 160 * 1024 - 512;
 constexpr int PT = 16;   // tangent sweep chunk
 
 // LDS of one workgroup whose stripe boundaries use rings of R columns
 size_t lds_tangent_r(int mode, int R) {
-    const int buf = 65 * PT * (mode == HVP ? 2 : 1) + PT * 64 + 64 + 64 + 64;
+    const int buf = 65 * PT * (mode == HVP ? 2 : 1) + PT * 64 + 64 + 64;
     return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + PT)) * sizeof(float);
 }
 size_t lds_tangent(int mode, int max_L1, int max_L2) {
@@ -601,7 +603,7 @@ size_t lds_tangent(int mode, int max_L1, int max_L2) {
 }
 
 size_t lds_dual_r(bool has_v, bool dot, int P, int R) {
-    const int buf = 65 * P * (has_v ? 2 : 1) + 2 * P * 64 + 128 + (dot ? 0 : 65 * P) + 128;
+    const int buf = 65 * P * (has_v ? 2 : 1) + 2 * P * 64 + 128 + (dot ? 0 : 65 * P) + 64;
     return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + P)) * sizeof(float4);
 }
 

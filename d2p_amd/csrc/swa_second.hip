@@ -57,8 +57,7 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
     constexpr int AR = VT + (HAS_V ? Tile::FLOATS : 0);   // 3 planes x P alpha rows
     constexpr int RR = AR + 3 * P * 64;                   // 3 planes x row above
     constexpr int TR = RR + 3 * 64;                       // 3 tangent rows of the part above
-    constexpr int FS = TR + 3 * 64;                       // prefetched progress word
-    constexpr int BUF = FS + 64;
+    constexpr int BUF = TR + 3 * 64;
     constexpr int SINK = 64 + P;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
@@ -72,7 +71,8 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float* buf = smem + wave * BUF;
-    float* fslot = buf + FS;
+    __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
+                                  // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
     float4* rings = reinterpret_cast<float4*>(smem + NW * BUF);
     float4* sink = rings + NW * R + wave * SINK;
@@ -352,8 +352,7 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     constexpr int FBU = OT + (DOT ? 0 : Tile::FLOATS);
     constexpr int FBD = FBU + 64;
     constexpr int FBE = FBD + 64;
-    constexpr int FS = FBE + 64;                          // prefetched progress word
-    constexpr int BUF = FS + 64;
+    constexpr int BUF = FBE + 64;
     static_assert(4 * P <= 64, "boundary flows fit their buffers");
     extern __shared__ float smem[];
     __shared__ int prog[NW];
@@ -369,7 +368,8 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float* buf = smem + wave * BUF;
     float* otile = buf + OT;
-    float* fslot = buf + FS;
+    __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
+                                  // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
     // rings [NW][R]: (beta, g) up flows to (M, I); diagonal flows to (M, I); to D
     float4* ringU = reinterpret_cast<float4*>(smem + NW * BUF);
@@ -771,19 +771,21 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
 
 // ------------------------------------------------------------------ host side
 
-constexpr size_t kLdsLimit = 160 * 1024 - 256;
+// dynamic LDS bound: 160 KiB less the kernels' static arrays (progress words,
+// reductions, the prefetched progress-word slot)
+constexpr size_t kLdsLimit = 160 * 1024 - 512;
 constexpr int PT = 8;   // tangent sweep chunk
 constexpr int PD = 4;   // reverse sweep chunk
 
 // LDS of one workgroup whose stripe boundaries use rings of R columns
 size_t lds_tangent_r(bool has_v, int R) {
-    const int buf = 65 * PT * (has_v ? 2 : 1) + 3 * PT * 64 + 3 * 64 + 3 * 64 + 64;
+    const int buf = 65 * PT * (has_v ? 2 : 1) + 3 * PT * 64 + 3 * 64 + 3 * 64;
     return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + PT)) * sizeof(float4);
 }
 size_t lds_tangent(bool has_v, int L1, int L2) { return lds_tangent_r(has_v, ring_len(L1, L2, 256)); }
 
 size_t lds_dual_r(bool has_v, bool dot, int R) {
-    const int buf = 65 * PD * (has_v ? 2 : 1) + 6 * PD * 64 + 6 * 64 + (dot ? 0 : 65 * PD) + 4 * 64;
+    const int buf = 65 * PD * (has_v ? 2 : 1) + 6 * PD * 64 + 6 * 64 + (dot ? 0 : 65 * PD) + 3 * 64;
     return (size_t)NW * buf * sizeof(float) +
            (size_t)NW * R * (2 * sizeof(float4) + sizeof(float2));
 }
