@@ -215,11 +215,23 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 float x;
                 if (MODE == HVP) {
                     x = (((e0 * (td + vd) + e1 * tu) + e2 * tl) + e3 * vd) * rin;
-                } else if (MODE == GAP) {
-                    x = ((e0 * td + e1 * (tu + 1.0f)) + e2 * (tl + 1.0f)) * rin;
                 } else {
-                    const float ev = (((e0 * v0 + e1 * v1) + e2 * v2) + e3 * sc) * rin;
-                    x = ((e0 * td + e1 * tu) + e2 * tl) * rin + (a0 - ev) * rT;
+                    // The parameter tangents pass E_w[d] on as the candidate of the
+                    // largest value plus the weighted differences: the weights' sum
+                    // differs from 1 by an ulp or two, and taken whole that factor
+                    // would compound along the alignment into tangents that grow with
+                    // its length (the Jacobian subtracts dS/dtheta from them).
+                    const float d1 = MODE == GAP ? tu + 1.0f : tu;
+                    const float d2 = MODE == GAP ? tl + 1.0f : tl;
+                    const float pd = v0 >= m ? td : (v1 >= m ? d1 : (v2 >= m ? d2 : 0.0f));
+                    x = pd + (((e0 * (td - pd) + e1 * (d1 - pd)) + e2 * (d2 - pd)) - e3 * pd) * rin;
+                    if (MODE == TEMP) {
+                        // alpha - E_w[v], both relative to the largest value m
+                        const float ev =
+                            (((e0 * (v0 - m) + e1 * (v1 - m)) + e2 * (v2 - m)) + e3 * (sc - m)) *
+                            rin;
+                        x += ((a0 - m) - ev) * rT;
+                    }
                 }
                 cur = ok ? x : 0.0f;
                 lane_store(toutc + u * 64, ul4, cur);
@@ -503,16 +515,34 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 } else {
                     d0 = dgx; d1 = upx; d2 = x1; d3 = 0.0f;
                 }
-                const float mean = ((w0 * d0 + w1 * d1) + w2 * d2) + w3 * d3;
-                float dw0 = w0 * (d0 - mean) * rT, dw1 = w1 * (d1 - mean) * rT;
-                float dw2 = w2 * (d2 - mean) * rT, dw3 = w3 * (d3 - mean) * rT;
-                if (MODE == TEMP) {
-                    const float ev = ((w0 * v0 + w1 * v1) + w2 * v2) + w3 * sc;
-                    const float rT2 = rT * rT;
-                    dw0 += w0 * (ev - v0) * rT2;
-                    dw1 += w1 * (ev - v1) * rT2;
-                    dw2 += w2 * (ev - v2) * rT2;
-                    dw3 += w3 * (ev - sc) * rT2;
+                float dw0, dw1, dw2, dw3;
+                if (MODE == HVP) {
+                    const float mean = ((w0 * d0 + w1 * d1) + w2 * d2) + w3 * d3;
+                    dw0 = w0 * (d0 - mean) * rT;
+                    dw1 = w1 * (d1 - mean) * rT;
+                    dw2 = w2 * (d2 - mean) * rT;
+                    dw3 = w3 * (d3 - mean) * rT;
+                } else {
+                    // the parameter Jacobians take E_w[d] - d_k and E_w[v] - v_k relative
+                    // to the candidate of the largest value: the weights' sum differs
+                    // from 1 by an ulp or two, which must not multiply tangents and
+                    // values that grow with the alignment length
+                    const float p = v0 >= m ? d0 : (v1 >= m ? d1 : (v2 >= m ? d2 : d3));
+                    const float q0 = d0 - p, q1 = d1 - p, q2 = d2 - p, q3 = d3 - p;
+                    const float mean = ((w0 * q0 + w1 * q1) + w2 * q2) + w3 * q3;
+                    dw0 = w0 * (q0 - mean) * rT;
+                    dw1 = w1 * (q1 - mean) * rT;
+                    dw2 = w2 * (q2 - mean) * rT;
+                    dw3 = w3 * (q3 - mean) * rT;
+                    if (MODE == TEMP) {
+                        const float p0 = v0 - m, p1 = v1 - m, p2 = v2 - m, p3 = sc - m;
+                        const float ev = ((w0 * p0 + w1 * p1) + w2 * p2) + w3 * p3;
+                        const float rT2 = rT * rT;
+                        dw0 += w0 * (ev - p0) * rT2;
+                        dw1 += w1 * (ev - p1) * rT2;
+                        dw2 += w2 * (ev - p2) * rT2;
+                        dw3 += w3 * (ev - p3) * rT2;
+                    }
                 }
                 // channels in the reference's accumulation order
                 float lp = (a0 - S) * c;

@@ -255,17 +255,30 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
                     xI = (f0 * tuM + f1 * tuI) * ri;
                     xD = (g0 * cM + g1 * cD) * rd;
                 } else {
+                    // The parameter tangents pass E_w[d] on as the candidate of the
+                    // largest value plus the weighted differences (two candidates:
+                    // d_0 + w_1 (d_1 - d_0)): the weights' sum differs from 1 by an ulp
+                    // or two, and taken whole that factor would compound along the
+                    // alignment into tangents that grow with its length (the Jacobian
+                    // subtracts dS/dtheta from them).
                     const float ao = MODE == OPEN ? 1.0f : 0.0f, ae = MODE == EXT ? 1.0f : 0.0f;
-                    xM = ((e0 * tdM + e1 * tdI) + e2 * tdD) * r4;
-                    xI = (f0 * (tuM + ao) + f1 * (tuI + ae)) * ri;
-                    xD = (g0 * (cM + ao) + g1 * (cD + ae)) * rd;
+                    const float pM = v0 >= m4 ? tdM : (v1 >= m4 ? tdI : (v2 >= m4 ? tdD : 0.0f));
+                    xM = pM + (((e0 * (tdM - pM) + e1 * (tdI - pM)) + e2 * (tdD - pM)) - e3 * pM) * r4;
+                    const float di0 = tuM + ao, di1 = tuI + ae;
+                    xI = ri > 0.0f ? di0 + f1 * ri * (di1 - di0) : 0.0f;
+                    const float dd0 = cM + ao, dd1 = cD + ae;
+                    xD = rd > 0.0f ? dd0 + g1 * rd * (dd1 - dd0) : 0.0f;
                     if (MODE == TEMP) {
-                        const float E4 = (((e0 * v0 + e1 * v1) + e2 * v2) + e3 * sc) * r4;
-                        const float E2i = (f0 * i0v + f1 * i1v) * ri;
-                        const float E2d = (g0 * d0v + g1 * d1v) * rd;
-                        xM += (AM[u + 2] - E4) * rT;
-                        xI += ri > 0.0f ? (AI[u + 2] - E2i) * rT : 0.0f;
-                        xD += rd > 0.0f ? (AD[u + 2] - E2d) * rT : 0.0f;
+                        // alpha - E_w[v] of each state, both relative to its largest
+                        // candidate (the weights' sum differs from 1 by an ulp or two)
+                        const float E4 =
+                            (((e0 * (v0 - m4) + e1 * (v1 - m4)) + e2 * (v2 - m4)) + e3 * (sc - m4)) *
+                            r4;
+                        const float E2i = (f0 * (i0v - mi) + f1 * (i1v - mi)) * ri;
+                        const float E2d = (g0 * (d0v - md) + g1 * (d1v - md)) * rd;
+                        xM += ((AM[u + 2] - m4) - E4) * rT;
+                        xI += ri > 0.0f ? ((AI[u + 2] - mi) - E2i) * rT : 0.0f;
+                        xD += rd > 0.0f ? ((AD[u + 2] - md) - E2d) * rT : 0.0f;
                     }
                 }
                 cM = ok ? xM : 0.0f;
@@ -633,26 +646,53 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 const float dm0 = dxM + vt, dm1 = dxI + vt, dm2 = dxD + vt, dm3 = vt;
                 const float di0 = uxM + ao, di1 = uxI + ae;
                 const float dd0 = lxM + ao, dd1 = lxD + ae;
-                const float mM = ((w0 * dm0 + w1 * dm1) + w2 * dm2) + w3 * dm3;
-                const float mI = wi0 * di0 + wi1 * di1;
-                const float mD = wd0 * dd0 + wd1 * dd1;
-                float dw0 = w0 * (dm0 - mM) * rT, dw1 = w1 * (dm1 - mM) * rT;
-                float dw2 = w2 * (dm2 - mM) * rT, dw3 = w3 * (dm3 - mM) * rT;
-                float dwi0 = wi0 * (di0 - mI) * rT, dwi1 = wi1 * (di1 - mI) * rT;
-                float dwd0 = wd0 * (dd0 - mD) * rT, dwd1 = wd1 * (dd1 - mD) * rT;
-                if (MODE == TEMP) {
-                    const float rT2 = rT * rT;
-                    const float E4 = ((w0 * v0 + w1 * v1) + w2 * v2) + w3 * sc;
-                    dw0 += w0 * (E4 - v0) * rT2;
-                    dw1 += w1 * (E4 - v1) * rT2;
-                    dw2 += w2 * (E4 - v2) * rT2;
-                    dw3 += w3 * (E4 - sc) * rT2;
-                    const float Ei = wi0 * i0v + wi1 * i1v;
-                    dwi0 += wi0 * (Ei - i0v) * rT2;
-                    dwi1 += wi1 * (Ei - i1v) * rT2;
-                    const float Ed = wd0 * d0v + wd1 * d1v;
-                    dwd0 += wd0 * (Ed - d0v) * rT2;
-                    dwd1 += wd1 * (Ed - d1v) * rT2;
+                float dw0, dw1, dw2, dw3, dwi0, dwi1, dwd0, dwd1;
+                if (MODE == HVP) {
+                    const float mM = ((w0 * dm0 + w1 * dm1) + w2 * dm2) + w3 * dm3;
+                    const float mI = wi0 * di0 + wi1 * di1;
+                    const float mD = wd0 * dd0 + wd1 * dd1;
+                    dw0 = w0 * (dm0 - mM) * rT;
+                    dw1 = w1 * (dm1 - mM) * rT;
+                    dw2 = w2 * (dm2 - mM) * rT;
+                    dw3 = w3 * (dm3 - mM) * rT;
+                    dwi0 = wi0 * (di0 - mI) * rT;
+                    dwi1 = wi1 * (di1 - mI) * rT;
+                    dwd0 = wd0 * (dd0 - mD) * rT;
+                    dwd1 = wd1 * (dd1 - mD) * rT;
+                } else {
+                    // The parameter Jacobians take E_w[d] - d_k (and E_w[v] - v_k)
+                    // relative to the candidate of the largest value: the weights' sum
+                    // differs from 1 by an ulp or two, which must not multiply tangents
+                    // and values that grow with the alignment length.  With two
+                    // candidates, E_w[d] - d_0 = w_1 (d_1 - d_0) exactly.
+                    const float p = v0 >= m4 ? dm0 : (v1 >= m4 ? dm1 : (v2 >= m4 ? dm2 : dm3));
+                    const float q0 = dm0 - p, q1 = dm1 - p, q2 = dm2 - p, q3 = dm3 - p;
+                    const float mM = ((w0 * q0 + w1 * q1) + w2 * q2) + w3 * q3;
+                    dw0 = w0 * (q0 - mM) * rT;
+                    dw1 = w1 * (q1 - mM) * rT;
+                    dw2 = w2 * (q2 - mM) * rT;
+                    dw3 = w3 * (q3 - mM) * rT;
+                    const float wwi = wi0 * wi1 * rT, wwd = wd0 * wd1 * rT;
+                    dwi0 = wwi * (di0 - di1);
+                    dwi1 = -dwi0;
+                    dwd0 = wwd * (dd0 - dd1);
+                    dwd1 = -dwd0;
+                    if (MODE == TEMP) {
+                        const float rT2 = rT * rT;
+                        const float p0 = v0 - m4, p1 = v1 - m4, p2 = v2 - m4, p3 = sc - m4;
+                        const float E4 = ((w0 * p0 + w1 * p1) + w2 * p2) + w3 * p3;
+                        dw0 += w0 * (E4 - p0) * rT2;
+                        dw1 += w1 * (E4 - p1) * rT2;
+                        dw2 += w2 * (E4 - p2) * rT2;
+                        dw3 += w3 * (E4 - p3) * rT2;
+                        // w_0 (E - v_0) = w_0 w_1 (v_1 - v_0); 0 when either is impossible
+                        const float ti = wi1 > 0.0f ? wi0 * wi1 * (i1v - i0v) * rT2 : 0.0f;
+                        const float td = wd1 > 0.0f ? wd0 * wd1 * (d1v - d0v) * rT2 : 0.0f;
+                        dwi0 += ti;
+                        dwi1 -= ti;
+                        dwd0 += td;
+                        dwd1 -= td;
+                    }
                 }
                 // initial values of the two channels
                 float lp;

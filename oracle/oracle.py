@@ -9,7 +9,13 @@ numpy interface:
   follows);
 * ``_ref/libd2p_ref.so`` -- the reference's own CPU kernels
   (``/root/reference/src/{sw,sw_affine,dtw}/kernels_cpu.cpp``), compiled by
-  ``oracle/Makefile`` where those sources exist.
+  ``oracle/Makefile`` where those sources exist;
+* ``liboracle64.so`` -- the same C restatement compiled with every ``float`` as
+  ``double`` (and ``expf``/``logf``/``fabsf`` as their double versions): the
+  reference's algorithm in double precision, a near-exact value for quantities
+  whose fp32 evaluation is ill-conditioned (second-order Jacobians of long
+  elements), against which the fp32 reference's own error can be measured.
+  ``get("oracle64")`` takes and returns float64 arrays.
 
 Both expose the reference's CPU signatures (``src/sw/kernels_cpu.h:95-183``,
 ``src/sw_affine/kernels_cpu.h:80-167``, ``src/dtw/kernels_cpu.h:83-161``), so
@@ -28,6 +34,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_LIB = os.path.join(HERE, "liboracle.so")
+ORACLE64_LIB = os.path.join(HERE, "liboracle64.so")
 REF_LIB = os.path.join(HERE, "_ref", "libd2p_ref.so")
 
 _F = ctypes.POINTER(ctypes.c_float)
@@ -101,12 +108,13 @@ def _lengths(lengths, B, L1, L2) -> np.ndarray:
 
 
 class CpuKernels:
-    """numpy front end over one CPU library (``kind`` = "oracle" or "reference")."""
+    """numpy front end over one CPU library (``kind`` = "oracle", "reference" or
+    "oracle64")."""
 
     def __init__(self, kind: str = "oracle"):
-        if kind not in ("oracle", "reference"):
+        if kind not in ("oracle", "reference", "oracle64"):
             raise ValueError(kind)
-        path = ORACLE_LIB if kind == "oracle" else REF_LIB
+        path = {"oracle": ORACLE_LIB, "reference": REF_LIB, "oracle64": ORACLE64_LIB}[kind]
         if not os.path.exists(path):
             raise FileNotFoundError(
                 f"{path} is not built; run `make -C oracle` (reference build needs "
@@ -115,27 +123,34 @@ class CpuKernels:
             import torch  # noqa: F401  -- loads libtorch_cpu/libc10 the library links
         self.kind = kind
         self.path = path
+        self.ft = np.float64 if kind == "oracle64" else np.float32
+        # the double build takes double arrays and scalars where the others take float
+        wide = {_F: _D, _f: ctypes.c_double} if kind == "oracle64" else {}
         self.lib = ctypes.CDLL(path)
         self.fn = {}
         for name, (osym, rsym, argt) in _SIGS.items():
-            f = getattr(self.lib, osym if kind == "oracle" else rsym)
-            f.argtypes = argt
+            f = getattr(self.lib, rsym if kind == "reference" else osym)
+            f.argtypes = [wide.get(t, t) for t in argt]
             f.restype = None
             self.fn[name] = f
-        if kind == "oracle":
+        if kind != "reference":
             for name, (osym, argt) in _SIGS64.items():
                 f = getattr(self.lib, osym)
-                f.argtypes = argt
+                f.argtypes = [wide.get(t, t) for t in argt]
                 f.restype = None
                 self.fn[name] = f
+
+    def _a(self, a) -> np.ndarray:
+        """A contiguous array of the library's float type."""
+        return np.ascontiguousarray(np.asarray(a, dtype=self.ft))
 
     def param_grads64(self, family, inputs, lengths, *params, bandwidth=-1):
         """Per-element parameter gradients with the reference's per-cell terms summed
         in double (oracle only): SW [B,2] (gap, T), affine [B,3] (open, ext, T),
         DTW [B] (T)."""
-        if self.kind != "oracle":
+        if self.kind == "reference":
             raise RuntimeError("double-accumulated sums exist in the oracle only")
-        x = _f32(inputs)
+        x = self._a(inputs)
         B, L1, L2 = x.shape
         ln = _lengths(lengths, B, L1, L2)
         post = np.zeros_like(x)
@@ -162,33 +177,33 @@ class CpuKernels:
 
     # ---------------- linear-gap SW ----------------
     def sw_forward(self, scores, lengths, gap, T):
-        s = _f32(scores)
+        s = self._a(scores)
         B, L1, L2 = s.shape
         ln = _lengths(lengths, B, L1, L2)
-        alpha = np.zeros((B, (L1 + 1) * (L2 + 1)), np.float32)
-        part = np.zeros((B,), np.float32)
+        alpha = np.zeros((B, (L1 + 1) * (L2 + 1)), self.ft)
+        part = np.zeros((B,), self.ft)
         self.fn["sw_forward"](_p(s), _p(alpha), _p(part), _p(ln), B, L1, L2, gap, T)
         return alpha, part
 
     def sw_backward(self, alpha, scores, part, lengths, gap, T):
-        s = _f32(scores)
+        s = self._a(scores)
         B, L1, L2 = s.shape
         ln = _lengths(lengths, B, L1, L2)
         beta = np.zeros_like(alpha)
         post = np.zeros_like(s)
-        gg = np.zeros((B,), np.float32)
-        gt = np.zeros((B,), np.float32)
+        gg = np.zeros((B,), self.ft)
+        gt = np.zeros((B,), self.ft)
         self.fn["sw_backward"](_p(alpha), _p(s), _p(part), _p(beta), _p(post), _p(gg),
                                _p(gt), _p(ln), B, L1, L2, gap, T)
         return post, gg, gt
 
     def sw_hvp(self, alpha, scores, part, V, lengths, gap, T):
-        s = _f32(scores)
-        v = _f32(V)
+        s = self._a(scores)
+        v = self._a(V)
         B, L1, L2 = s.shape
         ln = _lengths(lengths, B, L1, L2)
         da = np.zeros_like(alpha)
-        dp = np.zeros((B,), np.float32)
+        dp = np.zeros((B,), self.ft)
         be = np.zeros_like(alpha)
         dbe = np.zeros_like(alpha)
         H = np.zeros_like(s)
@@ -197,10 +212,10 @@ class CpuKernels:
         return H, dp
 
     def sw_param_grad(self, alpha, scores, part, dS, lengths, gap, T, ptype):
-        s = _f32(scores)
+        s = self._a(scores)
         B, L1, L2 = s.shape
         ln = _lengths(lengths, B, L1, L2)
-        dS = _f32(dS)
+        dS = self._a(dS)
         U = np.zeros_like(alpha)
         be = np.zeros_like(alpha)
         W = np.zeros_like(alpha)
@@ -211,34 +226,34 @@ class CpuKernels:
 
     # ---------------- affine SW ----------------
     def swa_forward(self, scores, lengths, go, ge, T):
-        s = _f32(scores)
+        s = self._a(scores)
         B, L1, L2 = s.shape
         ln = _lengths(lengths, B, L1, L2)
-        alpha = np.zeros((B, 3 * (L1 + 1) * (L2 + 1)), np.float32)
-        part = np.zeros((B,), np.float32)
+        alpha = np.zeros((B, 3 * (L1 + 1) * (L2 + 1)), self.ft)
+        part = np.zeros((B,), self.ft)
         self.fn["swa_forward"](_p(s), _p(alpha), _p(part), _p(ln), B, L1, L2, go, ge, T)
         return alpha, part
 
     def swa_backward(self, alpha, scores, part, lengths, go, ge, T):
-        s = _f32(scores)
+        s = self._a(scores)
         B, L1, L2 = s.shape
         ln = _lengths(lengths, B, L1, L2)
         beta = np.zeros_like(alpha)
         post = np.zeros_like(s)
-        g_o = np.zeros((B,), np.float32)
-        g_e = np.zeros((B,), np.float32)
-        gt = np.zeros((B,), np.float32)
+        g_o = np.zeros((B,), self.ft)
+        g_e = np.zeros((B,), self.ft)
+        gt = np.zeros((B,), self.ft)
         self.fn["swa_backward"](_p(alpha), _p(s), _p(part), _p(beta), _p(post), _p(g_o),
                                 _p(g_e), _p(gt), _p(ln), B, L1, L2, go, ge, T)
         return post, g_o, g_e, gt
 
     def swa_hvp(self, alpha, scores, part, V, lengths, go, ge, T):
-        s = _f32(scores)
-        v = _f32(V)
+        s = self._a(scores)
+        v = self._a(V)
         B, L1, L2 = s.shape
         ln = _lengths(lengths, B, L1, L2)
         da = np.zeros_like(alpha)
-        dp = np.zeros((B,), np.float32)
+        dp = np.zeros((B,), self.ft)
         dbe = np.zeros_like(alpha)
         H = np.zeros_like(s)
         self.fn["swa_hvp"](_p(alpha), _p(s), _p(part), _p(v), _p(da), _p(dp), _p(dbe),
@@ -246,10 +261,10 @@ class CpuKernels:
         return H, dp
 
     def swa_param_grad(self, alpha, scores, part, dS, lengths, go, ge, T, ptype):
-        s = _f32(scores)
+        s = self._a(scores)
         B, L1, L2 = s.shape
         ln = _lengths(lengths, B, L1, L2)
-        dS = _f32(dS)
+        dS = self._a(dS)
         U = np.zeros_like(alpha)
         be = np.zeros_like(alpha)
         W = np.zeros_like(alpha)
@@ -260,32 +275,32 @@ class CpuKernels:
 
     # ---------------- DTW ----------------
     def dtw_forward(self, costs, lengths, T, bandwidth=-1):
-        c = _f32(costs)
+        c = self._a(costs)
         B, L1, L2 = c.shape
         ln = _lengths(lengths, B, L1, L2)
-        alpha = np.zeros((B, (L1 + 1) * (L2 + 1)), np.float32)
-        score = np.zeros((B,), np.float32)
+        alpha = np.zeros((B, (L1 + 1) * (L2 + 1)), self.ft)
+        score = np.zeros((B,), self.ft)
         self.fn["dtw_forward"](_p(c), _p(alpha), _p(score), _p(ln), B, L1, L2, T, bandwidth)
         return alpha, score
 
     def dtw_backward(self, alpha, costs, score, lengths, T, bandwidth=-1):
-        c = _f32(costs)
+        c = self._a(costs)
         B, L1, L2 = c.shape
         ln = _lengths(lengths, B, L1, L2)
         beta = np.zeros_like(alpha)
         post = np.zeros_like(c)
-        gt = np.zeros((B,), np.float32)
+        gt = np.zeros((B,), self.ft)
         self.fn["dtw_backward"](_p(alpha), _p(c), _p(score), _p(beta), _p(post), _p(gt),
                                 _p(ln), B, L1, L2, T, bandwidth)
         return post, gt
 
     def dtw_hvp(self, alpha, costs, score, V, lengths, T, bandwidth=-1):
-        c = _f32(costs)
-        v = _f32(V)
+        c = self._a(costs)
+        v = self._a(V)
         B, L1, L2 = c.shape
         ln = _lengths(lengths, B, L1, L2)
         da = np.zeros_like(alpha)
-        ds = np.zeros((B,), np.float32)
+        ds = np.zeros((B,), self.ft)
         be = np.zeros_like(alpha)
         dbe = np.zeros_like(alpha)
         H = np.zeros_like(c)
@@ -294,7 +309,7 @@ class CpuKernels:
         return H, ds
 
     def dtw_param_grad(self, alpha, costs, score, lengths, T, bandwidth=-1):
-        c = _f32(costs)
+        c = self._a(costs)
         B, L1, L2 = c.shape
         ln = _lengths(lengths, B, L1, L2)
         U = np.zeros_like(alpha)

@@ -339,3 +339,40 @@ def test_double_summed_parameter_gradients_against_math():
         _close(g[:, k], want, 2e-5, 2e-5, f"sums64 affine {k}")
     g = _k().param_grads64("dtw", c, ln, 0.7)
     _close(g, M.dtw(c, 0.7, -1, ln)[2], 2e-5, 2e-5, "sums64 dtw")
+
+
+# ------------------------------------------------------ the double-precision build
+
+def _k64():
+    return O.get("oracle64")
+
+
+@pytest.mark.parametrize("seed,B,L1,L2,T,lens", SECOND)
+def test_oracle64_against_math(seed, B, L1, L2, T, lens):
+    """liboracle64.so (the restatement compiled in double) matches the float64
+    autograd restatement to near double precision: values, marginals, HVPs and
+    every parameter Jacobian.  The GPU tests of long elements use it as the exact
+    value against which both the GPU's and the fp32 reference's errors are measured."""
+    s = _rand(seed + 40, (B, L1, L2)).astype(np.float64)
+    V = _rand(seed + 41, (B, L1, L2)).astype(np.float64)
+    c = np.abs(s) + 0.05
+    ln = None if lens is None else np.array(lens, np.int32)
+    k = _k64()
+    pairs = [(k.soft_sw(s, -0.8, T, ln), M.sw(s, -0.8, T, ln)),
+             (k.soft_sw_affine(s, -1.5, -0.4, T, ln), M.swa(s, -1.5, -0.4, T, ln)),
+             (k.soft_dtw(c, T, ln), M.dtw(c, T, -1, ln))]
+    for got, want in pairs:
+        for g, w in zip(got, want):
+            _close(g, w, 1e-9 * max(1.0, np.abs(w).max()), 0, "first order")
+    pairs = [(k.soft_sw_hvp(s, V, -0.8, T, ln), M.hvp("sw", s, V, (-0.8, T), ln)),
+             (k.soft_sw_affine_hvp(s, V, -1.5, -0.4, T, ln),
+              M.hvp("swa", s, V, (-1.5, -0.4, T), ln)),
+             (k.soft_dtw_hvp(c, V, T, ln), M.hvp("dtw", c, V, (T,), ln))]
+    pairs += [(k.soft_sw_param_jacobian(s, p, -0.8, T, ln),
+               M.param_jacobian("sw", s, (-0.8, T), p, ln)) for p in (0, 1)]
+    pairs += [(k.soft_sw_affine_param_jacobian(s, p, -1.5, -0.4, T, ln),
+               M.param_jacobian("swa", s, (-1.5, -0.4, T), p, ln)) for p in (0, 1, 2)]
+    pairs += [(k.soft_dtw_param_jacobian(c, T, ln), M.param_jacobian("dtw", c, (T,), 0, ln))]
+    for i, (got, want) in enumerate(pairs):
+        assert got.dtype == np.float64
+        _close(got, want, 1e-9 * max(1.0, np.abs(want).max()), 0, f"second order {i}")
