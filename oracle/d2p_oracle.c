@@ -15,7 +15,7 @@
  *
  * Pinning (no function here is unpinned): every entry point is checked
  *   - bit for bit against the reference's own CPU kernels compiled from
- *     /root/reference/src/{sw,sw_affine,dtw}/kernels_cpu.cpp by oracle/Makefile
+ *     /root/reference/src/{sw,sw_affine,dtw,nw}/kernels_cpu.cpp by oracle/Makefile
  *     (tests/test_oracle_reference.py), including low temperature, the exp clamp,
  *     large near-tied costs, ragged/empty lengths and DTW bands;
  *   - bit for bit against golden fixtures written from that build
@@ -66,6 +66,16 @@ static float lse2(float a, float b, float T) {   /* numerics.h:63-70 */
     kahan k = {0.0f, 0.0f};
     kadd(&k, xexp((a - m) / T));
     kadd(&k, xexp((b - m) / T));
+    return m + T * logf(k.s);
+}
+
+static float lse3(float a, float b, float c, float T) {   /* numerics.h:72-81 */
+    float m = fmax2(fmax2(a, b), c);
+    if (m <= NINF) return NINF;
+    kahan k = {0.0f, 0.0f};
+    kadd(&k, xexp((a - m) / T));
+    kadd(&k, xexp((b - m) / T));
+    kadd(&k, xexp((c - m) / T));
     return m + T * logf(k.s);
 }
 
@@ -1173,5 +1183,84 @@ void oracle_dtw_param_grad(const float* alpha, const float* costs, const float* 
             if (bu && wu > 0.0f) { be[AIDX(i - 1, j)] += bij * wu; ww[AIDX(i - 1, j)] += Wij * wu + bij * du; }
             if (bl && wl > 0.0f) { be[AIDX(i, j - 1)] += bij * wl; ww[AIDX(i, j - 1)] += Wij * wl + bij * dl; }
         }
+    }
+}
+
+/* =========================================================================
+ * Linear-gap soft Needleman-Wunsch (global alignment)
+ * ========================================================================= */
+
+/* nw/kernels_cpu.cpp:78-154: alpha[0,0] = 0, alpha[i,0] = i*gap, alpha[0,j] =
+ * j*gap, alpha[i,j] = LSE3(diag + s, up + gap, left + gap) with no sky term and no
+ * guards; the value is alpha[L1, L2]. */
+void oracle_nw_forward(const float* scores, float* alpha, float* score, const int* lengths,
+                       int B, int maxL1, int maxL2, float gap, float T) {
+    const size_t astride = (size_t)(maxL1 + 1) * (maxL2 + 1);
+    const size_t sstride = (size_t)maxL1 * maxL2;
+    const size_t acols = (size_t)maxL2 + 1, scols = (size_t)maxL2;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int b = 0; b < B; ++b) {
+        const float* s = scores + (size_t)b * sstride;
+        float* a = alpha + (size_t)b * astride;
+        const int L1 = lengths[2 * b], L2 = lengths[2 * b + 1];
+        for (size_t q = 0; q < astride; ++q) a[q] = NINF;
+        a[0] = 0.0f;
+        for (int i = 1; i <= L1; ++i) a[AIDX(i, 0)] = i * gap;
+        for (int j = 1; j <= L2; ++j) a[AIDX(0, j)] = j * gap;
+        FOR_DIAG_FWD(L1, L2, i, j) {
+            if (j < 1 || j > L2) continue;
+            const float sc = s[SIDX(i, j)];
+            a[AIDX(i, j)] = lse3(a[AIDX(i - 1, j - 1)] + sc, a[AIDX(i - 1, j)] + gap,
+                                 a[AIDX(i, j - 1)] + gap, T);
+        }
+        score[b] = a[AIDX(L1, L2)];
+    }
+}
+
+/* nw/kernels_cpu.cpp:160-265: beta[L1,L2] = 1; every visited cell passes beta on
+ * through its softmax weights (NINF options weigh 0) and its marginal is
+ * beta * w_diag.  dS/dgap adds the beta that reaches each boundary cell times the
+ * number of gaps it encodes (i for alpha[i,0], j for alpha[0,j]); dS/dT =
+ * (S - sum P*s - gap * dS/dgap) / T. */
+void oracle_nw_backward(const float* alpha, const float* scores, const float* score,
+                        float* beta, float* posteriors, float* grad_gap, float* grad_T,
+                        const int* lengths, int B, int maxL1, int maxL2, float gap, float T) {
+    const size_t astride = (size_t)(maxL1 + 1) * (maxL2 + 1);
+    const size_t sstride = (size_t)maxL1 * maxL2;
+    const size_t acols = (size_t)maxL2 + 1, scols = (size_t)maxL2;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int b = 0; b < B; ++b) {
+        const float* a = alpha + (size_t)b * astride;
+        const float* s = scores + (size_t)b * sstride;
+        float* be = beta + (size_t)b * astride;
+        float* post = posteriors + (size_t)b * sstride;
+        const float S = score[b];
+        const int L1 = lengths[2 * b], L2 = lengths[2 * b + 1];
+        memset(post, 0, sizeof(float) * sstride);
+        memset(be, 0, sizeof(float) * astride);
+        be[AIDX(L1, L2)] = 1.0f;
+        kahan gg = {0.0f, 0.0f}, ms = {0.0f, 0.0f};
+        FOR_DIAG_REV(L1, L2, i, j) {
+            if (j < 1 || j > L2) continue;
+            const float bij = be[AIDX(i, j)];
+            if (bij == 0.0f) continue;
+            const float sc = s[SIDX(i, j)];
+            float v[3] = {a[AIDX(i - 1, j - 1)] + sc, a[AIDX(i - 1, j)] + gap,
+                          a[AIDX(i, j - 1)] + gap};
+            float w[3];
+            softmax_w(v, w, 3, T);
+            const float pij = bij * w[0];
+            post[SIDX(i, j)] = pij;
+            kadd(&ms, pij * sc);
+            kadd(&gg, bij * (w[1] + w[2]));
+            if (w[0] > 0.0f) be[AIDX(i - 1, j - 1)] += bij * w[0];
+            if (w[1] > 0.0f) be[AIDX(i - 1, j)] += bij * w[1];
+            if (w[2] > 0.0f) be[AIDX(i, j - 1)] += bij * w[2];
+        }
+        for (int i = 1; i <= L1; ++i) kadd(&gg, be[AIDX(i, 0)] * (float)i);
+        for (int j = 1; j <= L2; ++j) kadd(&gg, be[AIDX(0, j)] * (float)j);
+        const float g = gg.s;
+        grad_gap[b] = g;
+        grad_T[b] = (S - (ms.s + g * gap)) / T;
     }
 }

@@ -75,6 +75,12 @@ void oracle_dtw_param_grad(const float* alpha, const float* costs, const float* 
  * the per-element parameter gradients also accumulated in double from the same
  * fp32 per-cell terms.  sums64: SW [B][2] (gap, T), affine [B][3] (open, ext, T),
  * DTW [B] (T). */
+void oracle_nw_forward(const float* scores, float* alpha, float* score, const int* lengths,
+                       int B, int maxL1, int maxL2, float gap, float T);
+void oracle_nw_backward(const float* alpha, const float* scores, const float* score,
+                        float* beta, float* posteriors, float* grad_gap, float* grad_T,
+                        const int* lengths, int B, int maxL1, int maxL2, float gap, float T);
+
 void oracle_sw_backward_sums64(const float* alpha, const float* scores, const float* partition,
                                float* beta, float* posteriors, double* sums64,
                                const int* lengths, int B, int L1, int L2, float gap, float T);

@@ -69,6 +69,10 @@ _SIGS = {
                 [_F, _F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _l]),
     "dtw_param_grad": ("oracle_dtw_param_grad", "dtw_param_grad_cpu",
                        [_F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _l]),
+    "nw_forward": ("oracle_nw_forward", "nw_forward_cpu",
+                   [_F, _F, _F, _I, _i, _i, _i, _f, _f]),
+    "nw_backward": ("oracle_nw_backward", "nw_backward_cpu",
+                    [_F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f]),
 }
 
 
@@ -320,7 +324,35 @@ class CpuKernels:
                                   _p(dP), _p(ln), B, L1, L2, T, bandwidth)
         return dP
 
+    # ---------------- linear-gap NW ----------------
+    def nw_forward(self, scores, lengths, gap, T):
+        s = self._a(scores)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        alpha = np.zeros((B, (L1 + 1) * (L2 + 1)), self.ft)
+        score = np.zeros((B,), self.ft)
+        self.fn["nw_forward"](_p(s), _p(alpha), _p(score), _p(ln), B, L1, L2, gap, T)
+        return alpha, score
+
+    def nw_backward(self, alpha, scores, score, lengths, gap, T):
+        s = self._a(scores)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        beta = np.zeros_like(alpha)
+        post = np.zeros_like(s)
+        gg = np.zeros((B,), self.ft)
+        gt = np.zeros((B,), self.ft)
+        self.fn["nw_backward"](_p(alpha), _p(s), _p(score), _p(beta), _p(post), _p(gg),
+                               _p(gt), _p(ln), B, L1, L2, gap, T)
+        return post, gg, gt
+
     # ---------------- binding-level composites ----------------
+    def soft_nw(self, scores, gap=-1.0, T=1.0, lengths=None):
+        """value, marginals, grad_gap, grad_T (src/nw/torch_cpu.cpp forward + backward)."""
+        alpha, score = self.nw_forward(scores, lengths, gap, T)
+        post, gg, gt = self.nw_backward(alpha, scores, score, lengths, gap, T)
+        return score, post, gg, gt
+
     def soft_sw(self, scores, gap=-1.0, T=1.0, lengths=None):
         """value, marginals, grad_gap, grad_T (src/sw/torch_cpu.cpp:114-165)."""
         alpha, part = self.sw_forward(scores, lengths, gap, T)

@@ -54,6 +54,23 @@ def sw_value(s, gap, T):
     return _lse(cells, T)
 
 
+def nw_value(s, gap, T):
+    """Global alignment: alpha[0,0] = 0, alpha[i,0] = i*gap, alpha[0,j] = j*gap,
+    alpha[i,j] = LSE(diag + s, up + gap, left + gap); the value is alpha[L1, L2]."""
+    L1, L2 = s.shape
+    a = [[None] * (L2 + 1) for _ in range(L1 + 1)]
+    a[0][0] = torch.zeros((), dtype=D) * gap
+    for i in range(1, L1 + 1):
+        a[i][0] = i * gap
+    for j in range(1, L2 + 1):
+        a[0][j] = j * gap
+    for i in range(1, L1 + 1):
+        for j in range(1, L2 + 1):
+            a[i][j] = _lse([a[i - 1][j - 1] + s[i - 1, j - 1], a[i - 1][j] + gap,
+                            a[i][j - 1] + gap], T)
+    return a[L1][L2]
+
+
 def swa_value(s, go, ge, T):
     L1, L2 = s.shape
     M = [[None] * (L2 + 1) for _ in range(L1 + 1)]
@@ -174,6 +191,11 @@ def sw(x, gap, T, lengths=None):
 def swa(x, go, ge, T, lengths=None):
     """(value, marginals, dS/dopen, dS/dext, dS/dT) for affine SW."""
     return _first_order(lambda s, o, e, t: swa_value(s, o, e, t), x, (go, ge, T), lengths)
+
+
+def nw(x, gap, T, lengths=None):
+    """(value, marginals, dS/dgap, dS/dT) for linear NW."""
+    return _first_order(lambda s, g, t: nw_value(s, g, t), x, (gap, T), lengths)
 
 
 def dtw(x, T, bw=-1, lengths=None):
@@ -307,3 +329,25 @@ def dtw_brute(c, T):
 
     rec(0, 0, float(c[0, 0]))
     return -T * math.log(acc)
+
+
+def nw_brute(s, gap, T):
+    """S = T log sum over global paths (0,0) -> (L1,L2) exp(score / T): each path
+    moves diagonally (+ the score of the cell it enters), down or right (+ gap)."""
+    L1, L2 = s.shape
+    acc = 0.0
+
+    def rec(i, j, sc):
+        nonlocal acc
+        if i == L1 and j == L2:
+            acc += math.exp(sc / T)
+            return
+        if i < L1 and j < L2:
+            rec(i + 1, j + 1, sc + float(s[i, j]))
+        if i < L1:
+            rec(i + 1, j, sc + gap)
+        if j < L2:
+            rec(i, j + 1, sc + gap)
+
+    rec(0, 0, 0.0)
+    return T * math.log(acc)

@@ -93,6 +93,8 @@ def test_values_against_path_enumeration(shape, T):
     S_sw = M.sw_brute(s[0], -0.7, T)
     S_swa = M.swa_brute(s[0], -1.3, -0.4, T)
     S_dtw = M.dtw_brute(c[0], T)
+    S_nw = M.nw_brute(s[0], -0.7, T)
+    _close(_k().soft_nw(s, -0.7, T)[0], [S_nw], 2e-6, 2e-6, "NW vs paths")
     _close(_k().soft_sw(s, -0.7, T)[0], [S_sw], 2e-6, 2e-6, "SW vs paths")
     _close(_k().soft_sw_affine(s, -1.3, -0.4, T)[0], [S_swa], 2e-6, 2e-6, "affine vs paths")
     _close(_k().soft_dtw(c, T)[0], [S_dtw], 2e-6, 2e-6, "DTW vs paths")
@@ -101,6 +103,22 @@ def test_values_against_path_enumeration(shape, T):
     assert float(M.sw_value(t(s[0]), t(-0.7), t(T))) == pytest.approx(S_sw, rel=1e-12)
     assert float(M.swa_value(t(s[0]), t(-1.3), t(-0.4), t(T))) == pytest.approx(S_swa, rel=1e-12)
     assert float(M.dtw_value(t(c[0]), t(T))) == pytest.approx(S_dtw, rel=1e-12)
+    assert float(M.nw_value(t(s[0]), t(-0.7), t(T))) == pytest.approx(S_nw, rel=1e-12)
+
+
+@pytest.mark.parametrize("s", [-3.0, 0.0, 2.5])
+@pytest.mark.parametrize("gap", [-1.0, 0.5])
+@pytest.mark.parametrize("T", [0.2, 1.0])
+def test_nw_1x1_closed_form(s, gap, T):
+    """1x1 global alignment: the diagonal (s) or a down and a right move in either
+    order (2 gap each): S = T log(e^{s/T} + 2 e^{2 gap/T}); P = the diagonal's share;
+    dS/dgap = 2 (1 - P)."""
+    x = np.full((1, 1, 1), s, np.float32)
+    S, P, gg, gt = _k().soft_nw(x, gap, T)
+    ed, eg = math.exp(s / T), 2 * math.exp(2 * gap / T)
+    _close(S, [T * math.log(ed + eg)], 1e-5, 1e-6, "value")
+    _close(P, [[[ed / (ed + eg)]]], 1e-6, 0, "marginal")
+    _close(gg, [2 * eg / (ed + eg)], 1e-5, 1e-5, "dS/dgap")
 
 
 # ------------------------------------------------------------------ float64 restatement
@@ -136,6 +154,18 @@ def test_swa_first_order_against_math(seed, B, L1, L2, T, lens):
     _close(post, m, 2e-5, 0, "marginals")
     _close(g_o, mo, 1e-4, 1e-4, "dS/dopen")
     _close(g_e, me, 1e-4, 1e-4, "dS/dext")
+    _close(gt, mt, 1e-4, 1e-4, "dS/dT")
+
+
+@pytest.mark.parametrize("seed,B,L1,L2,T,lens", FIRST)
+def test_nw_first_order_against_math(seed, B, L1, L2, T, lens):
+    s = _rand(seed + 60, (B, L1, L2))
+    ln = None if lens is None else np.array(lens, np.int32)
+    v, post, gg, gt = _k().soft_nw(s, -0.8, T, ln)
+    mv, m, mg, mt = M.nw(s, -0.8, T, ln)
+    _close(v, mv, 1e-5, 1e-6, "value")
+    _close(post, m, 2e-5, 0, "marginals")
+    _close(gg, mg, 1e-4, 1e-4, "dS/dgap")
     _close(gt, mt, 1e-4, 1e-4, "dS/dT")
 
 
@@ -360,7 +390,8 @@ def test_oracle64_against_math(seed, B, L1, L2, T, lens):
     k = _k64()
     pairs = [(k.soft_sw(s, -0.8, T, ln), M.sw(s, -0.8, T, ln)),
              (k.soft_sw_affine(s, -1.5, -0.4, T, ln), M.swa(s, -1.5, -0.4, T, ln)),
-             (k.soft_dtw(c, T, ln), M.dtw(c, T, -1, ln))]
+             (k.soft_dtw(c, T, ln), M.dtw(c, T, -1, ln)),
+             (k.soft_nw(s, -0.8, T, ln), M.nw(s, -0.8, T, ln))]
     for got, want in pairs:
         for g, w in zip(got, want):
             _close(g, w, 1e-9 * max(1.0, np.abs(w).max()), 0, "first order")

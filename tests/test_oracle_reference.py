@@ -1,7 +1,7 @@
 """The CPU oracle against the reference's own CPU kernels, bit for bit.
 
 ``oracle/_ref/libd2p_ref.so`` is compiled by ``oracle/Makefile`` from
-/root/reference/src/{sw,sw_affine,dtw}/kernels_cpu.cpp where those sources
+/root/reference/src/{sw,sw_affine,dtw,nw}/kernels_cpu.cpp where those sources
 exist (this container); both libraries are built with -ffp-contract=off, so
 every output of every function must be identical, including the regimes only
 the reference's own rounding fixes: low temperature, |x / T| beyond the
@@ -53,6 +53,13 @@ def test_sw_bit_exact(seed, B, L1, L2, scale, gap, T, lens):
     for p in (0, 1):
         _same(o.soft_sw_param_jacobian(s, p, gap, T, lens),
               r.soft_sw_param_jacobian(s, p, gap, T, lens), f"jacobian {p}")
+
+
+@pytest.mark.parametrize("seed,B,L1,L2,scale,gap,T,lens", SW_CASES)
+def test_nw_bit_exact(seed, B, L1, L2, scale, gap, T, lens):
+    o, r = O.get("oracle"), O.get("reference")
+    s = _rand(seed + 70, (B, L1, L2), scale)
+    _same(o.soft_nw(s, gap, T, lens), r.soft_nw(s, gap, T, lens), "soft_nw")
 
 
 @pytest.mark.parametrize("seed,B,L1,L2,scale,gap,T,lens", SW_CASES)
