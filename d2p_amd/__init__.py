@@ -1,7 +1,7 @@
 """d2p_amd -- MI355X (gfx950) soft-alignment dynamic programming for PyTorch-ROCm.
 
-Drop-in for the soft Smith-Waterman (linear/affine gap) and soft-DTW part of
-orikata-bio/d2p: same Python API (``soft_sw``, ``soft_sw_affine``,
+Drop-in for the soft Smith-Waterman (linear/affine gap), soft-DTW and
+(first-order) linear-gap soft Needleman-Wunsch part of orikata-bio/d2p: same Python API (``soft_sw``, ``soft_sw_affine``,
 ``soft_dtw``, the ``nn.Module`` wrappers, ``ops``, the legacy flat names) and
 the same ``torch.ops.d2p`` operator schemas, computed by hand-written HIP
 kernels for CDNA4.  Tensors must live on the HIP device.
@@ -11,6 +11,7 @@ from . import _compile  # noqa: F401  (fake/meta and autocast registrations)
 
 from .sw import soft_sw, soft_sw_affine, SWResult, SoftSW, SoftSWAffine
 from .dtw import soft_dtw, DTWResult, SoftDTW
+from .nw import soft_nw, NWResult, SoftNW
 from . import ops
 
 # legacy flat names (reference d2p/__init__.py:120-139)
@@ -29,6 +30,9 @@ soft_dtw_with_grads = _ops.soft_dtw_with_grads
 soft_dtw_hvp = _ops.soft_dtw_hvp
 soft_dtw_param_jacobian = _ops.soft_dtw_param_jacobian
 soft_dtw_backward_full = _ops.soft_dtw_backward_full
+soft_nw_float = _ops.soft_nw_float
+soft_nw_with_grads = _ops.soft_nw_with_grads
+soft_nw_forward = _ops.soft_nw_float
 
 __all__ = [
     "soft_sw", "soft_sw_affine", "SWResult", "SoftSW", "SoftSWAffine",
@@ -39,4 +43,5 @@ __all__ = [
     "soft_sw_affine_param_jacobian", "soft_sw_affine_backward_full",
     "soft_dtw_float", "soft_dtw_with_grads", "soft_dtw_hvp", "soft_dtw_param_jacobian",
     "soft_dtw_backward_full",
+    "soft_nw", "NWResult", "SoftNW", "soft_nw_float", "soft_nw_with_grads", "soft_nw_forward",
 ]

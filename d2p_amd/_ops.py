@@ -120,6 +120,14 @@ sw_affine_marginals_grad_gap_open = _wrap("sw_affine_marginals_grad_gap_open")
 sw_affine_marginals_grad_gap_ext = _wrap("sw_affine_marginals_grad_gap_ext")
 sw_affine_marginals_grad_temp = _wrap("sw_affine_marginals_grad_temp")
 
+# linear-gap Needleman-Wunsch (first order)
+soft_nw = _wrap("soft_nw")
+soft_nw_float = _wrap("soft_nw_float")
+soft_nw_with_grads = _wrap("soft_nw_with_grads")
+nw_forward = _wrap("nw_forward")
+nw_forward_t = _wrap("nw_forward_t")
+nw_value_grad_params = _wrap("nw_value_grad_params")
+
 # soft DTW
 soft_dtw = _wrap("soft_dtw")
 soft_dtw_float = _wrap("soft_dtw_float")

@@ -18,15 +18,19 @@ using wf::choose_split;
 int check_shape(int B, int max_L1, int max_L2, float temperature);
 
 // Forward sweep: alpha table, last rows and partition[B] (status words reset).
+// global: soft Needleman-Wunsch (gap boundary rows, no sky term); partition[B] then
+// receives the value alpha[L1, L2].
 int launch_forward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
-                   float gap, float T, const Layout& ws, float* partition, hipStream_t st);
+                   float gap, float T, const Layout& ws, float* partition, hipStream_t st,
+                   bool global = false);
 
 // Reverse sweep: marginals, dS/dgap and dS/dT per element, from a forward's table.
 // precise: sum dS/dgap and dS/dT in double (for the second-order paths).
+// global: soft Needleman-Wunsch, from a global forward's table and value.
 int launch_backward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                     float gap, float T, const Layout& ws, const float* partition,
                     float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
-                    bool precise = false);
+                    bool precise = false, bool global = false);
 
 }  // namespace sw
 }  // namespace d2p_amd

@@ -41,6 +41,13 @@ constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do 
 // after that part's progress word allows it; the last stripe of a part publishes its
 // own word two chunks behind its stores.  G == 1 writes the partition; G > 1 writes
 // the part's (max, scaled sum) for the partition merge.
+//
+// NWG: global alignment (soft Needleman-Wunsch, /root/reference/src/nw/kernels_cpu.cpp:
+// 78-154): no sky term, row 0 and column 0 hold j*gap and i*gap (the cells left of
+// column 0 carry their row's i*gap, so the left and diagonal neighbours of column 0
+// come out of the same registers), and `partition` receives the terminal cell
+// alpha[L1, L2] instead of the LSE over all cells.
+template <bool NWG = false>
 __global__ void __launch_bounds__(NW * 64)
 sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                   float* __restrict__ alpha_sk, float* __restrict__ brow,
@@ -52,6 +59,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red_m[NW], red_z[NW];
+    __shared__ float terminal;   // NWG: alpha[L1, L2]
     int b, part;
     split_decode(blockIdx.x, G, b, part);
     if (b >= B) return;
@@ -71,6 +79,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
 
     if (lane == 0) prog[wave] = -1;
     if (G == 1 && threadIdx.x == 0) *st = 0;               // G > 1: reset before the launch
+    if (NWG && threadIdx.x == 0) terminal = kNINF;
     __syncthreads();
 
     const int L1 = min(max(lengths[2 * b], 0), L1max);
@@ -104,8 +113,11 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
         const float* brow_up = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
         const bool x_in = l == 0 && part > 0;      // row above from the previous part
         const bool x_out = l == NL - 1 && has_next;  // last row feeds the next part
+        // the cells left of column 0: NINF, or (NWG) the row's boundary i*gap
+        const float left0 = NWG ? (float)(i0 + lane + 1) * gap : kNINF;
+        const bool last_row = NWG && i0 + lane == L1 - 1;
 #pragma unroll
-        for (int t = -APAD; t < 0; ++t) lane_store(out + t * 64, ul4, kNINF);
+        for (int t = -APAD; t < 0; ++t) lane_store(out + t * 64, ul4, left0);
         wave_lds_sync();   // the previous stripe's tile reads are complete
         const uint32_t tile_lds = lds_address(tiles);
         const uint32_t row_lds = lds_address(rbufs);
@@ -121,7 +133,9 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             issue_row(0);
         }
         dma_quads<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
-        float cur = kNINF, up_prev = kNINF;
+        // NWG: lane r starts beside column 0 of its row, its diagonal beside column 0
+        // of the row above (alpha[0,0] = 0 for lane 0 of the first stripe)
+        float cur = left0, up_prev = NWG ? (float)(i0 + lane) * gap : kNINF;
 
         for (int k = 0; k < nch; ++k) {
             const int t0 = k * P;
@@ -137,10 +151,13 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             const float* tile = tiles + (k & 1) * Tile::FLOATS;
             float sv[P], av[P];
             read_quads<P, 1>(tile, lane, sv);
-            // lane 0's up values: column t0+j sits in lane j (ring slot = producer step)
+            // lane 0's up values: column t0+j sits in lane j (ring slot = producer step);
+            // above the first stripe, row 0: NINF, or (NWG) alpha[0, t0+j+1] = (t0+j+1)*gap
             float rreg = kNINF;
             if (s > 0 && lane < P)
                 rreg = x_in ? rbufs[(k & 1) * 64 + lane] : ring_in[ring_index(t0 + lane + 63, R)];
+            else if (NWG && s == 0 && lane < P)
+                rreg = (float)(t0 + lane + 1) * gap;
             if (k + 1 < nch) {
                 if (x_in) {
                     const int need = min(k + 1 + lead(P), nch);
@@ -169,15 +186,29 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                     const float vd = diag + sv[u];
                     const float vu = up + gap;
                     const float vl = cur + gap;
-                    const float m = fmaxf(fmaxf(vd, vu), fmaxf(vl, sv[u]));
-                    const float sum = (fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c)) +
-                                      (fast_exp2((vl - m) * c) + fast_exp2((sv[u] - m) * c));
-                    const float a = m + tl * fast_log2(sum);
+                    float a;
+                    if (NWG) {
+                        const float m = fmaxf(fmaxf(vd, vu), vl);
+                        const float sum = (fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c)) +
+                                          fast_exp2((vl - m) * c);
+                        a = m + tl * fast_log2(sum);
+                    } else {
+                        const float m = fmaxf(fmaxf(vd, vu), fmaxf(vl, sv[u]));
+                        const float sum =
+                            (fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c)) +
+                            (fast_exp2((vl - m) * c) + fast_exp2((sv[u] - m) * c));
+                        a = m + tl * fast_log2(sum);
+                    }
                     if (FULL) {
                         cur = a;
                     } else {
-                        const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
-                        cur = ok ? a : kNINF;
+                        const int col = t - lane;
+                        const bool ok = (unsigned)col < (unsigned)L2eff;
+                        // NWG: the cells left of column 0 keep the row's boundary
+                        cur = ok ? a : (NWG && col < 0 ? left0 : kNINF);
+                        // the terminal cell never lies in a FULL chunk (lane 63's
+                        // column stays below L2 - 1 there)
+                        if (NWG && ok && last_row && col == L2 - 1) terminal = a;
                     }
                     lane_store(outc + u * 64, ul4, cur);
                     pub[u] = cur;
@@ -186,7 +217,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             };
             if (i0 + 63 < L1 && t0 >= 63 && t0 + P <= L2) steps(std::true_type{});
             else steps(std::false_type{});
-            acc.add_block<P>(av, c);
+            if (!NWG) acc.add_block<P>(av, c);
             // the stripe's last row (lane 63) by step, contiguous, for the reverse sweep
             // of the stripe below and the next part; one store instruction
             wave_lds_sync();
@@ -209,6 +240,14 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
         }
     }
 
+    if (NWG) {
+        // the value: the terminal cell, written by the part that owns the last stripe
+        // (part 0 for an element without stripes, whose value is its boundary)
+        __syncthreads();
+        const bool owner = NS > 0 ? (NL > 0 && s_begin + NL == NS) : part == 0;
+        if (threadIdx.x == 0 && owner) partition[b] = NS > 0 ? terminal : (float)(L1 + L2) * gap;
+        return;
+    }
     // partition: merge lanes, waves, and (once per element) the cell (0,0) whose alpha is 0
     wave_merge_lse(acc, c);
     if (lane == 0) { red_m[wave] = acc.m; red_z[wave] = acc.z; }
@@ -229,7 +268,10 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
 
 // PRECISE: accumulate dS/dgap and dS/dT per lane in double (second-order callers,
 // whose Jacobians amplify errors in these sums).
-template <int P, bool PRECISE = false>
+// NWG: global alignment (/root/reference/src/nw/kernels_cpu.cpp:160-265): beta starts
+// at 1 in the terminal cell only, the marginal is beta * w_diag, and the flows into
+// row 0 and column 0 (whose alphas encode j*gap and i*gap) add flow * gaps to dS/dgap.
+template <int P, bool PRECISE = false, bool NWG = false>
 __global__ void __launch_bounds__(NW * 64)
 sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                    const float* __restrict__ alpha_sk, const float* __restrict__ brow,
@@ -309,6 +351,12 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         const int s = s_begin + NL - 1 - q;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
+        // NWG: the terminal cell (L1, L2) starts with beta = 1; the flows into column 0
+        // count i (row i0+lane+1, left) and i - 1 (diagonal) gaps, those into row 0
+        // (first stripe, lane 0) the column's index
+        const int term_step = (NWG && i0 + lane == L1 - 1) ? L2 - 1 + lane : -1000000;
+        const float gi = (float)(i0 + lane + 1);
+        const bool top = NWG && s == 0 && lane == 0;
         // alpha tables of this stripe and of the one above, from step -APAD
         const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * NT * 64;
         const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
@@ -373,9 +421,12 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             A[1] = A[P + 1];
 #pragma unroll
             for (int j = 0; j < P; ++j) A[j + 2] = buf[ABUF + rows_row<P, -1>(j) * 64 + lane];
-            // lane j: alpha of the row above at lane-63 step t_hi - j + 63
+            // lane j: alpha of the row above at lane-63 step t_hi - j + 63 (column
+            // t_hi - j); above the first stripe, row 0: NINF, or (NWG) (column + 1) * gap
             float bv = buf[RBUF + lane];
             bv = (s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1) ? bv : kNINF;
+            if (NWG && s == 0)
+                bv = (lane <= P && t_hi - lane + 1 >= 0) ? (float)(t_hi - lane + 1) * gap : kNINF;
             // Contributions from the stripe below for lane 63.  The producer (lane 0 of
             // stripe s+1) wrote the pair for its column c into slot (nsteps-1-c) % R;
             // lane 63 at step u needs column t_hi-u-63 (up) and t_hi-u-62 (diagonal),
@@ -434,15 +485,22 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 // rounding is ~2^75 at the 1e30 sentinels of cells outside the element,
                 // so m is floored far below any real alpha (those cells' e_k become 0
                 // and their flows are selected away, not multiplied).
-                const float m = fmaxf(fmaxf(vd, vu), fmaxf(fmaxf(vl, sc), -1e20f));
+                const float m = NWG ? fmaxf(fmaxf(vd, vu), fmaxf(vl, -1e20f))
+                                    : fmaxf(fmaxf(vd, vu), fmaxf(fmaxf(vl, sc), -1e20f));
                 const float mc = m * c;
                 const float e0 = fast_exp2(fmaf(vd, c, -mc)), e1 = fast_exp2(fmaf(vu, c, -mc));
-                const float e2 = fast_exp2(fmaf(vl, c, -mc)), e3 = fast_exp2(fmaf(sc, c, -mc));
+                const float e2 = fast_exp2(fmaf(vl, c, -mc));
+                const float e3 = NWG ? 0.0f : fast_exp2(fmaf(sc, c, -mc));
                 const float e03 = e0 + e3, e12 = e1 + e2;
                 const float rin = fast_rcp(e12 + e03);
-                float lp = (a0 - S) * c;   // subtract first: exact for nearby values
-                lp = lp < 0.0f ? lp : 0.0f;
-                const float binit = fast_exp2(lp);
+                float binit;
+                if (NWG) {
+                    binit = t == term_step ? 1.0f : 0.0f;
+                } else {
+                    float lp = (a0 - S) * c;   // subtract first: exact for nearby values
+                    lp = lp < 0.0f ? lp : 0.0f;
+                    binit = fast_exp2(lp);
+                }
                 // reference accumulation order: init, diagonal, left, up successor
                 const float beta = ((binit + in_diag) + in_left) + in_up;
                 const bool live = ok && (beta <= 3.0e38f);    // skips inf / NaN like the reference
@@ -452,6 +510,14 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 buf[obase_lane + u] = pv;
                 if (PRECISE) gs[u] = (Acc)ou + (Acc)ol;
                 else gs[u] = br * e12;
+                if (NWG) {
+                    // flows into the boundary: column 0 (left: i gaps, diagonal: i - 1)
+                    // and row 0 (up: column + 1 gaps, diagonal: column); FULL chunks can
+                    // hold column 0 (lane 63) and row 1
+                    const int col = t - lane;
+                    if (col == 0) gs[u] += (Acc)(ol * gi) + (Acc)(od * (gi - 1.0f));
+                    if (top) gs[u] += (Acc)(ou * (float)(col + 1)) + (Acc)(od * (float)col);
+                }
                 ps[u] = (Acc)(pv * sc);
                 pub[u] = make_float2(ou, od);
                 // successor contributions for the next steps; lane 63 takes the ring
@@ -499,6 +565,8 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     if (threadIdx.x == 0) {
         Acc g = 0, p = 0;
         for (int w = 0; w < NW; ++w) { g += red_g[w]; p += red_p[w]; }
+        // NWG: an element without cells is its boundary, (L1 + L2) gaps (part 0 counts it)
+        if (NWG && NS == 0 && part == 0) g += (Acc)(L1 + L2);
         if (G == 1) {
             grad_gap[b] = (float)g;
             grad_T[b] = (float)(((Acc)S - (p + g * (Acc)gap)) / (Acc)T);
@@ -579,7 +647,8 @@ int check_shape(int B, int max_L1, int max_L2, float temperature) {
 }
 
 int launch_forward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
-                   float gap, float T, const Layout& ws, float* partition, hipStream_t st) {
+                   float gap, float T, const Layout& ws, float* partition, hipStream_t st,
+                   bool global) {
     const int ns = (max_L1 + 63) / 64;
     const Split sp = choose_split(B, max_L1, ws, max_stripes_forward(max_L1, max_L2));
     const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
@@ -587,9 +656,19 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     const uint32_t epoch = next_epoch();
     if (sp.G > 1 && wf::launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
-    D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel,
+    if (global) {
+        D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel<true>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        D2P_LAUNCH("nw_forward", sw_forward_kernel<true>, dim3(wf::split_grid(B, sp.G)),
+                   dim3(wf::NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
+                   ws.status, ws.fflag, ws.fpart, B, max_L1, max_L2, ns, gap, T, R, sp.G, sp.SPW,
+                   epoch);
+        D2P_HIP(hipGetLastError());
+        return D2P_OK;   // the owner part writes the value: no merge
+    }
+    D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel<false>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH("sw_forward", sw_forward_kernel, dim3(wf::split_grid(B, sp.G)),
+    D2P_LAUNCH("sw_forward", sw_forward_kernel<false>, dim3(wf::split_grid(B, sp.G)),
                dim3(wf::NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
                ws.status, ws.fflag, ws.fpart, B, max_L1, max_L2, ns, gap, T, R, sp.G, sp.SPW,
                epoch);
@@ -599,7 +678,7 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
     return D2P_OK;
 }
 
-template <int P, bool PRECISE>
+template <int P, bool PRECISE, bool NWG>
 int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                       float gap, float T, const Layout& ws, const float* partition,
                       float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
@@ -608,9 +687,10 @@ int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1
     const size_t lds = lds_backward_r(R, P);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     const uint32_t epoch = next_epoch();
-    D2P_HIP(hipFuncSetAttribute((const void*)sw_backward_kernel<P, PRECISE>,
+    D2P_HIP(hipFuncSetAttribute((const void*)sw_backward_kernel<P, PRECISE, NWG>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH("sw_backward", (sw_backward_kernel<P, PRECISE>), dim3(wf::split_grid(B, sp.G)),
+    D2P_LAUNCH(NWG ? "nw_backward" : "sw_backward", (sw_backward_kernel<P, PRECISE, NWG>),
+               dim3(wf::split_grid(B, sp.G)),
                dim3(wf::NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
                marginals, grad_gap, grad_T, ws.status, ws.trash, ws.bflag, ws.flows, ws.bpart, B,
                max_L1, max_L2, ns, gap, T, R, sp.G, sp.SPW, epoch);
@@ -624,16 +704,20 @@ int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1
 int launch_backward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                     float gap, float T, const Layout& ws, const float* partition,
                     float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
-                    bool precise) {
+                    bool precise, bool global) {
     const Split sp = choose_split(B, max_L1, ws, max_stripes_backward(max_L1, max_L2));
     const int rows = sp.G > 1 ? sp.SPW * 64 : max_L1;
     const int R = ring_backward(rows, max_L2);
     const int P = backward_chunk(rows, max_L2);
-#define D2P_SW_BWD(P_, PR_)                                                                   \
-    launch_backward_p<P_, PR_>(scores, lengths, B, max_L1, max_L2, gap, T, ws, partition,    \
-                               marginals, grad_gap, grad_T, st, sp, R)
-    if (P == 16) return precise ? D2P_SW_BWD(16, true) : D2P_SW_BWD(16, false);
-    return precise ? D2P_SW_BWD(8, true) : D2P_SW_BWD(8, false);
+#define D2P_SW_BWD(P_, PR_, G_)                                                               \
+    launch_backward_p<P_, PR_, G_>(scores, lengths, B, max_L1, max_L2, gap, T, ws, partition, \
+                                   marginals, grad_gap, grad_T, st, sp, R)
+    if (global) {
+        if (P == 16) return precise ? D2P_SW_BWD(16, true, true) : D2P_SW_BWD(16, false, true);
+        return precise ? D2P_SW_BWD(8, true, true) : D2P_SW_BWD(8, false, true);
+    }
+    if (P == 16) return precise ? D2P_SW_BWD(16, true, false) : D2P_SW_BWD(16, false, false);
+    return precise ? D2P_SW_BWD(8, true, false) : D2P_SW_BWD(8, false, false);
 #undef D2P_SW_BWD
 }
 
@@ -680,4 +764,29 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
     if (r != D2P_OK) return r;
     return sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
                                partition, marginals, grad_gap, grad_T, st);
+}
+
+extern "C" size_t d2p_nw_workspace_bytes(int B, int max_L1, int max_L2) {
+    return d2p_sw_workspace_bytes(B, max_L1, max_L2);
+}
+
+extern "C" int d2p_nw_forward_marginals(const float* scores, const int* lengths, int B,
+                                        int max_L1, int max_L2, float gap, float temperature,
+                                        float* value, float* marginals, float* grad_gap,
+                                        float* grad_T, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+    const int rc = sw::check_shape(B, max_L1, max_L2, temperature);
+    if (rc != D2P_OK) return rc;
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(scores && lengths && value && marginals && grad_gap && grad_T,
+                "null pointer argument");
+    const size_t need = d2p_nw_workspace_bytes(B, max_L1, max_L2);
+    D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 1, true);
+    int r = sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws, value,
+                               st, true);
+    if (r != D2P_OK) return r;
+    return sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws, value,
+                               marginals, grad_gap, grad_T, st, false, true);
 }

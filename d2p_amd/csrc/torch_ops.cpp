@@ -360,6 +360,122 @@ Tensor sw_marginals_grad_temp(Tensor s, double g, double t, c10::optional<Tensor
 }
 
 // ---------------------------------------------------------------------------
+// linear-gap soft Needleman-Wunsch (global alignment)
+// ---------------------------------------------------------------------------
+
+SwOut nw_run(const Tensor& scores, const Tensor& lengths, const Dims& d, float gap, float T) {
+    auto opt = scores.options();
+    SwOut o{torch::empty({d.B}, opt), torch::empty({d.B, d.L1, d.L2}, opt),
+            torch::empty({d.B}, opt), torch::empty({d.B}, opt)};
+    const size_t ws_bytes = d2p_nw_workspace_bytes(d.B, d.L1, d.L2);
+    Tensor ws = workspace(ws_bytes, scores);
+    D2P_CALL(d2p_nw_forward_marginals(
+        scores.data_ptr<float>(), lengths.data_ptr<int>(), d.B, d.L1, d.L2, gap, T,
+        o.partition.data_ptr<float>(), o.marginals.data_ptr<float>(),
+        o.grad_gap.data_ptr<float>(), o.grad_T.data_ptr<float>(), ws.data_ptr(), ws_bytes,
+        current_stream()));
+    return o;
+}
+
+// Autograd semantics of SoftNWCUDAFunction (/root/reference/src/nw/torch_cuda.cpp:115-260):
+// outputs {value, marginals}; d value / d scores = marginals.  The marginal path
+// (second order) is not part of this build's NW family: a defined marginal cotangent
+// raises.
+tensor_list nw_autograd_forward(AutogradContext* ctx, const Tensor& scores,
+                                const Tensor& lengths, double gap, double temperature) {
+    ctx->set_materialize_grads(false);
+    CHECK_INPUT_DEV(scores);
+    Dims d = checked_dims(scores, "NW");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    SwOut o = nw_run(scores, lengths, d, (float)gap, (float)temperature);
+    ctx->save_for_backward({o.marginals, o.grad_gap, o.grad_T});
+    return {o.partition, o.marginals};
+}
+
+tensor_list nw_autograd_backward(AutogradContext* ctx, const tensor_list& grads, bool want_gap,
+                                 bool want_T) {
+    auto saved = ctx->get_saved_variables();
+    Tensor marg = saved[0], ggap = saved[1], gT = saved[2];
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(marg.device());
+    Tensor grad_value = grads[0], grad_marg = grads[1];
+    TORCH_CHECK(!(grad_marg.defined() && grad_marg.numel() > 0),
+                "soft_nw: gradients through the alignment (marginals) output are not "
+                "implemented by d2p_amd; only the value path is differentiable");
+    Tensor grad_scores, grad_gap, grad_T;
+    if (grad_value.defined() && grad_value.numel() > 0) {
+        grad_scores = scale_by_batch(marg, grad_value);
+        if (want_gap) grad_gap = grad_param_sum(grad_value, ggap);
+        if (want_T) grad_T = grad_param_sum(grad_value, gT);
+    }
+    return {grad_scores, grad_gap, grad_T};
+}
+
+class SoftNWFloatFunction : public torch::autograd::Function<SoftNWFloatFunction> {
+   public:
+    static tensor_list forward(AutogradContext* ctx, Tensor scores, Tensor lengths, double gap,
+                               double temperature) {
+        return nw_autograd_forward(ctx, scores, lengths, gap, temperature);
+    }
+    static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
+        auto g = nw_autograd_backward(ctx, grads, false, false);
+        return {g[0], Tensor(), Tensor(), Tensor()};
+    }
+};
+
+class SoftNWTensorFunction : public torch::autograd::Function<SoftNWTensorFunction> {
+   public:
+    static tensor_list forward(AutogradContext* ctx, Tensor scores, Tensor gap_t, Tensor temp_t,
+                               Tensor lengths, double gap, double temperature) {
+        return nw_autograd_forward(ctx, scores, lengths, gap, temperature);
+    }
+    static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
+        auto g = nw_autograd_backward(ctx, grads, ctx->needs_input_grad(1),
+                                      ctx->needs_input_grad(2));
+        return {g[0], g[1], g[2], Tensor(), Tensor(), Tensor()};
+    }
+};
+
+std::vector<Tensor> soft_nw_t(Tensor scores, Tensor gap, Tensor temperature, Tensor lengths) {
+    CHECK_INPUT_DEV(scores);
+    Dims d = checked_dims(scores, "NW");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    const float g = scalar_value(gap, "gap");
+    const float T = scalar_value(temperature, "temperature");
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    return SoftNWTensorFunction::apply(scores, gap, temperature, l, g, T);
+}
+
+std::vector<Tensor> soft_nw_float(Tensor scores, double gap, double temperature,
+                                  c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    Dims d = checked_dims(scores, "NW");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    return SoftNWFloatFunction::apply(scores, l, gap, temperature);
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> soft_nw_with_grads(Tensor scores, double gap,
+                                                              double temperature,
+                                                              c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    Dims d = checked_dims(scores, "NW");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    SwOut o = nw_run(scores, l, d, (float)gap, (float)temperature);
+    return {o.partition, o.marginals, o.grad_gap, o.grad_T};
+}
+
+std::vector<Tensor> nw_forward(Tensor s, double g, double t, c10::optional<Tensor> l) {
+    return soft_nw_float(s, g, t, l);
+}
+std::vector<Tensor> nw_forward_t(Tensor s, Tensor g, Tensor t, Tensor l) { return soft_nw_t(s, g, t, l); }
+std::tuple<Tensor, Tensor> nw_value_grad_params(Tensor s, double g, double t,
+                                                c10::optional<Tensor> l) {
+    auto r = soft_nw_with_grads(s, g, t, l);
+    return {std::get<2>(r), std::get<3>(r)};
+}
+
+// ---------------------------------------------------------------------------
 // affine-gap soft Smith-Waterman
 // ---------------------------------------------------------------------------
 
@@ -834,6 +950,14 @@ TORCH_LIBRARY(d2p, m) {
     m.def("sw_affine_marginals_grad_temp(Tensor scores, float gap_open, float gap_ext, float temp, Tensor? lengths) -> Tensor");
 
     // /root/reference/src/dtw/registry.cpp:127-132
+    // /root/reference/src/nw/registry.cpp:35-45 (first-order operators)
+    m.def("soft_nw(Tensor scores, Tensor gap, Tensor temperature, Tensor lengths) -> Tensor[]");
+    m.def("soft_nw_float(Tensor scores, float gap, float temperature, Tensor? lengths) -> Tensor[]");
+    m.def("soft_nw_with_grads(Tensor scores, float gap, float temperature, Tensor? lengths) -> (Tensor, Tensor, Tensor, Tensor)");
+    m.def("nw_forward(Tensor scores, float gap, float temp, Tensor? lengths) -> Tensor[]");
+    m.def("nw_forward_t(Tensor scores, Tensor gap, Tensor temp, Tensor lengths) -> Tensor[]");
+    m.def("nw_value_grad_params(Tensor scores, float gap, float temp, Tensor? lengths) -> (Tensor, Tensor)");
+
     m.def("soft_dtw(Tensor costs, Tensor temperature, Tensor lengths, int bandwidth) -> Tensor[]");
     m.def("soft_dtw_float(Tensor costs, float temperature, Tensor? lengths, int? bandwidth) -> Tensor[]");
     m.def("soft_dtw_with_grads(Tensor costs, float temperature, Tensor? lengths, int? bandwidth) -> (Tensor, Tensor, Tensor)");
@@ -856,6 +980,13 @@ TORCH_LIBRARY_IMPL(d2p, CUDA, m) {
     m.impl("sw_marginals_hvp", sw_marginals_hvp);
     m.impl("sw_marginals_grad_gap", sw_marginals_grad_gap);
     m.impl("sw_marginals_grad_temp", sw_marginals_grad_temp);
+
+    m.impl("soft_nw", soft_nw_t);
+    m.impl("soft_nw_float", soft_nw_float);
+    m.impl("soft_nw_with_grads", soft_nw_with_grads);
+    m.impl("nw_forward", nw_forward);
+    m.impl("nw_forward_t", nw_forward_t);
+    m.impl("nw_value_grad_params", nw_value_grad_params);
 
     m.impl("soft_sw_affine", swa_t);
     m.impl("soft_sw_affine_float", swa_float);
@@ -893,6 +1024,10 @@ TORCH_LIBRARY_IMPL(d2p, AutogradCUDA, m) {
     m.impl("sw_affine_forward_t", swa_t);
     m.impl("soft_dtw", dtw_t);
     m.impl("soft_dtw_float", dtw_float);
+    m.impl("soft_nw", soft_nw_t);
+    m.impl("soft_nw_float", soft_nw_float);
+    m.impl("nw_forward", nw_forward);
+    m.impl("nw_forward_t", nw_forward_t);
 }
 
 namespace {
@@ -907,7 +1042,8 @@ const char* const kAllOps[] = {
     "sw_affine_value_grad_params", "sw_affine_marginals_backward", "sw_affine_marginals_hvp",
     "sw_affine_marginals_grad_gap_open", "sw_affine_marginals_grad_gap_ext",
     "sw_affine_marginals_grad_temp", "soft_dtw", "soft_dtw_float", "soft_dtw_with_grads",
-    "soft_dtw_hvp", "soft_dtw_param_jacobian", "soft_dtw_backward_full"};
+    "soft_dtw_hvp", "soft_dtw_param_jacobian", "soft_dtw_backward_full", "soft_nw",
+    "soft_nw_float", "soft_nw_with_grads", "nw_forward", "nw_forward_t", "nw_value_grad_params"};
 }  // namespace
 
 TORCH_LIBRARY_IMPL(d2p, CPU, m) {

@@ -18,4 +18,5 @@ from .._ops import (  # noqa: F401
     sw_affine_marginals_grad_gap_ext, sw_affine_marginals_grad_temp,
     soft_dtw, soft_dtw_float, soft_dtw_with_grads, soft_dtw_hvp, soft_dtw_param_jacobian,
     soft_dtw_backward_full,
+    soft_nw, soft_nw_float, soft_nw_with_grads, nw_forward, nw_forward_t, nw_value_grad_params,
 )

@@ -162,6 +162,27 @@ int d2p_swa_backward_full(const float* scores, const float* grad_alignment, cons
                           size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Linear-gap soft Needleman-Wunsch (global alignment)
+ * ------------------------------------------------------------------------- */
+
+/* Workspace bytes needed by d2p_nw_forward_marginals (status words first). */
+size_t d2p_nw_workspace_bytes(int B, int max_L1, int max_L2);
+
+/* Forward value and marginals in one call.
+ * Replaces the pair nw_forward + nw_backward (/root/reference/src/nw/kernels.cuh:97-140)
+ * as sequenced by SoftNWCUDAFunction::forward (/root/reference/src/nw/torch_cuda.cpp:
+ * 115-180); the CPU kernels restated are /root/reference/src/nw/kernels_cpu.cpp:78-265.
+ *   scores    [B, max_L1, max_L2]  input
+ *   value     [B]                  out: alpha[L1, L2] (alpha[i,0] = i*gap, alpha[0,j] = j*gap)
+ *   marginals [B, max_L1, max_L2]  out: dvalue/dscores (zero in padding)
+ *   grad_gap  [B]                  out: dvalue/dgap (boundary cells included)
+ *   grad_T    [B]                  out: dvalue/dtemperature */
+int d2p_nw_forward_marginals(const float* scores, const int* lengths, int B, int max_L1,
+                             int max_L2, float gap, float temperature, float* value,
+                             float* marginals, float* grad_gap, float* grad_T, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Soft dynamic time warping (optional Sakoe-Chiba band)
  * ------------------------------------------------------------------------- */
 

@@ -25,6 +25,8 @@ SIGNATURES = {
     "d2p_swa_workspace_bytes": (_z, [_i, _i, _i]),
     "d2p_swa_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _f, _f, _p, _p, _p, _p, _p, _p,
                                        _z, _p]),
+    "d2p_nw_workspace_bytes": (_z, [_i, _i, _i]),
+    "d2p_nw_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _f, _p, _p, _p, _p, _p, _z, _p]),
     "d2p_dtw_workspace_bytes": (_z, [_i, _i, _i]),
     "d2p_dtw_workspace_bytes_banded": (_z, [_i, _i, _i, _i]),
     "d2p_dtw_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _i, _p, _p, _p, _p, _z, _p]),
@@ -115,6 +117,22 @@ def _check_status(ws, B):
     st = ctypes.c_int(0)
     check(lib().d2p_sw_status(ptr(ws), B, ctypes.byref(st), stream()))
     assert st.value == 0, f"pipeline status {st.value}: a stripe wait hit its spin bound"
+
+
+def nw_forward_marginals(scores, lengths, gap, T):
+    """Linear-gap NW: (value, marginals, grad_gap, grad_T) through the C ABI."""
+    import torch
+    B, L1, L2 = scores.shape
+    dev = scores.device
+    lengths = _lengths(lengths, B, L1, L2, dev)
+    outs = [torch.empty(B, device=dev), torch.empty(B, L1, L2, device=dev),
+            torch.empty(B, device=dev), torch.empty(B, device=dev)]
+    nbytes = lib().d2p_nw_workspace_bytes(B, L1, L2)
+    ws = _workspace(nbytes, dev)
+    check(lib().d2p_nw_forward_marginals(ptr(scores), ptr(lengths), B, L1, L2, gap, T,
+                                         *[ptr(o) for o in outs], ptr(ws), nbytes, stream()))
+    _check_status(ws, B)
+    return tuple(outs)
 
 
 def swa_forward_marginals(scores, lengths, go, ge, T):
