@@ -14,7 +14,7 @@ metric's line; same output format): ``c3`` affine gap, ragged lengths;
 [16, 4096, 4096]; ``c5hvp`` the Hessian-vector product on the C5 shapes;
 ``c4band`` C4 under a Sakoe-Chiba band of 16; ``dtwlong`` soft DTW [16, 4096,
 4096] under a band of 64 (the banded sweeps; cells are the full tables' cells,
-as the reference sweeps them).
+as the reference sweeps them); ``c2nw`` soft Needleman-Wunsch on the C2 shapes.
 
 Prints one JSON line with:
   * ``roofline``: the dominant kernel (largest share of the timed region),
@@ -136,6 +136,17 @@ def make_c5(hvp=False):
         extra={"B": B, "L1": L, "L2": L})
 
 
+def make_c2nw():
+    cfg = make_c2()
+    cfg.update(
+        name="c2nw",
+        algo_kernel={"nw_forward": 4 * cfg["cells"], "nw_backward": 4 * cfg["cells"],
+                     "scale_by_batch": 8 * cfg["cells"]},
+        workload="C2 shapes, global alignment: soft_nw(scores [256,512,512], gap=-1, T=1), "
+                 "fwd (value+marginals) + value.sum().backward()")
+    return cfg
+
+
 def _band_cells(B, L1, L2, bw):
     """Cells of the Sakoe-Chiba band |j - i*L2/L1| <= bw, per the reference's float
     test (/root/reference/src/dtw/kernels_cpu.cpp:24-29)."""
@@ -185,7 +196,7 @@ def make_dtwlong():
 
 CONFIGS = {"c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5,
            "c5hvp": lambda: make_c5(hvp=True), "c4band": make_c4band,
-           "dtwlong": make_dtwlong}
+           "dtwlong": make_dtwlong, "c2nw": make_c2nw}
 
 
 def make_step(cfg, dev):
@@ -205,6 +216,10 @@ def make_step(cfg, dev):
         def step():
             c = x["costs"].detach().requires_grad_(True)
             d2p_amd.soft_dtw(c, temperature=0.1).cost.sum().backward()
+    elif name == "c2nw":
+        def step():
+            s = x["scores"].detach().requires_grad_(True)
+            d2p_amd.soft_nw(s, gap=-1.0, temperature=1.0).score.sum().backward()
     elif name in ("c4band", "dtwlong"):
         T, bw = cfg["temperature"], cfg["bandwidth"]
 
@@ -294,6 +309,14 @@ def cpu_baseline_config(cfg, max_elems):
             a, sc = k.dtw_forward(x["costs"], None, T, bw)
             k.dtw_backward(a, x["costs"], sc, None, T, bw)
             return k.dtw_backward(a, x["costs"], sc, None, T, bw)[0]
+        what = "fwd + 2x bwd DP + scale"
+    elif name == "c2nw":
+        cells = x["scores"].size
+
+        def step():
+            a, v = k.nw_forward(x["scores"], None, -1.0, 1.0)
+            k.nw_backward(a, x["scores"], v, None, -1.0, 1.0)
+            return k.nw_backward(a, x["scores"], v, None, -1.0, 1.0)[0]
         what = "fwd + 2x bwd DP + scale"
     elif name == "c5":
         cells = x["scores"].size
@@ -434,7 +457,7 @@ def main():
             out["cpu_baseline"] = cpu_baseline(cfg["inputs"]["scores"].numpy())
         else:
             sample = {"c3": 64, "c4": 512, "c5": 16, "c5hvp": 16, "c4band": 512,
-                      "dtwlong": 16}[cfg["name"]]
+                      "dtwlong": 16, "c2nw": 256}[cfg["name"]]
             out["cpu_baseline"] = cpu_baseline_config(cfg, sample)
     print(json.dumps(out), flush=True)
 
