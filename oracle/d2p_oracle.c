@@ -1264,3 +1264,141 @@ void oracle_nw_backward(const float* alpha, const float* scores, const float* sc
         grad_T[b] = (S - (ms.s + g * gap)) / T;
     }
 }
+
+/* nw/kernels_cpu.cpp:278-444: forward tangent da = sum w (da_pred + V [diag]) from
+ * zero boundary tangents; reverse (beta, dbeta) from (1, 0) at the terminal cell,
+ * skipping cells with beta == 0 and |dbeta| < 1e-20; H = dbeta w_diag +
+ * beta dw_diag with dw_k = w_k (dv_k - E_w[dv]) / T. */
+void oracle_nw_hvp(const float* alpha, const float* scores, const float* score, const float* V,
+                   float* d_alpha, float* d_score, float* beta, float* d_beta, float* H,
+                   const int* lengths, int B, int maxL1, int maxL2, float gap, float T) {
+    const size_t astride = (size_t)(maxL1 + 1) * (maxL2 + 1);
+    const size_t sstride = (size_t)maxL1 * maxL2;
+    const size_t acols = (size_t)maxL2 + 1, scols = (size_t)maxL2;
+    (void)score;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int b = 0; b < B; ++b) {
+        const float* a = alpha + (size_t)b * astride;
+        const float* s = scores + (size_t)b * sstride;
+        const float* v = V + (size_t)b * sstride;
+        float* da = d_alpha + (size_t)b * astride;
+        float* be = beta + (size_t)b * astride;
+        float* dbe = d_beta + (size_t)b * astride;
+        float* h = H + (size_t)b * sstride;
+        const int L1 = lengths[2 * b], L2 = lengths[2 * b + 1];
+        memset(da, 0, sizeof(float) * astride);
+        memset(be, 0, sizeof(float) * astride);
+        memset(dbe, 0, sizeof(float) * astride);
+        memset(h, 0, sizeof(float) * sstride);
+        FOR_DIAG_FWD(L1, L2, i, j) {
+            if (j < 1 || j > L2) continue;
+            const float sc = s[SIDX(i, j)], vij = v[SIDX(i, j)];
+            float lv[3] = {a[AIDX(i - 1, j - 1)] + sc, a[AIDX(i - 1, j)] + gap,
+                           a[AIDX(i, j - 1)] + gap};
+            float w[3];
+            softmax_w(lv, w, 3, T);
+            const float dd = da[AIDX(i - 1, j - 1)] + vij, du = da[AIDX(i - 1, j)],
+                        dl = da[AIDX(i, j - 1)];
+            da[AIDX(i, j)] = w[0] * dd + w[1] * du + w[2] * dl;
+        }
+        d_score[b] = da[AIDX(L1, L2)];
+        be[AIDX(L1, L2)] = 1.0f;
+        dbe[AIDX(L1, L2)] = 0.0f;
+        FOR_DIAG_REV(L1, L2, i, j) {
+            if (j < 1 || j > L2) continue;
+            const float sc = s[SIDX(i, j)], vij = v[SIDX(i, j)];
+            const float bij = be[AIDX(i, j)], dbij = dbe[AIDX(i, j)];
+            if (bij == 0.0f && fabsf(dbij) < 1e-20f) continue;
+            float lv[3] = {a[AIDX(i - 1, j - 1)] + sc, a[AIDX(i - 1, j)] + gap,
+                           a[AIDX(i, j - 1)] + gap};
+            float w[3];
+            softmax_w(lv, w, 3, T);
+            const float dd = da[AIDX(i - 1, j - 1)] + vij, du = da[AIDX(i - 1, j)],
+                        dl = da[AIDX(i, j - 1)];
+            const float E = w[0] * dd + w[1] * du + w[2] * dl;
+            const float wd = w[0] * (dd - E) / T, wu = w[1] * (du - E) / T,
+                        wl = w[2] * (dl - E) / T;
+            h[SIDX(i, j)] = dbij * w[0] + bij * wd;
+            if (w[0] > 0.0f) { be[AIDX(i - 1, j - 1)] += bij * w[0]; dbe[AIDX(i - 1, j - 1)] += dbij * w[0] + bij * wd; }
+            if (w[1] > 0.0f) { be[AIDX(i - 1, j)] += bij * w[1]; dbe[AIDX(i - 1, j)] += dbij * w[1] + bij * wu; }
+            if (w[2] > 0.0f) { be[AIDX(i, j - 1)] += bij * w[2]; dbe[AIDX(i, j - 1)] += dbij * w[2] + bij * wl; }
+        }
+    }
+}
+
+/* nw/kernels_cpu.cpp:450-642: dP/dtheta for theta = gap (param_type 0; boundary
+ * tangents i and j, +1 on the up / left candidates) or T (1; + (alpha - E_w[v]) / T
+ * in the tangent, + w_k (E_w[v] - v_k) / T^2 in the weight tangents).  The
+ * terminal beta is constant, so dS/dtheta does not enter. */
+void oracle_nw_param_grad(const float* alpha, const float* scores, const float* score,
+                          const float* dS_dtheta, float* U, float* beta, float* W, float* dP,
+                          const int* lengths, int B, int maxL1, int maxL2, float gap, float T,
+                          int ptype) {
+    const size_t astride = (size_t)(maxL1 + 1) * (maxL2 + 1);
+    const size_t sstride = (size_t)maxL1 * maxL2;
+    const size_t acols = (size_t)maxL2 + 1, scols = (size_t)maxL2;
+    (void)score;
+    (void)dS_dtheta;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int b = 0; b < B; ++b) {
+        const float* a = alpha + (size_t)b * astride;
+        const float* s = scores + (size_t)b * sstride;
+        float* u = U + (size_t)b * astride;
+        float* be = beta + (size_t)b * astride;
+        float* w = W + (size_t)b * astride;
+        float* dp = dP + (size_t)b * sstride;
+        const int L1 = lengths[2 * b], L2 = lengths[2 * b + 1];
+        memset(u, 0, sizeof(float) * astride);
+        memset(be, 0, sizeof(float) * astride);
+        memset(w, 0, sizeof(float) * astride);
+        memset(dp, 0, sizeof(float) * sstride);
+        if (ptype == 0) {
+            for (int i = 1; i <= L1; ++i) u[AIDX(i, 0)] = (float)i;
+            for (int j = 1; j <= L2; ++j) u[AIDX(0, j)] = (float)j;
+        }
+        FOR_DIAG_FWD(L1, L2, i, j) {
+            if (j < 1 || j > L2) continue;
+            const float sc = s[SIDX(i, j)];
+            float lv[3] = {a[AIDX(i - 1, j - 1)] + sc, a[AIDX(i - 1, j)] + gap,
+                           a[AIDX(i, j - 1)] + gap};
+            float wt[3];
+            softmax_w(lv, wt, 3, T);
+            float ud = u[AIDX(i - 1, j - 1)], uu = u[AIDX(i - 1, j)], ul = u[AIDX(i, j - 1)];
+            if (ptype == 0) { uu += 1.0f; ul += 1.0f; }
+            float x = wt[0] * ud + wt[1] * uu + wt[2] * ul;
+            if (ptype == 1) {
+                const float Ev = wt[0] * lv[0] + wt[1] * lv[1] + wt[2] * lv[2];
+                x += (a[AIDX(i, j)] - Ev) / T;
+            }
+            u[AIDX(i, j)] = x;
+        }
+        be[AIDX(L1, L2)] = 1.0f;
+        w[AIDX(L1, L2)] = 0.0f;
+        FOR_DIAG_REV(L1, L2, i, j) {
+            if (j < 1 || j > L2) continue;
+            const float sc = s[SIDX(i, j)];
+            const float bij = be[AIDX(i, j)], Wij = w[AIDX(i, j)];
+            if (bij == 0.0f && fabsf(Wij) < 1e-20f) continue;
+            float lv[3] = {a[AIDX(i - 1, j - 1)] + sc, a[AIDX(i - 1, j)] + gap,
+                           a[AIDX(i, j - 1)] + gap};
+            float wt[3];
+            softmax_w(lv, wt, 3, T);
+            float ud = u[AIDX(i - 1, j - 1)], uu = u[AIDX(i - 1, j)], ul = u[AIDX(i, j - 1)];
+            if (ptype == 0) { uu += 1.0f; ul += 1.0f; }
+            const float Eu = wt[0] * ud + wt[1] * uu + wt[2] * ul;
+            float dd = wt[0] * (ud - Eu) / T, du = wt[1] * (uu - Eu) / T,
+                  dl = wt[2] * (ul - Eu) / T;
+            if (ptype == 1) {
+                const float Ev = wt[0] * lv[0] + wt[1] * lv[1] + wt[2] * lv[2];
+                const float iT2 = 1.0f / (T * T);
+                dd += wt[0] * (Ev - lv[0]) * iT2;
+                du += wt[1] * (Ev - lv[1]) * iT2;
+                dl += wt[2] * (Ev - lv[2]) * iT2;
+            }
+            dp[SIDX(i, j)] = Wij * wt[0] + bij * dd;
+            if (wt[0] > 0.0f) { be[AIDX(i - 1, j - 1)] += bij * wt[0]; w[AIDX(i - 1, j - 1)] += Wij * wt[0] + bij * dd; }
+            if (wt[1] > 0.0f) { be[AIDX(i - 1, j)] += bij * wt[1]; w[AIDX(i - 1, j)] += Wij * wt[1] + bij * du; }
+            if (wt[2] > 0.0f) { be[AIDX(i, j - 1)] += bij * wt[2]; w[AIDX(i, j - 1)] += Wij * wt[2] + bij * dl; }
+        }
+    }
+}

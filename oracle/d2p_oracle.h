@@ -81,6 +81,14 @@ void oracle_nw_backward(const float* alpha, const float* scores, const float* sc
                         float* beta, float* posteriors, float* grad_gap, float* grad_T,
                         const int* lengths, int B, int maxL1, int maxL2, float gap, float T);
 
+void oracle_nw_hvp(const float* alpha, const float* scores, const float* score, const float* V,
+                   float* d_alpha, float* d_score, float* beta, float* d_beta, float* H,
+                   const int* lengths, int B, int maxL1, int maxL2, float gap, float T);
+void oracle_nw_param_grad(const float* alpha, const float* scores, const float* score,
+                          const float* dS_dtheta, float* U, float* beta, float* W, float* dP,
+                          const int* lengths, int B, int maxL1, int maxL2, float gap, float T,
+                          int ptype);
+
 void oracle_sw_backward_sums64(const float* alpha, const float* scores, const float* partition,
                                float* beta, float* posteriors, double* sums64,
                                const int* lengths, int B, int L1, int L2, float gap, float T);

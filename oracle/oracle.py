@@ -73,6 +73,10 @@ _SIGS = {
                    [_F, _F, _F, _I, _i, _i, _i, _f, _f]),
     "nw_backward": ("oracle_nw_backward", "nw_backward_cpu",
                     [_F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f]),
+    "nw_hvp": ("oracle_nw_hvp", "nw_hvp_cpu",
+               [_F, _F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f]),
+    "nw_param_grad": ("oracle_nw_param_grad", "nw_param_grad_cpu",
+                      [_F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f, _i]),
 }
 
 
@@ -346,7 +350,42 @@ class CpuKernels:
                                _p(gt), _p(ln), B, L1, L2, gap, T)
         return post, gg, gt
 
+    def nw_hvp(self, alpha, scores, score, V, lengths, gap, T):
+        s = self._a(scores)
+        v = self._a(V)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        da = np.zeros_like(alpha)
+        ds = np.zeros((B,), self.ft)
+        be = np.zeros_like(alpha)
+        dbe = np.zeros_like(alpha)
+        H = np.zeros_like(s)
+        self.fn["nw_hvp"](_p(alpha), _p(s), _p(score), _p(v), _p(da), _p(ds), _p(be), _p(dbe),
+                          _p(H), _p(ln), B, L1, L2, gap, T)
+        return H, ds
+
+    def nw_param_grad(self, alpha, scores, score, lengths, gap, T, ptype):
+        s = self._a(scores)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        dS = np.zeros((B,), self.ft)   # unused: the terminal beta is constant
+        U = np.zeros_like(alpha)
+        be = np.zeros_like(alpha)
+        W = np.zeros_like(alpha)
+        dP = np.zeros_like(s)
+        self.fn["nw_param_grad"](_p(alpha), _p(s), _p(score), _p(dS), _p(U), _p(be), _p(W),
+                                 _p(dP), _p(ln), B, L1, L2, gap, T, ptype)
+        return dP
+
     # ---------------- binding-level composites ----------------
+    def soft_nw_hvp(self, scores, V, gap=-1.0, T=1.0, lengths=None):
+        alpha, score = self.nw_forward(scores, lengths, gap, T)
+        return self.nw_hvp(alpha, scores, score, V, lengths, gap, T)[0]
+
+    def soft_nw_param_jacobian(self, scores, ptype, gap=-1.0, T=1.0, lengths=None):
+        alpha, score = self.nw_forward(scores, lengths, gap, T)
+        return self.nw_param_grad(alpha, scores, score, lengths, gap, T, ptype)
+
     def soft_nw(self, scores, gap=-1.0, T=1.0, lengths=None):
         """value, marginals, grad_gap, grad_T (src/nw/torch_cpu.cpp forward + backward)."""
         alpha, score = self.nw_forward(scores, lengths, gap, T)

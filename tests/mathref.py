@@ -249,6 +249,8 @@ def _value_fn(family, bw):
         return lambda s, o, e, t: swa_value(s, o, e, t)
     if family == "dtw":
         return lambda c, t: dtw_value(c, t, bw)
+    if family == "nw":
+        return lambda s, g, t: nw_value(s, g, t)
     raise ValueError(family)
 
 

@@ -205,7 +205,8 @@ def test_hvp_against_math(seed, B, L1, L2, T, lens):
             (_k().soft_sw_hvp(s, V, -0.8, T, ln), M.hvp("sw", s, V, (-0.8, T), ln)),
             (_k().soft_sw_affine_hvp(s, V, -1.5, -0.4, T, ln),
              M.hvp("swa", s, V, (-1.5, -0.4, T), ln)),
-            (_k().soft_dtw_hvp(c, V, T, ln), M.hvp("dtw", c, V, (T,), ln))):
+            (_k().soft_dtw_hvp(c, V, T, ln), M.hvp("dtw", c, V, (T,), ln)),
+            (_k().soft_nw_hvp(s, V, -0.8, T, ln), M.hvp("nw", s, V, (-0.8, T), ln))):
         _close(got, want, 1e-4 * max(1.0, np.abs(want).max()), 0, "hvp")
 
 
@@ -219,6 +220,8 @@ def test_param_jacobians_against_math(seed, B, L1, L2, T, lens):
     pairs += [(_k().soft_sw_affine_param_jacobian(s, p, -1.5, -0.4, T, ln),
                M.param_jacobian("swa", s, (-1.5, -0.4, T), p, ln)) for p in (0, 1, 2)]
     pairs += [(_k().soft_dtw_param_jacobian(c, T, ln), M.param_jacobian("dtw", c, (T,), 0, ln))]
+    pairs += [(_k().soft_nw_param_jacobian(s, p, -0.8, T, ln),
+               M.param_jacobian("nw", s, (-0.8, T), p, ln)) for p in (0, 1)]
     for i, (got, want) in enumerate(pairs):
         _close(got, want, 2e-4 * max(1.0, np.abs(want).max()), 0, f"jacobian {i}")
 
@@ -404,6 +407,9 @@ def test_oracle64_against_math(seed, B, L1, L2, T, lens):
     pairs += [(k.soft_sw_affine_param_jacobian(s, p, -1.5, -0.4, T, ln),
                M.param_jacobian("swa", s, (-1.5, -0.4, T), p, ln)) for p in (0, 1, 2)]
     pairs += [(k.soft_dtw_param_jacobian(c, T, ln), M.param_jacobian("dtw", c, (T,), 0, ln))]
+    pairs += [(k.soft_nw_hvp(s, V, -0.8, T, ln), M.hvp("nw", s, V, (-0.8, T), ln))]
+    pairs += [(k.soft_nw_param_jacobian(s, p, -0.8, T, ln),
+               M.param_jacobian("nw", s, (-0.8, T), p, ln)) for p in (0, 1)]
     for i, (got, want) in enumerate(pairs):
         assert got.dtype == np.float64
         _close(got, want, 1e-9 * max(1.0, np.abs(want).max()), 0, f"second order {i}")

@@ -60,6 +60,11 @@ def test_nw_bit_exact(seed, B, L1, L2, scale, gap, T, lens):
     o, r = O.get("oracle"), O.get("reference")
     s = _rand(seed + 70, (B, L1, L2), scale)
     _same(o.soft_nw(s, gap, T, lens), r.soft_nw(s, gap, T, lens), "soft_nw")
+    V = _rand(seed + 71, (B, L1, L2))
+    _same(o.soft_nw_hvp(s, V, gap, T, lens), r.soft_nw_hvp(s, V, gap, T, lens), "nw hvp")
+    for p in (0, 1):
+        _same(o.soft_nw_param_jacobian(s, p, gap, T, lens),
+              r.soft_nw_param_jacobian(s, p, gap, T, lens), f"nw jacobian {p}")
 
 
 @pytest.mark.parametrize("seed,B,L1,L2,scale,gap,T,lens", SW_CASES)
