@@ -33,6 +33,9 @@ soft_dtw_backward_full = _ops.soft_dtw_backward_full
 soft_nw_float = _ops.soft_nw_float
 soft_nw_with_grads = _ops.soft_nw_with_grads
 soft_nw_forward = _ops.soft_nw_float
+soft_nw_hvp = _ops.soft_nw_hvp
+soft_nw_param_jacobian = _ops.soft_nw_param_jacobian
+soft_nw_backward_full = _ops.soft_nw_backward_full
 
 __all__ = [
     "soft_sw", "soft_sw_affine", "SWResult", "SoftSW", "SoftSWAffine",
@@ -44,4 +47,5 @@ __all__ = [
     "soft_dtw_float", "soft_dtw_with_grads", "soft_dtw_hvp", "soft_dtw_param_jacobian",
     "soft_dtw_backward_full",
     "soft_nw", "NWResult", "SoftNW", "soft_nw_float", "soft_nw_with_grads", "soft_nw_forward",
+    "soft_nw_hvp", "soft_nw_param_jacobian", "soft_nw_backward_full",
 ]

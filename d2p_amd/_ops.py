@@ -127,6 +127,13 @@ soft_nw_with_grads = _wrap("soft_nw_with_grads")
 nw_forward = _wrap("nw_forward")
 nw_forward_t = _wrap("nw_forward_t")
 nw_value_grad_params = _wrap("nw_value_grad_params")
+soft_nw_hvp = _wrap("soft_nw_hvp")
+soft_nw_param_jacobian = _wrap("soft_nw_param_jacobian")
+soft_nw_backward_full = _wrap("soft_nw_backward_full")
+nw_marginals_backward = _wrap("nw_marginals_backward")
+nw_marginals_hvp = _wrap("nw_marginals_hvp")
+nw_marginals_grad_gap = _wrap("nw_marginals_grad_gap")
+nw_marginals_grad_temp = _wrap("nw_marginals_grad_temp")
 
 # soft DTW
 soft_dtw = _wrap("soft_dtw")

@@ -44,7 +44,7 @@ enum Mode { HVP = 0, GAP = 1, TEMP = 2 };
 
 // ------------------------------------------------------------------ tangent sweep
 
-template <int MODE, int P>
+template <int MODE, int P, bool NWG = false>
 __global__ void __launch_bounds__(NW * 64)
 sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                   const int* __restrict__ lengths, const float* __restrict__ alpha_sk,
@@ -138,16 +138,22 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             }
         };
 
-        // tangents of the column-0 boundary are 0
+        // NWG: the cells left of column 0 hold the row's boundary alpha i*gap, whose
+        // tangent is i for the gap Jacobian and 0 otherwise (SW: NINF and 0)
+        const float aleft = NWG ? (float)(i0 + lane + 1) * gap : kNINF;
+        const float xleft = (NWG && MODE == GAP) ? (float)(i0 + lane + 1) : 0.0f;
+        const int term_step = (NWG && i0 + lane == L1 - 1) ? L2 - 1 + lane : -1000000;
+        // tangents of the column-0 boundary
 #pragma unroll
-        for (int t = -APAD; t < 0; ++t) lane_store(tout + t * 64, ul4, 0.0f);
+        for (int t = -APAD; t < 0; ++t) lane_store(tout + t * 64, ul4, xleft);
         wave_lds_sync();
         if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
         issue_chunk(0);
         float Aw[P + 2];
-        Aw[P] = kNINF;        // alpha at steps -2, -1: column-0 boundary
-        Aw[P + 1] = kNINF;
-        float cur = 0.0f, up_prev = 0.0f;   // tangents: previous step, its up value
+        Aw[P] = aleft;        // alpha at steps -2, -1: column-0 boundary
+        Aw[P + 1] = aleft;
+        // tangents: previous step, its up value (NWG gap Jacobian: the boundary's)
+        float cur = xleft, up_prev = (NWG && MODE == GAP) ? (float)(i0 + lane) : 0.0f;
 
         for (int k = 0; k < nch; ++k) {
             const int t0 = k * P;
@@ -170,13 +176,18 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             Aw[1] = Aw[P + 1];
 #pragma unroll
             for (int j = 0; j < P; ++j) Aw[j + 2] = buf[AR + j * 64 + lane];
-            // lane j: alpha of the last row above at step t0 + 62 + j (row 0: NINF)
+            // lane j: alpha of the last row above at step t0 + 62 + j (row 0: NINF, or
+            // for NWG alpha[0, t0+j] = (t0+j)*gap)
             float bv = buf[RR + lane];
             bv = (s > 0 && lane <= P && t0 + 62 + lane <= nsteps - 1) ? bv : kNINF;
-            // lane 0's up tangents: column t0+j sits in lane j (row 0: 0)
+            if (NWG && s == 0) bv = lane <= P ? (float)(t0 + lane) * gap : kNINF;
+            // lane 0's up tangents: column t0+j sits in lane j (row 0: 0, or for the
+            // NWG gap Jacobian the boundary's t0+j+1 gaps)
             float rreg = 0.0f;
             if (s > 0 && lane < P)
                 rreg = x_in ? buf[TR + lane] : ring_in[ring_index(t0 + lane + 63, R)];
+            else if (NWG && MODE == GAP && s == 0 && lane < P)
+                rreg = (float)(t0 + lane + 1);
             wave_lds_sync();   // every read of the input buffer is complete
             if (k + 1 < nch) {
                 if (x_in) {
@@ -208,9 +219,11 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 up_prev = tu;
                 const float tl = cur;
                 const float v0 = dga + sc, v1 = upa + gap, v2 = a1 + gap;
-                const float m = fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
+                // NWG: no restart candidate
+                const float m = NWG ? fmaxf(fmaxf(v0, v1), v2) : fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
                 const float e0 = fast_exp2((v0 - m) * c), e1 = fast_exp2((v1 - m) * c);
-                const float e2 = fast_exp2((v2 - m) * c), e3 = fast_exp2((sc - m) * c);
+                const float e2 = fast_exp2((v2 - m) * c);
+                const float e3 = NWG ? 0.0f : fast_exp2((sc - m) * c);
                 const float rin = fast_rcp(((e0 + e1) + e2) + e3);
                 float x;
                 if (MODE == HVP) {
@@ -233,13 +246,18 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                         x += ((a0 - m) - ev) * rT;
                     }
                 }
-                cur = ok ? x : 0.0f;
+                cur = ok ? x : ((NWG && t - lane < 0) ? xleft : 0.0f);
                 lane_store(toutc + u * 64, ul4, cur);
                 pub[u] = cur;
                 if (MODE == HVP) {
-                    float lp = (a0 - S) * c;
-                    lp = lp < 0.0f ? lp : 0.0f;
-                    sacc += fast_exp2(lp) * cur;
+                    if (NWG) {
+                        // the value's tangent is the terminal cell's
+                        if (t == term_step) sacc += cur;
+                    } else {
+                        float lp = (a0 - S) * c;
+                        lp = lp < 0.0f ? lp : 0.0f;
+                        sacc += fast_exp2(lp) * cur;
+                    }
                 }
             }
             // the stripe's last row of tangents by step: one store instruction
@@ -280,7 +298,7 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
 
 // DOT: instead of writing the per-cell output, accumulate its dot product with the
 // matrix passed as V (the marginal cotangent) into dot[b].
-template <int MODE, int P, bool DOT>
+template <int MODE, int P, bool DOT, bool NWG = false>
 __global__ void __launch_bounds__(NW * 64)
 sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                const int* __restrict__ lengths, const float* __restrict__ alpha_sk,
@@ -361,6 +379,8 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
         const int s = s_begin + NL - 1 - q;
         const int i0 = s * 64;
         const int L2eff = (i0 + lane < L1) ? L2 : 0;
+        // NWG: beta starts at 1 in the terminal cell only (and its tangent at 0)
+        const int term_step = (NWG && i0 + lane == L1 - 1) ? L2 - 1 + lane : -1000000;
         const size_t sb = ((size_t)b * NSmax + s) * NT;
         const size_t ub = ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
         const float* astripe = alpha_sk + sb * 64;
@@ -446,6 +466,14 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             const bool row_ok = s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1;
             float bA = row_ok ? buf[RA + lane] : kNINF;
             float bX = row_ok ? buf[RX + lane] : 0.0f;
+            if (NWG && s == 0) {
+                // row 0 above the first stripe: alpha (col+1)*gap at column t_hi - lane,
+                // tangent col+1 for the gap Jacobian
+                const int jc = t_hi - lane + 1;
+                const bool in = lane <= P && jc >= 0;
+                bA = in ? (float)jc * gap : kNINF;
+                bX = (in && MODE == GAP) ? (float)jc : 0.0f;
+            }
             // flows from the stripe below for lane 63 (see the marginal backward):
             // lane 63-j holds step j; up flows from slot kP+j+63, diagonal kP+j+62
             float qub = 0.0f, qug = 0.0f, qdb = 0.0f, qdg = 0.0f;
@@ -501,9 +529,11 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 bA = nA;
                 bX = nX;
                 const float v0 = dga + sc, v1 = upa + gap, v2 = a1 + gap;
-                const float m = fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
+                // NWG: no restart candidate
+                const float m = NWG ? fmaxf(fmaxf(v0, v1), v2) : fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
                 const float e0 = fast_exp2((v0 - m) * c), e1 = fast_exp2((v1 - m) * c);
-                const float e2 = fast_exp2((v2 - m) * c), e3 = fast_exp2((sc - m) * c);
+                const float e2 = fast_exp2((v2 - m) * c);
+                const float e3 = NWG ? 0.0f : fast_exp2((sc - m) * c);
                 const float rin = fast_rcp(((e0 + e1) + e2) + e3);
                 const float w0 = e0 * rin, w1 = e1 * rin, w2 = e2 * rin, w3 = e3 * rin;
                 // candidate tangents and the weight tangents
@@ -535,7 +565,8 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                     dw2 = w2 * (q2 - mean) * rT;
                     dw3 = w3 * (q3 - mean) * rT;
                     if (MODE == TEMP) {
-                        const float p0 = v0 - m, p1 = v1 - m, p2 = v2 - m, p3 = sc - m;
+                        const float p0 = v0 - m, p1 = v1 - m, p2 = v2 - m;
+                        const float p3 = NWG ? 0.0f : sc - m;
                         const float ev = ((w0 * p0 + w1 * p1) + w2 * p2) + w3 * p3;
                         const float rT2 = rT * rT;
                         dw0 += w0 * (ev - p0) * rT2;
@@ -545,13 +576,23 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                     }
                 }
                 // channels in the reference's accumulation order
-                float lp = (a0 - S) * c;
-                lp = lp < 0.0f ? lp : 0.0f;
-                const float binit = fast_exp2(lp);
+                float binit;
+                if (NWG) {
+                    binit = t == term_step ? 1.0f : 0.0f;
+                } else {
+                    float lp = (a0 - S) * c;
+                    lp = lp < 0.0f ? lp : 0.0f;
+                    binit = fast_exp2(lp);
+                }
                 const float beta = ((binit + db) + lb) + ubt;
                 float g;
                 bool live;
-                if (MODE == HVP) {
+                if (NWG) {
+                    // the terminal beta is constant: no initial tangent; the reference
+                    // skips cells with beta == 0 and |g| < 1e-20
+                    g = ((dg + lg) + ug);
+                    live = ok && !(beta == 0.0f && fabsf(g) < 1e-20f);
+                } else if (MODE == HVP) {
                     g = ((binit * (x0 - dSb) * rT + dg) + lg) + ug;
                     live = ok && beta <= 3.0e38f && beta != 0.0f;
                 } else {
@@ -684,7 +725,7 @@ Second second_layout(void* ws, int B, int L1, int L2) {
     return w;
 }
 
-template <int MODE>
+template <int MODE, bool NWG = false>
 int launch_tangent(const float* scores, const float* V, const int* lengths, int B, int L1, int L2,
                    float gap, float T, const Second& w, float* sdot, hipStream_t st) {
     const int ns = (L1 + 63) / 64;
@@ -694,10 +735,10 @@ int launch_tangent(const float* scores, const float* V, const int* lengths, int 
     const int R = ring_len(sp.G > 1 ? sp.SPW * 64 : L1, L2, 256);
     const size_t lds = lds_tangent_r(MODE, R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
-    auto kern = sw_tangent_kernel<MODE, PT>;
+    auto kern = sw_tangent_kernel<MODE, PT, NWG>;
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
-    D2P_LAUNCH("sw_tangent", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
+    D2P_LAUNCH(NWG ? "nw_tangent" : "sw_tangent", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
                lengths, w.prim.alpha_sk, w.prim.brow, w.part, w.tan_sk, w.tan_brow, sdot,
                w.prim.status, w.prim.fflag, w.spart, B, L1, L2, ns, gap, T, R, sp.G, sp.SPW,
                next_epoch());
@@ -707,7 +748,7 @@ int launch_tangent(const float* scores, const float* V, const int* lengths, int 
     return D2P_OK;
 }
 
-template <int MODE, bool DOT>
+template <int MODE, bool DOT, bool NWG = false>
 int launch_dual(const float* scores, const float* V, const int* lengths, int B, int L1, int L2,
                 float gap, float T, const Second& w, const float* dS, float* out, float* dot,
                 hipStream_t st) {
@@ -720,12 +761,12 @@ int launch_dual(const float* scores, const float* V, const int* lengths, int B, 
     const int P = dual_chunk(has_v, DOT, rows, L2);
     D2P_REQUIRE(P > 0, "sequence too long for the LDS stripe rings");
     const size_t lds = lds_dual_r(has_v, DOT, P, R);
-    auto k8 = sw_dual_kernel<MODE, 8, DOT>;
-    auto k4 = sw_dual_kernel<MODE, 4, DOT>;
+    auto k8 = sw_dual_kernel<MODE, 8, DOT, NWG>;
+    auto k4 = sw_dual_kernel<MODE, 4, DOT, NWG>;
     auto kern = P == 8 ? k8 : k4;
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
-    D2P_LAUNCH("sw_dual", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
+    D2P_LAUNCH(NWG ? "nw_dual" : "sw_dual", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
                lengths, w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, w.part, dS, out, dot,
                w.prim.status, w.prim.trash, w.prim.bflag, w.flows4, w.spart, B, L1, L2, ns, gap,
                T, R, sp.G, sp.SPW, next_epoch());
@@ -756,9 +797,15 @@ extern "C" size_t d2p_sw_second_workspace_bytes(int B, int max_L1, int max_L2) {
     return sw2::second_layout(nullptr, B, max_L1, max_L2).bytes;
 }
 
-extern "C" int d2p_sw_hvp(const float* scores, const float* tangent, const int* lengths, int B,
-                          int max_L1, int max_L2, float gap, float temperature, float* hvp,
-                          void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+
+// The linear-gap second-order paths; global selects soft Needleman-Wunsch, whose
+// value is the terminal cell (its beta is the constant 1, so dS/dtheta never enters
+// the reverse sweeps and no marginal backward is needed for it).
+template <bool NWG>
+int hvp_impl(const float* scores, const float* tangent, const int* lengths, int B, int max_L1,
+             int max_L2, float gap, float temperature, float* hvp, void* workspace,
+             size_t workspace_bytes, void* stream) {
     D2P_TRY(sw2::check(B, max_L1, max_L2, temperature));
     if (B == 0) return D2P_OK;
     D2P_REQUIRE(scores && tangent && lengths && hvp, "null pointer argument");
@@ -767,17 +814,17 @@ extern "C" int d2p_sw_hvp(const float* scores, const float* tangent, const int* 
     hipStream_t st = (hipStream_t)stream;
     const sw2::Second w = sw2::second_layout(workspace, B, max_L1, max_L2);
     D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, w.prim,
-                               w.part, st));
-    D2P_TRY(sw2::launch_tangent<sw2::HVP>(scores, tangent, lengths, B, max_L1, max_L2, gap,
-                                          temperature, w, w.sdot, st));
-    return sw2::launch_dual<sw2::HVP, false>(scores, tangent, lengths, B, max_L1, max_L2, gap,
-                                             temperature, w, w.sdot, hvp, nullptr, st);
+                               w.part, st, NWG));
+    D2P_TRY(sw2::launch_tangent<sw2::HVP, NWG>(scores, tangent, lengths, B, max_L1, max_L2, gap,
+                                               temperature, w, w.sdot, st));
+    return sw2::launch_dual<sw2::HVP, false, NWG>(scores, tangent, lengths, B, max_L1, max_L2,
+                                                  gap, temperature, w, w.sdot, hvp, nullptr, st);
 }
 
-extern "C" int d2p_sw_param_jacobian(const float* scores, int param_type, const int* lengths,
-                                     int B, int max_L1, int max_L2, float gap, float temperature,
-                                     float* jacobian, void* workspace, size_t workspace_bytes,
-                                     void* stream) {
+template <bool NWG>
+int param_jacobian_impl(const float* scores, int param_type, const int* lengths, int B,
+                        int max_L1, int max_L2, float gap, float temperature, float* jacobian,
+                        void* workspace, size_t workspace_bytes, void* stream) {
     D2P_TRY(sw2::check(B, max_L1, max_L2, temperature));
     D2P_REQUIRE(param_type == 0 || param_type == 1, "param_type must be 0 or 1");
     if (B == 0) return D2P_OK;
@@ -787,29 +834,31 @@ extern "C" int d2p_sw_param_jacobian(const float* scores, int param_type, const 
     hipStream_t st = (hipStream_t)stream;
     const sw2::Second w = sw2::second_layout(workspace, B, max_L1, max_L2);
     D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, w.prim,
-                               w.part, st));
-    // dS/dtheta from the marginal backward; its marginals go to the output, which the
-    // reverse sweep below overwrites completely
-    D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, w.prim,
-                                w.part, jacobian, w.dgap, w.dT, st, true));
+                               w.part, st, NWG));
+    // SW: dS/dtheta from the marginal backward; its marginals go to the output, which
+    // the reverse sweep below overwrites completely
+    if (!NWG)
+        D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature,
+                                    w.prim, w.part, jacobian, w.dgap, w.dT, st, true));
     if (param_type == 0) {
-        D2P_TRY(sw2::launch_tangent<sw2::GAP>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
-                                              temperature, w, nullptr, st));
-        return sw2::launch_dual<sw2::GAP, false>(scores, nullptr, lengths, B, max_L1, max_L2,
-                                                 gap, temperature, w, w.dgap, jacobian, nullptr,
-                                                 st);
+        D2P_TRY(sw2::launch_tangent<sw2::GAP, NWG>(scores, nullptr, lengths, B, max_L1, max_L2,
+                                                   gap, temperature, w, nullptr, st));
+        return sw2::launch_dual<sw2::GAP, false, NWG>(scores, nullptr, lengths, B, max_L1,
+                                                      max_L2, gap, temperature, w, w.dgap,
+                                                      jacobian, nullptr, st);
     }
-    D2P_TRY(sw2::launch_tangent<sw2::TEMP>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
-                                           temperature, w, nullptr, st));
-    return sw2::launch_dual<sw2::TEMP, false>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
-                                              temperature, w, w.dT, jacobian, nullptr, st);
+    D2P_TRY(sw2::launch_tangent<sw2::TEMP, NWG>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
+                                                temperature, w, nullptr, st));
+    return sw2::launch_dual<sw2::TEMP, false, NWG>(scores, nullptr, lengths, B, max_L1, max_L2,
+                                                   gap, temperature, w, w.dT, jacobian, nullptr,
+                                                   st);
 }
 
-extern "C" int d2p_sw_backward_full(const float* scores, const float* grad_alignment,
-                                    const int* lengths, int B, int max_L1, int max_L2, float gap,
-                                    float temperature, float* grad_scores, float* grad_gap,
-                                    float* grad_T, void* workspace, size_t workspace_bytes,
-                                    void* stream) {
+template <bool NWG>
+int backward_full_impl(const float* scores, const float* grad_alignment, const int* lengths,
+                       int B, int max_L1, int max_L2, float gap, float temperature,
+                       float* grad_scores, float* grad_gap, float* grad_T, void* workspace,
+                       size_t workspace_bytes, void* stream) {
     D2P_TRY(sw2::check(B, max_L1, max_L2, temperature));
     if (B == 0) return D2P_OK;
     D2P_REQUIRE(scores && grad_alignment && lengths && grad_scores && grad_gap && grad_T,
@@ -820,22 +869,80 @@ extern "C" int d2p_sw_backward_full(const float* scores, const float* grad_align
     const sw2::Second w = sw2::second_layout(workspace, B, max_L1, max_L2);
     const float* ga = grad_alignment;
     D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, w.prim,
-                               w.part, st));
-    // dS/dgap and dS/dT; the marginals land in grad_scores, overwritten by the HVP
-    D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, w.prim,
-                                w.part, grad_scores, w.dgap, w.dT, st, true));
+                               w.part, st, NWG));
+    // SW: dS/dgap and dS/dT; the marginals land in grad_scores, overwritten by the HVP
+    if (!NWG)
+        D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature,
+                                    w.prim, w.part, grad_scores, w.dgap, w.dT, st, true));
     // grad_scores = H grad_alignment
-    D2P_TRY(sw2::launch_tangent<sw2::HVP>(scores, ga, lengths, B, max_L1, max_L2, gap,
-                                          temperature, w, w.sdot, st));
-    D2P_TRY(sw2::launch_dual<sw2::HVP, false>(scores, ga, lengths, B, max_L1, max_L2, gap,
-                                              temperature, w, w.sdot, grad_scores, nullptr, st));
+    D2P_TRY(sw2::launch_tangent<sw2::HVP, NWG>(scores, ga, lengths, B, max_L1, max_L2, gap,
+                                               temperature, w, w.sdot, st));
+    D2P_TRY(sw2::launch_dual<sw2::HVP, false, NWG>(scores, ga, lengths, B, max_L1, max_L2, gap,
+                                                   temperature, w, w.sdot, grad_scores, nullptr,
+                                                   st));
     // grad_gap[b] = <grad_alignment, dP/dgap>, grad_T[b] = <grad_alignment, dP/dT>
-    D2P_TRY(sw2::launch_tangent<sw2::GAP>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
-                                          temperature, w, nullptr, st));
-    D2P_TRY(sw2::launch_dual<sw2::GAP, true>(scores, ga, lengths, B, max_L1, max_L2, gap,
-                                             temperature, w, w.dgap, nullptr, grad_gap, st));
-    D2P_TRY(sw2::launch_tangent<sw2::TEMP>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
-                                           temperature, w, nullptr, st));
-    return sw2::launch_dual<sw2::TEMP, true>(scores, ga, lengths, B, max_L1, max_L2, gap,
-                                             temperature, w, w.dT, nullptr, grad_T, st);
+    D2P_TRY(sw2::launch_tangent<sw2::GAP, NWG>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
+                                               temperature, w, nullptr, st));
+    D2P_TRY(sw2::launch_dual<sw2::GAP, true, NWG>(scores, ga, lengths, B, max_L1, max_L2, gap,
+                                                  temperature, w, w.dgap, nullptr, grad_gap, st));
+    D2P_TRY(sw2::launch_tangent<sw2::TEMP, NWG>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
+                                                temperature, w, nullptr, st));
+    return sw2::launch_dual<sw2::TEMP, true, NWG>(scores, ga, lengths, B, max_L1, max_L2, gap,
+                                                  temperature, w, w.dT, nullptr, grad_T, st);
+}
+
+}  // namespace
+
+extern "C" int d2p_sw_hvp(const float* scores, const float* tangent, const int* lengths, int B,
+                          int max_L1, int max_L2, float gap, float temperature, float* hvp,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+    return hvp_impl<false>(scores, tangent, lengths, B, max_L1, max_L2, gap, temperature, hvp,
+                           workspace, workspace_bytes, stream);
+}
+
+extern "C" int d2p_sw_param_jacobian(const float* scores, int param_type, const int* lengths,
+                                     int B, int max_L1, int max_L2, float gap, float temperature,
+                                     float* jacobian, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+    return param_jacobian_impl<false>(scores, param_type, lengths, B, max_L1, max_L2, gap,
+                                      temperature, jacobian, workspace, workspace_bytes, stream);
+}
+
+extern "C" int d2p_sw_backward_full(const float* scores, const float* grad_alignment,
+                                    const int* lengths, int B, int max_L1, int max_L2, float gap,
+                                    float temperature, float* grad_scores, float* grad_gap,
+                                    float* grad_T, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+    return backward_full_impl<false>(scores, grad_alignment, lengths, B, max_L1, max_L2, gap,
+                                     temperature, grad_scores, grad_gap, grad_T, workspace,
+                                     workspace_bytes, stream);
+}
+
+extern "C" size_t d2p_nw_second_workspace_bytes(int B, int max_L1, int max_L2) {
+    return d2p_sw_second_workspace_bytes(B, max_L1, max_L2);
+}
+
+extern "C" int d2p_nw_hvp(const float* scores, const float* tangent, const int* lengths, int B,
+                          int max_L1, int max_L2, float gap, float temperature, float* hvp,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+    return hvp_impl<true>(scores, tangent, lengths, B, max_L1, max_L2, gap, temperature, hvp,
+                          workspace, workspace_bytes, stream);
+}
+
+extern "C" int d2p_nw_param_jacobian(const float* scores, int param_type, const int* lengths,
+                                     int B, int max_L1, int max_L2, float gap, float temperature,
+                                     float* jacobian, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+    return param_jacobian_impl<true>(scores, param_type, lengths, B, max_L1, max_L2, gap,
+                                     temperature, jacobian, workspace, workspace_bytes, stream);
+}
+
+extern "C" int d2p_nw_backward_full(const float* scores, const float* grad_alignment,
+                                    const int* lengths, int B, int max_L1, int max_L2, float gap,
+                                    float temperature, float* grad_scores, float* grad_gap,
+                                    float* grad_T, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+    return backward_full_impl<true>(scores, grad_alignment, lengths, B, max_L1, max_L2, gap,
+                                    temperature, grad_scores, grad_gap, grad_T, workspace,
+                                    workspace_bytes, stream);
 }

@@ -150,25 +150,36 @@ Tensor second_workspace(const Dims& d, const Tensor& like) {
     return workspace(d2p_sw_second_workspace_bytes(d.B, d.L1, d.L2), like);
 }
 
+// global: soft Needleman-Wunsch instead of Smith-Waterman (same workspace)
 Tensor sw_hvp_run(const Tensor& scores, const Tensor& tangent, const Tensor& lengths,
-                  const Dims& d, float gap, float T) {
+                  const Dims& d, float gap, float T, bool global = false) {
     Tensor out = torch::empty({d.B, d.L1, d.L2}, scores.options());
     Tensor ws = second_workspace(d, scores);
-    D2P_CALL(d2p_sw_hvp(scores.data_ptr<float>(), tangent.data_ptr<float>(),
-                        lengths.data_ptr<int>(), d.B, d.L1, d.L2, gap, T, out.data_ptr<float>(),
-                        ws.data_ptr(), ws.numel(), current_stream()));
+    D2P_CALL((global ? d2p_nw_hvp : d2p_sw_hvp)(
+        scores.data_ptr<float>(), tangent.data_ptr<float>(), lengths.data_ptr<int>(), d.B, d.L1,
+        d.L2, gap, T, out.data_ptr<float>(), ws.data_ptr(), ws.numel(), current_stream()));
+    return out;
+}
+
+Tensor sw_param_jacobian_run(const Tensor& scores, int param_type, const Tensor& lengths,
+                             const Dims& d, float gap, float T, bool global = false) {
+    Tensor out = torch::empty({d.B, d.L1, d.L2}, scores.options());
+    Tensor ws = second_workspace(d, scores);
+    D2P_CALL((global ? d2p_nw_param_jacobian : d2p_sw_param_jacobian)(
+        scores.data_ptr<float>(), param_type, lengths.data_ptr<int>(), d.B, d.L1, d.L2, gap, T,
+        out.data_ptr<float>(), ws.data_ptr(), ws.numel(), current_stream()));
     return out;
 }
 
 // returns (grad_scores [B,L1,L2], per-element <ga, dP/dgap> [B], <ga, dP/dT> [B])
 std::tuple<Tensor, Tensor, Tensor> sw_backward_full_run(const Tensor& scores, const Tensor& ga,
                                                         const Tensor& lengths, const Dims& d,
-                                                        float gap, float T) {
+                                                        float gap, float T, bool global = false) {
     auto opt = scores.options();
     Tensor gs = torch::empty({d.B, d.L1, d.L2}, opt);
     Tensor gg = torch::empty({d.B}, opt), gt = torch::empty({d.B}, opt);
     Tensor ws = second_workspace(d, scores);
-    D2P_CALL(d2p_sw_backward_full(scores.data_ptr<float>(), ga.data_ptr<float>(),
+    D2P_CALL((global ? d2p_nw_backward_full : d2p_sw_backward_full)(scores.data_ptr<float>(), ga.data_ptr<float>(),
                                   lengths.data_ptr<int>(), d.B, d.L1, d.L2, gap, T,
                                   gs.data_ptr<float>(), gg.data_ptr<float>(), gt.data_ptr<float>(),
                                   ws.data_ptr(), ws.numel(), current_stream()));
@@ -308,13 +319,7 @@ Tensor soft_sw_param_jacobian(Tensor scores, int64_t param_type, double gap, dou
     Dims d = checked_dims(scores, "SW");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
     Tensor l = resolve_lengths(lengths, d, scores.device());
-    Tensor out = torch::empty({d.B, d.L1, d.L2}, scores.options());
-    Tensor ws = second_workspace(d, scores);
-    D2P_CALL(d2p_sw_param_jacobian(scores.data_ptr<float>(), (int)param_type, l.data_ptr<int>(),
-                                   d.B, d.L1, d.L2, (float)gap, (float)temperature,
-                                   out.data_ptr<float>(), ws.data_ptr(), ws.numel(),
-                                   current_stream()));
-    return out;
+    return sw_param_jacobian_run(scores, (int)param_type, l, d, (float)gap, (float)temperature);
 }
 
 std::tuple<Tensor, Tensor, Tensor> soft_sw_backward_full(Tensor scores, Tensor grad_alignment,
@@ -377,10 +382,11 @@ SwOut nw_run(const Tensor& scores, const Tensor& lengths, const Dims& d, float g
     return o;
 }
 
-// Autograd semantics of SoftNWCUDAFunction (/root/reference/src/nw/torch_cuda.cpp:115-260):
-// outputs {value, marginals}; d value / d scores = marginals.  The marginal path
-// (second order) is not part of this build's NW family: a defined marginal cotangent
-// raises.
+// Autograd semantics of SoftNWCUDAFunction (/root/reference/src/nw/torch_cuda.cpp:115-330):
+// outputs {value, marginals}; d value / d scores = marginals, so the value path scales
+// the saved marginals; the marginal path adds the HVP against the marginal cotangent
+// and its dot products with dP/dgap and dP/dT; parameter gradients are summed over the
+// batch, shape [1].
 tensor_list nw_autograd_forward(AutogradContext* ctx, const Tensor& scores,
                                 const Tensor& lengths, double gap, double temperature) {
     ctx->set_materialize_grads(false);
@@ -388,24 +394,34 @@ tensor_list nw_autograd_forward(AutogradContext* ctx, const Tensor& scores,
     Dims d = checked_dims(scores, "NW");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
     SwOut o = nw_run(scores, lengths, d, (float)gap, (float)temperature);
-    ctx->save_for_backward({o.marginals, o.grad_gap, o.grad_T});
+    ctx->save_for_backward({scores, lengths, o.marginals, o.grad_gap, o.grad_T});
+    ctx->saved_data["gap"] = gap;
+    ctx->saved_data["temperature"] = temperature;
     return {o.partition, o.marginals};
 }
 
 tensor_list nw_autograd_backward(AutogradContext* ctx, const tensor_list& grads, bool want_gap,
                                  bool want_T) {
     auto saved = ctx->get_saved_variables();
-    Tensor marg = saved[0], ggap = saved[1], gT = saved[2];
+    Tensor scores = saved[0], lengths = saved[1], marg = saved[2], ggap = saved[3], gT = saved[4];
     c10::hip::HIPGuardMasqueradingAsCUDA guard(marg.device());
     Tensor grad_value = grads[0], grad_marg = grads[1];
-    TORCH_CHECK(!(grad_marg.defined() && grad_marg.numel() > 0),
-                "soft_nw: gradients through the alignment (marginals) output are not "
-                "implemented by d2p_amd; only the value path is differentiable");
     Tensor grad_scores, grad_gap, grad_T;
     if (grad_value.defined() && grad_value.numel() > 0) {
         grad_scores = scale_by_batch(marg, grad_value);
         if (want_gap) grad_gap = grad_param_sum(grad_value, ggap);
         if (want_T) grad_T = grad_param_sum(grad_value, gT);
+    }
+    if (grad_marg.defined() && grad_marg.numel() > 0) {
+        Tensor gm = prepare_cotangent(grad_marg, scores, "grad_posteriors");
+        const float gap = (float)ctx->saved_data["gap"].toDouble();
+        const float T = (float)ctx->saved_data["temperature"].toDouble();
+        Dims d = checked_dims(scores, "NW");
+        auto r = sw_backward_full_run(scores, gm, lengths, d, gap, T, true);
+        grad_scores = grad_scores.defined() ? grad_scores + std::get<0>(r) : std::get<0>(r);
+        Tensor tg = std::get<1>(r).sum().reshape({1}), tt = std::get<2>(r).sum().reshape({1});
+        if (want_gap) grad_gap = grad_gap.defined() ? grad_gap + tg : tg;
+        if (want_T) grad_T = grad_T.defined() ? grad_T + tt : tt;
     }
     return {grad_scores, grad_gap, grad_T};
 }
@@ -473,6 +489,65 @@ std::tuple<Tensor, Tensor> nw_value_grad_params(Tensor s, double g, double t,
                                                 c10::optional<Tensor> l) {
     auto r = soft_nw_with_grads(s, g, t, l);
     return {std::get<2>(r), std::get<3>(r)};
+}
+
+// second order: soft_nw_{hvp,param_jacobian,backward_full}_cuda
+// (/root/reference/src/nw/torch_cuda.cpp:442-709) and their nw_marginals_* aliases
+Tensor soft_nw_hvp(Tensor scores, Tensor tangent, double gap, double temperature,
+                   c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    CHECK_INPUT_DEV(tangent);
+    TORCH_CHECK(scores.sizes() == tangent.sizes(), "scores and tangent must have same shape");
+    TORCH_CHECK(tangent.device() == scores.device(), "tangent must be on same device as scores, got ",
+                tangent.device(), " vs ", scores.device());
+    Dims d = checked_dims(scores, "NW");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    return sw_hvp_run(scores, tangent, l, d, (float)gap, (float)temperature, true);
+}
+
+Tensor soft_nw_param_jacobian(Tensor scores, int64_t param_type, double gap, double temperature,
+                              c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    TORCH_CHECK(param_type >= 0 && param_type <= 1, "param_type must be 0 or 1");
+    Dims d = checked_dims(scores, "NW");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    return sw_param_jacobian_run(scores, (int)param_type, l, d, (float)gap, (float)temperature,
+                                 true);
+}
+
+std::tuple<Tensor, Tensor, Tensor> soft_nw_backward_full(Tensor scores, Tensor grad_alignment,
+                                                         double gap, double temperature,
+                                                         c10::optional<Tensor> lengths) {
+    CHECK_INPUT_DEV(scores);
+    TORCH_CHECK(grad_alignment.sizes() == scores.sizes(),
+                "grad_alignment must have same shape as scores");
+    TORCH_CHECK(grad_alignment.is_cuda(), "grad_alignment must be a CUDA tensor");
+    TORCH_CHECK(grad_alignment.device() == scores.device(),
+                "grad_alignment must be on same device as scores, got ", grad_alignment.device(),
+                " vs ", scores.device());
+    Dims d = checked_dims(scores, "NW");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
+    Tensor l = resolve_lengths(lengths, d, scores.device());
+    Tensor ga = grad_alignment.contiguous();
+    if (ga.scalar_type() != torch::kFloat32) ga = ga.to(torch::kFloat32);
+    auto r = sw_backward_full_run(scores, ga, l, d, (float)gap, (float)temperature, true);
+    return {std::get<0>(r), std::get<1>(r).sum().reshape({1}), std::get<2>(r).sum().reshape({1})};
+}
+
+std::tuple<Tensor, Tensor, Tensor> nw_marginals_backward(Tensor s, Tensor gm, double g, double t,
+                                                         c10::optional<Tensor> l) {
+    return soft_nw_backward_full(s, gm, g, t, l);
+}
+Tensor nw_marginals_hvp(Tensor s, Tensor v, double g, double t, c10::optional<Tensor> l) {
+    return soft_nw_hvp(s, v, g, t, l);
+}
+Tensor nw_marginals_grad_gap(Tensor s, double g, double t, c10::optional<Tensor> l) {
+    return soft_nw_param_jacobian(s, 0, g, t, l);
+}
+Tensor nw_marginals_grad_temp(Tensor s, double g, double t, c10::optional<Tensor> l) {
+    return soft_nw_param_jacobian(s, 1, g, t, l);
 }
 
 // ---------------------------------------------------------------------------
@@ -957,6 +1032,13 @@ TORCH_LIBRARY(d2p, m) {
     m.def("nw_forward(Tensor scores, float gap, float temp, Tensor? lengths) -> Tensor[]");
     m.def("nw_forward_t(Tensor scores, Tensor gap, Tensor temp, Tensor lengths) -> Tensor[]");
     m.def("nw_value_grad_params(Tensor scores, float gap, float temp, Tensor? lengths) -> (Tensor, Tensor)");
+    m.def("soft_nw_hvp(Tensor scores, Tensor tangent, float gap, float temperature, Tensor? lengths) -> Tensor");
+    m.def("soft_nw_param_jacobian(Tensor scores, int param_type, float gap, float temperature, Tensor? lengths) -> Tensor");
+    m.def("soft_nw_backward_full(Tensor scores, Tensor grad_alignment, float gap, float temperature, Tensor? lengths) -> (Tensor, Tensor, Tensor)");
+    m.def("nw_marginals_backward(Tensor scores, Tensor grad_marginals, float gap, float temp, Tensor? lengths) -> (Tensor, Tensor, Tensor)");
+    m.def("nw_marginals_hvp(Tensor scores, Tensor v, float gap, float temp, Tensor? lengths) -> Tensor");
+    m.def("nw_marginals_grad_gap(Tensor scores, float gap, float temp, Tensor? lengths) -> Tensor");
+    m.def("nw_marginals_grad_temp(Tensor scores, float gap, float temp, Tensor? lengths) -> Tensor");
 
     m.def("soft_dtw(Tensor costs, Tensor temperature, Tensor lengths, int bandwidth) -> Tensor[]");
     m.def("soft_dtw_float(Tensor costs, float temperature, Tensor? lengths, int? bandwidth) -> Tensor[]");
@@ -987,6 +1069,13 @@ TORCH_LIBRARY_IMPL(d2p, CUDA, m) {
     m.impl("nw_forward", nw_forward);
     m.impl("nw_forward_t", nw_forward_t);
     m.impl("nw_value_grad_params", nw_value_grad_params);
+    m.impl("soft_nw_hvp", soft_nw_hvp);
+    m.impl("soft_nw_param_jacobian", soft_nw_param_jacobian);
+    m.impl("soft_nw_backward_full", soft_nw_backward_full);
+    m.impl("nw_marginals_backward", nw_marginals_backward);
+    m.impl("nw_marginals_hvp", nw_marginals_hvp);
+    m.impl("nw_marginals_grad_gap", nw_marginals_grad_gap);
+    m.impl("nw_marginals_grad_temp", nw_marginals_grad_temp);
 
     m.impl("soft_sw_affine", swa_t);
     m.impl("soft_sw_affine_float", swa_float);
@@ -1043,7 +1132,10 @@ const char* const kAllOps[] = {
     "sw_affine_marginals_grad_gap_open", "sw_affine_marginals_grad_gap_ext",
     "sw_affine_marginals_grad_temp", "soft_dtw", "soft_dtw_float", "soft_dtw_with_grads",
     "soft_dtw_hvp", "soft_dtw_param_jacobian", "soft_dtw_backward_full", "soft_nw",
-    "soft_nw_float", "soft_nw_with_grads", "nw_forward", "nw_forward_t", "nw_value_grad_params"};
+    "soft_nw_float", "soft_nw_with_grads", "soft_nw_hvp", "soft_nw_param_jacobian",
+    "soft_nw_backward_full", "nw_forward", "nw_forward_t", "nw_value_grad_params",
+    "nw_marginals_backward", "nw_marginals_hvp", "nw_marginals_grad_gap",
+    "nw_marginals_grad_temp"};
 }  // namespace
 
 TORCH_LIBRARY_IMPL(d2p, CPU, m) {

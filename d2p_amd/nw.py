@@ -5,9 +5,10 @@ Same API as the reference's ``d2p.nw`` for the linear-gap family
 alignment)``; ``SoftNW`` is the ``nn.Module`` wrapper with optional learnable gap
 and temperature.  The value is alpha[L1, L2] of the global recurrence
 (alpha[i,0] = i*gap, alpha[0,j] = j*gap, no restart term); gradients flow through
-the value (scores, and gap / temperature when given as tensors).  Gradients
-through the alignment output raise: the NW second-order sweeps are not part of
-this build, and neither is the affine-gap NW family.
+the value (scores, and gap / temperature when given as tensors) and through the
+alignment output (the second-order sweeps: HVP against the alignment cotangent and
+its dot products with dP/dgap and dP/dT).  The affine-gap NW family is not part of
+this build.
 """
 from __future__ import annotations
 

@@ -19,4 +19,6 @@ from .._ops import (  # noqa: F401
     soft_dtw, soft_dtw_float, soft_dtw_with_grads, soft_dtw_hvp, soft_dtw_param_jacobian,
     soft_dtw_backward_full,
     soft_nw, soft_nw_float, soft_nw_with_grads, nw_forward, nw_forward_t, nw_value_grad_params,
+    soft_nw_hvp, soft_nw_param_jacobian, soft_nw_backward_full, nw_marginals_backward,
+    nw_marginals_hvp, nw_marginals_grad_gap, nw_marginals_grad_temp,
 )

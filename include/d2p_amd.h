@@ -182,6 +182,40 @@ int d2p_nw_forward_marginals(const float* scores, const int* lengths, int B, int
                              float* marginals, float* grad_gap, float* grad_T, void* workspace,
                              size_t workspace_bytes, void* stream);
 
+/* Workspace bytes of the second-order global-alignment entry points below
+ * (d2p_nw_hvp, d2p_nw_param_jacobian, d2p_nw_backward_full). */
+size_t d2p_nw_second_workspace_bytes(int B, int max_L1, int max_L2);
+
+/* Hessian-vector product of the value: hvp = (d^2 value / dscores^2) . tangent.
+ * Replaces nw_hvp (/root/reference/src/nw/kernels.cuh:146-171) as sequenced by
+ * soft_nw_hvp_cuda (/root/reference/src/nw/torch_cuda.cpp:442-503), which runs the
+ * forward first.  The boundary cells' tangents are 0; the terminal beta is 1.
+ *   tangent, hvp [B, max_L1, max_L2]                                              */
+int d2p_nw_hvp(const float* scores, const float* tangent, const int* lengths, int B,
+               int max_L1, int max_L2, float gap, float temperature, float* hvp,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* Jacobian of the marginals with respect to gap (param_type 0: the boundary cells'
+ * tangents are i and j) or temperature (1).  Replaces nw_param_grad
+ * (/root/reference/src/nw/kernels.cuh:173-200) as sequenced by
+ * soft_nw_param_jacobian_cuda (/root/reference/src/nw/torch_cuda.cpp:509-598); the
+ * reference's dS/dtheta input is unused by its kernel and not computed here.
+ *   jacobian [B, max_L1, max_L2]                                                  */
+int d2p_nw_param_jacobian(const float* scores, int param_type, const int* lengths, int B,
+                          int max_L1, int max_L2, float gap, float temperature,
+                          float* jacobian, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* Backward of the marginals output for a cotangent grad_alignment:
+ *   grad_scores = H . grad_alignment,
+ *   grad_gap[b] = <grad_alignment[b], dP_b/dgap>, grad_T[b] = <grad_alignment[b], dP_b/dT>
+ * (per element; soft_nw_backward_full_cuda, /root/reference/src/nw/torch_cuda.cpp:602-709,
+ * returns their sums over the batch). */
+int d2p_nw_backward_full(const float* scores, const float* grad_alignment, const int* lengths,
+                         int B, int max_L1, int max_L2, float gap, float temperature,
+                         float* grad_scores, float* grad_gap, float* grad_T, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Soft dynamic time warping (optional Sakoe-Chiba band)
  * ------------------------------------------------------------------------- */

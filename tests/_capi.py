@@ -34,6 +34,10 @@ SIGNATURES = {
     "d2p_sw_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _p, _p, _z, _p]),
     "d2p_sw_param_jacobian": (_i, [_p, _i, _p, _i, _i, _i, _f, _f, _p, _p, _z, _p]),
     "d2p_sw_backward_full": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _p, _p, _p, _p, _z, _p]),
+    "d2p_nw_second_workspace_bytes": (_z, [_i, _i, _i]),
+    "d2p_nw_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _p, _p, _z, _p]),
+    "d2p_nw_param_jacobian": (_i, [_p, _i, _p, _i, _i, _i, _f, _f, _p, _p, _z, _p]),
+    "d2p_nw_backward_full": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _p, _p, _p, _p, _z, _p]),
     "d2p_swa_second_workspace_bytes": (_z, [_i, _i, _i]),
     "d2p_swa_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _f, _p, _p, _z, _p]),
     "d2p_swa_param_jacobian": (_i, [_p, _i, _p, _i, _i, _i, _f, _f, _f, _p, _p, _z, _p]),
@@ -167,38 +171,39 @@ def dtw_forward_marginals(costs, lengths, T, bandwidth=-1):
     return tuple(outs)
 
 
-def _second_ws(B, L1, L2, dev):
-    nbytes = lib().d2p_sw_second_workspace_bytes(B, L1, L2)
+def _second_ws(B, L1, L2, dev, fam="sw"):
+    nbytes = getattr(lib(), f"d2p_{fam}_second_workspace_bytes")(B, L1, L2)
     return _workspace(nbytes, dev), nbytes
 
 
-def sw_hvp(scores, V, lengths, gap, T):
+def sw_hvp(scores, V, lengths, gap, T, fam="sw"):
     import torch
     B, L1, L2 = scores.shape
     dev = scores.device
     lengths = _lengths(lengths, B, L1, L2, dev)
     out = torch.empty(B, L1, L2, device=dev)
-    ws, nbytes = _second_ws(B, L1, L2, dev)
-    check(lib().d2p_sw_hvp(ptr(scores), ptr(V), ptr(lengths), B, L1, L2, gap, T, ptr(out),
-                           ptr(ws), nbytes, stream()))
+    ws, nbytes = _second_ws(B, L1, L2, dev, fam)
+    check(getattr(lib(), f"d2p_{fam}_hvp")(ptr(scores), ptr(V), ptr(lengths), B, L1, L2, gap,
+                                            T, ptr(out), ptr(ws), nbytes, stream()))
     _check_status(ws, B)
     return out
 
 
-def sw_param_jacobian(scores, ptype, lengths, gap, T):
+def sw_param_jacobian(scores, ptype, lengths, gap, T, fam="sw"):
     import torch
     B, L1, L2 = scores.shape
     dev = scores.device
     lengths = _lengths(lengths, B, L1, L2, dev)
     out = torch.empty(B, L1, L2, device=dev)
-    ws, nbytes = _second_ws(B, L1, L2, dev)
-    check(lib().d2p_sw_param_jacobian(ptr(scores), ptype, ptr(lengths), B, L1, L2, gap, T,
-                                      ptr(out), ptr(ws), nbytes, stream()))
+    ws, nbytes = _second_ws(B, L1, L2, dev, fam)
+    check(getattr(lib(), f"d2p_{fam}_param_jacobian")(ptr(scores), ptype, ptr(lengths), B, L1,
+                                                       L2, gap, T, ptr(out), ptr(ws), nbytes,
+                                                       stream()))
     _check_status(ws, B)
     return out
 
 
-def sw_backward_full(scores, grad_alignment, lengths, gap, T):
+def sw_backward_full(scores, grad_alignment, lengths, gap, T, fam="sw"):
     import torch
     B, L1, L2 = scores.shape
     dev = scores.device
@@ -206,10 +211,11 @@ def sw_backward_full(scores, grad_alignment, lengths, gap, T):
     gs = torch.empty(B, L1, L2, device=dev)
     gg = torch.empty(B, device=dev)
     gt = torch.empty(B, device=dev)
-    ws, nbytes = _second_ws(B, L1, L2, dev)
-    check(lib().d2p_sw_backward_full(ptr(scores), ptr(grad_alignment), ptr(lengths), B, L1, L2,
-                                     gap, T, ptr(gs), ptr(gg), ptr(gt), ptr(ws), nbytes,
-                                     stream()))
+    ws, nbytes = _second_ws(B, L1, L2, dev, fam)
+    check(getattr(lib(), f"d2p_{fam}_backward_full")(ptr(scores), ptr(grad_alignment),
+                                                      ptr(lengths), B, L1, L2, gap, T, ptr(gs),
+                                                      ptr(gg), ptr(gt), ptr(ws), nbytes,
+                                                      stream()))
     _check_status(ws, B)
     return gs, gg, gt
 
@@ -309,3 +315,15 @@ def scale_by_batch(src, g):
     B = src.shape[0]
     check(lib().d2p_scale_by_batch(ptr(src), ptr(g), ptr(out), B, src.numel() // B, stream()))
     return out
+
+
+def nw_hvp(scores, V, lengths, gap, T):
+    return sw_hvp(scores, V, lengths, gap, T, fam="nw")
+
+
+def nw_param_jacobian(scores, ptype, lengths, gap, T):
+    return sw_param_jacobian(scores, ptype, lengths, gap, T, fam="nw")
+
+
+def nw_backward_full(scores, grad_alignment, lengths, gap, T):
+    return sw_backward_full(scores, grad_alignment, lengths, gap, T, fam="nw")
