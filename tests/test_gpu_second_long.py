@@ -50,6 +50,21 @@ def test_sw_long(cuda, L):
 
 
 @pytest.mark.parametrize("L", [1000, 1600])
+def test_nw_long(cuda, L):
+    s = _seeded(L + 4, (1, L, L))
+    v = _seeded(L + 5, (1, L, L))
+    k32, k64 = O.get("oracle"), O.get("oracle64")
+    s64, v64 = s.numpy().astype(np.float64), v.numpy().astype(np.float64)
+    _check(_capi.nw_hvp(s.to(cuda), v.to(cuda), None, -1.0, 1.0),
+           k64.soft_nw_hvp(s64, v64, -1.0, 1.0), k32.soft_nw_hvp(s.numpy(), v.numpy(), -1.0, 1.0),
+           f"nw hvp {L}")
+    for p in (0, 1):
+        _check(_capi.nw_param_jacobian(s.to(cuda), p, None, -1.0, 1.0),
+               k64.soft_nw_param_jacobian(s64, p, -1.0, 1.0),
+               k32.soft_nw_param_jacobian(s.numpy(), p, -1.0, 1.0), f"nw dP/d{('gap', 'T')[p]} {L}")
+
+
+@pytest.mark.parametrize("L", [1000, 1600])
 def test_affine_long(cuda, L):
     s = _seeded(L + 2, (1, L, L))
     v = _seeded(L + 3, (1, L, L))
