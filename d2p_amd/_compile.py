@@ -1,7 +1,7 @@
 """torch.compile / AMP glue: fake (meta) kernels and autocast rules for d2p ops.
 
-Behaviour of the reference's ``d2p/_compile.py`` for the SW, affine and DTW
-families (fakes ``:24-250,371-415``, autocast ``:857-931``):
+Behaviour of the reference's ``d2p/_compile.py`` for the SW, affine, DTW and
+linear NW families (fakes ``:24-305,371-415``, autocast ``:857-931``):
 * every ``d2p::`` op gets a fake kernel describing its output shapes;
 * under ``torch.autocast("cuda")`` every op runs in float32 (inputs are upcast),
   because the DP recurrences accumulate error in 16-bit formats.
@@ -67,6 +67,20 @@ _FAKES = {
     "soft_dtw_hvp": lambda c, v, t, l, bw: c.new_empty(c.shape),
     "soft_dtw_param_jacobian": lambda c, t, l, bw: c.new_empty(c.shape),
     "soft_dtw_backward_full": lambda c, ga, t, l, bw: _full(c, 1),
+    # linear NW
+    "soft_nw": lambda s, g, t, l: _value_marginals(s),
+    "soft_nw_float": lambda s, g, t, l: _value_marginals(s),
+    "nw_forward": lambda s, g, t, l: _value_marginals(s),
+    "nw_forward_t": lambda s, g, t, l: _value_marginals(s),
+    "soft_nw_with_grads": lambda s, g, t, l: tuple(_value_marginals(s)) + _per_batch(s, 2),
+    "nw_value_grad_params": lambda s, g, t, l: _per_batch(s, 2),
+    "soft_nw_hvp": lambda s, v, g, t, l: s.new_empty(s.shape),
+    "nw_marginals_hvp": lambda s, v, g, t, l: s.new_empty(s.shape),
+    "soft_nw_param_jacobian": lambda s, p, g, t, l: s.new_empty(s.shape),
+    "nw_marginals_grad_gap": lambda s, g, t, l: s.new_empty(s.shape),
+    "nw_marginals_grad_temp": lambda s, g, t, l: s.new_empty(s.shape),
+    "soft_nw_backward_full": lambda s, ga, g, t, l: _full(s, 2),
+    "nw_marginals_backward": lambda s, ga, g, t, l: _full(s, 2),
 }
 
 for _name, _fn in _FAKES.items():

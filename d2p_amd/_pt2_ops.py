@@ -1,7 +1,7 @@
 """torch.compile-friendly custom ops (``d2p_py::``) over the ``torch.ops.d2p`` kernels.
 
-Behaviour of the reference's ``d2p/_pt2_ops.py`` for the SW, affine and DTW
-families (``:72-487,914-1083``): every op is an opaque ``torch.library``
+Behaviour of the reference's ``d2p/_pt2_ops.py`` for the SW, affine, DTW and
+linear NW families (``:72-487,914-1083``): every op is an opaque ``torch.library``
 custom op with a fake implementation, so dynamo and FakeTensor tracing never
 enter the HIP library; the two value ops of each family (tensor and float
 parameters) carry a Python autograd formula:
@@ -222,3 +222,46 @@ def _dtw_backward(ctx, grad_value, grad_marginals):
 
 soft_dtw.register_autograd(_dtw_backward, setup_context=_dtw_setup)
 soft_dtw_float.register_autograd(_dtw_backward, setup_context=_dtw_setup)
+
+# ------------------------------------------------------------------ linear-gap NW
+
+soft_nw_with_grads = _define(
+    "soft_nw_with_grads", f"(Tensor scores, {_SW_FLOAT}) -> (Tensor, Tensor, Tensor, Tensor)",
+    lambda s, g, t, l: (*_value_marginals_fake(s), s.new_empty([s.size(0)]),
+                        s.new_empty([s.size(0)])))
+soft_nw_hvp = _define(
+    "soft_nw_hvp", f"(Tensor scores, Tensor tangent, {_SW_FLOAT}) -> Tensor",
+    lambda s, v, g, t, l: s.new_empty(s.shape))
+soft_nw_param_jacobian = _define(
+    "soft_nw_param_jacobian", f"(Tensor scores, int param_type, {_SW_FLOAT}) -> Tensor",
+    lambda s, p, g, t, l: s.new_empty(s.shape))
+soft_nw_backward_full = _define(
+    "soft_nw_backward_full",
+    f"(Tensor scores, Tensor grad_alignment, {_SW_FLOAT}) -> (Tensor, Tensor, Tensor)",
+    lambda s, ga, g, t, l: (s.new_empty(s.shape), s.new_empty([1]), s.new_empty([1])))
+soft_nw = _define(
+    "soft_nw", "(Tensor scores, Tensor gap, Tensor temperature, Tensor lengths) -> "
+    "(Tensor, Tensor)", lambda s, g, t, l: _value_marginals_fake(s))
+soft_nw_float = _define(
+    "soft_nw_float", f"(Tensor scores, {_SW_FLOAT}) -> (Tensor, Tensor)",
+    lambda s, g, t, l: _value_marginals_fake(s))
+
+
+def _nw_backward(ctx, grad_value, grad_marginals):
+    scores, marginals = ctx.saved_tensors
+    want = ctx.needs_input_grad[1:3]
+    grad_scores = _scale_rows(grad_value, marginals)
+    grads = [None, None]
+    if grad_value is not None and any(want):
+        per_batch = soft_nw_with_grads(scores, *ctx.params, ctx.lengths)[2:]
+        grads = [_dot_sum(grad_value, g) if w else None for g, w in zip(per_batch, want)]
+    if grad_marginals is not None:
+        gs, *gp = soft_nw_backward_full(scores, grad_marginals.contiguous(), *ctx.params,
+                                        ctx.lengths)
+        grad_scores = _add(grad_scores, gs)
+        grads = [_add(a, b) if w else None for a, b, w in zip(grads, gp, want)]
+    return grad_scores, *grads, None
+
+
+soft_nw.register_autograd(_nw_backward, setup_context=_sw_setup)
+soft_nw_float.register_autograd(_nw_backward, setup_context=_sw_setup)

@@ -87,3 +87,23 @@ def test_torch_compile_dtw_and_affine(cuda):
     compiled(xc, yc).backward()
     assert torch.allclose(xc.grad, xe.grad, atol=1e-6) and torch.allclose(yc.grad, ye.grad,
                                                                           atol=1e-6)
+
+
+def test_torch_compile_nw(cuda):
+    """soft_nw under torch.compile (fake kernels for shapes), through both outputs."""
+    s = _seeded(8, (2, 40, 52)).to(cuda)
+    w = _seeded(9, (2, 40, 52)).to(cuda)
+
+    def loss(x):
+        r = d2p_amd.soft_nw(x, gap=-1.0, temperature=0.8)
+        return r.score.sum() + (r.alignment * w).sum()
+
+    compiled = torch.compile(loss, backend="aot_eager", fullgraph=True)
+    xe = s.clone().requires_grad_(True)
+    le = loss(xe)
+    le.backward()
+    xc = s.clone().requires_grad_(True)
+    lc = compiled(xc)
+    lc.backward()
+    assert torch.allclose(lc, le, rtol=1e-6, atol=1e-5)
+    assert torch.allclose(xc.grad, xe.grad, rtol=1e-5, atol=1e-5)

@@ -18,7 +18,7 @@ REF = "/root/reference"
 
 AUTOGRAD_OPS = {"soft_sw", "soft_sw_float", "sw_forward", "sw_forward_t", "soft_sw_affine",
                 "soft_sw_affine_float", "sw_affine_forward", "sw_affine_forward_t", "soft_dtw",
-                "soft_dtw_float"}
+                "soft_dtw_float", "soft_nw", "soft_nw_float", "nw_forward", "nw_forward_t"}
 
 
 def reference_schemas():
