@@ -24,7 +24,7 @@ AUTOGRAD_OPS = {"soft_sw", "soft_sw_float", "sw_forward", "sw_forward_t", "soft_
 def reference_schemas():
     out = {}
     for path in glob.glob(os.path.join(REF, "src", "*", "registry.cpp")):
-        if os.path.basename(os.path.dirname(path)) not in ("sw", "sw_affine", "dtw"):
+        if os.path.basename(os.path.dirname(path)) not in ("sw", "sw_affine", "dtw", "nw"):
             continue
         for s in re.findall(r'm\.def\("([^"]+)"\)', open(path).read()):
             out[s.split("(")[0]] = s
@@ -34,7 +34,7 @@ def reference_schemas():
 @pytest.mark.skipif(not os.path.isdir(REF), reason="reference sources absent")
 def test_schemas_byte_identical_to_reference():
     ref = reference_schemas()
-    assert len(ref) == 33          # 13 linear SW + 14 affine SW + 6 DTW
+    assert len(ref) == 46          # 13 linear SW + 14 affine SW + 6 DTW + 13 linear NW
     for name, schema in ref.items():
         ours = str(getattr(torch.ops.d2p, name).default._schema)
         assert ours == "d2p::" + schema, (ours, schema)
