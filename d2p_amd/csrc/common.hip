@@ -94,24 +94,28 @@ void profile_end(const char* name, hipStream_t stream, hipEvent_t start) {
     g_pending.push_back({name, start, end});
 }
 
-// dst = g[b] * src over [B, n]; float4 body when the row length allows it.
+// dst = g[b] * src over [B, n]; float4 body when the row length allows it.  Batch
+// rows run along blockIdx.y (stepping by gridDim.y), so the row factor is loaded once
+// per row and no index is divided.
 __global__ void __launch_bounds__(256)
 scale_by_batch_kernel(const float* __restrict__ src, const float* __restrict__ g,
-                      float* __restrict__ dst, long long n, long long total4, int vec) {
+                      float* __restrict__ dst, int B, long long n, int vec) {
     const long long stride = (long long)gridDim.x * blockDim.x;
-    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (vec) {
-        typedef float v4f __attribute__((ext_vector_type(4)));
-        const v4f* s4 = reinterpret_cast<const v4f*>(src);
-        v4f* d4 = reinterpret_cast<v4f*>(dst);
-        const long long n4 = n >> 2;
-        for (; idx < total4; idx += stride) {
-            const float gb = g[idx / n4];
-            v4f v = __builtin_nontemporal_load(s4 + idx);
-            __builtin_nontemporal_store(v * gb, d4 + idx);
+    const long long first = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    for (int b = blockIdx.y; b < B; b += gridDim.y) {
+        const float gb = g[b];
+        if (vec) {
+            const long long n4 = n >> 2;
+            const v4f* s4 = reinterpret_cast<const v4f*>(src) + (size_t)b * n4;
+            v4f* d4 = reinterpret_cast<v4f*>(dst) + (size_t)b * n4;
+            for (long long i = first; i < n4; i += stride)
+                __builtin_nontemporal_store(__builtin_nontemporal_load(s4 + i) * gb, d4 + i);
+        } else {
+            const float* s1 = src + (size_t)b * n;
+            float* d1 = dst + (size_t)b * n;
+            for (long long i = first; i < n; i += stride) d1[i] = gb * s1[i];
         }
-    } else {
-        for (; idx < total4; idx += stride) dst[idx] = g[idx / n] * src[idx];
     }
 }
 
@@ -155,12 +159,15 @@ extern "C" int d2p_scale_by_batch(const float* src, const float* g, float* dst, 
     if (B == 0 || per_batch == 0) return D2P_OK;
     D2P_REQUIRE(src && g && dst, "null pointer argument");
     const bool vec = (per_batch % 4 == 0) && (((uintptr_t)src | (uintptr_t)dst) % 16 == 0);
-    const long long total = (long long)B * per_batch;
-    const long long work = vec ? total / 4 : total;
-    long long blocks = (work + 255) / 256;
-    if (blocks > 256 * 64) blocks = 256 * 64;
-    D2P_LAUNCH("scale_by_batch", d2p_amd::scale_by_batch_kernel, dim3((unsigned)blocks),
-               dim3(256), 0, (hipStream_t)stream, src, g, dst, per_batch, work, vec ? 1 : 0);
+    // about 16384 workgroups in all: rows along y, each row's elements along x
+    const long long row_work = vec ? per_batch / 4 : per_batch;
+    const int by = B < 65535 ? B : 65535;
+    long long bx = (row_work + 255) / 256;
+    const long long cap = 16384 / by > 1 ? 16384 / by : 1;
+    if (bx > cap) bx = cap;
+    D2P_LAUNCH("scale_by_batch", d2p_amd::scale_by_batch_kernel,
+               dim3((unsigned)bx, (unsigned)by), dim3(256), 0, (hipStream_t)stream, src, g,
+               dst, B, per_batch, vec ? 1 : 0);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
