@@ -1402,3 +1402,148 @@ void oracle_nw_param_grad(const float* alpha, const float* scores, const float* 
         }
     }
 }
+
+/* ======================= affine-gap soft Needleman-Wunsch ======================= */
+
+/* softmax3, nw_affine/kernels_cpu.cpp:59-71: Kahan sum over the terms above NINF
+ * only; a non-positive sum gives NINF. */
+static float nwa_lse3(float a, float b, float c, float T) {
+    float m = fmax2(fmax2(a, b), c);
+    if (m <= NINF) return NINF;
+    kahan k = {0.0f, 0.0f};
+    if (a > NINF) kadd(&k, xexp((a - m) / T));
+    if (b > NINF) kadd(&k, xexp((b - m) / T));
+    if (c > NINF) kadd(&k, xexp((c - m) / T));
+    if (k.s <= 0.0f) return NINF;
+    return m + T * logf(k.s);
+}
+
+/* softmax3_weights, nw_affine/kernels_cpu.cpp:74-94: plain-sum normaliser. */
+static void nwa_w3(float a, float b, float c, float T, float* w) {
+    float m = fmax2(fmax2(a, b), c);
+    if (m <= NINF) { w[0] = w[1] = w[2] = 0.0f; return; }
+    float ea = (a > NINF) ? xexp((a - m) / T) : 0.0f;
+    float eb = (b > NINF) ? xexp((b - m) / T) : 0.0f;
+    float ec = (c > NINF) ? xexp((c - m) / T) : 0.0f;
+    float total = ea + eb + ec;
+    if (total > 0.0f) { w[0] = ea / total; w[1] = eb / total; w[2] = ec / total; }
+    else w[0] = w[1] = w[2] = 0.0f;
+}
+
+/* nw_affine/kernels_cpu.cpp:100-187: three states over (L1+1) x (L2+1),
+ * M(0,0) = 0, I(i,0) = open + (i-1) ext, D(0,j) = open + (j-1) ext, everything
+ * else NINF;  M = s + LSE(M, I, D)[diag],  I = LSE(M+open, I+ext, D+open)[up],
+ * D = LSE(M+open, I+open, D+ext)[left];  value LSE(M, I, D)[L1, L2]. */
+void oracle_nwa_forward(const float* scores, float* alpha, float* score, const int* lengths,
+                        int B, int maxL1, int maxL2, float go, float ge, float T) {
+    const size_t cstride = (size_t)(maxL1 + 1) * (maxL2 + 1);
+    const size_t astride = 3 * cstride;
+    const size_t sstride = (size_t)maxL1 * maxL2;
+    const size_t acols = (size_t)maxL2 + 1, scols = (size_t)maxL2;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int b = 0; b < B; ++b) {
+        const float* s = scores + (size_t)b * sstride;
+        float* a = alpha + (size_t)b * astride;
+        const int L1 = lengths[2 * b], L2 = lengths[2 * b + 1];
+        for (size_t q = 0; q < astride; ++q) a[q] = NINF;
+        a[PM(0)] = 0.0f;
+        for (int i = 1; i <= L1; ++i) a[PI(AIDX(i, 0))] = go + (i - 1) * ge;
+        for (int j = 1; j <= L2; ++j) a[PD(AIDX(0, j))] = go + (j - 1) * ge;
+        FOR_DIAG_FWD(L1, L2, i, j) {
+            const size_t c = AIDX(i, j), cd = AIDX(i - 1, j - 1), cu = AIDX(i - 1, j),
+                         cl = AIDX(i, j - 1);
+            const float sc = s[SIDX(i, j)];
+            a[PM(c)] = sc + nwa_lse3(a[PM(cd)], a[PI(cd)], a[PD(cd)], T);
+            a[PI(c)] = nwa_lse3(a[PM(cu)] + go, a[PI(cu)] + ge, a[PD(cu)] + go, T);
+            a[PD(c)] = nwa_lse3(a[PM(cl)] + go, a[PI(cl)] + go, a[PD(cl)] + ge, T);
+        }
+        const size_t f = AIDX(L1, L2);
+        score[b] = nwa_lse3(a[PM(f)], a[PI(f)], a[PD(f)], T);
+    }
+}
+
+/* nw_affine/kernels_cpu.cpp:193-347: beta of the three terminal states = their
+ * softmax weights; reverse anti-diagonals pass each state's beta (when above 1e-20
+ * and its predecessors' LSE is finite) to its predecessors by their weights; the
+ * marginal of (i, j) is beta_M; open / ext counts come from the I and D
+ * transitions and the boundary I(i,0), D(0,j) chains; dS/dT = (S - E[path score])
+ * / T with the match part Kahan-summed. */
+void oracle_nwa_backward(const float* alpha, const float* scores, const float* score,
+                         float* beta, float* posteriors, float* grad_open, float* grad_ext,
+                         float* grad_T, const int* lengths, int B, int maxL1, int maxL2,
+                         float go, float ge, float T) {
+    const size_t cstride = (size_t)(maxL1 + 1) * (maxL2 + 1);
+    const size_t astride = 3 * cstride;
+    const size_t sstride = (size_t)maxL1 * maxL2;
+    const size_t acols = (size_t)maxL2 + 1, scols = (size_t)maxL2;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int b = 0; b < B; ++b) {
+        const float* a = alpha + (size_t)b * astride;
+        const float* s = scores + (size_t)b * sstride;
+        float* be = beta + (size_t)b * astride;
+        float* post = posteriors + (size_t)b * sstride;
+        const float S = score[b];
+        const int L1 = lengths[2 * b], L2 = lengths[2 * b + 1];
+        for (size_t q = 0; q < astride; ++q) be[q] = 0.0f;
+        for (size_t q = 0; q < sstride; ++q) post[q] = 0.0f;
+        float w[3];
+        const size_t f = AIDX(L1, L2);
+        nwa_w3(a[PM(f)], a[PI(f)], a[PD(f)], T, w);
+        be[PM(f)] = w[0];
+        be[PI(f)] = w[1];
+        be[PD(f)] = w[2];
+        float so = 0.0f, se = 0.0f;
+        kahan ms = {0.0f, 0.0f};
+        FOR_DIAG_REV(L1, L2, i, j) {
+            const size_t c = AIDX(i, j), cd = AIDX(i - 1, j - 1), cu = AIDX(i - 1, j),
+                         cl = AIDX(i, j - 1);
+            const float sc = s[SIDX(i, j)];
+            const float bM = be[PM(c)], bI = be[PI(c)], bD = be[PD(c)];
+            if (bM > 1e-20f) {
+                const float m1 = a[PM(cd)], m2 = a[PI(cd)], m3 = a[PD(cd)];
+                if (nwa_lse3(m1, m2, m3, T) > NINF) {
+                    nwa_w3(m1, m2, m3, T, w);
+                    if (m1 > NINF) be[PM(cd)] += bM * w[0];
+                    if (m2 > NINF) be[PI(cd)] += bM * w[1];
+                    if (m3 > NINF) be[PD(cd)] += bM * w[2];
+                    post[SIDX(i, j)] += bM;
+                    kadd(&ms, bM * sc);
+                }
+            }
+            if (bI > 1e-20f) {
+                const float i1 = a[PM(cu)] + go, i2 = a[PI(cu)] + ge, i3 = a[PD(cu)] + go;
+                if (nwa_lse3(i1, i2, i3, T) > NINF) {
+                    nwa_w3(i1, i2, i3, T, w);
+                    be[PM(cu)] += bI * w[0];
+                    be[PI(cu)] += bI * w[1];
+                    be[PD(cu)] += bI * w[2];
+                    so += bI * (w[0] + w[2]);
+                    se += bI * w[1];
+                }
+            }
+            if (bD > 1e-20f) {
+                const float d1 = a[PM(cl)] + go, d2 = a[PI(cl)] + go, d3 = a[PD(cl)] + ge;
+                if (nwa_lse3(d1, d2, d3, T) > NINF) {
+                    nwa_w3(d1, d2, d3, T, w);
+                    be[PM(cl)] += bD * w[0];
+                    be[PI(cl)] += bD * w[1];
+                    be[PD(cl)] += bD * w[2];
+                    so += bD * (w[0] + w[1]);
+                    se += bD * w[2];
+                }
+            }
+        }
+        for (int i = 1; i <= L1; ++i) {
+            const float bb = be[PI(AIDX(i, 0))];
+            if (bb > 1e-20f) { so += bb; se += bb * (float)(i - 1); }
+        }
+        for (int j = 1; j <= L2; ++j) {
+            const float bb = be[PD(AIDX(0, j))];
+            if (bb > 1e-20f) { so += bb; se += bb * (float)(j - 1); }
+        }
+        grad_open[b] = so;
+        grad_ext[b] = se;
+        const float expected = ms.s + so * go + se * ge;
+        grad_T[b] = (S - expected) / T;
+    }
+}

@@ -103,6 +103,14 @@ void oracle_dtw_backward_sums64(const float* alpha, const float* costs, const fl
 
 int oracle_max_threads(void);
 
+/* affine-gap soft Needleman-Wunsch (nw_affine/kernels_cpu.cpp) */
+void oracle_nwa_forward(const float* scores, float* alpha, float* score, const int* lengths,
+                        int B, int maxL1, int maxL2, float go, float ge, float T);
+void oracle_nwa_backward(const float* alpha, const float* scores, const float* score,
+                         float* beta, float* posteriors, float* grad_open, float* grad_ext,
+                         float* grad_T, const int* lengths, int B, int maxL1, int maxL2,
+                         float go, float ge, float T);
+
 #ifdef __cplusplus
 }
 #endif

@@ -77,6 +77,10 @@ _SIGS = {
                [_F, _F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f]),
     "nw_param_grad": ("oracle_nw_param_grad", "nw_param_grad_cpu",
                       [_F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f, _i]),
+    "nwa_forward": ("oracle_nwa_forward", "nw_affine_forward_cpu",
+                    [_F, _F, _F, _I, _i, _i, _i, _f, _f, _f]),
+    "nwa_backward": ("oracle_nwa_backward", "nw_affine_backward_cpu",
+                     [_F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f, _f]),
 }
 
 
@@ -376,6 +380,33 @@ class CpuKernels:
         self.fn["nw_param_grad"](_p(alpha), _p(s), _p(score), _p(dS), _p(U), _p(be), _p(W),
                                  _p(dP), _p(ln), B, L1, L2, gap, T, ptype)
         return dP
+
+    # ---------------- affine-gap NW ----------------
+    def nwa_forward(self, scores, lengths, go, ge, T):
+        s = self._a(scores)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        alpha = np.zeros((B, 3 * (L1 + 1) * (L2 + 1)), self.ft)
+        score = np.zeros((B,), self.ft)
+        self.fn["nwa_forward"](_p(s), _p(alpha), _p(score), _p(ln), B, L1, L2, go, ge, T)
+        return alpha, score
+
+    def nwa_backward(self, alpha, scores, score, lengths, go, ge, T):
+        s = self._a(scores)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        beta = np.zeros_like(alpha)
+        post = np.zeros_like(s)
+        g = [np.zeros((B,), self.ft) for _ in range(3)]
+        self.fn["nwa_backward"](_p(alpha), _p(s), _p(score), _p(beta), _p(post), _p(g[0]),
+                                _p(g[1]), _p(g[2]), _p(ln), B, L1, L2, go, ge, T)
+        return post, g[0], g[1], g[2]
+
+    def soft_nw_affine(self, scores, go=-2.0, ge=-0.5, T=1.0, lengths=None):
+        """value, marginals, grad_open, grad_ext, grad_T (nw_affine forward + backward)."""
+        alpha, score = self.nwa_forward(scores, lengths, go, ge, T)
+        post, gO, gE, gT = self.nwa_backward(alpha, scores, score, lengths, go, ge, T)
+        return score, post, gO, gE, gT
 
     # ---------------- binding-level composites ----------------
     def soft_nw_hvp(self, scores, V, gap=-1.0, T=1.0, lengths=None):

@@ -413,3 +413,27 @@ def test_oracle64_against_math(seed, B, L1, L2, T, lens):
     for i, (got, want) in enumerate(pairs):
         assert got.dtype == np.float64
         _close(got, want, 1e-9 * max(1.0, np.abs(want).max()), 0, f"second order {i}")
+
+
+@pytest.mark.parametrize("s,go,ge,T", [(0.7, -2.0, -0.5, 1.0), (-1.3, -1.0, -0.2, 0.5),
+                                       (2.0, -3.0, -1.0, 2.0)])
+def test_nw_affine_small_closed_forms(s, go, ge, T):
+    """1x1: paths M (score s) and the two two-gap paths I->D / D->I (2 open each), so
+    value = T log(e^{s/T} + 2 e^{2 open/T}), marginal = e^{s/T} / that sum, and the
+    open count 4 e^{2 open/T} / sum.  Empty rows/columns: the boundary chain open +
+    (n-1) ext, with gradients 1 and n-1."""
+    k = O.get("oracle")
+    sc = np.array([[[s]]], np.float32)
+    v, post, gO, gE, gT = k.soft_nw_affine(sc, go, ge, T)
+    Z = np.exp(s / T) + 2 * np.exp(2 * go / T)
+    assert v[0] == pytest.approx(T * np.log(Z), rel=1e-6, abs=1e-6)
+    assert post[0, 0, 0] == pytest.approx(np.exp(s / T) / Z, rel=1e-5, abs=1e-6)
+    assert gO[0] == pytest.approx(4 * np.exp(2 * go / T) / Z, rel=1e-5, abs=1e-6)
+    assert gE[0] == pytest.approx(0.0, abs=1e-7)
+    x = np.zeros((3, 5, 4), np.float32)
+    lens = np.array([[5, 0], [0, 4], [0, 0]], np.int32)
+    v, post, gO, gE, gT = k.soft_nw_affine(x, go, ge, T, lens)
+    np.testing.assert_allclose(v, [go + 4 * ge, go + 3 * ge, 0.0], rtol=1e-6)
+    np.testing.assert_allclose(gO, [1.0, 1.0, 0.0])
+    np.testing.assert_allclose(gE, [4.0, 3.0, 0.0])
+    assert not post.any()

@@ -68,6 +68,18 @@ def test_nw_bit_exact(seed, B, L1, L2, scale, gap, T, lens):
 
 
 @pytest.mark.parametrize("seed,B,L1,L2,scale,gap,T,lens", SW_CASES)
+def test_nw_affine_bit_exact(seed, B, L1, L2, scale, gap, T, lens):
+    o, r = O.get("oracle"), O.get("reference")
+    s = _rand(seed + 80, (B, L1, L2), scale)
+    go, ge = -3.0 * abs(gap), -0.5 * abs(gap)
+    _same(o.soft_nw_affine(s, go, ge, T, lens), r.soft_nw_affine(s, go, ge, T, lens),
+          "soft_nw_affine")
+    alpha_o, _ = o.nwa_forward(s, lens, go, ge, T)
+    alpha_r, _ = r.nwa_forward(s, lens, go, ge, T)
+    _same(alpha_o, alpha_r, "nw_affine alpha")
+
+
+@pytest.mark.parametrize("seed,B,L1,L2,scale,gap,T,lens", SW_CASES)
 def test_affine_bit_exact(seed, B, L1, L2, scale, gap, T, lens):
     o, r = O.get("oracle"), O.get("reference")
     s = _rand(seed + 10, (B, L1, L2), scale)
