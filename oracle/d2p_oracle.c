@@ -1547,3 +1547,97 @@ void oracle_nwa_backward(const float* alpha, const float* scores, const float* s
         grad_T[b] = (S - expected) / T;
     }
 }
+
+/* nw_affine/kernels_cpu.cpp:353-613: forward tangents of the three states
+ * (M: V + E_w[d_pred] over the diagonal states; I, D: E_w over their up / left
+ * candidates; 0 where the predecessors' LSE is NINF), d_score = E_w[d] over the
+ * terminal states; reverse sweep with beta and its tangent, the weight tangents
+ * w_k (d_k - E_w[d]) / T, cells visited when beta > 1e-20 or |dbeta| > 1e-20;
+ * H(i, j) = dbeta_M. */
+void oracle_nwa_hvp(const float* alpha, const float* scores, const float* score,
+                    const float* V, float* d_alpha, float* d_score, float* beta,
+                    float* d_beta, float* H, const int* lengths, int B, int maxL1, int maxL2,
+                    float go, float ge, float T) {
+    const size_t cstride = (size_t)(maxL1 + 1) * (maxL2 + 1);
+    const size_t astride = 3 * cstride;
+    const size_t sstride = (size_t)maxL1 * maxL2;
+    const size_t acols = (size_t)maxL2 + 1, scols = (size_t)maxL2;
+    (void)score;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int b = 0; b < B; ++b) {
+        const float* a = alpha + (size_t)b * astride;
+        const float* v = V + (size_t)b * sstride;
+        float* da = d_alpha + (size_t)b * astride;
+        float* be = beta + (size_t)b * astride;
+        float* db = d_beta + (size_t)b * astride;
+        float* h = H + (size_t)b * sstride;
+        const int L1 = lengths[2 * b], L2 = lengths[2 * b + 1];
+        for (size_t q = 0; q < astride; ++q) { da[q] = 0.0f; be[q] = 0.0f; db[q] = 0.0f; }
+        for (size_t q = 0; q < sstride; ++q) h[q] = 0.0f;
+        float w[3];
+        FOR_DIAG_FWD(L1, L2, i, j) {
+            const size_t c = AIDX(i, j), cd = AIDX(i - 1, j - 1), cu = AIDX(i - 1, j),
+                         cl = AIDX(i, j - 1);
+            const float Vs = v[SIDX(i, j)];
+            {
+                const float m1 = a[PM(cd)], m2 = a[PI(cd)], m3 = a[PD(cd)];
+                if (nwa_lse3(m1, m2, m3, T) > NINF) {
+                    nwa_w3(m1, m2, m3, T, w);
+                    da[PM(c)] = Vs + w[0] * da[PM(cd)] + w[1] * da[PI(cd)] + w[2] * da[PD(cd)];
+                } else da[PM(c)] = 0.0f;
+            }
+            {
+                const float i1 = a[PM(cu)] + go, i2 = a[PI(cu)] + ge, i3 = a[PD(cu)] + go;
+                if (nwa_lse3(i1, i2, i3, T) > NINF) {
+                    nwa_w3(i1, i2, i3, T, w);
+                    da[PI(c)] = w[0] * da[PM(cu)] + w[1] * da[PI(cu)] + w[2] * da[PD(cu)];
+                } else da[PI(c)] = 0.0f;
+            }
+            {
+                const float d1 = a[PM(cl)] + go, d2 = a[PI(cl)] + go, d3 = a[PD(cl)] + ge;
+                if (nwa_lse3(d1, d2, d3, T) > NINF) {
+                    nwa_w3(d1, d2, d3, T, w);
+                    da[PD(c)] = w[0] * da[PM(cl)] + w[1] * da[PI(cl)] + w[2] * da[PD(cl)];
+                } else da[PD(c)] = 0.0f;
+            }
+        }
+        const size_t f = AIDX(L1, L2);
+        nwa_w3(a[PM(f)], a[PI(f)], a[PD(f)], T, w);
+        d_score[b] = w[0] * da[PM(f)] + w[1] * da[PI(f)] + w[2] * da[PD(f)];
+        be[PM(f)] = w[0];
+        be[PI(f)] = w[1];
+        be[PD(f)] = w[2];
+        {
+            const float dm = da[PM(f)], di = da[PI(f)], dd = da[PD(f)];
+            const float E = w[0] * dm + w[1] * di + w[2] * dd;
+            db[PM(f)] = w[0] * (dm - E) / T;
+            db[PI(f)] = w[1] * (di - E) / T;
+            db[PD(f)] = w[2] * (dd - E) / T;
+        }
+        FOR_DIAG_REV(L1, L2, i, j) {
+            const size_t c = AIDX(i, j);
+            const size_t pred[3] = {AIDX(i - 1, j - 1), AIDX(i - 1, j), AIDX(i, j - 1)};
+            for (int st = 0; st < 3; ++st) {   /* M (diagonal), I (up), D (left) */
+                const float bs = be[st * cstride + c], dbs = db[st * cstride + c];
+                if (!(bs > 1e-20f || fabsf(dbs) > 1e-20f)) continue;
+                const size_t p = pred[st];
+                float x[3];
+                if (st == 0) { x[0] = a[PM(p)]; x[1] = a[PI(p)]; x[2] = a[PD(p)]; }
+                else if (st == 1) { x[0] = a[PM(p)] + go; x[1] = a[PI(p)] + ge; x[2] = a[PD(p)] + go; }
+                else { x[0] = a[PM(p)] + go; x[1] = a[PI(p)] + go; x[2] = a[PD(p)] + ge; }
+                if (!(nwa_lse3(x[0], x[1], x[2], T) > NINF)) continue;
+                nwa_w3(x[0], x[1], x[2], T, w);
+                const float d0 = da[PM(p)], d1 = da[PI(p)], d2 = da[PD(p)];
+                const float E = w[0] * d0 + w[1] * d1 + w[2] * d2;
+                const float dw[3] = {w[0] * (d0 - E) / T, w[1] * (d1 - E) / T,
+                                     w[2] * (d2 - E) / T};
+                for (int q = 0; q < 3; ++q) {
+                    if (st == 0 && !(x[q] > NINF)) continue;   /* only M checks its inputs */
+                    be[q * cstride + p] += bs * w[q];
+                    db[q * cstride + p] += dbs * w[q] + bs * dw[q];
+                }
+                if (st == 0) h[SIDX(i, j)] += dbs;
+            }
+        }
+    }
+}

@@ -110,6 +110,10 @@ void oracle_nwa_backward(const float* alpha, const float* scores, const float* s
                          float* beta, float* posteriors, float* grad_open, float* grad_ext,
                          float* grad_T, const int* lengths, int B, int maxL1, int maxL2,
                          float go, float ge, float T);
+void oracle_nwa_hvp(const float* alpha, const float* scores, const float* score,
+                    const float* V, float* d_alpha, float* d_score, float* beta,
+                    float* d_beta, float* H, const int* lengths, int B, int maxL1, int maxL2,
+                    float go, float ge, float T);
 
 #ifdef __cplusplus
 }

@@ -81,6 +81,8 @@ _SIGS = {
                     [_F, _F, _F, _I, _i, _i, _i, _f, _f, _f]),
     "nwa_backward": ("oracle_nwa_backward", "nw_affine_backward_cpu",
                      [_F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f, _f]),
+    "nwa_hvp": ("oracle_nwa_hvp", "nw_affine_hvp_cpu",
+                [_F, _F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f, _f]),
 }
 
 
@@ -401,6 +403,24 @@ class CpuKernels:
         self.fn["nwa_backward"](_p(alpha), _p(s), _p(score), _p(beta), _p(post), _p(g[0]),
                                 _p(g[1]), _p(g[2]), _p(ln), B, L1, L2, go, ge, T)
         return post, g[0], g[1], g[2]
+
+    def nwa_hvp(self, alpha, scores, score, V, lengths, go, ge, T):
+        s = self._a(scores)
+        v = self._a(V)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        da = np.zeros_like(alpha)
+        ds = np.zeros((B,), self.ft)
+        be = np.zeros_like(alpha)
+        dbe = np.zeros_like(alpha)
+        H = np.zeros_like(s)
+        self.fn["nwa_hvp"](_p(alpha), _p(s), _p(score), _p(v), _p(da), _p(ds), _p(be), _p(dbe),
+                           _p(H), _p(ln), B, L1, L2, go, ge, T)
+        return H, ds
+
+    def soft_nw_affine_hvp(self, scores, V, go=-2.0, ge=-0.5, T=1.0, lengths=None):
+        alpha, score = self.nwa_forward(scores, lengths, go, ge, T)
+        return self.nwa_hvp(alpha, scores, score, V, lengths, go, ge, T)[0]
 
     def soft_nw_affine(self, scores, go=-2.0, ge=-0.5, T=1.0, lengths=None):
         """value, marginals, grad_open, grad_ext, grad_T (nw_affine forward + backward)."""

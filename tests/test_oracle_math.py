@@ -437,3 +437,24 @@ def test_nw_affine_small_closed_forms(s, go, ge, T):
     np.testing.assert_allclose(gO, [1.0, 1.0, 0.0])
     np.testing.assert_allclose(gE, [4.0, 3.0, 0.0])
     assert not post.any()
+
+
+@pytest.mark.parametrize("seed,L1,L2,T", [(0, 5, 7, 1.0), (1, 9, 6, 0.5), (2, 12, 12, 2.0)])
+def test_nw_affine_hvp_is_derivative_of_marginals(seed, L1, L2, T):
+    """In double precision the affine NW HVP equals the central difference of the
+    marginals along V (the marginals are dvalue/dscores, so H V = d marginals / d eps)."""
+    k = O.get("oracle64")
+    rng = np.random.default_rng(seed)
+    s = rng.standard_normal((2, L1, L2))
+    V = rng.standard_normal((2, L1, L2))
+    go, ge, eps = -2.0, -0.5, 1e-6
+    H = k.soft_nw_affine_hvp(s, V, go, ge, T)
+    mp = k.soft_nw_affine(s + eps * V, go, ge, T)[1]
+    mm = k.soft_nw_affine(s - eps * V, go, ge, T)[1]
+    np.testing.assert_allclose(H, (mp - mm) / (2 * eps), rtol=1e-5, atol=1e-7)
+    # and the marginals are the value's gradient
+    vp = k.soft_nw_affine(s + eps * V, go, ge, T)[0]
+    vm = k.soft_nw_affine(s - eps * V, go, ge, T)[0]
+    m = k.soft_nw_affine(s, go, ge, T)[1]
+    np.testing.assert_allclose((vp - vm) / (2 * eps), (m * V).sum(axis=(1, 2)), rtol=1e-6,
+                               atol=1e-8)

@@ -77,6 +77,9 @@ def test_nw_affine_bit_exact(seed, B, L1, L2, scale, gap, T, lens):
     alpha_o, _ = o.nwa_forward(s, lens, go, ge, T)
     alpha_r, _ = r.nwa_forward(s, lens, go, ge, T)
     _same(alpha_o, alpha_r, "nw_affine alpha")
+    V = _rand(seed + 81, (B, L1, L2))
+    _same(o.soft_nw_affine_hvp(s, V, go, ge, T, lens), r.soft_nw_affine_hvp(s, V, go, ge, T, lens),
+          "nw_affine hvp")
 
 
 @pytest.mark.parametrize("seed,B,L1,L2,scale,gap,T,lens", SW_CASES)
