@@ -1641,3 +1641,136 @@ void oracle_nwa_hvp(const float* alpha, const float* scores, const float* score,
         }
     }
 }
+
+/* nw_affine/kernels_cpu.cpp:619-1002: dP/dtheta for theta = open (0), ext (1) or
+ * T (2).  Forward tangents U: boundary chains I(i,0), D(0,j) start at 1 (open) or
+ * i-1 / j-1 (ext); each state's candidates carry their direct derivative (open:
+ * M->I, D->I, M->D, I->D; ext: I->I, D->D), and for T the state adds
+ * (alpha - E_w[v]) / T (M: v includes the score).  Reverse sweep as the HVP's with
+ * weight tangents w_k (u_k - E_w[u]) / T (+ w_k (E_w[v] - v_k) / T^2 for T);
+ * dP(i, j) = W_M.  dS/dtheta is unused: the terminal betas carry their own
+ * tangents. */
+void oracle_nwa_param_grad(const float* alpha, const float* scores, const float* score,
+                           const float* dS_dtheta, float* U, float* beta, float* W, float* dP,
+                           const int* lengths, int B, int maxL1, int maxL2, float go, float ge,
+                           float T, int ptype) {
+    const size_t cstride = (size_t)(maxL1 + 1) * (maxL2 + 1);
+    const size_t astride = 3 * cstride;
+    const size_t sstride = (size_t)maxL1 * maxL2;
+    const size_t acols = (size_t)maxL2 + 1, scols = (size_t)maxL2;
+    (void)score;
+    (void)dS_dtheta;
+    /* direct derivatives of the candidates (M, I, D predecessors) of I and of D */
+    const float dI[3] = {ptype == 0 ? 1.0f : 0.0f, ptype == 1 ? 1.0f : 0.0f,
+                         ptype == 0 ? 1.0f : 0.0f};
+    const float dD[3] = {ptype == 0 ? 1.0f : 0.0f, ptype == 0 ? 1.0f : 0.0f,
+                         ptype == 1 ? 1.0f : 0.0f};
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int b = 0; b < B; ++b) {
+        const float* a = alpha + (size_t)b * astride;
+        const float* s = scores + (size_t)b * sstride;
+        float* u = U + (size_t)b * astride;
+        float* be = beta + (size_t)b * astride;
+        float* wt = W + (size_t)b * astride;
+        float* dp = dP + (size_t)b * sstride;
+        const int L1 = lengths[2 * b], L2 = lengths[2 * b + 1];
+        for (size_t q = 0; q < astride; ++q) { u[q] = 0.0f; be[q] = 0.0f; wt[q] = 0.0f; }
+        for (size_t q = 0; q < sstride; ++q) dp[q] = 0.0f;
+        if (ptype == 0 || ptype == 1) {
+            for (int i = 1; i <= L1; ++i) u[PI(AIDX(i, 0))] = ptype == 0 ? 1.0f : (float)(i - 1);
+            for (int j = 1; j <= L2; ++j) u[PD(AIDX(0, j))] = ptype == 0 ? 1.0f : (float)(j - 1);
+        }
+        float w[3];
+        FOR_DIAG_FWD(L1, L2, i, j) {
+            const size_t c = AIDX(i, j), cd = AIDX(i - 1, j - 1), cu = AIDX(i - 1, j),
+                         cl = AIDX(i, j - 1);
+            {
+                const float m1 = a[PM(cd)], m2 = a[PI(cd)], m3 = a[PD(cd)];
+                if (nwa_lse3(m1, m2, m3, T) > NINF) {
+                    nwa_w3(m1, m2, m3, T, w);
+                    float x = w[0] * u[PM(cd)] + w[1] * u[PI(cd)] + w[2] * u[PD(cd)];
+                    if (ptype == 2) {
+                        const float Ev = w[0] * m1 + w[1] * m2 + w[2] * m3;
+                        x += (a[PM(c)] - (Ev + s[SIDX(i, j)])) / T;
+                    }
+                    u[PM(c)] = x;
+                }
+            }
+            {
+                const float i1 = a[PM(cu)] + go, i2 = a[PI(cu)] + ge, i3 = a[PD(cu)] + go;
+                if (nwa_lse3(i1, i2, i3, T) > NINF) {
+                    nwa_w3(i1, i2, i3, T, w);
+                    float x = w[0] * (u[PM(cu)] + dI[0]) + w[1] * (u[PI(cu)] + dI[1]) +
+                              w[2] * (u[PD(cu)] + dI[2]);
+                    if (ptype == 2) {
+                        const float Ev = w[0] * i1 + w[1] * i2 + w[2] * i3;
+                        x += (a[PI(c)] - Ev) / T;
+                    }
+                    u[PI(c)] = x;
+                }
+            }
+            {
+                const float d1 = a[PM(cl)] + go, d2 = a[PI(cl)] + go, d3 = a[PD(cl)] + ge;
+                if (nwa_lse3(d1, d2, d3, T) > NINF) {
+                    nwa_w3(d1, d2, d3, T, w);
+                    float x = w[0] * (u[PM(cl)] + dD[0]) + w[1] * (u[PI(cl)] + dD[1]) +
+                              w[2] * (u[PD(cl)] + dD[2]);
+                    if (ptype == 2) {
+                        const float Ev = w[0] * d1 + w[1] * d2 + w[2] * d3;
+                        x += (a[PD(c)] - Ev) / T;
+                    }
+                    u[PD(c)] = x;
+                }
+            }
+        }
+        const size_t f = AIDX(L1, L2);
+        nwa_w3(a[PM(f)], a[PI(f)], a[PD(f)], T, w);
+        for (int q = 0; q < 3; ++q) be[q * cstride + f] = w[q];
+        {
+            const float uk[3] = {u[PM(f)], u[PI(f)], u[PD(f)]};
+            const float Eu = w[0] * uk[0] + w[1] * uk[1] + w[2] * uk[2];
+            float dw[3];
+            for (int q = 0; q < 3; ++q) dw[q] = w[q] * (uk[q] - Eu) / T;
+            if (ptype == 2) {
+                const float Ev = w[0] * a[PM(f)] + w[1] * a[PI(f)] + w[2] * a[PD(f)];
+                const float iT2 = 1.0f / (T * T);
+                for (int q = 0; q < 3; ++q) dw[q] += w[q] * (Ev - a[q * cstride + f]) * iT2;
+            }
+            for (int q = 0; q < 3; ++q) wt[q * cstride + f] = dw[q];
+        }
+        FOR_DIAG_REV(L1, L2, i, j) {
+            const size_t c = AIDX(i, j);
+            const size_t pred[3] = {AIDX(i - 1, j - 1), AIDX(i - 1, j), AIDX(i, j - 1)};
+            for (int st = 0; st < 3; ++st) {   /* M (diagonal), I (up), D (left) */
+                const float bs = be[st * cstride + c], ws = wt[st * cstride + c];
+                if (!(bs > 1e-20f || fabsf(ws) > 1e-20f)) continue;
+                const size_t p = pred[st];
+                float x[3];
+                if (st == 0) { x[0] = a[PM(p)]; x[1] = a[PI(p)]; x[2] = a[PD(p)]; }
+                else if (st == 1) { x[0] = a[PM(p)] + go; x[1] = a[PI(p)] + ge; x[2] = a[PD(p)] + go; }
+                else { x[0] = a[PM(p)] + go; x[1] = a[PI(p)] + go; x[2] = a[PD(p)] + ge; }
+                if (!(nwa_lse3(x[0], x[1], x[2], T) > NINF)) continue;
+                nwa_w3(x[0], x[1], x[2], T, w);
+                float uk[3] = {u[PM(p)], u[PI(p)], u[PD(p)]};
+                if (st > 0) {
+                    const float* dd = st == 1 ? dI : dD;
+                    for (int q = 0; q < 3; ++q) if (dd[q] != 0.0f) uk[q] += 1.0f;
+                }
+                const float Eu = w[0] * uk[0] + w[1] * uk[1] + w[2] * uk[2];
+                float dw[3];
+                for (int q = 0; q < 3; ++q) dw[q] = w[q] * (uk[q] - Eu) / T;
+                if (ptype == 2) {
+                    const float Ev = w[0] * x[0] + w[1] * x[1] + w[2] * x[2];
+                    const float iT2 = 1.0f / (T * T);
+                    for (int q = 0; q < 3; ++q) dw[q] += w[q] * (Ev - x[q]) * iT2;
+                }
+                for (int q = 0; q < 3; ++q) {
+                    if (st == 0 && !(x[q] > NINF)) continue;   /* only M checks its inputs */
+                    be[q * cstride + p] += bs * w[q];
+                    wt[q * cstride + p] += ws * w[q] + bs * dw[q];
+                }
+                if (st == 0) dp[SIDX(i, j)] += ws;
+            }
+        }
+    }
+}

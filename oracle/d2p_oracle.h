@@ -114,6 +114,10 @@ void oracle_nwa_hvp(const float* alpha, const float* scores, const float* score,
                     const float* V, float* d_alpha, float* d_score, float* beta,
                     float* d_beta, float* H, const int* lengths, int B, int maxL1, int maxL2,
                     float go, float ge, float T);
+void oracle_nwa_param_grad(const float* alpha, const float* scores, const float* score,
+                           const float* dS_dtheta, float* U, float* beta, float* W, float* dP,
+                           const int* lengths, int B, int maxL1, int maxL2, float go, float ge,
+                           float T, int ptype);
 
 #ifdef __cplusplus
 }

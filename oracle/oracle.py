@@ -83,6 +83,8 @@ _SIGS = {
                      [_F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f, _f]),
     "nwa_hvp": ("oracle_nwa_hvp", "nw_affine_hvp_cpu",
                 [_F, _F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f, _f]),
+    "nwa_param_grad": ("oracle_nwa_param_grad", "nw_affine_param_grad_cpu",
+                       [_F, _F, _F, _F, _F, _F, _F, _F, _I, _i, _i, _i, _f, _f, _f, _i]),
 }
 
 
@@ -421,6 +423,19 @@ class CpuKernels:
     def soft_nw_affine_hvp(self, scores, V, go=-2.0, ge=-0.5, T=1.0, lengths=None):
         alpha, score = self.nwa_forward(scores, lengths, go, ge, T)
         return self.nwa_hvp(alpha, scores, score, V, lengths, go, ge, T)[0]
+
+    def soft_nw_affine_param_jacobian(self, scores, ptype, go=-2.0, ge=-0.5, T=1.0,
+                                      lengths=None):
+        alpha, score = self.nwa_forward(scores, lengths, go, ge, T)
+        s = self._a(scores)
+        B, L1, L2 = s.shape
+        ln = _lengths(lengths, B, L1, L2)
+        dS = np.zeros((B,), self.ft)   # unused: the terminal betas carry their tangents
+        U, be, W = np.zeros_like(alpha), np.zeros_like(alpha), np.zeros_like(alpha)
+        dP = np.zeros_like(s)
+        self.fn["nwa_param_grad"](_p(alpha), _p(s), _p(score), _p(dS), _p(U), _p(be), _p(W),
+                                  _p(dP), _p(ln), B, L1, L2, go, ge, T, ptype)
+        return dP
 
     def soft_nw_affine(self, scores, go=-2.0, ge=-0.5, T=1.0, lengths=None):
         """value, marginals, grad_open, grad_ext, grad_T (nw_affine forward + backward)."""

@@ -458,3 +458,21 @@ def test_nw_affine_hvp_is_derivative_of_marginals(seed, L1, L2, T):
     m = k.soft_nw_affine(s, go, ge, T)[1]
     np.testing.assert_allclose((vp - vm) / (2 * eps), (m * V).sum(axis=(1, 2)), rtol=1e-6,
                                atol=1e-8)
+
+
+@pytest.mark.parametrize("seed,L1,L2,T", [(3, 6, 8, 1.0), (4, 10, 7, 0.7)])
+def test_nw_affine_jacobians_are_derivatives_of_marginals(seed, L1, L2, T):
+    """In double precision dP/d(open, ext, T) equal central differences of the
+    marginals, and the value's parameter gradients those of the value."""
+    k = O.get("oracle64")
+    rng = np.random.default_rng(seed)
+    s = rng.standard_normal((2, L1, L2))
+    p0, eps = np.array([-2.0, -0.5, T]), 1e-6
+    v, m, gO, gE, gT = k.soft_nw_affine(s, *p0)
+    for q, g in enumerate((gO, gE, gT)):
+        dp = np.zeros(3)
+        dp[q] = eps
+        hi, lo = k.soft_nw_affine(s, *(p0 + dp)), k.soft_nw_affine(s, *(p0 - dp))
+        J = k.soft_nw_affine_param_jacobian(s, q, *p0)
+        np.testing.assert_allclose(J, (hi[1] - lo[1]) / (2 * eps), rtol=1e-5, atol=1e-7)
+        np.testing.assert_allclose(g, (hi[0] - lo[0]) / (2 * eps), rtol=1e-6, atol=1e-8)

@@ -80,6 +80,9 @@ def test_nw_affine_bit_exact(seed, B, L1, L2, scale, gap, T, lens):
     V = _rand(seed + 81, (B, L1, L2))
     _same(o.soft_nw_affine_hvp(s, V, go, ge, T, lens), r.soft_nw_affine_hvp(s, V, go, ge, T, lens),
           "nw_affine hvp")
+    for p in (0, 1, 2):
+        _same(o.soft_nw_affine_param_jacobian(s, p, go, ge, T, lens),
+              r.soft_nw_affine_param_jacobian(s, p, go, ge, T, lens), f"nw_affine jacobian {p}")
 
 
 @pytest.mark.parametrize("seed,B,L1,L2,scale,gap,T,lens", SW_CASES)
