@@ -11,25 +11,22 @@ parameters) carry a Python autograd formula:
 * marginal path: ``*_backward_full`` (HVP against the marginal cotangent and its
   dot products with dP/dtheta).
 
+Parameters keep the form the caller gave them.  A tensor parameter (a learnable
+gap or temperature) is saved for backward like any other tensor and reaches the
+backward kernels through ``d2p_py::*_tp`` ops whose schema takes the parameters
+as ``Tensor[]``: their real implementation reads the values, so a compiled
+backward always runs with the parameters of its own forward.  (Reading a value
+while tracing would see a FakeTensor, which carries none.)
+
 ``d2p_amd._ops`` routes a call here while dynamo traces or when an argument is a
 FakeTensor; eager calls go straight to ``torch.ops.d2p``.
 """
 from __future__ import annotations
 
-from typing import Optional
+from typing import List, Optional, Sequence
 
 import torch
 from torch.library import custom_op
-
-from ._pt2_utils import _is_fake
-
-
-def _scalar(value, default: float = 0.0) -> float:
-    """A float from a Python number or a one-element tensor (fake tensors carry no
-    value: the default stands in; a positive one for temperatures)."""
-    if isinstance(value, torch.Tensor):
-        return default if _is_fake(value) else float(value.item())
-    return float(value)
 
 
 def _add(a: Optional[torch.Tensor], b: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
@@ -66,14 +63,79 @@ def _define(name: str, schema: str, fake):
     return op
 
 
+def _define_tp(name: str, head: str, tail: str, result: str, fake):
+    """``d2p_py::<name>_tp``: torch.ops.d2p.<name> with its float parameters passed as
+    one-element tensors.  ``head`` are the tensor arguments before the parameters,
+    ``tail`` the arguments after them."""
+    target = getattr(torch.ops.d2p, name)
+    n_head = head.count("Tensor")
+
+    def impl(*args):
+        lead, params, rest = args[:n_head], args[n_head], args[n_head + 1:]
+        values = [float(p.reshape(-1)[0].item()) for p in params]
+        out = target(*lead, *values, *rest)
+        return tuple(out) if isinstance(out, (list, tuple)) else out
+
+    schema = f"({head}, Tensor[] params, {tail}) -> {result}"
+    op = custom_op(f"d2p_py::{name}_tp", impl, mutates_args=(), schema=schema)
+    op.register_fake(fake)
+    return op
+
+
+# ------------------------------------------------------------------ saved parameters
+
+def _save(ctx, main: Sequence[torch.Tensor], params: Sequence, lengths) -> None:
+    """Saves the main tensors, the parameters (tensors through save_for_backward,
+    numbers as floats) and the lengths."""
+    tensors = list(main)
+    ctx.param_is_tensor = [isinstance(p, torch.Tensor) for p in params]
+    ctx.param_floats = [None if t else float(p) for p, t in zip(params, ctx.param_is_tensor)]
+    tensors += [p for p in params if isinstance(p, torch.Tensor)]
+    ctx.has_lengths = isinstance(lengths, torch.Tensor)
+    if ctx.has_lengths:
+        tensors.append(lengths)
+    ctx.n_main = len(main)
+    ctx.save_for_backward(*tensors)
+
+
+def _restore(ctx):
+    """(main tensors, parameters as saved, lengths or None)."""
+    saved = list(ctx.saved_tensors)
+    main, rest = saved[:ctx.n_main], saved[ctx.n_main:]
+    params = []
+    for is_t, f in zip(ctx.param_is_tensor, ctx.param_floats):
+        params.append(rest.pop(0) if is_t else f)
+    lengths = rest.pop(0) if ctx.has_lengths else None
+    return main, params, lengths
+
+
+def _param_tensors(params: List, like: torch.Tensor) -> List[torch.Tensor]:
+    return [p if isinstance(p, torch.Tensor) else like.new_tensor([p]) for p in params]
+
+
+def _call(float_op, tp_op, lead: Sequence[torch.Tensor], params: List, rest: Sequence):
+    """The float-parameter op when every parameter is a number, else the _tp op."""
+    if any(isinstance(p, torch.Tensor) for p in params):
+        return tp_op(*lead, _param_tensors(params, lead[0]), *rest)
+    return float_op(*lead, *params, *rest)
+
+
 # ------------------------------------------------------------------ linear-gap SW
 
 _SW_FLOAT = "float gap, float temperature, Tensor? lengths"
 
+
+def _sw_grads_fake(s, *_):
+    return (*_value_marginals_fake(s), s.new_empty([s.size(0)]), s.new_empty([s.size(0)]))
+
+
+def _sw_full_fake(s, ga, *_):
+    return s.new_empty(s.shape), s.new_empty([1]), s.new_empty([1])
+
+
 soft_sw_with_grads = _define(
     "soft_sw_with_grads", f"(Tensor scores, {_SW_FLOAT}) -> (Tensor, Tensor, Tensor, Tensor)",
-    lambda s, g, t, l: (*_value_marginals_fake(s), s.new_empty([s.size(0)]),
-                        s.new_empty([s.size(0)])))
+    _sw_grads_fake)
 soft_sw_hvp = _define(
     "soft_sw_hvp", f"(Tensor scores, Tensor tangent, {_SW_FLOAT}) -> Tensor",
     lambda s, v, g, t, l: s.new_empty(s.shape))
@@ -83,50 +145,70 @@ soft_sw_param_jacobian = _define(
 soft_sw_backward_full = _define(
     "soft_sw_backward_full",
     f"(Tensor scores, Tensor grad_alignment, {_SW_FLOAT}) -> (Tensor, Tensor, Tensor)",
-    lambda s, ga, g, t, l: (s.new_empty(s.shape), s.new_empty([1]), s.new_empty([1])))
+    _sw_full_fake)
 soft_sw = _define(
     "soft_sw", "(Tensor scores, Tensor gap, Tensor temperature, Tensor lengths) -> "
     "(Tensor, Tensor)", lambda s, g, t, l: _value_marginals_fake(s))
 soft_sw_float = _define(
     "soft_sw_float", f"(Tensor scores, {_SW_FLOAT}) -> (Tensor, Tensor)",
     lambda s, g, t, l: _value_marginals_fake(s))
+soft_sw_with_grads_tp = _define_tp(
+    "soft_sw_with_grads", "Tensor scores", "Tensor? lengths",
+    "(Tensor, Tensor, Tensor, Tensor)", _sw_grads_fake)
+soft_sw_backward_full_tp = _define_tp(
+    "soft_sw_backward_full", "Tensor scores, Tensor grad_alignment", "Tensor? lengths",
+    "(Tensor, Tensor, Tensor)", _sw_full_fake)
 
 
-def _sw_setup(ctx, inputs, output):
-    scores, gap, temperature, lengths = inputs
-    ctx.save_for_backward(scores, output[1])
-    ctx.params = (_scalar(gap), _scalar(temperature, 1.0))
-    ctx.lengths = lengths
+def _first_order_setup(ctx, inputs, output):
+    """Inputs (scores, *params, lengths) of a family's value op."""
+    scores, *params, lengths = inputs
+    _save(ctx, (scores, output[1]), params, lengths)
 
 
-def _sw_backward(ctx, grad_value, grad_marginals):
-    scores, marginals = ctx.saved_tensors
-    want = ctx.needs_input_grad[1:3]
-    grad_scores = _scale_rows(grad_value, marginals)
-    grads = [None, None]
-    if grad_value is not None and any(want):
-        per_batch = soft_sw_with_grads(scores, *ctx.params, ctx.lengths)[2:]
-        grads = [_dot_sum(grad_value, g) if w else None for g, w in zip(per_batch, want)]
-    if grad_marginals is not None:
-        gs, *gp = soft_sw_backward_full(scores, grad_marginals.contiguous(), *ctx.params,
-                                        ctx.lengths)
-        grad_scores = _add(grad_scores, gs)
-        grads = [_add(a, b) if w else None for a, b, w in zip(grads, gp, want)]
-    return grad_scores, *grads, None
+def _first_order_backward(with_grads, with_grads_tp, backward_full, backward_full_tp):
+    """Autograd formula of a family's value ops (value path and marginal path)."""
+
+    def backward(ctx, grad_value, grad_marginals):
+        (scores, marginals), params, lengths = _restore(ctx)
+        want = ctx.needs_input_grad[1:1 + len(params)]
+        grad_scores = _scale_rows(grad_value, marginals)
+        grads = [None] * len(params)
+        if grad_value is not None and any(want):
+            per_batch = _call(with_grads, with_grads_tp, (scores,), params, (lengths,))[2:]
+            grads = [_dot_sum(grad_value, g) if w else None for g, w in zip(per_batch, want)]
+        if grad_marginals is not None:
+            gs, *gp = _call(backward_full, backward_full_tp,
+                            (scores, grad_marginals.contiguous()), params, (lengths,))
+            grad_scores = _add(grad_scores, gs)
+            grads = [_add(a, b) if w else None for a, b, w in zip(grads, gp, want)]
+        return grad_scores, *grads, None
+
+    return backward
 
 
-soft_sw.register_autograd(_sw_backward, setup_context=_sw_setup)
-soft_sw_float.register_autograd(_sw_backward, setup_context=_sw_setup)
+_sw_backward = _first_order_backward(soft_sw_with_grads, soft_sw_with_grads_tp,
+                                     soft_sw_backward_full, soft_sw_backward_full_tp)
+soft_sw.register_autograd(_sw_backward, setup_context=_first_order_setup)
+soft_sw_float.register_autograd(_sw_backward, setup_context=_first_order_setup)
 
 # ------------------------------------------------------------------ affine-gap SW
 
 _SWA_FLOAT = "float gap_open, float gap_ext, float temperature, Tensor? lengths"
 
+
+def _swa_grads_fake(s, *_):
+    return (*_value_marginals_fake(s), *(s.new_empty([s.size(0)]) for _ in range(3)))
+
+
+def _swa_full_fake(s, ga, *_):
+    return (s.new_empty(s.shape), *(s.new_empty([1]) for _ in range(3)))
+
+
 soft_sw_affine_with_grads = _define(
     "soft_sw_affine_with_grads",
     f"(Tensor scores, {_SWA_FLOAT}) -> (Tensor, Tensor, Tensor, Tensor, Tensor)",
-    lambda s, o, e, t, l: (*_value_marginals_fake(s),
-                           *(s.new_empty([s.size(0)]) for _ in range(3))))
+    _swa_grads_fake)
 soft_sw_affine_hvp = _define(
     "soft_sw_affine_hvp", f"(Tensor scores, Tensor tangent, {_SWA_FLOAT}) -> Tensor",
     lambda s, v, o, e, t, l: s.new_empty(s.shape))
@@ -136,48 +218,42 @@ soft_sw_affine_param_jacobian = _define(
 soft_sw_affine_backward_full = _define(
     "soft_sw_affine_backward_full",
     f"(Tensor scores, Tensor grad_alignment, {_SWA_FLOAT}) -> (Tensor, Tensor, Tensor, Tensor)",
-    lambda s, ga, o, e, t, l: (s.new_empty(s.shape), *(s.new_empty([1]) for _ in range(3))))
+    _swa_full_fake)
 soft_sw_affine = _define(
     "soft_sw_affine", "(Tensor scores, Tensor gap_open, Tensor gap_ext, Tensor temperature, "
     "Tensor lengths) -> (Tensor, Tensor)", lambda s, o, e, t, l: _value_marginals_fake(s))
 soft_sw_affine_float = _define(
     "soft_sw_affine_float", f"(Tensor scores, {_SWA_FLOAT}) -> (Tensor, Tensor)",
     lambda s, o, e, t, l: _value_marginals_fake(s))
+soft_sw_affine_with_grads_tp = _define_tp(
+    "soft_sw_affine_with_grads", "Tensor scores", "Tensor? lengths",
+    "(Tensor, Tensor, Tensor, Tensor, Tensor)", _swa_grads_fake)
+soft_sw_affine_backward_full_tp = _define_tp(
+    "soft_sw_affine_backward_full", "Tensor scores, Tensor grad_alignment", "Tensor? lengths",
+    "(Tensor, Tensor, Tensor, Tensor)", _swa_full_fake)
 
-
-def _swa_setup(ctx, inputs, output):
-    scores, go, ge, temperature, lengths = inputs
-    ctx.save_for_backward(scores, output[1])
-    ctx.params = (_scalar(go), _scalar(ge), _scalar(temperature, 1.0))
-    ctx.lengths = lengths
-
-
-def _swa_backward(ctx, grad_value, grad_marginals):
-    scores, marginals = ctx.saved_tensors
-    want = ctx.needs_input_grad[1:4]
-    grad_scores = _scale_rows(grad_value, marginals)
-    grads = [None, None, None]
-    if grad_value is not None and any(want):
-        per_batch = soft_sw_affine_with_grads(scores, *ctx.params, ctx.lengths)[2:]
-        grads = [_dot_sum(grad_value, g) if w else None for g, w in zip(per_batch, want)]
-    if grad_marginals is not None:
-        gs, *gp = soft_sw_affine_backward_full(scores, grad_marginals.contiguous(), *ctx.params,
-                                               ctx.lengths)
-        grad_scores = _add(grad_scores, gs)
-        grads = [_add(a, b) if w else None for a, b, w in zip(grads, gp, want)]
-    return grad_scores, *grads, None
-
-
-soft_sw_affine.register_autograd(_swa_backward, setup_context=_swa_setup)
-soft_sw_affine_float.register_autograd(_swa_backward, setup_context=_swa_setup)
+_swa_backward = _first_order_backward(soft_sw_affine_with_grads, soft_sw_affine_with_grads_tp,
+                                      soft_sw_affine_backward_full,
+                                      soft_sw_affine_backward_full_tp)
+soft_sw_affine.register_autograd(_swa_backward, setup_context=_first_order_setup)
+soft_sw_affine_float.register_autograd(_swa_backward, setup_context=_first_order_setup)
 
 # ------------------------------------------------------------------ soft DTW
 
 _DTW_FLOAT = "float temperature, Tensor? lengths, int? bandwidth"
 
+
+def _dtw_grads_fake(c, *_):
+    return (*_value_marginals_fake(c), c.new_empty([c.size(0)]))
+
+
+def _dtw_full_fake(c, ga, *_):
+    return c.new_empty(c.shape), c.new_empty([1])
+
+
 soft_dtw_with_grads = _define(
     "soft_dtw_with_grads", f"(Tensor costs, {_DTW_FLOAT}) -> (Tensor, Tensor, Tensor)",
-    lambda c, t, l, bw: (*_value_marginals_fake(c), c.new_empty([c.size(0)])))
+    _dtw_grads_fake)
 soft_dtw_hvp = _define(
     "soft_dtw_hvp", f"(Tensor costs, Tensor tangent, {_DTW_FLOAT}) -> Tensor",
     lambda c, v, t, l, bw: c.new_empty(c.shape))
@@ -186,34 +262,39 @@ soft_dtw_param_jacobian = _define(
     lambda c, t, l, bw: c.new_empty(c.shape))
 soft_dtw_backward_full = _define(
     "soft_dtw_backward_full", f"(Tensor costs, Tensor grad_alignment, {_DTW_FLOAT}) -> "
-    "(Tensor, Tensor)", lambda c, ga, t, l, bw: (c.new_empty(c.shape), c.new_empty([1])))
+    "(Tensor, Tensor)", _dtw_full_fake)
 soft_dtw = _define(
     "soft_dtw", "(Tensor costs, Tensor temperature, Tensor lengths, int bandwidth) -> "
     "(Tensor, Tensor)", lambda c, t, l, bw: _value_marginals_fake(c))
 soft_dtw_float = _define(
     "soft_dtw_float", f"(Tensor costs, {_DTW_FLOAT}) -> (Tensor, Tensor)",
     lambda c, t, l, bw: _value_marginals_fake(c))
+soft_dtw_with_grads_tp = _define_tp(
+    "soft_dtw_with_grads", "Tensor costs", "Tensor? lengths, int? bandwidth",
+    "(Tensor, Tensor, Tensor)", _dtw_grads_fake)
+soft_dtw_backward_full_tp = _define_tp(
+    "soft_dtw_backward_full", "Tensor costs, Tensor grad_alignment",
+    "Tensor? lengths, int? bandwidth", "(Tensor, Tensor)", _dtw_full_fake)
 
 
 def _dtw_setup(ctx, inputs, output):
     costs, temperature, lengths, bandwidth = inputs
-    ctx.save_for_backward(costs, output[1])
-    ctx.temperature = _scalar(temperature, 1.0)
-    ctx.lengths = lengths
+    _save(ctx, (costs, output[1]), [temperature], lengths)
     ctx.bandwidth = bandwidth
 
 
 def _dtw_backward(ctx, grad_value, grad_marginals):
-    costs, marginals = ctx.saved_tensors
+    (costs, marginals), params, lengths = _restore(ctx)
     want_T = ctx.needs_input_grad[1]
+    rest = (lengths, ctx.bandwidth)
     grad_costs = _scale_rows(grad_value, marginals)
     grad_T = None
     if grad_value is not None and want_T:
-        per_batch = soft_dtw_with_grads(costs, ctx.temperature, ctx.lengths, ctx.bandwidth)[2]
+        per_batch = _call(soft_dtw_with_grads, soft_dtw_with_grads_tp, (costs,), params, rest)[2]
         grad_T = _dot_sum(grad_value, per_batch)
     if grad_marginals is not None:
-        gc, gt = soft_dtw_backward_full(costs, grad_marginals.contiguous(), ctx.temperature,
-                                        ctx.lengths, ctx.bandwidth)
+        gc, gt = _call(soft_dtw_backward_full, soft_dtw_backward_full_tp,
+                       (costs, grad_marginals.contiguous()), params, rest)
         grad_costs = _add(grad_costs, gc)
         if want_T:
             grad_T = _add(grad_T, gt)
@@ -227,8 +308,7 @@ soft_dtw_float.register_autograd(_dtw_backward, setup_context=_dtw_setup)
 
 soft_nw_with_grads = _define(
     "soft_nw_with_grads", f"(Tensor scores, {_SW_FLOAT}) -> (Tensor, Tensor, Tensor, Tensor)",
-    lambda s, g, t, l: (*_value_marginals_fake(s), s.new_empty([s.size(0)]),
-                        s.new_empty([s.size(0)])))
+    _sw_grads_fake)
 soft_nw_hvp = _define(
     "soft_nw_hvp", f"(Tensor scores, Tensor tangent, {_SW_FLOAT}) -> Tensor",
     lambda s, v, g, t, l: s.new_empty(s.shape))
@@ -238,30 +318,21 @@ soft_nw_param_jacobian = _define(
 soft_nw_backward_full = _define(
     "soft_nw_backward_full",
     f"(Tensor scores, Tensor grad_alignment, {_SW_FLOAT}) -> (Tensor, Tensor, Tensor)",
-    lambda s, ga, g, t, l: (s.new_empty(s.shape), s.new_empty([1]), s.new_empty([1])))
+    _sw_full_fake)
 soft_nw = _define(
     "soft_nw", "(Tensor scores, Tensor gap, Tensor temperature, Tensor lengths) -> "
     "(Tensor, Tensor)", lambda s, g, t, l: _value_marginals_fake(s))
 soft_nw_float = _define(
     "soft_nw_float", f"(Tensor scores, {_SW_FLOAT}) -> (Tensor, Tensor)",
     lambda s, g, t, l: _value_marginals_fake(s))
+soft_nw_with_grads_tp = _define_tp(
+    "soft_nw_with_grads", "Tensor scores", "Tensor? lengths",
+    "(Tensor, Tensor, Tensor, Tensor)", _sw_grads_fake)
+soft_nw_backward_full_tp = _define_tp(
+    "soft_nw_backward_full", "Tensor scores, Tensor grad_alignment", "Tensor? lengths",
+    "(Tensor, Tensor, Tensor)", _sw_full_fake)
 
-
-def _nw_backward(ctx, grad_value, grad_marginals):
-    scores, marginals = ctx.saved_tensors
-    want = ctx.needs_input_grad[1:3]
-    grad_scores = _scale_rows(grad_value, marginals)
-    grads = [None, None]
-    if grad_value is not None and any(want):
-        per_batch = soft_nw_with_grads(scores, *ctx.params, ctx.lengths)[2:]
-        grads = [_dot_sum(grad_value, g) if w else None for g, w in zip(per_batch, want)]
-    if grad_marginals is not None:
-        gs, *gp = soft_nw_backward_full(scores, grad_marginals.contiguous(), *ctx.params,
-                                        ctx.lengths)
-        grad_scores = _add(grad_scores, gs)
-        grads = [_add(a, b) if w else None for a, b, w in zip(grads, gp, want)]
-    return grad_scores, *grads, None
-
-
-soft_nw.register_autograd(_nw_backward, setup_context=_sw_setup)
-soft_nw_float.register_autograd(_nw_backward, setup_context=_sw_setup)
+_nw_backward = _first_order_backward(soft_nw_with_grads, soft_nw_with_grads_tp,
+                                     soft_nw_backward_full, soft_nw_backward_full_tp)
+soft_nw.register_autograd(_nw_backward, setup_context=_first_order_setup)
+soft_nw_float.register_autograd(_nw_backward, setup_context=_first_order_setup)

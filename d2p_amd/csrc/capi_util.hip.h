@@ -51,3 +51,10 @@ uint32_t next_epoch();
             return D2P_ERR_HIP;                                                  \
         }                                                                        \
     } while (0)
+
+// Returns from the enclosing entry point when a launch step fails.
+#define D2P_TRY(...)                    \
+    do {                                \
+        const int rc_ = (__VA_ARGS__);  \
+        if (rc_ != D2P_OK) return rc_;  \
+    } while (0)

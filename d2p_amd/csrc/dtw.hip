@@ -591,6 +591,7 @@ int launch_backward_p(const float* costs, const int* lengths, int B, int max_L1,
     const int ns = (max_L1 + 63) / 64;
     const size_t lds = lds_backward_r(R, P);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
+    if (sp.G > 1) D2P_TRY(launch_flag_reset(ws.bflag, B * sp.G, st));
     D2P_HIP(hipFuncSetAttribute((const void*)dtw_backward_kernel<P>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     D2P_LAUNCH("dtw_backward", dtw_backward_kernel<P>, dim3(split_grid(B, sp.G)), dim3(NW * 64),
@@ -608,8 +609,10 @@ int launch_backward_p(const float* costs, const int* lengths, int B, int max_L1,
 int check_shape(int B, int max_L1, int max_L2, float temperature) {
     D2P_REQUIRE(B >= 0 && max_L1 >= 0 && max_L2 >= 0, "negative dimension");
     D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
-    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 4, "max_L2 too large");
-    D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
+    D2P_REQUIRE(wf::table_fits_int32(max_L1, max_L2),
+                "DP table too large: (max_L1 + 1) * (max_L2 + 1) exceeds 2147483647");
+    D2P_REQUIRE(max_L2 <= wf::MAX_L2, "max_L2 exceeds 262080 (the stripe pipeline's limit)");
+    D2P_REQUIRE(max_L1 <= wf::MAX_L1, "max_L1 exceeds 2097088 (the stripe pipeline's limit)");
     // rings that do not fit for an unsplit element force parts of at most NW
     // stripes, whose minimum rings fit whatever the row length
     return D2P_OK;
@@ -678,9 +681,10 @@ extern "C" int d2p_dtw_forward_marginals(const float* costs, const int* lengths,
     hipStream_t st = (hipStream_t)stream;
     const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 1, true, 8,
                                      dtw::band_elem_steps(max_L1, max_L2, bandwidth));
-    const int r = dtw::launch_forward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth,
-                                      ws, value, st);
-    if (r != D2P_OK) return r;
-    return dtw::launch_backward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth, ws,
-                                marginals, grad_T, st);
+    D2P_TRY(dtw::launch_forward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth, ws,
+                                value, st));
+    D2P_TRY(dtw::launch_backward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth, ws,
+                                 marginals, grad_T, st));
+    return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr, value,
+                             grad_T, nullptr, nullptr, st);
 }

@@ -688,6 +688,7 @@ int launch_tangent(const float* input, const int* lengths, int B, int L1, int L2
     const size_t lds = lds_tangent_r(R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     auto kern = dtw_tangent_kernel<MODE, PT>;
+    if (sp.G > 1) D2P_TRY(launch_flag_reset(w.prim.fflag, B * sp.G, st));
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
     D2P_LAUNCH("dtw_tangent", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, input,
@@ -712,6 +713,7 @@ int launch_dual(const float* V, const int* lengths, int B, int L1, int L2, float
     auto k8 = dtw_dual_kernel<MODE, 8, DOT>;
     auto k4 = dtw_dual_kernel<MODE, 4, DOT>;
     auto kern = P == 16 ? k16 : (P == 8 ? k8 : k4);
+    if (sp.G > 1) D2P_TRY(launch_flag_reset(w.prim.bflag, B * sp.G, st));
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
     D2P_LAUNCH("dtw_dual", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, V, lengths,
@@ -731,12 +733,6 @@ int check(int B, int L1, int L2, float T) { return dtw::check_shape(B, L1, L2, T
 }  // namespace d2p_amd
 
 using namespace d2p_amd;
-
-#define D2P_TRY(...)                    \
-    do {                                \
-        const int rc_ = (__VA_ARGS__);  \
-        if (rc_ != D2P_OK) return rc_;  \
-    } while (0)
 
 extern "C" size_t d2p_dtw_second_workspace_bytes_banded(int B, int max_L1, int max_L2,
                                                          int bandwidth) {
@@ -764,8 +760,10 @@ extern "C" int d2p_dtw_hvp(const float* costs, const float* tangent, const int* 
                                 w.value, st));
     D2P_TRY(dtw2::launch_tangent<dtw2::HVP>(tangent, lengths, B, max_L1, max_L2, temperature,
                                             bandwidth, w, st));
-    return dtw2::launch_dual<dtw2::HVP, false>(nullptr, lengths, B, max_L1, max_L2, temperature,
-                                               bandwidth, w, hvp, nullptr, st);
+    D2P_TRY(dtw2::launch_dual<dtw2::HVP, false>(nullptr, lengths, B, max_L1, max_L2, temperature,
+                                                bandwidth, w, hvp, nullptr, st));
+    return wf::launch_poison(w.prim.status, B, (long long)max_L1 * max_L2, hvp, nullptr, nullptr,
+                             nullptr, nullptr, nullptr, st);
 }
 
 extern "C" int d2p_dtw_param_jacobian(const float* costs, const int* lengths, int B, int max_L1,
@@ -785,8 +783,10 @@ extern "C" int d2p_dtw_param_jacobian(const float* costs, const int* lengths, in
                                 w.value, st));
     D2P_TRY(dtw2::launch_tangent<dtw2::TEMP>(costs, lengths, B, max_L1, max_L2, temperature,
                                              bandwidth, w, st));
-    return dtw2::launch_dual<dtw2::TEMP, false>(nullptr, lengths, B, max_L1, max_L2, temperature,
-                                                bandwidth, w, jacobian, nullptr, st);
+    D2P_TRY(dtw2::launch_dual<dtw2::TEMP, false>(nullptr, lengths, B, max_L1, max_L2,
+                                                 temperature, bandwidth, w, jacobian, nullptr, st));
+    return wf::launch_poison(w.prim.status, B, (long long)max_L1 * max_L2, jacobian, nullptr,
+                             nullptr, nullptr, nullptr, nullptr, st);
 }
 
 extern "C" int d2p_dtw_backward_full(const float* costs, const float* grad_alignment,
@@ -812,6 +812,8 @@ extern "C" int d2p_dtw_backward_full(const float* costs, const float* grad_align
                                                 bandwidth, w, grad_costs, nullptr, st));
     D2P_TRY(dtw2::launch_tangent<dtw2::TEMP>(costs, lengths, B, max_L1, max_L2, temperature,
                                              bandwidth, w, st));
-    return dtw2::launch_dual<dtw2::TEMP, true>(grad_alignment, lengths, B, max_L1, max_L2,
-                                               temperature, bandwidth, w, nullptr, grad_T, st);
+    D2P_TRY(dtw2::launch_dual<dtw2::TEMP, true>(grad_alignment, lengths, B, max_L1, max_L2,
+                                                temperature, bandwidth, w, nullptr, grad_T, st));
+    return wf::launch_poison(w.prim.status, B, (long long)max_L1 * max_L2, grad_costs, nullptr,
+                             grad_T, nullptr, nullptr, nullptr, st);
 }

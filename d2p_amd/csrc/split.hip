@@ -3,6 +3,8 @@
 
 #include <stdlib.h>
 
+#include <vector>
+
 #include "wavefront.hip.h"
 #include "capi_util.hip.h"
 
@@ -20,6 +22,11 @@ __global__ void split_reset_kernel(int* __restrict__ status, uint64_t* __restric
         store_flag(fflag + i, 0);
         store_flag(bflag + i, 0);
     }
+}
+
+__global__ void flag_reset_kernel(uint64_t* __restrict__ flags, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) store_flag(flags + i, 0);
 }
 
 // partition[b] of a split element: the parts' (max, scaled sum) and the cell (0,0).
@@ -48,7 +55,44 @@ __global__ void sum_parts_kernel(const float* __restrict__ spart, float* __restr
     out[b] = t;
 }
 
+// NaN into every output of an element whose status word is set; one workgroup per
+// element (a clean element reads its word and returns).
+__global__ void __launch_bounds__(256)
+poison_kernel(const int* __restrict__ status, int B, long long n, float* __restrict__ m0,
+              float* __restrict__ m1, float* __restrict__ v0, float* __restrict__ v1,
+              float* __restrict__ v2, float* __restrict__ v3) {
+    const int b = blockIdx.x;
+    if (b >= B || __builtin_amdgcn_readfirstlane(status[b]) == 0) return;
+    const float nan = __builtin_nanf("");
+    if (threadIdx.x == 0) {
+        if (v0) v0[b] = nan;
+        if (v1) v1[b] = nan;
+        if (v2) v2[b] = nan;
+        if (v3) v3[b] = nan;
+    }
+    for (long long i = threadIdx.x; i < n; i += blockDim.x) {
+        if (m0) m0[(size_t)b * n + i] = nan;
+        if (m1) m1[(size_t)b * n + i] = nan;
+    }
+}
+
 }  // namespace
+
+std::vector<int (*)(int)>& spin_setters() {
+    static std::vector<int (*)(int)> setters;
+    return setters;
+}
+
+void register_spin_setter(int (*setter)(int)) { spin_setters().push_back(setter); }
+
+int launch_poison(const int* status, int B, long long per_elem, float* mat0, float* mat1,
+                  float* vec0, float* vec1, float* vec2, float* vec3, hipStream_t st) {
+    if (B <= 0) return D2P_OK;
+    D2P_LAUNCH("poison", poison_kernel, dim3(B), dim3(256), 0, st, status, B, per_elem, mat0,
+               mat1, vec0, vec1, vec2, vec3);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
 
 int launch_sum_parts(const float* spart, float* out, int B, int G, hipStream_t st) {
     D2P_LAUNCH("sum_parts", sum_parts_kernel, dim3((B + 255) / 256), dim3(256), 0, st, spart, out,
@@ -94,6 +138,13 @@ int launch_split_reset(const Layout& ws, int B, int G, hipStream_t st) {
     return D2P_OK;
 }
 
+int launch_flag_reset(uint64_t* flags, int n, hipStream_t st) {
+    if (n <= 0) return D2P_OK;
+    D2P_LAUNCH("flag_reset", flag_reset_kernel, dim3((n + 255) / 256), dim3(256), 0, st, flags, n);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
 int launch_partition_merge(const Layout& ws, float* partition, int B, int G, float T,
                            hipStream_t st) {
     D2P_LAUNCH("partition_merge", partition_merge_kernel, dim3((B + 255) / 256), dim3(256), 0,
@@ -104,3 +155,10 @@ int launch_partition_merge(const Layout& ws, float* partition, int B, int G, flo
 
 }  // namespace wf
 }  // namespace d2p_amd
+
+extern "C" int d2p_set_spin_limit(int spins) {
+    D2P_REQUIRE(spins >= 1, "spin limit must be positive");
+    for (auto setter : d2p_amd::wf::spin_setters())
+        D2P_REQUIRE(setter(spins) == 0, "hipMemcpyToSymbol of the spin limit failed");
+    return D2P_OK;
+}

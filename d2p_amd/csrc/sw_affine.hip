@@ -686,8 +686,10 @@ int max_stripes_backward(int max_L1, int max_L2) {
 int check_shape(int B, int max_L1, int max_L2, float temperature) {
     D2P_REQUIRE(B >= 0 && max_L1 >= 0 && max_L2 >= 0, "negative dimension");
     D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
-    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 4, "max_L2 too large");
-    D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
+    D2P_REQUIRE(wf::table_fits_int32(max_L1, max_L2),
+                "DP table too large: (max_L1 + 1) * (max_L2 + 1) exceeds 2147483647");
+    D2P_REQUIRE(max_L2 <= wf::MAX_L2, "max_L2 exceeds 262080 (the stripe pipeline's limit)");
+    D2P_REQUIRE(max_L1 <= wf::MAX_L1, "max_L1 exceeds 2097088 (the stripe pipeline's limit)");
     // rings that do not fit for an unsplit element force parts of at most NW
     // stripes, whose minimum rings fit whatever the row length
     return D2P_OK;
@@ -732,6 +734,7 @@ int launch_backward(const float* scores, const int* lengths, int B, int max_L1, 
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     float4* flows4 = reinterpret_cast<float4*>(ws.flows);
     float* flows1 = sp.G > 1 ? reinterpret_cast<float*>(flows4 + ws.flow_slots) : nullptr;
+    if (sp.G > 1) D2P_TRY(launch_flag_reset(ws.bflag, B * sp.G, st));
     D2P_HIP(hipFuncSetAttribute((const void*)swa_backward_kernel,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     D2P_LAUNCH("swa_backward", swa_backward_kernel, dim3(split_grid(B, sp.G)), dim3(NW * 64),
@@ -771,10 +774,11 @@ extern "C" int d2p_swa_forward_marginals(const float* scores, const int* lengths
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
     const wf::Layout ws = swa::affine_layout(workspace, B, max_L1, max_L2, true);
-    const int r = swa::launch_forward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
-                                      temperature, ws, partition, st);
-    if (r != D2P_OK) return r;
-    return swa::launch_backward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
-                                temperature, ws, partition, marginals, grad_open, grad_ext,
-                                grad_T, st);
+    D2P_TRY(swa::launch_forward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
+                                temperature, ws, partition, st));
+    D2P_TRY(swa::launch_backward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
+                                 temperature, ws, partition, marginals, grad_open, grad_ext,
+                                 grad_T, st));
+    return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr,
+                             partition, grad_open, grad_ext, grad_T, st);
 }

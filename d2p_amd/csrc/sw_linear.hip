@@ -638,9 +638,10 @@ int max_stripes_backward(int max_L1, int max_L2) {
 int check_shape(int B, int max_L1, int max_L2, float temperature) {
     D2P_REQUIRE(B >= 0 && max_L1 >= 0 && max_L2 >= 0, "negative dimension");
     D2P_REQUIRE(temperature > 0.0f, "temperature must be positive");
-    D2P_REQUIRE(max_L2 + 63 < (1 << 16) * 4, "max_L2 too large");
-    // per-lane byte offsets within one batch element are 32-bit
-    D2P_REQUIRE((size_t)max_L1 * max_L2 < ((size_t)1 << 30), "DP table too large");
+    D2P_REQUIRE(wf::table_fits_int32(max_L1, max_L2),
+                "DP table too large: (max_L1 + 1) * (max_L2 + 1) exceeds 2147483647");
+    D2P_REQUIRE(max_L2 <= wf::MAX_L2, "max_L2 exceeds 262080 (the stripe pipeline's limit)");
+    D2P_REQUIRE(max_L1 <= wf::MAX_L1, "max_L1 exceeds 2097088 (the stripe pipeline's limit)");
     // rings that do not fit for an unsplit element force parts of at most NW
     // stripes, whose minimum rings fit whatever the row length
     return D2P_OK;
@@ -687,6 +688,7 @@ int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1
     const size_t lds = lds_backward_r(R, P);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     const uint32_t epoch = next_epoch();
+    if (sp.G > 1) D2P_TRY(wf::launch_flag_reset(ws.bflag, B * sp.G, st));
     D2P_HIP(hipFuncSetAttribute((const void*)sw_backward_kernel<P, PRECISE, NWG>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     D2P_LAUNCH(NWG ? "nw_backward" : "sw_backward", (sw_backward_kernel<P, PRECISE, NWG>),
@@ -759,11 +761,12 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
     const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 1, true);
-    int r = sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
-                               partition, st);
-    if (r != D2P_OK) return r;
-    return sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
-                               partition, marginals, grad_gap, grad_T, st);
+    D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
+                               partition, st));
+    D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
+                                partition, marginals, grad_gap, grad_T, st));
+    return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr,
+                             partition, grad_gap, grad_T, nullptr, st);
 }
 
 extern "C" size_t d2p_nw_workspace_bytes(int B, int max_L1, int max_L2) {
@@ -784,9 +787,10 @@ extern "C" int d2p_nw_forward_marginals(const float* scores, const int* lengths,
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
     const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 1, true);
-    int r = sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws, value,
-                               st, true);
-    if (r != D2P_OK) return r;
-    return sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws, value,
-                               marginals, grad_gap, grad_T, st, false, true);
+    D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws, value,
+                               st, true));
+    D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws, value,
+                                marginals, grad_gap, grad_T, st, false, true));
+    return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr, value,
+                             grad_gap, grad_T, nullptr, st);
 }

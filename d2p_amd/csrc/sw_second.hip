@@ -736,6 +736,7 @@ int launch_tangent(const float* scores, const float* V, const int* lengths, int 
     const size_t lds = lds_tangent_r(MODE, R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     auto kern = sw_tangent_kernel<MODE, PT, NWG>;
+    if (sp.G > 1) D2P_TRY(launch_flag_reset(w.prim.fflag, B * sp.G, st));
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
     D2P_LAUNCH(NWG ? "nw_tangent" : "sw_tangent", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
@@ -764,6 +765,7 @@ int launch_dual(const float* scores, const float* V, const int* lengths, int B, 
     auto k8 = sw_dual_kernel<MODE, 8, DOT, NWG>;
     auto k4 = sw_dual_kernel<MODE, 4, DOT, NWG>;
     auto kern = P == 8 ? k8 : k4;
+    if (sp.G > 1) D2P_TRY(launch_flag_reset(w.prim.bflag, B * sp.G, st));
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
     D2P_LAUNCH(NWG ? "nw_dual" : "sw_dual", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
@@ -785,12 +787,6 @@ int check(int B, int L1, int L2, float T) {
 }  // namespace d2p_amd
 
 using namespace d2p_amd;
-
-#define D2P_TRY(...)                    \
-    do {                                \
-        const int rc_ = (__VA_ARGS__);  \
-        if (rc_ != D2P_OK) return rc_;  \
-    } while (0)
 
 extern "C" size_t d2p_sw_second_workspace_bytes(int B, int max_L1, int max_L2) {
     if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
@@ -817,8 +813,10 @@ int hvp_impl(const float* scores, const float* tangent, const int* lengths, int 
                                w.part, st, NWG));
     D2P_TRY(sw2::launch_tangent<sw2::HVP, NWG>(scores, tangent, lengths, B, max_L1, max_L2, gap,
                                                temperature, w, w.sdot, st));
-    return sw2::launch_dual<sw2::HVP, false, NWG>(scores, tangent, lengths, B, max_L1, max_L2,
-                                                  gap, temperature, w, w.sdot, hvp, nullptr, st);
+    D2P_TRY(sw2::launch_dual<sw2::HVP, false, NWG>(scores, tangent, lengths, B, max_L1, max_L2,
+                                                   gap, temperature, w, w.sdot, hvp, nullptr, st));
+    return wf::launch_poison(w.prim.status, B, (long long)max_L1 * max_L2, hvp, nullptr, nullptr,
+                             nullptr, nullptr, nullptr, st);
 }
 
 template <bool NWG>
@@ -843,15 +841,18 @@ int param_jacobian_impl(const float* scores, int param_type, const int* lengths,
     if (param_type == 0) {
         D2P_TRY(sw2::launch_tangent<sw2::GAP, NWG>(scores, nullptr, lengths, B, max_L1, max_L2,
                                                    gap, temperature, w, nullptr, st));
-        return sw2::launch_dual<sw2::GAP, false, NWG>(scores, nullptr, lengths, B, max_L1,
-                                                      max_L2, gap, temperature, w, w.dgap,
-                                                      jacobian, nullptr, st);
+        D2P_TRY(sw2::launch_dual<sw2::GAP, false, NWG>(scores, nullptr, lengths, B, max_L1,
+                                                       max_L2, gap, temperature, w, w.dgap,
+                                                       jacobian, nullptr, st));
+    } else {
+        D2P_TRY(sw2::launch_tangent<sw2::TEMP, NWG>(scores, nullptr, lengths, B, max_L1, max_L2,
+                                                    gap, temperature, w, nullptr, st));
+        D2P_TRY(sw2::launch_dual<sw2::TEMP, false, NWG>(scores, nullptr, lengths, B, max_L1,
+                                                        max_L2, gap, temperature, w, w.dT,
+                                                        jacobian, nullptr, st));
     }
-    D2P_TRY(sw2::launch_tangent<sw2::TEMP, NWG>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
-                                                temperature, w, nullptr, st));
-    return sw2::launch_dual<sw2::TEMP, false, NWG>(scores, nullptr, lengths, B, max_L1, max_L2,
-                                                   gap, temperature, w, w.dT, jacobian, nullptr,
-                                                   st);
+    return wf::launch_poison(w.prim.status, B, (long long)max_L1 * max_L2, jacobian, nullptr,
+                             nullptr, nullptr, nullptr, nullptr, st);
 }
 
 template <bool NWG>
@@ -887,8 +888,10 @@ int backward_full_impl(const float* scores, const float* grad_alignment, const i
                                                   temperature, w, w.dgap, nullptr, grad_gap, st));
     D2P_TRY(sw2::launch_tangent<sw2::TEMP, NWG>(scores, nullptr, lengths, B, max_L1, max_L2, gap,
                                                 temperature, w, nullptr, st));
-    return sw2::launch_dual<sw2::TEMP, true, NWG>(scores, ga, lengths, B, max_L1, max_L2, gap,
-                                                  temperature, w, w.dT, nullptr, grad_T, st);
+    D2P_TRY(sw2::launch_dual<sw2::TEMP, true, NWG>(scores, ga, lengths, B, max_L1, max_L2, gap,
+                                                   temperature, w, w.dT, nullptr, grad_T, st));
+    return wf::launch_poison(w.prim.status, B, (long long)max_L1 * max_L2, grad_scores, nullptr,
+                             grad_gap, grad_T, nullptr, nullptr, st);
 }
 
 }  // namespace

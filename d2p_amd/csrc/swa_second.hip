@@ -889,6 +889,7 @@ int launch_tangent(const float* scores, const float* V, const int* lengths, int 
     const size_t lds = lds_tangent_r(has_v, R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     auto kern = swa_tangent_kernel<MODE, PT>;
+    if (sp.G > 1) D2P_TRY(launch_flag_reset(w.prim.fflag, B * sp.G, st));
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
     D2P_LAUNCH("swa_tangent", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
@@ -913,6 +914,7 @@ int launch_dual(const float* scores, const float* V, const int* lengths, int B, 
     const size_t lds = lds_dual_r(has_v, DOT, R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     auto kern = swa_dual_kernel<MODE, PD, DOT>;
+    if (sp.G > 1) D2P_TRY(launch_flag_reset(w.prim.bflag, B * sp.G, st));
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
     D2P_LAUNCH("swa_dual", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
@@ -944,12 +946,6 @@ int check(int B, int L1, int L2, float T) { return swa::check_shape(B, L1, L2, T
 
 using namespace d2p_amd;
 
-#define D2P_TRY(...)                    \
-    do {                                \
-        const int rc_ = (__VA_ARGS__);  \
-        if (rc_ != D2P_OK) return rc_;  \
-    } while (0)
-
 extern "C" size_t d2p_swa_second_workspace_bytes(int B, int max_L1, int max_L2) {
     if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
     return swa2::second_layout(nullptr, B, max_L1, max_L2).bytes;
@@ -970,9 +966,11 @@ extern "C" int d2p_swa_hvp(const float* scores, const float* tangent, const int*
                                 temperature, w.prim, w.part, st));
     D2P_TRY(swa2::launch_tangent<swa2::HVP>(scores, tangent, lengths, B, max_L1, max_L2, gap_open,
                                             gap_ext, temperature, w, w.sdot, st));
-    return swa2::launch_dual<swa2::HVP, false>(scores, tangent, lengths, B, max_L1, max_L2,
-                                               gap_open, gap_ext, temperature, w, w.sdot, hvp,
-                                               nullptr, st);
+    D2P_TRY(swa2::launch_dual<swa2::HVP, false>(scores, tangent, lengths, B, max_L1, max_L2,
+                                                gap_open, gap_ext, temperature, w, w.sdot, hvp,
+                                                nullptr, st));
+    return wf::launch_poison(w.prim.status, B, (long long)max_L1 * max_L2, hvp, nullptr, nullptr,
+                             nullptr, nullptr, nullptr, st);
 }
 
 extern "C" int d2p_swa_param_jacobian(const float* scores, int param_type, const int* lengths,
@@ -995,18 +993,22 @@ extern "C" int d2p_swa_param_jacobian(const float* scores, int param_type, const
                                  st));
     switch (param_type) {
         case 0:
-            return swa2::param_pass<swa2::OPEN, false>(scores, nullptr, lengths, B, max_L1, max_L2,
-                                                       gap_open, gap_ext, temperature, w,
-                                                       jacobian, nullptr, st);
+            D2P_TRY(swa2::param_pass<swa2::OPEN, false>(scores, nullptr, lengths, B, max_L1,
+                                                        max_L2, gap_open, gap_ext, temperature, w,
+                                                        jacobian, nullptr, st));
+            break;
         case 1:
-            return swa2::param_pass<swa2::EXT, false>(scores, nullptr, lengths, B, max_L1, max_L2,
-                                                      gap_open, gap_ext, temperature, w, jacobian,
-                                                      nullptr, st);
+            D2P_TRY(swa2::param_pass<swa2::EXT, false>(scores, nullptr, lengths, B, max_L1, max_L2,
+                                                       gap_open, gap_ext, temperature, w, jacobian,
+                                                       nullptr, st));
+            break;
         default:
-            return swa2::param_pass<swa2::TEMP, false>(scores, nullptr, lengths, B, max_L1, max_L2,
-                                                       gap_open, gap_ext, temperature, w,
-                                                       jacobian, nullptr, st);
+            D2P_TRY(swa2::param_pass<swa2::TEMP, false>(scores, nullptr, lengths, B, max_L1,
+                                                        max_L2, gap_open, gap_ext, temperature, w,
+                                                        jacobian, nullptr, st));
     }
+    return wf::launch_poison(w.prim.status, B, (long long)max_L1 * max_L2, jacobian, nullptr,
+                             nullptr, nullptr, nullptr, nullptr, st);
 }
 
 extern "C" int d2p_swa_backward_full(const float* scores, const float* grad_alignment,
@@ -1039,6 +1041,8 @@ extern "C" int d2p_swa_backward_full(const float* scores, const float* grad_alig
                                                gap_ext, temperature, w, nullptr, grad_open, st));
     D2P_TRY(swa2::param_pass<swa2::EXT, true>(scores, ga, lengths, B, max_L1, max_L2, gap_open,
                                               gap_ext, temperature, w, nullptr, grad_ext, st));
-    return swa2::param_pass<swa2::TEMP, true>(scores, ga, lengths, B, max_L1, max_L2, gap_open,
-                                              gap_ext, temperature, w, nullptr, grad_T, st);
+    D2P_TRY(swa2::param_pass<swa2::TEMP, true>(scores, ga, lengths, B, max_L1, max_L2, gap_open,
+                                               gap_ext, temperature, w, nullptr, grad_T, st));
+    return wf::launch_poison(w.prim.status, B, (long long)max_L1 * max_L2, grad_scores, nullptr,
+                             grad_open, grad_ext, grad_T, nullptr, st);
 }

@@ -16,6 +16,8 @@
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
+#include <cstdlib>
+#include <cstring>
 #include <limits>
 #include <tuple>
 #include <vector>
@@ -97,6 +99,23 @@ Tensor resolve_lengths(const c10::optional<Tensor>& lengths_opt, const Dims& d,
     return lengths;
 }
 
+// D2P_AMD_CHECK_STATUS=1 (opt-in; it synchronises the stream after every call):
+// raise when a pipeline wait of some batch element gave up.  Without it such an
+// element's outputs come back NaN (the kernel library overwrites them), and nothing
+// waits for the device.
+bool status_check_enabled() {
+    const char* e = std::getenv("D2P_AMD_CHECK_STATUS");
+    return e != nullptr && e[0] != '\0' && std::strcmp(e, "0") != 0;
+}
+
+void check_status(const Tensor& ws, int B) {
+    if (B <= 0 || !status_check_enabled()) return;
+    int st = 0;
+    D2P_CALL(d2p_sw_status(ws.data_ptr(), B, &st, current_stream()));
+    TORCH_CHECK(st == 0, "d2p_amd: a pipeline wait of the DP sweeps gave up (status ", st,
+                "); the affected batch elements' outputs are NaN");
+}
+
 Tensor workspace(size_t bytes, const Tensor& like) {
     return torch::empty({(int64_t)std::max<size_t>(bytes, 1)},
                         like.options().dtype(torch::kUInt8));
@@ -142,6 +161,7 @@ SwOut sw_run(const Tensor& scores, const Tensor& lengths, const Dims& d, float g
         o.partition.data_ptr<float>(), o.marginals.data_ptr<float>(),
         o.grad_gap.data_ptr<float>(), o.grad_T.data_ptr<float>(), ws.data_ptr(), ws_bytes,
         current_stream()));
+    check_status(ws, d.B);
     return o;
 }
 
@@ -158,6 +178,7 @@ Tensor sw_hvp_run(const Tensor& scores, const Tensor& tangent, const Tensor& len
     D2P_CALL((global ? d2p_nw_hvp : d2p_sw_hvp)(
         scores.data_ptr<float>(), tangent.data_ptr<float>(), lengths.data_ptr<int>(), d.B, d.L1,
         d.L2, gap, T, out.data_ptr<float>(), ws.data_ptr(), ws.numel(), current_stream()));
+    check_status(ws, d.B);
     return out;
 }
 
@@ -168,6 +189,7 @@ Tensor sw_param_jacobian_run(const Tensor& scores, int param_type, const Tensor&
     D2P_CALL((global ? d2p_nw_param_jacobian : d2p_sw_param_jacobian)(
         scores.data_ptr<float>(), param_type, lengths.data_ptr<int>(), d.B, d.L1, d.L2, gap, T,
         out.data_ptr<float>(), ws.data_ptr(), ws.numel(), current_stream()));
+    check_status(ws, d.B);
     return out;
 }
 
@@ -183,6 +205,7 @@ std::tuple<Tensor, Tensor, Tensor> sw_backward_full_run(const Tensor& scores, co
                                   lengths.data_ptr<int>(), d.B, d.L1, d.L2, gap, T,
                                   gs.data_ptr<float>(), gg.data_ptr<float>(), gt.data_ptr<float>(),
                                   ws.data_ptr(), ws.numel(), current_stream()));
+    check_status(ws, d.B);
     return {gs, gg, gt};
 }
 
@@ -303,7 +326,8 @@ Tensor soft_sw_hvp(Tensor scores, Tensor tangent, double gap, double temperature
                    c10::optional<Tensor> lengths) {
     CHECK_INPUT_DEV(scores);
     CHECK_INPUT_DEV(tangent);
-    TORCH_CHECK(tangent.sizes() == scores.sizes(), "tangent must have same shape as scores");
+    TORCH_CHECK(scores.dim() == 3, "scores must be 3D");
+    TORCH_CHECK(scores.sizes() == tangent.sizes(), "scores and tangent must have same shape");
     TORCH_CHECK(tangent.device() == scores.device(), "tangent must be on same device as scores, got ",
                 tangent.device(), " vs ", scores.device());
     Dims d = checked_dims(scores, "SW");
@@ -379,6 +403,7 @@ SwOut nw_run(const Tensor& scores, const Tensor& lengths, const Dims& d, float g
         o.partition.data_ptr<float>(), o.marginals.data_ptr<float>(),
         o.grad_gap.data_ptr<float>(), o.grad_T.data_ptr<float>(), ws.data_ptr(), ws_bytes,
         current_stream()));
+    check_status(ws, d.B);
     return o;
 }
 
@@ -582,6 +607,7 @@ SwaOut swa_run(const Tensor& scores, const Tensor& lengths, const Dims& d, float
         o.partition.data_ptr<float>(), o.marginals.data_ptr<float>(),
         o.grad_open.data_ptr<float>(), o.grad_ext.data_ptr<float>(), o.grad_T.data_ptr<float>(),
         ws.data_ptr(), ws_bytes, current_stream()));
+    check_status(ws, d.B);
     return o;
 }
 
@@ -605,6 +631,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> swa_backward_full_run(const Tensor& s
                                    gs.data_ptr<float>(), g_o.data_ptr<float>(),
                                    g_e.data_ptr<float>(), g_t.data_ptr<float>(), ws.data_ptr(),
                                    ws.numel(), current_stream()));
+    check_status(ws, d.B);
     return {gs, g_o, g_e, g_t};
 }
 
@@ -739,6 +766,7 @@ Tensor swa_hvp(Tensor scores, Tensor tangent, double gap_open, double gap_ext, d
     D2P_CALL(d2p_swa_hvp(scores.data_ptr<float>(), tangent.data_ptr<float>(), l.data_ptr<int>(),
                          d.B, d.L1, d.L2, (float)gap_open, (float)gap_ext, (float)temperature,
                          out.data_ptr<float>(), ws.data_ptr(), ws.numel(), current_stream()));
+    check_status(ws, d.B);
     return out;
 }
 
@@ -757,6 +785,7 @@ Tensor swa_param_jacobian(Tensor scores, int64_t param_type, double gap_open, do
                                     d.B, d.L1, d.L2, (float)gap_open, (float)gap_ext,
                                     (float)temperature, out.data_ptr<float>(), ws.data_ptr(),
                                     ws.numel(), current_stream()));
+    check_status(ws, d.B);
     return out;
 }
 
@@ -836,6 +865,7 @@ DtwOut dtw_run(const Tensor& costs, const Tensor& lengths, const Dims& d, float 
         costs.data_ptr<float>(), lengths.data_ptr<int>(), d.B, d.L1, d.L2, T, bw,
         o.value.data_ptr<float>(), o.marginals.data_ptr<float>(), o.grad_T.data_ptr<float>(),
         ws.data_ptr(), ws_bytes, current_stream()));
+    check_status(ws, d.B);
     return o;
 }
 
@@ -854,6 +884,7 @@ std::tuple<Tensor, Tensor> dtw_backward_full_run(const Tensor& costs, const Tens
                                    lengths.data_ptr<int>(), d.B, d.L1, d.L2, T, bw,
                                    gc.data_ptr<float>(), gt.data_ptr<float>(), ws.data_ptr(),
                                    ws.numel(), current_stream()));
+    check_status(ws, d.B);
     return {gc, gt};
 }
 
@@ -946,6 +977,7 @@ Tensor dtw_hvp(Tensor costs, Tensor tangent, double temperature, c10::optional<T
     D2P_CALL(d2p_dtw_hvp(costs.data_ptr<float>(), tangent.data_ptr<float>(), l.data_ptr<int>(),
                          d.B, d.L1, d.L2, (float)temperature, bw, out.data_ptr<float>(),
                          ws.data_ptr(), ws.numel(), current_stream()));
+    check_status(ws, d.B);
     return out;
 }
 
@@ -961,6 +993,7 @@ Tensor dtw_param_jacobian(Tensor costs, double temperature, c10::optional<Tensor
     D2P_CALL(d2p_dtw_param_jacobian(costs.data_ptr<float>(), l.data_ptr<int>(), d.B, d.L1, d.L2,
                                     (float)temperature, bw, out.data_ptr<float>(), ws.data_ptr(),
                                     ws.numel(), current_stream()));
+    check_status(ws, d.B);
     return out;
 }
 

@@ -29,11 +29,23 @@ namespace d2p_amd {
 namespace wf {
 
 constexpr int NW = 8;                 // waves per workgroup
-constexpr int SPIN_LIMIT = 1 << 22;   // ~0.2 s of polling before giving up
+constexpr int SPIN_LIMIT = 1 << 22;   // default polls before a wait gives up (~0.2 s in LDS)
 constexpr int PROG_STRIDE = 1 << 16;  // progress word = stripe * PROG_STRIDE + chunks done
 constexpr int APAD = 18;              // table steps stored before step 0 (>= P + 2)
 constexpr int STEP_QUANTUM = 16;      // stored steps are a multiple of this (>= every P)
 constexpr size_t TRASH_BYTES = 256;   // one line that masked lanes store into
+
+// Shape limits of the pipeline beyond the reference's (L1 + 1) * (L2 + 1) <= INT32_MAX:
+// progress words count a stripe's chunks in 16 bits (P >= 4 steps per chunk, so
+// max_L2 + 63 < 2^18) and its stripe in the high half of an int (< 32768 stripes).
+// Per-lane matrix offsets are taken from the stripe's first row, so they span at
+// most 64 rows and set no limit of their own.
+constexpr int MAX_L2 = (1 << 18) - 64;
+constexpr int MAX_L1 = 32767 * 64;
+
+__host__ inline bool table_fits_int32(int max_L1, int max_L2) {
+    return ((long long)max_L1 + 1) * ((long long)max_L2 + 1) <= 2147483647LL;
+}
 
 // A stripe's chunk k reads boundary values the neighbouring stripe produces up to
 // 62 + P steps later in its own sweep, i.e. in its chunk k + 1 + 62/P; so it waits
@@ -144,12 +156,23 @@ Split choose_split(int B, int max_L1, const Layout& ws, int max_spw = 0);
 
 // Before a split forward sweep: status words and progress words to zero.
 int launch_split_reset(const Layout& ws, int B, int G, hipStream_t st);
+// Before every other split sweep: the n progress words it uses to zero (words the
+// forward did not reset may hold anything, e.g. when this sweep has more parts).
+int launch_flag_reset(uint64_t* flags, int n, hipStream_t st);
 // After it: partition[b] from the parts' (max, scaled sum) in ws.fpart and the cell
 // (0, 0), whose value is 0.
 int launch_partition_merge(const Layout& ws, float* partition, int B, int G, float T,
                            hipStream_t st);
 // out[b] = sum of the G parts' partial results spart[b][part].
 int launch_sum_parts(const float* spart, float* out, int B, int G, hipStream_t st);
+
+// The last launch of every entry point: each output of an element whose status word
+// is set (one of its pipeline waits gave up, so its results rest on data that had
+// not arrived) becomes NaN.  mats: up to two [B][per_elem] matrices, vecs: up to
+// four [B] vectors; null pointers are skipped.  An element that is clean costs one
+// load of its status word.
+int launch_poison(const int* status, int B, long long per_elem, float* mat0, float* mat1,
+                  float* vec0, float* vec1, float* vec2, float* vec3, hipStream_t st);
 
 // Issue priority of a wave by its stripe's place in the pipeline: every stripe
 // waits on the one before it, so the upstream stripes set the pace and are served
@@ -217,6 +240,22 @@ __device__ __forceinline__ void store_sys4(float4* p, float4 v) {
     __asm__ volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(p), "v"(w) : "memory");
 }
 
+// Polls a pipeline wait makes before it gives up (this translation unit's copy, per
+// device).  d2p_set_spin_limit lowers it from the host so that tests can drive every
+// wait down its give-up path; kernels read it only once a wait is not satisfied at
+// once, so the hot path never loads it.
+static __device__ int g_spin_limit = SPIN_LIMIT;
+
+// Host side: every translation unit that includes this header registers a setter for
+// its own copy of g_spin_limit (d2p_set_spin_limit calls them all).
+void register_spin_setter(int (*setter)(int));
+static int set_spin_limit_here(int spins) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_spin_limit), &spins, sizeof(int)) == hipSuccess ? 0 : -1;
+}
+static struct SpinSetterRegistration {
+    SpinSetterRegistration() { register_spin_setter(&set_spin_limit_here); }
+} g_spin_setter_registration;
+
 // A progress word: the launch's epoch in the high half, the chunks done in the low.
 __device__ __forceinline__ uint64_t progress_word(uint32_t epoch, int chunks) {
     return ((uint64_t)epoch << 32) | (uint32_t)chunks;
@@ -241,21 +280,25 @@ __device__ __forceinline__ int flag_chunks_lds(const float* slot, uint32_t epoch
 }
 
 // Waits until the part's progress word reports `need` chunks of this epoch; returns
-// the chunks seen.  Bounded by wall time (0.2 s of the 100 MHz counter); on timeout,
-// or when another wave of the element has already timed out, the element's status
-// gets bit 0 and the wait gives up.
+// the chunks seen.  Bounded by a count of polls (a quarter of the spin limit; each
+// poll is two device-coherent loads and a sleep, about 1 us), not by wall time, so a
+// workgroup that is descheduled while it waits does not run its bound down.  On
+// timeout, or when another wave of the element has already timed out, the element's
+// status gets bit 0 and the wait gives up.
 __device__ __forceinline__ int wait_part(const uint64_t* flag, uint32_t epoch, int need,
                                          int* status_b) {
-    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    while (true) {
-        const int got = flag_chunks(load_flag(flag), epoch);
-        if (got >= need) return got;
+    int got = flag_chunks(load_flag(flag), epoch);
+    if (got >= need) return got;
+    const int limit = max(__builtin_amdgcn_readfirstlane(g_spin_limit) >> 2, 1);
+    for (int polls = 1;; ++polls) {
         if (__builtin_amdgcn_readfirstlane(load_status(status_b)) != 0) return need;
-        if (__builtin_amdgcn_s_memrealtime() - t0 > 20000000ull) {
+        if (polls >= limit) {
             atomicOr(status_b, 1);
             return need;
         }
         __builtin_amdgcn_s_sleep(8);
+        got = flag_chunks(load_flag(flag), epoch);
+        if (got >= need) return got;
     }
 }
 
@@ -271,16 +314,25 @@ __device__ __forceinline__ void publish(int* prog, int wave, int value) {
     __hip_atomic_store(prog + wave, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Waits until prog[w] >= need; bounded.  The loaded value is made wave-uniform.
+__device__ __forceinline__ int prog_load(int* prog, int w) {
+    return __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(prog + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+}
+
+// Waits until prog[w] >= need; bounded by g_spin_limit polls, after which the
+// element's status gets bit 0 and the wave goes on.  The loaded value is made
+// wave-uniform.
 __device__ __forceinline__ void wait_for(int* prog, int w, int need, int* status_b) {
-    int spins = 0;
-    while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(
-               prog + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) < need) {
-        __builtin_amdgcn_s_sleep(2);
-        if (++spins >= SPIN_LIMIT) {
-            atomicOr(status_b, 1);
-            break;
-        }
+    if (prog_load(prog, w) < need) {
+        const int limit = __builtin_amdgcn_readfirstlane(g_spin_limit);
+        int spins = 0;
+        do {
+            __builtin_amdgcn_s_sleep(2);
+            if (++spins >= limit) {
+                atomicOr(status_b, 1);
+                break;
+            }
+        } while (prog_load(prog, w) < need);
     }
     wave_lds_sync();
 }
@@ -448,10 +500,18 @@ __device__ __forceinline__ bool chunk_inside(int i0, int L1max, int L2max, int t
     return lo >= 0 && hi < L2max && i0 + 63 < L1max;
 }
 
+// Offset (floats) of the lane's cell of instruction 0 from the stripe's first row.
+// The tile helpers address a matrix from the wave-uniform row pointer of the stripe
+// (stripe_row), so a lane offset spans at most 64 rows whatever the element's size.
 template <int P, int DIR>
-__device__ __forceinline__ int chunk_offset0(int i0, int L2max, int lane, int t_first) {
+__device__ __forceinline__ int chunk_offset0(int L2max, int lane, int t_first) {
     const int u = lane % P, pj = lane - u;
-    return (i0 + pj) * L2max + t_first + DIR * u - pj;
+    return pj * L2max + t_first + DIR * u - pj;
+}
+
+template <class T>
+__device__ __forceinline__ T* stripe_row(T* mbase, int i0, int L2max) {
+    return mbase + (size_t)i0 * L2max;
 }
 
 // Issues the P loads of one chunk of a row-major [L1max][L2max] matrix into a tile.
@@ -460,20 +520,21 @@ __device__ __forceinline__ int chunk_offset0(int i0, int L2max, int lane, int t_
 template <int P, int DIR>
 __device__ __forceinline__ void dma_tile(uint32_t tile_lds, const float* mbase, int i0, int L1max,
                                          int L2max, int lane, int t_first) {
+    const float* sbase = stripe_row(mbase, i0, L2max);
     if (chunk_inside<P, DIR>(i0, L1max, L2max, t_first)) {
-        uint32_t voff = (uint32_t)chunk_offset0<P, DIR>(i0, L2max, lane, t_first) * 4u;
+        uint32_t voff = (uint32_t)chunk_offset0<P, DIR>(L2max, lane, t_first) * 4u;
         const uint32_t vstep = (uint32_t)(L2max - 1) * 4u;
 #pragma unroll
-        for (int i = 0; i < P; ++i) lds_dma_dword<260>(mbase, voff, tile_lds, vstep);
+        for (int i = 0; i < P; ++i) lds_dma_dword<260>(sbase, voff, tile_lds, vstep);
     } else {
         const int u = lane % P, pj = lane - u;
         // row/column of instruction 0; instruction i moves one row down, one column left
         int row = i0 + pj, col = t_first + DIR * u - pj;
 #pragma unroll
         for (int i = 0; i < P; ++i) {
-            uint32_t voff = (uint32_t)(min(row, L1max - 1) * L2max +
+            uint32_t voff = (uint32_t)((min(row, L1max - 1) - i0) * L2max +
                                        min(max(col, 0), L2max - 1)) * 4u;
-            lds_dma_dword<260>(mbase, voff, tile_lds, 0u);
+            lds_dma_dword<260>(sbase, voff, tile_lds, 0u);
             ++row;
             --col;
         }
@@ -490,7 +551,8 @@ __device__ __forceinline__ void write_tile(const float* tile, float* obase, floa
                                            int L1, int L2, int L1max, int L2max, int lane,
                                            int t_first) {
     if (chunk_inside<P, DIR>(i0, L1max, L2max, t_first)) {
-        uint32_t off4 = (uint32_t)chunk_offset0<P, DIR>(i0, L2max, lane, t_first) * 4u;
+        float* sbase = stripe_row(obase, i0, L2max);
+        uint32_t off4 = (uint32_t)chunk_offset0<P, DIR>(L2max, lane, t_first) * 4u;
         const uint32_t step4 = (uint32_t)(L2max - 1) * 4u;
         // all LDS reads first (one wait), then the stores: the empty asm that keeps
         // one running offset would otherwise order each read behind the last store
@@ -499,7 +561,7 @@ __device__ __forceinline__ void write_tile(const float* tile, float* obase, floa
         for (int i = 0; i < P; ++i) v[i] = tile[65 * i + lane];
 #pragma unroll
         for (int i = 0; i < P; ++i) {
-            lane_store(obase, off4, v[i]);
+            lane_store(sbase, off4, v[i]);
             off4 += step4;
             __asm__ volatile("" : "+v"(off4));   // keep one running offset
         }
@@ -553,16 +615,16 @@ __device__ __forceinline__ void quad_cell(int f, int t_first, int& r, int& col) 
     col = t_first + DIR * Q::template step<DIR>(q, s & 3) - r;
 }
 
-// Byte offset in the matrix of the 16 bytes an inside chunk's instruction 0 moves
-// for this lane (the lowest column of the lane's quad); instruction i adds
-// i * ROWS_X4 * (L2max - 1) floats.
+// Byte offset from the stripe's first row (stripe_row) of the 16 bytes an inside
+// chunk's instruction 0 moves for this lane (the lowest column of the lane's quad);
+// instruction i adds i * ROWS_X4 * (L2max - 1) floats.
 template <int P, int DIR>
-__device__ __forceinline__ uint32_t quad_offset0(int i0, int L2max, int lane, int t_first) {
+__device__ __forceinline__ uint32_t quad_offset0(int L2max, int lane, int t_first) {
     using Q = QuadTile<P>;
     const int r = lane / Q::NQ;
     const int q = (lane % Q::NQ) ^ Q::swz(r);
     const int c_lo = DIR > 0 ? t_first + 4 * q - r : t_first - 4 * q - 3 - r;
-    return (uint32_t)((i0 + r) * L2max + c_lo) * 4u;
+    return (uint32_t)(r * L2max + c_lo) * 4u;
 }
 
 // Issues the loads of one chunk of a row-major [L1max][L2max] matrix into a quad tile.
@@ -570,19 +632,20 @@ template <int P, int DIR>
 __device__ __forceinline__ void dma_quads(uint32_t tile_lds, const float* mbase, int i0,
                                           int L1max, int L2max, int lane, int t_first) {
     using Q = QuadTile<P>;
+    const float* sbase = stripe_row(mbase, i0, L2max);
     if (chunk_inside<P, DIR>(i0, L1max, L2max, t_first)) {
-        uint32_t voff = quad_offset0<P, DIR>(i0, L2max, lane, t_first);
+        uint32_t voff = quad_offset0<P, DIR>(L2max, lane, t_first);
         const uint32_t vstep = (uint32_t)(Q::ROWS_X4 * (L2max - 1)) * 4u;
 #pragma unroll
-        for (int i = 0; i < Q::NQ; ++i) lds_dma_dwordx4<1024>(mbase, voff, tile_lds, vstep);
+        for (int i = 0; i < Q::NQ; ++i) lds_dma_dwordx4<1024>(sbase, voff, tile_lds, vstep);
     } else {
 #pragma unroll
         for (int j = 0; j < P; ++j) {
             int r, col;
             quad_cell<P, DIR>(64 * j + lane, t_first, r, col);
-            uint32_t voff = (uint32_t)(min(i0 + r, L1max - 1) * L2max +
+            uint32_t voff = (uint32_t)((min(i0 + r, L1max - 1) - i0) * L2max +
                                        min(max(col, 0), L2max - 1)) * 4u;
-            lds_dma_dword<256>(mbase, voff, tile_lds, 0u);
+            lds_dma_dword<256>(sbase, voff, tile_lds, 0u);
         }
     }
 }
@@ -622,7 +685,8 @@ __device__ __forceinline__ void write_quads(const float* tile, float* obase, flo
                                             int t_first) {
     using Q = QuadTile<P>;
     if (chunk_inside<P, DIR>(i0, L1max, L2max, t_first)) {
-        uint32_t off = quad_offset0<P, DIR>(i0, L2max, lane, t_first);
+        char* sbase = reinterpret_cast<char*>(stripe_row(obase, i0, L2max));
+        uint32_t off = quad_offset0<P, DIR>(L2max, lane, t_first);
         const uint32_t step = (uint32_t)(Q::ROWS_X4 * (L2max - 1)) * 4u;
         float4 v[Q::NQ];
 #pragma unroll
@@ -630,7 +694,7 @@ __device__ __forceinline__ void write_quads(const float* tile, float* obase, flo
             v[i] = *reinterpret_cast<const float4*>(tile + 256 * i + 4 * lane);
 #pragma unroll
         for (int i = 0; i < Q::NQ; ++i) {
-            *reinterpret_cast<float4*>(reinterpret_cast<char*>(obase) + off) = v[i];
+            *reinterpret_cast<float4*>(sbase + off) = v[i];
             off += step;
             __asm__ volatile("" : "+v"(off));   // keep one running offset
         }

@@ -47,11 +47,21 @@ void d2p_profile_reset(void);
 /* Workspace bytes needed by d2p_sw_forward_marginals for the given padded shape. */
 size_t d2p_sw_workspace_bytes(int B, int max_L1, int max_L2);
 
-/* Status of the last d2p_sw_forward_marginals call that used `workspace`: ORs the
- * per-element status words into *status (0 = clean; bit 0 = a pipeline wait hit its
- * spin bound, i.e. the results are not to be trusted).  Synchronises `stream`.  No
- * counterpart in the reference (its kernels do not wait on each other). */
+/* Status of the last call of any entry point below that used `workspace` (every
+ * workspace starts with the [B] per-element status words): ORs them into *status
+ * (0 = clean; bit 0 = a pipeline wait of some element reached its bound and gave up).
+ * The outputs of such an element are NaN: every entry point ends with a pass that
+ * overwrites them, so a timed-out element can never pass for a result.  Synchronises
+ * `stream`.  No counterpart in the reference (its kernels do not wait on each other). */
 int d2p_sw_status(const void* workspace, int B, int* status, void* stream);
+
+/* Bound of every pipeline wait of this library's kernels on the current device, in
+ * polls (default 4194304, about 0.2 s of polling inside a workgroup; the waits
+ * between workgroups of a split element poll a quarter as often, each poll about
+ * 1 us).  A wait that reaches it gives up as described under d2p_sw_status, and the
+ * kernel still runs to its end.  A test hook with no counterpart in the reference:
+ * a small bound drives the timeout path without any kernel hanging. */
+int d2p_set_spin_limit(int spins);
 
 /* Forward value and marginals in one call.
  * Replaces the pair sw_regular_forward[_warp] + sw_regular_backward[_warp]

@@ -119,7 +119,7 @@ def test_forward_validation(lib):
     assert rc == D2P_ERR_ARG and "workspace" in _err(lib)
     rc = lib.d2p_sw_forward_marginals(FAKE, FAKE, 2, 10, 1 << 20, -1.0, 1.0, FAKE, FAKE, FAKE,
                                       FAKE, FAKE, z, None)
-    assert rc == D2P_ERR_ARG and "too large" in _err(lib)
+    assert rc == D2P_ERR_ARG and "max_L2 exceeds" in _err(lib)
 
 
 def test_empty_batch_is_a_no_op(lib):
@@ -160,3 +160,17 @@ def test_profile_report_buffer(lib):
     lib.d2p_profile_reset()
     buf = ctypes.create_string_buffer(256)
     assert lib.d2p_profile_report(buf, 256) == D2P_OK
+
+
+def test_c_abi_accepts_the_reference_table_range(lib):
+    """The C ABI sizes a workspace for any table the reference accepts, up to
+    (L1 + 1) * (L2 + 1) = INT32_MAX (here [1, 40000, 40000], 1.6e9 cells), and
+    rejects the next shape up; no kernel runs."""
+    assert lib.d2p_sw_workspace_bytes(1, 40000, 40000) > 40000 * 40000 * 4
+    rc = lib.d2p_sw_forward_marginals(FAKE, FAKE, 1, 46341, 46341, -1.0, 1.0, FAKE, FAKE, FAKE,
+                                      FAKE, FAKE, 1 << 40, None)
+    assert rc == D2P_ERR_ARG and b"DP table too large" in lib.d2p_last_error()
+    # rows longer than the pipeline's chunk counters allow: its own message
+    rc = lib.d2p_swa_forward_marginals(FAKE, FAKE, 1, 2, 262081, -2.0, -0.5, 1.0, FAKE, FAKE,
+                                       FAKE, FAKE, FAKE, FAKE, 1 << 40, None)
+    assert rc == D2P_ERR_ARG and b"max_L2 exceeds 262080" in lib.d2p_last_error()

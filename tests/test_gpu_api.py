@@ -107,3 +107,41 @@ def test_torch_compile_nw(cuda):
     lc.backward()
     assert torch.allclose(lc, le, rtol=1e-6, atol=1e-5)
     assert torch.allclose(xc.grad, xe.grad, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("family", ["sw", "nw", "swa", "dtw"])
+def test_torch_compile_learnable_parameters(cuda, family):
+    """Modules with learnable parameters under torch.compile: the compiled backward
+    runs the kernels with the forward's own gap/temperature values (tensors saved for
+    backward, not placeholders), on the value path and on the marginal path."""
+    torch.manual_seed(0)
+    s = _seeded(10, (2, 40, 48)).to(cuda)
+    w = _seeded(11, (2, 40, 48)).to(cuda)
+    if family == "dtw":
+        s = s.abs()
+    make = {"sw": lambda: d2p_amd.SoftSW(gap=-0.7, temperature=0.6, learn_gap=True,
+                                         learn_temperature=True),
+            "nw": lambda: d2p_amd.SoftNW(gap=-0.7, temperature=0.6, learnable=True),
+            "swa": lambda: d2p_amd.SoftSWAffine(gap_open=-1.5, gap_ext=-0.4, temperature=0.6,
+                                                learn_gap_open=True, learn_gap_ext=True,
+                                                learn_temperature=True),
+            "dtw": lambda: d2p_amd.SoftDTW(temperature=0.6, learnable=True)}[family]
+
+    def run(mod, x):
+        r = mod(x)
+        return r[0].sum() + (r[1] * w).sum()
+
+    results = []
+    for compiled in (False, True):
+        mod = make().to(cuda)
+        x = s.clone().requires_grad_(True)
+        fn = torch.compile(run, backend="aot_eager") if compiled else run
+        loss = fn(mod, x)
+        loss.backward()
+        results.append((loss.detach(), x.grad, [p.grad.clone() for p in mod.parameters()]))
+    (le, ge, pe), (lc, gc, pc) = results
+    assert len(pe) == len(pc) > 0
+    assert torch.allclose(lc, le, rtol=1e-6, atol=1e-5)
+    assert torch.allclose(gc, ge, rtol=1e-5, atol=1e-5)
+    for a, b in zip(pc, pe):
+        assert torch.allclose(a, b, rtol=1e-5, atol=1e-4), (a, b)

@@ -113,6 +113,61 @@ def test_pt2_value_ops_trace_with_autograd():
             assert gx.shape == x.shape
 
 
+def test_pt2_parameter_gradients_trace_with_tensor_parameters():
+    """Tensor gap/temperature reach the backward as saved tensors (the _tp ops), so
+    their gradients trace under fake tensors on both paths."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from d2p_amd import _pt2_ops as P
+    with FakeTensorMode():
+        x = torch.empty(2, 5, 7, requires_grad=True)
+        lens = torch.empty(2, 2, dtype=torch.int32)
+        gap = torch.empty(1, requires_grad=True)
+        temp = torch.empty(1, requires_grad=True)
+        for out, params in ((P.soft_sw(x, gap, temp, lens), (gap, temp)),
+                            (P.soft_nw(x, gap, temp, lens), (gap, temp)),
+                            (P.soft_sw_affine(x, gap, gap, temp, lens), (gap, temp)),
+                            (P.soft_dtw(x, temp, lens, -1), (temp,))):
+            value, marg = out
+            grads = torch.autograd.grad(value.sum() + marg.sum(), (x, *params))
+            assert grads[0].shape == x.shape
+            assert all(g.shape == (1,) for g in grads[1:])
+
+
+def test_pt2_saved_parameters_round_trip():
+    """Numbers stay numbers and tensors come back as the saved tensors."""
+    from d2p_amd import _pt2_ops as P
+
+    class Ctx:
+        def save_for_backward(self, *t):
+            self.saved_tensors = t
+
+    ctx = Ctx()
+    s, m, g, lens = torch.zeros(1, 2, 2), torch.ones(1, 2, 2), torch.tensor([-3.0]), \
+        torch.zeros(1, 2, dtype=torch.int32)
+    P._save(ctx, (s, m), [g, 0.25], lens)
+    (s2, m2), params, l2 = P._restore(ctx)
+    assert s2 is s and m2 is m and params[0] is g and params[1] == 0.25 and l2 is lens
+    ctx = Ctx()
+    P._save(ctx, (s, m), [-1.0, 2.0], None)
+    assert P._restore(ctx)[1:] == ([-1.0, 2.0], None)
+
+
+def test_use_pt2_ops_predicate():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from d2p_amd._pt2_utils import use_pt2_ops
+    real = torch.zeros(2)
+    assert not use_pt2_ops(real, 1.0, None)
+    with FakeTensorMode():
+        fake = torch.zeros(2)
+    assert use_pt2_ops(real, fake)
+
+    def f(x):
+        return x + (1.0 if use_pt2_ops() else 0.0)
+
+    assert torch.compile(f, backend="eager", fullgraph=True)(real).tolist() == [1.0, 1.0]
+    assert f(real).tolist() == [0.0, 0.0]
+
+
 def test_meta_tensors_route_to_fakes():
     x = torch.empty(3, 4, 6, device="meta")
     v, m = torch.ops.d2p.soft_sw_float(x, -1.0, 1.0, None)
