@@ -19,6 +19,7 @@
 
 #include <atomic>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
 #include <vector>
 
@@ -761,6 +762,70 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
     const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 1, true);
+    D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
+                               partition, st));
+    D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
+                                partition, marginals, grad_gap, grad_T, st));
+    return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr,
+                             partition, grad_gap, grad_T, nullptr, st);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant of d2p_sw_forward_marginals: the workspace is a static
+// device array of this file, one copy per GPU (held from the library's first use
+// on that device to the end of the process).
+// ---------------------------------------------------------------------------
+namespace {
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the current device, resolved once per device (the
+// array's name is only a host-side handle: never pass it to a kernel).
+int scratch_on_current_device(void** out) {
+    int dev = -1;
+    D2P_HIP(hipGetDevice(&dev));
+    D2P_REQUIRE(dev >= 0 && dev < kMaxDevices, "device ordinal out of range");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        D2P_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        D2P_REQUIRE(p != nullptr, "hipGetSymbolAddress returned a null scratch address");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return D2P_OK;
+}
+}  // namespace
+
+extern "C" size_t d2p_sw_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+extern "C" int d2p_sw_forward_marginals_noalloc(const float* scores, const int* lengths, int B,
+                                                int max_L1, int max_L2, float gap,
+                                                float temperature, float* partition,
+                                                float* marginals, float* grad_gap,
+                                                float* grad_T, void* stream) {
+    const int rc = sw::check_shape(B, max_L1, max_L2, temperature);
+    if (rc != D2P_OK) return rc;
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(scores && lengths && partition && marginals && grad_gap && grad_T,
+                "null pointer argument");
+    const size_t need = d2p_sw_workspace_bytes(B, max_L1, max_L2);
+    if (need > kScratchBytes) {
+        set_last_error("shape needs %zu workspace bytes, more than the %zu-byte static scratch "
+                       "of d2p_sw_forward_marginals_noalloc (use d2p_sw_forward_marginals)",
+                       need, kScratchBytes);
+        return D2P_ERR_ARG;
+    }
+    void* ws_ptr = nullptr;
+    D2P_TRY(scratch_on_current_device(&ws_ptr));
+    // the sweeps reset every word of the workspace they rely on (status and progress
+    // words) themselves, with kernels: the previous call's contents do not matter
+    hipStream_t st = (hipStream_t)stream;
+    const wf::Layout ws = wf::layout(ws_ptr, B, max_L1, max_L2, 1, true);
     D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
                                partition, st));
     D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,

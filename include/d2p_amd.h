@@ -77,6 +77,22 @@ int d2p_sw_forward_marginals(const float* scores, const int* lengths, int B, int
                              float* marginals, float* grad_gap, float* grad_T,
                              void* workspace, size_t workspace_bytes, void* stream);
 
+/* d2p_sw_forward_marginals with no workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  Its scratch
+ * memory is a static device array of d2p_sw_noalloc_scratch_bytes() = 64 MiB that
+ * each GPU the library runs on holds until the process ends; the call allocates
+ * nothing (with the opt-in launch profile off).  Shapes whose
+ * d2p_sw_workspace_bytes(B, max_L1, max_L2) exceeds the array are rejected with an
+ * error.  Every call on one GPU shares that GPU's array: calls that overlap in time
+ * on one GPU (other streams, other host threads) race and must be serialised by
+ * the caller.  Same outputs as d2p_sw_forward_marginals. */
+int d2p_sw_forward_marginals_noalloc(const float* scores, const int* lengths, int B,
+                                     int max_L1, int max_L2, float gap, float temperature,
+                                     float* partition, float* marginals, float* grad_gap,
+                                     float* grad_T, void* stream);
+size_t d2p_sw_noalloc_scratch_bytes(void);
+
 /* Workspace bytes of the second-order linear-gap entry points below (d2p_sw_hvp,
  * d2p_sw_param_jacobian, d2p_sw_backward_full). */
 size_t d2p_sw_second_workspace_bytes(int B, int max_L1, int max_L2);

@@ -22,6 +22,8 @@ SIGNATURES = {
     "d2p_sw_workspace_bytes": (_z, [_i, _i, _i]),
     "d2p_sw_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _f, _p, _p, _p, _p, _p, _z, _p]),
     "d2p_sw_status": (_i, [_p, _i, ctypes.POINTER(_i), _p]),
+    "d2p_sw_forward_marginals_noalloc": (_i, [_p, _p, _i, _i, _i, _f, _f, _p, _p, _p, _p, _p]),
+    "d2p_sw_noalloc_scratch_bytes": (_z, []),
     "d2p_set_spin_limit": (_i, [_i]),
     "d2p_swa_workspace_bytes": (_z, [_i, _i, _i]),
     "d2p_swa_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _f, _f, _p, _p, _p, _p, _p, _p,
