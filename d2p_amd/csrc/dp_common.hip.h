@@ -111,6 +111,18 @@ struct OnlineLSE {
         z = z * fast_exp2((m - M) * c) + tree_sum<N>(e);
         m = M;
     }
+    // add_block with the block's max already known: bmax, the max of the values
+    // (and of -1e20, so that cells at the -1e30 sentinel add exact zeros), tracked by
+    // the caller as the values were made.
+    template <int N>
+    __device__ __forceinline__ void add_block_max(const float* x, float bmax, float c) {
+        const float M = fmaxf(m, bmax);
+        float e[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) e[i] = fast_exp2((x[i] - M) * c);
+        z = fmaf(z, fast_exp2((m - M) * c), tree_sum<N>(e));
+        m = M;
+    }
     __device__ __forceinline__ void merge(float m2, float z2, float c) {
         float M = fmaxf(m, m2);
         float za = (m <= kNINF) ? 0.0f : z * fast_exp2((m - M) * c);

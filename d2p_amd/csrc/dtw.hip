@@ -71,8 +71,8 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
     }
     __syncthreads();
 
-    const int L1 = min(max(lengths[2 * b], 0), L1max);
-    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
+    const int L2 = lengths ? min(max(lengths[2 * b + 1], 0), L2max) : L2max;
     const float c = kLog2e / T;
     const float tl = T * kLn2;
     // a band test with an empty side is always true (reference: L1 == 0 || L2 == 0)
@@ -293,8 +293,8 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
 
-    const int L1 = min(max(lengths[2 * b], 0), L1max);
-    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
+    const int L2 = lengths ? min(max(lengths[2 * b + 1], 0), L2max) : L2max;
     const float c = kLog2e / T;
     const float bw = (bandwidth < 0 || L1 == 0 || L2 == 0) ? -1.0f : (float)bandwidth;
     const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
@@ -675,7 +675,7 @@ extern "C" int d2p_dtw_forward_marginals(const float* costs, const int* lengths,
     const int rc = dtw::check_shape(B, max_L1, max_L2, temperature);
     if (rc != D2P_OK) return rc;
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(costs && lengths && value && marginals && grad_T, "null pointer argument");
+    D2P_REQUIRE(costs && value && marginals && grad_T, "null pointer argument");
     const size_t need = d2p_dtw_workspace_bytes_banded(B, max_L1, max_L2, bandwidth);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;

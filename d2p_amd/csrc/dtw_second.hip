@@ -76,8 +76,8 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
 
-    const int L1 = min(max(lengths[2 * b], 0), L1max);
-    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
+    const int L2 = lengths ? min(max(lengths[2 * b + 1], 0), L2max) : L2max;
     const float c = kLog2e / T;
     const float rT = 1.0f / T;
     const float bw = (bandwidth < 0 || L1 == 0 || L2 == 0) ? -1.0f : (float)bandwidth;
@@ -316,8 +316,8 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
 
-    const int L1 = min(max(lengths[2 * b], 0), L1max);
-    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
+    const int L2 = lengths ? min(max(lengths[2 * b + 1], 0), L2max) : L2max;
     const float c = kLog2e / T;
     const float rT = 1.0f / T;
     const float bw = (bandwidth < 0 || L1 == 0 || L2 == 0) ? -1.0f : (float)bandwidth;
@@ -749,7 +749,7 @@ extern "C" int d2p_dtw_hvp(const float* costs, const float* tangent, const int* 
                            void* workspace, size_t workspace_bytes, void* stream) {
     D2P_TRY(dtw2::check(B, max_L1, max_L2, temperature));
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(costs && tangent && lengths && hvp, "null pointer argument");
+    D2P_REQUIRE(costs && tangent && hvp, "null pointer argument");
     D2P_REQUIRE(workspace && workspace_bytes >=
                                  d2p_dtw_second_workspace_bytes_banded(B, max_L1, max_L2,
                                                                        bandwidth),
@@ -772,7 +772,7 @@ extern "C" int d2p_dtw_param_jacobian(const float* costs, const int* lengths, in
                                       void* stream) {
     D2P_TRY(dtw2::check(B, max_L1, max_L2, temperature));
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(costs && lengths && jacobian, "null pointer argument");
+    D2P_REQUIRE(costs && jacobian, "null pointer argument");
     D2P_REQUIRE(workspace && workspace_bytes >=
                                  d2p_dtw_second_workspace_bytes_banded(B, max_L1, max_L2,
                                                                        bandwidth),
@@ -796,7 +796,7 @@ extern "C" int d2p_dtw_backward_full(const float* costs, const float* grad_align
                                      void* stream) {
     D2P_TRY(dtw2::check(B, max_L1, max_L2, temperature));
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(costs && grad_alignment && lengths && grad_costs && grad_T,
+    D2P_REQUIRE(costs && grad_alignment && grad_costs && grad_T,
                 "null pointer argument");
     D2P_REQUIRE(workspace && workspace_bytes >=
                                  d2p_dtw_second_workspace_bytes_banded(B, max_L1, max_L2,

@@ -85,8 +85,8 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     if (G == 1 && threadIdx.x == 0) *st = 0;              // G > 1: reset before the launch
     __syncthreads();
 
-    const int L1 = min(max(lengths[2 * b], 0), L1max);
-    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
+    const int L2 = lengths ? min(max(lengths[2 * b + 1], 0), L2max) : L2max;
     const float c = kLog2e / T;
     const float tl = T * kLn2;
     const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
@@ -323,8 +323,8 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
 
-    const int L1 = min(max(lengths[2 * b], 0), L1max);
-    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
+    const int L2 = lengths ? min(max(lengths[2 * b + 1], 0), L2max) : L2max;
     const float c = kLog2e / T;
     const float S = partition[b];
     const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
@@ -768,7 +768,7 @@ extern "C" int d2p_swa_forward_marginals(const float* scores, const int* lengths
     const int rc = swa::check_shape(B, max_L1, max_L2, temperature);
     if (rc != D2P_OK) return rc;
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(scores && lengths && partition && marginals && grad_open && grad_ext && grad_T,
+    D2P_REQUIRE(scores && partition && marginals && grad_open && grad_ext && grad_T,
                 "null pointer argument");
     const size_t need = d2p_swa_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");

@@ -27,10 +27,15 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
 // Reverse sweep: marginals, dS/dgap and dS/dT per element, from a forward's table.
 // precise: sum dS/dgap and dS/dT in double (for the second-order paths).
 // global: soft Needleman-Wunsch, from a global forward's table and value.
+// poison_value: when the call's last sweep is this one, the value array; if the
+// sweep runs unsplit, its epilogue writes NaN into all outputs of elements whose
+// status word is set (value included) and *poisoned comes back true, so that the
+// caller needs no separate poison pass.
 int launch_backward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                     float gap, float T, const Layout& ws, const float* partition,
                     float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
-                    bool precise = false, bool global = false);
+                    bool precise = false, bool global = false, float* poison_value = nullptr,
+                    bool* poisoned = nullptr);
 
 }  // namespace sw
 }  // namespace d2p_amd

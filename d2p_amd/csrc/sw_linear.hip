@@ -68,9 +68,10 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = QuadTile<P>;
-    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 64;        // two score chunks, two rows
+    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 64 + P;    // two score chunks, two rows
     float* tiles = smem + wave * WBUF;                     // double-buffered score chunk
     float* rbufs = tiles + 2 * Tile::FLOATS;               // boundary row of a chunk
+    float* upbuf = rbufs + 2 * 64;                         // the chunk's row above, by step
     __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
                                   // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
@@ -83,8 +84,8 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     if (NWG && threadIdx.x == 0) terminal = kNINF;
     __syncthreads();
 
-    const int L1 = min(max(lengths[2 * b], 0), L1max);
-    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
+    const int L2 = lengths ? min(max(lengths[2 * b + 1], 0), L2max) : L2max;
     const float c = kLog2e / T;
     const float tl = T * kLn2;
     const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
@@ -137,8 +138,10 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
         // NWG: lane r starts beside column 0 of its row, its diagonal beside column 0
         // of the row above (alpha[0,0] = 0 for lane 0 of the first stripe)
         float cur = left0, up_prev = NWG ? (float)(i0 + lane) * gap : kNINF;
+        float bm = -1e20f;   // the running max of this lane's alphas (partition)
+        int slot0 = 0;       // ring slot of step t0: t0 % R (R is a multiple of P)
 
-        for (int k = 0; k < nch; ++k) {
+        for (int k = 0; k < nch; ++k, slot0 = slot0 + P < R ? slot0 + P : slot0 + P - R) {
             const int t0 = k * P;
             chunk_waits<P>(prog, l, NL, k, nch, R, st);
             // this chunk's loads were issued one chunk ago and followed by at least the
@@ -152,13 +155,31 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             const float* tile = tiles + (k & 1) * Tile::FLOATS;
             float sv[P], av[P];
             read_quads<P, 1>(tile, lane, sv);
-            // lane 0's up values: column t0+j sits in lane j (ring slot = producer step);
-            // above the first stripe, row 0: NINF, or (NWG) alpha[0, t0+j+1] = (t0+j+1)*gap
-            float rreg = kNINF;
-            if (s > 0 && lane < P)
-                rreg = x_in ? rbufs[(k & 1) * 64 + lane] : ring_in[ring_index(t0 + lane + 63, R)];
-            else if (NWG && s == 0 && lane < P)
-                rreg = (float)(t0 + lane + 1) * gap;
+            // lane 0's up values, column t0+j from lane j (ring slot = producer step),
+            // staged so that step j reads them back with one broadcast LDS read; above
+            // the first stripe, row 0: NINF, or (NWG) alpha[0, t0+j+1] = (t0+j+1)*gap
+            if (lane < P) {
+                float rreg = kNINF;
+                if (s > 0) {
+                    int slot = slot0 + lane + 63;
+                    slot = slot < R ? slot : slot - R;
+                    rreg = x_in ? rbufs[(k & 1) * 64 + lane] : ring_in[slot];
+                } else if (NWG) {
+                    rreg = (float)(t0 + lane + 1) * gap;
+                }
+                upbuf[lane] = rreg;
+            }
+            // all P of them into registers before the steps (four 16-byte reads; a read
+            // inside the steps would wait behind the ring stores)
+            float upv[P];
+#pragma unroll
+            for (int q = 0; q < P / 4; ++q) {
+                const float4 x = reinterpret_cast<const float4*>(upbuf)[q];
+                upv[4 * q] = x.x;
+                upv[4 * q + 1] = x.y;
+                upv[4 * q + 2] = x.z;
+                upv[4 * q + 3] = x.w;
+            }
             if (k + 1 < nch) {
                 if (x_in) {
                     const int need = min(k + 1 + lead(P), nch);
@@ -171,7 +192,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             }
             // lane 63 publishes its alpha of step u into ring slot (t0+u) % R; the
             // other lanes write into the sink (R is a multiple of P: no wrap in a chunk)
-            float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
+            float* pub = (lane == 63) ? ring_out + slot0 : sink + lane;
             float* outc = out + (size_t)t0 * 64;
             // FULL: every cell of the chunk lies inside the element, no validity masks
             auto steps = [&](auto full) {
@@ -179,26 +200,29 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
 #pragma unroll
                 for (int u = 0; u < P; ++u) {
                     const int t = t0 + u;
-                    const float up = wave_shr1_or(cur, rreg);   // lane 0: stripe above
-                    rreg = wave_shl1(rreg);
+                    const float up = wave_shr1_or(cur, upv[u]);   // lane 0: stripe above
                     const float diag = up_prev;
                     up_prev = up;
                     // out-of-table neighbours are NINF, so no i>1 / j>1 guards are needed
                     const float vd = diag + sv[u];
                     const float vu = up + gap;
                     const float vl = cur + gap;
+                    // exponents (v - m) / T with the subtraction first, as the
+                    // reference: an fma against a rounded m*c would add the rounding of
+                    // m*c to alpha itself (about an ulp), which the temperature
+                    // Jacobians' (alpha - S) / T^2 terms amplify
                     float a;
                     if (NWG) {
                         const float m = fmaxf(fmaxf(vd, vu), vl);
                         const float sum = (fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c)) +
                                           fast_exp2((vl - m) * c);
-                        a = m + tl * fast_log2(sum);
+                        a = fmaf(tl, fast_log2(sum), m);
                     } else {
                         const float m = fmaxf(fmaxf(vd, vu), fmaxf(vl, sv[u]));
                         const float sum =
                             (fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c)) +
                             (fast_exp2((vl - m) * c) + fast_exp2((sv[u] - m) * c));
-                        a = m + tl * fast_log2(sum);
+                        a = fmaf(tl, fast_log2(sum), m);
                     }
                     if (FULL) {
                         cur = a;
@@ -214,16 +238,17 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                     lane_store(outc + u * 64, ul4, cur);
                     pub[u] = cur;
                     av[u] = cur;
+                    if (!NWG) bm = fmaxf(bm, cur);
                 }
             };
             if (i0 + 63 < L1 && t0 >= 63 && t0 + P <= L2) steps(std::true_type{});
             else steps(std::false_type{});
-            if (!NWG) acc.add_block<P>(av, c);
+            if (!NWG) acc.add_block_max<P>(av, bm, c);
             // the stripe's last row (lane 63) by step, contiguous, for the reverse sweep
             // of the stripe below and the next part; one store instruction
             wave_lds_sync();
             if (lane < P) {
-                const float v = ring_out[t0 % R + lane];
+                const float v = ring_out[slot0 + lane];
                 if (x_out) store_sys(brow_s + t0 + lane, v);
                 else lane_store(brow_s, (unsigned)(t0 + lane) * 4u, v);
             }
@@ -280,8 +305,9 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                    float* __restrict__ post, float* __restrict__ grad_gap,
                    float* __restrict__ grad_T, int* __restrict__ status, float* __restrict__ trash,
                    uint64_t* __restrict__ bflag, float2* __restrict__ flows,
-                   double* __restrict__ bpart, int B, int L1max, int L2max, int NSmax, float gap,
-                   float T, int R, int G, int SPW, uint32_t epoch) {
+                   double* __restrict__ bpart, float* __restrict__ poison_value, int B, int L1max,
+                   int L2max, int NSmax, float gap, float T, int R, int G, int SPW,
+                   uint32_t epoch) {
     extern __shared__ float smem[];
     __shared__ int prog[NW];
     using Acc = typename std::conditional<PRECISE, double, float>::type;
@@ -320,8 +346,8 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
 
-    const int L1 = min(max(lengths[2 * b], 0), L1max);
-    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
+    const int L2 = lengths ? min(max(lengths[2 * b + 1], 0), L2max) : L2max;
     const float c = kLog2e / T;
     const float S = partition[b];
     const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
@@ -403,8 +429,9 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
         issue_chunk(0);
         float in_left = 0.0f, in_up = 0.0f, in_diag = 0.0f, in_diag_next = 0.0f;
+        int slot0 = 0;   // ring slot of step k*P: (k*P) % R (R is a multiple of P)
 
-        for (int k = 0; k < nch; ++k) {
+        for (int k = 0; k < nch; ++k, slot0 = slot0 + P < R ? slot0 + P : slot0 + P - R) {
             const int t_hi = nsteps - 1 - k * P;
             chunk_waits<P>(prog, q, NL, k, nch, R, st);
             // this chunk's loads were issued one chunk ago and followed by exactly the P
@@ -440,8 +467,12 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     pre_u = buf[FBUF + 2 * (j + 1)];
                     pre_d = buf[FBUF + 2 * j + 1];
                 } else {
-                    pre_u = ring_in[ring_index(k * P + j + 63, R)].x;
-                    pre_d = ring_in[ring_index(k * P + j + 62, R)].y;
+                    // slots kP+j+63 and kP+j+62, below 2R (R >= 128 > P + 63)
+                    int su = slot0 + j + 63;
+                    su = su < R ? su : su - R;
+                    const int sd = su > 0 ? su - 1 : R - 1;
+                    pre_u = ring_in[su].x;
+                    pre_d = ring_in[sd].y;
                 }
             }
             if (k + 1 < nch) {
@@ -453,13 +484,16 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             // lane 0 publishes (up, diag) of step u into slot (kP+u) % R
-            float2* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
+            float2* pub = (lane == 0) ? ring_out + slot0 : sink + lane;
             // lane 63 starts the chunk with the ring's values for steps 0 and 1
             {
                 const float u0 = lane_bcast(pre_u, 63), d0 = lane_bcast(pre_d, 63);
                 const float d1 = lane_bcast(pre_d, 62);
                 if (lane == 63) { in_up = u0; in_diag = d0; in_diag_next = d1; }
             }
+            // PRECISE and NWG: the chunk's parameter-gradient terms are kept for balanced
+            // sums; otherwise each term goes into its accumulator with one fma
+            constexpr bool TERMS = PRECISE || NWG;
             Acc gs[P], ps[P];
             float pre_d2 = wave_shr1(pre_d);   // lane 63 = step 1 (then shifted on)
             pre_d2 = wave_shr1(pre_d2);        // lane 63 = step 2
@@ -510,7 +544,8 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const float pv = br * e03;
                 buf[obase_lane + u] = pv;
                 if (PRECISE) gs[u] = (Acc)ou + (Acc)ol;
-                else gs[u] = br * e12;
+                else if (TERMS) gs[u] = br * e12;
+                else g_acc = fmaf(br, e12, g_acc);
                 if (NWG) {
                     // flows into the boundary: column 0 (left: i gaps, diagonal: i - 1)
                     // and row 0 (up: column + 1 gaps, diagonal: column); FULL chunks can
@@ -519,7 +554,8 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     if (col == 0) gs[u] += (Acc)(ol * gi) + (Acc)(od * (gi - 1.0f));
                     if (top) gs[u] += (Acc)(ou * (float)(col + 1)) + (Acc)(od * (float)col);
                 }
-                ps[u] = (Acc)(pv * sc);
+                if (TERMS) ps[u] = (Acc)(pv * sc);
+                else p_acc = fmaf(pv, sc, p_acc);
                 pub[u] = make_float2(ou, od);
                 // successor contributions for the next steps; lane 63 takes the ring
                 pre_u = wave_shr1(pre_u);
@@ -534,8 +570,10 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             else steps(std::false_type{});
 
             // the chunk's parameter-gradient terms: balanced sums, then one add each
-            g_acc += tree_sum<P>(gs);
-            p_acc += tree_sum<P>(ps);
+            if (TERMS) {
+                g_acc += tree_sum<P>(gs);
+                p_acc += tree_sum<P>(ps);
+            }
             wave_lds_sync();
             // write this chunk's marginals back over the cells the scores came from:
             // exactly P stores (cells outside the element's lengths go to the trash
@@ -544,7 +582,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             publish(prog, wave, q * PROG_STRIDE + k + 1);
             if (x_out) {
                 // this chunk's flows to the part above, by producer step
-                if (lane < P) store_sys2(flows_out + k * P + lane, ring_out[ring_index(k * P, R) + lane]);
+                if (lane < P) store_sys2(flows_out + k * P + lane, ring_out[slot0 + lane]);
                 if (k >= 2) {
                     // at least 2 * (P/4 + P + 1) + P + 3 vector-memory operations follow
                     // the flow stores of chunk k - 2: those are complete
@@ -574,6 +612,20 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         } else {
             bpart[((size_t)b * G + part) * 2] = (double)g;
             bpart[((size_t)b * G + part) * 2 + 1] = (double)p;
+        }
+    }
+    // The last sweep of an unsplit call: every wave's stores are complete (barrier
+    // above), and the forward's status bits are visible; an element whose waits gave
+    // up gets NaN in all its outputs (the separate poison pass of split calls).
+    if (G == 1 && poison_value != nullptr &&
+        __builtin_amdgcn_readfirstlane(load_status(st)) != 0) {
+        __syncthreads();
+        const float nan = __builtin_nanf("");
+        for (size_t i = threadIdx.x; i < (size_t)L1max * L2max; i += NW * 64) pbase[i] = nan;
+        if (threadIdx.x == 0) {
+            poison_value[b] = nan;
+            grad_gap[b] = nan;
+            grad_T[b] = nan;
         }
     }
 }
@@ -608,7 +660,7 @@ constexpr size_t kLdsLimit = 160 * 1024 - 512;
 
 // LDS of one workgroup whose stripes' boundaries use rings of R columns
 size_t lds_forward_r(int R) {
-    return (size_t)wf::NW * (2 * 64 * PF + 2 * 64) * sizeof(float) +
+    return (size_t)wf::NW * (2 * 64 * PF + 2 * 64 + PF) * sizeof(float) +
            ((size_t)wf::NW * R + wf::NW * DUMMY) * sizeof(float);
 }
 size_t lds_backward_r(int R, int P) {
@@ -684,7 +736,7 @@ template <int P, bool PRECISE, bool NWG>
 int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                       float gap, float T, const Layout& ws, const float* partition,
                       float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
-                      const Split& sp, int R) {
+                      const Split& sp, int R, float* poison_value) {
     const int ns = (max_L1 + 63) / 64;
     const size_t lds = lds_backward_r(R, P);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
@@ -695,8 +747,9 @@ int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1
     D2P_LAUNCH(NWG ? "nw_backward" : "sw_backward", (sw_backward_kernel<P, PRECISE, NWG>),
                dim3(wf::split_grid(B, sp.G)),
                dim3(wf::NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
-               marginals, grad_gap, grad_T, ws.status, ws.trash, ws.bflag, ws.flows, ws.bpart, B,
-               max_L1, max_L2, ns, gap, T, R, sp.G, sp.SPW, epoch);
+               marginals, grad_gap, grad_T, ws.status, ws.trash, ws.bflag, ws.flows, ws.bpart,
+               sp.G == 1 ? poison_value : nullptr, B, max_L1, max_L2, ns, gap, T, R, sp.G, sp.SPW,
+               epoch);
     if (sp.G > 1)
         D2P_LAUNCH("sw_grad_merge", sw_grad_merge<PRECISE>, dim3((B + 255) / 256), dim3(256), 0,
                    st, ws.bpart, partition, grad_gap, grad_T, B, sp.G, gap, T);
@@ -707,14 +760,15 @@ int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1
 int launch_backward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                     float gap, float T, const Layout& ws, const float* partition,
                     float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
-                    bool precise, bool global) {
+                    bool precise, bool global, float* poison_value, bool* poisoned) {
     const Split sp = choose_split(B, max_L1, ws, max_stripes_backward(max_L1, max_L2));
+    if (poisoned != nullptr) *poisoned = sp.G == 1 && poison_value != nullptr;
     const int rows = sp.G > 1 ? sp.SPW * 64 : max_L1;
     const int R = ring_backward(rows, max_L2);
     const int P = backward_chunk(rows, max_L2);
 #define D2P_SW_BWD(P_, PR_, G_)                                                               \
     launch_backward_p<P_, PR_, G_>(scores, lengths, B, max_L1, max_L2, gap, T, ws, partition, \
-                                   marginals, grad_gap, grad_T, st, sp, R)
+                                   marginals, grad_gap, grad_T, st, sp, R, poison_value)
     if (global) {
         if (P == 16) return precise ? D2P_SW_BWD(16, true, true) : D2P_SW_BWD(16, false, true);
         return precise ? D2P_SW_BWD(8, true, true) : D2P_SW_BWD(8, false, true);
@@ -756,7 +810,7 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
     const int rc = sw::check_shape(B, max_L1, max_L2, temperature);
     if (rc != D2P_OK) return rc;
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(scores && lengths && partition && marginals && grad_gap && grad_T,
+    D2P_REQUIRE(scores && partition && marginals && grad_gap && grad_T,
                 "null pointer argument");
     const size_t need = d2p_sw_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
@@ -764,8 +818,11 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
     const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 1, true);
     D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
                                partition, st));
+    bool poisoned = false;
     D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
-                                partition, marginals, grad_gap, grad_T, st));
+                                partition, marginals, grad_gap, grad_T, st, false, false,
+                                partition, &poisoned));
+    if (poisoned) return D2P_OK;
     return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr,
                              partition, grad_gap, grad_T, nullptr, st);
 }
@@ -811,7 +868,7 @@ extern "C" int d2p_sw_forward_marginals_noalloc(const float* scores, const int* 
     const int rc = sw::check_shape(B, max_L1, max_L2, temperature);
     if (rc != D2P_OK) return rc;
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(scores && lengths && partition && marginals && grad_gap && grad_T,
+    D2P_REQUIRE(scores && partition && marginals && grad_gap && grad_T,
                 "null pointer argument");
     const size_t need = d2p_sw_workspace_bytes(B, max_L1, max_L2);
     if (need > kScratchBytes) {
@@ -828,8 +885,11 @@ extern "C" int d2p_sw_forward_marginals_noalloc(const float* scores, const int* 
     const wf::Layout ws = wf::layout(ws_ptr, B, max_L1, max_L2, 1, true);
     D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
                                partition, st));
+    bool poisoned = false;
     D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
-                                partition, marginals, grad_gap, grad_T, st));
+                                partition, marginals, grad_gap, grad_T, st, false, false,
+                                partition, &poisoned));
+    if (poisoned) return D2P_OK;
     return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr,
                              partition, grad_gap, grad_T, nullptr, st);
 }
@@ -846,7 +906,7 @@ extern "C" int d2p_nw_forward_marginals(const float* scores, const int* lengths,
     const int rc = sw::check_shape(B, max_L1, max_L2, temperature);
     if (rc != D2P_OK) return rc;
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(scores && lengths && value && marginals && grad_gap && grad_T,
+    D2P_REQUIRE(scores && value && marginals && grad_gap && grad_T,
                 "null pointer argument");
     const size_t need = d2p_nw_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
@@ -854,8 +914,10 @@ extern "C" int d2p_nw_forward_marginals(const float* scores, const int* lengths,
     const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 1, true);
     D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws, value,
                                st, true));
+    bool poisoned = false;
     D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws, value,
-                                marginals, grad_gap, grad_T, st, false, true));
+                                marginals, grad_gap, grad_T, st, false, true, value, &poisoned));
+    if (poisoned) return D2P_OK;
     return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr, value,
                              grad_gap, grad_T, nullptr, st);
 }

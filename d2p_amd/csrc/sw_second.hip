@@ -85,8 +85,8 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
 
-    const int L1 = min(max(lengths[2 * b], 0), L1max);
-    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
+    const int L2 = lengths ? min(max(lengths[2 * b + 1], 0), L2max) : L2max;
     const float c = kLog2e / T;
     const float rT = 1.0f / T;
     const float S = partition[b];
@@ -346,8 +346,8 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
 
-    const int L1 = min(max(lengths[2 * b], 0), L1max);
-    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
+    const int L2 = lengths ? min(max(lengths[2 * b + 1], 0), L2max) : L2max;
     const float c = kLog2e / T;
     const float rT = 1.0f / T;
     const float S = partition[b];
@@ -804,7 +804,7 @@ int hvp_impl(const float* scores, const float* tangent, const int* lengths, int 
              size_t workspace_bytes, void* stream) {
     D2P_TRY(sw2::check(B, max_L1, max_L2, temperature));
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(scores && tangent && lengths && hvp, "null pointer argument");
+    D2P_REQUIRE(scores && tangent && hvp, "null pointer argument");
     const size_t need = d2p_sw_second_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
@@ -826,7 +826,7 @@ int param_jacobian_impl(const float* scores, int param_type, const int* lengths,
     D2P_TRY(sw2::check(B, max_L1, max_L2, temperature));
     D2P_REQUIRE(param_type == 0 || param_type == 1, "param_type must be 0 or 1");
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(scores && lengths && jacobian, "null pointer argument");
+    D2P_REQUIRE(scores && jacobian, "null pointer argument");
     const size_t need = d2p_sw_second_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
@@ -862,7 +862,7 @@ int backward_full_impl(const float* scores, const float* grad_alignment, const i
                        size_t workspace_bytes, void* stream) {
     D2P_TRY(sw2::check(B, max_L1, max_L2, temperature));
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(scores && grad_alignment && lengths && grad_scores && grad_gap && grad_T,
+    D2P_REQUIRE(scores && grad_alignment && grad_scores && grad_gap && grad_T,
                 "null pointer argument");
     const size_t need = d2p_sw_second_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");

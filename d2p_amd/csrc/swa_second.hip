@@ -82,8 +82,8 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
 
-    const int L1 = min(max(lengths[2 * b], 0), L1max);
-    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
+    const int L2 = lengths ? min(max(lengths[2 * b + 1], 0), L2max) : L2max;
     const float c = kLog2e / T;
     const float rT = 1.0f / T;
     const float S = partition[b];
@@ -394,8 +394,8 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
 
-    const int L1 = min(max(lengths[2 * b], 0), L1max);
-    const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+    const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
+    const int L2 = lengths ? min(max(lengths[2 * b + 1], 0), L2max) : L2max;
     const float c = kLog2e / T;
     const float rT = 1.0f / T;
     const float S = partition[b];
@@ -957,7 +957,7 @@ extern "C" int d2p_swa_hvp(const float* scores, const float* tangent, const int*
                            size_t workspace_bytes, void* stream) {
     D2P_TRY(swa2::check(B, max_L1, max_L2, temperature));
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(scores && tangent && lengths && hvp, "null pointer argument");
+    D2P_REQUIRE(scores && tangent && hvp, "null pointer argument");
     D2P_REQUIRE(workspace && workspace_bytes >= d2p_swa_second_workspace_bytes(B, max_L1, max_L2),
                 "workspace too small");
     hipStream_t st = (hipStream_t)stream;
@@ -980,7 +980,7 @@ extern "C" int d2p_swa_param_jacobian(const float* scores, int param_type, const
     D2P_TRY(swa2::check(B, max_L1, max_L2, temperature));
     D2P_REQUIRE(param_type >= 0 && param_type <= 2, "param_type must be 0, 1 or 2");
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(scores && lengths && jacobian, "null pointer argument");
+    D2P_REQUIRE(scores && jacobian, "null pointer argument");
     D2P_REQUIRE(workspace && workspace_bytes >= d2p_swa_second_workspace_bytes(B, max_L1, max_L2),
                 "workspace too small");
     hipStream_t st = (hipStream_t)stream;
@@ -1019,7 +1019,7 @@ extern "C" int d2p_swa_backward_full(const float* scores, const float* grad_alig
                                      void* stream) {
     D2P_TRY(swa2::check(B, max_L1, max_L2, temperature));
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(scores && grad_alignment && lengths && grad_scores && grad_open && grad_ext &&
+    D2P_REQUIRE(scores && grad_alignment && grad_scores && grad_open && grad_ext &&
                     grad_T,
                 "null pointer argument");
     D2P_REQUIRE(workspace && workspace_bytes >= d2p_swa_second_workspace_bytes(B, max_L1, max_L2),

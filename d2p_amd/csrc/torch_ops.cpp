@@ -74,11 +74,9 @@ Dims checked_dims(const Tensor& x, const char* family) {
 Tensor resolve_lengths(const c10::optional<Tensor>& lengths_opt, const Dims& d,
                        const torch::Device& device, const char* input = "scores") {
     if (!lengths_opt.has_value() || !lengths_opt->defined()) {
-        // built on the device: no host round trip, nothing to validate
-        Tensor l = torch::empty({d.B, 2}, torch::TensorOptions().dtype(torch::kInt32).device(device));
-        l.select(1, 0).fill_(d.L1);
-        l.select(1, 1).fill_(d.L2);
-        return l;
+        // full lengths: the kernels take a null lengths pointer as (L1, L2) for every
+        // element, so nothing is built, copied or validated
+        return Tensor();
     }
     const Tensor& lengths = *lengths_opt;
     TORCH_CHECK(lengths.is_cuda(), "lengths must be a CUDA tensor");
@@ -114,6 +112,18 @@ void check_status(const Tensor& ws, int B) {
     D2P_CALL(d2p_sw_status(ws.data_ptr(), B, &st, current_stream()));
     TORCH_CHECK(st == 0, "d2p_amd: a pipeline wait of the DP sweeps gave up (status ", st,
                 "); the affected batch elements' outputs are NaN");
+}
+
+// The lengths argument of the C ABI: null for full lengths.
+const int* lengths_ptr(const Tensor& lengths) {
+    return lengths.defined() ? lengths.data_ptr<int>() : nullptr;
+}
+
+// Lengths as an autograd Function input: absent (full lengths) is passed as an empty
+// optional, which the Function treats as a non-differentiable, non-tensor input
+// (an undefined Tensor input has no device for the autograd node to record).
+c10::optional<Tensor> lengths_arg(const Tensor& lengths) {
+    return lengths.defined() ? c10::optional<Tensor>(lengths) : c10::nullopt;
 }
 
 Tensor workspace(size_t bytes, const Tensor& like) {
@@ -157,7 +167,7 @@ SwOut sw_run(const Tensor& scores, const Tensor& lengths, const Dims& d, float g
     const size_t ws_bytes = d2p_sw_workspace_bytes(d.B, d.L1, d.L2);
     Tensor ws = workspace(ws_bytes, scores);
     D2P_CALL(d2p_sw_forward_marginals(
-        scores.data_ptr<float>(), lengths.data_ptr<int>(), d.B, d.L1, d.L2, gap, T,
+        scores.data_ptr<float>(), lengths_ptr(lengths), d.B, d.L1, d.L2, gap, T,
         o.partition.data_ptr<float>(), o.marginals.data_ptr<float>(),
         o.grad_gap.data_ptr<float>(), o.grad_T.data_ptr<float>(), ws.data_ptr(), ws_bytes,
         current_stream()));
@@ -176,7 +186,7 @@ Tensor sw_hvp_run(const Tensor& scores, const Tensor& tangent, const Tensor& len
     Tensor out = torch::empty({d.B, d.L1, d.L2}, scores.options());
     Tensor ws = second_workspace(d, scores);
     D2P_CALL((global ? d2p_nw_hvp : d2p_sw_hvp)(
-        scores.data_ptr<float>(), tangent.data_ptr<float>(), lengths.data_ptr<int>(), d.B, d.L1,
+        scores.data_ptr<float>(), tangent.data_ptr<float>(), lengths_ptr(lengths), d.B, d.L1,
         d.L2, gap, T, out.data_ptr<float>(), ws.data_ptr(), ws.numel(), current_stream()));
     check_status(ws, d.B);
     return out;
@@ -187,7 +197,7 @@ Tensor sw_param_jacobian_run(const Tensor& scores, int param_type, const Tensor&
     Tensor out = torch::empty({d.B, d.L1, d.L2}, scores.options());
     Tensor ws = second_workspace(d, scores);
     D2P_CALL((global ? d2p_nw_param_jacobian : d2p_sw_param_jacobian)(
-        scores.data_ptr<float>(), param_type, lengths.data_ptr<int>(), d.B, d.L1, d.L2, gap, T,
+        scores.data_ptr<float>(), param_type, lengths_ptr(lengths), d.B, d.L1, d.L2, gap, T,
         out.data_ptr<float>(), ws.data_ptr(), ws.numel(), current_stream()));
     check_status(ws, d.B);
     return out;
@@ -202,7 +212,7 @@ std::tuple<Tensor, Tensor, Tensor> sw_backward_full_run(const Tensor& scores, co
     Tensor gg = torch::empty({d.B}, opt), gt = torch::empty({d.B}, opt);
     Tensor ws = second_workspace(d, scores);
     D2P_CALL((global ? d2p_nw_backward_full : d2p_sw_backward_full)(scores.data_ptr<float>(), ga.data_ptr<float>(),
-                                  lengths.data_ptr<int>(), d.B, d.L1, d.L2, gap, T,
+                                  lengths_ptr(lengths), d.B, d.L1, d.L2, gap, T,
                                   gs.data_ptr<float>(), gg.data_ptr<float>(), gt.data_ptr<float>(),
                                   ws.data_ptr(), ws.numel(), current_stream()));
     check_status(ws, d.B);
@@ -269,9 +279,9 @@ tensor_list sw_autograd_backward(AutogradContext* ctx, const tensor_list& grads,
 
 class SoftSWFloatFunction : public torch::autograd::Function<SoftSWFloatFunction> {
    public:
-    static tensor_list forward(AutogradContext* ctx, Tensor scores, Tensor lengths, double gap,
-                               double temperature) {
-        return sw_autograd_forward(ctx, scores, lengths, gap, temperature);
+    static tensor_list forward(AutogradContext* ctx, Tensor scores,
+                               c10::optional<Tensor> lengths, double gap, double temperature) {
+        return sw_autograd_forward(ctx, scores, lengths.value_or(Tensor()), gap, temperature);
     }
     static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
         auto g = sw_autograd_backward(ctx, grads, false, false);
@@ -308,7 +318,7 @@ std::vector<Tensor> soft_sw_float(Tensor scores, double gap, double temperature,
     Dims d = checked_dims(scores, "SW");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
     Tensor l = resolve_lengths(lengths, d, scores.device());
-    return SoftSWFloatFunction::apply(scores, l, gap, temperature);
+    return SoftSWFloatFunction::apply(scores, lengths_arg(l), gap, temperature);
 }
 
 std::tuple<Tensor, Tensor, Tensor, Tensor> soft_sw_with_grads(Tensor scores, double gap,
@@ -399,7 +409,7 @@ SwOut nw_run(const Tensor& scores, const Tensor& lengths, const Dims& d, float g
     const size_t ws_bytes = d2p_nw_workspace_bytes(d.B, d.L1, d.L2);
     Tensor ws = workspace(ws_bytes, scores);
     D2P_CALL(d2p_nw_forward_marginals(
-        scores.data_ptr<float>(), lengths.data_ptr<int>(), d.B, d.L1, d.L2, gap, T,
+        scores.data_ptr<float>(), lengths_ptr(lengths), d.B, d.L1, d.L2, gap, T,
         o.partition.data_ptr<float>(), o.marginals.data_ptr<float>(),
         o.grad_gap.data_ptr<float>(), o.grad_T.data_ptr<float>(), ws.data_ptr(), ws_bytes,
         current_stream()));
@@ -453,9 +463,9 @@ tensor_list nw_autograd_backward(AutogradContext* ctx, const tensor_list& grads,
 
 class SoftNWFloatFunction : public torch::autograd::Function<SoftNWFloatFunction> {
    public:
-    static tensor_list forward(AutogradContext* ctx, Tensor scores, Tensor lengths, double gap,
-                               double temperature) {
-        return nw_autograd_forward(ctx, scores, lengths, gap, temperature);
+    static tensor_list forward(AutogradContext* ctx, Tensor scores,
+                               c10::optional<Tensor> lengths, double gap, double temperature) {
+        return nw_autograd_forward(ctx, scores, lengths.value_or(Tensor()), gap, temperature);
     }
     static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
         auto g = nw_autograd_backward(ctx, grads, false, false);
@@ -492,7 +502,7 @@ std::vector<Tensor> soft_nw_float(Tensor scores, double gap, double temperature,
     Dims d = checked_dims(scores, "NW");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
     Tensor l = resolve_lengths(lengths, d, scores.device());
-    return SoftNWFloatFunction::apply(scores, l, gap, temperature);
+    return SoftNWFloatFunction::apply(scores, lengths_arg(l), gap, temperature);
 }
 
 std::tuple<Tensor, Tensor, Tensor, Tensor> soft_nw_with_grads(Tensor scores, double gap,
@@ -603,7 +613,7 @@ SwaOut swa_run(const Tensor& scores, const Tensor& lengths, const Dims& d, float
     const size_t ws_bytes = d2p_swa_workspace_bytes(d.B, d.L1, d.L2);
     Tensor ws = workspace(ws_bytes, scores);
     D2P_CALL(d2p_swa_forward_marginals(
-        scores.data_ptr<float>(), lengths.data_ptr<int>(), d.B, d.L1, d.L2, go, ge, T,
+        scores.data_ptr<float>(), lengths_ptr(lengths), d.B, d.L1, d.L2, go, ge, T,
         o.partition.data_ptr<float>(), o.marginals.data_ptr<float>(),
         o.grad_open.data_ptr<float>(), o.grad_ext.data_ptr<float>(), o.grad_T.data_ptr<float>(),
         ws.data_ptr(), ws_bytes, current_stream()));
@@ -627,7 +637,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> swa_backward_full_run(const Tensor& s
     Tensor g_t = torch::empty({d.B}, opt);
     Tensor ws = swa_second_workspace(d, scores);
     D2P_CALL(d2p_swa_backward_full(scores.data_ptr<float>(), ga.data_ptr<float>(),
-                                   lengths.data_ptr<int>(), d.B, d.L1, d.L2, go, ge, T,
+                                   lengths_ptr(lengths), d.B, d.L1, d.L2, go, ge, T,
                                    gs.data_ptr<float>(), g_o.data_ptr<float>(),
                                    g_e.data_ptr<float>(), g_t.data_ptr<float>(), ws.data_ptr(),
                                    ws.numel(), current_stream()));
@@ -687,9 +697,9 @@ tensor_list swa_autograd_backward(AutogradContext* ctx, const tensor_list& grads
 
 class SoftSWAffineFloatFunction : public torch::autograd::Function<SoftSWAffineFloatFunction> {
    public:
-    static tensor_list forward(AutogradContext* ctx, Tensor scores, Tensor lengths, double go,
-                               double ge, double T) {
-        return swa_autograd_forward(ctx, scores, lengths, go, ge, T);
+    static tensor_list forward(AutogradContext* ctx, Tensor scores,
+                               c10::optional<Tensor> lengths, double go, double ge, double T) {
+        return swa_autograd_forward(ctx, scores, lengths.value_or(Tensor()), go, ge, T);
     }
     static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
         auto g = swa_autograd_backward(ctx, grads, false, false, false);
@@ -728,7 +738,8 @@ std::vector<Tensor> swa_float(Tensor scores, double gap_open, double gap_ext, do
     Dims d = checked_dims_affine(scores);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
     Tensor l = resolve_lengths(lengths, d, scores.device());
-    return SoftSWAffineFloatFunction::apply(scores, l, gap_open, gap_ext, temperature);
+    return SoftSWAffineFloatFunction::apply(scores, lengths_arg(l), gap_open, gap_ext,
+                                            temperature);
 }
 
 std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> swa_with_grads(Tensor scores, double gap_open,
@@ -763,7 +774,7 @@ Tensor swa_hvp(Tensor scores, Tensor tangent, double gap_open, double gap_ext, d
     Tensor l = resolve_lengths(lengths, d, scores.device());
     Tensor out = torch::empty({d.B, d.L1, d.L2}, scores.options());
     Tensor ws = swa_second_workspace(d, scores);
-    D2P_CALL(d2p_swa_hvp(scores.data_ptr<float>(), tangent.data_ptr<float>(), l.data_ptr<int>(),
+    D2P_CALL(d2p_swa_hvp(scores.data_ptr<float>(), tangent.data_ptr<float>(), lengths_ptr(l),
                          d.B, d.L1, d.L2, (float)gap_open, (float)gap_ext, (float)temperature,
                          out.data_ptr<float>(), ws.data_ptr(), ws.numel(), current_stream()));
     check_status(ws, d.B);
@@ -781,7 +792,7 @@ Tensor swa_param_jacobian(Tensor scores, int64_t param_type, double gap_open, do
     Tensor l = resolve_lengths(lengths, d, scores.device());
     Tensor out = torch::empty({d.B, d.L1, d.L2}, scores.options());
     Tensor ws = swa_second_workspace(d, scores);
-    D2P_CALL(d2p_swa_param_jacobian(scores.data_ptr<float>(), (int)param_type, l.data_ptr<int>(),
+    D2P_CALL(d2p_swa_param_jacobian(scores.data_ptr<float>(), (int)param_type, lengths_ptr(l),
                                     d.B, d.L1, d.L2, (float)gap_open, (float)gap_ext,
                                     (float)temperature, out.data_ptr<float>(), ws.data_ptr(),
                                     ws.numel(), current_stream()));
@@ -862,7 +873,7 @@ DtwOut dtw_run(const Tensor& costs, const Tensor& lengths, const Dims& d, float 
     const size_t ws_bytes = d2p_dtw_workspace_bytes_banded(d.B, d.L1, d.L2, bw);
     Tensor ws = workspace(ws_bytes, costs);
     D2P_CALL(d2p_dtw_forward_marginals(
-        costs.data_ptr<float>(), lengths.data_ptr<int>(), d.B, d.L1, d.L2, T, bw,
+        costs.data_ptr<float>(), lengths_ptr(lengths), d.B, d.L1, d.L2, T, bw,
         o.value.data_ptr<float>(), o.marginals.data_ptr<float>(), o.grad_T.data_ptr<float>(),
         ws.data_ptr(), ws_bytes, current_stream()));
     check_status(ws, d.B);
@@ -881,7 +892,7 @@ std::tuple<Tensor, Tensor> dtw_backward_full_run(const Tensor& costs, const Tens
     Tensor gt = torch::empty({d.B}, costs.options());
     Tensor ws = dtw_second_workspace(d, bw, costs);
     D2P_CALL(d2p_dtw_backward_full(costs.data_ptr<float>(), ga.data_ptr<float>(),
-                                   lengths.data_ptr<int>(), d.B, d.L1, d.L2, T, bw,
+                                   lengths_ptr(lengths), d.B, d.L1, d.L2, T, bw,
                                    gc.data_ptr<float>(), gt.data_ptr<float>(), ws.data_ptr(),
                                    ws.numel(), current_stream()));
     check_status(ws, d.B);
@@ -894,7 +905,7 @@ std::tuple<Tensor, Tensor> dtw_backward_full_run(const Tensor& costs, const Tens
 class SoftDTWFunction : public torch::autograd::Function<SoftDTWFunction> {
    public:
     static tensor_list forward(AutogradContext* ctx, Tensor costs, Tensor temperature,
-                               Tensor lengths, int64_t bandwidth) {
+                               c10::optional<Tensor> lengths, int64_t bandwidth) {
         ctx->set_materialize_grads(false);
         CHECK_INPUT_DEV(costs);
         Dims d = checked_dims_dtw(costs);
@@ -946,7 +957,8 @@ std::vector<Tensor> dtw_float(Tensor costs, double temperature, c10::optional<Te
     c10::hip::HIPGuardMasqueradingAsCUDA guard(costs.device());
     Tensor temp_t = torch::tensor({(float)temperature}, costs.options());
     Tensor l = resolve_lengths(lengths, d, costs.device(), "costs");
-    return SoftDTWFunction::apply(costs, temp_t, l, bandwidth.has_value() ? *bandwidth : -1);
+    return SoftDTWFunction::apply(costs, temp_t, lengths_arg(l),
+                                  bandwidth.has_value() ? *bandwidth : -1);
 }
 
 std::tuple<Tensor, Tensor, Tensor> dtw_with_grads(Tensor costs, double temperature,
@@ -974,7 +986,7 @@ Tensor dtw_hvp(Tensor costs, Tensor tangent, double temperature, c10::optional<T
     const int bw = checked_bandwidth(bandwidth.has_value() ? *bandwidth : -1);
     Tensor out = torch::empty({d.B, d.L1, d.L2}, costs.options());
     Tensor ws = dtw_second_workspace(d, bw, costs);
-    D2P_CALL(d2p_dtw_hvp(costs.data_ptr<float>(), tangent.data_ptr<float>(), l.data_ptr<int>(),
+    D2P_CALL(d2p_dtw_hvp(costs.data_ptr<float>(), tangent.data_ptr<float>(), lengths_ptr(l),
                          d.B, d.L1, d.L2, (float)temperature, bw, out.data_ptr<float>(),
                          ws.data_ptr(), ws.numel(), current_stream()));
     check_status(ws, d.B);
@@ -990,7 +1002,7 @@ Tensor dtw_param_jacobian(Tensor costs, double temperature, c10::optional<Tensor
     const int bw = checked_bandwidth(bandwidth.has_value() ? *bandwidth : -1);
     Tensor out = torch::empty({d.B, d.L1, d.L2}, costs.options());
     Tensor ws = dtw_second_workspace(d, bw, costs);
-    D2P_CALL(d2p_dtw_param_jacobian(costs.data_ptr<float>(), l.data_ptr<int>(), d.B, d.L1, d.L2,
+    D2P_CALL(d2p_dtw_param_jacobian(costs.data_ptr<float>(), lengths_ptr(l), d.B, d.L1, d.L2,
                                     (float)temperature, bw, out.data_ptr<float>(), ws.data_ptr(),
                                     ws.numel(), current_stream()));
     check_status(ws, d.B);

@@ -5,7 +5,8 @@
  * reference: extern "C" host wrappers in src/{sw,sw_affine,dtw}/kernels.cuh that
  * take plain device pointers and sizes).  Every entry point:
  *   - takes device pointers to caller-owned, contiguous buffers (float32 data,
- *     int32 lengths [B,2] with 0 <= lengths[b,0] <= max_L1, 0 <= lengths[b,1] <= max_L2),
+ *     int32 lengths [B,2] with 0 <= lengths[b,0] <= max_L1, 0 <= lengths[b,1] <= max_L2;
+ *     a NULL lengths pointer means every element has lengths (max_L1, max_L2)),
  *   - never allocates: scratch memory is a caller-provided workspace whose size the
  *     matching *_workspace_bytes() function returns,
  *   - enqueues its kernels on `stream` (a hipStream_t passed as void*; NULL = the

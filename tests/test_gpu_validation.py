@@ -156,3 +156,22 @@ def test_value_path_launches_no_second_order_kernels(cuda, family):
     names = _kernels_launched(marginal_path)
     prefix = {"sw": "sw", "swa": "swa", "dtw": "dtw", "nw": "nw"}[family]
     assert {f"{prefix}_tangent", f"{prefix}_dual"} <= names, names
+
+
+def test_null_lengths_mean_full_lengths(cuda):
+    """A NULL lengths pointer in the C ABI is the full (max_L1, max_L2) of every
+    element: bit-identical to passing those lengths."""
+    from _capi import ptr, stream, sw_forward_marginals
+    g = torch.Generator().manual_seed(71)
+    B, L1, L2 = 3, 200, 150
+    x = torch.randn((B, L1, L2), generator=g).to(cuda)
+    want = sw_forward_marginals(x, None, -1.0, 1.0)
+    outs = [torch.empty(B, device=cuda), torch.empty(B, L1, L2, device=cuda),
+            torch.empty(B, device=cuda), torch.empty(B, device=cuda)]
+    n = lib().d2p_sw_workspace_bytes(B, L1, L2)
+    ws = torch.empty(n, dtype=torch.uint8, device=cuda)
+    check(lib().d2p_sw_forward_marginals(ptr(x), None, B, L1, L2, -1.0, 1.0,
+                                         *[ptr(o) for o in outs], ptr(ws), n, stream()))
+    torch.cuda.synchronize()
+    for a, b in zip(outs, want):
+        assert torch.equal(a, b)
