@@ -49,6 +49,10 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 CPU_TARGET_S = 10.0   # CPU baseline: repeat the step for about this long
+# Threads of the CPU baseline: the reference's at::parallel_for uses every core it is
+# given; on the GPU box a process is given a share of 16 host cores per GPU (worker
+# pools are sized to it), so the threaded leg uses min(available cores, 16).
+CPU_SHARE = 16
 METRIC = "DP cells/sec fwd+bwd, soft_sw B=256 512x512 fp32; achieved HBM GB/s %"
 
 
@@ -287,7 +291,8 @@ def cpu_baseline_config(cfg, max_elems):
     kind = "reference" if O.reference_available() else "port"
     k = O.get("oracle" if kind == "port" else "reference")
     n = min(max_elems, len(next(iter(cfg["inputs"].values()))))
-    cores = max(1, min(16, os.cpu_count() or 1, n))
+    cores, info = baseline_threads()
+    cores = min(cores, n)
     O.set_threads(cores)
     name = cfg["name"]
     x = {kk: v[:n].contiguous().numpy() for kk, v in cfg["inputs"].items()}
@@ -334,9 +339,38 @@ def cpu_baseline_config(cfg, max_elems):
             return k.sw_hvp(a, x["scores"], p, x["V"], None, -1.0, 1.0)[0]
         what = "fwd + HVP sweeps"
     t, runs = _timed_runs(step)
+    O.set_threads(1)
+    t1, runs1 = _timed_runs(step, target_s=CPU_TARGET_S / 2, max_runs=20)
     return {"value": cells / t, "unit": "cells/s", "cores": cores, "kind": kind,
+            "one_thread_value": cells / t1, **info,
             "sample": f"first {n} of {len(next(iter(cfg['inputs'].values())))} batch elements, "
-                      f"{what}, median of {runs} runs after 1 warm-up ({t:.3f} s each)"}
+                      f"{what}, median of {runs} runs after 1 warm-up ({t:.3f} s each); "
+                      f"1 thread: median of {runs1} runs ({t1:.3f} s each)"}
+
+
+def host_info():
+    """Host facts recorded beside the CPU baseline."""
+    import platform
+    model = platform.processor() or ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    import torch
+    return {"nproc": os.cpu_count(), "available_cores": avail, "cpu_model": model,
+            "torch_threads_default": torch.get_num_threads()}
+
+
+def baseline_threads():
+    info = host_info()
+    return max(1, min(CPU_SHARE, info["available_cores"])), info
 
 
 def _timed_runs(step, target_s=CPU_TARGET_S, max_runs=200):
@@ -359,7 +393,7 @@ def cpu_baseline(scores_np):
     from oracle import oracle as O
     kind = "reference" if O.reference_available() else "port"
     k = O.get("oracle" if kind == "port" else "reference")
-    cores = max(1, min(16, os.cpu_count() or 1))
+    cores, info = baseline_threads()
     O.set_threads(cores)
     ones = np.ones((scores_np.shape[0], 1, 1), np.float32)
 
@@ -371,9 +405,25 @@ def cpu_baseline(scores_np):
 
     t, runs = _timed_runs(step)
     cells = scores_np.shape[0] * scores_np.shape[1] * scores_np.shape[2]
+    # one thread: the first 16 elements of the batch (the per-element work is the
+    # same; the full batch would take minutes on one core)
+    sub_np = np.ascontiguousarray(scores_np[:16])
+    O.set_threads(1)
+
+    def step1():
+        alpha, part = k.sw_forward(sub_np, None, -1.0, 1.0)
+        k.sw_backward(alpha, sub_np, part, None, -1.0, 1.0)
+        post, _, _ = k.sw_backward(alpha, sub_np, part, None, -1.0, 1.0)
+        return post
+
+    t1, runs1 = _timed_runs(step1, target_s=CPU_TARGET_S / 2, max_runs=20)
+    cells1 = sub_np.shape[0] * sub_np.shape[1] * sub_np.shape[2]
     return {"value": cells / t, "unit": "cells/s", "cores": cores, "kind": kind,
-            "sample": f"full C2 batch {list(scores_np.shape)} fwd + 2x bwd DP + scale, "
-                      f"median of {runs} runs after 1 warm-up ({t:.3f} s each)"}
+            "one_thread_value": cells1 / t1, **info,
+            "sample": f"full C2 batch {list(scores_np.shape)} fwd + 2x bwd DP + scale on "
+                      f"{cores} threads, median of {runs} runs after 1 warm-up ({t:.3f} s "
+                      f"each); 1 thread: first 16 elements, median of {runs1} runs "
+                      f"({t1:.3f} s each)"}
 
 
 def main():
