@@ -16,6 +16,7 @@ import pytest
 import torch
 
 import _capi
+from _parity import close_entrywise, dot_consistent
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -29,10 +30,7 @@ def _seeded(seed, shape, scale=1.0):
 
 
 def _close(gpu, ref, what, extra=0.0):
-    gpu = gpu.detach().cpu().numpy() if torch.is_tensor(gpu) else np.asarray(gpu)
-    tol = ATOL * max(1.0, float(np.abs(ref).max())) + extra
-    err = float(np.abs(gpu - ref).max())
-    assert err <= tol, f"{what}: max |gpu - ref| = {err:.3e} > {tol:.3e}"
+    close_entrywise(gpu, ref, what, extra, ATOL)
 
 
 CASES = [
@@ -122,3 +120,8 @@ def test_dtw_backward_full_and_marginal_autograd(cuda):
     _close(x.grad, H + 0.25 * rm, "dtw marginal-path grad_costs")
     ref = dT + 0.25 * float(rgt.sum())
     assert abs(float(T.grad) - ref) <= tol + 1e-3 * abs(ref), (float(T.grad), ref)
+    # against the GPU's own Jacobian and value-path gradient
+    _, _, dt = _capi.dtw_forward_marginals(c.to(cuda), None, 0.8)
+    Jg = _capi.dtw_param_jacobian(c.to(cuda), None, 0.8)
+    dot_consistent(T.grad, Jg, W, 0.25 * float(dt.double().sum()), "dtw T")
+    dot_consistent(gt, Jg, W, 0.0, "dtw backward_full T")

@@ -18,6 +18,7 @@ import pytest
 import torch
 
 import _capi
+from _parity import close_entrywise, dot_consistent
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -38,10 +39,7 @@ def parts(monkeypatch):
 
 
 def _close(gpu, ref, what, extra=0.0):
-    gpu = gpu.detach().cpu().numpy() if torch.is_tensor(gpu) else np.asarray(gpu)
-    tol = ATOL * max(1.0, float(np.abs(ref).max(initial=0.0))) + extra
-    err = float(np.abs(gpu - ref).max(initial=0.0))
-    assert err <= tol, f"{what}: max |gpu - ref| = {err:.3e} > {tol:.3e}"
+    close_entrywise(gpu, ref, what, extra, ATOL)
 
 
 def _jacobian_ref(s, ptype, gap, T, lengths=None):
@@ -174,6 +172,11 @@ def test_nw_marginal_path_autograd(cuda):
         tol = (ATOL * max(1.0, np.abs(J).max()) + allow) * float(np.abs(W.numpy()).sum()) \
             + 1e-3 * abs(ref)
         assert abs(float(g.grad) - ref) <= tol, (p, float(g.grad), ref, tol)
+    # the same gradients against the GPU's own Jacobians and value-path gradients
+    _, _, dg, dt = _capi.nw_forward_marginals(s.to(cuda), None, -1.0, 0.8)
+    for p, g, dv in ((0, gap, dg), (1, T, dt)):
+        Jg = _capi.nw_param_jacobian(s.to(cuda), p, None, -1.0, 0.8)
+        dot_consistent(g.grad, Jg, W, 0.5 * float(dv.double().sum()), f"nw param {p}")
     # float parameters: the scores gradient alone, equal to the tensor-parameter one
     x2 = s.to(cuda).requires_grad_(True)
     r2 = d2p_amd.soft_nw(x2, gap=-1.0, temperature=0.8)

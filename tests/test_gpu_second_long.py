@@ -16,6 +16,7 @@ import pytest
 import torch
 
 import _capi
+from _parity import check_vs_exact as _check
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -26,12 +27,6 @@ def _seeded(seed, shape):
     return torch.randn(shape, generator=g, dtype=torch.float32)
 
 
-def _check(gpu, exact, ref32, what):
-    gpu = gpu.detach().cpu().numpy().astype(np.float64)
-    e_gpu = float(np.abs(gpu - exact).max())
-    e_ref = float(np.abs(ref32.astype(np.float64) - exact).max())
-    tol = max(1e-4 * max(1.0, float(np.abs(exact).max())), 2.0 * e_ref)
-    assert e_gpu <= tol, f"{what}: |gpu - exact| {e_gpu:.3e} > {tol:.3e} (fp32 reference {e_ref:.3e})"
 
 
 @pytest.mark.parametrize("L", [1000, 1600])

@@ -22,6 +22,7 @@ import pytest
 import torch
 
 import _capi
+from _parity import close_entrywise, dot_consistent
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -59,10 +60,7 @@ def _noise_move(k, s, ptype, go, ge, T, lengths, J):
 
 
 def _close(gpu, ref, what, extra=0.0):
-    gpu = gpu.detach().cpu().numpy() if torch.is_tensor(gpu) else np.asarray(gpu)
-    tol = ATOL * max(1.0, float(np.abs(ref).max())) + extra
-    err = float(np.abs(gpu - ref).max())
-    assert err <= tol, f"{what}: max |gpu - ref| = {err:.3e} > {tol:.3e}"
+    close_entrywise(gpu, ref, what, extra, ATOL)
 
 
 CASES = [
@@ -181,6 +179,11 @@ def test_swa_marginal_path_autograd(cuda):
         tol = (1e-4 * max(1.0, np.abs(J).max()) + allow) * float(np.abs(W.numpy()).sum()) \
             + 1e-3 * abs(ref)
         assert abs(float(g.grad) - ref) <= tol, (NAMES[p], float(g.grad), ref, tol)
+    # the same gradients against the GPU's own Jacobians and value-path gradients
+    _, _, d_o, d_e, d_t = _capi.swa_forward_marginals(s.to(cuda), None, -2.0, -0.5, 0.8)
+    for p, g, dv in ((0, go, d_o), (1, ge, d_e), (2, T, d_t)):
+        Jg = _capi.swa_param_jacobian(s.to(cuda), p, None, -2.0, -0.5, 0.8)
+        dot_consistent(g.grad, Jg, W, 0.5 * float(dv.double().sum()), f"affine {NAMES[p]}")
 
 
 def test_swa_marginal_path_float_params(cuda):

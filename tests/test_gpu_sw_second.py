@@ -25,6 +25,7 @@ import pytest
 import torch
 
 import _capi
+from _parity import close_entrywise, dot_consistent
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -61,10 +62,7 @@ def _noise_move(k, s, ptype, gap, T, lengths, J):
 
 
 def _close(gpu, ref, what, extra=0.0):
-    gpu = gpu.detach().cpu().numpy() if torch.is_tensor(gpu) else np.asarray(gpu)
-    tol = ATOL * max(1.0, float(np.abs(ref).max())) + extra
-    err = float(np.abs(gpu - ref).max())
-    assert err <= tol, f"{what}: max |gpu - ref| = {err:.3e} > {tol:.3e}"
+    close_entrywise(gpu, ref, what, extra, ATOL)
 
 
 CASES = [
@@ -171,3 +169,8 @@ def test_sw_marginal_path_autograd(cuda):
         ref = float((J.astype(np.float64) * W.numpy()).sum() + 0.5 * rv.sum())
         tol = (1e-4 * max(1.0, np.abs(J).max()) + allow) * float(np.abs(W.numpy()).sum()) + 1e-3 * abs(ref)
         assert abs(float(g.grad) - ref) <= tol, (p, float(g.grad), ref, tol)
+    # the same gradients against the GPU's own Jacobians and value-path gradients
+    _, _, dg, dt = _capi.sw_forward_marginals(s.to(cuda), None, -1.0, 0.8)
+    for p, g, dv in ((0, gap, dg), (1, T, dt)):
+        Jg = _capi.sw_param_jacobian(s.to(cuda), p, None, -1.0, 0.8)
+        dot_consistent(g.grad, Jg, W, 0.5 * float(dv.double().sum()), f"sw param {p}")
