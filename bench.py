@@ -24,9 +24,12 @@ Prints one JSON line with:
     rocprofv3 --pmc (FETCH_SIZE x2 calibration + WRITE_SIZE), read from
     profiles/<kernel>_<config>_pmc.md when that summary exists;
   * ``step_roofline``: the whole step at its algorithmic bytes;
-  * ``valu``: VALUBusy of the dominant kernel measured with rocprofv3 SQ counters,
-    read from profiles/sw_<config>_valu.md when that summary exists (the sweeps
-    are bound by their per-step dependency chain, not by HBM);
+  * ``valu``: VALUBusy of the sweeps measured with rocprofv3 SQ counters, read
+    from profiles/<family>_<config>_valu.md when that summary exists (the sweeps
+    are bound by their per-step dependency chain, not by HBM), and the VALU-bound
+    cells/s derived from it: cells / (kernel time x VALUBusy) for the dominant
+    kernel, and for the step with every other kernel at the better of that figure
+    and its HBM roofline;
   * ``cpu_baseline``: the reference's own CPU kernels (oracle/_ref, built from
     the reference sources; else the C restatement) run in the reference's autograd
     call sequence on up to 16 host cores, on the configuration's full batch: the
@@ -259,10 +262,11 @@ def measured_traffic(kernel, config):
 
 
 def measured_valu(kernel, config):
-    """VALUBusy (%) of a kernel from a committed rocprofv3 SQ-counter summary, if
+    """VALUBusy (%) of each kernel from a committed rocprofv3 SQ-counter summary,
+    profiles/<family>_<config>_valu.md (family = the kernel's prefix, sw or swa), if
     present: the table row ``| VALUBusy (%) | ... |`` under a header naming each
-    kernel in backticks."""
-    path = os.path.join(ROOT, "profiles", f"sw_{config}_valu.md")
+    kernel in backticks.  Returns {kernel short name: percent} or None."""
+    path = os.path.join(ROOT, "profiles", f"{kernel.split('_')[0]}_{config}_valu.md")
     if not os.path.exists(path):
         return None
     head, busy = None, None
@@ -276,11 +280,33 @@ def measured_valu(kernel, config):
             busy = cells
     if head is None or busy is None:
         return None
-    for name, val in zip(head, busy):
-        if name.strip("`").startswith(kernel):
-            return {"kernel": kernel, "valu_busy_pct": float(val),
-                    "source": os.path.relpath(path, ROOT)}
-    return None
+    out = {}
+    for name, val in zip(head[1:], busy[1:]):
+        short = re.sub(r"_kernel.*$", "", name.strip("`").split("::")[-1])
+        out[short] = float(val)
+    return {"busy_pct": out, "source": os.path.relpath(path, ROOT)}
+
+
+def valu_bound(valu, kstats, cfg, dominant):
+    """The rate each sweep would reach at 100% VALUBusy with the same instruction
+    stream (its measured time x VALUBusy), for the dominant kernel and for the step,
+    where a kernel with no VALU figure (or one that is HBM-bound first) counts at
+    its HBM roofline (algorithmic bytes / peak)."""
+    if valu is None or dominant not in valu["busy_pct"]:
+        return None
+    busy = valu["busy_pct"]
+    t_dom = kstats[dominant]["avg_ms"] * busy[dominant] / 100.0
+    step_ms = 0.0
+    for k, algo in cfg["algo_kernel"].items():
+        if k not in kstats:
+            continue
+        hbm_ms = algo / (HBM_PEAK_GBS * 1e9) * 1e3
+        v_ms = kstats[k]["avg_ms"] * busy[k] / 100.0 if k in busy else 0.0
+        step_ms += max(hbm_ms, v_ms) * kstats[k]["launches"] / max(1, kstats[dominant]["launches"])
+    return {"kernel": dominant, "valu_busy_pct": busy[dominant],
+            "kernel_valu_bound_cells_per_s": cfg["cells"] / (t_dom * 1e-3),
+            "step_valu_bound_cells_per_s": cfg["cells"] / (step_ms * 1e-3),
+            "busy_pct": busy, "source": valu["source"]}
 
 
 def cpu_baseline_config(cfg, max_elems):
@@ -499,7 +525,7 @@ def main():
                      "avg_launch_ms": d["avg_ms"]},
         "step_roofline": {"algo_bytes_per_step": cfg["algo_step"], "achieved": step_gbs,
                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": step_gbs / HBM_PEAK_GBS},
-        "valu": measured_valu(dominant, cfg["name"]),
+        "valu": valu_bound(measured_valu(dominant, cfg["name"]), kstats, cfg, dominant),
         "kernels_ms": {k: round(v["avg_ms"], 5) for k, v in kstats.items()},
     }
     if not args.no_cpu_baseline:
