@@ -43,6 +43,12 @@ __device__ __forceinline__ float lse2(float a, float b, float c, float tl) {
     return m + tl * fast_log2(fast_exp2((a - m) * c) + fast_exp2((b - m) * c));
 }
 
+__device__ __forceinline__ float lse3(float a, float b, float x, float c, float tl) {
+    const float m = fmaxf(fmaxf(a, b), x);
+    const float z = (fast_exp2((a - m) * c) + fast_exp2((b - m) * c)) + fast_exp2((x - m) * c);
+    return m + tl * fast_log2(z);
+}
+
 __device__ __forceinline__ float lse4(float a, float b, float x, float y, float c, float tl) {
     const float m = fmaxf(fmaxf(a, b), fmaxf(x, y));
     const float z = ((fast_exp2((a - m) * c) + fast_exp2((b - m) * c)) + fast_exp2((x - m) * c)) +
@@ -50,6 +56,14 @@ __device__ __forceinline__ float lse4(float a, float b, float x, float y, float 
     return m + tl * fast_log2(z);
 }
 
+// NWA: global alignment with affine gaps (soft Needleman-Wunsch,
+// /root/reference/src/nw_affine/kernels_cpu.cpp:100-187): M = s + LSE(M, I, D) of
+// the diagonal, I = LSE(M + open, I + ext, D + open) of the cell above, D = LSE(M +
+// open, I + open, D + ext) of the cell to the left; the boundary is M[0,0] = 0,
+// I[i,0] = open + (i-1) ext, D[0,j] = open + (j-1) ext (NINF elsewhere), and the
+// value is LSE(M, I, D) of the terminal cell (L1, L2).  The cells left of column 0
+// hold the row's boundary in the tables; row 0 is generated in registers.
+template <bool NWA = false>
 __global__ void __launch_bounds__(NW * 64)
 swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                    float* __restrict__ alpha_sk, float* __restrict__ brow,
@@ -61,6 +75,7 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red_m[NW], red_z[NW];
+    __shared__ float term[3];     // NWA: (M, I, D) of the terminal cell
     // part of the element as in the linear forward: the first stripe of a part > 0
     // reads the previous part's last rows (M, I, D) from brow
     int b, part;
@@ -83,6 +98,7 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
 
     if (lane == 0) prog[wave] = -1;
     if (G == 1 && threadIdx.x == 0) *st = 0;              // G > 1: reset before the launch
+    if (NWA && threadIdx.x < 3) term[threadIdx.x] = kNINF;
     __syncthreads();
 
     const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
@@ -117,11 +133,14 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         const bool x_in = l == 0 && part > 0;        // rows above from the previous part
         const bool x_out = l == NL - 1 && has_next;  // last rows feed the next part
         int seen = -1;       // chunks of the previous part known to be complete
-        // steps t < 0 hold the column-0 boundary (NINF), read by the reverse sweep
+        // NWA: I of this lane's row (i0 + lane + 1) at column 0
+        const float bndI = (NWA && i0 + lane < L1) ? go + (float)(i0 + lane) * ge : kNINF;
+        // steps t < 0 hold the column-0 boundary (NINF; NWA: I = bndI), read by the
+        // reverse sweep
 #pragma unroll
         for (int t = -APAD; t < 0; ++t) {
             lane_store(out + t * 64, ul4, kNINF);
-            lane_store(out + PLANE + t * 64, ul4, kNINF);
+            lane_store(out + PLANE + t * 64, ul4, bndI);
             lane_store(out + 2 * PLANE + t * 64, ul4, kNINF);
         }
         wave_lds_sync();   // the previous stripe's tile reads are complete
@@ -142,8 +161,13 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             issue_rows(0);
         }
         dma_tile<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
-        float cM = kNINF, cI = kNINF, cD = kNINF;      // this lane's previous step
+        float cM = kNINF, cI = bndI, cD = kNINF;       // this lane's previous step
         float pM = kNINF, pI = kNINF, pD = kNINF;      // up values of the previous step
+        if (NWA && lane == 0) {
+            // lane 0's first diagonal: (i0, 0), the start cell M[0,0] = 0 or I's boundary
+            if (s == 0) pM = 0.0f;
+            else pI = go + (float)(i0 - 1) * ge;
+        }
 
         for (int k = 0; k < nch; ++k) {
             const int t0 = k * P;
@@ -160,8 +184,10 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             float sv[P], aM[P], aI[P], aD[P];
 #pragma unroll
             for (int u = 0; u < P; ++u) sv[u] = tile[tbase + u];
-            // lane 0's up values: column t0+j sits in lane j
+            // lane 0's up values: column t0+j sits in lane j (NWA, first stripe: row 0,
+            // where only D[0, t0+j+1] = open + (t0+j) ext is finite)
             float rM = kNINF, rI = kNINF, rD = kNINF;
+            if (NWA && s == 0 && lane < P) rD = go + (float)(t0 + lane) * ge;
             if (s > 0 && lane < P) {
                 if (x_in) {
                     const float* rb = rbufs + (k & 1) * 3 * 64;
@@ -204,13 +230,27 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 pD = uD;
                 const float sc = sv[u];
                 // out-of-table neighbours are NINF: no i>1 / j>1 guards are needed
-                const float M = lse4(dM + sc, dI + sc, dD + sc, sc, c, tl);
-                const float I = lse2(uM + go, uI + ge, c, tl);
-                const float D = lse2(cM + go, cD + ge, c, tl);
+                float M, I, D;
+                if (NWA) {
+                    M = sc + lse3(dM, dI, dD, c, tl);
+                    I = lse3(uM + go, uI + ge, uD + go, c, tl);
+                    D = lse3(cM + go, cI + go, cD + ge, c, tl);
+                } else {
+                    M = lse4(dM + sc, dI + sc, dD + sc, sc, c, tl);
+                    I = lse2(uM + go, uI + ge, c, tl);
+                    D = lse2(cM + go, cD + ge, c, tl);
+                }
                 const bool ok = FULL || (unsigned)(t - lane) < (unsigned)L2eff;
+                // NWA: the cells left of column 0 keep the row's boundary
+                const bool left = NWA && !FULL && t < lane;
                 cM = ok ? M : kNINF;
-                cI = ok ? I : kNINF;
+                cI = ok ? I : (left ? bndI : kNINF);
                 cD = ok ? D : kNINF;
+                if (NWA && ok && i0 + lane == L1 - 1 && t - lane == L2 - 1) {
+                    term[0] = M;
+                    term[1] = I;
+                    term[2] = D;
+                }
                 lane_store(outc + u * 64, ul4, cM);
                 lane_store(outc + PLANE + u * 64, ul4, cI);
                 lane_store(outc + 2 * PLANE + u * 64, ul4, cD);
@@ -222,9 +262,11 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             };
             if (i0 + 63 < L1 && t0 >= 63 && t0 + P <= L2) steps(std::true_type{});
             else steps(std::false_type{});
-            acc.add_block<P>(aM, c);
-            acc.add_block<P>(aI, c);
-            acc.add_block<P>(aD, c);
+            if (!NWA) {
+                acc.add_block<P>(aM, c);
+                acc.add_block<P>(aI, c);
+                acc.add_block<P>(aD, c);
+            }
             // the stripe's last row by step, per plane: three store instructions
             wave_lds_sync();
             if (lane < P) {
@@ -254,6 +296,21 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         }
     }
 
+    if (NWA) {
+        // the value: the terminal cell, written by the part that owns the last stripe;
+        // an element without cells is its boundary cell (L1, L2)
+        __syncthreads();
+        const bool owner = NS > 0 ? (NL > 0 && s_begin + NL == NS) : part == 0;
+        if (threadIdx.x == 0 && owner) {
+            float v;
+            if (NS > 0) v = lse3(term[0], term[1], term[2], c, tl);
+            else if (L1 > 0) v = go + (float)(L1 - 1) * ge;
+            else if (L2 > 0) v = go + (float)(L2 - 1) * ge;
+            else v = 0.0f;
+            partition[b] = v;
+        }
+        return;
+    }
     // partition: merge lanes, waves, and the cell M[0,0] = 0
     wave_merge_lse(acc, c);
     if (lane == 0) { red_m[wave] = acc.m; red_z[wave] = acc.z; }
@@ -272,6 +329,14 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     }
 }
 
+// NWA: global alignment (/root/reference/src/nw_affine/kernels_cpu.cpp:193-347): beta
+// starts at the terminal cell only, with the weights of its three states; every state
+// has three candidates (I and D also take D above / I to the left with an open), so
+// the up and left flows reach all three states; a state passes flow only when its
+// beta exceeds 1e-20; the flows into column 0 (I[i,0]) and row 0 (D[0,j]) add the
+// boundary's own open and (i-1) or (j-1) extends to the parameter gradients.
+// The second flow ring carries (diagonal D, up D) pairs instead of the diagonal D.
+template <bool NWA = false>
 __global__ void __launch_bounds__(NW * 64)
 swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                     const float* __restrict__ alpha_sk, const float* __restrict__ brow,
@@ -303,20 +368,23 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
     constexpr int RROW = AROWS + 3 * P * 64;        // 3 planes x 64
     constexpr int OTILE = RROW + 3 * 64;
     constexpr int FB4 = OTILE + Tile::FLOATS;       // flows from the part below: float4s
-    constexpr int FB1 = FB4 + 64;                   // ... and the diagonal D flows
-    constexpr int WFLOATS = FB1 + 64;
+    constexpr int FB1 = FB4 + 64;                   // ... and the diagonal D flows (NWA:
+    constexpr int WFLOATS = FB1 + 64;               // (diagonal D, up D) pairs)
     static_assert(4 * P + 4 <= 64, "boundary flows fit their buffer");
+    using F1 = std::conditional_t<NWA, float2, float>;   // second ring entry
     float* wbuf = smem + wave * WFLOATS;
     float* otile = wbuf + OTILE;
     __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
                                   // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
-    // rings [NW][R]: (up M, up I, diag M, diag I) and diag D, from lane 0 upward
+    // rings [NW][R]: (up M, up I, diag M, diag I) and diag D (NWA: (diag D, up D)),
+    // from lane 0 upward
     float4* ring4 = reinterpret_cast<float4*>(smem + NW * WFLOATS);
-    float* ring1 = reinterpret_cast<float*>(ring4 + NW * R);
+    F1* ring1 = reinterpret_cast<F1*>(ring4 + NW * R);
     float4* sink4 = reinterpret_cast<float4*>(ring1 + NW * R) + wave * (64 + P);
-    float* sink1 = reinterpret_cast<float*>(reinterpret_cast<float4*>(ring1 + NW * R) +
-                                            NW * (64 + P)) + wave * (64 + P);
+    F1* sink1 = reinterpret_cast<F1*>(reinterpret_cast<float4*>(ring1 + NW * R) +
+                                      NW * (64 + P)) + wave * (64 + P);
+    F1* flowsF = reinterpret_cast<F1*>(flows1);
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
 
@@ -356,9 +424,9 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
         const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * 3 * PLANE;   // M at step -APAD
         const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * 3 * NT;
         const float4* r4_in = ring_from(ring4, q, R);
-        const float* r1_in = ring_from(ring1, q, R);
+        const F1* r1_in = ring_from(ring1, q, R);
         float4* r4_out = ring_of(ring4, q, R);
-        float* r1_out = ring_of(ring1, q, R);
+        F1* r1_out = ring_of(ring1, q, R);
         const bool x_in = q == 0 && has_next;             // flows from the part below
         const bool x_out = q == NL - 1 && part > 0;       // flows to the part above
         const bool below = q > 0 || x_in;
@@ -367,7 +435,7 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
         const size_t fo = ((size_t)b * NSmax + s) * NT;
         const size_t fi = ((size_t)b * NSmax + (x_in ? s + 1 : s)) * NT;
         const float* f4_in = reinterpret_cast<const float*>(flows4 + fi);
-        const float* f1_in = flows1 + fi;
+        const float* f1_in = reinterpret_cast<const float*>(flowsF + fi);
         int seen = -1;       // chunks of the part below known to be complete
 
         // Loads of chunk k (t_hi = nsteps-1-kP): the score tile, P alpha rows per plane
@@ -394,7 +462,10 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                                            (nsteps - 1) * 4 + 3) * 4u;
                 uint32_t l = in_lds + FB4 * 4;
                 lds_dma_dword_sys<0>(f4_in, o, l, 0u);
-                o = (uint32_t)min(k * P + 62 + min(lane, P), nsteps - 1) * 4u;
+                // NWA: float f of the (diag D, up D) pairs from slot kP+62 in lane f
+                o = NWA ? (uint32_t)min((k * P + 62) * 2 + min(lane, 2 * P + 3),
+                                        (nsteps - 1) * 2 + 1) * 4u
+                        : (uint32_t)min(k * P + 62 + min(lane, P), nsteps - 1) * 4u;
                 l = in_lds + FB1 * 4;
                 lds_dma_dword_sys<0>(f1_in, o, l, 0u);
             }
@@ -416,9 +487,15 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
         wave_lds_sync();   // the previous stripe's buffer reads are complete
         if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
         issue_chunk(0);
+        // NWA: the terminal cell's step on this lane; I[i,0] of this lane's row and of
+        // the row above count (i-1) and (i-2) extends; row 0 (first stripe, lane 0)
+        // counts the column's
+        const int term_step = (NWA && i0 + lane == L1 - 1) ? L2 - 1 + lane : -1000000;
+        const float ext_left = (float)(i0 + lane), ext_diag = (float)(i0 + lane - 1);
+        const bool top = NWA && s == 0 && lane == 0;
         // successor contributions waiting for this lane's next steps
-        float lM = 0.0f, lD = 0.0f;                              // from (i, j+1)
-        float uM = 0.0f, uI = 0.0f;                              // from (i+1, j)
+        float lM = 0.0f, lI = 0.0f, lD = 0.0f;                   // from (i, j+1)
+        float uM = 0.0f, uI = 0.0f, uD = 0.0f;                   // from (i+1, j)
         float dM = 0.0f, dI = 0.0f, dD = 0.0f;                   // from (i+1, j+1)
         float dM2 = 0.0f, dI2 = 0.0f, dD2 = 0.0f;                // ... one step later
 
@@ -453,9 +530,15 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
             float bM = row_ok ? wbuf[RROW + lane] : kNINF;
             float bI = row_ok ? wbuf[RROW + 64 + lane] : kNINF;
             float bD = row_ok ? wbuf[RROW + 128 + lane] : kNINF;
+            if (NWA && s == 0 && lane <= P) {
+                // row 0 at column t_hi - lane (0-based; -1 is the start cell M[0,0] = 0)
+                const int c0 = t_hi - lane;
+                bM = c0 == -1 ? 0.0f : kNINF;
+                bD = c0 >= 0 ? go + (float)c0 * ge : kNINF;
+            }
             // Contributions from the stripe below for lane 63 (see the linear kernel):
             // lane 63-j holds step j; up flows from slot kP+j+63, diagonal from kP+j+62.
-            float qUM = 0.0f, qUI = 0.0f, qDM = 0.0f, qDI = 0.0f, qDD = 0.0f;
+            float qUM = 0.0f, qUI = 0.0f, qUD = 0.0f, qDM = 0.0f, qDI = 0.0f, qDD = 0.0f;
             if (below && lane >= 64 - P) {
                 const int j = 63 - lane;
                 if (x_in) {
@@ -463,16 +546,27 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                     qUI = wbuf[FB4 + 4 * (j + 1) + 1];
                     qDM = wbuf[FB4 + 4 * j + 2];
                     qDI = wbuf[FB4 + 4 * j + 3];
-                    qDD = wbuf[FB1 + j];
+                    if (NWA) {
+                        qDD = wbuf[FB1 + 2 * j];
+                        qUD = wbuf[FB1 + 2 * (j + 1) + 1];
+                    } else {
+                        qDD = wbuf[FB1 + j];
+                    }
                 } else {
-                    const float4 ru = r4_in[ring_index(k * P + j + 63, R)];
+                    const int iu = ring_index(k * P + j + 63, R);
+                    const float4 ru = r4_in[iu];
                     const int id = ring_index(k * P + j + 62, R);
                     const float4 rd = r4_in[id];
                     qUM = ru.x;
                     qUI = ru.y;
                     qDM = rd.z;
                     qDI = rd.w;
-                    qDD = r1_in[id];
+                    if constexpr (NWA) {
+                        qDD = r1_in[id].x;
+                        qUD = r1_in[iu].y;
+                    } else {
+                        qDD = r1_in[id];
+                    }
                 }
             }
             wave_lds_sync();   // every read of the input buffer is complete
@@ -485,9 +579,11 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             float4* pub4 = (lane == 0) ? r4_out + ring_index(k * P, R) : sink4 + lane;
-            float* pub1 = (lane == 0) ? r1_out + ring_index(k * P, R) : sink1 + lane;
+            F1* pub1 = (lane == 0) ? r1_out + ring_index(k * P, R) : sink1 + lane;
             // lane 63 starts the chunk with the ring's values for steps 0 and 1
             {
+                const float u0D = NWA ? lane_bcast(qUD, 63) : 0.0f;
+                if (NWA && lane == 63) uD = u0D;
                 const float u0M = lane_bcast(qUM, 63), u0I = lane_bcast(qUI, 63);
                 const float d0M = lane_bcast(qDM, 63), d0I = lane_bcast(qDI, 63),
                             d0D = lane_bcast(qDD, 63);
@@ -517,53 +613,94 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 const float nbM = wave_shl1(bM), nbI = wave_shl1(bI),
                             nbD = wave_shl1(bD);
                 const float upM = wave_shr1_or(AM[u + 1], bM), upI = wave_shr1_or(AI[u + 1], bI);
+                const float upD = NWA ? wave_shr1_or(AD[u + 1], bD) : kNINF;
                 const float dgM = wave_shr1_or(AM[u + 2], nbM), dgI = wave_shr1_or(AI[u + 2], nbI),
                             dgD = wave_shr1_or(AD[u + 2], nbD);
                 bM = nbM;
                 bI = nbI;
                 bD = nbD;
-                const float lfM = AM[u + 1], lfD = AD[u + 1];
-                // M: diagonal + start weights
-                const float v0 = dgM + sc, v1 = dgI + sc, v2 = dgD + sc;
-                const float m4 = fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
+                const float lfM = AM[u + 1], lfI = AI[u + 1], lfD = AD[u + 1];
+                // M: diagonal + start weights (NWA: the diagonal only)
+                const float v0 = NWA ? dgM : dgM + sc, v1 = NWA ? dgI : dgI + sc,
+                            v2 = NWA ? dgD : dgD + sc;
+                const float m4 = NWA ? fmaxf(fmaxf(v0, v1), v2) : fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
                 const float e0 = fast_exp2((v0 - m4) * c), e1 = fast_exp2((v1 - m4) * c);
-                const float e2 = fast_exp2((v2 - m4) * c), e3 = fast_exp2((sc - m4) * c);
-                const float esum = ((e0 + e1) + e2) + e3;
-                // I: open from M above, extend from I above
-                const float i0v = upM + go, i1v = upI + ge;
-                const float mi = fmaxf(i0v, i1v);
+                const float e2 = fast_exp2((v2 - m4) * c);
+                const float e3 = NWA ? 0.0f : fast_exp2((sc - m4) * c);
+                const float esum = NWA ? (e0 + e1) + e2 : ((e0 + e1) + e2) + e3;
+                // I: open from M above, extend from I above (NWA: open from D above)
+                const float i0v = upM + go, i1v = upI + ge, i2v = upD + go;
+                const float mi = NWA ? fmaxf(fmaxf(i0v, i1v), i2v) : fmaxf(i0v, i1v);
                 const float f0 = fast_exp2((i0v - mi) * c), f1 = fast_exp2((i1v - mi) * c);
-                // D: open from M left, extend from D left
-                const float d0v = lfM + go, d1v = lfD + ge;
-                const float md = fmaxf(d0v, d1v);
+                const float f2 = NWA ? fast_exp2((i2v - mi) * c) : 0.0f;
+                // D: open from M left, extend from D left (NWA: open from I left)
+                const float d0v = lfM + go, d1v = lfD + ge, d2v = lfI + go;
+                const float md = NWA ? fmaxf(fmaxf(d0v, d1v), d2v) : fmaxf(d0v, d1v);
                 const float g0 = fast_exp2((d0v - md) * c), g1 = fast_exp2((d1v - md) * c);
-                // betas in the reference's accumulation order
-                float lp;
-                lp = (AM[u] - S) * c;   // subtract first: exact for nearby values
-                const float initM = fast_exp2(lp < 0.0f ? lp : 0.0f);
-                lp = (AI[u] - S) * c;
-                const float initI = fast_exp2(lp < 0.0f ? lp : 0.0f);
-                lp = (AD[u] - S) * c;
-                const float initD = fast_exp2(lp < 0.0f ? lp : 0.0f);
+                const float g2 = NWA ? fast_exp2((d2v - md) * c) : 0.0f;
+                // betas in the reference's accumulation order (NWA: the terminal cell's
+                // softmax weights over its three states start the recursion)
+                float initM, initI, initD;
+                if (NWA) {
+                    initM = initI = initD = 0.0f;
+                    if (t == term_step) {
+                        const float m = fmaxf(fmaxf(AM[u], AI[u]), AD[u]);
+                        const float eM = fast_exp2((AM[u] - m) * c), eI = fast_exp2((AI[u] - m) * c);
+                        const float eD = fast_exp2((AD[u] - m) * c);
+                        const float r = fast_rcp((eM + eI) + eD);
+                        initM = eM * r;
+                        initI = eI * r;
+                        initD = eD * r;
+                    }
+                } else {
+                    float lp;
+                    lp = (AM[u] - S) * c;   // subtract first: exact for nearby values
+                    initM = fast_exp2(lp < 0.0f ? lp : 0.0f);
+                    lp = (AI[u] - S) * c;
+                    initI = fast_exp2(lp < 0.0f ? lp : 0.0f);
+                    lp = (AD[u] - S) * c;
+                    initD = fast_exp2(lp < 0.0f ? lp : 0.0f);
+                }
                 const float betaM = ((initM + dM) + lM) + uM;
-                const float betaI = (initI + dI) + uI;
-                const float betaD = (initD + dD) + lD;
-                // skip inf / NaN betas like the reference; cells outside the element
-                const float brM = (ok && betaM <= 3.0e38f) ? betaM * fast_rcp(esum) : 0.0f;
-                const float brI = (ok && betaI <= 3.0e38f) ? betaI * fast_rcp(f0 + f1) : 0.0f;
-                const float brD = (ok && betaD <= 3.0e38f) ? betaD * fast_rcp(g0 + g1) : 0.0f;
+                const float betaI = NWA ? ((initI + dI) + uI) + lI : (initI + dI) + uI;
+                const float betaD = NWA ? ((initD + dD) + lD) + uD : (initD + dD) + lD;
+                // skip inf / NaN betas like the reference; cells outside the element;
+                // NWA: betas at most 1e-20 pass nothing
+                const float lo = NWA ? 1e-20f : -1.0f;
+                const float brM = (ok && betaM > lo && betaM <= 3.0e38f) ? betaM * fast_rcp(esum) : 0.0f;
+                const float brI = (ok && betaI > lo && betaI <= 3.0e38f)
+                                      ? betaI * fast_rcp(NWA ? (f0 + f1) + f2 : f0 + f1) : 0.0f;
+                const float brD = (ok && betaD > lo && betaD <= 3.0e38f)
+                                      ? betaD * fast_rcp(NWA ? (g0 + g1) + g2 : g0 + g1) : 0.0f;
                 const float pv = brM * esum;
                 otile[tbase + u] = pv;
                 p_acc += pv * sc;
-                const float oUM = brI * f0, oUI = brI * f1;            // to (i-1, j)
-                const float oLM = brD * g0, oLD = brD * g1;            // to (i, j-1)
+                const float oUM = brI * f0, oUI = brI * f1, oUD = brI * f2;   // to (i-1, j)
+                const float oLM = brD * g0, oLD = brD * g1, oLI = brD * g2;   // to (i, j-1)
                 const float oDM = brM * e0, oDI = brM * e1, oDD = brM * e2;   // to (i-1, j-1)
                 g_open += oUM;
                 g_open += oLM;
                 g_ext += oUI;
                 g_ext += oLD;
+                if (NWA) {
+                    g_open += oUD;
+                    g_open += oLI;
+                    // the boundary cells' own open and extends: I[i,0] (left from column
+                    // 0, diagonal from column 0 into the row above; no FULL chunk has a
+                    // column 0) and D[0,j] (up and diagonal flows of the first row)
+                    const int col = t - lane;
+                    if (!FULL && col == 0) {
+                        g_open += oLI + oDI;
+                        g_ext += oLI * ext_left + oDI * ext_diag;
+                    }
+                    if (top) {
+                        g_open += oUD + oDD;
+                        g_ext += oUD * (float)col + oDD * (float)(col - 1);
+                    }
+                }
                 pub4[u] = make_float4(oUM, oUI, oDM, oDI);
-                pub1[u] = oDD;
+                if constexpr (NWA) pub1[u] = make_float2(oDD, oUD);
+                else pub1[u] = oDD;
                 // successor contributions for the next steps; lane 63 takes the ring
                 qUM = wave_shr1(qUM);
                 qUI = wave_shr1(qUI);
@@ -571,6 +708,11 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 lD = oLD;
                 uM = wave_shl1_or(oUM, qUM);
                 uI = wave_shl1_or(oUI, qUI);
+                if (NWA) {
+                    qUD = wave_shr1(qUD);
+                    lI = oLI;
+                    uD = wave_shl1_or(oUD, qUD);
+                }
                 dM = dM2;
                 dI = dI2;
                 dD = dD2;
@@ -582,8 +724,10 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 qDD = wave_shr1(qDD);
             }
             };
-            if (i0 + 63 < L1 && t_hi - P - 62 >= 0 && t_hi < L2) steps(std::true_type{});
-            else steps(std::false_type{});
+            if (i0 + 63 < L1 && t_hi - P - 62 >= (NWA ? 1 : 0) && t_hi < L2)
+                steps(std::true_type{});
+            else
+                steps(std::false_type{});
             wave_lds_sync();
             write_tile<P, -1>(otile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             publish(prog, wave, q * PROG_STRIDE + k + 1);
@@ -592,7 +736,8 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 if (lane < P) {
                     const int slot = ring_index(k * P, R) + lane;
                     store_sys4(flows4 + fo + k * P + lane, r4_out[slot]);
-                    store_sys(flows1 + fo + k * P + lane, r1_out[slot]);
+                    if constexpr (NWA) store_sys2(flowsF + fo + k * P + lane, r1_out[slot]);
+                    else store_sys(flows1 + fo + k * P + lane, r1_out[slot]);
                 }
                 if (k >= 2) {
                     // at least P + 3P/4 + 3 loads, 2P marginal stores and 4 flow stores
@@ -616,6 +761,11 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
     if (threadIdx.x == 0) {
         float go_s = 0.0f, ge_s = 0.0f, p = 0.0f;
         for (int w = 0; w < NW; ++w) { go_s += red_o[w]; ge_s += red_e[w]; p += red_p[w]; }
+        if (NWA && NS == 0 && part == 0 && L1 + L2 > 0) {
+            // an element without cells is its boundary cell: one open, L - 1 extends
+            go_s += 1.0f;
+            ge_s += (float)(L1 + L2 - 1);
+        }
         if (G == 1) {
             grad_open[b] = go_s;
             grad_ext[b] = ge_s;
@@ -664,11 +814,11 @@ size_t lds_forward_r(int R) {
     return (size_t)NW * (2 * 65 * PF + 2 * 3 * 64) * sizeof(float) +
            ((size_t)NW * R + NW * DUMMY) * sizeof(float4);
 }
-size_t lds_backward_r(int R) {
+size_t lds_backward_r(int R, bool nwa) {
     const size_t wfloats = 65 * PB + 3 * PB * 64 + 3 * 64 + 65 * PB + 2 * 64;
-    return (size_t)NW * wfloats * sizeof(float) +
-           (size_t)NW * R * (sizeof(float4) + sizeof(float)) +
-           (size_t)NW * (64 + PB) * (sizeof(float4) + sizeof(float));
+    const size_t f1 = nwa ? sizeof(float2) : sizeof(float);
+    return (size_t)NW * wfloats * sizeof(float) + (size_t)NW * R * (sizeof(float4) + f1) +
+           (size_t)NW * (64 + PB) * (sizeof(float4) + f1);
 }
 int ring_forward(int rows, int max_L2) { return ring_len(rows, max_L2, 256); }
 int ring_backward(int rows, int max_L2) { return ring_len(rows, max_L2, 128); }
@@ -678,8 +828,8 @@ int ring_backward(int rows, int max_L2) { return ring_len(rows, max_L2, 128); }
 int max_stripes_forward(int max_L1, int max_L2) {
     return lds_forward_r(ring_forward(max_L1, max_L2)) <= kLdsLimit ? 0 : NW;
 }
-int max_stripes_backward(int max_L1, int max_L2) {
-    return lds_backward_r(ring_backward(max_L1, max_L2)) <= kLdsLimit ? 0 : NW;
+int max_stripes_backward(int max_L1, int max_L2, bool nwa) {
+    return lds_backward_r(ring_backward(max_L1, max_L2), nwa) <= kLdsLimit ? 0 : NW;
 }
 }  // namespace
 
@@ -695,9 +845,9 @@ int check_shape(int B, int max_L1, int max_L2, float temperature) {
     return D2P_OK;
 }
 
-// The affine layout's flows area: a float4 plane, then a float plane, of
-// ws.flow_slots entries each.
-constexpr int kFlowBytes = sizeof(float4) + sizeof(float);
+// The affine layout's flows area: a float4 plane, then a float plane (global
+// alignment: a float2 plane), of ws.flow_slots entries each.
+constexpr int kFlowBytes = sizeof(float4) + sizeof(float2);
 
 Layout affine_layout(void* workspace, int B, int max_L1, int max_L2, bool split) {
     return layout(workspace, B, max_L1, max_L2, 3, split, kFlowBytes);
@@ -705,19 +855,22 @@ Layout affine_layout(void* workspace, int B, int max_L1, int max_L2, bool split)
 
 int launch_forward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                    float go, float ge, float T, const Layout& ws, float* partition,
-                   hipStream_t st) {
+                   hipStream_t st, bool nwa) {
     const int ns = (max_L1 + 63) / 64;
     const Split sp = choose_split(B, max_L1, ws, max_stripes_forward(max_L1, max_L2));
     const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
     const size_t lds = lds_forward_r(R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     if (sp.G > 1 && launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
-    D2P_HIP(hipFuncSetAttribute((const void*)swa_forward_kernel,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH("swa_forward", swa_forward_kernel, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds,
-               st, scores, lengths, ws.alpha_sk, ws.brow, partition, ws.status, ws.fflag,
-               ws.fpart, B, max_L1, max_L2, ns, go, ge, T, R, sp.G, sp.SPW, next_epoch());
-    if (sp.G > 1 && launch_partition_merge(ws, partition, B, sp.G, T, st) != D2P_OK)
+    auto kern = nwa ? swa_forward_kernel<true> : swa_forward_kernel<false>;
+    D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+    D2P_LAUNCH(nwa ? "nwa_forward" : "swa_forward", kern, dim3(split_grid(B, sp.G)),
+               dim3(NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
+               ws.status, ws.fflag, ws.fpart, B, max_L1, max_L2, ns, go, ge, T, R, sp.G, sp.SPW,
+               next_epoch());
+    // global alignment: the part owning the terminal cell writes the value itself
+    if (!nwa && sp.G > 1 && launch_partition_merge(ws, partition, B, sp.G, T, st) != D2P_OK)
         return D2P_ERR_HIP;
     D2P_HIP(hipGetLastError());
     return D2P_OK;
@@ -726,21 +879,22 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
 int launch_backward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                     float go, float ge, float T, const Layout& ws, const float* partition,
                     float* marginals, float* grad_open, float* grad_ext, float* grad_T,
-                    hipStream_t st) {
+                    hipStream_t st, bool nwa) {
     const int ns = (max_L1 + 63) / 64;
-    const Split sp = choose_split(B, max_L1, ws, max_stripes_backward(max_L1, max_L2));
+    const Split sp = choose_split(B, max_L1, ws, max_stripes_backward(max_L1, max_L2, nwa));
     const int R = ring_backward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
-    const size_t lds = lds_backward_r(R);
+    const size_t lds = lds_backward_r(R, nwa);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     float4* flows4 = reinterpret_cast<float4*>(ws.flows);
     float* flows1 = sp.G > 1 ? reinterpret_cast<float*>(flows4 + ws.flow_slots) : nullptr;
     if (sp.G > 1) D2P_TRY(launch_flag_reset(ws.bflag, B * sp.G, st));
-    D2P_HIP(hipFuncSetAttribute((const void*)swa_backward_kernel,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH("swa_backward", swa_backward_kernel, dim3(split_grid(B, sp.G)), dim3(NW * 64),
-               lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition, marginals, grad_open,
-               grad_ext, grad_T, ws.status, ws.trash, ws.bflag, flows4, flows1, ws.bpart, B,
-               max_L1, max_L2, ns, go, ge, T, R, sp.G, sp.SPW, next_epoch());
+    auto kern = nwa ? swa_backward_kernel<true> : swa_backward_kernel<false>;
+    D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+    D2P_LAUNCH(nwa ? "nwa_backward" : "swa_backward", kern, dim3(split_grid(B, sp.G)),
+               dim3(NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
+               marginals, grad_open, grad_ext, grad_T, ws.status, ws.trash, ws.bflag, flows4,
+               flows1, ws.bpart, B, max_L1, max_L2, ns, go, ge, T, R, sp.G, sp.SPW, next_epoch());
     if (sp.G > 1)
         D2P_LAUNCH("swa_grad_merge", swa_grad_merge, dim3((B + 255) / 256), dim3(256), 0, st,
                    ws.bpart, partition, grad_open, grad_ext, grad_T, B, sp.G, go, ge, T);
@@ -760,25 +914,51 @@ extern "C" size_t d2p_swa_workspace_bytes(int B, int max_L1, int max_L2) {
     return swa::affine_layout(nullptr, B, max_L1, max_L2, true).bytes;
 }
 
-extern "C" int d2p_swa_forward_marginals(const float* scores, const int* lengths, int B,
-                                         int max_L1, int max_L2, float gap_open, float gap_ext,
-                                         float temperature, float* partition, float* marginals,
-                                         float* grad_open, float* grad_ext, float* grad_T,
-                                         void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+int affine_forward_marginals(const float* scores, const int* lengths, int B, int max_L1,
+                             int max_L2, float gap_open, float gap_ext, float temperature,
+                             float* value, float* marginals, float* grad_open, float* grad_ext,
+                             float* grad_T, void* workspace, size_t workspace_bytes,
+                             void* stream, bool nwa) {
     const int rc = swa::check_shape(B, max_L1, max_L2, temperature);
     if (rc != D2P_OK) return rc;
     if (B == 0) return D2P_OK;
-    D2P_REQUIRE(scores && partition && marginals && grad_open && grad_ext && grad_T,
+    D2P_REQUIRE(scores && value && marginals && grad_open && grad_ext && grad_T,
                 "null pointer argument");
     const size_t need = d2p_swa_workspace_bytes(B, max_L1, max_L2);
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
     const wf::Layout ws = swa::affine_layout(workspace, B, max_L1, max_L2, true);
     D2P_TRY(swa::launch_forward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
-                                temperature, ws, partition, st));
+                                temperature, ws, value, st, nwa));
     D2P_TRY(swa::launch_backward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
-                                 temperature, ws, partition, marginals, grad_open, grad_ext,
-                                 grad_T, st));
+                                 temperature, ws, value, marginals, grad_open, grad_ext, grad_T,
+                                 st, nwa));
     return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr,
-                             partition, grad_open, grad_ext, grad_T, st);
+                             value, grad_open, grad_ext, grad_T, st);
+}
+}  // namespace
+
+extern "C" int d2p_swa_forward_marginals(const float* scores, const int* lengths, int B,
+                                         int max_L1, int max_L2, float gap_open, float gap_ext,
+                                         float temperature, float* partition, float* marginals,
+                                         float* grad_open, float* grad_ext, float* grad_T,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+    return affine_forward_marginals(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
+                                    temperature, partition, marginals, grad_open, grad_ext,
+                                    grad_T, workspace, workspace_bytes, stream, false);
+}
+
+extern "C" size_t d2p_nwa_workspace_bytes(int B, int max_L1, int max_L2) {
+    return d2p_swa_workspace_bytes(B, max_L1, max_L2);
+}
+
+extern "C" int d2p_nwa_forward_marginals(const float* scores, const int* lengths, int B,
+                                         int max_L1, int max_L2, float gap_open, float gap_ext,
+                                         float temperature, float* value, float* marginals,
+                                         float* grad_open, float* grad_ext, float* grad_T,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+    return affine_forward_marginals(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
+                                    temperature, value, marginals, grad_open, grad_ext, grad_T,
+                                    workspace, workspace_bytes, stream, true);
 }

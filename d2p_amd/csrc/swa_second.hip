@@ -39,9 +39,53 @@ using namespace wf;
 
 enum Mode { HVP = 0, OPEN = 1, EXT = 2, TEMP = 3 };
 
+// Softmax weights w of three candidate values v (none when all are NINF) and their
+// tangents dw_k = w_k (d_k - E_w[d]) / T for candidate tangents d; the parameter
+// modes take the differences relative to the largest candidate's tangent (the
+// weights' sum differs from 1 by an ulp or two), and the temperature adds
+// w_k (E_w[v] - v_k) / T^2.
+template <int MODE>
+__device__ __forceinline__ void softmax3_tangent(const float (&v)[3], const float (&d)[3],
+                                                 float c, float rT, float (&w)[3],
+                                                 float (&dw)[3]) {
+    const float m = fmaxf(fmaxf(v[0], v[1]), v[2]);
+    const float e0 = fast_exp2((v[0] - m) * c), e1 = fast_exp2((v[1] - m) * c);
+    const float e2 = fast_exp2((v[2] - m) * c);
+    const float r = m > kNINF ? fast_rcp((e0 + e1) + e2) : 0.0f;
+    w[0] = e0 * r;
+    w[1] = e1 * r;
+    w[2] = e2 * r;
+    if (MODE == HVP) {
+        const float E = (w[0] * d[0] + w[1] * d[1]) + w[2] * d[2];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) dw[k] = w[k] * (d[k] - E) * rT;
+    } else {
+        const float p = v[0] >= m ? d[0] : (v[1] >= m ? d[1] : d[2]);
+        const float q0 = d[0] - p, q1 = d[1] - p, q2 = d[2] - p;
+        const float E = (w[0] * q0 + w[1] * q1) + w[2] * q2;
+        dw[0] = w[0] * (q0 - E) * rT;
+        dw[1] = w[1] * (q1 - E) * rT;
+        dw[2] = w[2] * (q2 - E) * rT;
+        if (MODE == TEMP) {
+            const float rT2 = rT * rT;
+            const float p0 = v[0] - m, p1 = v[1] - m, p2 = v[2] - m;
+            const float Ev = (w[0] * p0 + w[1] * p1) + w[2] * p2;
+            dw[0] += w[0] > 0.0f ? w[0] * (Ev - p0) * rT2 : 0.0f;
+            dw[1] += w[1] > 0.0f ? w[1] * (Ev - p1) * rT2 : 0.0f;
+            dw[2] += w[2] > 0.0f ? w[2] * (Ev - p2) * rT2 : 0.0f;
+        }
+    }
+}
+
 // ------------------------------------------------------------------ tangent sweep
 
-template <int MODE, int P>
+// NWA: global alignment with affine gaps (/root/reference/src/nw_affine/kernels_cpu.cpp:
+// 353-613 and 619-1002): each state has three candidates (M: the diagonal states, no
+// start; I: M, I, D above; D: M, I, D to the left); the HVP tangent of M adds V to
+// the weighted diagonal tangents; the boundary chains I[i,0], D[0,j] carry the
+// tangents 1 (open) or i-1 / j-1 (ext).  The value's tangent is taken at the terminal
+// cell by the reverse sweep, so no per-cell sum is formed here.
+template <int MODE, int P, bool NWA = false>
 __global__ void __launch_bounds__(NW * 64)
 swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                    const int* __restrict__ lengths, const float* __restrict__ alpha_sk,
@@ -141,17 +185,26 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
             }
         };
 
+        // NWA: the boundary I[i,0] of this lane's row, its value and tangent
+        const bool rowv = NWA && i0 + lane < L1;
+        const float bndI = rowv ? go + (float)(i0 + lane) * ge : kNINF;
+        const float xbI = rowv ? (MODE == OPEN ? 1.0f : (MODE == EXT ? (float)(i0 + lane) : 0.0f))
+                               : 0.0f;
 #pragma unroll
         for (int t = -APAD; t < 0; ++t)
 #pragma unroll
-            for (int pl = 0; pl < 3; ++pl) lane_store(tout + pl * PL + t * 64, ul4, 0.0f);
+            for (int pl = 0; pl < 3; ++pl)
+                lane_store(tout + pl * PL + t * 64, ul4, pl == 1 ? xbI : 0.0f);
         wave_lds_sync();
         if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
         issue_chunk(0);
         float AM[P + 2], AI[P + 2], AD[P + 2];
-        AM[P] = AM[P + 1] = AI[P] = AI[P + 1] = AD[P] = AD[P + 1] = kNINF;
-        float cM = 0.0f, cI = 0.0f, cD = 0.0f;      // tangents at the previous step
+        AM[P] = AM[P + 1] = AD[P] = AD[P + 1] = kNINF;
+        AI[P] = AI[P + 1] = bndI;
+        float cM = 0.0f, cI = xbI, cD = 0.0f;       // tangents at the previous step
         float pM = 0.0f, pI = 0.0f, pD = 0.0f;      // their up values
+        if (NWA && lane == 0 && s > 0)   // lane 0's first diagonal: I[i0, 0]
+            pI = MODE == OPEN ? 1.0f : (MODE == EXT ? (float)(i0 - 1) : 0.0f);
 
         for (int k = 0; k < nch; ++k) {
             const int t0 = k * P;
@@ -184,6 +237,17 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
             float bI = row_ok ? buf[RR + 64 + lane] : kNINF;
             float bD = row_ok ? buf[RR + 128 + lane] : kNINF;
             float rM = 0.0f, rI = 0.0f, rD = 0.0f;
+            if (NWA && s == 0) {
+                // row 0: lane j <= P the values at column t0 - 1 + j (0-based; -1 is
+                // the start cell), lane j < P the tangents at column t0 + j
+                const int c0 = t0 - 1 + lane;
+                if (lane <= P) {
+                    bM = c0 == -1 ? 0.0f : kNINF;
+                    bD = c0 >= 0 ? go + (float)c0 * ge : kNINF;
+                }
+                if (lane < P)
+                    rD = MODE == OPEN ? 1.0f : (MODE == EXT ? (float)(t0 + lane) : 0.0f);
+            }
             if (s > 0 && lane < P) {
                 if (x_in) {
                     rM = buf[TR + lane];
@@ -219,10 +283,11 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
                 const float nbM = wave_shl1(bM), nbI = wave_shl1(bI),
                             nbD = wave_shl1(bD);
                 const float uM = wave_shr1_or(AM[u + 1], nbM), uI = wave_shr1_or(AI[u + 1], nbI);
+                const float uD = NWA ? wave_shr1_or(AD[u + 1], nbD) : kNINF;
                 bM = nbM;
                 bI = nbI;
                 bD = nbD;
-                const float lM = AM[u + 1], lD = AD[u + 1];
+                const float lM = AM[u + 1], lI = AI[u + 1], lD = AD[u + 1];
                 // tangent predecessors
                 const float tuM = wave_shr1_or(cM, rM), tuI = wave_shr1_or(cI, rI),
                             tuD = wave_shr1_or(cD, rD);
@@ -233,6 +298,62 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
                 pM = tuM;
                 pI = tuI;
                 pD = tuD;
+                float xM, xI, xD;
+                if constexpr (NWA) {
+                    const float ao = MODE == OPEN ? 1.0f : 0.0f, ae = MODE == EXT ? 1.0f : 0.0f;
+                    // M over the diagonal states
+                    const float m3 = fmaxf(fmaxf(dM, dI), dD);
+                    const float e0 = fast_exp2((dM - m3) * c), e1 = fast_exp2((dI - m3) * c);
+                    const float e2 = fast_exp2((dD - m3) * c);
+                    const float r3 = m3 > kNINF ? fast_rcp((e0 + e1) + e2) : 0.0f;
+                    // I over M + open, I + ext, D + open above
+                    const float i0v = uM + go, i1v = uI + ge, i2v = uD + go;
+                    const float mi = fmaxf(fmaxf(i0v, i1v), i2v);
+                    const float f0 = fast_exp2((i0v - mi) * c), f1 = fast_exp2((i1v - mi) * c);
+                    const float f2 = fast_exp2((i2v - mi) * c);
+                    const float ri = mi > kNINF ? fast_rcp((f0 + f1) + f2) : 0.0f;
+                    // D over M + open, D + ext, I + open to the left
+                    const float d0v = lM + go, d1v = lD + ge, d2v = lI + go;
+                    const float md = fmaxf(fmaxf(d0v, d1v), d2v);
+                    const float g0 = fast_exp2((d0v - md) * c), g1 = fast_exp2((d1v - md) * c);
+                    const float g2 = fast_exp2((d2v - md) * c);
+                    const float rd = md > kNINF ? fast_rcp((g0 + g1) + g2) : 0.0f;
+                    const float di0 = tuM + ao, di1 = tuI + ae, di2 = tuD + ao;
+                    const float dd0 = cM + ao, dd1 = cD + ae, dd2 = cI + ao;
+                    if (MODE == HVP) {
+                        xM = r3 > 0.0f ? vd + ((e0 * tdM + e1 * tdI) + e2 * tdD) * r3 : 0.0f;
+                        xI = ((f0 * di0 + f1 * di1) + f2 * di2) * ri;
+                        xD = ((g0 * dd0 + g1 * dd1) + g2 * dd2) * rd;
+                    } else {
+                        // E_w[d] as the largest candidate's tangent plus the weighted
+                        // differences (see the linear-gap kernel)
+                        const float pm = dM >= m3 ? tdM : (dI >= m3 ? tdI : tdD);
+                        xM = r3 > 0.0f
+                                 ? pm + ((e0 * (tdM - pm) + e1 * (tdI - pm)) + e2 * (tdD - pm)) * r3
+                                 : 0.0f;
+                        const float pi = i0v >= mi ? di0 : (i1v >= mi ? di1 : di2);
+                        xI = ri > 0.0f
+                                 ? pi + ((f0 * (di0 - pi) + f1 * (di1 - pi)) + f2 * (di2 - pi)) * ri
+                                 : 0.0f;
+                        const float pd = d0v >= md ? dd0 : (d1v >= md ? dd1 : dd2);
+                        xD = rd > 0.0f
+                                 ? pd + ((g0 * (dd0 - pd) + g1 * (dd1 - pd)) + g2 * (dd2 - pd)) * rd
+                                 : 0.0f;
+                        if (MODE == TEMP) {
+                            // alpha - E_w[v] per state, relative to the largest candidate
+                            // (M: alpha - s - E_w[diagonal])
+                            const float E3 =
+                                ((e0 * (dM - m3) + e1 * (dI - m3)) + e2 * (dD - m3)) * r3;
+                            const float E3i =
+                                ((f0 * (i0v - mi) + f1 * (i1v - mi)) + f2 * (i2v - mi)) * ri;
+                            const float E3d =
+                                ((g0 * (d0v - md) + g1 * (d1v - md)) + g2 * (d2v - md)) * rd;
+                            xM += r3 > 0.0f ? ((AM[u + 2] - sc - m3) - E3) * rT : 0.0f;
+                            xI += ri > 0.0f ? ((AI[u + 2] - mi) - E3i) * rT : 0.0f;
+                            xD += rd > 0.0f ? ((AD[u + 2] - md) - E3d) * rT : 0.0f;
+                        }
+                    }
+                } else {
                 // M
                 const float v0 = dM + sc, v1 = dI + sc, v2 = dD + sc;
                 const float m4 = fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
@@ -249,7 +370,6 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
                 const float md = fmaxf(d0v, d1v);
                 const float g0 = fast_exp2((d0v - md) * c), g1 = fast_exp2((d1v - md) * c);
                 const float rd = md > kNINF ? fast_rcp(g0 + g1) : 0.0f;
-                float xM, xI, xD;
                 if (MODE == HVP) {
                     xM = (((e0 * (tdM + vd) + e1 * (tdI + vd)) + e2 * (tdD + vd)) + e3 * vd) * r4;
                     xI = (f0 * tuM + f1 * tuI) * ri;
@@ -281,14 +401,15 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
                         xD += rd > 0.0f ? ((AD[u + 2] - md) - E2d) * rT : 0.0f;
                     }
                 }
+                }
                 cM = ok ? xM : 0.0f;
-                cI = ok ? xI : 0.0f;
+                cI = ok ? xI : (NWA && t < lane ? xbI : 0.0f);   // NWA: left of column 0
                 cD = ok ? xD : 0.0f;
                 lane_store(toutc + u * 64, ul4, cM);
                 lane_store(toutc + PL + u * 64, ul4, cI);
                 lane_store(toutc + 2 * PL + u * 64, ul4, cD);
                 pub[u] = make_float4(cM, cI, cD, 0.0f);
-                if (MODE == HVP) {
+                if (MODE == HVP && !NWA) {
                     float lp;
                     lp = (AM[u + 2] - S) * c;
                     sacc += fast_exp2(lp < 0.0f ? lp : 0.0f) * cM;
@@ -326,7 +447,7 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
         }
     }
 
-    if (MODE == HVP) {
+    if (MODE == HVP && !NWA) {
         sacc = wave_sum(sacc);
         if (lane == 0) red[wave] = sacc;
         __syncthreads();
@@ -341,7 +462,12 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
 
 // ------------------------------------------------------------------ reverse sweep
 
-template <int MODE, int P, bool DOT>
+// NWA: global alignment: beta and g start at the terminal cell only, beta_X = w_X and
+// g_X = w_X (x_X - E_w[x]) / T (+ w_X (E_w[a] - a_X) / T^2 for the temperature) over
+// its three states, computed there from the tables; a state passes flow when beta >
+// 1e-20 or |g| > 1e-20; the output is g_M (the marginal is beta_M).  The third ring
+// carries (diagonal D, up D) (beta, g) pairs.
+template <int MODE, int P, bool DOT, bool NWA = false>
 __global__ void __launch_bounds__(NW * 64)
 swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 const int* __restrict__ lengths, const float* __restrict__ alpha_sk,
@@ -366,7 +492,8 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     constexpr int FBD = FBU + 64;
     constexpr int FBE = FBD + 64;
     constexpr int BUF = FBE + 64;
-    static_assert(4 * P <= 64, "boundary flows fit their buffers");
+    static_assert(4 * P + 4 <= 64, "boundary flows fit their buffers");
+    using FE = std::conditional_t<NWA, float4, float2>;
     extern __shared__ float smem[];
     __shared__ int prog[NW];
     __shared__ float red[NW];
@@ -387,7 +514,8 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     // rings [NW][R]: (beta, g) up flows to (M, I); diagonal flows to (M, I); to D
     float4* ringU = reinterpret_cast<float4*>(smem + NW * BUF);
     float4* ringD = ringU + NW * R;
-    float2* ringE = reinterpret_cast<float2*>(ringD + NW * R);
+    FE* ringE = reinterpret_cast<FE*>(ringD + NW * R);
+    FE* fEx = reinterpret_cast<FE*>(fE);
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
 
@@ -436,10 +564,10 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
         const float* bupX = tan_brow + ub * NT;
         const float4* inU = ring_from(ringU, q, R);
         const float4* inD = ring_from(ringD, q, R);
-        const float2* inE = ring_from(ringE, q, R);
+        const FE* inE = ring_from(ringE, q, R);
         float4* outU = ring_of(ringU, q, R);
         float4* outD = ring_of(ringD, q, R);
-        float2* outE = ring_of(ringE, q, R);
+        FE* outE = ring_of(ringE, q, R);
         const bool x_in = q == 0 && has_next;             // flows from the part below
         const bool x_out = q == NL - 1 && part > 0;       // flows to the part above
         const bool below = q > 0 || x_in;
@@ -477,9 +605,11 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 o = (uint32_t)min((k * P + 62) * 4 + min(lane, 4 * P - 1), last * 4 + 3) * 4u;
                 l = in_lds + FBD * 4;
                 lds_dma_dword_sys<0>(reinterpret_cast<const float*>(fD + fi), o, l, 0u);
-                o = (uint32_t)min((k * P + 62) * 2 + min(lane, 2 * P - 1), last * 2 + 1) * 4u;
+                // NWA: (diagonal D, up D) quads of slots kP+62 .. kP+62+P
+                o = NWA ? (uint32_t)min((k * P + 62) * 4 + min(lane, 4 * P + 3), last * 4 + 3) * 4u
+                        : (uint32_t)min((k * P + 62) * 2 + min(lane, 2 * P - 1), last * 2 + 1) * 4u;
                 l = in_lds + FBE * 4;
-                lds_dma_dword_sys<0>(reinterpret_cast<const float*>(fE + fi), o, l, 0u);
+                lds_dma_dword_sys<0>(reinterpret_cast<const float*>(fEx + fi), o, l, 0u);
             }
         };
 
@@ -508,6 +638,9 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
         // (i+1, j) to M and I; from (i+1, j+1) to M, I, D (this step and the next)
         float lbM = 0, lgM = 0, lbD = 0, lgD = 0;
         float ubM = 0, ugM = 0, ubI = 0, ugI = 0;
+        float lbI = 0, lgI = 0, ubD = 0, ugD = 0;          // NWA: left to I, up to D
+        // NWA: the terminal cell's step on this lane
+        const int term_step = (NWA && i0 + lane == L1 - 1) ? L2 - 1 + lane : -1000000;
         float dbM = 0, dgM = 0, dbI = 0, dgI = 0, dbD = 0, dgD = 0;
         float ebM = 0, egM = 0, ebI = 0, egI = 0, ebD = 0, egD = 0;
 
@@ -551,9 +684,16 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             float bXM = row_ok ? buf[RX + lane] : 0.0f;
             float bXI = row_ok ? buf[RX + 64 + lane] : 0.0f;
             float bXD = row_ok ? buf[RX + 128 + lane] : 0.0f;
+            if (NWA && s == 0 && lane <= P) {
+                // row 0 at column t_hi - lane (0-based; -1 is the start cell)
+                const int c0 = t_hi - lane;
+                bAM = c0 == -1 ? 0.0f : kNINF;
+                bAD = c0 >= 0 ? go + (float)c0 * ge : kNINF;
+                bXD = c0 >= 0 ? (MODE == OPEN ? 1.0f : (MODE == EXT ? (float)c0 : 0.0f)) : 0.0f;
+            }
             // flows from the stripe below for lane 63: lane 63-j holds step j
             float4 qU = make_float4(0, 0, 0, 0), qD = make_float4(0, 0, 0, 0);
-            float2 qE = make_float2(0, 0);
+            float2 qE = make_float2(0, 0), qEu = make_float2(0, 0);
             if (below && lane >= 64 - P) {
                 const int j = 63 - lane;
                 if (x_in) {
@@ -561,12 +701,24 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                                      buf[FBU + 4 * j + 3]);
                     qD = make_float4(buf[FBD + 4 * j], buf[FBD + 4 * j + 1], buf[FBD + 4 * j + 2],
                                      buf[FBD + 4 * j + 3]);
-                    qE = make_float2(buf[FBE + 2 * j], buf[FBE + 2 * j + 1]);
+                    if (NWA) {
+                        qE = make_float2(buf[FBE + 4 * j], buf[FBE + 4 * j + 1]);
+                        qEu = make_float2(buf[FBE + 4 * (j + 1) + 2], buf[FBE + 4 * (j + 1) + 3]);
+                    } else {
+                        qE = make_float2(buf[FBE + 2 * j], buf[FBE + 2 * j + 1]);
+                    }
                 } else {
-                    qU = inU[ring_index(k * P + j + 63, R)];
+                    const int iu = ring_index(k * P + j + 63, R);
+                    qU = inU[iu];
                     const int id = ring_index(k * P + j + 62, R);
                     qD = inD[id];
-                    qE = inE[id];
+                    if constexpr (NWA) {
+                        const float4 e = inE[id], eu = inE[iu];
+                        qE = make_float2(e.x, e.y);
+                        qEu = make_float2(eu.z, eu.w);
+                    } else {
+                        qE = inE[id];
+                    }
                 }
             }
             wave_lds_sync();
@@ -588,6 +740,10 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 const float n0 = lane_bcast(qD.x, 62), n1 = lane_bcast(qD.y, 62);
                 const float n2 = lane_bcast(qD.z, 62), n3 = lane_bcast(qD.w, 62);
                 const float n4 = lane_bcast(qE.x, 62), n5 = lane_bcast(qE.y, 62);
+                if (NWA) {
+                    const float a4 = lane_bcast(qEu.x, 63), a5 = lane_bcast(qEu.y, 63);
+                    if (lane == 63) { ubD = a4; ugD = a5; }
+                }
                 if (lane == 63) {
                     ubM = a0; ugM = a1; ubI = a2; ugI = a3;
                     dbM = d0; dgM = d1; dbI = d2; dgI = d3; dbD = d4; dgD = d5;
@@ -601,6 +757,89 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             float qdb2 = wave_shr1(wave_shr1(qE.x));
             float qdg2 = wave_shr1(wave_shr1(qE.y));
             float qub0 = qU.x, qug0 = qU.y, qub1 = qU.z, qug1 = qU.w;
+            float qub2 = qEu.x, qug2 = qEu.y;
+            // NWA: one cell of the reverse sweep and the flows' shifts after it
+            auto nwa_cell = [&](int u, int t, bool ok, float vd, float sc, float dgAM, float dgAI,
+                                float dgAD, float dxM, float dxI, float dxD, float upM,
+                                float upI, float upD, float uxM, float uxI, float uxD, float lfM,
+                                float lfI, float lfD, float lxM, float lxI, float lxD) {
+                (void)sc;
+                const float ao = MODE == OPEN ? 1.0f : 0.0f, ae = MODE == EXT ? 1.0f : 0.0f;
+                // M over the diagonal states; I over (M + open, I + ext, D + open) above;
+                // D over (M + open, D + ext, I + open) to the left
+                float w[3], dw[3], wi[3], dwi[3], wd[3], dwd[3];
+                softmax3_tangent<MODE>({dgAM, dgAI, dgAD}, {dxM, dxI, dxD}, c, rT, w, dw);
+                softmax3_tangent<MODE>({upM + go, upI + ge, upD + go}, {uxM + ao, uxI + ae, uxD + ao},
+                                       c, rT, wi, dwi);
+                softmax3_tangent<MODE>({lfM + go, lfD + ge, lfI + go}, {lxM + ao, lxD + ae, lxI + ao},
+                                       c, rT, wd, dwd);
+                // the terminal cell seeds both channels with its states' softmax weights,
+                // normalised from the states themselves: exp((X - S) / T) with the
+                // rounded value S sums to 1 only within ulp(S) / T, an error that the
+                // tangents (of the alignment length's size) would carry into every entry
+                float biM = 0.0f, biI = 0.0f, biD = 0.0f, giM = 0.0f, giI = 0.0f, giD = 0.0f;
+                if (t == term_step) {
+                    float wt[3], dwt[3];
+                    softmax3_tangent<MODE>({AM[u], AI[u], AD[u]}, {XM[u], XI[u], XD[u]}, c, rT,
+                                           wt, dwt);
+                    biM = wt[0]; biI = wt[1]; biD = wt[2];
+                    giM = dwt[0]; giI = dwt[1]; giD = dwt[2];
+                }
+                const float bM = ((biM + dbM) + lbM) + ubM;
+                const float bI = ((biI + dbI) + ubI) + lbI;
+                const float bD = ((biD + dbD) + lbD) + ubD;
+                const float gM = ((giM + dgM) + lgM) + ugM;
+                const float gI = ((giI + dgI) + ugI) + lgI;
+                const float gD = ((giD + dgD) + lgD) + ugD;
+                // a state passes flow only when beta > 1e-20 or |g| > 1e-20
+                const bool pM_ = ok && (bM > 1e-20f || fabsf(gM) > 1e-20f);
+                const bool pI_ = ok && (bI > 1e-20f || fabsf(gI) > 1e-20f);
+                const bool pD_ = ok && (bD > 1e-20f || fabsf(gD) > 1e-20f);
+                const float BM = pM_ ? bM : 0.0f, BI = pI_ ? bI : 0.0f, BD = pD_ ? bD : 0.0f;
+                const float GM = pM_ ? gM : 0.0f, GI = pI_ ? gI : 0.0f, GD = pD_ ? gD : 0.0f;
+                if (DOT) dacc += GM * vd;
+                else otile[tbase + u] = GM;
+                const float obM0 = BM * w[0], obI0 = BM * w[1], obD0 = BM * w[2];
+                const float ogM0 = GM * w[0] + BM * dw[0], ogI0 = GM * w[1] + BM * dw[1];
+                const float ogD0 = GM * w[2] + BM * dw[2];
+                const float obMu = BI * wi[0], obIu = BI * wi[1], obDu = BI * wi[2];
+                const float ogMu = GI * wi[0] + BI * dwi[0], ogIu = GI * wi[1] + BI * dwi[1];
+                const float ogDu = GI * wi[2] + BI * dwi[2];
+                const float obMl = BD * wd[0], obDl = BD * wd[1], obIl = BD * wd[2];
+                const float ogMl = GD * wd[0] + BD * dwd[0], ogDl = GD * wd[1] + BD * dwd[1];
+                const float ogIl = GD * wd[2] + BD * dwd[2];
+                if (lane == 0) {
+                    outU[slot0 + u] = make_float4(obMu, ogMu, obIu, ogIu);
+                    outD[slot0 + u] = make_float4(obM0, ogM0, obI0, ogI0);
+                    if constexpr (NWA) outE[slot0 + u] = make_float4(obD0, ogD0, obDu, ogDu);
+                }
+                qub0 = wave_shr1(qub0);
+                qug0 = wave_shr1(qug0);
+                qub1 = wave_shr1(qub1);
+                qug1 = wave_shr1(qug1);
+                qub2 = wave_shr1(qub2);
+                qug2 = wave_shr1(qug2);
+                lbM = obMl; lgM = ogMl; lbD = obDl; lgD = ogDl; lbI = obIl; lgI = ogIl;
+                ubM = wave_shl1_or(obMu, qub0);
+                ugM = wave_shl1_or(ogMu, qug0);
+                ubI = wave_shl1_or(obIu, qub1);
+                ugI = wave_shl1_or(ogIu, qug1);
+                ubD = wave_shl1_or(obDu, qub2);
+                ugD = wave_shl1_or(ogDu, qug2);
+                dbM = ebM; dgM = egM; dbI = ebI; dgI = egI; dbD = ebD; dgD = egD;
+                ebM = wave_shl1_or(obM0, qdb0);
+                egM = wave_shl1_or(ogM0, qdg0);
+                ebI = wave_shl1_or(obI0, qdb1);
+                egI = wave_shl1_or(ogI0, qdg1);
+                ebD = wave_shl1_or(obD0, qdb2);
+                egD = wave_shl1_or(ogD0, qdg2);
+                qdb0 = wave_shr1(qdb0);
+                qdg0 = wave_shr1(qdg0);
+                qdb1 = wave_shr1(qdb1);
+                qdg1 = wave_shr1(qdg1);
+                qdb2 = wave_shr1(qdb2);
+                qdg2 = wave_shr1(qdg2);
+            };
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t_hi - u;
@@ -614,6 +853,8 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                             nXD = wave_shl1(bXD);
                 const float upM = wave_shr1_or(AM[u + 1], bAM), upI = wave_shr1_or(AI[u + 1], bAI);
                 const float uxM = wave_shr1_or(XM[u + 1], bXM), uxI = wave_shr1_or(XI[u + 1], bXI);
+                const float upD = NWA ? wave_shr1_or(AD[u + 1], bAD) : kNINF;
+                const float uxD = NWA ? wave_shr1_or(XD[u + 1], bXD) : 0.0f;
                 const float dgAM = wave_shr1_or(AM[u + 2], nAM), dgAI = wave_shr1_or(AI[u + 2], nAI),
                             dgAD = wave_shr1_or(AD[u + 2], nAD);
                 const float dxM = wave_shr1_or(XM[u + 2], nXM), dxI = wave_shr1_or(XI[u + 2], nXI),
@@ -621,6 +862,12 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 bAM = nAM; bAI = nAI; bAD = nAD;
                 bXM = nXM; bXI = nXI; bXD = nXD;
                 const float lfM = AM[u + 1], lfD = AD[u + 1], lxM = XM[u + 1], lxD = XD[u + 1];
+                const float lfI = AI[u + 1], lxI = XI[u + 1];
+                if constexpr (NWA) {
+                    nwa_cell(u, t, ok, vd, sc, dgAM, dgAI, dgAD, dxM, dxI, dxD, upM, upI, upD,
+                             uxM, uxI, uxD, lfM, lfI, lfD, lxM, lxI, lxD);
+                    continue;
+                }
                 // M: weights over (M, I, D) diagonal + s, and s
                 const float v0 = dgAM + sc, v1 = dgAI + sc, v2 = dgAD + sc;
                 const float m4 = fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
@@ -745,7 +992,7 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 if (lane == 0) {
                     outU[slot0 + u] = make_float4(obMu, ogMu, obIu, ogIu);
                     outD[slot0 + u] = make_float4(obM0, ogM0, obI0, ogI0);
-                    outE[slot0 + u] = make_float2(obD0, ogD0);
+                    if constexpr (!NWA) outE[slot0 + u] = make_float2(obD0, ogD0);
                 }
                 // successor flows for the next steps; lane 63 takes the rings
                 qub0 = wave_shr1(qub0);
@@ -780,7 +1027,8 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                     const int sl = slot0 + lane;
                     store_sys4(fU + fo + k * P + lane, outU[sl]);
                     store_sys4(fD + fo + k * P + lane, outD[sl]);
-                    store_sys2(fE + fo + k * P + lane, outE[sl]);
+                    if constexpr (NWA) store_sys4(fEx + fo + k * P + lane, outE[sl]);
+                    else store_sys2(fE + fo + k * P + lane, outE[sl]);
                 }
                 if (k >= 2) {
                     // at least P + 3P/2 + 6 loads, 6 flow stores and (DOT: none, else 2P)
@@ -824,18 +1072,19 @@ size_t lds_tangent_r(bool has_v, int R) {
 }
 size_t lds_tangent(bool has_v, int L1, int L2) { return lds_tangent_r(has_v, ring_len(L1, L2, 256)); }
 
-size_t lds_dual_r(bool has_v, bool dot, int R) {
+size_t lds_dual_r(bool has_v, bool dot, int R, bool nwa) {
     const int buf = 65 * PD * (has_v ? 2 : 1) + 6 * PD * 64 + 6 * 64 + (dot ? 0 : 65 * PD) + 3 * 64;
     return (size_t)NW * buf * sizeof(float) +
-           (size_t)NW * R * (2 * sizeof(float4) + sizeof(float2));
+           (size_t)NW * R * (2 * sizeof(float4) + (nwa ? sizeof(float4) : sizeof(float2)));
 }
-size_t lds_dual(bool has_v, bool dot, int L1, int L2) {
-    return lds_dual_r(has_v, dot, ring_len(L1, L2, 128));
+size_t lds_dual(bool has_v, bool dot, int L1, int L2, bool nwa) {
+    return lds_dual_r(has_v, dot, ring_len(L1, L2, 128), nwa);
 }
 
 // Workspace after the primal layout: tangent tables + last rows, [B] scalars, then for
 // split elements the parts' partial sums and the reverse sweep's boundary flows by
-// step (up and diagonal (beta, g) pairs to M and I, float4 each; diagonal pair to D).
+// step (up and diagonal (beta, g) pairs to M and I, float4 each; diagonal pair to D,
+// and for global alignment the up pair to D beside it: a float4 slot).
 struct Second {
     Layout prim;
     float* tan_sk;
@@ -873,12 +1122,12 @@ Second second_layout(void* ws, int B, int L1, int L2) {
     w.fD = (float4*)p;
     p += round256(slots * sizeof(float4));
     w.fE = (float2*)p;
-    p += round256(slots * sizeof(float2));
+    p += round256(slots * sizeof(float4));
     w.bytes = (size_t)(p - (char*)ws);
     return w;
 }
 
-template <int MODE>
+template <int MODE, bool NWA = false>
 int launch_tangent(const float* scores, const float* V, const int* lengths, int B, int L1, int L2,
                    float go, float ge, float T, const Second& w, float* sdot, hipStream_t st) {
     const int ns = (L1 + 63) / 64;
@@ -888,36 +1137,38 @@ int launch_tangent(const float* scores, const float* V, const int* lengths, int 
     const int R = ring_len(sp.G > 1 ? sp.SPW * 64 : L1, L2, 256);
     const size_t lds = lds_tangent_r(has_v, R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
-    auto kern = swa_tangent_kernel<MODE, PT>;
+    auto kern = swa_tangent_kernel<MODE, PT, NWA>;
     if (sp.G > 1) D2P_TRY(launch_flag_reset(w.prim.fflag, B * sp.G, st));
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
-    D2P_LAUNCH("swa_tangent", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
+    D2P_LAUNCH(NWA ? "nwa_tangent" : "swa_tangent", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
                lengths, w.prim.alpha_sk, w.prim.brow, w.part, w.tan_sk, w.tan_brow, sdot,
                w.prim.status, w.prim.fflag, w.spart, B, L1, L2, ns, go, ge, T, R, sp.G, sp.SPW,
                next_epoch());
-    if (MODE == HVP && sp.G > 1 && launch_sum_parts(w.spart, sdot, B, sp.G, st) != D2P_OK)
+    if (MODE == HVP && !NWA && sp.G > 1 && launch_sum_parts(w.spart, sdot, B, sp.G, st) != D2P_OK)
         return D2P_ERR_HIP;
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
 
-template <int MODE, bool DOT>
+// dS: the value's tangent (or dS/dtheta) per element, seeding every cell; global
+// alignment seeds the terminal cell from the tables instead and ignores it.
+template <int MODE, bool DOT, bool NWA = false>
 int launch_dual(const float* scores, const float* V, const int* lengths, int B, int L1, int L2,
                 float go, float ge, float T, const Second& w, const float* dS, float* out,
                 float* dot, hipStream_t st) {
     const int ns = (L1 + 63) / 64;
     constexpr bool has_v = MODE == HVP || DOT;
     const Split sp =
-        choose_split(B, L1, w.prim, lds_dual(has_v, DOT, L1, L2) <= kLdsLimit ? 0 : NW);
+        choose_split(B, L1, w.prim, lds_dual(has_v, DOT, L1, L2, NWA) <= kLdsLimit ? 0 : NW);
     const int R = ring_len(sp.G > 1 ? sp.SPW * 64 : L1, L2, 128);
-    const size_t lds = lds_dual_r(has_v, DOT, R);
+    const size_t lds = lds_dual_r(has_v, DOT, R, NWA);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
-    auto kern = swa_dual_kernel<MODE, PD, DOT>;
+    auto kern = swa_dual_kernel<MODE, PD, DOT, NWA>;
     if (sp.G > 1) D2P_TRY(launch_flag_reset(w.prim.bflag, B * sp.G, st));
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
-    D2P_LAUNCH("swa_dual", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
+    D2P_LAUNCH(NWA ? "nwa_dual" : "swa_dual", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st, scores, V,
                lengths, w.prim.alpha_sk, w.prim.brow, w.tan_sk, w.tan_brow, w.part, dS, out, dot,
                w.prim.status, w.prim.trash, w.prim.bflag, w.fU, w.fD, w.fE, w.spart, B, L1, L2,
                ns, go, ge, T, R, sp.G, sp.SPW, next_epoch());
@@ -927,15 +1178,15 @@ int launch_dual(const float* scores, const float* V, const int* lengths, int B, 
     return D2P_OK;
 }
 
-template <int MODE, bool DOT>
+template <int MODE, bool DOT, bool NWA = false>
 int param_pass(const float* scores, const float* ga, const int* lengths, int B, int L1, int L2,
                float go, float ge, float T, const Second& w, float* out, float* dot,
                hipStream_t st) {
-    const int rc = launch_tangent<MODE>(scores, nullptr, lengths, B, L1, L2, go, ge, T, w,
-                                        nullptr, st);
+    const int rc = launch_tangent<MODE, NWA>(scores, nullptr, lengths, B, L1, L2, go, ge, T, w,
+                                             nullptr, st);
     if (rc != D2P_OK) return rc;
-    return launch_dual<MODE, DOT>(scores, ga, lengths, B, L1, L2, go, ge, T, w, w.dS[MODE - 1],
-                                  out, dot, st);
+    return launch_dual<MODE, DOT, NWA>(scores, ga, lengths, B, L1, L2, go, ge, T, w,
+                                       w.dS[MODE - 1], out, dot, st);
 }
 
 // rings that do not fit for an unsplit element force parts of at most NW stripes
@@ -1043,6 +1294,111 @@ extern "C" int d2p_swa_backward_full(const float* scores, const float* grad_alig
                                               gap_ext, temperature, w, nullptr, grad_ext, st));
     D2P_TRY(swa2::param_pass<swa2::TEMP, true>(scores, ga, lengths, B, max_L1, max_L2, gap_open,
                                                gap_ext, temperature, w, nullptr, grad_T, st));
+    return wf::launch_poison(w.prim.status, B, (long long)max_L1 * max_L2, grad_scores, nullptr,
+                             grad_open, grad_ext, grad_T, nullptr, st);
+}
+
+// ------------------------------------------------------------------ global alignment
+// soft_nw_affine's second-order entry points (reference: src/nw_affine/torch_cuda.cpp):
+// the NW mode of the same sweeps.  Neither the HVP nor the Jacobians need the marginal
+// backward: the reverse sweep seeds the terminal cell from the tables.
+
+extern "C" size_t d2p_nwa_second_workspace_bytes(int B, int max_L1, int max_L2) {
+    return d2p_swa_second_workspace_bytes(B, max_L1, max_L2);
+}
+
+extern "C" int d2p_nwa_hvp(const float* scores, const float* tangent, const int* lengths, int B,
+                           int max_L1, int max_L2, float gap_open, float gap_ext,
+                           float temperature, float* hvp, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    D2P_TRY(swa2::check(B, max_L1, max_L2, temperature));
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(scores && tangent && hvp, "null pointer argument");
+    D2P_REQUIRE(workspace && workspace_bytes >= d2p_nwa_second_workspace_bytes(B, max_L1, max_L2),
+                "workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    const swa2::Second w = swa2::second_layout(workspace, B, max_L1, max_L2);
+    D2P_TRY(swa::launch_forward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
+                                temperature, w.prim, w.part, st, true));
+    D2P_TRY((swa2::launch_tangent<swa2::HVP, true>(scores, tangent, lengths, B, max_L1, max_L2,
+                                                   gap_open, gap_ext, temperature, w, w.sdot,
+                                                   st)));
+    D2P_TRY((swa2::launch_dual<swa2::HVP, false, true>(scores, tangent, lengths, B, max_L1,
+                                                       max_L2, gap_open, gap_ext, temperature, w,
+                                                       w.sdot, hvp, nullptr, st)));
+    return wf::launch_poison(w.prim.status, B, (long long)max_L1 * max_L2, hvp, nullptr, nullptr,
+                             nullptr, nullptr, nullptr, st);
+}
+
+extern "C" int d2p_nwa_param_jacobian(const float* scores, int param_type, const int* lengths,
+                                      int B, int max_L1, int max_L2, float gap_open,
+                                      float gap_ext, float temperature, float* jacobian,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+    D2P_TRY(swa2::check(B, max_L1, max_L2, temperature));
+    D2P_REQUIRE(param_type >= 0 && param_type <= 2, "param_type must be 0, 1 or 2");
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(scores && jacobian, "null pointer argument");
+    D2P_REQUIRE(workspace && workspace_bytes >= d2p_nwa_second_workspace_bytes(B, max_L1, max_L2),
+                "workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    const swa2::Second w = swa2::second_layout(workspace, B, max_L1, max_L2);
+    D2P_TRY(swa::launch_forward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
+                                temperature, w.prim, w.part, st, true));
+    switch (param_type) {
+        case 0:
+            D2P_TRY((swa2::param_pass<swa2::OPEN, false, true>(scores, nullptr, lengths, B, max_L1,
+                                                               max_L2, gap_open, gap_ext,
+                                                               temperature, w, jacobian, nullptr,
+                                                               st)));
+            break;
+        case 1:
+            D2P_TRY((swa2::param_pass<swa2::EXT, false, true>(scores, nullptr, lengths, B, max_L1,
+                                                              max_L2, gap_open, gap_ext,
+                                                              temperature, w, jacobian, nullptr,
+                                                              st)));
+            break;
+        default:
+            D2P_TRY((swa2::param_pass<swa2::TEMP, false, true>(scores, nullptr, lengths, B, max_L1,
+                                                               max_L2, gap_open, gap_ext,
+                                                               temperature, w, jacobian, nullptr,
+                                                               st)));
+    }
+    return wf::launch_poison(w.prim.status, B, (long long)max_L1 * max_L2, jacobian, nullptr,
+                             nullptr, nullptr, nullptr, nullptr, st);
+}
+
+extern "C" int d2p_nwa_backward_full(const float* scores, const float* grad_alignment,
+                                     const int* lengths, int B, int max_L1, int max_L2,
+                                     float gap_open, float gap_ext, float temperature,
+                                     float* grad_scores, float* grad_open, float* grad_ext,
+                                     float* grad_T, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+    D2P_TRY(swa2::check(B, max_L1, max_L2, temperature));
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(scores && grad_alignment && grad_scores && grad_open && grad_ext && grad_T,
+                "null pointer argument");
+    D2P_REQUIRE(workspace && workspace_bytes >= d2p_nwa_second_workspace_bytes(B, max_L1, max_L2),
+                "workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    const swa2::Second w = swa2::second_layout(workspace, B, max_L1, max_L2);
+    const float* ga = grad_alignment;
+    D2P_TRY(swa::launch_forward(scores, lengths, B, max_L1, max_L2, gap_open, gap_ext,
+                                temperature, w.prim, w.part, st, true));
+    D2P_TRY((swa2::launch_tangent<swa2::HVP, true>(scores, ga, lengths, B, max_L1, max_L2,
+                                                   gap_open, gap_ext, temperature, w, w.sdot,
+                                                   st)));
+    D2P_TRY((swa2::launch_dual<swa2::HVP, false, true>(scores, ga, lengths, B, max_L1, max_L2,
+                                                       gap_open, gap_ext, temperature, w, w.sdot,
+                                                       grad_scores, nullptr, st)));
+    D2P_TRY((swa2::param_pass<swa2::OPEN, true, true>(scores, ga, lengths, B, max_L1, max_L2,
+                                                      gap_open, gap_ext, temperature, w, nullptr,
+                                                      grad_open, st)));
+    D2P_TRY((swa2::param_pass<swa2::EXT, true, true>(scores, ga, lengths, B, max_L1, max_L2,
+                                                     gap_open, gap_ext, temperature, w, nullptr,
+                                                     grad_ext, st)));
+    D2P_TRY((swa2::param_pass<swa2::TEMP, true, true>(scores, ga, lengths, B, max_L1, max_L2,
+                                                      gap_open, gap_ext, temperature, w, nullptr,
+                                                      grad_T, st)));
     return wf::launch_poison(w.prim.status, B, (long long)max_L1 * max_L2, grad_scores, nullptr,
                              grad_open, grad_ext, grad_T, nullptr, st);
 }

@@ -244,6 +244,69 @@ int d2p_nw_backward_full(const float* scores, const float* grad_alignment, const
                          size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Affine-gap soft Needleman-Wunsch (global alignment, three states)
+ * M = s + LSE(M, I, D)[i-1,j-1], I = LSE(M + open, I + ext, D + open)[i-1,j],
+ * D = LSE(M + open, I + open, D + ext)[i,j-1]; M[0,0] = 0, I[i,0] = open + (i-1) ext,
+ * D[0,j] = open + (j-1) ext; value = LSE(M, I, D)[L1, L2]
+ * (/root/reference/src/nw_affine/kernels_cpu.cpp:100-187).
+ * ------------------------------------------------------------------------- */
+
+/* Workspace bytes needed by d2p_nwa_forward_marginals (status words first). */
+size_t d2p_nwa_workspace_bytes(int B, int max_L1, int max_L2);
+
+/* Forward value and marginals in one call.
+ * Replaces the pair nw_affine_forward + nw_affine_backward
+ * (/root/reference/src/nw_affine/kernels.cuh:77-130) as sequenced by
+ * soft_nw_affine_cuda_with_grads (/root/reference/src/nw_affine/torch_cuda.cpp:387-432);
+ * the CPU kernels restated are /root/reference/src/nw_affine/kernels_cpu.cpp:100-347.
+ *   scores    [B, max_L1, max_L2]  input
+ *   value     [B]                  out: LSE of the terminal cell's three states
+ *   marginals [B, max_L1, max_L2]  out: dvalue/dscores (zero in padding)
+ *   grad_open, grad_ext [B]        out: dvalue/dgap_open, dvalue/dgap_ext (boundary
+ *                                  chains I[i,0] and D[0,j] included)
+ *   grad_T    [B]                  out: dvalue/dtemperature */
+int d2p_nwa_forward_marginals(const float* scores, const int* lengths, int B, int max_L1,
+                              int max_L2, float gap_open, float gap_ext, float temperature,
+                              float* value, float* marginals, float* grad_open, float* grad_ext,
+                              float* grad_T, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/* Workspace bytes of the second-order entry points below (d2p_nwa_hvp,
+ * d2p_nwa_param_jacobian, d2p_nwa_backward_full). */
+size_t d2p_nwa_second_workspace_bytes(int B, int max_L1, int max_L2);
+
+/* Hessian-vector product of the value: hvp = (d^2 value / dscores^2) . tangent.
+ * Replaces nw_affine_hvp (/root/reference/src/nw_affine/kernels.cuh:132-159) as
+ * sequenced by soft_nw_affine_hvp_cuda (/root/reference/src/nw_affine/torch_cuda.cpp:
+ * 435-482), which runs the forward first.
+ *   tangent, hvp [B, max_L1, max_L2]                                              */
+int d2p_nwa_hvp(const float* scores, const float* tangent, const int* lengths, int B,
+                int max_L1, int max_L2, float gap_open, float gap_ext, float temperature,
+                float* hvp, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Jacobian of the marginals with respect to gap_open (param_type 0), gap_ext (1) or
+ * temperature (2).  Replaces nw_affine_param_grad
+ * (/root/reference/src/nw_affine/kernels.cuh:161-190) as sequenced by
+ * soft_nw_affine_param_jacobian_cuda (/root/reference/src/nw_affine/torch_cuda.cpp:
+ * 484-553); the reference's dS/dtheta input is unused by its kernel and not computed
+ * here.
+ *   jacobian [B, max_L1, max_L2]                                                  */
+int d2p_nwa_param_jacobian(const float* scores, int param_type, const int* lengths, int B,
+                           int max_L1, int max_L2, float gap_open, float gap_ext,
+                           float temperature, float* jacobian, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* Backward of the marginals output for a cotangent grad_alignment:
+ *   grad_scores = H . grad_alignment, grad_X[b] = <grad_alignment[b], dP_b/dX> for
+ *   X in (open, ext, T) (per element; soft_nw_affine_backward_full_cuda,
+ *   /root/reference/src/nw_affine/torch_cuda.cpp:555-665, returns their sums). */
+int d2p_nwa_backward_full(const float* scores, const float* grad_alignment, const int* lengths,
+                          int B, int max_L1, int max_L2, float gap_open, float gap_ext,
+                          float temperature, float* grad_scores, float* grad_open,
+                          float* grad_ext, float* grad_T, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Soft dynamic time warping (optional Sakoe-Chiba band)
  * ------------------------------------------------------------------------- */
 

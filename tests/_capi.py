@@ -46,6 +46,14 @@ SIGNATURES = {
     "d2p_swa_param_jacobian": (_i, [_p, _i, _p, _i, _i, _i, _f, _f, _f, _p, _p, _z, _p]),
     "d2p_swa_backward_full": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _f, _p, _p, _p, _p, _p, _z,
                                    _p]),
+    "d2p_nwa_workspace_bytes": (_z, [_i, _i, _i]),
+    "d2p_nwa_forward_marginals": (_i, [_p, _p, _i, _i, _i, _f, _f, _f, _p, _p, _p, _p, _p, _p,
+                                       _z, _p]),
+    "d2p_nwa_second_workspace_bytes": (_z, [_i, _i, _i]),
+    "d2p_nwa_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _f, _p, _p, _z, _p]),
+    "d2p_nwa_param_jacobian": (_i, [_p, _i, _p, _i, _i, _i, _f, _f, _f, _p, _p, _z, _p]),
+    "d2p_nwa_backward_full": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _f, _p, _p, _p, _p, _p, _z,
+                                   _p]),
     "d2p_dtw_second_workspace_bytes": (_z, [_i, _i, _i]),
     "d2p_dtw_second_workspace_bytes_banded": (_z, [_i, _i, _i, _i]),
     "d2p_dtw_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _i, _p, _p, _z, _p]),
@@ -142,18 +150,20 @@ def nw_forward_marginals(scores, lengths, gap, T):
     return tuple(outs)
 
 
-def swa_forward_marginals(scores, lengths, go, ge, T):
-    """Affine gap: (partition, marginals, grad_open, grad_ext, grad_T) through the C ABI."""
+def swa_forward_marginals(scores, lengths, go, ge, T, fam="swa"):
+    """Affine gap: (partition, marginals, grad_open, grad_ext, grad_T) through the C ABI
+    (fam "nwa": global alignment, the value instead of the partition)."""
     import torch
     B, L1, L2 = scores.shape
     dev = scores.device
     lengths = _lengths(lengths, B, L1, L2, dev)
     outs = [torch.empty(B, device=dev), torch.empty(B, L1, L2, device=dev)] + \
         [torch.empty(B, device=dev) for _ in range(3)]
-    nbytes = lib().d2p_swa_workspace_bytes(B, L1, L2)
+    nbytes = getattr(lib(), f"d2p_{fam}_workspace_bytes")(B, L1, L2)
     ws = _workspace(nbytes, dev)
-    check(lib().d2p_swa_forward_marginals(ptr(scores), ptr(lengths), B, L1, L2, go, ge, T,
-                                          *[ptr(o) for o in outs], ptr(ws), nbytes, stream()))
+    check(getattr(lib(), f"d2p_{fam}_forward_marginals")(ptr(scores), ptr(lengths), B, L1, L2,
+                                                          go, ge, T, *[ptr(o) for o in outs],
+                                                          ptr(ws), nbytes, stream()))
     _check_status(ws, B)
     return tuple(outs)
 
@@ -223,50 +233,69 @@ def sw_backward_full(scores, grad_alignment, lengths, gap, T, fam="sw"):
     return gs, gg, gt
 
 
-def _swa_second_ws(B, L1, L2, dev):
-    nbytes = lib().d2p_swa_second_workspace_bytes(B, L1, L2)
+def _swa_second_ws(B, L1, L2, dev, fam="swa"):
+    nbytes = getattr(lib(), f"d2p_{fam}_second_workspace_bytes")(B, L1, L2)
     return _workspace(nbytes, dev), nbytes
 
 
-def swa_hvp(scores, V, lengths, go, ge, T):
+def swa_hvp(scores, V, lengths, go, ge, T, fam="swa"):
     import torch
     B, L1, L2 = scores.shape
     dev = scores.device
     lengths = _lengths(lengths, B, L1, L2, dev)
     out = torch.empty(B, L1, L2, device=dev)
-    ws, nbytes = _swa_second_ws(B, L1, L2, dev)
-    check(lib().d2p_swa_hvp(ptr(scores), ptr(V), ptr(lengths), B, L1, L2, go, ge, T, ptr(out),
-                            ptr(ws), nbytes, stream()))
+    ws, nbytes = _swa_second_ws(B, L1, L2, dev, fam)
+    check(getattr(lib(), f"d2p_{fam}_hvp")(ptr(scores), ptr(V), ptr(lengths), B, L1, L2, go, ge,
+                                           T, ptr(out), ptr(ws), nbytes, stream()))
     _check_status(ws, B)
     return out
 
 
-def swa_param_jacobian(scores, ptype, lengths, go, ge, T):
+def swa_param_jacobian(scores, ptype, lengths, go, ge, T, fam="swa"):
     import torch
     B, L1, L2 = scores.shape
     dev = scores.device
     lengths = _lengths(lengths, B, L1, L2, dev)
     out = torch.empty(B, L1, L2, device=dev)
-    ws, nbytes = _swa_second_ws(B, L1, L2, dev)
-    check(lib().d2p_swa_param_jacobian(ptr(scores), ptype, ptr(lengths), B, L1, L2, go, ge, T,
-                                       ptr(out), ptr(ws), nbytes, stream()))
+    ws, nbytes = _swa_second_ws(B, L1, L2, dev, fam)
+    check(getattr(lib(), f"d2p_{fam}_param_jacobian")(ptr(scores), ptype, ptr(lengths), B, L1,
+                                                      L2, go, ge, T, ptr(out), ptr(ws), nbytes,
+                                                      stream()))
     _check_status(ws, B)
     return out
 
 
-def swa_backward_full(scores, grad_alignment, lengths, go, ge, T):
+def swa_backward_full(scores, grad_alignment, lengths, go, ge, T, fam="swa"):
     import torch
     B, L1, L2 = scores.shape
     dev = scores.device
     lengths = _lengths(lengths, B, L1, L2, dev)
     gs = torch.empty(B, L1, L2, device=dev)
     gp = [torch.empty(B, device=dev) for _ in range(3)]
-    ws, nbytes = _swa_second_ws(B, L1, L2, dev)
-    check(lib().d2p_swa_backward_full(ptr(scores), ptr(grad_alignment), ptr(lengths), B, L1, L2,
-                                      go, ge, T, ptr(gs), *[ptr(g) for g in gp], ptr(ws), nbytes,
-                                      stream()))
+    ws, nbytes = _swa_second_ws(B, L1, L2, dev, fam)
+    check(getattr(lib(), f"d2p_{fam}_backward_full")(ptr(scores), ptr(grad_alignment),
+                                                     ptr(lengths), B, L1, L2, go, ge, T, ptr(gs),
+                                                     *[ptr(g) for g in gp], ptr(ws), nbytes,
+                                                     stream()))
     _check_status(ws, B)
     return (gs, *gp)
+
+
+def nwa_forward_marginals(scores, lengths, go, ge, T):
+    """Affine-gap NW: (value, marginals, grad_open, grad_ext, grad_T) through the C ABI."""
+    return swa_forward_marginals(scores, lengths, go, ge, T, fam="nwa")
+
+
+def nwa_hvp(scores, V, lengths, go, ge, T):
+    return swa_hvp(scores, V, lengths, go, ge, T, fam="nwa")
+
+
+def nwa_param_jacobian(scores, ptype, lengths, go, ge, T):
+    return swa_param_jacobian(scores, ptype, lengths, go, ge, T, fam="nwa")
+
+
+def nwa_backward_full(scores, grad_alignment, lengths, go, ge, T):
+    return swa_backward_full(scores, grad_alignment, lengths, go, ge, T, fam="nwa")
 
 
 def dtw_hvp(costs, V, lengths, T, bw=-1):

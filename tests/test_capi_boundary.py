@@ -62,6 +62,7 @@ def test_abi_version_and_error_string(lib):
 
 @pytest.mark.parametrize("fn,planes", [("d2p_sw_workspace_bytes", 1),
                                        ("d2p_swa_workspace_bytes", 3),
+                                       ("d2p_nwa_workspace_bytes", 3),
                                        ("d2p_dtw_workspace_bytes", 1)])
 def test_workspace_sizes(lib, fn, planes):
     f = getattr(lib, fn)
@@ -76,9 +77,10 @@ def test_workspace_sizes(lib, fn, planes):
     if fn in ("d2p_sw_workspace_bytes", "d2p_dtw_workspace_bytes"):
         # split elements: boundary flows, one (up, diagonal) pair per stripe and step
         table += 2 * 2 * steps * 2 * 4
-    elif fn == "d2p_swa_workspace_bytes":
-        # split elements: boundary flows, a float4 and a float per stripe and step
-        table += 2 * 2 * steps * 5 * 4
+    else:
+        # split elements: boundary flows, a float4 and a float2 per stripe and step (the
+        # global alignment's second flow entry is a pair)
+        table += 2 * 2 * steps * 6 * 4
     assert table <= small <= table + 4096
     # every workspace starts with status words: never zero for B > 0
     assert f(1, 0, 0) > 0
@@ -89,6 +91,7 @@ def test_second_workspaces_hold_the_first(lib):
     for first, second, planes in (
             ("d2p_sw_workspace_bytes", "d2p_sw_second_workspace_bytes", 1),
             ("d2p_swa_workspace_bytes", "d2p_swa_second_workspace_bytes", 3),
+            ("d2p_nwa_workspace_bytes", "d2p_nwa_second_workspace_bytes", 3),
             ("d2p_dtw_workspace_bytes", "d2p_dtw_second_workspace_bytes", 1)):
         a = getattr(lib, first)(3, 200, 90)
         b = getattr(lib, second)(3, 200, 90)
