@@ -1,9 +1,10 @@
 """d2p_amd -- MI355X (gfx950) soft-alignment dynamic programming for PyTorch-ROCm.
 
-Drop-in for the soft Smith-Waterman (linear/affine gap), soft-DTW and
-(first-order) linear-gap soft Needleman-Wunsch part of orikata-bio/d2p: same Python API (``soft_sw``, ``soft_sw_affine``,
-``soft_dtw``, the ``nn.Module`` wrappers, ``ops``, the legacy flat names) and
-the same ``torch.ops.d2p`` operator schemas, computed by hand-written HIP
+Drop-in for the soft Smith-Waterman (linear and affine gap), soft-DTW and soft
+Needleman-Wunsch (linear and affine gap) part of orikata-bio/d2p, first and second
+order: the same Python API (``soft_sw``, ``soft_sw_affine``, ``soft_dtw``,
+``soft_nw``, ``soft_nw_affine``, the ``nn.Module`` wrappers, ``ops``, the legacy flat
+names) and the same ``torch.ops.d2p`` operator schemas, computed by hand-written HIP
 kernels for CDNA4.  Tensors must live on the HIP device.
 """
 from . import _ops
@@ -11,7 +12,7 @@ from . import _compile  # noqa: F401  (fake/meta and autocast registrations)
 
 from .sw import soft_sw, soft_sw_affine, SWResult, SoftSW, SoftSWAffine
 from .dtw import soft_dtw, DTWResult, SoftDTW
-from .nw import soft_nw, NWResult, SoftNW
+from .nw import soft_nw, soft_nw_affine, NWResult, SoftNW, SoftNWAffine
 from . import ops
 
 # legacy flat names (reference d2p/__init__.py:120-139)
@@ -36,6 +37,11 @@ soft_nw_forward = _ops.soft_nw_float
 soft_nw_hvp = _ops.soft_nw_hvp
 soft_nw_param_jacobian = _ops.soft_nw_param_jacobian
 soft_nw_backward_full = _ops.soft_nw_backward_full
+soft_nw_affine_float = _ops.soft_nw_affine_float
+soft_nw_affine_with_grads = _ops.soft_nw_affine_with_grads
+soft_nw_affine_hvp = _ops.soft_nw_affine_hvp
+soft_nw_affine_param_jacobian = _ops.soft_nw_affine_param_jacobian
+soft_nw_affine_backward_full = _ops.soft_nw_affine_backward_full
 
 __all__ = [
     "soft_sw", "soft_sw_affine", "SWResult", "SoftSW", "SoftSWAffine",
@@ -48,4 +54,6 @@ __all__ = [
     "soft_dtw_backward_full",
     "soft_nw", "NWResult", "SoftNW", "soft_nw_float", "soft_nw_with_grads", "soft_nw_forward",
     "soft_nw_hvp", "soft_nw_param_jacobian", "soft_nw_backward_full",
+    "soft_nw_affine", "SoftNWAffine", "soft_nw_affine_float", "soft_nw_affine_with_grads",
+    "soft_nw_affine_hvp", "soft_nw_affine_param_jacobian", "soft_nw_affine_backward_full",
 ]

@@ -1,7 +1,7 @@
 """torch.compile / AMP glue: fake (meta) kernels and autocast rules for d2p ops.
 
 Behaviour of the reference's ``d2p/_compile.py`` for the SW, affine, DTW and
-linear NW families (fakes ``:24-305,371-415``, autocast ``:857-931``):
+NW families (fakes ``:24-415``, autocast ``:857-931``):
 * every ``d2p::`` op gets a fake kernel describing its output shapes;
 * under ``torch.autocast("cuda")`` every op runs in float32 (inputs are upcast),
   because the DP recurrences accumulate error in 16-bit formats.
@@ -81,6 +81,22 @@ _FAKES = {
     "nw_marginals_grad_temp": lambda s, g, t, l: s.new_empty(s.shape),
     "soft_nw_backward_full": lambda s, ga, g, t, l: _full(s, 2),
     "nw_marginals_backward": lambda s, ga, g, t, l: _full(s, 2),
+    # affine NW
+    "soft_nw_affine": lambda s, go, ge, t, l: _value_marginals(s),
+    "soft_nw_affine_float": lambda s, go, ge, t, l: _value_marginals(s),
+    "nw_affine_forward": lambda s, go, ge, t, l: _value_marginals(s),
+    "nw_affine_forward_t": lambda s, go, ge, t, l: _value_marginals(s),
+    "soft_nw_affine_with_grads":
+        lambda s, go, ge, t, l: tuple(_value_marginals(s)) + _per_batch(s, 3),
+    "nw_affine_value_grad_params": lambda s, go, ge, t, l: _per_batch(s, 3),
+    "soft_nw_affine_hvp": lambda s, v, go, ge, t, l: s.new_empty(s.shape),
+    "nw_affine_marginals_hvp": lambda s, v, go, ge, t, l: s.new_empty(s.shape),
+    "soft_nw_affine_param_jacobian": lambda s, p, go, ge, t, l: s.new_empty(s.shape),
+    "nw_affine_marginals_grad_gap_open": lambda s, go, ge, t, l: s.new_empty(s.shape),
+    "nw_affine_marginals_grad_gap_ext": lambda s, go, ge, t, l: s.new_empty(s.shape),
+    "nw_affine_marginals_grad_temp": lambda s, go, ge, t, l: s.new_empty(s.shape),
+    "soft_nw_affine_backward_full": lambda s, ga, go, ge, t, l: _full(s, 3),
+    "nw_affine_marginals_backward": lambda s, ga, go, ge, t, l: _full(s, 3),
 }
 
 for _name, _fn in _FAKES.items():

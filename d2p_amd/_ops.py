@@ -135,6 +135,22 @@ nw_marginals_hvp = _wrap("nw_marginals_hvp")
 nw_marginals_grad_gap = _wrap("nw_marginals_grad_gap")
 nw_marginals_grad_temp = _wrap("nw_marginals_grad_temp")
 
+# affine-gap Needleman-Wunsch
+soft_nw_affine = _wrap("soft_nw_affine")
+soft_nw_affine_float = _wrap("soft_nw_affine_float")
+soft_nw_affine_with_grads = _wrap("soft_nw_affine_with_grads")
+soft_nw_affine_hvp = _wrap("soft_nw_affine_hvp")
+soft_nw_affine_param_jacobian = _wrap("soft_nw_affine_param_jacobian")
+soft_nw_affine_backward_full = _wrap("soft_nw_affine_backward_full")
+nw_affine_forward = _wrap("nw_affine_forward")
+nw_affine_forward_t = _wrap("nw_affine_forward_t")
+nw_affine_value_grad_params = _wrap("nw_affine_value_grad_params")
+nw_affine_marginals_backward = _wrap("nw_affine_marginals_backward")
+nw_affine_marginals_hvp = _wrap("nw_affine_marginals_hvp")
+nw_affine_marginals_grad_gap_open = _wrap("nw_affine_marginals_grad_gap_open")
+nw_affine_marginals_grad_gap_ext = _wrap("nw_affine_marginals_grad_gap_ext")
+nw_affine_marginals_grad_temp = _wrap("nw_affine_marginals_grad_temp")
+
 # soft DTW
 soft_dtw = _wrap("soft_dtw")
 soft_dtw_float = _wrap("soft_dtw_float")

@@ -336,3 +336,38 @@ _nw_backward = _first_order_backward(soft_nw_with_grads, soft_nw_with_grads_tp,
                                      soft_nw_backward_full, soft_nw_backward_full_tp)
 soft_nw.register_autograd(_nw_backward, setup_context=_first_order_setup)
 soft_nw_float.register_autograd(_nw_backward, setup_context=_first_order_setup)
+
+# ------------------------------------------------------------------ affine-gap NW
+
+soft_nw_affine_with_grads = _define(
+    "soft_nw_affine_with_grads",
+    f"(Tensor scores, {_SWA_FLOAT}) -> (Tensor, Tensor, Tensor, Tensor, Tensor)",
+    _swa_grads_fake)
+soft_nw_affine_hvp = _define(
+    "soft_nw_affine_hvp", f"(Tensor scores, Tensor tangent, {_SWA_FLOAT}) -> Tensor",
+    lambda s, v, o, e, t, l: s.new_empty(s.shape))
+soft_nw_affine_param_jacobian = _define(
+    "soft_nw_affine_param_jacobian", f"(Tensor scores, int param_type, {_SWA_FLOAT}) -> Tensor",
+    lambda s, p, o, e, t, l: s.new_empty(s.shape))
+soft_nw_affine_backward_full = _define(
+    "soft_nw_affine_backward_full",
+    f"(Tensor scores, Tensor grad_alignment, {_SWA_FLOAT}) -> (Tensor, Tensor, Tensor, Tensor)",
+    _swa_full_fake)
+soft_nw_affine = _define(
+    "soft_nw_affine", "(Tensor scores, Tensor gap_open, Tensor gap_ext, Tensor temperature, "
+    "Tensor lengths) -> (Tensor, Tensor)", lambda s, o, e, t, l: _value_marginals_fake(s))
+soft_nw_affine_float = _define(
+    "soft_nw_affine_float", f"(Tensor scores, {_SWA_FLOAT}) -> (Tensor, Tensor)",
+    lambda s, o, e, t, l: _value_marginals_fake(s))
+soft_nw_affine_with_grads_tp = _define_tp(
+    "soft_nw_affine_with_grads", "Tensor scores", "Tensor? lengths",
+    "(Tensor, Tensor, Tensor, Tensor, Tensor)", _swa_grads_fake)
+soft_nw_affine_backward_full_tp = _define_tp(
+    "soft_nw_affine_backward_full", "Tensor scores, Tensor grad_alignment", "Tensor? lengths",
+    "(Tensor, Tensor, Tensor, Tensor)", _swa_full_fake)
+
+_nwa_backward = _first_order_backward(soft_nw_affine_with_grads, soft_nw_affine_with_grads_tp,
+                                      soft_nw_affine_backward_full,
+                                      soft_nw_affine_backward_full_tp)
+soft_nw_affine.register_autograd(_nwa_backward, setup_context=_first_order_setup)
+soft_nw_affine_float.register_autograd(_nwa_backward, setup_context=_first_order_setup)

@@ -601,28 +601,53 @@ Dims checked_dims_affine(const Tensor& x) {
     return d;
 }
 
+// /root/reference/src/nw_affine/torch_cuda.cpp:32-78 (global alignment)
+Dims checked_dims_nwa(const Tensor& x) {
+    TORCH_CHECK(x.dim() == 3, "scores must be 3D (B, L1, L2)");
+    auto dim = [](int64_t v, const char* name) {
+        TORCH_CHECK(v >= 0 && v <= std::numeric_limits<int>::max(), "scores dimension ", name,
+                    " must fit in int32, got ", v);
+        return (int)v;
+    };
+    Dims d{dim(x.size(0), "B"), dim(x.size(1), "L1"), dim(x.size(2), "L2")};
+    TORCH_CHECK(d.L1 <= std::numeric_limits<int>::max() - d.L2,
+                "scores dimensions L1 + L2 must fit in int32, got ", d.L1, " + ", d.L2);
+    const int64_t cells = 3 * (int64_t(d.L1) + 1) * (int64_t(d.L2) + 1);
+    TORCH_CHECK(cells <= std::numeric_limits<int>::max(),
+                "nw_affine alpha workspace size must fit in int32, got ", cells);
+    return d;
+}
+
+// the affine family: local (soft_sw_affine) or global (soft_nw_affine) alignment
+Dims checked_dims_aff(const Tensor& x, bool global) {
+    return global ? checked_dims_nwa(x) : checked_dims_affine(x);
+}
+
 struct SwaOut {
     Tensor partition, marginals, grad_open, grad_ext, grad_T;
 };
 
 SwaOut swa_run(const Tensor& scores, const Tensor& lengths, const Dims& d, float go, float ge,
-               float T) {
+               float T, bool global = false) {
     auto opt = scores.options();
     SwaOut o{torch::empty({d.B}, opt), torch::empty({d.B, d.L1, d.L2}, opt),
              torch::empty({d.B}, opt), torch::empty({d.B}, opt), torch::empty({d.B}, opt)};
-    const size_t ws_bytes = d2p_swa_workspace_bytes(d.B, d.L1, d.L2);
+    const size_t ws_bytes = global ? d2p_nwa_workspace_bytes(d.B, d.L1, d.L2)
+                                   : d2p_swa_workspace_bytes(d.B, d.L1, d.L2);
     Tensor ws = workspace(ws_bytes, scores);
-    D2P_CALL(d2p_swa_forward_marginals(
-        scores.data_ptr<float>(), lengths_ptr(lengths), d.B, d.L1, d.L2, go, ge, T,
-        o.partition.data_ptr<float>(), o.marginals.data_ptr<float>(),
-        o.grad_open.data_ptr<float>(), o.grad_ext.data_ptr<float>(), o.grad_T.data_ptr<float>(),
-        ws.data_ptr(), ws_bytes, current_stream()));
+    auto fn = global ? d2p_nwa_forward_marginals : d2p_swa_forward_marginals;
+    D2P_CALL(fn(scores.data_ptr<float>(), lengths_ptr(lengths), d.B, d.L1, d.L2, go, ge, T,
+                o.partition.data_ptr<float>(), o.marginals.data_ptr<float>(),
+                o.grad_open.data_ptr<float>(), o.grad_ext.data_ptr<float>(),
+                o.grad_T.data_ptr<float>(), ws.data_ptr(), ws_bytes, current_stream()));
     check_status(ws, d.B);
     return o;
 }
 
-Tensor swa_second_workspace(const Dims& d, const Tensor& like) {
-    return workspace(d2p_swa_second_workspace_bytes(d.B, d.L1, d.L2), like);
+Tensor swa_second_workspace(const Dims& d, const Tensor& like, bool global = false) {
+    return workspace(global ? d2p_nwa_second_workspace_bytes(d.B, d.L1, d.L2)
+                            : d2p_swa_second_workspace_bytes(d.B, d.L1, d.L2),
+                     like);
 }
 
 // returns (grad_scores [B,L1,L2], per-element <ga, dP/dopen>, <ga, dP/dext>, <ga, dP/dT> [B])
@@ -630,35 +655,38 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> swa_backward_full_run(const Tensor& s
                                                                  const Tensor& ga,
                                                                  const Tensor& lengths,
                                                                  const Dims& d, float go, float ge,
-                                                                 float T) {
+                                                                 float T, bool global = false) {
     auto opt = scores.options();
     Tensor gs = torch::empty({d.B, d.L1, d.L2}, opt);
     Tensor g_o = torch::empty({d.B}, opt), g_e = torch::empty({d.B}, opt);
     Tensor g_t = torch::empty({d.B}, opt);
-    Tensor ws = swa_second_workspace(d, scores);
-    D2P_CALL(d2p_swa_backward_full(scores.data_ptr<float>(), ga.data_ptr<float>(),
-                                   lengths_ptr(lengths), d.B, d.L1, d.L2, go, ge, T,
-                                   gs.data_ptr<float>(), g_o.data_ptr<float>(),
-                                   g_e.data_ptr<float>(), g_t.data_ptr<float>(), ws.data_ptr(),
-                                   ws.numel(), current_stream()));
+    Tensor ws = swa_second_workspace(d, scores, global);
+    auto fn = global ? d2p_nwa_backward_full : d2p_swa_backward_full;
+    D2P_CALL(fn(scores.data_ptr<float>(), ga.data_ptr<float>(), lengths_ptr(lengths), d.B, d.L1,
+                d.L2, go, ge, T, gs.data_ptr<float>(), g_o.data_ptr<float>(),
+                g_e.data_ptr<float>(), g_t.data_ptr<float>(), ws.data_ptr(), ws.numel(),
+                current_stream()));
     check_status(ws, d.B);
     return {gs, g_o, g_e, g_t};
 }
 
 // Autograd semantics of SoftSWAffineCUDAFunction
-// (/root/reference/src/sw_affine/torch_cuda.cpp:126-400): outputs {value, marginals};
-// d value / d scores = marginals; parameter gradients sum_b grad_value[b] * dS_b/dtheta.
+// (/root/reference/src/sw_affine/torch_cuda.cpp:126-400) and of
+// SoftNWAffineCUDAFunction (/root/reference/src/nw_affine/torch_cuda.cpp:164-345):
+// outputs {value, marginals}; d value / d scores = marginals; parameter gradients
+// sum_b grad_value[b] * dS_b/dtheta.
 tensor_list swa_autograd_forward(AutogradContext* ctx, const Tensor& scores, const Tensor& lengths,
-                                 double go, double ge, double T) {
+                                 double go, double ge, double T, bool global) {
     ctx->set_materialize_grads(false);
     CHECK_INPUT_DEV(scores);
-    Dims d = checked_dims_affine(scores);
+    Dims d = checked_dims_aff(scores, global);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
-    SwaOut o = swa_run(scores, lengths, d, (float)go, (float)ge, (float)T);
+    SwaOut o = swa_run(scores, lengths, d, (float)go, (float)ge, (float)T, global);
     ctx->save_for_backward({scores, lengths, o.marginals, o.grad_open, o.grad_ext, o.grad_T});
     ctx->saved_data["gap_open"] = go;
     ctx->saved_data["gap_ext"] = ge;
     ctx->saved_data["temperature"] = T;
+    ctx->saved_data["global"] = global;
     return {o.partition, o.marginals};
 }
 
@@ -678,13 +706,15 @@ tensor_list swa_autograd_backward(AutogradContext* ctx, const tensor_list& grads
     }
     if (grad_marg.defined() && grad_marg.numel() > 0) {
         // marginal path: HVP against the cotangent plus its dot products with
-        // dP/dopen, dP/dext and dP/dT (/root/reference/src/sw_affine/torch_cuda.cpp:284-393)
+        // dP/dopen, dP/dext and dP/dT (/root/reference/src/sw_affine/torch_cuda.cpp:284-393,
+        // /root/reference/src/nw_affine/torch_cuda.cpp:277-342)
         Tensor gm = prepare_cotangent(grad_marg, scores, "grad_posteriors");
-        Dims d = checked_dims_affine(scores);
+        const bool global = ctx->saved_data["global"].toBool();
+        Dims d = checked_dims_aff(scores, global);
         auto r = swa_backward_full_run(scores, gm, lengths, d,
                                        (float)ctx->saved_data["gap_open"].toDouble(),
                                        (float)ctx->saved_data["gap_ext"].toDouble(),
-                                       (float)ctx->saved_data["temperature"].toDouble());
+                                       (float)ctx->saved_data["temperature"].toDouble(), global);
         gs = gs.defined() ? gs + std::get<0>(r) : std::get<0>(r);
         Tensor to = std::get<1>(r).sum().reshape({1}), te = std::get<2>(r).sum().reshape({1});
         Tensor tt = std::get<3>(r).sum().reshape({1});
@@ -698,130 +728,206 @@ tensor_list swa_autograd_backward(AutogradContext* ctx, const tensor_list& grads
 class SoftSWAffineFloatFunction : public torch::autograd::Function<SoftSWAffineFloatFunction> {
    public:
     static tensor_list forward(AutogradContext* ctx, Tensor scores,
-                               c10::optional<Tensor> lengths, double go, double ge, double T) {
-        return swa_autograd_forward(ctx, scores, lengths.value_or(Tensor()), go, ge, T);
+                               c10::optional<Tensor> lengths, double go, double ge, double T,
+                               bool global) {
+        return swa_autograd_forward(ctx, scores, lengths.value_or(Tensor()), go, ge, T, global);
     }
     static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
         auto g = swa_autograd_backward(ctx, grads, false, false, false);
-        return {g[0], Tensor(), Tensor(), Tensor(), Tensor()};
+        return {g[0], Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
     }
 };
 
 class SoftSWAffineTensorFunction : public torch::autograd::Function<SoftSWAffineTensorFunction> {
    public:
     static tensor_list forward(AutogradContext* ctx, Tensor scores, Tensor go_t, Tensor ge_t,
-                               Tensor temp_t, Tensor lengths, double go, double ge, double T) {
-        return swa_autograd_forward(ctx, scores, lengths, go, ge, T);
+                               Tensor temp_t, Tensor lengths, double go, double ge, double T,
+                               bool global) {
+        return swa_autograd_forward(ctx, scores, lengths, go, ge, T, global);
     }
     static tensor_list backward(AutogradContext* ctx, tensor_list grads) {
         auto g = swa_autograd_backward(ctx, grads, ctx->needs_input_grad(1),
                                        ctx->needs_input_grad(2), ctx->needs_input_grad(3));
-        return {g[0], g[1], g[2], g[3], Tensor(), Tensor(), Tensor(), Tensor()};
+        return {g[0], g[1], g[2], g[3], Tensor(), Tensor(), Tensor(), Tensor(), Tensor()};
     }
 };
 
-std::vector<Tensor> swa_t(Tensor scores, Tensor gap_open, Tensor gap_ext, Tensor temperature,
-                          Tensor lengths) {
+std::vector<Tensor> aff_t(Tensor scores, Tensor gap_open, Tensor gap_ext, Tensor temperature,
+                          Tensor lengths, bool global) {
     CHECK_INPUT_DEV(scores);
-    Dims d = checked_dims_affine(scores);
+    Dims d = checked_dims_aff(scores, global);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
     const float go = scalar_value(gap_open, "gap_open");
     const float ge = scalar_value(gap_ext, "gap_ext");
     const float T = scalar_value(temperature, "temperature");
     Tensor l = resolve_lengths(lengths, d, scores.device());
-    return SoftSWAffineTensorFunction::apply(scores, gap_open, gap_ext, temperature, l, go, ge, T);
+    return SoftSWAffineTensorFunction::apply(scores, gap_open, gap_ext, temperature, l, go, ge, T,
+                                             global);
 }
 
-std::vector<Tensor> swa_float(Tensor scores, double gap_open, double gap_ext, double temperature,
-                              c10::optional<Tensor> lengths) {
+std::vector<Tensor> aff_float(Tensor scores, double gap_open, double gap_ext, double temperature,
+                              c10::optional<Tensor> lengths, bool global) {
     CHECK_INPUT_DEV(scores);
-    Dims d = checked_dims_affine(scores);
+    Dims d = checked_dims_aff(scores, global);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
     Tensor l = resolve_lengths(lengths, d, scores.device());
     return SoftSWAffineFloatFunction::apply(scores, lengths_arg(l), gap_open, gap_ext,
-                                            temperature);
+                                            temperature, global);
 }
 
-std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> swa_with_grads(Tensor scores, double gap_open,
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> aff_with_grads(Tensor scores, double gap_open,
                                                                   double gap_ext,
                                                                   double temperature,
-                                                                  c10::optional<Tensor> lengths) {
+                                                                  c10::optional<Tensor> lengths,
+                                                                  bool global) {
     CHECK_INPUT_DEV(scores);
-    Dims d = checked_dims_affine(scores);
+    Dims d = checked_dims_aff(scores, global);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
     Tensor l = resolve_lengths(lengths, d, scores.device());
-    SwaOut o = swa_run(scores, l, d, (float)gap_open, (float)gap_ext, (float)temperature);
+    SwaOut o = swa_run(scores, l, d, (float)gap_open, (float)gap_ext, (float)temperature, global);
     return {o.partition, o.marginals, o.grad_open, o.grad_ext, o.grad_T};
 }
 
-std::tuple<Tensor, Tensor, Tensor> swa_value_grad_params(Tensor s, double go, double ge, double t,
-                                                         c10::optional<Tensor> l) {
-    auto r = swa_with_grads(s, go, ge, t, l);
-    return {std::get<2>(r), std::get<3>(r), std::get<4>(r)};
-}
-
-// /root/reference/src/sw_affine/torch_cuda.cpp:508-578
-Tensor swa_hvp(Tensor scores, Tensor tangent, double gap_open, double gap_ext, double temperature,
-               c10::optional<Tensor> lengths) {
+// /root/reference/src/sw_affine/torch_cuda.cpp:508-578,
+// /root/reference/src/nw_affine/torch_cuda.cpp:435-482
+Tensor aff_hvp(Tensor scores, Tensor tangent, double gap_open, double gap_ext, double temperature,
+               c10::optional<Tensor> lengths, bool global) {
     CHECK_INPUT_DEV(scores);
     CHECK_INPUT_DEV(tangent);
-    TORCH_CHECK(scores.dim() == 3, "scores must be 3D");
+    TORCH_CHECK(scores.dim() == 3, global ? "scores must be 3D (B, L1, L2)" : "scores must be 3D");
+    if (global) TORCH_CHECK(tangent.dim() == 3, "tangent must be 3D (B, L1, L2)");
     TORCH_CHECK(scores.sizes() == tangent.sizes(), "scores and tangent must have same shape");
     TORCH_CHECK(tangent.device() == scores.device(), "tangent must be on same device as scores, got ",
                 tangent.device(), " vs ", scores.device());
-    Dims d = checked_dims_affine(scores);
+    Dims d = checked_dims_aff(scores, global);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
     Tensor l = resolve_lengths(lengths, d, scores.device());
     Tensor out = torch::empty({d.B, d.L1, d.L2}, scores.options());
-    Tensor ws = swa_second_workspace(d, scores);
-    D2P_CALL(d2p_swa_hvp(scores.data_ptr<float>(), tangent.data_ptr<float>(), lengths_ptr(l),
-                         d.B, d.L1, d.L2, (float)gap_open, (float)gap_ext, (float)temperature,
-                         out.data_ptr<float>(), ws.data_ptr(), ws.numel(), current_stream()));
+    Tensor ws = swa_second_workspace(d, scores, global);
+    auto fn = global ? d2p_nwa_hvp : d2p_swa_hvp;
+    D2P_CALL(fn(scores.data_ptr<float>(), tangent.data_ptr<float>(), lengths_ptr(l), d.B, d.L1,
+                d.L2, (float)gap_open, (float)gap_ext, (float)temperature, out.data_ptr<float>(),
+                ws.data_ptr(), ws.numel(), current_stream()));
     check_status(ws, d.B);
     return out;
 }
 
-// /root/reference/src/sw_affine/torch_cuda.cpp:580-679
-Tensor swa_param_jacobian(Tensor scores, int64_t param_type, double gap_open, double gap_ext,
-                          double temperature, c10::optional<Tensor> lengths) {
+// /root/reference/src/sw_affine/torch_cuda.cpp:580-679,
+// /root/reference/src/nw_affine/torch_cuda.cpp:484-553
+Tensor aff_param_jacobian(Tensor scores, int64_t param_type, double gap_open, double gap_ext,
+                          double temperature, c10::optional<Tensor> lengths, bool global) {
     CHECK_INPUT_DEV(scores);
-    TORCH_CHECK(scores.dim() == 3, "scores must be 3D");
+    TORCH_CHECK(scores.dim() == 3, global ? "scores must be 3D (B, L1, L2)" : "scores must be 3D");
     TORCH_CHECK(param_type >= 0 && param_type <= 2, "param_type must be 0, 1, or 2");
-    Dims d = checked_dims_affine(scores);
+    Dims d = checked_dims_aff(scores, global);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
     Tensor l = resolve_lengths(lengths, d, scores.device());
     Tensor out = torch::empty({d.B, d.L1, d.L2}, scores.options());
-    Tensor ws = swa_second_workspace(d, scores);
-    D2P_CALL(d2p_swa_param_jacobian(scores.data_ptr<float>(), (int)param_type, lengths_ptr(l),
-                                    d.B, d.L1, d.L2, (float)gap_open, (float)gap_ext,
-                                    (float)temperature, out.data_ptr<float>(), ws.data_ptr(),
-                                    ws.numel(), current_stream()));
+    Tensor ws = swa_second_workspace(d, scores, global);
+    auto fn = global ? d2p_nwa_param_jacobian : d2p_swa_param_jacobian;
+    D2P_CALL(fn(scores.data_ptr<float>(), (int)param_type, lengths_ptr(l), d.B, d.L1, d.L2,
+                (float)gap_open, (float)gap_ext, (float)temperature, out.data_ptr<float>(),
+                ws.data_ptr(), ws.numel(), current_stream()));
     check_status(ws, d.B);
     return out;
 }
 
-// /root/reference/src/sw_affine/torch_cuda.cpp:681-817
-std::tuple<Tensor, Tensor, Tensor, Tensor> swa_backward_full(Tensor scores, Tensor grad_alignment,
+// /root/reference/src/sw_affine/torch_cuda.cpp:681-817,
+// /root/reference/src/nw_affine/torch_cuda.cpp:555-665
+std::tuple<Tensor, Tensor, Tensor, Tensor> aff_backward_full(Tensor scores, Tensor grad_alignment,
                                                              double gap_open, double gap_ext,
                                                              double temperature,
-                                                             c10::optional<Tensor> lengths) {
+                                                             c10::optional<Tensor> lengths,
+                                                             bool global) {
     CHECK_INPUT_DEV(scores);
     TORCH_CHECK(scores.dim() == 3, "scores must be 3D (B, L1, L2)");
+    if (global) TORCH_CHECK(grad_alignment.dim() == 3, "grad_alignment must be 3D (B, L1, L2)");
     TORCH_CHECK(grad_alignment.sizes() == scores.sizes(),
                 "grad_alignment must have same shape as scores");
     TORCH_CHECK(grad_alignment.is_cuda(), "grad_alignment must be a CUDA tensor");
     TORCH_CHECK(grad_alignment.device() == scores.device(),
                 "grad_alignment must be on same device as scores, got ", grad_alignment.device(),
                 " vs ", scores.device());
-    Dims d = checked_dims_affine(scores);
+    Dims d = checked_dims_aff(scores, global);
     c10::hip::HIPGuardMasqueradingAsCUDA guard(scores.device());
     Tensor l = resolve_lengths(lengths, d, scores.device());
     Tensor ga = grad_alignment.contiguous();
     if (ga.scalar_type() != torch::kFloat32) ga = ga.to(torch::kFloat32);
     auto r = swa_backward_full_run(scores, ga, l, d, (float)gap_open, (float)gap_ext,
-                                   (float)temperature);
+                                   (float)temperature, global);
     return {std::get<0>(r), std::get<1>(r).sum().reshape({1}), std::get<2>(r).sum().reshape({1}),
             std::get<3>(r).sum().reshape({1})};
+}
+
+// soft_sw_affine ops
+std::vector<Tensor> swa_t(Tensor s, Tensor go, Tensor ge, Tensor t, Tensor l) {
+    return aff_t(s, go, ge, t, l, false);
+}
+std::vector<Tensor> swa_float(Tensor s, double go, double ge, double t, c10::optional<Tensor> l) {
+    return aff_float(s, go, ge, t, l, false);
+}
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> swa_with_grads(Tensor s, double go, double ge,
+                                                                  double t,
+                                                                  c10::optional<Tensor> l) {
+    return aff_with_grads(s, go, ge, t, l, false);
+}
+std::tuple<Tensor, Tensor, Tensor> swa_value_grad_params(Tensor s, double go, double ge, double t,
+                                                         c10::optional<Tensor> l) {
+    auto r = swa_with_grads(s, go, ge, t, l);
+    return {std::get<2>(r), std::get<3>(r), std::get<4>(r)};
+}
+Tensor swa_hvp(Tensor s, Tensor v, double go, double ge, double t, c10::optional<Tensor> l) {
+    return aff_hvp(s, v, go, ge, t, l, false);
+}
+Tensor swa_param_jacobian(Tensor s, int64_t p, double go, double ge, double t,
+                          c10::optional<Tensor> l) {
+    return aff_param_jacobian(s, p, go, ge, t, l, false);
+}
+std::tuple<Tensor, Tensor, Tensor, Tensor> swa_backward_full(Tensor s, Tensor ga, double go,
+                                                             double ge, double t,
+                                                             c10::optional<Tensor> l) {
+    return aff_backward_full(s, ga, go, ge, t, l, false);
+}
+
+// soft_nw_affine ops (/root/reference/src/nw_affine/registry.cpp:35-50): the same
+// sweeps in global-alignment mode
+std::vector<Tensor> nwa_t(Tensor s, Tensor go, Tensor ge, Tensor t, Tensor l) {
+    return aff_t(s, go, ge, t, l, true);
+}
+std::vector<Tensor> nwa_float(Tensor s, double go, double ge, double t, c10::optional<Tensor> l) {
+    return aff_float(s, go, ge, t, l, true);
+}
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> nwa_with_grads(Tensor s, double go, double ge,
+                                                                  double t,
+                                                                  c10::optional<Tensor> l) {
+    return aff_with_grads(s, go, ge, t, l, true);
+}
+// (score, grad_gap_open, grad_gap_ext): /root/reference/src/nw_affine/torch_cuda.cpp:687-698
+std::tuple<Tensor, Tensor, Tensor> nwa_value_grad_params(Tensor s, double go, double ge, double t,
+                                                         c10::optional<Tensor> l) {
+    auto r = nwa_with_grads(s, go, ge, t, l);
+    return {std::get<0>(r), std::get<2>(r), std::get<3>(r)};
+}
+Tensor nwa_hvp(Tensor s, Tensor v, double go, double ge, double t, c10::optional<Tensor> l) {
+    return aff_hvp(s, v, go, ge, t, l, true);
+}
+Tensor nwa_param_jacobian(Tensor s, int64_t p, double go, double ge, double t,
+                          c10::optional<Tensor> l) {
+    return aff_param_jacobian(s, p, go, ge, t, l, true);
+}
+std::tuple<Tensor, Tensor, Tensor, Tensor> nwa_backward_full(Tensor s, Tensor ga, double go,
+                                                             double ge, double t,
+                                                             c10::optional<Tensor> l) {
+    return aff_backward_full(s, ga, go, ge, t, l, true);
+}
+Tensor nwa_marg_grad_open(Tensor s, double go, double ge, double t, c10::optional<Tensor> l) {
+    return nwa_param_jacobian(s, 0, go, ge, t, l);
+}
+Tensor nwa_marg_grad_ext(Tensor s, double go, double ge, double t, c10::optional<Tensor> l) {
+    return nwa_param_jacobian(s, 1, go, ge, t, l);
+}
+Tensor nwa_marg_grad_temp(Tensor s, double go, double ge, double t, c10::optional<Tensor> l) {
+    return nwa_param_jacobian(s, 2, go, ge, t, l);
 }
 
 // sw_affine_marginals_grad_{gap_open,gap_ext,temp}
@@ -1069,6 +1175,22 @@ TORCH_LIBRARY(d2p, m) {
     m.def("sw_affine_marginals_grad_gap_ext(Tensor scores, float gap_open, float gap_ext, float temp, Tensor? lengths) -> Tensor");
     m.def("sw_affine_marginals_grad_temp(Tensor scores, float gap_open, float gap_ext, float temp, Tensor? lengths) -> Tensor");
 
+    // /root/reference/src/nw_affine/registry.cpp:35-50
+    m.def("soft_nw_affine(Tensor scores, Tensor gap_open, Tensor gap_ext, Tensor temperature, Tensor lengths) -> Tensor[]");
+    m.def("soft_nw_affine_float(Tensor scores, float gap_open, float gap_ext, float temperature, Tensor? lengths) -> Tensor[]");
+    m.def("soft_nw_affine_with_grads(Tensor scores, float gap_open, float gap_ext, float temperature, Tensor? lengths) -> (Tensor, Tensor, Tensor, Tensor, Tensor)");
+    m.def("soft_nw_affine_hvp(Tensor scores, Tensor tangent, float gap_open, float gap_ext, float temperature, Tensor? lengths) -> Tensor");
+    m.def("soft_nw_affine_param_jacobian(Tensor scores, int param_type, float gap_open, float gap_ext, float temperature, Tensor? lengths) -> Tensor");
+    m.def("soft_nw_affine_backward_full(Tensor scores, Tensor grad_alignment, float gap_open, float gap_ext, float temperature, Tensor? lengths) -> (Tensor, Tensor, Tensor, Tensor)");
+    m.def("nw_affine_forward(Tensor scores, float gap_open, float gap_ext, float temp, Tensor? lengths) -> Tensor[]");
+    m.def("nw_affine_forward_t(Tensor scores, Tensor gap_open, Tensor gap_ext, Tensor temp, Tensor lengths) -> Tensor[]");
+    m.def("nw_affine_value_grad_params(Tensor scores, float gap_open, float gap_ext, float temp, Tensor? lengths) -> (Tensor, Tensor, Tensor)");
+    m.def("nw_affine_marginals_backward(Tensor scores, Tensor grad_marginals, float gap_open, float gap_ext, float temp, Tensor? lengths) -> (Tensor, Tensor, Tensor, Tensor)");
+    m.def("nw_affine_marginals_hvp(Tensor scores, Tensor v, float gap_open, float gap_ext, float temp, Tensor? lengths) -> Tensor");
+    m.def("nw_affine_marginals_grad_gap_open(Tensor scores, float gap_open, float gap_ext, float temp, Tensor? lengths) -> Tensor");
+    m.def("nw_affine_marginals_grad_gap_ext(Tensor scores, float gap_open, float gap_ext, float temp, Tensor? lengths) -> Tensor");
+    m.def("nw_affine_marginals_grad_temp(Tensor scores, float gap_open, float gap_ext, float temp, Tensor? lengths) -> Tensor");
+
     // /root/reference/src/dtw/registry.cpp:127-132
     // /root/reference/src/nw/registry.cpp:35-45 (first-order operators)
     m.def("soft_nw(Tensor scores, Tensor gap, Tensor temperature, Tensor lengths) -> Tensor[]");
@@ -1136,6 +1258,20 @@ TORCH_LIBRARY_IMPL(d2p, CUDA, m) {
     m.impl("sw_affine_marginals_grad_gap_open", swa_marg_grad_open);
     m.impl("sw_affine_marginals_grad_gap_ext", swa_marg_grad_ext);
     m.impl("sw_affine_marginals_grad_temp", swa_marg_grad_temp);
+    m.impl("soft_nw_affine", nwa_t);
+    m.impl("soft_nw_affine_float", nwa_float);
+    m.impl("soft_nw_affine_with_grads", nwa_with_grads);
+    m.impl("soft_nw_affine_hvp", nwa_hvp);
+    m.impl("soft_nw_affine_param_jacobian", nwa_param_jacobian);
+    m.impl("soft_nw_affine_backward_full", nwa_backward_full);
+    m.impl("nw_affine_forward", nwa_float);
+    m.impl("nw_affine_forward_t", nwa_t);
+    m.impl("nw_affine_value_grad_params", nwa_value_grad_params);
+    m.impl("nw_affine_marginals_backward", nwa_backward_full);
+    m.impl("nw_affine_marginals_hvp", nwa_hvp);
+    m.impl("nw_affine_marginals_grad_gap_open", nwa_marg_grad_open);
+    m.impl("nw_affine_marginals_grad_gap_ext", nwa_marg_grad_ext);
+    m.impl("nw_affine_marginals_grad_temp", nwa_marg_grad_temp);
 
     m.impl("soft_dtw", dtw_t);
     m.impl("soft_dtw_float", dtw_float);
@@ -1162,6 +1298,10 @@ TORCH_LIBRARY_IMPL(d2p, AutogradCUDA, m) {
     m.impl("soft_nw_float", soft_nw_float);
     m.impl("nw_forward", nw_forward);
     m.impl("nw_forward_t", nw_forward_t);
+    m.impl("soft_nw_affine", nwa_t);
+    m.impl("soft_nw_affine_float", nwa_float);
+    m.impl("nw_affine_forward", nwa_float);
+    m.impl("nw_affine_forward_t", nwa_t);
 }
 
 namespace {
@@ -1180,7 +1320,12 @@ const char* const kAllOps[] = {
     "soft_nw_float", "soft_nw_with_grads", "soft_nw_hvp", "soft_nw_param_jacobian",
     "soft_nw_backward_full", "nw_forward", "nw_forward_t", "nw_value_grad_params",
     "nw_marginals_backward", "nw_marginals_hvp", "nw_marginals_grad_gap",
-    "nw_marginals_grad_temp"};
+    "nw_marginals_grad_temp", "soft_nw_affine", "soft_nw_affine_float",
+    "soft_nw_affine_with_grads", "soft_nw_affine_hvp", "soft_nw_affine_param_jacobian",
+    "soft_nw_affine_backward_full", "nw_affine_forward", "nw_affine_forward_t",
+    "nw_affine_value_grad_params", "nw_affine_marginals_backward", "nw_affine_marginals_hvp",
+    "nw_affine_marginals_grad_gap_open", "nw_affine_marginals_grad_gap_ext",
+    "nw_affine_marginals_grad_temp"};
 }  // namespace
 
 TORCH_LIBRARY_IMPL(d2p, CPU, m) {

@@ -1,24 +1,26 @@
-"""Soft Needleman-Wunsch (global alignment, linear gap) on the HIP device.
+"""Soft Needleman-Wunsch (global alignment) on the HIP device, linear and affine gaps.
 
-Same API as the reference's ``d2p.nw`` for the linear-gap family
-(/root/reference/d2p/nw.py:68-200): ``soft_nw`` returns ``NWResult(score,
-alignment)``; ``SoftNW`` is the ``nn.Module`` wrapper with optional learnable gap
-and temperature.  The value is alpha[L1, L2] of the global recurrence
-(alpha[i,0] = i*gap, alpha[0,j] = j*gap, no restart term); gradients flow through
-the value (scores, and gap / temperature when given as tensors) and through the
-alignment output (the second-order sweeps: HVP against the alignment cotangent and
-its dot products with dP/dgap and dP/dT).  The affine-gap NW family is not part of
-this build.
+Same API as the reference's ``d2p.nw`` (/root/reference/d2p/nw.py:68-240):
+``soft_nw`` and ``soft_nw_affine`` return ``NWResult(score, alignment)``; ``SoftNW``
+and ``SoftNWAffine`` are the ``nn.Module`` wrappers with optional learnable
+parameters.  The linear-gap value is alpha[L1, L2] of the global recurrence
+(alpha[i,0] = i*gap, alpha[0,j] = j*gap, no restart term); the affine-gap value is
+the LSE of the terminal cell's three states (M, I, D), with the boundary chains
+I[i,0] = open + (i-1) ext and D[0,j] = open + (j-1) ext.  Gradients flow through the
+value (scores, and the parameters when given as tensors) and through the alignment
+output (the second-order sweeps: HVP against the alignment cotangent and its dot
+products with the parameter Jacobians of the marginals).
 """
 from __future__ import annotations
 
+import warnings
 from typing import NamedTuple, Optional, Union
 
 import torch
 import torch.nn as nn
 
 from . import _ops
-from .sw import _validate_gap, _validate_temperature
+from .sw import _validate_temperature
 
 Param = Union[float, torch.Tensor]
 
@@ -28,6 +30,13 @@ class NWResult(NamedTuple):
     marginal probability that each cell pair is aligned [B, L1, L2]."""
     score: torch.Tensor
     alignment: torch.Tensor
+
+
+def _validate_gap(gap: Param, name: str = "gap") -> None:
+    """Warns on a positive float gap (the text of /root/reference/d2p/nw.py:54-60)."""
+    if isinstance(gap, (int, float)) and gap > 0:
+        warnings.warn(f"{name}={gap} is positive. Gap penalties are typically negative.",
+                      UserWarning, stacklevel=3)
 
 
 def _make_lengths(scores: torch.Tensor) -> torch.Tensor:
@@ -77,3 +86,60 @@ class SoftNW(nn.Module):
             lengths = _make_lengths(scores)
         out = _ops.soft_nw(scores, self.gap, self.temperature, lengths)
         return NWResult(out[0], out[1])
+
+
+def soft_nw_affine(scores: torch.Tensor, gap_open: Param = -2.0, gap_ext: Param = -0.5,
+                   temperature: Param = 1.0,
+                   lengths: Optional[torch.Tensor] = None) -> NWResult:
+    """Soft Needleman-Wunsch global alignment of scores [B, L1, L2] with affine gaps
+    (a gap of length k costs gap_open + (k - 1) * gap_ext)."""
+    _validate_temperature(temperature)
+    _validate_gap(gap_open, "gap_open")
+    _validate_gap(gap_ext, "gap_ext")
+    if lengths is None:
+        lengths = _make_lengths(scores)
+    params = [gap_open, gap_ext, temperature]
+    if any(isinstance(p, torch.Tensor) for p in params):
+        params = [p if isinstance(p, torch.Tensor) else torch.tensor([p], device=scores.device)
+                  for p in params]
+        out = _ops.soft_nw_affine(scores, *params, lengths)
+    else:
+        out = _ops.soft_nw_affine_float(scores, *params, lengths)
+    return NWResult(out[0], out[1])
+
+
+class SoftNWAffine(nn.Module):
+    """Affine-gap soft Needleman-Wunsch as a module; ``learnable=True`` makes
+    gap_open, gap_ext and temperature parameters."""
+
+    def __init__(self, gap_open: float = -2.0, gap_ext: float = -0.5, temperature: float = 1.0,
+                 learnable: bool = False):
+        super().__init__()
+        if temperature <= 0:
+            raise ValueError(f"temperature must be positive, got {temperature}")
+        for name, v in (("gap_open", gap_open), ("gap_ext", gap_ext),
+                        ("temperature", temperature)):
+            t = torch.tensor([v])
+            if learnable:
+                setattr(self, name, nn.Parameter(t))
+            else:
+                self.register_buffer(name, t)
+
+    def forward(self, scores: torch.Tensor, lengths: Optional[torch.Tensor] = None) -> NWResult:
+        if lengths is None:
+            lengths = _make_lengths(scores)
+        out = _ops.soft_nw_affine(scores, self.gap_open, self.gap_ext, self.temperature, lengths)
+        return NWResult(out[0], out[1])
+
+
+# low-level re-exports, as in /root/reference/d2p/nw.py:243-256
+soft_nw_forward = _ops.soft_nw_float
+soft_nw_with_grads = _ops.soft_nw_with_grads
+soft_nw_hvp = _ops.soft_nw_hvp
+soft_nw_param_jacobian = _ops.soft_nw_param_jacobian
+soft_nw_backward_full = _ops.soft_nw_backward_full
+soft_nw_affine_forward = _ops.soft_nw_affine_float
+soft_nw_affine_with_grads = _ops.soft_nw_affine_with_grads
+soft_nw_affine_hvp = _ops.soft_nw_affine_hvp
+soft_nw_affine_param_jacobian = _ops.soft_nw_affine_param_jacobian
+soft_nw_affine_backward_full = _ops.soft_nw_affine_backward_full

@@ -21,4 +21,9 @@ from .._ops import (  # noqa: F401
     soft_nw, soft_nw_float, soft_nw_with_grads, nw_forward, nw_forward_t, nw_value_grad_params,
     soft_nw_hvp, soft_nw_param_jacobian, soft_nw_backward_full, nw_marginals_backward,
     nw_marginals_hvp, nw_marginals_grad_gap, nw_marginals_grad_temp,
+    soft_nw_affine, soft_nw_affine_float, soft_nw_affine_with_grads, soft_nw_affine_hvp,
+    soft_nw_affine_param_jacobian, soft_nw_affine_backward_full, nw_affine_forward,
+    nw_affine_forward_t, nw_affine_value_grad_params, nw_affine_marginals_backward,
+    nw_affine_marginals_hvp, nw_affine_marginals_grad_gap_open, nw_affine_marginals_grad_gap_ext,
+    nw_affine_marginals_grad_temp,
 )

@@ -109,7 +109,7 @@ def test_torch_compile_nw(cuda):
     assert torch.allclose(xc.grad, xe.grad, rtol=1e-5, atol=1e-5)
 
 
-@pytest.mark.parametrize("family", ["sw", "nw", "swa", "dtw"])
+@pytest.mark.parametrize("family", ["sw", "nw", "swa", "nwa", "dtw"])
 def test_torch_compile_learnable_parameters(cuda, family):
     """Modules with learnable parameters under torch.compile: the compiled backward
     runs the kernels with the forward's own gap/temperature values (tensors saved for
@@ -125,6 +125,8 @@ def test_torch_compile_learnable_parameters(cuda, family):
             "swa": lambda: d2p_amd.SoftSWAffine(gap_open=-1.5, gap_ext=-0.4, temperature=0.6,
                                                 learn_gap_open=True, learn_gap_ext=True,
                                                 learn_temperature=True),
+            "nwa": lambda: d2p_amd.SoftNWAffine(gap_open=-1.5, gap_ext=-0.4, temperature=0.6,
+                                                learnable=True),
             "dtw": lambda: d2p_amd.SoftDTW(temperature=0.6, learnable=True)}[family]
 
     def run(mod, x):

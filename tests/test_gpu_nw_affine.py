@@ -216,3 +216,98 @@ def test_nwa_backward_full(cuda):
         ref = (J.astype(np.float64) * W).sum(axis=(1, 2))
         tol = 1e-5 * np.abs(J * W).sum(axis=(1, 2)) + 1e-6
         assert np.all(np.abs(g.cpu().numpy() - ref) <= tol), (NAMES[p], g.cpu().numpy(), ref)
+
+
+# ------------------------------------------------------------------ torch API
+
+def test_nwa_api_value_path(cuda):
+    """soft_nw_affine's value backpropagates through the marginals; tensor gap_open,
+    gap_ext and temperature receive the batch sums of dS/dX (against the double
+    oracle); float parameters and the module give the same value."""
+    import d2p_amd
+    s = _seeded(60, (3, 50, 40))
+    x = s.to(cuda).requires_grad_(True)
+    go = torch.tensor([-1.8], device=cuda, requires_grad=True)
+    ge = torch.tensor([-0.4], device=cuda, requires_grad=True)
+    T = torch.tensor([0.9], device=cuda, requires_grad=True)
+    res = d2p_amd.soft_nw_affine(x, gap_open=go, gap_ext=ge, temperature=T)
+    w = torch.tensor([1.0, -2.0, 0.5], device=cuda)
+    (res.score * w).sum().backward()
+    ev, em, eo, ee, et = O.get("oracle64").soft_nw_affine(s.numpy().astype(np.float64), -1.8,
+                                                          -0.4, 0.9)
+    np.testing.assert_allclose(res.score.detach().cpu().numpy(), ev, rtol=1e-5, atol=1e-5)
+    wn = w.cpu().numpy()
+    assert np.abs(x.grad.cpu().numpy() - em * wn[:, None, None]).max() <= 2e-4
+    for g, e in ((go, eo), (ge, ee), (T, et)):
+        np.testing.assert_allclose(g.grad.cpu().numpy(), [(e * wn).sum()], rtol=1e-3, atol=1e-3)
+    r2 = d2p_amd.soft_nw_affine(s.to(cuda), gap_open=-1.8, gap_ext=-0.4, temperature=0.9)
+    torch.testing.assert_close(r2.score, res.score.detach(), rtol=0, atol=0)
+    m = d2p_amd.SoftNWAffine(gap_open=-1.8, gap_ext=-0.4, temperature=0.9).to(cuda)
+    torch.testing.assert_close(m(s.to(cuda)).score, res.score.detach(), rtol=0, atol=0)
+
+
+def test_nwa_marginal_path_autograd(cuda):
+    """loss = <W, alignment> + 0.5 sum(score): d loss / d scores = H W + 0.5 P and the
+    parameter gradients <W, dP/dX> + 0.5 sum dS/dX, the latter against the double
+    dot product of the GPU's own (entry-pinned) Jacobians."""
+    import d2p_amd
+    from _parity import dot_consistent
+    s = _seeded(31, (2, 40, 45))
+    W = _seeded(32, (2, 40, 45))
+    x = s.to(cuda).requires_grad_(True)
+    ps = [torch.tensor([v], device=cuda, requires_grad=True) for v in (-2.0, -0.5, 0.8)]
+    res = d2p_amd.soft_nw_affine(x, gap_open=ps[0], gap_ext=ps[1], temperature=ps[2])
+    ((res.alignment * W.to(cuda)).sum() + 0.5 * res.score.sum()).backward()
+    k = O.get("oracle")
+    _, rm, _, _, _ = k.soft_nw_affine(s.numpy(), -2.0, -0.5, 0.8)
+    expect = k.soft_nw_affine_hvp(s.numpy(), W.numpy(), -2.0, -0.5, 0.8) + 0.5 * rm
+    _close(x.grad, expect, "marginal-path grad_scores")
+    per = _capi.nwa_forward_marginals(s.to(cuda), None, -2.0, -0.5, 0.8)[2:]
+    for p, (g, dv) in enumerate(zip(ps, per)):
+        J = _capi.nwa_param_jacobian(s.to(cuda), p, None, -2.0, -0.5, 0.8)
+        dot_consistent(g.grad, J, W, 0.5 * float(dv.double().sum()), f"nwa {NAMES[p]}")
+    # float parameters: the scores gradient alone, equal to the tensor-parameter one
+    x2 = s.to(cuda).requires_grad_(True)
+    r2 = d2p_amd.soft_nw_affine(x2, gap_open=-2.0, gap_ext=-0.5, temperature=0.8)
+    ((r2.alignment * W.to(cuda)).sum() + 0.5 * r2.score.sum()).backward()
+    torch.testing.assert_close(x2.grad, x.grad, rtol=0, atol=0)
+
+
+def test_nwa_ops_match_capi(cuda):
+    """torch.ops.d2p NW-affine ops route to the same kernels as the C ABI."""
+    import d2p_amd
+    from d2p_amd import ops
+    s = _seeded(21, (2, 50, 60)).to(cuda)
+    v = _seeded(22, (2, 50, 60)).to(cuda)
+    h = _capi.nwa_hvp(s, v, None, -2.0, -0.5, 1.0)
+    torch.testing.assert_close(d2p_amd.soft_nw_affine_hvp(s, v, -2.0, -0.5, 1.0, None), h,
+                               rtol=0, atol=0)
+    torch.testing.assert_close(ops.nw_affine_marginals_hvp(s, v, -2.0, -0.5, 1.0, None), h,
+                               rtol=0, atol=0)
+    for p, fn in enumerate((ops.nw_affine_marginals_grad_gap_open,
+                            ops.nw_affine_marginals_grad_gap_ext,
+                            ops.nw_affine_marginals_grad_temp)):
+        J = _capi.nwa_param_jacobian(s, p, None, -2.0, -0.5, 1.0)
+        torch.testing.assert_close(fn(s, -2.0, -0.5, 1.0, None), J, rtol=0, atol=0)
+        torch.testing.assert_close(d2p_amd.soft_nw_affine_param_jacobian(s, p, -2.0, -0.5, 1.0,
+                                                                         None), J, rtol=0, atol=0)
+    ref = _capi.nwa_forward_marginals(s, None, -2.0, -0.5, 1.0)
+    got = d2p_amd.soft_nw_affine_with_grads(s, -2.0, -0.5, 1.0, None)
+    for a, b in zip(got, ref):
+        torch.testing.assert_close(a, b, rtol=0, atol=0)
+    vg = ops.nw_affine_value_grad_params(s, -2.0, -0.5, 1.0, None)
+    for a, b in zip(vg, (ref[0], ref[2], ref[3])):
+        torch.testing.assert_close(a, b, rtol=0, atol=0)
+    gs, *gp = _capi.nwa_backward_full(s, v, None, -2.0, -0.5, 1.0)
+    for fn in (d2p_amd.soft_nw_affine_backward_full, ops.nw_affine_marginals_backward):
+        r = fn(s, v, -2.0, -0.5, 1.0, None)
+        torch.testing.assert_close(r[0], gs, rtol=0, atol=0)
+        for a, b in zip(r[1:], gp):
+            torch.testing.assert_close(a, b.sum().reshape(1), rtol=0, atol=0)
+    for fwd in (ops.nw_affine_forward(s, -2.0, -0.5, 1.0, None),
+                ops.nw_affine_forward_t(s, *[torch.tensor([v], device=cuda)
+                                             for v in (-2.0, -0.5, 1.0)],
+                                        torch.tensor([[50, 60]] * 2, dtype=torch.int32,
+                                                     device=cuda))):
+        torch.testing.assert_close(fwd[0], ref[0], rtol=0, atol=0)
+        torch.testing.assert_close(fwd[1], ref[1], rtol=0, atol=0)

@@ -28,25 +28,28 @@ INT32_MAX = 2 ** 31 - 1
     ([[-1, 5]], r"lengths\[0,0\] must be between 0 and 4"),
     ([[4, 6]], r"lengths\[0,1\] must be between 0 and 5"),
 ])
-@pytest.mark.parametrize("family", ["sw", "swa", "nw", "dtw"])
+@pytest.mark.parametrize("family", ["sw", "swa", "nw", "nwa", "dtw"])
 def test_invalid_lengths_raise(cuda, family, lengths, match):
     scores = torch.randn(1, 4, 5, device=cuda)
     ln = torch.tensor(lengths, dtype=torch.int32, device=cuda)
     call = {"sw": lambda: d2p_amd.soft_sw_float(scores, -1.0, 1.0, ln),
             "swa": lambda: d2p_amd.soft_sw_affine_float(scores, -2.0, -0.5, 1.0, ln),
             "nw": lambda: d2p_amd.soft_nw_float(scores, -1.0, 1.0, ln),
+            "nwa": lambda: d2p_amd.soft_nw_affine_float(scores, -2.0, -0.5, 1.0, ln),
             "dtw": lambda: d2p_amd.soft_dtw_float(scores.abs(), 1.0, ln, -1)}[family]
     with pytest.raises(RuntimeError, match=match):
         call()
 
 
-@pytest.mark.parametrize("family", ["sw", "swa", "nw"])
+@pytest.mark.parametrize("family", ["sw", "swa", "nw", "nwa"])
 def test_hvp_shape_mismatch_raises(cuda, family):
     scores = torch.randn(1, 4, 5, device=cuda)
     tangent = torch.randn(1, 4, 4, device=cuda)
     call = {"sw": lambda: d2p_amd.soft_sw_hvp(scores, tangent, -1.0, 1.0, None),
             "swa": lambda: d2p_amd.soft_sw_affine_hvp(scores, tangent, -2.0, -0.5, 1.0, None),
-            "nw": lambda: d2p_amd.soft_nw_hvp(scores, tangent, -1.0, 1.0, None)}[family]
+            "nw": lambda: d2p_amd.soft_nw_hvp(scores, tangent, -1.0, 1.0, None),
+            "nwa": lambda: d2p_amd.soft_nw_affine_hvp(scores, tangent, -2.0, -0.5, 1.0,
+                                                      None)}[family]
     with pytest.raises(RuntimeError, match=r"scores and tangent must have same shape"):
         call()
 
@@ -59,13 +62,15 @@ def test_dtw_hvp_shape_mismatch_raises(cuda):
         d2p_amd.soft_dtw_backward_full(costs, torch.rand(1, 4, 4, device=cuda), 1.0, None, -1)
 
 
-@pytest.mark.parametrize("family", ["sw", "swa", "nw"])
+@pytest.mark.parametrize("family", ["sw", "swa", "nw", "nwa"])
 def test_backward_full_rejects_bad_grad_alignment(cuda, family):
     scores = torch.randn(2, 3, 4, device=cuda)
     fn = {"sw": lambda ga: d2p_amd.soft_sw_backward_full(scores, ga, -1.0, 1.0, None),
           "swa": lambda ga: d2p_amd.soft_sw_affine_backward_full(scores, ga, -2.0, -0.5, 1.0,
                                                                  None),
-          "nw": lambda ga: d2p_amd.soft_nw_backward_full(scores, ga, -1.0, 1.0, None)}[family]
+          "nw": lambda ga: d2p_amd.soft_nw_backward_full(scores, ga, -1.0, 1.0, None),
+          "nwa": lambda ga: d2p_amd.soft_nw_affine_backward_full(scores, ga, -2.0, -0.5, 1.0,
+                                                                 None)}[family]
     with pytest.raises(RuntimeError, match=r"grad_alignment must have same shape as scores"):
         fn(torch.randn(2, 3, 3, device=cuda))
     with pytest.raises(RuntimeError, match=r"grad_alignment must be a CUDA tensor"):
@@ -128,10 +133,11 @@ def _kernels_launched(fn):
 
 
 SECOND_ORDER = ("sw_tangent", "sw_dual", "nw_tangent", "nw_dual", "swa_tangent", "swa_dual",
+                "nwa_tangent", "nwa_dual",
                 "dtw_tangent", "dtw_dual")
 
 
-@pytest.mark.parametrize("family", ["sw", "swa", "dtw", "nw"])
+@pytest.mark.parametrize("family", ["sw", "swa", "dtw", "nw", "nwa"])
 def test_value_path_launches_no_second_order_kernels(cuda, family):
     s = torch.randn(2, 70, 90, device=cuda)
     if family == "dtw":
@@ -139,7 +145,8 @@ def test_value_path_launches_no_second_order_kernels(cuda, family):
     fn = {"sw": lambda x: d2p_amd.soft_sw(x, gap=-1.0, temperature=1.0),
           "swa": lambda x: d2p_amd.soft_sw_affine(x, gap_open=-2.0, gap_ext=-0.5),
           "dtw": lambda x: d2p_amd.soft_dtw(x, temperature=0.5),
-          "nw": lambda x: d2p_amd.soft_nw(x, gap=-1.0, temperature=1.0)}[family]
+          "nw": lambda x: d2p_amd.soft_nw(x, gap=-1.0, temperature=1.0),
+          "nwa": lambda x: d2p_amd.soft_nw_affine(x, gap_open=-2.0, gap_ext=-0.5)}[family]
 
     def value_path():
         x = s.clone().requires_grad_(True)
@@ -154,7 +161,7 @@ def test_value_path_launches_no_second_order_kernels(cuda, family):
     assert "scale_by_batch" in names
     assert not names & set(SECOND_ORDER), names
     names = _kernels_launched(marginal_path)
-    prefix = {"sw": "sw", "swa": "swa", "dtw": "dtw", "nw": "nw"}[family]
+    prefix = {"sw": "sw", "swa": "swa", "dtw": "dtw", "nw": "nw", "nwa": "nwa"}[family]
     assert {f"{prefix}_tangent", f"{prefix}_dual"} <= names, names
 
 

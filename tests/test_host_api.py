@@ -18,13 +18,16 @@ REF = "/root/reference"
 
 AUTOGRAD_OPS = {"soft_sw", "soft_sw_float", "sw_forward", "sw_forward_t", "soft_sw_affine",
                 "soft_sw_affine_float", "sw_affine_forward", "sw_affine_forward_t", "soft_dtw",
-                "soft_dtw_float", "soft_nw", "soft_nw_float", "nw_forward", "nw_forward_t"}
+                "soft_dtw_float", "soft_nw", "soft_nw_float", "nw_forward", "nw_forward_t",
+                "soft_nw_affine", "soft_nw_affine_float", "nw_affine_forward",
+                "nw_affine_forward_t"}
 
 
 def reference_schemas():
     out = {}
     for path in glob.glob(os.path.join(REF, "src", "*", "registry.cpp")):
-        if os.path.basename(os.path.dirname(path)) not in ("sw", "sw_affine", "dtw", "nw"):
+        if os.path.basename(os.path.dirname(path)) not in ("sw", "sw_affine", "dtw", "nw",
+                                                           "nw_affine"):
             continue
         for s in re.findall(r'm\.def\("([^"]+)"\)', open(path).read()):
             out[s.split("(")[0]] = s
@@ -34,7 +37,7 @@ def reference_schemas():
 @pytest.mark.skipif(not os.path.isdir(REF), reason="reference sources absent")
 def test_schemas_byte_identical_to_reference():
     ref = reference_schemas()
-    assert len(ref) == 46          # 13 linear SW + 14 affine SW + 6 DTW + 13 linear NW
+    assert len(ref) == 60   # 13 linear SW + 14 affine SW + 6 DTW + 13 linear NW + 14 affine NW
     for name, schema in ref.items():
         ours = str(getattr(torch.ops.d2p, name).default._schema)
         assert ours == "d2p::" + schema, (ours, schema)
@@ -74,6 +77,12 @@ def _fake_calls(x):
         "soft_sw_affine_backward_full": ((s, s, -2.0, -0.5, f1, l),
                                          [(2, 5, 7), (1,), (1,), (1,)]),
         "sw_affine_value_grad_params": ((s, -2.0, -0.5, f1, l), [(2,), (2,), (2,)]),
+        "soft_nw_affine_float": ((s, -2.0, -0.5, f1, l), [(2,), (2, 5, 7)]),
+        "soft_nw_affine_with_grads": ((s, -2.0, -0.5, f1, l),
+                                      [(2,), (2, 5, 7), (2,), (2,), (2,)]),
+        "soft_nw_affine_backward_full": ((s, s, -2.0, -0.5, f1, l),
+                                         [(2, 5, 7), (1,), (1,), (1,)]),
+        "nw_affine_value_grad_params": ((s, -2.0, -0.5, f1, l), [(2,), (2,), (2,)]),
         "soft_dtw_float": ((s, f1, l, -1), [(2,), (2, 5, 7)]),
         "soft_dtw_with_grads": ((s, f1, l, -1), [(2,), (2, 5, 7), (2,)]),
         "soft_dtw_backward_full": ((s, s, f1, l, -1), [(2, 5, 7), (1,)]),
