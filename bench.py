@@ -183,6 +183,41 @@ def make_c4band():
     return cfg
 
 
+def make_c4xy(fused):
+    """C4 from its features: the same seeded x, y [512, 256, 64] as make_c4, the whole
+    job from features to gradients.  fused: d2p_amd.soft_dtw_sqeuclidean (costs formed
+    inside the sweeps); else torch.cdist(x, y) ** 2 + soft_dtw, the reference's
+    documented sequence (/root/reference/docs/algorithms/dtw.md:52; cdist's default mode
+    takes the matrix-product form at these sizes, and its exact-difference mode fails
+    to launch at [512, 256, 64] on this ROCm build).  Both: cost.sum().backward() into
+    x and y."""
+    import torch
+    g = torch.Generator().manual_seed(3)
+    B, L, D = 512, 256, 64
+    x = _randn(g, (B, L, D))
+    y = _randn(g, (B, L, D))
+    cells = B * L * L
+    feat = 4 * B * L * D
+    if fused:
+        return dict(
+            name="c4fused", inputs={"x": x, "y": y}, cells=cells,
+            # read x and y, write the alignment (= dcost/dcosts) and grad x, y (the GEMMs
+            # also read the alignment)
+            algo_step=2 * feat + 8 * cells + 2 * feat,
+            algo_kernel={"dtw_fused_forward": 2 * feat, "dtw_fused_backward": 4 * cells},
+            workload="C4 fused: soft_dtw_sqeuclidean(x, y, T=0.1), x, y [512,256,64] "
+                     "(costs formed in the sweeps), fwd + cost.sum().backward() into x, y",
+            extra={"B": B, "L1": L, "L2": L, "D": D, "temperature": 0.1})
+    return dict(
+        name="c4xy", inputs={"x": x, "y": y}, cells=cells,
+        algo_step=2 * feat + 8 * cells + 2 * feat,
+        algo_kernel={"dtw_forward": 4 * cells, "dtw_backward": 4 * cells,
+                     "scale_by_batch": 8 * cells},
+        workload="C4 from features: torch.cdist(x, y) ** 2 + soft_dtw(T=0.1), "
+                 "x, y [512,256,64], fwd + cost.sum().backward() into x, y",
+        extra={"B": B, "L1": L, "L2": L, "D": D, "temperature": 0.1})
+
+
 def make_dtwlong():
     import torch
     g = torch.Generator().manual_seed(5)
@@ -203,10 +238,12 @@ def make_dtwlong():
 
 CONFIGS = {"c2": make_c2, "c3": make_c3, "c4": make_c4, "c5": make_c5,
            "c5hvp": lambda: make_c5(hvp=True), "c4band": make_c4band,
+           "c4xy": lambda: make_c4xy(False), "c4fused": lambda: make_c4xy(True),
            "dtwlong": make_dtwlong, "c2nw": make_c2nw}
 
 
 def make_step(cfg, dev):
+    import torch
     import d2p_amd
     x = {k: v.to(dev) for k, v in cfg["inputs"].items()}
     name = cfg["name"]
@@ -227,6 +264,17 @@ def make_step(cfg, dev):
         def step():
             s = x["scores"].detach().requires_grad_(True)
             d2p_amd.soft_nw(s, gap=-1.0, temperature=1.0).score.sum().backward()
+    elif name == "c4xy":
+        def step():
+            a = x["x"].detach().requires_grad_(True)
+            b = x["y"].detach().requires_grad_(True)
+            c = torch.cdist(a, b) ** 2
+            d2p_amd.soft_dtw(c, temperature=0.1).cost.sum().backward()
+    elif name == "c4fused":
+        def step():
+            a = x["x"].detach().requires_grad_(True)
+            b = x["y"].detach().requires_grad_(True)
+            d2p_amd.soft_dtw_sqeuclidean(a, b, temperature=0.1).cost.sum().backward()
     elif name in ("c4band", "dtwlong"):
         T, bw = cfg["temperature"], cfg["bandwidth"]
 
@@ -332,6 +380,22 @@ def cpu_baseline_config(cfg, max_elems):
             post = k.swa_backward(a, x["scores"], p, ln, -11.0, -1.0, 0.5)[0]
             return post
         what = "fwd + 2x bwd DP + scale"
+    elif name in ("c4xy", "c4fused"):
+        # the reference's documented sequence on the CPU: cdist ** 2 (torch, same
+        # threads), the DP, and the gradients into x and y
+        import torch
+        cells = n * x["x"].shape[1] * x["y"].shape[1]
+        xt, yt = torch.from_numpy(x["x"]), torch.from_numpy(x["y"])
+
+        def step():
+            c = (torch.cdist(xt, yt) ** 2).numpy()
+            a, sc = k.dtw_forward(c, None, 0.1, -1)
+            k.dtw_backward(a, c, sc, None, 0.1, -1)
+            G = torch.from_numpy(k.dtw_backward(a, c, sc, None, 0.1, -1)[0])
+            gx = 2 * (xt * G.sum(2, keepdim=True) - torch.bmm(G, yt))
+            gy = 2 * (yt * G.sum(1).unsqueeze(-1) - torch.bmm(G.transpose(1, 2), xt))
+            return gx, gy
+        what = "cdist ** 2 + fwd + 2x bwd DP + gradient GEMMs"
     elif name in ("c4", "c4band", "dtwlong"):
         cells = x["costs"].size
         T, bw = cfg.get("temperature", 0.1), cfg.get("bandwidth", -1)
@@ -533,7 +597,7 @@ def main():
             out["cpu_baseline"] = cpu_baseline(cfg["inputs"]["scores"].numpy())
         else:
             sample = {"c3": 64, "c4": 512, "c5": 16, "c5hvp": 16, "c4band": 512,
-                      "dtwlong": 16, "c2nw": 256}[cfg["name"]]
+                      "dtwlong": 16, "c2nw": 256, "c4xy": 512, "c4fused": 512}[cfg["name"]]
             out["cpu_baseline"] = cpu_baseline_config(cfg, sample)
     print(json.dumps(out), flush=True)
 

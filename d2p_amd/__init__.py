@@ -11,7 +11,7 @@ from . import _ops
 from . import _compile  # noqa: F401  (fake/meta and autocast registrations)
 
 from .sw import soft_sw, soft_sw_affine, SWResult, SoftSW, SoftSWAffine
-from .dtw import soft_dtw, DTWResult, SoftDTW
+from .dtw import soft_dtw, soft_dtw_sqeuclidean, DTWResult, SoftDTW
 from .nw import soft_nw, soft_nw_affine, NWResult, SoftNW, SoftNWAffine
 from . import ops
 
@@ -45,7 +45,7 @@ soft_nw_affine_backward_full = _ops.soft_nw_affine_backward_full
 
 __all__ = [
     "soft_sw", "soft_sw_affine", "SWResult", "SoftSW", "SoftSWAffine",
-    "soft_dtw", "DTWResult", "SoftDTW", "ops",
+    "soft_dtw", "soft_dtw_sqeuclidean", "DTWResult", "SoftDTW", "ops",
     "soft_sw_float", "soft_sw_with_grads", "soft_sw_hvp", "soft_sw_param_jacobian",
     "soft_sw_backward_full",
     "soft_sw_affine_float", "soft_sw_affine_with_grads", "soft_sw_affine_hvp",

@@ -102,6 +102,16 @@ _FAKES = {
 for _name, _fn in _FAKES.items():
     register_fake(f"d2p::{_name}")(_fn)
 
+# ops of this build without a reference counterpart (namespace d2p_amd)
+_AMD_FAKES = {
+    "soft_dtw_sqeuclidean": lambda x, y, t, l, bw: (
+        x.new_empty([x.size(0)]), x.new_empty([x.size(0), x.size(1), y.size(1)]),
+        x.new_empty([x.size(0)])),
+    "pairwise_sqdist": lambda x, y: x.new_empty([x.size(0), x.size(1), y.size(1)]),
+}
+for _name, _fn in _AMD_FAKES.items():
+    register_fake(f"d2p_amd::{_name}")(_fn)
+
 try:
     from torch.library import register_autocast
 except ImportError:  # older torch: autocast rules unavailable
@@ -110,5 +120,7 @@ except ImportError:  # older torch: autocast rules unavailable
 if register_autocast is not None:
     for _name in _FAKES:
         register_autocast(f"d2p::{_name}", "cuda", torch.float32)
+    for _name in _AMD_FAKES:
+        register_autocast(f"d2p_amd::{_name}", "cuda", torch.float32)
 
 OPS = tuple(_FAKES)

@@ -33,15 +33,131 @@ using namespace wf;
 
 constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do not publish
 
+// ------------------------------------------------------------------ fused costs
+// The fused forward sweep (DC > 0) forms the costs itself from two feature sequences,
+// c[i,j] = sum_d (x[i,d] - y[j,d])^2, instead of reading a cost matrix: the
+// squared-Euclidean cost that callers otherwise build with
+// torch.cdist(x, y) ** 2 (/root/reference/docs/algorithms/dtw.md:52) before the
+// reference's sweeps read it (/root/reference/src/dtw/kernels.cu:55-114).  Each lane
+// keeps its row of x in registers; the element's y rows sit in LDS at a stride of
+// DC + 4 floats, so the 16-byte reads of 16 consecutive columns hit distinct banks
+// (the dynamic LDS base is 16-byte aligned: unaligned 16-byte LDS reads are served
+// correctly but several times slower).  D is padded to DC with zeros, which add exact
+// zeros.  The reverse sweep needs no costs at all.  Both forms below (y from LDS,
+// x from LDS) run the same four partial sums in the same order, so every kernel that
+// forms these costs (the fused forward and pairwise_sqdist) agrees bit for bit.
+
+// Loads per group: all of a group's LDS reads are issued before the first is used
+// (one LDS latency per group instead of one per read), at most 16 float4 in flight.
+template <int DC>
+constexpr int feature_group() { return DC < 64 ? DC / 4 : 16; }
+
+// sum_d (x[d] - y[d])^2, x in registers, y a 16-byte aligned LDS row.  Four partial
+// sums (features d = 4k + m into sum m), added pairwise at the end: four independent
+// fma chains instead of one.
+template <int DC>
+__device__ __forceinline__ float sq_euclid(const float (&xr)[DC], const float* yrow) {
+    constexpr int G = feature_group<DC>();
+    const float4* q = reinterpret_cast<const float4*>(yrow);
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+    for (int g0 = 0; g0 < DC / 4; g0 += G) {
+        float4 v[G];
+#pragma unroll
+        for (int k = 0; k < G; ++k) v[k] = q[g0 + k];
+        __builtin_amdgcn_sched_barrier(0);   // keep the group's reads ahead of their uses
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+            const int d = 4 * (g0 + k);
+            const float d0 = xr[d] - v[k].x, d1 = xr[d + 1] - v[k].y;
+            const float d2 = xr[d + 2] - v[k].z, d3 = xr[d + 3] - v[k].w;
+            a0 = fmaf(d0, d0, a0);
+            a1 = fmaf(d1, d1, a1);
+            a2 = fmaf(d2, d2, a2);
+            a3 = fmaf(d3, d3, a3);
+        }
+    }
+    return (a0 + a1) + (a2 + a3);
+}
+
+// The same sum with x a 16-byte aligned LDS row (read by every lane: a broadcast) and
+// y in registers.
+template <int DC>
+__device__ __forceinline__ float sq_euclid_xl(const float* xrow, const float (&yr)[DC]) {
+    constexpr int G = feature_group<DC>();
+    const float4* q = reinterpret_cast<const float4*>(xrow);
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+    for (int g0 = 0; g0 < DC / 4; g0 += G) {
+        float4 v[G];
+#pragma unroll
+        for (int k = 0; k < G; ++k) v[k] = q[g0 + k];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+            const int d = 4 * (g0 + k);
+            const float d0 = v[k].x - yr[d], d1 = v[k].y - yr[d + 1];
+            const float d2 = v[k].z - yr[d + 2], d3 = v[k].w - yr[d + 3];
+            a0 = fmaf(d0, d0, a0);
+            a1 = fmaf(d1, d1, a1);
+            a2 = fmaf(d2, d2, a2);
+            a3 = fmaf(d3, d3, a3);
+        }
+    }
+    return (a0 + a1) + (a2 + a3);
+}
+
+// row `row` of a [rows][D] matrix into registers, zero past D
+template <int DC>
+__device__ __forceinline__ void load_feature_row(float (&xr)[DC], const float* base, int row,
+                                                 int D) {
+    const float* p = base + (size_t)row * D;
+#pragma unroll
+    for (int d = 0; d < DC; ++d) xr[d] = d < D ? p[d] : 0.0f;
+}
+
+// This lane's P cells of a forward chunk, (i0 + lane, t + u - lane), into its slots of
+// a cost tile (the layout the DMA path fills); columns are clamped into the matrix and
+// cells outside the element are masked by the sweep.  Two cells per iteration of a
+// rolled loop: unrolled over all P, the compiler would hoist every cell's LDS reads
+// and spill.
+template <int DC, int P>
+__device__ __forceinline__ void fused_costs(float* tile, int tbase, const float (&xr)[DC],
+                                            const float* ylds, int t, int lane, int L2max) {
+#pragma unroll 1
+    for (int u = 0; u < P; u += 2) {
+        const int j0 = min(max(t + u - lane, 0), L2max - 1);
+        const int j1 = min(max(t + u + 1 - lane, 0), L2max - 1);
+        const float c0 = sq_euclid<DC>(xr, ylds + j0 * (DC + 4));
+        const float c1 = sq_euclid<DC>(xr, ylds + j1 * (DC + 4));
+        tile[tbase + u] = c0;
+        tile[tbase + u + 1] = c1;
+    }
+}
+
+// the element's [L2max][D] rows of y into LDS rows of DC + 4 floats (zero past D);
+// the caller synchronises the workgroup after it
+template <int DC>
+__device__ __forceinline__ void stage_features(float* ylds, const float* yb, int L2max, int D) {
+    for (int idx = threadIdx.x; idx < L2max * DC; idx += NW * 64) {
+        const int j = idx / DC, d = idx % DC;
+        ylds[j * (DC + 4) + d] = d < D ? yb[(size_t)j * D + d] : 0.0f;
+    }
+}
+
+// DC > 0: fused costs from fx [B, L1max, D] and fy [B, L2max, D] (costs unused)
+template <int DC = 0>
 __global__ void __launch_bounds__(NW * 64)
 dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ lengths,
                    float* __restrict__ alpha_sk, float* __restrict__ brow,
                    float* __restrict__ value, int* __restrict__ status,
                    uint64_t* __restrict__ fflag, int B, int L1max, int L2max, int NSmax,
                    size_t elem_steps, float T, int bandwidth, int R, int G, int SPW,
-                   uint32_t epoch) {
+                   uint32_t epoch, const float* __restrict__ fx, const float* __restrict__ fy,
+                   int D) {
     constexpr int P = PF;
-    extern __shared__ float smem[];
+    constexpr bool FUSED = DC > 0;
+    extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     __shared__ float terminal;
     // part of the element as in the linear-SW forward: the first stripe of a part > 0
@@ -53,14 +169,16 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = ChunkTile<P>;
-    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 64;        // two cost chunks, two rows
+    // two cost chunks (fused: one, computed in place), two rows
+    constexpr int WBUF = (FUSED ? 1 : 2) * Tile::FLOATS + 2 * 64;
     float* tiles = smem + wave * WBUF;                     // double-buffered cost chunk
-    float* rbufs = tiles + 2 * Tile::FLOATS;               // boundary row of a chunk
+    float* rbufs = tiles + (FUSED ? 1 : 2) * Tile::FLOATS; // boundary row of a chunk
     __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
                                   // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
     float* rings = smem + NW * WBUF;                       // [NW][R]
     float* sink = rings + NW * R + wave * DUMMY;           // per-wave write sink
+    float* ylds = rings + NW * R + NW * DUMMY;             // fused: [L2max][DC + 4]
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
 
@@ -69,6 +187,7 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
         if (G == 1) *st = 0;                               // G > 1: reset before the launch
         terminal = kPINF;
     }
+    if constexpr (FUSED) stage_features<DC>(ylds, fy + (size_t)b * L2max * D, L2max, D);
     __syncthreads();
 
     const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
@@ -121,6 +240,9 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
         const bool x_in = l == 0 && part > 0;        // row above from the previous part
         const bool x_out = l == NL - 1 && has_next;  // last row feeds the next part
         int seen = -1;       // chunks of the previous part known to be complete
+        float xr[FUSED ? DC : 1];                    // fused: this lane's row of x
+        if constexpr (FUSED)
+            load_feature_row<DC>(xr, fx + (size_t)b * L1max * D, min(i0 + lane, L1max - 1), D);
         // the APAD steps before the window hold the column-0 / off-band boundary
         // (PINF), read by the reverse sweep; so does the chunk after it
 #pragma unroll
@@ -153,8 +275,9 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                 seen = wait_part(flag_in, epoch, min(k_lo + lead(P), nch), st);
                 issue_row(k_lo);
             }
-            dma_tile<P, 1>(tile_lds + (k_lo & 1) * Tile::FLOATS * 4, cbase, i0, L1max, L2max,
-                           lane, k_lo * P);
+            if (!FUSED)
+                dma_tile<P, 1>(tile_lds + (k_lo & 1) * Tile::FLOATS * 4, cbase, i0, L1max, L2max,
+                               lane, k_lo * P);
         }
         // lane 0 of the first stripe sees alpha[0,0] = 0 as its first diagonal (when
         // its window starts at step 0)
@@ -171,8 +294,9 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                 const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
-            const float* tile = tiles + (k & 1) * Tile::FLOATS;
+            const float* tile = tiles + (FUSED ? 0 : (k & 1) * Tile::FLOATS);
             float cv[P];
+            if constexpr (FUSED) fused_costs<DC, P>(tiles, tbase, xr, ylds, t0, lane, L2max);
 #pragma unroll
             for (int u = 0; u < P; ++u) cv[u] = tile[tbase + u];
             // lane 0's up values: column t0+j sits in lane j (row 0 is PINF; so are the
@@ -189,8 +313,9 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
                     issue_row(k + 1);
                 }
-                dma_tile<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, cbase, i0, L1max,
-                               L2max, lane, t0 + P);
+                if (!FUSED)
+                    dma_tile<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, cbase, i0, L1max,
+                                   L2max, lane, t0 + P);
                 if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
@@ -230,9 +355,9 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
             }
             publish(prog, wave, l * PROG_STRIDE + k + 1);
             if (x_out && k >= 2) {
-                // at least P loads and 2P + 2 stores follow the row store of chunk k - 2:
-                // it (and everything before) is complete
-                wait_vmcnt<3 * P + 2>();
+                // at least P loads (none when fused) and 2P + 2 stores follow the row
+                // store of chunk k - 2: it (and everything before) is complete
+                wait_vmcnt<(FUSED ? 2 * P + 2 : 3 * P + 2)>();
                 if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
             }
         }
@@ -251,9 +376,14 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
         value[b] = NS > 0 ? terminal : ((L1 == 0 && L2 == 0) ? 0.0f : kPINF);
 }
 
+// The reverse sweep reads the forward's alpha table and nothing else: a cell's
+// softmin weights over its predecessors and its softmin value (the temperature
+// gradient's term) are both recomputed from the predecessors' alpha with the forward's
+// own arithmetic, so the costs are never loaded and the fused squared-Euclidean path
+// shares this sweep unchanged.
 template <int P>
 __global__ void __launch_bounds__(NW * 64)
-dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ lengths,
+dtw_backward_kernel(const int* __restrict__ lengths,
                     const float* __restrict__ alpha_sk, const float* __restrict__ brow,
                     float* __restrict__ post, float* __restrict__ grad_T,
                     int* __restrict__ status, float* __restrict__ trash,
@@ -261,7 +391,7 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
                     double* __restrict__ bpart, int B, int L1max, int L2max, int NSmax,
                     size_t elem_steps, float T, int bandwidth, int R, int G, int SPW,
                     uint32_t epoch) {
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     __shared__ float red_g[NW];
     // parts run bottom-up as in the linear-SW backward
@@ -272,9 +402,9 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // Per wave, two chunk buffers, each: the cost tile (then the chunk's marginals),
+    // Per wave, two chunk buffers, each: the tile that stages the chunk's marginals,
     // P alpha rows (steps t_hi-2 .. t_hi-P-1) and one row of values from the stripe
-    // above.  All three arrive by direct-to-LDS loads one chunk ahead.
+    // above; the last two arrive by direct-to-LDS loads one chunk ahead.
     using Tile = ChunkTile<P>;
     constexpr int ABUF = Tile::FLOATS;
     constexpr int RBUF = ABUF + P * 64;
@@ -296,12 +426,12 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
     const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
     const int L2 = lengths ? min(max(lengths[2 * b + 1], 0), L2max) : L2max;
     const float c = kLog2e / T;
+    const float tl = T * kLn2;
     const float bw = (bandwidth < 0 || L1 == 0 || L2 == 0) ? -1.0f : (float)bandwidth;
     const int NS = L2 > 0 ? (L1 + 63) >> 6 : 0;
     const int nsteps = L2 + 63;
     const int nch = (nsteps + P - 1) / P;
     const size_t NT = (size_t)stored_steps(L2max);
-    const float* cbase = costs + (size_t)b * L1max * L2max;
     float* pbase = post + (size_t)b * L1max * L2max;
 
     {   // each part zeroes its share of the rows' padding
@@ -365,7 +495,6 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
             const uint32_t buf = lds_address(bufs + (k & 1) * BUF);
-            dma_tile<P, -1>(buf, cbase, i0, L1max, L2max, lane, th);
             dma_rows<P, -1>(buf + ABUF * 4, astripe, th - 2 - sh, ul4);
             uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
             uint32_t rl = buf + RBUF * 4;
@@ -424,9 +553,6 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
             }
             float* buf = bufs + (k & 1) * BUF;
             float* tile = buf;
-            float cv[P];
-#pragma unroll
-            for (int u = 0; u < P; ++u) cv[u] = tile[tbase + u];
             A[0] = A[P];
             A[1] = A[P + 1];
 #pragma unroll
@@ -472,7 +598,7 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
                 const int t = t_hi - u;
                 const int col = t - lane;
                 const bool ok = FULL || ((unsigned)col < (unsigned)L2eff && in_band(ej, col + 1, bw));
-                const float a0 = A[u], a1 = A[u + 1];
+                const float a1 = A[u + 1];
                 const float bv_next = wave_shl1(bv);
                 const float upa = wave_shr1_or(a1, bv);
                 const float dga = wave_shr1_or(A[u + 2], bv_next);
@@ -481,7 +607,8 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
                 const float m = fminf(fminf(dga, upa), a1);
                 const float ed = fast_exp2((m - dga) * c), eu = fast_exp2((m - upa) * c);
                 const float el = fast_exp2((m - a1) * c);
-                const float rin = m < kPINF ? fast_rcp((ed + eu) + el) : 0.0f;
+                const float z = (ed + eu) + el;
+                const float rin = m < kPINF ? fast_rcp(z) : 0.0f;
                 // reference accumulation order: init, diagonal, left, up successor
                 const float binit = t == term_step ? 1.0f : 0.0f;
                 const float beta = ((binit + in_diag) + in_left) + in_up;
@@ -489,9 +616,10 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
                 const float br = bl * rin;
                 const float od = br * ed, ou = br * eu, ol = br * el;
                 tile[tbase + u] = bl;
-                // temperature gradient: beta * (softmin value - E_w[predecessor alpha])
-                const float cost = ok ? cv[u] : 0.0f;
-                const float smv = a0 - cost;
+                // temperature gradient: beta * (softmin value - E_w[predecessor alpha]);
+                // the softmin value is the forward's m - T ln2 log2(z), bit for bit
+                // (PINF, hence skipped, when every predecessor is PINF)
+                const float smv = m - tl * fast_log2(z);
                 const float ea = (od * dga + ou * upa) + ol * a1;   // beta * E_w[alpha_pred]
                 g_acc += (ok && smv < kPINF) ? bl * smv - ea : 0.0f;
                 pub[u] = make_float2(ou, od);
@@ -512,9 +640,9 @@ dtw_backward_kernel(const float* __restrict__ costs, const int* __restrict__ len
                 // this chunk's flows to the part above, by producer step
                 if (lane < P) store_sys2(flows_out + k * P + lane, ring_out[ring_index(k * P, R) + lane]);
                 if (k >= 2) {
-                    // at least P + P/4 + 1 loads, 2P marginal stores and 2 flow stores
+                    // at least P/4 + 1 loads, 2P marginal stores and 2 flow stores
                     // follow the flow store of chunk k - 2: it is complete
-                    wait_vmcnt<3 * P + P / 4 + 3>();
+                    wait_vmcnt<2 * P + P / 4 + 3>();
                     if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
                 }
             }
@@ -585,7 +713,7 @@ int max_stripes_backward(int max_L1, int max_L2) {
 }
 
 template <int P>
-int launch_backward_p(const float* costs, const int* lengths, int B, int max_L1, int max_L2,
+int launch_backward_p(const int* lengths, int B, int max_L1, int max_L2,
                       float T, int bandwidth, const Layout& ws, float* marginals, float* grad_T,
                       hipStream_t st, const Split& sp, int R) {
     const int ns = (max_L1 + 63) / 64;
@@ -595,8 +723,8 @@ int launch_backward_p(const float* costs, const int* lengths, int B, int max_L1,
     D2P_HIP(hipFuncSetAttribute((const void*)dtw_backward_kernel<P>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     D2P_LAUNCH("dtw_backward", dtw_backward_kernel<P>, dim3(split_grid(B, sp.G)), dim3(NW * 64),
-               lds, st, costs, lengths, ws.alpha_sk, ws.brow, marginals, grad_T, ws.status,
-               ws.trash, ws.bflag, ws.flows, ws.bpart, B, max_L1, max_L2, ns, ws.elem_steps, T,
+               lds, st, lengths, ws.alpha_sk, ws.brow, marginals, grad_T, ws.status, ws.trash,
+               ws.bflag, ws.flows, ws.bpart, B, max_L1, max_L2, ns, ws.elem_steps, T,
                bandwidth, R, sp.G, sp.SPW, next_epoch());
     if (sp.G > 1)
         D2P_LAUNCH("dtw_grad_merge", dtw_grad_merge, dim3((B + 255) / 256), dim3(256), 0, st,
@@ -626,32 +754,162 @@ int launch_forward(const float* costs, const int* lengths, int B, int max_L1, in
     const size_t lds = lds_forward_r(R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     if (sp.G > 1 && launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
-    D2P_HIP(hipFuncSetAttribute((const void*)dtw_forward_kernel,
+    D2P_HIP(hipFuncSetAttribute((const void*)dtw_forward_kernel<0>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH("dtw_forward", dtw_forward_kernel, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds,
-               st, costs, lengths, ws.alpha_sk, ws.brow, value, ws.status, ws.fflag, B, max_L1,
-               max_L2, ns, ws.elem_steps, T, bandwidth, R, sp.G, sp.SPW, next_epoch());
+    D2P_LAUNCH("dtw_forward", dtw_forward_kernel<0>, dim3(split_grid(B, sp.G)), dim3(NW * 64),
+               lds, st, costs, lengths, ws.alpha_sk, ws.brow, value, ws.status, ws.fflag, B,
+               max_L1, max_L2, ns, ws.elem_steps, T, bandwidth, R, sp.G, sp.SPW, next_epoch(),
+               nullptr, nullptr, 0);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
 
-int launch_backward(const float* costs, const int* lengths, int B, int max_L1, int max_L2,
-                    float T, int bandwidth, const Layout& ws, float* marginals, float* grad_T,
+int launch_backward(const int* lengths, int B, int max_L1, int max_L2, float T,
+                    int bandwidth, const Layout& ws, float* marginals, float* grad_T,
                     hipStream_t st) {
     const Split sp = choose_split(B, max_L1, ws, max_stripes_backward(max_L1, max_L2));
     const int rows = sp.G > 1 ? sp.SPW * 64 : max_L1;
     const int R = ring_backward(rows, max_L2);
     if (backward_chunk(rows, max_L2) == 16)
-        return launch_backward_p<16>(costs, lengths, B, max_L1, max_L2, T, bandwidth, ws,
-                                     marginals, grad_T, st, sp, R);
-    return launch_backward_p<8>(costs, lengths, B, max_L1, max_L2, T, bandwidth, ws, marginals,
-                                grad_T, st, sp, R);
+        return launch_backward_p<16>(lengths, B, max_L1, max_L2, T, bandwidth, ws, marginals,
+                                     grad_T, st, sp, R);
+    return launch_backward_p<8>(lengths, B, max_L1, max_L2, T, bandwidth, ws, marginals, grad_T,
+                                st, sp, R);
+}
+
+// ---------------------------------------------------------------- fused costs
+
+// Feature padding of the fused sweeps: D rounded up to 32, 64 or 128 (0: too wide).
+int feature_chunk(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 0; }
+
+size_t feature_lds(int max_L2, int DC) { return (size_t)max_L2 * (DC + 4) * sizeof(float); }
+
+size_t lds_forward_fused(int R, int DC, int max_L2) {
+    return (size_t)NW * (65 * PF + 2 * 64) * sizeof(float) +
+           ((size_t)NW * R + NW * DUMMY) * sizeof(float) + feature_lds(max_L2, DC);
+}
+
+int check_fused(int B, int max_L1, int max_L2, int D, float T) {
+    D2P_TRY(check_shape(B, max_L1, max_L2, T));
+    D2P_REQUIRE(D >= 1 && feature_chunk(D) > 0, "feature dimension D must be between 1 and 128");
+    const int DC = feature_chunk(D);
+    D2P_REQUIRE(lds_forward_fused(ring_forward(64 * NW, max_L2), DC, max_L2) <= kLdsLimit,
+                "fused DTW: max_L2 * (D + 4) floats of y do not fit in LDS beside the stripe rings");
+    return D2P_OK;
+}
+
+template <int DC>
+int launch_fused(const float* x, const float* y, const int* lengths, int B, int max_L1,
+                 int max_L2, int D, float T, int bandwidth, const Layout& ws, float* value,
+                 float* marginals, float* grad_T, hipStream_t st) {
+    // forward: unsplit when the rings and y fit, else parts of at most NW stripes
+    const int ns = (max_L1 + 63) / 64;
+    const bool whole = lds_forward_fused(ring_forward(max_L1, max_L2), DC, max_L2) <= kLdsLimit;
+    const Split sp = choose_split(B, max_L1, ws, whole ? 0 : NW);
+    const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
+    const size_t lds = lds_forward_fused(R, DC, max_L2);
+    D2P_REQUIRE(lds <= kLdsLimit, "fused DTW: sequence too long for LDS");
+    if (sp.G > 1 && launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
+    auto kern = dtw_forward_kernel<DC>;
+    D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+    D2P_LAUNCH("dtw_fused_forward", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st,
+               nullptr, lengths, ws.alpha_sk, ws.brow, value, ws.status, ws.fflag, B, max_L1,
+               max_L2, ns, ws.elem_steps, T, bandwidth, R, sp.G, sp.SPW, next_epoch(), x, y, D);
+    D2P_HIP(hipGetLastError());
+    // the reverse sweep reads only the alpha table: the plain one
+    return launch_backward(lengths, B, max_L1, max_L2, T, bandwidth, ws, marginals, grad_T, st);
+}
+
+// costs[b, i, j] = sum_d (x[b,i,d] - y[b,j,d])^2 with the fused forward's arithmetic:
+// one thread per column (its row of y in registers), SQDIST_COLS columns and
+// SQDIST_ROWS rows of x (in LDS, read as broadcasts) per workgroup.
+constexpr int SQDIST_ROWS = 32;
+constexpr int SQDIST_COLS = 256;
+
+template <int DC>
+__global__ void __launch_bounds__(SQDIST_COLS)
+pairwise_sqdist_kernel(const float* __restrict__ x, const float* __restrict__ y,
+                       float* __restrict__ costs, int L1, int L2, int D) {
+    __shared__ __align__(16) float xs[SQDIST_ROWS * DC];
+    const int b = blockIdx.z, i0 = blockIdx.y * SQDIST_ROWS, j0 = blockIdx.x * SQDIST_COLS;
+    const int nrow = min(SQDIST_ROWS, L1 - i0), ncol = min(SQDIST_COLS, L2 - j0);
+    const float* xb = x + ((size_t)b * L1 + i0) * D;
+    for (int idx = threadIdx.x; idx < nrow * DC; idx += SQDIST_COLS) {
+        const int r = idx / DC, d = idx % DC;
+        xs[idx] = d < D ? xb[(size_t)r * D + d] : 0.0f;
+    }
+    float yr[DC];   // this thread's column (threads past the last column repeat it)
+    load_feature_row<DC>(yr, y + (size_t)b * L2 * D, j0 + min((int)threadIdx.x, ncol - 1), D);
+    __syncthreads();
+    if ((int)threadIdx.x >= ncol) return;
+    float* out = costs + ((size_t)b * L1 + i0) * L2 + j0 + threadIdx.x;
+#pragma unroll 1
+    for (int r = 0; r < nrow; ++r) out[(size_t)r * L2] = sq_euclid_xl<DC>(xs + r * DC, yr);
 }
 
 }  // namespace dtw
 }  // namespace d2p_amd
 
 using namespace d2p_amd;
+
+extern "C" int d2p_dtw_sqeuclid_forward_marginals(const float* x, const float* y,
+                                                  const int* lengths, int B, int max_L1,
+                                                  int max_L2, int D, float temperature,
+                                                  int bandwidth, float* value, float* marginals,
+                                                  float* grad_T, void* workspace,
+                                                  size_t workspace_bytes, void* stream) {
+    D2P_TRY(dtw::check_fused(B, max_L1, max_L2, D, temperature));
+    if (B == 0) return D2P_OK;
+    D2P_REQUIRE(x && y && value && marginals && grad_T, "null pointer argument");
+    const size_t need = d2p_dtw_workspace_bytes_banded(B, max_L1, max_L2, bandwidth);
+    D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 1, true, 8,
+                                     dtw::band_elem_steps(max_L1, max_L2, bandwidth));
+    switch (dtw::feature_chunk(D)) {
+        case 32:
+            D2P_TRY(dtw::launch_fused<32>(x, y, lengths, B, max_L1, max_L2, D, temperature,
+                                          bandwidth, ws, value, marginals, grad_T, st));
+            break;
+        case 64:
+            D2P_TRY(dtw::launch_fused<64>(x, y, lengths, B, max_L1, max_L2, D, temperature,
+                                          bandwidth, ws, value, marginals, grad_T, st));
+            break;
+        default:
+            D2P_TRY(dtw::launch_fused<128>(x, y, lengths, B, max_L1, max_L2, D, temperature,
+                                           bandwidth, ws, value, marginals, grad_T, st));
+    }
+    return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr, value,
+                             grad_T, nullptr, nullptr, st);
+}
+
+extern "C" int d2p_pairwise_sqdist(const float* x, const float* y, int B, int L1, int L2, int D,
+                                   float* costs, void* stream) {
+    D2P_REQUIRE(B >= 0 && L1 >= 0 && L2 >= 0, "negative dimension");
+    D2P_REQUIRE(D >= 1 && dtw::feature_chunk(D) > 0, "feature dimension D must be between 1 and 128");
+    D2P_REQUIRE(B <= 65535, "B must be at most 65535");
+    if (B == 0 || L1 == 0 || L2 == 0) return D2P_OK;
+    D2P_REQUIRE(x && y && costs, "null pointer argument");
+    hipStream_t st = (hipStream_t)stream;
+    const int DC = dtw::feature_chunk(D), CB = dtw::SQDIST_COLS;
+    const dim3 grid((L2 + CB - 1) / CB, (L1 + dtw::SQDIST_ROWS - 1) / dtw::SQDIST_ROWS, B);
+    switch (DC) {
+        case 32:
+            D2P_LAUNCH("pairwise_sqdist", dtw::pairwise_sqdist_kernel<32>, grid, dim3(CB), 0, st,
+                       x, y, costs, L1, L2, D);
+            break;
+        case 64:
+            D2P_LAUNCH("pairwise_sqdist", dtw::pairwise_sqdist_kernel<64>, grid, dim3(CB), 0, st,
+                       x, y, costs, L1, L2, D);
+            break;
+        default:
+            D2P_LAUNCH("pairwise_sqdist", dtw::pairwise_sqdist_kernel<128>, grid, dim3(CB), 0, st,
+                       x, y, costs, L1, L2, D);
+    }
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
 
 extern "C" size_t d2p_dtw_workspace_bytes_banded(int B, int max_L1, int max_L2, int bandwidth) {
     if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;
@@ -683,7 +941,7 @@ extern "C" int d2p_dtw_forward_marginals(const float* costs, const int* lengths,
                                      dtw::band_elem_steps(max_L1, max_L2, bandwidth));
     D2P_TRY(dtw::launch_forward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth, ws,
                                 value, st));
-    D2P_TRY(dtw::launch_backward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth, ws,
+    D2P_TRY(dtw::launch_backward(lengths, B, max_L1, max_L2, temperature, bandwidth, ws,
                                  marginals, grad_T, st));
     return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr, value,
                              grad_T, nullptr, nullptr, st);

@@ -106,9 +106,10 @@ int check_shape(int B, int max_L1, int max_L2, float temperature);
 int launch_forward(const float* costs, const int* lengths, int B, int max_L1, int max_L2,
                    float T, int bandwidth, const Layout& ws, float* value, hipStream_t st);
 
-// Reverse sweep: marginals and dvalue/dT per element, from a forward's table.
-int launch_backward(const float* costs, const int* lengths, int B, int max_L1, int max_L2,
-                    float T, int bandwidth, const Layout& ws, float* marginals, float* grad_T,
+// Reverse sweep: marginals and dvalue/dT per element, from a forward's table alone
+// (the costs are not needed).
+int launch_backward(const int* lengths, int B, int max_L1, int max_L2, float T,
+                    int bandwidth, const Layout& ws, float* marginals, float* grad_T,
                     hipStream_t st);
 
 }  // namespace dtw

@@ -54,7 +54,7 @@ dtw_tangent_kernel(const float* __restrict__ input, const int* __restrict__ leng
     constexpr int TR = RR + 64;           // tangent row of the part above
     constexpr int BUF = TR + 64;
     constexpr int SINK = 64 + P;
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     // parts as in the primal forward: part p > 0 takes its first stripe's tangent row
     // above from part p - 1 through tan_brow
@@ -291,7 +291,7 @@ dtw_dual_kernel(const float* __restrict__ V, const int* __restrict__ lengths,
     constexpr int BUF = FB + 64;
     static_assert(4 * P <= 64, "boundary flows fit their buffer");
     constexpr int SINK = 64 + P;
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     __shared__ float red[NW];
     // parts run bottom-up as in the primal backward; the last stripe of a part below

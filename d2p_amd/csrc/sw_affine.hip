@@ -72,7 +72,7 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                    int L2max, int NSmax, float go, float ge, float T, int R, int G, int SPW,
                    uint32_t epoch) {
     constexpr int P = PF;
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     __shared__ float red_m[NW], red_z[NW];
     __shared__ float term[3];     // NWA: (M, I, D) of the terminal cell
@@ -348,7 +348,7 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                     double* __restrict__ bpart, int B, int L1max, int L2max, int NSmax, float go,
                     float ge, float T, int R, int G, int SPW, uint32_t epoch) {
     constexpr int P = PB;
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     __shared__ float red_o[NW], red_e[NW], red_p[NW];
     // parts run bottom-up as in the linear backward; the last stripe of a part below

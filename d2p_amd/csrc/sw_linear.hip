@@ -57,7 +57,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                   int L2max, int NSmax, float gap, float T, int R, int G, int SPW,
                   uint32_t epoch) {
     constexpr int P = PF;
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     __shared__ float red_m[NW], red_z[NW];
     __shared__ float terminal;   // NWG: alpha[L1, L2]
@@ -308,7 +308,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                    double* __restrict__ bpart, float* __restrict__ poison_value, int B, int L1max,
                    int L2max, int NSmax, float gap, float T, int R, int G, int SPW,
                    uint32_t epoch) {
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     using Acc = typename std::conditional<PRECISE, double, float>::type;
     __shared__ Acc red_g[NW], red_p[NW];

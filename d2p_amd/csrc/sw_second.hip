@@ -62,7 +62,7 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     constexpr int TR = RR + 64;                              // tangent row of the part above
     constexpr int BUF = TR + 64;
     constexpr int SINK = 64 + P;
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     __shared__ float red[NW];
     // parts as in the primal forward: part p > 0 takes its first stripe's tangent row
@@ -321,7 +321,7 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     constexpr int BUF = FB + 64;
     static_assert(4 * P + 2 <= 64, "boundary flows fit their buffer");
     constexpr int SINK = 64 + P;
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     __shared__ float red[NW];
     // parts as in the primal backward: bottom-up, part p < G - 1 takes its last

@@ -103,7 +103,7 @@ swa_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V
     constexpr int TR = RR + 3 * 64;                       // 3 tangent rows of the part above
     constexpr int BUF = TR + 3 * 64;
     constexpr int SINK = 64 + P;
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     __shared__ float red[NW];
     // parts as in the primal forward: part p > 0 takes its first stripe's tangent rows
@@ -494,7 +494,7 @@ swa_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     constexpr int BUF = FBE + 64;
     static_assert(4 * P + 4 <= 64, "boundary flows fit their buffers");
     using FE = std::conditional_t<NWA, float4, float2>;
-    extern __shared__ float smem[];
+    extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     __shared__ float red[NW];
     // parts run bottom-up as in the primal backward; the last stripe of a part below

@@ -1143,6 +1143,67 @@ std::tuple<Tensor, Tensor> dtw_backward_full(Tensor costs, Tensor grad_alignment
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// fused squared-Euclidean costs + soft DTW (no counterpart in the reference: its
+// callers form torch.cdist(x, y) ** 2 first, /root/reference/docs/algorithms/dtw.md:52)
+// ---------------------------------------------------------------------------
+namespace {
+Dims checked_dims_xy(const Tensor& x, const Tensor& y) {
+    TORCH_CHECK(x.dim() == 3 && y.dim() == 3, "x and y must be 3D (B, L, D)");
+    TORCH_CHECK(x.size(0) == y.size(0), "x and y must have the same batch size, got ",
+                x.size(0), " and ", y.size(0));
+    TORCH_CHECK(x.size(2) == y.size(2), "x and y must have the same feature dimension, got ",
+                x.size(2), " and ", y.size(2));
+    TORCH_CHECK(x.size(2) >= 1 && x.size(2) <= 128, "feature dimension D must be between 1 and "
+                "128, got ", x.size(2));
+    TORCH_CHECK(y.device() == x.device(), "y must be on same device as x, got ", y.device(),
+                " vs ", x.device());
+    Dims d{checked_dim(x.size(0), "x batch dimension"), checked_dim(x.size(1), "x L1 dimension"),
+           checked_dim(y.size(1), "y L2 dimension")};
+    const int64_t cells = (int64_t(d.L1) + 1) * (int64_t(d.L2) + 1);
+    TORCH_CHECK(cells <= std::numeric_limits<int>::max(),
+                "DTW alpha table is too large for CUDA kernels: ", cells);
+    return d;
+}
+}  // namespace
+
+// (value [B], alignment [B, L1, L2], dvalue/dT [B]) of soft DTW over the costs
+// sum_d (x[b,i,d] - y[b,j,d])^2, formed inside the sweeps
+std::tuple<Tensor, Tensor, Tensor> dtw_sqeuclid(Tensor x, Tensor y, double temperature,
+                                                c10::optional<Tensor> lengths, int64_t bandwidth) {
+    CHECK_INPUT_DEV(x);
+    CHECK_INPUT_DEV(y);
+    TORCH_CHECK(temperature > 0, "temperature must be positive, got ", temperature);
+    Dims d = checked_dims_xy(x, y);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    Tensor l = resolve_lengths(lengths, d, x.device(), "x");
+    const int bw = checked_bandwidth(bandwidth);
+    auto opt = x.options();
+    Tensor value = torch::empty({d.B}, opt), marg = torch::empty({d.B, d.L1, d.L2}, opt);
+    Tensor gT = torch::empty({d.B}, opt);
+    const size_t ws_bytes = d2p_dtw_workspace_bytes_banded(d.B, d.L1, d.L2, bw);
+    Tensor ws = workspace(ws_bytes, x);
+    D2P_CALL(d2p_dtw_sqeuclid_forward_marginals(
+        x.data_ptr<float>(), y.data_ptr<float>(), lengths_ptr(l), d.B, d.L1, d.L2,
+        (int)x.size(2), (float)temperature, bw, value.data_ptr<float>(), marg.data_ptr<float>(),
+        gT.data_ptr<float>(), ws.data_ptr(), ws_bytes, current_stream()));
+    check_status(ws, d.B);
+    return {value, marg, gT};
+}
+
+// costs [B, L1, L2] = sum_d (x[b,i,d] - y[b,j,d])^2, bit-identical to the fused sweeps'
+Tensor pairwise_sqdist(Tensor x, Tensor y) {
+    CHECK_INPUT_DEV(x);
+    CHECK_INPUT_DEV(y);
+    Dims d = checked_dims_xy(x, y);
+    TORCH_CHECK(d.B <= 65535 && d.L1 <= 65535, "pairwise_sqdist: B and L1 must be at most 65535");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    Tensor out = torch::empty({d.B, d.L1, d.L2}, x.options());
+    D2P_CALL(d2p_pairwise_sqdist(x.data_ptr<float>(), y.data_ptr<float>(), d.B, d.L1, d.L2,
+                                 (int)x.size(2), out.data_ptr<float>(), current_stream()));
+    return out;
+}
+
 TORCH_LIBRARY(d2p, m) {
     // /root/reference/src/sw/registry.cpp:30-44
     m.def("soft_sw(Tensor scores, Tensor gap, Tensor temperature, Tensor lengths) -> Tensor[]");
@@ -1331,4 +1392,22 @@ const char* const kAllOps[] = {
 TORCH_LIBRARY_IMPL(d2p, CPU, m) {
     for (const char* name : kAllOps)
         m.impl(name, torch::CppFunction::makeFromBoxedFunction<&cpu_boxed>());
+}
+
+// Ops of this build with no counterpart in the reference live in their own namespace,
+// so that d2p:: holds exactly the reference's schemas.
+TORCH_LIBRARY(d2p_amd, m) {
+    m.def("soft_dtw_sqeuclidean(Tensor x, Tensor y, float temperature, Tensor? lengths, "
+          "int bandwidth) -> (Tensor, Tensor, Tensor)");
+    m.def("pairwise_sqdist(Tensor x, Tensor y) -> Tensor");
+}
+
+TORCH_LIBRARY_IMPL(d2p_amd, CUDA, m) {
+    m.impl("soft_dtw_sqeuclidean", dtw_sqeuclid);
+    m.impl("pairwise_sqdist", pairwise_sqdist);
+}
+
+TORCH_LIBRARY_IMPL(d2p_amd, CPU, m) {
+    m.impl("soft_dtw_sqeuclidean", torch::CppFunction::makeFromBoxedFunction<&cpu_boxed>());
+    m.impl("pairwise_sqdist", torch::CppFunction::makeFromBoxedFunction<&cpu_boxed>());
 }

@@ -3,6 +3,11 @@
 Drop-in for the reference's ``d2p/dtw.py`` (``soft_dtw`` ``:57-105``,
 ``SoftDTW`` ``:108-150``, ``DTWResult`` ``:30-38``).  ``bandwidth <= 0`` means
 no Sakoe-Chiba band and is passed to the operators as -1 (``d2p/dtw.py:98``).
+
+``soft_dtw_sqeuclidean(x, y)`` has no counterpart in the reference: it is soft DTW
+over the squared-Euclidean costs ``sum_d (x_i - y_j)^2`` that callers otherwise build
+with ``torch.cdist(x, y) ** 2`` (/root/reference/docs/algorithms/dtw.md:52), with the
+costs formed inside the HIP sweeps, so no [B, L1, L2] cost matrix is written or read.
 """
 from __future__ import annotations
 
@@ -84,3 +89,75 @@ soft_dtw_forward = _ops.soft_dtw_float
 soft_dtw_with_grads = _ops.soft_dtw_with_grads
 soft_dtw_hvp = _ops.soft_dtw_hvp
 soft_dtw_backward_full = _ops.soft_dtw_backward_full
+
+
+class _SoftDTWSqEuclidean(torch.autograd.Function):
+    """Value and alignment of soft DTW over c[b,i,j] = |x[b,i] - y[b,j]|^2.
+
+    Backward: the cost gradient G is grad_value[b] * alignment (value path) plus,
+    when the alignment itself receives a gradient, soft_dtw_backward_full over the
+    cost matrix (formed by d2p_amd::pairwise_sqdist, bit-identical to the sweeps'
+    costs); then dL/dx_i = 2 (rowsum(G)_i x_i - (G y)_i) and dL/dy_j = 2 (colsum(G)_j y_j
+    - (G^T x)_j), two float32 batched GEMMs.  On the value path alone G is a per-element
+    multiple of the alignment, so the sums and GEMMs run on the alignment itself and
+    the [B, L, D] results are scaled: no [B, L1, L2] temporary, no transposed copy."""
+
+    @staticmethod
+    def forward(ctx, x, y, temperature, lengths, bandwidth, t_tensor):
+        ctx.set_materialize_grads(False)   # an unused output's gradient stays None
+        value, align, grad_t = torch.ops.d2p_amd.soft_dtw_sqeuclidean(x, y, temperature, lengths,
+                                                                     bandwidth)
+        ctx.save_for_backward(x, y, align, grad_t, lengths if lengths is not None else x.new_empty(0))
+        ctx.temperature, ctx.bandwidth, ctx.has_lengths = temperature, bandwidth, lengths is not None
+        ctx.mark_non_differentiable(grad_t)
+        return value, align
+
+    @staticmethod
+    def backward(ctx, g_value, g_align):
+        x, y, align, grad_t, lengths = ctx.saved_tensors
+        lengths = lengths if ctx.has_lengths else None
+        # G = scale[b] * M: M the alignment (value path alone, scale = grad_value) or
+        # the full cost gradient (scale = 1)
+        M, scale, gT = None, None, None
+        if g_value is not None:
+            M, scale = align, g_value
+            gT = (g_value * grad_t).sum().reshape(1)
+        if g_align is not None:
+            costs = torch.ops.d2p_amd.pairwise_sqdist(x, y)
+            gs, gt2 = torch.ops.d2p.soft_dtw_backward_full(
+                costs, g_align.contiguous().float(), ctx.temperature, lengths, ctx.bandwidth)
+            M = gs if M is None else g_value[:, None, None] * align + gs
+            scale = None
+            gT = gt2 if gT is None else gT + gt2
+        gx = gy = None
+        if M is not None:
+            f = 2.0 * scale[:, None, None] if scale is not None else 2.0
+            if ctx.needs_input_grad[0]:
+                gx = f * (x * M.sum(dim=2, keepdim=True) - torch.bmm(M, y))
+            if ctx.needs_input_grad[1]:
+                # (M^T x) as (x^T M)^T: both GEMM operands stay row-major
+                xtm = torch.bmm(x.transpose(1, 2).contiguous(), M)
+                gy = f * (y * M.sum(dim=1)[:, :, None] - xtm.transpose(1, 2))
+        g_temp = gT if ctx.needs_input_grad[5] else None
+        return gx, gy, None, None, None, g_temp
+
+
+def soft_dtw_sqeuclidean(x: torch.Tensor, y: torch.Tensor,
+                         temperature: Union[float, torch.Tensor] = 1.0, bandwidth: int = 0,
+                         lengths: Optional[torch.Tensor] = None) -> DTWResult:
+    """Soft DTW between feature sequences x [B, L1, D] and y [B, L2, D] (1 <= D <= 128)
+    under the squared-Euclidean cost, formed inside the sweeps.
+
+    Same result as ``soft_dtw(torch.cdist(x, y) ** 2, ...)`` up to the rounding of the
+    costs (each a sum of D squares in float32); gradients flow to x, y and a tensor
+    temperature.  The element's y rows are staged in LDS: max_L2 * (D + 4) floats must
+    fit beside the stripe rings (about max_L2 <= 450 for D = 64).
+    """
+    _validate_temperature(temperature)
+    bw = bandwidth if bandwidth > 0 else -1
+    # the sweeps compute in float32 (as every d2p op under autocast)
+    x, y = x.float().contiguous(), y.float().contiguous()
+    t_tensor = temperature if isinstance(temperature, torch.Tensor) else None
+    T = float(temperature.detach().reshape(-1)[0]) if t_tensor is not None else float(temperature)
+    value, align = _SoftDTWSqEuclidean.apply(x, y, T, lengths, bw, t_tensor)
+    return DTWResult(value, align)

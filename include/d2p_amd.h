@@ -322,6 +322,31 @@ size_t d2p_dtw_workspace_bytes(int B, int max_L1, int max_L2);
  * full (L1+1) x (L2+1) tables, /root/reference/src/dtw/torch_cuda.cpp:166-169). */
 size_t d2p_dtw_workspace_bytes_banded(int B, int max_L1, int max_L2, int bandwidth);
 
+/* Fused squared-Euclidean costs + soft DTW: the forward value and marginals of soft
+ * DTW over c[b,i,j] = sum_d (x[b,i,d] - y[b,j,d])^2, formed inside the sweeps from
+ * the features instead of read from a cost matrix.  No counterpart in the reference:
+ * its callers build the costs with torch.cdist(x, y) ** 2
+ * (/root/reference/docs/algorithms/dtw.md:52) and its sweeps read them
+ * (/root/reference/src/dtw/kernels.cu:55-114); this entry point removes that
+ * [B, L1, L2] matrix.  The DP, outputs, lengths and band rules are those of
+ * d2p_dtw_forward_marginals (same workspace, d2p_dtw_workspace_bytes_banded).
+ *   x [B, max_L1, D], y [B, max_L2, D]  inputs, 1 <= D <= 128
+ *   value [B], marginals [B, max_L1, max_L2] (= dvalue/dcosts), grad_T [B]
+ * Limit: max_L2 * (D rounded up to 32, 64 or 128, plus 4) floats of y must fit in
+ * LDS beside the stripe rings (about max_L2 <= 450 for D = 64). */
+int d2p_dtw_sqeuclid_forward_marginals(const float* x, const float* y, const int* lengths, int B,
+                                       int max_L1, int max_L2, int D, float temperature,
+                                       int bandwidth, float* value, float* marginals,
+                                       float* grad_T, void* workspace, size_t workspace_bytes,
+                                       void* stream);
+
+/* costs[b,i,j] = sum_d (x[b,i,d] - y[b,j,d])^2 with exactly the arithmetic of the fused
+ * sweeps above (bit-identical costs), for callers that need the matrix itself (the
+ * fused op's marginal-path backward).  No counterpart in the reference (see above).
+ *   x [B, L1, D], y [B, L2, D], costs [B, L1, L2]; 1 <= D <= 128, L1, B <= 65535 */
+int d2p_pairwise_sqdist(const float* x, const float* y, int B, int L1, int L2, int D,
+                        float* costs, void* stream);
+
 /* Forward value and alignment marginals in one call.
  * Replaces the pair dtw_forward + dtw_backward (/root/reference/src/dtw/kernels.cuh:95-129)
  * as sequenced by SoftDTWCUDAFunction::forward (/root/reference/src/dtw/torch_cuda.cpp:141-205).

@@ -54,6 +54,9 @@ SIGNATURES = {
     "d2p_nwa_param_jacobian": (_i, [_p, _i, _p, _i, _i, _i, _f, _f, _f, _p, _p, _z, _p]),
     "d2p_nwa_backward_full": (_i, [_p, _p, _p, _i, _i, _i, _f, _f, _f, _p, _p, _p, _p, _p, _z,
                                    _p]),
+    "d2p_dtw_sqeuclid_forward_marginals": (_i, [_p, _p, _p, _i, _i, _i, _i, _f, _i, _p, _p,
+                                                _p, _p, _z, _p]),
+    "d2p_pairwise_sqdist": (_i, [_p, _p, _i, _i, _i, _i, _p, _p]),
     "d2p_dtw_second_workspace_bytes": (_z, [_i, _i, _i]),
     "d2p_dtw_second_workspace_bytes_banded": (_z, [_i, _i, _i, _i]),
     "d2p_dtw_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _i, _p, _p, _z, _p]),
@@ -359,3 +362,30 @@ def nw_param_jacobian(scores, ptype, lengths, gap, T):
 
 def nw_backward_full(scores, grad_alignment, lengths, gap, T):
     return sw_backward_full(scores, grad_alignment, lengths, gap, T, fam="nw")
+
+
+def dtw_sqeuclid_forward_marginals(x, y, lengths, T, bandwidth=-1):
+    """Fused squared-Euclidean soft DTW: (value, marginals, grad_T) through the C ABI."""
+    import torch
+    B, L1, D = x.shape
+    L2 = y.shape[1]
+    dev = x.device
+    lengths = _lengths(lengths, B, L1, L2, dev)
+    outs = [torch.empty(B, device=dev), torch.empty(B, L1, L2, device=dev),
+            torch.empty(B, device=dev)]
+    nbytes = lib().d2p_dtw_workspace_bytes_banded(B, L1, L2, bandwidth)
+    ws = _workspace(nbytes, dev)
+    check(lib().d2p_dtw_sqeuclid_forward_marginals(ptr(x), ptr(y), ptr(lengths), B, L1, L2, D, T,
+                                                   bandwidth, *[ptr(o) for o in outs], ptr(ws),
+                                                   nbytes, stream()))
+    _check_status(ws, B)
+    return tuple(outs)
+
+
+def pairwise_sqdist(x, y):
+    import torch
+    B, L1, D = x.shape
+    L2 = y.shape[1]
+    out = torch.empty(B, L1, L2, device=x.device)
+    check(lib().d2p_pairwise_sqdist(ptr(x), ptr(y), B, L1, L2, D, ptr(out), stream()))
+    return out
