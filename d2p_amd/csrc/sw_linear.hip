@@ -337,11 +337,17 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     float2* rings = reinterpret_cast<float2*>(smem + NW * 2 * BUF);  // [NW][R] (up, diag)
     float2* sink = rings + NW * R + wave * DUMMY;
     int* st = status + b;
-    // the chunk's marginals go to an output tile laid over its own buffer, whose
-    // inputs are all in registers by then (the next chunk loads into the other one)
+    // The chunk's marginals go to an output tile laid over its own score tile, whose
+    // values are all in registers by then (the next chunk loads into the other
+    // buffer).  QOUT: a quad tile, one 16-byte quad per lane and four steps (the
+    // swizzle keeps those writes conflict-free), leaving with P/4 16-byte stores;
+    // otherwise (PRECISE, NWG: those variants have no registers to spare) a dword tile,
+    // one write per step, leaving with P dword stores.
+    constexpr bool QOUT = !PRECISE && !NWG;
     using OutTile = ChunkTile<P>;
     static_assert(OutTile::FLOATS <= BUF, "output tile fits the chunk buffer");
     const int obase_lane = OutTile::read_base(lane);
+    constexpr int NSTORE = QOUT ? Tile::NQ : P;   // stores of an inside chunk
 
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
@@ -434,9 +440,10 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         for (int k = 0; k < nch; ++k, slot0 = slot0 + P < R ? slot0 + P : slot0 + P - R) {
             const int t_hi = nsteps - 1 - k * P;
             chunk_waits<P>(prog, q, NL, k, nch, R, st);
-            // this chunk's loads were issued one chunk ago and followed by exactly the P
-            // marginal stores of that chunk (the first chunk's are the last issued)
-            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            // this chunk's loads were issued one chunk ago and followed by at least the
+            // NSTORE marginal stores of that chunk (P in a boundary chunk; the first
+            // chunk's loads are the last issued)
+            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<NSTORE>();
             if (x_in && k > 0) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
@@ -495,6 +502,9 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             // sums; otherwise each term goes into its accumulator with one fma
             constexpr bool TERMS = PRECISE || NWG;
             Acc gs[P], ps[P];
+            // the quad being filled: memory-column order, i.e. step 4q + 3 - e in
+            // element e (the reverse sweep's columns fall with the step)
+            float4 quad = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             float pre_d2 = wave_shr1(pre_d);   // lane 63 = step 1 (then shifted on)
             pre_d2 = wave_shr1(pre_d2);        // lane 63 = step 2
             // FULL: every cell of the chunk lies inside the element, no validity masks
@@ -542,7 +552,17 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const float br = live ? beta * rin : 0.0f;
                 const float od = br * e0, ou = br * e1, ol = br * e2;
                 const float pv = br * e03;
-                buf[obase_lane + u] = pv;
+                if constexpr (QOUT) {
+                    if ((u & 3) == 0) quad.w = pv;
+                    if ((u & 3) == 1) quad.z = pv;
+                    if ((u & 3) == 2) quad.y = pv;
+                    if ((u & 3) == 3) {
+                        quad.x = pv;
+                        *reinterpret_cast<float4*>(buf + Tile::slot(lane, u >> 2)) = quad;
+                    }
+                } else {
+                    buf[obase_lane + u] = pv;
+                }
                 if (PRECISE) gs[u] = (Acc)ou + (Acc)ol;
                 else if (TERMS) gs[u] = br * e12;
                 else g_acc = fmaf(br, e12, g_acc);
@@ -576,17 +596,21 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             }
             wave_lds_sync();
             // write this chunk's marginals back over the cells the scores came from:
-            // exactly P stores (cells outside the element's lengths go to the trash
-            // line in boundary chunks, and carry 0 in inside chunks)
-            write_tile<P, -1>(buf, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
+            // NSTORE stores (P dword stores in a boundary chunk, where cells outside the
+            // element's lengths go to the trash line; inside chunks carry 0 there)
+            if constexpr (QOUT)
+                write_quads<P, -1>(buf, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
+            else
+                write_tile<P, -1>(buf, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             publish(prog, wave, q * PROG_STRIDE + k + 1);
             if (x_out) {
                 // this chunk's flows to the part above, by producer step
                 if (lane < P) store_sys2(flows_out + k * P + lane, ring_out[slot0 + lane]);
                 if (k >= 2) {
-                    // at least 2 * (P/4 + P + 1) + P + 3 vector-memory operations follow
-                    // the flow stores of chunk k - 2: those are complete
-                    wait_vmcnt<2 * Tile::NQ + 2 * P + 3>();
+                    // at least (2 P/4 + 1) loads and NSTORE stores of chunk k - 1, NSTORE
+                    // stores of chunk k and the two chunks' flow stores follow the flow
+                    // store of chunk k - 2: it is complete
+                    wait_vmcnt<2 * Tile::NQ + 2 * NSTORE + 3>();
                     if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
                 }
             }

@@ -688,20 +688,16 @@ __device__ __forceinline__ void write_quads(const float* tile, float* obase, flo
         char* sbase = reinterpret_cast<char*>(stripe_row(obase, i0, L2max));
         uint32_t off = quad_offset0<P, DIR>(L2max, lane, t_first);
         const uint32_t step = (uint32_t)(Q::ROWS_X4 * (L2max - 1)) * 4u;
-        float4 v[Q::NQ];
-#pragma unroll
-        for (int i = 0; i < Q::NQ; ++i)
-            v[i] = *reinterpret_cast<const float4*>(tile + 256 * i + 4 * lane);
 #pragma unroll
         for (int i = 0; i < Q::NQ; ++i) {
-            *reinterpret_cast<float4*>(sbase + off) = v[i];
+            const float4 v = *reinterpret_cast<const float4*>(tile + 256 * i + 4 * lane);
+            *reinterpret_cast<float4*>(sbase + off) = v;
             off += step;
             __asm__ volatile("" : "+v"(off));   // keep one running offset
         }
     } else {
-        float v[P];
-#pragma unroll
-        for (int j = 0; j < P; ++j) v[j] = tile[64 * j + lane];
+        // one value at a time: boundary chunks are few, and the kernels that call this
+        // run near their register budget
 #pragma unroll
         for (int j = 0; j < P; ++j) {
             int r, col;
@@ -709,7 +705,7 @@ __device__ __forceinline__ void write_quads(const float* tile, float* obase, flo
             const int row = i0 + r;
             const bool in = row < L1 && col >= 0 && col < L2;
             float* dst = in ? obase + (size_t)row * L2max + col : trash + lane;
-            *dst = v[j];
+            *dst = tile[64 * j + lane];
         }
     }
 }
