@@ -186,7 +186,7 @@ def make_c4band():
 def make_c4xy(fused):
     """C4 from its features: the same seeded x, y [512, 256, 64] as make_c4, the whole
     job from features to gradients.  fused: d2p_amd.soft_dtw_sqeuclidean (costs formed
-    inside the sweeps); else torch.cdist(x, y) ** 2 + soft_dtw, the reference's
+    inside the forward sweep); else torch.cdist(x, y) ** 2 + soft_dtw, the reference's
     documented sequence (/root/reference/docs/algorithms/dtw.md:52; cdist's default mode
     takes the matrix-product form at these sizes, and its exact-difference mode fails
     to launch at [512, 256, 64] on this ROCm build).  Both: cost.sum().backward() into
@@ -206,7 +206,7 @@ def make_c4xy(fused):
             algo_step=2 * feat + 8 * cells + 2 * feat,
             algo_kernel={"dtw_fused_forward": 2 * feat, "dtw_fused_backward": 4 * cells},
             workload="C4 fused: soft_dtw_sqeuclidean(x, y, T=0.1), x, y [512,256,64] "
-                     "(costs formed in the sweeps), fwd + cost.sum().backward() into x, y",
+                     "(costs formed in the forward sweep), fwd + cost.sum().backward() into x, y",
             extra={"B": B, "L1": L, "L2": L, "D": D, "temperature": 0.1})
     return dict(
         name="c4xy", inputs={"x": x, "y": y}, cells=cells,

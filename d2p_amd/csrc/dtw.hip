@@ -779,7 +779,7 @@ int launch_backward(const int* lengths, int B, int max_L1, int max_L2, float T,
 
 // ---------------------------------------------------------------- fused costs
 
-// Feature padding of the fused sweeps: D rounded up to 32, 64 or 128 (0: too wide).
+// Feature padding of the fused forward: D rounded up to 32, 64 or 128 (0: too wide).
 int feature_chunk(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 0; }
 
 size_t feature_lds(int max_L2, int DC) { return (size_t)max_L2 * (DC + 4) * sizeof(float); }
@@ -889,6 +889,8 @@ extern "C" int d2p_pairwise_sqdist(const float* x, const float* y, int B, int L1
     D2P_REQUIRE(B >= 0 && L1 >= 0 && L2 >= 0, "negative dimension");
     D2P_REQUIRE(D >= 1 && dtw::feature_chunk(D) > 0, "feature dimension D must be between 1 and 128");
     D2P_REQUIRE(B <= 65535, "B must be at most 65535");
+    D2P_REQUIRE((L1 + dtw::SQDIST_ROWS - 1) / dtw::SQDIST_ROWS <= 65535,
+                "L1 must be at most 2097120");
     if (B == 0 || L1 == 0 || L2 == 0) return D2P_OK;
     D2P_REQUIRE(x && y && costs, "null pointer argument");
     hipStream_t st = (hipStream_t)stream;

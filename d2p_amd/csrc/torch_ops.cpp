@@ -1168,7 +1168,7 @@ Dims checked_dims_xy(const Tensor& x, const Tensor& y) {
 }  // namespace
 
 // (value [B], alignment [B, L1, L2], dvalue/dT [B]) of soft DTW over the costs
-// sum_d (x[b,i,d] - y[b,j,d])^2, formed inside the sweeps
+// sum_d (x[b,i,d] - y[b,j,d])^2, formed inside the forward sweep
 std::tuple<Tensor, Tensor, Tensor> dtw_sqeuclid(Tensor x, Tensor y, double temperature,
                                                 c10::optional<Tensor> lengths, int64_t bandwidth) {
     CHECK_INPUT_DEV(x);
@@ -1191,7 +1191,7 @@ std::tuple<Tensor, Tensor, Tensor> dtw_sqeuclid(Tensor x, Tensor y, double tempe
     return {value, marg, gT};
 }
 
-// costs [B, L1, L2] = sum_d (x[b,i,d] - y[b,j,d])^2, bit-identical to the fused sweeps'
+// costs [B, L1, L2] = sum_d (x[b,i,d] - y[b,j,d])^2, bit-identical to the fused forward's
 Tensor pairwise_sqdist(Tensor x, Tensor y) {
     CHECK_INPUT_DEV(x);
     CHECK_INPUT_DEV(y);

@@ -7,7 +7,8 @@ no Sakoe-Chiba band and is passed to the operators as -1 (``d2p/dtw.py:98``).
 ``soft_dtw_sqeuclidean(x, y)`` has no counterpart in the reference: it is soft DTW
 over the squared-Euclidean costs ``sum_d (x_i - y_j)^2`` that callers otherwise build
 with ``torch.cdist(x, y) ** 2`` (/root/reference/docs/algorithms/dtw.md:52), with the
-costs formed inside the HIP sweeps, so no [B, L1, L2] cost matrix is written or read.
+costs formed inside the HIP forward sweep, so no [B, L1, L2] cost matrix is written or
+read.
 """
 from __future__ import annotations
 
@@ -96,11 +97,11 @@ class _SoftDTWSqEuclidean(torch.autograd.Function):
 
     Backward: the cost gradient G is grad_value[b] * alignment (value path) plus,
     when the alignment itself receives a gradient, soft_dtw_backward_full over the
-    cost matrix (formed by d2p_amd::pairwise_sqdist, bit-identical to the sweeps'
-    costs); then dL/dx_i = 2 (rowsum(G)_i x_i - (G y)_i) and dL/dy_j = 2 (colsum(G)_j y_j
+    cost matrix (formed by d2p_amd::pairwise_sqdist, bit-identical to the forward
+    sweep's costs); then dL/dx_i = 2 (rowsum(G)_i x_i - (G y)_i) and dL/dy_j = 2 (colsum(G)_j y_j
     - (G^T x)_j), two float32 batched GEMMs.  On the value path alone G is a per-element
     multiple of the alignment, so the sums and GEMMs run on the alignment itself and
-    the [B, L, D] results are scaled: no [B, L1, L2] temporary, no transposed copy."""
+    the [B, L, D] results are scaled: no [B, L1, L2] temporary or transposed copy."""
 
     @staticmethod
     def forward(ctx, x, y, temperature, lengths, bandwidth, t_tensor):
@@ -146,7 +147,7 @@ def soft_dtw_sqeuclidean(x: torch.Tensor, y: torch.Tensor,
                          temperature: Union[float, torch.Tensor] = 1.0, bandwidth: int = 0,
                          lengths: Optional[torch.Tensor] = None) -> DTWResult:
     """Soft DTW between feature sequences x [B, L1, D] and y [B, L2, D] (1 <= D <= 128)
-    under the squared-Euclidean cost, formed inside the sweeps.
+    under the squared-Euclidean cost, formed inside the forward sweep.
 
     Same result as ``soft_dtw(torch.cdist(x, y) ** 2, ...)`` up to the rounding of the
     costs (each a sum of D squares in float32); gradients flow to x, y and a tensor

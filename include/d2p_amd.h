@@ -323,8 +323,9 @@ size_t d2p_dtw_workspace_bytes(int B, int max_L1, int max_L2);
 size_t d2p_dtw_workspace_bytes_banded(int B, int max_L1, int max_L2, int bandwidth);
 
 /* Fused squared-Euclidean costs + soft DTW: the forward value and marginals of soft
- * DTW over c[b,i,j] = sum_d (x[b,i,d] - y[b,j,d])^2, formed inside the sweeps from
- * the features instead of read from a cost matrix.  No counterpart in the reference:
+ * DTW over c[b,i,j] = sum_d (x[b,i,d] - y[b,j,d])^2, formed inside the forward sweep
+ * from the features instead of read from a cost matrix (the reverse sweep needs no
+ * costs).  No counterpart in the reference:
  * its callers build the costs with torch.cdist(x, y) ** 2
  * (/root/reference/docs/algorithms/dtw.md:52) and its sweeps read them
  * (/root/reference/src/dtw/kernels.cu:55-114); this entry point removes that
@@ -343,7 +344,8 @@ int d2p_dtw_sqeuclid_forward_marginals(const float* x, const float* y, const int
 /* costs[b,i,j] = sum_d (x[b,i,d] - y[b,j,d])^2 with exactly the arithmetic of the fused
  * sweeps above (bit-identical costs), for callers that need the matrix itself (the
  * fused op's marginal-path backward).  No counterpart in the reference (see above).
- *   x [B, L1, D], y [B, L2, D], costs [B, L1, L2]; 1 <= D <= 128, L1, B <= 65535 */
+ *   x [B, L1, D], y [B, L2, D], costs [B, L1, L2]; 1 <= D <= 128, B <= 65535,
+ *   L1 <= 2097120 */
 int d2p_pairwise_sqdist(const float* x, const float* y, int B, int L1, int L2, int D,
                         float* costs, void* stream);
 

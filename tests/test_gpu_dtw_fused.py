@@ -2,7 +2,7 @@
 
 No counterpart in the reference (its callers build torch.cdist(x, y) ** 2 first,
 /root/reference/docs/algorithms/dtw.md:52).  Pinned three ways:
-- the costs: d2p_amd::pairwise_sqdist (the sweeps' own arithmetic) within the
+- the costs: d2p_amd::pairwise_sqdist (the fused forward's own arithmetic) within the
   summation bound (D + 2) u sum_d (x - y)^2 (u = 2^-24) of the exact float64 costs,
   and against torch.cdist(x, y, compute_mode="donot_use_mm_for_euclid_dist") ** 2
   within twice that bound (both are float32 sums of D squares, in different orders);
