@@ -17,6 +17,7 @@
 // layout (one alpha plane).  The band test needs i*L2/L1 per row: each lane computes
 // it once per stripe, so the per-cell test is a subtraction and a compare.
 
+#include <cstdlib>
 #include <vector>
 
 #include <type_traits>
@@ -116,16 +117,17 @@ __device__ __forceinline__ void load_feature_row(float (&xr)[DC], const float* b
     for (int d = 0; d < DC; ++d) xr[d] = d < D ? p[d] : 0.0f;
 }
 
-// This lane's P cells of a forward chunk, (i0 + lane, t + u - lane), into its slots of
-// a cost tile (the layout the DMA path fills); columns are clamped into the matrix and
-// cells outside the element are masked by the sweep.  Two cells per iteration of a
-// rolled loop: unrolled over all P, the compiler would hoist every cell's LDS reads
-// and spill.
-template <int DC, int P>
+// This lane's cells u in [U0, U1) of a forward chunk, (i0 + lane, t + u - lane), into
+// its slots of a cost tile (the layout the DMA path fills); columns are clamped into
+// the matrix and cells outside the element are masked by the sweep.  Two cells per
+// iteration of a rolled loop: unrolled over all P, the compiler would hoist every
+// cell's LDS reads and spill.
+template <int DC, int U0, int U1>
 __device__ __forceinline__ void fused_costs(float* tile, int tbase, const float (&xr)[DC],
                                             const float* ylds, int t, int lane, int L2max) {
+    static_assert((U1 - U0) % 2 == 0, "cells come in pairs");
 #pragma unroll 1
-    for (int u = 0; u < P; u += 2) {
+    for (int u = U0; u < U1; u += 2) {
         const int j0 = min(max(t + u - lane, 0), L2max - 1);
         const int j1 = min(max(t + u + 1 - lane, 0), L2max - 1);
         const float c0 = sq_euclid<DC>(xr, ylds + j0 * (DC + 4));
@@ -145,8 +147,17 @@ __device__ __forceinline__ void stage_features(float* ylds, const float* yb, int
     }
 }
 
-// DC > 0: fused costs from fx [B, L1max, D] and fy [B, L2max, D] (costs unused)
-template <int DC = 0>
+// Steps of a fused chunk whose costs a helper wave forms (HELP); the sweeping wave
+// forms the rest itself, just before its DP steps (the split balances the two waves'
+// instruction streams on their shared SIMD).
+constexpr int HELP_U = 12;
+
+// DC > 0: fused costs from fx [B, L1max, D] and fy [B, L2max, D] (costs unused).
+// HELP (fused, at most NW/2 stripes per part): wave NW/2 + l forms steps
+// [0, HELP_U) of every chunk of stripe l's costs into a double-buffered tile one chunk
+// ahead, publishing cprog[l] = chunks formed; it reuses a buffer once the sweeping
+// wave l has finished the chunk that read it (prog[l]).
+template <int DC = 0, bool HELP = false>
 __global__ void __launch_bounds__(NW * 64)
 dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ lengths,
                    float* __restrict__ alpha_sk, float* __restrict__ brow,
@@ -157,8 +168,11 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                    int D) {
     constexpr int P = PF;
     constexpr bool FUSED = DC > 0;
+    static_assert(!HELP || FUSED, "helper waves form fused costs");
+    static_assert(!HELP || P == 16, "the helper split assumes 16-step chunks");
     extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
+    __shared__ int cprog[NW];     // HELP: chunks of stripe l's costs formed by its helper
     __shared__ float terminal;
     // part of the element as in the linear-SW forward: the first stripe of a part > 0
     // reads the previous part's last row from brow
@@ -169,10 +183,11 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = ChunkTile<P>;
-    // two cost chunks (fused: one, computed in place), two rows
-    constexpr int WBUF = (FUSED ? 1 : 2) * Tile::FLOATS + 2 * 64;
+    // two cost chunks (fused without helpers: one, computed in place), two rows
+    constexpr int NTILE = (FUSED && !HELP) ? 1 : 2;
+    constexpr int WBUF = NTILE * Tile::FLOATS + 2 * 64;
     float* tiles = smem + wave * WBUF;                     // double-buffered cost chunk
-    float* rbufs = tiles + (FUSED ? 1 : 2) * Tile::FLOATS; // boundary row of a chunk
+    float* rbufs = tiles + NTILE * Tile::FLOATS;           // boundary row of a chunk
     __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
                                   // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
@@ -182,7 +197,10 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
 
-    if (lane == 0) prog[wave] = -1;
+    if (lane == 0) {
+        prog[wave] = -1;
+        cprog[wave] = -1;
+    }
     if (threadIdx.x == 0) {
         if (G == 1) *st = 0;                               // G > 1: reset before the launch
         terminal = kPINF;
@@ -210,6 +228,34 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
     if ((size_t)NS * stride > elem_steps) {   // never: the host reserves enough
         if (threadIdx.x == 0) atomicOr(st, 2);
         return;
+    }
+
+    if constexpr (HELP) {
+        if (NL > NW / 2) {   // never: the host picks HELP for parts of at most NW/2 stripes
+            if (threadIdx.x == 0) atomicOr(st, 2);
+            return;
+        }
+        // helper of stripe l: its chunks' costs, steps [0, HELP_U), one chunk ahead
+        const int l = wave - NW / 2;
+        if (l >= 0 && l < NL) {
+            const int s = s_begin + l;
+            int t_lo, t_hi;
+            band_window(s, L1, L2, bw, t_lo, t_hi);
+            const int k_lo =
+                __builtin_amdgcn_readfirstlane(t_lo <= t_hi ? min(t_lo / P, nch) : nch);
+            const int k_end = __builtin_amdgcn_readfirstlane(t_lo <= t_hi ? t_hi / P + 1 : nch);
+            float xr[DC];
+            load_feature_row<DC>(xr, fx + (size_t)b * L1max * D, min(s * 64 + lane, L1max - 1),
+                                 D);
+            float* ctiles = smem + l * WBUF;   // stripe l's two cost tiles
+            for (int k = k_lo; k < k_end; ++k) {
+                // buffer k & 1 last held chunk k - 2: free once wave l has finished it
+                if (k >= k_lo + 2) wait_for(prog, l, l * PROG_STRIDE + k - 1, st);
+                fused_costs<DC, 0, HELP_U>(ctiles + (k & 1) * Tile::FLOATS, tbase, xr, ylds,
+                                           k * P, lane, L2max);
+                publish(cprog, l, k + 1);
+            }
+        }
     }
 
     for (int l = wave; l < NL; l += NW) {
@@ -294,9 +340,14 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                 const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
-            const float* tile = tiles + (FUSED ? 0 : (k & 1) * Tile::FLOATS);
+            float* tile = tiles + (NTILE == 2 ? (k & 1) * Tile::FLOATS : 0);
             float cv[P];
-            if constexpr (FUSED) fused_costs<DC, P>(tiles, tbase, xr, ylds, t0, lane, L2max);
+            if constexpr (HELP) {
+                wait_for(cprog, l, k + 1, st);   // the helper's steps [0, HELP_U)
+                fused_costs<DC, HELP_U, P>(tile, tbase, xr, ylds, t0, lane, L2max);
+            } else if constexpr (FUSED) {
+                fused_costs<DC, 0, P>(tile, tbase, xr, ylds, t0, lane, L2max);
+            }
 #pragma unroll
             for (int u = 0; u < P; ++u) cv[u] = tile[tbase + u];
             // lane 0's up values: column t0+j sits in lane j (row 0 is PINF; so are the
@@ -784,9 +835,16 @@ int feature_chunk(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 :
 
 size_t feature_lds(int max_L2, int DC) { return (size_t)max_L2 * (DC + 4) * sizeof(float); }
 
-size_t lds_forward_fused(int R, int DC, int max_L2) {
-    return (size_t)NW * (65 * PF + 2 * 64) * sizeof(float) +
+// LDS of a fused forward workgroup with ntile cost tiles per wave (2: helper waves)
+size_t lds_forward_fused(int R, int DC, int max_L2, int ntile = 1) {
+    return (size_t)NW * (ntile * 65 * PF + 2 * 64) * sizeof(float) +
            ((size_t)NW * R + NW * DUMMY) * sizeof(float) + feature_lds(max_L2, DC);
+}
+
+// D2P_AMD_FUSED_HELPERS=0 turns the helper waves off (for tests: both forms must agree)
+bool force_no_helpers() {
+    const char* e = std::getenv("D2P_AMD_FUSED_HELPERS");
+    return e && e[0] == '0';
 }
 
 int check_fused(int B, int max_L1, int max_L2, int D, float T) {
@@ -807,10 +865,15 @@ int launch_fused(const float* x, const float* y, const int* lengths, int B, int 
     const bool whole = lds_forward_fused(ring_forward(max_L1, max_L2), DC, max_L2) <= kLdsLimit;
     const Split sp = choose_split(B, max_L1, ws, whole ? 0 : NW);
     const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
-    const size_t lds = lds_forward_fused(R, DC, max_L2);
+    // helper waves form most of each chunk's costs when a part has at most NW/2
+    // stripes (the other waves are idle) and two cost tiles per wave fit
+    const int part_stripes = sp.G > 1 ? sp.SPW : ns;
+    const bool help = part_stripes <= NW / 2 &&
+                      lds_forward_fused(R, DC, max_L2, 2) <= kLdsLimit && !force_no_helpers();
+    const size_t lds = lds_forward_fused(R, DC, max_L2, help ? 2 : 1);
     D2P_REQUIRE(lds <= kLdsLimit, "fused DTW: sequence too long for LDS");
     if (sp.G > 1 && launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
-    auto kern = dtw_forward_kernel<DC>;
+    auto kern = help ? dtw_forward_kernel<DC, true> : dtw_forward_kernel<DC, false>;
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
     D2P_LAUNCH("dtw_fused_forward", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st,

@@ -108,6 +108,22 @@ def test_fused_ragged_and_split(cuda, parts):
         assert torch.equal(f.alignment, p.alignment), n
 
 
+@pytest.mark.parametrize("B,L1,L2,D,n_parts", [(4, 256, 256, 64, 1), (2, 700, 110, 24, 4),
+                                               (1, 200, 130, 128, 1), (3, 64, 90, 5, 1)])
+def test_fused_helper_waves_bit_identical(cuda, parts, monkeypatch, B, L1, L2, D, n_parts):
+    """Parts of at most four stripes form most of each chunk's costs in helper waves;
+    a cell's cost is the same arithmetic whichever wave forms it, so every output
+    equals the single-wave form bit for bit (split parts included)."""
+    x, y = _seeded(31, (B, L1, D)).to(cuda), _seeded(32, (B, L2, D)).to(cuda)
+    parts(n_parts)
+    monkeypatch.setenv("D2P_AMD_FUSED_HELPERS", "1")
+    with_h = _capi.dtw_sqeuclid_forward_marginals(x, y, None, 0.3)
+    monkeypatch.setenv("D2P_AMD_FUSED_HELPERS", "0")
+    without = _capi.dtw_sqeuclid_forward_marginals(x, y, None, 0.3)
+    for a, b in zip(with_h, without):
+        assert torch.equal(a, b)
+
+
 def test_fused_rejects_bad_inputs(cuda):
     import d2p_amd
     x = torch.randn(2, 10, 8, device=cuda)
