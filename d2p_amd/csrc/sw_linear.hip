@@ -297,8 +297,16 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
 // NWG: global alignment (/root/reference/src/nw/kernels_cpu.cpp:160-265): beta starts
 // at 1 in the terminal cell only, the marginal is beta * w_diag, and the flows into
 // row 0 and column 0 (whose alphas encode j*gap and i*gap) add flow * gaps to dS/dgap.
-template <int P, bool PRECISE = false, bool NWG = false>
-__global__ void __launch_bounds__(NW * 64)
+// HELP (plain variant, parts of at most NW/2 stripes): wave NW/2 + q moves stripe order
+// q's data, so the sweeping wave only sweeps.  It loads each chunk's score quads and
+// alpha rows one chunk ahead (publishing hprog[q] = chunks loaded), and writes a
+// chunk's marginals out once wave q has finished the chunk (prog[q]).  The marginals
+// go to the helper's own (otherwise unused) chunk buffers, so the helper can reload
+// the sweeping wave's input buffer before it writes them out.
+// (one workgroup per CU: its LDS allows no second; waves_per_eu says so, so that the
+// register allocator does not spill to reach an occupancy the launch cannot have)
+template <int P, bool PRECISE = false, bool NWG = false, bool HELP = false>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
 sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                    const float* __restrict__ alpha_sk, const float* __restrict__ brow,
                    const float* __restrict__ partition,
@@ -344,12 +352,17 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     // otherwise (PRECISE, NWG: those variants have no registers to spare) a dword tile,
     // one write per step, leaving with P dword stores.
     constexpr bool QOUT = !PRECISE && !NWG;
+    static_assert(!HELP || QOUT, "helper waves write quad output tiles");
+    __shared__ int hprog[NW];     // HELP: chunks of stripe order q loaded by its helper
     using OutTile = ChunkTile<P>;
     static_assert(OutTile::FLOATS <= BUF, "output tile fits the chunk buffer");
     const int obase_lane = OutTile::read_base(lane);
     constexpr int NSTORE = QOUT ? Tile::NQ : P;   // stores of an inside chunk
 
-    if (lane == 0) prog[wave] = -1;
+    if (lane == 0) {
+        prog[wave] = -1;
+        hprog[wave] = -1;
+    }
     __syncthreads();
 
     const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
@@ -376,6 +389,47 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     const bool has_next = s_begin + NL < NS;
     const uint64_t* flag_in = bflag + (size_t)b * G + (part + 1 < G ? part + 1 : part);
     uint64_t* flag_out = bflag + (size_t)b * G + part;
+
+    if constexpr (HELP) {
+        if (NL > NW / 2) {   // never: the host picks HELP for parts of at most NW/2 stripes
+            if (threadIdx.x == 0) atomicOr(st, 2);
+            return;
+        }
+        const int q = wave - NW / 2;
+        if (q >= 0 && q < NL) {
+            const int s = s_begin + NL - 1 - q;
+            const int i0 = s * 64;
+            const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * NT * 64;
+            float* qbufs = smem + q * 2 * BUF;   // the sweeping wave's two chunk buffers
+            float* obufs = smem + wave * 2 * BUF;  // its output tiles (this wave's buffers)
+            auto load = [&](int k) {
+                const int th = nsteps - 1 - k * P;
+                const uint32_t buf = lds_address(qbufs + (k & 1) * BUF);
+                dma_quads<P, -1>(buf, sbase, i0, L1max, L2max, lane, th);
+                dma_rows<P, -1>(buf + ABUF * 4, astripe, th - 2, ul4);
+            };
+            if (nch > 0) {
+                load(0);
+                wait_vmcnt<0>();
+                publish(hprog, q, 1);
+                if (nch > 1) load(1);
+            }
+            for (int k = 0; k < nch; ++k) {
+                if (k + 1 < nch) {
+                    // chunk k + 1's loads: the last issued at k = 0, else followed by
+                    // the (at least P/4) marginal stores of chunk k - 1
+                    if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<Tile::NQ>();
+                    publish(hprog, q, k + 2);   // also completes this wave's LDS reads
+                }
+                // once wave q has finished chunk k, its input buffer k & 1 takes chunk
+                // k + 2 and its marginals (in output tile k & 1) leave
+                wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
+                if (k + 2 < nch) load(k + 2);
+                write_quads<P, -1>(obufs + (k & 1) * BUF, pbase, trash, i0, L1, L2, L1max, L2max,
+                                   lane, nsteps - 1 - k * P);
+            }
+        }
+    }
 
     // Stripes run bottom-up: order q = 0..NL-1 handles stripe s_begin+NL-1-q, on wave
     // q % NW.
@@ -411,8 +465,10 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
             const uint32_t buf = lds_address(bufs + (k & 1) * BUF);
-            dma_quads<P, -1>(buf, sbase, i0, L1max, L2max, lane, th);
-            dma_rows<P, -1>(buf + ABUF * 4, astripe, th - 2, ul4);
+            if (!HELP) {
+                dma_quads<P, -1>(buf, sbase, i0, L1max, L2max, lane, th);
+                dma_rows<P, -1>(buf + ABUF * 4, astripe, th - 2, ul4);
+            }
             uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
             uint32_t rl = buf + RBUF * 4;
             lds_dma_dword<0>(bup, roff, rl, 0u);
@@ -442,14 +498,25 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             chunk_waits<P>(prog, q, NL, k, nch, R, st);
             // this chunk's loads were issued one chunk ago and followed by at least the
             // NSTORE marginal stores of that chunk (P in a boundary chunk; the first
-            // chunk's loads are the last issued)
-            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<NSTORE>();
+            // chunk's loads are the last issued).  HELP: the helper loads the tiles; this
+            // wave's own loads (row above, flows) are followed by nothing, or by the
+            // previous chunk's flow store (x_out)
+            if constexpr (HELP) {
+                if (x_out && k > 0) wait_vmcnt<1>(); else wait_vmcnt<0>();
+                wait_for(hprog, q, k + 1, st);
+            } else {
+                if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<NSTORE>();
+            }
             if (x_in && k > 0) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
             float* buf = bufs + (k & 1) * BUF;
+            // the chunk's marginal quads: over its own score tile, or (HELP) in the
+            // helper's buffer k & 1, whose previous tile the helper has written out
+            // before publishing this chunk as loaded
+            float* obuf = HELP ? smem + (wave + NW / 2) * 2 * BUF + (k & 1) * BUF : buf;
             float sv[P];
             read_quads<P, -1>(buf, lane, sv);
             A[0] = A[P];
@@ -558,7 +625,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     if ((u & 3) == 2) quad.y = pv;
                     if ((u & 3) == 3) {
                         quad.x = pv;
-                        *reinterpret_cast<float4*>(buf + Tile::slot(lane, u >> 2)) = quad;
+                        *reinterpret_cast<float4*>(obuf + Tile::slot(lane, u >> 2)) = quad;
                     }
                 } else {
                     buf[obase_lane + u] = pv;
@@ -598,7 +665,9 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             // write this chunk's marginals back over the cells the scores came from:
             // NSTORE stores (P dword stores in a boundary chunk, where cells outside the
             // element's lengths go to the trash line; inside chunks carry 0 there)
-            if constexpr (QOUT)
+            if constexpr (HELP)
+                ;   // the helper writes the tile once this chunk is published
+            else if constexpr (QOUT)
                 write_quads<P, -1>(buf, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             else
                 write_tile<P, -1>(buf, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
@@ -609,8 +678,10 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 if (k >= 2) {
                     // at least (2 P/4 + 1) loads and NSTORE stores of chunk k - 1, NSTORE
                     // stores of chunk k and the two chunks' flow stores follow the flow
-                    // store of chunk k - 2: it is complete
-                    wait_vmcnt<2 * Tile::NQ + 2 * NSTORE + 3>();
+                    // store of chunk k - 2 (HELP: the row-above load issued in chunk
+                    // k - 1 and the two flow stores): it is complete
+                    if constexpr (HELP) wait_vmcnt<3>();
+                    else wait_vmcnt<2 * Tile::NQ + 2 * NSTORE + 3>();
                     if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
                 }
             }
@@ -756,7 +827,7 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
     return D2P_OK;
 }
 
-template <int P, bool PRECISE, bool NWG>
+template <int P, bool PRECISE, bool NWG, bool HELP = false>
 int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                       float gap, float T, const Layout& ws, const float* partition,
                       float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
@@ -766,9 +837,9 @@ int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     const uint32_t epoch = next_epoch();
     if (sp.G > 1) D2P_TRY(wf::launch_flag_reset(ws.bflag, B * sp.G, st));
-    D2P_HIP(hipFuncSetAttribute((const void*)sw_backward_kernel<P, PRECISE, NWG>,
+    D2P_HIP(hipFuncSetAttribute((const void*)sw_backward_kernel<P, PRECISE, NWG, HELP>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH(NWG ? "nw_backward" : "sw_backward", (sw_backward_kernel<P, PRECISE, NWG>),
+    D2P_LAUNCH(NWG ? "nw_backward" : "sw_backward", (sw_backward_kernel<P, PRECISE, NWG, HELP>),
                dim3(wf::split_grid(B, sp.G)),
                dim3(wf::NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
                marginals, grad_gap, grad_T, ws.status, ws.trash, ws.bflag, ws.flows, ws.bpart,
@@ -779,6 +850,12 @@ int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1
                    st, ws.bpart, partition, grad_gap, grad_T, B, sp.G, gap, T);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
+}
+
+// D2P_AMD_SW_HELPERS=0 turns the helper waves off (for tests: both forms must agree)
+static bool helpers_enabled() {
+    const char* e = std::getenv("D2P_AMD_SW_HELPERS");
+    return !(e && e[0] == '0');
 }
 
 int launch_backward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
@@ -797,6 +874,12 @@ int launch_backward(const float* scores, const int* lengths, int B, int max_L1, 
         if (P == 16) return precise ? D2P_SW_BWD(16, true, true) : D2P_SW_BWD(16, false, true);
         return precise ? D2P_SW_BWD(8, true, true) : D2P_SW_BWD(8, false, true);
     }
+    // helper waves move the data when a part has at most NW/2 stripes (the others idle)
+    const bool help = !precise && P == 16 && (rows + 63) / 64 <= wf::NW / 2 && helpers_enabled();
+    if (help)
+        return launch_backward_p<16, false, false, true>(scores, lengths, B, max_L1, max_L2, gap,
+                                                         T, ws, partition, marginals, grad_gap,
+                                                         grad_T, st, sp, R, poison_value);
     if (P == 16) return precise ? D2P_SW_BWD(16, true, false) : D2P_SW_BWD(16, false, false);
     return precise ? D2P_SW_BWD(8, true, false) : D2P_SW_BWD(8, false, false);
 #undef D2P_SW_BWD
