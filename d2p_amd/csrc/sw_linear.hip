@@ -48,7 +48,13 @@ constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do 
 // column 0 carry their row's i*gap, so the left and diagonal neighbours of column 0
 // come out of the same registers), and `partition` receives the terminal cell
 // alpha[L1, L2] instead of the LSE over all cells.
-template <bool NWG = false>
+//
+// HELP (parts of at most NW/2 stripes): wave NW/2 + l moves stripe l's data, so the
+// sweeping wave only sweeps.  It loads each chunk's score quads one chunk ahead
+// (publishing hprog[l] = chunks loaded), and writes a chunk's alpha rows (which the
+// sweeping wave leaves in the helper's own, otherwise unused, tile buffers) to the
+// table as one contiguous 4 KB block once wave l has finished the chunk (prog[l]).
+template <bool NWG = false, bool HELP = false>
 __global__ void __launch_bounds__(NW * 64)
 sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                   float* __restrict__ alpha_sk, float* __restrict__ brow,
@@ -59,6 +65,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     constexpr int P = PF;
     extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
+    __shared__ int hprog[NW];     // HELP: chunks of stripe l loaded by its helper
     __shared__ float red_m[NW], red_z[NW];
     __shared__ float terminal;   // NWG: alpha[L1, L2]
     int b, part;
@@ -79,7 +86,10 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     float* sink = rings + NW * R + wave * DUMMY;           // per-wave write sink
     int* st = status + b;
 
-    if (lane == 0) prog[wave] = -1;
+    if (lane == 0) {
+        prog[wave] = -1;
+        hprog[wave] = -1;
+    }
     if (G == 1 && threadIdx.x == 0) *st = 0;               // G > 1: reset before the launch
     if (NWG && threadIdx.x == 0) terminal = kNINF;
     __syncthreads();
@@ -101,6 +111,49 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
 
     OnlineLSE acc;
     acc.init_open();
+
+    if constexpr (HELP) {
+        if (NL > NW / 2) {   // never: the host picks HELP for parts of at most NW/2 stripes
+            if (threadIdx.x == 0) atomicOr(st, 2);
+            return;
+        }
+        const int l = wave - NW / 2;
+        if (l >= 0 && l < NL) {
+            const int i0 = (s_begin + l) * 64;
+            float* out = alpha_sk + (((size_t)b * NSmax + s_begin + l) * NT + APAD) * 64;
+            const uint32_t ltiles = lds_address(smem + l * WBUF);   // wave l's score tiles
+            const float* atiles = smem + wave * WBUF;                // its alpha tiles
+            auto load = [&](int k) {
+                dma_quads<P, 1>(ltiles + (k & 1) * Tile::FLOATS * 4, sbase, i0, L1max, L2max,
+                                lane, k * P);
+            };
+            if (nch > 0) {
+                load(0);
+                wait_vmcnt<0>();
+                publish(hprog, l, 1);
+                if (nch > 1) load(1);
+            }
+            for (int k = 0; k < nch; ++k) {
+                if (k + 1 < nch) {
+                    // chunk k + 1's loads: the last issued at k = 0, else followed by
+                    // the P/4 alpha stores of chunk k - 1
+                    if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<Tile::NQ>();
+                    publish(hprog, l, k + 2);   // also completes this wave's LDS reads
+                }
+                // once wave l has finished chunk k, its score tile k & 1 takes chunk
+                // k + 2 and its alpha rows (alpha tile k & 1) go to the table
+                wait_for(prog, l, l * PROG_STRIDE + k + 1, st);
+                if (k + 2 < nch) load(k + 2);
+                const float* at = atiles + (k & 1) * Tile::FLOATS;
+                float* dst = out + (size_t)k * P * 64;
+#pragma unroll
+                for (int i = 0; i < Tile::NQ; ++i) {
+                    const float4 v = *reinterpret_cast<const float4*>(at + 256 * i + 4 * lane);
+                    *reinterpret_cast<float4*>(dst + 256 * i + 4 * lane) = v;
+                }
+            }
+        }
+    }
 
     for (int l = wave; l < NL; l += NW) {
         const int s = s_begin + l;
@@ -134,7 +187,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
             issue_row(0);
         }
-        dma_quads<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
+        if (!HELP) dma_quads<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
         // NWG: lane r starts beside column 0 of its row, its diagonal beside column 0
         // of the row above (alpha[0,0] = 0 for lane 0 of the first stripe)
         float cur = left0, up_prev = NWG ? (float)(i0 + lane) * gap : kNINF;
@@ -145,8 +198,15 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             const int t0 = k * P;
             chunk_waits<P>(prog, l, NL, k, nch, R, st);
             // this chunk's loads were issued one chunk ago and followed by at least the
-            // P + 1 stores of that chunk (the first chunk's loads are the last issued)
-            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            // P + 1 stores of that chunk (the first chunk's loads are the last issued).
+            // HELP: the helper loads the scores; this wave's own loads (the row above
+            // of a part's first stripe) are followed by the last-row store
+            if constexpr (HELP) {
+                if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<1>();
+                wait_for(hprog, l, k + 1, st);
+            } else {
+                if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            }
             if (x_in && k > 0) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
@@ -186,14 +246,19 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
                     issue_row(k + 1);
                 }
-                dma_quads<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0, L1max,
-                                  L2max, lane, t0 + P);
+                if (!HELP)
+                    dma_quads<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0,
+                                    L1max, L2max, lane, t0 + P);
                 if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             // lane 63 publishes its alpha of step u into ring slot (t0+u) % R; the
             // other lanes write into the sink (R is a multiple of P: no wrap in a chunk)
             float* pub = (lane == 63) ? ring_out + slot0 : sink + lane;
             float* outc = out + (size_t)t0 * 64;
+            // HELP: the chunk's alphas by step in the helper's tile k & 1 (written out
+            // by the helper; it has written that tile's previous chunk before
+            // publishing this one as loaded)
+            float* atile = smem + (wave + NW / 2) * WBUF + (k & 1) * Tile::FLOATS + lane;
             // FULL: every cell of the chunk lies inside the element, no validity masks
             auto steps = [&](auto full) {
                 constexpr bool FULL = decltype(full)::value;
@@ -235,7 +300,8 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                         // column stays below L2 - 1 there)
                         if (NWG && ok && last_row && col == L2 - 1) terminal = a;
                     }
-                    lane_store(outc + u * 64, ul4, cur);
+                    if (HELP) atile[u * 64] = cur;
+                    else lane_store(outc + u * 64, ul4, cur);
                     pub[u] = cur;
                     av[u] = cur;
                     if (!NWG) bm = fmaxf(bm, cur);
@@ -254,9 +320,11 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             }
             publish(prog, wave, l * PROG_STRIDE + k + 1);
             if (x_out && k >= 2) {
-                // at least 2 * (P/4 + P + 1) vector-memory operations follow the row
-                // stores of chunk k - 2: those (and everything before) are complete
-                wait_vmcnt<2 * (Tile::NQ + P + 1) - Tile::NQ>();
+                // at least 2 * (P/4 + P + 1) vector-memory operations (HELP: the last
+                // row stores of chunks k - 1 and k) follow the row stores of chunk
+                // k - 2: those (and everything before) are complete
+                if constexpr (HELP) wait_vmcnt<2>();
+                else wait_vmcnt<2 * (Tile::NQ + P + 1) - Tile::NQ>();
                 if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
             }
         }
@@ -795,6 +863,27 @@ int check_shape(int B, int max_L1, int max_L2, float temperature) {
     return D2P_OK;
 }
 
+// D2P_AMD_SW_HELPERS=0 turns the helper waves off (for tests: both forms must agree)
+static bool helpers_enabled() {
+    const char* e = std::getenv("D2P_AMD_SW_HELPERS");
+    return !(e && e[0] == '0');
+}
+
+template <bool NWG, bool HELP>
+int launch_forward_k(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
+                     float gap, float T, const Layout& ws, float* partition, hipStream_t st,
+                     const Split& sp, int R, size_t lds, uint32_t epoch) {
+    const int ns = (max_L1 + 63) / 64;
+    D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel<NWG, HELP>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    D2P_LAUNCH(NWG ? "nw_forward" : "sw_forward", (sw_forward_kernel<NWG, HELP>),
+               dim3(wf::split_grid(B, sp.G)), dim3(wf::NW * 64), lds, st, scores, lengths,
+               ws.alpha_sk, ws.brow, partition, ws.status, ws.fflag, ws.fpart, B, max_L1, max_L2,
+               ns, gap, T, R, sp.G, sp.SPW, epoch);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
 int launch_forward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                    float gap, float T, const Layout& ws, float* partition, hipStream_t st,
                    bool global) {
@@ -805,22 +894,15 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     const uint32_t epoch = next_epoch();
     if (sp.G > 1 && wf::launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
-    if (global) {
-        D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel<true>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        D2P_LAUNCH("nw_forward", sw_forward_kernel<true>, dim3(wf::split_grid(B, sp.G)),
-                   dim3(wf::NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
-                   ws.status, ws.fflag, ws.fpart, B, max_L1, max_L2, ns, gap, T, R, sp.G, sp.SPW,
-                   epoch);
-        D2P_HIP(hipGetLastError());
-        return D2P_OK;   // the owner part writes the value: no merge
-    }
-    D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel<false>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH("sw_forward", sw_forward_kernel<false>, dim3(wf::split_grid(B, sp.G)),
-               dim3(wf::NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
-               ws.status, ws.fflag, ws.fpart, B, max_L1, max_L2, ns, gap, T, R, sp.G, sp.SPW,
-               epoch);
+    // helper waves move the data when a part has at most NW/2 stripes (the others idle)
+    const bool help = ((sp.G > 1 ? sp.SPW : ns) <= wf::NW / 2) && helpers_enabled();
+#define D2P_SW_FWD(G_, H_) \
+    launch_forward_k<G_, H_>(scores, lengths, B, max_L1, max_L2, gap, T, ws, partition, st, sp, R, \
+                             lds, epoch)
+    if (global) return help ? D2P_SW_FWD(true, true) : D2P_SW_FWD(true, false);
+    // (the owner part writes the NW value: no merge)
+    D2P_TRY(help ? D2P_SW_FWD(false, true) : D2P_SW_FWD(false, false));
+#undef D2P_SW_FWD
     if (sp.G > 1 && wf::launch_partition_merge(ws, partition, B, sp.G, T, st) != D2P_OK)
         return D2P_ERR_HIP;
     D2P_HIP(hipGetLastError());
@@ -850,12 +932,6 @@ int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1
                    st, ws.bpart, partition, grad_gap, grad_T, B, sp.G, gap, T);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
-}
-
-// D2P_AMD_SW_HELPERS=0 turns the helper waves off (for tests: both forms must agree)
-static bool helpers_enabled() {
-    const char* e = std::getenv("D2P_AMD_SW_HELPERS");
-    return !(e && e[0] == '0');
 }
 
 int launch_backward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,

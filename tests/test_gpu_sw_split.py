@@ -76,18 +76,23 @@ def test_sw_split_ragged(cuda, parts):
 
 @pytest.mark.parametrize("B,L1,L2,n", [(2, 700, 260, 4), (3, 200, 300, 1), (1, 1500, 90, 8),
                                        (4, 64, 64, 1)])
-def test_sw_backward_helper_waves_bit_identical(cuda, parts, monkeypatch, B, L1, L2, n):
-    """Parts of at most four stripes hand their data movement (tile loads, marginal
-    write-out) to helper waves; the arithmetic is unchanged, so every output equals the
-    single-wave form bit for bit, ragged lengths and split parts included."""
+def test_sw_helper_waves_bit_identical(cuda, parts, monkeypatch, B, L1, L2, n):
+    """Parts of at most four stripes hand their data movement (tile loads, the alpha
+    table and marginal write-outs) to helper waves in the forward and reverse sweeps;
+    the arithmetic is unchanged, so every output equals the single-wave form bit for
+    bit: SW and NW first order and the SW HVP (whose primal forward is the same sweep),
+    ragged lengths and split parts included."""
     s = _seeded(41, (B, L1, L2)).to(cuda)
     lens = torch.tensor([[max(1, L1 - 37 * i), max(1, L2 - 11 * i)] for i in range(B)],
                         dtype=torch.int32, device=cuda)
+    V = _seeded(42, (B, L1, L2)).to(cuda)
     parts(n)
     out = {}
     for flag in ("1", "0"):
         monkeypatch.setenv("D2P_AMD_SW_HELPERS", flag)
-        out[flag] = _capi.sw_forward_marginals(s, lens, -1.0, 0.9)
+        out[flag] = (list(_capi.sw_forward_marginals(s, lens, -1.0, 0.9)) +
+                     list(_capi.nw_forward_marginals(s, lens, -1.0, 0.9)) +
+                     [_capi.sw_hvp(s, V, lens, -1.0, 0.9)])
     for a, b in zip(out["1"], out["0"]):
         assert torch.equal(a, b)
     ref = O.get("oracle").soft_sw(s.cpu().numpy(), -1.0, 0.9, lens.cpu().numpy())
