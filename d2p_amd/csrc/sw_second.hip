@@ -28,6 +28,7 @@
 // Inputs arrive by direct-to-LDS loads one chunk ahead into one buffer per wave,
 // copied to registers at the start of each chunk before the next chunk's loads.
 
+#include <type_traits>
 #include <vector>
 
 #include "wavefront.hip.h"
@@ -55,7 +56,7 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                   int L2max, int NSmax, float gap, float T, int R, int G, int SPW,
                   uint32_t epoch) {
     constexpr bool HAS_V = MODE == HVP;
-    using Tile = ChunkTile<P>;
+    using Tile = QuadTile<P>;                                // 16-byte score/direction loads
     constexpr int VT = Tile::FLOATS;                         // direction tile
     constexpr int AR = VT + (HAS_V ? Tile::FLOATS : 0);      // P alpha rows
     constexpr int RR = AR + P * 64;                          // row above
@@ -80,7 +81,6 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     float* rings = smem + NW * BUF;                          // [NW][R] tangent of lane 63
     float* sink = rings + NW * R + wave * SINK;
     int* st = status + b;
-    const int tbase = Tile::read_base(lane);
 
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
@@ -124,8 +124,8 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
         // t0 + 62 + j (clamped; lanes past P repeat lane P).
         auto issue_chunk = [&](int k) {
             const int t0 = k * P;
-            dma_tile<P, 1>(in_lds, sbase, i0, L1max, L2max, lane, t0);
-            if (HAS_V) dma_tile<P, 1>(in_lds + VT * 4, vbase, i0, L1max, L2max, lane, t0);
+            dma_quads<P, 1>(in_lds, sbase, i0, L1max, L2max, lane, t0);
+            if (HAS_V) dma_quads<P, 1>(in_lds + VT * 4, vbase, i0, L1max, L2max, lane, t0);
             dma_rows<P, 1>(in_lds + AR * 4, astripe, t0, ul4);
             uint32_t roff = (uint32_t)min(t0 + 62 + min(lane, P), nsteps - 1) * 4u;
             uint32_t rl = in_lds + RR * 4;
@@ -167,10 +167,12 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 seen = got > seen ? got : seen;
             }
             float sv[P], vv[P];
+            read_quads<P, 1>(buf, lane, sv);
+            if (HAS_V) {
+                read_quads<P, 1>(buf + VT, lane, vv);
+            } else {
 #pragma unroll
-            for (int u = 0; u < P; ++u) {
-                sv[u] = buf[tbase + u];
-                vv[u] = HAS_V ? buf[VT + tbase + u] : 0.0f;
+                for (int u = 0; u < P; ++u) vv[u] = 0.0f;
             }
             Aw[0] = Aw[P];
             Aw[1] = Aw[P + 1];
@@ -269,9 +271,9 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             }
             publish(prog, wave, l * PROG_STRIDE + k + 1);
             if (x_out && k >= 2) {
-                // at least P + P/4 + 1 loads and 2P + 2 stores follow the row store of
-                // chunk k - 2: it (and everything before) is complete
-                wait_vmcnt<3 * P + P / 4 + 3>();
+                // at least P/4 + P/4 + 1 loads and 2P + 2 stores follow the row store
+                // of chunk k - 2: it (and everything before) is complete
+                wait_vmcnt<2 * P + Tile::NQ + P / 4 + 3>();
                 if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
             }
         }
@@ -310,7 +312,12 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                float* __restrict__ spart, int B, int L1max, int L2max, int NSmax, float gap,
                float T, int R, int G, int SPW, uint32_t epoch) {
     constexpr bool HAS_V = MODE == HVP || DOT;
-    using Tile = ChunkTile<P>;
+    // QT (8- and 16-step chunks): score, direction and output tiles move as 16-byte
+    // quads (P/4 instructions each); 4-step chunks keep dword tiles
+    constexpr bool QT = P == 8 || P == 16;
+    using Tile = typename std::conditional<QT, QuadTile<(QT ? P : 8)>, ChunkTile<P>>::type;
+    constexpr int NQ = P / 4;
+    constexpr int NSTORE = DOT ? 0 : (QT ? NQ : P);         // output stores, inside chunk
     constexpr int VT = Tile::FLOATS;
     constexpr int AR = VT + (HAS_V ? Tile::FLOATS : 0);     // P alpha rows
     constexpr int XR = AR + P * 64;                         // P tangent rows
@@ -341,7 +348,7 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     float4* rings = reinterpret_cast<float4*>(smem + NW * BUF);   // [NW][R]
     float4* sink = rings + NW * R + wave * SINK;
     int* st = status + b;
-    const int tbase = Tile::read_base(lane);
+    const int tbase = ChunkTile<P>::read_base(lane);   // dword tiles (4-step chunks)
 
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
@@ -400,8 +407,13 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
 
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
-            dma_tile<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
-            if (HAS_V) dma_tile<P, -1>(in_lds + VT * 4, vbase, i0, L1max, L2max, lane, th);
+            if constexpr (QT) {
+                dma_quads<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
+                if (HAS_V) dma_quads<P, -1>(in_lds + VT * 4, vbase, i0, L1max, L2max, lane, th);
+            } else {
+                dma_tile<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
+                if (HAS_V) dma_tile<P, -1>(in_lds + VT * 4, vbase, i0, L1max, L2max, lane, th);
+            }
             dma_rows<P, -1>(in_lds + AR * 4, astripe, th - 2, ul4);
             dma_rows<P, -1>(in_lds + XR * 4, xstripe, th - 2, ul4);
             const uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
@@ -439,20 +451,30 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
         for (int k = 0; k < nch; ++k) {
             const int t_hi = nsteps - 1 - k * P;
             chunk_waits<P>(prog, q, NL, k, nch, R, st);
-            // this chunk's loads, followed by at least the P output stores of the
+            // this chunk's loads, followed by at least the NSTORE output stores of the
             // previous chunk (none when accumulating a dot product; the first chunk's
             // loads are the last issued)
-            if (k == 0 || DOT) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (k == 0 || DOT) wait_vmcnt<0>(); else wait_vmcnt<NSTORE>();
             if (x_in && k > 0) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
             float sv[P], vv[P];
+            if constexpr (QT) {
+                read_quads<P, -1>(buf, lane, sv);
+                if (HAS_V) {
+                    read_quads<P, -1>(buf + VT, lane, vv);
+                } else {
 #pragma unroll
-            for (int u = 0; u < P; ++u) {
-                sv[u] = buf[tbase + u];
-                vv[u] = HAS_V ? buf[VT + tbase + u] : 0.0f;
+                    for (int u = 0; u < P; ++u) vv[u] = 0.0f;
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < P; ++u) {
+                    sv[u] = buf[tbase + u];
+                    vv[u] = HAS_V ? buf[VT + tbase + u] : 0.0f;
+                }
             }
             A[0] = A[P];
             A[1] = A[P + 1];
@@ -515,6 +537,9 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             }
             qdb = wave_shr1(wave_shr1(qdb));
             qdg = wave_shr1(wave_shr1(qdg));
+            // QT: the output quad being filled, memory-column order (step 4q + 3 - e in
+            // element e); one 16-byte LDS write per four steps
+            float4 quad = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t_hi - u;
@@ -604,8 +629,19 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 const float bl = live ? beta : 0.0f;
                 const float gl = live ? g : 0.0f;
                 const float o = gl * (w0 + w3) + bl * (dw0 + dw3);
-                if (DOT) dacc += o * vd;
-                else otile[tbase + u] = o;
+                if (DOT) {
+                    dacc += o * vd;
+                } else if constexpr (QT) {
+                    if ((u & 3) == 0) quad.w = o;
+                    if ((u & 3) == 1) quad.z = o;
+                    if ((u & 3) == 2) quad.y = o;
+                    if ((u & 3) == 3) {
+                        quad.x = o;
+                        *reinterpret_cast<float4*>(otile + Tile::slot(lane, u >> 2)) = quad;
+                    }
+                } else {
+                    otile[tbase + u] = o;
+                }
                 const float ob0 = bl * w0, ob1 = bl * w1, ob2 = bl * w2;
                 const float og0 = gl * w0 + bl * dw0, og1 = gl * w1 + bl * dw1;
                 const float og2 = gl * w2 + bl * dw2;
@@ -625,15 +661,20 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 qdg = wave_shr1(qdg);
             }
             wave_lds_sync();
-            if (!DOT) write_tile<P, -1>(otile, obase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
+            if constexpr (!DOT) {
+                if constexpr (QT)
+                    write_quads<P, -1>(otile, obase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
+                else
+                    write_tile<P, -1>(otile, obase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
+            }
             publish(prog, wave, q * PROG_STRIDE + k + 1);
             if (x_out) {
                 // this chunk's flows to the part above, by producer step
                 if (lane < P) store_sys4(flows_out + k * P + lane, ring_out[ring_index(k * P, R) + lane]);
                 if (k >= 2) {
-                    // at least P + P/2 + 2 loads, 2 flow stores and (DOT: none, else 2P)
+                    // at least (QT ? P/4 : P) + P/2 + 2 loads, 2 flow stores and 2 NSTORE
                     // output stores follow the flow store of chunk k - 2: it is complete
-                    wait_vmcnt<(DOT ? P + P / 2 + 4 : 3 * P + P / 2 + 4)>();
+                    wait_vmcnt<(QT ? NQ : P) + P / 2 + 4 + 2 * NSTORE>();
                     if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
                 }
             }
