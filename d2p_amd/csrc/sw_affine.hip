@@ -84,7 +84,7 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    using Tile = ChunkTile<P>;
+    using Tile = QuadTile<P>;                             // 16-byte score loads
     constexpr int WBUF = 2 * Tile::FLOATS + 2 * 3 * 64;
     float* tiles = smem + wave * WBUF;                    // double-buffered score chunk
     float* rbufs = tiles + 2 * Tile::FLOATS;              // [2][plane][64] rows above
@@ -94,7 +94,6 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     float4* rings = reinterpret_cast<float4*>(smem + NW * WBUF);   // [NW][R]
     float4* sink = rings + NW * R + wave * DUMMY;
     int* st = status + b;
-    const int tbase = Tile::read_base(lane);
 
     if (lane == 0) prog[wave] = -1;
     if (G == 1 && threadIdx.x == 0) *st = 0;              // G > 1: reset before the launch
@@ -160,7 +159,7 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
             issue_rows(0);
         }
-        dma_tile<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
+        dma_quads<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
         float cM = kNINF, cI = bndI, cD = kNINF;       // this lane's previous step
         float pM = kNINF, pI = kNINF, pD = kNINF;      // up values of the previous step
         if (NWA && lane == 0) {
@@ -182,8 +181,7 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             }
             const float* tile = tiles + (k & 1) * Tile::FLOATS;
             float sv[P], aM[P], aI[P], aD[P];
-#pragma unroll
-            for (int u = 0; u < P; ++u) sv[u] = tile[tbase + u];
+            read_quads<P, 1>(tile, lane, sv);
             // lane 0's up values: column t0+j sits in lane j (NWA, first stripe: row 0,
             // where only D[0, t0+j+1] = open + (t0+j) ext is finite)
             float rM = kNINF, rI = kNINF, rD = kNINF;
@@ -207,8 +205,8 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
                     issue_rows(k + 1);
                 }
-                dma_tile<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0, L1max,
-                               L2max, lane, t0 + P);
+                dma_quads<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0, L1max,
+                                L2max, lane, t0 + P);
                 if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             float4* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
@@ -284,7 +282,7 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             }
             publish(prog, wave, l * PROG_STRIDE + k + 1);
             if (x_out && k >= 2) {
-                // at least P loads and 6P + 6 stores follow the row stores of chunk
+                // at least P/4 loads and 6P + 6 stores follow the row stores of chunk
                 // k - 2 (more than the counter holds): those are complete
                 wait_vmcnt<63>();
                 if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
@@ -362,8 +360,13 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // Per wave: one in-flight input buffer (scores tile, P rows of each alpha plane,
     // the row above for each plane), read into registers at the start of each chunk
-    // before the next chunk's loads are issued into it, and one output tile.
-    using Tile = ChunkTile<P>;
+    // before the next chunk's loads are issued into it, and one output tile.  In the
+    // local form (QT) the score and output tiles move as 16-byte quads (P/4
+    // instructions each), and the output quad of four steps is assembled in
+    // registers; the global form runs at the register limit and keeps dword tiles.
+    constexpr bool QT = !NWA;
+    using Tile = std::conditional_t<QT, QuadTile<P>, ChunkTile<P>>;
+    constexpr int NQ = QT ? P / 4 : P;              // tile load or store instructions
     constexpr int AROWS = Tile::FLOATS;             // 3 planes x P rows x 64
     constexpr int RROW = AROWS + 3 * P * 64;        // 3 planes x 64
     constexpr int OTILE = RROW + 3 * 64;
@@ -386,7 +389,7 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                                       NW * (64 + P)) + wave * (64 + P);
     F1* flowsF = reinterpret_cast<F1*>(flows1);
     int* st = status + b;
-    const int tbase = Tile::read_base(lane);
+    const int tbase = ChunkTile<P>::read_base(lane);   // dword tiles
 
     if (lane == 0) prog[wave] = -1;
     __syncthreads();
@@ -441,10 +444,11 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
         // Loads of chunk k (t_hi = nsteps-1-kP): the score tile, P alpha rows per plane
         // (steps t_hi-2 .. t_hi-P-1) and the stripe above's last row per plane at steps
         // t_hi - j + 63 for lane j <= P (clamped; lanes past P repeat lane P).
-        // P + 3P/4 + 3 loads.
+        // NQ + 3P/4 + 3 loads.
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
-            dma_tile<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
+            if constexpr (QT) dma_quads<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
+            else dma_tile<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
 #pragma unroll
             for (int pl = 0; pl < 3; ++pl)
                 dma_rows<P, -1>(in_lds + (AROWS + pl * P * 64) * 4, astripe + pl * PLANE, th - 2,
@@ -502,17 +506,21 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
         for (int k = 0; k < nch; ++k) {
             const int t_hi = nsteps - 1 - k * P;
             chunk_waits<P>(prog, q, NL, k, nch, R, st);
-            // this chunk's loads, followed by at least the P marginal stores of the
+            // this chunk's loads, followed by at least the NQ marginal stores of the
             // previous chunk (the first chunk's loads are the last issued)
-            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<NQ>();
             if (x_in && k > 0) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
             float sv[P];
+            if constexpr (QT) {
+                read_quads<P, -1>(wbuf, lane, sv);
+            } else {
 #pragma unroll
-            for (int u = 0; u < P; ++u) sv[u] = wbuf[tbase + u];
+                for (int u = 0; u < P; ++u) sv[u] = wbuf[tbase + u];
+            }
             AM[0] = AM[P];
             AM[1] = AM[P + 1];
             AI[0] = AI[P];
@@ -599,6 +607,9 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
             qDM = wave_shr1(wave_shr1(qDM));
             qDI = wave_shr1(wave_shr1(qDI));
             qDD = wave_shr1(wave_shr1(qDD));
+            // the output quad being filled, memory-column order (step 4q + 3 - e in
+            // element e)
+            float4 quad = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             // FULL: every cell of the chunk lies inside the element, no validity masks
             auto steps = [&](auto full) {
             constexpr bool FULL = decltype(full)::value;
@@ -673,7 +684,17 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 const float brD = (ok && betaD > lo && betaD <= 3.0e38f)
                                       ? betaD * fast_rcp(NWA ? (g0 + g1) + g2 : g0 + g1) : 0.0f;
                 const float pv = brM * esum;
-                otile[tbase + u] = pv;
+                if constexpr (QT) {
+                    if ((u & 3) == 0) quad.w = pv;
+                    if ((u & 3) == 1) quad.z = pv;
+                    if ((u & 3) == 2) quad.y = pv;
+                    if ((u & 3) == 3) {
+                        quad.x = pv;
+                        *reinterpret_cast<float4*>(otile + Tile::slot(lane, u >> 2)) = quad;
+                    }
+                } else {
+                    otile[tbase + u] = pv;
+                }
                 p_acc += pv * sc;
                 const float oUM = brI * f0, oUI = brI * f1, oUD = brI * f2;   // to (i-1, j)
                 const float oLM = brD * g0, oLD = brD * g1, oLI = brD * g2;   // to (i, j-1)
@@ -729,7 +750,10 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
             else
                 steps(std::false_type{});
             wave_lds_sync();
-            write_tile<P, -1>(otile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
+            if constexpr (QT)
+                write_quads<P, -1>(otile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
+            else
+                write_tile<P, -1>(otile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             publish(prog, wave, q * PROG_STRIDE + k + 1);
             if (x_out) {
                 // this chunk's flows to the part above, by producer step
@@ -740,9 +764,9 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                     else store_sys(flows1 + fo + k * P + lane, r1_out[slot]);
                 }
                 if (k >= 2) {
-                    // at least P + 3P/4 + 3 loads, 2P marginal stores and 4 flow stores
+                    // at least NQ + 3P/4 + 3 loads, 2 NQ marginal stores and 4 flow stores
                     // follow the flow stores of chunk k - 2: those are complete
-                    wait_vmcnt<3 * P + 3 * P / 4 + 7>();
+                    wait_vmcnt<3 * NQ + 3 * P / 4 + 7>();
                     if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
                 }
             }
@@ -811,11 +835,12 @@ constexpr size_t kLdsLimit = 160 * 1024 - 512;
 
 // LDS of one workgroup whose stripe boundaries use rings of R columns
 size_t lds_forward_r(int R) {
-    return (size_t)NW * (2 * 65 * PF + 2 * 3 * 64) * sizeof(float) +
+    return (size_t)NW * (2 * 64 * PF + 2 * 3 * 64) * sizeof(float) +
            ((size_t)NW * R + NW * DUMMY) * sizeof(float4);
 }
 size_t lds_backward_r(int R, bool nwa) {
-    const size_t wfloats = 65 * PB + 3 * PB * 64 + 3 * 64 + 65 * PB + 2 * 64;
+    const size_t tile = (nwa ? 65 : 64) * PB;   // dword or quad tiles
+    const size_t wfloats = tile + 3 * PB * 64 + 3 * 64 + tile + 2 * 64;
     const size_t f1 = nwa ? sizeof(float2) : sizeof(float);
     return (size_t)NW * wfloats * sizeof(float) + (size_t)NW * R * (sizeof(float4) + f1) +
            (size_t)NW * (64 + PB) * (sizeof(float4) + f1);
