@@ -54,8 +54,8 @@ constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do 
 // (publishing hprog[l] = chunks loaded), and writes a chunk's alpha rows (which the
 // sweeping wave leaves in the helper's own, otherwise unused, tile buffers) to the
 // table as one contiguous 4 KB block once wave l has finished the chunk (prog[l]).
-template <bool NWG = false, bool HELP = false>
-__global__ void __launch_bounds__(NW * 64)
+template <bool NWG = false, bool HELP = false, bool WIDE = false>
+__global__ void __launch_bounds__(WIDE ? 2 * NW * 64 : NW * 64)
 sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                   float* __restrict__ alpha_sk, float* __restrict__ brow,
                   float* __restrict__ partition, int* __restrict__ status,
@@ -86,7 +86,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     float* sink = rings + NW * R + wave * DUMMY;           // per-wave write sink
     int* st = status + b;
 
-    if (lane == 0) {
+    if (lane == 0 && wave < NW) {
         prog[wave] = -1;
         hprog[wave] = -1;
     }
@@ -113,16 +113,20 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     acc.init_open();
 
     if constexpr (HELP) {
-        if (NL > NW / 2) {   // never: the host picks HELP for parts of at most NW/2 stripes
+        // helpers: waves HB..HB+NL-1 (WIDE: a second set of NW waves)
+        constexpr int HB = WIDE ? NW : NW / 2;
+        if (NL > HB) {   // never: the host picks HELP for parts of at most HB stripes
             if (threadIdx.x == 0) atomicOr(st, 2);
             return;
         }
-        const int l = wave - NW / 2;
+        const int l = wave - HB;
         if (l >= 0 && l < NL) {
             const int i0 = (s_begin + l) * 64;
             float* out = alpha_sk + (((size_t)b * NSmax + s_begin + l) * NT + APAD) * 64;
             const uint32_t ltiles = lds_address(smem + l * WBUF);   // wave l's score tiles
-            const float* atiles = smem + wave * WBUF;                // its alpha tiles
+            // its alpha tiles: this wave's own buffers, or (WIDE: no LDS for those) its
+            // score tiles, once their scores are in wave l's registers
+            const float* atiles = smem + (WIDE ? l : wave) * WBUF;
             auto load = [&](int k) {
                 dma_quads<P, 1>(ltiles + (k & 1) * Tile::FLOATS * 4, sbase, i0, L1max, L2max,
                                 lane, k * P);
@@ -135,15 +139,15 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             }
             for (int k = 0; k < nch; ++k) {
                 if (k + 1 < nch) {
-                    // chunk k + 1's loads: the last issued at k = 0, else followed by
-                    // the P/4 alpha stores of chunk k - 1
-                    if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<Tile::NQ>();
+                    // chunk k + 1's loads: the last issued at k = 0 (WIDE: always),
+                    // else followed by the P/4 alpha stores of chunk k - 1
+                    if (WIDE || k == 0) wait_vmcnt<0>(); else wait_vmcnt<Tile::NQ>();
                     publish(hprog, l, k + 2);   // also completes this wave's LDS reads
                 }
                 // once wave l has finished chunk k, its score tile k & 1 takes chunk
                 // k + 2 and its alpha rows (alpha tile k & 1) go to the table
                 wait_for(prog, l, l * PROG_STRIDE + k + 1, st);
-                if (k + 2 < nch) load(k + 2);
+                if (!WIDE && k + 2 < nch) load(k + 2);
                 const float* at = atiles + (k & 1) * Tile::FLOATS;
                 float* dst = out + (size_t)k * P * 64;
 #pragma unroll
@@ -151,6 +155,9 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                     const float4 v = *reinterpret_cast<const float4*>(at + 256 * i + 4 * lane);
                     *reinterpret_cast<float4*>(dst + 256 * i + 4 * lane) = v;
                 }
+                // WIDE: the alpha tile lies over the score tile the load refills (the
+                // stores above have read it: their data dependence waits for the reads)
+                if (WIDE && k + 2 < nch) load(k + 2);
             }
         }
     }
@@ -257,8 +264,10 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             float* outc = out + (size_t)t0 * 64;
             // HELP: the chunk's alphas by step in the helper's tile k & 1 (written out
             // by the helper; it has written that tile's previous chunk before
-            // publishing this one as loaded)
-            float* atile = smem + (wave + NW / 2) * WBUF + (k & 1) * Tile::FLOATS + lane;
+            // publishing this one as loaded); WIDE: over this chunk's score tile, whose
+            // scores are in registers
+            float* atile = smem + (WIDE ? wave : wave + NW / 2) * WBUF + (k & 1) * Tile::FLOATS +
+                           lane;
             // FULL: every cell of the chunk lies inside the element, no validity masks
             auto steps = [&](auto full) {
                 constexpr bool FULL = decltype(full)::value;
@@ -344,7 +353,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     }
     // partition: merge lanes, waves, and (once per element) the cell (0,0) whose alpha is 0
     wave_merge_lse(acc, c);
-    if (lane == 0) { red_m[wave] = acc.m; red_z[wave] = acc.z; }
+    if (lane == 0 && wave < NW) { red_m[wave] = acc.m; red_z[wave] = acc.z; }
     __syncthreads();
     if (threadIdx.x == 0) {
         OnlineLSE tot;
@@ -373,8 +382,9 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
 // the sweeping wave's input buffer before it writes them out.
 // (one workgroup per CU: its LDS allows no second; waves_per_eu says so, so that the
 // register allocator does not spill to reach an occupancy the launch cannot have)
-template <int P, bool PRECISE = false, bool NWG = false, bool HELP = false>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
+template <int P, bool PRECISE = false, bool NWG = false, bool HELP = false, bool WIDE = false>
+__global__ void __launch_bounds__(WIDE ? 2 * NW * 64 : NW * 64)
+__attribute__((amdgpu_waves_per_eu(WIDE ? 4 : 1, WIDE ? 4 : 2)))
 sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                    const float* __restrict__ alpha_sk, const float* __restrict__ brow,
                    const float* __restrict__ partition,
@@ -427,7 +437,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     const int obase_lane = OutTile::read_base(lane);
     constexpr int NSTORE = QOUT ? Tile::NQ : P;   // stores of an inside chunk
 
-    if (lane == 0) {
+    if (lane == 0 && wave < NW) {
         prog[wave] = -1;
         hprog[wave] = -1;
     }
@@ -446,7 +456,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
 
     {   // each part zeroes its share of the rows' padding
         const int rows = (L1max + G - 1) / G;
-        zero_padding(pbase, L1, L2, L1max, L2max, NW * 64, part * rows,
+        zero_padding(pbase, L1, L2, L1max, L2max, (int)blockDim.x, part * rows,
                      min(L1max, part * rows + rows));
     }
 
@@ -459,42 +469,105 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     uint64_t* flag_out = bflag + (size_t)b * G + part;
 
     if constexpr (HELP) {
-        if (NL > NW / 2) {   // never: the host picks HELP for parts of at most NW/2 stripes
+        // helpers: waves HB..HB+NL-1 (WIDE: a second set of NW waves)
+        constexpr int HB = WIDE ? NW : NW / 2;
+        if (NL > HB) {   // never: the host picks HELP for parts of at most HB stripes
             if (threadIdx.x == 0) atomicOr(st, 2);
             return;
         }
-        const int q = wave - NW / 2;
+        const int q = wave - HB;
         if (q >= 0 && q < NL) {
             const int s = s_begin + NL - 1 - q;
             const int i0 = s * 64;
             const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * NT * 64;
             float* qbufs = smem + q * 2 * BUF;   // the sweeping wave's two chunk buffers
-            float* obufs = smem + wave * 2 * BUF;  // its output tiles (this wave's buffers)
+            // its output tiles: this wave's own buffers, or (WIDE: no LDS for those) its
+            // input buffers, over the score tile it has read into registers
+            float* obufs = smem + (WIDE ? q : wave) * 2 * BUF;
             auto load = [&](int k) {
                 const int th = nsteps - 1 - k * P;
                 const uint32_t buf = lds_address(qbufs + (k & 1) * BUF);
                 dma_quads<P, -1>(buf, sbase, i0, L1max, L2max, lane, th);
                 dma_rows<P, -1>(buf + ABUF * 4, astripe, th - 2, ul4);
             };
-            if (nch > 0) {
+            if constexpr (WIDE) {
+                // The output tile lies over the input buffer, which can take chunk k + 2
+                // only once chunk k's marginals have left: too late for a load issued
+                // then.  So chunks 0 and 1 go straight to LDS, and every later chunk is
+                // staged in this wave's registers two chunks ahead (set k & 1 holds
+                // chunk k + 2 while wave q sweeps chunk k) and written into its buffer
+                // once the marginals there have left.  Every vector-memory operation
+                // of the loop below is unconditional (stages past the last chunk
+                // reload it, unused), so that the compiler's own waits for the staged
+                // registers count exactly the operations issued since: a conditional
+                // one would make them wait for the marginal stores just issued as well.
+                struct Stage {
+                    StagedQuads<P> sq;
+                    f32x4 rows[P / 4];
+                };
+                Stage set0, set1;
+                auto stage = [&](Stage& g, int k) {
+                    const int th = nsteps - 1 - k * P;
+                    int ln = lane;
+                    __asm__ volatile("" : "+v"(ln));
+                    stage_quads<P, -1>(g.sq, sbase, i0, L1max, L2max, ln, th);
+                    stage_rows<P, -1>(g.rows, astripe, th - 2, ln);
+                };
+                // nch >= 4: nsteps = L2 + 63
                 load(0);
                 wait_vmcnt<0>();
                 publish(hprog, q, 1);
-                if (nch > 1) load(1);
-            }
-            for (int k = 0; k < nch; ++k) {
-                if (k + 1 < nch) {
-                    // chunk k + 1's loads: the last issued at k = 0, else followed by
-                    // the (at least P/4) marginal stores of chunk k - 1
-                    if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<Tile::NQ>();
-                    publish(hprog, q, k + 2);   // also completes this wave's LDS reads
+                load(1);
+                stage(set0, 2);
+                stage(set1, 3);
+                // chunk 1's loads: followed by the (at least 2 (P/4 + P/4)) staged loads
+                wait_vmcnt<2 * (Tile::NQ + P / 4)>();
+                publish(hprog, q, 2);
+                auto half = [&](Stage& g, int k) {
+                    float* buf = qbufs + (k & 1) * BUF;
+                    // an opaque copy of the lane index per chunk keeps the compiler from
+                    // hoisting the per-lane offsets of boundary chunks out of the loop
+                    // (registers that the two stages need)
+                    int ln = lane;
+                    __asm__ volatile("" : "+v"(ln));
+                    wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
+                    write_quads<P, -1>(buf, pbase, trash, i0, L1, L2, L1max, L2max, ln,
+                                       nsteps - 1 - k * P);
+                    if (k + 2 < nch) {
+                        // (LDS runs this wave's reads above before these writes)
+                        put_staged_quads<P>(buf, g.sq, lane);
+                        put_staged_rows<P>(buf + ABUF, g.rows, lane);
+                        publish(hprog, q, k + 3);
+                    }
+                    stage(g, min(k + 4, nch - 1));
+                };
+                int k = 0;
+                for (; k + 1 < nch; k += 2) {
+                    half(set0, k);
+                    half(set1, k + 1);
                 }
-                // once wave q has finished chunk k, its input buffer k & 1 takes chunk
-                // k + 2 and its marginals (in output tile k & 1) leave
-                wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
-                if (k + 2 < nch) load(k + 2);
-                write_quads<P, -1>(obufs + (k & 1) * BUF, pbase, trash, i0, L1, L2, L1max, L2max,
-                                   lane, nsteps - 1 - k * P);
+                if (k < nch) half(set0, k);
+            } else {
+                if (nch > 0) {
+                    load(0);
+                    wait_vmcnt<0>();
+                    publish(hprog, q, 1);
+                    if (nch > 1) load(1);
+                }
+                for (int k = 0; k < nch; ++k) {
+                    if (k + 1 < nch) {
+                        // chunk k + 1's loads: the last issued at k = 0, else followed
+                        // by the (at least P/4) marginal stores of chunk k - 1
+                        if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<Tile::NQ>();
+                        publish(hprog, q, k + 2);   // also completes this wave's LDS reads
+                    }
+                    // once wave q has finished chunk k, its input buffer k & 1 takes
+                    // chunk k + 2 and its marginals (in output tile k & 1) leave
+                    wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
+                    if (k + 2 < nch) load(k + 2);
+                    write_quads<P, -1>(obufs + (k & 1) * BUF, pbase, trash, i0, L1, L2, L1max,
+                                       L2max, lane, nsteps - 1 - k * P);
+                }
             }
         }
     }
@@ -584,7 +657,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             // the chunk's marginal quads: over its own score tile, or (HELP) in the
             // helper's buffer k & 1, whose previous tile the helper has written out
             // before publishing this chunk as loaded
-            float* obuf = HELP ? smem + (wave + NW / 2) * 2 * BUF + (k & 1) * BUF : buf;
+            float* obuf = HELP && !WIDE ? smem + (wave + NW / 2) * 2 * BUF + (k & 1) * BUF : buf;
             float sv[P];
             read_quads<P, -1>(buf, lane, sv);
             A[0] = A[P];
@@ -762,7 +835,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
 
     g_acc = wave_sum(g_acc);
     p_acc = wave_sum(p_acc);
-    if (lane == 0) { red_g[wave] = g_acc; red_p[wave] = p_acc; }
+    if (lane == 0 && wave < NW) { red_g[wave] = g_acc; red_p[wave] = p_acc; }
     __syncthreads();
     if (threadIdx.x == 0) {
         Acc g = 0, p = 0;
@@ -784,7 +857,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         __builtin_amdgcn_readfirstlane(load_status(st)) != 0) {
         __syncthreads();
         const float nan = __builtin_nanf("");
-        for (size_t i = threadIdx.x; i < (size_t)L1max * L2max; i += NW * 64) pbase[i] = nan;
+        for (size_t i = threadIdx.x; i < (size_t)L1max * L2max; i += blockDim.x) pbase[i] = nan;
         if (threadIdx.x == 0) {
             poison_value[b] = nan;
             grad_gap[b] = nan;
@@ -869,15 +942,16 @@ static bool helpers_enabled() {
     return !(e && e[0] == '0');
 }
 
-template <bool NWG, bool HELP>
+template <bool NWG, bool HELP, bool WIDE = false>
 int launch_forward_k(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                      float gap, float T, const Layout& ws, float* partition, hipStream_t st,
                      const Split& sp, int R, size_t lds, uint32_t epoch) {
     const int ns = (max_L1 + 63) / 64;
-    D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel<NWG, HELP>,
+    D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel<NWG, HELP, WIDE>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH(NWG ? "nw_forward" : "sw_forward", (sw_forward_kernel<NWG, HELP>),
-               dim3(wf::split_grid(B, sp.G)), dim3(wf::NW * 64), lds, st, scores, lengths,
+    D2P_LAUNCH(NWG ? "nw_forward" : "sw_forward", (sw_forward_kernel<NWG, HELP, WIDE>),
+               dim3(wf::split_grid(B, sp.G)), dim3((WIDE ? 2 : 1) * wf::NW * 64), lds, st, scores,
+               lengths,
                ws.alpha_sk, ws.brow, partition, ws.status, ws.fflag, ws.fpart, B, max_L1, max_L2,
                ns, gap, T, R, sp.G, sp.SPW, epoch);
     D2P_HIP(hipGetLastError());
@@ -894,14 +968,20 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     const uint32_t epoch = next_epoch();
     if (sp.G > 1 && wf::launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
-    // helper waves move the data when a part has at most NW/2 stripes (the others idle)
-    const bool help = ((sp.G > 1 ? sp.SPW : ns) <= wf::NW / 2) && helpers_enabled();
-#define D2P_SW_FWD(G_, H_) \
-    launch_forward_k<G_, H_>(scores, lengths, B, max_L1, max_L2, gap, T, ws, partition, st, sp, R, \
-                             lds, epoch)
-    if (global) return help ? D2P_SW_FWD(true, true) : D2P_SW_FWD(true, false);
+    // helper waves move the data: the idle waves when a part has at most NW/2
+    // stripes, a second set of NW waves when it has at most NW
+    const int part_stripes = sp.G > 1 ? sp.SPW : ns;
+    const bool help = part_stripes <= wf::NW / 2 && helpers_enabled();
+    const bool wide = !help && part_stripes <= wf::NW && helpers_enabled();
+#define D2P_SW_FWD(G_, H_, W_) \
+    launch_forward_k<G_, H_, W_>(scores, lengths, B, max_L1, max_L2, gap, T, ws, partition, st, \
+                                 sp, R, lds, epoch)
+    if (global)
+        return help ? D2P_SW_FWD(true, true, false)
+                    : wide ? D2P_SW_FWD(true, true, true) : D2P_SW_FWD(true, false, false);
     // (the owner part writes the NW value: no merge)
-    D2P_TRY(help ? D2P_SW_FWD(false, true) : D2P_SW_FWD(false, false));
+    D2P_TRY(help ? D2P_SW_FWD(false, true, false)
+                 : wide ? D2P_SW_FWD(false, true, true) : D2P_SW_FWD(false, false, false));
 #undef D2P_SW_FWD
     if (sp.G > 1 && wf::launch_partition_merge(ws, partition, B, sp.G, T, st) != D2P_OK)
         return D2P_ERR_HIP;
@@ -909,7 +989,7 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
     return D2P_OK;
 }
 
-template <int P, bool PRECISE, bool NWG, bool HELP = false>
+template <int P, bool PRECISE, bool NWG, bool HELP = false, bool WIDE = false>
 int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                       float gap, float T, const Layout& ws, const float* partition,
                       float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
@@ -919,11 +999,11 @@ int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     const uint32_t epoch = next_epoch();
     if (sp.G > 1) D2P_TRY(wf::launch_flag_reset(ws.bflag, B * sp.G, st));
-    D2P_HIP(hipFuncSetAttribute((const void*)sw_backward_kernel<P, PRECISE, NWG, HELP>,
+    D2P_HIP(hipFuncSetAttribute((const void*)sw_backward_kernel<P, PRECISE, NWG, HELP, WIDE>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH(NWG ? "nw_backward" : "sw_backward", (sw_backward_kernel<P, PRECISE, NWG, HELP>),
-               dim3(wf::split_grid(B, sp.G)),
-               dim3(wf::NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
+    D2P_LAUNCH(NWG ? "nw_backward" : "sw_backward",
+               (sw_backward_kernel<P, PRECISE, NWG, HELP, WIDE>), dim3(wf::split_grid(B, sp.G)),
+               dim3((WIDE ? 2 : 1) * wf::NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
                marginals, grad_gap, grad_T, ws.status, ws.trash, ws.bflag, ws.flows, ws.bpart,
                sp.G == 1 ? poison_value : nullptr, B, max_L1, max_L2, ns, gap, T, R, sp.G, sp.SPW,
                epoch);
@@ -950,12 +1030,19 @@ int launch_backward(const float* scores, const int* lengths, int B, int max_L1, 
         if (P == 16) return precise ? D2P_SW_BWD(16, true, true) : D2P_SW_BWD(16, false, true);
         return precise ? D2P_SW_BWD(8, true, true) : D2P_SW_BWD(8, false, true);
     }
-    // helper waves move the data when a part has at most NW/2 stripes (the others idle)
-    const bool help = !precise && P == 16 && (rows + 63) / 64 <= wf::NW / 2 && helpers_enabled();
+    // helper waves move the data: the idle waves when a part has at most NW/2
+    // stripes, a second set of NW waves when it has at most NW
+    const int part_stripes = (rows + 63) / 64;
+    const bool help = !precise && P == 16 && part_stripes <= wf::NW / 2 && helpers_enabled();
+    const bool wide = !precise && P == 16 && !help && part_stripes <= wf::NW && helpers_enabled();
     if (help)
         return launch_backward_p<16, false, false, true>(scores, lengths, B, max_L1, max_L2, gap,
                                                          T, ws, partition, marginals, grad_gap,
                                                          grad_T, st, sp, R, poison_value);
+    if (wide)
+        return launch_backward_p<16, false, false, true, true>(
+            scores, lengths, B, max_L1, max_L2, gap, T, ws, partition, marginals, grad_gap,
+            grad_T, st, sp, R, poison_value);
     if (P == 16) return precise ? D2P_SW_BWD(16, true, false) : D2P_SW_BWD(16, false, false);
     return precise ? D2P_SW_BWD(8, true, false) : D2P_SW_BWD(8, false, false);
 #undef D2P_SW_BWD

@@ -243,8 +243,12 @@ __device__ __forceinline__ void store_sys4(float4* p, float4 v) {
 // Polls a pipeline wait makes before it gives up (this translation unit's copy, per
 // device).  d2p_set_spin_limit lowers it from the host so that tests can drive every
 // wait down its give-up path; kernels read it only once a wait is not satisfied at
-// once, so the hot path never loads it.
-static __device__ int g_spin_limit = SPIN_LIMIT;
+// once, so the hot path never loads it.  It lives in constant memory: a kernel reads
+// it with a scalar load, whose wait leaves the wave's vector-memory operations in
+// flight (a vector load would be followed by a wait for all of them, draining the
+// loads issued ahead and the stores just issued at every wait that is not satisfied
+// at once).
+static __constant__ int g_spin_limit = SPIN_LIMIT;
 
 // Host side: every translation unit that includes this header registers a setter for
 // its own copy of g_spin_limit (d2p_set_spin_limit calls them all).
@@ -704,10 +708,82 @@ __device__ __forceinline__ void write_quads(const float* tile, float* obase, flo
             quad_cell<P, DIR>(64 * j + lane, t_first, r, col);
             const int row = i0 + r;
             const bool in = row < L1 && col >= 0 && col < L2;
-            float* dst = in ? obase + (size_t)row * L2max + col : trash + lane;
+            // (the offset stays below L1max * L2max < 2^31)
+            float* dst = in ? obase + (uint32_t)(row * L2max + col) : trash + lane;
             *dst = tile[64 * j + lane];
         }
     }
+}
+
+// Register staging of a chunk's quad tile, for helper waves that load further ahead
+// than their LDS buffers allow: stage_quads issues the loads dma_quads would issue,
+// into the lane's registers (P/4 16-byte loads inside, P dword loads at a boundary),
+// and put_staged_quads writes them where dma_quads would have put them.  The compiler
+// tracks these loads itself and waits for them before the LDS writes.
+template <int P>
+struct StagedQuads {
+    float v[P];
+    bool inside;
+};
+template <int P, int DIR>
+__device__ __forceinline__ void stage_quads(StagedQuads<P>& sq, const float* mbase, int i0,
+                                            int L1max, int L2max, int lane, int t_first) {
+    using Q = QuadTile<P>;
+    const float* sbase = stripe_row(mbase, i0, L2max);
+    sq.inside = chunk_inside<P, DIR>(i0, L1max, L2max, t_first);
+    if (sq.inside) {
+        const char* cbase = reinterpret_cast<const char*>(sbase);
+        uint32_t off = quad_offset0<P, DIR>(L2max, lane, t_first);
+        const uint32_t step = (uint32_t)(Q::ROWS_X4 * (L2max - 1)) * 4u;
+#pragma unroll
+        for (int i = 0; i < Q::NQ; ++i) {
+            const float4 x = *reinterpret_cast<const float4*>(cbase + off);
+            sq.v[4 * i] = x.x;
+            sq.v[4 * i + 1] = x.y;
+            sq.v[4 * i + 2] = x.z;
+            sq.v[4 * i + 3] = x.w;
+            off += step;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            int r, col;
+            quad_cell<P, DIR>(64 * j + lane, t_first, r, col);
+            // (the offset stays below L1max * L2max < 2^31)
+            sq.v[j] = sbase[(uint32_t)((min(i0 + r, L1max - 1) - i0) * L2max +
+                                       min(max(col, 0), L2max - 1))];
+        }
+    }
+}
+template <int P>
+__device__ __forceinline__ void put_staged_quads(float* tile, const StagedQuads<P>& sq, int lane) {
+    if (sq.inside) {
+#pragma unroll
+        for (int i = 0; i < P / 4; ++i)
+            *reinterpret_cast<float4*>(tile + 256 * i + 4 * lane) =
+                make_float4(sq.v[4 * i], sq.v[4 * i + 1], sq.v[4 * i + 2], sq.v[4 * i + 3]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < P; ++j) tile[64 * j + lane] = sq.v[j];
+    }
+}
+
+// Register staging of dma_rows: the same P/4 non-temporal 16-byte loads per lane, and
+// the LDS writes that put them where dma_rows would.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+template <int P, int DIR>
+__device__ __forceinline__ void stage_rows(f32x4 (&a)[P / 4], const float* plane_base, int t_first,
+                                           int lane) {
+    static_assert(P % 4 == 0, "rows come in fours");
+    const int t_lo = DIR > 0 ? t_first : t_first - (P - 1);
+    const f32x4* src = reinterpret_cast<const f32x4*>(plane_base + (size_t)(t_lo + APAD) * 64) + lane;
+#pragma unroll
+    for (int j = 0; j < P / 4; ++j) a[j] = __builtin_nontemporal_load(src + 64 * j);
+}
+template <int P>
+__device__ __forceinline__ void put_staged_rows(float* rows, const f32x4 (&a)[P / 4], int lane) {
+#pragma unroll
+    for (int j = 0; j < P / 4; ++j) reinterpret_cast<f32x4*>(rows)[64 * j + lane] = a[j];
 }
 
 // Issues the loads of P consecutive steps of one plane of a skewed table (plane_base =

@@ -75,13 +75,16 @@ def test_sw_split_ragged(cuda, parts):
 
 
 @pytest.mark.parametrize("B,L1,L2,n", [(2, 700, 260, 4), (3, 200, 300, 1), (1, 1500, 90, 8),
-                                       (4, 64, 64, 1)])
+                                       (4, 64, 64, 1), (3, 512, 300, 1), (2, 330, 200, 1),
+                                       (2, 1500, 90, 3)])
 def test_sw_helper_waves_bit_identical(cuda, parts, monkeypatch, B, L1, L2, n):
-    """Parts of at most four stripes hand their data movement (tile loads, the alpha
-    table and marginal write-outs) to helper waves in the forward and reverse sweeps;
-    the arithmetic is unchanged, so every output equals the single-wave form bit for
-    bit: SW and NW first order and the SW HVP (whose primal forward is the same sweep),
-    ragged lengths and split parts included."""
+    """Parts hand their data movement (tile loads, the alpha table and marginal
+    write-outs) to helper waves in the forward and reverse sweeps: the idle waves of the
+    workgroup for parts of at most four stripes, a second set of eight waves for parts
+    of five to eight (the last three cases).  The arithmetic is unchanged, so every
+    output equals the single-wave form bit for bit: SW and NW first order and the SW
+    HVP (whose primal forward is the same sweep), ragged lengths and split parts
+    included."""
     s = _seeded(41, (B, L1, L2)).to(cuda)
     lens = torch.tensor([[max(1, L1 - 37 * i), max(1, L2 - 11 * i)] for i in range(B)],
                         dtype=torch.int32, device=cuda)
