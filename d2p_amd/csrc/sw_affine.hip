@@ -610,9 +610,21 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
             // the output quad being filled, memory-column order (step 4q + 3 - e in
             // element e)
             float4 quad = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            // FULL: every cell of the chunk lies inside the element, no validity masks
-            auto steps = [&](auto full) {
+            // (local) the betas' start terms 2^min((alpha - S) c, 0) are exactly 0 below
+            // 2^-150: a chunk none of whose alphas comes within 150 c^-1 of S skips
+            // those exponentials (most chunks: alpha grows towards S)
+            bool inits = NWA;
+            if (!NWA) {
+                float amax = fmaxf(fmaxf(AM[0], AI[0]), AD[0]);
+#pragma unroll
+                for (int u = 1; u < P; ++u) amax = fmaxf(amax, fmaxf(fmaxf(AM[u], AI[u]), AD[u]));
+                inits = __builtin_amdgcn_ballot_w64((amax - S) * c >= -151.0f) != 0;
+            }
+            // FULL: every cell of the chunk lies inside the element, no validity masks;
+            // INIT: some cell of the chunk has a nonzero start term
+            auto steps = [&](auto full, auto init) {
             constexpr bool FULL = decltype(full)::value;
+            constexpr bool INIT = decltype(init)::value;
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t_hi - u;
@@ -663,7 +675,7 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                         initI = eI * r;
                         initD = eD * r;
                     }
-                } else {
+                } else if (INIT) {
                     float lp;
                     lp = (AM[u] - S) * c;   // subtract first: exact for nearby values
                     initM = fast_exp2(lp < 0.0f ? lp : 0.0f);
@@ -671,6 +683,8 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                     initI = fast_exp2(lp < 0.0f ? lp : 0.0f);
                     lp = (AD[u] - S) * c;
                     initD = fast_exp2(lp < 0.0f ? lp : 0.0f);
+                } else {
+                    initM = initI = initD = 0.0f;
                 }
                 const float betaM = ((initM + dM) + lM) + uM;
                 const float betaI = NWA ? ((initI + dI) + uI) + lI : (initI + dI) + uI;
@@ -745,10 +759,13 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 qDD = wave_shr1(qDD);
             }
             };
-            if (i0 + 63 < L1 && t_hi - P - 62 >= (NWA ? 1 : 0) && t_hi < L2)
-                steps(std::true_type{});
-            else
-                steps(std::false_type{});
+            if (i0 + 63 < L1 && t_hi - P - 62 >= (NWA ? 1 : 0) && t_hi < L2) {
+                if (inits) steps(std::true_type{}, std::true_type{});
+                else steps(std::true_type{}, std::false_type{});
+            } else {
+                if (inits) steps(std::false_type{}, std::true_type{});
+                else steps(std::false_type{}, std::false_type{});
+            }
             wave_lds_sync();
             if constexpr (QT)
                 write_quads<P, -1>(otile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);

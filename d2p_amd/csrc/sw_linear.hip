@@ -715,9 +715,21 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             float4 quad = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             float pre_d2 = wave_shr1(pre_d);   // lane 63 = step 1 (then shifted on)
             pre_d2 = wave_shr1(pre_d2);        // lane 63 = step 2
-            // FULL: every cell of the chunk lies inside the element, no validity masks
-            auto steps = [&](auto full) {
+            // (SW) beta_init = 2^min((alpha - S) c, 0) is exactly 0 below 2^-150: a chunk
+            // none of whose alphas comes within 150 c^-1 of S skips those exponentials
+            // (most chunks: alpha grows along the anti-diagonals towards S)
+            bool inits = NWG;
+            if (!NWG) {
+                float amax = A[0];
+#pragma unroll
+                for (int u = 1; u < P; ++u) amax = fmaxf(amax, A[u]);
+                inits = __builtin_amdgcn_ballot_w64((amax - S) * c >= -151.0f) != 0;
+            }
+            // FULL: every cell of the chunk lies inside the element, no validity masks;
+            // INIT: some cell of the chunk has a nonzero beta_init
+            auto steps = [&](auto full, auto init) {
             constexpr bool FULL = decltype(full)::value;
+            constexpr bool INIT = decltype(init)::value;
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t_hi - u;
@@ -749,10 +761,12 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 float binit;
                 if (NWG) {
                     binit = t == term_step ? 1.0f : 0.0f;
-                } else {
+                } else if (INIT) {
                     float lp = (a0 - S) * c;   // subtract first: exact for nearby values
                     lp = lp < 0.0f ? lp : 0.0f;
                     binit = fast_exp2(lp);
+                } else {
+                    binit = 0.0f;
                 }
                 // reference accumulation order: init, diagonal, left, up successor
                 const float beta = ((binit + in_diag) + in_left) + in_up;
@@ -794,8 +808,13 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 pre_d2 = wave_shr1(pre_d2);
             }
             };
-            if (i0 + 63 < L1 && t_hi - P - 62 >= 0 && t_hi < L2) steps(std::true_type{});
-            else steps(std::false_type{});
+            if (i0 + 63 < L1 && t_hi - P - 62 >= 0 && t_hi < L2) {
+                if (inits) steps(std::true_type{}, std::true_type{});
+                else steps(std::true_type{}, std::false_type{});
+            } else {
+                if (inits) steps(std::false_type{}, std::true_type{});
+                else steps(std::false_type{}, std::false_type{});
+            }
 
             // the chunk's parameter-gradient terms: balanced sums, then one add each
             if (TERMS) {

@@ -201,6 +201,18 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             }
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             float* toutc = tout + (size_t)t0 * 64;
+            // (HVP, SW) beta_init = 2^min((alpha - S) c, 0) is exactly 0 below 2^-150: a
+            // chunk none of whose alphas comes within 150 c^-1 of S skips its share of the
+            // value's tangent (most chunks: alpha grows along the anti-diagonals towards S)
+            bool inits = true;
+            if constexpr (MODE == HVP && !NWG) {
+                float amax = Aw[2];
+#pragma unroll
+                for (int u = 1; u < P; ++u) amax = fmaxf(amax, Aw[u + 2]);
+                inits = __builtin_amdgcn_ballot_w64((amax - S) * c >= -151.0f) != 0;
+            }
+            auto steps = [&](auto init) {
+            constexpr bool INIT = decltype(init)::value;
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t0 + u;
@@ -255,13 +267,16 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                     if (NWG) {
                         // the value's tangent is the terminal cell's
                         if (t == term_step) sacc += cur;
-                    } else {
+                    } else if (INIT) {
                         float lp = (a0 - S) * c;
                         lp = lp < 0.0f ? lp : 0.0f;
                         sacc += fast_exp2(lp) * cur;
                     }
                 }
             }
+            };
+            if (inits) steps(std::true_type{});
+            else steps(std::false_type{});
             // the stripe's last row of tangents by step: one store instruction
             wave_lds_sync();
             if (lane < P) {
@@ -540,6 +555,18 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             // QT: the output quad being filled, memory-column order (step 4q + 3 - e in
             // element e); one 16-byte LDS write per four steps
             float4 quad = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            // (SW) beta_init = 2^min((alpha - S) c, 0) is exactly 0 below 2^-150: a chunk
+            // none of whose alphas comes within 150 c^-1 of S skips those exponentials
+            // (most chunks: alpha grows along the anti-diagonals towards S)
+            bool inits = true;
+            if constexpr (!NWG) {
+                float amax = A[0];
+#pragma unroll
+                for (int u = 1; u < P; ++u) amax = fmaxf(amax, A[u]);
+                inits = __builtin_amdgcn_ballot_w64((amax - S) * c >= -151.0f) != 0;
+            }
+            auto steps = [&](auto init) {
+            constexpr bool INIT = decltype(init)::value;
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t_hi - u;
@@ -604,10 +631,12 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 float binit;
                 if (NWG) {
                     binit = t == term_step ? 1.0f : 0.0f;
-                } else {
+                } else if (INIT) {
                     float lp = (a0 - S) * c;
                     lp = lp < 0.0f ? lp : 0.0f;
                     binit = fast_exp2(lp);
+                } else {
+                    binit = 0.0f;
                 }
                 const float beta = ((binit + db) + lb) + ubt;
                 float g;
@@ -660,6 +689,9 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 qdb = wave_shr1(qdb);
                 qdg = wave_shr1(qdg);
             }
+            };
+            if (inits) steps(std::true_type{});
+            else steps(std::false_type{});
             wave_lds_sync();
             if constexpr (!DOT) {
                 if constexpr (QT)
