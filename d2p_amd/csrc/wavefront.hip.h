@@ -602,7 +602,7 @@ struct QuadTile {
     static constexpr int FLOATS = 64 * P;
     static constexpr int NQ = P / 4;                // quads per row
     static constexpr int ROWS_X4 = 64 / NQ;         // rows per 16-byte instruction
-    __device__ static int swz(int r) { return (r / (16 / NQ)) & (NQ - 1); }
+    __device__ static int swz(int r) { return (int)(((unsigned)r / (16 / NQ)) & (NQ - 1)); }
     __device__ static int slot(int r, int q) { return P * r + 4 * (q ^ swz(r)); }
     // step of element e of the quad q
     template <int DIR>
@@ -613,8 +613,8 @@ struct QuadTile {
 template <int P, int DIR>
 __device__ __forceinline__ void quad_cell(int f, int t_first, int& r, int& col) {
     using Q = QuadTile<P>;
-    r = f / P;
-    const int s = f % P;
+    r = (int)((unsigned)f / P);   // f >= 0: unsigned division is a shift
+    const int s = (int)((unsigned)f % P);
     const int q = (s >> 2) ^ Q::swz(r);
     col = t_first + DIR * Q::template step<DIR>(q, s & 3) - r;
 }
@@ -719,10 +719,13 @@ __device__ __forceinline__ void write_quads(const float* tile, float* obase, flo
 // than their LDS buffers allow: stage_quads issues the loads dma_quads would issue,
 // into the lane's registers (P/4 16-byte loads inside, P dword loads at a boundary),
 // and put_staged_quads writes them where dma_quads would have put them.  The compiler
-// tracks these loads itself and waits for them before the LDS writes.
+// tracks these loads itself and waits for them before the LDS writes.  The quads are
+// held as vectors: as scalars, the compiler would split each 16-byte load into four
+// and merge them with the boundary form's loads.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 template <int P>
 struct StagedQuads {
-    float v[P];
+    f32x4 q[P / 4];
     bool inside;
 };
 template <int P, int DIR>
@@ -737,11 +740,8 @@ __device__ __forceinline__ void stage_quads(StagedQuads<P>& sq, const float* mba
         const uint32_t step = (uint32_t)(Q::ROWS_X4 * (L2max - 1)) * 4u;
 #pragma unroll
         for (int i = 0; i < Q::NQ; ++i) {
-            const float4 x = *reinterpret_cast<const float4*>(cbase + off);
-            sq.v[4 * i] = x.x;
-            sq.v[4 * i + 1] = x.y;
-            sq.v[4 * i + 2] = x.z;
-            sq.v[4 * i + 3] = x.w;
+            // (a 4-byte aligned address: 16-byte loads need no more on this part)
+            sq.q[i] = *reinterpret_cast<const f32x4*>(cbase + off);
             off += step;
         }
     } else {
@@ -750,8 +750,8 @@ __device__ __forceinline__ void stage_quads(StagedQuads<P>& sq, const float* mba
             int r, col;
             quad_cell<P, DIR>(64 * j + lane, t_first, r, col);
             // (the offset stays below L1max * L2max < 2^31)
-            sq.v[j] = sbase[(uint32_t)((min(i0 + r, L1max - 1) - i0) * L2max +
-                                       min(max(col, 0), L2max - 1))];
+            sq.q[j / 4][j % 4] = sbase[(uint32_t)((min(i0 + r, L1max - 1) - i0) * L2max +
+                                                  min(max(col, 0), L2max - 1))];
         }
     }
 }
@@ -759,18 +759,15 @@ template <int P>
 __device__ __forceinline__ void put_staged_quads(float* tile, const StagedQuads<P>& sq, int lane) {
     if (sq.inside) {
 #pragma unroll
-        for (int i = 0; i < P / 4; ++i)
-            *reinterpret_cast<float4*>(tile + 256 * i + 4 * lane) =
-                make_float4(sq.v[4 * i], sq.v[4 * i + 1], sq.v[4 * i + 2], sq.v[4 * i + 3]);
+        for (int i = 0; i < P / 4; ++i) reinterpret_cast<f32x4*>(tile)[64 * i + lane] = sq.q[i];
     } else {
 #pragma unroll
-        for (int j = 0; j < P; ++j) tile[64 * j + lane] = sq.v[j];
+        for (int j = 0; j < P; ++j) tile[64 * j + lane] = sq.q[j / 4][j % 4];
     }
 }
 
 // Register staging of dma_rows: the same P/4 non-temporal 16-byte loads per lane, and
 // the LDS writes that put them where dma_rows would.
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 template <int P, int DIR>
 __device__ __forceinline__ void stage_rows(f32x4 (&a)[P / 4], const float* plane_base, int t_first,
                                            int lane) {
