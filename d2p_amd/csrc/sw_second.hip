@@ -28,6 +28,7 @@
 // Inputs arrive by direct-to-LDS loads one chunk ahead into one buffer per wave,
 // copied to registers at the start of each chunk before the next chunk's loads.
 
+#include <cstdlib>
 #include <type_traits>
 #include <vector>
 
@@ -315,7 +316,13 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
 
 // DOT: instead of writing the per-cell output, accumulate its dot product with the
 // matrix passed as V (the marginal cotangent) into dot[b].
-template <int MODE, int P, bool DOT, bool NWG = false>
+// HELP (quad tiles, per-cell output, parts of at most NW/2 stripes): wave NW/2 + q
+// moves stripe order q's data.  Chunk k's buffer is wave q's own for even k and the
+// helper's for odd k.  The helper loads a chunk's scores, direction, alpha and
+// tangent rows into its buffer (publishing hprog[q] = chunks loaded), writes the
+// chunk's output tile out once wave q has finished the chunk (prog[q]), and then
+// loads chunk k + 2 into that buffer.  Wave q loads only its rows above and flows.
+template <int MODE, int P, bool DOT, bool NWG = false, bool HELP = false>
 __global__ void __launch_bounds__(NW * 64)
 sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                const int* __restrict__ lengths, const float* __restrict__ alpha_sk,
@@ -330,6 +337,7 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     // QT (8- and 16-step chunks): score, direction and output tiles move as 16-byte
     // quads (P/4 instructions each); 4-step chunks keep dword tiles
     constexpr bool QT = P == 8 || P == 16;
+    static_assert(!HELP || (QT && !DOT), "helper waves move quad tiles and write the output");
     using Tile = typename std::conditional<QT, QuadTile<(QT ? P : 8)>, ChunkTile<P>>::type;
     constexpr int NQ = P / 4;
     constexpr int NSTORE = DOT ? 0 : (QT ? NQ : P);         // output stores, inside chunk
@@ -345,6 +353,7 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     constexpr int SINK = 64 + P;
     extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
+    __shared__ int hprog[NW];     // HELP: chunks of stripe order q loaded by its helper
     __shared__ float red[NW];
     // parts as in the primal backward: bottom-up, part p < G - 1 takes its last
     // stripe's flows from below from part p + 1 through flows4
@@ -355,8 +364,7 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     const int lane = threadIdx.x & 63;
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    float* buf = smem + wave * BUF;
-    float* otile = buf + OT;
+    float* wbuf = smem + wave * BUF;   // this wave's chunk buffer
     __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
                                   // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
@@ -365,7 +373,10 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     int* st = status + b;
     const int tbase = ChunkTile<P>::read_base(lane);   // dword tiles (4-step chunks)
 
-    if (lane == 0) prog[wave] = -1;
+    if (lane == 0) {
+        prog[wave] = -1;
+        hprog[wave] = -1;
+    }
     __syncthreads();
 
     const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
@@ -381,7 +392,6 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     const float* sbase = scores + (size_t)b * L1max * L2max;
     const float* vbase = HAS_V ? V + (size_t)b * L1max * L2max : nullptr;
     float* obase = DOT ? nullptr : out + (size_t)b * L1max * L2max;
-    const uint32_t in_lds = lds_address(buf);
 
     if (!DOT) {   // each part zeroes its share of the rows' padding
         const int rows = (L1max + G - 1) / G;
@@ -396,6 +406,51 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     const bool has_next = s_begin + NL < NS;
     const uint64_t* flag_in = dflag + (size_t)b * G + (part + 1 < G ? part + 1 : part);
     uint64_t* flag_out = dflag + (size_t)b * G + part;
+
+    if constexpr (HELP) {
+        if (NL > NW / 2) {   // never: the host picks HELP for parts of at most NW/2 stripes
+            if (threadIdx.x == 0) atomicOr(st, 2);
+            return;
+        }
+        const int q = wave - NW / 2;
+        if (q >= 0 && q < NL) {
+            const int s = s_begin + NL - 1 - q;
+            const int i0 = s * 64;
+            const size_t sb = ((size_t)b * NSmax + s) * NT;
+            const float* astripe = alpha_sk + sb * 64;
+            const float* xstripe = tan_sk + sb * 64;
+            // chunk k's buffer: wave q's own (even k) or this wave's (odd k)
+            auto cbuf = [&](int k) { return smem + (k & 1 ? wave : q) * BUF; };
+            auto load = [&](int k) {
+                const int th = nsteps - 1 - k * P;
+                const uint32_t in = lds_address(cbuf(k));
+                dma_quads<P, -1>(in, sbase, i0, L1max, L2max, lane, th);
+                if (HAS_V) dma_quads<P, -1>(in + VT * 4, vbase, i0, L1max, L2max, lane, th);
+                dma_rows<P, -1>(in + AR * 4, astripe, th - 2, ul4);
+                dma_rows<P, -1>(in + XR * 4, xstripe, th - 2, ul4);
+            };
+            if (nch > 0) {
+                load(0);
+                wait_vmcnt<0>();
+                publish(hprog, q, 1);
+                if (nch > 1) load(1);
+            }
+            for (int k = 0; k < nch; ++k) {
+                if (k + 1 < nch) {
+                    // chunk k + 1's loads are the last issued
+                    wait_vmcnt<0>();
+                    publish(hprog, q, k + 2);   // also completes this wave's LDS reads
+                }
+                // once wave q has finished chunk k, its output tile leaves and the
+                // buffer takes chunk k + 2 (the stores have read the tile: their data
+                // dependence waits for the reads)
+                wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
+                write_quads<P, -1>(cbuf(k) + OT, obase, trash, i0, L1, L2, L1max, L2max, lane,
+                                   nsteps - 1 - k * P);
+                if (k + 2 < nch) load(k + 2);
+            }
+        }
+    }
 
     for (int q = wave; q < NL; q += NW) {
         const int s = s_begin + NL - 1 - q;
@@ -420,29 +475,36 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             flows4 + ((size_t)b * NSmax + (x_in ? s + 1 : s)) * NT);
         int seen = -1;       // chunks of the part below known to be complete
 
+        // chunk k's buffer: this wave's own, or (HELP, odd k) its helper's
+        auto kbuf = [&](int k) { return HELP && (k & 1) ? smem + (wave + NW / 2) * BUF : wbuf; };
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
-            if constexpr (QT) {
-                dma_quads<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
-                if (HAS_V) dma_quads<P, -1>(in_lds + VT * 4, vbase, i0, L1max, L2max, lane, th);
+            const uint32_t in = lds_address(kbuf(k));
+            if constexpr (HELP) {
+                // (the helper loads the tiles and rows)
+            } else if constexpr (QT) {
+                dma_quads<P, -1>(in, sbase, i0, L1max, L2max, lane, th);
+                if (HAS_V) dma_quads<P, -1>(in + VT * 4, vbase, i0, L1max, L2max, lane, th);
             } else {
-                dma_tile<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
-                if (HAS_V) dma_tile<P, -1>(in_lds + VT * 4, vbase, i0, L1max, L2max, lane, th);
+                dma_tile<P, -1>(in, sbase, i0, L1max, L2max, lane, th);
+                if (HAS_V) dma_tile<P, -1>(in + VT * 4, vbase, i0, L1max, L2max, lane, th);
             }
-            dma_rows<P, -1>(in_lds + AR * 4, astripe, th - 2, ul4);
-            dma_rows<P, -1>(in_lds + XR * 4, xstripe, th - 2, ul4);
+            if constexpr (!HELP) {
+                dma_rows<P, -1>(in + AR * 4, astripe, th - 2, ul4);
+                dma_rows<P, -1>(in + XR * 4, xstripe, th - 2, ul4);
+            }
             const uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
-            uint32_t o = roff, l = in_lds + RA * 4;
+            uint32_t o = roff, l = in + RA * 4;
             lds_dma_dword<0>(bup, o, l, 0u);
             o = roff;
-            l = in_lds + RX * 4;
+            l = in + RX * 4;
             lds_dma_dword<0>(xup, o, l, 0u);
             if (x_in) {
                 // flows of producer slots kP+62 .. kP+62+P (float4 each): float f of the
                 // range in lane f, clamped to the last slot
                 uint32_t foff = (uint32_t)min((k * P + 62) * 4 + min(lane, 4 * P + 1),
                                               (nsteps - 1) * 4 + 3) * 4u;
-                uint32_t fdst = in_lds + FB * 4;
+                uint32_t fdst = in + FB * 4;
                 lds_dma_dword_sys<0>(flows_in, foff, fdst, 0u);
             }
         };
@@ -468,8 +530,17 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             chunk_waits<P>(prog, q, NL, k, nch, R, st);
             // this chunk's loads, followed by at least the NSTORE output stores of the
             // previous chunk (none when accumulating a dot product; the first chunk's
-            // loads are the last issued)
-            if (k == 0 || DOT) wait_vmcnt<0>(); else wait_vmcnt<NSTORE>();
+            // loads are the last issued).  HELP: the helper loads the tiles and rows;
+            // this wave's own loads (rows above, flows) are followed by nothing, or by
+            // the previous chunk's flow store (x_out)
+            if constexpr (HELP) {
+                if (x_out && k > 0) wait_vmcnt<1>(); else wait_vmcnt<0>();
+                wait_for(hprog, q, k + 1, st);
+            } else {
+                if (k == 0 || DOT) wait_vmcnt<0>(); else wait_vmcnt<NSTORE>();
+            }
+            float* buf = kbuf(k);
+            float* otile = buf + OT;
             if (x_in && k > 0) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
@@ -693,7 +764,9 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             if (inits) steps(std::true_type{});
             else steps(std::false_type{});
             wave_lds_sync();
-            if constexpr (!DOT) {
+            if constexpr (HELP) {
+                // (the helper writes the tile out once this chunk is published)
+            } else if constexpr (!DOT) {
                 if constexpr (QT)
                     write_quads<P, -1>(otile, obase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
                 else
@@ -705,8 +778,11 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 if (lane < P) store_sys4(flows_out + k * P + lane, ring_out[ring_index(k * P, R) + lane]);
                 if (k >= 2) {
                     // at least (QT ? P/4 : P) + P/2 + 2 loads, 2 flow stores and 2 NSTORE
-                    // output stores follow the flow store of chunk k - 2: it is complete
-                    wait_vmcnt<(QT ? NQ : P) + P / 2 + 4 + 2 * NSTORE>();
+                    // output stores follow the flow store of chunk k - 2 (HELP: the two
+                    // rows-above loads issued in chunk k - 1 and the two flow stores): it
+                    // is complete
+                    if constexpr (HELP) wait_vmcnt<4>();
+                    else wait_vmcnt<(QT ? NQ : P) + P / 2 + 4 + 2 * NSTORE>();
                     if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
                 }
             }
@@ -822,6 +898,12 @@ int launch_tangent(const float* scores, const float* V, const int* lengths, int 
     return D2P_OK;
 }
 
+// D2P_AMD_SW_HELPERS=0 turns the helper waves off (for tests: both forms must agree)
+static bool helpers_enabled() {
+    const char* e = std::getenv("D2P_AMD_SW_HELPERS");
+    return !(e && e[0] == '0');
+}
+
 template <int MODE, bool DOT, bool NWG = false>
 int launch_dual(const float* scores, const float* V, const int* lengths, int B, int L1, int L2,
                 float gap, float T, const Second& w, const float* dS, float* out, float* dot,
@@ -838,6 +920,11 @@ int launch_dual(const float* scores, const float* V, const int* lengths, int B, 
     auto k8 = sw_dual_kernel<MODE, 8, DOT, NWG>;
     auto k4 = sw_dual_kernel<MODE, 4, DOT, NWG>;
     auto kern = P == 8 ? k8 : k4;
+    // helper waves move the data when a part has at most NW/2 stripes (the others idle)
+    if constexpr (!DOT) {
+        if (P == 8 && (rows + 63) / 64 <= NW / 2 && helpers_enabled())
+            kern = sw_dual_kernel<MODE, 8, DOT, NWG, true>;
+    }
     if (sp.G > 1) D2P_TRY(launch_flag_reset(w.prim.bflag, B * sp.G, st));
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));

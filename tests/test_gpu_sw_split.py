@@ -80,10 +80,11 @@ def test_sw_split_ragged(cuda, parts):
 def test_sw_helper_waves_bit_identical(cuda, parts, monkeypatch, B, L1, L2, n):
     """Parts hand their data movement (tile loads, the alpha table and marginal
     write-outs) to helper waves in the forward and reverse sweeps: the idle waves of the
-    workgroup for parts of at most four stripes, a second set of eight waves for parts
-    of five to eight (the last three cases).  The arithmetic is unchanged, so every
-    output equals the single-wave form bit for bit: SW and NW first order and the SW
-    HVP (whose primal forward is the same sweep), ragged lengths and split parts
+    workgroup for parts of at most four stripes (also in the second-order reverse
+    sweep), a second set of eight waves for parts of five to eight (the last three
+    cases).  The arithmetic is unchanged, so every output equals the single-wave form
+    bit for bit: SW and NW first order, the SW and NW HVPs, the SW parameter
+    Jacobians and the marginal-path backward, ragged lengths and split parts
     included."""
     s = _seeded(41, (B, L1, L2)).to(cuda)
     lens = torch.tensor([[max(1, L1 - 37 * i), max(1, L2 - 11 * i)] for i in range(B)],
@@ -95,7 +96,10 @@ def test_sw_helper_waves_bit_identical(cuda, parts, monkeypatch, B, L1, L2, n):
         monkeypatch.setenv("D2P_AMD_SW_HELPERS", flag)
         out[flag] = (list(_capi.sw_forward_marginals(s, lens, -1.0, 0.9)) +
                      list(_capi.nw_forward_marginals(s, lens, -1.0, 0.9)) +
-                     [_capi.sw_hvp(s, V, lens, -1.0, 0.9)])
+                     [_capi.sw_hvp(s, V, lens, -1.0, 0.9), _capi.nw_hvp(s, V, lens, -1.0, 0.9),
+                      _capi.sw_param_jacobian(s, 0, lens, -1.0, 0.9),
+                      _capi.sw_param_jacobian(s, 1, lens, -1.0, 0.9)] +
+                     list(_capi.sw_backward_full(s, V, lens, -1.0, 0.9)))
     for a, b in zip(out["1"], out["0"]):
         assert torch.equal(a, b)
     ref = O.get("oracle").soft_sw(s.cpu().numpy(), -1.0, 0.9, lens.cpu().numpy())
