@@ -22,6 +22,7 @@
 
 #include <vector>
 
+#include <cstdlib>
 #include <type_traits>
 
 #include "wavefront.hip.h"
@@ -334,7 +335,13 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
 // beta exceeds 1e-20; the flows into column 0 (I[i,0]) and row 0 (D[0,j]) add the
 // boundary's own open and (i-1) or (j-1) extends to the parameter gradients.
 // The second flow ring carries (diagonal D, up D) pairs instead of the diagonal D.
-template <bool NWA = false>
+// HELP (local alignment, parts of at most NW/2 stripes): wave NW/2 + q moves stripe
+// order q's data.  Chunk k's buffer is wave q's own for even k and the helper's for
+// odd k.  The helper loads a chunk's scores and alpha rows one chunk ahead
+// (publishing hprog[q] = chunks loaded), writes the chunk's output tile out once
+// wave q has finished the chunk (prog[q]), and then loads chunk k + 2 into that
+// buffer.  Wave q loads only its rows above and flows.
+template <bool NWA = false, bool HELP = false>
 __global__ void __launch_bounds__(NW * 64)
 swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                     const float* __restrict__ alpha_sk, const float* __restrict__ brow,
@@ -346,8 +353,10 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                     double* __restrict__ bpart, int B, int L1max, int L2max, int NSmax, float go,
                     float ge, float T, int R, int G, int SPW, uint32_t epoch) {
     constexpr int P = PB;
+    static_assert(!HELP || !NWA, "helper waves move quad tiles");
     extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
+    __shared__ int hprog[NW];     // HELP: chunks of stripe order q loaded by its helper
     __shared__ float red_o[NW], red_e[NW], red_p[NW];
     // parts run bottom-up as in the linear backward; the last stripe of a part below
     // the first hands its flows to the part above through flows4 / flows1
@@ -375,8 +384,7 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
     constexpr int WFLOATS = FB1 + 64;               // (diagonal D, up D) pairs)
     static_assert(4 * P + 4 <= 64, "boundary flows fit their buffer");
     using F1 = std::conditional_t<NWA, float2, float>;   // second ring entry
-    float* wbuf = smem + wave * WFLOATS;
-    float* otile = wbuf + OTILE;
+    float* const wbuf0 = smem + wave * WFLOATS;   // this wave's chunk buffer
     __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
                                   // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
@@ -391,7 +399,10 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
     int* st = status + b;
     const int tbase = ChunkTile<P>::read_base(lane);   // dword tiles
 
-    if (lane == 0) prog[wave] = -1;
+    if (lane == 0) {
+        prog[wave] = -1;
+        hprog[wave] = -1;
+    }
     __syncthreads();
 
     const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
@@ -420,6 +431,50 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
     const uint64_t* flag_in = bflag + (size_t)b * G + (part + 1 < G ? part + 1 : part);
     uint64_t* flag_out = bflag + (size_t)b * G + part;
 
+    if constexpr (HELP) {
+        if (NL > NW / 2) {   // never: the host picks HELP for parts of at most NW/2 stripes
+            if (threadIdx.x == 0) atomicOr(st, 2);
+            return;
+        }
+        const int q = wave - NW / 2;
+        if (q >= 0 && q < NL) {
+            const int s = s_begin + NL - 1 - q;
+            const int i0 = s * 64;
+            const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * 3 * PLANE;
+            // chunk k's buffer: wave q's own (even k) or this wave's (odd k)
+            auto cbuf = [&](int k) { return smem + (k & 1 ? wave : q) * WFLOATS; };
+            auto load = [&](int k) {
+                const int th = nsteps - 1 - k * P;
+                const uint32_t in = lds_address(cbuf(k));
+                dma_quads<P, -1>(in, sbase, i0, L1max, L2max, lane, th);
+#pragma unroll
+                for (int pl = 0; pl < 3; ++pl)
+                    dma_rows<P, -1>(in + (AROWS + pl * P * 64) * 4, astripe + pl * PLANE, th - 2,
+                                    ul4);
+            };
+            if (nch > 0) {
+                load(0);
+                wait_vmcnt<0>();
+                publish(hprog, q, 1);
+                if (nch > 1) load(1);
+            }
+            for (int k = 0; k < nch; ++k) {
+                if (k + 1 < nch) {
+                    // chunk k + 1's loads are the last issued
+                    wait_vmcnt<0>();
+                    publish(hprog, q, k + 2);   // also completes this wave's LDS reads
+                }
+                // once wave q has finished chunk k, its output tile leaves and the
+                // buffer takes chunk k + 2 (the stores have read the tile: their data
+                // dependence waits for the reads)
+                wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
+                write_quads<P, -1>(cbuf(k) + OTILE, pbase, trash, i0, L1, L2, L1max, L2max, lane,
+                                   nsteps - 1 - k * P);
+                if (k + 2 < nch) load(k + 2);
+            }
+        }
+    }
+
     for (int q = wave; q < NL; q += NW) {
         const int s = s_begin + NL - 1 - q;
         const int i0 = s * 64;
@@ -433,7 +488,10 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
         const bool x_in = q == 0 && has_next;             // flows from the part below
         const bool x_out = q == NL - 1 && part > 0;       // flows to the part above
         const bool below = q > 0 || x_in;
-        const uint32_t in_lds = lds_address(wbuf);
+        // chunk k's buffer: this wave's own, or (HELP, odd k) its helper's
+        auto kbuf = [&](int k) {
+            return HELP && (k & 1) ? smem + (wave + NW / 2) * WFLOATS : wbuf0;
+        };
         // boundary flows by producer step: written by stripe s (x_out), read from s + 1
         const size_t fo = ((size_t)b * NSmax + s) * NT;
         const size_t fi = ((size_t)b * NSmax + (x_in ? s + 1 : s)) * NT;
@@ -444,15 +502,18 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
         // Loads of chunk k (t_hi = nsteps-1-kP): the score tile, P alpha rows per plane
         // (steps t_hi-2 .. t_hi-P-1) and the stripe above's last row per plane at steps
         // t_hi - j + 63 for lane j <= P (clamped; lanes past P repeat lane P).
-        // NQ + 3P/4 + 3 loads.
+        // NQ + 3P/4 + 3 loads (HELP: the helper loads the tile and rows; 3 loads).
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
-            if constexpr (QT) dma_quads<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
-            else dma_tile<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
+            const uint32_t in_lds = lds_address(kbuf(k));
+            if constexpr (!HELP) {
+                if constexpr (QT) dma_quads<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
+                else dma_tile<P, -1>(in_lds, sbase, i0, L1max, L2max, lane, th);
 #pragma unroll
-            for (int pl = 0; pl < 3; ++pl)
-                dma_rows<P, -1>(in_lds + (AROWS + pl * P * 64) * 4, astripe + pl * PLANE, th - 2,
-                                ul4);
+                for (int pl = 0; pl < 3; ++pl)
+                    dma_rows<P, -1>(in_lds + (AROWS + pl * P * 64) * 4, astripe + pl * PLANE,
+                                    th - 2, ul4);
+            }
             const uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
 #pragma unroll
             for (int pl = 0; pl < 3; ++pl) {
@@ -507,13 +568,22 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
             const int t_hi = nsteps - 1 - k * P;
             chunk_waits<P>(prog, q, NL, k, nch, R, st);
             // this chunk's loads, followed by at least the NQ marginal stores of the
-            // previous chunk (the first chunk's loads are the last issued)
-            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<NQ>();
+            // previous chunk (the first chunk's loads are the last issued).  HELP: the
+            // helper loads the tile and rows; this wave's own loads (rows above, flows)
+            // are followed by nothing, or by the previous chunk's two flow stores (x_out)
+            if constexpr (HELP) {
+                if (x_out && k > 0) wait_vmcnt<2>(); else wait_vmcnt<0>();
+                wait_for(hprog, q, k + 1, st);
+            } else {
+                if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<NQ>();
+            }
             if (x_in && k > 0) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
+            float* const wbuf = kbuf(k);
+            float* const otile = wbuf + OTILE;
             float sv[P];
             if constexpr (QT) {
                 read_quads<P, -1>(wbuf, lane, sv);
@@ -767,7 +837,9 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 else steps(std::false_type{}, std::false_type{});
             }
             wave_lds_sync();
-            if constexpr (QT)
+            if constexpr (HELP)
+                ;   // the helper writes the tile out once this chunk is published
+            else if constexpr (QT)
                 write_quads<P, -1>(otile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             else
                 write_tile<P, -1>(otile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
@@ -782,8 +854,10 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 }
                 if (k >= 2) {
                     // at least NQ + 3P/4 + 3 loads, 2 NQ marginal stores and 4 flow stores
-                    // follow the flow stores of chunk k - 2: those are complete
-                    wait_vmcnt<3 * NQ + 3 * P / 4 + 7>();
+                    // (HELP: the 3 rows-above loads issued in chunk k - 1 and 4 flow
+                    // stores) follow the flow stores of chunk k - 2: those are complete
+                    if constexpr (HELP) wait_vmcnt<7>();
+                    else wait_vmcnt<3 * NQ + 3 * P / 4 + 7>();
                     if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
                 }
             }
@@ -918,6 +992,12 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
     return D2P_OK;
 }
 
+// D2P_AMD_SW_HELPERS=0 turns the helper waves off (for tests: both forms must agree)
+static bool helpers_enabled() {
+    const char* e = std::getenv("D2P_AMD_SW_HELPERS");
+    return !(e && e[0] == '0');
+}
+
 int launch_backward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                     float go, float ge, float T, const Layout& ws, const float* partition,
                     float* marginals, float* grad_open, float* grad_ext, float* grad_T,
@@ -931,6 +1011,9 @@ int launch_backward(const float* scores, const int* lengths, int B, int max_L1, 
     float* flows1 = sp.G > 1 ? reinterpret_cast<float*>(flows4 + ws.flow_slots) : nullptr;
     if (sp.G > 1) D2P_TRY(launch_flag_reset(ws.bflag, B * sp.G, st));
     auto kern = nwa ? swa_backward_kernel<true> : swa_backward_kernel<false>;
+    // helper waves move the data when a part has at most NW/2 stripes (the others idle)
+    const int part_stripes = sp.G > 1 ? sp.SPW : ns;
+    if (!nwa && part_stripes <= NW / 2 && helpers_enabled()) kern = swa_backward_kernel<false, true>;
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
     D2P_LAUNCH(nwa ? "nwa_backward" : "swa_backward", kern, dim3(split_grid(B, sp.G)),

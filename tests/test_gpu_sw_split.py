@@ -84,8 +84,8 @@ def test_sw_helper_waves_bit_identical(cuda, parts, monkeypatch, B, L1, L2, n):
     sweep), a second set of eight waves for parts of five to eight (the last three
     cases).  The arithmetic is unchanged, so every output equals the single-wave form
     bit for bit: SW and NW first order, the SW and NW HVPs, the SW parameter
-    Jacobians and the marginal-path backward, ragged lengths and split parts
-    included."""
+    Jacobians, the marginal-path backward and affine SW first order, ragged lengths
+    and split parts included."""
     s = _seeded(41, (B, L1, L2)).to(cuda)
     lens = torch.tensor([[max(1, L1 - 37 * i), max(1, L2 - 11 * i)] for i in range(B)],
                         dtype=torch.int32, device=cuda)
@@ -99,7 +99,8 @@ def test_sw_helper_waves_bit_identical(cuda, parts, monkeypatch, B, L1, L2, n):
                      [_capi.sw_hvp(s, V, lens, -1.0, 0.9), _capi.nw_hvp(s, V, lens, -1.0, 0.9),
                       _capi.sw_param_jacobian(s, 0, lens, -1.0, 0.9),
                       _capi.sw_param_jacobian(s, 1, lens, -1.0, 0.9)] +
-                     list(_capi.sw_backward_full(s, V, lens, -1.0, 0.9)))
+                     list(_capi.sw_backward_full(s, V, lens, -1.0, 0.9)) +
+                     list(_capi.swa_forward_marginals(s, lens, -3.0, -0.5, 0.9)))
     for a, b in zip(out["1"], out["0"]):
         assert torch.equal(a, b)
     ref = O.get("oracle").soft_sw(s.cpu().numpy(), -1.0, 0.9, lens.cpu().numpy())
