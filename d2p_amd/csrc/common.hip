@@ -159,11 +159,12 @@ extern "C" int d2p_scale_by_batch(const float* src, const float* g, float* dst, 
     if (B == 0 || per_batch == 0) return D2P_OK;
     D2P_REQUIRE(src && g && dst, "null pointer argument");
     const bool vec = (per_batch % 4 == 0) && (((uintptr_t)src | (uintptr_t)dst) % 16 == 0);
-    // about 16384 workgroups in all: rows along y, each row's elements along x
+    // about 32768 workgroups in all (measured on [256, 512 x 512]: 82 us against 85
+    // with 16384 and 92 with 8192): rows along y, each row's elements along x
     const long long row_work = vec ? per_batch / 4 : per_batch;
     const int by = B < 65535 ? B : 65535;
     long long bx = (row_work + 255) / 256;
-    const long long cap = 16384 / by > 1 ? 16384 / by : 1;
+    const long long cap = 32768 / by > 1 ? 32768 / by : 1;
     if (bx > cap) bx = cap;
     D2P_LAUNCH("scale_by_batch", d2p_amd::scale_by_batch_kernel,
                dim3((unsigned)bx, (unsigned)by), dim3(256), 0, (hipStream_t)stream, src, g,

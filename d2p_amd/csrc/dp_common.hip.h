@@ -53,6 +53,17 @@ __device__ __forceinline__ float wave_shl1_or(float v, float old) {
         __float_as_int(old), __float_as_int(v), 0x130, 0xf, 0xf, false));
 }
 
+// max(max(a, b), max(c, d)) as one v_max_f32 and one v_max3_f32.  Through fmaxf the
+// compiler first quiets (canonicalises) each operand that is not the result of
+// arithmetic, e.g. a score read from LDS: one more instruction per use.  A quiet NaN
+// operand gives the other operands' max, as fmaxf; a signalling NaN gives a NaN.
+__device__ __forceinline__ float max4_raw(float a, float b, float c, float d) {
+    float t, m;
+    __asm__("v_max_f32 %0, %1, %2" : "=v"(t) : "v"(c), "v"(d));
+    __asm__("v_max3_f32 %0, %1, %2, %3" : "=v"(m) : "v"(a), "v"(b), "v"(t));
+    return m;
+}
+
 __device__ __forceinline__ float lane_bcast(float v, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }

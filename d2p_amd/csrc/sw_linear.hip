@@ -292,7 +292,10 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                                           fast_exp2((vl - m) * c);
                         a = fmaf(tl, fast_log2(sum), m);
                     } else {
-                        const float m = fmaxf(fmaxf(vd, vu), fmaxf(vl, sv[u]));
+                        // (FULL: the raw max saves the scores' canonicalisation; in
+                        // the masked form it only moves instructions)
+                        const float m = FULL ? max4_raw(vd, vu, vl, sv[u])
+                                             : fmaxf(fmaxf(vd, vu), fmaxf(vl, sv[u]));
                         const float sum =
                             (fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c)) +
                             (fast_exp2((vl - m) * c) + fast_exp2((sv[u] - m) * c));
@@ -715,6 +718,19 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             float4 quad = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             float pre_d2 = wave_shr1(pre_d);   // lane 63 = step 1 (then shifted on)
             pre_d2 = wave_shr1(pre_d2);        // lane 63 = step 2
+            // AHEAD: the ring's up values shifted one step ahead (lane 63 = step 1), and
+            // lane 0's row-above alphas too (bv of step u + 1): each step shifts the next
+            // copy out before its DPP consumes this one as the fill value, so no copy of
+            // a live fill register is needed.  The up alpha of step u + 1 is the
+            // diagonal of step u.  (PRECISE keeps one register each: its double
+            // accumulators leave none to spare.)
+            constexpr bool AHEAD = !PRECISE;
+            float upa_next = 0.0f;
+            if constexpr (AHEAD) {
+                pre_u = wave_shr1(pre_u);
+                upa_next = wave_shr1_or(A[1], bv);
+                bv = wave_shl1(bv);
+            }
             // (SW) beta_init = 2^min((alpha - S) c, 0) is exactly 0 below 2^-150: a chunk
             // none of whose alphas comes within 150 c^-1 of S skips those exponentials
             // (most chunks: alpha grows along the anti-diagonals towards S)
@@ -738,10 +754,19 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const float sc = ok ? sv[u] : kNINF;
                 const float a0 = A[u], a1 = A[u + 1];
                 // up / diagonal alphas from lane r-1; lane 0 takes the row above
-                const float bv_next = wave_shl1(bv);
-                const float upa = wave_shr1_or(a1, bv);
-                const float dga = wave_shr1_or(A[u + 2], bv_next);
-                bv = bv_next;
+                float upa, dga;
+                if constexpr (AHEAD) {
+                    const float bv2 = wave_shl1(bv);
+                    upa = upa_next;
+                    dga = wave_shr1_or(A[u + 2], bv);
+                    upa_next = dga;
+                    bv = bv2;
+                } else {
+                    const float bv_next = wave_shl1(bv);
+                    upa = wave_shr1_or(a1, bv);
+                    dga = wave_shr1_or(A[u + 2], bv_next);
+                    bv = bv_next;
+                }
                 const float vd = dga + sc;
                 const float vu = upa + gap;
                 const float vl = a1 + gap;
@@ -768,8 +793,10 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 } else {
                     binit = 0.0f;
                 }
-                // reference accumulation order: init, diagonal, left, up successor
-                const float beta = ((binit + in_diag) + in_left) + in_up;
+                // reference accumulation order: init, diagonal, left, up successor (the
+                // flows are never -0, so without a start term 0 + in_diag is in_diag)
+                const float beta = (NWG || INIT || !AHEAD) ? ((binit + in_diag) + in_left) + in_up
+                                                           : (in_diag + in_left) + in_up;
                 const bool live = ok && (beta <= 3.0e38f);    // skips inf / NaN like the reference
                 const float br = live ? beta * rin : 0.0f;
                 const float od = br * e0, ou = br * e1, ol = br * e2;
@@ -800,9 +827,16 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 else p_acc = fmaf(pv, sc, p_acc);
                 pub[u] = make_float2(ou, od);
                 // successor contributions for the next steps; lane 63 takes the ring
-                pre_u = wave_shr1(pre_u);
-                in_left = ol;
-                in_up = wave_shl1_or(ou, pre_u);
+                if constexpr (AHEAD) {
+                    const float pre_u2 = wave_shr1(pre_u);
+                    in_left = ol;
+                    in_up = wave_shl1_or(ou, pre_u);
+                    pre_u = pre_u2;
+                } else {
+                    pre_u = wave_shr1(pre_u);
+                    in_left = ol;
+                    in_up = wave_shl1_or(ou, pre_u);
+                }
                 in_diag = in_diag_next;
                 in_diag_next = wave_shl1_or(od, pre_d2);
                 pre_d2 = wave_shr1(pre_d2);
