@@ -432,7 +432,13 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
 // gradient's term) are both recomputed from the predecessors' alpha with the forward's
 // own arithmetic, so the costs are never loaded and the fused squared-Euclidean path
 // shares this sweep unchanged.
-template <int P>
+//
+// HELP (unbanded parts of at most NW/2 stripes, e.g. 256-row elements): wave NW/2 + q
+// helps the wave of stripe order q.  It loads the alpha rows one chunk ahead into that
+// wave's buffers (publishing hprog[q] = chunks loaded) and writes the chunk's marginals
+// out of a tile in its own, otherwise unused, buffers once wave q has finished the
+// chunk; wave q keeps only the row above and the boundary flows.
+template <int P, bool HELP = false>
 __global__ void __launch_bounds__(NW * 64)
 dtw_backward_kernel(const int* __restrict__ lengths,
                     const float* __restrict__ alpha_sk, const float* __restrict__ brow,
@@ -444,6 +450,7 @@ dtw_backward_kernel(const int* __restrict__ lengths,
                     uint32_t epoch) {
     extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
+    __shared__ int hprog[NW];     // HELP: chunks of stripe order q loaded by its helper
     __shared__ float red_g[NW];
     // parts run bottom-up as in the linear-SW backward
     int b, dpart;
@@ -471,7 +478,10 @@ dtw_backward_kernel(const int* __restrict__ lengths,
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
 
-    if (lane == 0) prog[wave] = -1;
+    if (lane == 0) {
+        prog[wave] = -1;
+        hprog[wave] = -1;
+    }
     __syncthreads();
 
     const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
@@ -502,6 +512,47 @@ dtw_backward_kernel(const int* __restrict__ lengths,
     if ((size_t)NS * stride > elem_steps) {   // never: the host reserves enough
         if (threadIdx.x == 0) atomicOr(st, 2);
         return;
+    }
+
+    if constexpr (HELP) {
+        if (NL > NW / 2 || bandwidth >= 0) {   // never: the host picks HELP for these only
+            if (threadIdx.x == 0) atomicOr(st, 2);
+            return;
+        }
+        const int q = wave - NW / 2;
+        if (q >= 0 && q < NL) {
+            const int s = s_begin + NL - 1 - q;
+            const int i0 = s * 64;
+            // unbanded: the window is every chunk and the table starts at step 0
+            const float* astripe = band_stripe(alpha_sk, b, elem_steps, s, stride);
+            float* qbufs = smem + q * 2 * BUF;      // the sweeping wave's two chunk buffers
+            float* obufs = smem + wave * 2 * BUF;   // its output tiles: this wave's buffers
+            auto load = [&](int k) {
+                const int th = nsteps - 1 - k * P;
+                dma_rows<P, -1>(lds_address(qbufs + (k & 1) * BUF) + ABUF * 4, astripe, th - 2,
+                                ul4);
+            };
+            if (nch > 0) {
+                load(0);
+                wait_vmcnt<0>();
+                publish(hprog, q, 1);
+                if (nch > 1) load(1);
+            }
+            for (int k = 0; k < nch; ++k) {
+                if (k + 1 < nch) {
+                    // chunk k + 1's loads: the last issued at k = 0, else followed by the
+                    // P marginal stores of chunk k - 1
+                    if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+                    publish(hprog, q, k + 2);   // also completes this wave's LDS reads
+                }
+                // once wave q has finished chunk k, its buffer k & 1 takes chunk k + 2
+                // and its marginals (in output tile k & 1) leave
+                wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
+                if (k + 2 < nch) load(k + 2);
+                write_tile<P, -1>(obufs + (k & 1) * BUF, pbase, trash, i0, L1, L2, L1max,
+                                  L2max, lane, nsteps - 1 - k * P);
+            }
+        }
     }
 
     // Stripes run bottom-up: order q = 0..NL-1 handles stripe s_begin+NL-1-q, on wave
@@ -546,7 +597,7 @@ dtw_backward_kernel(const int* __restrict__ lengths,
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
             const uint32_t buf = lds_address(bufs + (k & 1) * BUF);
-            dma_rows<P, -1>(buf + ABUF * 4, astripe, th - 2 - sh, ul4);
+            if (!HELP) dma_rows<P, -1>(buf + ABUF * 4, astripe, th - 2 - sh, ul4);
             uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
             uint32_t rl = buf + RBUF * 4;
             lds_dma_dword<0>(bup, roff, rl, 0u);
@@ -595,15 +646,25 @@ dtw_backward_kernel(const int* __restrict__ lengths,
             const int t_hi = nsteps - 1 - k * P;
             chunk_waits<P>(prog, q, NL, k, nch, R, st, k_lo);
             // this chunk's loads were issued one chunk ago and followed by at least the
-            // P marginal stores of that chunk (the first chunk's are the last issued)
-            if (k == k_lo) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            // P marginal stores of that chunk (the first chunk's are the last issued).
+            // HELP: the helper loads the alpha rows; this wave's own loads (row above,
+            // flows) are followed by nothing, or by the previous chunk's flow store
+            if constexpr (HELP) {
+                if (x_out && k > k_lo) wait_vmcnt<1>(); else wait_vmcnt<0>();
+                wait_for(hprog, q, k + 1, st);
+            } else {
+                if (k == k_lo) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            }
             if (x_in && k > k_lo) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
             float* buf = bufs + (k & 1) * BUF;
-            float* tile = buf;
+            // the chunk's marginals: over its own buffer's tile, or (HELP) in the
+            // helper's buffer k & 1, whose previous tile the helper has written out
+            // before publishing this chunk as loaded
+            float* tile = HELP ? smem + (wave + NW / 2) * 2 * BUF + (k & 1) * BUF : buf;
             A[0] = A[P];
             A[1] = A[P + 1];
 #pragma unroll
@@ -685,15 +746,19 @@ dtw_backward_kernel(const int* __restrict__ lengths,
             if (bw < 0 && i0 + 63 < L1 && t_hi - P - 62 >= 0 && t_hi < L2) steps(std::true_type{});
             else steps(std::false_type{});
             wave_lds_sync();
-            write_tile<P, -1>(tile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
+            // (HELP: the helper writes the tile once this chunk is published)
+            if constexpr (!HELP)
+                write_tile<P, -1>(tile, pbase, trash, i0, L1, L2, L1max, L2max, lane, t_hi);
             publish(prog, wave, q * PROG_STRIDE + k + 1);
             if (x_out) {
                 // this chunk's flows to the part above, by producer step
                 if (lane < P) store_sys2(flows_out + k * P + lane, ring_out[ring_index(k * P, R) + lane]);
                 if (k >= 2) {
                     // at least P/4 + 1 loads, 2P marginal stores and 2 flow stores
-                    // follow the flow store of chunk k - 2: it is complete
-                    wait_vmcnt<2 * P + P / 4 + 3>();
+                    // follow the flow store of chunk k - 2 (HELP: the row-above load
+                    // issued in chunk k - 1 and the two flow stores): it is complete
+                    if constexpr (HELP) wait_vmcnt<3>();
+                    else wait_vmcnt<2 * P + P / 4 + 3>();
                     if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
                 }
             }
@@ -763,6 +828,13 @@ int max_stripes_backward(int max_L1, int max_L2) {
     return lds_backward_r(ring_backward(max_L1, max_L2), 8) <= kLdsLimit ? 0 : NW;
 }
 
+// D2P_AMD_DTW_HELPERS=0 turns the reverse sweep's helper waves off (for tests: both
+// forms must agree bit for bit)
+bool dtw_helpers_enabled() {
+    const char* e = std::getenv("D2P_AMD_DTW_HELPERS");
+    return !(e && e[0] == '0');
+}
+
 template <int P>
 int launch_backward_p(const int* lengths, int B, int max_L1, int max_L2,
                       float T, int bandwidth, const Layout& ws, float* marginals, float* grad_T,
@@ -771,9 +843,13 @@ int launch_backward_p(const int* lengths, int B, int max_L1, int max_L2,
     const size_t lds = lds_backward_r(R, P);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     if (sp.G > 1) D2P_TRY(launch_flag_reset(ws.bflag, B * sp.G, st));
-    D2P_HIP(hipFuncSetAttribute((const void*)dtw_backward_kernel<P>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH("dtw_backward", dtw_backward_kernel<P>, dim3(split_grid(B, sp.G)), dim3(NW * 64),
+    // helper waves for unbanded parts of at most NW/2 stripes (waves NW/2.. would idle)
+    const int part_stripes = sp.G > 1 ? sp.SPW : ns;
+    const bool help = bandwidth < 0 && part_stripes <= NW / 2 && dtw_helpers_enabled();
+    auto kern = help ? dtw_backward_kernel<P, true> : dtw_backward_kernel<P, false>;
+    D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+    D2P_LAUNCH("dtw_backward", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64),
                lds, st, lengths, ws.alpha_sk, ws.brow, marginals, grad_T, ws.status, ws.trash,
                ws.bflag, ws.flows, ws.bpart, B, max_L1, max_L2, ns, ws.elem_steps, T,
                bandwidth, R, sp.G, sp.SPW, next_epoch());

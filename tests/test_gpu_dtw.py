@@ -92,6 +92,29 @@ def test_dtw_config_c4_style(cuda):
     _check(gpu, ref, c.numpy(), 0.1)
 
 
+@pytest.mark.parametrize("B,L1,L2,n_parts,ragged", [(4, 256, 256, 1, False),
+                                                    (3, 700, 110, 4, True),
+                                                    (2, 130, 300, 1, True),
+                                                    (5, 64, 90, 1, True)])
+def test_dtw_helper_waves_bit_identical(cuda, monkeypatch, B, L1, L2, n_parts, ragged):
+    """Unbanded parts of at most four stripes run the reverse sweep with helper waves
+    that load the alpha rows and write the marginals out; the arithmetic is the
+    sweeping wave's either way, so every output equals the form without helpers bit
+    for bit (split parts and ragged lengths included)."""
+    c = _sq_dist_costs(41, B, L1, L2, 16).to(cuda)
+    lens = None
+    if ragged:
+        rows = [[L1, L2], [max(L1 - 37, 1), L2 // 2], [0, 7], [5, 0], [1, 1]][:B]
+        lens = torch.tensor(rows, dtype=torch.int32, device=cuda)
+    monkeypatch.setenv("D2P_AMD_SPLIT", str(n_parts))
+    monkeypatch.setenv("D2P_AMD_DTW_HELPERS", "1")
+    with_h = _capi.dtw_forward_marginals(c, lens, 0.3)
+    monkeypatch.setenv("D2P_AMD_DTW_HELPERS", "0")
+    without = _capi.dtw_forward_marginals(c, lens, 0.3)
+    for a, b in zip(with_h, without):
+        assert torch.equal(a, b)
+
+
 def test_dtw_ragged_lengths_and_band(cuda):
     B, L1, L2 = 6, 150, 170
     c = _seeded(4, (B, L1, L2)).abs()
