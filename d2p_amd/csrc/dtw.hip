@@ -157,6 +157,10 @@ constexpr int HELP_U = 12;
 // [0, HELP_U) of every chunk of stripe l's costs into a double-buffered tile one chunk
 // ahead, publishing cprog[l] = chunks formed; it reuses a buffer once the sweeping
 // wave l has finished the chunk that read it (prog[l]).
+// HELP (costs from memory, unbanded, at most NW/2 stripes per part): wave NW/2 + l
+// loads stripe l's cost chunks one chunk ahead into wave l's tiles (cprog[l] = chunks
+// loaded) and writes each chunk's alpha rows to the table from a tile in its own,
+// otherwise unused, buffers once wave l has finished the chunk.
 template <int DC = 0, bool HELP = false>
 __global__ void __launch_bounds__(NW * 64)
 dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ lengths,
@@ -168,11 +172,11 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                    int D) {
     constexpr int P = PF;
     constexpr bool FUSED = DC > 0;
-    static_assert(!HELP || FUSED, "helper waves form fused costs");
     static_assert(!HELP || P == 16, "the helper split assumes 16-step chunks");
     extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
-    __shared__ int cprog[NW];     // HELP: chunks of stripe l's costs formed by its helper
+    __shared__ int cprog[NW];     // HELP: chunks of stripe l's costs formed (or loaded)
+                                  // by its helper
     __shared__ float terminal;
     // part of the element as in the linear-SW forward: the first stripe of a part > 0
     // reads the previous part's last row from brow
@@ -230,7 +234,52 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
         return;
     }
 
-    if constexpr (HELP) {
+    if constexpr (HELP && !FUSED) {
+        if (NL > NW / 2 || bandwidth >= 0) {   // never: the host picks HELP for these only
+            if (threadIdx.x == 0) atomicOr(st, 2);
+            return;
+        }
+        const int l = wave - NW / 2;
+        if (l >= 0 && l < NL) {
+            const int s = s_begin + l;
+            const int i0 = s * 64;
+            // unbanded: the window is every chunk and the table starts at step 0
+            float* out = band_stripe(alpha_sk, b, elem_steps, s, stride) + APAD * 64;
+            const uint32_t ltiles = lds_address(smem + l * WBUF);   // wave l's cost tiles
+            const float* atiles = smem + wave * WBUF;               // its alpha tiles
+            auto load = [&](int k) {
+                dma_tile<P, 1>(ltiles + (k & 1) * Tile::FLOATS * 4, cbase, i0, L1max, L2max,
+                               lane, k * P);
+            };
+            if (nch > 0) {
+                load(0);
+                wait_vmcnt<0>();
+                publish(cprog, l, 1);
+                if (nch > 1) load(1);
+            }
+            for (int k = 0; k < nch; ++k) {
+                if (k + 1 < nch) {
+                    // chunk k + 1's loads: the last issued at k = 0, else followed by the
+                    // P/4 alpha stores of chunk k - 1
+                    if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P / 4>();
+                    publish(cprog, l, k + 2);   // also completes this wave's LDS reads
+                }
+                // once wave l has finished chunk k, its cost tile k & 1 takes chunk k + 2
+                // and its alpha rows (alpha tile k & 1) go to the table
+                wait_for(prog, l, l * PROG_STRIDE + k + 1, st);
+                if (k + 2 < nch) load(k + 2);
+                const float* at = atiles + (k & 1) * Tile::FLOATS;
+                float* dst = out + (size_t)k * P * 64;
+#pragma unroll
+                for (int i = 0; i < P / 4; ++i) {
+                    const float4 v = *reinterpret_cast<const float4*>(at + 256 * i + 4 * lane);
+                    *reinterpret_cast<float4*>(dst + 256 * i + 4 * lane) = v;
+                }
+            }
+        }
+    }
+
+    if constexpr (HELP && FUSED) {
         if (NL > NW / 2) {   // never: the host picks HELP for parts of at most NW/2 stripes
             if (threadIdx.x == 0) atomicOr(st, 2);
             return;
@@ -321,7 +370,7 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                 seen = wait_part(flag_in, epoch, min(k_lo + lead(P), nch), st);
                 issue_row(k_lo);
             }
-            if (!FUSED)
+            if (!FUSED && !HELP)
                 dma_tile<P, 1>(tile_lds + (k_lo & 1) * Tile::FLOATS * 4, cbase, i0, L1max, L2max,
                                lane, k_lo * P);
         }
@@ -333,8 +382,10 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
             const int t0 = k * P;
             chunk_waits<P>(prog, l, NL, k, nch, R, st, k_lo);
             // this chunk's costs: loaded one chunk ago, followed by at least the P + 1
-            // stores of that chunk (the first chunk's load is the last issued)
-            if (k == k_lo) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            // stores of that chunk (the first chunk's load is the last issued).
+            // HELP from memory: the helper loads the costs; this wave's own loads (the
+            // row above of a part's first stripe) are followed by the last-row store
+            if (k == k_lo) wait_vmcnt<0>(); else if (HELP && !FUSED) wait_vmcnt<1>(); else wait_vmcnt<P>();
             if (x_in && k > k_lo) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
@@ -342,7 +393,9 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
             }
             float* tile = tiles + (NTILE == 2 ? (k & 1) * Tile::FLOATS : 0);
             float cv[P];
-            if constexpr (HELP) {
+            if constexpr (HELP && !FUSED) {
+                wait_for(cprog, l, k + 1, st);   // the chunk's costs, loaded by the helper
+            } else if constexpr (HELP) {
                 wait_for(cprog, l, k + 1, st);   // the helper's steps [0, HELP_U)
                 fused_costs<DC, HELP_U, P>(tile, tbase, xr, ylds, t0, lane, L2max);
             } else if constexpr (FUSED) {
@@ -364,13 +417,17 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
                     issue_row(k + 1);
                 }
-                if (!FUSED)
+                if (!FUSED && !HELP)
                     dma_tile<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, cbase, i0, L1max,
                                    L2max, lane, t0 + P);
                 if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             float* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             float* outc = out + (size_t)(t0 - sh) * 64;
+            // HELP from memory: the chunk's alphas by step in the helper's alpha tile
+            // k & 1 (written to the table by the helper, which has written that tile's
+            // previous chunk before publishing this chunk's costs as loaded)
+            float* atile = smem + (wave + NW / 2) * WBUF + (k & 1) * Tile::FLOATS + lane;
             // FULL: every cell of the chunk lies inside the element, no validity masks
             auto steps = [&](auto full) {
             constexpr bool FULL = decltype(full)::value;
@@ -389,7 +446,8 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                 const int col = t - lane;
                 const bool ok = FULL || ((unsigned)col < (unsigned)L2eff && in_band(ej, col + 1, bw));
                 cur = ok ? a : kPINF;
-                lane_store(outc + u * 64, ul4, cur);
+                if (HELP && !FUSED) atile[u * 64] = cur;
+                else lane_store(outc + u * 64, ul4, cur);
                 pub[u] = cur;
                 if (ok && last_row && col == L2 - 1) terminal = cur;
             }
@@ -407,8 +465,10 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
             publish(prog, wave, l * PROG_STRIDE + k + 1);
             if (x_out && k >= 2) {
                 // at least P loads (none when fused) and 2P + 2 stores follow the row
-                // store of chunk k - 2: it (and everything before) is complete
-                wait_vmcnt<(FUSED ? 2 * P + 2 : 3 * P + 2)>();
+                // store of chunk k - 2 (HELP from memory: the last-row stores of chunks
+                // k - 1 and k): it (and everything before) is complete
+                if constexpr (HELP && !FUSED) wait_vmcnt<2>();
+                else wait_vmcnt<(FUSED ? 2 * P + 2 : 3 * P + 2)>();
                 if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
             }
         }
@@ -881,9 +941,13 @@ int launch_forward(const float* costs, const int* lengths, int B, int max_L1, in
     const size_t lds = lds_forward_r(R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     if (sp.G > 1 && launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
-    D2P_HIP(hipFuncSetAttribute((const void*)dtw_forward_kernel<0>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH("dtw_forward", dtw_forward_kernel<0>, dim3(split_grid(B, sp.G)), dim3(NW * 64),
+    // helper waves for unbanded parts of at most NW/2 stripes (waves NW/2.. would idle)
+    const int part_stripes = sp.G > 1 ? sp.SPW : ns;
+    const bool help = bandwidth < 0 && part_stripes <= NW / 2 && dtw_helpers_enabled();
+    auto kern = help ? dtw_forward_kernel<0, true> : dtw_forward_kernel<0, false>;
+    D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds));
+    D2P_LAUNCH("dtw_forward", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64),
                lds, st, costs, lengths, ws.alpha_sk, ws.brow, value, ws.status, ws.fflag, B,
                max_L1, max_L2, ns, ws.elem_steps, T, bandwidth, R, sp.G, sp.SPW, next_epoch(),
                nullptr, nullptr, 0);

@@ -97,10 +97,11 @@ def test_dtw_config_c4_style(cuda):
                                                     (2, 130, 300, 1, True),
                                                     (5, 64, 90, 1, True)])
 def test_dtw_helper_waves_bit_identical(cuda, monkeypatch, B, L1, L2, n_parts, ragged):
-    """Unbanded parts of at most four stripes run the reverse sweep with helper waves
-    that load the alpha rows and write the marginals out; the arithmetic is the
-    sweeping wave's either way, so every output equals the form without helpers bit
-    for bit (split parts and ragged lengths included)."""
+    """Unbanded parts of at most four stripes run both sweeps with helper waves (the
+    forward's load the costs and write the alpha table, the reverse sweep's load the
+    alpha rows and write the marginals); the arithmetic is the sweeping wave's either
+    way, so every output equals the form without helpers bit for bit (split parts and
+    ragged lengths included)."""
     c = _sq_dist_costs(41, B, L1, L2, 16).to(cuda)
     lens = None
     if ragged:
