@@ -99,12 +99,12 @@ void profile_end(const char* name, hipStream_t stream, hipEvent_t start) {
 // per row and no index is divided.
 __global__ void __launch_bounds__(256)
 scale_by_batch_kernel(const float* __restrict__ src, const float* __restrict__ g,
-                      float* __restrict__ dst, int B, long long n, int vec) {
+                      long long g_stride, float* __restrict__ dst, int B, long long n, int vec) {
     const long long stride = (long long)gridDim.x * blockDim.x;
     const long long first = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     typedef float v4f __attribute__((ext_vector_type(4)));
     for (int b = blockIdx.y; b < B; b += gridDim.y) {
-        const float gb = g[b];
+        const float gb = g[(size_t)b * g_stride];
         if (vec) {
             const long long n4 = n >> 2;
             const v4f* s4 = reinterpret_cast<const v4f*>(src) + (size_t)b * n4;
@@ -155,7 +155,13 @@ extern "C" int d2p_profile_report(char* buf, size_t len) {
 
 extern "C" int d2p_scale_by_batch(const float* src, const float* g, float* dst, int B,
                                   long long per_batch, void* stream) {
+    return d2p_scale_by_batch_strided(src, g, 1, dst, B, per_batch, stream);
+}
+
+extern "C" int d2p_scale_by_batch_strided(const float* src, const float* g, long long g_stride,
+                                          float* dst, int B, long long per_batch, void* stream) {
     D2P_REQUIRE(B >= 0 && per_batch >= 0, "negative size");
+    D2P_REQUIRE(g_stride >= 0, "negative factor stride");
     if (B == 0 || per_batch == 0) return D2P_OK;
     D2P_REQUIRE(src && g && dst, "null pointer argument");
     const bool vec = (per_batch % 4 == 0) && (((uintptr_t)src | (uintptr_t)dst) % 16 == 0);
@@ -168,7 +174,7 @@ extern "C" int d2p_scale_by_batch(const float* src, const float* g, float* dst, 
     if (bx > cap) bx = cap;
     D2P_LAUNCH("scale_by_batch", d2p_amd::scale_by_batch_kernel,
                dim3((unsigned)bx, (unsigned)by), dim3(256), 0, (hipStream_t)stream, src, g,
-               dst, B, per_batch, vec ? 1 : 0);
+               g_stride, dst, B, per_batch, vec ? 1 : 0);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }

@@ -140,15 +140,21 @@ Tensor grad_param_sum(const Tensor& grad_value, const Tensor& per_batch) {
     return (grad_value.to(torch::kFloat32) * per_batch).sum().reshape({1});
 }
 
-// g[b] * src, through the C ABI (autograd backward of value -> scores)
+// g[b] * src, through the C ABI (autograd backward of value -> scores).  The factors
+// are read in place by stride: the gradient of `value.sum()` arrives as one value
+// expanded over the batch (stride 0), which needs no copy.
 Tensor scale_by_batch(const Tensor& src, const Tensor& g) {
-    Tensor gg = g.to(src.device(), torch::kFloat32).contiguous();
+    Tensor gg = g.to(src.device(), torch::kFloat32);
     TORCH_CHECK(gg.numel() == src.size(0), "grad_value must have one entry per batch element");
+    if (gg.dim() != 1) gg = gg.reshape({-1});
+    if (gg.numel() > 0 && gg.stride(0) < 0) gg = gg.contiguous();
     Tensor out = torch::empty_like(src);
-    D2P_CALL(d2p_scale_by_batch(src.data_ptr<float>(), gg.data_ptr<float>(),
-                                out.data_ptr<float>(), (int)src.size(0),
-                                (long long)(src.numel() / std::max<int64_t>(src.size(0), 1)),
-                                current_stream()));
+    D2P_CALL(d2p_scale_by_batch_strided(src.data_ptr<float>(), gg.data_ptr<float>(),
+                                        (long long)gg.stride(0), out.data_ptr<float>(),
+                                        (int)src.size(0),
+                                        (long long)(src.numel() /
+                                                    std::max<int64_t>(src.size(0), 1)),
+                                        current_stream()));
     return out;
 }
 

@@ -404,6 +404,14 @@ int d2p_dtw_backward_full(const float* costs, const float* grad_alignment, const
 int d2p_scale_by_batch(const float* src, const float* g, float* dst, int B,
                        long long per_batch, void* stream);
 
+/* The same with g[b] read at g + b * g_stride (g_stride >= 0; 0: one factor for every
+ * row, as in the expanded gradient of `value.sum()`), so that a caller holding a
+ * strided or broadcast gradient needs no copy of it.  Replaces the same ATen
+ * expression, which broadcasts a strided grad_score
+ * (/root/reference/src/sw/torch_cuda.cpp:314). */
+int d2p_scale_by_batch_strided(const float* src, const float* g, long long g_stride,
+                               float* dst, int B, long long per_batch, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,7 @@ SIGNATURES = {
     "d2p_profile_report": (_i, [ctypes.c_char_p, _z]),
     "d2p_profile_reset": (None, []),
     "d2p_scale_by_batch": (_i, [_p, _p, _p, _i, _ll, _p]),
+    "d2p_scale_by_batch_strided": (_i, [_p, _p, _ll, _p, _i, _ll, _p]),
 }
 
 _lib = None
@@ -349,6 +350,16 @@ def scale_by_batch(src, g):
     out = torch.empty_like(src)
     B = src.shape[0]
     check(lib().d2p_scale_by_batch(ptr(src), ptr(g), ptr(out), B, src.numel() // B, stream()))
+    return out
+
+
+def scale_by_batch_strided(src, g):
+    """g: a 1-d view with one factor per batch row, any non-negative stride."""
+    import torch
+    out = torch.empty_like(src)
+    B = src.shape[0]
+    check(lib().d2p_scale_by_batch_strided(ptr(src), ptr(g), g.stride(0), ptr(out), B,
+                                           src.numel() // B, stream()))
     return out
 
 

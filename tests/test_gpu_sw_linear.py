@@ -111,6 +111,20 @@ def test_scale_by_batch(cuda, shape):
     torch.testing.assert_close(out, g.view(-1, 1, 1) * src, rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("kind", ["expanded", "every_other", "contiguous"])
+def test_scale_by_batch_strided(cuda, kind):
+    """Factors read in place by stride: one value expanded over the batch (stride 0,
+    the gradient of value.sum()), every other element of a longer vector, and a
+    contiguous vector; each bit-identical to the broadcast product."""
+    src = _seeded(5, (6, 40, 36)).to(cuda)
+    base = _seeded(6, (12,)).to(cuda)
+    g = {"expanded": base[3:4].expand(6), "every_other": base[::2],
+         "contiguous": base[:6]}[kind]
+    out = _capi.scale_by_batch_strided(src, g)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out, g.reshape(-1, 1, 1) * src, rtol=0, atol=0)
+
+
 def test_soft_sw_api_value_backward(cuda):
     """d2p_amd.soft_sw + value.sum().backward(): grad equals the marginals."""
     import d2p_amd
