@@ -46,7 +46,12 @@ enum Mode { HVP = 0, GAP = 1, TEMP = 2 };
 
 // ------------------------------------------------------------------ tangent sweep
 
-template <int MODE, int P, bool NWG = false>
+// HELP (parts of at most NW/2 stripes): wave NW/2 + l loads stripe l's inputs (score
+// and direction quads, alpha rows, the row above) one chunk ahead, publishing
+// hprog[l] = chunks loaded.  Chunk k's buffer is wave l's own for even k and the
+// helper's for odd k, and the helper refills it with chunk k + 2 once wave l has
+// finished chunk k (prog[l]).  Wave l keeps only the tangent row of the part above.
+template <int MODE, int P, bool NWG = false, bool HELP = false>
 __global__ void __launch_bounds__(NW * 64)
 sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                   const int* __restrict__ lengths, const float* __restrict__ alpha_sk,
@@ -66,6 +71,7 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     constexpr int SINK = 64 + P;
     extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
+    __shared__ int hprog[NW];     // HELP: chunks of stripe l loaded by its helper
     __shared__ float red[NW];
     // parts as in the primal forward: part p > 0 takes its first stripe's tangent row
     // above from part p - 1 through tan_brow
@@ -83,7 +89,10 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     float* sink = rings + NW * R + wave * SINK;
     int* st = status + b;
 
-    if (lane == 0) prog[wave] = -1;
+    if (lane == 0) {
+        prog[wave] = -1;
+        hprog[wave] = -1;
+    }
     __syncthreads();
 
     const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
@@ -104,6 +113,48 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     const bool has_next = s_begin + NL < NS;
     const uint64_t* flag_in = tflag + (size_t)b * G + (part > 0 ? part - 1 : 0);
     uint64_t* flag_out = tflag + (size_t)b * G + part;
+    // HELP: chunk k's input buffer (wave l's for even k, its helper's for odd k)
+    auto kbuf = [&](int l, int k) { return smem + ((k & 1) ? l + NW / 2 : l) * BUF; };
+
+    if constexpr (HELP) {
+        if (NL > NW / 2) {   // never: the host picks HELP for parts of at most NW/2 stripes
+            if (threadIdx.x == 0) atomicOr(st, 2);
+            return;
+        }
+        const int l = wave - NW / 2;
+        if (l >= 0 && l < NL) {
+            const int s = s_begin + l;
+            const int i0 = s * 64;
+            const float* astripe = alpha_sk + ((size_t)b * NSmax + s) * NT * 64;
+            const float* bup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
+            auto load = [&](int k) {
+                const int t0 = k * P;
+                const uint32_t base = lds_address(kbuf(l, k));
+                dma_quads<P, 1>(base, sbase, i0, L1max, L2max, lane, t0);
+                if (HAS_V) dma_quads<P, 1>(base + VT * 4, vbase, i0, L1max, L2max, lane, t0);
+                dma_rows<P, 1>(base + AR * 4, astripe, t0, ul4);
+                uint32_t roff = (uint32_t)min(t0 + 62 + min(lane, P), nsteps - 1) * 4u;
+                uint32_t rl = base + RR * 4;
+                lds_dma_dword<0>(bup, roff, rl, 0u);
+            };
+            if (nch > 0) {
+                load(0);
+                wait_vmcnt<0>();
+                publish(hprog, l, 1);
+                if (nch > 1) load(1);
+            }
+            for (int k = 0; k < nch; ++k) {
+                if (k + 1 < nch) {
+                    // chunk k + 1's loads are the last issued
+                    wait_vmcnt<0>();
+                    publish(hprog, l, k + 2);
+                }
+                // once wave l has finished chunk k, its buffer takes chunk k + 2
+                wait_for(prog, l, l * PROG_STRIDE + k + 1, st);
+                if (k + 2 < nch) load(k + 2);
+            }
+        }
+    }
 
     for (int l = wave; l < NL; l += NW) {
         const int s = s_begin + l;
@@ -123,18 +174,22 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
         // Loads of chunk k (steps t0 .. t0+P-1): the score (and direction) tiles, the
         // P alpha rows, and for lane j <= P the last row of the stripe above at step
         // t0 + 62 + j (clamped; lanes past P repeat lane P).
+        // (HELP: the helper issues all but the tangent row above, into buffer kbuf)
         auto issue_chunk = [&](int k) {
             const int t0 = k * P;
-            dma_quads<P, 1>(in_lds, sbase, i0, L1max, L2max, lane, t0);
-            if (HAS_V) dma_quads<P, 1>(in_lds + VT * 4, vbase, i0, L1max, L2max, lane, t0);
-            dma_rows<P, 1>(in_lds + AR * 4, astripe, t0, ul4);
-            uint32_t roff = (uint32_t)min(t0 + 62 + min(lane, P), nsteps - 1) * 4u;
-            uint32_t rl = in_lds + RR * 4;
-            lds_dma_dword<0>(bup, roff, rl, 0u);
+            const uint32_t base = HELP ? lds_address(kbuf(l, k)) : in_lds;
+            if (!HELP) {
+                dma_quads<P, 1>(base, sbase, i0, L1max, L2max, lane, t0);
+                if (HAS_V) dma_quads<P, 1>(base + VT * 4, vbase, i0, L1max, L2max, lane, t0);
+                dma_rows<P, 1>(base + AR * 4, astripe, t0, ul4);
+                uint32_t roff = (uint32_t)min(t0 + 62 + min(lane, P), nsteps - 1) * 4u;
+                uint32_t rl = base + RR * 4;
+                lds_dma_dword<0>(bup, roff, rl, 0u);
+            }
             if (x_in) {
                 // lane j < P: the tangent of the last row above at step t0 + 63 + j
                 uint32_t toff = (uint32_t)min(t0 + 63 + min(lane, P - 1), nsteps - 1) * 4u;
-                uint32_t tl = in_lds + TR * 4;
+                uint32_t tl = base + TR * 4;
                 lds_dma_dword_sys<0>(tb_up, toff, tl, 0u);
             }
         };
@@ -162,11 +217,13 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             // this chunk's loads, followed by at least the P + 1 stores of the previous
             // chunk (the first chunk's loads are the last issued)
             if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+            if (HELP) wait_for(hprog, l, k + 1, st);   // the helper's loads of chunk k
             if (x_in && k > 0) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
+            float* buf = HELP ? kbuf(l, k) : smem + wave * BUF;
             float sv[P], vv[P];
             read_quads<P, 1>(buf, lane, sv);
             if (HAS_V) {
@@ -288,8 +345,10 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             publish(prog, wave, l * PROG_STRIDE + k + 1);
             if (x_out && k >= 2) {
                 // at least P/4 + P/4 + 1 loads and 2P + 2 stores follow the row store
-                // of chunk k - 2: it (and everything before) is complete
-                wait_vmcnt<2 * P + Tile::NQ + P / 4 + 3>();
+                // of chunk k - 2 (HELP: the 2P + 2 stores): it (and everything before)
+                // is complete
+                if constexpr (HELP) wait_vmcnt<2 * P + 2>();
+                else wait_vmcnt<2 * P + Tile::NQ + P / 4 + 3>();
                 if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
             }
         }
@@ -874,6 +933,8 @@ Second second_layout(void* ws, int B, int L1, int L2) {
     return w;
 }
 
+static bool helpers_enabled();
+
 template <int MODE, bool NWG = false>
 int launch_tangent(const float* scores, const float* V, const int* lengths, int B, int L1, int L2,
                    float gap, float T, const Second& w, float* sdot, hipStream_t st) {
@@ -884,7 +945,11 @@ int launch_tangent(const float* scores, const float* V, const int* lengths, int 
     const int R = ring_len(sp.G > 1 ? sp.SPW * 64 : L1, L2, 256);
     const size_t lds = lds_tangent_r(MODE, R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
-    auto kern = sw_tangent_kernel<MODE, PT, NWG>;
+    // helper waves for parts of at most NW/2 stripes (waves NW/2.. would idle)
+    const int part_stripes = sp.G > 1 ? sp.SPW : ns;
+    auto kern = part_stripes <= NW / 2 && helpers_enabled()
+                    ? sw_tangent_kernel<MODE, PT, NWG, true>
+                    : sw_tangent_kernel<MODE, PT, NWG, false>;
     if (sp.G > 1) D2P_TRY(launch_flag_reset(w.prim.fflag, B * sp.G, st));
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
