@@ -64,7 +64,12 @@ __device__ __forceinline__ float lse4(float a, float b, float x, float y, float 
 // I[i,0] = open + (i-1) ext, D[0,j] = open + (j-1) ext (NINF elsewhere), and the
 // value is LSE(M, I, D) of the terminal cell (L1, L2).  The cells left of column 0
 // hold the row's boundary in the tables; row 0 is generated in registers.
-template <bool NWA = false>
+// HELP (local alignment, parts of at most NW/2 stripes): wave NW/2 + l loads stripe
+// l's score chunks one chunk ahead (hprog[l] = chunks loaded) and writes the M and I
+// planes of each chunk's alphas to the table once wave l has finished the chunk:
+// wave l leaves them in a tile of the helper's (its own buffer for even chunks, a
+// region after the rings for odd ones) and stores only the D plane itself.
+template <bool NWA = false, bool HELP = false>
 __global__ void __launch_bounds__(NW * 64)
 swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                    float* __restrict__ alpha_sk, float* __restrict__ brow,
@@ -73,8 +78,10 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                    int L2max, int NSmax, float go, float ge, float T, int R, int G, int SPW,
                    uint32_t epoch) {
     constexpr int P = PF;
+    static_assert(!HELP || !NWA, "helper waves serve the local form");
     extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
+    __shared__ int hprog[NW];     // HELP: score chunks of stripe l loaded by its helper
     __shared__ float red_m[NW], red_z[NW];
     __shared__ float term[3];     // NWA: (M, I, D) of the terminal cell
     // part of the element as in the linear forward: the first stripe of a part > 0
@@ -94,9 +101,17 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     const uint32_t fslot_lds = lds_address(fslot);
     float4* rings = reinterpret_cast<float4*>(smem + NW * WBUF);   // [NW][R]
     float4* sink = rings + NW * R + wave * DUMMY;
+    // HELP: the M and I alpha tiles ([2][P][64]) of stripe l's chunk k
+    float* xtra = reinterpret_cast<float*>(rings + NW * R + NW * DUMMY);   // [NW/2][2P][64]
+    auto mi_tile = [&](int l, int k) {
+        return (k & 1) ? xtra + l * 2 * P * 64 : smem + (l + NW / 2) * WBUF;
+    };
     int* st = status + b;
 
-    if (lane == 0) prog[wave] = -1;
+    if (lane == 0) {
+        prog[wave] = -1;
+        hprog[wave] = -1;
+    }
     if (G == 1 && threadIdx.x == 0) *st = 0;              // G > 1: reset before the launch
     if (NWA && threadIdx.x < 3) term[threadIdx.x] = kNINF;
     __syncthreads();
@@ -120,6 +135,53 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
 
     OnlineLSE acc;
     acc.init_open();
+
+    if constexpr (HELP) {
+        if (NL > NW / 2) {   // never: the host picks HELP for parts of at most NW/2 stripes
+            if (threadIdx.x == 0) atomicOr(st, 2);
+            return;
+        }
+        const int l = wave - NW / 2;
+        if (l >= 0 && l < NL) {
+            const int s = s_begin + l;
+            const int i0 = s * 64;
+            float* out = alpha_sk + ((size_t)b * NSmax + s) * 3 * PLANE + APAD * 64;
+            const uint32_t ltiles = lds_address(smem + l * WBUF);   // wave l's score tiles
+            auto load = [&](int k) {
+                dma_quads<P, 1>(ltiles + (k & 1) * Tile::FLOATS * 4, sbase, i0, L1max, L2max,
+                                lane, k * P);
+            };
+            if (nch > 0) {
+                load(0);
+                wait_vmcnt<0>();
+                publish(hprog, l, 1);
+                if (nch > 1) load(1);
+            }
+            for (int k = 0; k < nch; ++k) {
+                if (k + 1 < nch) {
+                    // chunk k + 1's loads: the last issued at k = 0, else followed by the
+                    // 2 P/4 alpha stores of chunk k - 1
+                    if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<2 * (P / 4)>();
+                    publish(hprog, l, k + 2);   // also completes this wave's LDS reads
+                }
+                // once wave l has finished chunk k, its score tile k & 1 takes chunk
+                // k + 2 and its M and I rows go to the table
+                wait_for(prog, l, l * PROG_STRIDE + k + 1, st);
+                if (k + 2 < nch) load(k + 2);
+                const float* at = mi_tile(l, k);
+                float* dst = out + (size_t)k * P * 64;
+#pragma unroll
+                for (int pl = 0; pl < 2; ++pl) {
+#pragma unroll
+                    for (int i = 0; i < P / 4; ++i) {
+                        const float4 v =
+                            *reinterpret_cast<const float4*>(at + pl * P * 64 + 256 * i + 4 * lane);
+                        *reinterpret_cast<float4*>(dst + pl * PLANE + 256 * i + 4 * lane) = v;
+                    }
+                }
+            }
+        }
+    }
 
     for (int l = wave; l < NL; l += NW) {
         const int s = s_begin + l;
@@ -160,7 +222,7 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
             issue_rows(0);
         }
-        dma_quads<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
+        if (!HELP) dma_quads<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
         float cM = kNINF, cI = bndI, cD = kNINF;       // this lane's previous step
         float pM = kNINF, pI = kNINF, pD = kNINF;      // up values of the previous step
         if (NWA && lane == 0) {
@@ -173,8 +235,11 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             const int t0 = k * P;
             chunk_waits<P>(prog, l, NL, k, nch, R, st);
             // this chunk's scores: loaded one chunk ago and followed by at least the
-            // 3P + 3 stores of that chunk (the first chunk's load is the last issued)
-            if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<3 * P>();
+            // 3P + 3 stores of that chunk (the first chunk's load is the last issued).
+            // HELP: the helper loads the scores; this wave's own loads (the rows above
+            // of a part's first stripe) are followed by at least its P + 3 stores
+            if (k == 0) wait_vmcnt<0>(); else if (HELP) wait_vmcnt<P>(); else wait_vmcnt<3 * P>();
+            if (HELP) wait_for(hprog, l, k + 1, st);
             if (x_in && k > 0) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
@@ -206,12 +271,17 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
                     issue_rows(k + 1);
                 }
-                dma_quads<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0, L1max,
-                                L2max, lane, t0 + P);
+                if (!HELP)
+                    dma_quads<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0,
+                                    L1max, L2max, lane, t0 + P);
                 if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             float4* pub = (lane == 63) ? ring_out + ring_index(t0, R) : sink + lane;
             float* outc = out + (size_t)t0 * 64;
+            // HELP: the M and I rows of this chunk in the helper's tile (written to the
+            // table by the helper, which has written that tile's previous chunk before
+            // publishing this chunk's scores as loaded)
+            float* mit = mi_tile(l, k) + lane;
             // FULL: every cell of the chunk lies inside the element, no validity masks
             auto steps = [&](auto full) {
             constexpr bool FULL = decltype(full)::value;
@@ -250,8 +320,13 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     term[1] = I;
                     term[2] = D;
                 }
-                lane_store(outc + u * 64, ul4, cM);
-                lane_store(outc + PLANE + u * 64, ul4, cI);
+                if (HELP) {
+                    mit[u * 64] = cM;
+                    mit[P * 64 + u * 64] = cI;
+                } else {
+                    lane_store(outc + u * 64, ul4, cM);
+                    lane_store(outc + PLANE + u * 64, ul4, cI);
+                }
                 lane_store(outc + 2 * PLANE + u * 64, ul4, cD);
                 pub[u] = make_float4(cM, cI, cD, 0.0f);
                 aM[u] = cM;
@@ -284,8 +359,10 @@ swa_forward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             publish(prog, wave, l * PROG_STRIDE + k + 1);
             if (x_out && k >= 2) {
                 // at least P/4 loads and 6P + 6 stores follow the row stores of chunk
-                // k - 2 (more than the counter holds): those are complete
-                wait_vmcnt<63>();
+                // k - 2 (more than the counter holds; HELP: the 2P + 6 D-plane and
+                // row stores of chunks k - 1 and k): those are complete
+                if constexpr (HELP) wait_vmcnt<2 * P + 6>();
+                else wait_vmcnt<63>();
                 if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
             }
         }
@@ -969,16 +1046,26 @@ Layout affine_layout(void* workspace, int B, int max_L1, int max_L2, bool split)
     return layout(workspace, B, max_L1, max_L2, 3, split, kFlowBytes);
 }
 
+static bool helpers_enabled();
+
 int launch_forward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                    float go, float ge, float T, const Layout& ws, float* partition,
                    hipStream_t st, bool nwa) {
     const int ns = (max_L1 + 63) / 64;
     const Split sp = choose_split(B, max_L1, ws, max_stripes_forward(max_L1, max_L2));
     const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
-    const size_t lds = lds_forward_r(R);
+    size_t lds = lds_forward_r(R);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     if (sp.G > 1 && launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
-    auto kern = nwa ? swa_forward_kernel<true> : swa_forward_kernel<false>;
+    // helper waves (local form, parts of at most NW/2 stripes) need the odd chunks' M
+    // and I tiles after the rings: NW/2 x 2P x 64 floats
+    const int part_stripes = sp.G > 1 ? sp.SPW : ns;
+    const size_t lds_help = lds + (size_t)(NW / 2) * 2 * PF * 64 * sizeof(float);
+    const bool help =
+        !nwa && part_stripes <= NW / 2 && lds_help <= kLdsLimit && helpers_enabled();
+    if (help) lds = lds_help;
+    auto kern = nwa ? swa_forward_kernel<true>
+                    : (help ? swa_forward_kernel<false, true> : swa_forward_kernel<false, false>);
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
     D2P_LAUNCH(nwa ? "nwa_forward" : "swa_forward", kern, dim3(split_grid(B, sp.G)),
