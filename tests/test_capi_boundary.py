@@ -103,6 +103,19 @@ def _err(lib):
     return lib.d2p_last_error().decode()
 
 
+def test_scale_by_batch_validation(lib):
+    """Argument checks that run before any device work (no GPU needed)."""
+    rc = lib.d2p_scale_by_batch_strided(FAKE, FAKE, -1, FAKE, 2, 16, None)
+    assert rc == D2P_ERR_ARG and "negative factor stride" in _err(lib)
+    rc = lib.d2p_scale_by_batch_strided(FAKE, FAKE, 0, FAKE, -1, 16, None)
+    assert rc == D2P_ERR_ARG and "negative" in _err(lib)
+    rc = lib.d2p_scale_by_batch(FAKE, FAKE, FAKE, 2, -3, None)
+    assert rc == D2P_ERR_ARG and "negative" in _err(lib)
+    # empty work is a no-op, even with null pointers
+    assert lib.d2p_scale_by_batch_strided(None, None, 0, None, 0, 16, None) == 0
+    assert lib.d2p_scale_by_batch(None, None, None, 4, 0, None) == 0
+
+
 def test_forward_validation(lib):
     z = ctypes.c_size_t(1 << 20)
     rc = lib.d2p_sw_forward_marginals(FAKE, FAKE, 2, 10, 10, -1.0, 0.0, FAKE, FAKE, FAKE, FAKE,
