@@ -17,6 +17,7 @@
 // layout (one alpha plane).  The band test needs i*L2/L1 per row: each lane computes
 // it once per stripe, so the per-cell test is a subtraction and a compare.
 
+#include <algorithm>
 #include <cstdlib>
 #include <vector>
 
@@ -1026,29 +1027,38 @@ int launch_fused(const float* x, const float* y, const int* lengths, int B, int 
 
 // costs[b, i, j] = sum_d (x[b,i,d] - y[b,j,d])^2 with the fused forward's arithmetic:
 // one thread per column (its row of y in registers), SQDIST_COLS columns and
-// SQDIST_ROWS rows of x (in LDS, read as broadcasts) per workgroup.
+// SQDIST_ROWS rows of x (in LDS, read as broadcasts) per tile.  Workgroups stride over
+// the batch (grid z) and the row tiles (grid y), so any B and L1 fit the grid limits.
 constexpr int SQDIST_ROWS = 32;
 constexpr int SQDIST_COLS = 256;
+constexpr int SQDIST_GRID_MAX = 65535;   // grid y and z extents
 
 template <int DC>
 __global__ void __launch_bounds__(SQDIST_COLS)
 pairwise_sqdist_kernel(const float* __restrict__ x, const float* __restrict__ y,
-                       float* __restrict__ costs, int L1, int L2, int D) {
+                       float* __restrict__ costs, int B, int L1, int L2, int D) {
     __shared__ __align__(16) float xs[SQDIST_ROWS * DC];
-    const int b = blockIdx.z, i0 = blockIdx.y * SQDIST_ROWS, j0 = blockIdx.x * SQDIST_COLS;
-    const int nrow = min(SQDIST_ROWS, L1 - i0), ncol = min(SQDIST_COLS, L2 - j0);
-    const float* xb = x + ((size_t)b * L1 + i0) * D;
-    for (int idx = threadIdx.x; idx < nrow * DC; idx += SQDIST_COLS) {
-        const int r = idx / DC, d = idx % DC;
-        xs[idx] = d < D ? xb[(size_t)r * D + d] : 0.0f;
-    }
-    float yr[DC];   // this thread's column (threads past the last column repeat it)
-    load_feature_row<DC>(yr, y + (size_t)b * L2 * D, j0 + min((int)threadIdx.x, ncol - 1), D);
-    __syncthreads();
-    if ((int)threadIdx.x >= ncol) return;
-    float* out = costs + ((size_t)b * L1 + i0) * L2 + j0 + threadIdx.x;
+    const int j0 = blockIdx.x * SQDIST_COLS;
+    const int ncol = min(SQDIST_COLS, L2 - j0);
+    for (int b = blockIdx.z; b < B; b += gridDim.z) {
+        float yr[DC];   // this thread's column (threads past the last column repeat it)
+        load_feature_row<DC>(yr, y + (size_t)b * L2 * D, j0 + min((int)threadIdx.x, ncol - 1), D);
+        for (int i0 = blockIdx.y * SQDIST_ROWS; i0 < L1; i0 += gridDim.y * SQDIST_ROWS) {
+            const int nrow = min(SQDIST_ROWS, L1 - i0);
+            const float* xb = x + ((size_t)b * L1 + i0) * D;
+            __syncthreads();   // the previous tile's reads of xs are complete
+            for (int idx = threadIdx.x; idx < nrow * DC; idx += SQDIST_COLS) {
+                const int r = idx / DC, d = idx % DC;
+                xs[idx] = d < D ? xb[(size_t)r * D + d] : 0.0f;
+            }
+            __syncthreads();
+            if ((int)threadIdx.x < ncol) {
+                float* out = costs + ((size_t)b * L1 + i0) * L2 + j0 + threadIdx.x;
 #pragma unroll 1
-    for (int r = 0; r < nrow; ++r) out[(size_t)r * L2] = sq_euclid_xl<DC>(xs + r * DC, yr);
+                for (int r = 0; r < nrow; ++r) out[(size_t)r * L2] = sq_euclid_xl<DC>(xs + r * DC, yr);
+            }
+        }
+    }
 }
 
 }  // namespace dtw
@@ -1091,26 +1101,26 @@ extern "C" int d2p_pairwise_sqdist(const float* x, const float* y, int B, int L1
                                    float* costs, void* stream) {
     D2P_REQUIRE(B >= 0 && L1 >= 0 && L2 >= 0, "negative dimension");
     D2P_REQUIRE(D >= 1 && dtw::feature_chunk(D) > 0, "feature dimension D must be between 1 and 128");
-    D2P_REQUIRE(B <= 65535, "B must be at most 65535");
-    D2P_REQUIRE((L1 + dtw::SQDIST_ROWS - 1) / dtw::SQDIST_ROWS <= 65535,
-                "L1 must be at most 2097120");
     if (B == 0 || L1 == 0 || L2 == 0) return D2P_OK;
     D2P_REQUIRE(x && y && costs, "null pointer argument");
     hipStream_t st = (hipStream_t)stream;
     const int DC = dtw::feature_chunk(D), CB = dtw::SQDIST_COLS;
-    const dim3 grid((L2 + CB - 1) / CB, (L1 + dtw::SQDIST_ROWS - 1) / dtw::SQDIST_ROWS, B);
+    // (the kernel strides over batch elements and row tiles beyond the grid extents)
+    const dim3 grid((L2 + CB - 1) / CB,
+                    std::min((L1 + dtw::SQDIST_ROWS - 1) / dtw::SQDIST_ROWS, dtw::SQDIST_GRID_MAX),
+                    std::min(B, dtw::SQDIST_GRID_MAX));
     switch (DC) {
         case 32:
             D2P_LAUNCH("pairwise_sqdist", dtw::pairwise_sqdist_kernel<32>, grid, dim3(CB), 0, st,
-                       x, y, costs, L1, L2, D);
+                       x, y, costs, B, L1, L2, D);
             break;
         case 64:
             D2P_LAUNCH("pairwise_sqdist", dtw::pairwise_sqdist_kernel<64>, grid, dim3(CB), 0, st,
-                       x, y, costs, L1, L2, D);
+                       x, y, costs, B, L1, L2, D);
             break;
         default:
             D2P_LAUNCH("pairwise_sqdist", dtw::pairwise_sqdist_kernel<128>, grid, dim3(CB), 0, st,
-                       x, y, costs, L1, L2, D);
+                       x, y, costs, B, L1, L2, D);
     }
     D2P_HIP(hipGetLastError());
     return D2P_OK;

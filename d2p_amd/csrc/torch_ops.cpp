@@ -1202,7 +1202,6 @@ Tensor pairwise_sqdist(Tensor x, Tensor y) {
     CHECK_INPUT_DEV(x);
     CHECK_INPUT_DEV(y);
     Dims d = checked_dims_xy(x, y);
-    TORCH_CHECK(d.B <= 65535 && d.L1 <= 65535, "pairwise_sqdist: B and L1 must be at most 65535");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
     Tensor out = torch::empty({d.B, d.L1, d.L2}, x.options());
     D2P_CALL(d2p_pairwise_sqdist(x.data_ptr<float>(), y.data_ptr<float>(), d.B, d.L1, d.L2,

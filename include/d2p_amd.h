@@ -344,8 +344,8 @@ int d2p_dtw_sqeuclid_forward_marginals(const float* x, const float* y, const int
 /* costs[b,i,j] = sum_d (x[b,i,d] - y[b,j,d])^2 with exactly the arithmetic of the fused
  * sweeps above (bit-identical costs), for callers that need the matrix itself (the
  * fused op's marginal-path backward).  No counterpart in the reference (see above).
- *   x [B, L1, D], y [B, L2, D], costs [B, L1, L2]; 1 <= D <= 128, B <= 65535,
- *   L1 <= 2097120 */
+ *   x [B, L1, D], y [B, L2, D], costs [B, L1, L2]; 1 <= D <= 128 (any B and L1: the
+ *   kernel strides over batch elements and row tiles past the grid limits) */
 int d2p_pairwise_sqdist(const float* x, const float* y, int B, int L1, int L2, int D,
                         float* costs, void* stream);
 

@@ -190,3 +190,14 @@ def test_c_abi_accepts_the_reference_table_range(lib):
     rc = lib.d2p_swa_forward_marginals(FAKE, FAKE, 1, 2, 262081, -2.0, -0.5, 1.0, FAKE, FAKE,
                                        FAKE, FAKE, FAKE, FAKE, 1 << 40, None)
     assert rc == D2P_ERR_ARG and b"max_L2 exceeds 262080" in lib.d2p_last_error()
+
+
+def test_pairwise_sqdist_has_no_grid_limits(lib):
+    """d2p_pairwise_sqdist strides over batch elements and row tiles, so shapes past
+    the grid extents (B > 65535, L1 > 32 * 65535) reach the null-pointer check
+    instead of a size limit; D outside [1, 128] is refused.  No kernel runs."""
+    rc = lib.d2p_pairwise_sqdist(None, FAKE, 70000, 3_000_000, 8, 16, FAKE, None)
+    assert rc == D2P_ERR_ARG and "null pointer" in _err(lib)
+    rc = lib.d2p_pairwise_sqdist(FAKE, FAKE, 2, 4, 4, 129, FAKE, None)
+    assert rc == D2P_ERR_ARG and "feature dimension" in _err(lib)
+    assert lib.d2p_pairwise_sqdist(None, None, 70000, 0, 8, 16, None, None) == D2P_OK
