@@ -20,9 +20,15 @@ int check_shape(int B, int max_L1, int max_L2, float temperature);
 // Forward sweep: alpha table, last rows and partition[B] (status words reset).
 // global: soft Needleman-Wunsch (gap boundary rows, no sky term); partition[B] then
 // receives the value alpha[L1, L2].
+// ckpt: store only the checkpoint rows a recomputing reverse sweep starts from (where
+// helper waves write the table; otherwise the whole table, which holds them too).
 int launch_forward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                    float gap, float T, const Layout& ws, float* partition, hipStream_t st,
-                   bool global = false);
+                   bool global = false, bool ckpt = false);
+
+// Whether a first-order call recomputes alpha in its reverse sweep (and so runs the
+// forward in checkpoint mode).
+bool recompute_alpha(int B, int max_L1, int max_L2, const Layout& ws);
 
 // Reverse sweep: marginals, dS/dgap and dS/dT per element, from a forward's table.
 // precise: sum dS/dgap and dS/dT in double (for the second-order paths).
@@ -35,7 +41,7 @@ int launch_backward(const float* scores, const int* lengths, int B, int max_L1, 
                     float gap, float T, const Layout& ws, const float* partition,
                     float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
                     bool precise = false, bool global = false, float* poison_value = nullptr,
-                    bool* poisoned = nullptr);
+                    bool* poisoned = nullptr, bool recompute = false);
 
 }  // namespace sw
 }  // namespace d2p_amd

@@ -35,6 +35,45 @@ using namespace wf;
 
 constexpr int PF = 16;               // steps per chunk, forward sweep
 constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do not publish
+constexpr int PR = 16;               // steps per chunk of the reverse sweeps that recompute
+
+// One cell of the forward recurrence from its neighbours' alphas and its score: the LSE
+// of the diagonal, up and left candidates and (SW) the sky term.  The forward sweep and
+// the reverse sweep's recomputation of alpha from checkpoints both call this, so they
+// produce the same bits.  RAWMAX: the max without canonicalising the score (the same
+// value for every non-NaN input).
+template <bool NWG, bool RAWMAX>
+__device__ __forceinline__ float fwd_cell(float diag, float up, float cur, float sc, float gap,
+                                          float c, float tl) {
+    // out-of-table neighbours are NINF, so no i>1 / j>1 guards are needed
+    const float vd = diag + sc;
+    const float vu = up + gap;
+    const float vl = cur + gap;
+    // exponents (v - m) / T with the subtraction first, as the reference: an fma
+    // against a rounded m*c would add the rounding of m*c to alpha itself (about an
+    // ulp), which the temperature Jacobians' (alpha - S) / T^2 terms amplify
+    if (NWG) {
+        const float m = fmaxf(fmaxf(vd, vu), vl);
+        const float sum = (fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c)) +
+                          fast_exp2((vl - m) * c);
+        return fmaf(tl, fast_log2(sum), m);
+    } else {
+        const float m = RAWMAX ? max4_raw(vd, vu, vl, sc) : fmaxf(fmaxf(vd, vu), fmaxf(vl, sc));
+        const float sum = (fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c)) +
+                          (fast_exp2((vl - m) * c) + fast_exp2((sc - m) * c));
+        return fmaf(tl, fast_log2(sum), m);
+    }
+}
+
+// Checkpoint steps of a stripe of nsteps steps for reverse sweeps of PR-step chunks that
+// recompute alpha: chunk k (its highest step t_hi = nsteps - 1 - PR*k) rebuilds steps
+// t_hi - PR - 1 .. t_hi - 2 from the stored steps t_hi - PR - 2 and t_hi - PR - 3,
+// i.e. the steps congruent to nsteps - 3 and nsteps - 4 modulo PR; the first chunk also
+// starts from the last two steps.  A forward in checkpoint mode stores only these.
+__device__ __forceinline__ bool ckpt_step(int t, int nsteps) {
+    const int d = (nsteps - 3 - t) & (PR - 1);
+    return d == 0 || d == PR - 1 || t >= nsteps - 2;
+}
 
 // One part (G > 1: a workgroup owns stripes [part*SPW, part*SPW + SPW) of its element;
 // G == 1: all of them).  The first stripe of a part > 0 reads the last row of the
@@ -61,8 +100,9 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                   float* __restrict__ partition, int* __restrict__ status,
                   uint64_t* __restrict__ fflag, float2* __restrict__ fpart, int B, int L1max,
                   int L2max, int NSmax, float gap, float T, int R, int G, int SPW,
-                  uint32_t epoch) {
+                  uint32_t epoch, int ckpt) {
     constexpr int P = PF;
+    static_assert(PF == PR, "checkpoint rows are chosen per forward chunk");
     extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     __shared__ int hprog[NW];     // HELP: chunks of stripe l loaded by its helper
@@ -75,10 +115,12 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = QuadTile<P>;
-    constexpr int WBUF = 2 * Tile::FLOATS + 2 * 64 + P;    // two score chunks, two rows
-    float* tiles = smem + wave * WBUF;                     // double-buffered score chunk
-    float* rbufs = tiles + 2 * Tile::FLOATS;               // boundary row of a chunk
-    float* upbuf = rbufs + 2 * 64;                         // the chunk's row above, by step
+    // score tiles per sweeping wave: chunk k uses tile k % NTB (WIDE: four, so that the
+    // helper can load three chunks ahead)
+    constexpr int NTB = WIDE ? 4 : 2;
+    constexpr int WBUF = NTB * Tile::FLOATS + 2 * 64 + P;  // score chunks, two rows, pad
+    float* tiles = smem + wave * WBUF;                     // the score chunks
+    float* rbufs = tiles + NTB * Tile::FLOATS;             // boundary row of a chunk
     __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
                                   // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
@@ -128,36 +170,101 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             // score tiles, once their scores are in wave l's registers
             const float* atiles = smem + (WIDE ? l : wave) * WBUF;
             auto load = [&](int k) {
-                dma_quads<P, 1>(ltiles + (k & 1) * Tile::FLOATS * 4, sbase, i0, L1max, L2max,
-                                lane, k * P);
+                dma_quads<P, 1>(ltiles + (k & (NTB - 1)) * Tile::FLOATS * 4, sbase, i0, L1max,
+                                L2max, lane, k * P);
             };
-            if (nch > 0) {
+            // the stripe's last row (lane 63 of wave l) by step, from its ring, for the
+            // reverse sweep; a part's last stripe with a next part stores its own (its
+            // progress word must follow those stores).  The ring slots of chunk k are
+            // rewritten R / P chunks later; wave l cannot run that far ahead of this
+            // wave, whose loads it waits for.
+            const bool l_x_out = l == NL - 1 && has_next;
+            float* hbrow = brow + ((size_t)b * NSmax + s_begin + l) * NT;
+            const float* hring = ring_of(smem + NW * WBUF, l, R);
+            auto store_row = [&](int k) {
+                if (!l_x_out && lane < P) {
+                    const int t0 = k * P;
+                    lane_store(hbrow, (unsigned)(t0 + lane) * 4u, hring[(t0 % R) + lane]);
+                }
+            };
+            // the chunk's alpha rows (alpha tile k % NTB) to the table: Tile::NQ stores
+            auto store_alpha = [&](int k) {
+                const float* at = atiles + (k & (NTB - 1)) * Tile::FLOATS;
+                float* dst = out + (size_t)k * P * 64;
+                if (ckpt) {
+                    // checkpoint mode: only the rows a recomputing reverse sweep starts
+                    // from (ckpt_step): the chunk's steps congruent to nsteps - 3 and
+                    // nsteps - 4 modulo PR, and the stripe's last two steps where they
+                    // lie in this chunk (else the first two again).  Tile::NQ stores,
+                    // as the full write-out issues: the load waits count on it.
+                    const int t0 = k * P;
+                    const int u0 = (nsteps - 4 - t0) & (PR - 1);
+                    const int u1 = (nsteps - 3 - t0) & (PR - 1);
+                    const int u2 = (unsigned)(nsteps - 2 - t0) < (unsigned)P ? nsteps - 2 - t0 : u0;
+                    const int u3 = (unsigned)(nsteps - 1 - t0) < (unsigned)P ? nsteps - 1 - t0 : u1;
+                    static_assert(Tile::NQ == 4, "four checkpoint stores per chunk");
+                    const float v0 = at[u0 * 64 + lane], v1 = at[u1 * 64 + lane];
+                    const float v2 = at[u2 * 64 + lane], v3 = at[u3 * 64 + lane];
+                    dst[u0 * 64 + lane] = v0;
+                    dst[u1 * 64 + lane] = v1;
+                    dst[u2 * 64 + lane] = v2;
+                    dst[u3 * 64 + lane] = v3;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < Tile::NQ; ++i) {
+                        const float4 v =
+                            *reinterpret_cast<const float4*>(at + 256 * i + 4 * lane);
+                        *reinterpret_cast<float4*>(dst + 256 * i + 4 * lane) = v;
+                    }
+                }
+            };
+            if constexpr (WIDE) {
+                // Chunk k's alpha rows lie over its score tile once wave l has read the
+                // scores.  Iteration k starts once wave l has finished chunk k - 1 and
+                // that chunk's rows have left, so its tile takes chunk k + 3: every load
+                // has about three chunks of time.  (nch >= 4: nsteps = L2 + 63.)
+                load(0);
+                load(1);
+                load(2);
+                wait_vmcnt<2 * Tile::NQ>();   // chunk 0 (at least 2 NQ loads follow)
+                publish(hprog, l, 1);
+                wait_vmcnt<Tile::NQ>();
+                publish(hprog, l, 2);
+                for (int k = 0; k < nch; ++k) {
+                    const bool more = k + 3 < nch;
+                    if (more) load(k + 3);
+                    wait_for(prog, l, l * PROG_STRIDE + k + 1, st);
+                    store_alpha(k);
+                    store_row(k);
+                    if (k + 2 < nch) {
+                        // chunk k + 2's loads (issued at iteration k - 1, or before the
+                        // loop) are followed by chunk k - 1's alpha stores (k >= 1),
+                        // chunk k + 3's loads (more) and chunk k's alpha stores
+                        if (k >= 1 && more) wait_vmcnt<3 * Tile::NQ>();
+                        else if (k >= 1 || more) wait_vmcnt<2 * Tile::NQ>();
+                        else wait_vmcnt<Tile::NQ>();
+                        publish(hprog, l, k + 3);   // also completes this wave's LDS reads
+                    }
+                }
+            } else if (nch > 0) {
                 load(0);
                 wait_vmcnt<0>();
                 publish(hprog, l, 1);
                 if (nch > 1) load(1);
-            }
-            for (int k = 0; k < nch; ++k) {
-                if (k + 1 < nch) {
-                    // chunk k + 1's loads: the last issued at k = 0 (WIDE: always),
-                    // else followed by the P/4 alpha stores of chunk k - 1
-                    if (WIDE || k == 0) wait_vmcnt<0>(); else wait_vmcnt<Tile::NQ>();
-                    publish(hprog, l, k + 2);   // also completes this wave's LDS reads
+                for (int k = 0; k < nch; ++k) {
+                    if (k + 1 < nch) {
+                        // chunk k + 1's loads: the last issued at k = 0, else followed by
+                        // the P/4 alpha stores of chunk k - 1
+                        if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<Tile::NQ>();
+                        publish(hprog, l, k + 2);   // also completes this wave's LDS reads
+                    }
+                    // once wave l has finished chunk k, its score tile k & 1 takes chunk
+                    // k + 2 and its alpha rows (alpha tile k & 1) go to the table
+                    wait_for(prog, l, l * PROG_STRIDE + k + 1, st);
+                    if (k + 2 < nch) load(k + 2);
+                    store_alpha(k);
+                    store_row(k);
                 }
-                // once wave l has finished chunk k, its score tile k & 1 takes chunk
-                // k + 2 and its alpha rows (alpha tile k & 1) go to the table
-                wait_for(prog, l, l * PROG_STRIDE + k + 1, st);
-                if (!WIDE && k + 2 < nch) load(k + 2);
-                const float* at = atiles + (k & 1) * Tile::FLOATS;
-                float* dst = out + (size_t)k * P * 64;
-#pragma unroll
-                for (int i = 0; i < Tile::NQ; ++i) {
-                    const float4 v = *reinterpret_cast<const float4*>(at + 256 * i + 4 * lane);
-                    *reinterpret_cast<float4*>(dst + 256 * i + 4 * lane) = v;
-                }
-                // WIDE: the alpha tile lies over the score tile the load refills (the
-                // stores above have read it: their data dependence waits for the reads)
-                if (WIDE && k + 2 < nch) load(k + 2);
             }
         }
     }
@@ -200,17 +307,23 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
         float cur = left0, up_prev = NWG ? (float)(i0 + lane) * gap : kNINF;
         float bm = -1e20f;   // the running max of this lane's alphas (partition)
         int slot0 = 0;       // ring slot of step t0: t0 % R (R is a multiple of P)
+        ProgAhead ahead;     // progress words read during the previous chunk
+        prog_ahead_reset(ahead);
 
         for (int k = 0; k < nch; ++k, slot0 = slot0 + P < R ? slot0 + P : slot0 + P - R) {
             const int t0 = k * P;
-            chunk_waits<P>(prog, l, NL, k, nch, R, st);
+            chunk_waits_ahead<P>(ahead, prog, l, NL, k, nch, R, st);
             // this chunk's loads were issued one chunk ago and followed by at least the
             // P + 1 stores of that chunk (the first chunk's loads are the last issued).
-            // HELP: the helper loads the scores; this wave's own loads (the row above
-            // of a part's first stripe) are followed by the last-row store
+            // HELP: the helper loads the scores; this wave loads only the row above of a
+            // part's first stripe (followed by the last-row store), and waits for
+            // nothing else: a wait for its own stores would stall it behind the
+            // helpers' memory traffic
             if constexpr (HELP) {
-                if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<1>();
-                wait_for(hprog, l, k + 1, st);
+                if (x_in) {
+                    if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<1>();
+                }
+                wait_for_ahead(ahead.help, hprog, l, k + 1, st);
             } else {
                 if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
             }
@@ -219,33 +332,22 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                 const int got = flag_chunks_lds(fslot, epoch);
                 seen = got > seen ? got : seen;
             }
-            const float* tile = tiles + (k & 1) * Tile::FLOATS;
+            const float* tile = tiles + (k & (NTB - 1)) * Tile::FLOATS;
             float sv[P], av[P];
             read_quads<P, 1>(tile, lane, sv);
-            // lane 0's up values, column t0+j from lane j (ring slot = producer step),
-            // staged so that step j reads them back with one broadcast LDS read; above
-            // the first stripe, row 0: NINF, or (NWG) alpha[0, t0+j+1] = (t0+j+1)*gap
-            if (lane < P) {
-                float rreg = kNINF;
-                if (s > 0) {
+            // lane 0's up values: lane j < P holds column t0 + j of the row above (ring
+            // slot = producer step); each step shifts the next one into lane 0 (one DPP
+            // move instead of staging them through LDS).  Above the first stripe, row 0:
+            // NINF, or (NWG) alpha[0, t0+j+1] = (t0+j+1)*gap
+            float upsh = kNINF;
+            if (s > 0) {
+                if (lane < P) {
                     int slot = slot0 + lane + 63;
                     slot = slot < R ? slot : slot - R;
-                    rreg = x_in ? rbufs[(k & 1) * 64 + lane] : ring_in[slot];
-                } else if (NWG) {
-                    rreg = (float)(t0 + lane + 1) * gap;
+                    upsh = x_in ? rbufs[(k & 1) * 64 + lane] : ring_in[slot];
                 }
-                upbuf[lane] = rreg;
-            }
-            // all P of them into registers before the steps (four 16-byte reads; a read
-            // inside the steps would wait behind the ring stores)
-            float upv[P];
-#pragma unroll
-            for (int q = 0; q < P / 4; ++q) {
-                const float4 x = reinterpret_cast<const float4*>(upbuf)[q];
-                upv[4 * q] = x.x;
-                upv[4 * q + 1] = x.y;
-                upv[4 * q + 2] = x.z;
-                upv[4 * q + 3] = x.w;
+            } else if (NWG) {
+                upsh = (float)(t0 + lane + 1) * gap;
             }
             if (k + 1 < nch) {
                 if (x_in) {
@@ -266,41 +368,22 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             // by the helper; it has written that tile's previous chunk before
             // publishing this one as loaded); WIDE: over this chunk's score tile, whose
             // scores are in registers
-            float* atile = smem + (WIDE ? wave : wave + NW / 2) * WBUF + (k & 1) * Tile::FLOATS +
-                           lane;
+            float* atile = smem + (WIDE ? wave : wave + NW / 2) * WBUF +
+                           (k & (NTB - 1)) * Tile::FLOATS + lane;
             // FULL: every cell of the chunk lies inside the element, no validity masks
             auto steps = [&](auto full) {
                 constexpr bool FULL = decltype(full)::value;
 #pragma unroll
                 for (int u = 0; u < P; ++u) {
                     const int t = t0 + u;
-                    const float up = wave_shr1_or(cur, upv[u]);   // lane 0: stripe above
+                    const float up = wave_shr1_or(cur, upsh);   // lane 0: stripe above
+                    upsh = wave_shl1(upsh);
                     const float diag = up_prev;
                     up_prev = up;
                     // out-of-table neighbours are NINF, so no i>1 / j>1 guards are needed
-                    const float vd = diag + sv[u];
-                    const float vu = up + gap;
-                    const float vl = cur + gap;
-                    // exponents (v - m) / T with the subtraction first, as the
-                    // reference: an fma against a rounded m*c would add the rounding of
-                    // m*c to alpha itself (about an ulp), which the temperature
-                    // Jacobians' (alpha - S) / T^2 terms amplify
-                    float a;
-                    if (NWG) {
-                        const float m = fmaxf(fmaxf(vd, vu), vl);
-                        const float sum = (fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c)) +
-                                          fast_exp2((vl - m) * c);
-                        a = fmaf(tl, fast_log2(sum), m);
-                    } else {
-                        // (FULL: the raw max saves the scores' canonicalisation; in
-                        // the masked form it only moves instructions)
-                        const float m = FULL ? max4_raw(vd, vu, vl, sv[u])
-                                             : fmaxf(fmaxf(vd, vu), fmaxf(vl, sv[u]));
-                        const float sum =
-                            (fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c)) +
-                            (fast_exp2((vl - m) * c) + fast_exp2((sv[u] - m) * c));
-                        a = fmaf(tl, fast_log2(sum), m);
-                    }
+                    // (FULL: the raw max saves the scores' canonicalisation; in the
+                    // masked form it only moves instructions)
+                    const float a = fwd_cell<NWG, FULL>(diag, up, cur, sv[u], gap, c, tl);
                     if (FULL) {
                         cur = a;
                     } else {
@@ -321,14 +404,17 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             };
             if (i0 + 63 < L1 && t0 >= 63 && t0 + P <= L2) steps(std::true_type{});
             else steps(std::false_type{});
+            prog_ahead(ahead, prog, HELP ? hprog : nullptr, l, NL, l);
             if (!NWG) acc.add_block_max<P>(av, bm, c);
             // the stripe's last row (lane 63) by step, contiguous, for the reverse sweep
             // of the stripe below and the next part; one store instruction
             wave_lds_sync();
-            if (lane < P) {
-                const float v = ring_out[slot0 + lane];
-                if (x_out) store_sys(brow_s + t0 + lane, v);
-                else lane_store(brow_s, (unsigned)(t0 + lane) * 4u, v);
+            if (!HELP || x_out) {
+                if (lane < P) {
+                    const float v = ring_out[slot0 + lane];
+                    if (x_out) store_sys(brow_s + t0 + lane, v);
+                    else lane_store(brow_s, (unsigned)(t0 + lane) * 4u, v);
+                }
             }
             publish(prog, wave, l * PROG_STRIDE + k + 1);
             if (x_out && k >= 2) {
@@ -385,7 +471,11 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
 // the sweeping wave's input buffer before it writes them out.
 // (one workgroup per CU: its LDS allows no second; waves_per_eu says so, so that the
 // register allocator does not spill to reach an occupancy the launch cannot have)
-template <int P, bool PRECISE = false, bool NWG = false, bool HELP = false, bool WIDE = false>
+// RECOMP (plain variant, with HELP and WIDE): the helper waves rebuild each chunk's alpha
+// rows from a checkpoint-mode forward's stored steps (ckpt_step) instead of loading
+// them from a full table.
+template <int P, bool PRECISE = false, bool NWG = false, bool HELP = false, bool WIDE = false,
+          bool RECOMP = false>
 __global__ void __launch_bounds__(WIDE ? 2 * NW * 64 : NW * 64)
 __attribute__((amdgpu_waves_per_eu(WIDE ? 4 : 1, WIDE ? 4 : 2)))
 sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
@@ -487,13 +577,134 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             // its output tiles: this wave's own buffers, or (WIDE: no LDS for those) its
             // input buffers, over the score tile it has read into registers
             float* obufs = smem + (WIDE ? q : wave) * 2 * BUF;
+            // the row above (the stripe above's last row): lane j <= P holds its alpha
+            // at step t_hi - j + 63, clamped to the last step
+            const float* hbup = brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
+            auto rowup_off = [&](int th, int ln) {
+                return (uint32_t)min(th - min(ln, P) + 63, nsteps - 1) * 4u;
+            };
             auto load = [&](int k) {
                 const int th = nsteps - 1 - k * P;
                 const uint32_t buf = lds_address(qbufs + (k & 1) * BUF);
                 dma_quads<P, -1>(buf, sbase, i0, L1max, L2max, lane, th);
                 dma_rows<P, -1>(buf + ABUF * 4, astripe, th - 2, ul4);
+                uint32_t roff = rowup_off(th, lane);
+                uint32_t rl = buf + RBUF * 4;
+                lds_dma_dword<0>(hbup, roff, rl, 0u);
             };
-            if constexpr (WIDE) {
+            if constexpr (RECOMP) {
+                static_assert(WIDE && P == PR && !NWG, "recomputing helpers: 16-wave SW sweep");
+                // Chunk k's alpha rows (steps t_lo = t_hi - P - 1 .. t_hi - 2) are rebuilt
+                // by running the forward recurrence from the stored alphas of steps
+                // t_lo - 1 and t_lo - 2, with the row above taken from the stripe above's
+                // last row (brow) and this lane's own scores; step t_lo + m goes to row m
+                // of the alpha rows, where the sweeping wave reads it as it would a loaded
+                // row.  Inputs are staged in registers two chunks ahead and the output
+                // tile lies over the input buffer, as in the loading form below; the
+                // recurrence for chunk k + 2 runs while wave q sweeps chunk k.
+                const float tl = T * kLn2;
+                const int L2eff = (i0 + lane < L1) ? L2 : 0;
+                // RW: this lane's scores of steps t_hi - P - 3 .. t_hi (its own row, as
+                // P/4 + 1 quads in memory-column order): the recurrence reads steps t_lo
+                // .. t_lo + P - 1, and the top P steps are the chunk's quad tile for
+                // the sweeping wave (quad q of the tile is quad P/4 - q here).
+                constexpr int RW = P / 4 + 1;
+                struct RStage {
+                    f32x4 row[RW];
+                    float ck0, ck1;      // alphas of steps t_lo - 1 and t_lo - 2
+                    float bb;            // lane j: the row above at step t_lo + 62 + j
+                    float rowup;         // the sweeping wave's row above (rowup_off)
+                };
+                RStage set0, set1;
+                auto stage = [&](RStage& g, int k) {
+                    const int th = nsteps - 1 - k * P, t0 = th - P - 1;
+                    int ln = lane;
+                    __asm__ volatile("" : "+v"(ln));
+                    stage_row<4 * RW>(g.row, sbase, i0, L1max, L2max, ln, th - 4 * RW + 1);
+                    // (steps below -APAD are column-0 boundary cells, set in recomp)
+                    g.ck0 = lane_load(astripe + (size_t)(max(t0 - 1, -APAD) + APAD) * 64, ul4);
+                    g.ck1 = lane_load(astripe + (size_t)(max(t0 - 2, -APAD) + APAD) * 64, ul4);
+                    g.bb = lane_load(hbup, (unsigned)min(t0 + 62 + min(ln, P), nsteps - 1) * 4u);
+                    g.rowup = lane_load(hbup, rowup_off(th, ln));
+                };
+                auto recomp = [&](const RStage& g, int k, float (&rows)[P]) {
+                    const int t0 = nsteps - 1 - k * P - P - 1;
+                    float sv[P];   // step t0 + u: element u + 2 of the staged row
+#pragma unroll
+                    for (int u = 0; u < P; ++u) sv[u] = g.row[(u + 2) / 4][(u + 2) % 4];
+                    // steps before 0 lie left of column 0: NINF, as in the table
+                    float cur = t0 - 1 >= 0 ? g.ck0 : kNINF;
+                    float bb = s > 0 ? g.bb : kNINF;
+                    // the diagonal of step t0: lane r - 1's alpha of step t0 - 2, lane 0
+                    // the row above at step t0 - 1 + 63
+                    float up_prev = wave_shr1_or(t0 - 2 >= 0 ? g.ck1 : kNINF, bb);
+                    auto run = [&](auto full) {
+                        constexpr bool FULL = decltype(full)::value;
+#pragma unroll
+                        for (int u = 0; u < P; ++u) {
+                            bb = wave_shl1(bb);   // lane 0: the row above at step t0 + u + 63
+                            const float up = wave_shr1_or(cur, bb);
+                            const float diag = up_prev;
+                            up_prev = up;
+                            const float a = fwd_cell<false, FULL>(diag, up, cur, sv[u], gap, c, tl);
+                            if (FULL) {
+                                cur = a;
+                            } else {
+                                const int col = t0 + u - lane;
+                                cur = (unsigned)col < (unsigned)L2eff ? a : kNINF;
+                            }
+                            rows[u] = cur;
+                        }
+                    };
+                    if (i0 + 63 < L1 && t0 >= 63 && t0 + P <= L2) run(std::true_type{});
+                    else run(std::false_type{});
+                };
+                auto put = [&](const RStage& g, int k, const float (&rows)[P]) {
+                    float* buf = qbufs + (k & 1) * BUF;
+#pragma unroll
+                    for (int q2 = 0; q2 < Tile::NQ; ++q2)
+                        *reinterpret_cast<f32x4*>(buf + Tile::slot(lane, q2)) = g.row[Tile::NQ - q2];
+#pragma unroll
+                    for (int u = 0; u < P; ++u) buf[ABUF + u * 64 + lane] = rows[u];
+                    buf[RBUF + lane] = g.rowup;
+                };
+                // nch >= 4: nsteps = L2 + 63
+                {
+                    float rows[P];
+                    stage(set0, 0);
+                    stage(set1, 1);
+                    recomp(set0, 0, rows);
+                    put(set0, 0, rows);
+                    publish(hprog, q, 1);
+                    stage(set0, 2);
+                    recomp(set1, 1, rows);
+                    put(set1, 1, rows);
+                    publish(hprog, q, 2);
+                    stage(set1, 3);
+                }
+                auto half = [&](RStage& g, int k) {
+                    float rows[P];
+                    const bool more = k + 2 < nch;
+                    if (more) recomp(g, k + 2, rows);
+                    int ln = lane;
+                    __asm__ volatile("" : "+v"(ln));
+                    wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
+                    write_quads<P, -1>(qbufs + (k & 1) * BUF, pbase, trash, i0, L1, L2, L1max,
+                                       L2max, ln, nsteps - 1 - k * P);
+                    if (more) {
+                        // (LDS runs this wave's reads above before these writes)
+                        put(g, k + 2, rows);
+                        publish(hprog, q, k + 3);
+                    }
+                    stage(g, min(k + 4, nch - 1));
+                };
+                int k = 0;
+                for (; k + 1 < nch; k += 2) {
+                    half(set0, k);
+                    half(set1, k + 1);
+                }
+                if (k < nch) half(set0, k);
+            } else if constexpr (WIDE) {
                 // The output tile lies over the input buffer, which can take chunk k + 2
                 // only once chunk k's marginals have left: too late for a load issued
                 // then.  So chunks 0 and 1 go straight to LDS, and every later chunk is
@@ -507,6 +718,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 struct Stage {
                     StagedQuads<P> sq;
                     f32x4 rows[P / 4];
+                    float rowup;
                 };
                 Stage set0, set1;
                 auto stage = [&](Stage& g, int k) {
@@ -515,6 +727,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     __asm__ volatile("" : "+v"(ln));
                     stage_quads<P, -1>(g.sq, sbase, i0, L1max, L2max, ln, th);
                     stage_rows<P, -1>(g.rows, astripe, th - 2, ln);
+                    g.rowup = lane_load(hbup, rowup_off(th, ln));
                 };
                 // nch >= 4: nsteps = L2 + 63
                 load(0);
@@ -540,6 +753,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                         // (LDS runs this wave's reads above before these writes)
                         put_staged_quads<P>(buf, g.sq, lane);
                         put_staged_rows<P>(buf + ABUF, g.rows, lane);
+                        buf[RBUF + lane] = g.rowup;
                         publish(hprog, q, k + 3);
                     }
                     stage(g, min(k + 4, nch - 1));
@@ -613,9 +827,11 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 dma_quads<P, -1>(buf, sbase, i0, L1max, L2max, lane, th);
                 dma_rows<P, -1>(buf + ABUF * 4, astripe, th - 2, ul4);
             }
-            uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
-            uint32_t rl = buf + RBUF * 4;
-            lds_dma_dword<0>(bup, roff, rl, 0u);
+            if (!HELP) {
+                uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
+                uint32_t rl = buf + RBUF * 4;
+                lds_dma_dword<0>(bup, roff, rl, 0u);
+            }
             if (x_in) {
                 // flows of producer slots kP+62 .. kP+62+P (float2 each): float f of the
                 // range in lane f, clamped to the last slot
@@ -636,18 +852,22 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         issue_chunk(0);
         float in_left = 0.0f, in_up = 0.0f, in_diag = 0.0f, in_diag_next = 0.0f;
         int slot0 = 0;   // ring slot of step k*P: (k*P) % R (R is a multiple of P)
+        ProgAhead ahead;   // progress words read during the previous chunk
+        prog_ahead_reset(ahead);
 
         for (int k = 0; k < nch; ++k, slot0 = slot0 + P < R ? slot0 + P : slot0 + P - R) {
             const int t_hi = nsteps - 1 - k * P;
-            chunk_waits<P>(prog, q, NL, k, nch, R, st);
+            chunk_waits_ahead<P>(ahead, prog, q, NL, k, nch, R, st);
             // this chunk's loads were issued one chunk ago and followed by at least the
             // NSTORE marginal stores of that chunk (P in a boundary chunk; the first
-            // chunk's loads are the last issued).  HELP: the helper loads the tiles; this
-            // wave's own loads (row above, flows) are followed by nothing, or by the
-            // previous chunk's flow store (x_out)
+            // chunk's loads are the last issued).  HELP: the helper loads the tiles and
+            // the row above; this wave loads only the flows from the part below (x_in),
+            // followed by nothing, or by the previous chunk's flow store (x_out)
             if constexpr (HELP) {
-                if (x_out && k > 0) wait_vmcnt<1>(); else wait_vmcnt<0>();
-                wait_for(hprog, q, k + 1, st);
+                if (x_in) {
+                    if (x_out && k > 0) wait_vmcnt<1>(); else wait_vmcnt<0>();
+                }
+                wait_for_ahead(ahead.help, hprog, q, k + 1, st);
             } else {
                 if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<NSTORE>();
             }
@@ -849,6 +1069,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 if (inits) steps(std::false_type{}, std::true_type{});
                 else steps(std::false_type{}, std::false_type{});
             }
+            prog_ahead(ahead, prog, HELP ? hprog : nullptr, q, NL, q);
 
             // the chunk's parameter-gradient terms: balanced sums, then one add each
             if (TERMS) {
@@ -903,12 +1124,18 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             bpart[((size_t)b * G + part) * 2 + 1] = (double)p;
         }
     }
-    // The last sweep of an unsplit call: every wave's stores are complete (barrier
-    // above), and the forward's status bits are visible; an element whose waits gave
-    // up gets NaN in all its outputs (the separate poison pass of split calls).
-    if (G == 1 && poison_value != nullptr &&
-        __builtin_amdgcn_readfirstlane(load_status(st)) != 0) {
+    // The last sweep of an unsplit call: an element whose waits gave up (in the forward
+    // or in this sweep) gets NaN in all its outputs (the separate poison pass of split
+    // calls).  Every wave first completes its own status atomics and stores; then one
+    // thread reads the status word and every wave branches on that one value, so the
+    // fill below runs in every wave or in none.
+    if (G == 1 && poison_value != nullptr) {
+        __shared__ int poison_flag;
+        wait_vmcnt<0>();
         __syncthreads();
+        if (threadIdx.x == 0) poison_flag = load_status(st);
+        __syncthreads();
+        if (poison_flag == 0) return;
         const float nan = __builtin_nanf("");
         for (size_t i = threadIdx.x; i < (size_t)L1max * L2max; i += blockDim.x) pbase[i] = nan;
         if (threadIdx.x == 0) {
@@ -948,8 +1175,9 @@ namespace {
 constexpr size_t kLdsLimit = 160 * 1024 - 512;
 
 // LDS of one workgroup whose stripes' boundaries use rings of R columns
-size_t lds_forward_r(int R) {
-    return (size_t)wf::NW * (2 * 64 * PF + 2 * 64 + PF) * sizeof(float) +
+// ntb: score tiles per sweeping wave (4 in the 16-wave forward)
+size_t lds_forward_r(int R, int ntb = 2) {
+    return (size_t)wf::NW * (ntb * 64 * PF + 2 * 64 + PF) * sizeof(float) +
            ((size_t)wf::NW * R + wf::NW * DUMMY) * sizeof(float);
 }
 size_t lds_backward_r(int R, int P) {
@@ -998,7 +1226,7 @@ static bool helpers_enabled() {
 template <bool NWG, bool HELP, bool WIDE = false>
 int launch_forward_k(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                      float gap, float T, const Layout& ws, float* partition, hipStream_t st,
-                     const Split& sp, int R, size_t lds, uint32_t epoch) {
+                     const Split& sp, int R, size_t lds, uint32_t epoch, bool ckpt) {
     const int ns = (max_L1 + 63) / 64;
     D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel<NWG, HELP, WIDE>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
@@ -1006,14 +1234,14 @@ int launch_forward_k(const float* scores, const int* lengths, int B, int max_L1,
                dim3(wf::split_grid(B, sp.G)), dim3((WIDE ? 2 : 1) * wf::NW * 64), lds, st, scores,
                lengths,
                ws.alpha_sk, ws.brow, partition, ws.status, ws.fflag, ws.fpart, B, max_L1, max_L2,
-               ns, gap, T, R, sp.G, sp.SPW, epoch);
+               ns, gap, T, R, sp.G, sp.SPW, epoch, ckpt ? 1 : 0);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
 
 int launch_forward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                    float gap, float T, const Layout& ws, float* partition, hipStream_t st,
-                   bool global) {
+                   bool global, bool ckpt) {
     const int ns = (max_L1 + 63) / 64;
     const Split sp = choose_split(B, max_L1, ws, max_stripes_forward(max_L1, max_L2));
     const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
@@ -1025,10 +1253,11 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
     // stripes, a second set of NW waves when it has at most NW
     const int part_stripes = sp.G > 1 ? sp.SPW : ns;
     const bool help = part_stripes <= wf::NW / 2 && helpers_enabled();
-    const bool wide = !help && part_stripes <= wf::NW && helpers_enabled();
+    const bool wide = !help && part_stripes <= wf::NW && helpers_enabled() &&
+                      lds_forward_r(R, 4) <= kLdsLimit;
 #define D2P_SW_FWD(G_, H_, W_) \
     launch_forward_k<G_, H_, W_>(scores, lengths, B, max_L1, max_L2, gap, T, ws, partition, st, \
-                                 sp, R, lds, epoch)
+                                 sp, R, W_ ? lds_forward_r(R, 4) : lds, epoch, ckpt && !global)
     if (global)
         return help ? D2P_SW_FWD(true, true, false)
                     : wide ? D2P_SW_FWD(true, true, true) : D2P_SW_FWD(true, false, false);
@@ -1042,7 +1271,8 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
     return D2P_OK;
 }
 
-template <int P, bool PRECISE, bool NWG, bool HELP = false, bool WIDE = false>
+template <int P, bool PRECISE, bool NWG, bool HELP = false, bool WIDE = false,
+          bool RECOMP = false>
 int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                       float gap, float T, const Layout& ws, const float* partition,
                       float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
@@ -1052,10 +1282,12 @@ int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
     const uint32_t epoch = next_epoch();
     if (sp.G > 1) D2P_TRY(wf::launch_flag_reset(ws.bflag, B * sp.G, st));
-    D2P_HIP(hipFuncSetAttribute((const void*)sw_backward_kernel<P, PRECISE, NWG, HELP, WIDE>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    D2P_HIP(hipFuncSetAttribute(
+        (const void*)sw_backward_kernel<P, PRECISE, NWG, HELP, WIDE, RECOMP>,
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     D2P_LAUNCH(NWG ? "nw_backward" : "sw_backward",
-               (sw_backward_kernel<P, PRECISE, NWG, HELP, WIDE>), dim3(wf::split_grid(B, sp.G)),
+               (sw_backward_kernel<P, PRECISE, NWG, HELP, WIDE, RECOMP>),
+               dim3(wf::split_grid(B, sp.G)),
                dim3((WIDE ? 2 : 1) * wf::NW * 64), lds, st, scores, lengths, ws.alpha_sk, ws.brow, partition,
                marginals, grad_gap, grad_T, ws.status, ws.trash, ws.bflag, ws.flows, ws.bpart,
                sp.G == 1 ? poison_value : nullptr, B, max_L1, max_L2, ns, gap, T, R, sp.G, sp.SPW,
@@ -1067,15 +1299,49 @@ int launch_backward_p(const float* scores, const int* lengths, int B, int max_L1
     return D2P_OK;
 }
 
+namespace {
+// The reverse sweep's launch shape: parts, and whether its helper waves run as half the
+// workgroup (parts of at most NW/2 stripes) or as a second set of NW waves.
+struct BackwardShape {
+    Split sp;
+    int rows, R, P;
+    bool help, wide;
+};
+BackwardShape backward_shape(int B, int max_L1, int max_L2, const Layout& ws, bool precise) {
+    BackwardShape bs;
+    bs.sp = choose_split(B, max_L1, ws, max_stripes_backward(max_L1, max_L2));
+    bs.rows = bs.sp.G > 1 ? bs.sp.SPW * 64 : max_L1;
+    bs.R = ring_backward(bs.rows, max_L2);
+    bs.P = backward_chunk(bs.rows, max_L2);
+    const int part_stripes = (bs.rows + 63) / 64;
+    bs.help = !precise && bs.P == 16 && part_stripes <= wf::NW / 2 && helpers_enabled();
+    bs.wide = !precise && bs.P == 16 && !bs.help && part_stripes <= wf::NW && helpers_enabled();
+    return bs;
+}
+}  // namespace
+
+// Store or recompute: whether a first-order SW call stores only the forward's checkpoint
+// rows and lets the reverse sweep rebuild alpha (only the 16-wave reverse sweep can).
+// Measured at C2 ([256, 512, 512]): the checkpoint forward takes 161 us against 168,
+// but the recomputing reverse sweep 307 us against 262 (its helper waves' recurrence
+// competes with the sweeping waves for the same SIMDs), 0.571 ms per step against
+// 0.540: the full table is the default.  D2P_AMD_SW_RECOMPUTE=1 recomputes wherever
+// the 16-wave reverse sweep runs.
+bool recompute_alpha(int B, int max_L1, int max_L2, const Layout& ws) {
+    const char* e = std::getenv("D2P_AMD_SW_RECOMPUTE");
+    if (!(e && e[0] == '1')) return false;
+    return backward_shape(B, max_L1, max_L2, ws, false).wide;
+}
+
 int launch_backward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                     float gap, float T, const Layout& ws, const float* partition,
                     float* marginals, float* grad_gap, float* grad_T, hipStream_t st,
-                    bool precise, bool global, float* poison_value, bool* poisoned) {
-    const Split sp = choose_split(B, max_L1, ws, max_stripes_backward(max_L1, max_L2));
+                    bool precise, bool global, float* poison_value, bool* poisoned,
+                    bool recompute) {
+    const BackwardShape bs = backward_shape(B, max_L1, max_L2, ws, precise);
+    const Split& sp = bs.sp;
     if (poisoned != nullptr) *poisoned = sp.G == 1 && poison_value != nullptr;
-    const int rows = sp.G > 1 ? sp.SPW * 64 : max_L1;
-    const int R = ring_backward(rows, max_L2);
-    const int P = backward_chunk(rows, max_L2);
+    const int R = bs.R, P = bs.P;
 #define D2P_SW_BWD(P_, PR_, G_)                                                               \
     launch_backward_p<P_, PR_, G_>(scores, lengths, B, max_L1, max_L2, gap, T, ws, partition, \
                                    marginals, grad_gap, grad_T, st, sp, R, poison_value)
@@ -1085,9 +1351,12 @@ int launch_backward(const float* scores, const int* lengths, int B, int max_L1, 
     }
     // helper waves move the data: the idle waves when a part has at most NW/2
     // stripes, a second set of NW waves when it has at most NW
-    const int part_stripes = (rows + 63) / 64;
-    const bool help = !precise && P == 16 && part_stripes <= wf::NW / 2 && helpers_enabled();
-    const bool wide = !precise && P == 16 && !help && part_stripes <= wf::NW && helpers_enabled();
+    const bool help = bs.help, wide = bs.wide;
+    D2P_REQUIRE(!recompute || (wide && !global), "recomputation needs the 16-wave reverse sweep");
+    if (recompute)
+        return launch_backward_p<16, false, false, true, true, true>(
+            scores, lengths, B, max_L1, max_L2, gap, T, ws, partition, marginals, grad_gap,
+            grad_T, st, sp, R, poison_value);
     if (help)
         return launch_backward_p<16, false, false, true>(scores, lengths, B, max_L1, max_L2, gap,
                                                          T, ws, partition, marginals, grad_gap,
@@ -1139,12 +1408,13 @@ extern "C" int d2p_sw_forward_marginals(const float* scores, const int* lengths,
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
     const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 1, true);
+    const bool recompute = sw::recompute_alpha(B, max_L1, max_L2, ws);
     D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
-                               partition, st));
+                               partition, st, false, recompute));
     bool poisoned = false;
     D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
                                 partition, marginals, grad_gap, grad_T, st, false, false,
-                                partition, &poisoned));
+                                partition, &poisoned, recompute));
     if (poisoned) return D2P_OK;
     return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr,
                              partition, grad_gap, grad_T, nullptr, st);
@@ -1206,12 +1476,13 @@ extern "C" int d2p_sw_forward_marginals_noalloc(const float* scores, const int* 
     // words) themselves, with kernels: the previous call's contents do not matter
     hipStream_t st = (hipStream_t)stream;
     const wf::Layout ws = wf::layout(ws_ptr, B, max_L1, max_L2, 1, true);
+    const bool recompute = sw::recompute_alpha(B, max_L1, max_L2, ws);
     D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
-                               partition, st));
+                               partition, st, false, recompute));
     bool poisoned = false;
     D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature, ws,
                                 partition, marginals, grad_gap, grad_T, st, false, false,
-                                partition, &poisoned));
+                                partition, &poisoned, recompute));
     if (poisoned) return D2P_OK;
     return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr,
                              partition, grad_gap, grad_T, nullptr, st);

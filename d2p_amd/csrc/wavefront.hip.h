@@ -360,6 +360,46 @@ __device__ __forceinline__ void chunk_waits(int* prog, int q, int NS, int k, int
     }
 }
 
+// Progress words read one chunk ahead.  A sweep issues these LDS reads right after a
+// chunk's steps, so that their latency overlaps the rest of that chunk's work; at the
+// next chunk's start, a wait whose condition the value read already meets costs a
+// compare.  The values may be stale, but progress only grows, so a condition they meet
+// holds; one they do not meet falls back to wait_for.  The reads stay in VGPRs until
+// the compare (a readfirstlane right after each read would wait for it at once).
+struct ProgAhead {
+    int prod, cons, help;   // the producer's and consumer's words, the helper's chunks
+};
+__device__ __forceinline__ int prog_peek(int* prog, int w) {
+    return __hip_atomic_load(prog + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void prog_ahead(ProgAhead& a, int* prog, int* hprog, int q, int NS,
+                                           int h) {
+    a.prod = q > 0 ? prog_peek(prog, (q - 1) % NW) : 0;
+    a.cons = q + 1 < NS ? prog_peek(prog, (q + 1) % NW) : 0;
+    a.help = hprog != nullptr ? prog_peek(hprog, h) : 0;
+}
+__device__ __forceinline__ void prog_ahead_reset(ProgAhead& a) { a.prod = a.cons = a.help = -1; }
+// wait_for(prog, w, need, ...) unless the value read ahead already shows need
+__device__ __forceinline__ void wait_for_ahead(int seen, int* prog, int w, int need,
+                                               int* status_b) {
+    if (__builtin_amdgcn_readfirstlane(seen) < need) wait_for(prog, w, need, status_b);
+}
+// chunk_waits with the producer's and consumer's words read ahead
+template <int P>
+__device__ __forceinline__ void chunk_waits_ahead(const ProgAhead& a, int* prog, int q, int NS,
+                                                  int k, int nch, int R, int* status_b) {
+    if (k == 0 && q >= NW)
+        wait_for(prog, (q + 1) % NW, (q - NW + 1) * PROG_STRIDE + nch, status_b);
+    if (q > 0)
+        wait_for_ahead(a.prod, prog, (q - 1) % NW,
+                       (q - 1) * PROG_STRIDE + min(k + lead(P), nch), status_b);
+    if (q + 1 < NS) {
+        const int need = k - 2 - R / P;   // slots of steps < kP+P-R must be consumed
+        if (need > 0)
+            wait_for_ahead(a.cons, prog, (q + 1) % NW, (q + 1) * PROG_STRIDE + need, status_b);
+    }
+}
+
 __device__ __forceinline__ int ring_index(int slot, int R) {
     slot %= R;
     return slot < 0 ? slot + R : slot;
@@ -763,6 +803,31 @@ __device__ __forceinline__ void put_staged_quads(float* tile, const StagedQuads<
     } else {
 #pragma unroll
         for (int j = 0; j < P; ++j) tile[64 * j + lane] = sq.q[j / 4][j % 4];
+    }
+}
+
+// Register staging of P consecutive steps of the lane's own row (row i0 + lane) of a
+// row-major [L1max][L2max] matrix: step t_first + j is column t_first + j - lane.  A
+// chunk inside the matrix takes P/4 16-byte loads per lane (4-byte aligned), one at a
+// boundary P dword loads from clamped addresses (the sweeps mask those cells).
+template <int P>
+__device__ __forceinline__ void stage_row(f32x4 (&v)[P / 4], const float* mbase, int i0,
+                                          int L1max, int L2max, int lane, int t_first) {
+    const float* sbase = stripe_row(mbase, i0, L2max);
+    if (i0 + 63 < L1max && t_first - 63 >= 0 && t_first + P - 1 < L2max) {
+        const char* cbase = reinterpret_cast<const char*>(sbase);
+        // (the offset spans at most 64 rows)
+        const uint32_t off = (uint32_t)(lane * (L2max - 1) + t_first) * 4u;
+#pragma unroll
+        for (int i = 0; i < P / 4; ++i)
+            v[i] = *reinterpret_cast<const f32x4*>(cbase + off + 16u * (uint32_t)i);
+    } else {
+        const int r = min(i0 + lane, L1max - 1) - i0;
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            const int col = min(max(t_first + j - lane, 0), L2max - 1);
+            v[j / 4][j % 4] = sbase[(uint32_t)(r * L2max + col)];
+        }
     }
 }
 
