@@ -583,6 +583,13 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             auto rowup_off = [&](int th, int ln) {
                 return (uint32_t)min(th - min(ln, P) + 63, nsteps - 1) * 4u;
             };
+            // 16-wave form: whole 64-byte row segments of marginals where rows start
+            // aligned (write_quads_aligned), else the chunk's own row segments (also in
+            // the recomputing form, whose registers hold the recurrence instead)
+            const bool aligned = WIDE && !RECOMP && P == 16 && (L2max & 15) == 0;
+            AlignedCarry carry;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) carry.v[i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
             auto load = [&](int k) {
                 const int th = nsteps - 1 - k * P;
                 const uint32_t buf = lds_address(qbufs + (k & 1) * BUF);
@@ -747,8 +754,12 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     int ln = lane;
                     __asm__ volatile("" : "+v"(ln));
                     wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
-                    write_quads<P, -1>(buf, pbase, trash, i0, L1, L2, L1max, L2max, ln,
-                                       nsteps - 1 - k * P);
+                    if (aligned)
+                        write_quads_aligned(buf, pbase, trash, carry, i0, L1max, L2max, ln,
+                                            nsteps - 1 - k * P);
+                    else
+                        write_quads<P, -1>(buf, pbase, trash, i0, L1, L2, L1max, L2max, ln,
+                                           nsteps - 1 - k * P);
                     if (k + 2 < nch) {
                         // (LDS runs this wave's reads above before these writes)
                         put_staged_quads<P>(buf, g.sq, lane);

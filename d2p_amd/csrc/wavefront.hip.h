@@ -755,6 +755,45 @@ __device__ __forceinline__ void write_quads(const float* tile, float* obase, flo
     }
 }
 
+// Aligned write-out of a reverse sweep's 16-step output quad tiles, for matrices whose
+// rows start 64-byte aligned (L2max % 16 == 0).  Chunk t_hi of row r covers columns
+// c - 15 .. c (c = t_hi - r); the row's aligned 64-byte segment [a, a + 15], a = c & ~15,
+// takes its columns <= c from this chunk's tile and the others from the previous
+// chunk's, which the caller keeps in `carry` from the previous call (zeros before a
+// stripe's first chunk: those columns lie past the element).  Each row therefore gets
+// exactly one whole segment per chunk, and the stripe's chunks cover every segment of
+// the row.  Lane l moves quarter l % 4 of the segments of rows 16 i + l / 4, one
+// 16-byte store each (P/4 stores, as write_quads); a segment outside the matrix goes to
+// the trash line.  Cells outside the element hold 0 in the tiles.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+struct AlignedCarry {
+    f32x4 v[4];
+};
+__device__ __forceinline__ void write_quads_aligned(const float* tile, float* obase, float* trash,
+                                                    AlignedCarry& cy, int i0, int L1max,
+                                                    int L2max, int lane, int t_hi) {
+    using Q = QuadTile<16>;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 16 * i + (lane >> 2), p = lane & 3;
+        const int c = t_hi - r;
+        const int a = c & ~15;
+        const int u0 = (c & 15) - 4 * p;   // element e is step u0 - e of this chunk
+        f32x4 out;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int u1 = u0 - e;          // < 0: the previous chunk's step u1 + 16
+            const int u = u1 & 15;
+            const float rd = tile[Q::slot(r, u >> 2) + 3 - (u & 3)];
+            out[e] = u1 >= 0 ? rd : cy.v[i][e];
+            cy.v[i][e] = rd;                // the next segment's share of this chunk
+        }
+        const bool in = a >= 0 && a + 15 < L2max && i0 + r < L1max;
+        float* dst = in ? obase + (size_t)(i0 + r) * L2max + a + 4 * p : trash + 4 * (lane & 15);
+        *reinterpret_cast<f32x4*>(dst) = out;
+    }
+}
+
 // Register staging of a chunk's quad tile, for helper waves that load further ahead
 // than their LDS buffers allow: stage_quads issues the loads dma_quads would issue,
 // into the lane's registers (P/4 16-byte loads inside, P dword loads at a boundary),
@@ -762,7 +801,6 @@ __device__ __forceinline__ void write_quads(const float* tile, float* obase, flo
 // tracks these loads itself and waits for them before the LDS writes.  The quads are
 // held as vectors: as scalars, the compiler would split each 16-byte load into four
 // and merge them with the boundary form's loads.
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 template <int P>
 struct StagedQuads {
     f32x4 q[P / 4];

@@ -76,13 +76,16 @@ def test_sw_split_ragged(cuda, parts):
 
 @pytest.mark.parametrize("B,L1,L2,n", [(2, 700, 260, 4), (3, 200, 300, 1), (1, 1500, 90, 8),
                                        (4, 64, 64, 1), (3, 512, 300, 1), (2, 330, 200, 1),
-                                       (2, 1500, 90, 3)])
+                                       (2, 1500, 90, 3), (3, 512, 512, 1), (2, 330, 208, 1),
+                                       (3, 400, 64, 1), (2, 1500, 96, 3)])
 def test_sw_helper_waves_bit_identical(cuda, parts, monkeypatch, B, L1, L2, n):
     """Parts hand their data movement (tile loads, the alpha table and marginal
     write-outs) to helper waves in the forward and reverse sweeps: the idle waves of the
     workgroup for parts of at most four stripes (also in the second-order reverse
     sweep), a second set of eight waves for parts of five to eight (the last three
-    cases).  The arithmetic is unchanged, so every output equals the single-wave form
+    cases; those whose rows start 64-byte aligned, L2 a multiple of 16, also write the
+    marginals as whole aligned row segments).  The arithmetic is unchanged, so every
+    output equals the single-wave form
     bit for bit: SW and NW first order, the SW and NW HVPs, the SW parameter
     Jacobians, the marginal-path backward and affine SW first order, ragged lengths
     and split parts included."""
