@@ -593,6 +593,11 @@ dtw_backward_kernel(const int* __restrict__ lengths,
                 dma_rows<P, -1>(lds_address(qbufs + (k & 1) * BUF) + ABUF * 4, astripe, th - 2,
                                 ul4);
             };
+            // whole row segments of marginals where rows start aligned (write_aligned):
+            // P/4 stores per chunk instead of P
+            const bool aligned = (L2max & (P - 1)) == 0;
+            AlignedCarry<P> carry;
+            carry.clear();
             if (nch > 0) {
                 load(0);
                 wait_vmcnt<0>();
@@ -602,16 +607,22 @@ dtw_backward_kernel(const int* __restrict__ lengths,
             for (int k = 0; k < nch; ++k) {
                 if (k + 1 < nch) {
                     // chunk k + 1's loads: the last issued at k = 0, else followed by the
-                    // P marginal stores of chunk k - 1
-                    if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+                    // marginal stores of chunk k - 1 (P, or P/4 aligned ones)
+                    if (k == 0) wait_vmcnt<0>();
+                    else if (aligned) wait_vmcnt<P / 4>();
+                    else wait_vmcnt<P>();
                     publish(hprog, q, k + 2);   // also completes this wave's LDS reads
                 }
                 // once wave q has finished chunk k, its buffer k & 1 takes chunk k + 2
                 // and its marginals (in output tile k & 1) leave
                 wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
                 if (k + 2 < nch) load(k + 2);
-                write_tile<P, -1>(obufs + (k & 1) * BUF, pbase, trash, i0, L1, L2, L1max,
-                                  L2max, lane, nsteps - 1 - k * P);
+                if (aligned)
+                    write_aligned<P, false>(obufs + (k & 1) * BUF, pbase, trash, carry, i0,
+                                            L1max, L2max, lane, nsteps - 1 - k * P);
+                else
+                    write_tile<P, -1>(obufs + (k & 1) * BUF, pbase, trash, i0, L1, L2, L1max,
+                                      L2max, lane, nsteps - 1 - k * P);
             }
         }
     }

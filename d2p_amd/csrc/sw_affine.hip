@@ -529,6 +529,10 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                     dma_rows<P, -1>(in + (AROWS + pl * P * 64) * 4, astripe + pl * PLANE, th - 2,
                                     ul4);
             };
+            // whole row segments of marginals where rows start aligned (write_aligned)
+            const bool aligned = (L2max & (P - 1)) == 0;
+            AlignedCarry<P> carry;
+            carry.clear();
             if (nch > 0) {
                 load(0);
                 wait_vmcnt<0>();
@@ -545,8 +549,12 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 // buffer takes chunk k + 2 (the stores have read the tile: their data
                 // dependence waits for the reads)
                 wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
-                write_quads<P, -1>(cbuf(k) + OTILE, pbase, trash, i0, L1, L2, L1max, L2max, lane,
-                                   nsteps - 1 - k * P);
+                if (aligned)
+                    write_aligned<P, true>(cbuf(k) + OTILE, pbase, trash, carry, i0, L1max,
+                                           L2max, lane, nsteps - 1 - k * P);
+                else
+                    write_quads<P, -1>(cbuf(k) + OTILE, pbase, trash, i0, L1, L2, L1max, L2max,
+                                       lane, nsteps - 1 - k * P);
                 if (k + 2 < nch) load(k + 2);
             }
         }

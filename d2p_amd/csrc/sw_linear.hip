@@ -583,13 +583,12 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             auto rowup_off = [&](int th, int ln) {
                 return (uint32_t)min(th - min(ln, P) + 63, nsteps - 1) * 4u;
             };
-            // 16-wave form: whole 64-byte row segments of marginals where rows start
-            // aligned (write_quads_aligned), else the chunk's own row segments (also in
-            // the recomputing form, whose registers hold the recurrence instead)
-            const bool aligned = WIDE && !RECOMP && P == 16 && (L2max & 15) == 0;
-            AlignedCarry carry;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) carry.v[i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+            // whole 64-byte row segments of marginals where rows start aligned
+            // (write_aligned), else the chunk's own row segments (also in the
+            // recomputing form, whose registers hold the recurrence instead)
+            const bool aligned = !RECOMP && (L2max & (P - 1)) == 0;
+            AlignedCarry<P> carry;
+            carry.clear();
             auto load = [&](int k) {
                 const int th = nsteps - 1 - k * P;
                 const uint32_t buf = lds_address(qbufs + (k & 1) * BUF);
@@ -755,8 +754,8 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     __asm__ volatile("" : "+v"(ln));
                     wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
                     if (aligned)
-                        write_quads_aligned(buf, pbase, trash, carry, i0, L1max, L2max, ln,
-                                            nsteps - 1 - k * P);
+                        write_aligned<P, true>(buf, pbase, trash, carry, i0, L1max, L2max, ln,
+                                               nsteps - 1 - k * P);
                     else
                         write_quads<P, -1>(buf, pbase, trash, i0, L1, L2, L1max, L2max, ln,
                                            nsteps - 1 - k * P);
@@ -793,8 +792,12 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     // chunk k + 2 and its marginals (in output tile k & 1) leave
                     wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
                     if (k + 2 < nch) load(k + 2);
-                    write_quads<P, -1>(obufs + (k & 1) * BUF, pbase, trash, i0, L1, L2, L1max,
-                                       L2max, lane, nsteps - 1 - k * P);
+                    if (aligned)
+                        write_aligned<P, true>(obufs + (k & 1) * BUF, pbase, trash, carry, i0,
+                                               L1max, L2max, lane, nsteps - 1 - k * P);
+                    else
+                        write_quads<P, -1>(obufs + (k & 1) * BUF, pbase, trash, i0, L1, L2,
+                                           L1max, L2max, lane, nsteps - 1 - k * P);
                 }
             }
         }

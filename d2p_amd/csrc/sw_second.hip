@@ -488,6 +488,10 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 dma_rows<P, -1>(in + AR * 4, astripe, th - 2, ul4);
                 dma_rows<P, -1>(in + XR * 4, xstripe, th - 2, ul4);
             };
+            // whole row segments of the output where rows start aligned (write_aligned)
+            const bool aligned = (L2max & (P - 1)) == 0;
+            AlignedCarry<P> carry;
+            carry.clear();
             if (nch > 0) {
                 load(0);
                 wait_vmcnt<0>();
@@ -504,8 +508,12 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 // buffer takes chunk k + 2 (the stores have read the tile: their data
                 // dependence waits for the reads)
                 wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
-                write_quads<P, -1>(cbuf(k) + OT, obase, trash, i0, L1, L2, L1max, L2max, lane,
-                                   nsteps - 1 - k * P);
+                if (aligned)
+                    write_aligned<P, true>(cbuf(k) + OT, obase, trash, carry, i0, L1max, L2max,
+                                           lane, nsteps - 1 - k * P);
+                else
+                    write_quads<P, -1>(cbuf(k) + OT, obase, trash, i0, L1, L2, L1max, L2max,
+                                       lane, nsteps - 1 - k * P);
                 if (k + 2 < nch) load(k + 2);
             }
         }

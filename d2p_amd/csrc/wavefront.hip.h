@@ -755,40 +755,50 @@ __device__ __forceinline__ void write_quads(const float* tile, float* obase, flo
     }
 }
 
-// Aligned write-out of a reverse sweep's 16-step output quad tiles, for matrices whose
-// rows start 64-byte aligned (L2max % 16 == 0).  Chunk t_hi of row r covers columns
-// c - 15 .. c (c = t_hi - r); the row's aligned 64-byte segment [a, a + 15], a = c & ~15,
-// takes its columns <= c from this chunk's tile and the others from the previous
-// chunk's, which the caller keeps in `carry` from the previous call (zeros before a
-// stripe's first chunk: those columns lie past the element).  Each row therefore gets
-// exactly one whole segment per chunk, and the stripe's chunks cover every segment of
-// the row.  Lane l moves quarter l % 4 of the segments of rows 16 i + l / 4, one
-// 16-byte store each (P/4 stores, as write_quads); a segment outside the matrix goes to
-// the trash line.  Cells outside the element hold 0 in the tiles.
+// Aligned write-out of a reverse sweep's output tiles of P = 8 or 16 steps (quad tiles,
+// QUAD, or dword chunk tiles), for matrices whose rows start P-float aligned (L2max %
+// P == 0; a P-float segment is then two or one whole 32-byte sectors).  Chunk t_hi of
+// row r covers columns c - (P - 1) .. c (c = t_hi - r); the row's aligned segment
+// [a, a + P - 1], a = c & ~(P - 1), takes its columns <= c from this chunk's tile and the
+// others from the previous chunk's, which the caller keeps in `carry` from the previous
+// call (zeros before a stripe's first chunk: those columns lie past the element).  Each
+// row therefore gets exactly one whole segment per chunk, and a stripe's chunks cover
+// every segment of its rows.  Lane l moves quarter l % (P/4) of the segments of rows
+// (64/(P/4)) i + l / (P/4), one 16-byte store each (P/4 stores, as write_quads); a
+// segment outside the matrix goes to the trash line.  Cells outside the element must
+// hold 0 in the tiles.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+template <int P>
 struct AlignedCarry {
-    f32x4 v[4];
-};
-__device__ __forceinline__ void write_quads_aligned(const float* tile, float* obase, float* trash,
-                                                    AlignedCarry& cy, int i0, int L1max,
-                                                    int L2max, int lane, int t_hi) {
-    using Q = QuadTile<16>;
+    f32x4 v[P / 4];
+    __device__ void clear() {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = 16 * i + (lane >> 2), p = lane & 3;
+        for (int i = 0; i < P / 4; ++i) v[i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    }
+};
+template <int P, bool QUAD>
+__device__ __forceinline__ void write_aligned(const float* tile, float* obase, float* trash,
+                                              AlignedCarry<P>& cy, int i0, int L1max, int L2max,
+                                              int lane, int t_hi) {
+    static_assert(P == 8 || P == 16, "aligned write-out of 8- or 16-step tiles");
+    constexpr int NQ = P / 4, RPI = 64 / NQ;   // slots per lane, rows per instruction
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+        const int r = RPI * i + lane / NQ, p = lane % NQ;
         const int c = t_hi - r;
-        const int a = c & ~15;
-        const int u0 = (c & 15) - 4 * p;   // element e is step u0 - e of this chunk
+        const int a = c & ~(P - 1);
+        const int u0 = (c & (P - 1)) - 4 * p;   // element e is step u0 - e of this chunk
         f32x4 out;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int u1 = u0 - e;          // < 0: the previous chunk's step u1 + 16
-            const int u = u1 & 15;
-            const float rd = tile[Q::slot(r, u >> 2) + 3 - (u & 3)];
+            const int u1 = u0 - e;               // < 0: the previous chunk's step u1 + P
+            const int u = u1 & (P - 1);
+            const float rd = QUAD ? tile[QuadTile<P>::slot(r, u >> 2) + 3 - (u & 3)]
+                                  : tile[65 * (r % P) + P * (r / P) + u];
             out[e] = u1 >= 0 ? rd : cy.v[i][e];
-            cy.v[i][e] = rd;                // the next segment's share of this chunk
+            cy.v[i][e] = rd;                     // the next segment's share of this chunk
         }
-        const bool in = a >= 0 && a + 15 < L2max && i0 + r < L1max;
+        const bool in = a >= 0 && a + P - 1 < L2max && i0 + r < L1max;
         float* dst = in ? obase + (size_t)(i0 + r) * L2max + a + 4 * p : trash + 4 * (lane & 15);
         *reinterpret_cast<f32x4*>(dst) = out;
     }
