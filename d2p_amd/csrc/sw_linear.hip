@@ -584,9 +584,9 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 return (uint32_t)min(th - min(ln, P) + 63, nsteps - 1) * 4u;
             };
             // whole 64-byte row segments of marginals where rows start aligned
-            // (write_aligned), else the chunk's own row segments (also in the
+            // (write_aligned), else the chunk's own row segments (also in the 16-wave
             // recomputing form, whose registers hold the recurrence instead)
-            const bool aligned = !RECOMP && (L2max & (P - 1)) == 0;
+            const bool aligned = !(RECOMP && WIDE) && (L2max & (P - 1)) == 0;
             AlignedCarry<P> carry;
             carry.clear();
             auto load = [&](int k) {
@@ -599,15 +599,16 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 lds_dma_dword<0>(hbup, roff, rl, 0u);
             };
             if constexpr (RECOMP) {
-                static_assert(WIDE && P == PR && !NWG, "recomputing helpers: 16-wave SW sweep");
+                static_assert(HELP && P == PR && !NWG, "recomputing helpers: 16-step SW sweep");
                 // Chunk k's alpha rows (steps t_lo = t_hi - P - 1 .. t_hi - 2) are rebuilt
                 // by running the forward recurrence from the stored alphas of steps
                 // t_lo - 1 and t_lo - 2, with the row above taken from the stripe above's
                 // last row (brow) and this lane's own scores; step t_lo + m goes to row m
                 // of the alpha rows, where the sweeping wave reads it as it would a loaded
-                // row.  Inputs are staged in registers two chunks ahead and the output
-                // tile lies over the input buffer, as in the loading form below; the
-                // recurrence for chunk k + 2 runs while wave q sweeps chunk k.
+                // row.  Inputs are staged in registers two chunks ahead (the output tile
+                // lies over the input buffer in the 16-wave form, in this wave's own
+                // buffers otherwise); the recurrence for chunk k + 2 runs while wave q
+                // sweeps chunk k.
                 const float tl = T * kLn2;
                 const int L2eff = (i0 + lane < L1) ? L2 : 0;
                 // RW: this lane's scores of steps t_hi - P - 3 .. t_hi (its own row, as
@@ -695,8 +696,12 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     int ln = lane;
                     __asm__ volatile("" : "+v"(ln));
                     wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
-                    write_quads<P, -1>(qbufs + (k & 1) * BUF, pbase, trash, i0, L1, L2, L1max,
-                                       L2max, ln, nsteps - 1 - k * P);
+                    if (aligned)
+                        write_aligned<P, true>(obufs + (k & 1) * BUF, pbase, trash, carry, i0,
+                                               L1max, L2max, ln, nsteps - 1 - k * P);
+                    else
+                        write_quads<P, -1>(obufs + (k & 1) * BUF, pbase, trash, i0, L1, L2,
+                                           L1max, L2max, ln, nsteps - 1 - k * P);
                     if (more) {
                         // (LDS runs this wave's reads above before these writes)
                         put(g, k + 2, rows);
@@ -1344,7 +1349,8 @@ BackwardShape backward_shape(int B, int max_L1, int max_L2, const Layout& ws, bo
 bool recompute_alpha(int B, int max_L1, int max_L2, const Layout& ws) {
     const char* e = std::getenv("D2P_AMD_SW_RECOMPUTE");
     if (!(e && e[0] == '1')) return false;
-    return backward_shape(B, max_L1, max_L2, ws, false).wide;
+    const BackwardShape bs = backward_shape(B, max_L1, max_L2, ws, false);
+    return bs.wide || bs.help;
 }
 
 int launch_backward(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
@@ -1366,9 +1372,14 @@ int launch_backward(const float* scores, const int* lengths, int B, int max_L1, 
     // helper waves move the data: the idle waves when a part has at most NW/2
     // stripes, a second set of NW waves when it has at most NW
     const bool help = bs.help, wide = bs.wide;
-    D2P_REQUIRE(!recompute || (wide && !global), "recomputation needs the 16-wave reverse sweep");
-    if (recompute)
+    D2P_REQUIRE(!recompute || ((wide || help) && !global),
+                "recomputation needs a reverse sweep with helper waves");
+    if (recompute && wide)
         return launch_backward_p<16, false, false, true, true, true>(
+            scores, lengths, B, max_L1, max_L2, gap, T, ws, partition, marginals, grad_gap,
+            grad_T, st, sp, R, poison_value);
+    if (recompute)
+        return launch_backward_p<16, false, false, true, false, true>(
             scores, lengths, B, max_L1, max_L2, gap, T, ws, partition, marginals, grad_gap,
             grad_T, st, sp, R, poison_value);
     if (help)

@@ -1,6 +1,7 @@
-"""Store or recompute: first-order linear-gap SW calls whose reverse sweep runs in
-16-wave workgroups (parts of five to eight stripes, C2's 512-row elements) store only
-the forward's checkpoint rows (two steps per 16-step chunk and the last two steps)
+"""Store or recompute: first-order linear-gap SW calls whose reverse sweep runs with
+helper waves (16-wave workgroups for parts of five to eight stripes, C2's 512-row
+elements; half-workgroup helpers for parts of at most four, C5's split parts) can
+store only the forward's checkpoint rows (two steps per 16-step chunk and the last two steps)
 and rebuild every other alpha row in the reverse sweep's helper waves, from those
 rows, the stripe above's last row and the scores.  The rebuilt rows must equal the
 stored ones, so every output equals the full-table form
@@ -40,6 +41,11 @@ CASES = [
     (64, 2, 320, 257, 1, True),     # five stripes, a last stripe of full height
     (65, 1, 1500, 90, 3, False),    # three parts of eight stripes
     (66, 9, 450, 33, 1, True),      # B not a multiple of 8, ragged
+    # parts of at most four stripes (half-workgroup helpers)
+    (70, 3, 256, 300, 1, False),    # four stripes, unsplit
+    (71, 2, 1024, 512, 4, True),    # four parts of four stripes, ragged
+    (72, 1, 2048, 640, 0, False),   # automatic split
+    (73, 5, 200, 96, 1, True),      # aligned rows, ragged, four stripes
 ]
 
 
