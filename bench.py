@@ -129,9 +129,10 @@ def make_c5(hvp=False):
     if hvp:
         return dict(
             name="c5hvp", inputs={"scores": scores, "V": V}, cells=cells, algo_step=12 * cells,
-            # read scores + V, write H
-            algo_kernel={"sw_forward": 4 * cells, "sw_tangent": 4 * cells,
-                         "sw_dual": 4 * cells},
+            # read scores + V (the fused forward and tangent sweep), write H (the dual
+            # sweep); the unfused form (D2P_AMD_SW_FUSED_TANGENT=0) reads V in sw_tangent
+            algo_kernel={"sw_forward_tangent": 8 * cells, "sw_dual": 4 * cells,
+                         "sw_forward": 4 * cells, "sw_tangent": 4 * cells},
             workload="C5 HVP: soft_sw_hvp(scores, V, -1, 1) on [16,4096,4096]",
             extra={"B": B, "L1": L, "L2": L})
     return dict(

@@ -143,6 +143,37 @@ struct OnlineLSE {
     }
 };
 
+// OnlineLSE that also carries w = sum_i 2^((x_i - m) c) y_i for a companion value y_i
+// of each x_i: w / z is then the softmax-weighted mean of the y_i (the value's
+// tangent from the cells' tangents, with the partition's own weights).
+struct OnlineLSEDot {
+    float m, z, w;
+    __device__ __forceinline__ void init_open() { m = -3.0e38f; z = 0.0f; w = 0.0f; }
+    template <int N>
+    __device__ __forceinline__ void add_block_max(const float* x, const float* y, float bmax,
+                                                  float c) {
+        const float M = fmaxf(m, bmax);
+        const float r = fast_exp2((m - M) * c);
+        float e[N], ey[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            e[i] = fast_exp2((x[i] - M) * c);
+            ey[i] = e[i] * y[i];
+        }
+        z = fmaf(z, r, tree_sum<N>(e));
+        w = fmaf(w, r, tree_sum<N>(ey));
+        m = M;
+    }
+    __device__ __forceinline__ void merge(float m2, float z2, float w2, float c) {
+        const float M = fmaxf(m, m2);
+        const float ra = (m <= kNINF) ? 0.0f : fast_exp2((m - M) * c);
+        const float rb = (m2 <= kNINF) ? 0.0f : fast_exp2((m2 - M) * c);
+        m = M;
+        z = z * ra + z2 * rb;
+        w = w * ra + w2 * rb;
+    }
+};
+
 template <typename Op>
 __device__ __forceinline__ float wave_reduce(float v, Op op) {
 #pragma unroll
@@ -165,6 +196,15 @@ __device__ __forceinline__ void wave_merge_lse(OnlineLSE& s, float c) {
         float m2 = __shfl_xor(s.m, off, 64);
         float z2 = __shfl_xor(s.z, off, 64);
         s.merge(m2, z2, c);
+    }
+}
+__device__ __forceinline__ void wave_merge_lse(OnlineLSEDot& s, float c) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        float m2 = __shfl_xor(s.m, off, 64);
+        float z2 = __shfl_xor(s.z, off, 64);
+        float w2 = __shfl_xor(s.w, off, 64);
+        s.merge(m2, z2, w2, c);
     }
 }
 

@@ -45,6 +45,25 @@ __global__ void partition_merge_kernel(const float2* __restrict__ fpart,
     partition[b] = tot.m + T * kLn2 * fast_log2(tot.z);
 }
 
+__global__ void partition_dot_merge_kernel(const float2* __restrict__ fpart,
+                                           const float* __restrict__ wpart,
+                                           float* __restrict__ partition,
+                                           float* __restrict__ sdot, int B, int G, float T) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    const float c = kLog2e / T;
+    OnlineLSEDot tot;
+    tot.m = 0.0f;
+    tot.z = 1.0f;
+    tot.w = 0.0f;
+    for (int g = 0; g < G; ++g) {
+        const float2 v = fpart[(size_t)b * G + g];
+        tot.merge(v.x, v.y, wpart[(size_t)b * G + g], c);
+    }
+    partition[b] = tot.m + T * kLn2 * fast_log2(tot.z);
+    sdot[b] = tot.w / tot.z;
+}
+
 // Sum of the parts' partial results of a split element.
 __global__ void sum_parts_kernel(const float* __restrict__ spart, float* __restrict__ out, int B,
                                  int G) {
@@ -149,6 +168,14 @@ int launch_partition_merge(const Layout& ws, float* partition, int B, int G, flo
                            hipStream_t st) {
     D2P_LAUNCH("partition_merge", partition_merge_kernel, dim3((B + 255) / 256), dim3(256), 0,
                st, ws.fpart, partition, B, G, T);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
+int launch_partition_dot_merge(const Layout& ws, const float* wpart, float* partition,
+                               float* sdot, int B, int G, float T, hipStream_t st) {
+    D2P_LAUNCH("partition_merge", partition_dot_merge_kernel, dim3((B + 255) / 256), dim3(256),
+               0, st, ws.fpart, wpart, partition, sdot, B, G, T);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }

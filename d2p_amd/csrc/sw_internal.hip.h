@@ -26,6 +26,15 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
                    float gap, float T, const Layout& ws, float* partition, hipStream_t st,
                    bool global = false, bool ckpt = false);
 
+// The forward sweep and the HVP's forward tangent sweep along V in one pass: the
+// alpha table, last rows and partition as launch_forward, the tangent table and its
+// last rows, and sdot[B], the value's tangent.  wpart: [B][parts] scratch for split
+// elements (at least B * stripes floats).
+int launch_forward_tangent(const float* scores, const float* V, const int* lengths, int B,
+                           int max_L1, int max_L2, float gap, float T, const Layout& ws,
+                           float* partition, float* tan_sk, float* tan_brow, float* sdot,
+                           float* wpart, hipStream_t st, bool global = false);
+
 // Whether a first-order call recomputes alpha in its reverse sweep (and so runs the
 // forward in checkpoint mode).
 bool recompute_alpha(int B, int max_L1, int max_L2, const Layout& ws);

@@ -43,8 +43,8 @@ constexpr int PR = 16;               // steps per chunk of the reverse sweeps th
 // produce the same bits.  RAWMAX: the max without canonicalising the score (the same
 // value for every non-NaN input).
 template <bool NWG, bool RAWMAX>
-__device__ __forceinline__ float fwd_cell(float diag, float up, float cur, float sc, float gap,
-                                          float c, float tl) {
+__device__ __forceinline__ float fwd_cell_e(float diag, float up, float cur, float sc, float gap,
+                                            float c, float tl, float (&e)[4], float& sum) {
     // out-of-table neighbours are NINF, so no i>1 / j>1 guards are needed
     const float vd = diag + sc;
     const float vu = up + gap;
@@ -54,15 +54,41 @@ __device__ __forceinline__ float fwd_cell(float diag, float up, float cur, float
     // ulp), which the temperature Jacobians' (alpha - S) / T^2 terms amplify
     if (NWG) {
         const float m = fmaxf(fmaxf(vd, vu), vl);
-        const float sum = (fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c)) +
-                          fast_exp2((vl - m) * c);
+        e[0] = fast_exp2((vd - m) * c);
+        e[1] = fast_exp2((vu - m) * c);
+        e[2] = fast_exp2((vl - m) * c);
+        e[3] = 0.0f;
+        sum = (e[0] + e[1]) + e[2];
         return fmaf(tl, fast_log2(sum), m);
     } else {
         const float m = RAWMAX ? max4_raw(vd, vu, vl, sc) : fmaxf(fmaxf(vd, vu), fmaxf(vl, sc));
-        const float sum = (fast_exp2((vd - m) * c) + fast_exp2((vu - m) * c)) +
-                          (fast_exp2((vl - m) * c) + fast_exp2((sc - m) * c));
+        e[0] = fast_exp2((vd - m) * c);
+        e[1] = fast_exp2((vu - m) * c);
+        e[2] = fast_exp2((vl - m) * c);
+        e[3] = fast_exp2((sc - m) * c);
+        sum = (e[0] + e[1]) + (e[2] + e[3]);
         return fmaf(tl, fast_log2(sum), m);
     }
+}
+template <bool NWG, bool RAWMAX>
+__device__ __forceinline__ float fwd_cell(float diag, float up, float cur, float sc, float gap,
+                                          float c, float tl) {
+    float e[4], sum;
+    return fwd_cell_e<NWG, RAWMAX>(diag, up, cur, sc, gap, c, tl, e, sum);
+}
+// fwd_cell and the cell's tangent x along a direction v (the HVP's forward tangent,
+// /root/reference/src/sw/kernels_cpu.cpp:279-477): the candidates' tangents
+// (x_diag + v, x_up, x_left, v) weighted by the softmax weights of the same exponentials.
+template <bool NWG, bool RAWMAX>
+__device__ __forceinline__ float fwd_cell_tan(float diag, float up, float cur, float sc,
+                                              float gap, float c, float tl, float td, float tu,
+                                              float tc, float v, float& x) {
+    float e[4], sum;
+    const float a = fwd_cell_e<NWG, RAWMAX>(diag, up, cur, sc, gap, c, tl, e, sum);
+    const float num = NWG ? (e[0] * (td + v) + e[1] * tu) + e[2] * tc
+                          : ((e[0] * (td + v) + e[1] * tu) + e[2] * tc) + e[3] * v;
+    x = num * fast_rcp(sum);
+    return a;
 }
 
 // Checkpoint steps of a stripe of nsteps steps for reverse sweeps of PR-step chunks that
@@ -93,21 +119,40 @@ __device__ __forceinline__ bool ckpt_step(int t, int nsteps) {
 // (publishing hprog[l] = chunks loaded), and writes a chunk's alpha rows (which the
 // sweeping wave leaves in the helper's own, otherwise unused, tile buffers) to the
 // table as one contiguous 4 KB block once wave l has finished the chunk (prog[l]).
-template <bool NWG = false, bool HELP = false, bool WIDE = false>
+//
+// TAN (not WIDE): the HVP's forward tangent sweep in the same pass
+// (/root/reference/src/sw/kernels_cpu.cpp:279-477): each cell also takes its tangent
+// along the direction V from the forward's own softmax weights (fwd_cell_tan), writes
+// it to tan_sk / tan_brow as the tangent sweep does, passes it across stripes through a
+// second ring, and folds it into the value's tangent dS = sum_cells p_cell x_cell with
+// the partition's own weights (OnlineLSEDot: no second pass for the cell
+// probabilities, which need S).  G > 1 writes the part's sum beside its (max, sum).
+// The direction's quads come with the scores (a second tile per chunk), the tangent
+// rows leave with the alpha rows (a second tile in the helper's buffer).
+struct TanArgs {
+    const float* V;
+    float* tan_sk;
+    float* tan_brow;
+    float* sdot;      // [B]: the value's tangent (G == 1)
+    float* wpart;     // [B][G]: a part's tangent sum at its (max, sum) scale (G > 1)
+};
+template <bool NWG = false, bool HELP = false, bool WIDE = false, bool TAN = false>
 __global__ void __launch_bounds__(WIDE ? 2 * NW * 64 : NW * 64)
 sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ lengths,
                   float* __restrict__ alpha_sk, float* __restrict__ brow,
                   float* __restrict__ partition, int* __restrict__ status,
                   uint64_t* __restrict__ fflag, float2* __restrict__ fpart, int B, int L1max,
                   int L2max, int NSmax, float gap, float T, int R, int G, int SPW,
-                  uint32_t epoch, int ckpt) {
+                  uint32_t epoch, int ckpt, TanArgs ta) {
     constexpr int P = PF;
     static_assert(PF == PR, "checkpoint rows are chosen per forward chunk");
+    static_assert(!(TAN && WIDE), "the tangent sweep has no 16-wave form");
     extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     __shared__ int hprog[NW];     // HELP: chunks of stripe l loaded by its helper
-    __shared__ float red_m[NW], red_z[NW];
+    __shared__ float red_m[NW], red_z[NW], red_w[NW];
     __shared__ float terminal;   // NWG: alpha[L1, L2]
+    __shared__ float tterm;      // NWG, TAN: its tangent
     int b, part;
     split_decode(blockIdx.x, G, b, part);
     if (b >= B) return;
@@ -118,14 +163,18 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     // score tiles per sweeping wave: chunk k uses tile k % NTB (WIDE: four, so that the
     // helper can load three chunks ahead)
     constexpr int NTB = WIDE ? 4 : 2;
-    constexpr int WBUF = NTB * Tile::FLOATS + 2 * 64 + P;  // score chunks, two rows, pad
+    constexpr int NTL = TAN ? 2 : 1;   // tiles per chunk: scores (TAN: and the direction)
+    // score chunks (TAN: then the direction's), two boundary rows (TAN: then two of the
+    // tangent), pad
+    constexpr int WBUF = NTL * (NTB * Tile::FLOATS + 2 * 64) + P;
     float* tiles = smem + wave * WBUF;                     // the score chunks
-    float* rbufs = tiles + NTB * Tile::FLOATS;             // boundary row of a chunk
+    float* rbufs = tiles + NTL * NTB * Tile::FLOATS;       // boundary row of a chunk
     __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
                                   // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
-    float* rings = smem + NW * WBUF;                       // [NW][R]
-    float* sink = rings + NW * R + wave * DUMMY;           // per-wave write sink
+    float* rings = smem + NW * WBUF;                       // [NW][R] (TAN: twice)
+    float* trings = rings + NW * R;                        // TAN: the tangent's
+    float* sink = rings + NTL * NW * R + wave * DUMMY;     // per-wave write sink
     int* st = status + b;
 
     if (lane == 0 && wave < NW) {
@@ -133,7 +182,10 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
         hprog[wave] = -1;
     }
     if (G == 1 && threadIdx.x == 0) *st = 0;               // G > 1: reset before the launch
-    if (NWG && threadIdx.x == 0) terminal = kNINF;
+    if (NWG && threadIdx.x == 0) {
+        terminal = kNINF;
+        tterm = 0.0f;
+    }
     __syncthreads();
 
     const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
@@ -145,13 +197,15 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
     const int nch = (nsteps + P - 1) / P;
     const size_t NT = (size_t)stored_steps(L2max);
     const float* sbase = scores + (size_t)b * L1max * L2max;
+    const float* vbase = TAN ? ta.V + (size_t)b * L1max * L2max : nullptr;
     const int s_begin = part * SPW;
     const int NL = max(min(NS, s_begin + SPW) - s_begin, 0);   // stripes of this part
     const bool has_next = s_begin + NL < NS;
     const uint64_t* flag_in = fflag + (size_t)b * G + (part > 0 ? part - 1 : 0);
     uint64_t* flag_out = fflag + (size_t)b * G + part;
 
-    OnlineLSE acc;
+    // the partition (TAN: and the tangent sum at its scale)
+    typename std::conditional<TAN, OnlineLSEDot, OnlineLSE>::type acc;
     acc.init_open();
 
     if constexpr (HELP) {
@@ -169,9 +223,14 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             // its alpha tiles: this wave's own buffers, or (WIDE: no LDS for those) its
             // score tiles, once their scores are in wave l's registers
             const float* atiles = smem + (WIDE ? l : wave) * WBUF;
+            // TAN: the direction's tiles follow the score tiles, the tangent's the alpha
+            // tiles
             auto load = [&](int k) {
                 dma_quads<P, 1>(ltiles + (k & (NTB - 1)) * Tile::FLOATS * 4, sbase, i0, L1max,
                                 L2max, lane, k * P);
+                if (TAN)
+                    dma_quads<P, 1>(ltiles + (NTB + (k & (NTB - 1))) * Tile::FLOATS * 4, vbase,
+                                    i0, L1max, L2max, lane, k * P);
             };
             // the stripe's last row (lane 63 of wave l) by step, from its ring, for the
             // reverse sweep; a part's last stripe with a next part stores its own (its
@@ -181,17 +240,34 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             const bool l_x_out = l == NL - 1 && has_next;
             float* hbrow = brow + ((size_t)b * NSmax + s_begin + l) * NT;
             const float* hring = ring_of(smem + NW * WBUF, l, R);
+            float* htbrow = TAN ? ta.tan_brow + ((size_t)b * NSmax + s_begin + l) * NT : nullptr;
+            const float* htring = ring_of(smem + NW * WBUF + NW * R, l, R);
             auto store_row = [&](int k) {
                 if (!l_x_out && lane < P) {
                     const int t0 = k * P;
                     lane_store(hbrow, (unsigned)(t0 + lane) * 4u, hring[(t0 % R) + lane]);
+                    if (TAN)
+                        lane_store(htbrow, (unsigned)(t0 + lane) * 4u, htring[(t0 % R) + lane]);
                 }
             };
+            float* tout = TAN ? ta.tan_sk + (((size_t)b * NSmax + s_begin + l) * NT + APAD) * 64
+                              : nullptr;
             // the chunk's alpha rows (alpha tile k % NTB) to the table: Tile::NQ stores
+            // (TAN: and as many for the tangent rows)
             auto store_alpha = [&](int k) {
                 const float* at = atiles + (k & (NTB - 1)) * Tile::FLOATS;
                 float* dst = out + (size_t)k * P * 64;
-                if (ckpt) {
+                if (TAN) {
+                    const float* tt = at + NTB * Tile::FLOATS;
+                    float* tdst = tout + (size_t)k * P * 64;
+#pragma unroll
+                    for (int i = 0; i < Tile::NQ; ++i) {
+                        const float4 v =
+                            *reinterpret_cast<const float4*>(tt + 256 * i + 4 * lane);
+                        *reinterpret_cast<float4*>(tdst + 256 * i + 4 * lane) = v;
+                    }
+                }
+                if (!TAN && ckpt) {
                     // checkpoint mode: only the rows a recomputing reverse sweep starts
                     // from (ckpt_step): the chunk's steps congruent to nsteps - 3 and
                     // nsteps - 4 modulo PR, and the stripe's last two steps where they
@@ -254,8 +330,8 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                 for (int k = 0; k < nch; ++k) {
                     if (k + 1 < nch) {
                         // chunk k + 1's loads: the last issued at k = 0, else followed by
-                        // the P/4 alpha stores of chunk k - 1
-                        if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<Tile::NQ>();
+                        // the P/4 alpha stores of chunk k - 1 (TAN: and P/4 tangent stores)
+                        if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<NTL * Tile::NQ>();
                         publish(hprog, l, k + 2);   // also completes this wave's LDS reads
                     }
                     // once wave l has finished chunk k, its score tile k & 1 takes chunk
@@ -285,26 +361,50 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
         // the cells left of column 0: NINF, or (NWG) the row's boundary i*gap
         const float left0 = NWG ? (float)(i0 + lane + 1) * gap : kNINF;
         const bool last_row = NWG && i0 + lane == L1 - 1;
+        // TAN: the tangent table, last rows and ring (the boundary's tangents are 0)
+        float* tout = TAN ? ta.tan_sk + (((size_t)b * NSmax + s) * NT + APAD) * 64 : nullptr;
+        float* tb_s = TAN ? ta.tan_brow + ((size_t)b * NSmax + s) * NT : nullptr;
+        const float* tb_up =
+            TAN ? ta.tan_brow + ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT : nullptr;
+        const float* tring_in = ring_from(trings, l, R);
+        float* tring_out = ring_of(trings, l, R);
 #pragma unroll
-        for (int t = -APAD; t < 0; ++t) lane_store(out + t * 64, ul4, left0);
+        for (int t = -APAD; t < 0; ++t) {
+            lane_store(out + t * 64, ul4, left0);
+            if (TAN) lane_store(tout + t * 64, ul4, 0.0f);
+        }
         wave_lds_sync();   // the previous stripe's tile reads are complete
         const uint32_t tile_lds = lds_address(tiles);
         const uint32_t row_lds = lds_address(rbufs);
-        // the boundary row of chunk k: lane j < P carries the step kP + 63 + j
+        // the boundary row of chunk k: lane j < P carries the step kP + 63 + j (TAN: its
+        // tangents too, two buffers on)
         auto issue_row = [&](int k) {
             uint32_t off = (uint32_t)min(k * P + 63 + min(lane, P - 1), nsteps - 1) * 4u;
             uint32_t dst = row_lds + (uint32_t)((k & 1) * 64 * 4);
             lds_dma_dword_sys<0>(brow_up, off, dst, 0u);
+            if (TAN) {
+                uint32_t tdst = dst + 2 * 64 * 4;
+                lds_dma_dword_sys<0>(tb_up, off, tdst, 0u);
+            }
+        };
+        // plain form: chunk k's score (TAN: and direction) tiles, by this wave
+        auto issue_tiles = [&](int k) {
+            const uint32_t base = tile_lds + (uint32_t)((k & 1) * Tile::FLOATS * 4);
+            dma_quads<P, 1>(base, sbase, i0, L1max, L2max, lane, k * P);
+            if (TAN)
+                dma_quads<P, 1>(base + NTB * Tile::FLOATS * 4, vbase, i0, L1max, L2max, lane,
+                                k * P);
         };
         int seen = -1;       // chunks of the previous part known to be complete
         if (x_in) {
             seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
             issue_row(0);
         }
-        if (!HELP) dma_quads<P, 1>(tile_lds, sbase, i0, L1max, L2max, lane, 0);
+        if (!HELP) issue_tiles(0);
         // NWG: lane r starts beside column 0 of its row, its diagonal beside column 0
         // of the row above (alpha[0,0] = 0 for lane 0 of the first stripe)
         float cur = left0, up_prev = NWG ? (float)(i0 + lane) * gap : kNINF;
+        float tcur = 0.0f, tup_prev = 0.0f;   // TAN: the same for the tangents
         float bm = -1e20f;   // the running max of this lane's alphas (partition)
         int slot0 = 0;       // ring slot of step t0: t0 % R (R is a multiple of P)
         ProgAhead ahead;     // progress words read during the previous chunk
@@ -325,7 +425,8 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                 }
                 wait_for_ahead(ahead.help, hprog, l, k + 1, st);
             } else {
-                if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<P>();
+                // (TAN: the 2P + 2 stores of that chunk)
+                if (k == 0) wait_vmcnt<0>(); else wait_vmcnt<NTL * P>();
             }
             if (x_in && k > 0) {
                 // its progress word, loaded one chunk ago before those stores
@@ -334,7 +435,9 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             }
             const float* tile = tiles + (k & (NTB - 1)) * Tile::FLOATS;
             float sv[P], av[P];
+            float vv[P], xv[P];   // TAN: direction, tangents
             read_quads<P, 1>(tile, lane, sv);
+            if (TAN) read_quads<P, 1>(tile + NTB * Tile::FLOATS, lane, vv);
             // lane 0's up values: lane j < P holds column t0 + j of the row above (ring
             // slot = producer step); each step shifts the next one into lane 0 (one DPP
             // move instead of staging them through LDS).  Above the first stripe, row 0:
@@ -349,27 +452,35 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             } else if (NWG) {
                 upsh = (float)(t0 + lane + 1) * gap;
             }
+            // TAN: the tangents of the row above the same way (row 0: 0)
+            float tupsh = 0.0f;
+            if (TAN && s > 0 && lane < P) {
+                int slot = slot0 + lane + 63;
+                slot = slot < R ? slot : slot - R;
+                tupsh = x_in ? rbufs[(2 + (k & 1)) * 64 + lane] : tring_in[slot];
+            }
             if (k + 1 < nch) {
                 if (x_in) {
                     const int need = min(k + 1 + lead(P), nch);
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
                     issue_row(k + 1);
                 }
-                if (!HELP)
-                    dma_quads<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, sbase, i0,
-                                    L1max, L2max, lane, t0 + P);
+                if (!HELP) issue_tiles(k + 1);
                 if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             // lane 63 publishes its alpha of step u into ring slot (t0+u) % R; the
             // other lanes write into the sink (R is a multiple of P: no wrap in a chunk)
             float* pub = (lane == 63) ? ring_out + slot0 : sink + lane;
+            float* tpub = (lane == 63) ? tring_out + slot0 : sink + lane;
             float* outc = out + (size_t)t0 * 64;
+            float* toutc = TAN ? tout + (size_t)t0 * 64 : nullptr;
             // HELP: the chunk's alphas by step in the helper's tile k & 1 (written out
             // by the helper; it has written that tile's previous chunk before
             // publishing this one as loaded); WIDE: over this chunk's score tile, whose
-            // scores are in registers
+            // scores are in registers.  TAN: the tangents in the helper's tile NTB + k & 1
             float* atile = smem + (WIDE ? wave : wave + NW / 2) * WBUF +
                            (k & (NTB - 1)) * Tile::FLOATS + lane;
+            float* ttile = atile + NTB * Tile::FLOATS;
             // FULL: every cell of the chunk lies inside the element, no validity masks
             auto steps = [&](auto full) {
                 constexpr bool FULL = decltype(full)::value;
@@ -383,46 +494,78 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                     // out-of-table neighbours are NINF, so no i>1 / j>1 guards are needed
                     // (FULL: the raw max saves the scores' canonicalisation; in the
                     // masked form it only moves instructions)
-                    const float a = fwd_cell<NWG, FULL>(diag, up, cur, sv[u], gap, c, tl);
+                    float a, x = 0.0f;
+                    if constexpr (TAN) {
+                        const float tu = wave_shr1_or(tcur, tupsh);
+                        tupsh = wave_shl1(tupsh);
+                        const float td = tup_prev;
+                        tup_prev = tu;
+                        a = fwd_cell_tan<NWG, FULL>(diag, up, cur, sv[u], gap, c, tl, td, tu,
+                                                    tcur, vv[u], x);
+                    } else {
+                        a = fwd_cell<NWG, FULL>(diag, up, cur, sv[u], gap, c, tl);
+                    }
                     if (FULL) {
                         cur = a;
+                        tcur = x;
                     } else {
                         const int col = t - lane;
                         const bool ok = (unsigned)col < (unsigned)L2eff;
                         // NWG: the cells left of column 0 keep the row's boundary
                         cur = ok ? a : (NWG && col < 0 ? left0 : kNINF);
+                        tcur = ok ? x : 0.0f;
                         // the terminal cell never lies in a FULL chunk (lane 63's
                         // column stays below L2 - 1 there)
-                        if (NWG && ok && last_row && col == L2 - 1) terminal = a;
+                        if (NWG && ok && last_row && col == L2 - 1) {
+                            terminal = a;
+                            if (TAN) tterm = x;
+                        }
                     }
                     if (HELP) atile[u * 64] = cur;
                     else lane_store(outc + u * 64, ul4, cur);
                     pub[u] = cur;
                     av[u] = cur;
                     if (!NWG) bm = fmaxf(bm, cur);
+                    if constexpr (TAN) {
+                        if (HELP) ttile[u * 64] = tcur;
+                        else lane_store(toutc + u * 64, ul4, tcur);
+                        tpub[u] = tcur;
+                        xv[u] = tcur;
+                    }
                 }
             };
             if (i0 + 63 < L1 && t0 >= 63 && t0 + P <= L2) steps(std::true_type{});
             else steps(std::false_type{});
             prog_ahead(ahead, prog, HELP ? hprog : nullptr, l, NL, l);
-            if (!NWG) acc.add_block_max<P>(av, bm, c);
+            if constexpr (TAN) {
+                if (!NWG) acc.template add_block_max<P>(av, xv, bm, c);
+            } else {
+                if (!NWG) acc.template add_block_max<P>(av, bm, c);
+            }
             // the stripe's last row (lane 63) by step, contiguous, for the reverse sweep
-            // of the stripe below and the next part; one store instruction
+            // of the stripe below and the next part; one store instruction (TAN: two)
             wave_lds_sync();
             if (!HELP || x_out) {
                 if (lane < P) {
                     const float v = ring_out[slot0 + lane];
                     if (x_out) store_sys(brow_s + t0 + lane, v);
                     else lane_store(brow_s, (unsigned)(t0 + lane) * 4u, v);
+                    if (TAN) {
+                        const float tv = tring_out[slot0 + lane];
+                        if (x_out) store_sys(tb_s + t0 + lane, tv);
+                        else lane_store(tb_s, (unsigned)(t0 + lane) * 4u, tv);
+                    }
                 }
             }
             publish(prog, wave, l * PROG_STRIDE + k + 1);
             if (x_out && k >= 2) {
                 // at least 2 * (P/4 + P + 1) vector-memory operations (HELP: the last
                 // row stores of chunks k - 1 and k) follow the row stores of chunk
-                // k - 2: those (and everything before) are complete
-                if constexpr (HELP) wait_vmcnt<2>();
-                else wait_vmcnt<2 * (Tile::NQ + P + 1) - Tile::NQ>();
+                // k - 2: those (and everything before) are complete.  TAN: at least
+                // 2 * (2P + 2), beyond the counter's range of 63 (HELP: 2 * 2)
+                constexpr int AFTER = TAN ? 4 * P + 4 : 2 * (Tile::NQ + P + 1) - Tile::NQ;
+                if constexpr (HELP) wait_vmcnt<NTL * 2>();
+                else wait_vmcnt<(AFTER < 63 ? AFTER : 63)>();
                 if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
             }
         }
@@ -437,14 +580,37 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
         // (part 0 for an element without stripes, whose value is its boundary)
         __syncthreads();
         const bool owner = NS > 0 ? (NL > 0 && s_begin + NL == NS) : part == 0;
-        if (threadIdx.x == 0 && owner) partition[b] = NS > 0 ? terminal : (float)(L1 + L2) * gap;
+        if (threadIdx.x == 0 && owner) {
+            partition[b] = NS > 0 ? terminal : (float)(L1 + L2) * gap;
+            if (TAN) ta.sdot[b] = NS > 0 ? tterm : 0.0f;   // the terminal cell's tangent
+        }
         return;
     }
     // partition: merge lanes, waves, and (once per element) the cell (0,0) whose alpha is 0
+    // (TAN: and whose tangent is 0); the value's tangent is then w / z
     wave_merge_lse(acc, c);
-    if (lane == 0 && wave < NW) { red_m[wave] = acc.m; red_z[wave] = acc.z; }
+    if (lane == 0 && wave < NW) {
+        red_m[wave] = acc.m;
+        red_z[wave] = acc.z;
+        if constexpr (TAN) red_w[wave] = acc.w;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
+        if constexpr (TAN) {
+            OnlineLSEDot tot;
+            tot.m = G == 1 ? 0.0f : kNINF;
+            tot.z = G == 1 ? 1.0f : 0.0f;
+            tot.w = 0.0f;
+            for (int w = 0; w < NW; ++w) tot.merge(red_m[w], red_z[w], red_w[w], c);
+            if (G == 1) {
+                partition[b] = tot.m + tl * fast_log2(tot.z);
+                ta.sdot[b] = tot.w / tot.z;
+            } else {
+                fpart[(size_t)b * G + part] = make_float2(tot.m, tot.z);
+                ta.wpart[(size_t)b * G + part] = tot.w;
+            }
+            return;
+        }
         OnlineLSE tot;
         if (G == 1) {
             tot.m = 0.0f;
@@ -1195,9 +1361,11 @@ constexpr size_t kLdsLimit = 160 * 1024 - 512;
 
 // LDS of one workgroup whose stripes' boundaries use rings of R columns
 // ntb: score tiles per sweeping wave (4 in the 16-wave forward)
-size_t lds_forward_r(int R, int ntb = 2) {
-    return (size_t)wf::NW * (ntb * 64 * PF + 2 * 64 + PF) * sizeof(float) +
-           ((size_t)wf::NW * R + wf::NW * DUMMY) * sizeof(float);
+// (tan: the fused tangent sweep's second tile per chunk, rows and ring)
+size_t lds_forward_r(int R, int ntb = 2, bool tan = false) {
+    const int ntl = tan ? 2 : 1;
+    return (size_t)wf::NW * (ntl * (ntb * 64 * PF + 2 * 64) + PF) * sizeof(float) +
+           ((size_t)ntl * wf::NW * R + wf::NW * DUMMY) * sizeof(float);
 }
 size_t lds_backward_r(int R, int P) {
     return (size_t)wf::NW * 2 * (64 * P + 64 * P + 64 + 64) * sizeof(float) +
@@ -1242,18 +1410,21 @@ static bool helpers_enabled() {
     return !(e && e[0] == '0');
 }
 
-template <bool NWG, bool HELP, bool WIDE = false>
+template <bool NWG, bool HELP, bool WIDE = false, bool TAN = false>
 int launch_forward_k(const float* scores, const int* lengths, int B, int max_L1, int max_L2,
                      float gap, float T, const Layout& ws, float* partition, hipStream_t st,
-                     const Split& sp, int R, size_t lds, uint32_t epoch, bool ckpt) {
+                     const Split& sp, int R, size_t lds, uint32_t epoch, bool ckpt,
+                     TanArgs ta = TanArgs{}) {
     const int ns = (max_L1 + 63) / 64;
-    D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel<NWG, HELP, WIDE>,
+    D2P_HIP(hipFuncSetAttribute((const void*)sw_forward_kernel<NWG, HELP, WIDE, TAN>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    D2P_LAUNCH(NWG ? "nw_forward" : "sw_forward", (sw_forward_kernel<NWG, HELP, WIDE>),
+    D2P_LAUNCH(TAN ? (NWG ? "nw_forward_tangent" : "sw_forward_tangent")
+                   : (NWG ? "nw_forward" : "sw_forward"),
+               (sw_forward_kernel<NWG, HELP, WIDE, TAN>),
                dim3(wf::split_grid(B, sp.G)), dim3((WIDE ? 2 : 1) * wf::NW * 64), lds, st, scores,
                lengths,
                ws.alpha_sk, ws.brow, partition, ws.status, ws.fflag, ws.fpart, B, max_L1, max_L2,
-               ns, gap, T, R, sp.G, sp.SPW, epoch, ckpt ? 1 : 0);
+               ns, gap, T, R, sp.G, sp.SPW, epoch, ckpt ? 1 : 0, ta);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -1285,6 +1456,36 @@ int launch_forward(const float* scores, const int* lengths, int B, int max_L1, i
                  : wide ? D2P_SW_FWD(false, true, true) : D2P_SW_FWD(false, false, false));
 #undef D2P_SW_FWD
     if (sp.G > 1 && wf::launch_partition_merge(ws, partition, B, sp.G, T, st) != D2P_OK)
+        return D2P_ERR_HIP;
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
+int launch_forward_tangent(const float* scores, const float* V, const int* lengths, int B,
+                           int max_L1, int max_L2, float gap, float T, const Layout& ws,
+                           float* partition, float* tan_sk, float* tan_brow, float* sdot,
+                           float* wpart, hipStream_t st, bool global) {
+    // rings of an unsplit element that do not fit: parts of at most NW stripes, whose
+    // rings (256 steps) fit whatever the row length
+    const int ns = (max_L1 + 63) / 64;
+    const bool whole = lds_forward_r(ring_forward(max_L1, max_L2), 2, true) <= kLdsLimit;
+    const Split sp = choose_split(B, max_L1, ws, whole ? 0 : wf::NW);
+    const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
+    const size_t lds = lds_forward_r(R, 2, true);
+    D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
+    const uint32_t epoch = next_epoch();
+    if (sp.G > 1 && wf::launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
+    const int part_stripes = sp.G > 1 ? sp.SPW : ns;
+    const bool help = part_stripes <= wf::NW / 2 && helpers_enabled();
+    const TanArgs ta{V, tan_sk, tan_brow, sdot, wpart};
+#define D2P_SW_FWDT(G_, H_) \
+    launch_forward_k<G_, H_, false, true>(scores, lengths, B, max_L1, max_L2, gap, T, ws, \
+                                          partition, st, sp, R, lds, epoch, false, ta)
+    if (global) return help ? D2P_SW_FWDT(true, true) : D2P_SW_FWDT(true, false);
+    D2P_TRY(help ? D2P_SW_FWDT(false, true) : D2P_SW_FWDT(false, false));
+#undef D2P_SW_FWDT
+    if (sp.G > 1 &&
+        wf::launch_partition_dot_merge(ws, wpart, partition, sdot, B, sp.G, T, st) != D2P_OK)
         return D2P_ERR_HIP;
     D2P_HIP(hipGetLastError());
     return D2P_OK;

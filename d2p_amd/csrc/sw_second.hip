@@ -1011,6 +1011,25 @@ int launch_dual(const float* scores, const float* V, const int* lengths, int B, 
     return D2P_OK;
 }
 
+// D2P_AMD_SW_FUSED_TANGENT=0: the forward and the HVP's tangent sweep as two launches
+// (for tests: both forms must agree)
+static bool fused_tangent() {
+    const char* e = std::getenv("D2P_AMD_SW_FUSED_TANGENT");
+    return !(e && e[0] == '0');
+}
+
+// The primal forward (alpha table, partition) and the HVP's forward tangent along V
+// (tangent table, w.sdot = the value's tangent): one fused sweep, or two.
+template <bool NWG>
+int forward_and_tangent(const float* scores, const float* V, const int* lengths, int B, int L1,
+                        int L2, float gap, float T, const Second& w, hipStream_t st) {
+    if (fused_tangent())
+        return sw::launch_forward_tangent(scores, V, lengths, B, L1, L2, gap, T, w.prim, w.part,
+                                          w.tan_sk, w.tan_brow, w.sdot, w.spart, st, NWG);
+    D2P_TRY(sw::launch_forward(scores, lengths, B, L1, L2, gap, T, w.prim, w.part, st, NWG));
+    return launch_tangent<HVP, NWG>(scores, V, lengths, B, L1, L2, gap, T, w, w.sdot, st);
+}
+
 int check(int B, int L1, int L2, float T) {
     // rings that do not fit for an unsplit element force parts of at most NW stripes
     return sw::check_shape(B, L1, L2, T);
@@ -1042,10 +1061,8 @@ int hvp_impl(const float* scores, const float* tangent, const int* lengths, int 
     D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
     hipStream_t st = (hipStream_t)stream;
     const sw2::Second w = sw2::second_layout(workspace, B, max_L1, max_L2);
-    D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, w.prim,
-                               w.part, st, NWG));
-    D2P_TRY(sw2::launch_tangent<sw2::HVP, NWG>(scores, tangent, lengths, B, max_L1, max_L2, gap,
-                                               temperature, w, w.sdot, st));
+    D2P_TRY(sw2::forward_and_tangent<NWG>(scores, tangent, lengths, B, max_L1, max_L2, gap,
+                                          temperature, w, st));
     D2P_TRY(sw2::launch_dual<sw2::HVP, false, NWG>(scores, tangent, lengths, B, max_L1, max_L2,
                                                    gap, temperature, w, w.sdot, hvp, nullptr, st));
     return wf::launch_poison(w.prim.status, B, (long long)max_L1 * max_L2, hvp, nullptr, nullptr,
@@ -1102,15 +1119,14 @@ int backward_full_impl(const float* scores, const float* grad_alignment, const i
     hipStream_t st = (hipStream_t)stream;
     const sw2::Second w = sw2::second_layout(workspace, B, max_L1, max_L2);
     const float* ga = grad_alignment;
-    D2P_TRY(sw::launch_forward(scores, lengths, B, max_L1, max_L2, gap, temperature, w.prim,
-                               w.part, st, NWG));
+    // the forward with the tangent along grad_alignment (for grad_scores = H ga)
+    D2P_TRY(sw2::forward_and_tangent<NWG>(scores, ga, lengths, B, max_L1, max_L2, gap,
+                                          temperature, w, st));
     // SW: dS/dgap and dS/dT; the marginals land in grad_scores, overwritten by the HVP
     if (!NWG)
         D2P_TRY(sw::launch_backward(scores, lengths, B, max_L1, max_L2, gap, temperature,
                                     w.prim, w.part, grad_scores, w.dgap, w.dT, st, true));
     // grad_scores = H grad_alignment
-    D2P_TRY(sw2::launch_tangent<sw2::HVP, NWG>(scores, ga, lengths, B, max_L1, max_L2, gap,
-                                               temperature, w, w.sdot, st));
     D2P_TRY(sw2::launch_dual<sw2::HVP, false, NWG>(scores, ga, lengths, B, max_L1, max_L2, gap,
                                                    temperature, w, w.sdot, grad_scores, nullptr,
                                                    st));
