@@ -152,16 +152,18 @@ struct OnlineLSEDot {
     template <int N>
     __device__ __forceinline__ void add_block_max(const float* x, const float* y, float bmax,
                                                   float c) {
+        // (products and sums as explicit fmas: a contraction left to the compiler
+        // can differ between instantiations, and so would the bits)
+        static_assert(N % 2 == 0, "pairs of values");
         const float M = fmaxf(m, bmax);
         const float r = fast_exp2((m - M) * c);
-        float e[N], ey[N];
+        float e[N], ey[N / 2];
 #pragma unroll
-        for (int i = 0; i < N; ++i) {
-            e[i] = fast_exp2((x[i] - M) * c);
-            ey[i] = e[i] * y[i];
-        }
+        for (int i = 0; i < N; ++i) e[i] = fast_exp2((x[i] - M) * c);
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) ey[i] = fmaf(e[2 * i], y[2 * i], e[2 * i + 1] * y[2 * i + 1]);
         z = fmaf(z, r, tree_sum<N>(e));
-        w = fmaf(w, r, tree_sum<N>(ey));
+        w = fmaf(w, r, tree_sum<N / 2>(ey));
         m = M;
     }
     __device__ __forceinline__ void merge(float m2, float z2, float w2, float c) {
@@ -169,8 +171,8 @@ struct OnlineLSEDot {
         const float ra = (m <= kNINF) ? 0.0f : fast_exp2((m - M) * c);
         const float rb = (m2 <= kNINF) ? 0.0f : fast_exp2((m2 - M) * c);
         m = M;
-        z = z * ra + z2 * rb;
-        w = w * ra + w2 * rb;
+        z = fmaf(z2, rb, z * ra);
+        w = fmaf(w2, rb, w * ra);
     }
 };
 

@@ -60,8 +60,10 @@ __global__ void partition_dot_merge_kernel(const float2* __restrict__ fpart,
         const float2 v = fpart[(size_t)b * G + g];
         tot.merge(v.x, v.y, wpart[(size_t)b * G + g], c);
     }
-    partition[b] = tot.m + T * kLn2 * fast_log2(tot.z);
-    sdot[b] = tot.w / tot.z;
+    // the cells' weights 2^((alpha - S) c) with S rounded to fp32 (not w / z)
+    const float S = tot.m + T * kLn2 * fast_log2(tot.z);
+    partition[b] = S;
+    sdot[b] = tot.w * fast_exp2((tot.m - S) * c);
 }
 
 // Sum of the parts' partial results of a split element.

@@ -85,8 +85,9 @@ __device__ __forceinline__ float fwd_cell_tan(float diag, float up, float cur, f
                                               float tc, float v, float& x) {
     float e[4], sum;
     const float a = fwd_cell_e<NWG, RAWMAX>(diag, up, cur, sc, gap, c, tl, e, sum);
-    const float num = NWG ? (e[0] * (td + v) + e[1] * tu) + e[2] * tc
-                          : ((e[0] * (td + v) + e[1] * tu) + e[2] * tc) + e[3] * v;
+    // (explicit fmas: the same bits in every instantiation)
+    const float n2 = fmaf(e[2], tc, fmaf(e[1], tu, e[0] * (td + v)));
+    const float num = NWG ? n2 : fmaf(e[3], v, n2);
     x = num * fast_rcp(sum);
     return a;
 }
@@ -587,7 +588,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
         return;
     }
     // partition: merge lanes, waves, and (once per element) the cell (0,0) whose alpha is 0
-    // (TAN: and whose tangent is 0); the value's tangent is then w / z
+    // (TAN: and whose tangent is 0)
     wave_merge_lse(acc, c);
     if (lane == 0 && wave < NW) {
         red_m[wave] = acc.m;
@@ -603,8 +604,13 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             tot.w = 0.0f;
             for (int w = 0; w < NW; ++w) tot.merge(red_m[w], red_z[w], red_w[w], c);
             if (G == 1) {
-                partition[b] = tot.m + tl * fast_log2(tot.z);
-                ta.sdot[b] = tot.w / tot.z;
+                // the cells' weights 2^((alpha - S) c) with S rounded to fp32, as the
+                // two-sweep form and the reference take them: w 2^((m - S) c), not w / z
+                // (their sum differs from 1 by the rounding of S, e.g. 6e-5 at |S| = 500
+                // and T = 0.5, and the reverse sweep's start relies on the same weights)
+                const float S = tot.m + tl * fast_log2(tot.z);
+                partition[b] = S;
+                ta.sdot[b] = tot.w * fast_exp2((tot.m - S) * c);
             } else {
                 fpart[(size_t)b * G + part] = make_float2(tot.m, tot.z);
                 ta.wpart[(size_t)b * G + part] = tot.w;

@@ -376,11 +376,12 @@ sw_tangent_kernel(const float* __restrict__ scores, const float* __restrict__ V,
 // DOT: instead of writing the per-cell output, accumulate its dot product with the
 // matrix passed as V (the marginal cotangent) into dot[b].
 // HELP (quad tiles, per-cell output, parts of at most NW/2 stripes): wave NW/2 + q
-// moves stripe order q's data.  Chunk k's buffer is wave q's own for even k and the
-// helper's for odd k.  The helper loads a chunk's scores, direction, alpha and
-// tangent rows into its buffer (publishing hprog[q] = chunks loaded), writes the
-// chunk's output tile out once wave q has finished the chunk (prog[q]), and then
-// loads chunk k + 2 into that buffer.  Wave q loads only its rows above and flows.
+// moves stripe order q's data.  Chunk k's buffer is the k % 3-th of three: wave q's
+// own, the helper's, and one of NW/2 more after the waves' buffers.  The helper loads
+// a chunk's scores, direction, alpha and tangent rows and rows above into its buffer
+// (publishing hprog[q] = chunks loaded), writes the chunk's output tile out once wave
+// q has finished the chunk (prog[q]), and then loads chunk k + 3 into that buffer: its
+// loads have two chunks of time.  Wave q loads only a part's flows from below.
 template <int MODE, int P, bool DOT, bool NWG = false, bool HELP = false>
 __global__ void __launch_bounds__(NW * 64)
 sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
@@ -427,7 +428,8 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
     __shared__ float fslot[64];   // progress word prefetched by wave 0, the only wave whose
                                   // stripe borders another part
     const uint32_t fslot_lds = lds_address(fslot);
-    float4* rings = reinterpret_cast<float4*>(smem + NW * BUF);   // [NW][R]
+    // (HELP: NW/2 more chunk buffers, then the rings)
+    float4* rings = reinterpret_cast<float4*>(smem + (HELP ? NW + NW / 2 : NW) * BUF);  // [NW][R]
     float4* sink = rings + NW * R + wave * SINK;
     int* st = status + b;
     const int tbase = ChunkTile<P>::read_base(lane);   // dword tiles (4-step chunks)
@@ -478,8 +480,17 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             const size_t sb = ((size_t)b * NSmax + s) * NT;
             const float* astripe = alpha_sk + sb * 64;
             const float* xstripe = tan_sk + sb * 64;
-            // chunk k's buffer: wave q's own (even k) or this wave's (odd k)
-            auto cbuf = [&](int k) { return smem + (k & 1 ? wave : q) * BUF; };
+            const size_t ub = ((size_t)b * NSmax + (s > 0 ? s - 1 : 0)) * NT;
+            const float* bup = brow + ub;
+            const float* xup = tan_brow + ub;
+            // chunk k's buffer: wave q's own, this wave's, or the extra one
+            auto cbuf = [&](int k) {
+                const int r = k % 3;
+                return smem + (r == 0 ? q : (r == 1 ? wave : NW + q)) * BUF;
+            };
+            // the loads of a chunk: at least NLD instructions (more in a chunk that
+            // reaches past the element, whose quads load as dwords)
+            constexpr int NLD = NQ * (HAS_V ? 2 : 1) + 2 * (P / 4) + 2;
             auto load = [&](int k) {
                 const int th = nsteps - 1 - k * P;
                 const uint32_t in = lds_address(cbuf(k));
@@ -487,6 +498,13 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 if (HAS_V) dma_quads<P, -1>(in + VT * 4, vbase, i0, L1max, L2max, lane, th);
                 dma_rows<P, -1>(in + AR * 4, astripe, th - 2, ul4);
                 dma_rows<P, -1>(in + XR * 4, xstripe, th - 2, ul4);
+                // lane j <= P: the last rows above (alpha, tangent) at step th - j + 63
+                const uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
+                uint32_t o = roff, l = in + RA * 4;
+                lds_dma_dword<0>(bup, o, l, 0u);
+                o = roff;
+                l = in + RX * 4;
+                lds_dma_dword<0>(xup, o, l, 0u);
             };
             // whole row segments of the output where rows start aligned (write_aligned)
             const bool aligned = (L2max & (P - 1)) == 0;
@@ -497,15 +515,21 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 wait_vmcnt<0>();
                 publish(hprog, q, 1);
                 if (nch > 1) load(1);
+                if (nch > 2) load(2);
             }
             for (int k = 0; k < nch; ++k) {
                 if (k + 1 < nch) {
-                    // chunk k + 1's loads are the last issued
-                    wait_vmcnt<0>();
+                    // chunk k + 1's loads, followed by chunk k + 2's (if any) and, from
+                    // k = 1 on, by chunk k - 1's NQ output stores
+                    if (k == 0) {
+                        if (nch > 2) wait_vmcnt<NLD>(); else wait_vmcnt<0>();
+                    } else {
+                        if (k + 2 < nch) wait_vmcnt<NQ + NLD>(); else wait_vmcnt<NQ>();
+                    }
                     publish(hprog, q, k + 2);   // also completes this wave's LDS reads
                 }
                 // once wave q has finished chunk k, its output tile leaves and the
-                // buffer takes chunk k + 2 (the stores have read the tile: their data
+                // buffer takes chunk k + 3 (the stores have read the tile: their data
                 // dependence waits for the reads)
                 wait_for(prog, q, q * PROG_STRIDE + k + 1, st);
                 if (aligned)
@@ -514,7 +538,7 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 else
                     write_quads<P, -1>(cbuf(k) + OT, obase, trash, i0, L1, L2, L1max, L2max,
                                        lane, nsteps - 1 - k * P);
-                if (k + 2 < nch) load(k + 2);
+                if (k + 3 < nch) load(k + 3);
             }
         }
     }
@@ -542,8 +566,12 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             flows4 + ((size_t)b * NSmax + (x_in ? s + 1 : s)) * NT);
         int seen = -1;       // chunks of the part below known to be complete
 
-        // chunk k's buffer: this wave's own, or (HELP, odd k) its helper's
-        auto kbuf = [&](int k) { return HELP && (k & 1) ? smem + (wave + NW / 2) * BUF : wbuf; };
+        // chunk k's buffer: this wave's own, or (HELP) the k % 3-th of its three
+        auto kbuf = [&](int k) {
+            if (!HELP) return wbuf;
+            const int r = k % 3;
+            return smem + (r == 0 ? wave : (r == 1 ? wave + NW / 2 : NW + wave)) * BUF;
+        };
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
             const uint32_t in = lds_address(kbuf(k));
@@ -559,13 +587,13 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             if constexpr (!HELP) {
                 dma_rows<P, -1>(in + AR * 4, astripe, th - 2, ul4);
                 dma_rows<P, -1>(in + XR * 4, xstripe, th - 2, ul4);
+                const uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
+                uint32_t o = roff, l = in + RA * 4;
+                lds_dma_dword<0>(bup, o, l, 0u);
+                o = roff;
+                l = in + RX * 4;
+                lds_dma_dword<0>(xup, o, l, 0u);
             }
-            const uint32_t roff = (uint32_t)min(th - min(lane, P) + 63, nsteps - 1) * 4u;
-            uint32_t o = roff, l = in + RA * 4;
-            lds_dma_dword<0>(bup, o, l, 0u);
-            o = roff;
-            l = in + RX * 4;
-            lds_dma_dword<0>(xup, o, l, 0u);
             if (x_in) {
                 // flows of producer slots kP+62 .. kP+62+P (float4 each): float f of the
                 // range in lane f, clamped to the last slot
@@ -598,10 +626,13 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             // this chunk's loads, followed by at least the NSTORE output stores of the
             // previous chunk (none when accumulating a dot product; the first chunk's
             // loads are the last issued).  HELP: the helper loads the tiles and rows;
-            // this wave's own loads (rows above, flows) are followed by nothing, or by
-            // the previous chunk's flow store (x_out)
+            // this wave's own loads (a part's flows from below) are followed by
+            // nothing, or by the previous chunk's flow store (x_out); other stripes
+            // wait for no memory operation of their own
             if constexpr (HELP) {
-                if (x_out && k > 0) wait_vmcnt<1>(); else wait_vmcnt<0>();
+                if (x_in) {
+                    if (x_out && k > 0) wait_vmcnt<1>(); else wait_vmcnt<0>();
+                }
                 wait_for(hprog, q, k + 1, st);
             } else {
                 if (k == 0 || DOT) wait_vmcnt<0>(); else wait_vmcnt<NSTORE>();
@@ -846,9 +877,8 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 if (k >= 2) {
                     // at least (QT ? P/4 : P) + P/2 + 2 loads, 2 flow stores and 2 NSTORE
                     // output stores follow the flow store of chunk k - 2 (HELP: the two
-                    // rows-above loads issued in chunk k - 1 and the two flow stores): it
-                    // is complete
-                    if constexpr (HELP) wait_vmcnt<4>();
+                    // flow stores): it is complete
+                    if constexpr (HELP) wait_vmcnt<2>();
                     else wait_vmcnt<(QT ? NQ : P) + P / 2 + 4 + 2 * NSTORE>();
                     if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
                 }
@@ -889,9 +919,11 @@ size_t lds_tangent(int mode, int max_L1, int max_L2) {
     return lds_tangent_r(mode, ring_len(max_L1, max_L2, 256));
 }
 
-size_t lds_dual_r(bool has_v, bool dot, int P, int R) {
+// (help: the helper form's NW/2 extra chunk buffers)
+size_t lds_dual_r(bool has_v, bool dot, int P, int R, bool help = false) {
     const int buf = 65 * P * (has_v ? 2 : 1) + 2 * P * 64 + 128 + (dot ? 0 : 65 * P) + 64;
-    return (size_t)NW * buf * sizeof(float) + ((size_t)NW * R + NW * (64 + P)) * sizeof(float4);
+    return (size_t)(help ? NW + NW / 2 : NW) * buf * sizeof(float) +
+           ((size_t)NW * R + NW * (64 + P)) * sizeof(float4);
 }
 
 // Largest reverse-sweep chunk (8 or 4 steps) whose buffers and rings fit in LDS, for a
@@ -989,14 +1021,17 @@ int launch_dual(const float* scores, const float* V, const int* lengths, int B, 
     const int R = ring_len(rows, L2, 128);
     const int P = dual_chunk(has_v, DOT, rows, L2);
     D2P_REQUIRE(P > 0, "sequence too long for the LDS stripe rings");
-    const size_t lds = lds_dual_r(has_v, DOT, P, R);
+    size_t lds = lds_dual_r(has_v, DOT, P, R);
     auto k8 = sw_dual_kernel<MODE, 8, DOT, NWG>;
     auto k4 = sw_dual_kernel<MODE, 4, DOT, NWG>;
     auto kern = P == 8 ? k8 : k4;
     // helper waves move the data when a part has at most NW/2 stripes (the others idle)
     if constexpr (!DOT) {
-        if (P == 8 && (rows + 63) / 64 <= NW / 2 && helpers_enabled())
+        if (P == 8 && (rows + 63) / 64 <= NW / 2 && helpers_enabled() &&
+            lds_dual_r(has_v, DOT, P, R, true) <= kLdsLimit) {
             kern = sw_dual_kernel<MODE, 8, DOT, NWG, true>;
+            lds = lds_dual_r(has_v, DOT, P, R, true);
+        }
     }
     if (sp.G > 1) D2P_TRY(launch_flag_reset(w.prim.bflag, B * sp.G, st));
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,

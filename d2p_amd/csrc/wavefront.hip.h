@@ -164,7 +164,8 @@ int launch_flag_reset(uint64_t* flags, int n, hipStream_t st);
 int launch_partition_merge(const Layout& ws, float* partition, int B, int G, float T,
                            hipStream_t st);
 // The same, and sdot[b] = the value's tangent from the parts' tangent sums wpart[b][part]
-// at their (max, scaled sum) scale (the cell (0, 0) adds a tangent of 0).
+// at their (max, scaled sum) scale (the cell (0, 0) adds a tangent of 0), weighted as
+// 2^((alpha - S) c) with the fp32 partition S.
 int launch_partition_dot_merge(const Layout& ws, const float* wpart, float* partition,
                                float* sdot, int B, int G, float T, hipStream_t st);
 // out[b] = sum of the G parts' partial results spart[b][part].

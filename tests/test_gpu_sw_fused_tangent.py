@@ -103,6 +103,22 @@ def test_fused_tangent_hvp(cuda, monkeypatch, seed, fam, B, L1, L2, parts, helpe
               f"|fp32 reference - exact| {er:.3e}", flush=True)
 
 
+@pytest.mark.parametrize("parts", [1, 3])
+def test_fused_tangent_large_values(cuda, monkeypatch, parts):
+    """Scores of about 50 at T = 0.5 (values near 2000, as the reference's clamp
+    fixture): the value's tangent must weight the cells by 2^((alpha - S) c) with the
+    fp32 partition S, whose rounding moves the weights' sum off 1 by about 1e-4 here,
+    as the reverse sweep and the reference do."""
+    monkeypatch.setenv("D2P_AMD_SPLIT", str(parts))
+    s = _seeded(93, (2, 700, 90)) * 50.0
+    v = _seeded(94, (2, 700, 90))
+    sd, vd = s.to(cuda), v.to(cuda)
+    fused, two = _both(monkeypatch, lambda: [_capi.sw_hvp(sd, vd, None, -1.0, 0.5)])
+    ref = O.get("oracle").soft_sw_hvp(s.numpy(), v.numpy(), -1.0, 0.5)
+    close_entrywise(fused[0], ref, "hvp fused, large values")
+    close_entrywise(two[0], ref, "hvp two sweeps, large values")
+
+
 @pytest.mark.parametrize("fam", ["sw", "nw"])
 def test_fused_tangent_backward_full(cuda, monkeypatch, fam):
     s = _seeded(91, (3, 200, 150))

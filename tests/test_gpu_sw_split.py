@@ -104,8 +104,8 @@ def test_sw_helper_waves_bit_identical(cuda, parts, monkeypatch, B, L1, L2, n):
                       _capi.sw_param_jacobian(s, 1, lens, -1.0, 0.9)] +
                      list(_capi.sw_backward_full(s, V, lens, -1.0, 0.9)) +
                      list(_capi.swa_forward_marginals(s, lens, -3.0, -0.5, 0.9)))
-    for a, b in zip(out["1"], out["0"]):
-        assert torch.equal(a, b)
+    for i, (a, b) in enumerate(zip(out["1"], out["0"])):
+        assert torch.equal(a, b), f"output {i}: max |diff| {float((a - b).abs().max()):.3e}"
     ref = O.get("oracle").soft_sw(s.cpu().numpy(), -1.0, 0.9, lens.cpu().numpy())
     np.testing.assert_allclose(out["1"][0].cpu().numpy(), ref[0], rtol=1e-5, atol=1e-6)
 
