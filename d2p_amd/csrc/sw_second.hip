@@ -572,6 +572,15 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             const int r = k % 3;
             return smem + (r == 0 ? wave : (r == 1 ? wave + NW / 2 : NW + wave)) * BUF;
         };
+        // x_in: the flows of chunk k from the part below, producer slots kP+62 ..
+        // kP+62+P (float4 each): float f of the range in lane f, clamped to the last
+        // slot (HELP: two chunks ahead, into chunk k's buffer; else one chunk ahead)
+        auto issue_flows = [&](int k) {
+            uint32_t foff = (uint32_t)min((k * P + 62) * 4 + min(lane, 4 * P + 1),
+                                          (nsteps - 1) * 4 + 3) * 4u;
+            uint32_t fdst = lds_address(kbuf(k)) + FB * 4;
+            lds_dma_dword_sys<0>(flows_in, foff, fdst, 0u);
+        };
         auto issue_chunk = [&](int k) {
             const int th = nsteps - 1 - k * P;
             const uint32_t in = lds_address(kbuf(k));
@@ -594,14 +603,7 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 l = in + RX * 4;
                 lds_dma_dword<0>(xup, o, l, 0u);
             }
-            if (x_in) {
-                // flows of producer slots kP+62 .. kP+62+P (float4 each): float f of the
-                // range in lane f, clamped to the last slot
-                uint32_t foff = (uint32_t)min((k * P + 62) * 4 + min(lane, 4 * P + 1),
-                                              (nsteps - 1) * 4 + 3) * 4u;
-                uint32_t fdst = in + FB * 4;
-                lds_dma_dword_sys<0>(flows_in, foff, fdst, 0u);
-            }
+            if (!HELP && x_in) issue_flows(k);
         };
 
         {
@@ -614,8 +616,12 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             __asm__ volatile("" ::"v"(A[P]), "v"(A[P + 1]), "v"(X[P]), "v"(X[P + 1]));
         }
         wave_lds_sync();
-        if (x_in) seen = wait_part(flag_in, epoch, min(lead(P), nch), st);
+        if (x_in) seen = wait_part(flag_in, epoch, min(lead(P) + (HELP ? 1 : 0), nch), st);
         issue_chunk(0);
+        if (HELP && x_in) {
+            issue_flows(0);
+            if (nch > 1) issue_flows(1);
+        }
         // successor flows: (beta, g) from the left successor, up successor, diagonal
         float lb = 0.0f, lg = 0.0f, ubt = 0.0f, ug = 0.0f;
         float db = 0.0f, dg = 0.0f, db2 = 0.0f, dg2 = 0.0f;
@@ -630,8 +636,14 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             // nothing, or by the previous chunk's flow store (x_out); other stripes
             // wait for no memory operation of their own
             if constexpr (HELP) {
+                // x_in: chunk k's flows (loaded two chunks ago) and the progress word
+                // loaded one chunk ago, followed by chunk k + 1's flows (k + 1 < nch)
+                // and the previous chunk's flow store (x_out)
                 if (x_in) {
-                    if (x_out && k > 0) wait_vmcnt<1>(); else wait_vmcnt<0>();
+                    if (k == 0) wait_vmcnt<0>();
+                    else if (x_out && k + 1 < nch) wait_vmcnt<2>();
+                    else if (x_out || k + 1 < nch) wait_vmcnt<1>();
+                    else wait_vmcnt<0>();
                 }
                 wait_for(hprog, q, k + 1, st);
             } else {
@@ -701,26 +713,39 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             }
             wave_lds_sync();   // every read of the input buffer is complete
             if (k + 1 < nch) {
-                if (x_in) {
-                    const int need = min(k + 1 + lead(P), nch);
-                    if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                if constexpr (HELP) {
+                    // the progress word, then (once the part below has published enough
+                    // chunks) chunk k + 2's flows
+                    if (x_in) {
+                        flag_load_lds(flag_in, fslot_lds, lane);
+                        if (k + 2 < nch) {
+                            const int need = min(k + 2 + lead(P), nch);
+                            if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                            issue_flows(k + 2);
+                        }
+                    }
+                } else {
+                    if (x_in) {
+                        const int need = min(k + 1 + lead(P), nch);
+                        if (seen < need) seen = wait_part(flag_in, epoch, need, st);
+                    }
+                    issue_chunk(k + 1);
+                    if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
                 }
-                issue_chunk(k + 1);
-                if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
             }
             float4* pub = (lane == 0) ? ring_out + ring_index(k * P, R) : sink + lane;
             {
-                const float u0b = lane_bcast(qub, 63), u0g = lane_bcast(qug, 63);
-                const float d0b = lane_bcast(qdb, 63), d0g = lane_bcast(qdg, 63);
-                const float d1b = lane_bcast(qdb, 62), d1g = lane_bcast(qdg, 62);
+                // lane 63 starts from step 0's flows (its own) and step 1's diagonal
+                // flows (lane 62's, one DPP shift)
+                const float d1b = wave_shr1(qdb), d1g = wave_shr1(qdg);
                 if (lane == 63) {
-                    ubt = u0b; ug = u0g;
-                    db = d0b; dg = d0g;
+                    ubt = qub; ug = qug;
+                    db = qdb; dg = qdg;
                     db2 = d1b; dg2 = d1g;
                 }
+                qdb = wave_shr1(d1b);
+                qdg = wave_shr1(d1g);
             }
-            qdb = wave_shr1(wave_shr1(qdb));
-            qdg = wave_shr1(wave_shr1(qdg));
             // QT: the output quad being filled, memory-column order (step 4q + 3 - e in
             // element e); one 16-byte LDS write per four steps
             float4 quad = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -734,14 +759,18 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 for (int u = 1; u < P; ++u) amax = fmaxf(amax, A[u]);
                 inits = __builtin_amdgcn_ballot_w64((amax - S) * c >= -151.0f) != 0;
             }
-            auto steps = [&](auto init) {
+            // INIT: some cell of the chunk may have beta_init > 0 (else the initial terms
+            // are left out: adding their exact zeros changes no bit); FULL: every cell
+            // of the chunk lies inside the element (no validity masks; the raw max)
+            auto steps = [&](auto init, auto full) {
             constexpr bool INIT = decltype(init)::value;
+            constexpr bool FULL = decltype(full)::value;
 #pragma unroll
             for (int u = 0; u < P; ++u) {
                 const int t = t_hi - u;
-                const bool ok = (unsigned)(t - lane) < (unsigned)L2eff;
-                const float sc = ok ? sv[u] : kNINF;
-                const float vd = ok ? vv[u] : 0.0f;
+                const bool ok = FULL || (unsigned)(t - lane) < (unsigned)L2eff;
+                const float sc = FULL ? sv[u] : (ok ? sv[u] : kNINF);
+                const float vd = FULL ? vv[u] : (ok ? vv[u] : 0.0f);
                 // primal and tangent predecessors
                 const float a0 = A[u], a1 = A[u + 1], x0 = X[u], x1 = X[u + 1];
                 const float nA = wave_shl1(bA), nX = wave_shl1(bX);
@@ -751,7 +780,9 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 bX = nX;
                 const float v0 = dga + sc, v1 = upa + gap, v2 = a1 + gap;
                 // NWG: no restart candidate
-                const float m = NWG ? fmaxf(fmaxf(v0, v1), v2) : fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
+                const float m = NWG ? fmaxf(fmaxf(v0, v1), v2)
+                                    : (FULL ? max4_raw(v0, v1, v2, sc)
+                                            : fmaxf(fmaxf(v0, v1), fmaxf(v2, sc)));
                 const float e0 = fast_exp2((v0 - m) * c), e1 = fast_exp2((v1 - m) * c);
                 const float e2 = fast_exp2((v2 - m) * c);
                 const float e3 = NWG ? 0.0f : fast_exp2((sc - m) * c);
@@ -807,7 +838,7 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 } else {
                     binit = 0.0f;
                 }
-                const float beta = ((binit + db) + lb) + ubt;
+                const float beta = (NWG || INIT) ? ((binit + db) + lb) + ubt : (db + lb) + ubt;
                 float g;
                 bool live;
                 if (NWG) {
@@ -816,12 +847,15 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                     g = ((dg + lg) + ug);
                     live = ok && !(beta == 0.0f && fabsf(g) < 1e-20f);
                 } else if (MODE == HVP) {
-                    g = ((binit * (x0 - dSb) * rT + dg) + lg) + ug;
+                    g = INIT ? ((binit * (x0 - dSb) * rT + dg) + lg) + ug : (dg + lg) + ug;
                     live = ok && beta <= 3.0e38f && beta != 0.0f;
                 } else {
-                    float init = binit * (x0 - dSb) * rT;
-                    if (MODE == TEMP) init -= binit * (a0 - S) * rT * rT;
-                    g = ((dg + lg) + ug) + init;
+                    g = (dg + lg) + ug;
+                    if (INIT) {
+                        float init = binit * (x0 - dSb) * rT;
+                        if (MODE == TEMP) init -= binit * (a0 - S) * rT * rT;
+                        g = g + init;
+                    }
                     live = ok && !(beta <= 1e-20f && fabsf(g) <= 1e-20f);
                 }
                 const float bl = live ? beta : 0.0f;
@@ -859,8 +893,14 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 qdg = wave_shr1(qdg);
             }
             };
-            if (inits) steps(std::true_type{});
-            else steps(std::false_type{});
+            const bool full = i0 + 64 <= L1 && t_hi - (P - 1) >= 63 && t_hi <= L2 - 1;
+            if (inits) {
+                if (full) steps(std::true_type{}, std::true_type{});
+                else steps(std::true_type{}, std::false_type{});
+            } else {
+                if (full) steps(std::false_type{}, std::true_type{});
+                else steps(std::false_type{}, std::false_type{});
+            }
             wave_lds_sync();
             if constexpr (HELP) {
                 // (the helper writes the tile out once this chunk is published)
@@ -874,13 +914,19 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
             if (x_out) {
                 // this chunk's flows to the part above, by producer step
                 if (lane < P) store_sys4(flows_out + k * P + lane, ring_out[ring_index(k * P, R) + lane]);
-                if (k >= 2) {
-                    // at least (QT ? P/4 : P) + P/2 + 2 loads, 2 flow stores and 2 NSTORE
-                    // output stores follow the flow store of chunk k - 2 (HELP: the two
-                    // flow stores): it is complete
-                    if constexpr (HELP) wait_vmcnt<2>();
+                // HELP: the word reports the chunks up to k - XD, whose flow stores (and
+                // everything before) are complete once at most XD memory operations are
+                // outstanding (the flow stores of chunks k - XD + 1 .. k follow them):
+                // device-coherent stores take several chunk periods to complete in the
+                // sweep's busiest phase, and a wait for the last two chunks' stalled
+                // this stripe, and through the rings its whole part, on every chunk.
+                // Plain form: at least (QT ? P/4 : P) + P/2 + 2 loads, 2 flow stores and
+                // 2 NSTORE output stores follow the flow store of chunk k - 2.
+                constexpr int XD = HELP ? 4 : 2;
+                if (k >= XD) {
+                    if constexpr (HELP) wait_vmcnt<XD>();
                     else wait_vmcnt<(QT ? NQ : P) + P / 2 + 4 + 2 * NSTORE>();
-                    if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
+                    if (lane == 0) store_flag(flag_out, progress_word(epoch, k - XD + 1));
                 }
             }
         }
