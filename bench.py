@@ -187,7 +187,8 @@ def make_c4band():
 def make_c4xy(fused):
     """C4 from its features: the same seeded x, y [512, 256, 64] as make_c4, the whole
     job from features to gradients.  fused: d2p_amd.soft_dtw_sqeuclidean (costs formed
-    inside the forward sweep); else torch.cdist(x, y) ** 2 + soft_dtw, the reference's
+    on the matrix cores into the alignment buffer, which the forward sweep reads and
+    the reverse sweep overwrites); else torch.cdist(x, y) ** 2 + soft_dtw, the reference's
     documented sequence (/root/reference/docs/algorithms/dtw.md:52; cdist's default mode
     takes the matrix-product form at these sizes, and its exact-difference mode fails
     to launch at [512, 256, 64] on this ROCm build).  Both: cost.sum().backward() into
@@ -202,12 +203,15 @@ def make_c4xy(fused):
     if fused:
         return dict(
             name="c4fused", inputs={"x": x, "y": y}, cells=cells,
-            # read x and y, write the alignment (= dcost/dcosts) and grad x, y (the GEMMs
-            # also read the alignment)
+            # read x and y, write the alignment (= dcost/dcosts) and grad x, y (the
+            # gradient also reads the alignment); per kernel: the costs' formation
+            # (features in, costs out), the forward (costs in) and the reverse sweep
+            # (alignment out), the costs passing through the alignment buffer
             algo_step=2 * feat + 8 * cells + 2 * feat,
-            algo_kernel={"dtw_fused_forward": 2 * feat, "dtw_fused_backward": 4 * cells},
+            algo_kernel={"pairwise_sqdist": 2 * feat + 4 * cells, "dtw_forward": 4 * cells,
+                         "dtw_backward": 4 * cells},
             workload="C4 fused: soft_dtw_sqeuclidean(x, y, T=0.1), x, y [512,256,64] "
-                     "(costs formed in the forward sweep), fwd + cost.sum().backward() into x, y",
+                     "(costs on the matrix cores), fwd + cost.sum().backward() into x, y",
             extra={"B": B, "L1": L, "L2": L, "D": D, "temperature": 0.1})
     return dict(
         name="c4xy", inputs={"x": x, "y": y}, cells=cells,

@@ -108,6 +108,7 @@ _AMD_FAKES = {
         x.new_empty([x.size(0)]), x.new_empty([x.size(0), x.size(1), y.size(1)]),
         x.new_empty([x.size(0)])),
     "pairwise_sqdist": lambda x, y: x.new_empty([x.size(0), x.size(1), y.size(1)]),
+    "sqeuclid_feature_grad": lambda G, x, y, s: (x.new_empty(x.shape), y.new_empty(y.shape)),
 }
 for _name, _fn in _AMD_FAKES.items():
     register_fake(f"d2p_amd::{_name}")(_fn)

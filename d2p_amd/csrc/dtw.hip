@@ -35,144 +35,19 @@ using namespace wf;
 
 constexpr int DUMMY = 64 + PF;       // per-wave LDS sink for the lanes that do not publish
 
-// ------------------------------------------------------------------ fused costs
-// The fused forward sweep (DC > 0) forms the costs itself from two feature sequences,
-// c[i,j] = sum_d (x[i,d] - y[j,d])^2, instead of reading a cost matrix: the
-// squared-Euclidean cost that callers otherwise build with
-// torch.cdist(x, y) ** 2 (/root/reference/docs/algorithms/dtw.md:52) before the
-// reference's sweeps read it (/root/reference/src/dtw/kernels.cu:55-114).  Each lane
-// keeps its row of x in registers; the element's y rows sit in LDS at a stride of
-// DC + 4 floats, so the 16-byte reads of 16 consecutive columns hit distinct banks
-// (the dynamic LDS base is 16-byte aligned: unaligned 16-byte LDS reads are served
-// correctly but several times slower).  D is padded to DC with zeros, which add exact
-// zeros.  The reverse sweep needs no costs at all.  Both forms below (y from LDS,
-// x from LDS) run the same four partial sums in the same order, so every kernel that
-// forms these costs (the fused forward and pairwise_sqdist) agrees bit for bit.
-
-// Loads per group: all of a group's LDS reads are issued before the first is used
-// (one LDS latency per group instead of one per read), at most 16 float4 in flight.
-template <int DC>
-constexpr int feature_group() { return DC < 64 ? DC / 4 : 16; }
-
-// sum_d (x[d] - y[d])^2, x in registers, y a 16-byte aligned LDS row.  Four partial
-// sums (features d = 4k + m into sum m), added pairwise at the end: four independent
-// fma chains instead of one.
-template <int DC>
-__device__ __forceinline__ float sq_euclid(const float (&xr)[DC], const float* yrow) {
-    constexpr int G = feature_group<DC>();
-    const float4* q = reinterpret_cast<const float4*>(yrow);
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-#pragma unroll
-    for (int g0 = 0; g0 < DC / 4; g0 += G) {
-        float4 v[G];
-#pragma unroll
-        for (int k = 0; k < G; ++k) v[k] = q[g0 + k];
-        __builtin_amdgcn_sched_barrier(0);   // keep the group's reads ahead of their uses
-#pragma unroll
-        for (int k = 0; k < G; ++k) {
-            const int d = 4 * (g0 + k);
-            const float d0 = xr[d] - v[k].x, d1 = xr[d + 1] - v[k].y;
-            const float d2 = xr[d + 2] - v[k].z, d3 = xr[d + 3] - v[k].w;
-            a0 = fmaf(d0, d0, a0);
-            a1 = fmaf(d1, d1, a1);
-            a2 = fmaf(d2, d2, a2);
-            a3 = fmaf(d3, d3, a3);
-        }
-    }
-    return (a0 + a1) + (a2 + a3);
-}
-
-// The same sum with x a 16-byte aligned LDS row (read by every lane: a broadcast) and
-// y in registers.
-template <int DC>
-__device__ __forceinline__ float sq_euclid_xl(const float* xrow, const float (&yr)[DC]) {
-    constexpr int G = feature_group<DC>();
-    const float4* q = reinterpret_cast<const float4*>(xrow);
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-#pragma unroll
-    for (int g0 = 0; g0 < DC / 4; g0 += G) {
-        float4 v[G];
-#pragma unroll
-        for (int k = 0; k < G; ++k) v[k] = q[g0 + k];
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int k = 0; k < G; ++k) {
-            const int d = 4 * (g0 + k);
-            const float d0 = v[k].x - yr[d], d1 = v[k].y - yr[d + 1];
-            const float d2 = v[k].z - yr[d + 2], d3 = v[k].w - yr[d + 3];
-            a0 = fmaf(d0, d0, a0);
-            a1 = fmaf(d1, d1, a1);
-            a2 = fmaf(d2, d2, a2);
-            a3 = fmaf(d3, d3, a3);
-        }
-    }
-    return (a0 + a1) + (a2 + a3);
-}
-
-// row `row` of a [rows][D] matrix into registers, zero past D
-template <int DC>
-__device__ __forceinline__ void load_feature_row(float (&xr)[DC], const float* base, int row,
-                                                 int D) {
-    const float* p = base + (size_t)row * D;
-#pragma unroll
-    for (int d = 0; d < DC; ++d) xr[d] = d < D ? p[d] : 0.0f;
-}
-
-// This lane's cells u in [U0, U1) of a forward chunk, (i0 + lane, t + u - lane), into
-// its slots of a cost tile (the layout the DMA path fills); columns are clamped into
-// the matrix and cells outside the element are masked by the sweep.  Two cells per
-// iteration of a rolled loop: unrolled over all P, the compiler would hoist every
-// cell's LDS reads and spill.
-template <int DC, int U0, int U1>
-__device__ __forceinline__ void fused_costs(float* tile, int tbase, const float (&xr)[DC],
-                                            const float* ylds, int t, int lane, int L2max) {
-    static_assert((U1 - U0) % 2 == 0, "cells come in pairs");
-#pragma unroll 1
-    for (int u = U0; u < U1; u += 2) {
-        const int j0 = min(max(t + u - lane, 0), L2max - 1);
-        const int j1 = min(max(t + u + 1 - lane, 0), L2max - 1);
-        const float c0 = sq_euclid<DC>(xr, ylds + j0 * (DC + 4));
-        const float c1 = sq_euclid<DC>(xr, ylds + j1 * (DC + 4));
-        tile[tbase + u] = c0;
-        tile[tbase + u + 1] = c1;
-    }
-}
-
-// the element's [L2max][D] rows of y into LDS rows of DC + 4 floats (zero past D);
-// the caller synchronises the workgroup after it
-template <int DC>
-__device__ __forceinline__ void stage_features(float* ylds, const float* yb, int L2max, int D) {
-    for (int idx = threadIdx.x; idx < L2max * DC; idx += NW * 64) {
-        const int j = idx / DC, d = idx % DC;
-        ylds[j * (DC + 4) + d] = d < D ? yb[(size_t)j * D + d] : 0.0f;
-    }
-}
-
-// Steps of a fused chunk whose costs a helper wave forms (HELP); the sweeping wave
-// forms the rest itself, just before its DP steps (the split balances the two waves'
-// instruction streams on their shared SIMD).
-constexpr int HELP_U = 12;
-
-// DC > 0: fused costs from fx [B, L1max, D] and fy [B, L2max, D] (costs unused).
-// HELP (fused, at most NW/2 stripes per part): wave NW/2 + l forms steps
-// [0, HELP_U) of every chunk of stripe l's costs into a double-buffered tile one chunk
-// ahead, publishing cprog[l] = chunks formed; it reuses a buffer once the sweeping
-// wave l has finished the chunk that read it (prog[l]).
 // HELP (costs from memory, unbanded, at most NW/2 stripes per part): wave NW/2 + l
 // loads stripe l's cost chunks one chunk ahead into wave l's tiles (cprog[l] = chunks
 // loaded) and writes each chunk's alpha rows to the table from a tile in its own,
 // otherwise unused, buffers once wave l has finished the chunk.
-template <int DC = 0, bool HELP = false>
+template <bool HELP = false>
 __global__ void __launch_bounds__(NW * 64)
 dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ lengths,
                    float* __restrict__ alpha_sk, float* __restrict__ brow,
                    float* __restrict__ value, int* __restrict__ status,
                    uint64_t* __restrict__ fflag, int B, int L1max, int L2max, int NSmax,
                    size_t elem_steps, float T, int bandwidth, int R, int G, int SPW,
-                   uint32_t epoch, const float* __restrict__ fx, const float* __restrict__ fy,
-                   int D) {
+                   uint32_t epoch) {
     constexpr int P = PF;
-    constexpr bool FUSED = DC > 0;
     static_assert(!HELP || P == 16, "the helper split assumes 16-step chunks");
     extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
@@ -188,8 +63,8 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
     const unsigned ul4 = (unsigned)lane * 4u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     using Tile = ChunkTile<P>;
-    // two cost chunks (fused without helpers: one, computed in place), two rows
-    constexpr int NTILE = (FUSED && !HELP) ? 1 : 2;
+    // two cost chunks, two rows
+    constexpr int NTILE = 2;
     constexpr int WBUF = NTILE * Tile::FLOATS + 2 * 64;
     float* tiles = smem + wave * WBUF;                     // double-buffered cost chunk
     float* rbufs = tiles + NTILE * Tile::FLOATS;           // boundary row of a chunk
@@ -198,7 +73,6 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
     const uint32_t fslot_lds = lds_address(fslot);
     float* rings = smem + NW * WBUF;                       // [NW][R]
     float* sink = rings + NW * R + wave * DUMMY;           // per-wave write sink
-    float* ylds = rings + NW * R + NW * DUMMY;             // fused: [L2max][DC + 4]
     int* st = status + b;
     const int tbase = Tile::read_base(lane);
 
@@ -210,7 +84,6 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
         if (G == 1) *st = 0;                               // G > 1: reset before the launch
         terminal = kPINF;
     }
-    if constexpr (FUSED) stage_features<DC>(ylds, fy + (size_t)b * L2max * D, L2max, D);
     __syncthreads();
 
     const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
@@ -235,7 +108,7 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
         return;
     }
 
-    if constexpr (HELP && !FUSED) {
+    if constexpr (HELP) {
         if (NL > NW / 2 || bandwidth >= 0) {   // never: the host picks HELP for these only
             if (threadIdx.x == 0) atomicOr(st, 2);
             return;
@@ -280,34 +153,6 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
         }
     }
 
-    if constexpr (HELP && FUSED) {
-        if (NL > NW / 2) {   // never: the host picks HELP for parts of at most NW/2 stripes
-            if (threadIdx.x == 0) atomicOr(st, 2);
-            return;
-        }
-        // helper of stripe l: its chunks' costs, steps [0, HELP_U), one chunk ahead
-        const int l = wave - NW / 2;
-        if (l >= 0 && l < NL) {
-            const int s = s_begin + l;
-            int t_lo, t_hi;
-            band_window(s, L1, L2, bw, t_lo, t_hi);
-            const int k_lo =
-                __builtin_amdgcn_readfirstlane(t_lo <= t_hi ? min(t_lo / P, nch) : nch);
-            const int k_end = __builtin_amdgcn_readfirstlane(t_lo <= t_hi ? t_hi / P + 1 : nch);
-            float xr[DC];
-            load_feature_row<DC>(xr, fx + (size_t)b * L1max * D, min(s * 64 + lane, L1max - 1),
-                                 D);
-            float* ctiles = smem + l * WBUF;   // stripe l's two cost tiles
-            for (int k = k_lo; k < k_end; ++k) {
-                // buffer k & 1 last held chunk k - 2: free once wave l has finished it
-                if (k >= k_lo + 2) wait_for(prog, l, l * PROG_STRIDE + k - 1, st);
-                fused_costs<DC, 0, HELP_U>(ctiles + (k & 1) * Tile::FLOATS, tbase, xr, ylds,
-                                           k * P, lane, L2max);
-                publish(cprog, l, k + 1);
-            }
-        }
-    }
-
     for (int l = wave; l < NL; l += NW) {
         const int s = s_begin + l;
         const int i0 = s * 64;
@@ -336,9 +181,6 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
         const bool x_in = l == 0 && part > 0;        // row above from the previous part
         const bool x_out = l == NL - 1 && has_next;  // last row feeds the next part
         int seen = -1;       // chunks of the previous part known to be complete
-        float xr[FUSED ? DC : 1];                    // fused: this lane's row of x
-        if constexpr (FUSED)
-            load_feature_row<DC>(xr, fx + (size_t)b * L1max * D, min(i0 + lane, L1max - 1), D);
         // the APAD steps before the window hold the column-0 / off-band boundary
         // (PINF), read by the reverse sweep; so does the chunk after it
 #pragma unroll
@@ -371,7 +213,7 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                 seen = wait_part(flag_in, epoch, min(k_lo + lead(P), nch), st);
                 issue_row(k_lo);
             }
-            if (!FUSED && !HELP)
+            if (!HELP)
                 dma_tile<P, 1>(tile_lds + (k_lo & 1) * Tile::FLOATS * 4, cbase, i0, L1max, L2max,
                                lane, k_lo * P);
         }
@@ -386,7 +228,7 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
             // stores of that chunk (the first chunk's load is the last issued).
             // HELP from memory: the helper loads the costs; this wave's own loads (the
             // row above of a part's first stripe) are followed by the last-row store
-            if (k == k_lo) wait_vmcnt<0>(); else if (HELP && !FUSED) wait_vmcnt<1>(); else wait_vmcnt<P>();
+            if (k == k_lo) wait_vmcnt<0>(); else if (HELP) wait_vmcnt<1>(); else wait_vmcnt<P>();
             if (x_in && k > k_lo) {
                 // its progress word, loaded one chunk ago before those stores
                 const int got = flag_chunks_lds(fslot, epoch);
@@ -394,14 +236,7 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
             }
             float* tile = tiles + (NTILE == 2 ? (k & 1) * Tile::FLOATS : 0);
             float cv[P];
-            if constexpr (HELP && !FUSED) {
-                wait_for(cprog, l, k + 1, st);   // the chunk's costs, loaded by the helper
-            } else if constexpr (HELP) {
-                wait_for(cprog, l, k + 1, st);   // the helper's steps [0, HELP_U)
-                fused_costs<DC, HELP_U, P>(tile, tbase, xr, ylds, t0, lane, L2max);
-            } else if constexpr (FUSED) {
-                fused_costs<DC, 0, P>(tile, tbase, xr, ylds, t0, lane, L2max);
-            }
+            if constexpr (HELP) wait_for(cprog, l, k + 1, st);   // loaded by the helper
 #pragma unroll
             for (int u = 0; u < P; ++u) cv[u] = tile[tbase + u];
             // lane 0's up values: column t0+j sits in lane j (row 0 is PINF; so are the
@@ -418,7 +253,7 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                     if (seen < need) seen = wait_part(flag_in, epoch, need, st);
                     issue_row(k + 1);
                 }
-                if (!FUSED && !HELP)
+                if (!HELP)
                     dma_tile<P, 1>(tile_lds + ((k + 1) & 1) * Tile::FLOATS * 4, cbase, i0, L1max,
                                    L2max, lane, t0 + P);
                 if (x_in) flag_load_lds(flag_in, fslot_lds, lane);
@@ -447,7 +282,7 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                 const int col = t - lane;
                 const bool ok = FULL || ((unsigned)col < (unsigned)L2eff && in_band(ej, col + 1, bw));
                 cur = ok ? a : kPINF;
-                if (HELP && !FUSED) atile[u * 64] = cur;
+                if (HELP) atile[u * 64] = cur;
                 else lane_store(outc + u * 64, ul4, cur);
                 pub[u] = cur;
                 if (ok && last_row && col == L2 - 1) terminal = cur;
@@ -465,11 +300,11 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
             }
             publish(prog, wave, l * PROG_STRIDE + k + 1);
             if (x_out && k >= 2) {
-                // at least P loads (none when fused) and 2P + 2 stores follow the row
-                // store of chunk k - 2 (HELP from memory: the last-row stores of chunks
-                // k - 1 and k): it (and everything before) is complete
-                if constexpr (HELP && !FUSED) wait_vmcnt<2>();
-                else wait_vmcnt<(FUSED ? 2 * P + 2 : 3 * P + 2)>();
+                // at least P loads and 2P + 2 stores follow the row store of chunk k - 2
+                // (HELP from memory: the last-row stores of chunks k - 1 and k): it (and
+                // everything before) is complete
+                if constexpr (HELP) wait_vmcnt<2>();
+                else wait_vmcnt<3 * P + 2>();
                 if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
             }
         }
@@ -956,13 +791,12 @@ int launch_forward(const float* costs, const int* lengths, int B, int max_L1, in
     // helper waves for unbanded parts of at most NW/2 stripes (waves NW/2.. would idle)
     const int part_stripes = sp.G > 1 ? sp.SPW : ns;
     const bool help = bandwidth < 0 && part_stripes <= NW / 2 && dtw_helpers_enabled();
-    auto kern = help ? dtw_forward_kernel<0, true> : dtw_forward_kernel<0, false>;
+    auto kern = help ? dtw_forward_kernel<true> : dtw_forward_kernel<false>;
     D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds));
     D2P_LAUNCH("dtw_forward", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64),
                lds, st, costs, lengths, ws.alpha_sk, ws.brow, value, ws.status, ws.fflag, B,
-               max_L1, max_L2, ns, ws.elem_steps, T, bandwidth, R, sp.G, sp.SPW, next_epoch(),
-               nullptr, nullptr, 0);
+               max_L1, max_L2, ns, ws.elem_steps, T, bandwidth, R, sp.G, sp.SPW, next_epoch());
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }
@@ -980,162 +814,10 @@ int launch_backward(const int* lengths, int B, int max_L1, int max_L2, float T,
                                 st, sp, R);
 }
 
-// ---------------------------------------------------------------- fused costs
-
-// Feature padding of the fused forward: D rounded up to 32, 64 or 128 (0: too wide).
-int feature_chunk(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 0; }
-
-size_t feature_lds(int max_L2, int DC) { return (size_t)max_L2 * (DC + 4) * sizeof(float); }
-
-// LDS of a fused forward workgroup with ntile cost tiles per wave (2: helper waves)
-size_t lds_forward_fused(int R, int DC, int max_L2, int ntile = 1) {
-    return (size_t)NW * (ntile * 65 * PF + 2 * 64) * sizeof(float) +
-           ((size_t)NW * R + NW * DUMMY) * sizeof(float) + feature_lds(max_L2, DC);
-}
-
-// D2P_AMD_FUSED_HELPERS=0 turns the helper waves off (for tests: both forms must agree)
-bool force_no_helpers() {
-    const char* e = std::getenv("D2P_AMD_FUSED_HELPERS");
-    return e && e[0] == '0';
-}
-
-int check_fused(int B, int max_L1, int max_L2, int D, float T) {
-    D2P_TRY(check_shape(B, max_L1, max_L2, T));
-    D2P_REQUIRE(D >= 1 && feature_chunk(D) > 0, "feature dimension D must be between 1 and 128");
-    const int DC = feature_chunk(D);
-    D2P_REQUIRE(lds_forward_fused(ring_forward(64 * NW, max_L2), DC, max_L2) <= kLdsLimit,
-                "fused DTW: max_L2 * (D + 4) floats of y do not fit in LDS beside the stripe rings");
-    return D2P_OK;
-}
-
-template <int DC>
-int launch_fused(const float* x, const float* y, const int* lengths, int B, int max_L1,
-                 int max_L2, int D, float T, int bandwidth, const Layout& ws, float* value,
-                 float* marginals, float* grad_T, hipStream_t st) {
-    // forward: unsplit when the rings and y fit, else parts of at most NW stripes
-    const int ns = (max_L1 + 63) / 64;
-    const bool whole = lds_forward_fused(ring_forward(max_L1, max_L2), DC, max_L2) <= kLdsLimit;
-    const Split sp = choose_split(B, max_L1, ws, whole ? 0 : NW);
-    const int R = ring_forward(sp.G > 1 ? sp.SPW * 64 : max_L1, max_L2);
-    // helper waves form most of each chunk's costs when a part has at most NW/2
-    // stripes (the other waves are idle) and two cost tiles per wave fit
-    const int part_stripes = sp.G > 1 ? sp.SPW : ns;
-    const bool help = part_stripes <= NW / 2 &&
-                      lds_forward_fused(R, DC, max_L2, 2) <= kLdsLimit && !force_no_helpers();
-    const size_t lds = lds_forward_fused(R, DC, max_L2, help ? 2 : 1);
-    D2P_REQUIRE(lds <= kLdsLimit, "fused DTW: sequence too long for LDS");
-    if (sp.G > 1 && launch_split_reset(ws, B, sp.G, st) != D2P_OK) return D2P_ERR_HIP;
-    auto kern = help ? dtw_forward_kernel<DC, true> : dtw_forward_kernel<DC, false>;
-    D2P_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds));
-    D2P_LAUNCH("dtw_fused_forward", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64), lds, st,
-               nullptr, lengths, ws.alpha_sk, ws.brow, value, ws.status, ws.fflag, B, max_L1,
-               max_L2, ns, ws.elem_steps, T, bandwidth, R, sp.G, sp.SPW, next_epoch(), x, y, D);
-    D2P_HIP(hipGetLastError());
-    // the reverse sweep reads only the alpha table: the plain one
-    return launch_backward(lengths, B, max_L1, max_L2, T, bandwidth, ws, marginals, grad_T, st);
-}
-
-// costs[b, i, j] = sum_d (x[b,i,d] - y[b,j,d])^2 with the fused forward's arithmetic:
-// one thread per column (its row of y in registers), SQDIST_COLS columns and
-// SQDIST_ROWS rows of x (in LDS, read as broadcasts) per tile.  Workgroups stride over
-// the batch (grid z) and the row tiles (grid y), so any B and L1 fit the grid limits.
-constexpr int SQDIST_ROWS = 32;
-constexpr int SQDIST_COLS = 256;
-constexpr int SQDIST_GRID_MAX = 65535;   // grid y and z extents
-
-template <int DC>
-__global__ void __launch_bounds__(SQDIST_COLS)
-pairwise_sqdist_kernel(const float* __restrict__ x, const float* __restrict__ y,
-                       float* __restrict__ costs, int B, int L1, int L2, int D) {
-    __shared__ __align__(16) float xs[SQDIST_ROWS * DC];
-    const int j0 = blockIdx.x * SQDIST_COLS;
-    const int ncol = min(SQDIST_COLS, L2 - j0);
-    for (int b = blockIdx.z; b < B; b += gridDim.z) {
-        float yr[DC];   // this thread's column (threads past the last column repeat it)
-        load_feature_row<DC>(yr, y + (size_t)b * L2 * D, j0 + min((int)threadIdx.x, ncol - 1), D);
-        for (int i0 = blockIdx.y * SQDIST_ROWS; i0 < L1; i0 += gridDim.y * SQDIST_ROWS) {
-            const int nrow = min(SQDIST_ROWS, L1 - i0);
-            const float* xb = x + ((size_t)b * L1 + i0) * D;
-            __syncthreads();   // the previous tile's reads of xs are complete
-            for (int idx = threadIdx.x; idx < nrow * DC; idx += SQDIST_COLS) {
-                const int r = idx / DC, d = idx % DC;
-                xs[idx] = d < D ? xb[(size_t)r * D + d] : 0.0f;
-            }
-            __syncthreads();
-            if ((int)threadIdx.x < ncol) {
-                float* out = costs + ((size_t)b * L1 + i0) * L2 + j0 + threadIdx.x;
-#pragma unroll 1
-                for (int r = 0; r < nrow; ++r) out[(size_t)r * L2] = sq_euclid_xl<DC>(xs + r * DC, yr);
-            }
-        }
-    }
-}
-
 }  // namespace dtw
 }  // namespace d2p_amd
 
 using namespace d2p_amd;
-
-extern "C" int d2p_dtw_sqeuclid_forward_marginals(const float* x, const float* y,
-                                                  const int* lengths, int B, int max_L1,
-                                                  int max_L2, int D, float temperature,
-                                                  int bandwidth, float* value, float* marginals,
-                                                  float* grad_T, void* workspace,
-                                                  size_t workspace_bytes, void* stream) {
-    D2P_TRY(dtw::check_fused(B, max_L1, max_L2, D, temperature));
-    if (B == 0) return D2P_OK;
-    D2P_REQUIRE(x && y && value && marginals && grad_T, "null pointer argument");
-    const size_t need = d2p_dtw_workspace_bytes_banded(B, max_L1, max_L2, bandwidth);
-    D2P_REQUIRE(workspace && workspace_bytes >= need, "workspace too small");
-    hipStream_t st = (hipStream_t)stream;
-    const wf::Layout ws = wf::layout(workspace, B, max_L1, max_L2, 1, true, 8,
-                                     dtw::band_elem_steps(max_L1, max_L2, bandwidth));
-    switch (dtw::feature_chunk(D)) {
-        case 32:
-            D2P_TRY(dtw::launch_fused<32>(x, y, lengths, B, max_L1, max_L2, D, temperature,
-                                          bandwidth, ws, value, marginals, grad_T, st));
-            break;
-        case 64:
-            D2P_TRY(dtw::launch_fused<64>(x, y, lengths, B, max_L1, max_L2, D, temperature,
-                                          bandwidth, ws, value, marginals, grad_T, st));
-            break;
-        default:
-            D2P_TRY(dtw::launch_fused<128>(x, y, lengths, B, max_L1, max_L2, D, temperature,
-                                           bandwidth, ws, value, marginals, grad_T, st));
-    }
-    return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr, value,
-                             grad_T, nullptr, nullptr, st);
-}
-
-extern "C" int d2p_pairwise_sqdist(const float* x, const float* y, int B, int L1, int L2, int D,
-                                   float* costs, void* stream) {
-    D2P_REQUIRE(B >= 0 && L1 >= 0 && L2 >= 0, "negative dimension");
-    D2P_REQUIRE(D >= 1 && dtw::feature_chunk(D) > 0, "feature dimension D must be between 1 and 128");
-    if (B == 0 || L1 == 0 || L2 == 0) return D2P_OK;
-    D2P_REQUIRE(x && y && costs, "null pointer argument");
-    hipStream_t st = (hipStream_t)stream;
-    const int DC = dtw::feature_chunk(D), CB = dtw::SQDIST_COLS;
-    // (the kernel strides over batch elements and row tiles beyond the grid extents)
-    const dim3 grid((L2 + CB - 1) / CB,
-                    std::min((L1 + dtw::SQDIST_ROWS - 1) / dtw::SQDIST_ROWS, dtw::SQDIST_GRID_MAX),
-                    std::min(B, dtw::SQDIST_GRID_MAX));
-    switch (DC) {
-        case 32:
-            D2P_LAUNCH("pairwise_sqdist", dtw::pairwise_sqdist_kernel<32>, grid, dim3(CB), 0, st,
-                       x, y, costs, B, L1, L2, D);
-            break;
-        case 64:
-            D2P_LAUNCH("pairwise_sqdist", dtw::pairwise_sqdist_kernel<64>, grid, dim3(CB), 0, st,
-                       x, y, costs, B, L1, L2, D);
-            break;
-        default:
-            D2P_LAUNCH("pairwise_sqdist", dtw::pairwise_sqdist_kernel<128>, grid, dim3(CB), 0, st,
-                       x, y, costs, B, L1, L2, D);
-    }
-    D2P_HIP(hipGetLastError());
-    return D2P_OK;
-}
 
 extern "C" size_t d2p_dtw_workspace_bytes_banded(int B, int max_L1, int max_L2, int bandwidth) {
     if (B <= 0 || max_L1 < 0 || max_L2 < 0) return 0;

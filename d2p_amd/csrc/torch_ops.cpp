@@ -1209,6 +1209,35 @@ Tensor pairwise_sqdist(Tensor x, Tensor y) {
     return out;
 }
 
+// (grad_x, grad_y) through the squared-Euclidean costs from G = dL/dcosts and an
+// optional per-element factor scale [B]
+std::tuple<Tensor, Tensor> sqeuclid_feature_grad(Tensor G, Tensor x, Tensor y,
+                                                 c10::optional<Tensor> scale) {
+    CHECK_INPUT_DEV(G);
+    CHECK_INPUT_DEV(x);
+    CHECK_INPUT_DEV(y);
+    Dims d = checked_dims_xy(x, y);
+    TORCH_CHECK(G.dim() == 3 && G.size(0) == d.B && G.size(1) == d.L1 && G.size(2) == d.L2,
+                "G must be [B, L1, L2] = [", d.B, ", ", d.L1, ", ", d.L2, "]");
+    TORCH_CHECK(G.device() == x.device(), "G must be on same device as x");
+    const float* sp = nullptr;
+    Tensor sc;
+    if (scale.has_value()) {
+        sc = scale->contiguous();
+        TORCH_CHECK(sc.scalar_type() == torch::kFloat32 && sc.numel() == d.B &&
+                        sc.device() == x.device(),
+                    "scale must be a float32 [B] tensor on x's device");
+        sp = sc.data_ptr<float>();
+    }
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    Tensor gx = torch::empty_like(x), gy = torch::empty_like(y);
+    D2P_CALL(d2p_sqeuclid_feature_grad(G.data_ptr<float>(), x.data_ptr<float>(),
+                                       y.data_ptr<float>(), sp, d.B, d.L1, d.L2,
+                                       (int)x.size(2), gx.data_ptr<float>(),
+                                       gy.data_ptr<float>(), current_stream()));
+    return {gx, gy};
+}
+
 TORCH_LIBRARY(d2p, m) {
     // /root/reference/src/sw/registry.cpp:30-44
     m.def("soft_sw(Tensor scores, Tensor gap, Tensor temperature, Tensor lengths) -> Tensor[]");
@@ -1405,14 +1434,17 @@ TORCH_LIBRARY(d2p_amd, m) {
     m.def("soft_dtw_sqeuclidean(Tensor x, Tensor y, float temperature, Tensor? lengths, "
           "int bandwidth) -> (Tensor, Tensor, Tensor)");
     m.def("pairwise_sqdist(Tensor x, Tensor y) -> Tensor");
+    m.def("sqeuclid_feature_grad(Tensor G, Tensor x, Tensor y, Tensor? scale) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(d2p_amd, CUDA, m) {
     m.impl("soft_dtw_sqeuclidean", dtw_sqeuclid);
     m.impl("pairwise_sqdist", pairwise_sqdist);
+    m.impl("sqeuclid_feature_grad", sqeuclid_feature_grad);
 }
 
 TORCH_LIBRARY_IMPL(d2p_amd, CPU, m) {
     m.impl("soft_dtw_sqeuclidean", torch::CppFunction::makeFromBoxedFunction<&cpu_boxed>());
     m.impl("pairwise_sqdist", torch::CppFunction::makeFromBoxedFunction<&cpu_boxed>());
+    m.impl("sqeuclid_feature_grad", torch::CppFunction::makeFromBoxedFunction<&cpu_boxed>());
 }

@@ -7,8 +7,8 @@ no Sakoe-Chiba band and is passed to the operators as -1 (``d2p/dtw.py:98``).
 ``soft_dtw_sqeuclidean(x, y)`` has no counterpart in the reference: it is soft DTW
 over the squared-Euclidean costs ``sum_d (x_i - y_j)^2`` that callers otherwise build
 with ``torch.cdist(x, y) ** 2`` (/root/reference/docs/algorithms/dtw.md:52), with the
-costs formed inside the HIP forward sweep, so no [B, L1, L2] cost matrix is written or
-read.
+costs formed on the matrix cores into the alignment buffer (which the forward sweep
+reads and the reverse sweep overwrites), so no [B, L1, L2] memory beyond the outputs.
 """
 from __future__ import annotations
 
@@ -97,11 +97,12 @@ class _SoftDTWSqEuclidean(torch.autograd.Function):
 
     Backward: the cost gradient G is grad_value[b] * alignment (value path) plus,
     when the alignment itself receives a gradient, soft_dtw_backward_full over the
-    cost matrix (formed by d2p_amd::pairwise_sqdist, bit-identical to the forward
-    sweep's costs); then dL/dx_i = 2 (rowsum(G)_i x_i - (G y)_i) and dL/dy_j = 2 (colsum(G)_j y_j
-    - (G^T x)_j), two float32 batched GEMMs.  On the value path alone G is a per-element
-    multiple of the alignment, so the sums and GEMMs run on the alignment itself and
-    the [B, L, D] results are scaled: no [B, L1, L2] temporary or transposed copy."""
+    cost matrix (formed by d2p_amd::pairwise_sqdist, bit-identical to the op's own
+    costs); then dL/dx_i = 2 (rowsum(G)_i x_i - (G y)_i) and dL/dy_j = 2 (colsum(G)_j y_j
+    - (G^T x)_j) in one kernel (d2p_amd::sqeuclid_feature_grad, the products on the
+    matrix cores).  On the value path alone G is a per-element multiple of the
+    alignment, so the kernel reads the alignment itself with the per-element factor:
+    no [B, L1, L2] temporary."""
 
     @staticmethod
     def forward(ctx, x, y, temperature, lengths, bandwidth, t_tensor):
@@ -131,14 +132,13 @@ class _SoftDTWSqEuclidean(torch.autograd.Function):
             scale = None
             gT = gt2 if gT is None else gT + gt2
         gx = gy = None
-        if M is not None:
-            f = 2.0 * scale[:, None, None] if scale is not None else 2.0
-            if ctx.needs_input_grad[0]:
-                gx = f * (x * M.sum(dim=2, keepdim=True) - torch.bmm(M, y))
-            if ctx.needs_input_grad[1]:
-                # (M^T x) as (x^T M)^T: both GEMM operands stay row-major
-                xtm = torch.bmm(x.transpose(1, 2).contiguous(), M)
-                gy = f * (y * M.sum(dim=1)[:, :, None] - xtm.transpose(1, 2))
+        if M is not None and (ctx.needs_input_grad[0] or ctx.needs_input_grad[1]):
+            # dL/dx = 2 s (x rowsum(M) - M y), dL/dy = 2 s (y colsum(M) - M^T x): one
+            # kernel, the products on the matrix cores
+            s = scale.float().contiguous() if scale is not None else None
+            gx, gy = torch.ops.d2p_amd.sqeuclid_feature_grad(M.contiguous(), x, y, s)
+            gx = gx if ctx.needs_input_grad[0] else None
+            gy = gy if ctx.needs_input_grad[1] else None
         g_temp = gT if ctx.needs_input_grad[5] else None
         return gx, gy, None, None, None, g_temp
 
@@ -147,12 +147,12 @@ def soft_dtw_sqeuclidean(x: torch.Tensor, y: torch.Tensor,
                          temperature: Union[float, torch.Tensor] = 1.0, bandwidth: int = 0,
                          lengths: Optional[torch.Tensor] = None) -> DTWResult:
     """Soft DTW between feature sequences x [B, L1, D] and y [B, L2, D] (1 <= D <= 128)
-    under the squared-Euclidean cost, formed inside the forward sweep.
+    under the squared-Euclidean cost |x_i|^2 + |y_j|^2 - 2 x_i . y_j (clamped at 0),
+    with the dot products on the matrix cores.
 
     Same result as ``soft_dtw(torch.cdist(x, y) ** 2, ...)`` up to the rounding of the
-    costs (each a sum of D squares in float32); gradients flow to x, y and a tensor
-    temperature.  The element's y rows are staged in LDS: max_L2 * (D + 4) floats must
-    fit beside the stripe rings (about max_L2 <= 450 for D = 64).
+    costs (torch.cdist takes the same expansion at these sizes); gradients flow to x, y
+    and a tensor temperature.
     """
     _validate_temperature(temperature)
     bw = bandwidth if bandwidth > 0 else -1

@@ -322,32 +322,45 @@ size_t d2p_dtw_workspace_bytes(int B, int max_L1, int max_L2);
  * full (L1+1) x (L2+1) tables, /root/reference/src/dtw/torch_cuda.cpp:166-169). */
 size_t d2p_dtw_workspace_bytes_banded(int B, int max_L1, int max_L2, int bandwidth);
 
-/* Fused squared-Euclidean costs + soft DTW: the forward value and marginals of soft
- * DTW over c[b,i,j] = sum_d (x[b,i,d] - y[b,j,d])^2, formed inside the forward sweep
- * from the features instead of read from a cost matrix (the reverse sweep needs no
- * costs).  No counterpart in the reference:
- * its callers build the costs with torch.cdist(x, y) ** 2
- * (/root/reference/docs/algorithms/dtw.md:52) and its sweeps read them
- * (/root/reference/src/dtw/kernels.cu:55-114); this entry point removes that
- * [B, L1, L2] matrix.  The DP, outputs, lengths and band rules are those of
- * d2p_dtw_forward_marginals (same workspace, d2p_dtw_workspace_bytes_banded).
+/* Squared-Euclidean costs + soft DTW: the forward value and marginals of soft DTW
+ * over c[b,i,j] = max(|x_i|^2 + |y_j|^2 - 2 x_i . y_j, 0) (the dot products on the
+ * matrix cores), formed from the features by d2p_pairwise_sqdist's kernel into the
+ * marginals buffer, read there by the forward sweep and overwritten by the reverse
+ * sweep (which reads only the alpha table): no [B, L1, L2] memory beyond the outputs.
+ * No counterpart in the reference: its callers build the costs with
+ * torch.cdist(x, y) ** 2 (/root/reference/docs/algorithms/dtw.md:52; the same
+ * expansion at these sizes) and its sweeps read them
+ * (/root/reference/src/dtw/kernels.cu:55-114).  The DP, outputs, lengths and band
+ * rules are those of d2p_dtw_forward_marginals (same workspace,
+ * d2p_dtw_workspace_bytes_banded).
  *   x [B, max_L1, D], y [B, max_L2, D]  inputs, 1 <= D <= 128
- *   value [B], marginals [B, max_L1, max_L2] (= dvalue/dcosts), grad_T [B]
- * Limit: max_L2 * (D rounded up to 32, 64 or 128, plus 4) floats of y must fit in
- * LDS beside the stripe rings (about max_L2 <= 450 for D = 64). */
+ *   value [B], marginals [B, max_L1, max_L2] (= dvalue/dcosts), grad_T [B] */
 int d2p_dtw_sqeuclid_forward_marginals(const float* x, const float* y, const int* lengths, int B,
                                        int max_L1, int max_L2, int D, float temperature,
                                        int bandwidth, float* value, float* marginals,
                                        float* grad_T, void* workspace, size_t workspace_bytes,
                                        void* stream);
 
-/* costs[b,i,j] = sum_d (x[b,i,d] - y[b,j,d])^2 with exactly the arithmetic of the fused
- * sweeps above (bit-identical costs), for callers that need the matrix itself (the
- * fused op's marginal-path backward).  No counterpart in the reference (see above).
- *   x [B, L1, D], y [B, L2, D], costs [B, L1, L2]; 1 <= D <= 128 (any B and L1: the
- *   kernel strides over batch elements and row tiles past the grid limits) */
+/* costs[b,i,j] = max(|x_i|^2 + |y_j|^2 - 2 x_i . y_j, 0), the costs of the entry point
+ * above bit for bit, for callers that need the matrix itself (the op's marginal-path
+ * backward).  Within (D + 4) u (|x_i| + |y_j|)^2 (u = 2^-24) of the exact squared
+ * distance.  No counterpart in the reference (see above).
+ *   x [B, L1, D], y [B, L2, D], costs [B, L1, L2]; 1 <= D <= 128 (any B, L1 and L2:
+ *   the kernel strides over batch elements and tiles past the grid limits) */
 int d2p_pairwise_sqdist(const float* x, const float* y, int B, int L1, int L2, int D,
                         float* costs, void* stream);
+
+/* Gradients into the features through the costs above, from G = dL/dc [B, L1, L2]:
+ *   grad_x[b,i] = 2 s_b (x_i sum_j G[b,i,j] - sum_j G[b,i,j] y_j)
+ *   grad_y[b,j] = 2 s_b (y_j sum_i G[b,i,j] - sum_i G[b,i,j] x_i)
+ * with s_b = scale[b] (scale may be null: s_b = 1), the products on the matrix cores.
+ * No counterpart in the reference, whose callers leave this to torch's autograd of
+ * torch.cdist(x, y) ** 2 (/root/reference/docs/algorithms/dtw.md:52).
+ *   G [B, L1, L2], x [B, L1, D], y [B, L2, D], scale [B] or null
+ *   grad_x [B, L1, D], grad_y [B, L2, D]; 1 <= D <= 128 */
+int d2p_sqeuclid_feature_grad(const float* G, const float* x, const float* y,
+                              const float* scale, int B, int L1, int L2, int D, float* grad_x,
+                              float* grad_y, void* stream);
 
 /* Forward value and alignment marginals in one call.
  * Replaces the pair dtw_forward + dtw_backward (/root/reference/src/dtw/kernels.cuh:95-129)

@@ -57,6 +57,7 @@ SIGNATURES = {
     "d2p_dtw_sqeuclid_forward_marginals": (_i, [_p, _p, _p, _i, _i, _i, _i, _f, _i, _p, _p,
                                                 _p, _p, _z, _p]),
     "d2p_pairwise_sqdist": (_i, [_p, _p, _i, _i, _i, _i, _p, _p]),
+    "d2p_sqeuclid_feature_grad": (_i, [_p, _p, _p, _p, _i, _i, _i, _i, _p, _p, _p]),
     "d2p_dtw_second_workspace_bytes": (_z, [_i, _i, _i]),
     "d2p_dtw_second_workspace_bytes_banded": (_z, [_i, _i, _i, _i]),
     "d2p_dtw_hvp": (_i, [_p, _p, _p, _i, _i, _i, _f, _i, _p, _p, _z, _p]),
@@ -391,6 +392,18 @@ def dtw_sqeuclid_forward_marginals(x, y, lengths, T, bandwidth=-1):
                                                    nbytes, stream()))
     _check_status(ws, B)
     return tuple(outs)
+
+
+def sqeuclid_feature_grad(G, x, y, scale=None):
+    import torch
+    B, L1, D = x.shape
+    L2 = y.shape[1]
+    gx = torch.empty_like(x)
+    gy = torch.empty_like(y)
+    check(lib().d2p_sqeuclid_feature_grad(ptr(G), ptr(x), ptr(y),
+                                          ptr(scale) if scale is not None else None, B, L1,
+                                          L2, D, ptr(gx), ptr(gy), stream()))
+    return gx, gy
 
 
 def pairwise_sqdist(x, y):

@@ -1,11 +1,13 @@
-"""Fused squared-Euclidean costs + soft DTW (d2p_amd.soft_dtw_sqeuclidean).
+"""Squared-Euclidean costs + soft DTW from features (d2p_amd.soft_dtw_sqeuclidean).
 
 No counterpart in the reference (its callers build torch.cdist(x, y) ** 2 first,
 /root/reference/docs/algorithms/dtw.md:52).  Pinned three ways:
-- the costs: d2p_amd::pairwise_sqdist (the fused forward's own arithmetic) within the
-  summation bound (D + 2) u sum_d (x - y)^2 (u = 2^-24) of the exact float64 costs,
-  and against torch.cdist(x, y, compute_mode="donot_use_mm_for_euclid_dist") ** 2
-  within twice that bound (both are float32 sums of D squares, in different orders);
+- the costs: d2p_amd::pairwise_sqdist (the op's own costs, |x|^2 + |y|^2 - 2 x.y with
+  the dot products on the matrix cores, clamped at 0) within the expansion's bound
+  (D + 4) u (|x_i| + |y_j|)^2 (u = 2^-24) of the exact float64 costs, and against
+  torch.cdist(x, y, compute_mode="donot_use_mm_for_euclid_dist") ** 2 within that bound
+  plus the direct sum's own (D + 2) u c (torch.cdist's default mode takes the same
+  expansion at these sizes);
 - the sweeps: the fused op against soft_dtw on the kernel's own costs, bit for bit
   (the same costs feed the same forward recurrence, and both run the one reverse
   sweep, which reads only the alpha table); and those results against the CPU oracle
@@ -53,11 +55,13 @@ def test_pairwise_sqdist_bounds(cuda, B, L1, L2, D):
     got = torch.ops.d2p_amd.pairwise_sqdist(x.to(cuda), y.to(cuda)).cpu().double()
     assert torch.equal(got.float(), _capi.pairwise_sqdist(x.to(cuda), y.to(cuda)).cpu())
     exact = _exact_costs(x, y)
-    bound = (D + 2) * U * exact + 1e-30
+    nx = x.double().norm(dim=2)[:, :, None]
+    ny = y.double().norm(dim=2)[:, None, :]
+    bound = (D + 4) * U * (nx + ny) ** 2 + 1e-30
     assert torch.all((got - exact).abs() <= bound), float(((got - exact).abs() / bound).max())
     cd = torch.cdist(x.to(cuda), y.to(cuda), compute_mode="donot_use_mm_for_euclid_dist") ** 2
     err = (got - cd.cpu().double()).abs()
-    assert torch.all(err <= 2 * bound + 1e-6), float(err.max())
+    assert torch.all(err <= bound + (D + 2) * U * exact + 1e-6), float(err.max())
     print(f"costs: max |kernel - exact| / bound = {float(((got - exact).abs() / bound).max()):.2f},"
           f" max |kernel - cdist^2| = {float(err.max()):.2e}")
 
@@ -111,14 +115,14 @@ def test_fused_ragged_and_split(cuda, parts):
 @pytest.mark.parametrize("B,L1,L2,D,n_parts", [(4, 256, 256, 64, 1), (2, 700, 110, 24, 4),
                                                (1, 200, 130, 128, 1), (3, 64, 90, 5, 1)])
 def test_fused_helper_waves_bit_identical(cuda, parts, monkeypatch, B, L1, L2, D, n_parts):
-    """Parts of at most four stripes form most of each chunk's costs in helper waves;
-    a cell's cost is the same arithmetic whichever wave forms it, so every output
-    equals the single-wave form bit for bit (split parts included)."""
+    """Parts of at most four stripes move their data in helper waves in both sweeps;
+    the arithmetic is unchanged, so every output equals the single-wave form bit for
+    bit (split parts included)."""
     x, y = _seeded(31, (B, L1, D)).to(cuda), _seeded(32, (B, L2, D)).to(cuda)
     parts(n_parts)
-    monkeypatch.setenv("D2P_AMD_FUSED_HELPERS", "1")
+    monkeypatch.setenv("D2P_AMD_DTW_HELPERS", "1")
     with_h = _capi.dtw_sqeuclid_forward_marginals(x, y, None, 0.3)
-    monkeypatch.setenv("D2P_AMD_FUSED_HELPERS", "0")
+    monkeypatch.setenv("D2P_AMD_DTW_HELPERS", "0")
     without = _capi.dtw_sqeuclid_forward_marginals(x, y, None, 0.3)
     for a, b in zip(with_h, without):
         assert torch.equal(a, b)
@@ -134,9 +138,16 @@ def test_fused_rejects_bad_inputs(cuda):
     with pytest.raises(RuntimeError, match="between 1 and 128"):
         d2p_amd.soft_dtw_sqeuclidean(torch.randn(1, 4, 129, device=cuda),
                                      torch.randn(1, 4, 129, device=cuda))
-    with pytest.raises(RuntimeError, match="do not fit in LDS"):
-        d2p_amd.soft_dtw_sqeuclidean(torch.randn(1, 4, 64, device=cuda),
-                                     torch.randn(1, 5000, 64, device=cuda))
+
+
+
+def test_fused_long_sequences(cuda):
+    """No length limit beyond the sweeps' own: the costs are not staged in LDS."""
+    import d2p_amd
+    x, y = _seeded(41, (2, 300, 64)).to(cuda), _seeded(42, (2, 5000, 64)).to(cuda)
+    f = d2p_amd.soft_dtw_sqeuclidean(x, y, temperature=0.5)
+    p = d2p_amd.soft_dtw(torch.ops.d2p_amd.pairwise_sqdist(x, y), temperature=0.5)
+    assert torch.equal(f.cost, p.cost) and torch.equal(f.alignment, p.alignment)
 
 
 def _grad_refs(x, y, T, W=None):
@@ -202,3 +213,32 @@ def test_fused_temperature_gradient_and_autocast(cuda):
     ref = d2p_amd.soft_dtw_sqeuclidean(x.to(cuda).bfloat16().float(),
                                        y.to(cuda).bfloat16().float(), 0.8)
     assert torch.equal(rb.cost, ref.cost)
+
+
+@pytest.mark.parametrize("B,L1,L2,D,scaled", [(2, 256, 256, 64, True), (3, 70, 130, 5, False),
+                                              (1, 1, 200, 128, True), (2, 65, 1, 32, False),
+                                              (1, 300, 90, 100, True), (2, 64, 64, 1, False)])
+def test_feature_grad_kernel(cuda, B, L1, L2, D, scaled):
+    """d2p_amd::sqeuclid_feature_grad (one kernel, the products on the matrix cores)
+    against the chain rule in float64: within the summation bound (K + 4) u |f|
+    (|x_i| sum_j |G_ij| + sum_j |G_ij| |y_j|) per entry (K the contraction length),
+    and equal to the C ABI entry point bit for bit."""
+    import d2p_amd  # noqa: F401
+    G, x, y = _seeded(51, (B, L1, L2)), _seeded(52, (B, L1, D)), _seeded(53, (B, L2, D))
+    s = _seeded(54, (B,)) if scaled else None
+    args = [G.to(cuda), x.to(cuda), y.to(cuda), s.to(cuda) if scaled else None]
+    gx, gy = torch.ops.d2p_amd.sqeuclid_feature_grad(*args)
+    cx, cy = _capi.sqeuclid_feature_grad(*args)
+    assert torch.equal(gx, cx) and torch.equal(gy, cy)
+    G64, x64, y64 = G.double(), x.double(), y.double()
+    f = 2.0 * (s.double() if scaled else torch.ones(B, dtype=torch.float64))[:, None, None]
+    ex = f * (x64 * G64.sum(2, keepdim=True) - torch.bmm(G64, y64))
+    ey = f * (y64 * G64.sum(1)[:, :, None] - torch.bmm(G64.transpose(1, 2), x64))
+    aG = G64.abs()
+    bx = (L2 + 4) * U * f.abs() * (x64.abs() * aG.sum(2, keepdim=True) + torch.bmm(aG, y64.abs()))
+    by = (L1 + 4) * U * f.abs() * (y64.abs() * aG.sum(1)[:, :, None] +
+                                   torch.bmm(aG.transpose(1, 2), x64.abs()))
+    for got, exact, bound, what in ((gx, ex, bx, "dL/dx"), (gy, ey, by, "dL/dy")):
+        err = (got.cpu().double() - exact).abs()
+        assert torch.all(err <= bound + 1e-30), (what, float((err / (bound + 1e-30)).max()))
+        print(f"{what}: max err / bound {float((err / (bound + 1e-30)).max()):.3f}")
