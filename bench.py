@@ -209,7 +209,8 @@ def make_c4xy(fused):
             # (alignment out), the costs passing through the alignment buffer
             algo_step=2 * feat + 8 * cells + 2 * feat,
             algo_kernel={"pairwise_sqdist": 2 * feat + 4 * cells, "dtw_forward": 4 * cells,
-                         "dtw_backward": 4 * cells},
+                         "dtw_backward": 4 * cells,
+                         "sqeuclid_feature_grad": 4 * cells + 4 * feat},
             workload="C4 fused: soft_dtw_sqeuclidean(x, y, T=0.1), x, y [512,256,64] "
                      "(costs on the matrix cores), fwd + cost.sum().backward() into x, y",
             extra={"B": B, "L1": L, "L2": L, "D": D, "temperature": 0.1})
