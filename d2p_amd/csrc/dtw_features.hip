@@ -226,29 +226,56 @@ int launch_sqdist(const float* x, const float* y, float* costs, int B, int L1, i
 //   dL/dy_j = 2 s_b (y_j sum_i G_ij - sum_i G_ij x_i)
 // (the chain rule of the squared distance, which the expansion's derivative equals
 // away from its clamp at 0).  The two products are [L, K] x [K, D] contractions on the
-// matrix cores; the row sums of A ride along the staging.  Workgroup (m, b): m = 0
-// makes dL/dx (A = G, K = L2, B = y), m = 1 dL/dy (A = G^T, K = L1, B = x), in passes
-// of RB output rows, so that each element's features are read once per pass and G
-// twice in all.  A pass stages K in chunks of FG_KC through LDS, with the next chunk's
-// loads in registers during the current chunk's products.  Four waves each own RB/4
-// rows by all KP columns: (RB/128) x (KP/32) accumulator tiles of 32 x 32, every
-// operand read feeding several of them.
+// matrix cores.  Workgroup (m, b): m = 0 makes dL/dx (A = G, K = L2, B = y), m = 1
+// dL/dy (A = G^T, K = L1, B = x), in passes of RB output rows, so that each element's
+// features are read once per pass and G twice in all.  A pass stages K in chunks of
+// FG_KC through LDS, with the next chunk's loads in registers during the current
+// chunk's products.  Four waves each own RB/4 rows by all KP columns: (RB/128) x
+// (KP/32) accumulator tiles of 32 x 32, every operand read feeding several of them.
+//
+// Memory goes through buffer resources, one per chunk or pass whose records end at
+// the element's last row: rows past the element read as zero (or, for a store, are
+// dropped) with no test in the code, and a lane whose column lies past K or D starts
+// from an offset of 2^31, past every resource's records.  No load result passes
+// through a select, so loads stay in flight until their values are stored to LDS.
+// W = 4: 16-byte loads (rows of G, x and y a multiple of 4 floats, 16-byte aligned
+// bases); W = 1: 4-byte loads.
 constexpr int FG_KC = 32;                   // K chunk staged per step
+constexpr unsigned FG_OOB = 0x80000000u;    // an offset past every resource's records
+
+// raw buffer (stride 0) over `bytes` bytes from base (clamped to [0, 2^31 - 1]), the
+// gfx9 data-format word
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t fg_rsrc(const float* base, long long bytes) {
+    const int n = (int)(bytes < 0 ? 0 : bytes > 0x7fffffffLL ? 0x7fffffffLL : bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, n, 0x00020000);
+}
+
+template <int W>
+__device__ __forceinline__ void fg_load(float* v, __amdgpu_buffer_rsrc_t r, unsigned off) {
+    if constexpr (W == 4) {
+        typedef unsigned u4 __attribute__((ext_vector_type(4)));
+        const u4 q = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+        v[0] = __uint_as_float(q.x);
+        v[1] = __uint_as_float(q.y);
+        v[2] = __uint_as_float(q.z);
+        v[3] = __uint_as_float(q.w);
+    } else {
+        v[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+    }
+}
 
 template <int KP>
 struct FG {
     static constexpr int RB = KP == 128 ? 128 : 256;   // output rows per pass
     static constexpr int RTW = RB / 128;               // row tiles per wave
     static constexpr int CT = KP / 32;                 // column tiles
-    static constexpr int NA = RB * FG_KC / 256;        // A values staged per thread
-    static constexpr int NB = FG_KC * KP / 256;        // B values staged per thread
     // A chunk: dL/dx [RB][FG_KC + 1] (rows r, k), dL/dy [FG_KC][RB] (k, rows r)
     static constexpr int AFLOATS = RB * (FG_KC + 1);
     static constexpr size_t lds() { return ((size_t)AFLOATS + FG_KC * KP + RB) * sizeof(float); }
 };
 
 // ROWS: dL/dx (rows of G, K = L2) or dL/dy (columns of G, K = L1)
-template <int KP, bool ROWS>
+template <int KP, bool ROWS, int W>
 __device__ __forceinline__ void feature_grad_block(const float* __restrict__ G,
                                                    const float* __restrict__ x,
                                                    const float* __restrict__ y,
@@ -256,7 +283,7 @@ __device__ __forceinline__ void feature_grad_block(const float* __restrict__ G,
                                                    float* __restrict__ gx, float* __restrict__ gy,
                                                    int B, int L1, int L2, int D, float* sm) {
     using F = FG<KP>;
-    constexpr int RB = F::RB, RTW = F::RTW, CT = F::CT, NA = F::NA, NB = F::NB;
+    constexpr int RB = F::RB, RTW = F::RTW, CT = F::CT;
     constexpr int KCS = FG_KC + 1;
     float* As = sm;                              // the A chunk
     float* Bs = As + F::AFLOATS;                 // [FG_KC][KP]: B rows of the k chunk
@@ -268,16 +295,24 @@ __device__ __forceinline__ void feature_grad_block(const float* __restrict__ G,
     const int wr = wave * (RB / 4);              // this wave's first row of the pass
     // lane l's A operand of row tile t at k pair kk: row wr + 32 t + l % 32, k kk + l / 32
     const int arow = wr + (lane & 31), ak = lane >> 5;
-    // row sums: RPT threads per row, each a k range of FG_KC / RPT
+    // A items of W values: dL/dx: item (i, j) = row i, k j..j+W-1 of the [RB][FG_KC]
+    // chunk; dL/dy: k row i, rows j..j+W-1 of the [FG_KC][RB] chunk.  Thread t holds
+    // items (a_i + A_DI n, a_j).
+    constexpr int A_IPR = (ROWS ? FG_KC : RB) / W;          // items per chunk row
+    constexpr int A_DI = 256 / A_IPR;
+    constexpr int NA = RB * FG_KC / W / 256;
+    const int a_i = threadIdx.x / A_IPR, a_j = (threadIdx.x % A_IPR) * W;
+    // B items: k row b_k + B_DK n, features b_d..b_d+W-1 of the [FG_KC][KP] chunk
+    constexpr int B_IPR = KP / W;
+    constexpr int B_DK = 256 / B_IPR;
+    constexpr int NB = FG_KC * KP / W / 256;
+    const int b_k = threadIdx.x / B_IPR, b_d = (threadIdx.x % B_IPR) * W;
+    // row sums: from the staged registers when W = 4 (dL/dx: NA rows of W values per
+    // thread, reduced over the A_IPR lanes of a row; dL/dy: W rows per thread, reduced
+    // over the A_DI threads of a row through LDS); from LDS when W = 1 (RPT threads per
+    // row, FG_KC / RPT values each)
     constexpr int RPT = 256 / RB;
     const int srow = threadIdx.x / RPT, spart = threadIdx.x % RPT;
-    // thread t's staged A values: dL/dx element t + 256 n of the [RB][FG_KC] chunk, dL/dy
-    // of the [FG_KC][RB] chunk
-    const int a_r = ROWS ? threadIdx.x / FG_KC : threadIdx.x % RB;
-    const int a_k = ROWS ? threadIdx.x % FG_KC : threadIdx.x / RB;
-    constexpr int A_DR = 256 / FG_KC, A_DK = 256 / RB;   // per n: rows (dL/dx), k (dL/dy)
-    const int bk0 = threadIdx.x / KP, bd = threadIdx.x % KP;
-    constexpr int BDK = 256 / KP;                // B rows per n (KP <= 256)
     for (int b = blockIdx.y; b < B; b += gridDim.y) {
         const float* Gb = G + (size_t)b * L1 * L2;
         const float* Bsrc = (ROWS ? y : x) + (size_t)b * K * D;   // B rows: [K][D]
@@ -285,34 +320,29 @@ __device__ __forceinline__ void feature_grad_block(const float* __restrict__ G,
         float* out = (ROWS ? gx : gy) + (size_t)b * L * D;
         const float f = 2.0f * (scale ? scale[b] : 1.0f);
         for (int r0 = 0; r0 < L; r0 += RB) {
-            const float* gb = Gb + (ROWS ? (size_t)r0 * L2 : (size_t)r0);
-            float av[NA], bv[NB];
-            // branch-free: clamped in-bounds reads; the values past the element, K and D
-            // are zeroed only when the chunk is stored to LDS (a select at load time
-            // would wait for each load at once)
-            auto a_ok = [&](int k0, int n) {
-                return ROWS ? (r0 + a_r + A_DR * n < L1 && k0 + a_k < L2)
-                            : (r0 + a_r < L2 && k0 + a_k + A_DK * n < L1);
-            };
-            auto b_ok = [&](int k0, int n) { return k0 + bk0 + BDK * n < K && bd < D; };
+            float av[NA][W], bv[NB][W];
+            // lane bases of the items (n = 0): past L2 (dL/dy: columns of G) or D, the
+            // out-of-range offset; rows past L1 (dL/dx) and k past K fall outside the
+            // chunk's records
+            const unsigned a_base = (unsigned)(a_i * L2 + a_j) * 4u;
+            const unsigned a_lane = ROWS || r0 + a_j < L2 ? a_base : FG_OOB;
+            const unsigned b_lane = b_d < D ? (unsigned)(b_k * D + b_d) * 4u : FG_OOB;
             auto load = [&](int k0) {
+                // dL/dx: rows r0.. from column k0 (k past L2 tested per chunk); dL/dy:
+                // rows k0.. from column r0
+                const float* pa = Gb + (ROWS ? (size_t)r0 * L2 + k0 : (size_t)k0 * L2 + r0);
+                const long long a_bytes =
+                    ROWS ? ((long long)(L1 - r0) * L2 - k0) * 4 : ((long long)(L1 - k0) * L2 - r0) * 4;
+                const __amdgpu_buffer_rsrc_t ra = fg_rsrc(pa, a_bytes);
+                const unsigned a0 = !ROWS || k0 + a_j < L2 ? a_lane : FG_OOB;
 #pragma unroll
-                for (int n = 0; n < NA; ++n) {
-                    unsigned off;
-                    if (ROWS) {
-                        const int r = a_r + A_DR * n, k = k0 + a_k;
-                        off = (unsigned)(min(r, L1 - 1 - r0) * L2 + min(k, L2 - 1));
-                    } else {
-                        const int k = k0 + a_k + A_DK * n;
-                        off = (unsigned)(min(k, L1 - 1) * L2 + min(a_r, L2 - 1 - r0));
-                    }
-                    av[n] = lane_load(gb, off * 4u);
-                }
+                for (int n = 0; n < NA; ++n)
+                    fg_load<W>(av[n], ra, a0 + (unsigned)(A_DI * n * L2) * 4u);
+                const __amdgpu_buffer_rsrc_t rb_ =
+                    fg_rsrc(Bsrc + (size_t)k0 * D, (long long)(K - k0) * D * 4);
 #pragma unroll
-                for (int n = 0; n < NB; ++n) {
-                    const int k = k0 + bk0 + BDK * n;
-                    bv[n] = lane_load(Bsrc, (unsigned)(min(k, K - 1) * D + min(bd, D - 1)) * 4u);
-                }
+                for (int n = 0; n < NB; ++n)
+                    fg_load<W>(bv[n], rb_, b_lane + (unsigned)(B_DK * n * D) * 4u);
             };
             f32x16 acc[RTW][CT];
 #pragma unroll
@@ -321,26 +351,57 @@ __device__ __forceinline__ void feature_grad_block(const float* __restrict__ G,
                 for (int c = 0; c < CT; ++c)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) acc[t][c][v] = 0.0f;
-            float rsum = 0.0f;
-            load(0);
+            float rsum[ROWS ? NA : W];   // W = 4: this thread's partial row sums
+#pragma unroll
+            for (int n = 0; n < (ROWS ? NA : W); ++n) rsum[n] = 0.0f;
+            if (K > 0) load(0);
             for (int k0 = 0; k0 < K; k0 += FG_KC) {
                 __syncthreads();   // the previous chunk's reads are complete
 #pragma unroll
                 for (int n = 0; n < NA; ++n) {
-                    const int idx = threadIdx.x + 256 * n;
-                    const float v = a_ok(k0, n) ? av[n] : 0.0f;
-                    if (ROWS) As[(idx / FG_KC) * KCS + idx % FG_KC] = v;
-                    else As[idx] = v;   // [k][r]: element idx = k RB + r
+                    const int i = a_i + A_DI * n;
+                    if (ROWS) {
+#pragma unroll
+                        for (int w = 0; w < W; ++w) As[i * KCS + a_j + w] = av[n][w];
+                    } else if (W == 4) {
+                        *reinterpret_cast<float4*>(As + i * RB + a_j) =
+                            make_float4(av[n][0], av[n][W > 1 ? 1 : 0], av[n][W > 2 ? 2 : 0],
+                                        av[n][W > 3 ? 3 : 0]);
+                    } else {
+                        As[i * RB + a_j] = av[n][0];
+                    }
+                    if (W == 4) {
+                        if (ROWS) {
+                            rsum[n] += (av[n][0] + av[n][W > 1 ? 1 : 0]) +
+                                       (av[n][W > 2 ? 2 : 0] + av[n][W > 3 ? 3 : 0]);
+                        } else {
+#pragma unroll
+                            for (int w = 0; w < W; ++w) rsum[w] += av[n][w];
+                        }
+                    }
                 }
 #pragma unroll
-                for (int n = 0; n < NB; ++n) Bs[threadIdx.x + 256 * n] = b_ok(k0, n) ? bv[n] : 0.0f;
+                for (int n = 0; n < NB; ++n) {
+                    float* dst = Bs + (b_k + B_DK * n) * KP + b_d;
+                    if (W == 4)
+                        *reinterpret_cast<float4*>(dst) =
+                            make_float4(bv[n][0], bv[n][W > 1 ? 1 : 0], bv[n][W > 2 ? 2 : 0],
+                                        bv[n][W > 3 ? 3 : 0]);
+                    else
+                        dst[0] = bv[n][0];
+                }
                 // the next chunk's loads are in flight during this chunk's products
-                if (k0 + FG_KC < K) load(k0 + FG_KC);
+                // (unconditional: past K every offset is out of range and reads zero,
+                // with no memory access; a conditional refill would keep the staged
+                // values alive beside the new ones, in copies)
+                load(k0 + FG_KC);
                 __syncthreads();
+                if (W == 1) {
 #pragma unroll
-                for (int kk = 0; kk < FG_KC / RPT; ++kk) {
-                    const int k = spart * (FG_KC / RPT) + kk;
-                    rsum += ROWS ? As[srow * KCS + k] : As[k * RB + srow];
+                    for (int kk = 0; kk < FG_KC / RPT; ++kk) {
+                        const int k = spart * (FG_KC / RPT) + kk;
+                        rsum[0] += ROWS ? As[srow * KCS + k] : As[k * RB + srow];
+                    }
                 }
 #pragma unroll 2
                 for (int kk = 0; kk < FG_KC; kk += 2) {
@@ -359,74 +420,101 @@ __device__ __forceinline__ void feature_grad_block(const float* __restrict__ G,
                                                                              acc[t][c], 0, 0, 0);
                 }
             }
-            if (RPT > 1) rsum += __shfl_xor(rsum, 1, 64);   // the row's other k half
-            if (spart == 0) rs[srow] = rsum;
+            if (W == 1) {
+                if (RPT > 1) rsum[0] += __shfl_xor(rsum[0], 1, 64);   // the row's other half
+                if (spart == 0) rs[srow] = rsum[0];
+            } else if (ROWS) {
+                // the A_IPR consecutive lanes of a row
+#pragma unroll
+                for (int n = 0; n < NA; ++n) {
+#pragma unroll
+                    for (int o = 1; o < A_IPR; o *= 2) rsum[n] += __shfl_xor(rsum[n], o, 64);
+                    if (a_j == 0) rs[a_i + A_DI * n] = rsum[n];
+                }
+            } else {
+                // the A_DI threads of a row (one per k row of an item set) through LDS
+                __syncthreads();   // the last chunk's reads are complete
+#pragma unroll
+                for (int w = 0; w < W; ++w) As[a_i * RB + a_j + w] = rsum[w];
+                __syncthreads();
+                if (threadIdx.x < RB) {
+                    float t = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < A_DI; ++i) t += As[i * RB + threadIdx.x];
+                    rs[threadIdx.x] = t;
+                }
+            }
             __syncthreads();
             // accumulator v of lane l in tile (t, c): row 8 (v / 4) + 4 (l / 32) + v % 4,
-            // column l % 32.  Lane l's rows are rb + (32 t + 8 (v / 4) + v % 4): a
-            // per-lane base and offsets common to the wave (scalar registers).  Per tile,
-            // the 16 feature loads go out together before any store (a load inside each
-            // store's bounds test would wait for memory once per output); in a pass past
-            // the element's end the rows are clamped for the loads and tested for the
-            // stores.
+            // column l % 32.  Lane l's rows are rb + (32 t + 8 (v / 4) + v % 4).  Per
+            // tile, the 16 feature loads go out together before any store.
             const int rb = wr + 4 * (lane >> 5);
-            auto epilogue = [&](auto full) {
-                constexpr bool FULL = decltype(full)::value;
+            const long long pass_bytes = (long long)(L - r0) * D * 4;   // rows past L: out of range
+            const __amdgpu_buffer_rsrc_t rself = fg_rsrc(self + (size_t)r0 * D, pass_bytes);
+            const __amdgpu_buffer_rsrc_t rout = fg_rsrc(out + (size_t)r0 * D, pass_bytes);
 #pragma unroll
-                for (int t = 0; t < RTW; ++t) {
+            for (int t = 0; t < RTW; ++t) {
 #pragma unroll
-                    for (int c = 0; c < CT; ++c) {
-                        const int d = 32 * c + (lane & 31);
-                        const int dc = min(d, D - 1);
-                        const float* sp = self + (size_t)(r0 + rb) * D + dc;
-                        float* op = out + (size_t)(r0 + rb) * D + d;
-                        float sv[16];
+                for (int c = 0; c < CT; ++c) {
+                    const int d = 32 * c + (lane & 31);
+                    const unsigned o0 = d < D ? (unsigned)(rb * D + d) * 4u : FG_OOB;
+                    float sv[16];
 #pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            const int dr = 32 * t + 8 * (v >> 2) + (v & 3);
-                            sv[v] = FULL ? sp[(size_t)dr * D]
-                                         : self[(size_t)min(r0 + rb + dr, L - 1) * D + dc];
-                        }
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            const int dr = 32 * t + 8 * (v >> 2) + (v & 3);
-                            if ((FULL || r0 + rb + dr < L) && d < D)
-                                op[(size_t)dr * D] = f * fmaf(sv[v], rs[rb + dr], -acc[t][c][v]);
-                        }
+                    for (int v = 0; v < 16; ++v) {
+                        const int dr = 32 * t + 8 * (v >> 2) + (v & 3);
+                        fg_load<1>(&sv[v], rself, o0 + (unsigned)(dr * D) * 4u);
                     }
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int dr = 32 * t + 8 * (v >> 2) + (v & 3);
+                        const float g = f * fmaf(sv[v], rs[rb + dr], -acc[t][c][v]);
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(g), rout,
+                                                              o0 + (unsigned)(dr * D) * 4u, 0, 0);
+                    }
+                    // one tile's loads in flight at a time (registers)
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-            };
-            if (r0 + RB <= L) epilogue(std::true_type{});
-            else epilogue(std::false_type{});
+            }
             __syncthreads();   // rs and the chunks are rewritten by the next pass
         }
     }
 }
 
-template <int KP>
-__global__ void __launch_bounds__(256)
+// (two waves per SIMD for the 16-byte form, its accumulators in the architectural
+// registers; the 4-byte form needs more)
+template <int KP, int W>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(W == 4 ? 2 : 1)))
 feature_grad_kernel(const float* __restrict__ G, const float* __restrict__ x,
                     const float* __restrict__ y, const float* __restrict__ scale,
                     float* __restrict__ gx, float* __restrict__ gy, int B, int L1, int L2,
                     int D) {
     extern __shared__ __align__(16) float sm[];
     if (blockIdx.x == 0)
-        feature_grad_block<KP, true>(G, x, y, scale, gx, gy, B, L1, L2, D, sm);
+        feature_grad_block<KP, true, W>(G, x, y, scale, gx, gy, B, L1, L2, D, sm);
     else
-        feature_grad_block<KP, false>(G, x, y, scale, gx, gy, B, L1, L2, D, sm);
+        feature_grad_block<KP, false, W>(G, x, y, scale, gx, gy, B, L1, L2, D, sm);
+}
+
+template <int KP, int W>
+int launch_feature_grad_w(const float* G, const float* x, const float* y, const float* scale,
+                          float* gx, float* gy, int B, int L1, int L2, int D, hipStream_t st) {
+    const size_t lds = FG<KP>::lds();
+    D2P_HIP(hipFuncSetAttribute((const void*)feature_grad_kernel<KP, W>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    const dim3 grid(2, std::min(B, SQ_GRID_MAX));
+    D2P_LAUNCH("sqeuclid_feature_grad", (feature_grad_kernel<KP, W>), grid, dim3(256), lds, st,
+               G, x, y, scale, gx, gy, B, L1, L2, D);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
 }
 
 template <int KP>
 int launch_feature_grad_k(const float* G, const float* x, const float* y, const float* scale,
                           float* gx, float* gy, int B, int L1, int L2, int D, hipStream_t st) {
-    const size_t lds = FG<KP>::lds();
-    D2P_HIP(hipFuncSetAttribute((const void*)feature_grad_kernel<KP>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    const dim3 grid(2, std::min(B, SQ_GRID_MAX));
-    D2P_LAUNCH("sqeuclid_feature_grad", feature_grad_kernel<KP>, grid, dim3(256), lds, st, G, x,
-               y, scale, gx, gy, B, L1, L2, D);
-    D2P_HIP(hipGetLastError());
-    return D2P_OK;
+    const bool vec = (D & 3) == 0 && (L2 & 3) == 0 &&
+                     (((uintptr_t)G | (uintptr_t)x | (uintptr_t)y) & 15) == 0;
+    return vec ? launch_feature_grad_w<KP, 4>(G, x, y, scale, gx, gy, B, L1, L2, D, st)
+               : launch_feature_grad_w<KP, 1>(G, x, y, scale, gx, gy, B, L1, L2, D, st);
 }
 
 }  // namespace dtw

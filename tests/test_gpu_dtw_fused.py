@@ -217,7 +217,9 @@ def test_fused_temperature_gradient_and_autocast(cuda):
 
 @pytest.mark.parametrize("B,L1,L2,D,scaled", [(2, 256, 256, 64, True), (3, 70, 130, 5, False),
                                               (1, 1, 200, 128, True), (2, 65, 1, 32, False),
-                                              (1, 300, 90, 100, True), (2, 64, 64, 1, False)])
+                                              (1, 300, 90, 100, True), (2, 64, 64, 1, False),
+                                              (2, 300, 260, 36, True), (1, 129, 132, 128, False),
+                                              (3, 33, 516, 20, True)])
 def test_feature_grad_kernel(cuda, B, L1, L2, D, scaled):
     """d2p_amd::sqeuclid_feature_grad (one kernel, the products on the matrix cores)
     against the chain rule in float64: within the summation bound (K + 4) u |f|
