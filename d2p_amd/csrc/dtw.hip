@@ -341,9 +341,9 @@ dtw_backward_kernel(const int* __restrict__ lengths,
                     float* __restrict__ post, float* __restrict__ grad_T,
                     int* __restrict__ status, float* __restrict__ trash,
                     uint64_t* __restrict__ bflag, float2* __restrict__ flows,
-                    double* __restrict__ bpart, int B, int L1max, int L2max, int NSmax,
-                    size_t elem_steps, float T, int bandwidth, int R, int G, int SPW,
-                    uint32_t epoch) {
+                    double* __restrict__ bpart, float* __restrict__ poison_value, int B,
+                    int L1max, int L2max, int NSmax, size_t elem_steps, float T, int bandwidth,
+                    int R, int G, int SPW, uint32_t epoch) {
     extern __shared__ __align__(16) float smem[];
     __shared__ int prog[NW];
     __shared__ int hprog[NW];     // HELP: chunks of stripe order q loaded by its helper
@@ -686,6 +686,24 @@ dtw_backward_kernel(const int* __restrict__ lengths,
         if (G == 1) grad_T[b] = g / T;
         else bpart[((size_t)b * G + part) * 4] = g;
     }
+    // An unsplit element whose waits gave up (in the forward or in this sweep) gets NaN
+    // in all its outputs here (the separate poison pass of split calls).  Every wave
+    // first completes its own status atomics and stores; then one thread reads the
+    // status word and every wave branches on that one value.
+    if (G == 1 && poison_value != nullptr) {
+        __shared__ int poison_flag;
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (threadIdx.x == 0) poison_flag = load_status(st);
+        __syncthreads();
+        if (poison_flag == 0) return;
+        const float nan = __builtin_nanf("");
+        for (size_t i = threadIdx.x; i < (size_t)L1max * L2max; i += blockDim.x) pbase[i] = nan;
+        if (threadIdx.x == 0) {
+            poison_value[b] = nan;
+            grad_T[b] = nan;
+        }
+    }
 }
 
 // grad_T[b] of a split element from the parts' sums.
@@ -745,7 +763,7 @@ bool dtw_helpers_enabled() {
 template <int P>
 int launch_backward_p(const int* lengths, int B, int max_L1, int max_L2,
                       float T, int bandwidth, const Layout& ws, float* marginals, float* grad_T,
-                      hipStream_t st, const Split& sp, int R) {
+                      hipStream_t st, const Split& sp, int R, float* poison_value) {
     const int ns = (max_L1 + 63) / 64;
     const size_t lds = lds_backward_r(R, P);
     D2P_REQUIRE(lds <= kLdsLimit, "sequence too long for the LDS stripe rings");
@@ -758,8 +776,8 @@ int launch_backward_p(const int* lengths, int B, int max_L1, int max_L2,
                                 (int)lds));
     D2P_LAUNCH("dtw_backward", kern, dim3(split_grid(B, sp.G)), dim3(NW * 64),
                lds, st, lengths, ws.alpha_sk, ws.brow, marginals, grad_T, ws.status, ws.trash,
-               ws.bflag, ws.flows, ws.bpart, B, max_L1, max_L2, ns, ws.elem_steps, T,
-               bandwidth, R, sp.G, sp.SPW, next_epoch());
+               ws.bflag, ws.flows, ws.bpart, sp.G == 1 ? poison_value : nullptr, B, max_L1,
+               max_L2, ns, ws.elem_steps, T, bandwidth, R, sp.G, sp.SPW, next_epoch());
     if (sp.G > 1)
         D2P_LAUNCH("dtw_grad_merge", dtw_grad_merge, dim3((B + 255) / 256), dim3(256), 0, st,
                    ws.bpart, grad_T, B, sp.G, T);
@@ -803,15 +821,16 @@ int launch_forward(const float* costs, const int* lengths, int B, int max_L1, in
 
 int launch_backward(const int* lengths, int B, int max_L1, int max_L2, float T,
                     int bandwidth, const Layout& ws, float* marginals, float* grad_T,
-                    hipStream_t st) {
+                    hipStream_t st, float* poison_value, bool* poisoned) {
     const Split sp = choose_split(B, max_L1, ws, max_stripes_backward(max_L1, max_L2));
     const int rows = sp.G > 1 ? sp.SPW * 64 : max_L1;
     const int R = ring_backward(rows, max_L2);
+    if (poisoned != nullptr) *poisoned = sp.G == 1 && poison_value != nullptr;
     if (backward_chunk(rows, max_L2) == 16)
         return launch_backward_p<16>(lengths, B, max_L1, max_L2, T, bandwidth, ws, marginals,
-                                     grad_T, st, sp, R);
+                                     grad_T, st, sp, R, poison_value);
     return launch_backward_p<8>(lengths, B, max_L1, max_L2, T, bandwidth, ws, marginals, grad_T,
-                                st, sp, R);
+                                st, sp, R, poison_value);
 }
 
 }  // namespace dtw
@@ -849,8 +868,10 @@ extern "C" int d2p_dtw_forward_marginals(const float* costs, const int* lengths,
                                      dtw::band_elem_steps(max_L1, max_L2, bandwidth));
     D2P_TRY(dtw::launch_forward(costs, lengths, B, max_L1, max_L2, temperature, bandwidth, ws,
                                 value, st));
+    bool poisoned = false;
     D2P_TRY(dtw::launch_backward(lengths, B, max_L1, max_L2, temperature, bandwidth, ws,
-                                 marginals, grad_T, st));
+                                 marginals, grad_T, st, value, &poisoned));
+    if (poisoned) return D2P_OK;
     return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr, value,
                              grad_T, nullptr, nullptr, st);
 }

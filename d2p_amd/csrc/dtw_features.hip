@@ -543,8 +543,10 @@ extern "C" int d2p_dtw_sqeuclid_forward_marginals(const float* x, const float* y
         D2P_TRY(dtw::launch_sqdist(x, y, marginals, B, max_L1, max_L2, D, st));
     D2P_TRY(dtw::launch_forward(marginals, lengths, B, max_L1, max_L2, temperature, bandwidth,
                                 ws, value, st));
+    bool poisoned = false;
     D2P_TRY(dtw::launch_backward(lengths, B, max_L1, max_L2, temperature, bandwidth, ws,
-                                 marginals, grad_T, st));
+                                 marginals, grad_T, st, value, &poisoned));
+    if (poisoned) return D2P_OK;
     return wf::launch_poison(ws.status, B, (long long)max_L1 * max_L2, marginals, nullptr, value,
                              grad_T, nullptr, nullptr, st);
 }

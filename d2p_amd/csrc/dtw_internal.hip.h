@@ -107,10 +107,12 @@ int launch_forward(const float* costs, const int* lengths, int B, int max_L1, in
                    float T, int bandwidth, const Layout& ws, float* value, hipStream_t st);
 
 // Reverse sweep: marginals and dvalue/dT per element, from a forward's table alone
-// (the costs are not needed).
+// (the costs are not needed).  With poison_value (the forward's value[B]) and an unsplit
+// element, the sweep itself puts NaN in the outputs of an element whose waits gave up,
+// and *poisoned reports that no separate poison pass is needed.
 int launch_backward(const int* lengths, int B, int max_L1, int max_L2, float T,
                     int bandwidth, const Layout& ws, float* marginals, float* grad_T,
-                    hipStream_t st);
+                    hipStream_t st, float* poison_value = nullptr, bool* poisoned = nullptr);
 
 }  // namespace dtw
 }  // namespace d2p_amd

@@ -107,6 +107,10 @@ def test_sw_forward_marginals_gives_up_to_nan(cuda, low_spin_limit, monkeypatch,
 def test_second_order_and_other_families_give_up_to_nan(cuda, low_spin_limit):
     s = _scores(2, 200, 90, 42).to(cuda)
     v = _scores(2, 200, 90, 43).to(cuda)
+    # (unsplit soft DTW: its reverse sweep writes the NaN itself, value included)
+    dtw = d2p_amd.soft_dtw(s.abs(), temperature=0.5)
+    fx, fy = _scores(2, 200, 16, 44).to(cuda), _scores(2, 90, 16, 45).to(cuda)
+    dtw_feat = d2p_amd.soft_dtw_sqeuclidean(fx, fy, 0.5)
     outs = {
         "sw_hvp": d2p_amd.soft_sw_hvp(s, v, -1.0, 1.0, None),
         "sw_jac": d2p_amd.soft_sw_param_jacobian(s, 1, -1.0, 1.0, None),
@@ -114,7 +118,10 @@ def test_second_order_and_other_families_give_up_to_nan(cuda, low_spin_limit):
         "nw_hvp": d2p_amd.soft_nw_hvp(s, v, -1.0, 1.0, None),
         "swa": d2p_amd.soft_sw_affine(s, gap_open=-2.0, gap_ext=-0.5).marginals,
         "swa_hvp": d2p_amd.soft_sw_affine_hvp(s, v, -2.0, -0.5, 1.0, None),
-        "dtw": d2p_amd.soft_dtw(s.abs(), temperature=0.5).alignment,
+        "dtw": dtw.alignment,
+        "dtw_cost": dtw.cost,
+        "dtw_feat": dtw_feat.alignment,
+        "dtw_feat_cost": dtw_feat.cost,
         "dtw_hvp": d2p_amd.soft_dtw_hvp(s.abs(), v, 0.5, None, None),
     }
     torch.cuda.synchronize()
