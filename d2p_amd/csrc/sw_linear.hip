@@ -255,6 +255,27 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                               : nullptr;
             // the chunk's alpha rows (alpha tile k % NTB) to the table: Tile::NQ stores
             // (TAN: and as many for the tangent rows)
+            // The partition of stripe l (TAN: with the tangent sum), from the chunk's alpha
+            // tile: lane r takes its own row's P alphas (column r of the tile) and runs
+            // the block update the sweeping wave would run, with the same running max,
+            // so the lane states are the same bit for bit; the sweeping wave's chain is
+            // spared the P exponentials per chunk.
+            float hbm = -1e20f;   // the running max of lane r's alphas
+            auto partition_block = [&](int k) {
+                if constexpr (!NWG) {
+                    const float* at = atiles + (k & (NTB - 1)) * Tile::FLOATS + lane;
+                    float av[P], xv[P];
+#pragma unroll
+                    for (int u = 0; u < P; ++u) {
+                        av[u] = at[u * 64];
+                        if (TAN) xv[u] = at[NTB * Tile::FLOATS + u * 64];
+                    }
+#pragma unroll
+                    for (int u = 0; u < P; ++u) hbm = fmaxf(hbm, av[u]);
+                    if constexpr (TAN) acc.template add_block_max<P>(av, xv, hbm, c);
+                    else acc.template add_block_max<P>(av, hbm, c);
+                }
+            };
             auto store_alpha = [&](int k) {
                 const float* at = atiles + (k & (NTB - 1)) * Tile::FLOATS;
                 float* dst = out + (size_t)k * P * 64;
@@ -313,6 +334,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                     wait_for(prog, l, l * PROG_STRIDE + k + 1, st);
                     store_alpha(k);
                     store_row(k);
+                    partition_block(k);
                     if (k + 2 < nch) {
                         // chunk k + 2's loads (issued at iteration k - 1, or before the
                         // loop) are followed by chunk k - 1's alpha stores (k >= 1),
@@ -341,6 +363,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                     if (k + 2 < nch) load(k + 2);
                     store_alpha(k);
                     store_row(k);
+                    partition_block(k);
                 }
             }
         }
@@ -526,7 +549,7 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                     else lane_store(outc + u * 64, ul4, cur);
                     pub[u] = cur;
                     av[u] = cur;
-                    if (!NWG) bm = fmaxf(bm, cur);
+                    if (!NWG && !HELP) bm = fmaxf(bm, cur);
                     if constexpr (TAN) {
                         if (HELP) ttile[u * 64] = tcur;
                         else lane_store(toutc + u * 64, ul4, tcur);
@@ -539,9 +562,9 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
             else steps(std::false_type{});
             prog_ahead(ahead, prog, HELP ? hprog : nullptr, l, NL, l);
             if constexpr (TAN) {
-                if (!NWG) acc.template add_block_max<P>(av, xv, bm, c);
+                if (!NWG && !HELP) acc.template add_block_max<P>(av, xv, bm, c);
             } else {
-                if (!NWG) acc.template add_block_max<P>(av, bm, c);
+                if (!NWG && !HELP) acc.template add_block_max<P>(av, bm, c);
             }
             // the stripe's last row (lane 63) by step, contiguous, for the reverse sweep
             // of the stripe below and the next part; one store instruction (TAN: two)
@@ -588,12 +611,23 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
         return;
     }
     // partition: merge lanes, waves, and (once per element) the cell (0,0) whose alpha is 0
-    // (TAN: and whose tangent is 0)
+    // (TAN: and whose tangent is 0).  Slot l holds stripe l's state: from sweeping wave l,
+    // or (HELP) from its helper, wave HB + l; the other slots stay at the empty state.
     wave_merge_lse(acc, c);
-    if (lane == 0 && wave < NW) {
-        red_m[wave] = acc.m;
-        red_z[wave] = acc.z;
-        if constexpr (TAN) red_w[wave] = acc.w;
+    constexpr int HB = WIDE ? NW : NW / 2;
+    if constexpr (HELP) {
+        if (lane == 0 && wave < NW) {
+            red_m[wave] = -3.0e38f;
+            red_z[wave] = 0.0f;
+            if constexpr (TAN) red_w[wave] = 0.0f;
+        }
+        __syncthreads();
+    }
+    const int slot = HELP ? wave - HB : wave;
+    if (lane == 0 && slot >= 0 && slot < NW) {
+        red_m[slot] = acc.m;
+        red_z[slot] = acc.z;
+        if constexpr (TAN) red_w[slot] = acc.w;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
