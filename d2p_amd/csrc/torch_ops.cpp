@@ -86,6 +86,28 @@ Tensor resolve_lengths(const c10::optional<Tensor>& lengths_opt, const Dims& d,
     TORCH_CHECK(lengths.scalar_type() == torch::kInt32, "lengths must be int32");
     TORCH_CHECK(lengths.device() == device, "lengths must be on same device as ", input,
                 ", got ", lengths.device(), " vs ", device);
+    // The values are checked on the host, as the reference does
+    // (/root/reference/src/sw_affine/torch_cuda.cpp:85-96): a copy that waits for the
+    // stream.  A tensor checked by this thread's previous call against the same (L1, L2),
+    // still alive, on the same memory and not modified since (same version counter,
+    // which every in-place change and every view's change bumps), is not copied again,
+    // so a training loop
+    // that passes the same lengths every step does not synchronise each call.
+    // (Inference tensors carry no version counter: always checked.)
+    struct Checked {
+        c10::weak_intrusive_ptr<c10::TensorImpl, c10::UndefinedTensorImpl> impl{
+            c10::intrusive_ptr<c10::TensorImpl, c10::UndefinedTensorImpl>()};
+        int64_t version = 0;
+        const void* data = nullptr;
+        int L1 = -1, L2 = -1;
+    };
+    static thread_local Checked last;
+    const bool versioned = !lengths.is_inference();
+    if (versioned && last.L1 == d.L1 && last.L2 == d.L2 && last.data == lengths.data_ptr() &&
+        last.version == lengths._version()) {
+        auto alive = last.impl.lock();
+        if (alive.get() == lengths.unsafeGetTensorImpl()) return lengths;
+    }
     auto host = lengths.to(torch::kCPU);
     auto acc = host.accessor<int32_t, 2>();
     for (int b = 0; b < d.B; ++b) {
@@ -93,6 +115,14 @@ Tensor resolve_lengths(const c10::optional<Tensor>& lengths_opt, const Dims& d,
                     ",0] must be between 0 and ", d.L1, ", got ", acc[b][0]);
         TORCH_CHECK(acc[b][1] >= 0 && acc[b][1] <= d.L2, "lengths[", b,
                     ",1] must be between 0 and ", d.L2, ", got ", acc[b][1]);
+    }
+    if (versioned) {
+        last.impl = c10::weak_intrusive_ptr<c10::TensorImpl, c10::UndefinedTensorImpl>(
+            lengths.getIntrusivePtr());
+        last.version = lengths._version();
+        last.data = lengths.data_ptr();
+        last.L1 = d.L1;
+        last.L2 = d.L2;
     }
     return lengths;
 }

@@ -41,6 +41,42 @@ def test_invalid_lengths_raise(cuda, family, lengths, match):
         call()
 
 
+def test_lengths_checked_again_after_any_change(cuda):
+    """A lengths tensor checked on the host by the previous call is not copied again
+    while it is unchanged; any change is checked again: an in-place write (to the
+    tensor or through a view), other memory under the same tensor, another (L1, L2),
+    another tensor with the same values."""
+    scores = torch.randn(2, 4, 5, device=cuda)
+    ln = torch.tensor([[4, 5], [3, 2]], dtype=torch.int32, device=cuda)
+    first = d2p_amd.soft_sw_affine_float(scores, -2.0, -0.5, 1.0, ln)
+    again = d2p_amd.soft_sw_affine_float(scores, -2.0, -0.5, 1.0, ln)
+    assert torch.equal(first[0], again[0]) and torch.equal(first[1], again[1])
+    ln[1, 0] = 9                                     # in place
+    with pytest.raises(RuntimeError, match=r"lengths\[1,0\] must be between 0 and 4"):
+        d2p_amd.soft_sw_affine_float(scores, -2.0, -0.5, 1.0, ln)
+    ln[1, 0] = 3
+    d2p_amd.soft_sw_affine_float(scores, -2.0, -0.5, 1.0, ln)
+    ln[:, 1].fill_(7)                                # through a view
+    with pytest.raises(RuntimeError, match=r"lengths\[0,1\] must be between 0 and 5"):
+        d2p_amd.soft_sw_affine_float(scores, -2.0, -0.5, 1.0, ln)
+    ln[:, 1].fill_(5)
+    d2p_amd.soft_sw_affine_float(scores, -2.0, -0.5, 1.0, ln)
+    ln.data = torch.tensor([[4, 5], [-1, 2]], dtype=torch.int32, device=cuda)   # new memory
+    with pytest.raises(RuntimeError, match=r"lengths\[1,0\] must be between 0 and 4"):
+        d2p_amd.soft_sw_affine_float(scores, -2.0, -0.5, 1.0, ln)
+    small = torch.randn(2, 3, 5, device=cuda)        # another L1
+    ok = torch.tensor([[3, 5], [3, 2]], dtype=torch.int32, device=cuda)
+    d2p_amd.soft_sw_affine_float(scores, -2.0, -0.5, 1.0, ok)
+    ok[0, 0] = 4
+    d2p_amd.soft_sw_affine_float(scores, -2.0, -0.5, 1.0, ok)
+    with pytest.raises(RuntimeError, match=r"lengths\[0,0\] must be between 0 and 3"):
+        d2p_amd.soft_sw_affine_float(small, -2.0, -0.5, 1.0, ok)
+    with torch.inference_mode():                     # no version counter: always checked
+        inf = torch.tensor([[4, 5], [5, 2]], dtype=torch.int32, device=cuda)
+        with pytest.raises(RuntimeError, match=r"lengths\[1,0\] must be between 0 and 4"):
+            d2p_amd.soft_sw_affine_float(scores, -2.0, -0.5, 1.0, inf)
+
+
 @pytest.mark.parametrize("family", ["sw", "swa", "nw", "nwa"])
 def test_hvp_shape_mismatch_raises(cuda, family):
     scores = torch.randn(1, 4, 5, device=cuda)
