@@ -628,9 +628,17 @@ dtw_backward_kernel(const int* __restrict__ lengths,
                 const float el = fast_exp2((m - a1) * c);
                 const float z = (ed + eu) + el;
                 const float rin = m < kPINF ? fast_rcp(z) : 0.0f;
-                // reference accumulation order: init, diagonal, left, up successor
-                const float binit = t == term_step ? 1.0f : 0.0f;
-                const float beta = ((binit + in_diag) + in_left) + in_up;
+                // reference accumulation order: init, diagonal, left, up successor.  A
+                // FULL chunk never holds the terminal cell (its lane-0 row lies above
+                // L1 - 1 and every other lane's terminal step above t_hi), and the flows
+                // are never -0, so there the zero start term is left out exactly
+                float beta;
+                if (FULL) {
+                    beta = (in_diag + in_left) + in_up;
+                } else {
+                    const float binit = t == term_step ? 1.0f : 0.0f;
+                    beta = ((binit + in_diag) + in_left) + in_up;
+                }
                 const float bl = ok ? beta : 0.0f;
                 const float br = bl * rin;
                 const float od = br * ed, ou = br * eu, ol = br * el;

@@ -1239,9 +1239,11 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                     binit = 0.0f;
                 }
                 // reference accumulation order: init, diagonal, left, up successor (the
-                // flows are never -0, so without a start term 0 + in_diag is in_diag)
-                const float beta = (NWG || INIT || !AHEAD) ? ((binit + in_diag) + in_left) + in_up
-                                                           : (in_diag + in_left) + in_up;
+                // flows are never -0, so without a start term 0 + in_diag is in_diag;
+                // NWG: a FULL chunk never holds the terminal cell)
+                const float beta = ((NWG && !FULL) || INIT || !AHEAD)
+                                       ? ((binit + in_diag) + in_left) + in_up
+                                       : (in_diag + in_left) + in_up;
                 const bool live = ok && (beta <= 3.0e38f);    // skips inf / NaN like the reference
                 const float br = live ? beta * rin : 0.0f;
                 const float od = br * e0, ou = br * e1, ol = br * e2;
