@@ -285,7 +285,9 @@ dtw_forward_kernel(const float* __restrict__ costs, const int* __restrict__ leng
                 if (HELP) atile[u * 64] = cur;
                 else lane_store(outc + u * 64, ul4, cur);
                 pub[u] = cur;
-                if (ok && last_row && col == L2 - 1) terminal = cur;
+                // (the terminal cell never lies in a FULL chunk: lane 0's row is above
+                // L1 - 1, and the other lanes' columns stay below L2 - 1)
+                if (!FULL && ok && last_row && col == L2 - 1) terminal = cur;
             }
             };
             if (bw < 0 && i0 + 63 < L1 && t0 >= 63 && t0 + P <= L2) steps(std::true_type{});
