@@ -39,9 +39,12 @@ constexpr int PF = 16;           // steps per chunk, forward
 constexpr int PB = 8;            // steps per chunk, backward (three alpha planes staged)
 constexpr int DUMMY = 64 + PF;   // per-wave sink entries for the lanes that do not publish
 
+// (the larger term's exponential is exp2(0) = 1 exactly, and the other's argument
+// (min - max) c is -|a - b| c bit for bit: one exponential, the same sum; a NaN in a
+// or b still makes the sum NaN)
 __device__ __forceinline__ float lse2(float a, float b, float c, float tl) {
     const float m = fmaxf(a, b);
-    return m + tl * fast_log2(fast_exp2((a - m) * c) + fast_exp2((b - m) * c));
+    return m + tl * fast_log2(1.0f + fast_exp2(-fabsf(a - b) * c));
 }
 
 __device__ __forceinline__ float lse3(float a, float b, float x, float c, float tl) {
@@ -844,14 +847,17 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 const float betaM = ((initM + dM) + lM) + uM;
                 const float betaI = NWA ? ((initI + dI) + uI) + lI : (initI + dI) + uI;
                 const float betaD = NWA ? ((initD + dD) + lD) + uD : (initD + dD) + lD;
-                // skip inf / NaN betas like the reference; cells outside the element;
-                // NWA: betas at most 1e-20 pass nothing
-                const float lo = NWA ? 1e-20f : -1.0f;
-                const float brM = (ok && betaM > lo && betaM <= 3.0e38f) ? betaM * fast_rcp(esum) : 0.0f;
-                const float brI = (ok && betaI > lo && betaI <= 3.0e38f)
-                                      ? betaI * fast_rcp(NWA ? (f0 + f1) + f2 : f0 + f1) : 0.0f;
-                const float brD = (ok && betaD > lo && betaD <= 3.0e38f)
-                                      ? betaD * fast_rcp(NWA ? (g0 + g1) + g2 : g0 + g1) : 0.0f;
+                // skip inf / NaN betas like the reference (a NaN fails <= too); cells
+                // outside the element; NWA: betas at most 1e-20 pass nothing (the local
+                // form's betas are sums of flows >= 0, so it needs no lower test)
+                auto pass = [&](float beta) {
+                    return ok && (!NWA || beta > 1e-20f) && beta <= 3.0e38f;
+                };
+                const float brM = pass(betaM) ? betaM * fast_rcp(esum) : 0.0f;
+                const float brI = pass(betaI) ? betaI * fast_rcp(NWA ? (f0 + f1) + f2 : f0 + f1)
+                                              : 0.0f;
+                const float brD = pass(betaD) ? betaD * fast_rcp(NWA ? (g0 + g1) + g2 : g0 + g1)
+                                              : 0.0f;
                 const float pv = brM * esum;
                 if constexpr (QT) {
                     if ((u & 3) == 0) quad.w = pv;
