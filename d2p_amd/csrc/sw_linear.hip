@@ -731,6 +731,13 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
     constexpr bool QOUT = !PRECISE && !NWG;
     static_assert(!HELP || QOUT, "helper waves write quad output tiles");
     __shared__ int hprog[NW];     // HELP: chunks of stripe order q loaded by its helper
+    // BCAST (FULL chunks of the plain variant): lane 63's flows from the stripe below
+    // come as per-step broadcast LDS reads, each read used once as the boundary
+    // operand of a DPP shift, instead of registers shifted one lane per step (two DPP
+    // moves per step fewer).  A stripe with no stripe below reads zero flows from
+    // zpairs.
+    constexpr bool BCAST = !PRECISE && !NWG;
+    __shared__ __align__(16) float2 zpairs[P];
     using OutTile = ChunkTile<P>;
     static_assert(OutTile::FLOATS <= BUF, "output tile fits the chunk buffer");
     const int obase_lane = OutTile::read_base(lane);
@@ -740,6 +747,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
         prog[wave] = -1;
         hprog[wave] = -1;
     }
+    if (BCAST && threadIdx.x < P) zpairs[threadIdx.x] = make_float2(0.0f, 0.0f);
     __syncthreads();
 
     const int L1 = lengths ? min(max(lengths[2 * b], 0), L1max) : L1max;
@@ -1106,25 +1114,61 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             // helper's buffer k & 1, whose previous tile the helper has written out
             // before publishing this chunk as loaded
             float* obuf = HELP && !WIDE ? smem + (wave + NW / 2) * 2 * BUF + (k & 1) * BUF : buf;
+            // QOUT: the score quads are read one quad ahead of their steps (quad q of
+            // the output tile lies over score quad q of this lane's row and is written
+            // after that quad's last step), so only two quads are live at a time
             float sv[P];
-            read_quads<P, -1>(buf, lane, sv);
+            auto read_sq = [&](int qq) {
+                const float4 x = *reinterpret_cast<const float4*>(buf + Tile::slot(lane, qq));
+                sv[Tile::template step<-1>(qq, 0)] = x.x;
+                sv[Tile::template step<-1>(qq, 1)] = x.y;
+                sv[Tile::template step<-1>(qq, 2)] = x.z;
+                sv[Tile::template step<-1>(qq, 3)] = x.w;
+            };
+            if constexpr (QOUT) read_sq(0);
+            else read_quads<P, -1>(buf, lane, sv);
             A[0] = A[P];
             A[1] = A[P + 1];
 #pragma unroll
             for (int j = 0; j < P; ++j) A[j + 2] = buf[ABUF + rows_row<P, -1>(j) * 64 + lane];
             // lane j: alpha of the row above at lane-63 step t_hi - j + 63 (column
             // t_hi - j); above the first stripe, row 0: NINF, or (NWG) (column + 1) * gap
-            float bv = buf[RBUF + lane];
-            bv = (s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1) ? bv : kNINF;
-            if (NWG && s == 0)
-                bv = (lane <= P && t_hi - lane + 1 >= 0) ? (float)(t_hi - lane + 1) * gap : kNINF;
+            // FULL: every cell of the chunk lies inside the element
+            const bool inside = i0 + 63 < L1 && t_hi - P - 62 >= 0 && t_hi < L2;
+            const bool bcast = BCAST && inside;
+            float bv = 0.0f;
             // Contributions from the stripe below for lane 63.  The producer (lane 0 of
             // stripe s+1) wrote the pair for its column c into slot (nsteps-1-c) % R;
             // lane 63 at step u needs column t_hi-u-63 (up) and t_hi-u-62 (diagonal),
             // i.e. slots kP+u+63 and kP+u+62.  Lane 63-j holds step j; the register is
             // shifted up one lane per step so lane 63 sees the step it needs next.
+            // bcast: step u takes the up value of step u + 1 and the diagonal value of
+            // step u + 2, both in slot kP+u+64, from a broadcast read of that pair (with
+            // x_in: flow pair u + 2 of the chunk's FBUF range, which starts at slot
+            // kP+62); the chunk starts from slots kP+62 and kP+63.  In a FULL chunk
+            // those slots lie below nsteps - 1 (no clamped flows) and kP+64 .. kP+64+P-1
+            // lie in one ring block of P slots (slot0 and R are multiples of P).  The
+            // reads run BD steps ahead of their use, in a window of registers.
             float pre_u = 0.0f, pre_d = 0.0f;
-            if (below && lane >= 64 - P) {
+            constexpr int BD = 2;
+            float2 rp[P], r62 = make_float2(0.0f, 0.0f), r63 = make_float2(0.0f, 0.0f);
+            const float2* pp = zpairs;
+            if (bcast) {
+                const int s64 = slot0 + 64 < R ? slot0 + 64 : slot0 + 64 - R;
+                const int s62 = s64 >= 2 ? s64 - 2 : s64 - 2 + R;
+                const float2* fb = reinterpret_cast<const float2*>(buf + FBUF);
+                pp = !below ? zpairs : x_in ? fb + 2 : ring_in + s64;
+                const float2* pq = !below ? zpairs : x_in ? fb : ring_in + s62;
+                r62 = pq[0];
+                r63 = pq[1];
+#pragma unroll
+                for (int u = 0; u < BD; ++u) rp[u] = pp[u];
+            }
+            bv = buf[RBUF + lane];
+            bv = (s > 0 && lane <= P && t_hi - lane + 63 <= nsteps - 1) ? bv : kNINF;
+            if (NWG && s == 0)
+                bv = (lane <= P && t_hi - lane + 1 >= 0) ? (float)(t_hi - lane + 1) * gap : kNINF;
+            if (!bcast && below && lane >= 64 - P) {
                 const int j = 63 - lane;
                 if (x_in) {
                     pre_u = buf[FBUF + 2 * (j + 1)];
@@ -1150,8 +1194,9 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             float2* pub = (lane == 0) ? ring_out + slot0 : sink + lane;
             // lane 63 starts the chunk with the ring's values for steps 0 and 1
             {
-                const float u0 = lane_bcast(pre_u, 63), d0 = lane_bcast(pre_d, 63);
-                const float d1 = lane_bcast(pre_d, 62);
+                const float u0 = bcast ? r63.x : lane_bcast(pre_u, 63);
+                const float d0 = bcast ? r62.y : lane_bcast(pre_d, 63);
+                const float d1 = bcast ? r63.y : lane_bcast(pre_d, 62);
                 if (lane == 63) { in_up = u0; in_diag = d0; in_diag_next = d1; }
             }
             // PRECISE and NWG: the chunk's parameter-gradient terms are kept for balanced
@@ -1161,8 +1206,11 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             // the quad being filled: memory-column order, i.e. step 4q + 3 - e in
             // element e (the reverse sweep's columns fall with the step)
             float4 quad = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            float pre_d2 = wave_shr1(pre_d);   // lane 63 = step 1 (then shifted on)
-            pre_d2 = wave_shr1(pre_d2);        // lane 63 = step 2
+            float pre_d2 = 0.0f;
+            if (!bcast) {
+                pre_d2 = wave_shr1(pre_d);    // lane 63 = step 1 (then shifted on)
+                pre_d2 = wave_shr1(pre_d2);   // lane 63 = step 2
+            }
             // AHEAD: the ring's up values shifted one step ahead (lane 63 = step 1), and
             // lane 0's row-above alphas too (bv of step u + 1): each step shifts the next
             // copy out before its DPP consumes this one as the fill value, so no copy of
@@ -1172,7 +1220,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             constexpr bool AHEAD = !PRECISE;
             float upa_next = 0.0f;
             if constexpr (AHEAD) {
-                pre_u = wave_shr1(pre_u);
+                if (!bcast) pre_u = wave_shr1(pre_u);
                 upa_next = wave_shr1_or(A[1], bv);
                 bv = wave_shl1(bv);
             }
@@ -1200,6 +1248,12 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 const float a0 = A[u], a1 = A[u + 1];
                 // up / diagonal alphas from lane r-1; lane 0 takes the row above
                 float upa, dga;
+                if constexpr (QOUT) {
+                    if ((u & 3) == 0 && u + 4 < P) read_sq((u >> 2) + 1);
+                }
+                if constexpr (FULL && BCAST) {
+                    if (u + BD < P) rp[u + BD] = pp[u + BD];
+                }
                 if constexpr (AHEAD) {
                     const float bv2 = wave_shl1(bv);
                     upa = upa_next;
@@ -1220,8 +1274,14 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 // rounding is ~2^75 at the 1e30 sentinels of cells outside the element,
                 // so m is floored far below any real alpha (those cells' e_k become 0
                 // and their flows are selected away, not multiplied).
-                const float m = NWG ? fmaxf(fmaxf(vd, vu), fmaxf(vl, -1e20f))
-                                    : fmaxf(fmaxf(vd, vu), fmaxf(fmaxf(vl, sc), -1e20f));
+                // (FULL: the cell's own alpha a0 = m + T ln(sum) takes the max's place.
+                // The forward formed it from these same operands, so a0 >= m, every
+                // exponent is at most 0 and the largest term at least 1/4 (a sum of at
+                // most four terms); the shift cancels in the normalisation as m's does.
+                // PRECISE keeps the max: its registers are all in use.)
+                const float m = (FULL && !PRECISE) ? a0
+                                : NWG ? fmaxf(fmaxf(vd, vu), fmaxf(vl, -1e20f))
+                                      : fmaxf(fmaxf(vd, vu), fmaxf(fmaxf(vl, sc), -1e20f));
                 const float mc = m * c;
                 const float e0 = fast_exp2(fmaf(vd, c, -mc)), e1 = fast_exp2(fmaf(vu, c, -mc));
                 const float e2 = fast_exp2(fmaf(vl, c, -mc));
@@ -1274,22 +1334,29 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
                 else p_acc = fmaf(pv, sc, p_acc);
                 pub[u] = make_float2(ou, od);
                 // successor contributions for the next steps; lane 63 takes the ring
-                if constexpr (AHEAD) {
-                    const float pre_u2 = wave_shr1(pre_u);
+                if constexpr (FULL && BCAST) {
                     in_left = ol;
-                    in_up = wave_shl1_or(ou, pre_u);
-                    pre_u = pre_u2;
+                    in_up = wave_shl1_or(ou, rp[u].x);
+                    in_diag = in_diag_next;
+                    in_diag_next = wave_shl1_or(od, rp[u].y);
                 } else {
-                    pre_u = wave_shr1(pre_u);
-                    in_left = ol;
-                    in_up = wave_shl1_or(ou, pre_u);
+                    if constexpr (AHEAD) {
+                        const float pre_u2 = wave_shr1(pre_u);
+                        in_left = ol;
+                        in_up = wave_shl1_or(ou, pre_u);
+                        pre_u = pre_u2;
+                    } else {
+                        pre_u = wave_shr1(pre_u);
+                        in_left = ol;
+                        in_up = wave_shl1_or(ou, pre_u);
+                    }
+                    in_diag = in_diag_next;
+                    in_diag_next = wave_shl1_or(od, pre_d2);
+                    pre_d2 = wave_shr1(pre_d2);
                 }
-                in_diag = in_diag_next;
-                in_diag_next = wave_shl1_or(od, pre_d2);
-                pre_d2 = wave_shr1(pre_d2);
             }
             };
-            if (i0 + 63 < L1 && t_hi - P - 62 >= 0 && t_hi < L2) {
+            if (inside) {
                 if (inits) steps(std::true_type{}, std::true_type{});
                 else steps(std::true_type{}, std::false_type{});
             } else {
