@@ -804,21 +804,46 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                 // M: diagonal + start weights (NWA: the diagonal only)
                 const float v0 = NWA ? dgM : dgM + sc, v1 = NWA ? dgI : dgI + sc,
                             v2 = NWA ? dgD : dgD + sc;
-                const float m4 = NWA ? fmaxf(fmaxf(v0, v1), v2) : fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
+                // (local FULL: the cell's own M alpha, which the forward formed from these
+                // operands as m + T ln(sum) >= m, takes the max's place: every exponent
+                // is at most 0, the largest term at least 1/4, and the shift cancels in
+                // the normalisation)
+                const float m4 = NWA ? fmaxf(fmaxf(v0, v1), v2)
+                                     : FULL ? AM[u] : fmaxf(fmaxf(v0, v1), fmaxf(v2, sc));
                 const float e0 = fast_exp2((v0 - m4) * c), e1 = fast_exp2((v1 - m4) * c);
                 const float e2 = fast_exp2((v2 - m4) * c);
                 const float e3 = NWA ? 0.0f : fast_exp2((sc - m4) * c);
                 const float esum = NWA ? (e0 + e1) + e2 : ((e0 + e1) + e2) + e3;
                 // I: open from M above, extend from I above (NWA: open from D above)
+                // (local: two terms, the larger one's weight exactly 1 and the other's
+                // exponent -|a - b| c bit for bit, as lse2 forms them: one exponential)
                 const float i0v = upM + go, i1v = upI + ge, i2v = upD + go;
-                const float mi = NWA ? fmaxf(fmaxf(i0v, i1v), i2v) : fmaxf(i0v, i1v);
-                const float f0 = fast_exp2((i0v - mi) * c), f1 = fast_exp2((i1v - mi) * c);
-                const float f2 = NWA ? fast_exp2((i2v - mi) * c) : 0.0f;
+                float f0, f1, f2 = 0.0f;
+                if constexpr (NWA) {
+                    const float mi = fmaxf(fmaxf(i0v, i1v), i2v);
+                    f0 = fast_exp2((i0v - mi) * c);
+                    f1 = fast_exp2((i1v - mi) * c);
+                    f2 = fast_exp2((i2v - mi) * c);
+                } else {
+                    const float di = i0v - i1v;
+                    const float fs = fast_exp2(-fabsf(di) * c);
+                    f0 = di >= 0.0f ? 1.0f : fs;
+                    f1 = di >= 0.0f ? fs : 1.0f;
+                }
                 // D: open from M left, extend from D left (NWA: open from I left)
                 const float d0v = lfM + go, d1v = lfD + ge, d2v = lfI + go;
-                const float md = NWA ? fmaxf(fmaxf(d0v, d1v), d2v) : fmaxf(d0v, d1v);
-                const float g0 = fast_exp2((d0v - md) * c), g1 = fast_exp2((d1v - md) * c);
-                const float g2 = NWA ? fast_exp2((d2v - md) * c) : 0.0f;
+                float g0, g1, g2 = 0.0f;
+                if constexpr (NWA) {
+                    const float md = fmaxf(fmaxf(d0v, d1v), d2v);
+                    g0 = fast_exp2((d0v - md) * c);
+                    g1 = fast_exp2((d1v - md) * c);
+                    g2 = fast_exp2((d2v - md) * c);
+                } else {
+                    const float dd = d0v - d1v;
+                    const float gs = fast_exp2(-fabsf(dd) * c);
+                    g0 = dd >= 0.0f ? 1.0f : gs;
+                    g1 = dd >= 0.0f ? gs : 1.0f;
+                }
                 // betas in the reference's accumulation order (NWA: the terminal cell's
                 // softmax weights over its three states start the recursion)
                 float initM, initI, initD;
