@@ -779,9 +779,13 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 bA = nA;
                 bX = nX;
                 const float v0 = dga + sc, v1 = upa + gap, v2 = a1 + gap;
-                // NWG: no restart candidate
+                // NWG: no restart candidate.  (FULL HVP: the cell's own alpha, which the
+                // forward formed from these operands as m + T ln(sum) >= m, takes the
+                // max's place: every exponent is at most 0, the largest term at least
+                // 1/4, and the shift cancels in the normalisation.  The parameter
+                // Jacobians use m itself below.)
                 const float m = NWG ? fmaxf(fmaxf(v0, v1), v2)
-                                    : (FULL ? max4_raw(v0, v1, v2, sc)
+                                    : (FULL ? (MODE == HVP ? a0 : max4_raw(v0, v1, v2, sc))
                                             : fmaxf(fmaxf(v0, v1), fmaxf(v2, sc)));
                 const float e0 = fast_exp2((v0 - m) * c), e1 = fast_exp2((v1 - m) * c);
                 const float e2 = fast_exp2((v2 - m) * c);
@@ -798,8 +802,10 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                     d0 = dgx; d1 = upx; d2 = x1; d3 = 0.0f;
                 }
                 float dw0, dw1, dw2, dw3;
+                float mean_hvp = 0.0f;
                 if (MODE == HVP) {
                     const float mean = ((w0 * d0 + w1 * d1) + w2 * d2) + w3 * d3;
+                    mean_hvp = mean;
                     dw0 = w0 * (d0 - mean) * rT;
                     dw1 = w1 * (d1 - mean) * rT;
                     dw2 = w2 * (d2 - mean) * rT;
@@ -860,7 +866,25 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 }
                 const float bl = live ? beta : 0.0f;
                 const float gl = live ? g : 0.0f;
-                const float o = gl * (w0 + w3) + bl * (dw0 + dw3);
+                // FULL HVP: gl w_k + bl dw_k = w_k (gl + bl (d_k - mean) / T), and the
+                // output takes the candidates 0 and 3 (fewer instructions than the
+                // weight tangents themselves; the same sums up to rounding)
+                constexpr bool GROUPED = FULL && MODE == HVP && !NWG;
+                float og0, og1, og2, o;
+                if constexpr (GROUPED) {
+                    const float bT = bl * rT;
+                    const float t0 = fmaf(bT, d0 - mean_hvp, gl), t1 = fmaf(bT, d1 - mean_hvp, gl);
+                    const float t2 = fmaf(bT, d2 - mean_hvp, gl), t3 = fmaf(bT, d3 - mean_hvp, gl);
+                    og0 = w0 * t0;
+                    og1 = w1 * t1;
+                    og2 = w2 * t2;
+                    o = fmaf(w3, t3, og0);
+                } else {
+                    o = gl * (w0 + w3) + bl * (dw0 + dw3);
+                    og0 = gl * w0 + bl * dw0;
+                    og1 = gl * w1 + bl * dw1;
+                    og2 = gl * w2 + bl * dw2;
+                }
                 if (DOT) {
                     dacc += o * vd;
                 } else if constexpr (QT) {
@@ -875,8 +899,6 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                     otile[tbase + u] = o;
                 }
                 const float ob0 = bl * w0, ob1 = bl * w1, ob2 = bl * w2;
-                const float og0 = gl * w0 + bl * dw0, og1 = gl * w1 + bl * dw1;
-                const float og2 = gl * w2 + bl * dw2;
                 pub[u] = make_float4(ob1, og1, ob0, og0);
                 // successor flows for the next steps; lane 63 takes the ring
                 qub = wave_shr1(qub);
