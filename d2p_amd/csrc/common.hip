@@ -119,6 +119,49 @@ scale_by_batch_kernel(const float* __restrict__ src, const float* __restrict__ g
     }
 }
 
+// The same for [B, max_L1, max_L2] tensors that are zero outside each element's
+// lengths (the marginals): cells inside the lengths are scaled as above; the others
+// are written as g[b] * 0 without being read (the same bits as g[b] * src where src
+// is +0, NaN where g[b] is not finite).  A workgroup handles whole rows of one element
+// (rows along x, elements along y); vec: 16-byte quads (max_L2 a multiple of 4 and
+// both bases 16-byte aligned).
+__global__ void __launch_bounds__(256)
+scale_by_batch_lengths_kernel(const float* __restrict__ src, const float* __restrict__ g,
+                              long long g_stride, float* __restrict__ dst,
+                              const int* __restrict__ lengths, int B, int L1max, int L2max,
+                              int vec) {
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    for (int b = blockIdx.y; b < B; b += gridDim.y) {
+        const float gb = g[(size_t)b * g_stride];
+        const float z = gb * 0.0f;
+        const int L1 = min(max(lengths[2 * b], 0), L1max);
+        const int L2 = min(max(lengths[2 * b + 1], 0), L2max);
+        for (int i = blockIdx.x; i < L1max; i += gridDim.x) {
+            const size_t row = ((size_t)b * L1max + i) * (size_t)L2max;
+            const int lim = i < L1 ? L2 : 0;   // columns read in this row
+            if (vec) {
+                const v4f* s4 = reinterpret_cast<const v4f*>(src + row);
+                v4f* d4 = reinterpret_cast<v4f*>(dst + row);
+                for (int q = threadIdx.x; q < (L2max >> 2); q += blockDim.x) {
+                    const int c0 = 4 * q;
+                    v4f v = {z, z, z, z};
+                    if (c0 < lim) {
+                        const v4f x = __builtin_nontemporal_load(s4 + q);
+                        v.x = x.x * gb;
+                        v.y = c0 + 1 < lim ? x.y * gb : z;
+                        v.z = c0 + 2 < lim ? x.z * gb : z;
+                        v.w = c0 + 3 < lim ? x.w * gb : z;
+                    }
+                    __builtin_nontemporal_store(v, d4 + q);
+                }
+            } else {
+                for (int j = threadIdx.x; j < L2max; j += blockDim.x)
+                    dst[row + j] = j < lim ? src[row + j] * gb : z;
+            }
+        }
+    }
+}
+
 }  // namespace d2p_amd
 
 extern "C" const char* d2p_last_error(void) { return d2p_amd::g_last_error; }
@@ -175,6 +218,28 @@ extern "C" int d2p_scale_by_batch_strided(const float* src, const float* g, long
     D2P_LAUNCH("scale_by_batch", d2p_amd::scale_by_batch_kernel,
                dim3((unsigned)bx, (unsigned)by), dim3(256), 0, (hipStream_t)stream, src, g,
                g_stride, dst, B, per_batch, vec ? 1 : 0);
+    D2P_HIP(hipGetLastError());
+    return D2P_OK;
+}
+
+extern "C" int d2p_scale_by_batch_lengths(const float* src, const float* g, long long g_stride,
+                                          const int* lengths, float* dst, int B, int max_L1,
+                                          int max_L2, void* stream) {
+    D2P_REQUIRE(B >= 0 && max_L1 >= 0 && max_L2 >= 0, "negative size");
+    D2P_REQUIRE(g_stride >= 0, "negative factor stride");
+    if (B == 0 || max_L1 == 0 || max_L2 == 0) return D2P_OK;
+    if (lengths == nullptr)
+        return d2p_scale_by_batch_strided(src, g, g_stride, dst, B,
+                                          (long long)max_L1 * max_L2, stream);
+    D2P_REQUIRE(src && g && dst, "null pointer argument");
+    const bool vec = (max_L2 % 4 == 0) && (((uintptr_t)src | (uintptr_t)dst) % 16 == 0);
+    // about 32768 workgroups in all, as the flat form: elements along y, rows along x
+    const int by = B < 65535 ? B : 65535;
+    const int cap = 32768 / by > 1 ? 32768 / by : 1;
+    const int bx = max_L1 < cap ? max_L1 : cap;
+    D2P_LAUNCH("scale_by_batch", d2p_amd::scale_by_batch_lengths_kernel, dim3(bx, by),
+               dim3(256), 0, (hipStream_t)stream, src, g, g_stride, dst, lengths, B, max_L1,
+               max_L2, vec ? 1 : 0);
     D2P_HIP(hipGetLastError());
     return D2P_OK;
 }

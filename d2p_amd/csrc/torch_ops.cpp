@@ -172,13 +172,23 @@ Tensor grad_param_sum(const Tensor& grad_value, const Tensor& per_batch) {
 
 // g[b] * src, through the C ABI (autograd backward of value -> scores).  The factors
 // are read in place by stride: the gradient of `value.sum()` arrives as one value
-// expanded over the batch (stride 0), which needs no copy.
-Tensor scale_by_batch(const Tensor& src, const Tensor& g) {
+// expanded over the batch (stride 0), which needs no copy.  With lengths (the checked
+// int32 [B, 2] tensor of the forward) src is a [B, L1, L2] table that is zero outside
+// them: only the cells inside are read.
+Tensor scale_by_batch(const Tensor& src, const Tensor& g, const Tensor& lengths = Tensor()) {
     Tensor gg = g.to(src.device(), torch::kFloat32);
     TORCH_CHECK(gg.numel() == src.size(0), "grad_value must have one entry per batch element");
     if (gg.dim() != 1) gg = gg.reshape({-1});
     if (gg.numel() > 0 && gg.stride(0) < 0) gg = gg.contiguous();
     Tensor out = torch::empty_like(src);
+    if (lengths.defined() && src.dim() == 3) {
+        D2P_CALL(d2p_scale_by_batch_lengths(src.data_ptr<float>(), gg.data_ptr<float>(),
+                                            (long long)gg.stride(0), lengths.data_ptr<int>(),
+                                            out.data_ptr<float>(), (int)src.size(0),
+                                            (int)src.size(1), (int)src.size(2),
+                                            current_stream()));
+        return out;
+    }
     D2P_CALL(d2p_scale_by_batch_strided(src.data_ptr<float>(), gg.data_ptr<float>(),
                                         (long long)gg.stride(0), out.data_ptr<float>(),
                                         (int)src.size(0),
@@ -295,7 +305,7 @@ tensor_list sw_autograd_backward(AutogradContext* ctx, const tensor_list& grads,
     Tensor grad_value = grads[0], grad_marg = grads[1];
     Tensor grad_scores, grad_gap, grad_T;
     if (grad_value.defined() && grad_value.numel() > 0) {
-        grad_scores = scale_by_batch(marg, grad_value);
+        grad_scores = scale_by_batch(marg, grad_value, lengths);
         if (want_gap) grad_gap = grad_param_sum(grad_value, ggap);
         if (want_T) grad_T = grad_param_sum(grad_value, gT);
     }
@@ -479,7 +489,7 @@ tensor_list nw_autograd_backward(AutogradContext* ctx, const tensor_list& grads,
     Tensor grad_value = grads[0], grad_marg = grads[1];
     Tensor grad_scores, grad_gap, grad_T;
     if (grad_value.defined() && grad_value.numel() > 0) {
-        grad_scores = scale_by_batch(marg, grad_value);
+        grad_scores = scale_by_batch(marg, grad_value, lengths);
         if (want_gap) grad_gap = grad_param_sum(grad_value, ggap);
         if (want_T) grad_T = grad_param_sum(grad_value, gT);
     }
@@ -735,7 +745,7 @@ tensor_list swa_autograd_backward(AutogradContext* ctx, const tensor_list& grads
     Tensor grad_value = grads[0], grad_marg = grads[1];
     Tensor gs, go, ge, gT;
     if (grad_value.defined() && grad_value.numel() > 0) {
-        gs = scale_by_batch(marg, grad_value);
+        gs = scale_by_batch(marg, grad_value, lengths);
         if (want_o) go = grad_param_sum(grad_value, saved[3]);
         if (want_e) ge = grad_param_sum(grad_value, saved[4]);
         if (want_T) gT = grad_param_sum(grad_value, saved[5]);
@@ -1069,7 +1079,7 @@ class SoftDTWFunction : public torch::autograd::Function<SoftDTWFunction> {
         Tensor grad_value = grads[0], grad_marg = grads[1];
         Tensor gc, gt;
         if (grad_value.defined() && grad_value.numel() > 0) {
-            gc = scale_by_batch(marg, grad_value);
+            gc = scale_by_batch(marg, grad_value, lengths);
             if (ctx->needs_input_grad(1)) gt = grad_param_sum(grad_value, gT);
         }
         if (grad_marg.defined() && grad_marg.numel() > 0) {

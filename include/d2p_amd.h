@@ -425,6 +425,17 @@ int d2p_scale_by_batch(const float* src, const float* g, float* dst, int B,
 int d2p_scale_by_batch_strided(const float* src, const float* g, long long g_stride,
                                float* dst, int B, long long per_batch, void* stream);
 
+/* dst = g[b] * src over [B, max_L1, max_L2] tensors that are zero outside each
+ * element's lengths (int32 [B, 2] on the device; null: full lengths, the strided form
+ * above): cells outside (L1, L2) are written as g[b] * 0 without being read, the same
+ * bits as the full product of a zero there.  For a ragged batch this reads only the
+ * valid cells.  Replaces the same ATen expression of the reference's autograd backward
+ * (/root/reference/src/sw_affine/torch_cuda.cpp, src/sw/torch_cuda.cpp:314), whose
+ * posteriors hold zeros outside the lengths. */
+int d2p_scale_by_batch_lengths(const float* src, const float* g, long long g_stride,
+                               const int* lengths, float* dst, int B, int max_L1, int max_L2,
+                               void* stream);
+
 #ifdef __cplusplus
 }
 #endif

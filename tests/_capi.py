@@ -68,6 +68,7 @@ SIGNATURES = {
     "d2p_profile_reset": (None, []),
     "d2p_scale_by_batch": (_i, [_p, _p, _p, _i, _ll, _p]),
     "d2p_scale_by_batch_strided": (_i, [_p, _p, _ll, _p, _i, _ll, _p]),
+    "d2p_scale_by_batch_lengths": (_i, [_p, _p, _ll, _p, _p, _i, _i, _i, _p]),
 }
 
 _lib = None
@@ -361,6 +362,17 @@ def scale_by_batch_strided(src, g):
     B = src.shape[0]
     check(lib().d2p_scale_by_batch_strided(ptr(src), ptr(g), g.stride(0), ptr(out), B,
                                            src.numel() // B, stream()))
+    return out
+
+
+def scale_by_batch_lengths(src, g, lengths):
+    """src [B, L1, L2] zero outside lengths (int32 [B, 2] on the device, or None)."""
+    import torch
+    out = torch.empty_like(src)
+    B, L1, L2 = src.shape
+    check(lib().d2p_scale_by_batch_lengths(ptr(src), ptr(g), g.stride(0),
+                                           ptr(lengths) if lengths is not None else None,
+                                           ptr(out), B, L1, L2, stream()))
     return out
 
 

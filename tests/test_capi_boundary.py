@@ -111,6 +111,11 @@ def test_scale_by_batch_validation(lib):
     assert rc == D2P_ERR_ARG and "negative" in _err(lib)
     rc = lib.d2p_scale_by_batch(FAKE, FAKE, FAKE, 2, -3, None)
     assert rc == D2P_ERR_ARG and "negative" in _err(lib)
+    rc = lib.d2p_scale_by_batch_lengths(FAKE, FAKE, -1, FAKE, FAKE, 2, 4, 4, None)
+    assert rc == D2P_ERR_ARG and "negative factor stride" in _err(lib)
+    rc = lib.d2p_scale_by_batch_lengths(FAKE, FAKE, 0, FAKE, FAKE, 2, -4, 4, None)
+    assert rc == D2P_ERR_ARG and "negative" in _err(lib)
+    assert lib.d2p_scale_by_batch_lengths(None, None, 0, None, None, 0, 4, 4, None) == 0
     # empty work is a no-op, even with null pointers
     assert lib.d2p_scale_by_batch_strided(None, None, 0, None, 0, 16, None) == 0
     assert lib.d2p_scale_by_batch(None, None, None, 4, 0, None) == 0

@@ -125,6 +125,53 @@ def test_scale_by_batch_strided(cuda, kind):
     torch.testing.assert_close(out, g.reshape(-1, 1, 1) * src, rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("shape,kind", [((5, 33, 17), "contiguous"), ((6, 64, 80), "expanded"),
+                                        ((4, 40, 36), "every_other"), ((3, 7, 5), "contiguous")])
+def test_scale_by_batch_lengths(cuda, shape, kind):
+    """Tables that are zero outside ragged lengths (empty, partial and full elements):
+    bit-identical to the broadcast product, padding included (g * 0 keeps the sign of
+    a negative factor), with only the cells inside the lengths read (the padding
+    holds NaN in src here, which a read would carry into the output)."""
+    B, L1, L2 = shape
+    src = _seeded(7, shape).to(cuda)
+    lens = torch.tensor([[L1, L2], [0, L2], [L1 - 3, 1], [2, L2 - 1], [L1, 0], [1, 1]][:B],
+                        dtype=torch.int32)
+    mask = torch.zeros(shape, dtype=torch.bool)
+    for b in range(B):
+        mask[b, :lens[b, 0], :lens[b, 1]] = True
+    mask = mask.to(cuda)
+    base = _seeded(8, (2 * B,)).to(cuda)
+    g = {"expanded": base[3:4].expand(B), "every_other": base[::2],
+         "contiguous": base[:B]}[kind]
+    expect = g.reshape(-1, 1, 1) * torch.where(mask, src, torch.zeros_like(src))
+    poisoned = torch.where(mask, src, torch.full_like(src, float("nan")))
+    out = _capi.scale_by_batch_lengths(poisoned, g, lens.to(cuda))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out, expect, rtol=0, atol=0)
+    assert torch.equal(torch.signbit(out), torch.signbit(expect))
+    # no lengths: the full product
+    full = _capi.scale_by_batch_lengths(src, g, None)
+    torch.testing.assert_close(full, g.reshape(-1, 1, 1) * src, rtol=0, atol=0)
+
+
+def test_ragged_value_backward_is_the_scaled_marginals(cuda):
+    """soft_sw / soft_sw_affine with ragged lengths, value.sum() and a weighted sum
+    backward: the gradient equals grad_value[b] * marginals bit for bit."""
+    import d2p_amd
+    s = _seeded(9, (3, 70, 90)).to(cuda)
+    lens = torch.tensor([[70, 90], [33, 41], [5, 90]], dtype=torch.int32, device=cuda)
+    w = torch.tensor([1.5, -2.0, 0.25], device=cuda)
+    for fn in (lambda x: d2p_amd.soft_sw(x, gap=-1.0, temperature=1.0, lengths=lens),
+               lambda x: d2p_amd.soft_sw_affine(x, gap_open=-2.0, gap_ext=-0.5,
+                                                temperature=1.0, lengths=lens)):
+        x = s.detach().requires_grad_(True)
+        r = fn(x)
+        (r.value * w).sum().backward()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(x.grad, w.view(-1, 1, 1) * r.marginals.detach(),
+                                   rtol=0, atol=0)
+
+
 def test_soft_sw_api_value_backward(cuda):
     """d2p_amd.soft_sw + value.sum().backward(): grad equals the marginals."""
     import d2p_amd
