@@ -1150,7 +1150,7 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             // lie in one ring block of P slots (slot0 and R are multiples of P).  The
             // reads run BD steps ahead of their use, in a window of registers.
             float pre_u = 0.0f, pre_d = 0.0f;
-            constexpr int BD = 2;
+            constexpr int BD = 1;
             float2 rp[P], r62 = make_float2(0.0f, 0.0f), r63 = make_float2(0.0f, 0.0f);
             const float2* pp = zpairs;
             if (bcast) {
