@@ -938,13 +938,15 @@ sw_dual_kernel(const float* __restrict__ scores, const float* __restrict__ V,
                 if (lane < P) store_sys4(flows_out + k * P + lane, ring_out[ring_index(k * P, R) + lane]);
                 // HELP: the word reports the chunks up to k - XD, whose flow stores (and
                 // everything before) are complete once at most XD memory operations are
-                // outstanding (the flow stores of chunks k - XD + 1 .. k follow them):
-                // device-coherent stores take several chunk periods to complete in the
-                // sweep's busiest phase, and a wait for the last two chunks' stalled
-                // this stripe, and through the rings its whole part, on every chunk.
+                // outstanding (this wave's only other memory operations are its flag
+                // stores and, when the part has one stripe, the flow loads of its x_in
+                // side, all issued before this chunk's flow store).  XD = 1 reports the
+                // chunks before this one: the part above learns of a chunk's flows one
+                // chunk after their store (measured at C5 HVP: 3276-3280 us against
+                // 3305-3310 with XD = 2 and 3346-3356 with XD = 4).
                 // Plain form: at least (QT ? P/4 : P) + P/2 + 2 loads, 2 flow stores and
                 // 2 NSTORE output stores follow the flow store of chunk k - 2.
-                constexpr int XD = HELP ? 4 : 2;
+                constexpr int XD = HELP ? 1 : 2;
                 if (k >= XD) {
                     if constexpr (HELP) wait_vmcnt<XD>();
                     else wait_vmcnt<(QT ? NQ : P) + P / 2 + 4 + 2 * NSTORE>();
