@@ -582,7 +582,17 @@ sw_forward_kernel(const float* __restrict__ scores, const int* __restrict__ leng
                 }
             }
             publish(prog, wave, l * PROG_STRIDE + k + 1);
-            if (x_out && k >= 2) {
+            if (TAN && HELP && x_out && !x_in && k >= 1) {
+                // TAN with helpers, a part's last stripe that is not also its first:
+                // this wave's only memory operations are its last-row stores (NTL per
+                // chunk) and its flag stores (one per chunk from chunk 1 on), so once at
+                // most the previous chunk's flag store and this chunk's row stores are
+                // outstanding, every chunk before this one is complete.  (Measured at
+                // C5: the tangent forward 1974 against 1994-1999 us; the plain forward
+                // 1319-1324 against 1307-1314, so it keeps the report below.)
+                if (k == 1) wait_vmcnt<NTL>(); else wait_vmcnt<NTL + 1>();
+                if (lane == 0) store_flag(flag_out, progress_word(epoch, k));
+            } else if (x_out && k >= 2) {
                 // at least 2 * (P/4 + P + 1) vector-memory operations (HELP: the last
                 // row stores of chunks k - 1 and k) follow the row stores of chunk
                 // k - 2: those (and everything before) are complete.  TAN: at least
@@ -1384,11 +1394,19 @@ sw_backward_kernel(const float* __restrict__ scores, const int* __restrict__ len
             if (x_out) {
                 // this chunk's flows to the part above, by producer step
                 if (lane < P) store_sys2(flows_out + k * P + lane, ring_out[slot0 + lane]);
-                if (k >= 2) {
+                if (HELP && !x_in && k >= 1) {
+                    // HELP, a part's last stripe that is not also its first: its only
+                    // memory operations are its flow stores and its flag stores (one
+                    // per chunk from chunk 1 on), so once at most the previous chunk's
+                    // flag store and this chunk's flow store are outstanding, every
+                    // chunk before this one is complete
+                    if (k == 1) wait_vmcnt<1>(); else wait_vmcnt<2>();
+                    if (lane == 0) store_flag(flag_out, progress_word(epoch, k));
+                } else if (k >= 2) {
                     // at least (2 P/4 + 1) loads and NSTORE stores of chunk k - 1, NSTORE
                     // stores of chunk k and the two chunks' flow stores follow the flow
-                    // store of chunk k - 2 (HELP: the row-above load issued in chunk
-                    // k - 1 and the two flow stores): it is complete
+                    // store of chunk k - 2 (HELP: the flow loads of chunk k + 1 and the
+                    // two flow stores): it is complete
                     if constexpr (HELP) wait_vmcnt<3>();
                     else wait_vmcnt<2 * Tile::NQ + 2 * NSTORE + 3>();
                     if (lane == 0) store_flag(flag_out, progress_word(epoch, k - 1));
