@@ -968,7 +968,19 @@ swa_backward_kernel(const float* __restrict__ scores, const int* __restrict__ le
                     if constexpr (NWA) store_sys2(flowsF + fo + k * P + lane, r1_out[slot]);
                     else store_sys(flows1 + fo + k * P + lane, r1_out[slot]);
                 }
-                if (k >= 2) {
+                if (HELP && !x_in && k >= 1) {
+                    // HELP, a part's last stripe that is not also its first: after the
+                    // flow stores of chunk k - 1 it issued only that chunk's flag store
+                    // (from chunk 1 on), the 3 rows-above loads of chunk k + 1 (when
+                    // there is one) and this chunk's 2 flow stores; once at most those
+                    // are outstanding, every chunk before this one is complete
+                    const bool more = k + 1 < nch;
+                    if (k >= 2 && more) wait_vmcnt<6>();
+                    else if (more) wait_vmcnt<5>();
+                    else if (k >= 2) wait_vmcnt<3>();
+                    else wait_vmcnt<2>();
+                    if (lane == 0) store_flag(flag_out, progress_word(epoch, k));
+                } else if (k >= 2) {
                     // at least NQ + 3P/4 + 3 loads, 2 NQ marginal stores and 4 flow stores
                     // (HELP: the 3 rows-above loads issued in chunk k - 1 and 4 flow
                     // stores) follow the flow stores of chunk k - 2: those are complete
